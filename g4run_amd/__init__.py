@@ -1,0 +1,304 @@
+"""g4run_amd -- MI355X (gfx950) implementation of g4run's quantized
+weight x activation hot path, reached through the C ABI of include/g4hip.h.
+
+This module is a thin ctypes front end over g4run_amd/libg4hip.so (built by
+g4run_amd/build.py).  It has no CPU fallback: importing it without the built
+library, or calling it without a gfx950 device, raises.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libg4hip.so")
+INCLUDE = os.path.join(os.path.dirname(HERE), "include", "g4hip.h")
+
+# type ids (g4run.h:80-94)
+F32, F16, Q4_0, Q8_0, Q2_K, Q3_K, Q4_K, Q8_K = 0, 1, 2, 8, 10, 11, 12, 15
+BLCK = {F32: 1, F16: 1, Q4_0: 32, Q8_0: 32, Q2_K: 256, Q3_K: 256, Q4_K: 256, Q8_K: 256}
+SIZE = {F32: 4, F16: 2, Q4_0: 18, Q8_0: 34, Q2_K: 84, Q3_K: 110, Q4_K: 144, Q8_K: 292}
+TYPE_NAMES = {Q4_0: "q4_0", Q8_0: "q8_0", Q2_K: "q2_K", Q3_K: "q3_K", Q4_K: "q4_K", Q8_K: "q8_K", F16: "f16", F32: "f32"}
+
+OK, ERR_ARG, ERR_TYPE, ERR_SHAPE, ERR_NOMEM, ERR_DEVICE, ERR_HIP = range(7)
+
+_vp, _i64, _sz, _int = C.c_void_p, C.c_int64, C.c_size_t, C.c_int
+
+
+class G4HError(RuntimeError):
+    def __init__(self, status: int, message: str):
+        super().__init__(f"[{status}] {message}")
+        self.status = status
+
+
+# (name, restype, argtypes) for every entry point of include/g4hip.h
+_SIGS = [
+    ("g4h_init", _int, [_int]),
+    ("g4h_last_error", C.c_char_p, []),
+    ("g4h_status_str", C.c_char_p, [_int]),
+    ("g4h_debug_fail_alloc", None, [_int]),
+    ("g4h_malloc", _int, [C.POINTER(_vp), _sz]),
+    ("g4h_free", _int, [_vp]),
+    ("g4h_memcpy_h2d", _int, [_vp, _vp, _sz, _vp]),
+    ("g4h_memcpy_d2h", _int, [_vp, _vp, _sz, _vp]),
+    ("g4h_memcpy_d2d", _int, [_vp, _vp, _sz, _vp]),
+    ("g4h_memset", _int, [_vp, _int, _sz, _vp]),
+    ("g4h_stream_create", _int, [C.POINTER(_vp)]),
+    ("g4h_stream_destroy", _int, [_vp]),
+    ("g4h_stream_synchronize", _int, [_vp]),
+    ("g4h_event_create", _int, [C.POINTER(_vp)]),
+    ("g4h_event_destroy", _int, [_vp]),
+    ("g4h_event_record", _int, [_vp, _vp]),
+    ("g4h_event_elapsed_ms", _int, [C.POINTER(C.c_float), _vp, _vp]),
+    ("g4h_graph_begin", _int, [_vp]),
+    ("g4h_graph_end", _int, [_vp, C.POINTER(_vp)]),
+    ("g4h_graph_launch", _int, [_vp, _vp]),
+    ("g4h_graph_destroy", _int, [_vp]),
+    ("g4h_row_size", _sz, [_int, _i64]),
+    ("g4h_act_type", _int, [_int]),
+    ("g4h_act_stride", _sz, [_int, _i64]),
+    ("g4h_quantize_q8_0", _int, [_vp, _sz, _vp, _sz, _i64, _int, _vp]),
+    ("g4h_quantize_q8_K", _int, [_vp, _sz, _vp, _sz, _i64, _int, _vp]),
+    ("g4h_quantize_q4_0", _int, [_vp, _sz, _vp, _sz, _i64, _int, _vp]),
+    ("g4h_dequant_rows", _int, [_int, _vp, _sz, _vp, _sz, _i64, _int, _vp]),
+    ("g4h_vec_dot", _int, [_int, _vp, _sz, _vp, _i64, _int, _vp, _vp]),
+    ("g4h_tensor_create", _int, [_int, _i64, _i64, C.POINTER(_vp)]),
+    ("g4h_tensor_load", _int, [_vp, _vp, _int, _vp]),
+    ("g4h_tensor_store", _int, [_vp, _vp, _vp]),
+    ("g4h_tensor_free", _int, [_vp]),
+    ("g4h_tensor_bytes", _sz, [_vp]),
+    ("g4h_tensor_info", _int, [_vp, C.POINTER(_int), C.POINTER(_i64), C.POINTER(_i64)]),
+    ("g4h_matmul", _int, [_vp, _vp, _vp, _sz, _vp, _int, _vp]),
+    ("g4h_matmul_ex", _int, [_vp, _vp, _vp, _sz, _vp, _int, _int, _vp]),
+    ("g4h_matmul_path", _int, [_vp, _int]),
+    ("g4h_block_sums", _int, [_vp, _vp, _sz, _int, _vp, _vp]),
+]
+
+_lib = None
+
+
+def exported_names():
+    return [s[0] for s in _SIGS]
+
+
+def lib():
+    """Load libg4hip.so (raises if it has not been built)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise ImportError(f"{LIB_PATH} is missing: run `python -c 'import __graft_entry__ as g; g.build()'` "
+                              "(the HIP library has no CPU fallback)")
+        L = C.CDLL(LIB_PATH)
+        for name, res, args in _SIGS:
+            f = getattr(L, name)
+            f.restype = res
+            f.argtypes = args
+        _lib = L
+    return _lib
+
+
+def check(rc: int) -> None:
+    if rc != OK:
+        raise G4HError(rc, lib().g4h_last_error().decode())
+
+
+_inited = False
+
+
+def init(device: int = 0) -> None:
+    global _inited
+    if not _inited:
+        check(lib().g4h_init(device))
+        _inited = True
+
+
+def row_size(t: int, n: int) -> int:
+    return lib().g4h_row_size(t, n)
+
+
+def act_type(wtype: int) -> int:
+    return lib().g4h_act_type(wtype)
+
+
+def act_stride(wtype: int, ncols: int) -> int:
+    return lib().g4h_act_stride(wtype, ncols)
+
+
+# --------------------------------------------------------------- plumbing
+class Buffer:
+    """A device allocation owned by Python."""
+
+    def __init__(self, nbytes: int):
+        init()
+        p = _vp()
+        check(lib().g4h_malloc(C.byref(p), int(nbytes)))
+        self.ptr = p.value
+        self.nbytes = int(nbytes)
+
+    @classmethod
+    def from_array(cls, a: np.ndarray, stream=None) -> "Buffer":
+        a = np.ascontiguousarray(a)
+        b = cls(a.nbytes)
+        b.upload(a, stream)
+        return b
+
+    def upload(self, a: np.ndarray, stream=None) -> None:
+        a = np.ascontiguousarray(a)
+        assert a.nbytes <= self.nbytes
+        check(lib().g4h_memcpy_h2d(self.ptr, a.ctypes.data_as(_vp), a.nbytes, stream))
+        check(lib().g4h_stream_synchronize(stream))
+
+    def download(self, dtype, shape, offset: int = 0, stream=None) -> np.ndarray:
+        out = np.empty(shape, dtype=dtype)
+        assert offset + out.nbytes <= self.nbytes
+        check(lib().g4h_memcpy_d2h(out.ctypes.data_as(_vp), self.ptr + offset, out.nbytes, stream))
+        return out
+
+    def zero(self, stream=None) -> None:
+        check(lib().g4h_memset(self.ptr, 0, self.nbytes, stream))
+
+    def free(self) -> None:
+        if self.ptr:
+            check(lib().g4h_free(self.ptr))
+            self.ptr = 0
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+def synchronize(stream=None) -> None:
+    check(lib().g4h_stream_synchronize(stream))
+
+
+class Stream:
+    def __init__(self):
+        init()
+        p = _vp()
+        check(lib().g4h_stream_create(C.byref(p)))
+        self.ptr = p.value
+
+    def synchronize(self):
+        check(lib().g4h_stream_synchronize(self.ptr))
+
+
+class Event:
+    def __init__(self):
+        p = _vp()
+        check(lib().g4h_event_create(C.byref(p)))
+        self.ptr = p.value
+
+    def record(self, stream=None):
+        check(lib().g4h_event_record(self.ptr, stream))
+
+    def elapsed_ms(self, end: "Event") -> float:
+        ms = C.c_float()
+        check(lib().g4h_event_elapsed_ms(C.byref(ms), self.ptr, end.ptr))
+        return ms.value
+
+
+class Graph:
+    """Stream capture of a sequence of library calls, replayed with launch()."""
+
+    def __init__(self, stream, fn):
+        check(lib().g4h_graph_begin(stream))
+        try:
+            fn()
+        finally:
+            p = _vp()
+            check(lib().g4h_graph_end(stream, C.byref(p)))
+        self.ptr = p.value
+
+    def launch(self, stream):
+        check(lib().g4h_graph_launch(self.ptr, stream))
+
+    def __del__(self):
+        try:
+            if self.ptr:
+                lib().g4h_graph_destroy(self.ptr)
+        except Exception:
+            pass
+
+
+# ------------------------------------------------------------------ ops
+def quantize(qtype: int, x: Buffer, n: int, rows: int, y: Buffer, x_stride: int = 0, y_stride: int = 0, stream=None) -> None:
+    """g4_quantize_q8_0 / q8_K / q4_0 on device rows."""
+    fn = {Q8_0: lib().g4h_quantize_q8_0, Q8_K: lib().g4h_quantize_q8_K, Q4_0: lib().g4h_quantize_q4_0}[qtype]
+    check(fn(x.ptr if isinstance(x, Buffer) else x, x_stride or n,
+             y.ptr if isinstance(y, Buffer) else y, y_stride or row_size(qtype, n), n, rows, stream))
+
+
+def dequant_rows(qtype: int, x, n: int, rows: int, y, x_stride: int = 0, y_stride: int = 0, stream=None) -> None:
+    check(lib().g4h_dequant_rows(qtype, _p(x), x_stride or row_size(qtype, n), _p(y), y_stride or n, n, rows, stream))
+
+
+def vec_dot(wtype: int, w, a, n: int, rows: int, out, w_stride: int = 0, stream=None) -> None:
+    check(lib().g4h_vec_dot(wtype, _p(w), w_stride or row_size(wtype, n), _p(a), n, rows, _p(out), stream))
+
+
+def _p(x):
+    return x.ptr if isinstance(x, (Buffer, Tensor)) else x
+
+
+class Tensor:
+    """Weight matrix resident in HBM (g4h_tensor)."""
+
+    def __init__(self, qtype: int, ncols: int, nrows: int):
+        init()
+        p = _vp()
+        check(lib().g4h_tensor_create(qtype, ncols, nrows, C.byref(p)))
+        self.ptr = p.value
+        self.type, self.ncols, self.nrows = qtype, ncols, nrows
+
+    @classmethod
+    def from_rows(cls, qtype: int, rows: np.ndarray, ncols: int, stream=None) -> "Tensor":
+        rows = np.ascontiguousarray(rows, dtype=np.uint8)
+        rs = row_size(qtype, ncols)
+        assert rows.size % rs == 0
+        t = cls(qtype, ncols, rows.size // rs)
+        check(lib().g4h_tensor_load(t.ptr, rows.ctypes.data_as(_vp), 0, stream))
+        return t
+
+    def load_device(self, rows_dev, stream=None) -> None:
+        check(lib().g4h_tensor_load(self.ptr, _p(rows_dev), 1, stream))
+
+    def to_rows(self) -> np.ndarray:
+        rs = row_size(self.type, self.ncols)
+        b = Buffer(rs * self.nrows)
+        check(lib().g4h_tensor_store(self.ptr, b.ptr, None))
+        return b.download(np.uint8, (self.nrows, rs))
+
+    @property
+    def nbytes(self) -> int:
+        return lib().g4h_tensor_bytes(self.ptr)
+
+    def free(self):
+        if self.ptr:
+            check(lib().g4h_tensor_free(self.ptr))
+            self.ptr = 0
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+def matmul(W: Tensor, Y, nb: int = 1, x=None, pre=None, pre_stride: int = 0, path: int = 0, stream=None) -> None:
+    """matmul_b: Y[nb][nrows] = W @ act, act from x (fp32, quantized here) or pre."""
+    check(lib().g4h_matmul_ex(W.ptr, _p(x) if x is not None else None, _p(pre) if pre is not None else None,
+                              pre_stride or (act_stride(W.type, W.ncols) if pre is not None else 0),
+                              _p(Y), nb, path, stream))
+
+
+def block_sums(W: Tensor, pre, out, tok: int = 0, pre_stride: int = 0, stream=None) -> None:
+    check(lib().g4h_block_sums(W.ptr, _p(pre), pre_stride or act_stride(W.type, W.ncols), tok, _p(out), stream))
+
+
+def n_block_sums(W: Tensor) -> int:
+    nb = W.ncols // BLCK[W.type]
+    return nb * (2 if W.type in (Q2_K, Q4_K) else 1)

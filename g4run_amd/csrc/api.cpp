@@ -1,0 +1,386 @@
+// api.cpp -- the C ABI declared in include/g4hip.h: validation, status codes,
+// resident-tensor management and dispatch to the gfx950 kernels.
+#include "../../include/g4hip.h"
+
+#include <atomic>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <unordered_map>
+
+#include "kernels.h"
+
+using namespace g4;
+
+// ----------------------------------------------------------- errors ----
+static thread_local char g_err[512] = "";
+
+static int fail(int status, const char *fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof g_err, fmt, ap);
+    va_end(ap);
+    return status;
+}
+static int hip_fail(hipError_t e, const char *what) {
+    return fail(G4H_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+#define G4_HIP(call)                                          \
+    do {                                                      \
+        hipError_t e_ = (call);                               \
+        if (e_ != hipSuccess) return hip_fail(e_, #call);     \
+    } while (0)
+
+static int g_device = -1;
+static std::atomic<int> g_fail_alloc{0};
+
+#define G4_NEED_INIT() \
+    do { if (g_device < 0) return fail(G4H_ERR_DEVICE, "g4h_init() has not been called"); } while (0)
+
+extern "C" const char *g4h_last_error(void) { return g_err; }
+
+extern "C" const char *g4h_status_str(int s) {
+    switch (s) {
+    case G4H_OK: return "ok";
+    case G4H_ERR_ARG: return "invalid argument";
+    case G4H_ERR_TYPE: return "unsupported type";
+    case G4H_ERR_SHAPE: return "invalid shape";
+    case G4H_ERR_NOMEM: return "out of device memory";
+    case G4H_ERR_DEVICE: return "no usable device";
+    case G4H_ERR_HIP: return "HIP runtime error";
+    default: return "unknown status";
+    }
+}
+
+extern "C" void g4h_debug_fail_alloc(int n) { g_fail_alloc.store(n < 0 ? 0 : n); }
+
+extern "C" int g4h_init(int device) {
+    int n = 0;
+    hipError_t e = hipGetDeviceCount(&n);
+    if (e != hipSuccess || n == 0) return fail(G4H_ERR_DEVICE, "no HIP device (%s)", hipGetErrorString(e));
+    if (device < 0 || device >= n) return fail(G4H_ERR_DEVICE, "device %d out of range (%d devices)", device, n);
+    G4_HIP(hipSetDevice(device));
+    hipDeviceProp_t p;
+    G4_HIP(hipGetDeviceProperties(&p, device));
+    if (strncmp(p.gcnArchName, "gfx950", 6) != 0)
+        return fail(G4H_ERR_DEVICE, "device %d is %s; this library is built for gfx950 only", device, p.gcnArchName);
+    g_device = device;
+    return G4H_OK;
+}
+
+// ------------------------------------------------------------ plumbing ----
+static int dev_alloc(void **p, size_t bytes) {
+    if (g_fail_alloc.load() > 0) {
+        g_fail_alloc.fetch_sub(1);
+        *p = nullptr;
+        return fail(G4H_ERR_NOMEM, "device allocation of %zu bytes failed (injected)", bytes);
+    }
+    hipError_t e = hipMalloc(p, bytes ? bytes : 1);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        *p = nullptr;
+        return fail(G4H_ERR_NOMEM, "device allocation of %zu bytes failed: %s", bytes, hipGetErrorString(e));
+    }
+    return G4H_OK;
+}
+
+extern "C" int g4h_malloc(void **ptr, size_t bytes) {
+    G4_NEED_INIT();
+    if (!ptr) return fail(G4H_ERR_ARG, "g4h_malloc: null out pointer");
+    return dev_alloc(ptr, bytes);
+}
+extern "C" int g4h_free(void *ptr) {
+    if (ptr) G4_HIP(hipFree(ptr));
+    return G4H_OK;
+}
+extern "C" int g4h_memcpy_h2d(void *d, const void *s, size_t n, void *st) {
+    G4_HIP(hipMemcpyAsync(d, s, n, hipMemcpyHostToDevice, (hipStream_t)st));
+    return G4H_OK;
+}
+extern "C" int g4h_memcpy_d2h(void *d, const void *s, size_t n, void *st) {
+    G4_HIP(hipMemcpyAsync(d, s, n, hipMemcpyDeviceToHost, (hipStream_t)st));
+    G4_HIP(hipStreamSynchronize((hipStream_t)st));
+    return G4H_OK;
+}
+extern "C" int g4h_memcpy_d2d(void *d, const void *s, size_t n, void *st) {
+    G4_HIP(hipMemcpyAsync(d, s, n, hipMemcpyDeviceToDevice, (hipStream_t)st));
+    return G4H_OK;
+}
+extern "C" int g4h_memset(void *d, int v, size_t n, void *st) {
+    G4_HIP(hipMemsetAsync(d, v, n, (hipStream_t)st));
+    return G4H_OK;
+}
+extern "C" int g4h_stream_create(void **s) {
+    G4_NEED_INIT();
+    G4_HIP(hipStreamCreateWithFlags((hipStream_t *)s, hipStreamNonBlocking));
+    return G4H_OK;
+}
+extern "C" int g4h_stream_destroy(void *s) { G4_HIP(hipStreamDestroy((hipStream_t)s)); return G4H_OK; }
+extern "C" int g4h_stream_synchronize(void *s) { G4_HIP(hipStreamSynchronize((hipStream_t)s)); return G4H_OK; }
+extern "C" int g4h_event_create(void **e) { G4_HIP(hipEventCreate((hipEvent_t *)e)); return G4H_OK; }
+extern "C" int g4h_event_destroy(void *e) { G4_HIP(hipEventDestroy((hipEvent_t)e)); return G4H_OK; }
+extern "C" int g4h_event_record(void *e, void *s) { G4_HIP(hipEventRecord((hipEvent_t)e, (hipStream_t)s)); return G4H_OK; }
+extern "C" int g4h_event_elapsed_ms(float *ms, void *a, void *b) {
+    G4_HIP(hipEventSynchronize((hipEvent_t)b));
+    G4_HIP(hipEventElapsedTime(ms, (hipEvent_t)a, (hipEvent_t)b));
+    return G4H_OK;
+}
+extern "C" int g4h_graph_begin(void *s) {
+    G4_HIP(hipStreamBeginCapture((hipStream_t)s, hipStreamCaptureModeThreadLocal));
+    return G4H_OK;
+}
+extern "C" int g4h_graph_end(void *s, void **exec) {
+    hipGraph_t g;
+    G4_HIP(hipStreamEndCapture((hipStream_t)s, &g));
+    hipError_t e = hipGraphInstantiate((hipGraphExec_t *)exec, g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    if (e != hipSuccess) return hip_fail(e, "hipGraphInstantiate");
+    return G4H_OK;
+}
+extern "C" int g4h_graph_launch(void *exec, void *s) { G4_HIP(hipGraphLaunch((hipGraphExec_t)exec, (hipStream_t)s)); return G4H_OK; }
+extern "C" int g4h_graph_destroy(void *exec) { G4_HIP(hipGraphExecDestroy((hipGraphExec_t)exec)); return G4H_OK; }
+
+// ------------------------------------------------------------- sizes ----
+static bool supported(int t) { return t == Q4_0 || t == Q8_0 || t == Q2_K || t == Q3_K || t == Q4_K; }
+
+extern "C" size_t g4h_row_size(int type, int64_t n) {
+    const int b = blck(type);
+    if (b == 0 || n <= 0 || n % b) return 0;
+    return (size_t)(n / b) * bsize(type);
+}
+extern "C" int g4h_act_type(int wtype) {
+    switch (wtype) {
+    case Q4_0: case Q8_0: return Q8_0;
+    case Q2_K: case Q3_K: case Q4_K: return Q8_K;
+    default: return -1;
+    }
+}
+extern "C" size_t g4h_act_stride(int wtype, int64_t ncols) {
+    const int at = g4h_act_type(wtype);
+    if (at < 0) return 0;
+    const size_t r = g4h_row_size(at, ncols);
+    return (r + 63) & ~(size_t)63;
+}
+
+// Per-stream scratch for activations quantized inside g4h_matmul.  Growth
+// synchronizes that stream first; calls on one stream are ordered, calls on
+// different streams use different buffers.
+static std::mutex g_scratch_mu;
+static std::unordered_map<hipStream_t, std::pair<void *, size_t>> g_scratch;
+
+static int scratch_for(hipStream_t s, size_t bytes, void **out) {
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    auto &e = g_scratch[s];
+    if (e.second < bytes) {
+        if (e.first) {
+            G4_HIP(hipStreamSynchronize(s));
+            G4_HIP(hipFree(e.first));
+            e.first = nullptr;
+            e.second = 0;
+        }
+        const size_t want = bytes < (1u << 20) ? (1u << 20) : bytes;
+        int rc = dev_alloc(&e.first, want);
+        if (rc) return rc;
+        e.second = want;
+    }
+    *out = e.first;
+    return G4H_OK;
+}
+
+// --------------------------------------------------------- quantizers ----
+static int check_q(const char *fn, int qt, const float *x, size_t xs, void *y, size_t ys, int64_t n, int rows) {
+    G4_NEED_INIT();
+    if (!x || !y) return fail(G4H_ERR_ARG, "%s: null pointer", fn);
+    if (rows < 0 || n <= 0) return fail(G4H_ERR_ARG, "%s: bad size n=%lld rows=%d", fn, (long long)n, rows);
+    if (n % blck(qt)) return fail(G4H_ERR_SHAPE, "%s: n=%lld is not a multiple of %d", fn, (long long)n, blck(qt));
+    if (rows > 1 && (xs < (size_t)n || ys < g4h_row_size(qt, n)))
+        return fail(G4H_ERR_ARG, "%s: row strides smaller than a row", fn);
+    if ((uintptr_t)x % 4) return fail(G4H_ERR_ARG, "%s: x must be 4-byte aligned", fn);
+    const size_t ya = qt == Q8_K ? 4 : 2;
+    if ((uintptr_t)y % ya || ys % ya) return fail(G4H_ERR_ARG, "%s: y and y_stride must be %zu-byte aligned", fn, ya);
+    return G4H_OK;
+}
+
+extern "C" int g4h_quantize_q8_0(const float *x, size_t xs, void *y, size_t ys, int64_t n, int rows, void *s) {
+    if (int rc = check_q("g4h_quantize_q8_0", Q8_0, x, xs, y, ys, n, rows)) return rc;
+    if (rows == 0) return G4H_OK;
+    G4_HIP(launch_quantize_q8_0(x, xs, (uint8_t *)y, ys, n, rows, (hipStream_t)s));
+    return G4H_OK;
+}
+extern "C" int g4h_quantize_q8_K(const float *x, size_t xs, void *y, size_t ys, int64_t n, int rows, void *s) {
+    if (int rc = check_q("g4h_quantize_q8_K", Q8_K, x, xs, y, ys, n, rows)) return rc;
+    if (rows == 0) return G4H_OK;
+    G4_HIP(launch_quantize_q8_K(x, xs, (uint8_t *)y, ys, n, rows, (hipStream_t)s));
+    return G4H_OK;
+}
+extern "C" int g4h_quantize_q4_0(const float *x, size_t xs, void *y, size_t ys, int64_t n, int rows, void *s) {
+    if (int rc = check_q("g4h_quantize_q4_0", Q4_0, x, xs, y, ys, n, rows)) return rc;
+    if (rows == 0) return G4H_OK;
+    G4_HIP(launch_quantize_q4_0(x, xs, (uint8_t *)y, ys, n, rows, (hipStream_t)s));
+    return G4H_OK;
+}
+
+extern "C" int g4h_dequant_rows(int type, const void *x, size_t xs, float *y, size_t ys, int64_t n, int rows, void *s) {
+    G4_NEED_INIT();
+    if (!x || !y || n <= 0 || rows < 0) return fail(G4H_ERR_ARG, "g4h_dequant_rows: bad argument");
+    if (!supported(type) && type != F16 && type != F32) return fail(G4H_ERR_TYPE, "g4h_dequant_rows: type %d unsupported", type);
+    if (n % blck(type)) return fail(G4H_ERR_SHAPE, "g4h_dequant_rows: n=%lld not a multiple of %d", (long long)n, blck(type));
+    if (rows == 0) return G4H_OK;
+    G4_HIP(launch_dequant(type, (const uint8_t *)x, xs, y, ys, n, rows, (hipStream_t)s));
+    return G4H_OK;
+}
+
+extern "C" int g4h_vec_dot(int wtype, const void *w, size_t ws, const void *a, int64_t n, int rows, float *out, void *s) {
+    G4_NEED_INIT();
+    if (!w || !a || !out || n <= 0 || rows < 0) return fail(G4H_ERR_ARG, "g4h_vec_dot: bad argument");
+    if (!supported(wtype)) return fail(G4H_ERR_TYPE, "g4h_vec_dot: weight type %d unsupported", wtype);
+    if (n % blck(wtype)) return fail(G4H_ERR_SHAPE, "g4h_vec_dot: n=%lld not a multiple of %d", (long long)n, blck(wtype));
+    if ((uintptr_t)a % 4) return fail(G4H_ERR_ARG, "g4h_vec_dot: activation must be 4-byte aligned");
+    if (rows > 1 && ws < g4h_row_size(wtype, n)) return fail(G4H_ERR_ARG, "g4h_vec_dot: row stride smaller than a row");
+    if (gemv_lds_bytes(wtype, 1, n / blck(wtype)) > 65536) return fail(G4H_ERR_SHAPE, "g4h_vec_dot: row too long");
+    if (rows == 0) return G4H_OK;
+    G4_HIP(launch_vec_dot_raw(wtype, (const uint8_t *)w, ws, (const uint8_t *)a, n, rows, out, (hipStream_t)s));
+    return G4H_OK;
+}
+
+// ------------------------------------------------------------ tensors ----
+static size_t al256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+extern "C" int g4h_tensor_create(int type, int64_t ncols, int64_t nrows, g4h_tensor **out) {
+    G4_NEED_INIT();
+    if (!out) return fail(G4H_ERR_ARG, "g4h_tensor_create: null out");
+    *out = nullptr;
+    if (!supported(type)) return fail(G4H_ERR_TYPE, "g4h_tensor_create: type %d unsupported", type);
+    if (ncols <= 0 || nrows <= 0) return fail(G4H_ERR_ARG, "g4h_tensor_create: empty shape");
+    if (ncols % blck(type)) return fail(G4H_ERR_SHAPE, "g4h_tensor_create: ncols=%lld not a multiple of %d", (long long)ncols, blck(type));
+    const int64_t nb = ncols / blck(type);
+    if (gemv_lds_bytes(type, 1, nb) > 65536) return fail(G4H_ERR_SHAPE, "g4h_tensor_create: ncols=%lld exceeds the supported row length", (long long)ncols);
+    const size_t n = (size_t)(nrows * nb);
+    size_t qs = 0, sc = 0, ex = 0, dd = 0;
+    switch (type) {
+    case Q8_0: qs = n * 32; sc = n * 2; break;
+    case Q4_0: qs = n * 16; sc = n * 2; break;
+    case Q4_K: qs = n * 144; break;
+    case Q2_K: qs = n * 64; sc = n * 16; ex = n * 4; break;
+    case Q3_K: qs = n * 64; ex = n * 32; sc = n * 12; dd = n * 2; break;
+    }
+    const size_t total = al256(qs) + al256(sc) + al256(ex) + al256(dd);
+    g4h_tensor *t = new g4h_tensor();
+    t->type = type; t->ncols = ncols; t->nrows = nrows; t->nb = nb;
+    void *base = nullptr;
+    if (int rc = dev_alloc(&base, total)) { delete t; return rc; }
+    t->base = (uint8_t *)base;
+    t->bytes = total;
+    t->qs = t->base;
+    t->sc = t->qs + al256(qs);
+    t->ex = t->sc + al256(sc);
+    t->dd = t->ex + al256(ex);
+    *out = t;
+    return G4H_OK;
+}
+
+extern "C" int g4h_tensor_load(g4h_tensor *t, const void *rows, int src_is_device, void *s) {
+    G4_NEED_INIT();
+    if (!t || !rows) return fail(G4H_ERR_ARG, "g4h_tensor_load: null pointer");
+    const size_t bytes = (size_t)t->nrows * g4h_row_size(t->type, t->ncols);
+    const hipStream_t st = (hipStream_t)s;
+    if (src_is_device) {
+        G4_HIP(launch_repack(*t, (const uint8_t *)rows, st));
+        return G4H_OK;
+    }
+    void *tmp = nullptr;
+    if (int rc = dev_alloc(&tmp, bytes)) return rc;
+    hipError_t e = hipMemcpyAsync(tmp, rows, bytes, hipMemcpyHostToDevice, st);
+    if (e == hipSuccess) e = launch_repack(*t, (const uint8_t *)tmp, st);
+    if (e == hipSuccess) e = hipStreamSynchronize(st);
+    (void)hipFree(tmp);
+    if (e != hipSuccess) return hip_fail(e, "g4h_tensor_load");
+    return G4H_OK;
+}
+
+extern "C" int g4h_tensor_store(const g4h_tensor *t, void *rows_dev, void *s) {
+    G4_NEED_INIT();
+    if (!t || !rows_dev) return fail(G4H_ERR_ARG, "g4h_tensor_store: null pointer");
+    G4_HIP(launch_unpack(*t, (uint8_t *)rows_dev, (hipStream_t)s));
+    return G4H_OK;
+}
+
+extern "C" int g4h_tensor_free(g4h_tensor *t) {
+    if (!t) return G4H_OK;
+    hipError_t e = hipFree(t->base);
+    delete t;
+    if (e != hipSuccess) return hip_fail(e, "g4h_tensor_free");
+    return G4H_OK;
+}
+extern "C" size_t g4h_tensor_bytes(const g4h_tensor *t) { return t ? t->bytes : 0; }
+extern "C" int g4h_tensor_info(const g4h_tensor *t, int *type, int64_t *ncols, int64_t *nrows) {
+    if (!t) return fail(G4H_ERR_ARG, "g4h_tensor_info: null tensor");
+    if (type) *type = t->type;
+    if (ncols) *ncols = t->ncols;
+    if (nrows) *nrows = t->nrows;
+    return G4H_OK;
+}
+
+// ------------------------------------------------------------- matmul ----
+static constexpr size_t kMaxLds = 65536;
+
+extern "C" int g4h_matmul_path(const g4h_tensor *W, int nb) {
+    (void)W;
+    return nb <= 8 ? 1 : 1;
+}
+
+static int check_act(const char *fn, const g4h_tensor *W, const void *pre, size_t stride, int nb) {
+    if ((uintptr_t)pre % 4 || stride % 4) return fail(G4H_ERR_ARG, "%s: activations must be 4-byte aligned with a 4-byte multiple stride", fn);
+    if (nb > 1 && stride < g4h_row_size(g4h_act_type(W->type), W->ncols))
+        return fail(G4H_ERR_ARG, "%s: activation stride %zu smaller than a row", fn, stride);
+    return G4H_OK;
+}
+
+extern "C" int g4h_matmul_ex(const g4h_tensor *W, const float *x, const void *pre, size_t pre_stride, float *Y, int nb,
+                             int path, void *stream) {
+    G4_NEED_INIT();
+    if (!W || !Y) return fail(G4H_ERR_ARG, "g4h_matmul: null tensor or output");
+    if ((x == nullptr) == (pre == nullptr)) return fail(G4H_ERR_ARG, "g4h_matmul: pass exactly one of x_dev and pre_dev");
+    if (nb < 0) return fail(G4H_ERR_ARG, "g4h_matmul: nb=%d", nb);
+    if (path < 0 || path > 2) return fail(G4H_ERR_ARG, "g4h_matmul: path=%d", path);
+    if (nb == 0) return G4H_OK;
+    const hipStream_t s = (hipStream_t)stream;
+    const uint8_t *act = (const uint8_t *)pre;
+    size_t stride = pre_stride;
+    if (x) {
+        if ((uintptr_t)x % 4) return fail(G4H_ERR_ARG, "g4h_matmul: x must be 4-byte aligned");
+        stride = g4h_act_stride(W->type, W->ncols);
+        void *buf;
+        if (int rc = scratch_for(s, stride * nb, &buf)) return rc;
+        const hipError_t e = g4h_act_type(W->type) == Q8_0
+                                 ? launch_quantize_q8_0(x, W->ncols, (uint8_t *)buf, stride, W->ncols, nb, s)
+                                 : launch_quantize_q8_K(x, W->ncols, (uint8_t *)buf, stride, W->ncols, nb, s);
+        if (e != hipSuccess) return hip_fail(e, "g4h_matmul: quantize");
+        act = (const uint8_t *)buf;
+    } else if (int rc = check_act("g4h_matmul", W, pre, pre_stride, nb)) {
+        return rc;
+    }
+    // GEMV family in token chunks of 8/4/2/1 that fit the LDS budget
+    int done = 0;
+    while (done < nb) {
+        int chunk = 8;
+        while (chunk > nb - done || (chunk > 1 && gemv_lds_bytes(W->type, chunk, W->nb) > kMaxLds)) chunk >>= 1;
+        const hipError_t e = launch_gemv(*W, act + (size_t)done * stride, stride, Y + (size_t)done * W->nrows, chunk, s);
+        if (e != hipSuccess) return hip_fail(e, "g4h_matmul: gemv launch");
+        done += chunk;
+    }
+    return G4H_OK;
+}
+
+extern "C" int g4h_matmul(const g4h_tensor *W, const float *x, const void *pre, size_t pre_stride, float *Y, int nb, void *s) {
+    return g4h_matmul_ex(W, x, pre, pre_stride, Y, nb, 0, s);
+}
+
+extern "C" int g4h_block_sums(const g4h_tensor *W, const void *pre, size_t pre_stride, int tok, int32_t *sums, void *s) {
+    G4_NEED_INIT();
+    if (!W || !pre || !sums || tok < 0) return fail(G4H_ERR_ARG, "g4h_block_sums: bad argument");
+    if (int rc = check_act("g4h_block_sums", W, pre, pre_stride, tok + 1)) return rc;
+    G4_HIP(launch_block_sums(*W, (const uint8_t *)pre, pre_stride, tok, sums, (hipStream_t)s));
+    return G4H_OK;
+}

@@ -1,0 +1,320 @@
+// formats.h -- per-format "unit" arithmetic of the quantized dots.
+//
+// A unit is the piece of one weight row a single lane handles:
+//   q8_0 / q4_0 : one 32-element block;
+//   q2_K / q3_K / q4_K : a quarter of a 256-element superblock (64 elements).
+// Each format provides
+//   Frag              registers holding one unit's weight bytes,
+//   load(...)         the unit's global loads from the resident layout,
+//   isums(...)        the exact integer sums of the unit against one token's
+//                     activation held in LDS (the integers the reference
+//                     scales, quants.c:535-762),
+//   accum(...)        acc + those sums times their scales (fp32).
+// The GEMV, the block-sum instrument and the raw-row vec_dot all go through
+// these functions, so the integers checked bit-exactly by the tests are the
+// ones the fast path scales.
+#pragma once
+
+#include "common.h"
+
+namespace g4 {
+
+// ---------------------------------------------------------------- LDS act --
+// Activation of NB tokens staged in LDS.
+// q8_0 act (blocks of 32): per token t: Q0[nb] int4 (qs 0..15), Q1[nb] int4
+// (qs 16..31), D[nb] float (fp16 d widened), S[nb] int (sum of qs).
+// q8_K act (superblocks of 256): per token t: QK[nb][256] int8, DK[nb] float,
+// BS[nb][16] int16.
+struct ActQ8_0 {
+    static __host__ __device__ size_t bytes_per_token(int nb) { return ((size_t)nb * 40 + 15) & ~(size_t)15; }
+    int4 *q0, *q1; float *d; int *s;
+    __device__ ActQ8_0(uint8_t *base, int nb, int t) {
+        uint8_t *p = base + (size_t)t * bytes_per_token(nb);
+        q0 = (int4 *)p; q1 = q0 + nb; d = (float *)(q1 + nb); s = (int *)(d + nb);
+    }
+};
+struct ActQ8_K {
+    static __host__ __device__ size_t bytes_per_token(int nb) { return ((size_t)nb * (256 + 4 + 32) + 15) & ~(size_t)15; }
+    int8_t *q; float *d; int16_t *bs;
+    __device__ ActQ8_K(uint8_t *base, int nb, int t) {
+        uint8_t *p = base + (size_t)t * bytes_per_token(nb);
+        q = (int8_t *)p; d = (float *)(q + (size_t)nb * 256); bs = (int16_t *)(d + nb);
+    }
+};
+
+// Stage NB tokens of GGUF q8_0 activation rows (act_stride bytes apart, 4-B
+// aligned) into LDS.  Pairs of blocks are 68 B = 17 aligned dwords.
+template <int NB>
+__device__ void stage_q8_0(uint8_t *lds, const uint8_t *act, size_t stride, int nb) {
+    const int npair = nb >> 1;
+    for (int i = threadIdx.x; i < NB * npair; i += blockDim.x) {
+        const int t = i / npair, pr = i - t * npair;
+        const uint32_t *src = (const uint32_t *)(act + (size_t)t * stride + (size_t)pr * 68);
+        uint32_t v[17];
+#pragma unroll
+        for (int k = 0; k < 17; k++) v[k] = src[k];
+        ActQ8_0 A(lds, nb, t);
+        const int b = 2 * pr;
+        int4 a0, a1;
+        a0.x = __builtin_amdgcn_alignbyte(v[1], v[0], 2); a0.y = __builtin_amdgcn_alignbyte(v[2], v[1], 2);
+        a0.z = __builtin_amdgcn_alignbyte(v[3], v[2], 2); a0.w = __builtin_amdgcn_alignbyte(v[4], v[3], 2);
+        a1.x = __builtin_amdgcn_alignbyte(v[5], v[4], 2); a1.y = __builtin_amdgcn_alignbyte(v[6], v[5], 2);
+        a1.z = __builtin_amdgcn_alignbyte(v[7], v[6], 2); a1.w = __builtin_amdgcn_alignbyte(v[8], v[7], 2);
+        A.q0[b] = a0; A.q1[b] = a1; A.d[b] = h2f((uint16_t)(v[0] & 0xffff));
+        int s = 0;
+        s = dot4(a0.x, 0x01010101, s); s = dot4(a0.y, 0x01010101, s); s = dot4(a0.z, 0x01010101, s); s = dot4(a0.w, 0x01010101, s);
+        s = dot4(a1.x, 0x01010101, s); s = dot4(a1.y, 0x01010101, s); s = dot4(a1.z, 0x01010101, s); s = dot4(a1.w, 0x01010101, s);
+        A.s[b] = s;
+        int4 c0 = make_int4(v[9], v[10], v[11], v[12]), c1 = make_int4(v[13], v[14], v[15], v[16]);
+        A.q0[b + 1] = c0; A.q1[b + 1] = c1; A.d[b + 1] = h2f((uint16_t)(v[8] >> 16));
+        s = 0;
+        s = dot4(c0.x, 0x01010101, s); s = dot4(c0.y, 0x01010101, s); s = dot4(c0.z, 0x01010101, s); s = dot4(c0.w, 0x01010101, s);
+        s = dot4(c1.x, 0x01010101, s); s = dot4(c1.y, 0x01010101, s); s = dot4(c1.z, 0x01010101, s); s = dot4(c1.w, 0x01010101, s);
+        A.s[b + 1] = s;
+    }
+    if (nb & 1) {   // odd block count: last block with 16-bit loads
+        for (int t = threadIdx.x; t < NB; t += blockDim.x) {
+            const uint16_t *src = (const uint16_t *)(act + (size_t)t * stride + (size_t)(nb - 1) * 34);
+            uint32_t w[8];
+#pragma unroll
+            for (int k = 0; k < 8; k++) w[k] = (uint32_t)src[1 + 2 * k] | ((uint32_t)src[2 + 2 * k] << 16);
+            ActQ8_0 A(lds, nb, t);
+            int4 a0 = make_int4(w[0], w[1], w[2], w[3]), a1 = make_int4(w[4], w[5], w[6], w[7]);
+            A.q0[nb - 1] = a0; A.q1[nb - 1] = a1; A.d[nb - 1] = h2f(src[0]);
+            int s = 0;
+#pragma unroll
+            for (int k = 0; k < 8; k++) s = dot4(w[k], 0x01010101, s);
+            A.s[nb - 1] = s;
+        }
+    }
+}
+
+// Stage NB tokens of GGUF q8_K rows (292-B superblocks, dword aligned).
+template <int NB>
+__device__ void stage_q8_K(uint8_t *lds, const uint8_t *act, size_t stride, int nb) {
+    const int per = nb * 73;
+    for (int i = threadIdx.x; i < NB * per; i += blockDim.x) {
+        const int t = i / per, r = i - t * per, sb = r / 73, w = r - sb * 73;
+        const uint32_t v = ((const uint32_t *)(act + (size_t)t * stride))[r];
+        ActQ8_K A(lds, nb, t);
+        if (w == 0) A.d[sb] = __builtin_bit_cast(float, v);
+        else if (w <= 64) ((uint32_t *)(A.q + (size_t)sb * 256))[w - 1] = v;
+        else ((uint32_t *)(A.bs + (size_t)sb * 16))[w - 65] = v;
+    }
+}
+
+// ------------------------------------------------------------------ q8_0 --
+struct FQ8_0 {
+    static constexpr int type = Q8_0;
+    using Act = ActQ8_0;
+    static constexpr int units_per_block = 1;
+    struct Frag { int4 w0, w1; uint16_t d; };
+    static __device__ __forceinline__ void load(Frag &f, const g4h_tensor &W, int64_t row, int u) {
+        const size_t j = (size_t)row * W.nb + u;
+        const uint8_t *q = W.qs + j * 32;
+        f.w0 = ld4(q); f.w1 = ld4(q + 16);
+        f.d = ((const uint16_t *)W.sc)[j];
+    }
+    static __device__ __forceinline__ int isum(const Frag &f, const Act &A, int u) {
+        const int4 a0 = A.q0[u], a1 = A.q1[u];
+        int s = dot4(f.w0.x, a0.x, 0);
+        s = dot4(f.w0.y, a0.y, s); s = dot4(f.w0.z, a0.z, s); s = dot4(f.w0.w, a0.w, s);
+        s = dot4(f.w1.x, a1.x, s); s = dot4(f.w1.y, a1.y, s); s = dot4(f.w1.z, a1.z, s); s = dot4(f.w1.w, a1.w, s);
+        return s;
+    }
+    // block value: float(sumi) * (d_w * d_a), accumulated with one fma as the
+    // reference's per-block step (quants.c:992,996)
+    static __device__ __forceinline__ float accum(const Frag &f, const Act &A, int u, float acc) {
+        return __builtin_fmaf(h2f(f.d) * A.d[u], (float)isum(f, A, u), acc);
+    }
+    static constexpr int nsums = 1;
+    static __device__ __forceinline__ void sums(const Frag &f, const Act &A, int u, int *out) { out[0] = isum(f, A, u); }
+};
+
+// ------------------------------------------------------------------ q4_0 --
+// Elements j<16 are the low nibbles of qs[j], j>=16 the high nibbles of
+// qs[j-16] (quants.c:364-371); value q-8.  sum (q-8)*a = sum q*a - 8*sum a.
+struct FQ4_0 {
+    static constexpr int type = Q4_0;
+    using Act = ActQ8_0;
+    static constexpr int units_per_block = 1;
+    struct Frag { int4 w; uint16_t d; };
+    static __device__ __forceinline__ void load(Frag &f, const g4h_tensor &W, int64_t row, int u) {
+        const size_t j = (size_t)row * W.nb + u;
+        f.w = ld4(W.qs + j * 16);
+        f.d = ((const uint16_t *)W.sc)[j];
+    }
+    static __device__ __forceinline__ int isum(const Frag &f, const Act &A, int u) {
+        const int m = 0x0F0F0F0F;
+        const int4 a0 = A.q0[u], a1 = A.q1[u];
+        const uint32_t x = f.w.x, y = f.w.y, z = f.w.z, w = f.w.w;
+        int s = dot4(x & m, a0.x, 0);
+        s = dot4(y & m, a0.y, s); s = dot4(z & m, a0.z, s); s = dot4(w & m, a0.w, s);
+        s = dot4((x >> 4) & m, a1.x, s); s = dot4((y >> 4) & m, a1.y, s);
+        s = dot4((z >> 4) & m, a1.z, s); s = dot4((w >> 4) & m, a1.w, s);
+        return s - 8 * A.s[u];
+    }
+    static __device__ __forceinline__ float accum(const Frag &f, const Act &A, int u, float acc) {
+        return __builtin_fmaf(h2f(f.d) * A.d[u], (float)isum(f, A, u), acc);
+    }
+    static constexpr int nsums = 1;
+    static __device__ __forceinline__ void sums(const Frag &f, const Act &A, int u, int *out) { out[0] = isum(f, A, u); }
+};
+
+// ------------------------------------------------------------------ q4_K --
+// Part p of a superblock covers elements 64p..64p+63: low nibbles of
+// qs[32p..32p+31] (sub-block 2p) and their high nibbles (sub-block 2p+1)
+// (quants.c:479-495).  6-bit (scale,min) pairs per quants.c:417-423.
+struct FQ4_K {
+    static constexpr int type = Q4_K;
+    using Act = ActQ8_K;
+    static constexpr int units_per_block = 4;
+    struct Frag { int4 h, q0, q1; };
+    static __device__ __forceinline__ void load(Frag &f, const g4h_tensor &W, int64_t row, int u) {
+        const uint8_t *b = W.qs + ((size_t)row * W.nb + (u >> 2)) * 144;
+        const int p = u & 3;
+        f.h = ld4(b);
+        f.q0 = ld4(b + 16 + 32 * p); f.q1 = ld4(b + 32 + 32 * p);
+    }
+    static __device__ __forceinline__ uint32_t sbyte(const Frag &f, int k) {   // scales[k], k < 12
+        const uint32_t w = k < 4 ? (uint32_t)f.h.y : k < 8 ? (uint32_t)f.h.z : (uint32_t)f.h.w;
+        return (w >> (8 * (k & 3))) & 0xff;
+    }
+    static __device__ __forceinline__ void scale_min(const Frag &f, int j, int &sc, int &mn) {
+        if (j < 4) { sc = sbyte(f, j) & 63; mn = sbyte(f, j + 4) & 63; }
+        else { sc = (sbyte(f, j + 4) & 15) | ((sbyte(f, j - 4) >> 6) << 4); mn = (sbyte(f, j + 4) >> 4) | ((sbyte(f, j) >> 6) << 4); }
+    }
+    static __device__ __forceinline__ void isums(const Frag &f, const Act &A, int u, int &is, int &ms) {
+        const int sb = u >> 2, p = u & 3, m = 0x0F0F0F0F;
+        const int4 *a = (const int4 *)(A.q + (size_t)sb * 256 + 64 * p);
+        const int4 l0 = a[0], l1 = a[1], h0 = a[2], h1 = a[3];
+        const uint32_t w[8] = {(uint32_t)f.q0.x, (uint32_t)f.q0.y, (uint32_t)f.q0.z, (uint32_t)f.q0.w,
+                               (uint32_t)f.q1.x, (uint32_t)f.q1.y, (uint32_t)f.q1.z, (uint32_t)f.q1.w};
+        int sl = dot4(w[0] & m, l0.x, 0);
+        sl = dot4(w[1] & m, l0.y, sl); sl = dot4(w[2] & m, l0.z, sl); sl = dot4(w[3] & m, l0.w, sl);
+        sl = dot4(w[4] & m, l1.x, sl); sl = dot4(w[5] & m, l1.y, sl); sl = dot4(w[6] & m, l1.z, sl); sl = dot4(w[7] & m, l1.w, sl);
+        int sh = dot4((w[0] >> 4) & m, h0.x, 0);
+        sh = dot4((w[1] >> 4) & m, h0.y, sh); sh = dot4((w[2] >> 4) & m, h0.z, sh); sh = dot4((w[3] >> 4) & m, h0.w, sh);
+        sh = dot4((w[4] >> 4) & m, h1.x, sh); sh = dot4((w[5] >> 4) & m, h1.y, sh); sh = dot4((w[6] >> 4) & m, h1.z, sh); sh = dot4((w[7] >> 4) & m, h1.w, sh);
+        int sc0, m0, sc1, m1;
+        scale_min(f, 2 * p, sc0, m0);
+        scale_min(f, 2 * p + 1, sc1, m1);
+        const int16_t *bs = A.bs + (size_t)sb * 16 + 4 * p;
+        is = sc0 * sl + sc1 * sh;
+        ms = m0 * (bs[0] + bs[1]) + m1 * (bs[2] + bs[3]);
+    }
+    // superblock value d_a*(d_w*isum - dmin_w*msum) (quants.c:744-758), spread
+    // over the four parts
+    static __device__ __forceinline__ float accum(const Frag &f, const Act &A, int u, float acc) {
+        int is, ms; isums(f, A, u, is, ms);
+        const float da = A.d[u >> 2];
+        const uint32_t dd = (uint32_t)f.h.x;
+        acc = __builtin_fmaf(da * h2f((uint16_t)(dd & 0xffff)), (float)is, acc);
+        return __builtin_fmaf(-da * h2f((uint16_t)(dd >> 16)), (float)ms, acc);
+    }
+    static constexpr int nsums = 2;
+    static __device__ __forceinline__ void sums(const Frag &f, const Act &A, int u, int *out) { isums(f, A, u, out[0], out[1]); }
+};
+
+// ------------------------------------------------------------------ q2_K --
+// Element e = 128h + 32j + 16k + l sits in byte qs[32h + 16k + l] at shift 2j,
+// scale byte scales[8h + 2j + k] (low nibble scale, high nibble min)
+// (quants.c:425-445).  Part p = 2h + k holds 16 quant bytes covering four
+// 16-element groups j = 0..3.
+struct FQ2_K {
+    static constexpr int type = Q2_K;
+    using Act = ActQ8_K;
+    static constexpr int units_per_block = 4;
+    struct Frag { int4 q, s; uint32_t dd; };
+    static __device__ __forceinline__ void load(Frag &f, const g4h_tensor &W, int64_t row, int u) {
+        const size_t j = (size_t)row * W.nb + (u >> 2);
+        f.q = ld4(W.qs + j * 64 + 16 * (u & 3));
+        f.s = ld4(W.sc + j * 16);
+        f.dd = ((const uint32_t *)W.ex)[j];
+    }
+    static __device__ __forceinline__ void isums(const Frag &f, const Act &A, int u, int &is, int &ms) {
+        const int sb = u >> 2, p = u & 3, h = p >> 1, k = p & 1;
+        const uint32_t w[4] = {(uint32_t)f.q.x, (uint32_t)f.q.y, (uint32_t)f.q.z, (uint32_t)f.q.w};
+        const uint32_t sw[4] = {(uint32_t)f.s.x, (uint32_t)f.s.y, (uint32_t)f.s.z, (uint32_t)f.s.w};
+        const int8_t *aq = A.q + (size_t)sb * 256 + 128 * h + 16 * k;
+        const int16_t *bs = A.bs + (size_t)sb * 16;
+        int isum = 0, msum = 0;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int4 a = *(const int4 *)(aq + 32 * j);
+            int s = dot4((w[0] >> (2 * j)) & 0x03030303, a.x, 0);
+            s = dot4((w[1] >> (2 * j)) & 0x03030303, a.y, s);
+            s = dot4((w[2] >> (2 * j)) & 0x03030303, a.z, s);
+            s = dot4((w[3] >> (2 * j)) & 0x03030303, a.w, s);
+            const int g = 8 * h + 2 * j + k;                       // 16-element group / scale index
+            const int sc = (sw[g >> 2] >> (8 * (g & 3))) & 0xff;
+            isum += (sc & 15) * s;
+            msum += (sc >> 4) * bs[g];
+        }
+        is = isum; ms = msum;
+    }
+    static __device__ __forceinline__ float accum(const Frag &f, const Act &A, int u, float acc) {
+        int is, ms; isums(f, A, u, is, ms);
+        const float da = A.d[u >> 2];
+        acc = __builtin_fmaf(da * h2f((uint16_t)(f.dd & 0xffff)), (float)is, acc);
+        return __builtin_fmaf(-da * h2f((uint16_t)(f.dd >> 16)), (float)ms, acc);
+    }
+    static constexpr int nsums = 2;
+    static __device__ __forceinline__ void sums(const Frag &f, const Act &A, int u, int *out) { isums(f, A, u, out[0], out[1]); }
+};
+
+// ------------------------------------------------------------------ q3_K --
+// Element e = 128h + 32j + 16k + l: low bits (qs[32h+16k+l] >> 2j) & 3, high
+// bit hmask[16k+l] bit (4h+j); value low - 4 when the high bit is clear
+// (quants.c:447-477).  6-bit scales biased by 32: low nibbles from
+// scales[0..7], high 2 bits from scales[8..11] (quants.c:456-461).
+// q3 = (low | hbit<<2) - 4, so sum q3*a = sum t*a - 4*bsum of the group.
+struct FQ3_K {
+    static constexpr int type = Q3_K;
+    using Act = ActQ8_K;
+    static constexpr int units_per_block = 4;
+    struct Frag { int4 q, hm; uint32_t s0, s1, s2; uint16_t d; };
+    static __device__ __forceinline__ void load(Frag &f, const g4h_tensor &W, int64_t row, int u) {
+        const size_t j = (size_t)row * W.nb + (u >> 2);
+        const int p = u & 3;
+        f.q = ld4(W.qs + j * 64 + 16 * p);
+        f.hm = ld4(W.ex + j * 32 + 16 * (p & 1));
+        const uint32_t *s = (const uint32_t *)(W.sc + j * 12);
+        f.s0 = s[0]; f.s1 = s[1]; f.s2 = s[2];
+        f.d = ((const uint16_t *)W.dd)[j];
+    }
+    static __device__ __forceinline__ int scale(const Frag &f, int i) {   // signed 6-bit scale i < 16
+        const uint32_t lo_w = (i & 7) < 4 ? f.s0 : f.s1;
+        const int lo = (lo_w >> (8 * (i & 3) + (i >= 8 ? 4 : 0))) & 15;
+        const int hi = (f.s2 >> (8 * (i & 3) + 2 * (i >> 2))) & 3;
+        return (lo | (hi << 4)) - 32;
+    }
+    static __device__ __forceinline__ int isum(const Frag &f, const Act &A, int u) {
+        const int sb = u >> 2, p = u & 3, h = p >> 1, k = p & 1;
+        const uint32_t w[4] = {(uint32_t)f.q.x, (uint32_t)f.q.y, (uint32_t)f.q.z, (uint32_t)f.q.w};
+        const uint32_t hb[4] = {(uint32_t)f.hm.x, (uint32_t)f.hm.y, (uint32_t)f.hm.z, (uint32_t)f.hm.w};
+        const int8_t *aq = A.q + (size_t)sb * 256 + 128 * h + 16 * k;
+        const int16_t *bs = A.bs + (size_t)sb * 16;
+        int total = 0;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int4 a = *(const int4 *)(aq + 32 * j);
+            const int sh = 4 * h + j;
+            int s = 0;
+            s = dot4(((w[0] >> (2 * j)) & 0x03030303) | (((hb[0] >> sh) & 0x01010101) << 2), a.x, s);
+            s = dot4(((w[1] >> (2 * j)) & 0x03030303) | (((hb[1] >> sh) & 0x01010101) << 2), a.y, s);
+            s = dot4(((w[2] >> (2 * j)) & 0x03030303) | (((hb[2] >> sh) & 0x01010101) << 2), a.z, s);
+            s = dot4(((w[3] >> (2 * j)) & 0x03030303) | (((hb[3] >> sh) & 0x01010101) << 2), a.w, s);
+            const int g = 8 * h + 2 * j + k;
+            total += scale(f, g) * (s - 4 * bs[g]);
+        }
+        return total;
+    }
+    static __device__ __forceinline__ float accum(const Frag &f, const Act &A, int u, float acc) {
+        return __builtin_fmaf(A.d[u >> 2] * h2f(f.d), (float)isum(f, A, u), acc);
+    }
+    static constexpr int nsums = 1;
+    static __device__ __forceinline__ void sums(const Frag &f, const Act &A, int u, int *out) { out[0] = isum(f, A, u); }
+};
+
+}  // namespace g4

@@ -1,0 +1,25 @@
+// kernels.h -- host-side launchers of the gfx950 kernels (internal).
+#pragma once
+
+#include "common.h"
+
+namespace g4 {
+
+// k_quant.hip
+hipError_t launch_quantize_q8_0(const float *x, size_t xs, uint8_t *y, size_t ys, int64_t n, int rows, hipStream_t s);
+hipError_t launch_quantize_q8_K(const float *x, size_t xs, uint8_t *y, size_t ys, int64_t n, int rows, hipStream_t s);
+hipError_t launch_quantize_q4_0(const float *x, size_t xs, uint8_t *y, size_t ys, int64_t n, int rows, hipStream_t s);
+hipError_t launch_dequant(int type, const uint8_t *x, size_t xs, float *y, size_t ys, int64_t n, int rows, hipStream_t s);
+hipError_t launch_repack(const g4h_tensor &t, const uint8_t *rows, hipStream_t s);
+hipError_t launch_unpack(const g4h_tensor &t, uint8_t *rows, hipStream_t s);
+hipError_t launch_vec_dot_raw(int wtype, const uint8_t *w, size_t ws, const uint8_t *a, int64_t n, int rows, float *out,
+                              hipStream_t s);
+
+// k_gemv.hip
+void gemv_shape(int type, int64_t nblk, int *lpr, int *upl);
+size_t gemv_lds_bytes(int type, int nb_tokens, int64_t nblk);
+hipError_t launch_gemv(const g4h_tensor &W, const uint8_t *act, size_t stride, float *Y, int nb, hipStream_t s);
+hipError_t launch_block_sums(const g4h_tensor &W, const uint8_t *act, size_t stride, int tok, int32_t *out, hipStream_t s);
+int block_sums_per_block(int type);
+
+}  // namespace g4

@@ -1,0 +1,147 @@
+/*
+ * g4hip.h -- C ABI of the MI355X (gfx950) quantized weight x activation path.
+ *
+ * This is the drop-in boundary for the hot path of the reference's g4run
+ * (a GGUF CPU inference engine).  Every entry point below names the reference
+ * interface it replaces.  Conventions:
+ *   - plain C, opaque handles, pointers and sizes only; `stream` is a
+ *     hipStream_t passed as void* (NULL = the null stream);
+ *   - all tensors/activations named *_dev live in device memory;
+ *   - every call returns an int status (G4H_OK == 0) and never exits the
+ *     process (the reference's g4_dequant_row calls exit(1), quants.c:529);
+ *     g4h_last_error() gives a message for the calling thread;
+ *   - calls are stream-ordered and asynchronous unless stated otherwise;
+ *   - block types and ids are the GGUF/ggml ones of g4run.h:80-118.
+ */
+#ifndef G4HIP_H
+#define G4HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Type ids: identical to enum g4_type, g4run.h:80-94 (Q8_K is ggml's id 15,
+ * used by the reference only as the K-quant activation format). */
+enum {
+    G4H_F32 = 0, G4H_F16 = 1, G4H_Q4_0 = 2, G4H_Q8_0 = 8,
+    G4H_Q2_K = 10, G4H_Q3_K = 11, G4H_Q4_K = 12, G4H_Q8_K = 15
+};
+
+enum {
+    G4H_OK = 0,
+    G4H_ERR_ARG = 1,      /* null pointer, bad size, bad stride           */
+    G4H_ERR_TYPE = 2,     /* type not supported on this path              */
+    G4H_ERR_SHAPE = 3,    /* n not a multiple of the block size (the reference
+                             silently truncates, e.g. quants.c:966)        */
+    G4H_ERR_NOMEM = 4,    /* device allocation failed                     */
+    G4H_ERR_DEVICE = 5,   /* no gfx950 device / not initialised           */
+    G4H_ERR_HIP = 6       /* a HIP runtime call failed                    */
+};
+
+/* ------------------------------------------------------------ runtime ---- */
+/* Replaces g4_init_tables() (g4run.h:70, main.c:1222): selects `device`,
+ * checks it is gfx950, uploads the fp16 GELU table. */
+int         g4h_init(int device);
+const char *g4h_last_error(void);
+const char *g4h_status_str(int status);
+/* Test hook: make the next `n` device allocations fail with G4H_ERR_NOMEM
+ * (lets host code exercise the failure path without a real OOM). */
+void        g4h_debug_fail_alloc(int n);
+
+/* Plumbing (thin wrappers over HIP so that callers need no HIP headers). */
+int g4h_malloc(void **ptr, size_t bytes);
+int g4h_free(void *ptr);
+int g4h_memcpy_h2d(void *dst_dev, const void *src, size_t bytes, void *stream);
+int g4h_memcpy_d2h(void *dst, const void *src_dev, size_t bytes, void *stream);
+int g4h_memcpy_d2d(void *dst_dev, const void *src_dev, size_t bytes, void *stream);
+int g4h_memset(void *dst_dev, int value, size_t bytes, void *stream);
+int g4h_stream_create(void **stream);
+int g4h_stream_destroy(void *stream);
+int g4h_stream_synchronize(void *stream);
+int g4h_event_create(void **event);
+int g4h_event_destroy(void *event);
+int g4h_event_record(void *event, void *stream);
+int g4h_event_elapsed_ms(float *ms, void *start, void *stop);   /* synchronizes on stop */
+int g4h_graph_begin(void *stream);                              /* hipStreamBeginCapture */
+int g4h_graph_end(void *stream, void **graph_exec);             /* capture -> instantiated graph */
+int g4h_graph_launch(void *graph_exec, void *stream);
+int g4h_graph_destroy(void *graph_exec);
+
+/* ----------------------------------------------------- sizes / classes ---- */
+/* g4_row_size (g4run.h:99, gguf.c:42-46): 0 when n is not a multiple of the
+ * block size or the type is unknown. */
+size_t g4h_row_size(int type, int64_t n);
+/* act_class (model.c:132-141): activation format a weight type dots against
+ * (G4H_Q8_0 for q4_0/q8_0, G4H_Q8_K for q2_K/q3_K/q4_K), -1 otherwise. */
+int    g4h_act_type(int wtype);
+/* prep_act stride (model.c:148-149,156-157): per-token bytes, 64-B padded. */
+size_t g4h_act_stride(int wtype, int64_t ncols);
+
+/* ---------------------------------------------------------- quantizers ---- */
+/* g4_quantize_q8_0 / g4_quantize_q8_K / g4_quantize_q4_0 (g4run.h:121-123),
+ * applied to `rows` rows of n floats (x row stride x_stride floats) writing
+ * GGUF blocks at y_stride bytes per row.  Bit-identical to the reference
+ * build (README flags) of quants.c:71-175. */
+int g4h_quantize_q8_0(const float *x_dev, size_t x_stride, void *y_dev, size_t y_stride,
+                      int64_t n, int rows, void *stream);
+int g4h_quantize_q8_K(const float *x_dev, size_t x_stride, void *y_dev, size_t y_stride,
+                      int64_t n, int rows, void *stream);
+int g4h_quantize_q4_0(const float *x_dev, size_t x_stride, void *y_dev, size_t y_stride,
+                      int64_t n, int rows, void *stream);
+
+/* g4_dequant_row (g4run.h:128) for `rows` GGUF rows of n elements. */
+int g4h_dequant_rows(int type, const void *x_dev, size_t x_stride, float *y_dev, size_t y_stride,
+                     int64_t n, int rows, void *stream);
+
+/* g4_dot_<fmt> (g4run.h:137-143) applied to `rows` raw GGUF weight rows at
+ * w_stride bytes against one quantized activation row:
+ *   out[r] = g4_dot_<wtype>(w + r*w_stride, a, n). */
+int g4h_vec_dot(int wtype, const void *w_dev, size_t w_stride, const void *a_dev, int64_t n,
+                int rows, float *out_dev, void *stream);
+
+/* --------------------------------------------------- resident weights ---- */
+/* A weight matrix resident in HBM in the layout the kernels stream (scales
+ * split from quants so every quant load is an aligned 128-bit load).  This is
+ * what replaces a g4_tensor's `data` pointer (g4run.h:177-184) on the GPU. */
+typedef struct g4h_tensor g4h_tensor;
+
+int    g4h_tensor_create(int type, int64_t ncols, int64_t nrows, g4h_tensor **out);
+/* Load GGUF rows (nrows x g4h_row_size(type,ncols) bytes, contiguous) from host
+ * memory (src_is_device == 0) or device memory, repacking on the device. */
+int    g4h_tensor_load(g4h_tensor *t, const void *rows, int src_is_device, void *stream);
+/* Write the tensor back as contiguous GGUF rows (device destination). */
+int    g4h_tensor_store(const g4h_tensor *t, void *rows_dev, void *stream);
+int    g4h_tensor_free(g4h_tensor *t);
+size_t g4h_tensor_bytes(const g4h_tensor *t);     /* resident bytes */
+int    g4h_tensor_info(const g4h_tensor *t, int *type, int64_t *ncols, int64_t *nrows);
+
+/* ------------------------------------------------------------- matmul ---- */
+/* matmul_b (model.c:257-270) with prep_act (model.c:144-187) fused ahead:
+ *   Y[b][r] = dot(W[r,:], act[b]),  b < nb,  r < nrows, Y token-major.
+ * Either x_dev (nb x ncols floats, quantized here to W's activation format) or
+ * pre_dev (already-quantized activations, nb rows at pre_stride bytes) is
+ * given; the other is NULL.  Token b's outputs are bit-identical for any nb
+ * within one kernel family (g4run.h:148-157 contract); families switch at
+ * nb thresholds given by g4h_matmul_path(). */
+int g4h_matmul(const g4h_tensor *W, const float *x_dev, const void *pre_dev, size_t pre_stride,
+               float *Y_dev, int nb, void *stream);
+/* Same with an explicit kernel family: 0 = auto, 1 = GEMV (nb <= 8),
+ * 2 = int8-MFMA tiles. */
+int g4h_matmul_ex(const g4h_tensor *W, const float *x_dev, const void *pre_dev, size_t pre_stride,
+                  float *Y_dev, int nb, int path, void *stream);
+int g4h_matmul_path(const g4h_tensor *W, int nb);
+
+/* Per-block integer sums of every row of W against token `tok` of pre_dev:
+ * q8_0/q4_0 one int32 per 32-block, q3_K one per superblock, q2_K/q4_K two per
+ * superblock (scale-weighted quant sum, min-weighted bsum), i.e. the integers
+ * the reference's dots scale (quants.c:535-762).  sums_dev: nrows x count. */
+int g4h_block_sums(const g4h_tensor *W, const void *pre_dev, size_t pre_stride, int tok,
+                   int32_t *sums_dev, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,166 @@
+/*
+ * g4o.h -- CPU oracle for the quantized weight x activation path.
+ *
+ * TEST INFRASTRUCTURE ONLY.  Nothing in the product (the g4run_amd package,
+ * its HIP library or its C ABI) links, loads or calls this code.  Only
+ * tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg use it, and
+ * only as the checker or the timed CPU baseline.
+ *
+ * It restates g4run's CPU arithmetic (src/g4run.h, src/quants.c, src/model.c,
+ * src/sampler.c of the reference) in plain C.  Each function cites the lines
+ * it follows.  Pinning status of every function (what checks it against
+ * something other than its own formula) is listed at the end of this header.
+ */
+#ifndef G4O_H
+#define G4O_H
+
+#include <stdint.h>
+#include <stddef.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ggml type ids, g4run.h:80-94 (values are a file-format contract). */
+enum {
+    G4O_F32 = 0, G4O_F16 = 1, G4O_Q4_0 = 2, G4O_Q8_0 = 8,
+    G4O_Q2_K = 10, G4O_Q3_K = 11, G4O_Q4_K = 12, G4O_Q8_K = 15
+};
+
+/* Packed block layouts, g4run.h:107-118.  Byte-for-byte the GGUF formats. */
+#pragma pack(push, 1)
+typedef struct { uint16_t d; uint8_t qs[16]; }  g4o_q4_0;                      /* 18 B  */
+typedef struct { uint16_t d; int8_t  qs[32]; }  g4o_q8_0;                      /* 34 B  */
+typedef struct { float d; int8_t qs[256]; int16_t bsums[16]; } g4o_q8_K;       /* 292 B */
+typedef struct { uint8_t scales[16]; uint8_t qs[64]; uint16_t d, dmin; } g4o_q2_K;        /* 84 B */
+typedef struct { uint8_t hmask[32]; uint8_t qs[64]; uint8_t scales[12]; uint16_t d; } g4o_q3_K; /* 110 B */
+typedef struct { uint16_t d, dmin; uint8_t scales[12]; uint8_t qs[128]; } g4o_q4_K;       /* 144 B */
+#pragma pack(pop)
+
+/* ---- type table (gguf.c:11-46) ---- */
+int    g4o_type_blck(int type);
+size_t g4o_type_size(int type);
+size_t g4o_row_size(int type, int64_t n);       /* 0 when n % blck != 0 (gguf.c:42-46) */
+
+/* ---- fp16 (g4run.h:37-59, quants.c:27-46) ---- */
+float    g4o_fp16_to_fp32(uint16_t h);
+uint16_t g4o_fp32_to_fp16(float f);
+int      g4o_nearest_int(float f);              /* quants.c:63-67 */
+void     g4o_fp16_to_fp32_n(const uint16_t *h, float *f, int64_t n);
+void     g4o_fp32_to_fp16_n(const float *f, uint16_t *h, int64_t n);
+
+/* ---- activation / KV quantizers (quants.c:71-175) ---- */
+void g4o_quantize_q8_0(const float *x, g4o_q8_0 *y, int64_t n);   /* AVX2 semantics, quants.c:74-109 */
+void g4o_quantize_q8_K(const float *x, g4o_q8_K *y, int64_t n);   /* quants.c:146-175 */
+void g4o_quantize_q4_0(const float *x, g4o_q4_0 *y, int64_t n);   /* quants.c:125-144 */
+
+/* ---- dequant (quants.c:364-531) ---- */
+int  g4o_dequant_row(int type, const void *x, float *y, int64_t n);  /* returns -1 on unknown type */
+
+/* ---- per-block integer sums ----
+ * q8_0 / q4_0: one int32 per 32-block: sum_j w_j * a_j (q4_0 elements are q-8).
+ * q2_K / q4_K: two int32 per superblock: isum (scale-weighted quant sum) and
+ *              msum (min-weighted bsums), so that the superblock value is
+ *              d_a*(d_w*isum - dmin_w*msum)   (quants.c:633-652, 743-758).
+ * q3_K: one int32 per superblock, isum = sum_s (scale_s-32) * sum q3*q8.      */
+void g4o_block_sums(int type, const void *w, const void *a, int64_t n, int32_t *out);
+
+/* ---- scalar reference dots (quants.c:535-762), sequential fp32 order ---- */
+float g4o_dot_ref(int type, const void *w, const void *a, int64_t n);
+
+/* ---- shipped AVX2-order dots: same integer lanes, the same fused
+ *      multiply-adds and the same horizontal-sum tree as quants.c:820-1259,
+ *      written in portable C.  Results are bit-identical to the reference's
+ *      AVX2 build. ---- */
+float g4o_dot(int type, const void *w, const void *a, int64_t n);
+float g4o_dot_f16(const uint16_t *w, const uint16_t *a, int64_t n);   /* quants.c:1319-1331 */
+
+/* ---- activation class + prep, matmul driver (model.c:132-270) ---- */
+int    g4o_act_type(int wtype);                 /* G4O_Q8_0 or G4O_Q8_K, -1 otherwise */
+size_t g4o_act_stride(int wtype, int64_t ncols);/* 64-B padded per-token stride (model.c:148-149) */
+void   g4o_prep_act(int wtype, const float *x, int64_t ncols, int nb, void *qa);
+/* Y[b][r] = dot(W[r,:], act[b]); token-major like model.c:197.  nthreads<=1: serial. */
+void   g4o_matmul(int wtype, const void *W, const void *act, size_t act_stride,
+                  float *Y, int64_t ncols, int64_t nrows, int nb, int nthreads);
+
+/* ---- thread pool: static contiguous split, caller runs chunk 0
+ *      (model.c:59-65, 117-125), pthreads instead of Win32 ---- */
+typedef void (*g4o_pf_fn)(int64_t r0, int64_t r1, void *ud, int tid);
+void g4o_pool_start(int nthreads);
+void g4o_pool_stop(void);
+void g4o_parallel_for(int64_t total, g4o_pf_fn fn, void *ud);
+
+/* ---- dot-function table used by the matmul driver; lets the same driver time
+ *      either this restatement or the reference's compiled kernels ---- */
+typedef float (*g4o_dot_fn)(const void *w, const void *a, int64_t n);
+void g4o_set_dot_fn(int wtype, g4o_dot_fn fn);  /* NULL restores the restatement */
+
+/* ---- norms, rope, gelu, argmax (model.c:338-367, g4run.h:73-77, quants.c:49-58,
+ *      sampler.c:139-144) ---- */
+void     g4o_rms_norm(const float *x, const float *w, float *y, int n, float eps);
+void     g4o_rope_cache(float *cs, int n_dims, int pos, float freq_base);
+void     g4o_rope_apply(float *x, const float *cs, int n_dims);
+uint16_t g4o_gelu_table_entry(uint16_t h);      /* fp16(gelu_tanh(fp32(h))) */
+float    g4o_gelu(float x);
+int      g4o_argmax(const float *v, int n);
+
+/* ---- decode attention over one KV head group (model.c:509-580), GQA mapping
+ *      kvh = h / (n_head/n_kv) as model.c:1099.  KV rows: [slot][n_kv][hd] in
+ *      kv_type (G4O_F16 or G4O_Q8_0).  q: [n_head][hd] fp32, out: [n_head][hd].
+ *      Attends positions 0..pos (no ring wrap; slots >= pos+1). ---- */
+void g4o_attn_decode(const float *q, const void *kc, const void *vc, int kv_type,
+                     int n_head, int n_kv, int hd, int pos, float *out, int nthreads);
+/* kv_store (model.c:583-589) */
+void g4o_kv_store(int kv_type, void *dst, const float *src, int hd);
+
+/* ---- synthetic gemma-style decoder (layer order of model.c:647-736,
+ *      head model.c:766-769), weights supplied by the caller ---- */
+typedef struct {
+    int n_layer, n_embd, n_head, n_kv, hd, n_ff, n_vocab, n_ctx;
+    float rope_base, eps;
+    int kv_type;                     /* G4O_F16 or G4O_Q8_0 */
+    /* per-layer weights, q4_0 rows (or any supported type in wtype) */
+    int wtype;
+    const void **wqkv;               /* [n_layer] fused rows: q (n_head*hd) | k (n_kv*hd) | v (n_kv*hd) */
+    const void **wo;                 /* [n_layer] n_embd rows x n_head*hd cols */
+    const void **wgu;                /* [n_layer] fused rows: gate (n_ff) | up (n_ff) */
+    const void **wdown;              /* [n_layer] n_embd rows x n_ff cols */
+    const float **attn_norm, **q_norm, **k_norm, **post_attn_norm, **ffn_norm, **post_ffw_norm;
+    const float *output_norm;
+    int head_type;                   /* G4O_Q8_0 */
+    const void *head;                /* n_vocab rows x n_embd (tied with the input embedding) */
+    void **kc, **vc;                 /* [n_layer] caches: n_ctx slots x n_kv x hd */
+} g4o_model;
+
+/* One decode step for `token` at `pos`.  Writes logits[n_vocab], returns argmax.
+ * scratch must hold g4o_model_scratch_bytes(m) bytes. */
+size_t g4o_model_scratch_bytes(const g4o_model *m);
+int    g4o_model_decode(const g4o_model *m, int token, int pos, float *logits,
+                        void *scratch, int nthreads);
+
+/*
+ * Pinning (checks that are not a retyping of the function's own formula):
+ *   fp16 both ways        exhaustive 65536-code round trip; RNE on ties and
+ *                         subnormals vs numpy float16 casts (tests)
+ *   quantize_q8_0/q8_K    bit-exact vs the reference build oracle/_ref and the
+ *                         committed fixtures; closed-form special cases
+ *   quantize_q4_0         bit-exact vs oracle/_ref
+ *   dequant (5 formats)   bit-exact vs oracle/_ref on random blocks
+ *   block_sums            brute-force dequant identity in exact integer math,
+ *                         and unit-scale calls of the reference _ref dots
+ *   dot_ref               bit-exact vs the reference's scalar _ref dots
+ *   dot (AVX2 order)      bit-exact vs the reference's AVX2 dots (oracle/_ref)
+ *   dot_f16               bit-exact vs the reference's g4_dot_f16
+ *   matmul                row loop of dot(); x4 == x1 invariant
+ *   rms_norm, rope, attention, decode graph
+ *                         model.c does not compile here (windows.h), so these
+ *                         are checked by invariants (softmax of a one-hot,
+ *                         rope as a rotation, attention of identical keys,
+ *                         float64 recomputation) -- see tests/test_oracle_model.py
+ *   gelu table            against math.tanh-based float64 recomputation
+ */
+
+#ifdef __cplusplus
+}
+#endif
+#endif

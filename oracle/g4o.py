@@ -1,0 +1,331 @@
+"""ctypes front end of the CPU oracle (oracle/liboracle.so) and of the
+reference build (oracle/_ref/libg4ref.so, the reference's src/quants.c
+compiled in place by `make -C oracle ref`).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and the
+cpu_baseline leg of bench.py -- never by the g4run_amd package.
+
+Quantized tensors are numpy uint8 arrays of raw GGUF bytes, shape
+[rows, row_bytes]; activations likewise, one row per token.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "liboracle.so")
+REF_PATH = os.path.join(HERE, "_ref", "libg4ref.so")
+
+F32, F16, Q4_0, Q8_0, Q2_K, Q3_K, Q4_K, Q8_K = 0, 1, 2, 8, 10, 11, 12, 15
+BLCK = {F32: 1, F16: 1, Q4_0: 32, Q8_0: 32, Q2_K: 256, Q3_K: 256, Q4_K: 256, Q8_K: 256}
+SIZE = {F32: 4, F16: 2, Q4_0: 18, Q8_0: 34, Q2_K: 84, Q3_K: 110, Q4_K: 144, Q8_K: 292}
+NAMES = {Q4_0: "q4_0", Q8_0: "q8_0", Q2_K: "q2_K", Q3_K: "q3_K", Q4_K: "q4_K"}
+ACT = {Q4_0: Q8_0, Q8_0: Q8_0, Q2_K: Q8_K, Q3_K: Q8_K, Q4_K: Q8_K}
+
+_lib = None
+_ref = None
+
+_vp = C.c_void_p
+_i64 = C.c_int64
+
+
+def row_size(t: int, n: int) -> int:
+    b = BLCK[t]
+    return 0 if n % b else (n // b) * SIZE[t]
+
+
+def act_stride(wtype: int, ncols: int) -> int:
+    return (row_size(ACT[wtype], ncols) + 63) & ~63
+
+
+def _ptr(a: np.ndarray):
+    assert a.flags["C_CONTIGUOUS"]
+    return a.ctypes.data_as(_vp)
+
+
+def lib():
+    """Load (building if needed) the oracle restatement."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            import subprocess
+            subprocess.run(["make", "-C", HERE, "liboracle.so"], check=True,
+                           stdout=subprocess.DEVNULL)
+        L = C.CDLL(LIB_PATH)
+        L.g4o_fp16_to_fp32.restype = C.c_float
+        L.g4o_fp16_to_fp32.argtypes = [C.c_uint16]
+        L.g4o_fp32_to_fp16.restype = C.c_uint16
+        L.g4o_fp32_to_fp16.argtypes = [C.c_float]
+        L.g4o_fp16_to_fp32_n.argtypes = [_vp, _vp, _i64]
+        L.g4o_fp32_to_fp16_n.argtypes = [_vp, _vp, _i64]
+        L.g4o_nearest_int.restype = C.c_int
+        L.g4o_nearest_int.argtypes = [C.c_float]
+        for q in ("q8_0", "q8_K", "q4_0"):
+            f = getattr(L, "g4o_quantize_" + q)
+            f.restype = None
+            f.argtypes = [_vp, _vp, _i64]
+        L.g4o_dequant_row.restype = C.c_int
+        L.g4o_dequant_row.argtypes = [C.c_int, _vp, _vp, _i64]
+        L.g4o_block_sums.restype = None
+        L.g4o_block_sums.argtypes = [C.c_int, _vp, _vp, _i64, _vp]
+        for f in (L.g4o_dot_ref, L.g4o_dot):
+            f.restype = C.c_float
+            f.argtypes = [C.c_int, _vp, _vp, _i64]
+        L.g4o_dot_f16.restype = C.c_float
+        L.g4o_dot_f16.argtypes = [_vp, _vp, _i64]
+        L.g4o_matmul.restype = None
+        L.g4o_matmul.argtypes = [C.c_int, _vp, _vp, C.c_size_t, _vp, _i64, _i64, C.c_int, C.c_int]
+        L.g4o_prep_act.restype = None
+        L.g4o_prep_act.argtypes = [C.c_int, _vp, _i64, C.c_int, _vp]
+        L.g4o_pool_start.argtypes = [C.c_int]
+        L.g4o_pool_stop.argtypes = []
+        L.g4o_set_dot_fn.argtypes = [C.c_int, _vp]
+        L.g4o_rms_norm.argtypes = [_vp, _vp, _vp, C.c_int, C.c_float]
+        L.g4o_rope_cache.argtypes = [_vp, C.c_int, C.c_int, C.c_float]
+        L.g4o_rope_apply.argtypes = [_vp, _vp, C.c_int]
+        L.g4o_gelu_table_entry.restype = C.c_uint16
+        L.g4o_gelu_table_entry.argtypes = [C.c_uint16]
+        L.g4o_gelu.restype = C.c_float
+        L.g4o_gelu.argtypes = [C.c_float]
+        L.g4o_argmax.restype = C.c_int
+        L.g4o_argmax.argtypes = [_vp, C.c_int]
+        L.g4o_attn_decode.argtypes = [_vp, _vp, _vp, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, _vp, C.c_int]
+        L.g4o_kv_store.argtypes = [C.c_int, _vp, _vp, C.c_int]
+        L.g4o_model_scratch_bytes.restype = C.c_size_t
+        L.g4o_model_scratch_bytes.argtypes = [_vp]
+        L.g4o_model_decode.restype = C.c_int
+        L.g4o_model_decode.argtypes = [_vp, C.c_int, C.c_int, _vp, _vp, C.c_int]
+        _lib = L
+    return _lib
+
+
+def ref_available() -> bool:
+    return os.path.exists(REF_PATH)
+
+
+def ref():
+    """The reference's own compiled kernels (oracle/_ref/libg4ref.so)."""
+    global _ref
+    if _ref is None:
+        R = C.CDLL(REF_PATH)
+        R.g4_init_tables()
+        for q in ("q8_0", "q8_K", "q4_0"):
+            f = getattr(R, "g4_quantize_" + q)
+            f.restype = None
+            f.argtypes = [_vp, _vp, _i64]
+        R.g4_dequant_row.restype = None
+        R.g4_dequant_row.argtypes = [C.c_int, _vp, _vp, _i64]
+        for nm in ("q4_0_q8_0", "q8_0_q8_0", "q2_K_q8_K", "q3_K_q8_K", "q4_K_q8_K"):
+            for suf in ("", "_ref"):
+                f = getattr(R, "g4_dot_" + nm + suf)
+                f.restype = C.c_float
+                f.argtypes = [_vp, _vp, _i64]
+            f = getattr(R, "g4_dot_" + nm + "_x4")
+            f.restype = None
+            f.argtypes = [_vp, C.POINTER(_vp), _i64, _vp]
+        R.g4_dot_f16.restype = C.c_float
+        R.g4_dot_f16.argtypes = [_vp, _vp, _i64]
+        R.g4_selftest_quants.restype = C.c_int
+        _ref = R
+    return _ref
+
+
+DOT_NAME = {Q4_0: "q4_0_q8_0", Q8_0: "q8_0_q8_0", Q2_K: "q2_K_q8_K", Q3_K: "q3_K_q8_K", Q4_K: "q4_K_q8_K"}
+
+
+# ------------------------------------------------------------------ wrappers
+def fp32_to_fp16(x: np.ndarray) -> np.ndarray:
+    flat = np.ascontiguousarray(x, dtype=np.float32).ravel()
+    out = np.empty(flat.size, dtype=np.uint16)
+    lib().g4o_fp32_to_fp16_n(_ptr(flat), _ptr(out), flat.size)
+    return out.reshape(np.shape(x))
+
+
+def fp16_to_fp32(h: np.ndarray) -> np.ndarray:
+    flat = np.ascontiguousarray(h, dtype=np.uint16).ravel()
+    out = np.empty(flat.size, dtype=np.float32)
+    lib().g4o_fp16_to_fp32_n(_ptr(flat), _ptr(out), flat.size)
+    return out.reshape(np.shape(h))
+
+
+def quantize(qtype: int, x: np.ndarray, use_ref: bool = False) -> np.ndarray:
+    """Quantize rows of x (shape [..., n]) to qtype; returns uint8 [rows, row_bytes]."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    n = x.shape[-1]
+    rows = x.reshape(-1, n)
+    out = np.zeros((rows.shape[0], row_size(qtype, n)), dtype=np.uint8)
+    name = {Q8_0: "q8_0", Q8_K: "q8_K", Q4_0: "q4_0"}[qtype]
+    f = getattr(ref(), "g4_quantize_" + name) if use_ref else getattr(lib(), "g4o_quantize_" + name)
+    for i in range(rows.shape[0]):
+        f(rows[i].ctypes.data_as(_vp), out[i].ctypes.data_as(_vp), n)
+    return out
+
+
+def dequant(qtype: int, w: np.ndarray, n: int, use_ref: bool = False) -> np.ndarray:
+    w = np.ascontiguousarray(w, dtype=np.uint8).reshape(-1, row_size(qtype, n))
+    out = np.zeros((w.shape[0], n), dtype=np.float32)
+    for i in range(w.shape[0]):
+        if use_ref:
+            ref().g4_dequant_row(qtype, w[i].ctypes.data_as(_vp), out[i].ctypes.data_as(_vp), n)
+        else:
+            rc = lib().g4o_dequant_row(qtype, w[i].ctypes.data_as(_vp), out[i].ctypes.data_as(_vp), n)
+            assert rc == 0
+    return out
+
+
+def n_sums_per_row(wtype: int, n: int) -> int:
+    if wtype in (Q8_0, Q4_0):
+        return n // 32
+    if wtype in (Q2_K, Q4_K):
+        return 2 * (n // 256)
+    return n // 256
+
+
+def block_sums(wtype: int, w: np.ndarray, a: np.ndarray, n: int) -> np.ndarray:
+    """Per-block integer sums of every weight row against one activation row."""
+    w = np.ascontiguousarray(w, dtype=np.uint8).reshape(-1, row_size(wtype, n))
+    a = np.ascontiguousarray(a, dtype=np.uint8).ravel()
+    out = np.zeros((w.shape[0], n_sums_per_row(wtype, n)), dtype=np.int32)
+    for i in range(w.shape[0]):
+        lib().g4o_block_sums(wtype, w[i].ctypes.data_as(_vp), a.ctypes.data_as(_vp), n, out[i].ctypes.data_as(_vp))
+    return out
+
+
+def dot(wtype: int, w_row: np.ndarray, a_row: np.ndarray, n: int, kind: str = "avx2") -> float:
+    """kind: 'avx2' (restated shipped order), 'ref' (restated scalar order),
+    'refbuild' / 'refbuild_scalar' (the reference's own compiled kernels)."""
+    wp, ap = _ptr(np.ascontiguousarray(w_row)), _ptr(np.ascontiguousarray(a_row))
+    if kind == "avx2":
+        return lib().g4o_dot(wtype, wp, ap, n)
+    if kind == "ref":
+        return lib().g4o_dot_ref(wtype, wp, ap, n)
+    fn = getattr(ref(), "g4_dot_" + DOT_NAME[wtype] + ("" if kind == "refbuild" else "_ref"))
+    return fn(wp, ap, n)
+
+
+def matmul(wtype: int, W: np.ndarray, act: np.ndarray, ncols: int, nthreads: int = 1) -> np.ndarray:
+    """Y[b][r] = dot(W[r], act[b]) with act rows at the 64-B padded stride."""
+    W = np.ascontiguousarray(W, dtype=np.uint8)
+    nrows = W.shape[0]
+    st = act_stride(wtype, ncols)
+    act = np.ascontiguousarray(act, dtype=np.uint8)
+    nb = act.size // st
+    Y = np.zeros((nb, nrows), dtype=np.float32)
+    lib().g4o_matmul(wtype, _ptr(W), _ptr(act), st, _ptr(Y), ncols, nrows, nb, nthreads)
+    return Y
+
+
+def prep_act(wtype: int, x: np.ndarray) -> np.ndarray:
+    """Quantize token rows x[nb][ncols] to the activation format at the padded stride."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    nb, ncols = x.reshape(-1, x.shape[-1]).shape
+    st = act_stride(wtype, ncols)
+    out = np.zeros((nb, st), dtype=np.uint8)
+    lib().g4o_prep_act(wtype, _ptr(x), ncols, nb, _ptr(out))
+    return out
+
+
+def use_reference_dots(enable: bool) -> None:
+    """Route the matmul driver through the reference build's AVX2 dots."""
+    L = lib()
+    for t, nm in DOT_NAME.items():
+        fn = C.cast(getattr(ref(), "g4_dot_" + nm), _vp) if enable else None
+        L.g4o_set_dot_fn(t, fn)
+
+
+def pool_start(n: int) -> None:
+    lib().g4o_pool_start(n)
+
+
+def pool_stop() -> None:
+    lib().g4o_pool_stop()
+
+
+def rms_norm(x: np.ndarray, w, eps: float) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    y = np.empty_like(x)
+    wp = _ptr(np.ascontiguousarray(w, dtype=np.float32)) if w is not None else None
+    lib().g4o_rms_norm(_ptr(x), wp, _ptr(y), x.size, eps)
+    return y
+
+
+def rope(x: np.ndarray, pos: int, base: float) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32).copy()
+    n = x.size
+    cs = np.zeros(n, dtype=np.float32)
+    lib().g4o_rope_cache(_ptr(cs), n, pos, base)
+    lib().g4o_rope_apply(_ptr(x), _ptr(cs), n)
+    return x
+
+
+def gelu_table() -> np.ndarray:
+    L = lib()
+    return np.array([L.g4o_gelu_table_entry(i) for i in range(65536)], dtype=np.uint16)
+
+
+def attn_decode(q: np.ndarray, kc: np.ndarray, vc: np.ndarray, kv_type: int, n_head: int,
+                n_kv: int, hd: int, pos: int, nthreads: int = 1) -> np.ndarray:
+    q = np.ascontiguousarray(q, dtype=np.float32)
+    out = np.zeros((n_head, hd), dtype=np.float32)
+    lib().g4o_attn_decode(_ptr(q), _ptr(np.ascontiguousarray(kc)), _ptr(np.ascontiguousarray(vc)),
+                          kv_type, n_head, n_kv, hd, pos, _ptr(out), nthreads)
+    return out
+
+
+class _Model(C.Structure):
+    _fields_ = [
+        ("n_layer", C.c_int), ("n_embd", C.c_int), ("n_head", C.c_int), ("n_kv", C.c_int),
+        ("hd", C.c_int), ("n_ff", C.c_int), ("n_vocab", C.c_int), ("n_ctx", C.c_int),
+        ("rope_base", C.c_float), ("eps", C.c_float), ("kv_type", C.c_int), ("wtype", C.c_int),
+        ("wqkv", C.POINTER(_vp)), ("wo", C.POINTER(_vp)), ("wgu", C.POINTER(_vp)), ("wdown", C.POINTER(_vp)),
+        ("attn_norm", C.POINTER(_vp)), ("q_norm", C.POINTER(_vp)), ("k_norm", C.POINTER(_vp)),
+        ("post_attn_norm", C.POINTER(_vp)), ("ffn_norm", C.POINTER(_vp)), ("post_ffw_norm", C.POINTER(_vp)),
+        ("output_norm", _vp), ("head_type", C.c_int), ("head", _vp),
+        ("kc", C.POINTER(_vp)), ("vc", C.POINTER(_vp)),
+    ]
+
+
+class Model:
+    """CPU restatement of the synthetic gemma-style decoder.
+
+    `w` is a dict of numpy arrays as produced by g4run_amd.model_weights():
+    per-layer lists 'wqkv', 'wo', 'wgu', 'wdown' (uint8 rows) and the norm
+    vectors, plus 'head' and 'output_norm'.  KV caches are numpy arrays owned
+    here ([n_layer][n_ctx*n_kv*row_bytes]).
+    """
+
+    def __init__(self, cfg: dict, w: dict, kc: list, vc: list):
+        self.cfg, self.w, self.kc, self.vc = cfg, w, kc, vc
+        L = cfg["n_layer"]
+
+        def arr(lst):
+            a = (_vp * L)(*[x.ctypes.data_as(_vp) for x in lst])
+            return a
+
+        self._keep = []
+        m = _Model()
+        for k in ("n_layer", "n_embd", "n_head", "n_kv", "hd", "n_ff", "n_vocab", "n_ctx"):
+            setattr(m, k, cfg[k])
+        m.rope_base, m.eps, m.kv_type, m.wtype = cfg["rope_base"], cfg["eps"], cfg["kv_type"], cfg["wtype"]
+        for k in ("wqkv", "wo", "wgu", "wdown", "attn_norm", "q_norm", "k_norm",
+                  "post_attn_norm", "ffn_norm", "post_ffw_norm"):
+            a = arr(w[k])
+            self._keep.append(a)
+            setattr(m, k, C.cast(a, C.POINTER(_vp)))
+        m.output_norm = w["output_norm"].ctypes.data_as(_vp)
+        m.head_type = cfg["head_type"]
+        m.head = w["head"].ctypes.data_as(_vp)
+        for k, lst in (("kc", kc), ("vc", vc)):
+            a = arr(lst)
+            self._keep.append(a)
+            setattr(m, k, C.cast(a, C.POINTER(_vp)))
+        self._m = m
+        self._scratch = np.zeros(lib().g4o_model_scratch_bytes(C.byref(m)), dtype=np.uint8)
+
+    def decode(self, token: int, pos: int, nthreads: int = 1):
+        logits = np.zeros(self.cfg["n_vocab"], dtype=np.float32)
+        tok = lib().g4o_model_decode(C.byref(self._m), token, pos, _ptr(logits), _ptr(self._scratch), nthreads)
+        return tok, logits
