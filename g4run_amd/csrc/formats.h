@@ -42,66 +42,141 @@ struct ActQ8_K {
     }
 };
 
-// Stage NB tokens of GGUF q8_0 activation rows (act_stride bytes apart, 4-B
-// aligned) into LDS.  Pairs of blocks are 68 B = 17 aligned dwords.
+// Activation staging is split in two so a kernel can issue the (small, mostly
+// L2-resident) activation loads before its weight stream, then finish the LDS
+// writes while the weights are in flight: global loads complete in issue order,
+// so waiting for activations issued first never waits for the weights.
+//
+// q8_0: one item = a pair of 34-B blocks = 17 aligned dwords.
+struct StageQ8_0 {
+    uint32_t v[17];
+    int t, pr;
+    bool ok;
+};
 template <int NB>
-__device__ void stage_q8_0(uint8_t *lds, const uint8_t *act, size_t stride, int nb) {
+__device__ __forceinline__ void stage_q8_0_load(StageQ8_0 &S, int item, const uint8_t *act, size_t stride, int nb) {
     const int npair = nb >> 1;
-    for (int i = threadIdx.x; i < NB * npair; i += blockDim.x) {
-        const int t = i / npair, pr = i - t * npair;
-        const uint32_t *src = (const uint32_t *)(act + (size_t)t * stride + (size_t)pr * 68);
-        uint32_t v[17];
+    S.ok = item < NB * npair;
+    S.t = S.ok ? item / npair : 0;
+    S.pr = S.ok ? item - S.t * npair : 0;
+    if (S.ok) {
+        const uint32_t *src = (const uint32_t *)(act + (size_t)S.t * stride + (size_t)S.pr * 68);
 #pragma unroll
-        for (int k = 0; k < 17; k++) v[k] = src[k];
-        ActQ8_0 A(lds, nb, t);
-        const int b = 2 * pr;
-        int4 a0, a1;
-        a0.x = __builtin_amdgcn_alignbyte(v[1], v[0], 2); a0.y = __builtin_amdgcn_alignbyte(v[2], v[1], 2);
-        a0.z = __builtin_amdgcn_alignbyte(v[3], v[2], 2); a0.w = __builtin_amdgcn_alignbyte(v[4], v[3], 2);
-        a1.x = __builtin_amdgcn_alignbyte(v[5], v[4], 2); a1.y = __builtin_amdgcn_alignbyte(v[6], v[5], 2);
-        a1.z = __builtin_amdgcn_alignbyte(v[7], v[6], 2); a1.w = __builtin_amdgcn_alignbyte(v[8], v[7], 2);
-        A.q0[b] = a0; A.q1[b] = a1; A.d[b] = h2f((uint16_t)(v[0] & 0xffff));
-        int s = 0;
-        s = dot4(a0.x, 0x01010101, s); s = dot4(a0.y, 0x01010101, s); s = dot4(a0.z, 0x01010101, s); s = dot4(a0.w, 0x01010101, s);
-        s = dot4(a1.x, 0x01010101, s); s = dot4(a1.y, 0x01010101, s); s = dot4(a1.z, 0x01010101, s); s = dot4(a1.w, 0x01010101, s);
-        A.s[b] = s;
-        int4 c0 = make_int4(v[9], v[10], v[11], v[12]), c1 = make_int4(v[13], v[14], v[15], v[16]);
-        A.q0[b + 1] = c0; A.q1[b + 1] = c1; A.d[b + 1] = h2f((uint16_t)(v[8] >> 16));
-        s = 0;
-        s = dot4(c0.x, 0x01010101, s); s = dot4(c0.y, 0x01010101, s); s = dot4(c0.z, 0x01010101, s); s = dot4(c0.w, 0x01010101, s);
-        s = dot4(c1.x, 0x01010101, s); s = dot4(c1.y, 0x01010101, s); s = dot4(c1.z, 0x01010101, s); s = dot4(c1.w, 0x01010101, s);
-        A.s[b + 1] = s;
+        for (int k = 0; k < 17; k++) S.v[k] = src[k];
     }
-    if (nb & 1) {   // odd block count: last block with 16-bit loads
+}
+__device__ __forceinline__ int sum_i8x16(int4 a) {
+    int s = dot4(a.x, 0x01010101, 0);
+    s = dot4(a.y, 0x01010101, s); s = dot4(a.z, 0x01010101, s); return dot4(a.w, 0x01010101, s);
+}
+__device__ __forceinline__ void stage_q8_0_store(const StageQ8_0 &S, uint8_t *lds, int nb) {
+    if (!S.ok) return;
+    ActQ8_0 A(lds, nb, S.t);
+    const uint32_t *v = S.v;
+    const int b = 2 * S.pr;
+    int4 a0, a1;
+    a0.x = __builtin_amdgcn_alignbyte(v[1], v[0], 2); a0.y = __builtin_amdgcn_alignbyte(v[2], v[1], 2);
+    a0.z = __builtin_amdgcn_alignbyte(v[3], v[2], 2); a0.w = __builtin_amdgcn_alignbyte(v[4], v[3], 2);
+    a1.x = __builtin_amdgcn_alignbyte(v[5], v[4], 2); a1.y = __builtin_amdgcn_alignbyte(v[6], v[5], 2);
+    a1.z = __builtin_amdgcn_alignbyte(v[7], v[6], 2); a1.w = __builtin_amdgcn_alignbyte(v[8], v[7], 2);
+    A.q0[b] = a0; A.q1[b] = a1; A.d[b] = h2f((uint16_t)(v[0] & 0xffff));
+    A.s[b] = sum_i8x16(a0) + sum_i8x16(a1);
+    const int4 c0 = make_int4(v[9], v[10], v[11], v[12]), c1 = make_int4(v[13], v[14], v[15], v[16]);
+    A.q0[b + 1] = c0; A.q1[b + 1] = c1; A.d[b + 1] = h2f((uint16_t)(v[8] >> 16));
+    A.s[b + 1] = sum_i8x16(c0) + sum_i8x16(c1);
+}
+// remaining items (rows longer than two blocks per thread) and an odd last block
+template <int NB>
+__device__ void stage_q8_0_rest(uint8_t *lds, const uint8_t *act, size_t stride, int nb) {
+    for (int i = threadIdx.x + blockDim.x; i < NB * (nb >> 1); i += blockDim.x) {
+        StageQ8_0 S;
+        stage_q8_0_load<NB>(S, i, act, stride, nb);
+        stage_q8_0_store(S, lds, nb);
+    }
+    if (nb & 1) {   // last block with 16-bit loads
         for (int t = threadIdx.x; t < NB; t += blockDim.x) {
             const uint16_t *src = (const uint16_t *)(act + (size_t)t * stride + (size_t)(nb - 1) * 34);
             uint32_t w[8];
 #pragma unroll
             for (int k = 0; k < 8; k++) w[k] = (uint32_t)src[1 + 2 * k] | ((uint32_t)src[2 + 2 * k] << 16);
             ActQ8_0 A(lds, nb, t);
-            int4 a0 = make_int4(w[0], w[1], w[2], w[3]), a1 = make_int4(w[4], w[5], w[6], w[7]);
+            const int4 a0 = make_int4(w[0], w[1], w[2], w[3]), a1 = make_int4(w[4], w[5], w[6], w[7]);
             A.q0[nb - 1] = a0; A.q1[nb - 1] = a1; A.d[nb - 1] = h2f(src[0]);
-            int s = 0;
-#pragma unroll
-            for (int k = 0; k < 8; k++) s = dot4(w[k], 0x01010101, s);
-            A.s[nb - 1] = s;
+            A.s[nb - 1] = sum_i8x16(a0) + sum_i8x16(a1);
         }
     }
 }
-
-// Stage NB tokens of GGUF q8_K rows (292-B superblocks, dword aligned).
 template <int NB>
-__device__ void stage_q8_K(uint8_t *lds, const uint8_t *act, size_t stride, int nb) {
-    const int per = nb * 73;
-    for (int i = threadIdx.x; i < NB * per; i += blockDim.x) {
-        const int t = i / per, r = i - t * per, sb = r / 73, w = r - sb * 73;
-        const uint32_t v = ((const uint32_t *)(act + (size_t)t * stride))[r];
-        ActQ8_K A(lds, nb, t);
-        if (w == 0) A.d[sb] = __builtin_bit_cast(float, v);
-        else if (w <= 64) ((uint32_t *)(A.q + (size_t)sb * 256))[w - 1] = v;
-        else ((uint32_t *)(A.bs + (size_t)sb * 16))[w - 65] = v;
+__device__ void stage_q8_0(uint8_t *lds, const uint8_t *act, size_t stride, int nb) {
+    StageQ8_0 S;
+    stage_q8_0_load<NB>(S, threadIdx.x, act, stride, nb);
+    stage_q8_0_store(S, lds, nb);
+    stage_q8_0_rest<NB>(lds, act, stride, nb);
+}
+
+// q8_K: one item = 16 bytes of quants (4 dwords) or, for chunk 16, the
+// superblock's d and 16 bsums (9 dwords): 17 items per 292-B superblock.
+struct StageQ8_K {
+    uint32_t v[9];
+    int t, sb, c;
+    bool ok;
+};
+template <int NB>
+__device__ __forceinline__ void stage_q8_K_load(StageQ8_K &S, int item, const uint8_t *act, size_t stride, int nb) {
+    const int per = nb * 17;
+    S.ok = item < NB * per;
+    const int it = S.ok ? item : 0;
+    S.t = it / per;
+    const int r = it - S.t * per;
+    S.sb = r / 17;
+    S.c = r - S.sb * 17;
+    if (S.ok) {
+        const uint32_t *src = (const uint32_t *)(act + (size_t)S.t * stride) + (size_t)S.sb * 73;
+        if (S.c < 16) {
+#pragma unroll
+            for (int k = 0; k < 4; k++) S.v[k] = src[1 + 4 * S.c + k];
+        } else {
+            S.v[0] = src[0];
+#pragma unroll
+            for (int k = 0; k < 8; k++) S.v[1 + k] = src[65 + k];
+        }
     }
 }
+__device__ __forceinline__ void stage_q8_K_store(const StageQ8_K &S, uint8_t *lds, int nb) {
+    if (!S.ok) return;
+    ActQ8_K A(lds, nb, S.t);
+    if (S.c < 16) {
+        *(int4 *)(A.q + (size_t)S.sb * 256 + 16 * S.c) = make_int4(S.v[0], S.v[1], S.v[2], S.v[3]);
+    } else {
+        A.d[S.sb] = __builtin_bit_cast(float, S.v[0]);
+        uint32_t *bs = (uint32_t *)(A.bs + (size_t)S.sb * 16);
+#pragma unroll
+        for (int k = 0; k < 8; k++) bs[k] = S.v[1 + k];
+    }
+}
+template <int NB>
+__device__ void stage_q8_K_rest(uint8_t *lds, const uint8_t *act, size_t stride, int nb) {
+    for (int i = threadIdx.x + blockDim.x; i < NB * nb * 17; i += blockDim.x) {
+        StageQ8_K S;
+        stage_q8_K_load<NB>(S, i, act, stride, nb);
+        stage_q8_K_store(S, lds, nb);
+    }
+}
+template <int NB>
+__device__ void stage_q8_K(uint8_t *lds, const uint8_t *act, size_t stride, int nb) {
+    StageQ8_K S;
+    stage_q8_K_load<NB>(S, threadIdx.x, act, stride, nb);
+    stage_q8_K_store(S, lds, nb);
+    stage_q8_K_rest<NB>(lds, act, stride, nb);
+}
+
+// Format -> staging helpers
+template <int T> struct StageOf;
+template <> struct StageOf<Q8_0> { using S = StageQ8_0; };
+template <> struct StageOf<Q4_0> { using S = StageQ8_0; };
+template <> struct StageOf<Q2_K> { using S = StageQ8_K; };
+template <> struct StageOf<Q3_K> { using S = StageQ8_K; };
+template <> struct StageOf<Q4_K> { using S = StageQ8_K; };
 
 // ------------------------------------------------------------------ q8_0 --
 struct FQ8_0 {

@@ -1,0 +1,146 @@
+// gemv.h -- decode GEMV / small-batch matmul over resident quantized
+// weights (the GPU form of matmul_b + mm_kernel, model.c:191-270).
+//
+// One workgroup = 4 waves.  A wave covers 64/LPR rows at a time; the LPR lanes
+// of a row split its units (blocks or quarter-superblocks) round-robin, each
+// lane holding up to UPL units of weight bytes in registers.  Every weight
+// byte is read from HBM exactly once with aligned 128-bit loads, issued before
+// the workgroup waits for its activation staging so the stream is in flight
+// while the activation lands in LDS.  The NB token activations of the call are
+// staged once per workgroup; the per-token fp32 accumulation order depends on
+// LPR only (chosen from the row length), never on NB, so token b's result is
+// bit-identical for any batch size (the x4 contract of g4run.h:148-157).
+#pragma once
+#include <cstdint>
+#include <cstdlib>
+
+#include "formats.h"
+#include "kernels.h"
+
+namespace g4 {
+
+template <class F>
+size_t act_lds_bytes(int nb_tokens, int64_t nblk) { return (size_t)nb_tokens * F::Act::bytes_per_token((int)nblk); }
+
+
+template <class F, int NB, int LPR, int UPL>
+__global__ __launch_bounds__(512) void k_gemv(g4h_tensor W, const uint8_t *__restrict__ act, size_t act_stride,
+                                               float *__restrict__ Y, int units) {
+    extern __shared__ __align__(16) uint8_t lds[];
+    using Act = typename F::Act;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, wpg = blockDim.x >> 6;
+    const int g = lane % LPR, rg = lane / LPR;
+    constexpr int RPW = 64 / LPR;
+    const int64_t row0 = ((int64_t)blockIdx.x * wpg + wave) * RPW + rg;
+    const bool row_ok = row0 < W.nrows;
+    const int64_t row = row_ok ? row0 : W.nrows - 1;
+
+    // activation loads first, then the weight stream (see formats.h)
+    typename StageOf<F::type>::S stg;
+    constexpr bool QK = F::type == Q4_0 || F::type == Q8_0;
+    if constexpr (QK) stage_q8_0_load<NB>(stg, threadIdx.x, act, act_stride, (int)W.nb);
+    else stage_q8_K_load<NB>(stg, threadIdx.x, act, act_stride, (int)W.nb);
+
+    typename F::Frag fr[UPL];
+#pragma unroll
+    for (int k = 0; k < UPL; k++) {
+        const int u = g + k * LPR;
+        if (u < units) F::load(fr[k], W, row, u);
+    }
+    if constexpr (QK) {
+        stage_q8_0_store(stg, lds, (int)W.nb);
+        stage_q8_0_rest<NB>(lds, act, act_stride, (int)W.nb);
+    } else {
+        stage_q8_K_store(stg, lds, (int)W.nb);
+        stage_q8_K_rest<NB>(lds, act, act_stride, (int)W.nb);
+    }
+    __syncthreads();
+
+    float acc[NB];
+#pragma unroll
+    for (int t = 0; t < NB; t++) acc[t] = 0.0f;
+#pragma unroll
+    for (int k = 0; k < UPL; k++) {
+        const int u = g + k * LPR;
+        if (u < units) {
+#pragma unroll
+            for (int t = 0; t < NB; t++) acc[t] = F::accum(fr[k], Act(lds, (int)W.nb, t), u, acc[t]);
+        }
+    }
+    // units beyond LPR*UPL (very long rows): further passes in the same order
+    for (int base = LPR * UPL; base < units; base += LPR * UPL) {
+#pragma unroll
+        for (int k = 0; k < UPL; k++) {
+            const int u = base + g + k * LPR;
+            if (u < units) F::load(fr[k], W, row, u);
+        }
+#pragma unroll
+        for (int k = 0; k < UPL; k++) {
+            const int u = base + g + k * LPR;
+            if (u < units) {
+#pragma unroll
+                for (int t = 0; t < NB; t++) acc[t] = F::accum(fr[k], Act(lds, (int)W.nb, t), u, acc[t]);
+            }
+        }
+    }
+#pragma unroll
+    for (int t = 0; t < NB; t++) acc[t] = group_sum<LPR>(acc[t]);
+    if (g == 0 && row_ok) {
+#pragma unroll
+        for (int t = 0; t < NB; t++) Y[(size_t)t * W.nrows + row] = acc[t];
+    }
+}
+
+// Waves per workgroup chosen so the grid is (close to) a multiple of the 256
+// CUs with equal rows per workgroup: every CU streams the same bytes.
+static inline int gemv_waves_per_group(int64_t nrows, int rpw) {
+    const int64_t waves = (nrows + rpw - 1) / rpw;
+    if (const char *e = getenv("G4H_GEMV_WPG")) return atoi(e) < 1 ? 1 : atoi(e) > 8 ? 8 : atoi(e);
+    // minimise the waves of the busiest CU, ceil(grid/256)*wpg, preferring
+    // larger groups (fewer activation stagings) on ties
+    int best = 1;
+    int64_t best_cost = INT64_MAX;
+    for (int w = 1; w <= 8; w++) {
+        const int64_t grid = (waves + w - 1) / w;
+        const int64_t cost = (grid + 255) / 256 * w;
+        if (cost <= best_cost) { best_cost = cost; best = w; }
+    }
+    return best;
+}
+
+template <class F, int NB, int LPR, int UPL>
+static hipError_t go(const g4h_tensor &W, const uint8_t *act, size_t stride, float *Y, int units, hipStream_t s) {
+    constexpr int RPW = 64 / LPR;
+    const int wpg = gemv_waves_per_group(W.nrows, RPW);
+    const int64_t waves = (W.nrows + RPW - 1) / RPW;
+    const unsigned grid = (unsigned)((waves + wpg - 1) / wpg);
+    const size_t lds = act_lds_bytes<F>(NB, W.nb);
+    hipLaunchKernelGGL((k_gemv<F, NB, LPR, UPL>), dim3(grid), dim3(64 * wpg), lds, s, W, act, stride, Y, units);
+    return hipGetLastError();
+}
+
+template <class F, int NB>
+static hipError_t pick(const g4h_tensor &W, const uint8_t *act, size_t stride, float *Y, hipStream_t s, int lpr, int upl) {
+    const int units = (int)(W.nb * F::units_per_block);
+#define G4_CASE(L, U) if (lpr == L && upl == U) return go<F, NB, L, U>(W, act, stride, Y, units, s)
+    G4_CASE(16, 2); G4_CASE(16, 4); G4_CASE(16, 8); G4_CASE(32, 2); G4_CASE(32, 4); G4_CASE(32, 8);
+    G4_CASE(64, 2); G4_CASE(64, 4); G4_CASE(64, 8);
+#undef G4_CASE
+    return hipErrorInvalidValue;
+}
+
+// Lanes per row from the row length only (so the fp32 order never depends on
+// the batch size): the fewest lanes that keep each lane at <= 8 units.
+// one translation unit per format instantiates these
+template <class F>
+hipError_t gemv_format(const g4h_tensor &W, const uint8_t *act, size_t stride, float *Y, int nb, hipStream_t s, int lpr, int upl) {
+    switch (nb) {
+    case 1: return pick<F, 1>(W, act, stride, Y, s, lpr, upl);
+    case 2: return pick<F, 2>(W, act, stride, Y, s, lpr, upl);
+    case 4: return pick<F, 4>(W, act, stride, Y, s, lpr, upl);
+    case 8: return pick<F, 8>(W, act, stride, Y, s, lpr, upl);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+}  // namespace g4

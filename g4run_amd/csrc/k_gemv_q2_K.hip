@@ -1,0 +1,9 @@
+// k_gemv_q2_K.hip -- GEMV instantiations for q2_K weights (see gemv.h).
+#include "gemv.h"
+
+namespace g4 {
+hipError_t launch_gemv_q2_K(const g4h_tensor &W, const uint8_t *act, size_t stride, float *Y, int nb, hipStream_t s, int lpr,
+                          int upl) {
+    return gemv_format<FQ2_K>(W, act, stride, Y, nb, s, lpr, upl);
+}
+}  // namespace g4

@@ -203,7 +203,7 @@ def test_fused_quantizer_equals_prequantized(gpu, oracle, name, qt):
 def test_ragged_shapes(gpu, oracle, name, qt):
     """Row counts that do not fill a workgroup, odd block counts, one row."""
     from g4run_amd import synth
-    for rows, cols in ((1, 256), (3, 768), (67, 1280), (129, 6400)):
+    for rows, cols in ((1, 256), (3, 768), (67, 1280), (129, 6400), (5, 800), (2, 96), (33, 2080)):
         if cols % oracle.BLCK[qt]:
             continue
         w = synth.weights(qt, rows, cols, seed=rows)
