@@ -74,6 +74,9 @@ _SIGS = [
     ("g4h_matmul_ex", _int, [_vp, _vp, _vp, _sz, _vp, _int, _int, _vp]),
     ("g4h_matmul_path", _int, [_vp, _int]),
     ("g4h_block_sums", _int, [_vp, _vp, _sz, _int, _vp, _vp]),
+    ("g4h_attn_workspace_bytes", _sz, [_int, _int, _int]),
+    ("g4h_attn_decode", _int, [_vp, _vp, _vp, _int, _int, _int, _int, _int, _vp, _vp, _sz, _vp]),
+    ("g4h_kv_store", _int, [_int, _vp, _vp, _int, _int, _sz, _vp]),
 ]
 
 _lib = None
@@ -302,3 +305,21 @@ def block_sums(W: Tensor, pre, out, tok: int = 0, pre_stride: int = 0, stream=No
 def n_block_sums(W: Tensor) -> int:
     nb = W.ncols // BLCK[W.type]
     return nb * (2 if W.type in (Q2_K, Q4_K) else 1)
+
+
+# ----------------------------------------------------------------- attention
+def attn_workspace_bytes(n_head: int, hd: int, n_pos: int) -> int:
+    return lib().g4h_attn_workspace_bytes(n_head, hd, n_pos)
+
+
+def attn_decode(q, kc, vc, kv_type: int, n_head: int, n_kv: int, hd: int, n_pos: int, out, ws=None, stream=None) -> None:
+    """attn_kernel for one decode token over cached positions [0, n_pos)."""
+    need = attn_workspace_bytes(n_head, hd, n_pos)
+    if ws is None:
+        ws = Buffer(need)
+    check(lib().g4h_attn_decode(_p(q), _p(kc), _p(vc), kv_type, n_head, n_kv, hd, n_pos, _p(out), _p(ws),
+                                ws.nbytes if isinstance(ws, Buffer) else need, stream))
+
+
+def kv_store(kv_type: int, src, dst, hd: int, rows: int = 1, dst_stride: int = 0, stream=None) -> None:
+    check(lib().g4h_kv_store(kv_type, _p(src), _p(dst), hd, rows, dst_stride, stream))

@@ -384,3 +384,46 @@ extern "C" int g4h_block_sums(const g4h_tensor *W, const void *pre, size_t pre_s
     G4_HIP(launch_block_sums(*W, (const uint8_t *)pre, pre_stride, tok, sums, (hipStream_t)s));
     return G4H_OK;
 }
+
+// ---------------------------------------------------------- attention ----
+extern "C" size_t g4h_attn_workspace_bytes(int n_head, int hd, int n_pos) {
+    if (n_head <= 0 || hd <= 0 || n_pos <= 0) return 0;
+    return attn_workspace_bytes(n_head, hd, n_pos);
+}
+
+static int check_attn_shape(const char *fn, int kv_type, int n_head, int n_kv, int hd) {
+    if (kv_type != F16 && kv_type != Q8_0) return fail(G4H_ERR_TYPE, "%s: KV type %d unsupported (f16, q8_0)", fn, kv_type);
+    if (n_kv <= 0 || n_head <= 0 || n_head % n_kv) return fail(G4H_ERR_SHAPE, "%s: n_head=%d not a multiple of n_kv=%d", fn, n_head, n_kv);
+    const int grp = n_head / n_kv;
+    if (grp != 1 && grp != 2 && grp != 4 && grp != 8) return fail(G4H_ERR_SHAPE, "%s: group size %d unsupported", fn, grp);
+    if (hd % 64 || hd > 256) return fail(G4H_ERR_SHAPE, "%s: hd=%d (must be a multiple of 64, at most 256)", fn, hd);
+    return G4H_OK;
+}
+
+extern "C" int g4h_attn_decode(const float *q, const void *kc, const void *vc, int kv_type, int n_head, int n_kv, int hd,
+                               int n_pos, float *out, void *ws, size_t ws_bytes, void *stream) {
+    G4_NEED_INIT();
+    if (!q || !kc || !vc || !out || !ws) return fail(G4H_ERR_ARG, "g4h_attn_decode: null pointer");
+    if (int rc = check_attn_shape("g4h_attn_decode", kv_type, n_head, n_kv, hd)) return rc;
+    if (n_pos <= 0) return fail(G4H_ERR_ARG, "g4h_attn_decode: n_pos=%d", n_pos);
+    if (ws_bytes < attn_workspace_bytes(n_head, hd, n_pos))
+        return fail(G4H_ERR_ARG, "g4h_attn_decode: workspace %zu < %zu bytes", ws_bytes, attn_workspace_bytes(n_head, hd, n_pos));
+    if ((uintptr_t)kc % 4 || (uintptr_t)vc % 4) return fail(G4H_ERR_ARG, "g4h_attn_decode: caches must be 4-byte aligned");
+    G4_HIP(launch_attn_decode(q, (const uint8_t *)kc, (const uint8_t *)vc, kv_type, n_head, n_kv, hd, n_pos, nullptr, n_pos, out,
+                              (uint8_t *)ws, (hipStream_t)stream));
+    return G4H_OK;
+}
+
+extern "C" int g4h_kv_store(int kv_type, const float *src, void *dst, int hd, int rows, size_t dst_stride, void *stream) {
+    G4_NEED_INIT();
+    if (!src || !dst || hd <= 0 || rows < 0) return fail(G4H_ERR_ARG, "g4h_kv_store: bad argument");
+    if (kv_type != F16 && kv_type != Q8_0 && kv_type != Q4_0) return fail(G4H_ERR_TYPE, "g4h_kv_store: type %d", kv_type);
+    if (hd % blck(kv_type)) return fail(G4H_ERR_SHAPE, "g4h_kv_store: hd=%d", hd);
+    const size_t rb = kv_type == F16 ? (size_t)hd * 2 : g4h_row_size(kv_type, hd);
+    if (dst_stride == 0) dst_stride = rb;
+    if (rows > 1 && dst_stride < rb) return fail(G4H_ERR_ARG, "g4h_kv_store: stride smaller than a row");
+    if ((uintptr_t)dst % 2 || dst_stride % 2) return fail(G4H_ERR_ARG, "g4h_kv_store: destination must be 2-byte aligned");
+    if (rows == 0) return G4H_OK;
+    G4_HIP(launch_kv_store(kv_type, src, (uint8_t *)dst, hd, rows, dst_stride, (hipStream_t)stream));
+    return G4H_OK;
+}

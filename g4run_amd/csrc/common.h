@@ -24,8 +24,16 @@ __host__ __device__ constexpr int bsize(int t) {
 // v_cvt_f32_f16 / v_cvt_f16_f32: exact widening and round-to-nearest-even
 // narrowing; fp16 denormals are kept (gfx9 default FP16 denorm mode), which
 // matters because about 30% of the synthetic q8_0 weight scales are subnormal.
+// The fp32 operand is made opaque first: otherwise the backend folds a
+// preceding multiply into v_fma_mix*_f16, which rounds the exact product to
+// fp16 once instead of rounding to fp32 and then to fp16 as the reference's
+// g4_fp32_to_fp16(x*y) does (and differs from it at fp16 rounding ties).
+__device__ __forceinline__ float opaque(float f) {
+    asm volatile("" : "+v"(f));
+    return f;
+}
 __device__ __forceinline__ float h2f(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
-__device__ __forceinline__ uint16_t f2h(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }
+__device__ __forceinline__ uint16_t f2h(float f) { return __builtin_bit_cast(uint16_t, (_Float16)opaque(f)); }
 
 __device__ __forceinline__ int dot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }
 

@@ -22,4 +22,10 @@ hipError_t launch_gemv(const g4h_tensor &W, const uint8_t *act, size_t stride, f
 hipError_t launch_block_sums(const g4h_tensor &W, const uint8_t *act, size_t stride, int tok, int32_t *out, hipStream_t s);
 int block_sums_per_block(int type);
 
+// k_attn.hip
+size_t attn_workspace_bytes(int n_head, int hd, int npos_max);
+hipError_t launch_attn_decode(const float *q, const uint8_t *kc, const uint8_t *vc, int kv_type, int n_head, int n_kv, int hd,
+                              int npos, const int *npos_dev, int npos_max, float *out, uint8_t *ws, hipStream_t s);
+hipError_t launch_kv_store(int kv_type, const float *src, uint8_t *dst, int hd, int rows, size_t dst_stride, hipStream_t s);
+
 }  // namespace g4

@@ -141,6 +141,24 @@ int g4h_matmul_path(const g4h_tensor *W, int nb);
 int g4h_block_sums(const g4h_tensor *W, const void *pre_dev, size_t pre_stride, int tok,
                    int32_t *sums_dev, void *stream);
 
+/* ---------------------------------------------------------- attention ---- */
+/* Decode attention (attn_kernel, model.c:509-580) for one token: n_head query
+ * heads (q_dev: n_head x hd fp32) over cached positions 0..n_pos-1.  Cache
+ * rows [slot][n_kv][hd] in kv_type (G4H_F16 or G4H_Q8_0) for K and V; query
+ * head h reads KV head h/(n_head/n_kv) (model.c:1099); no 1/sqrt(hd) factor
+ * (model.c:538).  hd in {64,128,192,256}; n_head/n_kv in {1,2,4,8}.
+ * ws_dev: g4h_attn_workspace_bytes() bytes of caller-owned scratch (the
+ * reference's attbuf, model.c:465).  out_dev: n_head x hd fp32. */
+size_t g4h_attn_workspace_bytes(int n_head, int hd, int n_pos);
+int g4h_attn_decode(const float *q_dev, const void *kc_dev, const void *vc_dev, int kv_type,
+                    int n_head, int n_kv, int hd, int n_pos, float *out_dev,
+                    void *ws_dev, size_t ws_bytes, void *stream);
+/* kv_store (model.c:583-589): `rows` rows of hd floats into cache rows
+ * dst_stride bytes apart (0 = packed rows), as f16 (RNE) or q8_0 / q4_0
+ * blocks. */
+int g4h_kv_store(int kv_type, const float *src_dev, void *dst_dev, int hd, int rows,
+                 size_t dst_stride, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -79,6 +79,15 @@ def quant_cases(n):
     e = rng.standard_normal(n); e[1::2] = e[0::2]; rows.append(e)            # repeated magnitudes
     s = rng.standard_normal(n) * 1e-5; rows.append(s)                        # subnormal fp16 scales
     h = np.full(n, 3.0); h[::2] = -3.0; rows.append(h)                       # |max| ties of opposite sign
+    # blocks whose scale amax*fp32(1/127) is an exact fp16 rounding tie (the
+    # fp32 product must be rounded before the fp16 conversion, quants.c:91-92)
+    c = np.float32(1.0 / 127.0)
+    cand = (rng.random(4000000) * 8 + 0.5).astype(np.float32)
+    ties = cand[((cand * c).view(np.uint32) & 0x1FFF) == 0x1000][: 2 * n // 32]
+    t2 = (rng.standard_normal((ties.size, 32)) * 0.2).astype(np.float32)
+    t2[:, 5] = ties * np.where(np.arange(ties.size) % 2, 1, -1)
+    t2 = t2.reshape(-1)
+    rows.append(t2[:n]); rows.append(t2[n:2 * n])
     return np.array(rows, dtype=np.float32)
 
 
