@@ -134,6 +134,70 @@ def cpu_baseline(sets, seconds: float):
         g4o.use_reference_dots(False)
 
 
+def bench_decode(G, steps: int, cpu_seconds: float, want_cpu: bool):
+    """tokens/s of the full decode step at context ~8192."""
+    m = G.Model(seed=1)
+    m.fill_kv(seed=2)
+    c = m.cfg
+    st = G.Stream()
+    pos0 = c["n_ctx"] - steps
+    m.set_state(1, pos0, st.ptr)
+    graph = G.Graph(st.ptr, lambda: m.forward_state(st.ptr))
+    graph.launch(st.ptr)                 # warm replay
+    st.synchronize()
+    m.set_state(1, pos0, st.ptr)
+    e0, e1 = G.Event(), G.Event()
+    e0.record(st.ptr)
+    for _ in range(steps):
+        graph.launch(st.ptr)
+    e1.record(st.ptr)
+    ms = e0.elapsed_ms(e1)
+    tok, pos = m.get_state(st.ptr)
+    assert pos == c["n_ctx"], pos
+    ms_tok = ms / steps
+    mean_ctx = pos0 + (steps + 1) / 2.0
+    kv_row = c["head_dim"] * 2
+    kv_bytes = 2 * c["n_layer"] * mean_ctx * c["n_kv"] * kv_row
+    alg = m.weight_bytes + kv_bytes
+    out = {"tok_per_s": round(1e3 / ms_tok, 1), "ms_per_token": round(ms_tok, 4), "steps": steps,
+           "positions": [pos0, c["n_ctx"] - 1], "alg_bytes_per_token": int(alg),
+           "GBps": round(alg / (ms_tok * 1e-3) / 1e9, 1),
+           "roofline_tok_per_s": round(PEAK_HBM * 1e9 / alg, 1),
+           "model": "26 layers, d_model 2560, 8 q / 4 kv heads x 256, FFN 10240 gated-GELU, q4_0 weights, "
+                    "q8_0 tied 32768-vocab head, f16 KV, greedy; one HIP graph per step"}
+    log(f"bench: decode {out['tok_per_s']} tok/s ({ms_tok:.3f} ms/token, {out['GBps']} GB/s algorithmic)")
+    if want_cpu:
+        from oracle import g4o
+        if g4o.ref_available():
+            w, kc, vc = m.host_copy()
+            om = g4o.Model({"n_layer": c["n_layer"], "n_embd": c["n_embd"], "n_head": c["n_head"], "n_kv": c["n_kv"],
+                            "hd": c["head_dim"], "n_ff": c["n_ff"], "n_vocab": c["n_vocab"], "n_ctx": c["n_ctx"],
+                            "rope_base": c["rope_base"], "eps": c["rms_eps"], "kv_type": c["kv_type"],
+                            "wtype": c["wtype"], "head_type": c["head_type"]}, w, kc, vc)
+            threads = min(physical_cores(), 32, 16)
+            g4o.use_reference_dots(True)
+            g4o.pool_start(threads)
+            try:
+                times, t_end, p = [], time.perf_counter() + cpu_seconds, c["n_ctx"] - 64
+                while time.perf_counter() < t_end or len(times) < 2:
+                    t0 = time.perf_counter()
+                    om.decode(1, p)
+                    times.append(time.perf_counter() - t0)
+                    p = p + 1 if p + 1 < c["n_ctx"] else c["n_ctx"] - 64
+            finally:
+                g4o.pool_stop()
+                g4o.use_reference_dots(False)
+            med = float(np.median(times))
+            out["cpu_baseline"] = {"tok_per_s": round(1 / med, 2), "ms_per_token": round(med * 1e3, 2), "cores": threads,
+                                   "kind": "reference",
+                                   "sample": f"{len(times)} decode steps at positions 8128..8191 of the same model "
+                                             "(weights and KV copied from the GPU); reference AVX2 dots incl. g4_dot_f16 "
+                                             "for scores; pthread row split (model.c:59-65), heads in parallel (model.c:706)"}
+            log(f"bench: cpu decode {out['cpu_baseline']['tok_per_s']} tok/s on {threads} threads")
+    m.free()
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -142,6 +206,7 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--all-configs", action="store_true", help="also time every GEMV config (stderr + JSON)")
+    ap.add_argument("--decode-steps", type=int, default=64, help="decode steps timed at context ~8192 (0 = skip)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (--gpus {args.gpus} requested); "
@@ -191,6 +256,10 @@ def main():
             del s
 
     cpu = None if args.no_cpu else cpu_baseline(sets, args.cpu_seconds)
+    for s_ in sets:
+        for t in s_.W:
+            t.free()
+    decode = bench_decode(G, args.decode_steps, args.cpu_seconds, not args.no_cpu) if args.decode_steps > 0 else None
     out = {
         "metric": "quant GEMV HBM GB/s (% peak) + decode tokens/sec, 1xMI355X vs host CPU",
         "value": round(value, 1),
@@ -216,6 +285,8 @@ def main():
     }
     if extra:
         out["configs"] = extra
+    if decode:
+        out["decode"] = decode
     print(json.dumps(out), flush=True)
 
 

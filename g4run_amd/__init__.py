@@ -77,6 +77,18 @@ _SIGS = [
     ("g4h_attn_workspace_bytes", _sz, [_int, _int, _int]),
     ("g4h_attn_decode", _int, [_vp, _vp, _vp, _int, _int, _int, _int, _int, _vp, _vp, _sz, _vp]),
     ("g4h_kv_store", _int, [_int, _vp, _vp, _int, _int, _sz, _vp]),
+    ("g4h_model_create", _int, [_vp, C.c_uint64, C.POINTER(_vp)]),
+    ("g4h_model_free", _int, [_vp]),
+    ("g4h_model_fill_kv", _int, [_vp, C.c_uint64, _vp]),
+    ("g4h_forward", _int, [_vp, _int, _int, C.POINTER(_int), _vp]),
+    ("g4h_forward_state", _int, [_vp, _vp]),
+    ("g4h_model_set_state", _int, [_vp, _int, _int, _vp]),
+    ("g4h_model_get_state", _int, [_vp, C.POINTER(_int), C.POINTER(_int), _vp]),
+    ("g4h_model_logits", _vp, [_vp]),
+    ("g4h_model_matrix", _vp, [_vp, _int, _int]),
+    ("g4h_model_norm", _vp, [_vp, _int, _int]),
+    ("g4h_model_kv", _int, [_vp, _int, C.POINTER(_vp), C.POINTER(_vp), C.POINTER(_sz)]),
+    ("g4h_model_weight_bytes", _sz, [_vp]),
 ]
 
 _lib = None
@@ -323,3 +335,128 @@ def attn_decode(q, kc, vc, kv_type: int, n_head: int, n_kv: int, hd: int, n_pos:
 
 def kv_store(kv_type: int, src, dst, hd: int, rows: int = 1, dst_stride: int = 0, stream=None) -> None:
     check(lib().g4h_kv_store(kv_type, _p(src), _p(dst), hd, rows, dst_stride, stream))
+
+
+# ---------------------------------------------------------------- decode step
+class ModelConfig(C.Structure):
+    _fields_ = [("n_layer", _int), ("n_embd", _int), ("n_head", _int), ("n_kv", _int), ("head_dim", _int),
+                ("n_ff", _int), ("n_vocab", _int), ("n_ctx", _int), ("rope_base", C.c_float), ("rms_eps", C.c_float),
+                ("wtype", _int), ("head_type", _int), ("kv_type", _int)]
+
+
+# 26 layers, d_model 2560, 8 q heads / 4 KV heads of
+# 256, gated-GELU FFN 10240, RoPE theta 1e6, q4_0 weights, q8_0 vocab-32768
+# head, f16 KV cache of 8192 positions
+GEMMA_STYLE = dict(n_layer=26, n_embd=2560, n_head=8, n_kv=4, head_dim=256, n_ff=10240, n_vocab=32768, n_ctx=8192,
+                   rope_base=1e6, rms_eps=1e-6, wtype=Q4_0, head_type=Q8_0, kv_type=F16)
+
+_MATS = {"wqkv": 0, "wo": 1, "wgu": 2, "wdown": 3}
+_NORMS = {"attn_norm": 0, "q_norm": 1, "k_norm": 2, "post_attn_norm": 3, "ffn_norm": 4, "post_ffw_norm": 5}
+
+
+class _View:
+    """A borrowed device tensor (owned by the model)."""
+
+    def __init__(self, ptr):
+        self.ptr = ptr
+        t, nc, nr = _int(), _i64(), _i64()
+        check(lib().g4h_tensor_info(ptr, C.byref(t), C.byref(nc), C.byref(nr)))
+        self.type, self.ncols, self.nrows = t.value, nc.value, nr.value
+
+    def to_rows(self) -> np.ndarray:
+        rs = row_size(self.type, self.ncols)
+        b = Buffer(rs * self.nrows)
+        check(lib().g4h_tensor_store(self.ptr, b.ptr, None))
+        return b.download(np.uint8, (self.nrows, rs))
+
+
+class Model:
+    """Device-resident decoder (g4h_model) and its decode step."""
+
+    def __init__(self, seed: int = 1, **cfg):
+        init()
+        c = dict(GEMMA_STYLE)
+        c.update(cfg)
+        self.cfg = c
+        self._c = ModelConfig(**c)
+        p = _vp()
+        check(lib().g4h_model_create(C.byref(self._c), seed, C.byref(p)))
+        self.ptr = p.value
+
+    def fill_kv(self, seed: int = 2, stream=None) -> None:
+        check(lib().g4h_model_fill_kv(self.ptr, seed, stream))
+
+    def forward(self, token: int, pos: int, stream=None) -> int:
+        nxt = _int()
+        check(lib().g4h_forward(self.ptr, token, pos, C.byref(nxt), stream))
+        return nxt.value
+
+    def forward_state(self, stream=None) -> None:
+        check(lib().g4h_forward_state(self.ptr, stream))
+
+    def set_state(self, token: int, pos: int, stream=None) -> None:
+        check(lib().g4h_model_set_state(self.ptr, token, pos, stream))
+
+    def get_state(self, stream=None):
+        t, p = _int(), _int()
+        check(lib().g4h_model_get_state(self.ptr, C.byref(t), C.byref(p), stream))
+        return t.value, p.value
+
+    def logits(self) -> np.ndarray:
+        n = self.cfg["n_vocab"]
+        out = np.empty(n, np.float32)
+        check(lib().g4h_memcpy_d2h(out.ctypes.data_as(_vp), lib().g4h_model_logits(self.ptr), n * 4, None))
+        return out
+
+    @property
+    def weight_bytes(self) -> int:
+        return lib().g4h_model_weight_bytes(self.ptr)
+
+    def matrix(self, layer: int, name: str) -> _View:
+        return _View(lib().g4h_model_matrix(self.ptr, layer, 4 if name == "head" else _MATS[name]))
+
+    def norm(self, layer: int, name: str) -> np.ndarray:
+        c = self.cfg
+        n = c["head_dim"] if name in ("q_norm", "k_norm") else c["n_embd"]
+        p = lib().g4h_model_norm(self.ptr, layer, 6 if name == "output_norm" else _NORMS[name])
+        out = np.empty(n, np.float32)
+        check(lib().g4h_memcpy_d2h(out.ctypes.data_as(_vp), p, n * 4, None))
+        return out
+
+    def kv(self, layer: int):
+        k, v, nb = _vp(), _vp(), _sz()
+        check(lib().g4h_model_kv(self.ptr, layer, C.byref(k), C.byref(v), C.byref(nb)))
+        out = []
+        for p in (k, v):
+            a = np.empty(nb.value, np.uint8)
+            check(lib().g4h_memcpy_d2h(a.ctypes.data_as(_vp), p.value, nb.value, None))
+            out.append(a)
+        return out
+
+    def host_copy(self):
+        """Every parameter and the KV cache as host arrays (for a CPU check)."""
+        c = self.cfg
+        w = {k: [] for k in list(_MATS) + list(_NORMS)}
+        kc, vc = [], []
+        for l in range(c["n_layer"]):
+            for k in _MATS:
+                w[k].append(self.matrix(l, k).to_rows())
+            for k in _NORMS:
+                w[k].append(self.norm(l, k))
+            a, b = self.kv(l)
+            kc.append(a)
+            vc.append(b)
+        w["head"] = self.matrix(0, "head").to_rows()
+        w["output_norm"] = self.norm(0, "output_norm")
+        return w, kc, vc
+
+    def free(self):
+        if getattr(self, "ptr", None):
+            check(lib().g4h_model_free(self.ptr))
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass

@@ -39,6 +39,8 @@ static std::atomic<int> g_fail_alloc{0};
     do { if (g_device < 0) return fail(G4H_ERR_DEVICE, "g4h_init() has not been called"); } while (0)
 
 extern "C" const char *g4h_last_error(void) { return g_err; }
+// status + message for the library's other host files (not part of the ABI)
+extern "C" int g4h_internal_fail(int status, const char *msg) { return fail(status, "%s", msg); }
 
 extern "C" const char *g4h_status_str(int s) {
     switch (s) {
@@ -410,7 +412,7 @@ extern "C" int g4h_attn_decode(const float *q, const void *kc, const void *vc, i
         return fail(G4H_ERR_ARG, "g4h_attn_decode: workspace %zu < %zu bytes", ws_bytes, attn_workspace_bytes(n_head, hd, n_pos));
     if ((uintptr_t)kc % 4 || (uintptr_t)vc % 4) return fail(G4H_ERR_ARG, "g4h_attn_decode: caches must be 4-byte aligned");
     G4_HIP(launch_attn_decode(q, (const uint8_t *)kc, (const uint8_t *)vc, kv_type, n_head, n_kv, hd, n_pos, nullptr, n_pos, out,
-                              (uint8_t *)ws, (hipStream_t)stream));
+                              nullptr, (uint8_t *)ws, (hipStream_t)stream));
     return G4H_OK;
 }
 

@@ -25,7 +25,8 @@ int block_sums_per_block(int type);
 // k_attn.hip
 size_t attn_workspace_bytes(int n_head, int hd, int npos_max);
 hipError_t launch_attn_decode(const float *q, const uint8_t *kc, const uint8_t *vc, int kv_type, int n_head, int n_kv, int hd,
-                              int npos, const int *npos_dev, int npos_max, float *out, uint8_t *ws, hipStream_t s);
+                              int npos, const int *npos_dev, int npos_max, float *out, uint8_t *q8out, uint8_t *ws,
+                              hipStream_t s);
 hipError_t launch_kv_store(int kv_type, const float *src, uint8_t *dst, int hd, int rows, size_t dst_stride, hipStream_t s);
 
 }  // namespace g4

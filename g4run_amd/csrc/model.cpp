@@ -1,0 +1,358 @@
+// model.cpp -- a synthetic gemma-style decoder resident on one MI355X and its
+// decode step (the GPU form of g4_forward / forward_layers, g4run.h:309-311,
+// model.c:593-775), built from this library's kernels.
+//
+// Per layer (model.c:647-736 without the gemma4-only per-layer embeddings,
+// sliding-window ring, shared KV and softcap):
+//   x <- x + rms(prev)*post_norm (fused into the next norm kernel)
+//   a  = q8_0(rms(x)*attn_norm)            k_norm_quant
+//   qkv = Wqkv a                            GEMV (fused q|k|v rows)
+//   q,k <- rms(.)*q_norm/k_norm, RoPE; v <- rms(v); store k,v at pos
+//   o  = attention(q, K[0..pos], V[0..pos])  split-K attention
+//   y  = Wo q8_0(o);  x <- x + rms(y)*post_attn_norm; a = q8_0(rms(x)*ffn_norm)
+//   g|u = Wgu a;  h = q8_0(gelu(g)*u);  y = Wdown h
+// then x <- x + rms(y)*post_ffw_norm, a = q8_0(rms(x)*output_norm),
+// logits = Head a (tied q8_0 embedding), token = argmax.
+#include "../../include/g4hip.h"
+
+#include <algorithm>
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <vector>
+
+#include "kernels.h"
+
+using namespace g4;
+
+extern "C" int g4h_internal_fail(int status, const char *msg);
+
+namespace g4 {
+hipError_t launch_rand_normal(float *y, int64_t n, uint64_t seed, float mean, float std, hipStream_t s);
+hipError_t launch_embed_planes(const g4h_tensor &head, const int *token, float *x, float es, hipStream_t s);
+hipError_t launch_norm_quant(float *x, const float *delta, const float *w_post, const float *w_pre, float eps, int n,
+                             uint8_t *act, float *xb_out, hipStream_t s);
+hipError_t launch_qkv_prep(const float *qkv, int n_head, int n_kv, int hd, const float *q_norm, const float *k_norm, float eps,
+                           const float *rope, const int *pos, float *q_out, uint8_t *kc, uint8_t *vc, int kv_type, hipStream_t s);
+hipError_t launch_gelu_quant(const float *gu, int n_ff, const uint16_t *tab, uint8_t *act, hipStream_t s);
+hipError_t launch_argmax_advance(const float *logits, int n, int *token, int *pos, int *npos, int advance, hipStream_t s);
+}  // namespace g4
+
+// Host-side fp16 conversions for building the GELU table, written from the
+// IEEE-754 binary16 definition (round to nearest even, gradual underflow).
+static float host_h2f(uint16_t h) {
+    const uint32_t sign = (uint32_t)(h >> 15) << 31, e = (h >> 10) & 31u, m = h & 1023u;
+    uint32_t u;
+    if (e == 31) u = sign | 0x7f800000u | (m << 13);
+    else if (e == 0) {
+        if (m == 0) u = sign;
+        else {
+            float f = std::ldexp((float)m, -24);
+            std::memcpy(&u, &f, 4);
+            u |= sign;
+        }
+    } else u = sign | ((e + 112u) << 23) | (m << 13);
+    float f;
+    std::memcpy(&f, &u, 4);
+    return f;
+}
+static uint16_t host_f2h(float f) {
+    uint32_t u;
+    std::memcpy(&u, &f, 4);
+    const uint16_t sign = (uint16_t)((u >> 16) & 0x8000u);
+    const uint32_t mag = u & 0x7fffffffu;
+    if (mag > 0x7f800000u) return (uint16_t)(sign | 0x7e00u | ((mag >> 13) & 1023u ? (mag >> 13) & 1023u : 1u));
+    if (mag >= 0x47800000u) return (uint16_t)(sign | 0x7c00u);
+    if (mag < 0x38800000u) {
+        // subnormal result: value / 2^-24 rounded half-even
+        const float scaled = std::fabs(f) * 16777216.0f;           // exact (power-of-two scaling)
+        return (uint16_t)(sign | (uint16_t)std::nearbyint(scaled));
+    }
+    const uint32_t r = mag + 0x0fffu + ((mag >> 13) & 1u);
+    return (uint16_t)(sign | ((r - 0x38000000u) >> 13));
+}
+
+struct g4h_model {
+    g4h_model_config c;
+    std::vector<g4h_tensor *> wqkv, wo, wgu, wdown;
+    g4h_tensor *head = nullptr;
+    float *norms = nullptr;          // [n_layer][6][n_embd-or-hd] + output norm
+    size_t norm_stride = 0;          // floats per (layer, which) slot
+    uint8_t *kv = nullptr;           // all caches
+    size_t kv_layer_bytes = 0;       // one of K or V for one layer
+    float *rope = nullptr;           // [n_ctx][hd] cos/sin pairs
+    uint16_t *gelu = nullptr;        // 65536 fp16 codes
+    int *state = nullptr;            // token, pos, npos
+    float *x = nullptr, *xb = nullptr, *qkv = nullptr, *q = nullptr, *att = nullptr, *ff = nullptr, *logits = nullptr;
+    uint8_t *act = nullptr, *ws = nullptr;
+    size_t act_bytes = 0, ws_bytes = 0;
+    std::vector<void *> allocs;
+};
+
+static int model_alloc(g4h_model *m, void **p, size_t bytes) {
+    if (int rc = g4h_malloc(p, bytes)) return rc;
+    m->allocs.push_back(*p);
+    return G4H_OK;
+}
+
+#define M_HIP(call)                                                                \
+    do {                                                                           \
+        hipError_t e_ = (call);                                                    \
+        if (e_ != hipSuccess) return g4h_internal_fail(G4H_ERR_HIP, hipGetErrorString(e_)); \
+    } while (0)
+#define M_RC(call)                  \
+    do {                            \
+        int rc_ = (call);           \
+        if (rc_) return rc_;        \
+    } while (0)
+
+// random matrix: N(0, std) fp32 -> quantized GGUF rows -> resident tensor
+static int init_matrix_into(int type, int64_t rows, int64_t cols, uint64_t seed, float *tmp_f, uint8_t *tmp_q,
+                            g4h_tensor *t, hipStream_t s);
+static int init_matrix(g4h_model *m, int type, int64_t rows, int64_t cols, uint64_t seed, float *tmp_f, uint8_t *tmp_q,
+                       g4h_tensor **out, hipStream_t s) {
+    (void)m;
+    M_RC(g4h_tensor_create(type, cols, rows, out));
+    const int rc = init_matrix_into(type, rows, cols, seed, tmp_f, tmp_q, *out, s);
+    if (rc) { g4h_tensor_free(*out); *out = nullptr; }
+    return rc;
+}
+static int init_matrix_into(int type, int64_t rows, int64_t cols, uint64_t seed, float *tmp_f, uint8_t *tmp_q,
+                            g4h_tensor *t, hipStream_t s) {
+    M_HIP(launch_rand_normal(tmp_f, rows * cols, seed, 0.0f, 0.02f, s));
+    const size_t rb = g4h_row_size(type, cols);
+    if (type == Q8_0) M_HIP(launch_quantize_q8_0(tmp_f, cols, tmp_q, rb, cols, (int)rows, s));
+    else if (type == Q4_0) M_HIP(launch_quantize_q4_0(tmp_f, cols, tmp_q, rb, cols, (int)rows, s));
+    else return g4h_internal_fail(G4H_ERR_TYPE, "g4h_model_create: weights must be q4_0 or q8_0");
+    M_RC(g4h_tensor_load(t, tmp_q, 1, s));
+    return G4H_OK;
+}
+
+extern "C" int g4h_model_create(const g4h_model_config *cfg, uint64_t seed, g4h_model **out) {
+    if (!cfg || !out) return g4h_internal_fail(G4H_ERR_ARG, "g4h_model_create: null argument");
+    *out = nullptr;
+    const g4h_model_config &c = *cfg;
+    if (c.n_layer <= 0 || c.n_embd <= 0 || c.n_head <= 0 || c.n_kv <= 0 || c.n_ff <= 0 || c.n_vocab <= 0 || c.n_ctx <= 0)
+        return g4h_internal_fail(G4H_ERR_ARG, "g4h_model_create: non-positive dimension");
+    if (c.n_embd % 32 || c.n_ff % 256 || c.head_dim % 64 || c.head_dim > 256 || c.n_head % c.n_kv || c.n_embd > 8192)
+        return g4h_internal_fail(G4H_ERR_SHAPE, "g4h_model_create: n_embd%32, n_ff%256, head_dim%64 (<=256), n_head%n_kv");
+    if ((c.wtype != Q4_0 && c.wtype != Q8_0) || c.head_type != Q8_0 || (c.kv_type != F16 && c.kv_type != Q8_0))
+        return g4h_internal_fail(G4H_ERR_TYPE, "g4h_model_create: wtype q4_0|q8_0, head q8_0, kv f16|q8_0");
+    g4h_model *m = new g4h_model();
+    m->c = c;
+    const int E = c.n_embd, H = c.n_head, KV = c.n_kv, hd = c.head_dim, F = c.n_ff;
+    const int qkv_rows = (H + 2 * KV) * hd, qd = H * hd;
+    hipStream_t s = nullptr;
+    int rc = G4H_OK;
+    auto bail = [&](int r) { g4h_model_free(m); return r; };
+
+    // scratch for init: the largest matrix as fp32 and as GGUF rows
+    int64_t big = (int64_t)c.n_vocab * E;
+    big = std::max(big, (int64_t)2 * F * E);
+    big = std::max(big, (int64_t)qkv_rows * E);
+    big = std::max(big, (int64_t)E * F);
+    float *tmp_f = nullptr;
+    uint8_t *tmp_q = nullptr;
+    if ((rc = g4h_malloc((void **)&tmp_f, big * 4))) return bail(rc);
+    if ((rc = g4h_malloc((void **)&tmp_q, big * 2))) { g4h_free(tmp_f); return bail(rc); }
+    uint64_t k = seed * 0x100000001b3ull + 17;
+    for (int l = 0; l < c.n_layer && !rc; l++) {
+        g4h_tensor *t;
+        if ((rc = init_matrix(m, c.wtype, qkv_rows, E, k++, tmp_f, tmp_q, &t, s))) break;
+        m->wqkv.push_back(t);
+        if ((rc = init_matrix(m, c.wtype, E, qd, k++, tmp_f, tmp_q, &t, s))) break;
+        m->wo.push_back(t);
+        if ((rc = init_matrix(m, c.wtype, 2 * F, E, k++, tmp_f, tmp_q, &t, s))) break;
+        m->wgu.push_back(t);
+        if ((rc = init_matrix(m, c.wtype, E, F, k++, tmp_f, tmp_q, &t, s))) break;
+        m->wdown.push_back(t);
+    }
+    if (!rc) rc = init_matrix(m, c.head_type, c.n_vocab, E, k++, tmp_f, tmp_q, &m->head, s);
+    hipStreamSynchronize(s);
+    g4h_free(tmp_f);
+    g4h_free(tmp_q);
+    if (rc) return bail(rc);
+
+    // norm weights ~ N(1, 0.05): [layer][6] slots of max(E, hd) floats + output norm
+    m->norm_stride = (size_t)std::max(E, hd);
+    const size_t n_norm = ((size_t)c.n_layer * 6 + 1) * m->norm_stride;
+    if ((rc = model_alloc(m, (void **)&m->norms, n_norm * 4))) return bail(rc);
+    if (launch_rand_normal(m->norms, (int64_t)n_norm, k++, 1.0f, 0.05f, s) != hipSuccess) return bail(G4H_ERR_HIP);
+
+    // KV caches: [layer][K|V][n_ctx][n_kv][row]
+    const size_t row = c.kv_type == F16 ? (size_t)hd * 2 : g4h_row_size(Q8_0, hd);
+    m->kv_layer_bytes = (size_t)c.n_ctx * KV * row;
+    if ((rc = model_alloc(m, (void **)&m->kv, m->kv_layer_bytes * 2 * c.n_layer))) return bail(rc);
+    hipMemsetAsync(m->kv, 0, m->kv_layer_bytes * 2 * c.n_layer, s);
+
+    // RoPE table, built as rope_cache (model.c:349-358) for every position
+    std::vector<float> rope((size_t)c.n_ctx * hd);
+    const float theta_scale = powf(c.rope_base, -2.0f / hd);
+    for (int p = 0; p < c.n_ctx; p++) {
+        float theta = (float)p;
+        for (int i = 0; i < hd / 2; i++) {
+            rope[(size_t)p * hd + 2 * i] = cosf(theta);
+            rope[(size_t)p * hd + 2 * i + 1] = sinf(theta);
+            theta *= theta_scale;
+        }
+    }
+    if ((rc = model_alloc(m, (void **)&m->rope, rope.size() * 4))) return bail(rc);
+    hipMemcpy(m->rope, rope.data(), rope.size() * 4, hipMemcpyHostToDevice);
+
+    // GELU fp16 table (quants.c:48-58)
+    std::vector<uint16_t> gt(65536);
+    for (uint32_t h = 0; h < 65536; h++) {
+        const float x = host_h2f((uint16_t)h);
+        const float g = 0.5f * x * (1.0f + tanhf(0.79788456080286535587989211986876f * x * (1.0f + 0.044715f * x * x)));
+        gt[h] = host_f2h(g);
+    }
+    if ((rc = model_alloc(m, (void **)&m->gelu, 65536 * 2))) return bail(rc);
+    hipMemcpy(m->gelu, gt.data(), 65536 * 2, hipMemcpyHostToDevice);
+
+    // activations and state
+    const int wide = std::max(std::max(E, 2 * F), std::max(qkv_rows, c.n_vocab));
+    if ((rc = model_alloc(m, (void **)&m->state, 64))) return bail(rc);
+    if ((rc = model_alloc(m, (void **)&m->x, E * 4))) return bail(rc);
+    if ((rc = model_alloc(m, (void **)&m->xb, E * 4))) return bail(rc);
+    if ((rc = model_alloc(m, (void **)&m->qkv, qkv_rows * 4))) return bail(rc);
+    if ((rc = model_alloc(m, (void **)&m->q, qd * 4))) return bail(rc);
+    if ((rc = model_alloc(m, (void **)&m->att, qd * 4))) return bail(rc);
+    if ((rc = model_alloc(m, (void **)&m->ff, 2 * F * 4))) return bail(rc);
+    if ((rc = model_alloc(m, (void **)&m->logits, (size_t)c.n_vocab * 4))) return bail(rc);
+    m->act_bytes = (g4h_row_size(Q8_0, std::max(E, std::max(F, qd))) + 63) & ~(size_t)63;
+    if ((rc = model_alloc(m, (void **)&m->act, m->act_bytes))) return bail(rc);
+    m->ws_bytes = g4h_attn_workspace_bytes(H, hd, c.n_ctx);
+    if ((rc = model_alloc(m, (void **)&m->ws, m->ws_bytes))) return bail(rc);
+    (void)wide;
+    hipMemset(m->state, 0, 64);
+    if (hipDeviceSynchronize() != hipSuccess) return bail(g4h_internal_fail(G4H_ERR_HIP, "g4h_model_create: init kernels failed"));
+    *out = m;
+    return G4H_OK;
+}
+
+extern "C" int g4h_model_free(g4h_model *m) {
+    if (!m) return G4H_OK;
+    for (auto *v : {&m->wqkv, &m->wo, &m->wgu, &m->wdown})
+        for (g4h_tensor *t : *v) g4h_tensor_free(t);
+    g4h_tensor_free(m->head);
+    for (void *p : m->allocs) g4h_free(p);
+    delete m;
+    return G4H_OK;
+}
+
+extern "C" int g4h_model_fill_kv(g4h_model *m, uint64_t seed, void *stream) {
+    if (!m) return g4h_internal_fail(G4H_ERR_ARG, "g4h_model_fill_kv: null model");
+    const hipStream_t s = (hipStream_t)stream;
+    const g4h_model_config &c = m->c;
+    const int64_t n = (int64_t)c.n_ctx * c.n_kv * c.head_dim;
+    float *tmp;
+    M_RC(g4h_malloc((void **)&tmp, n * 4));
+    const size_t row = c.kv_type == F16 ? (size_t)c.head_dim * 2 : g4h_row_size(Q8_0, c.head_dim);
+    for (int i = 0; i < 2 * c.n_layer; i++) {
+        launch_rand_normal(tmp, n, seed * 7919 + i, 0.0f, 1.0f, s);
+        launch_kv_store(c.kv_type, tmp, m->kv + (size_t)i * m->kv_layer_bytes, c.head_dim, (int)(n / c.head_dim), row, s);
+    }
+    hipStreamSynchronize(s);
+    g4h_free(tmp);
+    return G4H_OK;
+}
+
+static float *norm_of(g4h_model *m, int layer, int which) {
+    return m->norms + ((size_t)layer * 6 + which) * m->norm_stride;
+}
+
+// one decode step from the device state (token, pos); advances it
+extern "C" int g4h_forward_state(g4h_model *m, void *stream) {
+    if (!m) return g4h_internal_fail(G4H_ERR_ARG, "g4h_forward_state: null model");
+    const hipStream_t s = (hipStream_t)stream;
+    const g4h_model_config &c = m->c;
+    const int E = c.n_embd, H = c.n_head, KV = c.n_kv, hd = c.head_dim, F = c.n_ff;
+    int *token = m->state, *pos = m->state + 1, *npos = m->state + 2;
+    const size_t ast = m->act_bytes;
+    M_HIP(launch_embed_planes(*m->head, token, m->x, sqrtf((float)E), s));
+    for (int l = 0; l < c.n_layer; l++) {
+        uint8_t *kc = m->kv + (size_t)(2 * l) * m->kv_layer_bytes, *vc = kc + m->kv_layer_bytes;
+        M_HIP(launch_norm_quant(m->x, l ? m->xb : nullptr, l ? norm_of(m, l - 1, G4H_N_POST_FFW) : nullptr,
+                                norm_of(m, l, G4H_N_ATTN), c.rms_eps, E, m->act, nullptr, s));
+        M_HIP(launch_gemv(*m->wqkv[l], m->act, ast, m->qkv, 1, s));
+        M_HIP(launch_qkv_prep(m->qkv, H, KV, hd, norm_of(m, l, G4H_N_Q), norm_of(m, l, G4H_N_K), c.rms_eps, m->rope, pos, m->q,
+                              kc, vc, c.kv_type, s));
+        M_HIP(launch_attn_decode(m->q, kc, vc, c.kv_type, H, KV, hd, 0, npos, c.n_ctx, m->att, m->act, m->ws, s));
+        M_HIP(launch_gemv(*m->wo[l], m->act, ast, m->xb, 1, s));
+        M_HIP(launch_norm_quant(m->x, m->xb, norm_of(m, l, G4H_N_POST_ATTN), norm_of(m, l, G4H_N_FFN), c.rms_eps, E, m->act,
+                                nullptr, s));
+        M_HIP(launch_gemv(*m->wgu[l], m->act, ast, m->ff, 1, s));
+        M_HIP(launch_gelu_quant(m->ff, F, m->gelu, m->act, s));
+        M_HIP(launch_gemv(*m->wdown[l], m->act, ast, m->xb, 1, s));
+    }
+    M_HIP(launch_norm_quant(m->x, m->xb, norm_of(m, c.n_layer - 1, G4H_N_POST_FFW), norm_of(m, c.n_layer, 0), c.rms_eps, E,
+                            m->act, nullptr, s));
+    M_HIP(launch_gemv(*m->head, m->act, ast, m->logits, 1, s));
+    M_HIP(launch_argmax_advance(m->logits, c.n_vocab, token, pos, npos, 1, s));
+    return G4H_OK;
+}
+
+extern "C" int g4h_model_set_state(g4h_model *m, int token, int pos, void *stream) {
+    if (!m) return g4h_internal_fail(G4H_ERR_ARG, "g4h_model_set_state: null model");
+    if (pos < 0 || pos >= m->c.n_ctx) return g4h_internal_fail(G4H_ERR_ARG, "g4h_model_set_state: pos outside the context");
+    if (token < 0 || token >= m->c.n_vocab) return g4h_internal_fail(G4H_ERR_ARG, "g4h_model_set_state: token out of range");
+    const int st[3] = {token, pos, pos + 1};
+    M_HIP(hipMemcpyAsync(m->state, st, sizeof st, hipMemcpyHostToDevice, (hipStream_t)stream));
+    M_HIP(hipStreamSynchronize((hipStream_t)stream));
+    return G4H_OK;
+}
+
+extern "C" int g4h_model_get_state(g4h_model *m, int *token, int *pos, void *stream) {
+    if (!m) return g4h_internal_fail(G4H_ERR_ARG, "g4h_model_get_state: null model");
+    int st[3];
+    M_HIP(hipMemcpyAsync(st, m->state, sizeof st, hipMemcpyDeviceToHost, (hipStream_t)stream));
+    M_HIP(hipStreamSynchronize((hipStream_t)stream));
+    if (token) *token = st[0];
+    if (pos) *pos = st[1];
+    return G4H_OK;
+}
+
+extern "C" int g4h_forward(g4h_model *m, int token, int pos, int *next_token, void *stream) {
+    M_RC(g4h_model_set_state(m, token, pos, stream));
+    M_RC(g4h_forward_state(m, stream));
+    if (next_token) M_RC(g4h_model_get_state(m, next_token, nullptr, stream));
+    return G4H_OK;
+}
+
+extern "C" const float *g4h_model_logits(const g4h_model *m) { return m ? m->logits : nullptr; }
+
+extern "C" g4h_tensor *g4h_model_matrix(g4h_model *m, int layer, int which) {
+    if (!m) return nullptr;
+    if (which == G4H_W_HEAD) return m->head;
+    if (layer < 0 || layer >= m->c.n_layer) return nullptr;
+    switch (which) {
+    case G4H_W_QKV: return m->wqkv[layer];
+    case G4H_W_O: return m->wo[layer];
+    case G4H_W_GU: return m->wgu[layer];
+    case G4H_W_DOWN: return m->wdown[layer];
+    default: return nullptr;
+    }
+}
+
+extern "C" float *g4h_model_norm(g4h_model *m, int layer, int which) {
+    if (!m) return nullptr;
+    if (which == G4H_N_OUTPUT) return norm_of(m, m->c.n_layer, 0);
+    if (layer < 0 || layer >= m->c.n_layer || which < 0 || which > 5) return nullptr;
+    return norm_of(m, layer, which);
+}
+
+extern "C" int g4h_model_kv(g4h_model *m, int layer, void **k_dev, void **v_dev, size_t *bytes) {
+    if (!m || layer < 0 || layer >= m->c.n_layer) return g4h_internal_fail(G4H_ERR_ARG, "g4h_model_kv: bad layer");
+    if (k_dev) *k_dev = m->kv + (size_t)(2 * layer) * m->kv_layer_bytes;
+    if (v_dev) *v_dev = m->kv + (size_t)(2 * layer + 1) * m->kv_layer_bytes;
+    if (bytes) *bytes = m->kv_layer_bytes;
+    return G4H_OK;
+}
+
+extern "C" size_t g4h_model_weight_bytes(const g4h_model *m) {
+    if (!m) return 0;
+    size_t b = 0;
+    for (const auto *v : {&m->wqkv, &m->wo, &m->wgu, &m->wdown})
+        for (const g4h_tensor *t : *v) b += (size_t)t->nrows * g4h_row_size(t->type, t->ncols);
+    return b + (size_t)m->head->nrows * g4h_row_size(m->head->type, m->head->ncols);
+}

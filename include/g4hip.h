@@ -159,6 +159,48 @@ int g4h_attn_decode(const float *q_dev, const void *kc_dev, const void *vc_dev, 
 int g4h_kv_store(int kv_type, const float *src_dev, void *dst_dev, int hd, int rows,
                  size_t dst_stride, void *stream);
 
+/* -------------------------------------------------------- decode step ---- */
+/* A gemma-style decoder resident on the device (the model behind
+ * g4_ctx_init / g4_forward, g4run.h:303-311): layer order of model.c:647-736
+ * (RMSNorm, fused QKV projection, q/k RMSNorm + NeoX RoPE, KV store, attention,
+ * Wo, post-attention norm + residual, fused gate/up, GELU(gate)*up, down,
+ * post-FFN norm + residual), a tied q8_0 embedding / output head
+ * (model.c:605-612, 766-769) and greedy argmax (sampler.c:139-144).  Weights
+ * are random-initialised on the device: N(0, 0.02) quantized with the q4_0 /
+ * q8_0 quantizers, norm weights N(1, 0.05). */
+typedef struct {
+    int n_layer, n_embd, n_head, n_kv, head_dim, n_ff, n_vocab, n_ctx;
+    float rope_base, rms_eps;
+    int wtype;       /* layer weights: G4H_Q4_0 or G4H_Q8_0 */
+    int head_type;   /* G4H_Q8_0 */
+    int kv_type;     /* G4H_F16 or G4H_Q8_0 */
+} g4h_model_config;
+typedef struct g4h_model g4h_model;
+
+enum { G4H_W_QKV = 0, G4H_W_O = 1, G4H_W_GU = 2, G4H_W_DOWN = 3, G4H_W_HEAD = 4 };
+enum { G4H_N_ATTN = 0, G4H_N_Q = 1, G4H_N_K = 2, G4H_N_POST_ATTN = 3, G4H_N_FFN = 4,
+       G4H_N_POST_FFW = 5, G4H_N_OUTPUT = 6 };
+
+int  g4h_model_create(const g4h_model_config *cfg, uint64_t seed, g4h_model **out);
+int  g4h_model_free(g4h_model *m);
+/* Fill every KV slot of every layer with N(0,1) values (stored as kv_type). */
+int  g4h_model_fill_kv(g4h_model *m, uint64_t seed, void *stream);
+/* g4_forward (g4run.h:309-311): one decode step for `token` at `pos`
+ * (synchronous); logits stay on the device (g4h_model_logits), the greedy next
+ * token is returned in *next_token. */
+int  g4h_forward(g4h_model *m, int token, int pos, int *next_token, void *stream);
+/* The same step reading token/pos from device state and advancing it
+ * (token <- argmax, pos <- pos+1): asynchronous, capturable in a graph. */
+int  g4h_forward_state(g4h_model *m, void *stream);
+int  g4h_model_set_state(g4h_model *m, int token, int pos, void *stream);
+int  g4h_model_get_state(g4h_model *m, int *token, int *pos, void *stream);
+const float *g4h_model_logits(const g4h_model *m);
+/* Parameter access (for checking against a CPU implementation). */
+g4h_tensor *g4h_model_matrix(g4h_model *m, int layer, int which);
+float      *g4h_model_norm(g4h_model *m, int layer, int which);
+int         g4h_model_kv(g4h_model *m, int layer, void **k_dev, void **v_dev, size_t *bytes);
+size_t      g4h_model_weight_bytes(const g4h_model *m);
+
 #ifdef __cplusplus
 }
 #endif

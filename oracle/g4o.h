@@ -94,6 +94,8 @@ void g4o_parallel_for(int64_t total, g4o_pf_fn fn, void *ud);
  *      either this restatement or the reference's compiled kernels ---- */
 typedef float (*g4o_dot_fn)(const void *w, const void *a, int64_t n);
 void g4o_set_dot_fn(int wtype, g4o_dot_fn fn);  /* NULL restores the restatement */
+typedef float (*g4o_dot_f16_fn)(const void *w, const uint16_t *a, int64_t n);
+void g4o_set_dot_f16_fn(g4o_dot_f16_fn fn);      /* attention's f16 score dot */
 
 /* ---- norms, rope, gelu, argmax (model.c:338-367, g4run.h:73-77, quants.c:49-58,
  *      sampler.c:139-144) ---- */

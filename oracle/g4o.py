@@ -83,6 +83,7 @@ def lib():
         L.g4o_pool_start.argtypes = [C.c_int]
         L.g4o_pool_stop.argtypes = []
         L.g4o_set_dot_fn.argtypes = [C.c_int, _vp]
+        L.g4o_set_dot_f16_fn.argtypes = [_vp]
         L.g4o_rms_norm.argtypes = [_vp, _vp, _vp, C.c_int, C.c_float]
         L.g4o_rope_cache.argtypes = [_vp, C.c_int, C.c_int, C.c_float]
         L.g4o_rope_apply.argtypes = [_vp, _vp, C.c_int]
@@ -234,6 +235,7 @@ def use_reference_dots(enable: bool) -> None:
     for t, nm in DOT_NAME.items():
         fn = C.cast(getattr(ref(), "g4_dot_" + nm), _vp) if enable else None
         L.g4o_set_dot_fn(t, fn)
+    L.g4o_set_dot_f16_fn(C.cast(ref().g4_dot_f16, _vp) if enable else None)
 
 
 def pool_start(n: int) -> None:

@@ -12,6 +12,9 @@
 
 #include <math.h>
 #include <pthread.h>
+#if defined(__F16C__) && defined(__FMA__)
+#include <immintrin.h>
+#endif
 #include <stdlib.h>
 #include <string.h>
 
@@ -37,6 +40,11 @@ static g4o_dot_fn dot_for(int wtype) {
 }
 void g4o_set_dot_fn(int wtype, g4o_dot_fn fn) {
     if (wtype >= 0 && wtype < 16) dot_override[wtype] = fn;
+}
+static g4o_dot_f16_fn dot_f16_override;
+void g4o_set_dot_f16_fn(g4o_dot_f16_fn fn) { dot_f16_override = fn; }
+static float dot_f16(const uint16_t *w, const uint16_t *a, int64_t n) {
+    return dot_f16_override ? dot_f16_override(w, a, n) : g4o_dot_f16(w, a, n);
 }
 
 /* ---------------------------------------------------------- thread pool -- */
@@ -255,8 +263,8 @@ static void attn_heads(int64_t h0, int64_t h1, void *p, int tid) {
         for (int j = 0; j < nv; j++) {
             const uint8_t *krow = u->kc + ((size_t)j * u->n_kv + kvh) * u->row_bytes;
             float s;
-            if (u->kv_type == G4O_F16) s = g4o_dot_f16((const uint16_t *)krow, q16, hd);
-            else s = g4o_dot(u->kv_type, krow, q8, hd);
+            if (u->kv_type == G4O_F16) s = dot_f16((const uint16_t *)krow, q16, hd);
+            else s = dot_for(u->kv_type)(krow, q8, hd);
             att[j] = s;
             if (s > mx) mx = s;
         }
@@ -269,7 +277,17 @@ static void attn_heads(int64_t h0, int64_t h1, void *p, int tid) {
             if (u->kv_type == G4O_F16) {
                 const float wj = g4o_fp16_to_fp32(g4o_fp32_to_fp16(att[j] * inv));
                 const uint16_t *v = (const uint16_t *)vrow;
+#if defined(__F16C__) && defined(__FMA__)
+                /* model.c:553-562: 8 elements per step, F16C widening + FMA
+                 * (element-wise identical to the scalar form below) */
+                const __m256 wv = _mm256_set1_ps(wj);
+                for (int i = 0; i < hd; i += 8) {
+                    const __m256 vf = _mm256_cvtph_ps(_mm_loadu_si128((const __m128i *)(v + i)));
+                    _mm256_storeu_ps(o + i, _mm256_fmadd_ps(wv, vf, _mm256_loadu_ps(o + i)));
+                }
+#else
                 for (int i = 0; i < hd; i++) o[i] = fmaf(wj, g4o_fp16_to_fp32(v[i]), o[i]);
+#endif
             } else {
                 const float wj = att[j] * inv;
                 g4o_dequant_row(u->kv_type, vrow, vtmp, hd);

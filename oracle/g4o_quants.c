@@ -47,8 +47,15 @@ static inline uint32_t f2u(float f) { uint32_t u; memcpy(&u, &f, 4); return u; }
 static inline float u2f(uint32_t u) { float f; memcpy(&f, &u, 4); return f; }
 
 /* Half -> single, exact for every code (quants.c:27-46): subnormal halves are
- * normalised by shifting the significand up until its hidden bit appears. */
-float g4o_fp16_to_fp32(uint16_t h) {
+ * normalised by shifting the significand up until its hidden bit appears.
+ * Looked up in a table built once at load (as g4_init_tables does). */
+static float fp16_compute(uint16_t h);
+static float fp16_tab[65536];
+__attribute__((constructor)) static void fp16_tab_init(void) {
+    for (uint32_t i = 0; i < 65536; i++) fp16_tab[i] = fp16_compute((uint16_t)i);
+}
+float g4o_fp16_to_fp32(uint16_t h) { return fp16_tab[h]; }
+static float fp16_compute(uint16_t h) {
     uint32_t sign = (uint32_t)(h >> 15) << 31;
     uint32_t e = (h >> 10) & 31u, m = h & 1023u;
     if (e == 31) return u2f(sign | 0x7f800000u | (m << 13));

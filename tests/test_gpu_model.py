@@ -1,0 +1,81 @@
+"""The decode step (g4_forward) on the GPU against the CPU oracle's restated
+graph on identical weights and KV cache.
+
+Bar: the greedy token is identical, and the logits agree to within 1e-3 of the
+logit range.  The per-element 1e-3/1e-5 bar of the single kernels does not
+carry through a multi-layer stack: q8_0 re-quantization of activations between
+layers turns an fp32-order difference of one ulp into an occasional one-step
+change of an 8-bit code, so the stack is held to the range-relative bar.
+"""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+SMALL = dict(n_layer=2, n_embd=256, n_head=4, n_kv=2, head_dim=64, n_ff=512, n_vocab=512, n_ctx=64,
+             rope_base=1e6, rms_eps=1e-6)
+
+
+def oracle_model(oracle, G, m):
+    w, kc, vc = m.host_copy()
+    cfg = dict(m.cfg)
+    ocfg = dict(n_layer=cfg["n_layer"], n_embd=cfg["n_embd"], n_head=cfg["n_head"], n_kv=cfg["n_kv"],
+                hd=cfg["head_dim"], n_ff=cfg["n_ff"], n_vocab=cfg["n_vocab"], n_ctx=cfg["n_ctx"],
+                rope_base=cfg["rope_base"], eps=cfg["rms_eps"], kv_type=cfg["kv_type"], wtype=cfg["wtype"],
+                head_type=cfg["head_type"])
+    return oracle.Model(ocfg, w, kc, vc)
+
+
+@pytest.mark.parametrize("kv_type,wtype", [(1, 2), (8, 2), (1, 8)], ids=["f16-q4_0", "q8_0-q4_0", "f16-q8_0"])
+def test_decode_steps_match_oracle(gpu, oracle, kv_type, wtype):
+    G = gpu
+    m = G.Model(seed=11, kv_type=kv_type, wtype=wtype, **SMALL)
+    m.fill_kv(seed=12)
+    om = oracle_model(oracle, G, m)
+    tok, pos = 7, 40
+    for step in range(4):
+        nxt = m.forward(tok, pos)
+        lg = m.logits()
+        otok, olg = om.decode(tok, pos)
+        rng = float(olg.max() - olg.min())
+        err = float(np.abs(lg.astype(np.float64) - olg).max())
+        assert err <= 1e-3 * rng, f"step {step}: max logit diff {err:.3g} vs range {rng:.3g}"
+        assert nxt == int(np.argmax(lg))
+        top2 = np.sort(olg)[-2:]
+        if top2[1] - top2[0] > 2e-3 * rng:          # not a near-tie
+            assert nxt == otok, f"step {step}: token {nxt} vs oracle {otok}"
+        tok, pos = otok, pos + 1
+    m.free()
+
+
+def test_graph_replay_matches_eager(gpu):
+    """The state-driven step captured once and replayed gives the same tokens
+    and logits as eager calls, advancing the position each replay."""
+    G = gpu
+    m = G.Model(seed=3, **SMALL)
+    m.fill_kv(seed=4)
+    eager = []
+    tok = 5
+    for pos in range(20, 24):
+        tok = m.forward(tok, pos)
+        eager.append((tok, m.logits()))
+    m2 = G.Model(seed=3, **SMALL)
+    m2.fill_kv(seed=4)
+    st = G.Stream()
+    m2.set_state(5, 20, st.ptr)
+    g = G.Graph(st.ptr, lambda: m2.forward_state(st.ptr))
+    for i in range(4):
+        g.launch(st.ptr)
+        st.synchronize()
+        t, p = m2.get_state(st.ptr)
+        assert p == 21 + i
+        assert t == eager[i][0]
+        assert np.array_equal(m2.logits().view(np.uint32), eager[i][1].view(np.uint32))
+
+
+def test_model_bad_config(gpu):
+    G = gpu
+    with pytest.raises(G.G4HError):
+        G.Model(**dict(SMALL, head_dim=96))
+    with pytest.raises(G.G4HError):
+        G.Model(**dict(SMALL, kv_type=G.Q4_K))
