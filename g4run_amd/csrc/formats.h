@@ -59,6 +59,9 @@ __device__ __forceinline__ void stage_q8_0_load(StageQ8_0 &S, int item, const ui
     S.ok = item < NB * npair;
     S.t = S.ok ? item / npair : 0;
     S.pr = S.ok ? item - S.t * npair : 0;
+    // every register is defined on both paths, so the item stays in registers
+#pragma unroll
+    for (int k = 0; k < 17; k++) S.v[k] = 0;
     if (S.ok) {
         const uint32_t *src = (const uint32_t *)(act + (size_t)S.t * stride + (size_t)S.pr * 68);
 #pragma unroll
@@ -130,6 +133,8 @@ __device__ __forceinline__ void stage_q8_K_load(StageQ8_K &S, int item, const ui
     const int r = it - S.t * per;
     S.sb = r / 17;
     S.c = r - S.sb * 17;
+#pragma unroll
+    for (int k = 0; k < 9; k++) S.v[k] = 0;
     if (S.ok) {
         const uint32_t *src = (const uint32_t *)(act + (size_t)S.t * stride) + (size_t)S.sb * 73;
         if (S.c < 16) {

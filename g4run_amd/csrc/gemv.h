@@ -129,11 +129,12 @@ static hipError_t pick(const g4h_tensor &W, const uint8_t *act, size_t stride, f
     return hipErrorInvalidValue;
 }
 
-// Lanes per row from the row length only (so the fp32 order never depends on
-// the batch size): the fewest lanes that keep each lane at <= 8 units.
 // one translation unit per format instantiates these
 template <class F>
 hipError_t gemv_format(const g4h_tensor &W, const uint8_t *act, size_t stride, float *Y, int nb, hipStream_t s, int lpr, int upl) {
+    // eight K-quant tokens with more units in flight exceed the register file;
+    // a lane visits its units in the same order for any UPL, so results are unchanged
+    if (F::units_per_block == 4 && nb == 8 && upl > 2) upl = 2;
     switch (nb) {
     case 1: return pick<F, 1>(W, act, stride, Y, s, lpr, upl);
     case 2: return pick<F, 2>(W, act, stride, Y, s, lpr, upl);

@@ -16,11 +16,30 @@ hipError_t launch_vec_dot_raw(int wtype, const uint8_t *w, size_t ws, const uint
                               hipStream_t s);
 
 // k_gemv.hip
+
 void gemv_shape(int type, int64_t nblk, int *lpr, int *upl);
 size_t gemv_lds_bytes(int type, int nb_tokens, int64_t nblk);
 hipError_t launch_gemv(const g4h_tensor &W, const uint8_t *act, size_t stride, float *Y, int nb, hipStream_t s);
 hipError_t launch_block_sums(const g4h_tensor &W, const uint8_t *act, size_t stride, int tok, int32_t *out, hipStream_t s);
 int block_sums_per_block(int type);
+
+// k_model.hip: the decode step's single-workgroup steps (steps.h)
+struct QkvArgs {
+    int n_head = 0, n_kv = 0, hd = 0, kv_type = 0;
+    const float *q_norm = nullptr, *k_norm = nullptr, *rope = nullptr;
+    const int *pos = nullptr;
+    float *q_out = nullptr;
+    uint8_t *kc = nullptr, *vc = nullptr;
+    float eps = 0.0f;
+};
+hipError_t launch_rand_normal(float *y, int64_t n, uint64_t seed, float mean, float std, hipStream_t s);
+hipError_t launch_embed_norm(const g4h_tensor &head, const int *token, float *x, float es, const float *w_pre, float eps,
+                             uint8_t *act, hipStream_t s);
+hipError_t launch_norm_quant(float *x, const float *delta, const float *w_post, const float *w_pre, float eps, int n,
+                             uint8_t *act, hipStream_t s);
+hipError_t launch_qkv_prep(const float *qkv, const QkvArgs &a, hipStream_t s);
+hipError_t launch_gelu_quant(const float *gu, int n_ff, const uint16_t *tab, uint8_t *act, hipStream_t s);
+hipError_t launch_argmax_advance(const float *logits, int n, int *state, hipStream_t s);
 
 // k_attn.hip
 size_t attn_workspace_bytes(int n_head, int hd, int npos_max);

@@ -4,15 +4,17 @@
 //
 // Per layer (model.c:647-736 without the gemma4-only per-layer embeddings,
 // sliding-window ring, shared KV and softcap):
-//   x <- x + rms(prev)*post_norm (fused into the next norm kernel)
-//   a  = q8_0(rms(x)*attn_norm)            k_norm_quant
-//   qkv = Wqkv a                            GEMV (fused q|k|v rows)
-//   q,k <- rms(.)*q_norm/k_norm, RoPE; v <- rms(v); store k,v at pos
-//   o  = attention(q, K[0..pos], V[0..pos])  split-K attention
-//   y  = Wo q8_0(o);  x <- x + rms(y)*post_attn_norm; a = q8_0(rms(x)*ffn_norm)
-//   g|u = Wgu a;  h = q8_0(gelu(g)*u);  y = Wdown h
+//   a  = q8_0(rms(x)*attn_norm), x <- x + rms(prev)*post_ffw_norm first    k_norm_quant
+//   qkv = Wqkv a                                                            GEMV
+//   q,k <- rms(.)*q_norm/k_norm, RoPE; v <- rms(v); k,v stored at pos     k_qkv_prep
+//   o  = attention(q, K[0..pos], V[0..pos])     scores, softmax, V, combine (+ q8_0(o))
+//   y  = Wo q8_0(o)                                                         GEMV
+//   x <- x + rms(y)*post_attn_norm; a = q8_0(rms(x)*ffn_norm)               k_norm_quant
+//   g|u = Wgu a;  a = q8_0(gelu(g)*u)                                 GEMV, k_gelu_quant
+//   y  = Wdown a                                                            GEMV
 // then x <- x + rms(y)*post_ffw_norm, a = q8_0(rms(x)*output_norm),
-// logits = Head a (tied q8_0 embedding), token = argmax.
+// logits = Head a (tied q8_0 embedding), token = argmax.  The embedding
+// kernel also produces the first layer's a.
 #include "../../include/g4hip.h"
 
 #include <algorithm>
@@ -27,16 +29,6 @@ using namespace g4;
 
 extern "C" int g4h_internal_fail(int status, const char *msg);
 
-namespace g4 {
-hipError_t launch_rand_normal(float *y, int64_t n, uint64_t seed, float mean, float std, hipStream_t s);
-hipError_t launch_embed_planes(const g4h_tensor &head, const int *token, float *x, float es, hipStream_t s);
-hipError_t launch_norm_quant(float *x, const float *delta, const float *w_post, const float *w_pre, float eps, int n,
-                             uint8_t *act, float *xb_out, hipStream_t s);
-hipError_t launch_qkv_prep(const float *qkv, int n_head, int n_kv, int hd, const float *q_norm, const float *k_norm, float eps,
-                           const float *rope, const int *pos, float *q_out, uint8_t *kc, uint8_t *vc, int kv_type, hipStream_t s);
-hipError_t launch_gelu_quant(const float *gu, int n_ff, const uint16_t *tab, uint8_t *act, hipStream_t s);
-hipError_t launch_argmax_advance(const float *logits, int n, int *token, int *pos, int *npos, int advance, hipStream_t s);
-}  // namespace g4
 
 // Host-side fp16 conversions for building the GELU table, written from the
 // IEEE-754 binary16 definition (round to nearest even, gradual underflow).
@@ -107,25 +99,20 @@ static int model_alloc(g4h_model *m, void **p, size_t bytes) {
     } while (0)
 
 // random matrix: N(0, std) fp32 -> quantized GGUF rows -> resident tensor
-static int init_matrix_into(int type, int64_t rows, int64_t cols, uint64_t seed, float *tmp_f, uint8_t *tmp_q,
-                            g4h_tensor *t, hipStream_t s);
-static int init_matrix(g4h_model *m, int type, int64_t rows, int64_t cols, uint64_t seed, float *tmp_f, uint8_t *tmp_q,
-                       g4h_tensor **out, hipStream_t s) {
-    (void)m;
+// random matrix: N(0, std) fp32 -> quantized GGUF rows -> resident tensor
+static int init_matrix(int type, int64_t rows, int64_t cols, uint64_t seed, float *tmp_f, uint8_t *tmp_q, g4h_tensor **out,
+                       hipStream_t s) {
+    if (type != Q8_0 && type != Q4_0) return g4h_internal_fail(G4H_ERR_TYPE, "g4h_model_create: weights must be q4_0 or q8_0");
     M_RC(g4h_tensor_create(type, cols, rows, out));
-    const int rc = init_matrix_into(type, rows, cols, seed, tmp_f, tmp_q, *out, s);
+    const size_t rb = g4h_row_size(type, cols);
+    hipError_t e = launch_rand_normal(tmp_f, rows * cols, seed, 0.0f, 0.02f, s);
+    if (e == hipSuccess)
+        e = type == Q8_0 ? launch_quantize_q8_0(tmp_f, cols, tmp_q, rb, cols, (int)rows, s)
+                         : launch_quantize_q4_0(tmp_f, cols, tmp_q, rb, cols, (int)rows, s);
+    int rc = e == hipSuccess ? G4H_OK : g4h_internal_fail(G4H_ERR_HIP, hipGetErrorString(e));
+    if (!rc) rc = g4h_tensor_load(*out, tmp_q, 1, s);
     if (rc) { g4h_tensor_free(*out); *out = nullptr; }
     return rc;
-}
-static int init_matrix_into(int type, int64_t rows, int64_t cols, uint64_t seed, float *tmp_f, uint8_t *tmp_q,
-                            g4h_tensor *t, hipStream_t s) {
-    M_HIP(launch_rand_normal(tmp_f, rows * cols, seed, 0.0f, 0.02f, s));
-    const size_t rb = g4h_row_size(type, cols);
-    if (type == Q8_0) M_HIP(launch_quantize_q8_0(tmp_f, cols, tmp_q, rb, cols, (int)rows, s));
-    else if (type == Q4_0) M_HIP(launch_quantize_q4_0(tmp_f, cols, tmp_q, rb, cols, (int)rows, s));
-    else return g4h_internal_fail(G4H_ERR_TYPE, "g4h_model_create: weights must be q4_0 or q8_0");
-    M_RC(g4h_tensor_load(t, tmp_q, 1, s));
-    return G4H_OK;
 }
 
 extern "C" int g4h_model_create(const g4h_model_config *cfg, uint64_t seed, g4h_model **out) {
@@ -134,8 +121,9 @@ extern "C" int g4h_model_create(const g4h_model_config *cfg, uint64_t seed, g4h_
     const g4h_model_config &c = *cfg;
     if (c.n_layer <= 0 || c.n_embd <= 0 || c.n_head <= 0 || c.n_kv <= 0 || c.n_ff <= 0 || c.n_vocab <= 0 || c.n_ctx <= 0)
         return g4h_internal_fail(G4H_ERR_ARG, "g4h_model_create: non-positive dimension");
-    if (c.n_embd % 32 || c.n_ff % 256 || c.head_dim % 64 || c.head_dim > 256 || c.n_head % c.n_kv || c.n_embd > 8192)
-        return g4h_internal_fail(G4H_ERR_SHAPE, "g4h_model_create: n_embd%32, n_ff%256, head_dim%64 (<=256), n_head%n_kv");
+    if (c.n_embd % 32 || c.n_ff % 256 || c.head_dim % 64 || c.head_dim > 256 || c.n_head % c.n_kv || c.n_embd > 8192 ||
+        c.n_ff % 32)
+        return g4h_internal_fail(G4H_ERR_SHAPE, "g4h_model_create: n_embd%32 (<=8192), n_ff%256, head_dim%64 (<=256), n_head%n_kv");
     if ((c.wtype != Q4_0 && c.wtype != Q8_0) || c.head_type != Q8_0 || (c.kv_type != F16 && c.kv_type != Q8_0))
         return g4h_internal_fail(G4H_ERR_TYPE, "g4h_model_create: wtype q4_0|q8_0, head q8_0, kv f16|q8_0");
     g4h_model *m = new g4h_model();
@@ -158,20 +146,21 @@ extern "C" int g4h_model_create(const g4h_model_config *cfg, uint64_t seed, g4h_
     uint64_t k = seed * 0x100000001b3ull + 17;
     for (int l = 0; l < c.n_layer && !rc; l++) {
         g4h_tensor *t;
-        if ((rc = init_matrix(m, c.wtype, qkv_rows, E, k++, tmp_f, tmp_q, &t, s))) break;
+        if ((rc = init_matrix(c.wtype, qkv_rows, E, k++, tmp_f, tmp_q, &t, s))) break;
         m->wqkv.push_back(t);
-        if ((rc = init_matrix(m, c.wtype, E, qd, k++, tmp_f, tmp_q, &t, s))) break;
+        if ((rc = init_matrix(c.wtype, E, qd, k++, tmp_f, tmp_q, &t, s))) break;
         m->wo.push_back(t);
-        if ((rc = init_matrix(m, c.wtype, 2 * F, E, k++, tmp_f, tmp_q, &t, s))) break;
+        if ((rc = init_matrix(c.wtype, 2 * F, E, k++, tmp_f, tmp_q, &t, s))) break;
         m->wgu.push_back(t);
-        if ((rc = init_matrix(m, c.wtype, E, F, k++, tmp_f, tmp_q, &t, s))) break;
+        if ((rc = init_matrix(c.wtype, E, F, k++, tmp_f, tmp_q, &t, s))) break;
         m->wdown.push_back(t);
     }
-    if (!rc) rc = init_matrix(m, c.head_type, c.n_vocab, E, k++, tmp_f, tmp_q, &m->head, s);
-    hipStreamSynchronize(s);
+    if (!rc) rc = init_matrix(c.head_type, c.n_vocab, E, k++, tmp_f, tmp_q, &m->head, s);
+    const hipError_t init_err = hipStreamSynchronize(s);
     g4h_free(tmp_f);
     g4h_free(tmp_q);
     if (rc) return bail(rc);
+    if (init_err != hipSuccess) return bail(g4h_internal_fail(G4H_ERR_HIP, hipGetErrorString(init_err)));
 
     // norm weights ~ N(1, 0.05): [layer][6] slots of max(E, hd) floats + output norm
     m->norm_stride = (size_t)std::max(E, hd);
@@ -183,7 +172,7 @@ extern "C" int g4h_model_create(const g4h_model_config *cfg, uint64_t seed, g4h_
     const size_t row = c.kv_type == F16 ? (size_t)hd * 2 : g4h_row_size(Q8_0, hd);
     m->kv_layer_bytes = (size_t)c.n_ctx * KV * row;
     if ((rc = model_alloc(m, (void **)&m->kv, m->kv_layer_bytes * 2 * c.n_layer))) return bail(rc);
-    hipMemsetAsync(m->kv, 0, m->kv_layer_bytes * 2 * c.n_layer, s);
+    if (hipMemsetAsync(m->kv, 0, m->kv_layer_bytes * 2 * c.n_layer, s) != hipSuccess) return bail(G4H_ERR_HIP);
 
     // RoPE table, built as rope_cache (model.c:349-358) for every position
     std::vector<float> rope((size_t)c.n_ctx * hd);
@@ -197,7 +186,7 @@ extern "C" int g4h_model_create(const g4h_model_config *cfg, uint64_t seed, g4h_
         }
     }
     if ((rc = model_alloc(m, (void **)&m->rope, rope.size() * 4))) return bail(rc);
-    hipMemcpy(m->rope, rope.data(), rope.size() * 4, hipMemcpyHostToDevice);
+    if (hipMemcpy(m->rope, rope.data(), rope.size() * 4, hipMemcpyHostToDevice) != hipSuccess) return bail(G4H_ERR_HIP);
 
     // GELU fp16 table (quants.c:48-58)
     std::vector<uint16_t> gt(65536);
@@ -207,7 +196,7 @@ extern "C" int g4h_model_create(const g4h_model_config *cfg, uint64_t seed, g4h_
         gt[h] = host_f2h(g);
     }
     if ((rc = model_alloc(m, (void **)&m->gelu, 65536 * 2))) return bail(rc);
-    hipMemcpy(m->gelu, gt.data(), 65536 * 2, hipMemcpyHostToDevice);
+    if (hipMemcpy(m->gelu, gt.data(), 65536 * 2, hipMemcpyHostToDevice) != hipSuccess) return bail(G4H_ERR_HIP);
 
     // activations and state
     const int wide = std::max(std::max(E, 2 * F), std::max(qkv_rows, c.n_vocab));
@@ -224,7 +213,7 @@ extern "C" int g4h_model_create(const g4h_model_config *cfg, uint64_t seed, g4h_
     m->ws_bytes = g4h_attn_workspace_bytes(H, hd, c.n_ctx);
     if ((rc = model_alloc(m, (void **)&m->ws, m->ws_bytes))) return bail(rc);
     (void)wide;
-    hipMemset(m->state, 0, 64);
+    if (hipMemset(m->state, 0, 64) != hipSuccess) return bail(G4H_ERR_HIP);
     if (hipDeviceSynchronize() != hipSuccess) return bail(g4h_internal_fail(G4H_ERR_HIP, "g4h_model_create: init kernels failed"));
     *out = m;
     return G4H_OK;
@@ -248,12 +237,16 @@ extern "C" int g4h_model_fill_kv(g4h_model *m, uint64_t seed, void *stream) {
     float *tmp;
     M_RC(g4h_malloc((void **)&tmp, n * 4));
     const size_t row = c.kv_type == F16 ? (size_t)c.head_dim * 2 : g4h_row_size(Q8_0, c.head_dim);
-    for (int i = 0; i < 2 * c.n_layer; i++) {
-        launch_rand_normal(tmp, n, seed * 7919 + i, 0.0f, 1.0f, s);
-        launch_kv_store(c.kv_type, tmp, m->kv + (size_t)i * m->kv_layer_bytes, c.head_dim, (int)(n / c.head_dim), row, s);
+    hipError_t e = hipSuccess;
+    for (int i = 0; i < 2 * c.n_layer && e == hipSuccess; i++) {
+        e = launch_rand_normal(tmp, n, seed * 7919 + i, 0.0f, 1.0f, s);
+        if (e == hipSuccess)
+            e = launch_kv_store(c.kv_type, tmp, m->kv + (size_t)i * m->kv_layer_bytes, c.head_dim, (int)(n / c.head_dim), row, s);
     }
-    hipStreamSynchronize(s);
+    const hipError_t e2 = hipStreamSynchronize(s);
     g4h_free(tmp);
+    if (e != hipSuccess || e2 != hipSuccess)
+        return g4h_internal_fail(G4H_ERR_HIP, hipGetErrorString(e != hipSuccess ? e : e2));
     return G4H_OK;
 }
 
@@ -269,26 +262,38 @@ extern "C" int g4h_forward_state(g4h_model *m, void *stream) {
     const int E = c.n_embd, H = c.n_head, KV = c.n_kv, hd = c.head_dim, F = c.n_ff;
     int *token = m->state, *pos = m->state + 1, *npos = m->state + 2;
     const size_t ast = m->act_bytes;
-    M_HIP(launch_embed_planes(*m->head, token, m->x, sqrtf((float)E), s));
+    M_HIP(launch_embed_norm(*m->head, token, m->x, sqrtf((float)E), norm_of(m, 0, G4H_N_ATTN), c.rms_eps, m->act, s));
     for (int l = 0; l < c.n_layer; l++) {
         uint8_t *kc = m->kv + (size_t)(2 * l) * m->kv_layer_bytes, *vc = kc + m->kv_layer_bytes;
-        M_HIP(launch_norm_quant(m->x, l ? m->xb : nullptr, l ? norm_of(m, l - 1, G4H_N_POST_FFW) : nullptr,
-                                norm_of(m, l, G4H_N_ATTN), c.rms_eps, E, m->act, nullptr, s));
+        if (l) M_HIP(launch_norm_quant(m->x, m->xb, norm_of(m, l - 1, G4H_N_POST_FFW), norm_of(m, l, G4H_N_ATTN), c.rms_eps, E,
+                                       m->act, s));
         M_HIP(launch_gemv(*m->wqkv[l], m->act, ast, m->qkv, 1, s));
-        M_HIP(launch_qkv_prep(m->qkv, H, KV, hd, norm_of(m, l, G4H_N_Q), norm_of(m, l, G4H_N_K), c.rms_eps, m->rope, pos, m->q,
-                              kc, vc, c.kv_type, s));
+        QkvArgs qa;
+        qa.n_head = H;
+        qa.n_kv = KV;
+        qa.hd = hd;
+        qa.kv_type = c.kv_type;
+        qa.q_norm = norm_of(m, l, G4H_N_Q);
+        qa.k_norm = norm_of(m, l, G4H_N_K);
+        qa.rope = m->rope;
+        qa.pos = pos;
+        qa.q_out = m->q;
+        qa.kc = kc;
+        qa.vc = vc;
+        qa.eps = c.rms_eps;
+        M_HIP(launch_qkv_prep(m->qkv, qa, s));
         M_HIP(launch_attn_decode(m->q, kc, vc, c.kv_type, H, KV, hd, 0, npos, c.n_ctx, m->att, m->act, m->ws, s));
         M_HIP(launch_gemv(*m->wo[l], m->act, ast, m->xb, 1, s));
-        M_HIP(launch_norm_quant(m->x, m->xb, norm_of(m, l, G4H_N_POST_ATTN), norm_of(m, l, G4H_N_FFN), c.rms_eps, E, m->act,
-                                nullptr, s));
+        M_HIP(launch_norm_quant(m->x, m->xb, norm_of(m, l, G4H_N_POST_ATTN), norm_of(m, l, G4H_N_FFN), c.rms_eps, E, m->act, s));
         M_HIP(launch_gemv(*m->wgu[l], m->act, ast, m->ff, 1, s));
         M_HIP(launch_gelu_quant(m->ff, F, m->gelu, m->act, s));
         M_HIP(launch_gemv(*m->wdown[l], m->act, ast, m->xb, 1, s));
     }
     M_HIP(launch_norm_quant(m->x, m->xb, norm_of(m, c.n_layer - 1, G4H_N_POST_FFW), norm_of(m, c.n_layer, 0), c.rms_eps, E,
-                            m->act, nullptr, s));
+                            m->act, s));
     M_HIP(launch_gemv(*m->head, m->act, ast, m->logits, 1, s));
-    M_HIP(launch_argmax_advance(m->logits, c.n_vocab, token, pos, npos, 1, s));
+    M_HIP(launch_argmax_advance(m->logits, c.n_vocab, m->state, s));
+    (void)token;
     return G4H_OK;
 }
 

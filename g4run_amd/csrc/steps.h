@@ -1,0 +1,185 @@
+// steps.h -- the single-workgroup steps of the decode chain between the
+// GEMVs: residual + RMSNorm + q8_0, q/k/v head preparation, GELU + q8_0.
+//
+// Arithmetic (model.c:338-345 rms_norm, 359-367 rope, 711-736 residuals,
+// quants.c:74-109 q8_0): sums of squares in double, scale = 1/sqrtf(mean +
+// eps) with the mean rounded to float, products left to right; q8_0 with
+// d = fp16(amax * (1/127)), quants rint(x * 127/amax).  Every load a step
+// needs is issued before its first reduction, so a step costs one memory
+// round trip plus its reductions.
+#pragma once
+
+#include "kernels.h"
+
+namespace g4 {
+
+__device__ __forceinline__ float rms_scale(double ss, int n, float eps) {
+    const float mean = (float)(ss / n);
+    return 1.0f / __builtin_sqrtf(mean + eps);
+}
+
+__device__ __forceinline__ double wave_sum_dd(double v) {
+    for (int k = 32; k >= 1; k >>= 1) v += __shfl_xor(v, k, 64);
+    return v;
+}
+// Workgroup sum of doubles: wave butterflies, then the wave partials in order.
+__device__ __forceinline__ double wg_sum_double(double v, double *red) {
+    v = wave_sum_dd(v);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    double r = 0.0;
+    for (int w = 0; w < (int)(blockDim.x >> 6); w++) r += red[w];
+    __syncthreads();
+    return r;
+}
+
+// q8_0 of four consecutive values; the 8 consecutive lanes of a 32-element
+// block all call this (the block is owned by all of them or none).  Group gi
+// writes quants 4*(gi%8).. of GGUF block gi/8 of dst; its first lane the scale.
+__device__ __forceinline__ void q8_store4(const float v[4], int gi, bool own, uint8_t *dst) {
+    float am = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+    am = fmaxf(am, shfl_xor(am, 1));
+    am = fmaxf(am, shfl_xor(am, 2));
+    am = fmaxf(am, shfl_xor(am, 4));
+    if (!own) return;
+    const float id = am != 0.0f ? 127.0f / am : 0.0f;
+    uint32_t pk = 0;
+#pragma unroll
+    for (int j = 0; j < 4; j++) pk |= ((uint32_t)(int)__builtin_rintf(v[j] * id) & 0xffu) << (8 * j);
+    const int b = gi >> 3, k = gi & 7;
+    uint8_t *blk = dst + (size_t)b * 34;
+    uint16_t *p16 = (uint16_t *)(blk + 2 + 4 * k);
+    p16[0] = (uint16_t)(pk & 0xffff);
+    p16[1] = (uint16_t)(pk >> 16);
+    if (k == 0) *(uint16_t *)blk = f2h(am * (1.0f / 127.0f));
+}
+
+__device__ __forceinline__ float4 ldf4(const float *p) { return *(const float4 *)p; }
+__device__ __forceinline__ void f4(const float4 a, float o[4]) { o[0] = a.x; o[1] = a.y; o[2] = a.z; o[3] = a.w; }
+
+// If delta: x <- x + rms(delta)*w_post (stored back).  Then act <- q8_0(rms(x)*w_pre).
+// n % 32 == 0 and n/4 <= S * blockDim.x; all threads of the workgroup call it.
+template <int S>
+__device__ void wg_norm_quant(float *x, const float *delta, const float *w_post, const float *w_pre, float eps, int n,
+                              uint8_t *act) {
+    __shared__ double red[16];
+    const int ng = n >> 2, bd = blockDim.x, t = threadIdx.x;
+    float v[S][4], d[S][4], wp[S][4], wq[S][4];
+    const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int s = 0; s < S; s++) {
+        const int gi = t + s * bd;
+        const bool own = gi < ng;
+        f4(own ? ldf4(x + 4 * gi) : z, v[s]);
+        f4(own && delta ? ldf4(delta + 4 * gi) : z, d[s]);
+        f4(own && delta ? ldf4(w_post + 4 * gi) : z, wp[s]);
+        f4(own ? ldf4(w_pre + 4 * gi) : z, wq[s]);
+    }
+    if (delta) {
+        double ss = 0.0;
+#pragma unroll
+        for (int s = 0; s < S; s++)
+#pragma unroll
+            for (int k = 0; k < 4; k++) ss += (double)d[s][k] * d[s][k];
+        const float sc = rms_scale(wg_sum_double(ss, red), n, eps);
+#pragma unroll
+        for (int s = 0; s < S; s++) {
+            const int gi = t + s * bd;
+#pragma unroll
+            for (int k = 0; k < 4; k++) v[s][k] = v[s][k] + d[s][k] * sc * wp[s][k];
+            if (gi < ng) *(float4 *)(x + 4 * gi) = make_float4(v[s][0], v[s][1], v[s][2], v[s][3]);
+        }
+    }
+    double ss = 0.0;
+#pragma unroll
+    for (int s = 0; s < S; s++)
+#pragma unroll
+        for (int k = 0; k < 4; k++) ss += (double)v[s][k] * v[s][k];
+    const float sc = rms_scale(wg_sum_double(ss, red), n, eps);
+#pragma unroll
+    for (int s = 0; s < S; s++) {
+        if (s * bd >= ng) break;                      // uniform
+        const int gi = t + s * bd;
+        float o[4];
+#pragma unroll
+        for (int k = 0; k < 4; k++) o[k] = v[s][k] * sc * wq[s][k];
+        q8_store4(o, gi, gi < ng, act);
+    }
+}
+
+// One q/k/v head row r of the fused projection output, by one wave
+// (model.c:664-687): r < n_head is a query head (rms*q_norm, RoPE, to q_out),
+// then n_kv key heads (rms*k_norm, RoPE, to the K cache slot pos), then n_kv
+// value heads (rms without weight, to the V cache slot pos); f16 or q8_0 cache
+// rows.  Lane l holds elements hd/64*l ..; hd % 64 == 0, hd <= 256; `wb` is
+// 256 floats of LDS for this wave.
+__device__ void wave_qkv_row(const float *qkv, const QkvArgs &a, int r, float *wb) {
+    const int lane = threadIdx.x & 63;
+    const int hd = a.hd, epl = hd >> 6, half = hd >> 1;
+    const bool is_q = r < a.n_head, is_k = !is_q && r < a.n_head + a.n_kv;
+    const float *w = is_q ? a.q_norm : is_k ? a.k_norm : nullptr;
+    const float *src = qkv + (size_t)r * hd + lane * epl;
+    float v[4] = {0.f, 0.f, 0.f, 0.f}, wv[4] = {1.f, 1.f, 1.f, 1.f};
+    const int p = *a.pos;
+#pragma unroll
+    for (int e = 0; e < 4; e++)
+        if (e < epl) {
+            v[e] = src[e];
+            if (w) wv[e] = w[lane * epl + e];
+        }
+    // NeoX rotation pairs (i, i + hd/2): lanes below 32 hold the first halves
+    const bool lo = lane < 32;
+    float cs[4] = {1.f, 1.f, 1.f, 1.f}, sn[4] = {0.f, 0.f, 0.f, 0.f};
+    if (is_q || is_k) {
+#pragma unroll
+        for (int e = 0; e < 4; e++)
+            if (e < epl) {
+                const int tt = lane * epl + e, i = lo ? tt : tt - half;
+                cs[e] = a.rope[(size_t)p * hd + 2 * i];
+                sn[e] = a.rope[(size_t)p * hd + 2 * i + 1];
+            }
+    }
+    double ss = 0.0;
+#pragma unroll
+    for (int e = 0; e < 4; e++) ss += (double)v[e] * v[e];
+    const float sc = rms_scale(wave_sum_dd(ss), hd, a.eps);
+    float y[4];
+#pragma unroll
+    for (int e = 0; e < 4; e++) y[e] = w ? v[e] * sc * wv[e] : v[e] * sc;
+    if (is_q || is_k) {
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            if (e < epl) {                                   // uniform over the wave
+                const float other = __shfl_xor(y[e], 32, 64);
+                const float av = lo ? y[e] : other, bv = lo ? other : y[e];
+                y[e] = lo ? av * cs[e] - bv * sn[e] : av * sn[e] + bv * cs[e];
+            }
+        }
+    }
+    if (is_q) {
+#pragma unroll
+        for (int e = 0; e < 4; e++)
+            if (e < epl) a.q_out[(size_t)r * hd + lane * epl + e] = y[e];
+        return;
+    }
+    const int kvh = is_k ? r - a.n_head : r - a.n_head - a.n_kv;
+    uint8_t *cache = is_k ? a.kc : a.vc;
+    if (a.kv_type == F16) {
+        uint16_t *dst = (uint16_t *)cache + ((size_t)p * a.n_kv + kvh) * hd + lane * epl;
+#pragma unroll
+        for (int e = 0; e < 4; e++)
+            if (e < epl) dst[e] = f2h(y[e]);
+    } else {
+#pragma unroll
+        for (int e = 0; e < 4; e++)
+            if (e < epl) wb[lane * epl + e] = y[e];
+        __syncthreads();                                     // one-wave workgroup
+        const bool own = lane < hd / 4;
+        float o[4] = {0.f, 0.f, 0.f, 0.f};
+        if (own)
+            for (int k = 0; k < 4; k++) o[k] = wb[4 * lane + k];
+        q8_store4(o, lane, own, cache + ((size_t)p * a.n_kv + kvh) * (hd / 32) * 34);
+    }
+}
+
+}  // namespace g4
