@@ -26,6 +26,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 PEAK_HBM = 8000.0          # GB/s, MI355X published
+PEAK_INT8 = 5000.0         # dense int8 MFMA TOPS, MI355X published
 MALL = 256 << 20
 
 
@@ -83,6 +84,8 @@ def copies_for(nbytes: int) -> int:
 
 def time_graph(G, stream, fn, k):
     """Capture fn(i) for i < k into one graph; time one replay with events."""
+    fn(0)                               # outside capture: sizes any scratch first
+    stream.synchronize()
     graph = G.Graph(stream.ptr, lambda: [fn(i) for i in range(k)])
     graph.launch(stream.ptr)            # warm replay
     stream.synchronize()
@@ -132,6 +135,35 @@ def cpu_baseline(sets, seconds: float):
     finally:
         g4o.pool_stop()
         g4o.use_reference_dots(False)
+
+
+def bench_prefill(G, stream, Ms=(1, 8, 16, 32, 64, 128, 256, 512)):
+    """q8_0 4096x4096 x M tokens on the GEMV family (path 1)
+    and on the int8 matrix cores (path 2); weights rotated beyond the MALL,
+    activations quantized in the call (x fp32 resident)."""
+    from g4run_amd import synth
+    rows = cols = 4096
+    s = GemvSet(G, G.Q8_0, rows, cols, copies_for(rows * G.row_size(G.Q8_0, cols)), seed=1234)
+    out = {}
+    for M in Ms:
+        xb = G.Buffer.from_array(synth.activations(M, cols, seed=99))
+        Yb = G.Buffer(M * rows * 4)
+        alg = s.bytes - G.act_stride(G.Q8_0, cols) - rows * 4 + M * (G.act_stride(G.Q8_0, cols) + rows * 4)
+        ops = 2.0 * M * rows * cols
+        row = {"alg_bytes": int(alg), "gops": round(ops / 1e9, 3)}
+        for path, name in ((1, "gemv"), (2, "mfma")):
+            k = 100 if M <= 64 else 40
+            fn = lambda i: G.matmul(s.W[i % len(s.W)], Yb, nb=M, x=xb, path=path, stream=stream.ptr)
+            us = time_graph(G, stream, fn, k) / k * 1e3
+            row[name] = {"us": round(us, 2), "GBps": round(alg / us / 1e3, 1), "TOPS": round(ops / us / 1e6, 1),
+                         "pct_int8_peak": round(100 * ops / us / 1e6 / PEAK_INT8, 2)}
+        row["auto_path"] = G.matmul_path(s.W[0], M)
+        out[str(M)] = row
+        log(f"bench: prefill M={M}: gemv {row['gemv']['us']} us, mfma {row['mfma']['us']} us "
+            f"({row['mfma']['TOPS']} TOPS, {row['mfma']['GBps']} GB/s)")
+    for t in s.W:
+        t.free()
+    return out
 
 
 def bench_decode(G, steps: int, cpu_seconds: float, want_cpu: bool):
@@ -207,6 +239,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--all-configs", action="store_true", help="also time every GEMV config (stderr + JSON)")
     ap.add_argument("--decode-steps", type=int, default=64, help="decode steps timed at context ~8192 (0 = skip)")
+    ap.add_argument("--prefill", action="store_true", help="also time config 3 (GEMV vs matrix-core crossover)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (--gpus {args.gpus} requested); "
@@ -255,6 +288,8 @@ def main():
                 f"({100 * s.bytes / t_pre / 1e3 / PEAK_HBM:.1f}% of 8 TB/s); with quantize {t_fus:.3f} us")
             del s
 
+    prefill = bench_prefill(G, stream) if args.all_configs or args.prefill else None
+
     cpu = None if args.no_cpu else cpu_baseline(sets, args.cpu_seconds)
     for s_ in sets:
         for t in s_.W:
@@ -285,6 +320,8 @@ def main():
     }
     if extra:
         out["configs"] = extra
+    if prefill:
+        out["prefill"] = prefill
     if decode:
         out["decode"] = decode
     print(json.dumps(out), flush=True)

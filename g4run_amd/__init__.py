@@ -310,6 +310,11 @@ def matmul(W: Tensor, Y, nb: int = 1, x=None, pre=None, pre_stride: int = 0, pat
                               _p(Y), nb, path, stream))
 
 
+def matmul_path(W: Tensor, nb: int) -> int:
+    """Kernel family g4h_matmul picks for nb tokens: 1 GEMV, 2 int8 matrix cores."""
+    return lib().g4h_matmul_path(W.ptr, nb)
+
+
 def block_sums(W: Tensor, pre, out, tok: int = 0, pre_stride: int = 0, stream=None) -> None:
     check(lib().g4h_block_sums(W.ptr, _p(pre), pre_stride or act_stride(W.type, W.ncols), tok, _p(out), stream))
 

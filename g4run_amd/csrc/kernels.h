@@ -41,6 +41,11 @@ hipError_t launch_qkv_prep(const float *qkv, const QkvArgs &a, hipStream_t s);
 hipError_t launch_gelu_quant(const float *gu, int n_ff, const uint16_t *tab, uint8_t *act, hipStream_t s);
 hipError_t launch_argmax_advance(const float *logits, int n, int *state, hipStream_t s);
 
+// k_mfma.hip: many-token matmul on the int8 matrix cores (q8_0 / q4_0 weights)
+size_t mm_planar_bytes(int M, int64_t ncols);
+hipError_t launch_matmul_mfma(const g4h_tensor &W, const float *x, size_t x_stride, const uint8_t *act, size_t stride, int M,
+                              float *Y, uint8_t *ws, hipStream_t s);
+
 // k_attn.hip
 size_t attn_workspace_bytes(int n_head, int hd, int npos_max);
 hipError_t launch_attn_decode(const float *q, const uint8_t *kc, const uint8_t *vc, int kv_type, int n_head, int n_kv, int hd,

@@ -128,8 +128,11 @@ int    g4h_tensor_info(const g4h_tensor *t, int *type, int64_t *ncols, int64_t *
  * nb thresholds given by g4h_matmul_path(). */
 int g4h_matmul(const g4h_tensor *W, const float *x_dev, const void *pre_dev, size_t pre_stride,
                float *Y_dev, int nb, void *stream);
-/* Same with an explicit kernel family: 0 = auto, 1 = GEMV (nb <= 8),
- * 2 = int8-MFMA tiles. */
+/* Same with an explicit kernel family: 0 = auto (g4h_matmul_path), 1 = the
+ * GEMV family (token chunks of <= 8 staged per workgroup), 2 = int8 matrix-core
+ * tiles (q8_0 / q4_0 weights; every per-block integer sum exact, fp32 block
+ * scaling in block order).  g4h_matmul_path returns the family auto picks:
+ * 2 for q8_0 / q4_0 weights from 24 tokens on, else 1. */
 int g4h_matmul_ex(const g4h_tensor *W, const float *x_dev, const void *pre_dev, size_t pre_stride,
                   float *Y_dev, int nb, int path, void *stream);
 int g4h_matmul_path(const g4h_tensor *W, int nb);

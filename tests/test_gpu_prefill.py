@@ -1,0 +1,82 @@
+"""GPU parity of the batched-prefill matmul on the int8 matrix cores (path 2)
+against the CPU oracle's shipped-order dots (q8_0 4096x4096
+x M tokens), plus its batch-size invariance and error paths.
+
+The per-block integer sums come out of one int8 MFMA per block and are exact
+by construction; the fp32 results must be within |gpu - cpu| <= 1e-5 +
+1e-3*|cpu| of the oracle (the fp32 order differs from the CPU's 8-lane one).
+"""
+import numpy as np
+import pytest
+
+from test_gpu_gemv import assert_close, bits, gpu_matmul, oracle_matmul
+
+pytestmark = pytest.mark.gpu
+
+
+def _setup(G, qt, rows, cols, M, seed):
+    from g4run_amd import synth
+    w = synth.weights(qt, rows, cols, seed=seed)
+    x = synth.activations(M, cols, seed=seed + 1)
+    return w, x, G.Tensor.from_rows(qt, w, cols)
+
+
+@pytest.mark.parametrize("M", [16, 64, 512])
+def test_config3_q8_0_vs_oracle(gpu, oracle, M):
+    w, x, t = _setup(gpu, 8, 4096, 4096, M, seed=1234)
+    y = gpu_matmul(gpu, t, x=x, nb=M, path=2)
+    assert_close(y, oracle_matmul(oracle, 8, w, x), f"q8_0 4096x4096 M={M}")
+
+
+@pytest.mark.parametrize("rows,cols,M", [(10240, 2560, 128), (2560, 10240, 64)])
+def test_q4_0_ffn_shapes_vs_oracle(gpu, oracle, rows, cols, M):
+    w, x, t = _setup(gpu, 2, rows, cols, M, seed=rows)
+    assert_close(gpu_matmul(gpu, t, x=x, nb=M, path=2), oracle_matmul(oracle, 2, w, x), f"q4_0 {rows}x{cols} M={M}")
+
+
+@pytest.mark.parametrize("qt", [8, 2])
+def test_ragged_shapes(gpu, oracle, qt):
+    """Token and row counts that do not fill a tile, odd block counts."""
+    for rows, cols, M in ((1, 32, 16), (31, 96, 17), (100, 2080, 33), (65, 800, 65), (257, 1024, 100), (33, 4096, 129)):
+        w, x, t = _setup(gpu, qt, rows, cols, M, seed=rows + cols)
+        assert_close(gpu_matmul(gpu, t, x=x, nb=M, path=2), oracle_matmul(oracle, qt, w, x), f"{rows}x{cols} M={M}")
+
+
+@pytest.mark.parametrize("qt", [8, 2])
+def test_token_results_independent_of_batch(gpu, oracle, qt):
+    """Within the matrix-core family a token's outputs are bit-identical for any
+    batch size (small-M and large-M tile variants keep the same fp32 order)."""
+    w, x, t = _setup(gpu, qt, 384, 2048, 512, seed=5)
+    full = gpu_matmul(gpu, t, x=x, nb=512, path=2)
+    for M in (16, 40, 64, 65, 200):
+        part = gpu_matmul(gpu, t, x=x[:M].copy(), nb=M, path=2)
+        assert np.array_equal(bits(part), bits(full[:M])), f"M={M}"
+
+
+@pytest.mark.parametrize("qt", [8, 2])
+def test_fused_quantizer_equals_prequantized(gpu, oracle, qt):
+    w, x, t = _setup(gpu, qt, 256, 4096, 48, seed=9)
+    a = gpu_matmul(gpu, t, x=x, nb=48, path=2)
+    b = gpu_matmul(gpu, t, act=oracle.prep_act(qt, x), nb=48, path=2)
+    assert np.array_equal(bits(a), bits(b))
+
+
+def test_matrix_core_path_agrees_with_gemv_path(gpu, oracle):
+    w, x, t = _setup(gpu, 8, 512, 4096, 32, seed=3)
+    ref = oracle_matmul(oracle, 8, w, x)
+    assert_close(gpu_matmul(gpu, t, x=x, nb=32, path=1), ref, "gemv")
+    assert_close(gpu_matmul(gpu, t, x=x, nb=32, path=2), ref, "mfma")
+
+
+def test_path_selection_and_errors(gpu):
+    from g4run_amd import synth
+    G = gpu
+    t8 = G.Tensor.from_rows(8, synth.weights(8, 64, 256, seed=1), 256)
+    tk = G.Tensor.from_rows(12, synth.weights(12, 64, 256, seed=1), 256)
+    assert [G.matmul_path(t8, n) for n in (1, 8, 23, 24, 512)] == [1, 1, 1, 2, 2]
+    assert G.matmul_path(tk, 512) == 1
+    Y = G.Buffer(64 * 16 * 4)
+    x = G.Buffer.from_array(synth.activations(16, 256, seed=2))
+    with pytest.raises(G.G4HError) as e:
+        G.matmul(tk, Y, nb=16, x=x, path=2)
+    assert e.value.status == G.ERR_TYPE
