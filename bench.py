@@ -27,6 +27,11 @@ sys.path.insert(0, ROOT)
 
 PEAK_HBM = 8000.0          # GB/s, MI355X published
 PEAK_INT8 = 5000.0         # dense int8 MFMA TOPS, MI355X published
+# HBM bytes per launch of the roofline kernel (q4_0 10240x2560 GEMV) from two
+# rocprofv3 --pmc passes: FETCH_SIZE 7287.1 KiB x 2.00 + WRITE_SIZE 64.0 KiB x
+# 1.00, scales from a 256 MiB device copy in the same runs
+# (profiles/gemv_q4_0_ffn_traffic.md).
+TRAFFIC_UP = int((7287.1 * 2.00 + 64.0 * 1.00) * 1024)
 MALL = 256 << 20
 
 
@@ -240,6 +245,8 @@ def main():
     ap.add_argument("--all-configs", action="store_true", help="also time every GEMV config (stderr + JSON)")
     ap.add_argument("--decode-steps", type=int, default=64, help="decode steps timed at context ~8192 (0 = skip)")
     ap.add_argument("--prefill", action="store_true", help="also time config 3 (GEMV vs matrix-core crossover)")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="start with one 256 MiB device copy (the reference dispatch for rocprofv3 --pmc byte counters)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (--gpus {args.gpus} requested); "
@@ -249,6 +256,16 @@ def main():
     import g4run_amd as G
     G.init(0)
     stream = G.Stream()
+    if args.copy_calibration:
+        # one device copy of known size: the FETCH_SIZE / WRITE_SIZE scale for --pmc runs
+        n = 256 << 20
+        a_, b_ = G.Buffer(n), G.Buffer(n)
+        a_.zero()
+        G.synchronize()
+        G.lib().g4h_memcpy_d2d(b_.ptr, a_.ptr, n, stream.ptr)
+        stream.synchronize()
+        log(f"bench: calibration copy of {n} bytes done")
+        del a_, b_
     log("bench: building resident weight copies")
     up = GemvSet(G, G.Q4_0, 10240, 2560, copies_for(10240 * 1440), seed=1234)
     down = GemvSet(G, G.Q4_0, 2560, 10240, copies_for(2560 * 5760), seed=4321)
@@ -272,6 +289,7 @@ def main():
     ms_k = time_graph(G, stream, lambda i: up.call(G, i, stream.ptr, fused=False), kr)
     per_launch_us = ms_k / kr * 1e3
     achieved = up.bytes / (per_launch_us * 1e-6) / 1e9
+    kernel = G.matmul_describe(up.W[0], 1, 1)
 
     extra = {}
     if args.all_configs:
@@ -313,8 +331,8 @@ def main():
                                f"{len(up.W)}+{len(down.W)} resident copies",
                    "pct_of_peak": round(100 * value / PEAK_HBM, 1)},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM, "unit": "GB/s",
-                     "frac": round(achieved / PEAK_HBM, 4), "traffic": None,
-                     "kernel": "k_gemv<FQ4_0,1,16,8> (q4_0 10240x2560, pre-quantized q8_0 input)",
+                     "frac": round(achieved / PEAK_HBM, 4), "traffic": TRAFFIC_UP,
+                     "kernel": kernel + " (q4_0 10240x2560, pre-quantized q8_0 input)",
                      "alg_bytes_per_launch": up.bytes, "avg_launch_us": round(per_launch_us, 3)},
         "cpu_baseline": cpu,
     }

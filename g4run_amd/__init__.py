@@ -73,6 +73,7 @@ _SIGS = [
     ("g4h_matmul", _int, [_vp, _vp, _vp, _sz, _vp, _int, _vp]),
     ("g4h_matmul_ex", _int, [_vp, _vp, _vp, _sz, _vp, _int, _int, _vp]),
     ("g4h_matmul_path", _int, [_vp, _int]),
+    ("g4h_matmul_describe", _int, [_vp, _int, _int, C.c_char_p, C.c_size_t]),
     ("g4h_block_sums", _int, [_vp, _vp, _sz, _int, _vp, _vp]),
     ("g4h_attn_workspace_bytes", _sz, [_int, _int, _int]),
     ("g4h_attn_decode", _int, [_vp, _vp, _vp, _int, _int, _int, _int, _int, _vp, _vp, _sz, _vp]),
@@ -313,6 +314,13 @@ def matmul(W: Tensor, Y, nb: int = 1, x=None, pre=None, pre_stride: int = 0, pat
 def matmul_path(W: Tensor, nb: int) -> int:
     """Kernel family g4h_matmul picks for nb tokens: 1 GEMV, 2 int8 matrix cores."""
     return lib().g4h_matmul_path(W.ptr, nb)
+
+
+def matmul_describe(W: Tensor, nb: int = 1, path: int = 0) -> str:
+    """Kernel instantiation and launch shape of g4h_matmul_ex for nb tokens."""
+    buf = C.create_string_buffer(256)
+    check(lib().g4h_matmul_describe(W.ptr, nb, path, buf, 256))
+    return buf.value.decode()
 
 
 def block_sums(W: Tensor, pre, out, tok: int = 0, pre_stride: int = 0, stream=None) -> None:

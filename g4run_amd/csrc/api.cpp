@@ -338,6 +338,34 @@ extern "C" int g4h_matmul_path(const g4h_tensor *W, int nb) {
     return mfma_capable(W) && nb >= kMfmaMinTokens ? 2 : 1;
 }
 
+static const char *type_name(int t) {
+    switch (t) {
+    case Q4_0: return "q4_0";
+    case Q8_0: return "q8_0";
+    case Q2_K: return "q2_K";
+    case Q3_K: return "q3_K";
+    case Q4_K: return "q4_K";
+    default: return "?";
+    }
+}
+
+extern "C" int g4h_matmul_describe(const g4h_tensor *W, int nb, int path, char *buf, size_t len) {
+    if (!W || !buf || len == 0 || nb <= 0 || path < 0 || path > 2) return fail(G4H_ERR_ARG, "g4h_matmul_describe: bad argument");
+    if (path == 0) path = g4h_matmul_path(W, nb);
+    if (path == 2) {
+        if (!mfma_capable(W)) return fail(G4H_ERR_TYPE, "g4h_matmul_describe: the matrix-core path takes q8_0 / q4_0 weights");
+        mm_describe(*W, nb, buf, len);
+        return G4H_OK;
+    }
+    int lpr, upl, wpg;
+    int64_t grid;
+    gemv_launch_shape(*W, &lpr, &upl, &wpg, &grid);
+    const int chunk = nb >= 8 ? 8 : nb >= 4 ? 4 : nb >= 2 ? 2 : 1;
+    snprintf(buf, len, "k_gemv<%s,nb=%d,lpr=%d,upl=%d> grid=%lld block=%d (x%d launches)", type_name(W->type), chunk, lpr, upl,
+             (long long)grid, 64 * wpg, (nb + chunk - 1) / chunk);
+    return G4H_OK;
+}
+
 static int check_act(const char *fn, const g4h_tensor *W, const void *pre, size_t stride, int nb) {
     if ((uintptr_t)pre % 4 || stride % 4) return fail(G4H_ERR_ARG, "%s: activations must be 4-byte aligned with a 4-byte multiple stride", fn);
     if (nb > 1 && stride < g4h_row_size(g4h_act_type(W->type), W->ncols))

@@ -50,6 +50,14 @@ void gemv_shape(int type, int64_t nblk, int *lpr, int *upl) {
     *upl = per <= 2 ? 2 : per <= 4 ? 4 : 8;
 }
 
+void gemv_launch_shape(const g4h_tensor &W, int *lpr, int *upl, int *wpg, int64_t *grid) {
+    gemv_shape(W.type, W.nb, lpr, upl);
+    const int rpw = 64 / *lpr;
+    *wpg = gemv_waves_per_group(W.nrows, rpw);
+    const int64_t waves = (W.nrows + rpw - 1) / rpw;
+    *grid = (waves + *wpg - 1) / *wpg;
+}
+
 size_t gemv_lds_bytes(int type, int nb_tokens, int64_t nblk) {
     return (type == Q4_0 || type == Q8_0) ? act_lds_bytes<FQ8_0>(nb_tokens, nblk) : act_lds_bytes<FQ4_K>(nb_tokens, nblk);
 }

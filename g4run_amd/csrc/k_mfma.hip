@@ -22,6 +22,8 @@
 // 32 x 32 outputs per workgroup, each wave streaming all blocks (large M), or
 // one 32 x 32 tile whose blocks are split over KS waves and added in wave
 // order through LDS (small M: enough waves in flight to stream the weights).
+#include <cstdio>
+
 #include "formats.h"
 #include "kernels.h"
 #include "steps.h"
@@ -200,6 +202,21 @@ size_t mm_planar_bytes(int M, int64_t ncols) {
     return (((size_t)M * nb * 32 + 255) & ~(size_t)255) + (size_t)M * nb * 2;
 }
 
+// one 32 x 32 tile per workgroup with the blocks split over 4 waves while that
+// still gives <= 4 workgroups per CU; 64 x 64 tiles (less operand traffic) beyond
+static bool mm_small(const g4h_tensor &W, int M) {
+    const int64_t tiles = ((W.nrows + 31) / 32) * ((M + 31) / 32);
+    return tiles <= 4 * 256;
+}
+
+void mm_describe(const g4h_tensor &W, int M, char *buf, size_t len) {
+    const bool small = mm_small(W, M);
+    const int wm = small ? 1 : 2, wn = small ? 1 : 2;
+    snprintf(buf, len, "k_mm_mfma<%s,wm=%d,wn=%d,ks=%d,kb=%d> grid=%lldx%d block=256", W.type == Q8_0 ? "q8_0" : "q4_0", wm,
+             wn, small ? 4 : 1, small ? MM_KB_SMALL : 4, (long long)((W.nrows + 32 * wn - 1) / (32 * wn)),
+             (M + 32 * wm - 1) / (32 * wm));
+}
+
 template <int WT, int WM, int WN, int KS, int KB>
 static hipError_t mm_go(const g4h_tensor &W, const int8_t *qa, const uint16_t *da, int M, float *Y, hipStream_t s) {
     const dim3 grid((unsigned)((W.nrows + 32 * WN - 1) / (32 * WN)), (unsigned)((M + 32 * WM - 1) / (32 * WM)));
@@ -224,11 +241,7 @@ hipError_t launch_matmul_mfma(const g4h_tensor &W, const float *x, size_t x_stri
         hipLaunchKernelGGL(k_act_planar, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, act, stride, nb, M, qa, da);
     }
     if (hipError_t e = hipGetLastError()) return e;
-    // one 32 x 32 tile per workgroup with the blocks split over 4 waves while
-    // that still gives >= 4 workgroups per CU; 64 x 64 tiles (less operand
-    // traffic) beyond
-    const int64_t tiles = ((W.nrows + 31) / 32) * ((M + 31) / 32);
-    const bool small = tiles <= 4 * 256;
+    const bool small = mm_small(W, M);
     if (W.type == Q8_0) return small ? mm_go<Q8_0, 1, 1, 4, MM_KB_SMALL>(W, qa, da, M, Y, s) : mm_go<Q8_0, 2, 2, 1, 4>(W, qa, da, M, Y, s);
     return small ? mm_go<Q4_0, 1, 1, 4, MM_KB_SMALL>(W, qa, da, M, Y, s) : mm_go<Q4_0, 2, 2, 1, 4>(W, qa, da, M, Y, s);
 }

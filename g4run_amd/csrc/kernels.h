@@ -19,6 +19,7 @@ hipError_t launch_vec_dot_raw(int wtype, const uint8_t *w, size_t ws, const uint
 
 void gemv_shape(int type, int64_t nblk, int *lpr, int *upl);
 size_t gemv_lds_bytes(int type, int nb_tokens, int64_t nblk);
+void gemv_launch_shape(const g4h_tensor &W, int *lpr, int *upl, int *wpg, int64_t *grid);
 hipError_t launch_gemv(const g4h_tensor &W, const uint8_t *act, size_t stride, float *Y, int nb, hipStream_t s);
 hipError_t launch_block_sums(const g4h_tensor &W, const uint8_t *act, size_t stride, int tok, int32_t *out, hipStream_t s);
 int block_sums_per_block(int type);
@@ -43,6 +44,7 @@ hipError_t launch_argmax_advance(const float *logits, int n, int *state, hipStre
 
 // k_mfma.hip: many-token matmul on the int8 matrix cores (q8_0 / q4_0 weights)
 size_t mm_planar_bytes(int M, int64_t ncols);
+void mm_describe(const g4h_tensor &W, int M, char *buf, size_t len);
 hipError_t launch_matmul_mfma(const g4h_tensor &W, const float *x, size_t x_stride, const uint8_t *act, size_t stride, int M,
                               float *Y, uint8_t *ws, hipStream_t s);
 

@@ -136,6 +136,11 @@ int g4h_matmul(const g4h_tensor *W, const float *x_dev, const void *pre_dev, siz
 int g4h_matmul_ex(const g4h_tensor *W, const float *x_dev, const void *pre_dev, size_t pre_stride,
                   float *Y_dev, int nb, int path, void *stream);
 int g4h_matmul_path(const g4h_tensor *W, int nb);
+/* Diagnostic (no reference counterpart): the kernel instantiation and launch
+ * shape g4h_matmul_ex would use, e.g. "k_gemv<q4_0,nb=1,lpr=32,upl=4> grid=256
+ * block=512", written NUL-terminated into buf (at most len bytes).  Profiles
+ * and benchmarks name the kernel they time with it. */
+int g4h_matmul_describe(const g4h_tensor *W, int nb, int path, char *buf, size_t len);
 
 /* Per-block integer sums of every row of W against token `tok` of pre_dev:
  * q8_0/q4_0 one int32 per 32-block, q3_K one per superblock, q2_K/q4_K two per
