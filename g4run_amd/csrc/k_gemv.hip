@@ -75,6 +75,57 @@ hipError_t launch_gemv(const g4h_tensor &W, const uint8_t *act, size_t stride, f
     }
 }
 
+hipError_t launch_gemv_p_q8_0(const g4h_tensor &, const uint8_t *, float *, const GemvPro &, const GemvEpi &, hipStream_t, int,
+                              int, int);
+hipError_t launch_gemv_p_q4_0(const g4h_tensor &, const uint8_t *, float *, const GemvPro &, const GemvEpi &, hipStream_t, int,
+                              int, int);
+
+// Persistent family: the one-shot kernel's LPR/UPL (identical results), a
+// single pass over each row (units <= LPR*UPL), prologue inputs <= 16384 wide.
+// The GELU epilogue pairs rows inside a wave, so it caps LPR at 32.
+static bool gemv_p_shape(const g4h_tensor &W, const GemvEpi &epi, int *lpr, int *upl) {
+    gemv_shape(W.type, W.nb, lpr, upl);
+    if (epi.kind == EPI_GELU && *lpr > 32) {
+        *lpr = 32;
+        const int per = (int)((W.nb + 31) / 32);
+        *upl = per <= 2 ? 2 : per <= 4 ? 4 : 8;
+    }
+    return W.nb <= (int64_t)(*lpr) * (*upl);
+}
+
+bool gemv_p_fits(const g4h_tensor &W, const GemvPro &pro, const GemvEpi &epi) {
+    int lpr, upl;
+    if (W.type != Q4_0 && W.type != Q8_0) return false;
+    if (!gemv_p_shape(W, epi, &lpr, &upl)) return false;
+    if (pro.kind != PRO_ACT && (W.ncols > 16384 || W.ncols % 32 || pro.n != W.ncols)) return false;
+    if (epi.kind == EPI_GELU && W.nrows % 2) return false;
+    return true;
+}
+
+// workgroups: a fixed count per CU (G4H_GEMV_P_OCC overrides the default of 2)
+int gemv_p_grid_size() {
+    static const int occ = [] {
+        const char *e = getenv("G4H_GEMV_P_OCC");
+        const int v = e ? atoi(e) : 2;
+        return v < 1 ? 1 : v > 4 ? 4 : v;
+    }();
+    return 256 * occ;
+}
+
+hipError_t launch_gemv_p(const g4h_tensor &W, const uint8_t *act, float *Y, const GemvPro &pro, const GemvEpi &epi,
+                         hipStream_t s) {
+    if (!gemv_p_fits(W, pro, epi)) return hipErrorInvalidValue;
+    if (pro.kind == PRO_ACT && !act) return hipErrorInvalidValue;
+    if (pro.kind != PRO_ACT && !pro.x) return hipErrorInvalidValue;
+    if (pro.kind == PRO_NORM && (!pro.w_pre || !pro.x_out || (pro.delta && !pro.w_post))) return hipErrorInvalidValue;
+    if (epi.kind == EPI_GELU ? (!epi.h || !epi.gelu) : !Y) return hipErrorInvalidValue;
+    int lpr, upl;
+    gemv_p_shape(W, epi, &lpr, &upl);
+    const int grid = gemv_p_grid_size();
+    return W.type == Q8_0 ? launch_gemv_p_q8_0(W, act, Y, pro, epi, s, lpr, upl, grid)
+                          : launch_gemv_p_q4_0(W, act, Y, pro, epi, s, lpr, upl, grid);
+}
+
 template <class F>
 static hipError_t bs_go(const g4h_tensor &W, const uint8_t *act, size_t stride, int tok, int32_t *out, hipStream_t s) {
     const int64_t n = W.nrows * W.nb;

@@ -53,13 +53,6 @@ __global__ __launch_bounds__(512) void k_norm_quant(float *x, const float *delta
     wg_norm_quant<4>(x, delta, w_post, w_pre, eps, n, act);
 }
 
-// ------------------------------------------- q/k norm, RoPE, KV store --
-// one 64-thread workgroup per head row of the fused q|k|v output
-__global__ __launch_bounds__(64) void k_qkv_prep(const float *qkv, QkvArgs a) {
-    __shared__ float wb[256];
-    wave_qkv_row(qkv, a, blockIdx.x, wb);
-}
-
 // -------------------------------------------------------- gelu * up --
 // h = gelu(g) * u with the fp16 GELU table (model.c:725-729), quantized to
 // q8_0 for the down projection; 256 threads, 4 elements each.
@@ -141,11 +134,6 @@ hipError_t launch_norm_quant(float *x, const float *delta, const float *w_post, 
                              uint8_t *act, hipStream_t s) {
     if (n % 32 || n > 8192) return hipErrorInvalidValue;
     hipLaunchKernelGGL(k_norm_quant, dim3(1), dim3(512), 0, s, x, delta, w_post, w_pre, eps, n, act);
-    return hipGetLastError();
-}
-hipError_t launch_qkv_prep(const float *qkv, const QkvArgs &a, hipStream_t s) {
-    if (a.hd % 64 || a.hd > 256) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_qkv_prep, dim3(a.n_head + 2 * a.n_kv), dim3(64), 0, s, qkv, a);
     return hipGetLastError();
 }
 hipError_t launch_gelu_quant(const float *gu, int n_ff, const uint16_t *tab, uint8_t *act, hipStream_t s) {

@@ -20,16 +20,40 @@ hipError_t launch_vec_dot_raw(int wtype, const uint8_t *w, size_t ws, const uint
 void gemv_shape(int type, int64_t nblk, int *lpr, int *upl);
 size_t gemv_lds_bytes(int type, int nb_tokens, int64_t nblk);
 void gemv_launch_shape(const g4h_tensor &W, int *lpr, int *upl, int *wpg, int64_t *grid);
+
+// Persistent single-token GEMV (gemv_p.h) over q4_0 / q8_0 rows with a fused
+// activation prologue and an optional GELU epilogue.
+enum { PRO_ACT = 0, PRO_QUANT = 1, PRO_NORM = 2 };
+enum { EPI_STORE = 0, EPI_GELU = 1 };
+struct GemvPro {
+    int kind = PRO_ACT;
+    const float *x = nullptr;        // PRO_QUANT / PRO_NORM: fp32 input (n = W.ncols)
+    float *x_out = nullptr;          // PRO_NORM: the updated residual (written by workgroup 0)
+    const float *delta = nullptr;    // PRO_NORM: branch output added after its RMSNorm, or null
+    const float *w_post = nullptr;   // PRO_NORM: weight of that RMSNorm
+    const float *w_pre = nullptr;    // PRO_NORM: weight of the RMSNorm in front of the matmul
+    float eps = 0.0f;
+    int n = 0;
+};
+struct GemvEpi {
+    int kind = EPI_STORE;
+    const uint16_t *gelu = nullptr;  // EPI_GELU: fp16 GELU table
+    float *h = nullptr;              // EPI_GELU: nrows/2 outputs gelu(row 2i) * row 2i+1
+};
+// false when the shape is outside the persistent family (then use launch_gemv)
+bool gemv_p_fits(const g4h_tensor &W, const GemvPro &pro, const GemvEpi &epi);
+int gemv_p_grid_size();
+hipError_t launch_gemv_p(const g4h_tensor &W, const uint8_t *act, float *Y, const GemvPro &pro, const GemvEpi &epi,
+                         hipStream_t s);
 hipError_t launch_gemv(const g4h_tensor &W, const uint8_t *act, size_t stride, float *Y, int nb, hipStream_t s);
 hipError_t launch_block_sums(const g4h_tensor &W, const uint8_t *act, size_t stride, int tok, int32_t *out, hipStream_t s);
 int block_sums_per_block(int type);
 
-// k_model.hip: the decode step's single-workgroup steps (steps.h)
+// The decode step's q/k/v head preparation (folded into the attention score
+// pass) and k_model.hip's single-workgroup steps (steps.h).
 struct QkvArgs {
     int n_head = 0, n_kv = 0, hd = 0, kv_type = 0;
     const float *q_norm = nullptr, *k_norm = nullptr, *rope = nullptr;
-    const int *pos = nullptr;
-    float *q_out = nullptr;
     uint8_t *kc = nullptr, *vc = nullptr;
     float eps = 0.0f;
 };
@@ -38,7 +62,6 @@ hipError_t launch_embed_norm(const g4h_tensor &head, const int *token, float *x,
                              uint8_t *act, hipStream_t s);
 hipError_t launch_norm_quant(float *x, const float *delta, const float *w_post, const float *w_pre, float eps, int n,
                              uint8_t *act, hipStream_t s);
-hipError_t launch_qkv_prep(const float *qkv, const QkvArgs &a, hipStream_t s);
 hipError_t launch_gelu_quant(const float *gu, int n_ff, const uint16_t *tab, uint8_t *act, hipStream_t s);
 hipError_t launch_argmax_advance(const float *logits, int n, int *state, hipStream_t s);
 
@@ -50,9 +73,8 @@ hipError_t launch_matmul_mfma(const g4h_tensor &W, const float *x, size_t x_stri
 
 // k_attn.hip
 size_t attn_workspace_bytes(int n_head, int hd, int npos_max);
-hipError_t launch_attn_decode(const float *q, const uint8_t *kc, const uint8_t *vc, int kv_type, int n_head, int n_kv, int hd,
-                              int npos, const int *npos_dev, int npos_max, float *out, uint8_t *q8out, uint8_t *ws,
-                              hipStream_t s);
+hipError_t launch_attn_decode(const float *q, const float *qkv, const QkvArgs &a, int npos, const int *npos_dev, int npos_max,
+                              float *out, uint8_t *q8out, uint8_t *ws, hipStream_t s);
 hipError_t launch_kv_store(int kv_type, const float *src, uint8_t *dst, int hd, int rows, size_t dst_stride, hipStream_t s);
 
 }  // namespace g4

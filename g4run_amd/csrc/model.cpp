@@ -6,8 +6,8 @@
 // sliding-window ring, shared KV and softcap):
 //   a  = q8_0(rms(x)*attn_norm), x <- x + rms(prev)*post_ffw_norm first    k_norm_quant
 //   qkv = Wqkv a                                                            GEMV
-//   q,k <- rms(.)*q_norm/k_norm, RoPE; v <- rms(v); k,v stored at pos     k_qkv_prep
-//   o  = attention(q, K[0..pos], V[0..pos])     scores, softmax, V, combine (+ q8_0(o))
+//   q,k <- rms(.)*q_norm/k_norm, RoPE; v <- rms(v); k,v stored at pos
+//   o  = attention(q, K[0..pos], V[0..pos])     scores (+ the q/k/v preparation), V, combine (+ q8_0(o))
 //   y  = Wo q8_0(o)                                                         GEMV
 //   x <- x + rms(y)*post_attn_norm; a = q8_0(rms(x)*ffn_norm)               k_norm_quant
 //   g|u = Wgu a;  a = q8_0(gelu(g)*u)                                 GEMV, k_gelu_quant
@@ -260,7 +260,7 @@ extern "C" int g4h_forward_state(g4h_model *m, void *stream) {
     const hipStream_t s = (hipStream_t)stream;
     const g4h_model_config &c = m->c;
     const int E = c.n_embd, H = c.n_head, KV = c.n_kv, hd = c.head_dim, F = c.n_ff;
-    int *token = m->state, *pos = m->state + 1, *npos = m->state + 2;
+    int *token = m->state, *npos = m->state + 2;    // state: token, pos, npos = pos + 1
     const size_t ast = m->act_bytes;
     M_HIP(launch_embed_norm(*m->head, token, m->x, sqrtf((float)E), norm_of(m, 0, G4H_N_ATTN), c.rms_eps, m->act, s));
     for (int l = 0; l < c.n_layer; l++) {
@@ -276,13 +276,10 @@ extern "C" int g4h_forward_state(g4h_model *m, void *stream) {
         qa.q_norm = norm_of(m, l, G4H_N_Q);
         qa.k_norm = norm_of(m, l, G4H_N_K);
         qa.rope = m->rope;
-        qa.pos = pos;
-        qa.q_out = m->q;
         qa.kc = kc;
         qa.vc = vc;
         qa.eps = c.rms_eps;
-        M_HIP(launch_qkv_prep(m->qkv, qa, s));
-        M_HIP(launch_attn_decode(m->q, kc, vc, c.kv_type, H, KV, hd, 0, npos, c.n_ctx, m->att, m->act, m->ws, s));
+        M_HIP(launch_attn_decode(nullptr, m->qkv, qa, 0, npos, c.n_ctx, m->att, m->act, m->ws, s));
         M_HIP(launch_gemv(*m->wo[l], m->act, ast, m->xb, 1, s));
         M_HIP(launch_norm_quant(m->x, m->xb, norm_of(m, l, G4H_N_POST_ATTN), norm_of(m, l, G4H_N_FFN), c.rms_eps, E, m->act, s));
         M_HIP(launch_gemv(*m->wgu[l], m->act, ast, m->ff, 1, s));

@@ -1,5 +1,6 @@
 // steps.h -- the single-workgroup steps of the decode chain between the
-// GEMVs: residual + RMSNorm + q8_0, q/k/v head preparation, GELU + q8_0.
+// GEMVs (residual + RMSNorm + q8_0) and the q8_0 helper they share with the
+// attention and GELU kernels.
 //
 // Arithmetic (model.c:338-345 rms_norm, 359-367 rope, 711-736 residuals,
 // quants.c:74-109 q8_0): sums of squares in double, scale = 1/sqrtf(mean +
@@ -104,81 +105,6 @@ __device__ void wg_norm_quant(float *x, const float *delta, const float *w_post,
 #pragma unroll
         for (int k = 0; k < 4; k++) o[k] = v[s][k] * sc * wq[s][k];
         q8_store4(o, gi, gi < ng, act);
-    }
-}
-
-// One q/k/v head row r of the fused projection output, by one wave
-// (model.c:664-687): r < n_head is a query head (rms*q_norm, RoPE, to q_out),
-// then n_kv key heads (rms*k_norm, RoPE, to the K cache slot pos), then n_kv
-// value heads (rms without weight, to the V cache slot pos); f16 or q8_0 cache
-// rows.  Lane l holds elements hd/64*l ..; hd % 64 == 0, hd <= 256; `wb` is
-// 256 floats of LDS for this wave.
-__device__ void wave_qkv_row(const float *qkv, const QkvArgs &a, int r, float *wb) {
-    const int lane = threadIdx.x & 63;
-    const int hd = a.hd, epl = hd >> 6, half = hd >> 1;
-    const bool is_q = r < a.n_head, is_k = !is_q && r < a.n_head + a.n_kv;
-    const float *w = is_q ? a.q_norm : is_k ? a.k_norm : nullptr;
-    const float *src = qkv + (size_t)r * hd + lane * epl;
-    float v[4] = {0.f, 0.f, 0.f, 0.f}, wv[4] = {1.f, 1.f, 1.f, 1.f};
-    const int p = *a.pos;
-#pragma unroll
-    for (int e = 0; e < 4; e++)
-        if (e < epl) {
-            v[e] = src[e];
-            if (w) wv[e] = w[lane * epl + e];
-        }
-    // NeoX rotation pairs (i, i + hd/2): lanes below 32 hold the first halves
-    const bool lo = lane < 32;
-    float cs[4] = {1.f, 1.f, 1.f, 1.f}, sn[4] = {0.f, 0.f, 0.f, 0.f};
-    if (is_q || is_k) {
-#pragma unroll
-        for (int e = 0; e < 4; e++)
-            if (e < epl) {
-                const int tt = lane * epl + e, i = lo ? tt : tt - half;
-                cs[e] = a.rope[(size_t)p * hd + 2 * i];
-                sn[e] = a.rope[(size_t)p * hd + 2 * i + 1];
-            }
-    }
-    double ss = 0.0;
-#pragma unroll
-    for (int e = 0; e < 4; e++) ss += (double)v[e] * v[e];
-    const float sc = rms_scale(wave_sum_dd(ss), hd, a.eps);
-    float y[4];
-#pragma unroll
-    for (int e = 0; e < 4; e++) y[e] = w ? v[e] * sc * wv[e] : v[e] * sc;
-    if (is_q || is_k) {
-#pragma unroll
-        for (int e = 0; e < 4; e++) {
-            if (e < epl) {                                   // uniform over the wave
-                const float other = __shfl_xor(y[e], 32, 64);
-                const float av = lo ? y[e] : other, bv = lo ? other : y[e];
-                y[e] = lo ? av * cs[e] - bv * sn[e] : av * sn[e] + bv * cs[e];
-            }
-        }
-    }
-    if (is_q) {
-#pragma unroll
-        for (int e = 0; e < 4; e++)
-            if (e < epl) a.q_out[(size_t)r * hd + lane * epl + e] = y[e];
-        return;
-    }
-    const int kvh = is_k ? r - a.n_head : r - a.n_head - a.n_kv;
-    uint8_t *cache = is_k ? a.kc : a.vc;
-    if (a.kv_type == F16) {
-        uint16_t *dst = (uint16_t *)cache + ((size_t)p * a.n_kv + kvh) * hd + lane * epl;
-#pragma unroll
-        for (int e = 0; e < 4; e++)
-            if (e < epl) dst[e] = f2h(y[e]);
-    } else {
-#pragma unroll
-        for (int e = 0; e < 4; e++)
-            if (e < epl) wb[lane * epl + e] = y[e];
-        __syncthreads();                                     // one-wave workgroup
-        const bool own = lane < hd / 4;
-        float o[4] = {0.f, 0.f, 0.f, 0.f};
-        if (own)
-            for (int k = 0; k < 4; k++) o[k] = wb[4 * lane + k];
-        q8_store4(o, lane, own, cache + ((size_t)p * a.n_kv + kvh) * (hd / 32) * 34);
     }
 }
 
