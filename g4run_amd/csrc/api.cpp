@@ -360,13 +360,6 @@ extern "C" int g4h_matmul_describe(const g4h_tensor *W, int nb, int path, char *
     int lpr, upl, wpg;
     int64_t grid;
     gemv_launch_shape(*W, &lpr, &upl, &wpg, &grid);
-    GemvPro pro;
-    pro.kind = PRO_ACT;
-    if (nb == 1 && gemv_p_fits(*W, pro, GemvEpi())) {
-        snprintf(buf, len, "k_gemv_p<%s,lpr=%d,upl=%d> (persistent) grid=%d block=%d", type_name(W->type), lpr, upl,
-                 gemv_p_grid_size(), 64 * 8);
-        return G4H_OK;
-    }
     const int chunk = nb >= 8 ? 8 : nb >= 4 ? 4 : nb >= 2 ? 2 : 1;
     snprintf(buf, len, "k_gemv<%s,nb=%d,lpr=%d,upl=%d> grid=%lld block=%d (x%d launches)", type_name(W->type), chunk, lpr, upl,
              (long long)grid, 64 * wpg, (nb + chunk - 1) / chunk);
@@ -400,20 +393,6 @@ extern "C" int g4h_matmul_ex(const g4h_tensor *W, const float *x, const void *pr
         const hipError_t e = launch_matmul_mfma(*W, x, W->ncols, (const uint8_t *)pre, pre_stride, nb, Y, (uint8_t *)buf, s);
         if (e != hipSuccess) return hip_fail(e, "g4h_matmul: matrix-core launch");
         return G4H_OK;
-    }
-    if (nb == 1 && (!x || (uintptr_t)x % 16 == 0)) {
-        // one token over q4_0 / q8_0 rows: the persistent GEMV, quantizer fused
-        GemvPro pro;
-        pro.kind = x ? PRO_QUANT : PRO_ACT;
-        pro.x = x;
-        pro.n = (int)W->ncols;
-        const GemvEpi epi;
-        if (gemv_p_fits(*W, pro, epi)) {
-            if (!x)
-                if (int rc = check_act("g4h_matmul", W, pre, pre_stride, nb)) return rc;
-            G4_HIP(launch_gemv_p(*W, (const uint8_t *)pre, Y, pro, epi, s));
-            return G4H_OK;
-        }
     }
     const uint8_t *act = (const uint8_t *)pre;
     size_t stride = pre_stride;
