@@ -447,13 +447,20 @@ class Model:
         return out
 
     def host_copy(self):
-        """Every parameter and the KV cache as host arrays (for a CPU check)."""
+        """Every parameter and the KV cache as host arrays (for a CPU check).
+
+        The resident gate/up matrix stores its rows interleaved (gate_i, up_i);
+        it is returned as [gate | up] rows, the order of the reference's fused
+        w_gate_up (model.c:721-729)."""
         c = self.cfg
         w = {k: [] for k in list(_MATS) + list(_NORMS)}
         kc, vc = [], []
         for l in range(c["n_layer"]):
             for k in _MATS:
-                w[k].append(self.matrix(l, k).to_rows())
+                rows = self.matrix(l, k).to_rows()
+                if k == "wgu":
+                    rows = np.concatenate([rows[0::2], rows[1::2]])
+                w[k].append(rows)
             for k in _NORMS:
                 w[k].append(self.norm(l, k))
             a, b = self.kv(l)

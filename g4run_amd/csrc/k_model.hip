@@ -29,8 +29,9 @@ __global__ __launch_bounds__(256) void k_rand_normal(float *y, int64_t n, uint64
 // ------------------------------------------------------------- embedding --
 // x = dequant(row `token` of the tied q8_0 head) * sqrt(n_embd) (model.c:605-612),
 // read from the resident planes (qs [row][blk][32], d fp16); then
-// act = q8_0(rms(x)*w_pre), the first layer's attention-norm activation.
-// 512 threads, n <= 8192.
+// act = q8_0(rms(x)*w_pre), the first layer's attention-norm activation
+// (skipped without w_pre, when that norm runs in the Wqkv GEMV).  512 threads,
+// n <= 8192.
 __global__ __launch_bounds__(512) void k_embed_norm(const int8_t *qs, const uint16_t *sc, int64_t nb, const int *token,
                                                     float *x, int n, float es, const float *w_pre, float eps, uint8_t *act) {
     const int64_t r = *token;
@@ -40,7 +41,7 @@ __global__ __launch_bounds__(512) void k_embed_norm(const int8_t *qs, const uint
         x[i] = v * es;
     }
     __syncthreads();
-    wg_norm_quant<4>(x, nullptr, nullptr, w_pre, eps, n, act);
+    if (w_pre) wg_norm_quant<4>(x, nullptr, nullptr, w_pre, eps, n, act);
 }
 
 // ------------------------------------------------------ norm + quantize --
@@ -55,14 +56,18 @@ __global__ __launch_bounds__(512) void k_norm_quant(float *x, const float *delta
 
 // -------------------------------------------------------- gelu * up --
 // h = gelu(g) * u with the fp16 GELU table (model.c:725-729), quantized to
-// q8_0 for the down projection; 256 threads, 4 elements each.
+// q8_0 for the down projection; gu holds the (gate, up) pairs interleaved,
+// as the Wgu rows are stored.  256 threads, 4 elements each.
 __global__ __launch_bounds__(256) void k_gelu_quant(const float *gu, int n_ff, const uint16_t *tab, uint8_t *act) {
     const int gi = blockIdx.x * 256 + threadIdx.x;
     const bool own = 4 * gi < n_ff;
     float g[4] = {0.f, 0.f, 0.f, 0.f}, u[4] = {0.f, 0.f, 0.f, 0.f}, h[4];
     if (own) {
-        f4(ldf4(gu + 4 * gi), g);
-        f4(ldf4(gu + n_ff + 4 * gi), u);
+        float a[4], b[4];
+        f4(ldf4(gu + 8 * gi), a);
+        f4(ldf4(gu + 8 * gi + 4), b);
+        g[0] = a[0]; u[0] = a[1]; g[1] = a[2]; u[1] = a[3];
+        g[2] = b[0]; u[2] = b[1]; g[3] = b[2]; u[3] = b[3];
     }
 #pragma unroll
     for (int k = 0; k < 4; k++) {

@@ -20,12 +20,14 @@
 #include <algorithm>
 #include <cmath>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <vector>
 
 #include "kernels.h"
 
 using namespace g4;
+
 
 extern "C" int g4h_internal_fail(int status, const char *msg);
 
@@ -75,11 +77,23 @@ struct g4h_model {
     float *rope = nullptr;           // [n_ctx][hd] cos/sin pairs
     uint16_t *gelu = nullptr;        // 65536 fp16 codes
     int *state = nullptr;            // token, pos, npos
-    float *x = nullptr, *xb = nullptr, *qkv = nullptr, *q = nullptr, *att = nullptr, *ff = nullptr, *logits = nullptr;
+    float *x = nullptr, *x2 = nullptr, *xb = nullptr, *qkv = nullptr, *q = nullptr, *att = nullptr, *ff = nullptr, *logits = nullptr;
     uint8_t *act = nullptr, *ws = nullptr;
     size_t act_bytes = 0, ws_bytes = 0;
     std::vector<void *> allocs;
+    int fuse = 0;                    // FUSE_* steps folded into the GEMVs
 };
+
+// Steps of the chain folded into the persistent GEMV family (gemv_p.h):
+//   FUSE_QKV   residual + attention RMSNorm + q8_0 in front of Wqkv
+//   FUSE_GU    residual + FFN RMSNorm + q8_0 in front of Wgu, GELU(gate)*up after it
+//   FUSE_DOWN  q8_0 of h in front of Wdown (with FUSE_GU)
+//   FUSE_HEAD  residual + output RMSNorm + q8_0 in front of the head
+enum { FUSE_QKV = 1, FUSE_GU = 2, FUSE_DOWN = 4, FUSE_HEAD = 8 };
+// measured on the BASELINE decode step (tok/s): none 684, QKV 693, QKV|GU 704,
+// QKV|GU|DOWN 690, all 689 -- the persistent GEMV streams a little slower than
+// the one-shot one, so only the folds that remove two launches pay
+static constexpr int kDefaultFuse = FUSE_QKV | FUSE_GU;
 
 static int model_alloc(g4h_model *m, void **p, size_t bytes) {
     if (int rc = g4h_malloc(p, bytes)) return rc;
@@ -98,17 +112,25 @@ static int model_alloc(g4h_model *m, void **p, size_t bytes) {
         if (rc_) return rc_;        \
     } while (0)
 
-// random matrix: N(0, std) fp32 -> quantized GGUF rows -> resident tensor
-// random matrix: N(0, std) fp32 -> quantized GGUF rows -> resident tensor
-static int init_matrix(int type, int64_t rows, int64_t cols, uint64_t seed, float *tmp_f, uint8_t *tmp_q, g4h_tensor **out,
-                       hipStream_t s) {
+// random matrix: N(0, std) fp32 -> quantized GGUF rows -> resident tensor.
+// With `interleave` the random rows [A (rows/2) | B (rows/2)] are stored in
+// the order A0 B0 A1 B1 ... (the gate/up layout of Wgu).
+static int init_matrix(int type, int64_t rows, int64_t cols, uint64_t seed, float *tmp_f, uint8_t *tmp_q, bool interleave,
+                       g4h_tensor **out, hipStream_t s) {
     if (type != Q8_0 && type != Q4_0) return g4h_internal_fail(G4H_ERR_TYPE, "g4h_model_create: weights must be q4_0 or q8_0");
     M_RC(g4h_tensor_create(type, cols, rows, out));
     const size_t rb = g4h_row_size(type, cols);
+    auto quant = [&](const float *x, uint8_t *y, size_t ys, int64_t nr) {
+        return type == Q8_0 ? launch_quantize_q8_0(x, cols, y, ys, cols, (int)nr, s)
+                            : launch_quantize_q4_0(x, cols, y, ys, cols, (int)nr, s);
+    };
     hipError_t e = launch_rand_normal(tmp_f, rows * cols, seed, 0.0f, 0.02f, s);
-    if (e == hipSuccess)
-        e = type == Q8_0 ? launch_quantize_q8_0(tmp_f, cols, tmp_q, rb, cols, (int)rows, s)
-                         : launch_quantize_q4_0(tmp_f, cols, tmp_q, rb, cols, (int)rows, s);
+    if (e == hipSuccess && interleave) {
+        e = quant(tmp_f, tmp_q, 2 * rb, rows / 2);
+        if (e == hipSuccess) e = quant(tmp_f + (size_t)(rows / 2) * cols, tmp_q + rb, 2 * rb, rows / 2);
+    } else if (e == hipSuccess) {
+        e = quant(tmp_f, tmp_q, rb, rows);
+    }
     int rc = e == hipSuccess ? G4H_OK : g4h_internal_fail(G4H_ERR_HIP, hipGetErrorString(e));
     if (!rc) rc = g4h_tensor_load(*out, tmp_q, 1, s);
     if (rc) { g4h_tensor_free(*out); *out = nullptr; }
@@ -128,6 +150,8 @@ extern "C" int g4h_model_create(const g4h_model_config *cfg, uint64_t seed, g4h_
         return g4h_internal_fail(G4H_ERR_TYPE, "g4h_model_create: wtype q4_0|q8_0, head q8_0, kv f16|q8_0");
     g4h_model *m = new g4h_model();
     m->c = c;
+    m->fuse = kDefaultFuse;
+    if (const char *e = getenv("G4H_DECODE_FUSE")) m->fuse = atoi(e) & 15;
     const int E = c.n_embd, H = c.n_head, KV = c.n_kv, hd = c.head_dim, F = c.n_ff;
     const int qkv_rows = (H + 2 * KV) * hd, qd = H * hd;
     hipStream_t s = nullptr;
@@ -146,16 +170,16 @@ extern "C" int g4h_model_create(const g4h_model_config *cfg, uint64_t seed, g4h_
     uint64_t k = seed * 0x100000001b3ull + 17;
     for (int l = 0; l < c.n_layer && !rc; l++) {
         g4h_tensor *t;
-        if ((rc = init_matrix(c.wtype, qkv_rows, E, k++, tmp_f, tmp_q, &t, s))) break;
+        if ((rc = init_matrix(c.wtype, qkv_rows, E, k++, tmp_f, tmp_q, false, &t, s))) break;
         m->wqkv.push_back(t);
-        if ((rc = init_matrix(c.wtype, E, qd, k++, tmp_f, tmp_q, &t, s))) break;
+        if ((rc = init_matrix(c.wtype, E, qd, k++, tmp_f, tmp_q, false, &t, s))) break;
         m->wo.push_back(t);
-        if ((rc = init_matrix(c.wtype, 2 * F, E, k++, tmp_f, tmp_q, &t, s))) break;
+        if ((rc = init_matrix(c.wtype, 2 * F, E, k++, tmp_f, tmp_q, true, &t, s))) break;
         m->wgu.push_back(t);
-        if ((rc = init_matrix(c.wtype, E, F, k++, tmp_f, tmp_q, &t, s))) break;
+        if ((rc = init_matrix(c.wtype, E, F, k++, tmp_f, tmp_q, false, &t, s))) break;
         m->wdown.push_back(t);
     }
-    if (!rc) rc = init_matrix(c.head_type, c.n_vocab, E, k++, tmp_f, tmp_q, &m->head, s);
+    if (!rc) rc = init_matrix(c.head_type, c.n_vocab, E, k++, tmp_f, tmp_q, false, &m->head, s);
     const hipError_t init_err = hipStreamSynchronize(s);
     g4h_free(tmp_f);
     g4h_free(tmp_q);
@@ -202,6 +226,7 @@ extern "C" int g4h_model_create(const g4h_model_config *cfg, uint64_t seed, g4h_
     const int wide = std::max(std::max(E, 2 * F), std::max(qkv_rows, c.n_vocab));
     if ((rc = model_alloc(m, (void **)&m->state, 64))) return bail(rc);
     if ((rc = model_alloc(m, (void **)&m->x, E * 4))) return bail(rc);
+    if ((rc = model_alloc(m, (void **)&m->x2, E * 4))) return bail(rc);
     if ((rc = model_alloc(m, (void **)&m->xb, E * 4))) return bail(rc);
     if ((rc = model_alloc(m, (void **)&m->qkv, qkv_rows * 4))) return bail(rc);
     if ((rc = model_alloc(m, (void **)&m->q, qd * 4))) return bail(rc);
@@ -262,12 +287,41 @@ extern "C" int g4h_forward_state(g4h_model *m, void *stream) {
     const int E = c.n_embd, H = c.n_head, KV = c.n_kv, hd = c.head_dim, F = c.n_ff;
     int *token = m->state, *npos = m->state + 2;    // state: token, pos, npos = pos + 1
     const size_t ast = m->act_bytes;
-    M_HIP(launch_embed_norm(*m->head, token, m->x, sqrtf((float)E), norm_of(m, 0, G4H_N_ATTN), c.rms_eps, m->act, s));
+    const int fz = m->fuse;
+    float *x = m->x, *xn = m->x2;    // residual; a norm prologue writes x' to xn and the two swap
+    // GEMV over W with the residual update + RMSNorm + q8_0 in its prologue
+    auto norm_gemv = [&](const g4h_tensor &W, const float *delta, const float *w_post, const float *w_pre, float *Y,
+                         bool gelu) {
+        GemvPro pro;
+        pro.kind = PRO_NORM;
+        pro.x = x;
+        pro.x_out = xn;
+        pro.delta = delta;
+        pro.w_post = w_post;
+        pro.w_pre = w_pre;
+        pro.eps = c.rms_eps;
+        pro.n = E;
+        GemvEpi epi;
+        if (gelu) {
+            epi.kind = EPI_GELU;
+            epi.gelu = m->gelu;
+            epi.h = m->ff;
+        }
+        const hipError_t e = launch_gemv_p(W, nullptr, Y, pro, epi, s);
+        std::swap(x, xn);
+        return e;
+    };
+    M_HIP(launch_embed_norm(*m->head, token, x, sqrtf((float)E), (fz & FUSE_QKV) ? nullptr : norm_of(m, 0, G4H_N_ATTN),
+                            c.rms_eps, m->act, s));
     for (int l = 0; l < c.n_layer; l++) {
         uint8_t *kc = m->kv + (size_t)(2 * l) * m->kv_layer_bytes, *vc = kc + m->kv_layer_bytes;
-        if (l) M_HIP(launch_norm_quant(m->x, m->xb, norm_of(m, l - 1, G4H_N_POST_FFW), norm_of(m, l, G4H_N_ATTN), c.rms_eps, E,
-                                       m->act, s));
-        M_HIP(launch_gemv(*m->wqkv[l], m->act, ast, m->qkv, 1, s));
+        const float *prev_post = l ? norm_of(m, l - 1, G4H_N_POST_FFW) : nullptr;
+        if (fz & FUSE_QKV) {
+            M_HIP(norm_gemv(*m->wqkv[l], l ? m->xb : nullptr, prev_post, norm_of(m, l, G4H_N_ATTN), m->qkv, false));
+        } else {
+            if (l) M_HIP(launch_norm_quant(x, m->xb, prev_post, norm_of(m, l, G4H_N_ATTN), c.rms_eps, E, m->act, s));
+            M_HIP(launch_gemv(*m->wqkv[l], m->act, ast, m->qkv, 1, s));
+        }
         QkvArgs qa;
         qa.n_head = H;
         qa.n_kv = KV;
@@ -281,16 +335,33 @@ extern "C" int g4h_forward_state(g4h_model *m, void *stream) {
         qa.eps = c.rms_eps;
         M_HIP(launch_attn_decode(nullptr, m->qkv, qa, 0, npos, c.n_ctx, m->att, m->act, m->ws, s));
         M_HIP(launch_gemv(*m->wo[l], m->act, ast, m->xb, 1, s));
-        M_HIP(launch_norm_quant(m->x, m->xb, norm_of(m, l, G4H_N_POST_ATTN), norm_of(m, l, G4H_N_FFN), c.rms_eps, E, m->act, s));
-        M_HIP(launch_gemv(*m->wgu[l], m->act, ast, m->ff, 1, s));
-        M_HIP(launch_gelu_quant(m->ff, F, m->gelu, m->act, s));
-        M_HIP(launch_gemv(*m->wdown[l], m->act, ast, m->xb, 1, s));
+        if (fz & FUSE_GU) {
+            M_HIP(norm_gemv(*m->wgu[l], m->xb, norm_of(m, l, G4H_N_POST_ATTN), norm_of(m, l, G4H_N_FFN), nullptr, true));
+            if (fz & FUSE_DOWN) {
+                GemvPro pro;
+                pro.kind = PRO_QUANT;
+                pro.x = m->ff;
+                pro.n = F;
+                M_HIP(launch_gemv_p(*m->wdown[l], nullptr, m->xb, pro, GemvEpi(), s));
+            } else {
+                M_HIP(launch_quantize_q8_0(m->ff, F, m->act, ast, F, 1, s));
+                M_HIP(launch_gemv(*m->wdown[l], m->act, ast, m->xb, 1, s));
+            }
+        } else {
+            M_HIP(launch_norm_quant(x, m->xb, norm_of(m, l, G4H_N_POST_ATTN), norm_of(m, l, G4H_N_FFN), c.rms_eps, E, m->act, s));
+            M_HIP(launch_gemv(*m->wgu[l], m->act, ast, m->ff, 1, s));
+            M_HIP(launch_gelu_quant(m->ff, F, m->gelu, m->act, s));
+            M_HIP(launch_gemv(*m->wdown[l], m->act, ast, m->xb, 1, s));
+        }
     }
-    M_HIP(launch_norm_quant(m->x, m->xb, norm_of(m, c.n_layer - 1, G4H_N_POST_FFW), norm_of(m, c.n_layer, 0), c.rms_eps, E,
-                            m->act, s));
-    M_HIP(launch_gemv(*m->head, m->act, ast, m->logits, 1, s));
+    const float *last_post = norm_of(m, c.n_layer - 1, G4H_N_POST_FFW), *out_norm = norm_of(m, c.n_layer, 0);
+    if (fz & FUSE_HEAD) {
+        M_HIP(norm_gemv(*m->head, m->xb, last_post, out_norm, m->logits, false));
+    } else {
+        M_HIP(launch_norm_quant(x, m->xb, last_post, out_norm, c.rms_eps, E, m->act, s));
+        M_HIP(launch_gemv(*m->head, m->act, ast, m->logits, 1, s));
+    }
     M_HIP(launch_argmax_advance(m->logits, c.n_vocab, m->state, s));
-    (void)token;
     return G4H_OK;
 }
 

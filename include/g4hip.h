@@ -203,7 +203,9 @@ int  g4h_forward_state(g4h_model *m, void *stream);
 int  g4h_model_set_state(g4h_model *m, int token, int pos, void *stream);
 int  g4h_model_get_state(g4h_model *m, int *token, int *pos, void *stream);
 const float *g4h_model_logits(const g4h_model *m);
-/* Parameter access (for checking against a CPU implementation). */
+/* Parameter access (for checking against a CPU implementation).  The
+ * G4H_W_GU matrix holds its 2*n_ff rows interleaved: row 2i is gate row i,
+ * row 2i+1 is up row i (the reference's w_gate_up is [gate | up]). */
 g4h_tensor *g4h_model_matrix(g4h_model *m, int layer, int which);
 float      *g4h_model_norm(g4h_model *m, int layer, int which);
 int         g4h_model_kv(g4h_model *m, int layer, void **k_dev, void **v_dev, size_t *bytes);
