@@ -76,6 +76,7 @@ _SIGS = [
     ("g4h_matmul_describe", _int, [_vp, _int, _int, C.c_char_p, C.c_size_t]),
     ("g4h_block_sums", _int, [_vp, _vp, _sz, _int, _vp, _vp]),
     ("g4h_attn_workspace_bytes", _sz, [_int, _int, _int]),
+    ("g4h_attn_passes", _int, [_int, _int, _int, _int, _int, C.POINTER(_int)]),
     ("g4h_attn_decode", _int, [_vp, _vp, _vp, _int, _int, _int, _int, _int, _vp, _vp, _sz, _vp]),
     ("g4h_kv_store", _int, [_int, _vp, _vp, _int, _int, _sz, _vp]),
     ("g4h_model_create", _int, [_vp, C.c_uint64, C.POINTER(_vp)]),
@@ -335,6 +336,13 @@ def n_block_sums(W: Tensor) -> int:
 # ----------------------------------------------------------------- attention
 def attn_workspace_bytes(n_head: int, hd: int, n_pos: int) -> int:
     return lib().g4h_attn_workspace_bytes(n_head, hd, n_pos)
+
+
+def attn_passes(kv_type: int, n_head: int, n_kv: int, hd: int, n_pos: int) -> int:
+    """1 when this shape runs as one fused launch, 3 for the three-pass form."""
+    n = _int()
+    check(lib().g4h_attn_passes(kv_type, n_head, n_kv, hd, n_pos, C.byref(n)))
+    return n.value
 
 
 def attn_decode(q, kc, vc, kv_type: int, n_head: int, n_kv: int, hd: int, n_pos: int, out, ws=None, stream=None) -> None:

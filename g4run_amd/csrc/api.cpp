@@ -448,6 +448,15 @@ static int check_attn_shape(const char *fn, int kv_type, int n_head, int n_kv, i
     return G4H_OK;
 }
 
+extern "C" int g4h_attn_passes(int kv_type, int n_head, int n_kv, int hd, int n_pos, int *passes) {
+    G4_NEED_INIT();
+    if (!passes) return fail(G4H_ERR_ARG, "g4h_attn_passes: null pointer");
+    if (int rc = check_attn_shape("g4h_attn_passes", kv_type, n_head, n_kv, hd)) return rc;
+    if (n_pos <= 0) return fail(G4H_ERR_ARG, "g4h_attn_passes: n_pos=%d", n_pos);
+    *passes = attn_fused_fits(kv_type, n_head, n_kv, hd, n_pos) ? 1 : 3;
+    return G4H_OK;
+}
+
 extern "C" int g4h_attn_decode(const float *q, const void *kc, const void *vc, int kv_type, int n_head, int n_kv, int hd,
                                int n_pos, float *out, void *ws, size_t ws_bytes, void *stream) {
     G4_NEED_INIT();

@@ -28,6 +28,8 @@
 //            row for the output projection (quants.c:74-109).
 // Only the fp32 order of the value sum and the double grouping of the
 // normaliser differ from the CPU's sequential loops.
+#include <algorithm>
+
 #include "formats.h"
 #include "kernels.h"
 #include "steps.h"
@@ -128,14 +130,31 @@ struct AttnCtx {
     int nc;                  // chunk stride of the workspace
     float *out;              // [n_head][hd]
     uint8_t *q8out;          // optional q8_0 rows of out
+    // fused launch: tagged statistics T [n_head][nc][3] and partials
+    // PT [n_head][nc][hd]; this launch's tag is *epoch * tag_mul + tag_add + 1
+    uint64_t *T, *PT;
+    const unsigned *epoch;
+    unsigned tag_mul, tag_add;
+    unsigned *err;           // set when a poll gives up
 };
 
 __device__ __forceinline__ int npos_of(const AttnCtx &c) { return c.npos_dev ? *c.npos_dev : c.npos; }
 
+// loads and stores of data shared between the workgroups of one launch:
+// agent scope, coherent across the XCDs' L2 caches
+template <class T>
+__device__ __forceinline__ T ld_ag(const T *p) {
+    return __hip_atomic_load(const_cast<T *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+template <class T>
+__device__ __forceinline__ void st_ag(T *p, T v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // chunk statistics of GRP heads from per-thread scores: m_c over the valid
 // lanes (wave max + LDS), then l_c = sum exp((double)(s - m_c)) over the lanes
 // that own a position (`once`: one lane of a pair), waves in order
-template <int GRP, int NW>
+template <int GRP, int NW, bool AG>
 __device__ void chunk_stats(const float (&s)[GRP], bool ok, bool once, const AttnCtx &c, int h0, int ch, float (*wm)[GRP],
                             double (*wl)[GRP]) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -159,8 +178,13 @@ __device__ void chunk_stats(const float (&s)[GRP], bool ok, bool once, const Att
         const int g = threadIdx.x;
         double l = 0.0;
         for (int w = 0; w < NW; w++) l += wl[w][g];
-        c.Mc[(size_t)(h0 + g) * c.nc + ch] = mc[g];
-        c.Lc[(size_t)(h0 + g) * c.nc + ch] = l;
+        if constexpr (AG) {
+            st_ag(&c.Mc[(size_t)(h0 + g) * c.nc + ch], mc[g]);
+            st_ag(&c.Lc[(size_t)(h0 + g) * c.nc + ch], l);
+        } else {
+            c.Mc[(size_t)(h0 + g) * c.nc + ch] = mc[g];
+            c.Lc[(size_t)(h0 + g) * c.nc + ch] = l;
+        }
     }
 }
 
@@ -170,91 +194,97 @@ __device__ void chunk_stats(const float (&s)[GRP], bool ok, bool once, const Att
 // 8k+4..8k+7 (the shipped dot's eight lanes split in two), combined with the
 // same horizontal-sum tree.  Every K load of a lane is issued before any use;
 // the lane pair of the current position then takes the new key from LDS.
+
+// preparation state: rows r = 0..GRP-1 (queries), then key and value in the
+// chunk of the current position; row r on wave r % 4, slot r / 4
 template <int GRP>
-__global__ __launch_bounds__(256) void k_attn_scores_f16(AttnCtx c) {
-    __shared__ __align__(16) float4 qf[GRP][64];              // fp16-rounded query
-    __shared__ __align__(16) uint16_t kpos[256];              // the new key row (fp16 bits)
-    __shared__ float wm[4][GRP];
-    __shared__ double wl[4][GRP];
-    const int npos = npos_of(c);
-    const int kvh = blockIdx.x, ch = blockIdx.y, t = threadIdx.x;
-    const int lane = t & 63, wave = t >> 6, hf = lane & 1;
-    const int hd = c.a.hd, n_kv = c.a.n_kv, h0 = kvh * GRP, p = npos - 1;
-    if (ch * ATT_CHUNK >= npos) return;
-    const bool pos_chunk = c.qkv && ch == p / ATT_CHUNK;
-    // 1. preparation loads: rows r = 0..GRP-1 (queries), then key and value in
-    //    the position's chunk; row r on wave r % 4, slot r / 4
-    constexpr int SL = (GRP + 2 + 3) / 4;
-    const int nrow = c.qkv ? GRP + (pos_chunk ? 2 : 0) : 0;
+struct PrepF16 {
+    static constexpr int SL = (GRP + 2 + 3) / 4;
     PrepRow pr[SL];
     float cs[4], sn[4];
-    constexpr int QPT = GRP;                                   // ready queries: GRP*hd <= GRP*256 elements
-    float qv[QPT];
+    float qv[GRP];                   // given queries: GRP*hd <= 256*GRP elements
+    int nrow;
+};
+
+template <int GRP, int HD>
+__device__ __forceinline__ void prep_f16_issue(PrepF16<GRP> &st, const AttnCtx &c, int kvh, int p, bool pos_chunk) {
+    constexpr int hd = HD;
+    const int t = threadIdx.x, wave = t >> 6, h0 = kvh * GRP;
+    st.nrow = c.qkv ? GRP + (pos_chunk ? 2 : 0) : 0;
     if (c.qkv) {
-        rope_load(cs, sn, c.a.rope, p, hd);
+        rope_load(st.cs, st.sn, c.a.rope, p, hd);
 #pragma unroll
-        for (int sl = 0; sl < SL; sl++) {
+        for (int sl = 0; sl < PrepF16<GRP>::SL; sl++) {
             const int r = wave + 4 * sl;
-            if (r < nrow) {
-                const int src_row = r < GRP ? h0 + r : r == GRP ? c.a.n_head + kvh : c.a.n_head + n_kv + kvh;
+            if (r < st.nrow) {
+                const int src_row = r < GRP ? h0 + r : r == GRP ? c.a.n_head + kvh : c.a.n_head + c.a.n_kv + kvh;
                 const float *w = r < GRP ? c.a.q_norm : r == GRP ? c.a.k_norm : nullptr;
-                prep_load(pr[sl], c.qkv + (size_t)src_row * hd, w, hd);
+                prep_load(st.pr[sl], c.qkv + (size_t)src_row * hd, w, hd);
             }
         }
     } else {
 #pragma unroll
-        for (int k = 0; k < QPT; k++) {
+        for (int k = 0; k < GRP; k++) {
             const int i = t + 256 * k;
-            qv[k] = i < GRP * hd ? c.q[(size_t)h0 * hd + i] : 0.0f;
+            st.qv[k] = i < GRP * hd ? c.q[(size_t)h0 * hd + i] : 0.0f;
         }
     }
-    // 2. every K load of the lane
-    const int j = ch * ATT_CHUNK + wave * 32 + (lane >> 1);
-    const bool ok = j < npos;
-    const uint2 *row = (const uint2 *)(c.a.kc + ((size_t)(ok ? j : npos - 1) * n_kv + kvh) * hd * 2) + hf;
-    const int nk = hd >> 3;
-    uint2 kv[32];
-#pragma unroll
-    for (int k = 0; k < 32; k++)
-        if (k < nk) kv[k] = row[2 * k];
-    // 3. preparation arithmetic: queries to LDS; key / value rows to the caches
+}
+
+// queries (fp16-rounded) into LDS; the key / value rows of the current
+// position into the caches and, as fp16 bits, into kpos / vpos (vpos optional)
+template <int GRP, int HD>
+__device__ __forceinline__ void prep_f16_finish(const PrepF16<GRP> &st, const AttnCtx &c, int kvh, int p, float4 (*qf)[64],
+                                                uint16_t *kpos, uint16_t *vpos) {
+    constexpr int hd = HD, epl = hd >> 6;
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     if (c.qkv) {
-        const int epl = hd >> 6;
 #pragma unroll
-        for (int sl = 0; sl < SL; sl++) {
+        for (int sl = 0; sl < PrepF16<GRP>::SL; sl++) {
             const int r = wave + 4 * sl;
-            if (r < nrow) {                                          // uniform over the wave
+            if (r < st.nrow) {                                          // uniform over the wave
                 float y[4];
-                prep_finish(pr[sl], r <= GRP, r <= GRP, cs, sn, hd, c.a.eps, y);
+                prep_finish(st.pr[sl], r <= GRP, r <= GRP, st.cs, st.sn, hd, c.a.eps, y);
                 if (r < GRP) {
 #pragma unroll
                     for (int e = 0; e < 4; e++)
                         if (e < epl) ((float *)qf[r])[lane * epl + e] = h2f(f2h(y[e]));
                 } else {
                     uint8_t *cache = r == GRP ? c.a.kc : c.a.vc;
-                    cache_store(y, F16, cache + ((size_t)p * n_kv + kvh) * hd * 2, hd, nullptr);
-                    if (r == GRP) {
+                    cache_store(y, F16, cache + ((size_t)p * c.a.n_kv + kvh) * hd * 2, hd, nullptr);
+                    uint16_t *keep = r == GRP ? kpos : vpos;
+                    if (keep) {
 #pragma unroll
                         for (int e = 0; e < 4; e++)
-                            if (e < epl) kpos[lane * epl + e] = f2h(y[e]);
+                            if (e < epl) keep[lane * epl + e] = f2h(y[e]);
                     }
                 }
             }
         }
     } else {
 #pragma unroll
-        for (int k = 0; k < QPT; k++) {
+        for (int k = 0; k < GRP; k++) {
             const int i = t + 256 * k;
-            if (i < GRP * hd) ((float *)qf[i / hd])[i % hd] = h2f(f2h(qv[k]));
+            if (i < GRP * hd) ((float *)qf[i / hd])[i % hd] = h2f(f2h(st.qv[k]));
         }
     }
-    __syncthreads();
-    if (pos_chunk && j == p) {                                       // the new key, not the stale cache row
+}
+
+// the lane's K loads: 8 bytes of each 16-byte group of row j (clamped to the
+// last position), the half hf of the pair
+template <int HD>
+__device__ __forceinline__ void k_rows_load(uint2 (&kv)[32], const AttnCtx &c, int kvh, int j, int npos, int hf) {
+    constexpr int hd = HD, nk = hd >> 3;
+    const uint2 *row = (const uint2 *)(c.a.kc + ((size_t)min(j, npos - 1) * c.a.n_kv + kvh) * hd * 2) + hf;
 #pragma unroll
-        for (int k = 0; k < 32; k++)
-            if (k < nk) kv[k] = ((const uint2 *)kpos)[2 * k + hf];
-    }
-    // 4. scores
+    for (int k = 0; k < 32; k++)
+        if (k < nk) kv[k] = row[2 * k];
+}
+
+// the GRP scores of the lane pair's position (both lanes hold them)
+template <int GRP, int HD>
+__device__ __forceinline__ void scores_f16(const uint2 (&kv)[32], int hf, const float4 (*qf)[64], float (&s)[GRP]) {
+    constexpr int nk = HD >> 3;
     float acc[GRP][4];
 #pragma unroll
     for (int g = 0; g < GRP; g++)
@@ -275,7 +305,6 @@ __global__ __launch_bounds__(256) void k_attn_scores_f16(AttnCtx c) {
             }
         }
     }
-    float s[GRP];
 #pragma unroll
     for (int g = 0; g < GRP; g++) {
         // lane l of the eight is acc[l & 3] of the pair member l >> 2; r_i = v[i+4] + v[i]
@@ -283,15 +312,47 @@ __global__ __launch_bounds__(256) void k_attn_scores_f16(AttnCtx c) {
 #pragma unroll
         for (int i = 0; i < 4; i++) r[i] = acc[g][i] + shfl_xor(acc[g][i], 1);
         s[g] = (r[0] + r[2]) + (r[1] + r[3]);
-        if (ok && hf == 0) c.S[(size_t)(h0 + g) * npos + j] = s[g];
     }
-    chunk_stats<GRP, 4>(s, ok, hf == 0, c, h0, ch, wm, wl);
+}
+
+template <int GRP, int HD>
+__global__ __launch_bounds__(256) void k_attn_scores_f16(AttnCtx c) {
+    __shared__ __align__(16) float4 qf[GRP][64];              // fp16-rounded query
+    __shared__ __align__(16) uint16_t kpos[256];              // the new key row (fp16 bits)
+    __shared__ float wm[4][GRP];
+    __shared__ double wl[4][GRP];
+    const int npos = npos_of(c);
+    const int kvh = blockIdx.x, ch = blockIdx.y, t = threadIdx.x;
+    const int lane = t & 63, wave = t >> 6, hf = lane & 1;
+    constexpr int hd = HD;
+    const int h0 = kvh * GRP, p = npos - 1;
+    if (ch * ATT_CHUNK >= npos) return;
+    const bool pos_chunk = c.qkv && ch == p / ATT_CHUNK;
+    PrepF16<GRP> st;
+    prep_f16_issue<GRP, HD>(st, c, kvh, p, pos_chunk);
+    const int j = ch * ATT_CHUNK + wave * 32 + (lane >> 1);
+    const bool ok = j < npos;
+    uint2 kv[32];
+    k_rows_load<HD>(kv, c, kvh, j, npos, hf);
+    prep_f16_finish<GRP, HD>(st, c, kvh, p, qf, kpos, nullptr);
+    __syncthreads();
+    if (pos_chunk && j == p) {                                       // the new key, not the stale cache row
+#pragma unroll
+        for (int k = 0; k < 32; k++)
+            if (k < (hd >> 3)) kv[k] = ((const uint2 *)kpos)[2 * k + hf];
+    }
+    float s[GRP];
+    scores_f16<GRP, HD>(kv, hf, qf, s);
+#pragma unroll
+    for (int g = 0; g < GRP; g++)
+        if (ok && hf == 0) c.S[(size_t)(h0 + g) * npos + j] = s[g];
+    chunk_stats<GRP, 4, false>(s, ok, hf == 0, c, h0, ch, wm, wl);
 }
 
 // q8_0 cache.  128 threads, one lane per position; the query is q8_0-quantized
 // per block (model.c:533) and each block pair of the row is dotted in the AVX2
 // order of quants.c:984-999.
-template <int GRP>
+template <int GRP, int HD>
 __global__ __launch_bounds__(128) void k_attn_scores_q8(AttnCtx c) {
     __shared__ __align__(16) int4 qq[GRP][8][2];
     __shared__ float qd[GRP][8];
@@ -302,7 +363,8 @@ __global__ __launch_bounds__(128) void k_attn_scores_q8(AttnCtx c) {
     __shared__ double wl[2][GRP];
     const int npos = npos_of(c);
     const int kvh = blockIdx.x, ch = blockIdx.y, t = threadIdx.x, lane = t & 63, wave = t >> 6;
-    const int hd = c.a.hd, n_kv = c.a.n_kv, h0 = kvh * GRP, p = npos - 1;
+    constexpr int hd = HD;
+    const int n_kv = c.a.n_kv, h0 = kvh * GRP, p = npos - 1;
     if (ch * ATT_CHUNK >= npos) return;
     const bool pos_chunk = c.qkv && ch == p / ATT_CHUNK;
     // queries (prepared here or given) as fp32 rows in LDS; new key/value to the caches
@@ -379,23 +441,89 @@ __global__ __launch_bounds__(128) void k_attn_scores_q8(AttnCtx c) {
         s[g] = (r0 + r2) + (r1 + r3);
         if (ok) c.S[(size_t)(h0 + g) * npos + j] = s[g];
     }
-    chunk_stats<GRP, 2>(s, ok, true, c, h0, ch, wm, wl);
+    chunk_stats<GRP, 2, false>(s, ok, true, c, h0, ch, wm, wl);
 }
 
 // ------------------------------------------------------------ V partials --
+// f16 V rows: lane owns elements 4*lane .. 4*lane+3 of rows j0 .. j0+31
+// (clamped to the last position; lanes beyond hd/4 idle)
+template <int HD>
+__device__ __forceinline__ void v_rows_load(uint2 (&vv)[32], const AttnCtx &c, int kvh, int j0, int npos) {
+    constexpr int hd = HD;
+    const int lane = threadIdx.x & 63;
+    if (4 * lane < hd) {
+#pragma unroll
+        for (int k = 0; k < 32; k++) {
+            const int j = min(j0 + k, npos - 1);
+            vv[k] = *((const uint2 *)(c.a.vc + ((size_t)j * c.a.n_kv + kvh) * hd * 2) + lane);
+        }
+    }
+}
+
+// o[g] = sum over the wave's positions (in order) of w_j * V_j.  Positions
+// past the last one carry weight 0 (their rows are the last row again), which
+// leaves every sum as the loop that stops at the last position gives it.
+template <int GRP>
+__device__ __forceinline__ void v_accum_f16(const uint2 (&vv)[32], const float (*wts)[ATT_CHUNK], float (&o)[GRP][4]) {
+    const int wave = threadIdx.x >> 6;
+    float4 w4[GRP][8];
+#pragma unroll
+    for (int g = 0; g < GRP; g++)
+#pragma unroll
+        for (int q = 0; q < 8; q++) w4[g][q] = *(const float4 *)&wts[g][wave * 32 + 4 * q];
+#pragma unroll
+    for (int g = 0; g < GRP; g++)
+#pragma unroll
+        for (int e = 0; e < 4; e++) o[g][e] = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 32; k++) {
+        const float v[4] = {h2f((uint16_t)(vv[k].x & 0xffff)), h2f((uint16_t)(vv[k].x >> 16)),
+                            h2f((uint16_t)(vv[k].y & 0xffff)), h2f((uint16_t)(vv[k].y >> 16))};
+#pragma unroll
+        for (int g = 0; g < GRP; g++) {
+            const float4 q4 = w4[g][k >> 2];
+            const float w = (k & 3) == 0 ? q4.x : (k & 3) == 1 ? q4.y : (k & 3) == 2 ? q4.z : q4.w;
+#pragma unroll
+            for (int e = 0; e < 4; e++) o[g][e] = __builtin_fmaf(w, v[e], o[g][e]);
+        }
+    }
+}
+
+// the four waves' partials added in order into P[h][ch][hd]
+template <int GRP, int HD, bool AG>
+__device__ __forceinline__ void v_partial_store(const float (&o)[GRP][4], float (*part)[GRP][256], const AttnCtx &c, int h0,
+                                                int ch) {
+    constexpr int hd = HD;
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    if (4 * lane < hd) {
+#pragma unroll
+        for (int g = 0; g < GRP; g++)
+            *(float4 *)&part[wave][g][4 * lane] = make_float4(o[g][0], o[g][1], o[g][2], o[g][3]);
+    }
+    __syncthreads();
+    for (int i = t; i < GRP * hd; i += 256) {
+        const int g = i / hd, e = i - g * hd;
+        const float r = ((part[0][g][e] + part[1][g][e]) + part[2][g][e]) + part[3][g][e];
+        float *dst = &c.P[((size_t)(h0 + g) * c.nc + ch) * hd + e];
+        if constexpr (AG) st_ag(dst, r);
+        else *dst = r;
+    }
+}
+
 // grid (n_kv, chunks of 128), 256 threads.  M and the normaliser from the
 // chunk statistics; the chunk's weights go to LDS once; each wave then
 // accumulates w_j * V_j over its 32 positions (all V loads of the lane issued
 // up front), lane owning 4 consecutive elements; the waves add in order into
 // the partial P[h][c][hd].
-template <int KV, int GRP>
+template <int KV, int GRP, int HD>
 __global__ __launch_bounds__(256) void k_attn_v(AttnCtx c) {
     __shared__ float part[4][GRP][256];
-    __shared__ float wl[GRP][ATT_CHUNK];
+    __shared__ __align__(16) float wl[GRP][ATT_CHUNK];
     __shared__ float inv_s[GRP], max_s[GRP];
     const int npos = npos_of(c);
     const int kvh = blockIdx.x, ch = blockIdx.y, t = threadIdx.x, lane = t & 63, wave = t >> 6;
-    const int hd = c.a.hd, n_kv = c.a.n_kv, h0 = kvh * GRP;
+    constexpr int hd = HD;
+    const int n_kv = c.a.n_kv, h0 = kvh * GRP;
     if (ch * ATT_CHUNK >= npos) return;
     const int j0 = ch * ATT_CHUNK + wave * 32;
     const int nch = (npos + ATT_CHUNK - 1) / ATT_CHUNK;
@@ -420,13 +548,7 @@ __global__ __launch_bounds__(256) void k_attn_v(AttnCtx c) {
     // 2. the V rows: lane owns elements 4*lane .. 4*lane+3 (lanes beyond hd/4 idle)
     const bool lane_ok = 4 * lane < hd;
     uint2 vv[32];
-    if constexpr (KV == F16) {
-#pragma unroll
-        for (int k = 0; k < 32; k++) {
-            const int j = min(j0 + k, npos - 1);
-            if (lane_ok) vv[k] = *((const uint2 *)(c.a.vc + ((size_t)j * n_kv + kvh) * hd * 2) + lane);
-        }
-    }
+    if constexpr (KV == F16) v_rows_load<HD>(vv, c, kvh, j0, npos);
     // 3. global max and normaliser (chunks beyond 64 in further passes)
 #pragma unroll
     for (int q = 0; q < HPW; q++) {
@@ -456,30 +578,18 @@ __global__ __launch_bounds__(256) void k_attn_v(AttnCtx c) {
             const int g = i / ATT_CHUNK, pp = i - g * ATT_CHUNK;
             const float e = (float)exp((double)(sv[k] - max_s[g]));
             const float w = e * inv_s[g];
-            wl[g][pp] = KV == F16 ? h2f(f2h(w)) : w;
+            wl[g][pp] = ch * ATT_CHUNK + pp >= npos ? 0.0f : KV == F16 ? h2f(f2h(w)) : w;
         }
     }
     __syncthreads();
     float o[GRP][4];
-#pragma unroll
-    for (int g = 0; g < GRP; g++)
-#pragma unroll
-        for (int e = 0; e < 4; e++) o[g][e] = 0.0f;
     if constexpr (KV == F16) {
-#pragma unroll
-        for (int k = 0; k < 32; k++) {
-            if (j0 + k < npos) {
-                const float v[4] = {h2f((uint16_t)(vv[k].x & 0xffff)), h2f((uint16_t)(vv[k].x >> 16)),
-                                    h2f((uint16_t)(vv[k].y & 0xffff)), h2f((uint16_t)(vv[k].y >> 16))};
-#pragma unroll
-                for (int g = 0; g < GRP; g++) {
-                    const float w = wl[g][wave * 32 + k];
-#pragma unroll
-                    for (int e = 0; e < 4; e++) o[g][e] = __builtin_fmaf(w, v[e], o[g][e]);
-                }
-            }
-        }
+        v_accum_f16<GRP>(vv, wl, o);
     } else {
+#pragma unroll
+        for (int g = 0; g < GRP; g++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) o[g][e] = 0.0f;
         for (int k = 0; k < 32; k++) {
             const int j = j0 + k;
             if (j >= npos) break;
@@ -498,27 +608,15 @@ __global__ __launch_bounds__(256) void k_attn_v(AttnCtx c) {
             }
         }
     }
-    if (lane_ok) {
-#pragma unroll
-        for (int g = 0; g < GRP; g++)
-            *(float4 *)&part[wave][g][4 * lane] = make_float4(o[g][0], o[g][1], o[g][2], o[g][3]);
-    }
-    __syncthreads();
-    for (int i = t; i < GRP * hd; i += 256) {
-        const int g = i / hd, e = i - g * hd;
-        const float r = ((part[0][g][e] + part[1][g][e]) + part[2][g][e]) + part[3][g][e];
-        c.P[((size_t)(h0 + g) * c.nc + ch) * hd + e] = r;
-    }
+    v_partial_store<GRP, HD, false>(o, part, c, h0, ch);
 }
 
 // -------------------------------------------------------------- combine --
 // out[h][e] = sum over chunks in order (32 loads of a thread issued before the
-// adds); with q8out, each head row is also quantized to q8_0.  grid n_head.
-__global__ __launch_bounds__(256) void k_attn_combine(AttnCtx c) {
-    __shared__ float row[256];
-    const int npos = npos_of(c);
-    const int h = blockIdx.x, e = threadIdx.x, hd = c.a.hd;
-    const int nch = (npos + ATT_CHUNK - 1) / ATT_CHUNK;
+// adds); with q8out, the head row is also quantized to q8_0.  256 threads.
+template <bool AG>
+__device__ __forceinline__ void combine_head(const AttnCtx &c, int h, int nch, float *row) {
+    const int e = threadIdx.x, hd = c.a.hd;
     if (e < hd) {
         const float *p = c.P + (size_t)h * c.nc * hd + e;
         float r = 0.0f;
@@ -526,21 +624,271 @@ __global__ __launch_bounds__(256) void k_attn_combine(AttnCtx c) {
         for (; k0 + 32 <= nch; k0 += 32) {
             float v[32];
 #pragma unroll
-            for (int k = 0; k < 32; k++) v[k] = p[(size_t)(k0 + k) * hd];
+            for (int k = 0; k < 32; k++) v[k] = AG ? ld_ag(p + (size_t)(k0 + k) * hd) : p[(size_t)(k0 + k) * hd];
 #pragma unroll
             for (int k = 0; k < 32; k++) r += v[k];
         }
-        for (; k0 < nch; k0++) r += p[(size_t)k0 * hd];
+        for (; k0 < nch; k0++) r += AG ? ld_ag(p + (size_t)k0 * hd) : p[(size_t)k0 * hd];
         c.out[(size_t)h * hd + e] = r;
         row[e] = r;
     }
-    if (!c.q8out) return;
-    __syncthreads();
-    const bool own = e < hd / 4;
-    float v[4] = {0.f, 0.f, 0.f, 0.f};
-    if (own)
-        for (int k = 0; k < 4; k++) v[k] = row[4 * e + k];
-    if (e < 64) q8_store4(v, e, own, c.q8out + (size_t)h * (hd / 32) * 34);
+    if (c.q8out) {                                                   // uniform
+        __syncthreads();
+        const bool own = e < hd / 4;
+        float v[4] = {0.f, 0.f, 0.f, 0.f};
+        if (own)
+            for (int k = 0; k < 4; k++) v[k] = row[4 * e + k];
+        if (e < 64) q8_store4(v, e, own, c.q8out + (size_t)h * (hd / 32) * 34);
+        __syncthreads();                                             // row is reused for the next head
+    }
+}
+
+// grid n_head
+__global__ __launch_bounds__(256) void k_attn_combine(AttnCtx c) {
+    __shared__ float row[256];
+    const int npos = npos_of(c);
+    combine_head<false>(c, blockIdx.x, (npos + ATT_CHUNK - 1) / ATT_CHUNK, row);
+}
+
+// ------------------------------------------------------------ fused (f16) --
+// The three passes in one launch for an f16 cache, on a grid (KV head, chunk)
+// that the device holds resident all at once (the host checks occupancy).
+// A workgroup loads its chunk's K rows, computes the scores and chunk
+// statistics as the score pass does and publishes m_c and l_c; its V loads
+// go out next, so they stream while the other chunks' statistics arrive.  It
+// then reads every chunk's statistics of its heads, forms the weights and
+// value partial as the V pass does and publishes the partial.  Finally all
+// workgroups of the KV head (chunks past the last position included) share
+// the combine: 32-element blocks of its output rows, each summed over the
+// chunks in order and, with q8out, quantized to one q8_0 block.
+//
+// Hand-off without counters: every published value is a 64-bit word, the
+// value's bits low and the launch's tag high, stored at agent scope (coherent
+// across the XCDs' L2 caches).  A 64-bit store is single-copy atomic, so a
+// reader that sees the current tag sees the value stored with it; readers poll
+// until every word they need carries the tag.  Tags never repeat on one
+// workspace (see AttnCtx::tag).  A poll gives up after ATT_SPIN_LIMIT tries:
+// it sets the error word and writes NaN into the outputs it owns, so the
+// launch always ends.  Same arithmetic as the three passes: outputs are
+// bit-identical to theirs.
+constexpr unsigned ATT_SPIN_LIMIT = 1u << 20;
+constexpr int ATT_FUSED_MAXC = 128;  // chunks per KV head (two per lane)
+
+__device__ __forceinline__ uint32_t tag_of(const AttnCtx &c) { return *c.epoch * c.tag_mul + c.tag_add + 1u; }
+__device__ __forceinline__ void st_tag(uint64_t *p, uint32_t bits, uint32_t tag) { st_ag(p, ((uint64_t)tag << 32) | bits); }
+
+// N tagged words: all loads issued together; while any tag is not yet
+// current, the stale words are reloaded together
+template <int N>
+__device__ __forceinline__ bool poll_words(const uint64_t *const (&src)[N], const bool (&need)[N], uint32_t tag,
+                                           uint32_t (&bits)[N]) {
+    uint64_t w[N];
+#pragma unroll
+    for (int k = 0; k < N; k++) w[k] = need[k] ? ld_ag(src[k]) : ((uint64_t)tag << 32);
+    for (unsigned it = 0;; it++) {
+        bool all = true;
+#pragma unroll
+        for (int k = 0; k < N; k++) all &= (uint32_t)(w[k] >> 32) == tag;
+        if (all) break;
+        if (it == ATT_SPIN_LIMIT) return false;
+        __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+        for (int k = 0; k < N; k++)
+            if ((uint32_t)(w[k] >> 32) != tag) w[k] = ld_ag(src[k]);
+    }
+#pragma unroll
+    for (int k = 0; k < N; k++) bits[k] = (uint32_t)w[k];
+    return true;
+}
+
+template <int GRP, int HD>
+__global__ __launch_bounds__(256) void k_attn_fused_f16(AttnCtx c) {
+    __shared__ __align__(16) float4 qf[GRP][64];
+    __shared__ __align__(16) uint16_t kpos[256], vpos[256];
+    __shared__ float wm[4][GRP];
+    __shared__ double wl[4][GRP];
+    __shared__ __align__(16) float wts[GRP][ATT_CHUNK];
+    __shared__ float inv_s[GRP], max_s[GRP];
+    __shared__ __align__(16) float part[4][GRP][256];
+    __shared__ float vals[ATT_FUSED_MAXC * 32];                      // combine: [chunk][32]
+    __shared__ int bad;
+    const int npos = npos_of(c);
+    const uint32_t tag = tag_of(c);
+    const int kvh = blockIdx.x, ch = blockIdx.y, t = threadIdx.x;
+    const int lane = t & 63, wave = t >> 6, hf = lane & 1;
+    constexpr int hd = HD;
+    const int h0 = kvh * GRP, p = npos - 1;
+    const int nch = (npos + ATT_CHUNK - 1) / ATT_CHUNK;
+    const bool live = ch < nch;                                      // uniform over the workgroup
+    if (t == 0) bad = 0;
+    if (live) {
+        const int j = ch * ATT_CHUNK + wave * 32 + (lane >> 1), j0 = ch * ATT_CHUNK + wave * 32;
+        const bool pos_chunk = c.qkv && ch == p / ATT_CHUNK;
+        float s[GRP];
+        {
+            PrepF16<GRP> st;
+            prep_f16_issue<GRP, HD>(st, c, kvh, p, pos_chunk);
+            uint2 kv[32];
+            k_rows_load<HD>(kv, c, kvh, j, npos, hf);
+            prep_f16_finish<GRP, HD>(st, c, kvh, p, qf, kpos, vpos);
+            __syncthreads();
+            if (pos_chunk && j == p) {                               // the new key, not the stale cache row
+#pragma unroll
+                for (int k = 0; k < 32; k++)
+                    if (k < (hd >> 3)) kv[k] = ((const uint2 *)kpos)[2 * k + hf];
+            }
+            scores_f16<GRP, HD>(kv, hf, qf, s);
+        }
+        // chunk statistics (as chunk_stats), published as tagged words
+        const bool ok = j < npos, once = hf == 0;
+#pragma unroll
+        for (int g = 0; g < GRP; g++) {
+            const float m = wave_max(ok ? s[g] : -INFINITY);
+            if (lane == 0) wm[wave][g] = m;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int g = 0; g < GRP; g++) {
+            float mc = wm[0][g];
+            for (int w = 1; w < 4; w++) mc = fmaxf(mc, wm[w][g]);
+            const double e = ok && once ? exp((double)(s[g] - mc)) : 0.0;
+            const double l = wave_sum_d(e);
+            if (lane == 0) wl[wave][g] = l;
+        }
+        __syncthreads();
+        if (t < GRP) {
+            const int g = t;
+            float mc = wm[0][g];
+            for (int w = 1; w < 4; w++) mc = fmaxf(mc, wm[w][g]);
+            double l = 0.0;
+            for (int w = 0; w < 4; w++) l += wl[w][g];
+            uint64_t *w3 = c.T + ((size_t)(h0 + g) * c.nc + ch) * 3;
+            const uint64_t lb = (uint64_t)__double_as_longlong(l);
+            st_tag(w3, __float_as_uint(mc), tag);
+            st_tag(w3 + 1, (uint32_t)lb, tag);
+            st_tag(w3 + 2, (uint32_t)(lb >> 32), tag);
+        }
+        // the V rows stream in while the other chunks' statistics arrive
+        uint2 vv[32];
+        v_rows_load<HD>(vv, c, kvh, j0, npos);
+        if (pos_chunk && 4 * lane < hd) {                            // the new value row
+#pragma unroll
+            for (int k = 0; k < 32; k++)
+                if (j0 + k == p) vv[k] = ((const uint2 *)vpos)[lane];
+        }
+        // every chunk's statistics: global maximum and normaliser (as the V pass)
+        constexpr int HPW = (GRP + 3) / 4;
+#pragma unroll
+        for (int q = 0; q < HPW; q++) {
+            const int g = wave + 4 * q;
+            if (g < GRP) {                                           // uniform over the wave
+                const uint64_t *w3 = c.T + (size_t)(h0 + g) * c.nc * 3;
+                const uint64_t *src[6];
+                bool need[6];
+                uint32_t bits[6];
+#pragma unroll
+                for (int r = 0; r < 2; r++)
+#pragma unroll
+                    for (int k = 0; k < 3; k++) {
+                        const int ci = 64 * r + lane;
+                        src[3 * r + k] = w3 + (size_t)min(ci, nch - 1) * 3 + k;
+                        need[3 * r + k] = ci < nch;
+                    }
+                if (!poll_words<6>(src, need, tag, bits)) bad = 1;
+                float mc[2];
+                double lc[2];
+#pragma unroll
+                for (int r = 0; r < 2; r++) {
+                    const bool on = 64 * r + lane < nch;
+                    mc[r] = on ? __uint_as_float(bits[3 * r]) : -INFINITY;
+                    lc[r] = on ? __longlong_as_double((long long)(((uint64_t)bits[3 * r + 2] << 32) | bits[3 * r + 1])) : 0.0;
+                }
+                float m = wave_max(mc[0]);
+                if (nch > 64) m = fmaxf(m, wave_max(mc[1]));
+                double sum = wave_sum_d(lane < nch ? lc[0] * exp((double)mc[0] - (double)m) : 0.0);
+                if (nch > 64) sum += wave_sum_d(64 + lane < nch ? lc[1] * exp((double)mc[1] - (double)m) : 0.0);
+                if (lane == 0) {
+                    inv_s[g] = (float)(1.0 / sum);
+                    max_s[g] = m;
+                }
+            }
+        }
+        __syncthreads();
+        if (hf == 0) {
+#pragma unroll
+            for (int g = 0; g < GRP; g++) {
+                const float e = (float)exp((double)((j < npos ? s[g] : 0.0f) - max_s[g]));
+                wts[g][wave * 32 + (lane >> 1)] = j < npos ? h2f(f2h(e * inv_s[g])) : 0.0f;
+            }
+        }
+        __syncthreads();
+        // the chunk's value partial (as the V pass), published as tagged words
+        float o[GRP][4];
+        v_accum_f16<GRP>(vv, wts, o);
+        if (4 * lane < hd) {
+#pragma unroll
+            for (int g = 0; g < GRP; g++)
+                *(float4 *)&part[wave][g][4 * lane] = make_float4(o[g][0], o[g][1], o[g][2], o[g][3]);
+        }
+        __syncthreads();
+        for (int i = t; i < GRP * hd; i += 256) {
+            const int g = i / hd, e = i - g * hd;
+            const float r = ((part[0][g][e] + part[1][g][e]) + part[2][g][e]) + part[3][g][e];
+            st_tag(&c.PT[((size_t)(h0 + g) * c.nc + ch) * hd + e], __float_as_uint(r), tag);
+        }
+    }
+    // combine, shared by every workgroup of the KV head: blocks ch, ch + nwg, ...
+    // of its GRP*hd outputs; thread (slot r = t / 32, element i = t % 32)
+    // gathers chunks r, r + 8, ... into LDS, then 32 threads add them in chunk
+    // order (as the combine pass)
+    const int nblk = GRP * hd / 32, nwg = gridDim.y;
+    for (int b = ch; b < nblk; b += nwg) {                           // uniform over the workgroup
+        __syncthreads();
+        const int g = (b * 32) / hd, e0 = b * 32 - g * hd, i = t & 31, r0 = t >> 5;
+        const uint64_t *base = c.PT + (size_t)(h0 + g) * c.nc * hd + e0 + i;
+        constexpr int PER = ATT_FUSED_MAXC / 8;                      // chunks per thread
+        const uint64_t *src[PER];
+        bool need[PER];
+        uint32_t bits[PER];
+#pragma unroll
+        for (int q = 0; q < PER; q++) {
+            const int k = r0 + 8 * q;
+            src[q] = base + (size_t)min(k, nch - 1) * hd;
+            need[q] = k < nch;
+        }
+        if (!poll_words<PER>(src, need, tag, bits)) bad = 1;
+#pragma unroll
+        for (int q = 0; q < PER; q++)
+            if (need[q]) vals[(r0 + 8 * q) * 32 + i] = __uint_as_float(bits[q]);
+        __syncthreads();
+        float r = 0.0f;
+        if (t < 32) {
+            for (int k0 = 0; k0 < nch; k0 += 16) {                      // 16 reads in flight, adds in order
+                float v[16];
+#pragma unroll
+                for (int q = 0; q < 16; q++) v[q] = k0 + q < nch ? vals[(k0 + q) * 32 + t] : 0.0f;
+#pragma unroll
+                for (int q = 0; q < 16; q++)
+                    if (k0 + q < nch) r += v[q];
+            }
+            if (bad) {
+                r = __builtin_nanf("");
+                st_ag(c.err, 1u);
+            }
+            c.out[(size_t)(h0 + g) * hd + e0 + t] = r;
+        }
+        if (c.q8out) {                                               // uniform
+            __syncthreads();
+            if (t < 32) vals[t] = r;
+            __syncthreads();
+            if (t < 8) {
+                float v4[4];
+#pragma unroll
+                for (int k = 0; k < 4; k++) v4[k] = vals[4 * t + k];
+                q8_store4(v4, t, true, c.q8out + (size_t)(h0 + g) * (hd / 32) * 34 + (size_t)(e0 / 32) * 34);
+            }
+        }
+    }
 }
 
 // ------------------------------------------------------------- KV store --
@@ -551,26 +899,100 @@ __global__ __launch_bounds__(256) void k_kv_store_f16(const float *__restrict__ 
 }
 
 // ------------------------------------------------------------ launchers --
-// Workspace: S [n_head][npos] f32 scores, Mc [n_head][nc] f32 chunk maxima,
-// Lc [n_head][nc] f64 chunk sums, P [n_head][nc][hd] f32 partials.
-static size_t al256(size_t v) { return (v + 255) & ~(size_t)255; }
-size_t attn_workspace_bytes(int n_head, int hd, int npos_max) {
-    const size_t nc = (npos_max + ATT_CHUNK - 1) / ATT_CHUNK;
-    return al256((size_t)n_head * npos_max * 4) + al256((size_t)n_head * nc * 4) + al256((size_t)n_head * nc * 8) +
-           al256((size_t)n_head * nc * hd * 4);
+// zero the tagged words and the epoch / error words (their first use)
+__global__ void k_attn_clear(uint64_t *w, size_t n) {
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) w[i] = 0;
 }
 
-template <int KV, int GRP>
-static hipError_t attn_go(AttnCtx c, int n_head, int n_kv, int npos_max, uint8_t *ws, hipStream_t s) {
+// Workspace: S [n_head][npos] f32 scores, Mc [n_head][nc] f32 chunk maxima,
+// Lc [n_head][nc] f64 chunk sums, P [n_head][nc][hd] f32 partials (three
+// passes); then the fused launch's words: T [n_head][nc][3], PT
+// [n_head][nc][hd], and epoch, error (one 64-bit word each).
+static size_t al256(size_t v) { return (v + 255) & ~(size_t)255; }
+struct AttnWs {
+    size_t S, Mc, Lc, P, T, PT, misc, total;
+};
+static AttnWs attn_ws(int n_head, int hd, int npos_max) {
+    const size_t nc = (npos_max + ATT_CHUNK - 1) / ATT_CHUNK;
+    AttnWs w;
+    w.S = 0;
+    w.Mc = w.S + al256((size_t)n_head * npos_max * 4);
+    w.Lc = w.Mc + al256((size_t)n_head * nc * 4);
+    w.P = w.Lc + al256((size_t)n_head * nc * 8);
+    w.T = w.P + al256((size_t)n_head * nc * hd * 4);
+    w.PT = w.T + al256((size_t)n_head * nc * 3 * 8);
+    w.misc = w.PT + al256((size_t)n_head * nc * hd * 8);
+    w.total = w.misc + 256;
+    return w;
+}
+size_t attn_workspace_bytes(int n_head, int hd, int npos_max) { return attn_ws(n_head, hd, npos_max).total; }
+uint64_t *attn_ws_epoch(uint8_t *ws, int n_head, int hd, int npos_max) {
+    return (uint64_t *)(ws + attn_ws(n_head, hd, npos_max).misc);
+}
+
+// workgroups of the fused kernel the device holds resident at once
+template <int GRP, int HD>
+static int fused_capacity() {
+    static const int cap = [] {
+        int dev = 0, cus = 0, occ = 0;
+        if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+            hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, k_attn_fused_f16<GRP, HD>, 256, 0) != hipSuccess)
+            return 0;
+        return cus * occ;
+    }();
+    return cap;
+}
+
+template <int HD>
+static int fused_capacity(int grp) {
+    return grp == 1 ? fused_capacity<1, HD>() : grp == 2 ? fused_capacity<2, HD>() : grp == 4 ? fused_capacity<4, HD>()
+         : grp == 8 ? fused_capacity<8, HD>() : 0;
+}
+
+bool attn_fused_fits(int kv_type, int n_head, int n_kv, int hd, int npos_max) {
+    if (kv_type != F16) return false;
+    if (const char *e = getenv("G4H_ATTN_PASSES"))
+        if (atoi(e) == 3) return false;
+    const int nc = (npos_max + ATT_CHUNK - 1) / ATT_CHUNK, grp = n_head / n_kv;
+    if (nc > ATT_FUSED_MAXC) return false;
+    const int cap = hd == 64 ? fused_capacity<64>(grp) : hd == 128 ? fused_capacity<128>(grp) : hd == 192 ? fused_capacity<192>(grp)
+                  : hd == 256 ? fused_capacity<256>(grp) : 0;
+    return (int64_t)n_kv * nc <= cap;
+}
+
+template <int KV, int GRP, int HD>
+static hipError_t attn_go(AttnCtx c, int n_head, int n_kv, int npos_max, uint8_t *ws, const AttnTag *tg, hipStream_t s) {
+    const AttnWs w = attn_ws(n_head, c.a.hd, npos_max);
     const int nc = (npos_max + ATT_CHUNK - 1) / ATT_CHUNK;
     c.nc = nc;
-    c.S = (float *)ws;
-    c.Mc = (float *)(ws + al256((size_t)n_head * npos_max * 4));
-    c.Lc = (double *)((uint8_t *)c.Mc + al256((size_t)n_head * nc * 4));
-    c.P = (float *)((uint8_t *)c.Lc + al256((size_t)n_head * nc * 8));
-    if constexpr (KV == F16) hipLaunchKernelGGL((k_attn_scores_f16<GRP>), dim3(n_kv, nc), dim3(256), 0, s, c);
-    else hipLaunchKernelGGL((k_attn_scores_q8<GRP>), dim3(n_kv, nc), dim3(128), 0, s, c);
-    hipLaunchKernelGGL((k_attn_v<KV, GRP>), dim3(n_kv, nc), dim3(256), 0, s, c);
+    c.S = (float *)(ws + w.S);
+    c.Mc = (float *)(ws + w.Mc);
+    c.Lc = (double *)(ws + w.Lc);
+    c.P = (float *)(ws + w.P);
+    if constexpr (KV == F16) {
+        if (attn_fused_fits(KV, n_head, n_kv, HD, npos_max)) {
+            c.T = (uint64_t *)(ws + w.T);
+            c.PT = (uint64_t *)(ws + w.PT);
+            c.err = (unsigned *)(ws + w.misc + 8);
+            if (tg) {
+                c.epoch = tg->epoch;
+                c.tag_mul = tg->mul;
+                c.tag_add = tg->add;
+            } else {                                                 // tags start over on a cleared workspace
+                const size_t nw = (w.total - w.T) / 8;
+                hipLaunchKernelGGL(k_attn_clear, dim3((unsigned)std::min<size_t>((nw + 255) / 256, 1024)), dim3(256), 0, s,
+                                   (uint64_t *)(ws + w.T), nw);
+                c.epoch = (const unsigned *)(ws + w.misc);
+                c.tag_mul = 1;
+                c.tag_add = 0;
+            }
+            hipLaunchKernelGGL((k_attn_fused_f16<GRP, HD>), dim3(n_kv, nc), dim3(256), 0, s, c);
+            return hipGetLastError();
+        }
+    }
+    if constexpr (KV == F16) hipLaunchKernelGGL((k_attn_scores_f16<GRP, HD>), dim3(n_kv, nc), dim3(256), 0, s, c);
+    else hipLaunchKernelGGL((k_attn_scores_q8<GRP, HD>), dim3(n_kv, nc), dim3(128), 0, s, c);
+    hipLaunchKernelGGL((k_attn_v<KV, GRP, HD>), dim3(n_kv, nc), dim3(256), 0, s, c);
     hipLaunchKernelGGL(k_attn_combine, dim3(n_head), dim3(256), 0, s, c);
     return hipGetLastError();
 }
@@ -578,7 +1000,7 @@ static hipError_t attn_go(AttnCtx c, int n_head, int n_kv, int npos_max, uint8_t
 // q: prepared queries, or nullptr with `qkv` the raw q|k|v projection output
 // to prepare (its k/v rows go into the caches at position npos - 1).
 hipError_t launch_attn_decode(const float *q, const float *qkv, const QkvArgs &a, int npos, const int *npos_dev, int npos_max,
-                              float *out, uint8_t *q8out, uint8_t *ws, hipStream_t s) {
+                              float *out, uint8_t *q8out, uint8_t *ws, hipStream_t s, const AttnTag *tag) {
     if (a.hd % 64 || a.hd > 256 || a.n_kv <= 0 || a.n_head % a.n_kv) return hipErrorInvalidValue;
     if (qkv && (!a.rope || !a.q_norm || !a.k_norm)) return hipErrorInvalidValue;
     AttnCtx c{};
@@ -590,8 +1012,13 @@ hipError_t launch_attn_decode(const float *q, const float *qkv, const QkvArgs &a
     c.out = out;
     c.q8out = q8out;
     const int grp = a.n_head / a.n_kv;
-#define G4_ATT(KV, G) \
-    if (a.kv_type == KV && grp == G) return attn_go<KV, G>(c, a.n_head, a.n_kv, npos_max, ws, s)
+#define G4_ATT(KV, G)                                                                                 \
+    if (a.kv_type == KV && grp == G) {                                                                \
+        if (a.hd == 64) return attn_go<KV, G, 64>(c, a.n_head, a.n_kv, npos_max, ws, tag, s);       \
+        if (a.hd == 128) return attn_go<KV, G, 128>(c, a.n_head, a.n_kv, npos_max, ws, tag, s);     \
+        if (a.hd == 192) return attn_go<KV, G, 192>(c, a.n_head, a.n_kv, npos_max, ws, tag, s);     \
+        if (a.hd == 256) return attn_go<KV, G, 256>(c, a.n_head, a.n_kv, npos_max, ws, tag, s);     \
+    }
     G4_ATT(F16, 1); G4_ATT(F16, 2); G4_ATT(F16, 4); G4_ATT(F16, 8);
     G4_ATT(Q8_0, 1); G4_ATT(Q8_0, 2); G4_ATT(Q8_0, 4); G4_ATT(Q8_0, 8);
 #undef G4_ATT

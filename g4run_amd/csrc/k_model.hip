@@ -83,7 +83,8 @@ __global__ __launch_bounds__(256) void k_gelu_quant(const float *gu, int n_ff, c
 // ---------------------------------------------------- argmax + advance --
 // First index of the maximum (sampler.c:139-144: best starts at index 0 and
 // later values must be strictly larger, so NaNs never win and a NaN at index 0
-// keeps index 0); then token <- argmax, pos <- pos + 1, npos <- pos + 1.
+// keeps index 0); then token <- argmax, pos <- pos + 1, npos <- pos + 1 and
+// the step count (the attention hand-off tags) + 1.
 __device__ __forceinline__ void argmax_merge(float &v, int &i, float v2, int i2) {
     if (v2 > v || (v2 == v && i2 < i)) { v = v2; i = i2; }
 }
@@ -120,6 +121,7 @@ __global__ __launch_bounds__(1024) void k_argmax_advance(const float *logits, in
         state[0] = (idx == 0x7fffffff || __builtin_isnan(logits[0])) ? 0 : idx;
         state[1] += 1;
         state[2] = state[1] + 1;
+        state[3] += 1;                                   // steps taken (never reset)
     }
 }
 

@@ -73,8 +73,18 @@ hipError_t launch_matmul_mfma(const g4h_tensor &W, const float *x, size_t x_stri
 
 // k_attn.hip
 size_t attn_workspace_bytes(int n_head, int hd, int npos_max);
+// f16 caches run as one fused launch when its grid fits on the device at once
+// (attn_fused_fits).  Its hand-off words in ws carry a tag that must differ
+// from every earlier launch on that ws: *epoch * mul + add + 1 when `tag` is
+// given (a caller-kept counter, with ws zeroed before first use), else the
+// launch clears its words first and starts the tags over.
+struct AttnTag {
+    const unsigned *epoch;
+    unsigned mul, add;
+};
+bool attn_fused_fits(int kv_type, int n_head, int n_kv, int hd, int npos_max);
 hipError_t launch_attn_decode(const float *q, const float *qkv, const QkvArgs &a, int npos, const int *npos_dev, int npos_max,
-                              float *out, uint8_t *q8out, uint8_t *ws, hipStream_t s);
+                              float *out, uint8_t *q8out, uint8_t *ws, hipStream_t s, const AttnTag *tag = nullptr);
 hipError_t launch_kv_store(int kv_type, const float *src, uint8_t *dst, int hd, int rows, size_t dst_stride, hipStream_t s);
 
 }  // namespace g4

@@ -76,7 +76,7 @@ struct g4h_model {
     size_t kv_layer_bytes = 0;       // one of K or V for one layer
     float *rope = nullptr;           // [n_ctx][hd] cos/sin pairs
     uint16_t *gelu = nullptr;        // 65536 fp16 codes
-    int *state = nullptr;            // token, pos, npos
+    int *state = nullptr;            // token, pos, npos, steps taken
     float *x = nullptr, *x2 = nullptr, *xb = nullptr, *qkv = nullptr, *q = nullptr, *att = nullptr, *ff = nullptr, *logits = nullptr;
     uint8_t *act = nullptr, *ws = nullptr;
     size_t act_bytes = 0, ws_bytes = 0;
@@ -239,6 +239,7 @@ extern "C" int g4h_model_create(const g4h_model_config *cfg, uint64_t seed, g4h_
     if ((rc = model_alloc(m, (void **)&m->ws, m->ws_bytes))) return bail(rc);
     (void)wide;
     if (hipMemset(m->state, 0, 64) != hipSuccess) return bail(G4H_ERR_HIP);
+    if (hipMemset(m->ws, 0, m->ws_bytes) != hipSuccess) return bail(G4H_ERR_HIP);   // no attention tag seen yet
     if (hipDeviceSynchronize() != hipSuccess) return bail(g4h_internal_fail(G4H_ERR_HIP, "g4h_model_create: init kernels failed"));
     *out = m;
     return G4H_OK;
@@ -333,7 +334,8 @@ extern "C" int g4h_forward_state(g4h_model *m, void *stream) {
         qa.kc = kc;
         qa.vc = vc;
         qa.eps = c.rms_eps;
-        M_HIP(launch_attn_decode(nullptr, m->qkv, qa, 0, npos, c.n_ctx, m->att, m->act, m->ws, s));
+        const AttnTag tag{(const unsigned *)(m->state + 3), (unsigned)c.n_layer, (unsigned)l};
+        M_HIP(launch_attn_decode(nullptr, m->qkv, qa, 0, npos, c.n_ctx, m->att, m->act, m->ws, s, &tag));
         M_HIP(launch_gemv(*m->wo[l], m->act, ast, m->xb, 1, s));
         if (fz & FUSE_GU) {
             M_HIP(norm_gemv(*m->wgu[l], m->xb, norm_of(m, l, G4H_N_POST_ATTN), norm_of(m, l, G4H_N_FFN), nullptr, true));

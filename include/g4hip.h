@@ -158,6 +158,12 @@ int g4h_block_sums(const g4h_tensor *W, const void *pre_dev, size_t pre_stride, 
  * ws_dev: g4h_attn_workspace_bytes() bytes of caller-owned scratch (the
  * reference's attbuf, model.c:465).  out_dev: n_head x hd fp32. */
 size_t g4h_attn_workspace_bytes(int n_head, int hd, int n_pos);
+/* Diagnostic (no reference counterpart): *passes = the launches
+ * g4h_attn_decode makes for this shape, 1 when the f16 cache runs as one fused
+ * launch (its grid of n_kv x ceil(n_pos/128) workgroups fits on the device at
+ * once), else 3 (score, value and combine passes).  Both give the same bits;
+ * G4H_ATTN_PASSES=3 in the environment forces the three passes. */
+int g4h_attn_passes(int kv_type, int n_head, int n_kv, int hd, int n_pos, int *passes);
 int g4h_attn_decode(const float *q_dev, const void *kc_dev, const void *vc_dev, int kv_type,
                     int n_head, int n_kv, int hd, int n_pos, float *out_dev,
                     void *ws_dev, size_t ws_bytes, void *stream);

@@ -75,3 +75,49 @@ def test_attention_bad_shapes(gpu):
     assert L.g4h_attn_decode(b.ptr, b.ptr, b.ptr, G.F16, 8, 3, 256, 10, b.ptr, b.ptr, b.nbytes, None) == G.ERR_SHAPE
     assert L.g4h_attn_decode(b.ptr, b.ptr, b.ptr, G.F16, 8, 4, 96, 10, b.ptr, b.ptr, b.nbytes, None) == G.ERR_SHAPE
     assert L.g4h_attn_decode(b.ptr, b.ptr, b.ptr, G.F16, 8, 4, 256, 10, b.ptr, b.ptr, 16, None) == G.ERR_ARG
+
+
+def _attn(G, q, kb, vb, kv_type, n_head, n_kv, hd, n_pos, ws):
+    out = G.Buffer(n_head * hd * 4)
+    G.attn_decode(G.Buffer.from_array(q), kb, vb, kv_type, n_head, n_kv, hd, n_pos, out, ws=ws)
+    G.synchronize()
+    return out.download(np.float32, (n_head, hd))
+
+
+@pytest.mark.parametrize("n_head,n_kv,hd,n_pos", [
+    (8, 4, 256, 1), (8, 4, 256, 127), (8, 4, 256, 128), (8, 4, 256, 129), (8, 4, 256, 8192),
+    (4, 4, 64, 700), (8, 1, 128, 5000), (16, 2, 192, 333), (32, 4, 256, 2049), (8, 4, 256, 12000),
+    (4, 4, 64, 16384),
+])
+def test_attention_fused_equals_three_passes(gpu, oracle, monkeypatch, n_head, n_kv, hd, n_pos):
+    """The one-launch form (tagged hand-off words between workgroups) gives the
+    bits of the three-pass form; run twice on one workspace, then on a shorter
+    context, so stale words of an earlier launch are seen to be ignored."""
+    G = gpu
+    assert G.attn_passes(G.F16, n_head, n_kv, hd, n_pos) == 1
+    kb, vb, kh, vh = make_cache(G, oracle, G.F16, n_pos, n_kv, hd, seed=3 * n_pos + hd)
+    q = (np.random.default_rng(n_pos).standard_normal((n_head, hd)) * 0.5).astype(np.float32)
+    ws = G.Buffer(G.attn_workspace_bytes(n_head, hd, n_pos))
+    fused = [_attn(G, q, kb, vb, G.F16, n_head, n_kv, hd, n, ws) for n in (n_pos, n_pos, max(1, n_pos // 3))]
+    monkeypatch.setenv("G4H_ATTN_PASSES", "3")
+    assert G.attn_passes(G.F16, n_head, n_kv, hd, n_pos) == 3
+    three = [_attn(G, q, kb, vb, G.F16, n_head, n_kv, hd, n, ws) for n in (n_pos, max(1, n_pos // 3))]
+    assert np.isfinite(fused[0]).all()
+    assert np.array_equal(fused[0].view(np.uint32), three[0].view(np.uint32))
+    assert np.array_equal(fused[1].view(np.uint32), three[0].view(np.uint32))
+    assert np.array_equal(fused[2].view(np.uint32), three[1].view(np.uint32))
+    ref = oracle.attn_decode(q, kh, vh, G.F16, n_head, n_kv, hd, n_pos - 1)
+    assert (np.abs(fused[0] - ref) <= ATOL + RTOL * np.abs(ref)).all()
+
+
+def test_attention_long_context_falls_back_to_three_passes(gpu, oracle):
+    """A grid larger than the device holds at once runs the three passes."""
+    G = gpu
+    n_head, n_kv, hd, n_pos = 8, 8, 64, 40000                       # 8 x 313 workgroups
+    assert G.attn_passes(G.F16, n_head, n_kv, hd, n_pos) == 3
+    assert G.attn_passes(G.Q8_0, 8, 4, 256, 256) == 3                    # q8_0 caches always do
+    kb, vb, kh, vh = make_cache(G, oracle, G.F16, n_pos, n_kv, hd, seed=11)
+    q = np.random.default_rng(12).standard_normal((n_head, hd)).astype(np.float32)
+    got = _attn(G, q, kb, vb, G.F16, n_head, n_kv, hd, n_pos, None)
+    ref = oracle.attn_decode(q, kh, vh, G.F16, n_head, n_kv, hd, n_pos - 1)
+    assert (np.abs(got - ref) <= ATOL + RTOL * np.abs(ref)).all()
