@@ -13,7 +13,9 @@ import os
 import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "libg4hip.so")
+# G4H_LIB names another build of the same library (e.g. one compiled with
+# different flags for a side-by-side measurement)
+LIB_PATH = os.environ.get("G4H_LIB") or os.path.join(HERE, "libg4hip.so")
 INCLUDE = os.path.join(os.path.dirname(HERE), "include", "g4hip.h")
 
 # type ids (g4run.h:80-94)

@@ -327,6 +327,17 @@ extern "C" int g4h_tensor_info(const g4h_tensor *t, int *type, int64_t *ncols, i
 // ------------------------------------------------------------- matmul ----
 static constexpr size_t kMaxLds = 65536;
 
+// fp32 inputs of the GEMV family are quantized inside the GEMV (one launch)
+// unless G4H_GEMV_FUSED_QUANT=0 asks for the separate quantizer launch; the
+// results are the same bit for bit either way.
+static bool fused_quant_enabled() {
+    static const bool on = [] {
+        const char *e = getenv("G4H_GEMV_FUSED_QUANT");
+        return !(e && atoi(e) == 0);
+    }();
+    return on;
+}
+
 // Token count from which the matrix-core family replaces the GEMV family for
 // q8_0 / q4_0 weights: the measured crossover on q8_0 4096x4096 lies between 16
 // tokens (GEMV 18.5 us, matrix cores 20.3 us) and 32 (33.6 us vs 24.2 us).
@@ -396,6 +407,25 @@ extern "C" int g4h_matmul_ex(const g4h_tensor *W, const float *x, const void *pr
     }
     const uint8_t *act = (const uint8_t *)pre;
     size_t stride = pre_stride;
+    auto chunk_at = [&](int done) {                                  // GEMV token chunks of 8/4/2/1 within the LDS budget
+        int chunk = 8;
+        while (chunk > nb - done || (chunk > 1 && gemv_lds_bytes(W->type, chunk, W->nb) > kMaxLds)) chunk >>= 1;
+        return chunk;
+    };
+    if (x && (uintptr_t)x % 16 == 0 && fused_quant_enabled()) {
+        // q8_0 / q4_0 weights: every chunk quantizes its fp32 tokens in the GEMV prologue
+        bool fits = true;
+        for (int done = 0; done < nb && fits; done += chunk_at(done)) fits = gemv_fused_fits(*W, chunk_at(done));
+        if (fits) {
+            for (int done = 0; done < nb;) {
+                const int chunk = chunk_at(done);
+                const hipError_t e = launch_gemv_x(*W, x + (size_t)done * W->ncols, Y + (size_t)done * W->nrows, chunk, s);
+                if (e != hipSuccess) return hip_fail(e, "g4h_matmul: gemv launch");
+                done += chunk;
+            }
+            return G4H_OK;
+        }
+    }
     if (x) {
         if ((uintptr_t)x % 4) return fail(G4H_ERR_ARG, "g4h_matmul: x must be 4-byte aligned");
         stride = g4h_act_stride(W->type, W->ncols);
@@ -412,8 +442,7 @@ extern "C" int g4h_matmul_ex(const g4h_tensor *W, const float *x, const void *pr
     // GEMV family in token chunks of 8/4/2/1 that fit the LDS budget
     int done = 0;
     while (done < nb) {
-        int chunk = 8;
-        while (chunk > nb - done || (chunk > 1 && gemv_lds_bytes(W->type, chunk, W->nb) > kMaxLds)) chunk >>= 1;
+        const int chunk = chunk_at(done);
         const hipError_t e = launch_gemv(*W, act + (size_t)done * stride, stride, Y + (size_t)done * W->nrows, chunk, s);
         if (e != hipSuccess) return hip_fail(e, "g4h_matmul: gemv launch");
         done += chunk;

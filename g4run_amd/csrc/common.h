@@ -63,6 +63,35 @@ __device__ __forceinline__ int group_isum(int v) {
 
 __device__ __forceinline__ int4 ld4(const void *p) { return *reinterpret_cast<const int4 *>(p); }
 
+// 128-bit load of a stream that is read once per call (weight quants): the
+// non-temporal hint keeps those lines from displacing reused data (activations,
+// scales) in the caches.  -DG4_LD_PLAIN builds the plain form for comparison.
+typedef int g4_v4i __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ int4 ld4s(const void *p) {
+#ifdef G4_LD_PLAIN
+    return ld4(p);
+#else
+    const g4_v4i v = __builtin_nontemporal_load(reinterpret_cast<const g4_v4i *>(p));
+    return make_int4(v.x, v.y, v.z, v.w);
+#endif
+}
+
+// Workgroup barrier for LDS hand-offs only.  __syncthreads() also waits for
+// every outstanding global load of the calling wave (vmcnt(0)); a wave whose
+// weight stream is in flight would stall there until the whole stream has
+// landed.  This one waits for the wave's LDS and scalar traffic (lgkmcnt) and
+// meets the other waves, so global loads stay in flight across it.  Only LDS
+// data may be handed between waves through it.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+// Keeps the loads issued before it ahead of those after it: global loads
+// complete in issue order, so a small load that must be waited for early
+// (activations) has to be issued before the weight stream.
+__device__ __forceinline__ void issue_order() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+}
+
 }  // namespace g4
 
 // Resident weight matrix (the object behind the C ABI's g4h_tensor).

@@ -23,8 +23,10 @@ namespace g4 {
 // Activation of NB tokens staged in LDS.
 // q8_0 act (blocks of 32): per token t: Q0[nb] int4 (qs 0..15), Q1[nb] int4
 // (qs 16..31), D[nb] float (fp16 d widened), S[nb] int (sum of qs).
-// q8_K act (superblocks of 256): per token t: QK[nb][256] int8, DK[nb] float,
-// BS[nb][16] int16.
+// q8_K act (superblocks of 256): per token t and superblock, 304 bytes: the
+// GGUF block (d, 256 quants, 16 bsums: 292 bytes) shifted 12 bytes up, so d
+// sits at byte 12, the quants at 16..271 (16-byte aligned) and the bsums at
+// 272..303; the staging then moves whole 16-byte slots.
 struct ActQ8_0 {
     static __host__ __device__ size_t bytes_per_token(int nb) { return ((size_t)nb * 40 + 15) & ~(size_t)15; }
     int4 *q0, *q1; float *d; int *s;
@@ -34,19 +36,30 @@ struct ActQ8_0 {
     }
 };
 struct ActQ8_K {
-    static __host__ __device__ size_t bytes_per_token(int nb) { return ((size_t)nb * (256 + 4 + 32) + 15) & ~(size_t)15; }
-    int8_t *q; float *d; int16_t *bs;
-    __device__ ActQ8_K(uint8_t *base, int nb, int t) {
-        uint8_t *p = base + (size_t)t * bytes_per_token(nb);
-        q = (int8_t *)p; d = (float *)(q + (size_t)nb * 256); bs = (int16_t *)(d + nb);
-    }
+    static constexpr int SB = 304;
+    static __host__ __device__ size_t bytes_per_token(int nb) { return (size_t)nb * SB; }
+    uint8_t *p;
+    __device__ ActQ8_K(uint8_t *base, int nb, int t) : p(base + (size_t)t * bytes_per_token(nb)) {}
+    __device__ const int8_t *q(int sb) const { return (const int8_t *)(p + (size_t)sb * SB + 16); }
+    __device__ float d(int sb) const { return *(const float *)(p + (size_t)sb * SB + 12); }
+    __device__ const int16_t *bs(int sb) const { return (const int16_t *)(p + (size_t)sb * SB + 272); }
 };
 
-// Activation staging is split in two so a kernel can issue the (small, mostly
-// L2-resident) activation loads before its weight stream, then finish the LDS
-// writes while the weights are in flight: global loads complete in issue order,
-// so waiting for activations issued first never waits for the weights.
-//
+// Staging.  A kernel issues the (small, mostly L2-resident) activation loads
+// before its weight stream and writes LDS while the weights are in flight:
+// global loads complete in issue order, so waiting for activations issued
+// first never waits for the weights.  Loads and stores are branch-free: a load
+// whose only use sits under a per-thread branch is sunk by the compiler below
+// later loads (and its wait then covers them), and a branch join makes it wait
+// early.  So a thread without an item reads a pad in device memory (one
+// address for the whole wave: one request) and writes its own slot of a dump
+// area placed after the staged tokens (kStageDump bytes, included in the LDS
+// sizes; one slot per lane, so these writes do not collide in one bank).
+constexpr size_t kStageDump = 64 * 80;
+template <class Act>
+__device__ __forceinline__ uint8_t *stage_dump(uint8_t *lds, int ntok, int nb) { return lds + (size_t)ntok * Act::bytes_per_token(nb); }
+static __device__ uint32_t g_stage_pad[17];
+
 // q8_0: one item = a pair of 34-B blocks = 17 aligned dwords.
 struct StageQ8_0 {
     uint32_t v[17];
@@ -59,22 +72,17 @@ __device__ __forceinline__ void stage_q8_0_load(StageQ8_0 &S, int item, const ui
     S.ok = item < NB * npair;
     S.t = S.ok ? item / npair : 0;
     S.pr = S.ok ? item - S.t * npair : 0;
-    // every register is defined on both paths, so the item stays in registers
+    const uint32_t *src = S.ok ? (const uint32_t *)(act + (size_t)S.t * stride + (size_t)S.pr * 68) : g_stage_pad;
 #pragma unroll
-    for (int k = 0; k < 17; k++) S.v[k] = 0;
-    if (S.ok) {
-        const uint32_t *src = (const uint32_t *)(act + (size_t)S.t * stride + (size_t)S.pr * 68);
-#pragma unroll
-        for (int k = 0; k < 17; k++) S.v[k] = src[k];
-    }
+    for (int k = 0; k < 17; k++) S.v[k] = src[k];
 }
 __device__ __forceinline__ int sum_i8x16(int4 a) {
     int s = dot4(a.x, 0x01010101, 0);
     s = dot4(a.y, 0x01010101, s); s = dot4(a.z, 0x01010101, s); return dot4(a.w, 0x01010101, s);
 }
-__device__ __forceinline__ void stage_q8_0_store(const StageQ8_0 &S, uint8_t *lds, int nb) {
-    if (!S.ok) return;
-    ActQ8_0 A(lds, nb, S.t);
+__device__ __forceinline__ void stage_q8_0_store(const StageQ8_0 &S, uint8_t *lds, int nb, uint8_t *dump) {
+    // the dump slot: a two-block layout (80 B) per lane
+    ActQ8_0 A(S.ok ? lds : dump + 80 * (threadIdx.x & 63), S.ok ? nb : 2, S.t);
     const uint32_t *v = S.v;
     const int b = 2 * S.pr;
     int4 a0, a1;
@@ -94,7 +102,7 @@ __device__ void stage_q8_0_rest(uint8_t *lds, const uint8_t *act, size_t stride,
     for (int i = threadIdx.x + blockDim.x; i < NB * (nb >> 1); i += blockDim.x) {
         StageQ8_0 S;
         stage_q8_0_load<NB>(S, i, act, stride, nb);
-        stage_q8_0_store(S, lds, nb);
+        stage_q8_0_store(S, lds, nb, stage_dump<ActQ8_0>(lds, NB, nb));
     }
     if (nb & 1) {   // last block with 16-bit loads
         for (int t = threadIdx.x; t < NB; t += blockDim.x) {
@@ -109,69 +117,85 @@ __device__ void stage_q8_0_rest(uint8_t *lds, const uint8_t *act, size_t stride,
         }
     }
 }
+// q8_0 quantization of fp32 activations straight into the LDS layout: the
+// arithmetic of the standalone quantizer (k_quant.hip, quants.c:74-109), so
+// the staged token is bit-identical to quantizing first.  Four consecutive
+// values v of token t, group j (elements 4j..4j+3); the 8 consecutive lanes of
+// a 32-element block call it together (all lanes of the wave call it: the
+// block maximum is a lane shuffle), and only lanes with `own` write.
+__device__ __forceinline__ void q8_lds4(const float v[4], int j, bool own, uint8_t *lds, int nb, int t) {
+    float am = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+    am = fmaxf(am, shfl_xor(am, 1));
+    am = fmaxf(am, shfl_xor(am, 2));
+    am = fmaxf(am, shfl_xor(am, 4));
+    const float id = am != 0.0f ? 127.0f / am : 0.0f;
+    uint32_t pk = 0;
+#pragma unroll
+    for (int i = 0; i < 4; i++) pk |= ((uint32_t)(int)__builtin_rintf(v[i] * id) & 0xffu) << (8 * i);
+    int sum = dot4((int)pk, 0x01010101, 0);
+    sum += shfl_xor(sum, 1);
+    sum += shfl_xor(sum, 2);
+    sum += shfl_xor(sum, 4);
+    if (!own) return;
+    ActQ8_0 A(lds, nb, t);
+    const int b = j >> 3, k = j & 7;
+    ((uint32_t *)(k < 4 ? &A.q0[b] : &A.q1[b]))[k & 3] = pk;
+    if (k == 0) {
+        A.d[b] = h2f(f2h(am * (1.0f / 127.0f)));
+        A.s[b] = sum;
+    }
+}
+
 template <int NB>
 __device__ void stage_q8_0(uint8_t *lds, const uint8_t *act, size_t stride, int nb) {
     StageQ8_0 S;
     stage_q8_0_load<NB>(S, threadIdx.x, act, stride, nb);
-    stage_q8_0_store(S, lds, nb);
+    stage_q8_0_store(S, lds, nb, stage_dump<ActQ8_0>(lds, NB, nb));
     stage_q8_0_rest<NB>(lds, act, stride, nb);
 }
 
-// q8_K: one item = 16 bytes of quants (4 dwords) or, for chunk 16, the
-// superblock's d and 16 bsums (9 dwords): 17 items per 292-B superblock.
+// q8_K: one item = one 16-byte slot s (0..18) of a staged superblock, i.e.
+// dwords 4s-3 .. 4s of the GGUF block (slot 0 carries d in its last dword;
+// its first three are padding).
 struct StageQ8_K {
-    uint32_t v[9];
-    int t, sb, c;
+    uint32_t v[4];
+    int t, sb, s;
     bool ok;
 };
 template <int NB>
 __device__ __forceinline__ void stage_q8_K_load(StageQ8_K &S, int item, const uint8_t *act, size_t stride, int nb) {
-    const int per = nb * 17;
+    const int per = nb * 19;
     S.ok = item < NB * per;
     const int it = S.ok ? item : 0;
     S.t = it / per;
     const int r = it - S.t * per;
-    S.sb = r / 17;
-    S.c = r - S.sb * 17;
+    S.sb = r / 19;
+    S.s = r - S.sb * 19;
+    const uint32_t *src = S.ok ? (const uint32_t *)(act + (size_t)S.t * stride) + (size_t)S.sb * 73 + max(4 * S.s - 3, 0)
+                               : g_stage_pad;
 #pragma unroll
-    for (int k = 0; k < 9; k++) S.v[k] = 0;
-    if (S.ok) {
-        const uint32_t *src = (const uint32_t *)(act + (size_t)S.t * stride) + (size_t)S.sb * 73;
-        if (S.c < 16) {
-#pragma unroll
-            for (int k = 0; k < 4; k++) S.v[k] = src[1 + 4 * S.c + k];
-        } else {
-            S.v[0] = src[0];
-#pragma unroll
-            for (int k = 0; k < 8; k++) S.v[1 + k] = src[65 + k];
-        }
-    }
+    for (int k = 0; k < 4; k++) S.v[k] = src[k];
 }
-__device__ __forceinline__ void stage_q8_K_store(const StageQ8_K &S, uint8_t *lds, int nb) {
-    if (!S.ok) return;
-    ActQ8_K A(lds, nb, S.t);
-    if (S.c < 16) {
-        *(int4 *)(A.q + (size_t)S.sb * 256 + 16 * S.c) = make_int4(S.v[0], S.v[1], S.v[2], S.v[3]);
-    } else {
-        A.d[S.sb] = __builtin_bit_cast(float, S.v[0]);
-        uint32_t *bs = (uint32_t *)(A.bs + (size_t)S.sb * 16);
-#pragma unroll
-        for (int k = 0; k < 8; k++) bs[k] = S.v[1 + k];
-    }
+__device__ __forceinline__ void stage_q8_K_store(const StageQ8_K &S, uint8_t *lds, int nb, uint8_t *dump) {
+    uint8_t *dst = S.ok ? lds + (size_t)S.t * ActQ8_K::bytes_per_token(nb) + (size_t)S.sb * ActQ8_K::SB + 16 * S.s
+                        : dump + 16 * (threadIdx.x & 63);
+    const bool first = S.s == 0;                                     // d goes to the slot's last dword
+    *(int4 *)dst = make_int4(S.v[0], S.v[1], S.v[2], first ? S.v[0] : S.v[3]);
 }
+// items from `first` on (threads step by blockDim)
 template <int NB>
-__device__ void stage_q8_K_rest(uint8_t *lds, const uint8_t *act, size_t stride, int nb) {
-    for (int i = threadIdx.x + blockDim.x; i < NB * nb * 17; i += blockDim.x) {
+__device__ void stage_q8_K_rest(uint8_t *lds, const uint8_t *act, size_t stride, int nb, int first = 1) {
+    for (int i = threadIdx.x + first * blockDim.x; i < NB * nb * 19; i += blockDim.x) {
         StageQ8_K S;
         stage_q8_K_load<NB>(S, i, act, stride, nb);
-        stage_q8_K_store(S, lds, nb);
+        stage_q8_K_store(S, lds, nb, stage_dump<ActQ8_K>(lds, NB, nb));
     }
 }
 template <int NB>
 __device__ void stage_q8_K(uint8_t *lds, const uint8_t *act, size_t stride, int nb) {
     StageQ8_K S;
     stage_q8_K_load<NB>(S, threadIdx.x, act, stride, nb);
-    stage_q8_K_store(S, lds, nb);
+    stage_q8_K_store(S, lds, nb, stage_dump<ActQ8_K>(lds, NB, nb));
     stage_q8_K_rest<NB>(lds, act, stride, nb);
 }
 
@@ -192,7 +216,7 @@ struct FQ8_0 {
     static __device__ __forceinline__ void load(Frag &f, const g4h_tensor &W, int64_t row, int u) {
         const size_t j = (size_t)row * W.nb + u;
         const uint8_t *q = W.qs + j * 32;
-        f.w0 = ld4(q); f.w1 = ld4(q + 16);
+        f.w0 = ld4s(q); f.w1 = ld4s(q + 16);
         f.d = ((const uint16_t *)W.sc)[j];
     }
     static __device__ __forceinline__ int isum(const Frag &f, const Act &A, int u) {
@@ -221,7 +245,7 @@ struct FQ4_0 {
     struct Frag { int4 w; uint16_t d; };
     static __device__ __forceinline__ void load(Frag &f, const g4h_tensor &W, int64_t row, int u) {
         const size_t j = (size_t)row * W.nb + u;
-        f.w = ld4(W.qs + j * 16);
+        f.w = ld4s(W.qs + j * 16);
         f.d = ((const uint16_t *)W.sc)[j];
     }
     static __device__ __forceinline__ int isum(const Frag &f, const Act &A, int u) {
@@ -254,7 +278,7 @@ struct FQ4_K {
         const uint8_t *b = W.qs + ((size_t)row * W.nb + (u >> 2)) * 144;
         const int p = u & 3;
         f.h = ld4(b);
-        f.q0 = ld4(b + 16 + 32 * p); f.q1 = ld4(b + 32 + 32 * p);
+        f.q0 = ld4(b + 16 + 32 * p); f.q1 = ld4(b + 32 + 32 * p);   // plain: the header shares these lines
     }
     static __device__ __forceinline__ uint32_t sbyte(const Frag &f, int k) {   // scales[k], k < 12
         const uint32_t w = k < 4 ? (uint32_t)f.h.y : k < 8 ? (uint32_t)f.h.z : (uint32_t)f.h.w;
@@ -266,7 +290,7 @@ struct FQ4_K {
     }
     static __device__ __forceinline__ void isums(const Frag &f, const Act &A, int u, int &is, int &ms) {
         const int sb = u >> 2, p = u & 3, m = 0x0F0F0F0F;
-        const int4 *a = (const int4 *)(A.q + (size_t)sb * 256 + 64 * p);
+        const int4 *a = (const int4 *)(A.q(sb) + 64 * p);
         const int4 l0 = a[0], l1 = a[1], h0 = a[2], h1 = a[3];
         const uint32_t w[8] = {(uint32_t)f.q0.x, (uint32_t)f.q0.y, (uint32_t)f.q0.z, (uint32_t)f.q0.w,
                                (uint32_t)f.q1.x, (uint32_t)f.q1.y, (uint32_t)f.q1.z, (uint32_t)f.q1.w};
@@ -279,7 +303,7 @@ struct FQ4_K {
         int sc0, m0, sc1, m1;
         scale_min(f, 2 * p, sc0, m0);
         scale_min(f, 2 * p + 1, sc1, m1);
-        const int16_t *bs = A.bs + (size_t)sb * 16 + 4 * p;
+        const int16_t *bs = A.bs(sb) + 4 * p;
         is = sc0 * sl + sc1 * sh;
         ms = m0 * (bs[0] + bs[1]) + m1 * (bs[2] + bs[3]);
     }
@@ -287,7 +311,7 @@ struct FQ4_K {
     // over the four parts
     static __device__ __forceinline__ float accum(const Frag &f, const Act &A, int u, float acc) {
         int is, ms; isums(f, A, u, is, ms);
-        const float da = A.d[u >> 2];
+        const float da = A.d(u >> 2);
         const uint32_t dd = (uint32_t)f.h.x;
         acc = __builtin_fmaf(da * h2f((uint16_t)(dd & 0xffff)), (float)is, acc);
         return __builtin_fmaf(-da * h2f((uint16_t)(dd >> 16)), (float)ms, acc);
@@ -308,7 +332,7 @@ struct FQ2_K {
     struct Frag { int4 q, s; uint32_t dd; };
     static __device__ __forceinline__ void load(Frag &f, const g4h_tensor &W, int64_t row, int u) {
         const size_t j = (size_t)row * W.nb + (u >> 2);
-        f.q = ld4(W.qs + j * 64 + 16 * (u & 3));
+        f.q = ld4s(W.qs + j * 64 + 16 * (u & 3));
         f.s = ld4(W.sc + j * 16);
         f.dd = ((const uint32_t *)W.ex)[j];
     }
@@ -316,8 +340,8 @@ struct FQ2_K {
         const int sb = u >> 2, p = u & 3, h = p >> 1, k = p & 1;
         const uint32_t w[4] = {(uint32_t)f.q.x, (uint32_t)f.q.y, (uint32_t)f.q.z, (uint32_t)f.q.w};
         const uint32_t sw[4] = {(uint32_t)f.s.x, (uint32_t)f.s.y, (uint32_t)f.s.z, (uint32_t)f.s.w};
-        const int8_t *aq = A.q + (size_t)sb * 256 + 128 * h + 16 * k;
-        const int16_t *bs = A.bs + (size_t)sb * 16;
+        const int8_t *aq = A.q(sb) + 128 * h + 16 * k;
+        const int16_t *bs = A.bs(sb);
         int isum = 0, msum = 0;
 #pragma unroll
         for (int j = 0; j < 4; j++) {
@@ -335,7 +359,7 @@ struct FQ2_K {
     }
     static __device__ __forceinline__ float accum(const Frag &f, const Act &A, int u, float acc) {
         int is, ms; isums(f, A, u, is, ms);
-        const float da = A.d[u >> 2];
+        const float da = A.d(u >> 2);
         acc = __builtin_fmaf(da * h2f((uint16_t)(f.dd & 0xffff)), (float)is, acc);
         return __builtin_fmaf(-da * h2f((uint16_t)(f.dd >> 16)), (float)ms, acc);
     }
@@ -357,7 +381,7 @@ struct FQ3_K {
     static __device__ __forceinline__ void load(Frag &f, const g4h_tensor &W, int64_t row, int u) {
         const size_t j = (size_t)row * W.nb + (u >> 2);
         const int p = u & 3;
-        f.q = ld4(W.qs + j * 64 + 16 * p);
+        f.q = ld4s(W.qs + j * 64 + 16 * p);
         f.hm = ld4(W.ex + j * 32 + 16 * (p & 1));
         const uint32_t *s = (const uint32_t *)(W.sc + j * 12);
         f.s0 = s[0]; f.s1 = s[1]; f.s2 = s[2];
@@ -373,8 +397,8 @@ struct FQ3_K {
         const int sb = u >> 2, p = u & 3, h = p >> 1, k = p & 1;
         const uint32_t w[4] = {(uint32_t)f.q.x, (uint32_t)f.q.y, (uint32_t)f.q.z, (uint32_t)f.q.w};
         const uint32_t hb[4] = {(uint32_t)f.hm.x, (uint32_t)f.hm.y, (uint32_t)f.hm.z, (uint32_t)f.hm.w};
-        const int8_t *aq = A.q + (size_t)sb * 256 + 128 * h + 16 * k;
-        const int16_t *bs = A.bs + (size_t)sb * 16;
+        const int8_t *aq = A.q(sb) + 128 * h + 16 * k;
+        const int16_t *bs = A.bs(sb);
         int total = 0;
 #pragma unroll
         for (int j = 0; j < 4; j++) {
@@ -391,7 +415,7 @@ struct FQ3_K {
         return total;
     }
     static __device__ __forceinline__ float accum(const Frag &f, const Act &A, int u, float acc) {
-        return __builtin_fmaf(A.d[u >> 2] * h2f(f.d), (float)isum(f, A, u), acc);
+        return __builtin_fmaf(A.d(u >> 2) * h2f(f.d), (float)isum(f, A, u), acc);
     }
     static constexpr int nsums = 1;
     static __device__ __forceinline__ void sums(const Frag &f, const Act &A, int u, int *out) { out[0] = isum(f, A, u); }

@@ -20,12 +20,20 @@
 namespace g4 {
 
 template <class F>
-size_t act_lds_bytes(int nb_tokens, int64_t nblk) { return (size_t)nb_tokens * F::Act::bytes_per_token((int)nblk); }
+size_t act_lds_bytes(int nb_tokens, int64_t nblk) { return (size_t)nb_tokens * F::Act::bytes_per_token((int)nblk) + kStageDump; }
 
 
-template <class F, int NB, int LPR, int UPL>
+// XQ = 0: the NB activations are GGUF q8_0 / q8_K rows (act, act_stride).
+// XQ > 0: x holds the NB tokens as fp32 rows of ncols (contiguous) and every
+// workgroup quantizes them to q8_0 itself, in LDS (q8_lds4: the arithmetic of
+// the standalone quantizer, so results equal quantize-then-GEMV bit for bit);
+// XQ is the number of 4-float groups per thread (NB*ncols/4 <= XQ*blockDim).
+// The x loads go out before the weight stream and the quantization runs while
+// the weights are in flight; an LDS-only barrier hands the activation over
+// without waiting for the stream.
+template <class F, int NB, int LPR, int UPL, int XQ>
 __global__ __launch_bounds__(512) void k_gemv(g4h_tensor W, const uint8_t *__restrict__ act, size_t act_stride,
-                                               float *__restrict__ Y, int units) {
+                                               const float *__restrict__ x, float *__restrict__ Y, int units) {
     extern __shared__ __align__(16) uint8_t lds[];
     using Act = typename F::Act;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, wpg = blockDim.x >> 6;
@@ -34,27 +42,53 @@ __global__ __launch_bounds__(512) void k_gemv(g4h_tensor W, const uint8_t *__res
     const int64_t row0 = ((int64_t)blockIdx.x * wpg + wave) * RPW + rg;
     const bool row_ok = row0 < W.nrows;
     const int64_t row = row_ok ? row0 : W.nrows - 1;
-
-    // activation loads first, then the weight stream (see formats.h)
-    typename StageOf<F::type>::S stg;
     constexpr bool QK = F::type == Q4_0 || F::type == Q8_0;
-    if constexpr (QK) stage_q8_0_load<NB>(stg, threadIdx.x, act, act_stride, (int)W.nb);
-    else stage_q8_K_load<NB>(stg, threadIdx.x, act, act_stride, (int)W.nb);
+    static_assert(XQ == 0 || QK, "the fused quantizer produces q8_0 activations");
 
+    // activation loads first, then the weight stream (see formats.h); one
+    // K-quant token needs about two q8_K items per thread, both issued here
+    constexpr int KS = (!QK && NB == 1) ? 2 : 1;
+    typename StageOf<F::type>::S stg[KS];
+    float xv[XQ > 0 ? XQ : 1][4];
+    const int gpt = (int)(W.ncols >> 2);                            // 4-float groups per token
+    if constexpr (XQ > 0) {
+#pragma unroll
+        for (int s = 0; s < XQ; s++) {                                   // clamped, unconditional
+            const int gi = min((int)(threadIdx.x + s * blockDim.x), NB * gpt - 1);
+            const float4 v = *(const float4 *)(x + 4 * (size_t)gi);
+            xv[s][0] = v.x; xv[s][1] = v.y; xv[s][2] = v.z; xv[s][3] = v.w;
+        }
+    } else if constexpr (QK) {
+        stage_q8_0_load<NB>(stg[0], threadIdx.x, act, act_stride, (int)W.nb);
+    } else {
+#pragma unroll
+        for (int s = 0; s < KS; s++) stage_q8_K_load<NB>(stg[s], threadIdx.x + s * blockDim.x, act, act_stride, (int)W.nb);
+    }
+
+    issue_order();
+    // branch-free stream: lanes past the row's last unit reload that unit and
+    // leave it out of the sums (a load under a branch would make the compiler
+    // wait for the whole stream before the prologue below)
     typename F::Frag fr[UPL];
 #pragma unroll
-    for (int k = 0; k < UPL; k++) {
-        const int u = g + k * LPR;
-        if (u < units) F::load(fr[k], W, row, u);
-    }
-    if constexpr (QK) {
-        stage_q8_0_store(stg, lds, (int)W.nb);
+    for (int k = 0; k < UPL; k++) F::load(fr[k], W, row, min(g + k * LPR, units - 1));
+    issue_order();                                                   // the whole stream goes out before any wait
+    if constexpr (XQ > 0) {
+#pragma unroll
+        for (int s = 0; s < XQ; s++) {                                   // no branch: keeps the x loads up front
+            const int gi = threadIdx.x + s * blockDim.x;
+            const int t = gi / gpt;
+            q8_lds4(xv[s], gi - t * gpt, gi < NB * gpt, lds, (int)W.nb, t);
+        }
+    } else if constexpr (QK) {
+        stage_q8_0_store(stg[0], lds, (int)W.nb, stage_dump<ActQ8_0>(lds, NB, (int)W.nb));
         stage_q8_0_rest<NB>(lds, act, act_stride, (int)W.nb);
     } else {
-        stage_q8_K_store(stg, lds, (int)W.nb);
-        stage_q8_K_rest<NB>(lds, act, act_stride, (int)W.nb);
+#pragma unroll
+        for (int s = 0; s < KS; s++) stage_q8_K_store(stg[s], lds, (int)W.nb, stage_dump<ActQ8_K>(lds, NB, (int)W.nb));
+        stage_q8_K_rest<NB>(lds, act, act_stride, (int)W.nb, KS);
     }
-    __syncthreads();
+    lds_barrier();
 
     float acc[NB];
 #pragma unroll
@@ -108,38 +142,71 @@ static inline int gemv_waves_per_group(int64_t nrows, int rpw) {
     return best;
 }
 
+// 4-float groups per thread the fused quantizer needs (0 = no fused variant).
+// Every workgroup reads and quantizes all of x, so the fused form pays only
+// while x is small next to the workgroup's weights: up to two groups per
+// thread (q4_0 10240x2560: 5.5 us fused against 7.3 us for quantize + GEMV;
+// with eight groups, 2560x10240 took 8.8 us against 7.9 us).
+static inline int gemv_xq_slots(int64_t ncols, int nb, int threads) {
+    const int64_t per = ((int64_t)nb * (ncols / 4) + threads - 1) / threads;
+    return per <= 2 ? 2 : 0;
+}
+
 template <class F, int NB, int LPR, int UPL>
-static hipError_t go(const g4h_tensor &W, const uint8_t *act, size_t stride, float *Y, int units, hipStream_t s) {
+static hipError_t go(const g4h_tensor &W, const uint8_t *act, size_t stride, const float *x, float *Y, int units, hipStream_t s) {
     constexpr int RPW = 64 / LPR;
     const int wpg = gemv_waves_per_group(W.nrows, RPW);
     const int64_t waves = (W.nrows + RPW - 1) / RPW;
     const unsigned grid = (unsigned)((waves + wpg - 1) / wpg);
     const size_t lds = act_lds_bytes<F>(NB, W.nb);
-    hipLaunchKernelGGL((k_gemv<F, NB, LPR, UPL>), dim3(grid), dim3(64 * wpg), lds, s, W, act, stride, Y, units);
-    return hipGetLastError();
+    if (!x) {
+        hipLaunchKernelGGL((k_gemv<F, NB, LPR, UPL, 0>), dim3(grid), dim3(64 * wpg), lds, s, W, act, stride, x, Y, units);
+        return hipGetLastError();
+    }
+    if constexpr (F::type == Q4_0 || F::type == Q8_0) {
+        const int xq = gemv_xq_slots(W.ncols, NB, 64 * wpg);
+        if (xq == 2) hipLaunchKernelGGL((k_gemv<F, NB, LPR, UPL, 2>), dim3(grid), dim3(64 * wpg), lds, s, W, act, stride, x, Y, units);
+        else return hipErrorInvalidValue;
+        return hipGetLastError();
+    }
+    return hipErrorInvalidValue;
 }
 
 template <class F, int NB>
-static hipError_t pick(const g4h_tensor &W, const uint8_t *act, size_t stride, float *Y, hipStream_t s, int lpr, int upl) {
+static hipError_t pick(const g4h_tensor &W, const uint8_t *act, size_t stride, const float *x, float *Y, hipStream_t s, int lpr,
+                       int upl) {
     const int units = (int)(W.nb * F::units_per_block);
-#define G4_CASE(L, U) if (lpr == L && upl == U) return go<F, NB, L, U>(W, act, stride, Y, units, s)
-    G4_CASE(16, 2); G4_CASE(16, 4); G4_CASE(16, 8); G4_CASE(32, 2); G4_CASE(32, 4); G4_CASE(32, 8);
-    G4_CASE(64, 2); G4_CASE(64, 4); G4_CASE(64, 8);
+#define G4_CASE(L, U) if (lpr == L && upl == U) return go<F, NB, L, U>(W, act, stride, x, Y, units, s)
+    if constexpr (NB == 1) {
+        // one token: as many units per lane as the row needs, so no load is spare
+        const int per = (units + lpr - 1) / lpr;
+        upl = per < 1 ? 1 : per > 8 ? 8 : per;
+        G4_CASE(16, 1); G4_CASE(16, 2); G4_CASE(16, 3); G4_CASE(16, 4); G4_CASE(16, 5); G4_CASE(16, 6); G4_CASE(16, 7);
+        G4_CASE(16, 8); G4_CASE(32, 1); G4_CASE(32, 2); G4_CASE(32, 3); G4_CASE(32, 4); G4_CASE(32, 5); G4_CASE(32, 6);
+        G4_CASE(32, 7); G4_CASE(32, 8); G4_CASE(64, 1); G4_CASE(64, 2); G4_CASE(64, 3); G4_CASE(64, 4); G4_CASE(64, 5);
+        G4_CASE(64, 6); G4_CASE(64, 7); G4_CASE(64, 8);
+    } else {
+        G4_CASE(16, 2); G4_CASE(16, 4); G4_CASE(16, 8); G4_CASE(32, 2); G4_CASE(32, 4); G4_CASE(32, 8);
+        G4_CASE(64, 2); G4_CASE(64, 4); G4_CASE(64, 8);
+    }
 #undef G4_CASE
     return hipErrorInvalidValue;
 }
 
 // one translation unit per format instantiates these
+// x != nullptr: fp32 tokens quantized inside the kernel (q8_0 / q4_0 weights;
+// the caller checks gemv_fused_fits)
 template <class F>
-hipError_t gemv_format(const g4h_tensor &W, const uint8_t *act, size_t stride, float *Y, int nb, hipStream_t s, int lpr, int upl) {
+hipError_t gemv_format(const g4h_tensor &W, const uint8_t *act, size_t stride, const float *x, float *Y, int nb, hipStream_t s,
+                       int lpr, int upl) {
     // eight K-quant tokens with more units in flight exceed the register file;
     // a lane visits its units in the same order for any UPL, so results are unchanged
     if (F::units_per_block == 4 && nb == 8 && upl > 2) upl = 2;
     switch (nb) {
-    case 1: return pick<F, 1>(W, act, stride, Y, s, lpr, upl);
-    case 2: return pick<F, 2>(W, act, stride, Y, s, lpr, upl);
-    case 4: return pick<F, 4>(W, act, stride, Y, s, lpr, upl);
-    case 8: return pick<F, 8>(W, act, stride, Y, s, lpr, upl);
+    case 1: return pick<F, 1>(W, act, stride, x, Y, s, lpr, upl);
+    case 2: return pick<F, 2>(W, act, stride, x, Y, s, lpr, upl);
+    case 4: return pick<F, 4>(W, act, stride, x, Y, s, lpr, upl);
+    case 8: return pick<F, 8>(W, act, stride, x, Y, s, lpr, upl);
     default: return hipErrorInvalidValue;
     }
 }

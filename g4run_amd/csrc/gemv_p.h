@@ -57,30 +57,6 @@ __device__ __forceinline__ void pro_issue(ProLoads &r, const GemvPro &p) {
     }
 }
 
-// the q8_0 activation of token 0 into the LDS staging layout (ActQ8_0)
-__device__ __forceinline__ void q8_lds4(const float v[4], int gi, bool own, uint8_t *lds, int nb) {
-    float am = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
-    am = fmaxf(am, shfl_xor(am, 1));
-    am = fmaxf(am, shfl_xor(am, 2));
-    am = fmaxf(am, shfl_xor(am, 4));
-    const float id = am != 0.0f ? 127.0f / am : 0.0f;
-    uint32_t pk = 0;
-#pragma unroll
-    for (int j = 0; j < 4; j++) pk |= ((uint32_t)(int)__builtin_rintf(v[j] * id) & 0xffu) << (8 * j);
-    int sum = dot4((int)pk, 0x01010101, 0);
-    sum += shfl_xor(sum, 1);
-    sum += shfl_xor(sum, 2);
-    sum += shfl_xor(sum, 4);
-    if (!own) return;
-    ActQ8_0 A(lds, nb, 0);
-    const int b = gi >> 3, k = gi & 7;
-    ((uint32_t *)(k < 4 ? &A.q0[b] : &A.q1[b]))[k & 3] = pk;
-    if (k == 0) {
-        A.d[b] = h2f(f2h(am * (1.0f / 127.0f)));
-        A.s[b] = sum;
-    }
-}
-
 template <int PRO, int S>
 __device__ void pro_finish(ProLoads &r, const GemvPro &p, uint8_t *lds, int nb) {
     __shared__ double red[16];
@@ -120,7 +96,7 @@ __device__ void pro_finish(ProLoads &r, const GemvPro &p, uint8_t *lds, int nb) 
     for (int s = 0; s < S; s++) {
         if (s * bd >= ng) break;                                     // uniform
         const int gi = t + s * bd;
-        q8_lds4(r.v[s], gi, gi < ng, lds, nb);
+        q8_lds4(r.v[s], gi, gi < ng, lds, nb, 0);
     }
 }
 
@@ -138,13 +114,13 @@ __global__ __launch_bounds__(64 * GP_WAVES) void k_gemv_p(g4h_tensor W, const ui
     const int nb = (int)W.nb;
 
     auto row_of = [&](int64_t gq) { return min(gq * RPW + rg, W.nrows - 1); };
+    // branch-free loads (clamped to the last row / unit; the extras are not
+    // summed): a load under a branch makes the compiler wait for every load in
+    // flight before the prologue arithmetic
     auto load = [&](typename F::Frag (&fr)[UPL], int64_t gq) {
         const int64_t row = row_of(gq);
 #pragma unroll
-        for (int k = 0; k < UPL; k++) {
-            const int u = g + k * LPR;
-            if (u < units) F::load(fr[k], W, row, u);
-        }
+        for (int k = 0; k < UPL; k++) F::load(fr[k], W, row, min(g + k * LPR, units - 1));
     };
     auto finish = [&](const typename F::Frag (&fr)[UPL], int64_t gq) {
         float acc = 0.0f;
@@ -170,14 +146,16 @@ __global__ __launch_bounds__(64 * GP_WAVES) void k_gemv_p(g4h_tensor W, const ui
     if constexpr (PRO == PRO_ACT) stage_q8_0_load<1>(stg, threadIdx.x, act, 0, nb);
     else pro_issue<PRO, S>(pr, pro);
     typename F::Frag fa[UPL], fb[UPL];
-    if (grp < ngroups) load(fa, grp);
+    issue_order();
+    load(fa, grp);
+    issue_order();
     if constexpr (PRO == PRO_ACT) {
-        stage_q8_0_store(stg, lds, nb);
+        stage_q8_0_store(stg, lds, nb, stage_dump<ActQ8_0>(lds, 1, nb));
         stage_q8_0_rest<1>(lds, act, 0, nb);
     } else {
         pro_finish<PRO, S>(pr, pro, lds, nb);
     }
-    __syncthreads();
+    lds_barrier();                                                   // the first weight set stays in flight
 
     for (; grp < ngroups; grp += 2 * NW) {                            // wave-uniform
         const int64_t g2 = grp + NW, g3 = grp + 2 * NW;
@@ -193,7 +171,7 @@ template <class F, int LPR, int UPL, int PRO, int EPI>
 static hipError_t gp_go(const g4h_tensor &W, const uint8_t *act, float *Y, const GemvPro &pro, const GemvEpi &epi,
                         hipStream_t s, int grid) {
     const int units = (int)(W.nb * F::units_per_block);
-    const size_t lds = (size_t)F::Act::bytes_per_token((int)W.nb);
+    const size_t lds = (size_t)F::Act::bytes_per_token((int)W.nb) + kStageDump;
     const int slots = (int)((W.ncols / 4 + 64 * GP_WAVES - 1) / (64 * GP_WAVES));
 #define G4_GP(S_)                                                                                                \
     hipLaunchKernelGGL((k_gemv_p<F, LPR, UPL, PRO, EPI, S_>), dim3(grid), dim3(64 * GP_WAVES), lds, s, W, act, Y, \

@@ -4,11 +4,11 @@
 
 namespace g4 {
 
-hipError_t launch_gemv_q8_0(const g4h_tensor &, const uint8_t *, size_t, float *, int, hipStream_t, int, int);
-hipError_t launch_gemv_q4_0(const g4h_tensor &, const uint8_t *, size_t, float *, int, hipStream_t, int, int);
-hipError_t launch_gemv_q4_K(const g4h_tensor &, const uint8_t *, size_t, float *, int, hipStream_t, int, int);
-hipError_t launch_gemv_q3_K(const g4h_tensor &, const uint8_t *, size_t, float *, int, hipStream_t, int, int);
-hipError_t launch_gemv_q2_K(const g4h_tensor &, const uint8_t *, size_t, float *, int, hipStream_t, int, int);
+hipError_t launch_gemv_q8_0(const g4h_tensor &, const uint8_t *, size_t, const float *, float *, int, hipStream_t, int, int);
+hipError_t launch_gemv_q4_0(const g4h_tensor &, const uint8_t *, size_t, const float *, float *, int, hipStream_t, int, int);
+hipError_t launch_gemv_q4_K(const g4h_tensor &, const uint8_t *, size_t, const float *, float *, int, hipStream_t, int, int);
+hipError_t launch_gemv_q3_K(const g4h_tensor &, const uint8_t *, size_t, const float *, float *, int, hipStream_t, int, int);
+hipError_t launch_gemv_q2_K(const g4h_tensor &, const uint8_t *, size_t, const float *, float *, int, hipStream_t, int, int);
 
 // Exact per-block integer sums of every row against token `tok`: one thread
 // per (row, block); the parts of a superblock are added as integers.
@@ -62,17 +62,38 @@ size_t gemv_lds_bytes(int type, int nb_tokens, int64_t nblk) {
     return (type == Q4_0 || type == Q8_0) ? act_lds_bytes<FQ8_0>(nb_tokens, nblk) : act_lds_bytes<FQ4_K>(nb_tokens, nblk);
 }
 
-hipError_t launch_gemv(const g4h_tensor &W, const uint8_t *act, size_t stride, float *Y, int nb, hipStream_t s) {
+static hipError_t gemv_dispatch(const g4h_tensor &W, const uint8_t *act, size_t stride, const float *x, float *Y, int nb,
+                                hipStream_t s) {
     int lpr, upl;
     gemv_shape(W.type, W.nb, &lpr, &upl);
     switch (W.type) {
-    case Q8_0: return launch_gemv_q8_0(W, act, stride, Y, nb, s, lpr, upl);
-    case Q4_0: return launch_gemv_q4_0(W, act, stride, Y, nb, s, lpr, upl);
-    case Q4_K: return launch_gemv_q4_K(W, act, stride, Y, nb, s, lpr, upl);
-    case Q3_K: return launch_gemv_q3_K(W, act, stride, Y, nb, s, lpr, upl);
-    case Q2_K: return launch_gemv_q2_K(W, act, stride, Y, nb, s, lpr, upl);
+    case Q8_0: return launch_gemv_q8_0(W, act, stride, x, Y, nb, s, lpr, upl);
+    case Q4_0: return launch_gemv_q4_0(W, act, stride, x, Y, nb, s, lpr, upl);
+    case Q4_K: return launch_gemv_q4_K(W, act, stride, x, Y, nb, s, lpr, upl);
+    case Q3_K: return launch_gemv_q3_K(W, act, stride, x, Y, nb, s, lpr, upl);
+    case Q2_K: return launch_gemv_q2_K(W, act, stride, x, Y, nb, s, lpr, upl);
     default: return hipErrorInvalidValue;
     }
+}
+
+hipError_t launch_gemv(const g4h_tensor &W, const uint8_t *act, size_t stride, float *Y, int nb, hipStream_t s) {
+    return gemv_dispatch(W, act, stride, nullptr, Y, nb, s);
+}
+
+// The fused-quantizer variant exists for q8_0 / q4_0 weights when every
+// thread holds at most 8 groups of 4 inputs (nb * ncols <= 32 * threads).
+bool gemv_fused_fits(const g4h_tensor &W, int nb) {
+    if (W.type != Q8_0 && W.type != Q4_0) return false;
+    if (nb != 1 && nb != 2 && nb != 4 && nb != 8) return false;
+    int lpr, upl, wpg;
+    int64_t grid;
+    gemv_launch_shape(W, &lpr, &upl, &wpg, &grid);
+    return gemv_xq_slots(W.ncols, nb, 64 * wpg) != 0;
+}
+
+hipError_t launch_gemv_x(const g4h_tensor &W, const float *x, float *Y, int nb, hipStream_t s) {
+    if (!gemv_fused_fits(W, nb) || !x) return hipErrorInvalidValue;
+    return gemv_dispatch(W, nullptr, 0, x, Y, nb, s);
 }
 
 hipError_t launch_gemv_p_q8_0(const g4h_tensor &, const uint8_t *, float *, const GemvPro &, const GemvEpi &, hipStream_t, int,

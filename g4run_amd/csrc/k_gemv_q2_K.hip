@@ -2,8 +2,8 @@
 #include "gemv.h"
 
 namespace g4 {
-hipError_t launch_gemv_q2_K(const g4h_tensor &W, const uint8_t *act, size_t stride, float *Y, int nb, hipStream_t s, int lpr,
+hipError_t launch_gemv_q2_K(const g4h_tensor &W, const uint8_t *act, size_t stride, const float *x, float *Y, int nb, hipStream_t s, int lpr,
                           int upl) {
-    return gemv_format<FQ2_K>(W, act, stride, Y, nb, s, lpr, upl);
+    return gemv_format<FQ2_K>(W, act, stride, x, Y, nb, s, lpr, upl);
 }
 }  // namespace g4

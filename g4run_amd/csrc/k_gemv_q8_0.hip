@@ -3,9 +3,9 @@
 #include "gemv_p.h"
 
 namespace g4 {
-hipError_t launch_gemv_q8_0(const g4h_tensor &W, const uint8_t *act, size_t stride, float *Y, int nb, hipStream_t s, int lpr,
+hipError_t launch_gemv_q8_0(const g4h_tensor &W, const uint8_t *act, size_t stride, const float *x, float *Y, int nb, hipStream_t s, int lpr,
                           int upl) {
-    return gemv_format<FQ8_0>(W, act, stride, Y, nb, s, lpr, upl);
+    return gemv_format<FQ8_0>(W, act, stride, x, Y, nb, s, lpr, upl);
 }
 hipError_t launch_gemv_p_q8_0(const g4h_tensor &W, const uint8_t *act, float *Y, const GemvPro &pro, const GemvEpi &epi,
                              hipStream_t s, int lpr, int upl, int grid) {

@@ -316,7 +316,7 @@ hipError_t launch_unpack(const g4h_tensor &t, uint8_t *rows, hipStream_t s) {
 template <class F>
 static hipError_t vd_go(const uint8_t *w, size_t ws, const uint8_t *a, int64_t n, int rows, float *out, hipStream_t s) {
     const int nblk = (int)(n / blck(F::type));
-    hipLaunchKernelGGL(k_vec_dot_raw<F>, dim3((unsigned)((rows + 3) / 4)), dim3(256), F::Act::bytes_per_token(nblk), s,
+    hipLaunchKernelGGL(k_vec_dot_raw<F>, dim3((unsigned)((rows + 3) / 4)), dim3(256), F::Act::bytes_per_token(nblk) + kStageDump, s,
                        w, ws, a, nblk, rows, out);
     return hipGetLastError();
 }

@@ -46,6 +46,11 @@ int gemv_p_grid_size();
 hipError_t launch_gemv_p(const g4h_tensor &W, const uint8_t *act, float *Y, const GemvPro &pro, const GemvEpi &epi,
                          hipStream_t s);
 hipError_t launch_gemv(const g4h_tensor &W, const uint8_t *act, size_t stride, float *Y, int nb, hipStream_t s);
+// fp32 tokens x [nb][ncols] quantized to q8_0 inside the GEMV (q8_0 / q4_0
+// weights, nb in {1, 2, 4, 8}, when gemv_fused_fits); bit-identical to
+// launch_quantize_q8_0 followed by launch_gemv
+bool gemv_fused_fits(const g4h_tensor &W, int nb);
+hipError_t launch_gemv_x(const g4h_tensor &W, const float *x, float *Y, int nb, hipStream_t s);
 hipError_t launch_block_sums(const g4h_tensor &W, const uint8_t *act, size_t stride, int tok, int32_t *out, hipStream_t s);
 int block_sums_per_block(int type);
 

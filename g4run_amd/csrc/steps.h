@@ -24,13 +24,14 @@ __device__ __forceinline__ double wave_sum_dd(double v) {
     return v;
 }
 // Workgroup sum of doubles: wave butterflies, then the wave partials in order.
+// LDS-only barriers: global loads the caller has in flight stay in flight.
 __device__ __forceinline__ double wg_sum_double(double v, double *red) {
     v = wave_sum_dd(v);
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
-    __syncthreads();
+    lds_barrier();
     double r = 0.0;
     for (int w = 0; w < (int)(blockDim.x >> 6); w++) r += red[w];
-    __syncthreads();
+    lds_barrier();
     return r;
 }
 
