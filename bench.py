@@ -171,6 +171,40 @@ def bench_prefill(G, stream, Ms=(1, 8, 16, 32, 64, 128, 256, 512)):
     return out
 
 
+def bench_attention(G, stream, n_pos=8192, n_head=8, n_kv=4, hd=256, k=200):
+    """Decode attention of BASELINE configs[4] (8 query / 4 KV heads of 256, f16
+    cache at 8192 positions) as one g4h_attn_decode call, over KV caches
+    rotated beyond the MALL; HBM bytes = K + V rows read + q + out."""
+    from g4run_amd import synth
+    row = n_kv * hd * 2
+    cache_bytes = n_pos * row
+    copies = copies_for(2 * cache_bytes)
+    rng = np.random.default_rng(3)
+    kv = (rng.standard_normal(n_pos * n_kv * hd).astype(np.float16)).view(np.uint8)
+    src = G.Buffer.from_array(kv)
+    caches = []
+    for _ in range(copies):
+        kb, vb = G.Buffer(cache_bytes), G.Buffer(cache_bytes)
+        G.lib().g4h_memcpy_d2d(kb.ptr, src.ptr, cache_bytes, stream.ptr)
+        G.lib().g4h_memcpy_d2d(vb.ptr, src.ptr, cache_bytes, stream.ptr)
+        caches.append((kb, vb))
+    stream.synchronize()
+    q = G.Buffer.from_array(synth.activations(n_head, hd, seed=4))
+    out = G.Buffer(n_head * hd * 4)
+    ws = G.Buffer(G.attn_workspace_bytes(n_head, hd, n_pos))
+    ws.zero()
+    G.synchronize()
+    fn = lambda i: G.attn_decode(q, caches[i % copies][0], caches[i % copies][1], G.F16, n_head, n_kv, hd, n_pos, out,
+                                 ws=ws, stream=stream.ptr)
+    us = time_graph(G, stream, fn, k) / k * 1e3
+    alg = 2 * cache_bytes + n_head * hd * 4 * 2
+    res = {"us": round(us, 3), "alg_bytes": alg, "GBps": round(alg / us / 1e3, 1),
+           "pct_peak": round(100 * alg / us / 1e3 / PEAK_HBM, 1), "passes": G.attn_passes(G.F16, n_head, n_kv, hd, n_pos),
+           "shape": f"{n_head} q / {n_kv} kv heads x {hd}, f16 cache, {n_pos} positions, {copies} rotated cache copies"}
+    log(f"bench: attention {us:.3f} us/launch  {res['GBps']} GB/s ({res['pct_peak']}% of 8 TB/s), {res['passes']} launch(es)")
+    return res
+
+
 def bench_decode(G, steps: int, cpu_seconds: float, want_cpu: bool):
     """tokens/s of the full decode step at context ~8192."""
     m = G.Model(seed=1)
@@ -307,6 +341,7 @@ def main():
             del s
 
     prefill = bench_prefill(G, stream) if args.all_configs or args.prefill else None
+    attention = bench_attention(G, stream)
 
     cpu = None if args.no_cpu else cpu_baseline(sets, args.cpu_seconds)
     for s_ in sets:
@@ -340,6 +375,7 @@ def main():
         out["configs"] = extra
     if prefill:
         out["prefill"] = prefill
+    out["attention"] = attention
     if decode:
         out["decode"] = decode
     print(json.dumps(out), flush=True)

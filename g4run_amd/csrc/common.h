@@ -47,17 +47,72 @@ __device__ __forceinline__ int rne_prod(float a, float b) {
 template <typename T>
 __device__ __forceinline__ T shfl_xor(T v, int m) { return __shfl_xor(v, m, WAVE); }
 
-// wave-wide sum over groups of G lanes (G a power of two <= 64), fixed order
-template <int G>
-__device__ __forceinline__ float group_sum(float v) {
-#pragma unroll
-    for (int m = G / 2; m >= 1; m >>= 1) v += shfl_xor(v, m);
+// ------------------------------------------------------ lane exchanges ----
+// partner<M>(v): the value of a lane in the other half of the caller's
+// aligned group of 2M lanes, on the VALU (no LDS round trip): M = 1, 2 are
+// quad_perm DPP (lane ^ M), M = 4, 8 the row half-mirror / mirror DPP (lane i
+// of an 8- or 16-lane group meets lane 7 - i / 15 - i), M = 16, 32 gfx950's
+// v_permlane16_swap / v_permlane32_swap (lane ^ M).  A butterfly over
+// M = 1, 2, 4, ... therefore adds, at every step, the sums of the same two
+// aligned lane groups as the xor butterfly, and every lane of a group ends
+// with the same bits.
+template <int M>
+__device__ __forceinline__ uint32_t partner_u32(uint32_t v) {
+    if constexpr (M == 1) return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0xB1, 0xF, 0xF, false);
+    else if constexpr (M == 2) return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x4E, 0xF, 0xF, false);
+    else if constexpr (M == 4) return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x141, 0xF, 0xF, false);
+    else if constexpr (M == 8) return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x140, 0xF, 0xF, false);
+    else if constexpr (M == 16) {
+        const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+        return ((threadIdx.x >> 4) & 1) ? r[0] : r[1];
+    } else {
+        static_assert(M == 32, "partner<M>: M is a power of two up to 32");
+        const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+        return (threadIdx.x & 32) ? r[0] : r[1];
+    }
+}
+// exactly lane ^ 8 (DPP row_ror:8), for exchanges between lanes that hold
+// different quantities (partner<8> pairs lane i with 15 - i)
+__device__ __forceinline__ float xor8(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x128, 0xF, 0xF, false));
+}
+template <int M>
+__device__ __forceinline__ float partner(float v) { return __builtin_bit_cast(float, partner_u32<M>(__builtin_bit_cast(uint32_t, v))); }
+template <int M>
+__device__ __forceinline__ int partner(int v) { return (int)partner_u32<M>((uint32_t)v); }
+template <int M>
+__device__ __forceinline__ uint32_t partner(uint32_t v) { return partner_u32<M>(v); }
+template <int M>
+__device__ __forceinline__ double partner(double v) {
+    const uint64_t u = __builtin_bit_cast(uint64_t, v);
+    const uint64_t lo = partner_u32<M>((uint32_t)u), hi = partner_u32<M>((uint32_t)(u >> 32));
+    return __builtin_bit_cast(double, lo | (hi << 32));
+}
+
+// sums / maxima over aligned groups of G lanes (G a power of two <= 64),
+// in the fixed butterfly order M = 1, 2, 4, ...; every lane gets the result
+template <int G, typename T>
+__device__ __forceinline__ T group_sum_t(T v) {
+    if constexpr (G >= 2) v += partner<1>(v);
+    if constexpr (G >= 4) v += partner<2>(v);
+    if constexpr (G >= 8) v += partner<4>(v);
+    if constexpr (G >= 16) v += partner<8>(v);
+    if constexpr (G >= 32) v += partner<16>(v);
+    if constexpr (G >= 64) v += partner<32>(v);
     return v;
 }
 template <int G>
-__device__ __forceinline__ int group_isum(int v) {
-#pragma unroll
-    for (int m = G / 2; m >= 1; m >>= 1) v += shfl_xor(v, m);
+__device__ __forceinline__ float group_sum(float v) { return group_sum_t<G>(v); }
+template <int G>
+__device__ __forceinline__ int group_isum(int v) { return group_sum_t<G>(v); }
+template <int G>
+__device__ __forceinline__ float group_max(float v) {
+    if constexpr (G >= 2) v = fmaxf(v, partner<1>(v));
+    if constexpr (G >= 4) v = fmaxf(v, partner<2>(v));
+    if constexpr (G >= 8) v = fmaxf(v, partner<4>(v));
+    if constexpr (G >= 16) v = fmaxf(v, partner<8>(v));
+    if constexpr (G >= 32) v = fmaxf(v, partner<16>(v));
+    if constexpr (G >= 64) v = fmaxf(v, partner<32>(v));
     return v;
 }
 
@@ -83,6 +138,23 @@ __device__ __forceinline__ int4 ld4s(const void *p) {
 // meets the other waves, so global loads stay in flight across it.  Only LDS
 // data may be handed between waves through it.
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+// Meets the other waves of the workgroup without waiting for memory: loads
+// that any wave issued before it are queued ahead of loads any wave issues
+// after it.  Measured: a CU returns its waves' loads in issue order, so a
+// small load queued behind another wave's weight stream waits for that stream;
+// kernels issue their small loads, meet here, then start the streams.
+__device__ __forceinline__ void issue_barrier() {
+    asm volatile("s_barrier" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+}
+
+// Waits for every load this wave has in flight (s_waitcnt vmcnt(0)).  A kernel
+// whose first small loads miss the caches calls it before starting its
+// streams: once the whole device's streams are queued at the memory
+// controllers, a miss issued just before them is served in the controllers'
+// order, not first (measured: 0.8 us alone, 6-10 us behind the streams).
+__device__ __forceinline__ void wait_loads() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
 // Keeps the loads issued before it ahead of those after it: global loads
 // complete in issue order, so a small load that must be waited for early

@@ -124,18 +124,12 @@ __device__ void stage_q8_0_rest(uint8_t *lds, const uint8_t *act, size_t stride,
 // a 32-element block call it together (all lanes of the wave call it: the
 // block maximum is a lane shuffle), and only lanes with `own` write.
 __device__ __forceinline__ void q8_lds4(const float v[4], int j, bool own, uint8_t *lds, int nb, int t) {
-    float am = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
-    am = fmaxf(am, shfl_xor(am, 1));
-    am = fmaxf(am, shfl_xor(am, 2));
-    am = fmaxf(am, shfl_xor(am, 4));
+    const float am = group_max<8>(fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3]))));
     const float id = am != 0.0f ? 127.0f / am : 0.0f;
     uint32_t pk = 0;
 #pragma unroll
     for (int i = 0; i < 4; i++) pk |= ((uint32_t)(int)__builtin_rintf(v[i] * id) & 0xffu) << (8 * i);
-    int sum = dot4((int)pk, 0x01010101, 0);
-    sum += shfl_xor(sum, 1);
-    sum += shfl_xor(sum, 2);
-    sum += shfl_xor(sum, 4);
+    const int sum = group_isum<8>(dot4((int)pk, 0x01010101, 0));
     if (!own) return;
     ActQ8_0 A(lds, nb, t);
     const int b = j >> 3, k = j & 7;

@@ -65,7 +65,7 @@ __global__ __launch_bounds__(512) void k_gemv(g4h_tensor W, const uint8_t *__res
         for (int s = 0; s < KS; s++) stage_q8_K_load<NB>(stg[s], threadIdx.x + s * blockDim.x, act, act_stride, (int)W.nb);
     }
 
-    issue_order();
+    issue_barrier();
     // branch-free stream: lanes past the row's last unit reload that unit and
     // leave it out of the sums (a load under a branch would make the compiler
     // wait for the whole stream before the prologue below)

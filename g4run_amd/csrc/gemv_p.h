@@ -133,7 +133,7 @@ __global__ __launch_bounds__(64 * GP_WAVES) void k_gemv_p(g4h_tensor W, const ui
         acc = group_sum<LPR>(acc);
         const int64_t row0 = gq * RPW + rg;
         if constexpr (EPI == EPI_GELU) {
-            const float up = __shfl(acc, (lane + LPR) & 63, 64);     // row 2i+1 sits LPR lanes up
+            const float up = partner<LPR>(acc);                     // row 2i+1: lane ^ LPR (LPR 16 or 32)
             if (g == 0 && (rg & 1) == 0 && row0 < W.nrows) epi.h[row0 >> 1] = gelu_lut(epi.gelu, acc) * up;
         } else {
             if (g == 0 && row0 < W.nrows) Y[row0] = acc;
@@ -146,7 +146,7 @@ __global__ __launch_bounds__(64 * GP_WAVES) void k_gemv_p(g4h_tensor W, const ui
     if constexpr (PRO == PRO_ACT) stage_q8_0_load<1>(stg, threadIdx.x, act, 0, nb);
     else pro_issue<PRO, S>(pr, pro);
     typename F::Frag fa[UPL], fb[UPL];
-    issue_order();
+    issue_barrier();
     load(fa, grp);
     issue_order();
     if constexpr (PRO == PRO_ACT) {

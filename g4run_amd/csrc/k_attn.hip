@@ -38,14 +38,8 @@ namespace g4 {
 
 constexpr int ATT_CHUNK = 128;       // positions per score / V workgroup
 
-__device__ __forceinline__ float wave_max(float v) {
-    for (int k = 32; k >= 1; k >>= 1) v = fmaxf(v, shfl_xor(v, k));
-    return v;
-}
-__device__ __forceinline__ double wave_sum_d(double v) {
-    for (int k = 32; k >= 1; k >>= 1) v += __shfl_xor(v, k, 64);
-    return v;
-}
+__device__ __forceinline__ float wave_max(float v) { return group_max<64>(v); }
+__device__ __forceinline__ double wave_sum_d(double v) { return group_sum_t<64>(v); }
 
 // ------------------------------------------------------- row preparation --
 // One projection row handled by one wave, lane holding hd/64 consecutive
@@ -86,7 +80,7 @@ __device__ __forceinline__ void prep_finish(const PrepRow &r, bool weighted, boo
 #pragma unroll
         for (int e = 0; e < 4; e++) {
             if (e < epl) {                                           // uniform over the wave
-                const float other = __shfl_xor(y[e], 32, 64);
+                const float other = partner<32>(y[e]);
                 const float a = lo ? y[e] : other, b = lo ? other : y[e];
                 y[e] = lo ? a * cs[e] - b * sn[e] : a * sn[e] + b * cs[e];
             }
@@ -270,83 +264,136 @@ __device__ __forceinline__ void prep_f16_finish(const PrepF16<GRP> &st, const At
     }
 }
 
-// the lane's K loads: 8 bytes of each 16-byte group of row j (clamped to the
-// last position), the half hf of the pair
+// K and V rows of a wave's 32 positions as 16-byte non-temporal loads (the
+// cache is read once per step; measured 12.9 against 17.8 us for the whole
+// one-launch attention at 8192 positions with plain loads), coalesced: a row is
+// HD/8 slots of 8 elements; lane l = r * VS + q takes slot q of rows r, r + VR,
+// r + 2 VR, ... (VS = HD/8 rounded up to a power of two lanes per row, VR =
+// 64 / VS rows per load; lanes with q >= HD/8 load slot HD/8 - 1 again and
+// stay out of the sums).  Rows past the last position are the last row again.
 template <int HD>
-__device__ __forceinline__ void k_rows_load(uint2 (&kv)[32], const AttnCtx &c, int kvh, int j, int npos, int hf) {
-    constexpr int hd = HD, nk = hd >> 3;
-    const uint2 *row = (const uint2 *)(c.a.kc + ((size_t)min(j, npos - 1) * c.a.n_kv + kvh) * hd * 2) + hf;
+struct VGeo {
+    static constexpr int NS = HD / 8;                                // 8-element slots per row
+    static constexpr int VS = NS <= 8 ? 8 : NS <= 16 ? 16 : 32;
+    static constexpr int VR = 64 / VS;
+    static constexpr int NV = 32 / VR;                               // loads per lane
+};
+template <int HD>
+__device__ __forceinline__ void rows_load(uint4 (&rq)[16], const uint8_t *cache, int n_kv, int kvh, int j0, int npos) {
+    using G = VGeo<HD>;
+    const int lane = threadIdx.x & 63, r = lane / G::VS, q = min(lane % G::VS, G::NS - 1);
 #pragma unroll
-    for (int k = 0; k < 32; k++)
-        if (k < nk) kv[k] = row[2 * k];
-}
-
-// the GRP scores of the lane pair's position (both lanes hold them)
-template <int GRP, int HD>
-__device__ __forceinline__ void scores_f16(const uint2 (&kv)[32], int hf, const float4 (*qf)[64], float (&s)[GRP]) {
-    constexpr int nk = HD >> 3;
-    float acc[GRP][4];
-#pragma unroll
-    for (int g = 0; g < GRP; g++)
-#pragma unroll
-        for (int i = 0; i < 4; i++) acc[g][i] = 0.0f;
-#pragma unroll
-    for (int k = 0; k < 32; k++) {
-        if (k < nk) {
-            const float kf[4] = {h2f((uint16_t)(kv[k].x & 0xffff)), h2f((uint16_t)(kv[k].x >> 16)),
-                                 h2f((uint16_t)(kv[k].y & 0xffff)), h2f((uint16_t)(kv[k].y >> 16))};
-#pragma unroll
-            for (int g = 0; g < GRP; g++) {
-                const float4 qq = qf[g][2 * k + hf];
-                acc[g][0] = __builtin_fmaf(kf[0], qq.x, acc[g][0]);
-                acc[g][1] = __builtin_fmaf(kf[1], qq.y, acc[g][1]);
-                acc[g][2] = __builtin_fmaf(kf[2], qq.z, acc[g][2]);
-                acc[g][3] = __builtin_fmaf(kf[3], qq.w, acc[g][3]);
-            }
+    for (int i = 0; i < 16; i++) {
+        if (i < G::NV) {
+            const int j = min(j0 + i * G::VR + r, npos - 1);
+            const int4 w = ld4s((const uint4 *)(cache + ((size_t)j * n_kv + kvh) * HD * 2) + q);
+            rq[i] = make_uint4(w.x, w.y, w.z, w.w);
         }
     }
+}
+// the row of position p (in the wave's rows j0 ..) from an LDS copy (fp16
+// bits); p < 0: none.  A select, not a branch (a branch here would make the
+// compiler wait for all of the rows' loads at once).
+template <int HD>
+__device__ __forceinline__ void new_row(uint4 (&rq)[16], const uint16_t *row, int j0, int p) {
+    using G = VGeo<HD>;
+    const int lane = threadIdx.x & 63, r = lane / G::VS, q = min(lane % G::VS, G::NS - 1);
+    const uint4 nr = ((const uint4 *)row)[q];
+#pragma unroll
+    for (int i = 0; i < G::NV; i++) {
+        const bool hit = j0 + i * G::VR + r == p;
+        rq[i].x = hit ? nr.x : rq[i].x;
+        rq[i].y = hit ? nr.y : rq[i].y;
+        rq[i].z = hit ? nr.z : rq[i].z;
+        rq[i].w = hit ? nr.w : rq[i].w;
+    }
+}
+__device__ __forceinline__ void h8(const uint4 &w, float (&v)[8]) {
+    const uint32_t u[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+        v[2 * e] = h2f((uint16_t)(u[e] & 0xffff));
+        v[2 * e + 1] = h2f((uint16_t)(u[e] >> 16));
+    }
+}
+// the lane's 8 query elements of each head (fp16-rounded queries in LDS)
+template <int GRP, int HD>
+__device__ __forceinline__ void q_slot(const float4 (*qf)[64], float (&qv)[GRP][8]) {
+    using G = VGeo<HD>;
+    const int q = min((int)(threadIdx.x & 63) % G::VS, G::NS - 1);
 #pragma unroll
     for (int g = 0; g < GRP; g++) {
-        // lane l of the eight is acc[l & 3] of the pair member l >> 2; r_i = v[i+4] + v[i]
-        float r[4];
+        const float4 a = qf[g][2 * q], b = qf[g][2 * q + 1];
+        qv[g][0] = a.x; qv[g][1] = a.y; qv[g][2] = a.z; qv[g][3] = a.w;
+        qv[g][4] = b.x; qv[g][5] = b.y; qv[g][6] = b.z; qv[g][7] = b.w;
+    }
+}
+// Scores s_j = K_j . q (no 1/sqrt(d), model.c:538) of the wave's 32 positions
+// into sc[g][wave*32 + k]: each lane's 8 products in element order, then the
+// row's lanes summed by a butterfly (xor VS/2, ..., 1).  A fixed order, the
+// same in the three-pass and the one-launch forms; it differs from the CPU's
+// 8-lane accumulation only in the fp32 rounding of the sum.
+template <int GRP, int HD>
+__device__ __forceinline__ void scores_rows(const uint4 (&kq)[16], const float (&qv)[GRP][8], float (*sc)[ATT_CHUNK]) {
+    using G = VGeo<HD>;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, r = lane / G::VS, q = lane % G::VS;
+    const bool act = q < G::NS;
 #pragma unroll
-        for (int i = 0; i < 4; i++) r[i] = acc[g][i] + shfl_xor(acc[g][i], 1);
-        s[g] = (r[0] + r[2]) + (r[1] + r[3]);
+    for (int i = 0; i < G::NV; i++) {
+        float kf[8];
+        h8(kq[i], kf);
+#pragma unroll
+        for (int g = 0; g < GRP; g++) {
+            float acc = 0.0f;
+#pragma unroll
+            for (int e = 0; e < 8; e++) acc = __builtin_fmaf(kf[e], qv[g][e], acc);
+            acc = act ? acc : 0.0f;
+            acc = group_sum<G::VS>(acc);
+            if (q == 0) sc[g][wave * 32 + i * G::VR + r] = acc;
+        }
     }
 }
 
+// grid (n_kv, chunks of 128), 256 threads: wave w scores positions
+// ch*128 + 32w .. +31; lane l < 32 of the wave then owns position 32w + l for
+// the chunk statistics.  The chunk of the current position takes the new key
+// row from LDS in place of the stale cache row.
 template <int GRP, int HD>
 __global__ __launch_bounds__(256) void k_attn_scores_f16(AttnCtx c) {
     __shared__ __align__(16) float4 qf[GRP][64];              // fp16-rounded query
     __shared__ __align__(16) uint16_t kpos[256];              // the new key row (fp16 bits)
+    __shared__ float sc[GRP][ATT_CHUNK];
     __shared__ float wm[4][GRP];
     __shared__ double wl[4][GRP];
     const int npos = npos_of(c);
     const int kvh = blockIdx.x, ch = blockIdx.y, t = threadIdx.x;
-    const int lane = t & 63, wave = t >> 6, hf = lane & 1;
-    constexpr int hd = HD;
+    const int lane = t & 63, wave = t >> 6;
     const int h0 = kvh * GRP, p = npos - 1;
     if (ch * ATT_CHUNK >= npos) return;
     const bool pos_chunk = c.qkv && ch == p / ATT_CHUNK;
+    const int j0 = ch * ATT_CHUNK + wave * 32;
     PrepF16<GRP> st;
     prep_f16_issue<GRP, HD>(st, c, kvh, p, pos_chunk);
-    const int j = ch * ATT_CHUNK + wave * 32 + (lane >> 1);
-    const bool ok = j < npos;
-    uint2 kv[32];
-    k_rows_load<HD>(kv, c, kvh, j, npos, hf);
+    wait_loads();
+    uint4 kq[16];
+    rows_load<HD>(kq, c.a.kc, c.a.n_kv, kvh, j0, npos);
+    issue_order();
     prep_f16_finish<GRP, HD>(st, c, kvh, p, qf, kpos, nullptr);
-    __syncthreads();
-    if (pos_chunk && j == p) {                                       // the new key, not the stale cache row
-#pragma unroll
-        for (int k = 0; k < 32; k++)
-            if (k < (hd >> 3)) kv[k] = ((const uint2 *)kpos)[2 * k + hf];
-    }
+    lds_barrier();
+    new_row<HD>(kq, kpos, j0, pos_chunk ? p : -1);
+    float qv[GRP][8];
+    q_slot<GRP, HD>(qf, qv);
+    scores_rows<GRP, HD>(kq, qv, sc);
+    lds_barrier();
+    const int j = j0 + lane;
+    const bool ok = lane < 32 && j < npos;
     float s[GRP];
-    scores_f16<GRP, HD>(kv, hf, qf, s);
 #pragma unroll
-    for (int g = 0; g < GRP; g++)
-        if (ok && hf == 0) c.S[(size_t)(h0 + g) * npos + j] = s[g];
-    chunk_stats<GRP, 4, false>(s, ok, hf == 0, c, h0, ch, wm, wl);
+    for (int g = 0; g < GRP; g++) {
+        s[g] = lane < 32 ? sc[g][wave * 32 + lane] : 0.0f;
+        if (ok) c.S[(size_t)(h0 + g) * npos + j] = s[g];
+    }
+    chunk_stats<GRP, 4, false>(s, ok, lane < 32, c, h0, ch, wm, wl);
 }
 
 // q8_0 cache.  128 threads, one lane per position; the query is q8_0-quantized
@@ -395,7 +442,7 @@ __global__ __launch_bounds__(128) void k_attn_scores_q8(AttnCtx c) {
         const int g = i / (hd / 4), e4 = i - g * (hd / 4);
         const float v[4] = {qrow[g][4 * e4], qrow[g][4 * e4 + 1], qrow[g][4 * e4 + 2], qrow[g][4 * e4 + 3]};
         float am = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
-        am = fmaxf(am, shfl_xor(am, 1)); am = fmaxf(am, shfl_xor(am, 2)); am = fmaxf(am, shfl_xor(am, 4));
+        am = group_max<8>(am);
         const float id = am != 0.0f ? 127.0f / am : 0.0f;
         uint32_t pk = 0;
         for (int k = 0; k < 4; k++) pk |= ((uint32_t)(int)__builtin_rintf(v[k] * id) & 0xffu) << (8 * k);
@@ -445,54 +492,78 @@ __global__ __launch_bounds__(128) void k_attn_scores_q8(AttnCtx c) {
 }
 
 // ------------------------------------------------------------ V partials --
-// f16 V rows: lane owns elements 4*lane .. 4*lane+3 of rows j0 .. j0+31
-// (clamped to the last position; lanes beyond hd/4 idle)
-template <int HD>
-__device__ __forceinline__ void v_rows_load(uint2 (&vv)[32], const AttnCtx &c, int kvh, int j0, int npos) {
-    constexpr int hd = HD;
-    const int lane = threadIdx.x & 63;
-    if (4 * lane < hd) {
+// o[g][e] (elements 8q .. 8q+7, on lanes with r = 0) = sum over the wave's 32
+// positions of w_j * V_j: each lane sums its rows in order, then the VR row
+// classes are added in order (r = 0, 1, ...).  Positions past the last one
+// carry weight 0 (their rows are the last row again).
+template <int GRP, int HD>
+__device__ __forceinline__ void v_accum_f16(const uint4 (&vq)[16], const float (*wts)[ATT_CHUNK], float (&o)[GRP][8]) {
+    using G = VGeo<HD>;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, r = lane / G::VS;
 #pragma unroll
-        for (int k = 0; k < 32; k++) {
-            const int j = min(j0 + k, npos - 1);
-            vv[k] = *((const uint2 *)(c.a.vc + ((size_t)j * c.a.n_kv + kvh) * hd * 2) + lane);
+    for (int g = 0; g < GRP; g++)
+#pragma unroll
+        for (int e = 0; e < 8; e++) o[g][e] = 0.0f;
+#pragma unroll
+    for (int i = 0; i < G::NV; i++) {
+        const uint32_t w32[4] = {vq[i].x, vq[i].y, vq[i].z, vq[i].w};
+        float v[8];
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            v[2 * e] = h2f((uint16_t)(w32[e] & 0xffff));
+            v[2 * e + 1] = h2f((uint16_t)(w32[e] >> 16));
         }
-    }
-}
-
-// o[g] = sum over the wave's positions (in order) of w_j * V_j.  Positions
-// past the last one carry weight 0 (their rows are the last row again), which
-// leaves every sum as the loop that stops at the last position gives it.
-template <int GRP>
-__device__ __forceinline__ void v_accum_f16(const uint2 (&vv)[32], const float (*wts)[ATT_CHUNK], float (&o)[GRP][4]) {
-    const int wave = threadIdx.x >> 6;
-    float4 w4[GRP][8];
-#pragma unroll
-    for (int g = 0; g < GRP; g++)
-#pragma unroll
-        for (int q = 0; q < 8; q++) w4[g][q] = *(const float4 *)&wts[g][wave * 32 + 4 * q];
-#pragma unroll
-    for (int g = 0; g < GRP; g++)
-#pragma unroll
-        for (int e = 0; e < 4; e++) o[g][e] = 0.0f;
-#pragma unroll
-    for (int k = 0; k < 32; k++) {
-        const float v[4] = {h2f((uint16_t)(vv[k].x & 0xffff)), h2f((uint16_t)(vv[k].x >> 16)),
-                            h2f((uint16_t)(vv[k].y & 0xffff)), h2f((uint16_t)(vv[k].y >> 16))};
 #pragma unroll
         for (int g = 0; g < GRP; g++) {
-            const float4 q4 = w4[g][k >> 2];
-            const float w = (k & 3) == 0 ? q4.x : (k & 3) == 1 ? q4.y : (k & 3) == 2 ? q4.z : q4.w;
+            const float w = wts[g][wave * 32 + i * G::VR + r];
 #pragma unroll
-            for (int e = 0; e < 4; e++) o[g][e] = __builtin_fmaf(w, v[e], o[g][e]);
+            for (int e = 0; e < 8; e++) o[g][e] = __builtin_fmaf(w, v[e], o[g][e]);
         }
     }
+    // the VR row classes (lanes VS apart, same slot) by a butterfly over them;
+    // the exchanges are exact lane ^ 8 / 16 / 32, since the lanes of a class
+    // hold different elements
+#pragma unroll
+    for (int g = 0; g < GRP; g++)
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            float sum = o[g][e];
+            if constexpr (G::VS <= 8) sum += xor8(sum);
+            if constexpr (G::VS <= 16) sum += partner<16>(sum);
+            sum += partner<32>(sum);
+            o[g][e] = sum;
+        }
 }
 
 // the four waves' partials added in order into P[h][ch][hd]
 template <int GRP, int HD, bool AG>
-__device__ __forceinline__ void v_partial_store(const float (&o)[GRP][4], float (*part)[GRP][256], const AttnCtx &c, int h0,
+__device__ __forceinline__ void v_partial_store(const float (&o)[GRP][8], float (*part)[GRP][256], const AttnCtx &c, int h0,
                                                 int ch) {
+    using G = VGeo<HD>;
+    constexpr int hd = HD;
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    if (lane < G::NS) {
+#pragma unroll
+        for (int g = 0; g < GRP; g++) {
+            *(float4 *)&part[wave][g][8 * lane] = make_float4(o[g][0], o[g][1], o[g][2], o[g][3]);
+            *(float4 *)&part[wave][g][8 * lane + 4] = make_float4(o[g][4], o[g][5], o[g][6], o[g][7]);
+        }
+    }
+    __syncthreads();
+    for (int i = t; i < GRP * hd; i += 256) {
+        const int g = i / hd, e = i - g * hd;
+        const float r = ((part[0][g][e] + part[1][g][e]) + part[2][g][e]) + part[3][g][e];
+        float *dst = &c.P[((size_t)(h0 + g) * c.nc + ch) * hd + e];
+        if constexpr (AG) st_ag(dst, r);
+        else *dst = r;
+    }
+}
+
+// q8_0 V path: lane owns elements 4*lane .. 4*lane+3; the four waves'
+// partials added in order into P[h][ch][hd]
+template <int GRP, int HD>
+__device__ __forceinline__ void v_partial_store4(const float (&o)[GRP][4], float (*part)[GRP][256], const AttnCtx &c, int h0,
+                                                 int ch) {
     constexpr int hd = HD;
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     if (4 * lane < hd) {
@@ -503,10 +574,7 @@ __device__ __forceinline__ void v_partial_store(const float (&o)[GRP][4], float 
     __syncthreads();
     for (int i = t; i < GRP * hd; i += 256) {
         const int g = i / hd, e = i - g * hd;
-        const float r = ((part[0][g][e] + part[1][g][e]) + part[2][g][e]) + part[3][g][e];
-        float *dst = &c.P[((size_t)(h0 + g) * c.nc + ch) * hd + e];
-        if constexpr (AG) st_ag(dst, r);
-        else *dst = r;
+        c.P[((size_t)(h0 + g) * c.nc + ch) * hd + e] = ((part[0][g][e] + part[1][g][e]) + part[2][g][e]) + part[3][g][e];
     }
 }
 
@@ -545,10 +613,11 @@ __global__ __launch_bounds__(256) void k_attn_v(AttnCtx c) {
         const int i = t + 256 * k, g = i / ATT_CHUNK, jw = ch * ATT_CHUNK + (i - g * ATT_CHUNK);
         sv[k] = i < GRP * ATT_CHUNK && jw < npos ? c.S[(size_t)(h0 + g) * npos + jw] : 0.0f;
     }
-    // 2. the V rows: lane owns elements 4*lane .. 4*lane+3 (lanes beyond hd/4 idle)
+    // 2. the V rows (f16: 16-byte loads, see v_rows_load; q8_0: below, lane
+    // owning elements 4*lane .. 4*lane+3, lanes beyond hd/4 idle)
     const bool lane_ok = 4 * lane < hd;
-    uint2 vv[32];
-    if constexpr (KV == F16) v_rows_load<HD>(vv, c, kvh, j0, npos);
+    uint4 vq[16];
+    if constexpr (KV == F16) rows_load<HD>(vq, c.a.vc, n_kv, kvh, j0, npos);
     // 3. global max and normaliser (chunks beyond 64 in further passes)
 #pragma unroll
     for (int q = 0; q < HPW; q++) {
@@ -582,10 +651,12 @@ __global__ __launch_bounds__(256) void k_attn_v(AttnCtx c) {
         }
     }
     __syncthreads();
-    float o[GRP][4];
     if constexpr (KV == F16) {
-        v_accum_f16<GRP>(vv, wl, o);
+        float o[GRP][8];
+        v_accum_f16<GRP, HD>(vq, wl, o);
+        v_partial_store<GRP, HD, false>(o, part, c, h0, ch);
     } else {
+        float o[GRP][4];
 #pragma unroll
         for (int g = 0; g < GRP; g++)
 #pragma unroll
@@ -607,8 +678,8 @@ __global__ __launch_bounds__(256) void k_attn_v(AttnCtx c) {
                 }
             }
         }
+        v_partial_store4<GRP, HD>(o, part, c, h0, ch);
     }
-    v_partial_store<GRP, HD, false>(o, part, c, h0, ch);
 }
 
 // -------------------------------------------------------------- combine --
@@ -708,6 +779,7 @@ __global__ __launch_bounds__(256) void k_attn_fused_f16(AttnCtx c) {
     __shared__ float wm[4][GRP];
     __shared__ double wl[4][GRP];
     __shared__ __align__(16) float wts[GRP][ATT_CHUNK];
+    __shared__ float sc[GRP][ATT_CHUNK];
     __shared__ float inv_s[GRP], max_s[GRP];
     __shared__ __align__(16) float part[4][GRP][256];
     __shared__ float vals[ATT_FUSED_MAXC * 32];                      // combine: [chunk][32]
@@ -715,38 +787,49 @@ __global__ __launch_bounds__(256) void k_attn_fused_f16(AttnCtx c) {
     const int npos = npos_of(c);
     const uint32_t tag = tag_of(c);
     const int kvh = blockIdx.x, ch = blockIdx.y, t = threadIdx.x;
-    const int lane = t & 63, wave = t >> 6, hf = lane & 1;
+    const int lane = t & 63, wave = t >> 6;
     constexpr int hd = HD;
     const int h0 = kvh * GRP, p = npos - 1;
     const int nch = (npos + ATT_CHUNK - 1) / ATT_CHUNK;
     const bool live = ch < nch;                                      // uniform over the workgroup
     if (t == 0) bad = 0;
     if (live) {
-        const int j = ch * ATT_CHUNK + wave * 32 + (lane >> 1), j0 = ch * ATT_CHUNK + wave * 32;
+        const int j0 = ch * ATT_CHUNK + wave * 32, j = j0 + lane;  // lane < 32 owns position j
         const bool pos_chunk = c.qkv && ch == p / ATT_CHUNK;
+        const bool mine = lane < 32;
         float s[GRP];
+        uint4 vq[16];
         {
+            // every load goes out first: preparation rows, K, then V (which
+            // streams while the scores and the statistics hand-off proceed)
+            // the small loads first (landed before the streams start), then
+            // every wave's K, then V
             PrepF16<GRP> st;
             prep_f16_issue<GRP, HD>(st, c, kvh, p, pos_chunk);
-            uint2 kv[32];
-            k_rows_load<HD>(kv, c, kvh, j, npos, hf);
+            wait_loads();
+            uint4 kq[16];
+            rows_load<HD>(kq, c.a.kc, c.a.n_kv, kvh, j0, npos);
+            issue_barrier();
+            rows_load<HD>(vq, c.a.vc, c.a.n_kv, kvh, j0, npos);
+            issue_order();
             prep_f16_finish<GRP, HD>(st, c, kvh, p, qf, kpos, vpos);
-            __syncthreads();
-            if (pos_chunk && j == p) {                               // the new key, not the stale cache row
+            lds_barrier();
+            new_row<HD>(kq, kpos, j0, pos_chunk ? p : -1);           // the new key, not the stale cache row
+            float qv[GRP][8];
+            q_slot<GRP, HD>(qf, qv);
+            scores_rows<GRP, HD>(kq, qv, sc);
+            lds_barrier();
 #pragma unroll
-                for (int k = 0; k < 32; k++)
-                    if (k < (hd >> 3)) kv[k] = ((const uint2 *)kpos)[2 * k + hf];
-            }
-            scores_f16<GRP, HD>(kv, hf, qf, s);
+            for (int g = 0; g < GRP; g++) s[g] = mine ? sc[g][wave * 32 + lane] : 0.0f;
         }
         // chunk statistics (as chunk_stats), published as tagged words
-        const bool ok = j < npos, once = hf == 0;
+        const bool ok = mine && j < npos, once = mine;
 #pragma unroll
         for (int g = 0; g < GRP; g++) {
             const float m = wave_max(ok ? s[g] : -INFINITY);
             if (lane == 0) wm[wave][g] = m;
         }
-        __syncthreads();
+        lds_barrier();
 #pragma unroll
         for (int g = 0; g < GRP; g++) {
             float mc = wm[0][g];
@@ -755,7 +838,7 @@ __global__ __launch_bounds__(256) void k_attn_fused_f16(AttnCtx c) {
             const double l = wave_sum_d(e);
             if (lane == 0) wl[wave][g] = l;
         }
-        __syncthreads();
+        lds_barrier();
         if (t < GRP) {
             const int g = t;
             float mc = wm[0][g];
@@ -767,14 +850,6 @@ __global__ __launch_bounds__(256) void k_attn_fused_f16(AttnCtx c) {
             st_tag(w3, __float_as_uint(mc), tag);
             st_tag(w3 + 1, (uint32_t)lb, tag);
             st_tag(w3 + 2, (uint32_t)(lb >> 32), tag);
-        }
-        // the V rows stream in while the other chunks' statistics arrive
-        uint2 vv[32];
-        v_rows_load<HD>(vv, c, kvh, j0, npos);
-        if (pos_chunk && 4 * lane < hd) {                            // the new value row
-#pragma unroll
-            for (int k = 0; k < 32; k++)
-                if (j0 + k == p) vv[k] = ((const uint2 *)vpos)[lane];
         }
         // every chunk's statistics: global maximum and normaliser (as the V pass)
         constexpr int HPW = (GRP + 3) / 4;
@@ -813,24 +888,27 @@ __global__ __launch_bounds__(256) void k_attn_fused_f16(AttnCtx c) {
                 }
             }
         }
-        __syncthreads();
-        if (hf == 0) {
+        lds_barrier();
+        if (mine) {
 #pragma unroll
             for (int g = 0; g < GRP; g++) {
                 const float e = (float)exp((double)((j < npos ? s[g] : 0.0f) - max_s[g]));
-                wts[g][wave * 32 + (lane >> 1)] = j < npos ? h2f(f2h(e * inv_s[g])) : 0.0f;
+                wts[g][wave * 32 + lane] = j < npos ? h2f(f2h(e * inv_s[g])) : 0.0f;
             }
         }
-        __syncthreads();
+        lds_barrier();
         // the chunk's value partial (as the V pass), published as tagged words
-        float o[GRP][4];
-        v_accum_f16<GRP>(vv, wts, o);
-        if (4 * lane < hd) {
+        new_row<HD>(vq, vpos, j0, pos_chunk ? p : -1);               // the new value row
+        float o[GRP][8];
+        v_accum_f16<GRP, HD>(vq, wts, o);
+        if (lane < VGeo<HD>::NS) {
 #pragma unroll
-            for (int g = 0; g < GRP; g++)
-                *(float4 *)&part[wave][g][4 * lane] = make_float4(o[g][0], o[g][1], o[g][2], o[g][3]);
+            for (int g = 0; g < GRP; g++) {
+                *(float4 *)&part[wave][g][8 * lane] = make_float4(o[g][0], o[g][1], o[g][2], o[g][3]);
+                *(float4 *)&part[wave][g][8 * lane + 4] = make_float4(o[g][4], o[g][5], o[g][6], o[g][7]);
+            }
         }
-        __syncthreads();
+        lds_barrier();
         for (int i = t; i < GRP * hd; i += 256) {
             const int g = i / hd, e = i - g * hd;
             const float r = ((part[0][g][e] + part[1][g][e]) + part[2][g][e]) + part[3][g][e];
@@ -843,7 +921,7 @@ __global__ __launch_bounds__(256) void k_attn_fused_f16(AttnCtx c) {
     // order (as the combine pass)
     const int nblk = GRP * hd / 32, nwg = gridDim.y;
     for (int b = ch; b < nblk; b += nwg) {                           // uniform over the workgroup
-        __syncthreads();
+        lds_barrier();
         const int g = (b * 32) / hd, e0 = b * 32 - g * hd, i = t & 31, r0 = t >> 5;
         const uint64_t *base = c.PT + (size_t)(h0 + g) * c.nc * hd + e0 + i;
         constexpr int PER = ATT_FUSED_MAXC / 8;                      // chunks per thread
@@ -860,7 +938,7 @@ __global__ __launch_bounds__(256) void k_attn_fused_f16(AttnCtx c) {
 #pragma unroll
         for (int q = 0; q < PER; q++)
             if (need[q]) vals[(r0 + 8 * q) * 32 + i] = __uint_as_float(bits[q]);
-        __syncthreads();
+        lds_barrier();
         float r = 0.0f;
         if (t < 32) {
             for (int k0 = 0; k0 < nch; k0 += 16) {                      // 16 reads in flight, adds in order
@@ -878,9 +956,9 @@ __global__ __launch_bounds__(256) void k_attn_fused_f16(AttnCtx c) {
             c.out[(size_t)(h0 + g) * hd + e0 + t] = r;
         }
         if (c.q8out) {                                               // uniform
-            __syncthreads();
+            lds_barrier();
             if (t < 32) vals[t] = r;
-            __syncthreads();
+            lds_barrier();
             if (t < 8) {
                 float v4[4];
 #pragma unroll

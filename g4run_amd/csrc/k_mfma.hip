@@ -167,9 +167,7 @@ __global__ __launch_bounds__(256) void k_quantize_planar(const float *__restrict
     float v[4] = {0.f, 0.f, 0.f, 0.f};
     if (own) f4(ldf4(x + (size_t)m * xs + 4 * gi), v);
     float am = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
-    am = fmaxf(am, shfl_xor(am, 1));
-    am = fmaxf(am, shfl_xor(am, 2));
-    am = fmaxf(am, shfl_xor(am, 4));
+    am = group_max<8>(am);
     if (!own) return;
     const float id = am != 0.0f ? 127.0f / am : 0.0f;
     uint32_t pk = 0;

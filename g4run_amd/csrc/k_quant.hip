@@ -34,9 +34,7 @@ __global__ __launch_bounds__(256) void k_quantize_q8_0(const float *__restrict__
         for (int i = 0; i < 4; i++) v[i] = src[i];
     }
     float am = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
-    am = fmaxf(am, shfl_xor(am, 1));
-    am = fmaxf(am, shfl_xor(am, 2));
-    am = fmaxf(am, shfl_xor(am, 4));
+    am = group_max<8>(am);
     const float id = am != 0.0f ? 127.0f / am : 0.0f;
     uint32_t packed = 0;
 #pragma unroll

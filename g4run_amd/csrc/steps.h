@@ -19,10 +19,7 @@ __device__ __forceinline__ float rms_scale(double ss, int n, float eps) {
     return 1.0f / __builtin_sqrtf(mean + eps);
 }
 
-__device__ __forceinline__ double wave_sum_dd(double v) {
-    for (int k = 32; k >= 1; k >>= 1) v += __shfl_xor(v, k, 64);
-    return v;
-}
+__device__ __forceinline__ double wave_sum_dd(double v) { return group_sum_t<64>(v); }
 // Workgroup sum of doubles: wave butterflies, then the wave partials in order.
 // LDS-only barriers: global loads the caller has in flight stay in flight.
 __device__ __forceinline__ double wg_sum_double(double v, double *red) {
@@ -40,9 +37,7 @@ __device__ __forceinline__ double wg_sum_double(double v, double *red) {
 // writes quants 4*(gi%8).. of GGUF block gi/8 of dst; its first lane the scale.
 __device__ __forceinline__ void q8_store4(const float v[4], int gi, bool own, uint8_t *dst) {
     float am = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
-    am = fmaxf(am, shfl_xor(am, 1));
-    am = fmaxf(am, shfl_xor(am, 2));
-    am = fmaxf(am, shfl_xor(am, 4));
+    am = group_max<8>(am);
     if (!own) return;
     const float id = am != 0.0f ? 127.0f / am : 0.0f;
     uint32_t pk = 0;
