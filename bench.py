@@ -28,10 +28,10 @@ sys.path.insert(0, ROOT)
 PEAK_HBM = 8000.0          # GB/s, MI355X published
 PEAK_INT8 = 5000.0         # dense int8 MFMA TOPS, MI355X published
 # HBM bytes per launch of the roofline kernel (q4_0 10240x2560 GEMV) from two
-# rocprofv3 --pmc passes: FETCH_SIZE 7287.1 KiB x 2.00 + WRITE_SIZE 64.0 KiB x
+# rocprofv3 --pmc passes: FETCH_SIZE 7277.1 KiB x 2.00 + WRITE_SIZE 64.0 KiB x
 # 1.00, scales from a 256 MiB device copy in the same runs
 # (profiles/gemv_q4_0_ffn_traffic.md).
-TRAFFIC_UP = int((7287.1 * 2.00 + 64.0 * 1.00) * 1024)
+TRAFFIC_UP = int((7277.1 * 2.00 + 64.0 * 1.00) * 1024)
 MALL = 256 << 20
 
 
@@ -278,7 +278,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--all-configs", action="store_true", help="also time every GEMV config (stderr + JSON)")
     ap.add_argument("--decode-steps", type=int, default=64, help="decode steps timed at context ~8192 (0 = skip)")
-    ap.add_argument("--prefill", action="store_true", help="also time config 3 (GEMV vs matrix-core crossover)")
+    ap.add_argument("--prefill", nargs="?", const="1,8,16,32,64,128,256,512", default=None, metavar="M,...",
+                    help="also time config 3 (GEMV vs matrix-core crossover) at these token counts")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="start with one 256 MiB device copy (the reference dispatch for rocprofv3 --pmc byte counters)")
     args = ap.parse_args()
@@ -340,7 +341,8 @@ def main():
                 f"({100 * s.bytes / t_pre / 1e3 / PEAK_HBM:.1f}% of 8 TB/s); with quantize {t_fus:.3f} us")
             del s
 
-    prefill = bench_prefill(G, stream) if args.all_configs or args.prefill else None
+    prefill_ms = args.prefill or ("1,8,16,32,64,128,256,512" if args.all_configs else None)
+    prefill = bench_prefill(G, stream, tuple(int(m) for m in prefill_ms.split(","))) if prefill_ms else None
     attention = bench_attention(G, stream)
 
     cpu = None if args.no_cpu else cpu_baseline(sets, args.cpu_seconds)

@@ -372,6 +372,7 @@ extern "C" int g4h_matmul_describe(const g4h_tensor *W, int nb, int path, char *
     int64_t grid;
     gemv_launch_shape(*W, &lpr, &upl, &wpg, &grid);
     const int chunk = nb >= 8 ? 8 : nb >= 4 ? 4 : nb >= 2 ? 2 : 1;
+    upl = gemv_upl_final(W->type, W->nb, chunk, lpr, upl);
     snprintf(buf, len, "k_gemv<%s,nb=%d,lpr=%d,upl=%d> grid=%lld block=%d (x%d launches)", type_name(W->type), chunk, lpr, upl,
              (long long)grid, 64 * wpg, (nb + chunk - 1) / chunk);
     return G4H_OK;

@@ -177,10 +177,8 @@ static hipError_t pick(const g4h_tensor &W, const uint8_t *act, size_t stride, c
                        int upl) {
     const int units = (int)(W.nb * F::units_per_block);
 #define G4_CASE(L, U) if (lpr == L && upl == U) return go<F, NB, L, U>(W, act, stride, x, Y, units, s)
+    upl = gemv_upl_final(W.type, W.nb, NB, lpr, upl);
     if constexpr (NB == 1) {
-        // one token: as many units per lane as the row needs, so no load is spare
-        const int per = (units + lpr - 1) / lpr;
-        upl = per < 1 ? 1 : per > 8 ? 8 : per;
         G4_CASE(16, 1); G4_CASE(16, 2); G4_CASE(16, 3); G4_CASE(16, 4); G4_CASE(16, 5); G4_CASE(16, 6); G4_CASE(16, 7);
         G4_CASE(16, 8); G4_CASE(32, 1); G4_CASE(32, 2); G4_CASE(32, 3); G4_CASE(32, 4); G4_CASE(32, 5); G4_CASE(32, 6);
         G4_CASE(32, 7); G4_CASE(32, 8); G4_CASE(64, 1); G4_CASE(64, 2); G4_CASE(64, 3); G4_CASE(64, 4); G4_CASE(64, 5);
@@ -199,9 +197,6 @@ static hipError_t pick(const g4h_tensor &W, const uint8_t *act, size_t stride, c
 template <class F>
 hipError_t gemv_format(const g4h_tensor &W, const uint8_t *act, size_t stride, const float *x, float *Y, int nb, hipStream_t s,
                        int lpr, int upl) {
-    // eight K-quant tokens with more units in flight exceed the register file;
-    // a lane visits its units in the same order for any UPL, so results are unchanged
-    if (F::units_per_block == 4 && nb == 8 && upl > 2) upl = 2;
     switch (nb) {
     case 1: return pick<F, 1>(W, act, stride, x, Y, s, lpr, upl);
     case 2: return pick<F, 2>(W, act, stride, x, Y, s, lpr, upl);

@@ -1,33 +1,36 @@
 // k_attn.hip -- decode attention over an f16 or q8_0 KV cache (the GPU form of
 // attn_kernel + kv_store, model.c:509-589, with the q/k/v head preparation of
-// model.c:664-687 folded in), as three passes over 128-position chunks.
+// model.c:664-687 folded in) over 128-position chunks.
 //
 // Cache layout: [slot][n_kv][hd] rows (one row = one head's K or V for one
 // position), f16 or q8_0 blocks.  Query heads map to KV heads h / (n_head/n_kv)
 // (model.c:1099).
 //
-//   scores   grid (KV head, chunk).  Optionally prepares the rows first: the
-//            group's query heads (RMSNorm * q_norm, NeoX RoPE) and -- in the
-//            chunk holding the current position -- the new key (RMSNorm *
-//            k_norm, RoPE) and value (RMSNorm) rows, stored into the caches at
-//            that position.  q is rounded to the K cache's activation form
-//            (fp16, or q8_0 blocks, model.c:530-533) and dotted with each K
-//            row in the shipped dot's order: eight fp32 lanes of fused
-//            products and the same horizontal-sum tree (quants.c:1319-1331 /
-//            984-999), so scores equal the CPU's bit for bit; no 1/sqrt(d)
-//            (model.c:538).  Per chunk it also stores the maximum m_c and
-//            l_c = sum exp(s_j - m_c) in double.
-//   V        grid (KV head, chunk).  M = max_c m_c is the global maximum, so
-//            e_j = (float)exp(s_j - M) is the reference's expf(s_j - max)
-//            (model.c:547); the normaliser sum_c l_c exp(m_c - M) equals the
-//            reference's double sum up to the grouping of that sum, and
-//            inv = (float)(1/sum) (model.c:549).  Weights fp16(e_j*inv) for an
-//            f16 V cache, e_j*inv for q8_0 (model.c:555, 573); each wave
-//            accumulates w_j V_j over 32 positions into chunk partials.
-//   combine  grid n_head: the chunk partials in order, and q8_0 of each head
-//            row for the output projection (quants.c:74-109).
-// Only the fp32 order of the value sum and the double grouping of the
-// normaliser differ from the CPU's sequential loops.
+// Steps (one launch, k_attn_fused_f16, for f16 caches whose chunks the device
+// holds resident at once; otherwise three launches through global memory):
+//   preparation  optionally the group's query heads (RMSNorm * q_norm, NeoX
+//                RoPE) and -- in the chunk holding the current position -- the
+//                new key (RMSNorm * k_norm, RoPE) and value (RMSNorm) rows,
+//                stored into the caches at that position; q is rounded to the
+//                K cache's activation form (fp16, or q8_0 blocks, model.c:530-533).
+//   scores       s_j = K_j . q, no 1/sqrt(d) (model.c:538).  f16: each lane's 8
+//                products in element order, then a butterfly over the row's
+//                lanes -- a fixed order that differs from the CPU's 8-lane f16
+//                dot (quants.c:1319-1331) only in the fp32 rounding of the sum.
+//                q8_0: one lane per position in the AVX2 q8_0 dot's order
+//                (quants.c:984-999), equal to the CPU's bit for bit.  Per chunk
+//                the maximum m_c and l_c = sum exp(s_j - m_c) in double.
+//   weights      M = max_c m_c is the global maximum, so e_j = (float)exp(s_j - M)
+//                is the reference's expf(s_j - max) (model.c:547); the
+//                normaliser sum_c l_c exp(m_c - M) equals the reference's
+//                double sum up to the grouping of that sum, and inv =
+//                (float)(1/sum) (model.c:549).  Weights fp16(e_j*inv) for an f16
+//                V cache, e_j*inv for q8_0 (model.c:555, 573).
+//   V / combine  chunk partials of sum w_j V_j, added in chunk order, and q8_0
+//                of each head row for the output projection (quants.c:74-109).
+// Beyond the f16 score sum, only the fp32 order of the value sum and the
+// double grouping of the normaliser differ from the CPU's sequential loops;
+// the one-launch and three-launch forms give identical bits.
 #include <algorithm>
 
 #include "formats.h"

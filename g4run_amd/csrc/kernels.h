@@ -18,6 +18,18 @@ hipError_t launch_vec_dot_raw(int wtype, const uint8_t *w, size_t ws, const uint
 // k_gemv.hip
 
 void gemv_shape(int type, int64_t nblk, int *lpr, int *upl);
+// The units per lane a launch of nb_tokens tokens finally uses: one token takes
+// exactly as many as the row needs (1..8, so no load is spare); eight K-quant
+// tokens cap it at 2 (register file).  A lane visits its units in the same
+// order for any UPL, so results do not depend on it.
+inline int gemv_upl_final(int type, int64_t nblk, int nb_tokens, int lpr, int upl) {
+    const int upb = blck(type) == 256 ? 4 : 1;
+    if (nb_tokens == 1) {
+        const int per = (int)((nblk * upb + lpr - 1) / lpr);
+        return per < 1 ? 1 : per > 8 ? 8 : per;
+    }
+    return (upb == 4 && nb_tokens == 8 && upl > 2) ? 2 : upl;
+}
 size_t gemv_lds_bytes(int type, int nb_tokens, int64_t nblk);
 void gemv_launch_shape(const g4h_tensor &W, int *lpr, int *upl, int *wpg, int64_t *grid);
 

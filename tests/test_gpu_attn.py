@@ -1,7 +1,9 @@
 """Decode attention (attn_kernel, model.c:509-580) and kv_store on the GPU
 against the CPU oracle.  KV stores are bit-exact; the attention output is
-within |gpu-cpu| <= 1e-5 + 1e-3|cpu| (only the fp32 order of the final
-V accumulation differs from the CPU's loop)."""
+within |gpu-cpu| <= 1e-5 + 1e-3|cpu|.  The fp32 order of the f16 score sums,
+the grouping of the double softmax normaliser and the fp32 order of the final
+V accumulation differ from the CPU's loops; the fp16 rounding of q and of the
+weights is the reference's."""
 import numpy as np
 import pytest
 

@@ -73,6 +73,33 @@ def test_graph_replay_matches_eager(gpu):
         assert np.array_equal(m2.logits().view(np.uint32), eager[i][1].view(np.uint32))
 
 
+@pytest.mark.parametrize("kv_type", [1, 8], ids=["f16", "q8_0"])
+def test_fused_step_equals_unfused(gpu, monkeypatch, kv_type):
+    """The step with the residual norms folded into the Wqkv / Wgu prologues and
+    GELU into the Wgu epilogue (the default) gives the same tokens and logits,
+    bit for bit, as the step of separate norm / quantize / GELU kernels
+    (G4H_DECODE_FUSE=0)."""
+    G = gpu
+    runs = []
+    for fuse in (None, "0"):
+        if fuse is None:
+            monkeypatch.delenv("G4H_DECODE_FUSE", raising=False)
+        else:
+            monkeypatch.setenv("G4H_DECODE_FUSE", fuse)
+        m = G.Model(seed=21, kv_type=kv_type, **SMALL)
+        m.fill_kv(seed=22)
+        out, tok = [], 9
+        for pos in range(30, 33):
+            tok = m.forward(tok, pos)
+            out.append((tok, m.logits()))
+        m.free()
+        runs.append(out)
+    monkeypatch.delenv("G4H_DECODE_FUSE", raising=False)
+    for (t0, l0), (t1, l1) in zip(*runs):
+        assert t0 == t1
+        assert np.array_equal(l0.view(np.uint32), l1.view(np.uint32))
+
+
 def test_model_bad_config(gpu):
     G = gpu
     with pytest.raises(G.G4HError):
