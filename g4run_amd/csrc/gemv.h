@@ -32,7 +32,7 @@ size_t act_lds_bytes(int nb_tokens, int64_t nblk) { return (size_t)nb_tokens * F
 // the weights are in flight; an LDS-only barrier hands the activation over
 // without waiting for the stream.
 template <class F, int NB, int LPR, int UPL, int XQ>
-__global__ __launch_bounds__(512) void k_gemv(g4h_tensor W, const uint8_t *__restrict__ act, size_t act_stride,
+__global__ __launch_bounds__(XQ == 4 ? 1024 : 512) void k_gemv(g4h_tensor W, const uint8_t *__restrict__ act, size_t act_stride,
                                                const float *__restrict__ x, float *__restrict__ Y, int units) {
     extern __shared__ __align__(16) uint8_t lds[];
     using Act = typename F::Act;
@@ -147,9 +147,31 @@ static inline int gemv_waves_per_group(int64_t nrows, int rpw) {
 // while x is small next to the workgroup's weights: up to two groups per
 // thread (q4_0 10240x2560: 5.5 us fused against 7.3 us for quantize + GEMV;
 // with eight groups, 2560x10240 took 8.8 us against 7.9 us).
-static inline int gemv_xq_slots(int64_t ncols, int nb, int threads) {
-    const int64_t per = ((int64_t)nb * (ncols / 4) + threads - 1) / threads;
-    return per <= 2 ? 2 : 0;
+// One token with a wider input (the 10240-wide down projection) takes up to
+// four groups per thread instead, in workgroups of up to 16 waves chosen as
+// gemv_waves_per_group does: 2560x10240 runs 256 workgroups of 10 waves, one
+// per CU, so each CU reads and quantizes x once.  Returns 0, 2 or 4 and the
+// waves per workgroup of that launch.
+static inline int gemv_xq_shape(int64_t ncols, int nb, int64_t waves, int wpg, int *xwpg) {
+    const int64_t ng = (int64_t)nb * (ncols / 4);
+    *xwpg = wpg;
+    if (ng <= 2 * 64 * (int64_t)wpg) return 2;
+    static const bool wide = [] {
+        const char *e = getenv("G4H_GEMV_XQ4");
+        return !e || atoi(e) != 0;
+    }();
+    if (nb != 1 || !wide) return 0;
+    int best = 0;
+    int64_t best_cost = INT64_MAX;
+    for (int w = 1; w <= 16; w++) {
+        if (ng > 4 * 64 * (int64_t)w) continue;
+        const int64_t grid = (waves + w - 1) / w;
+        const int64_t cost = (grid + 255) / 256 * w;
+        if (cost < best_cost) { best_cost = cost; best = w; }
+    }
+    if (!best) return 0;
+    *xwpg = best;
+    return 4;
 }
 
 template <class F, int NB, int LPR, int UPL>
@@ -164,9 +186,17 @@ static hipError_t go(const g4h_tensor &W, const uint8_t *act, size_t stride, con
         return hipGetLastError();
     }
     if constexpr (F::type == Q4_0 || F::type == Q8_0) {
-        const int xq = gemv_xq_slots(W.ncols, NB, 64 * wpg);
-        if (xq == 2) hipLaunchKernelGGL((k_gemv<F, NB, LPR, UPL, 2>), dim3(grid), dim3(64 * wpg), lds, s, W, act, stride, x, Y, units);
-        else return hipErrorInvalidValue;
+        int xwpg;
+        const int xq = gemv_xq_shape(W.ncols, NB, waves, wpg, &xwpg);
+        if (xq == 2) {
+            hipLaunchKernelGGL((k_gemv<F, NB, LPR, UPL, 2>), dim3(grid), dim3(64 * wpg), lds, s, W, act, stride, x, Y, units);
+        } else if constexpr (NB == 1) {
+            if (xq != 4) return hipErrorInvalidValue;
+            const unsigned grid4 = (unsigned)((waves + xwpg - 1) / xwpg);
+            hipLaunchKernelGGL((k_gemv<F, 1, LPR, UPL, 4>), dim3(grid4), dim3(64 * xwpg), lds, s, W, act, stride, x, Y, units);
+        } else {
+            return hipErrorInvalidValue;
+        }
         return hipGetLastError();
     }
     return hipErrorInvalidValue;

@@ -81,14 +81,16 @@ hipError_t launch_gemv(const g4h_tensor &W, const uint8_t *act, size_t stride, f
 }
 
 // The fused-quantizer variant exists for q8_0 / q4_0 weights when every
-// thread holds at most 8 groups of 4 inputs (nb * ncols <= 32 * threads).
+// thread of the launch holds at most 2 groups of 4 inputs, or 4 for one token
+// (gemv_xq_shape).
 bool gemv_fused_fits(const g4h_tensor &W, int nb) {
     if (W.type != Q8_0 && W.type != Q4_0) return false;
     if (nb != 1 && nb != 2 && nb != 4 && nb != 8) return false;
-    int lpr, upl, wpg;
+    int lpr, upl, wpg, xwpg;
     int64_t grid;
     gemv_launch_shape(W, &lpr, &upl, &wpg, &grid);
-    return gemv_xq_slots(W.ncols, nb, 64 * wpg) != 0;
+    const int64_t waves = (W.nrows + 64 / lpr - 1) / (64 / lpr);
+    return gemv_xq_shape(W.ncols, nb, waves, wpg, &xwpg) != 0;
 }
 
 hipError_t launch_gemv_x(const g4h_tensor &W, const float *x, float *Y, int nb, hipStream_t s) {
