@@ -324,7 +324,7 @@ def main():
     ms_k = time_graph(G, stream, lambda i: up.call(G, i, stream.ptr, fused=False), kr)
     per_launch_us = ms_k / kr * 1e3
     achieved = up.bytes / (per_launch_us * 1e-6) / 1e9
-    kernel = G.matmul_describe(up.W[0], 1, 1)
+    kernel = G.matmul_describe(up.W[0], 1, 1).split(";")[0]
 
     extra = {}
     if args.all_configs:

@@ -338,6 +338,26 @@ static bool fused_quant_enabled() {
     return on;
 }
 
+// GEMV token chunks of 8/4/2/1 within the LDS budget: the chunk that starts at
+// token `done` of nb
+static int gemv_chunk_at(const g4h_tensor &W, int nb, int done) {
+    int chunk = 8;
+    while (chunk > nb - done || (chunk > 1 && gemv_lds_bytes(W.type, chunk, W.nb) > kMaxLds)) chunk >>= 1;
+    return chunk;
+}
+
+// whether an fp32-input call of nb tokens quantizes inside every GEMV chunk
+// (16-byte aligned x assumed); otherwise a quantizer launch runs first
+static bool x_fused(const g4h_tensor &W, int nb) {
+    if (!fused_quant_enabled()) return false;
+    for (int done = 0; done < nb;) {
+        const int chunk = gemv_chunk_at(W, nb, done);
+        if (!gemv_fused_fits(W, chunk)) return false;
+        done += chunk;
+    }
+    return true;
+}
+
 // Token count from which the matrix-core family replaces the GEMV family for
 // q8_0 / q4_0 weights: the measured crossover on q8_0 4096x4096 lies between 16
 // tokens (GEMV 18.5 us, matrix cores 20.3 us) and 32 (33.6 us vs 24.2 us).
@@ -373,8 +393,9 @@ extern "C" int g4h_matmul_describe(const g4h_tensor *W, int nb, int path, char *
     gemv_launch_shape(*W, &lpr, &upl, &wpg, &grid);
     const int chunk = nb >= 8 ? 8 : nb >= 4 ? 4 : nb >= 2 ? 2 : 1;
     upl = gemv_upl_final(W->type, W->nb, chunk, lpr, upl);
-    snprintf(buf, len, "k_gemv<%s,nb=%d,lpr=%d,upl=%d> grid=%lld block=%d (x%d launches)", type_name(W->type), chunk, lpr, upl,
-             (long long)grid, 64 * wpg, (nb + chunk - 1) / chunk);
+    snprintf(buf, len, "k_gemv<%s,nb=%d,lpr=%d,upl=%d> grid=%lld block=%d (x%d launches); fp32 x %s", type_name(W->type), chunk,
+             lpr, upl, (long long)grid, 64 * wpg, (nb + chunk - 1) / chunk,
+             x_fused(*W, nb) ? "quantized in-kernel" : "quantized by a separate launch");
     return G4H_OK;
 }
 
@@ -408,18 +429,11 @@ extern "C" int g4h_matmul_ex(const g4h_tensor *W, const float *x, const void *pr
     }
     const uint8_t *act = (const uint8_t *)pre;
     size_t stride = pre_stride;
-    auto chunk_at = [&](int done) {                                  // GEMV token chunks of 8/4/2/1 within the LDS budget
-        int chunk = 8;
-        while (chunk > nb - done || (chunk > 1 && gemv_lds_bytes(W->type, chunk, W->nb) > kMaxLds)) chunk >>= 1;
-        return chunk;
-    };
     if (x && (uintptr_t)x % 16 == 0 && fused_quant_enabled()) {
         // q8_0 / q4_0 weights: every chunk quantizes its fp32 tokens in the GEMV prologue
-        bool fits = true;
-        for (int done = 0; done < nb && fits; done += chunk_at(done)) fits = gemv_fused_fits(*W, chunk_at(done));
-        if (fits) {
+        if (x_fused(*W, nb)) {
             for (int done = 0; done < nb;) {
-                const int chunk = chunk_at(done);
+                const int chunk = gemv_chunk_at(*W, nb, done);
                 const hipError_t e = launch_gemv_x(*W, x + (size_t)done * W->ncols, Y + (size_t)done * W->nrows, chunk, s);
                 if (e != hipSuccess) return hip_fail(e, "g4h_matmul: gemv launch");
                 done += chunk;
@@ -443,7 +457,7 @@ extern "C" int g4h_matmul_ex(const g4h_tensor *W, const float *x, const void *pr
     // GEMV family in token chunks of 8/4/2/1 that fit the LDS budget
     int done = 0;
     while (done < nb) {
-        const int chunk = chunk_at(done);
+        const int chunk = gemv_chunk_at(*W, nb, done);
         const hipError_t e = launch_gemv(*W, act + (size_t)done * stride, stride, Y + (size_t)done * W->nrows, chunk, s);
         if (e != hipSuccess) return hip_fail(e, "g4h_matmul: gemv launch");
         done += chunk;

@@ -345,6 +345,8 @@ extern "C" int g4h_forward_state(g4h_model *m, void *stream) {
                 pro.x = m->ff;
                 pro.n = F;
                 M_HIP(launch_gemv_p(*m->wdown[l], nullptr, m->xb, pro, GemvEpi(), s));
+            } else if (gemv_fused_fits(*m->wdown[l], 1) && (uintptr_t)m->ff % 16 == 0) {
+                M_HIP(launch_gemv_x(*m->wdown[l], m->ff, m->xb, 1, s));      // h quantized in the GEMV
             } else {
                 M_HIP(launch_quantize_q8_0(m->ff, F, m->act, ast, F, 1, s));
                 M_HIP(launch_gemv(*m->wdown[l], m->act, ast, m->xb, 1, s));

@@ -190,13 +190,33 @@ def test_batch_bit_identical_to_single_token(gpu, oracle, name, qt):
 @pytest.mark.parametrize("name,qt", FMTS)
 def test_fused_quantizer_equals_prequantized(gpu, oracle, name, qt):
     from g4run_amd import synth
-    cols = 4096 if qt in (8, 2) else 4096
+    cols = 4096
     w = synth.weights(qt, 128, cols, seed=31)
     x = synth.activations(3, cols, seed=32)
     t = gpu.Tensor.from_rows(qt, w, cols)
     a = gpu_matmul(gpu, t, x=x, nb=3)
     b = gpu_matmul(gpu, t, act=oracle.prep_act(qt, x), nb=3)
     assert np.array_equal(bits(a), bits(b))
+
+
+@pytest.mark.parametrize("qt,rows,cols,nb", [
+    (2, 10240, 2560, 1), (2, 2560, 10240, 1), (8, 4096, 4096, 1), (2, 2048, 11008, 1), (8, 1000, 6400, 1),
+    (8, 4096, 2048, 2), (2, 4096, 256, 8),
+])
+def test_in_kernel_quantizer_equals_prequantized(gpu, oracle, qt, rows, cols, nb):
+    """The shapes whose fp32 input is quantized inside the GEMV (two groups of
+    four inputs per thread, or four for one token in larger workgroups) give
+    the bits of the GEMV on the separately quantized input."""
+    from g4run_amd import synth
+    w = synth.weights(qt, rows, cols, seed=rows + cols)
+    x = synth.activations(nb, cols, seed=nb)
+    t = gpu.Tensor.from_rows(qt, w, cols)
+    assert "quantized in-kernel" in gpu.matmul_describe(t, nb, 1)
+    a = gpu_matmul(gpu, t, x=x, nb=nb)
+    b = gpu_matmul(gpu, t, act=oracle.prep_act(qt, x), nb=nb)
+    assert np.array_equal(bits(a), bits(b))
+    if nb == 1:
+        assert_close(a, oracle_matmul(oracle, qt, w, x), f"{qt} {rows}x{cols}")
 
 
 @pytest.mark.parametrize("name,qt", FMTS)
