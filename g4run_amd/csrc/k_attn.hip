@@ -281,35 +281,43 @@ struct VGeo {
     static constexpr int VR = 64 / VS;
     static constexpr int NV = 32 / VR;                               // loads per lane
 };
+// load i of the lane: slot q of row j0 + i * VR + r
 template <int HD>
-__device__ __forceinline__ void rows_load(uint4 (&rq)[16], const uint8_t *cache, int n_kv, int kvh, int j0, int npos) {
+__device__ __forceinline__ uint4 row_load(const uint8_t *cache, int n_kv, int kvh, int j0, int i, int npos) {
     using G = VGeo<HD>;
     const int lane = threadIdx.x & 63, r = lane / G::VS, q = min(lane % G::VS, G::NS - 1);
+    const int j = min(j0 + i * G::VR + r, npos - 1);
+    const int4 w = ld4s((const uint4 *)(cache + ((size_t)j * n_kv + kvh) * HD * 2) + q);
+    return make_uint4(w.x, w.y, w.z, w.w);
+}
+template <int HD>
+__device__ __forceinline__ void rows_load(uint4 (&rq)[16], const uint8_t *cache, int n_kv, int kvh, int j0, int npos) {
 #pragma unroll
-    for (int i = 0; i < 16; i++) {
-        if (i < G::NV) {
-            const int j = min(j0 + i * G::VR + r, npos - 1);
-            const int4 w = ld4s((const uint4 *)(cache + ((size_t)j * n_kv + kvh) * HD * 2) + q);
-            rq[i] = make_uint4(w.x, w.y, w.z, w.w);
-        }
-    }
+    for (int i = 0; i < 16; i++)
+        if (i < VGeo<HD>::NV) rq[i] = row_load<HD>(cache, n_kv, kvh, j0, i, npos);
 }
 // the row of position p (in the wave's rows j0 ..) from an LDS copy (fp16
 // bits); p < 0: none.  A select, not a branch (a branch here would make the
 // compiler wait for all of the rows' loads at once).
 template <int HD>
-__device__ __forceinline__ void new_row(uint4 (&rq)[16], const uint16_t *row, int j0, int p) {
+__device__ __forceinline__ uint4 new_row_slot(const uint16_t *row) {
     using G = VGeo<HD>;
-    const int lane = threadIdx.x & 63, r = lane / G::VS, q = min(lane % G::VS, G::NS - 1);
-    const uint4 nr = ((const uint4 *)row)[q];
+    return ((const uint4 *)row)[min((int)(threadIdx.x & 63) % G::VS, G::NS - 1)];
+}
+template <int HD>
+__device__ __forceinline__ void new_row1(uint4 &rq, const uint4 &nr, int j0, int i, int p) {
+    using G = VGeo<HD>;
+    const bool hit = j0 + i * G::VR + (int)(threadIdx.x & 63) / G::VS == p;
+    rq.x = hit ? nr.x : rq.x;
+    rq.y = hit ? nr.y : rq.y;
+    rq.z = hit ? nr.z : rq.z;
+    rq.w = hit ? nr.w : rq.w;
+}
+template <int HD>
+__device__ __forceinline__ void new_row(uint4 (&rq)[16], const uint16_t *row, int j0, int p) {
+    const uint4 nr = new_row_slot<HD>(row);
 #pragma unroll
-    for (int i = 0; i < G::NV; i++) {
-        const bool hit = j0 + i * G::VR + r == p;
-        rq[i].x = hit ? nr.x : rq[i].x;
-        rq[i].y = hit ? nr.y : rq[i].y;
-        rq[i].z = hit ? nr.z : rq[i].z;
-        rq[i].w = hit ? nr.w : rq[i].w;
-    }
+    for (int i = 0; i < VGeo<HD>::NV; i++) new_row1<HD>(rq[i], nr, j0, i, p);
 }
 __device__ __forceinline__ void h8(const uint4 &w, float (&v)[8]) {
     const uint32_t u[4] = {w.x, w.y, w.z, w.w};
@@ -337,24 +345,26 @@ __device__ __forceinline__ void q_slot(const float4 (*qf)[64], float (&qv)[GRP][
 // same in the three-pass and the one-launch forms; it differs from the CPU's
 // 8-lane accumulation only in the fp32 rounding of the sum.
 template <int GRP, int HD>
-__device__ __forceinline__ void scores_rows(const uint4 (&kq)[16], const float (&qv)[GRP][8], float (*sc)[ATT_CHUNK]) {
+__device__ __forceinline__ void score_row(const uint4 &kq, const float (&qv)[GRP][8], float (*sc)[ATT_CHUNK], int i) {
     using G = VGeo<HD>;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, r = lane / G::VS, q = lane % G::VS;
     const bool act = q < G::NS;
+    float kf[8];
+    h8(kq, kf);
 #pragma unroll
-    for (int i = 0; i < G::NV; i++) {
-        float kf[8];
-        h8(kq[i], kf);
+    for (int g = 0; g < GRP; g++) {
+        float acc = 0.0f;
 #pragma unroll
-        for (int g = 0; g < GRP; g++) {
-            float acc = 0.0f;
-#pragma unroll
-            for (int e = 0; e < 8; e++) acc = __builtin_fmaf(kf[e], qv[g][e], acc);
-            acc = act ? acc : 0.0f;
-            acc = group_sum<G::VS>(acc);
-            if (q == 0) sc[g][wave * 32 + i * G::VR + r] = acc;
-        }
+        for (int e = 0; e < 8; e++) acc = __builtin_fmaf(kf[e], qv[g][e], acc);
+        acc = act ? acc : 0.0f;
+        acc = group_sum<G::VS>(acc);
+        if (q == 0) sc[g][wave * 32 + i * G::VR + r] = acc;
     }
+}
+template <int GRP, int HD>
+__device__ __forceinline__ void scores_rows(const uint4 (&kq)[16], const float (&qv)[GRP][8], float (*sc)[ATT_CHUNK]) {
+#pragma unroll
+    for (int i = 0; i < VGeo<HD>::NV; i++) score_row<GRP, HD>(kq[i], qv, sc, i);
 }
 
 // grid (n_kv, chunks of 128), 256 threads: wave w scores positions
@@ -803,24 +813,28 @@ __global__ __launch_bounds__(256) void k_attn_fused_f16(AttnCtx c) {
         float s[GRP];
         uint4 vq[16];
         {
-            // every load goes out first: preparation rows, K, then V (which
-            // streams while the scores and the statistics hand-off proceed)
             // the small loads first (landed before the streams start), then
-            // every wave's K, then V
+            // the wave's K rows; each V row is issued once the K row it
+            // follows has been scored, so the scores start with the first K
+            // row and V streams behind K while the statistics proceed
             PrepF16<GRP> st;
             prep_f16_issue<GRP, HD>(st, c, kvh, p, pos_chunk);
             wait_loads();
             uint4 kq[16];
             rows_load<HD>(kq, c.a.kc, c.a.n_kv, kvh, j0, npos);
-            issue_barrier();
-            rows_load<HD>(vq, c.a.vc, c.a.n_kv, kvh, j0, npos);
             issue_order();
             prep_f16_finish<GRP, HD>(st, c, kvh, p, qf, kpos, vpos);
             lds_barrier();
-            new_row<HD>(kq, kpos, j0, pos_chunk ? p : -1);           // the new key, not the stale cache row
             float qv[GRP][8];
             q_slot<GRP, HD>(qf, qv);
-            scores_rows<GRP, HD>(kq, qv, sc);
+            const uint4 nk = new_row_slot<HD>(kpos);
+#pragma unroll
+            for (int i = 0; i < VGeo<HD>::NV; i++) {
+                new_row1<HD>(kq[i], nk, j0, i, pos_chunk ? p : -1);  // the new key, not the stale cache row
+                score_row<GRP, HD>(kq[i], qv, sc, i);
+                vq[i] = row_load<HD>(c.a.vc, c.a.n_kv, kvh, j0, i, npos);
+                issue_order();
+            }
             lds_barrier();
 #pragma unroll
             for (int g = 0; g < GRP; g++) s[g] = mine ? sc[g][wave * 32 + lane] : 0.0f;
