@@ -40,6 +40,15 @@
 namespace g4 {
 
 constexpr int ATT_CHUNK = 128;       // positions per score / V workgroup
+constexpr int ATT_CSUM = 8;          // chunks per group in the combine's two-level sum
+// one-launch form: V loads per lane issued while K is scored; the rest are
+// issued after the statistics hand-off
+#ifndef ATT_V_EARLY
+#define ATT_V_EARLY 16
+#endif
+#ifndef ATT_POLL_SLEEP
+#define ATT_POLL_SLEEP 1
+#endif
 
 __device__ __forceinline__ float wave_max(float v) { return group_max<64>(v); }
 __device__ __forceinline__ double wave_sum_d(double v) { return group_sum_t<64>(v); }
@@ -127,7 +136,7 @@ struct AttnCtx {
     int nc;                  // chunk stride of the workspace
     float *out;              // [n_head][hd]
     uint8_t *q8out;          // optional q8_0 rows of out
-    // fused launch: tagged statistics T [n_head][nc][3] and partials
+    // fused launch: tagged statistics T [n_head][nc][ATT_TW] (3 words used) and partials
     // PT [n_head][nc][hd]; this launch's tag is *epoch * tag_mul + tag_add + 1
     uint64_t *T, *PT;
     const unsigned *epoch;
@@ -510,7 +519,8 @@ __global__ __launch_bounds__(128) void k_attn_scores_q8(AttnCtx c) {
 // classes are added in order (r = 0, 1, ...).  Positions past the last one
 // carry weight 0 (their rows are the last row again).
 template <int GRP, int HD>
-__device__ __forceinline__ void v_accum_f16(const uint4 (&vq)[16], const float (*wts)[ATT_CHUNK], float (&o)[GRP][8]) {
+__device__ __forceinline__ void v_accum_f16(const uint4 (&vq)[16], const float (*wts)[ATT_CHUNK], float (&o)[GRP][8],
+                                            uint4 nr = uint4{}, int j0 = 0, int p = -1) {
     using G = VGeo<HD>;
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, r = lane / G::VS;
 #pragma unroll
@@ -519,7 +529,9 @@ __device__ __forceinline__ void v_accum_f16(const uint4 (&vq)[16], const float (
         for (int e = 0; e < 8; e++) o[g][e] = 0.0f;
 #pragma unroll
     for (int i = 0; i < G::NV; i++) {
-        const uint32_t w32[4] = {vq[i].x, vq[i].y, vq[i].z, vq[i].w};
+        uint4 row = vq[i];
+        new_row1<HD>(row, nr, j0, i, p);                             // p >= 0: the new value row of position p
+        const uint32_t w32[4] = {row.x, row.y, row.z, row.w};
         float v[8];
 #pragma unroll
         for (int e = 0; e < 4; e++) {
@@ -703,16 +715,22 @@ __device__ __forceinline__ void combine_head(const AttnCtx &c, int h, int nch, f
     const int e = threadIdx.x, hd = c.a.hd;
     if (e < hd) {
         const float *p = c.P + (size_t)h * c.nc * hd + e;
+        // chunk order of the one-launch combine: groups of ATT_CSUM chunks,
+        // each summed in order, then the group sums in order
         float r = 0.0f;
-        int k0 = 0;
-        for (; k0 + 32 <= nch; k0 += 32) {
-            float v[32];
+        for (int k0 = 0; k0 < nch; k0 += ATT_CSUM) {
+            float v[ATT_CSUM];
 #pragma unroll
-            for (int k = 0; k < 32; k++) v[k] = AG ? ld_ag(p + (size_t)(k0 + k) * hd) : p[(size_t)(k0 + k) * hd];
+            for (int k = 0; k < ATT_CSUM; k++) {
+                const size_t kk = (size_t)min(k0 + k, nch - 1) * hd;
+                const float x = AG ? ld_ag(p + kk) : p[kk];
+                v[k] = k0 + k < nch ? x : 0.0f;
+            }
+            float sg = 0.0f;
 #pragma unroll
-            for (int k = 0; k < 32; k++) r += v[k];
+            for (int k = 0; k < ATT_CSUM; k++) sg += v[k];
+            r += sg;
         }
-        for (; k0 < nch; k0++) r += AG ? ld_ag(p + (size_t)k0 * hd) : p[(size_t)k0 * hd];
         c.out[(size_t)h * hd + e] = r;
         row[e] = r;
     }
@@ -757,6 +775,11 @@ __global__ __launch_bounds__(256) void k_attn_combine(AttnCtx c) {
 // bit-identical to theirs.
 constexpr unsigned ATT_SPIN_LIMIT = 1u << 20;
 constexpr int ATT_FUSED_MAXC = 128;  // chunks per KV head (two per lane)
+// words per (head, chunk) statistics record: its three tagged words alone in a
+// 128-byte line.  Measured: 64 workgroups polling words that share lines with
+// other writers see the last store about 2.0 us late, 0.75 us with one writer
+// per line.
+constexpr int ATT_TW = 16;
 
 __device__ __forceinline__ uint32_t tag_of(const AttnCtx &c) { return *c.epoch * c.tag_mul + c.tag_add + 1u; }
 __device__ __forceinline__ void st_tag(uint64_t *p, uint32_t bits, uint32_t tag) { st_ag(p, ((uint64_t)tag << 32) | bits); }
@@ -775,7 +798,7 @@ __device__ __forceinline__ bool poll_words(const uint64_t *const (&src)[N], cons
         for (int k = 0; k < N; k++) all &= (uint32_t)(w[k] >> 32) == tag;
         if (all) break;
         if (it == ATT_SPIN_LIMIT) return false;
-        __builtin_amdgcn_s_sleep(1);
+        __builtin_amdgcn_s_sleep(ATT_POLL_SLEEP);
 #pragma unroll
         for (int k = 0; k < N; k++)
             if ((uint32_t)(w[k] >> 32) != tag) w[k] = ld_ag(src[k]);
@@ -796,6 +819,7 @@ __global__ __launch_bounds__(256) void k_attn_fused_f16(AttnCtx c) {
     __shared__ float inv_s[GRP], max_s[GRP];
     __shared__ __align__(16) float part[4][GRP][256];
     __shared__ float vals[ATT_FUSED_MAXC * 32];                      // combine: [chunk][32]
+    __shared__ float gsum[ATT_FUSED_MAXC / ATT_CSUM * 32];           // combine: [chunk group][32]
     __shared__ int bad;
     const int npos = npos_of(c);
     const uint32_t tag = tag_of(c);
@@ -832,7 +856,7 @@ __global__ __launch_bounds__(256) void k_attn_fused_f16(AttnCtx c) {
             for (int i = 0; i < VGeo<HD>::NV; i++) {
                 new_row1<HD>(kq[i], nk, j0, i, pos_chunk ? p : -1);  // the new key, not the stale cache row
                 score_row<GRP, HD>(kq[i], qv, sc, i);
-                vq[i] = row_load<HD>(c.a.vc, c.a.n_kv, kvh, j0, i, npos);
+                if (i < ATT_V_EARLY) vq[i] = row_load<HD>(c.a.vc, c.a.n_kv, kvh, j0, i, npos);
                 issue_order();
             }
             lds_barrier();
@@ -862,7 +886,7 @@ __global__ __launch_bounds__(256) void k_attn_fused_f16(AttnCtx c) {
             for (int w = 1; w < 4; w++) mc = fmaxf(mc, wm[w][g]);
             double l = 0.0;
             for (int w = 0; w < 4; w++) l += wl[w][g];
-            uint64_t *w3 = c.T + ((size_t)(h0 + g) * c.nc + ch) * 3;
+            uint64_t *w3 = c.T + ((size_t)(h0 + g) * c.nc + ch) * ATT_TW;
             const uint64_t lb = (uint64_t)__double_as_longlong(l);
             st_tag(w3, __float_as_uint(mc), tag);
             st_tag(w3 + 1, (uint32_t)lb, tag);
@@ -874,7 +898,7 @@ __global__ __launch_bounds__(256) void k_attn_fused_f16(AttnCtx c) {
         for (int q = 0; q < HPW; q++) {
             const int g = wave + 4 * q;
             if (g < GRP) {                                           // uniform over the wave
-                const uint64_t *w3 = c.T + (size_t)(h0 + g) * c.nc * 3;
+                const uint64_t *w3 = c.T + (size_t)(h0 + g) * c.nc * ATT_TW;
                 const uint64_t *src[6];
                 bool need[6];
                 uint32_t bits[6];
@@ -883,7 +907,7 @@ __global__ __launch_bounds__(256) void k_attn_fused_f16(AttnCtx c) {
 #pragma unroll
                     for (int k = 0; k < 3; k++) {
                         const int ci = 64 * r + lane;
-                        src[3 * r + k] = w3 + (size_t)min(ci, nch - 1) * 3 + k;
+                        src[3 * r + k] = w3 + (size_t)min(ci, nch - 1) * ATT_TW + k;
                         need[3 * r + k] = ci < nch;
                     }
                 if (!poll_words<6>(src, need, tag, bits)) bad = 1;
@@ -906,6 +930,12 @@ __global__ __launch_bounds__(256) void k_attn_fused_f16(AttnCtx c) {
             }
         }
         lds_barrier();
+        // the rest of V, behind the statistics hand-off (a CU returns loads in
+        // issue order, so V rows issued before the poll would delay it); the
+        // weights are formed while these rows land
+#pragma unroll
+        for (int i = ATT_V_EARLY; i < VGeo<HD>::NV; i++) vq[i] = row_load<HD>(c.a.vc, c.a.n_kv, kvh, j0, i, npos);
+        issue_order();
         if (mine) {
 #pragma unroll
             for (int g = 0; g < GRP; g++) {
@@ -915,9 +945,8 @@ __global__ __launch_bounds__(256) void k_attn_fused_f16(AttnCtx c) {
         }
         lds_barrier();
         // the chunk's value partial (as the V pass), published as tagged words
-        new_row<HD>(vq, vpos, j0, pos_chunk ? p : -1);               // the new value row
         float o[GRP][8];
-        v_accum_f16<GRP, HD>(vq, wts, o);
+        v_accum_f16<GRP, HD>(vq, wts, o, new_row_slot<HD>(vpos), j0, pos_chunk ? p : -1);
         if (lane < VGeo<HD>::NS) {
 #pragma unroll
             for (int g = 0; g < GRP; g++) {
@@ -956,15 +985,37 @@ __global__ __launch_bounds__(256) void k_attn_fused_f16(AttnCtx c) {
         for (int q = 0; q < PER; q++)
             if (need[q]) vals[(r0 + 8 * q) * 32 + i] = __uint_as_float(bits[q]);
         lds_barrier();
+        // groups of ATT_CSUM chunks summed in order by 8 thread rows (group
+        // k of element i on thread row k % 8), then the group sums in order
+        // by 32 threads.  Slots past the last chunk add +0, which leaves every
+        // sum's bits unchanged (a sum of partials that start from +0 is never
+        // -0); the reads are unconditional, since reads under a per-slot
+        // condition each wait for LDS alone.
+        const int ngrp = (nch + ATT_CSUM - 1) / ATT_CSUM;
+        for (int gi = r0; gi < ngrp; gi += 8) {
+            float v[ATT_CSUM];
+#pragma unroll
+            for (int q = 0; q < ATT_CSUM; q++) {
+                const float x = vals[(gi * ATT_CSUM + q) * 32 + i];
+                v[q] = gi * ATT_CSUM + q < nch ? x : 0.0f;
+            }
+            float sg = 0.0f;
+#pragma unroll
+            for (int q = 0; q < ATT_CSUM; q++) sg += v[q];
+            gsum[gi * 32 + i] = sg;
+        }
+        lds_barrier();
         float r = 0.0f;
         if (t < 32) {
-            for (int k0 = 0; k0 < nch; k0 += 16) {                      // 16 reads in flight, adds in order
-                float v[16];
+            for (int g0 = 0; g0 < ngrp; g0 += 8) {
+                float v[8];
 #pragma unroll
-                for (int q = 0; q < 16; q++) v[q] = k0 + q < nch ? vals[(k0 + q) * 32 + t] : 0.0f;
+                for (int q = 0; q < 8; q++) {
+                    const float x = gsum[min(g0 + q, ATT_FUSED_MAXC / ATT_CSUM - 1) * 32 + t];
+                    v[q] = g0 + q < ngrp ? x : 0.0f;
+                }
 #pragma unroll
-                for (int q = 0; q < 16; q++)
-                    if (k0 + q < nch) r += v[q];
+                for (int q = 0; q < 8; q++) r += v[q];
             }
             if (bad) {
                 r = __builtin_nanf("");
@@ -1001,7 +1052,7 @@ __global__ void k_attn_clear(uint64_t *w, size_t n) {
 
 // Workspace: S [n_head][npos] f32 scores, Mc [n_head][nc] f32 chunk maxima,
 // Lc [n_head][nc] f64 chunk sums, P [n_head][nc][hd] f32 partials (three
-// passes); then the fused launch's words: T [n_head][nc][3], PT
+// passes); then the fused launch's words: T [n_head][nc][ATT_TW] (3 used), PT
 // [n_head][nc][hd], and epoch, error (one 64-bit word each).
 static size_t al256(size_t v) { return (v + 255) & ~(size_t)255; }
 struct AttnWs {
@@ -1015,7 +1066,7 @@ static AttnWs attn_ws(int n_head, int hd, int npos_max) {
     w.Lc = w.Mc + al256((size_t)n_head * nc * 4);
     w.P = w.Lc + al256((size_t)n_head * nc * 8);
     w.T = w.P + al256((size_t)n_head * nc * hd * 4);
-    w.PT = w.T + al256((size_t)n_head * nc * 3 * 8);
+    w.PT = w.T + al256((size_t)n_head * nc * ATT_TW * 8);
     w.misc = w.PT + al256((size_t)n_head * nc * hd * 8);
     w.total = w.misc + 256;
     return w;
