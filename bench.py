@@ -39,6 +39,16 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
+def cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown CPU"
+
+
 def physical_cores() -> int:
     seen = set()
     base = "/sys/devices/system/cpu"
@@ -135,7 +145,8 @@ def cpu_baseline(sets, seconds: float):
                 "sample": f"{len(times)} steps of the same up+down q4_0 GEMV pair (median), weights rotated over "
                           f"{len(host[0][1])} host copies; reference quants.c AVX2 dots built with README flags "
                           f"(-Ofast -march=x86-64-v3), pthread row split of model.c:59-65; "
-                          f"{ncores} physical cores, {threads} threads",
+                          f"{ncores} physical cores ({cpu_model()}), {threads} threads (the box's share; the "
+                          f"reference caps at 32)",
                 "ms_per_step": round(med * 1e3, 3)}
     finally:
         g4o.pool_stop()
@@ -261,9 +272,10 @@ def bench_decode(G, steps: int, cpu_seconds: float, want_cpu: bool):
             med = float(np.median(times))
             out["cpu_baseline"] = {"tok_per_s": round(1 / med, 2), "ms_per_token": round(med * 1e3, 2), "cores": threads,
                                    "kind": "reference",
-                                   "sample": f"{len(times)} decode steps at positions 8128..8191 of the same model "
-                                             "(weights and KV copied from the GPU); reference AVX2 dots incl. g4_dot_f16 "
-                                             "for scores; pthread row split (model.c:59-65), heads in parallel (model.c:706)"}
+                                   "sample": f"{len(times)} decode steps at positions {c['n_ctx'] - 64}..{c['n_ctx'] - 1} "
+                                             "of the same model (weights and KV copied from the GPU); reference AVX2 dots "
+                                             "incl. g4_dot_f16 for scores; pthread row split (model.c:59-65), heads in "
+                                             f"parallel (model.c:706); {cpu_model()}"}
             log(f"bench: cpu decode {out['cpu_baseline']['tok_per_s']} tok/s on {threads} threads")
     m.free()
     return out
@@ -277,7 +289,7 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--all-configs", action="store_true", help="also time every GEMV config (stderr + JSON)")
-    ap.add_argument("--decode-steps", type=int, default=64, help="decode steps timed at context ~8192 (0 = skip)")
+    ap.add_argument("--decode-steps", type=int, default=128, help="decode steps timed at context ~8192 (0 = skip)")
     ap.add_argument("--prefill", nargs="?", const="1,8,16,32,64,128,256,512", default=None, metavar="M,...",
                     help="also time config 3 (GEMV vs matrix-core crossover) at these token counts")
     ap.add_argument("--copy-calibration", action="store_true",

@@ -58,7 +58,7 @@ __device__ __forceinline__ void pro_issue(ProLoads &r, const GemvPro &p) {
 }
 
 template <int PRO, int S>
-__device__ void pro_finish(ProLoads &r, const GemvPro &p, uint8_t *lds, int nb) {
+__device__ void pro_finish(ProLoads &r, const GemvPro &p, uint8_t *lds, int nb, bool first = blockIdx.x == 0) {
     __shared__ double red[16];
     const int ng = p.n >> 2, bd = blockDim.x, t = threadIdx.x;
     if constexpr (PRO == PRO_NORM) {
@@ -74,7 +74,7 @@ __device__ void pro_finish(ProLoads &r, const GemvPro &p, uint8_t *lds, int nb) 
 #pragma unroll
                 for (int k = 0; k < 4; k++) r.v[s][k] = r.v[s][k] + r.d[s][k] * sc * r.wp[s][k];
         }
-        if (blockIdx.x == 0) {
+        if (first) {                                                 // one workgroup stores x
 #pragma unroll
             for (int s = 0; s < S; s++) {
                 const int gi = t + s * bd;

@@ -33,7 +33,10 @@
 // the one-launch and three-launch forms give identical bits.
 #include <algorithm>
 
+#include <type_traits>
+
 #include "formats.h"
+#include "gemv_p.h"
 #include "kernels.h"
 #include "steps.h"
 
@@ -45,6 +48,15 @@ constexpr int ATT_CSUM = 8;          // chunks per group in the combine's two-le
 // issued after the statistics hand-off
 #ifndef ATT_V_EARLY
 #define ATT_V_EARLY 16
+#endif
+#ifndef ATT_QKV_WAIT
+#define ATT_QKV_WAIT 1
+#endif
+#ifndef ATT_QKV_KLATE
+#define ATT_QKV_KLATE 0
+#endif
+#ifndef ATT_QKV_VFIRST
+#define ATT_QKV_VFIRST 0
 #endif
 #ifndef ATT_POLL_SLEEP
 #define ATT_POLL_SLEEP 1
@@ -142,6 +154,14 @@ struct AttnCtx {
     const unsigned *epoch;
     unsigned tag_mul, tag_add;
     unsigned *err;           // set when a poll gives up
+    // one launch with the q|k|v projection folded in (decode step): every
+    // workgroup computes qrows projection rows of W from the RMSNorm prologue
+    // `pro` and publishes them as tagged words QT [rows] (one 128-byte line
+    // per workgroup); the attention rows are then taken from QT
+    g4h_tensor W;
+    GemvPro pro;
+    uint64_t *QT;
+    int qrows;
 };
 
 __device__ __forceinline__ int npos_of(const AttnCtx &c) { return c.npos_dev ? *c.npos_dev : c.npos; }
@@ -212,6 +232,25 @@ struct PrepF16 {
     int nrow;
 };
 
+// decode step with the projection folded in: the rows' norm weights and RoPE
+// row here; their values come later from the projection's tagged words
+template <int GRP, int HD>
+__device__ __forceinline__ void prep_f16_issue_w(PrepF16<GRP> &st, const AttnCtx &c, int kvh, int p, bool pos_chunk) {
+    constexpr int hd = HD, epl = hd >> 6;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    st.nrow = GRP + (pos_chunk ? 2 : 0);
+    rope_load(st.cs, st.sn, c.a.rope, p, hd);
+#pragma unroll
+    for (int sl = 0; sl < PrepF16<GRP>::SL; sl++) {
+        const int r = wave + 4 * sl;
+        if (r < st.nrow) {
+            const float *w = r < GRP ? c.a.q_norm : r == GRP ? c.a.k_norm : nullptr;
+#pragma unroll
+            for (int e = 0; e < 4; e++) st.pr[sl].w[e] = e < epl && w ? w[lane * epl + e] : 1.0f;
+        }
+    }
+}
+
 template <int GRP, int HD>
 __device__ __forceinline__ void prep_f16_issue(PrepF16<GRP> &st, const AttnCtx &c, int kvh, int p, bool pos_chunk) {
     constexpr int hd = HD;
@@ -244,7 +283,7 @@ __device__ __forceinline__ void prep_f16_finish(const PrepF16<GRP> &st, const At
                                                 uint16_t *kpos, uint16_t *vpos) {
     constexpr int hd = HD, epl = hd >> 6;
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-    if (c.qkv) {
+    if (st.nrow > 0) {                                                  // rows to prepare (projection output)
 #pragma unroll
         for (int sl = 0; sl < PrepF16<GRP>::SL; sl++) {
             const int r = wave + 4 * sl;
@@ -808,8 +847,74 @@ __device__ __forceinline__ bool poll_words(const uint64_t *const (&src)[N], cons
     return true;
 }
 
+// the attention rows (queries, and the new key / value in the chunk of the
+// current position) from the projection's tagged words, for prep_f16_finish
 template <int GRP, int HD>
+__device__ __forceinline__ bool prep_f16_poll(PrepF16<GRP> &st, const AttnCtx &c, int kvh, uint32_t tag) {
+    constexpr int hd = HD, epl = hd >> 6;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, h0 = kvh * GRP;
+    bool ok = true;
+#pragma unroll
+    for (int sl = 0; sl < PrepF16<GRP>::SL; sl++) {
+        const int r = wave + 4 * sl;
+        if (r < st.nrow) {                                            // uniform over the wave
+            const int src_row = r < GRP ? h0 + r : r == GRP ? c.a.n_head + kvh : c.a.n_head + c.a.n_kv + kvh;
+            const uint64_t *src[4];
+            bool need[4];
+            uint32_t bits[4];
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                src[e] = c.QT + (size_t)src_row * hd + lane * epl + min(e, epl - 1);
+                need[e] = e < epl;
+            }
+            ok &= poll_words<4>(src, need, tag, bits);
+#pragma unroll
+            for (int e = 0; e < 4; e++) st.pr[sl].v[e] = e < epl ? __uint_as_float(bits[e]) : 0.0f;
+        }
+    }
+    return ok;
+}
+
+// The projection rows of this workgroup (QKV launches): rows L*qrows .. of W,
+// in passes of 4 waves x 64/LPR rows; a row's lanes, units and reduction are
+// those of k_gemv / k_gemv_p with the same LPR, so each row is bit-identical to
+// theirs.  The first two passes' weights are issued by qkv_issue (before the
+// K stream), later passes (small models only) after it.
+template <class FQ, int LPR, int UPL>
+struct QkvRows {
+    static constexpr int RPW = 64 / LPR;
+    typename FQ::Frag fa[UPL], fb[UPL];
+    int units;
+    __device__ __forceinline__ int64_t row_of(const AttnCtx &c, int L, int pass) const {
+        const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+        return (int64_t)L * c.qrows + pass * 4 * RPW + wave * RPW + lane / LPR;
+    }
+    __device__ __forceinline__ void load(typename FQ::Frag (&fr)[UPL], const AttnCtx &c, int L, int pass) const {
+        const int g = (threadIdx.x & 63) % LPR;
+        const int64_t row = min(row_of(c, L, pass), c.W.nrows - 1);
+#pragma unroll
+        for (int k = 0; k < UPL; k++) FQ::load(fr[k], c.W, row, min(g + k * LPR, units - 1));
+    }
+    __device__ __forceinline__ void finish(const typename FQ::Frag (&fr)[UPL], const AttnCtx &c, int L, int pass,
+                                           const uint8_t *act, uint32_t tag) const {
+        const int g = (threadIdx.x & 63) % LPR;
+        float acc = 0.0f;
+        const typename FQ::Act A(const_cast<uint8_t *>(act), (int)c.W.nb, 0);
+#pragma unroll
+        for (int k = 0; k < UPL; k++) {
+            const int u = g + k * LPR;
+            if (u < units) acc = FQ::accum(fr[k], A, u, acc);
+        }
+        acc = group_sum<LPR>(acc);
+        const int64_t row = row_of(c, L, pass);
+        if (g == 0 && row < c.W.nrows && row < (int64_t)(L + 1) * c.qrows) st_tag(&c.QT[row], __float_as_uint(acc), tag);
+    }
+};
+
+template <int GRP, int HD, class FQ = void, int LPR = 32, int UPL = 4>
 __global__ __launch_bounds__(256) void k_attn_fused_f16(AttnCtx c) {
+    constexpr bool QKV = !std::is_void<FQ>::value;
+    extern __shared__ __align__(16) uint8_t act_lds[];               // QKV: the projection's q8_0 activation
     __shared__ __align__(16) float4 qf[GRP][64];
     __shared__ __align__(16) uint16_t kpos[256], vpos[256];
     __shared__ float wm[4][GRP];
@@ -830,23 +935,63 @@ __global__ __launch_bounds__(256) void k_attn_fused_f16(AttnCtx c) {
     const int nch = (npos + ATT_CHUNK - 1) / ATT_CHUNK;
     const bool live = ch < nch;                                      // uniform over the workgroup
     if (t == 0) bad = 0;
+    const int j0 = ch * ATT_CHUNK + wave * 32, j = j0 + lane;      // lane < 32 owns position j
+    const bool pos_chunk = (QKV || c.qkv) && ch == p / ATT_CHUNK;
+    PrepF16<GRP> st;
+    uint4 kq[16], vq[16];
+    constexpr bool v_first = QKV && ATT_QKV_VFIRST;                   // V issued with K, before the projection poll
+    if constexpr (QKV) {
+        // the projection: prologue loads and the norm / RoPE rows, then its
+        // weights, then the K stream; the prologue arithmetic and the rows
+        // run while K streams, and the attention rows come back through QT
+        // (that poll completes behind the K rows, which the scores need next)
+        const int L = blockIdx.y * gridDim.x + blockIdx.x;
+        constexpr int S = 4;                                          // prologue groups of 4 per thread
+        ProLoads pr;
+        QkvRows<FQ, LPR, UPL> qr;
+        qr.units = (int)(c.W.nb * FQ::units_per_block);
+        const int np = (c.qrows + 4 * qr.RPW - 1) / (4 * qr.RPW);
+        if (live) prep_f16_issue_w<GRP, HD>(st, c, kvh, p, pos_chunk);
+        pro_issue<PRO_NORM, S>(pr, c.pro);
+        if (ATT_QKV_WAIT) wait_loads();                               // landed before the streams queue up
+        issue_barrier();
+        qr.load(qr.fa, c, L, 0);
+        qr.load(qr.fb, c, L, 1);                                      // unconditional: a load under a branch is waited for there
+        issue_order();
+        if (!ATT_QKV_KLATE) {
+            if (live) rows_load<HD>(kq, c.a.kc, c.a.n_kv, kvh, j0, npos);
+            if (v_first && live) rows_load<HD>(vq, c.a.vc, c.a.n_kv, kvh, j0, npos);
+            issue_order();
+        }
+        pro_finish<PRO_NORM, S>(pr, c.pro, act_lds, (int)c.W.nb, L == 0);
+        lds_barrier();
+        if (ATT_QKV_KLATE) {                                          // K (and V) behind the prologue arithmetic
+            if (live) rows_load<HD>(kq, c.a.kc, c.a.n_kv, kvh, j0, npos);
+            if (v_first && live) rows_load<HD>(vq, c.a.vc, c.a.n_kv, kvh, j0, npos);
+            issue_order();
+        }
+        qr.finish(qr.fa, c, L, 0, act_lds, tag);
+        if (np > 1) qr.finish(qr.fb, c, L, 1, act_lds, tag);
+        for (int pass = 2; pass < np; pass++) {                       // uniform; small models only
+            qr.load(qr.fa, c, L, pass);
+            qr.finish(qr.fa, c, L, pass, act_lds, tag);
+        }
+        if (live && !prep_f16_poll<GRP, HD>(st, c, kvh, tag)) bad = 1;
+    } else if (live) {
+        // the small loads first (landed before the streams start), then the
+        // wave's K rows
+        prep_f16_issue<GRP, HD>(st, c, kvh, p, pos_chunk);
+        wait_loads();
+        rows_load<HD>(kq, c.a.kc, c.a.n_kv, kvh, j0, npos);
+        issue_order();
+    }
     if (live) {
-        const int j0 = ch * ATT_CHUNK + wave * 32, j = j0 + lane;  // lane < 32 owns position j
-        const bool pos_chunk = c.qkv && ch == p / ATT_CHUNK;
         const bool mine = lane < 32;
         float s[GRP];
-        uint4 vq[16];
         {
-            // the small loads first (landed before the streams start), then
-            // the wave's K rows; each V row is issued once the K row it
-            // follows has been scored, so the scores start with the first K
-            // row and V streams behind K while the statistics proceed
-            PrepF16<GRP> st;
-            prep_f16_issue<GRP, HD>(st, c, kvh, p, pos_chunk);
-            wait_loads();
-            uint4 kq[16];
-            rows_load<HD>(kq, c.a.kc, c.a.n_kv, kvh, j0, npos);
-            issue_order();
+            // each V row is issued once the K row it follows has been scored,
+            // so the scores start with the first K row and V streams behind K
+            // while the statistics proceed
             prep_f16_finish<GRP, HD>(st, c, kvh, p, qf, kpos, vpos);
             lds_barrier();
             float qv[GRP][8];
@@ -856,7 +1001,7 @@ __global__ __launch_bounds__(256) void k_attn_fused_f16(AttnCtx c) {
             for (int i = 0; i < VGeo<HD>::NV; i++) {
                 new_row1<HD>(kq[i], nk, j0, i, pos_chunk ? p : -1);  // the new key, not the stale cache row
                 score_row<GRP, HD>(kq[i], qv, sc, i);
-                if (i < ATT_V_EARLY) vq[i] = row_load<HD>(c.a.vc, c.a.n_kv, kvh, j0, i, npos);
+                if (!v_first && i < ATT_V_EARLY) vq[i] = row_load<HD>(c.a.vc, c.a.n_kv, kvh, j0, i, npos);
                 issue_order();
             }
             lds_barrier();
@@ -934,7 +1079,8 @@ __global__ __launch_bounds__(256) void k_attn_fused_f16(AttnCtx c) {
         // issue order, so V rows issued before the poll would delay it); the
         // weights are formed while these rows land
 #pragma unroll
-        for (int i = ATT_V_EARLY; i < VGeo<HD>::NV; i++) vq[i] = row_load<HD>(c.a.vc, c.a.n_kv, kvh, j0, i, npos);
+        for (int i = ATT_V_EARLY; i < VGeo<HD>::NV; i++)
+            if (!v_first) vq[i] = row_load<HD>(c.a.vc, c.a.n_kv, kvh, j0, i, npos);
         issue_order();
         if (mine) {
 #pragma unroll
@@ -1141,6 +1287,65 @@ static hipError_t attn_go(AttnCtx c, int n_head, int n_kv, int npos_max, uint8_t
     hipLaunchKernelGGL((k_attn_v<KV, GRP, HD>), dim3(n_kv, nc), dim3(256), 0, s, c);
     hipLaunchKernelGGL(k_attn_combine, dim3(n_head), dim3(256), 0, s, c);
     return hipGetLastError();
+}
+
+// ------------------------------------------- projection + attention launch --
+template <int GRP, int HD, class FQ, int LPR, int UPL>
+static hipError_t attn_qkv_go(AttnCtx c, int npos_max, uint8_t *ws, hipStream_t s) {
+    const AttnWs w = attn_ws(c.a.n_head, HD, npos_max);
+    const int nc = (npos_max + ATT_CHUNK - 1) / ATT_CHUNK;
+    const int nwg = c.a.n_kv * nc;
+    c.nc = nc;
+    c.T = (uint64_t *)(ws + w.T);
+    c.PT = (uint64_t *)(ws + w.PT);
+    c.err = (unsigned *)(ws + w.misc + 8);
+    // rows per workgroup: a multiple of 16, so each workgroup's words fill whole 128-byte lines
+    c.qrows = (int)(((c.W.nrows + nwg - 1) / nwg + 15) / 16 * 16);
+    const size_t lds = ActQ8_0::bytes_per_token((int)c.W.nb) + kStageDump;
+    hipLaunchKernelGGL((k_attn_fused_f16<GRP, HD, FQ, LPR, UPL>), dim3(c.a.n_kv, nc), dim3(256), lds, s, c);
+    return hipGetLastError();
+}
+
+template <int GRP, int HD>
+static hipError_t attn_qkv_fmt(const AttnCtx &c, int lpr, int upl, int npos_max, uint8_t *ws, hipStream_t s) {
+#define G4_AQ(F, L, U) \
+    if (lpr == L && upl == U) return attn_qkv_go<GRP, HD, F, L, U>(c, npos_max, ws, s)
+    if (c.W.type == Q4_0) { G4_AQ(FQ4_0, 16, 2); G4_AQ(FQ4_0, 32, 4); G4_AQ(FQ4_0, 64, 2); }
+    if (c.W.type == Q8_0) { G4_AQ(FQ8_0, 16, 2); G4_AQ(FQ8_0, 32, 4); G4_AQ(FQ8_0, 64, 2); }
+#undef G4_AQ
+    return hipErrorInvalidValue;
+}
+
+bool attn_qkv_fits(const g4h_tensor &W, const QkvArgs &a, int npos_max) {
+    if (a.kv_type != F16 || !attn_fused_fits(F16, a.n_head, a.n_kv, a.hd, npos_max)) return false;
+    if (W.type != Q4_0 && W.type != Q8_0) return false;
+    if (W.ncols % 32 || W.ncols > 4 * 4 * 256 || W.nrows != (int64_t)(a.n_head + 2 * a.n_kv) * a.hd) return false;
+    const int grp = a.n_head / a.n_kv;
+    if (grp != 2 || (a.hd != 64 && a.hd != 256)) return false;
+    int lpr, upl;
+    gemv_shape(W.type, W.nb, &lpr, &upl);
+    const bool shape = (lpr == 16 && upl == 2) || (lpr == 32 && upl == 4) || (lpr == 64 && upl == 2);
+    return shape && W.nb * blck(W.type) / 32 <= (int64_t)lpr * upl;
+}
+
+hipError_t launch_attn_qkv(const g4h_tensor &W, const GemvPro &pro, const QkvArgs &a, const int *npos_dev, int npos_max,
+                           float *out, uint8_t *q8out, uint8_t *ws, uint64_t *qt, hipStream_t s, const AttnTag &tag) {
+    if (!attn_qkv_fits(W, a, npos_max) || pro.kind != PRO_NORM || pro.n != W.ncols || !qt) return hipErrorInvalidValue;
+    AttnCtx c{};
+    c.a = a;
+    c.npos_dev = npos_dev;
+    c.out = out;
+    c.q8out = q8out;
+    c.epoch = tag.epoch;
+    c.tag_mul = tag.mul;
+    c.tag_add = tag.add;
+    c.W = W;
+    c.pro = pro;
+    c.QT = qt;
+    int lpr, upl;
+    gemv_shape(W.type, W.nb, &lpr, &upl);
+    if (a.hd == 256) return attn_qkv_fmt<2, 256>(c, lpr, upl, npos_max, ws, s);
+    return attn_qkv_fmt<2, 64>(c, lpr, upl, npos_max, ws, s);
 }
 
 // q: prepared queries, or nullptr with `qkv` the raw q|k|v projection output

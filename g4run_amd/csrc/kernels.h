@@ -103,5 +103,14 @@ bool attn_fused_fits(int kv_type, int n_head, int n_kv, int hd, int npos_max);
 hipError_t launch_attn_decode(const float *q, const float *qkv, const QkvArgs &a, int npos, const int *npos_dev, int npos_max,
                               float *out, uint8_t *q8out, uint8_t *ws, hipStream_t s, const AttnTag *tag = nullptr);
 hipError_t launch_kv_store(int kv_type, const float *src, uint8_t *dst, int hd, int rows, size_t dst_stride, hipStream_t s);
+// The decode step's q|k|v projection W (q4_0 / q8_0) with its PRO_NORM
+// prologue computed inside the one-launch attention: every workgroup computes
+// a slice of the projection rows while its K stream is in flight and hands
+// them over as tagged words in qt ((n_head + 2 n_kv) * hd words, zeroed once,
+// 128-byte aligned).  Bit-identical to launch_gemv_p(W, PRO_NORM) followed by
+// launch_attn_decode on its output.
+bool attn_qkv_fits(const g4h_tensor &W, const QkvArgs &a, int npos_max);
+hipError_t launch_attn_qkv(const g4h_tensor &W, const GemvPro &pro, const QkvArgs &a, const int *npos_dev, int npos_max,
+                           float *out, uint8_t *q8out, uint8_t *ws, uint64_t *qt, hipStream_t s, const AttnTag &tag);
 
 }  // namespace g4

@@ -79,20 +79,26 @@ struct g4h_model {
     int *state = nullptr;            // token, pos, npos, steps taken
     float *x = nullptr, *x2 = nullptr, *xb = nullptr, *qkv = nullptr, *q = nullptr, *att = nullptr, *ff = nullptr, *logits = nullptr;
     uint8_t *act = nullptr, *ws = nullptr;
+    uint64_t *qt = nullptr;          // FUSE_QATT: tagged q|k|v projection rows
     size_t act_bytes = 0, ws_bytes = 0;
     std::vector<void *> allocs;
     int fuse = 0;                    // FUSE_* steps folded into the GEMVs
 };
 
-// Steps of the chain folded into the persistent GEMV family (gemv_p.h):
+// Steps of the chain folded into the persistent GEMV family (gemv_p.h) or
+// into the attention launch:
 //   FUSE_QKV   residual + attention RMSNorm + q8_0 in front of Wqkv
 //   FUSE_GU    residual + FFN RMSNorm + q8_0 in front of Wgu, GELU(gate)*up after it
 //   FUSE_DOWN  q8_0 of h in front of Wdown (with FUSE_GU)
 //   FUSE_HEAD  residual + output RMSNorm + q8_0 in front of the head
-enum { FUSE_QKV = 1, FUSE_GU = 2, FUSE_DOWN = 4, FUSE_HEAD = 8 };
-// measured on the BASELINE decode step (tok/s): none 684, QKV 693, QKV|GU 704,
-// QKV|GU|DOWN 690, all 689 -- the persistent GEMV streams a little slower than
-// the one-shot one, so only the folds that remove two launches pay
+//   FUSE_QATT  the Wqkv GEMV with its norm prologue inside the one-launch
+//              attention, its rows computed while the K stream is in flight
+enum { FUSE_QKV = 1, FUSE_GU = 2, FUSE_DOWN = 4, FUSE_HEAD = 8, FUSE_QATT = 16 };
+// measured on the BASELINE decode step (tok/s, 128 steps at ctx 8192): none
+// 842, QKV 856, GU 928, QKV|GU 955, QKV|GU|QATT 929.  In the QATT launch a
+// wave that has queued its K stream cannot run the projection until the
+// stream drains far enough to accept its loads, so the rows come out ~5.6 us
+// into the launch and the attention starts later than after a separate GEMV.
 static constexpr int kDefaultFuse = FUSE_QKV | FUSE_GU;
 
 static int model_alloc(g4h_model *m, void **p, size_t bytes) {
@@ -151,7 +157,7 @@ extern "C" int g4h_model_create(const g4h_model_config *cfg, uint64_t seed, g4h_
     g4h_model *m = new g4h_model();
     m->c = c;
     m->fuse = kDefaultFuse;
-    if (const char *e = getenv("G4H_DECODE_FUSE")) m->fuse = atoi(e) & 15;
+    if (const char *e = getenv("G4H_DECODE_FUSE")) m->fuse = atoi(e) & 31;
     const int E = c.n_embd, H = c.n_head, KV = c.n_kv, hd = c.head_dim, F = c.n_ff;
     const int qkv_rows = (H + 2 * KV) * hd, qd = H * hd;
     hipStream_t s = nullptr;
@@ -237,6 +243,8 @@ extern "C" int g4h_model_create(const g4h_model_config *cfg, uint64_t seed, g4h_
     if ((rc = model_alloc(m, (void **)&m->act, m->act_bytes))) return bail(rc);
     m->ws_bytes = g4h_attn_workspace_bytes(H, hd, c.n_ctx);
     if ((rc = model_alloc(m, (void **)&m->ws, m->ws_bytes))) return bail(rc);
+    if ((rc = model_alloc(m, (void **)&m->qt, (size_t)qkv_rows * 8))) return bail(rc);
+    if (hipMemset(m->qt, 0, (size_t)qkv_rows * 8) != hipSuccess) return bail(G4H_ERR_HIP);
     (void)wide;
     if (hipMemset(m->state, 0, 64) != hipSuccess) return bail(G4H_ERR_HIP);
     if (hipMemset(m->ws, 0, m->ws_bytes) != hipSuccess) return bail(G4H_ERR_HIP);   // no attention tag seen yet
@@ -312,17 +320,12 @@ extern "C" int g4h_forward_state(g4h_model *m, void *stream) {
         std::swap(x, xn);
         return e;
     };
-    M_HIP(launch_embed_norm(*m->head, token, x, sqrtf((float)E), (fz & FUSE_QKV) ? nullptr : norm_of(m, 0, G4H_N_ATTN),
+    const bool qkv_pro = fz & (FUSE_QKV | FUSE_QATT);     // the attention norm runs in a projection prologue
+    M_HIP(launch_embed_norm(*m->head, token, x, sqrtf((float)E), qkv_pro ? nullptr : norm_of(m, 0, G4H_N_ATTN),
                             c.rms_eps, m->act, s));
     for (int l = 0; l < c.n_layer; l++) {
         uint8_t *kc = m->kv + (size_t)(2 * l) * m->kv_layer_bytes, *vc = kc + m->kv_layer_bytes;
         const float *prev_post = l ? norm_of(m, l - 1, G4H_N_POST_FFW) : nullptr;
-        if (fz & FUSE_QKV) {
-            M_HIP(norm_gemv(*m->wqkv[l], l ? m->xb : nullptr, prev_post, norm_of(m, l, G4H_N_ATTN), m->qkv, false));
-        } else {
-            if (l) M_HIP(launch_norm_quant(x, m->xb, prev_post, norm_of(m, l, G4H_N_ATTN), c.rms_eps, E, m->act, s));
-            M_HIP(launch_gemv(*m->wqkv[l], m->act, ast, m->qkv, 1, s));
-        }
         QkvArgs qa;
         qa.n_head = H;
         qa.n_kv = KV;
@@ -335,7 +338,27 @@ extern "C" int g4h_forward_state(g4h_model *m, void *stream) {
         qa.vc = vc;
         qa.eps = c.rms_eps;
         const AttnTag tag{(const unsigned *)(m->state + 3), (unsigned)c.n_layer, (unsigned)l};
-        M_HIP(launch_attn_decode(nullptr, m->qkv, qa, 0, npos, c.n_ctx, m->att, m->act, m->ws, s, &tag));
+        if ((fz & FUSE_QATT) && attn_qkv_fits(*m->wqkv[l], qa, c.n_ctx)) {
+            GemvPro pro;
+            pro.kind = PRO_NORM;
+            pro.x = x;
+            pro.x_out = xn;
+            pro.delta = l ? m->xb : nullptr;
+            pro.w_post = prev_post;
+            pro.w_pre = norm_of(m, l, G4H_N_ATTN);
+            pro.eps = c.rms_eps;
+            pro.n = E;
+            M_HIP(launch_attn_qkv(*m->wqkv[l], pro, qa, npos, c.n_ctx, m->att, m->act, m->ws, m->qt, s, tag));
+            std::swap(x, xn);
+        } else {
+            if (qkv_pro) {
+                M_HIP(norm_gemv(*m->wqkv[l], l ? m->xb : nullptr, prev_post, norm_of(m, l, G4H_N_ATTN), m->qkv, false));
+            } else {
+                if (l) M_HIP(launch_norm_quant(x, m->xb, prev_post, norm_of(m, l, G4H_N_ATTN), c.rms_eps, E, m->act, s));
+                M_HIP(launch_gemv(*m->wqkv[l], m->act, ast, m->qkv, 1, s));
+            }
+            M_HIP(launch_attn_decode(nullptr, m->qkv, qa, 0, npos, c.n_ctx, m->att, m->act, m->ws, s, &tag));
+        }
         M_HIP(launch_gemv(*m->wo[l], m->act, ast, m->xb, 1, s));
         if (fz & FUSE_GU) {
             M_HIP(norm_gemv(*m->wgu[l], m->xb, norm_of(m, l, G4H_N_POST_ATTN), norm_of(m, l, G4H_N_FFN), nullptr, true));

@@ -73,19 +73,21 @@ def test_graph_replay_matches_eager(gpu):
         assert np.array_equal(m2.logits().view(np.uint32), eager[i][1].view(np.uint32))
 
 
-@pytest.mark.parametrize("kv_type", [1, 8], ids=["f16", "q8_0"])
-def test_fused_step_equals_unfused(gpu, monkeypatch, kv_type):
+@pytest.mark.parametrize("kv_type,fuse", [(1, None), (8, None), (1, "19"), (1, "31")],
+                         ids=["f16-default", "q8_0-default", "f16-qkv-in-attention", "f16-all"])
+def test_fused_step_equals_unfused(gpu, monkeypatch, kv_type, fuse):
     """The step with the residual norms folded into the Wqkv / Wgu prologues and
-    GELU into the Wgu epilogue (the default) gives the same tokens and logits,
-    bit for bit, as the step of separate norm / quantize / GELU kernels
-    (G4H_DECODE_FUSE=0)."""
+    GELU into the Wgu epilogue (the default), or with the Wqkv GEMV inside the
+    attention launch (G4H_DECODE_FUSE bit 16), gives the same tokens and
+    logits, bit for bit, as the step of separate norm / quantize / GELU
+    kernels (G4H_DECODE_FUSE=0)."""
     G = gpu
     runs = []
-    for fuse in (None, "0"):
-        if fuse is None:
+    for f in (fuse, "0"):
+        if f is None:
             monkeypatch.delenv("G4H_DECODE_FUSE", raising=False)
         else:
-            monkeypatch.setenv("G4H_DECODE_FUSE", fuse)
+            monkeypatch.setenv("G4H_DECODE_FUSE", f)
         m = G.Model(seed=21, kv_type=kv_type, **SMALL)
         m.fill_kv(seed=22)
         out, tok = [], 9
