@@ -28,10 +28,10 @@ sys.path.insert(0, ROOT)
 PEAK_HBM = 8000.0          # GB/s, MI355X published
 PEAK_INT8 = 5000.0         # dense int8 MFMA TOPS, MI355X published
 # HBM bytes per launch of the roofline kernel (q4_0 10240x2560 GEMV) from two
-# rocprofv3 --pmc passes: FETCH_SIZE 7277.1 KiB x 2.00 + WRITE_SIZE 64.0 KiB x
+# rocprofv3 --pmc passes: FETCH_SIZE 7281.1 KiB x 2.00 + WRITE_SIZE 64.0 KiB x
 # 1.00, scales from a 256 MiB device copy in the same runs
 # (profiles/gemv_q4_0_ffn_traffic.md).
-TRAFFIC_UP = int((7277.1 * 2.00 + 64.0 * 1.00) * 1024)
+TRAFFIC_UP = int((7281.1 * 2.00 + 64.0 * 1.00) * 1024)
 MALL = 256 << 20
 
 
