@@ -200,6 +200,7 @@ template <> struct StageOf<Q4_0> { using S = StageQ8_0; };
 template <> struct StageOf<Q2_K> { using S = StageQ8_K; };
 template <> struct StageOf<Q3_K> { using S = StageQ8_K; };
 template <> struct StageOf<Q4_K> { using S = StageQ8_K; };
+template <> struct StageOf<Q6_K> { using S = StageQ8_K; };
 
 // ------------------------------------------------------------------ q8_0 --
 struct FQ8_0 {
@@ -405,6 +406,61 @@ struct FQ3_K {
             s = dot4(((w[3] >> (2 * j)) & 0x03030303) | (((hb[3] >> sh) & 0x01010101) << 2), a.w, s);
             const int g = 8 * h + 2 * j + k;
             total += scale(f, g) * (s - 4 * bs[g]);
+        }
+        return total;
+    }
+    static __device__ __forceinline__ float accum(const Frag &f, const Act &A, int u, float acc) {
+        return __builtin_fmaf(A.d(u >> 2) * h2f(f.d), (float)isum(f, A, u), acc);
+    }
+    static constexpr int nsums = 1;
+    static __device__ __forceinline__ void sums(const Frag &f, const Act &A, int u, int *out) { out[0] = isum(f, A, u); }
+};
+
+// ------------------------------------------------------------------ q6_K --
+// Element e = 128h + 32j + l of a superblock (quants.c:379-400): low nibble of
+// ql[64h + 32(j&1) + l] (the high nibble for j >= 2), high 2 bits
+// (qh[32h + l] >> 2j) & 3, value (nibble | high<<4) - 32, int8 scale
+// scales[e/16].  Part p = 2h + k holds the 16 elements l = 16k..16k+15 of each
+// 32-element chunk j: 16 bytes of each ql half and 16 qh bytes, scales
+// 8h + k + 2j.  sum (q-32)*a = sum q*a - 32*bsum of the 16-element group.
+struct FQ6_K {
+    static constexpr int type = Q6_K;
+    using Act = ActQ8_K;
+    static constexpr int units_per_block = 4;
+    struct Frag { int4 l0, l1, hb; uint2 s; uint16_t d; };
+    static __device__ __forceinline__ void load(Frag &f, const g4h_tensor &W, int64_t row, int u) {
+        const size_t j = (size_t)row * W.nb + (u >> 2);
+        const int p = u & 3, h = p >> 1, k = p & 1;
+        const uint8_t *ql = W.qs + j * 128 + 64 * h + 16 * k;
+        f.l0 = ld4s(ql);
+        f.l1 = ld4s(ql + 32);
+        f.hb = ld4s(W.ex + j * 64 + 32 * h + 16 * k);
+        f.s = *(const uint2 *)(W.sc + j * 16 + 8 * h);
+        f.d = ((const uint16_t *)W.dd)[j];
+    }
+    static __device__ __forceinline__ int isum(const Frag &f, const Act &A, int u) {
+        const int sb = u >> 2, p = u & 3, h = p >> 1, k = p & 1;
+        const uint32_t L0[4] = {(uint32_t)f.l0.x, (uint32_t)f.l0.y, (uint32_t)f.l0.z, (uint32_t)f.l0.w};
+        const uint32_t L1[4] = {(uint32_t)f.l1.x, (uint32_t)f.l1.y, (uint32_t)f.l1.z, (uint32_t)f.l1.w};
+        const uint32_t H[4] = {(uint32_t)f.hb.x, (uint32_t)f.hb.y, (uint32_t)f.hb.z, (uint32_t)f.hb.w};
+        const int8_t *aq = A.q(sb) + 128 * h + 16 * k;
+        const int16_t *bs = A.bs(sb);
+        int total = 0;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int4 a = *(const int4 *)(aq + 32 * j);
+            const int lo = j >= 2 ? 4 : 0;
+            int q[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+                q[i] = (int)((((j & 1) ? L1[i] : L0[i]) >> lo) & 0x0F0F0F0F) | (int)(((H[i] >> (2 * j)) & 0x03030303) << 4);
+            int s = dot4(q[0], a.x, 0);
+            s = dot4(q[1], a.y, s);
+            s = dot4(q[2], a.z, s);
+            s = dot4(q[3], a.w, s);
+            const int sbyte = k + 2 * j;                               // scales[8h + k + 2j]
+            const int sc = (int)(int8_t)(((sbyte < 4 ? f.s.x : f.s.y) >> (8 * (sbyte & 3))) & 0xff);
+            total += sc * (s - 32 * bs[8 * h + 2 * j + k]);
         }
         return total;
     }

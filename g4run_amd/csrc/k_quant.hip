@@ -193,6 +193,13 @@ __global__ __launch_bounds__(256) void k_dequant(int type, const uint8_t *__rest
         q4k_sm(b + 4, ee >> 5, sc, mn);
         out = h2f(ld16(b)) * (float)sc * (float)q - h2f(ld16(b + 2)) * (float)mn;
     } break;
+    case Q6_K: {                                                   // quants.c:379-400
+        const uint8_t *b = row + (e >> 8) * 210;
+        const int ee = (int)(e & 255), h = ee >> 7, j = (ee >> 5) & 3, l = ee & 31;
+        const int byte = b[64 * h + 32 * (j & 1) + l];
+        const int q = ((j >= 2 ? byte >> 4 : byte & 15) | (((b[128 + 32 * h + l] >> (2 * j)) & 3) << 4)) - 32;
+        out = h2f(ld16(b + 208)) * (float)(int8_t)b[192 + (ee >> 4)] * (float)q;
+    } break;
     case F16: out = h2f(ld16(row + 2 * e)); break;
     default: out = ((const float *)row)[e]; break;
     }
@@ -219,6 +226,7 @@ __global__ __launch_bounds__(256) void k_repack(g4h_tensor t, uint8_t *__restric
     case Q4_K: mv(t.qs + i * 144, 0, 144); break;
     case Q2_K: mv(t.sc + i * 16, 0, 16); mv(t.qs + i * 64, 16, 64); mv(t.ex + i * 4, 80, 4); break;
     case Q3_K: mv(t.ex + i * 32, 0, 32); mv(t.qs + i * 64, 32, 64); mv(t.sc + i * 12, 96, 12); mv(t.dd + i * 2, 108, 2); break;
+    case Q6_K: mv(t.qs + i * 128, 0, 128); mv(t.ex + i * 64, 128, 64); mv(t.sc + i * 16, 192, 16); mv(t.dd + i * 2, 208, 2); break;
     default: break;
     }
 }
@@ -255,6 +263,13 @@ template <> __device__ void raw_frag<FQ3_K>(FQ3_K::Frag &f, const uint8_t *row, 
     const int p = u & 3;
     f.hm = ldu128(b + 16 * (p & 1)); f.q = ldu128(b + 32 + 16 * p);
     f.s0 = ldu32(b + 96); f.s1 = ldu32(b + 100); f.s2 = ldu32(b + 104); f.d = ld16(b + 108);
+}
+
+template <> __device__ void raw_frag<FQ6_K>(FQ6_K::Frag &f, const uint8_t *row, int u) {
+    const uint8_t *b = row + (size_t)(u >> 2) * 210;
+    const int p = u & 3, h = p >> 1, k = p & 1;
+    f.l0 = ldu128(b + 64 * h + 16 * k); f.l1 = ldu128(b + 64 * h + 32 + 16 * k); f.hb = ldu128(b + 128 + 32 * h + 16 * k);
+    f.s = make_uint2((uint32_t)ldu32(b + 192 + 8 * h), (uint32_t)ldu32(b + 196 + 8 * h)); f.d = ld16(b + 208);
 }
 
 template <class F>
@@ -326,6 +341,7 @@ hipError_t launch_vec_dot_raw(int wtype, const uint8_t *w, size_t ws, const uint
     case Q4_K: return vd_go<FQ4_K>(w, ws, a, n, rows, out, s);
     case Q3_K: return vd_go<FQ3_K>(w, ws, a, n, rows, out, s);
     case Q2_K: return vd_go<FQ2_K>(w, ws, a, n, rows, out, s);
+    case Q6_K: return vd_go<FQ6_K>(w, ws, a, n, rows, out, s);
     default: return hipErrorInvalidValue;
     }
 }

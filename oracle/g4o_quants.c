@@ -18,7 +18,7 @@ int g4o_type_blck(int t) {
     switch (t) {
     case G4O_F32: case G4O_F16: return 1;
     case G4O_Q4_0: case G4O_Q8_0: return 32;
-    case G4O_Q2_K: case G4O_Q3_K: case G4O_Q4_K: case G4O_Q8_K: return 256;
+    case G4O_Q2_K: case G4O_Q3_K: case G4O_Q4_K: case G4O_Q6_K: case G4O_Q8_K: return 256;
     default: return 0;
     }
 }
@@ -30,6 +30,7 @@ size_t g4o_type_size(int t) {
     case G4O_Q8_0: return sizeof(g4o_q8_0);
     case G4O_Q2_K: return sizeof(g4o_q2_K);
     case G4O_Q3_K: return sizeof(g4o_q3_K);
+    case G4O_Q6_K: return sizeof(g4o_q6_K);
     case G4O_Q4_K: return sizeof(g4o_q4_K);
     case G4O_Q8_K: return sizeof(g4o_q8_K);
     default: return 0;
@@ -214,6 +215,16 @@ static inline int q3k_q(const g4o_q3_K *b, int e) {
     int hb = (b->hmask[l] >> (4 * h + j)) & 1;
     return lo - (hb ? 0 : 4);
 }
+/* element e of a q6_K superblock: signed value -32..31 (quants.c:379-400):
+ * e = 128h + 32j + l, low nibble of ql[64h + 32(j&1) + l] (high nibble for
+ * j >= 2), high 2 bits (qh[32h + l] >> 2j) & 3; its scale is scales[e/16]. */
+static inline int q6k_q(const g4o_q6_K *b, int e) {
+    int h = e >> 7, j = (e >> 5) & 3, l = e & 31;
+    uint8_t byte = b->ql[64 * h + 32 * (j & 1) + l];
+    int lo = j >= 2 ? (byte >> 4) : (byte & 15);
+    int hi = (b->qh[32 * h + l] >> (2 * j)) & 3;
+    return (lo | (hi << 4)) - 32;
+}
 /* element e of a q4_K superblock: 0..15 and sub-block e/32 (quants.c:479-495). */
 static inline int q4k_q(const g4o_q4_K *b, int e) {
     int p = e >> 6, hi = (e >> 5) & 1, l = e & 31;
@@ -280,6 +291,14 @@ int g4o_dequant_row(int type, const void *vx, float *y, int64_t n) {
         }
         return 0;
     }
+    case G4O_Q6_K: {                                       /* quants.c:379-400: (d*sc)*q */
+        const g4o_q6_K *x = vx;
+        for (int64_t b = 0; b < n / 256; b++) {
+            float d = g4o_fp16_to_fp32(x[b].d);
+            for (int e = 0; e < 256; e++) y[256 * b + e] = d * x[b].scales[e >> 4] * q6k_q(&x[b], e);
+        }
+        return 0;
+    }
     default: return -1;
     }
 }
@@ -323,12 +342,19 @@ static void sums_q4_K(const g4o_q4_K *w, const g4o_q8_K *a, int32_t *isum, int32
     *isum = is; *msum = ms;
 }
 
+static int32_t sum_q6_K(const g4o_q6_K *w, const g4o_q8_K *a) {
+    int32_t s = 0;
+    for (int e = 0; e < 256; e++) s += w->scales[e >> 4] * q6k_q(w, e) * a->qs[e];
+    return s;
+}
+
 void g4o_block_sums(int type, const void *w, const void *a, int64_t n, int32_t *out) {
     switch (type) {
     case G4O_Q8_0: for (int64_t b = 0; b < n / 32; b++) out[b] = sum_q8_0((const g4o_q8_0 *)w + b, (const g4o_q8_0 *)a + b); break;
     case G4O_Q4_0: for (int64_t b = 0; b < n / 32; b++) out[b] = sum_q4_0((const g4o_q4_0 *)w + b, (const g4o_q8_0 *)a + b); break;
     case G4O_Q2_K: for (int64_t b = 0; b < n / 256; b++) sums_q2_K((const g4o_q2_K *)w + b, (const g4o_q8_K *)a + b, &out[2 * b], &out[2 * b + 1]); break;
     case G4O_Q3_K: for (int64_t b = 0; b < n / 256; b++) out[b] = sum_q3_K((const g4o_q3_K *)w + b, (const g4o_q8_K *)a + b); break;
+    case G4O_Q6_K: for (int64_t b = 0; b < n / 256; b++) out[b] = sum_q6_K((const g4o_q6_K *)w + b, (const g4o_q8_K *)a + b); break;
     case G4O_Q4_K: for (int64_t b = 0; b < n / 256; b++) sums_q4_K((const g4o_q4_K *)w + b, (const g4o_q8_K *)a + b, &out[2 * b], &out[2 * b + 1]); break;
     default: break;
     }
@@ -361,8 +387,8 @@ float g4o_dot_ref(int type, const void *vw, const void *va, int64_t n) {
         }
         return acc;
     }
-    case G4O_Q3_K: case G4O_Q4_K: {
-        /* quants.c:657-711 / 713-762: 8 int32 lanes (element e -> lane e%8)
+    case G4O_Q3_K: case G4O_Q4_K: case G4O_Q6_K: {
+        /* quants.c:657-711 / 713-762 / 582-622: 8 int32 lanes (element e -> lane e%8)
          * carry the scale-weighted sums of one superblock; each lane is scaled
          * into an 8-float accumulator; the lanes are summed at the end. */
         float sums[8] = {0};
@@ -374,6 +400,10 @@ float g4o_dot_ref(int type, const void *vw, const void *va, int64_t n) {
                 const g4o_q3_K *w = (const g4o_q3_K *)vw + b; const g4o_q8_K *a = (const g4o_q8_K *)va + b;
                 int sc[16]; q3k_scales(w->scales, sc);
                 for (int e = 0; e < 256; e++) lane[e & 7] += sc[e >> 4] * (q3k_q(w, e) * a->qs[e]);
+                d = g4o_fp16_to_fp32(w->d) * a->d;
+            } else if (type == G4O_Q6_K) {
+                const g4o_q6_K *w = (const g4o_q6_K *)vw + b; const g4o_q8_K *a = (const g4o_q8_K *)va + b;
+                for (int e = 0; e < 256; e++) lane[e & 7] += w->scales[e >> 4] * (q6k_q(w, e) * a->qs[e]);
                 d = g4o_fp16_to_fp32(w->d) * a->d;
             } else {
                 const g4o_q4_K *w = (const g4o_q4_K *)vw + b; const g4o_q8_K *a = (const g4o_q8_K *)va + b;
@@ -466,6 +496,18 @@ static float dot_q3_K_avx2(const g4o_q3_K *w, const g4o_q8_K *a, int64_t nb) {
     }
     return hsum8(acc);
 }
+/* q6_K (quants.c:1028-1094): lane i = bytes 4i..4i+3 of every 32-element
+ * chunk, scale-weighted (q6-32)*q8 sums, one FMA per superblock. */
+static float dot_q6_K_avx2(const g4o_q6_K *w, const g4o_q8_K *a, int64_t nb) {
+    float acc[8] = {0};
+    for (int64_t b = 0; b < nb; b++) {
+        const float d = a[b].d * g4o_fp16_to_fp32(w[b].d);
+        int32_t lane[8] = {0};
+        for (int e = 0; e < 256; e++) lane[(e & 31) >> 2] += w[b].scales[e >> 4] * q6k_q(&w[b], e) * a[b].qs[e];
+        for (int i = 0; i < 8; i++) acc[i] = fmaf(d, (float)lane[i], acc[i]);
+    }
+    return hsum8(acc);
+}
 /* q4_K (quants.c:1213-1259): mins go to a separate 4-lane accumulator
  * (lane i = mins 2i,2i+1 times bsum pairs), folded 0+2,1+3 then added. */
 static float dot_q4_K_avx2(const g4o_q4_K *w, const g4o_q8_K *a, int64_t nb) {
@@ -496,6 +538,7 @@ float g4o_dot(int type, const void *w, const void *a, int64_t n) {
     case G4O_Q2_K: return dot_q2_K_avx2(w, a, n / 256);
     case G4O_Q3_K: return dot_q3_K_avx2(w, a, n / 256);
     case G4O_Q4_K: return dot_q4_K_avx2(w, a, n / 256);
+    case G4O_Q6_K: return dot_q6_K_avx2(w, a, n / 256);
     default: return NAN;
     }
 }

@@ -26,14 +26,14 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(os.path.dirname(HERE))
 REF = os.path.join(ROOT, "oracle", "_ref", "libg4ref.so")
 
-Q4_0, Q8_0, Q2_K, Q3_K, Q4_K, Q8_K = 2, 8, 10, 11, 12, 15
-BLCK = {Q4_0: 32, Q8_0: 32, Q2_K: 256, Q3_K: 256, Q4_K: 256, Q8_K: 256}
-SIZE = {Q4_0: 18, Q8_0: 34, Q2_K: 84, Q3_K: 110, Q4_K: 144, Q8_K: 292}
-ACT = {Q4_0: Q8_0, Q8_0: Q8_0, Q2_K: Q8_K, Q3_K: Q8_K, Q4_K: Q8_K}
-NAME = {Q4_0: "q4_0", Q8_0: "q8_0", Q2_K: "q2_K", Q3_K: "q3_K", Q4_K: "q4_K", Q8_K: "q8_K"}
-DOT = {Q4_0: "q4_0_q8_0", Q8_0: "q8_0_q8_0", Q2_K: "q2_K_q8_K", Q3_K: "q3_K_q8_K", Q4_K: "q4_K_q8_K"}
+Q4_0, Q8_0, Q2_K, Q3_K, Q4_K, Q6_K, Q8_K = 2, 8, 10, 11, 12, 14, 15
+BLCK = {Q4_0: 32, Q8_0: 32, Q2_K: 256, Q3_K: 256, Q4_K: 256, Q6_K: 256, Q8_K: 256}
+SIZE = {Q4_0: 18, Q8_0: 34, Q2_K: 84, Q3_K: 110, Q4_K: 144, Q6_K: 210, Q8_K: 292}
+ACT = {Q4_0: Q8_0, Q8_0: Q8_0, Q2_K: Q8_K, Q3_K: Q8_K, Q4_K: Q8_K, Q6_K: Q8_K}
+NAME = {Q4_0: "q4_0", Q8_0: "q8_0", Q2_K: "q2_K", Q3_K: "q3_K", Q4_K: "q4_K", Q6_K: "q6_K", Q8_K: "q8_K"}
+DOT = {Q4_0: "q4_0_q8_0", Q8_0: "q8_0_q8_0", Q2_K: "q2_K_q8_K", Q3_K: "q3_K_q8_K", Q4_K: "q4_K_q8_K", Q6_K: "q6_K_q8_K"}
 # fp16 scale fields (d, dmin) inside a weight block and the f32 d of q8_K
-SCALES = {Q8_0: (0,), Q4_0: (0,), Q2_K: (80, 82), Q3_K: (108,), Q4_K: (0, 2)}
+SCALES = {Q8_0: (0,), Q4_0: (0,), Q2_K: (80, 82), Q3_K: (108,), Q4_K: (0, 2), Q6_K: (208,)}
 
 vp = C.c_void_p
 
@@ -120,7 +120,7 @@ def unit_sums(R, qt, w_row, a_row, n):
             ab[0:4] = np.frombuffer(np.float32(1.0).tobytes(), np.uint8)
         one = np.frombuffer(np.float16(1.0).tobytes(), np.uint8)
         zero = np.zeros(2, np.uint8)
-        if qt in (Q8_0, Q4_0, Q3_K):
+        if qt in (Q8_0, Q4_0, Q3_K, Q6_K):
             wb[SCALES[qt][0]:SCALES[qt][0] + 2] = one
             out[b] = int(f(ptr(wb), ptr(ab), BLCK[qt]))
         else:
@@ -132,7 +132,9 @@ def unit_sums(R, qt, w_row, a_row, n):
     return out
 
 
-def main():
+def main(only=None):
+    """Writes every fixture, or with format names as arguments (e.g. `q6_K`)
+    only those formats' dot fixtures."""
     if not os.path.exists(REF):
         sys.exit(f"{REF} missing: run `make -C oracle ref` first")
     R = load_ref()
@@ -140,11 +142,15 @@ def main():
 
     # activation quantizers
     for qt in (Q8_0, Q8_K, Q4_0):
+        if only:
+            break
         x = quant_cases(1024)
         np.savez_compressed(os.path.join(HERE, f"quant_{NAME[qt]}.npz"), x=x, y=quant(R, qt, x), flags=flags)
 
     # dots, x4, dequant, per-block sums
-    for qt in (Q8_0, Q4_0, Q2_K, Q3_K, Q4_K):
+    for qt in (Q8_0, Q4_0, Q2_K, Q3_K, Q4_K, Q6_K):
+        if only and NAME[qt] not in only:
+            continue
         rng = np.random.default_rng(100 + qt)
         n = 2048 if BLCK[qt] == 256 else 1024
         rows, nb_tok = 16, 4
@@ -170,6 +176,9 @@ def main():
         np.savez_compressed(os.path.join(HERE, f"dot_{NAME[qt]}.npz"), w=w, x=x, a=a, dot=dot, dot_ref=dot_ref,
                             dot_x4=dot_x4, deq=deq, sums=sums, n=n, flags=flags)
 
+    if only:
+        print("fixtures written to", HERE)
+        return
     f16 = np.ctypeslib.as_array((C.c_float * 65536).in_dll(R, "g4_fp16_to_fp32_table")).copy()
     gelu = np.ctypeslib.as_array((C.c_uint16 * 65536).in_dll(R, "g4_gelu_fp16_table")).copy()
     np.savez_compressed(os.path.join(HERE, "tables.npz"), fp16_to_fp32=f16.view(np.uint32), gelu=gelu, flags=flags)
@@ -177,4 +186,4 @@ def main():
 
 
 if __name__ == "__main__":
-    main()
+    main(sys.argv[1:] or None)

@@ -88,7 +88,7 @@ def test_quantize_q8_K_closed_form(oracle):
 
 
 # ---------------------------------------------------- dots / dequant / sums
-FMTS = [("q8_0", 8), ("q4_0", 2), ("q2_K", 10), ("q3_K", 11), ("q4_K", 12)]
+FMTS = [("q8_0", 8), ("q4_0", 2), ("q2_K", 10), ("q3_K", 11), ("q4_K", 12), ("q6_K", 14)]
 
 
 @pytest.mark.parametrize("name,qt", FMTS)
@@ -139,6 +139,8 @@ def test_block_sums_brute_force(oracle, name, qt):
         wv[:, :, 0:2] = one
     elif qt == 11:
         wv[:, :, 108:110] = one
+    elif qt == 14:
+        wv[:, :, 208:210] = one
     elif qt == 10:
         wv[:, :, 80:82] = one; wv[:, :, 82:84] = zero
     else:
