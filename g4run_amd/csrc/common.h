@@ -8,17 +8,17 @@
 
 namespace g4 {
 
-enum : int { F32 = 0, F16 = 1, Q4_0 = 2, Q8_0 = 8, Q2_K = 10, Q3_K = 11, Q4_K = 12, Q6_K = 14, Q8_K = 15 };
+enum : int { F32 = 0, F16 = 1, Q4_0 = 2, Q8_0 = 8, Q2_K = 10, Q3_K = 11, Q4_K = 12, Q5_K = 13, Q6_K = 14, Q8_K = 15 };
 
 constexpr int WAVE = 64;
 
 // GGUF block geometry (g4run.h:107-118, gguf.c:11-25)
 __host__ __device__ constexpr int blck(int t) {
-    return (t == Q4_0 || t == Q8_0) ? 32 : (t == Q2_K || t == Q3_K || t == Q4_K || t == Q6_K || t == Q8_K) ? 256
+    return (t == Q4_0 || t == Q8_0) ? 32 : (t == Q2_K || t == Q3_K || t == Q4_K || t == Q5_K || t == Q6_K || t == Q8_K) ? 256
          : (t == F32 || t == F16) ? 1 : 0;
 }
 __host__ __device__ constexpr int bsize(int t) {
-    return t == Q4_0 ? 18 : t == Q8_0 ? 34 : t == Q2_K ? 84 : t == Q3_K ? 110 : t == Q4_K ? 144 : t == Q6_K ? 210 : t == Q8_K ? 292
+    return t == Q4_0 ? 18 : t == Q8_0 ? 34 : t == Q2_K ? 84 : t == Q3_K ? 110 : t == Q4_K ? 144 : t == Q5_K ? 176 : t == Q6_K ? 210 : t == Q8_K ? 292
          : t == F16 ? 2 : t == F32 ? 4 : 0;
 }
 
@@ -173,6 +173,7 @@ __device__ __forceinline__ void issue_order() {
 //   q8_0: qs plane  [r][j][32] int8          sc plane [r][j] fp16 d
 //   q4_0: qs plane  [r][j][16] nibbles       sc plane [r][j] fp16 d
 //   q4_K: qs plane  [r][j][144] the GGUF block unchanged (16-B header + qs)
+//   q5_K: qs plane  [r][j][176] the GGUF block unchanged (16-B header, qh, qs)
 //   q2_K: qs plane  [r][j][64] 2-bit quants  sc plane [r][j][16] scale|min
 //         ex plane  [r][j] {fp16 d, fp16 dmin}
 //   q3_K: qs plane  [r][j][64] low bits + [r][j][32] hmask in ex plane,

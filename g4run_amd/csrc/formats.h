@@ -200,6 +200,7 @@ template <> struct StageOf<Q4_0> { using S = StageQ8_0; };
 template <> struct StageOf<Q2_K> { using S = StageQ8_K; };
 template <> struct StageOf<Q3_K> { using S = StageQ8_K; };
 template <> struct StageOf<Q4_K> { using S = StageQ8_K; };
+template <> struct StageOf<Q5_K> { using S = StageQ8_K; };
 template <> struct StageOf<Q6_K> { using S = StageQ8_K; };
 
 // ------------------------------------------------------------------ q8_0 --
@@ -304,6 +305,67 @@ struct FQ4_K {
     }
     // superblock value d_a*(d_w*isum - dmin_w*msum) (quants.c:744-758), spread
     // over the four parts
+    static __device__ __forceinline__ float accum(const Frag &f, const Act &A, int u, float acc) {
+        int is, ms; isums(f, A, u, is, ms);
+        const float da = A.d(u >> 2);
+        const uint32_t dd = (uint32_t)f.h.x;
+        acc = __builtin_fmaf(da * h2f((uint16_t)(dd & 0xffff)), (float)is, acc);
+        return __builtin_fmaf(-da * h2f((uint16_t)(dd >> 16)), (float)ms, acc);
+    }
+    static constexpr int nsums = 2;
+    static __device__ __forceinline__ void sums(const Frag &f, const Act &A, int u, int *out) { isums(f, A, u, out[0], out[1]); }
+};
+
+// ------------------------------------------------------------------ q5_K --
+// The q4_K block with a fifth bit per element (quants.c:497-515, 764-818):
+// 16-byte header (d, dmin, packed 6-bit scales / mins), qh[32] at 16, qs[128]
+// at 48.  Element e = 32c + l (chunk c = 0..7): nibble of qs[32(c/2) + l]
+// (low for even c) plus 16 * bit c of qh[l]; scale / min of sub-block c.
+// Part p covers chunks 2p, 2p+1 (the 32 qs bytes 32p..32p+31 and all 32 qh
+// bytes, which the four parts of a superblock share).
+struct FQ5_K {
+    static constexpr int type = Q5_K;
+    using Act = ActQ8_K;
+    static constexpr int units_per_block = 4;
+    struct Frag { int4 h, q0, q1, hb0, hb1; };
+    static __device__ __forceinline__ void load(Frag &f, const g4h_tensor &W, int64_t row, int u) {
+        const uint8_t *b = W.qs + ((size_t)row * W.nb + (u >> 2)) * 176;
+        const int p = u & 3;
+        f.h = ld4(b);
+        f.hb0 = ld4(b + 16); f.hb1 = ld4(b + 32);
+        f.q0 = ld4(b + 48 + 32 * p); f.q1 = ld4(b + 64 + 32 * p);
+    }
+    static __device__ __forceinline__ void isums(const Frag &f, const Act &A, int u, int &is, int &ms) {
+        const int sb = u >> 2, p = u & 3, m = 0x0F0F0F0F;
+        const int4 *a = (const int4 *)(A.q(sb) + 64 * p);
+        const int4 l0 = a[0], l1 = a[1], h0 = a[2], h1 = a[3];
+        const uint32_t w[8] = {(uint32_t)f.q0.x, (uint32_t)f.q0.y, (uint32_t)f.q0.z, (uint32_t)f.q0.w,
+                               (uint32_t)f.q1.x, (uint32_t)f.q1.y, (uint32_t)f.q1.z, (uint32_t)f.q1.w};
+        const uint32_t hb[8] = {(uint32_t)f.hb0.x, (uint32_t)f.hb0.y, (uint32_t)f.hb0.z, (uint32_t)f.hb0.w,
+                                (uint32_t)f.hb1.x, (uint32_t)f.hb1.y, (uint32_t)f.hb1.z, (uint32_t)f.hb1.w};
+        const int c0 = 2 * p, c1 = 2 * p + 1;
+        int lo[8], hi[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            lo[i] = (int)((w[i] & m) | (((hb[i] >> c0) & 0x01010101) << 4));
+            hi[i] = (int)(((w[i] >> 4) & m) | (((hb[i] >> c1) & 0x01010101) << 4));
+        }
+        int sl = dot4(lo[0], l0.x, 0);
+        sl = dot4(lo[1], l0.y, sl); sl = dot4(lo[2], l0.z, sl); sl = dot4(lo[3], l0.w, sl);
+        sl = dot4(lo[4], l1.x, sl); sl = dot4(lo[5], l1.y, sl); sl = dot4(lo[6], l1.z, sl); sl = dot4(lo[7], l1.w, sl);
+        int sh = dot4(hi[0], h0.x, 0);
+        sh = dot4(hi[1], h0.y, sh); sh = dot4(hi[2], h0.z, sh); sh = dot4(hi[3], h0.w, sh);
+        sh = dot4(hi[4], h1.x, sh); sh = dot4(hi[5], h1.y, sh); sh = dot4(hi[6], h1.z, sh); sh = dot4(hi[7], h1.w, sh);
+        FQ4_K::Frag hf;
+        hf.h = f.h;
+        int sc0, m0, sc1, m1;
+        FQ4_K::scale_min(hf, c0, sc0, m0);
+        FQ4_K::scale_min(hf, c1, sc1, m1);
+        const int16_t *bs = A.bs(sb) + 4 * p;
+        is = sc0 * sl + sc1 * sh;
+        ms = m0 * (bs[0] + bs[1]) + m1 * (bs[2] + bs[3]);
+    }
+    // superblock value d_a*(d_w*isum - dmin_w*msum), spread over the four parts
     static __device__ __forceinline__ float accum(const Frag &f, const Act &A, int u, float acc) {
         int is, ms; isums(f, A, u, is, ms);
         const float da = A.d(u >> 2);

@@ -8,6 +8,7 @@ hipError_t launch_gemv_q8_0(const g4h_tensor &, const uint8_t *, size_t, const f
 hipError_t launch_gemv_q4_0(const g4h_tensor &, const uint8_t *, size_t, const float *, float *, int, hipStream_t, int, int);
 hipError_t launch_gemv_q4_K(const g4h_tensor &, const uint8_t *, size_t, const float *, float *, int, hipStream_t, int, int);
 hipError_t launch_gemv_q3_K(const g4h_tensor &, const uint8_t *, size_t, const float *, float *, int, hipStream_t, int, int);
+hipError_t launch_gemv_q5_K(const g4h_tensor &, const uint8_t *, size_t, const float *, float *, int, hipStream_t, int, int);
 hipError_t launch_gemv_q6_K(const g4h_tensor &, const uint8_t *, size_t, const float *, float *, int, hipStream_t, int, int);
 hipError_t launch_gemv_q2_K(const g4h_tensor &, const uint8_t *, size_t, const float *, float *, int, hipStream_t, int, int);
 
@@ -72,6 +73,7 @@ static hipError_t gemv_dispatch(const g4h_tensor &W, const uint8_t *act, size_t 
     case Q4_0: return launch_gemv_q4_0(W, act, stride, x, Y, nb, s, lpr, upl);
     case Q4_K: return launch_gemv_q4_K(W, act, stride, x, Y, nb, s, lpr, upl);
     case Q3_K: return launch_gemv_q3_K(W, act, stride, x, Y, nb, s, lpr, upl);
+    case Q5_K: return launch_gemv_q5_K(W, act, stride, x, Y, nb, s, lpr, upl);
     case Q6_K: return launch_gemv_q6_K(W, act, stride, x, Y, nb, s, lpr, upl);
     case Q2_K: return launch_gemv_q2_K(W, act, stride, x, Y, nb, s, lpr, upl);
     default: return hipErrorInvalidValue;
@@ -165,12 +167,13 @@ hipError_t launch_block_sums(const g4h_tensor &W, const uint8_t *act, size_t str
     case Q4_0: return bs_go<FQ4_0>(W, act, stride, tok, out, s);
     case Q4_K: return bs_go<FQ4_K>(W, act, stride, tok, out, s);
     case Q3_K: return bs_go<FQ3_K>(W, act, stride, tok, out, s);
+    case Q5_K: return bs_go<FQ5_K>(W, act, stride, tok, out, s);
     case Q6_K: return bs_go<FQ6_K>(W, act, stride, tok, out, s);
     case Q2_K: return bs_go<FQ2_K>(W, act, stride, tok, out, s);
     default: return hipErrorInvalidValue;
     }
 }
 
-int block_sums_per_block(int type) { return (type == Q2_K || type == Q4_K) ? 2 : 1; }
+int block_sums_per_block(int type) { return (type == Q2_K || type == Q4_K || type == Q5_K) ? 2 : 1; }
 
 }  // namespace g4

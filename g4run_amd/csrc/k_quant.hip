@@ -193,6 +193,15 @@ __global__ __launch_bounds__(256) void k_dequant(int type, const uint8_t *__rest
         q4k_sm(b + 4, ee >> 5, sc, mn);
         out = h2f(ld16(b)) * (float)sc * (float)q - h2f(ld16(b + 2)) * (float)mn;
     } break;
+    case Q5_K: {                                                   // quants.c:497-515
+        const uint8_t *b = row + (e >> 8) * 176;
+        const int ee = (int)(e & 255), c = ee >> 5, l = ee & 31;
+        const int byte = b[48 + 32 * (c >> 1) + l];
+        const int q = ((c & 1) ? byte >> 4 : byte & 15) + (((b[16 + l] >> c) & 1) << 4);
+        int sc, mn;
+        q4k_sm(b + 4, c, sc, mn);
+        out = h2f(ld16(b)) * (float)sc * (float)q - h2f(ld16(b + 2)) * (float)mn;
+    } break;
     case Q6_K: {                                                   // quants.c:379-400
         const uint8_t *b = row + (e >> 8) * 210;
         const int ee = (int)(e & 255), h = ee >> 7, j = (ee >> 5) & 3, l = ee & 31;
@@ -224,6 +233,7 @@ __global__ __launch_bounds__(256) void k_repack(g4h_tensor t, uint8_t *__restric
     case Q8_0: mv(t.sc + i * 2, 0, 2); mv(t.qs + i * 32, 2, 32); break;
     case Q4_0: mv(t.sc + i * 2, 0, 2); mv(t.qs + i * 16, 2, 16); break;
     case Q4_K: mv(t.qs + i * 144, 0, 144); break;
+    case Q5_K: mv(t.qs + i * 176, 0, 176); break;
     case Q2_K: mv(t.sc + i * 16, 0, 16); mv(t.qs + i * 64, 16, 64); mv(t.ex + i * 4, 80, 4); break;
     case Q3_K: mv(t.ex + i * 32, 0, 32); mv(t.qs + i * 64, 32, 64); mv(t.sc + i * 12, 96, 12); mv(t.dd + i * 2, 108, 2); break;
     case Q6_K: mv(t.qs + i * 128, 0, 128); mv(t.ex + i * 64, 128, 64); mv(t.sc + i * 16, 192, 16); mv(t.dd + i * 2, 208, 2); break;
@@ -265,6 +275,12 @@ template <> __device__ void raw_frag<FQ3_K>(FQ3_K::Frag &f, const uint8_t *row, 
     f.s0 = ldu32(b + 96); f.s1 = ldu32(b + 100); f.s2 = ldu32(b + 104); f.d = ld16(b + 108);
 }
 
+template <> __device__ void raw_frag<FQ5_K>(FQ5_K::Frag &f, const uint8_t *row, int u) {
+    const uint8_t *b = row + (size_t)(u >> 2) * 176;
+    const int p = u & 3;
+    f.h = ldu128(b); f.hb0 = ldu128(b + 16); f.hb1 = ldu128(b + 32);
+    f.q0 = ldu128(b + 48 + 32 * p); f.q1 = ldu128(b + 64 + 32 * p);
+}
 template <> __device__ void raw_frag<FQ6_K>(FQ6_K::Frag &f, const uint8_t *row, int u) {
     const uint8_t *b = row + (size_t)(u >> 2) * 210;
     const int p = u & 3, h = p >> 1, k = p & 1;
@@ -341,6 +357,7 @@ hipError_t launch_vec_dot_raw(int wtype, const uint8_t *w, size_t ws, const uint
     case Q4_K: return vd_go<FQ4_K>(w, ws, a, n, rows, out, s);
     case Q3_K: return vd_go<FQ3_K>(w, ws, a, n, rows, out, s);
     case Q2_K: return vd_go<FQ2_K>(w, ws, a, n, rows, out, s);
+    case Q5_K: return vd_go<FQ5_K>(w, ws, a, n, rows, out, s);
     case Q6_K: return vd_go<FQ6_K>(w, ws, a, n, rows, out, s);
     default: return hipErrorInvalidValue;
     }

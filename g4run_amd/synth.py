@@ -4,7 +4,7 @@ Weights are generated directly as GGUF block bytes (numpy PCG64 streams, so
 the same seed gives the same bytes on every host):
   q8_0  quants uniform in [-127, 127], d = fp16(|N(0,1)| * 0.02/127)
   q4_0  nibbles uniform in 0..15,     d = fp16(|N(0,1)| * 0.02/8)
-  q2_K / q3_K / q4_K / q6_K  every quant, scale and hmask bit uniform random;
+  q2_K / q3_K / q4_K / q5_K / q6_K  every quant, scale and hmask bit uniform random;
         d and dmin = fp16(|N(0,1)| * 1e-4) so that they are finite.
 Activations x ~ N(0,1) in fp32.
 """
@@ -12,11 +12,11 @@ from __future__ import annotations
 
 import numpy as np
 
-from . import BLCK, Q2_K, Q3_K, Q4_0, Q4_K, Q6_K, Q8_0, SIZE
+from . import BLCK, Q2_K, Q3_K, Q4_0, Q4_K, Q5_K, Q6_K, Q8_0, SIZE
 
 # byte offsets of the fp16 scale fields inside each block (g4run.h:107-118)
-_SCALE_FIELDS = {Q8_0: (0,), Q4_0: (0,), Q2_K: (80, 82), Q3_K: (108,), Q4_K: (0, 2), Q6_K: (208,)}
-_SCALE_MUL = {Q8_0: 0.02 / 127, Q4_0: 0.02 / 8, Q2_K: 1e-4, Q3_K: 1e-4, Q4_K: 1e-4, Q6_K: 1e-5}
+_SCALE_FIELDS = {Q8_0: (0,), Q4_0: (0,), Q2_K: (80, 82), Q3_K: (108,), Q4_K: (0, 2), Q5_K: (0, 2), Q6_K: (208,)}
+_SCALE_MUL = {Q8_0: 0.02 / 127, Q4_0: 0.02 / 8, Q2_K: 1e-4, Q3_K: 1e-4, Q4_K: 1e-4, Q5_K: 1e-4, Q6_K: 1e-5}
 
 
 def _fp16_bits(v: np.ndarray) -> np.ndarray:
@@ -50,7 +50,8 @@ GEMV_CONFIGS = {
     "q4_K_4096x11008": (Q4_K, 4096, 11008),
     "q3_K_4096x11008": (Q3_K, 4096, 11008),
     "q2_K_4096x11008": (Q2_K, 4096, 11008),
-    # beyond BASELINE config 2: the next K-quant format of the same boundary
+    # beyond BASELINE config 2: the next K-quant formats of the same boundary
+    "q5_K_4096x11008": (Q5_K, 4096, 11008),
     "q6_K_4096x11008": (Q6_K, 4096, 11008),
 }
 

@@ -24,7 +24,7 @@ extern "C" {
 /* ggml type ids, g4run.h:80-94 (values are a file-format contract). */
 enum {
     G4O_F32 = 0, G4O_F16 = 1, G4O_Q4_0 = 2, G4O_Q8_0 = 8,
-    G4O_Q2_K = 10, G4O_Q3_K = 11, G4O_Q4_K = 12, G4O_Q6_K = 14, G4O_Q8_K = 15
+    G4O_Q2_K = 10, G4O_Q3_K = 11, G4O_Q4_K = 12, G4O_Q5_K = 13, G4O_Q6_K = 14, G4O_Q8_K = 15
 };
 
 /* Packed block layouts, g4run.h:107-118.  Byte-for-byte the GGUF formats. */
@@ -35,6 +35,7 @@ typedef struct { float d; int8_t qs[256]; int16_t bsums[16]; } g4o_q8_K;       /
 typedef struct { uint8_t scales[16]; uint8_t qs[64]; uint16_t d, dmin; } g4o_q2_K;        /* 84 B */
 typedef struct { uint8_t hmask[32]; uint8_t qs[64]; uint8_t scales[12]; uint16_t d; } g4o_q3_K; /* 110 B */
 typedef struct { uint16_t d, dmin; uint8_t scales[12]; uint8_t qs[128]; } g4o_q4_K;       /* 144 B */
+typedef struct { uint16_t d, dmin; uint8_t scales[12]; uint8_t qh[32]; uint8_t qs[128]; } g4o_q5_K; /* 176 B */
 typedef struct { uint8_t ql[128]; uint8_t qh[64]; int8_t scales[16]; uint16_t d; } g4o_q6_K; /* 210 B */
 #pragma pack(pop)
 
@@ -60,7 +61,7 @@ int  g4o_dequant_row(int type, const void *x, float *y, int64_t n);  /* returns 
 
 /* ---- per-block integer sums ----
  * q8_0 / q4_0: one int32 per 32-block: sum_j w_j * a_j (q4_0 elements are q-8).
- * q2_K / q4_K: two int32 per superblock: isum (scale-weighted quant sum) and
+ * q2_K / q4_K / q5_K: two int32 per superblock: isum (scale-weighted quant sum) and
  *              msum (min-weighted bsums), so that the superblock value is
  *              d_a*(d_w*isum - dmin_w*msum)   (quants.c:633-652, 743-758).
  * q3_K: one int32 per superblock, isum = sum_s (scale_s-32) * sum q3*q8.

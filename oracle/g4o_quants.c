@@ -18,7 +18,7 @@ int g4o_type_blck(int t) {
     switch (t) {
     case G4O_F32: case G4O_F16: return 1;
     case G4O_Q4_0: case G4O_Q8_0: return 32;
-    case G4O_Q2_K: case G4O_Q3_K: case G4O_Q4_K: case G4O_Q6_K: case G4O_Q8_K: return 256;
+    case G4O_Q2_K: case G4O_Q3_K: case G4O_Q4_K: case G4O_Q5_K: case G4O_Q6_K: case G4O_Q8_K: return 256;
     default: return 0;
     }
 }
@@ -30,6 +30,7 @@ size_t g4o_type_size(int t) {
     case G4O_Q8_0: return sizeof(g4o_q8_0);
     case G4O_Q2_K: return sizeof(g4o_q2_K);
     case G4O_Q3_K: return sizeof(g4o_q3_K);
+    case G4O_Q5_K: return sizeof(g4o_q5_K);
     case G4O_Q6_K: return sizeof(g4o_q6_K);
     case G4O_Q4_K: return sizeof(g4o_q4_K);
     case G4O_Q8_K: return sizeof(g4o_q8_K);
@@ -215,6 +216,14 @@ static inline int q3k_q(const g4o_q3_K *b, int e) {
     int hb = (b->hmask[l] >> (4 * h + j)) & 1;
     return lo - (hb ? 0 : 4);
 }
+/* element e of a q5_K superblock: 0..31 and sub-block e/32 (quants.c:497-515):
+ * chunk c = e/32, nibble of qs[32(c/2) + l] (low for even c) + 16 * bit c of
+ * qh[l]. */
+static inline int q5k_q(const g4o_q5_K *b, int e) {
+    int c = e >> 5, l = e & 31;
+    uint8_t byte = b->qs[32 * (c >> 1) + l];
+    return ((c & 1) ? (byte >> 4) : (byte & 15)) + (((b->qh[l] >> c) & 1) << 4);
+}
 /* element e of a q6_K superblock: signed value -32..31 (quants.c:379-400):
  * e = 128h + 32j + l, low nibble of ql[64h + 32(j&1) + l] (high nibble for
  * j >= 2), high 2 bits (qh[32h + l] >> 2j) & 3; its scale is scales[e/16]. */
@@ -291,6 +300,17 @@ int g4o_dequant_row(int type, const void *vx, float *y, int64_t n) {
         }
         return 0;
     }
+    case G4O_Q5_K: {                                       /* quants.c:497-515: (d*sc)*q - dmin*m */
+        const g4o_q5_K *x = vx;
+        for (int64_t b = 0; b < n / 256; b++) {
+            float d = g4o_fp16_to_fp32(x[b].d), dm = g4o_fp16_to_fp32(x[b].dmin);
+            for (int e = 0; e < 256; e++) {
+                int sc, mn; q4k_scale_min(x[b].scales, e >> 5, &sc, &mn);
+                y[256 * b + e] = d * sc * q5k_q(&x[b], e) - dm * mn;
+            }
+        }
+        return 0;
+    }
     case G4O_Q6_K: {                                       /* quants.c:379-400: (d*sc)*q */
         const g4o_q6_K *x = vx;
         for (int64_t b = 0; b < n / 256; b++) {
@@ -342,6 +362,15 @@ static void sums_q4_K(const g4o_q4_K *w, const g4o_q8_K *a, int32_t *isum, int32
     *isum = is; *msum = ms;
 }
 
+/* q5_K: as q4_K with 5-bit quants (quants.c:797-813). */
+static void sums_q5_K(const g4o_q5_K *w, const g4o_q8_K *a, int32_t *isum, int32_t *msum) {
+    int sc[8], mn[8];
+    for (int j = 0; j < 8; j++) q4k_scale_min(w->scales, j, &sc[j], &mn[j]);
+    int32_t is = 0, ms = 0;
+    for (int e = 0; e < 256; e++) is += sc[e >> 5] * q5k_q(w, e) * a->qs[e];
+    for (int g = 0; g < 16; g++) ms += a->bsums[g] * mn[g >> 1];
+    *isum = is; *msum = ms;
+}
 static int32_t sum_q6_K(const g4o_q6_K *w, const g4o_q8_K *a) {
     int32_t s = 0;
     for (int e = 0; e < 256; e++) s += w->scales[e >> 4] * q6k_q(w, e) * a->qs[e];
@@ -354,6 +383,7 @@ void g4o_block_sums(int type, const void *w, const void *a, int64_t n, int32_t *
     case G4O_Q4_0: for (int64_t b = 0; b < n / 32; b++) out[b] = sum_q4_0((const g4o_q4_0 *)w + b, (const g4o_q8_0 *)a + b); break;
     case G4O_Q2_K: for (int64_t b = 0; b < n / 256; b++) sums_q2_K((const g4o_q2_K *)w + b, (const g4o_q8_K *)a + b, &out[2 * b], &out[2 * b + 1]); break;
     case G4O_Q3_K: for (int64_t b = 0; b < n / 256; b++) out[b] = sum_q3_K((const g4o_q3_K *)w + b, (const g4o_q8_K *)a + b); break;
+    case G4O_Q5_K: for (int64_t b = 0; b < n / 256; b++) sums_q5_K((const g4o_q5_K *)w + b, (const g4o_q8_K *)a + b, &out[2 * b], &out[2 * b + 1]); break;
     case G4O_Q6_K: for (int64_t b = 0; b < n / 256; b++) out[b] = sum_q6_K((const g4o_q6_K *)w + b, (const g4o_q8_K *)a + b); break;
     case G4O_Q4_K: for (int64_t b = 0; b < n / 256; b++) sums_q4_K((const g4o_q4_K *)w + b, (const g4o_q8_K *)a + b, &out[2 * b], &out[2 * b + 1]); break;
     default: break;
@@ -387,7 +417,7 @@ float g4o_dot_ref(int type, const void *vw, const void *va, int64_t n) {
         }
         return acc;
     }
-    case G4O_Q3_K: case G4O_Q4_K: case G4O_Q6_K: {
+    case G4O_Q3_K: case G4O_Q4_K: case G4O_Q5_K: case G4O_Q6_K: {
         /* quants.c:657-711 / 713-762 / 582-622: 8 int32 lanes (element e -> lane e%8)
          * carry the scale-weighted sums of one superblock; each lane is scaled
          * into an 8-float accumulator; the lanes are summed at the end. */
@@ -405,6 +435,15 @@ float g4o_dot_ref(int type, const void *vw, const void *va, int64_t n) {
                 const g4o_q6_K *w = (const g4o_q6_K *)vw + b; const g4o_q8_K *a = (const g4o_q8_K *)va + b;
                 for (int e = 0; e < 256; e++) lane[e & 7] += w->scales[e >> 4] * (q6k_q(w, e) * a->qs[e]);
                 d = g4o_fp16_to_fp32(w->d) * a->d;
+            } else if (type == G4O_Q5_K) {                    /* quants.c:764-818 */
+                const g4o_q5_K *w = (const g4o_q5_K *)vw + b; const g4o_q8_K *a = (const g4o_q8_K *)va + b;
+                int32_t is, ms; sums_q5_K(w, a, &is, &ms);
+                int sc[8], mn[8];
+                for (int j = 0; j < 8; j++) q4k_scale_min(w->scales, j, &sc[j], &mn[j]);
+                for (int e = 0; e < 256; e++) lane[e & 7] += sc[e >> 5] * (q5k_q(w, e) * a->qs[e]);
+                d = g4o_fp16_to_fp32(w->d) * a->d;
+                float dmin = g4o_fp16_to_fp32(w->dmin) * a->d;
+                mins_acc -= dmin * ms;
             } else {
                 const g4o_q4_K *w = (const g4o_q4_K *)vw + b; const g4o_q8_K *a = (const g4o_q8_K *)va + b;
                 int32_t is, ms; sums_q4_K(w, a, &is, &ms);
@@ -508,6 +547,27 @@ static float dot_q6_K_avx2(const g4o_q6_K *w, const g4o_q8_K *a, int64_t nb) {
     }
     return hsum8(acc);
 }
+/* q5_K (quants.c:1261-1313): the mins sum of a superblock goes to one scalar
+ * accumulator, the scale-weighted products to 8 lanes as in q4_K; the result
+ * is hsum_float_8(acc) + summs.  The shipped -Ofast build evaluates
+ * summs += (-d_a*dmin_w) * msum as fma(-dmin_w, d_a*msum, summs) (the
+ * reassociation its fast-math flags allow); that is the form that reproduces
+ * the reference build's outputs bit for bit. */
+static float dot_q5_K_avx2(const g4o_q5_K *w, const g4o_q8_K *a, int64_t nb) {
+    float acc[8] = {0}, summs = 0.0f;
+    for (int64_t b = 0; b < nb; b++) {
+        const float d = a[b].d * g4o_fp16_to_fp32(w[b].d);
+        int sc[8], mn[8];
+        for (int j = 0; j < 8; j++) q4k_scale_min(w[b].scales, j, &sc[j], &mn[j]);
+        int32_t msum = 0;
+        for (int k = 0; k < 8; k++) msum += mn[k] * (a[b].bsums[2 * k] + a[b].bsums[2 * k + 1]);
+        summs = fmaf(-g4o_fp16_to_fp32(w[b].dmin), a[b].d * (float)msum, summs);
+        int32_t lane[8] = {0};
+        for (int e = 0; e < 256; e++) lane[(e & 31) >> 2] += sc[e >> 5] * q5k_q(&w[b], e) * a[b].qs[e];
+        for (int i = 0; i < 8; i++) acc[i] = fmaf(d, (float)lane[i], acc[i]);
+    }
+    return hsum8(acc) + summs;
+}
 /* q4_K (quants.c:1213-1259): mins go to a separate 4-lane accumulator
  * (lane i = mins 2i,2i+1 times bsum pairs), folded 0+2,1+3 then added. */
 static float dot_q4_K_avx2(const g4o_q4_K *w, const g4o_q8_K *a, int64_t nb) {
@@ -538,6 +598,7 @@ float g4o_dot(int type, const void *w, const void *a, int64_t n) {
     case G4O_Q2_K: return dot_q2_K_avx2(w, a, n / 256);
     case G4O_Q3_K: return dot_q3_K_avx2(w, a, n / 256);
     case G4O_Q4_K: return dot_q4_K_avx2(w, a, n / 256);
+    case G4O_Q5_K: return dot_q5_K_avx2(w, a, n / 256);
     case G4O_Q6_K: return dot_q6_K_avx2(w, a, n / 256);
     default: return NAN;
     }

@@ -36,6 +36,7 @@ def test_row_size_matches_type_table():
     assert G.row_size(G.Q4_K, 11008) == 6192
     assert G.row_size(G.Q3_K, 11008) == 4730
     assert G.row_size(G.Q2_K, 11008) == 3612
+    assert G.row_size(G.Q5_K, 11008) == 43 * 176
     assert G.row_size(G.Q6_K, 11008) == 43 * 210
     assert G.row_size(G.Q8_K, 11008) == 43 * 292
     assert G.row_size(G.Q8_0, 33) == 0
@@ -47,7 +48,7 @@ def test_act_class_and_stride():
     # model.c:132-141 activation classes; model.c:148-149 64-B padded stride
     import g4run_amd as G
     assert G.act_type(G.Q4_0) == G.Q8_0 and G.act_type(G.Q8_0) == G.Q8_0
-    for t in (G.Q2_K, G.Q3_K, G.Q4_K, G.Q6_K):
+    for t in (G.Q2_K, G.Q3_K, G.Q4_K, G.Q5_K, G.Q6_K):
         assert G.act_type(t) == G.Q8_K
     assert G.act_type(G.F32) == -1
     assert G.act_stride(G.Q8_0, 4096) == 4352

@@ -88,7 +88,7 @@ def test_quantize_q8_K_closed_form(oracle):
 
 
 # ---------------------------------------------------- dots / dequant / sums
-FMTS = [("q8_0", 8), ("q4_0", 2), ("q2_K", 10), ("q3_K", 11), ("q4_K", 12), ("q6_K", 14)]
+FMTS = [("q8_0", 8), ("q4_0", 2), ("q2_K", 10), ("q3_K", 11), ("q4_K", 12), ("q5_K", 13), ("q6_K", 14)]
 
 
 @pytest.mark.parametrize("name,qt", FMTS)
@@ -154,7 +154,7 @@ def test_block_sums_brute_force(oracle, name, qt):
     blk = oracle.BLCK[qt]
     expect = per.reshape(4, nb, blk).sum(-1)
     s = oracle.block_sums(qt, w, a, n)
-    got = s[:, 0::2] if qt in (10, 12) else s
+    got = s[:, 0::2] if qt in (10, 12, 13) else s
     assert np.array_equal(got.astype(np.int64), expect)
 
 
