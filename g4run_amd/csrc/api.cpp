@@ -488,7 +488,8 @@ extern "C" size_t g4h_attn_workspace_bytes(int n_head, int hd, int n_pos) {
 }
 
 static int check_attn_shape(const char *fn, int kv_type, int n_head, int n_kv, int hd) {
-    if (kv_type != F16 && kv_type != Q8_0) return fail(G4H_ERR_TYPE, "%s: KV type %d unsupported (f16, q8_0)", fn, kv_type);
+    if (kv_type != F16 && kv_type != Q8_0 && kv_type != Q4_0)
+        return fail(G4H_ERR_TYPE, "%s: KV type %d unsupported (f16, q8_0, q4_0)", fn, kv_type);
     if (n_kv <= 0 || n_head <= 0 || n_head % n_kv) return fail(G4H_ERR_SHAPE, "%s: n_head=%d not a multiple of n_kv=%d", fn, n_head, n_kv);
     const int grp = n_head / n_kv;
     if (grp != 1 && grp != 2 && grp != 4 && grp != 8) return fail(G4H_ERR_SHAPE, "%s: group size %d unsupported", fn, grp);

@@ -3,7 +3,7 @@
 // model.c:664-687 folded in) over 128-position chunks.
 //
 // Cache layout: [slot][n_kv][hd] rows (one row = one head's K or V for one
-// position), f16 or q8_0 blocks.  Query heads map to KV heads h / (n_head/n_kv)
+// position), f16, q8_0 or q4_0 blocks.  Query heads map to KV heads h / (n_head/n_kv)
 // (model.c:1099).
 //
 // Steps (one launch, k_attn_fused_f16, for f16 caches whose chunks the device
@@ -12,12 +12,13 @@
 //                RoPE) and -- in the chunk holding the current position -- the
 //                new key (RMSNorm * k_norm, RoPE) and value (RMSNorm) rows,
 //                stored into the caches at that position; q is rounded to the
-//                K cache's activation form (fp16, or q8_0 blocks, model.c:530-533).
+//                K cache's activation form (fp16, or q8_0 blocks for a q8_0 /
+//                q4_0 cache, model.c:530-533).
 //   scores       s_j = K_j . q, no 1/sqrt(d) (model.c:538).  f16: each lane's 8
 //                products in element order, then a butterfly over the row's
 //                lanes -- a fixed order that differs from the CPU's 8-lane f16
 //                dot (quants.c:1319-1331) only in the fp32 rounding of the sum.
-//                q8_0: one lane per position in the AVX2 q8_0 dot's order
+//                q8_0 / q4_0: one lane per position in the AVX2 q8_0 / q4_0 dot's order
 //                (quants.c:984-999), equal to the CPU's bit for bit.  Per chunk
 //                the maximum m_c and l_c = sum exp(s_j - m_c) in double.
 //   weights      M = max_c m_c is the global maximum, so e_j = (float)exp(s_j - M)
@@ -25,7 +26,7 @@
 //                normaliser sum_c l_c exp(m_c - M) equals the reference's
 //                double sum up to the grouping of that sum, and inv =
 //                (float)(1/sum) (model.c:549).  Weights fp16(e_j*inv) for an f16
-//                V cache, e_j*inv for q8_0 (model.c:555, 573).
+//                V cache, e_j*inv for q8_0 / q4_0 (model.c:555, 573).
 //   V / combine  chunk partials of sum w_j V_j, added in chunk order, and q8_0
 //                of each head row for the output projection (quants.c:74-109).
 // Beyond the f16 score sum, only the fp32 order of the value sum and the
@@ -111,8 +112,8 @@ __device__ __forceinline__ void prep_finish(const PrepRow &r, bool weighted, boo
         }
     }
 }
-// a prepared row into a cache slot (f16 RNE, or q8_0 blocks via an LDS row of
-// 256 floats for this wave); the whole wave calls it
+// a prepared row into a cache slot (f16 RNE, or q8_0 / q4_0 blocks via an LDS
+// row of 256 floats for this wave); the whole wave calls it
 __device__ __forceinline__ void cache_store(const float y[4], int kv_type, uint8_t *dst, int hd, float *wb) {
     const int lane = threadIdx.x & 63, epl = hd >> 6;
     if (kv_type == F16) {
@@ -131,7 +132,8 @@ __device__ __forceinline__ void cache_store(const float y[4], int kv_type, uint8
     float o[4] = {0.f, 0.f, 0.f, 0.f};
     if (own)
         for (int k = 0; k < 4; k++) o[k] = wb[4 * lane + k];
-    q8_store4(o, lane, own, dst);
+    if (kv_type == Q4_0) q4_store4(o, lane, own, dst);
+    else q8_store4(o, lane, own, dst);
     __builtin_amdgcn_wave_barrier();
 }
 
@@ -457,14 +459,16 @@ __global__ __launch_bounds__(256) void k_attn_scores_f16(AttnCtx c) {
     chunk_stats<GRP, 4, false>(s, ok, lane < 32, c, h0, ch, wm, wl);
 }
 
-// q8_0 cache.  128 threads, one lane per position; the query is q8_0-quantized
-// per block (model.c:533) and each block pair of the row is dotted in the AVX2
-// order of quants.c:984-999.
-template <int GRP, int HD>
+// q8_0 / q4_0 cache.  128 threads, one lane per position; the query is
+// q8_0-quantized per block (model.c:533) and each block pair of the row is
+// dotted in the AVX2 order of quants.c:984-999 (q8_0) / 964-982 (q4_0): eight
+// int32 lanes of 4 elements, one fma per lane and block, then hsum_float_8.
+template <int KV, int GRP, int HD>
 __global__ __launch_bounds__(128) void k_attn_scores_q8(AttnCtx c) {
+    constexpr int BS = KV == Q4_0 ? 18 : 34;                      // bytes per 32-element block
     __shared__ __align__(16) int4 qq[GRP][8][2];
     __shared__ float qd[GRP][8];
-    __shared__ __align__(16) uint8_t kpos[8 * 34 + 4];         // the new key row (q8_0 blocks)
+    __shared__ __align__(16) uint8_t kpos[8 * 34 + 4];         // the new key row (q8_0 / q4_0 blocks)
     __shared__ float wbuf[2][256];
     __shared__ float qrow[GRP][256];
     __shared__ float wm[2][GRP];
@@ -490,9 +494,9 @@ __global__ __launch_bounds__(128) void k_attn_scores_q8(AttnCtx c) {
             if (r < GRP) {
                 for (int e = 0; e < epl; e++) qrow[r][lane * epl + e] = y[e];
             } else {
-                uint8_t *dst = (r == GRP ? c.a.kc : c.a.vc) + ((size_t)p * n_kv + kvh) * (hd / 32) * 34;
-                cache_store(y, Q8_0, dst, hd, wbuf[wave]);
-                if (r == GRP) cache_store(y, Q8_0, kpos, hd, wbuf[wave]);
+                uint8_t *dst = (r == GRP ? c.a.kc : c.a.vc) + ((size_t)p * n_kv + kvh) * (hd / 32) * BS;
+                cache_store(y, KV, dst, hd, wbuf[wave]);
+                if (r == GRP) cache_store(y, KV, kpos, hd, wbuf[wave]);
             }
         }
     } else {
@@ -514,21 +518,44 @@ __global__ __launch_bounds__(128) void k_attn_scores_q8(AttnCtx c) {
     __syncthreads();
     const int j = ch * ATT_CHUNK + t;
     const bool ok = j < npos;
-    const uint8_t *row = pos_chunk && j == p ? kpos : c.a.kc + ((size_t)(ok ? j : npos - 1) * n_kv + kvh) * (hd / 32) * 34;
+    const uint8_t *row = pos_chunk && j == p ? kpos : c.a.kc + ((size_t)(ok ? j : npos - 1) * n_kv + kvh) * (hd / 32) * BS;
     float acc[GRP][8];
 #pragma unroll
     for (int g = 0; g < GRP; g++)
 #pragma unroll
         for (int l = 0; l < 8; l++) acc[g][l] = 0.0f;
     for (int b = 0; b < hd / 32; b += 2) {
-        uint32_t v[17];
-        const uint32_t *src = (const uint32_t *)(row + (size_t)b * 34);
-#pragma unroll
-        for (int k = 0; k < 17; k++) v[k] = src[k];
+        // the two blocks' 32 signed quants as 8 words each (lane l = elements 4l..4l+3)
         uint32_t w0[8], w1[8];
+        float d0, d1;
+        if constexpr (KV == Q4_0) {
+            uint32_t v[9];
+            const uint32_t *src = (const uint32_t *)(row + (size_t)b * 18);
 #pragma unroll
-        for (int k = 0; k < 8; k++) { w0[k] = __builtin_amdgcn_alignbyte(v[k + 1], v[k], 2); w1[k] = v[9 + k]; }
-        const float d0 = h2f((uint16_t)(v[0] & 0xffff)), d1 = h2f((uint16_t)(v[8] >> 16));
+            for (int k = 0; k < 9; k++) v[k] = src[k];
+            uint32_t n0[4], n1[4];
+#pragma unroll
+            for (int k = 0; k < 4; k++) { n0[k] = __builtin_amdgcn_alignbyte(v[k + 1], v[k], 2); n1[k] = v[5 + k]; }
+            // nibble n -> n - 8 as a signed byte, carry-free: (n + 0x78) ^ 0x80
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                w0[k] = ((n0[k] & 0x0F0F0F0Fu) + 0x78787878u) ^ 0x80808080u;
+                w0[k + 4] = (((n0[k] >> 4) & 0x0F0F0F0Fu) + 0x78787878u) ^ 0x80808080u;
+                w1[k] = ((n1[k] & 0x0F0F0F0Fu) + 0x78787878u) ^ 0x80808080u;
+                w1[k + 4] = (((n1[k] >> 4) & 0x0F0F0F0Fu) + 0x78787878u) ^ 0x80808080u;
+            }
+            d0 = h2f((uint16_t)(v[0] & 0xffff));
+            d1 = h2f((uint16_t)(v[4] >> 16));
+        } else {
+            uint32_t v[17];
+            const uint32_t *src = (const uint32_t *)(row + (size_t)b * 34);
+#pragma unroll
+            for (int k = 0; k < 17; k++) v[k] = src[k];
+#pragma unroll
+            for (int k = 0; k < 8; k++) { w0[k] = __builtin_amdgcn_alignbyte(v[k + 1], v[k], 2); w1[k] = v[9 + k]; }
+            d0 = h2f((uint16_t)(v[0] & 0xffff));
+            d1 = h2f((uint16_t)(v[8] >> 16));
+        }
 #pragma unroll
         for (int g = 0; g < GRP; g++) {
             const int4 a0 = qq[g][b][0], a1 = qq[g][b][1], c0 = qq[g][b + 1][0], c1 = qq[g][b + 1][1];
@@ -623,7 +650,7 @@ __device__ __forceinline__ void v_partial_store(const float (&o)[GRP][8], float 
     }
 }
 
-// q8_0 V path: lane owns elements 4*lane .. 4*lane+3; the four waves'
+// q8_0 / q4_0 V path: lane owns elements 4*lane .. 4*lane+3; the four waves'
 // partials added in order into P[h][ch][hd]
 template <int GRP, int HD>
 __device__ __forceinline__ void v_partial_store4(const float (&o)[GRP][4], float (*part)[GRP][256], const AttnCtx &c, int h0,
@@ -677,7 +704,7 @@ __global__ __launch_bounds__(256) void k_attn_v(AttnCtx c) {
         const int i = t + 256 * k, g = i / ATT_CHUNK, jw = ch * ATT_CHUNK + (i - g * ATT_CHUNK);
         sv[k] = i < GRP * ATT_CHUNK && jw < npos ? c.S[(size_t)(h0 + g) * npos + jw] : 0.0f;
     }
-    // 2. the V rows (f16: 16-byte loads, see v_rows_load; q8_0: below, lane
+    // 2. the V rows (f16: 16-byte loads, see v_rows_load; q8_0 / q4_0: below, lane
     // owning elements 4*lane .. 4*lane+3, lanes beyond hd/4 idle)
     const bool lane_ok = 4 * lane < hd;
     uint4 vq[16];
@@ -729,11 +756,21 @@ __global__ __launch_bounds__(256) void k_attn_v(AttnCtx c) {
             const int j = j0 + k;
             if (j >= npos) break;
             if (lane_ok) {
-                const uint8_t *blk = c.a.vc + ((size_t)j * n_kv + kvh) * (hd / 32) * 34 + (lane >> 3) * 34;
+                // the lane's 4 elements, dequantized as g4_dequant_row does (quants.c:364-378)
+                constexpr int BS = KV == Q4_0 ? 18 : 34;
+                const uint8_t *blk = c.a.vc + ((size_t)j * n_kv + kvh) * (hd / 32) * BS + (lane >> 3) * BS;
                 const float d = h2f((uint16_t)(blk[0] | (blk[1] << 8)));
                 float v[4];
 #pragma unroll
-                for (int e = 0; e < 4; e++) v[e] = (float)(int8_t)blk[2 + 4 * (lane & 7) + e] * d;
+                for (int e = 0; e < 4; e++) {
+                    const int jj = 4 * (lane & 7) + e;                       // element of the block
+                    if constexpr (KV == Q4_0) {
+                        const int nib = jj < 16 ? (blk[2 + jj] & 15) : (blk[2 + jj - 16] >> 4);
+                        v[e] = (float)(nib - 8) * d;
+                    } else {
+                        v[e] = (float)(int8_t)blk[2 + jj] * d;
+                    }
+                }
 #pragma unroll
                 for (int g = 0; g < GRP; g++) {
                     const float w = wl[g][wave * 32 + k];
@@ -1184,7 +1221,7 @@ __global__ __launch_bounds__(256) void k_attn_fused_f16(AttnCtx c) {
 }
 
 // ------------------------------------------------------------- KV store --
-// model.c:583-589: an f16 row (RNE) or q8_0 blocks per head row.
+// model.c:583-589: an f16 row (RNE) or q8_0 / q4_0 blocks per head row.
 __global__ __launch_bounds__(256) void k_kv_store_f16(const float *__restrict__ src, uint16_t *__restrict__ dst, int n) {
     const int i = blockIdx.x * 256 + threadIdx.x;
     if (i < n) dst[i] = f2h(src[i]);
@@ -1283,7 +1320,7 @@ static hipError_t attn_go(AttnCtx c, int n_head, int n_kv, int npos_max, uint8_t
         }
     }
     if constexpr (KV == F16) hipLaunchKernelGGL((k_attn_scores_f16<GRP, HD>), dim3(n_kv, nc), dim3(256), 0, s, c);
-    else hipLaunchKernelGGL((k_attn_scores_q8<GRP, HD>), dim3(n_kv, nc), dim3(128), 0, s, c);
+    else hipLaunchKernelGGL((k_attn_scores_q8<KV, GRP, HD>), dim3(n_kv, nc), dim3(128), 0, s, c);
     hipLaunchKernelGGL((k_attn_v<KV, GRP, HD>), dim3(n_kv, nc), dim3(256), 0, s, c);
     hipLaunchKernelGGL(k_attn_combine, dim3(n_head), dim3(256), 0, s, c);
     return hipGetLastError();
@@ -1372,6 +1409,7 @@ hipError_t launch_attn_decode(const float *q, const float *qkv, const QkvArgs &a
     }
     G4_ATT(F16, 1); G4_ATT(F16, 2); G4_ATT(F16, 4); G4_ATT(F16, 8);
     G4_ATT(Q8_0, 1); G4_ATT(Q8_0, 2); G4_ATT(Q8_0, 4); G4_ATT(Q8_0, 8);
+    G4_ATT(Q4_0, 1); G4_ATT(Q4_0, 2); G4_ATT(Q4_0, 4); G4_ATT(Q4_0, 8);
 #undef G4_ATT
     return hipErrorInvalidValue;
 }

@@ -152,8 +152,8 @@ extern "C" int g4h_model_create(const g4h_model_config *cfg, uint64_t seed, g4h_
     if (c.n_embd % 32 || c.n_ff % 256 || c.head_dim % 64 || c.head_dim > 256 || c.n_head % c.n_kv || c.n_embd > 8192 ||
         c.n_ff % 32)
         return g4h_internal_fail(G4H_ERR_SHAPE, "g4h_model_create: n_embd%32 (<=8192), n_ff%256, head_dim%64 (<=256), n_head%n_kv");
-    if ((c.wtype != Q4_0 && c.wtype != Q8_0) || c.head_type != Q8_0 || (c.kv_type != F16 && c.kv_type != Q8_0))
-        return g4h_internal_fail(G4H_ERR_TYPE, "g4h_model_create: wtype q4_0|q8_0, head q8_0, kv f16|q8_0");
+    if ((c.wtype != Q4_0 && c.wtype != Q8_0) || c.head_type != Q8_0 || (c.kv_type != F16 && c.kv_type != Q8_0 && c.kv_type != Q4_0))
+        return g4h_internal_fail(G4H_ERR_TYPE, "g4h_model_create: wtype q4_0|q8_0, head q8_0, kv f16|q8_0|q4_0");
     g4h_model *m = new g4h_model();
     m->c = c;
     m->fuse = kDefaultFuse;
@@ -199,7 +199,7 @@ extern "C" int g4h_model_create(const g4h_model_config *cfg, uint64_t seed, g4h_
     if (launch_rand_normal(m->norms, (int64_t)n_norm, k++, 1.0f, 0.05f, s) != hipSuccess) return bail(G4H_ERR_HIP);
 
     // KV caches: [layer][K|V][n_ctx][n_kv][row]
-    const size_t row = c.kv_type == F16 ? (size_t)hd * 2 : g4h_row_size(Q8_0, hd);
+    const size_t row = c.kv_type == F16 ? (size_t)hd * 2 : g4h_row_size(c.kv_type, hd);
     m->kv_layer_bytes = (size_t)c.n_ctx * KV * row;
     if ((rc = model_alloc(m, (void **)&m->kv, m->kv_layer_bytes * 2 * c.n_layer))) return bail(rc);
     if (hipMemsetAsync(m->kv, 0, m->kv_layer_bytes * 2 * c.n_layer, s) != hipSuccess) return bail(G4H_ERR_HIP);
@@ -270,7 +270,7 @@ extern "C" int g4h_model_fill_kv(g4h_model *m, uint64_t seed, void *stream) {
     const int64_t n = (int64_t)c.n_ctx * c.n_kv * c.head_dim;
     float *tmp;
     M_RC(g4h_malloc((void **)&tmp, n * 4));
-    const size_t row = c.kv_type == F16 ? (size_t)c.head_dim * 2 : g4h_row_size(Q8_0, c.head_dim);
+    const size_t row = c.kv_type == F16 ? (size_t)c.head_dim * 2 : g4h_row_size(c.kv_type, c.head_dim);
     hipError_t e = hipSuccess;
     for (int i = 0; i < 2 * c.n_layer && e == hipSuccess; i++) {
         e = launch_rand_normal(tmp, n, seed * 7919 + i, 0.0f, 1.0f, s);

@@ -51,6 +51,45 @@ __device__ __forceinline__ void q8_store4(const float v[4], int gi, bool own, ui
     if (k == 0) *(uint16_t *)blk = f2h(am * (1.0f / 127.0f));
 }
 
+// q4_0 of four consecutive values (quants.c:125-144 as the reference build
+// computes it): the 8 consecutive lanes of a 32-element block all call this
+// (the block is owned by all of them or none).  max = the element of largest
+// |x| (first on ties), d = max * -0.125, id = 1/d, q = min(15,
+// trunc(fma(x, id, 8.5))); lane k < 4 of a block writes bytes 4k..4k+3
+// (elements 4k.. low nibbles, 16+4k.. high), its first lane the scale.
+__device__ __forceinline__ void q4_store4(const float v[4], int gi, bool own, uint8_t *dst) {
+    const int k = gi & 7;
+    float ba = fabsf(v[0]), bv = v[0];
+    int bi = 4 * k;
+#pragma unroll
+    for (int i = 1; i < 4; i++)
+        if (fabsf(v[i]) > ba) { ba = fabsf(v[i]); bv = v[i]; bi = 4 * k + i; }
+#pragma unroll
+    for (int m = 1; m < 8; m <<= 1) {
+        const float oa = shfl_xor(ba, m), ov = shfl_xor(bv, m);
+        const int oi = shfl_xor(bi, m);
+        if (oa > ba || (oa == ba && oi < bi)) { ba = oa; bv = ov; bi = oi; }
+    }
+    const float d = bv * -0.125f;
+    const float id = d != 0.0f ? 1.0f / d : 0.0f;
+    uint32_t q4 = 0;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        int q = (int)__builtin_fmaf(v[i], id, 8.5f);
+        q = q > 15 ? 15 : q;
+        q4 |= (uint32_t)q << (8 * i);
+    }
+    const uint32_t hi = shfl_xor(q4, 4);
+    if (own && k < 4) {
+        uint8_t *blk = dst + (size_t)(gi >> 3) * 18;
+        const uint32_t packed = q4 | (hi << 4);
+        uint16_t *p16 = (uint16_t *)(blk + 2 + 4 * k);
+        p16[0] = (uint16_t)(packed & 0xffff);
+        p16[1] = (uint16_t)(packed >> 16);
+        if (k == 0) *(uint16_t *)blk = f2h(d);
+    }
+}
+
 __device__ __forceinline__ float4 ldf4(const float *p) { return *(const float4 *)p; }
 __device__ __forceinline__ void f4(const float4 a, float o[4]) { o[0] = a.x; o[1] = a.y; o[2] = a.z; o[3] = a.w; }
 

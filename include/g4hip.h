@@ -153,7 +153,7 @@ int g4h_block_sums(const g4h_tensor *W, const void *pre_dev, size_t pre_stride, 
 /* ---------------------------------------------------------- attention ---- */
 /* Decode attention (attn_kernel, model.c:509-580) for one token: n_head query
  * heads (q_dev: n_head x hd fp32) over cached positions 0..n_pos-1.  Cache
- * rows [slot][n_kv][hd] in kv_type (G4H_F16 or G4H_Q8_0) for K and V; query
+ * rows [slot][n_kv][hd] in kv_type (G4H_F16, G4H_Q8_0 or G4H_Q4_0) for K and V; query
  * head h reads KV head h/(n_head/n_kv) (model.c:1099); no 1/sqrt(hd) factor
  * (model.c:538).  hd in {64,128,192,256}; n_head/n_kv in {1,2,4,8}.
  * ws_dev: g4h_attn_workspace_bytes() bytes of caller-owned scratch (the
@@ -188,7 +188,7 @@ typedef struct {
     float rope_base, rms_eps;
     int wtype;       /* layer weights: G4H_Q4_0 or G4H_Q8_0 */
     int head_type;   /* G4H_Q8_0 */
-    int kv_type;     /* G4H_F16 or G4H_Q8_0 */
+    int kv_type;     /* G4H_F16, G4H_Q8_0 or G4H_Q4_0 */
 } g4h_model_config;
 typedef struct g4h_model g4h_model;
 

@@ -30,7 +30,7 @@ def make_cache(G, oracle, kv_type, n_slot, n_kv, hd, seed):
     return kb, vb, kh, vh
 
 
-@pytest.mark.parametrize("kv_type", [1, 8], ids=["f16", "q8_0"])
+@pytest.mark.parametrize("kv_type", [1, 8, 2], ids=["f16", "q8_0", "q4_0"])
 @pytest.mark.parametrize("n_head,n_kv,hd,n_pos,qscale", [
     (8, 4, 256, 1, 1.0), (8, 4, 256, 65, 1.0), (8, 4, 256, 1000, 1.0), (8, 4, 256, 8192, 1.0),
     (8, 4, 256, 3000, 0.02), (4, 4, 128, 300, 0.1), (8, 1, 64, 777, 0.3), (16, 2, 192, 129, 1.0),

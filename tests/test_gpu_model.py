@@ -26,7 +26,7 @@ def oracle_model(oracle, G, m):
     return oracle.Model(ocfg, w, kc, vc)
 
 
-@pytest.mark.parametrize("kv_type,wtype", [(1, 2), (8, 2), (1, 8)], ids=["f16-q4_0", "q8_0-q4_0", "f16-q8_0"])
+@pytest.mark.parametrize("kv_type,wtype", [(1, 2), (8, 2), (2, 2), (1, 8)], ids=["f16-q4_0", "q8_0-q4_0", "q4_0-q4_0", "f16-q8_0"])
 def test_decode_steps_match_oracle(gpu, oracle, kv_type, wtype):
     G = gpu
     m = G.Model(seed=11, kv_type=kv_type, wtype=wtype, **SMALL)
@@ -73,8 +73,8 @@ def test_graph_replay_matches_eager(gpu):
         assert np.array_equal(m2.logits().view(np.uint32), eager[i][1].view(np.uint32))
 
 
-@pytest.mark.parametrize("kv_type,fuse", [(1, None), (8, None), (1, "19"), (1, "31")],
-                         ids=["f16-default", "q8_0-default", "f16-qkv-in-attention", "f16-all"])
+@pytest.mark.parametrize("kv_type,fuse", [(1, None), (8, None), (2, None), (1, "19"), (1, "31")],
+                         ids=["f16-default", "q8_0-default", "q4_0-default", "f16-qkv-in-attention", "f16-all"])
 def test_fused_step_equals_unfused(gpu, monkeypatch, kv_type, fuse):
     """The step with the residual norms folded into the Wqkv / Wgu prologues and
     GELU into the Wgu epilogue (the default), or with the Wqkv GEMV inside the
