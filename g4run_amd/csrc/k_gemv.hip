@@ -1,6 +1,9 @@
 // k_gemv.hip -- GEMV dispatch (kernel family in gemv.h, one instantiation unit
 // per weight format) and the per-block integer-sum instrument.
+#include <algorithm>
+
 #include "gemv.h"
+#include "gemv_p.h"
 
 namespace g4 {
 
@@ -148,7 +151,10 @@ hipError_t launch_gemv_p(const g4h_tensor &W, const uint8_t *act, float *Y, cons
     if (epi.kind == EPI_GELU ? (!epi.h || !epi.gelu) : !Y) return hipErrorInvalidValue;
     int lpr, upl;
     gemv_p_shape(W, epi, &lpr, &upl);
-    const int grid = gemv_p_grid_size();
+    // no more workgroups than row groups to give each wave one (a wave without
+    // a row group would still stream a clamped duplicate of the last row)
+    const int64_t groups = (W.nrows + 64 / lpr - 1) / (64 / lpr);
+    const int grid = (int)std::min<int64_t>(gemv_p_grid_size(), (groups + GP_WAVES - 1) / GP_WAVES);
     return W.type == Q8_0 ? launch_gemv_p_q8_0(W, act, Y, pro, epi, s, lpr, upl, grid)
                           : launch_gemv_p_q4_0(W, act, Y, pro, epi, s, lpr, upl, grid);
 }
