@@ -122,6 +122,20 @@ __global__ __launch_bounds__(64 * GP_WAVES) void k_gemv_p(g4h_tensor W, const ui
 #pragma unroll
         for (int k = 0; k < UPL; k++) F::load(fr[k], W, row, min(g + k * LPR, units - 1));
     };
+    // GELU epilogue, one row group behind: the table entry of a group's gate
+    // is loaded (every lane, unconditionally, behind the next group's weights)
+    // and used once the next group is done, so its latency is not waited for
+    // on its own.  gelu(x) = 0 for x <= -10, x for x >= 10, else the fp16
+    // table (g4run.h:73-77).
+    float p_gate = 0.0f, p_up = 0.0f;
+    uint16_t p_tab = 0;
+    int64_t p_row = -1;
+    auto gelu_flush = [&]() {
+        if (p_row >= 0 && g == 0 && (rg & 1) == 0 && p_row < W.nrows) {
+            const float gl = p_gate <= -10.0f ? 0.0f : p_gate >= 10.0f ? p_gate : h2f(p_tab);
+            epi.h[p_row >> 1] = gl * p_up;
+        }
+    };
     auto finish = [&](const typename F::Frag (&fr)[UPL], int64_t gq) {
         float acc = 0.0f;
         const Act A(lds, nb, 0);
@@ -134,7 +148,10 @@ __global__ __launch_bounds__(64 * GP_WAVES) void k_gemv_p(g4h_tensor W, const ui
         const int64_t row0 = gq * RPW + rg;
         if constexpr (EPI == EPI_GELU) {
             const float up = partner<LPR>(acc);                     // row 2i+1: lane ^ LPR (LPR 16 or 32)
-            if (g == 0 && (rg & 1) == 0 && row0 < W.nrows) epi.h[row0 >> 1] = gelu_lut(epi.gelu, acc) * up;
+            const uint16_t tab = epi.gelu[f2h(acc)];
+            issue_order();
+            gelu_flush();                                            // the previous group's output
+            p_gate = acc; p_up = up; p_tab = tab; p_row = row0;
         } else {
             if (g == 0 && row0 < W.nrows) Y[row0] = acc;
         }
@@ -165,6 +182,7 @@ __global__ __launch_bounds__(64 * GP_WAVES) void k_gemv_p(g4h_tensor W, const ui
         if (g3 < ngroups) load(fa, g3);
         finish(fb, g2);
     }
+    if constexpr (EPI == EPI_GELU) gelu_flush();
 }
 
 template <class F, int LPR, int UPL, int PRO, int EPI>
