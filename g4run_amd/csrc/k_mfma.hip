@@ -35,6 +35,7 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v16i __attribute__((ext_vector_type(16)));
 typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 typedef float v16f __attribute__((ext_vector_type(16)));
+typedef float v32f __attribute__((ext_vector_type(32)));
 
 constexpr int MM_KB_SMALL = 8;       // blocks per operand set, one-tile workgroups
 
@@ -158,14 +159,18 @@ __global__ __launch_bounds__(256) void k_mm_mfma(g4h_tensor W, const int8_t *__r
     }
 }
 
-// LDS-staged tiles for many tokens.  A workgroup of TM x TN waves owns a
-// (32 TM) token x (32 TN) row output tile; wave (im, in) its 32 x 32 subtile.
-// The K loop runs over stages of KB blocks: every thread loads a share of the
-// stage's activation and weight bytes (and fp16 scales) into registers while
-// the waves multiply the previous stage from LDS, then writes them to the other
-// LDS buffer.  Per block and subtile the arithmetic is that of k_mm_mfma: one
-// int8 MFMA for the exact block sums, one f16 MFMA for the scale outer product,
-// an fma into the accumulator of the block's residue mod 4, and at the end
+// LDS-staged tiles for many tokens (nb a multiple of KB).  A workgroup of
+// TM x TN waves owns a (32 TM) token x (32 TN) row output tile; wave (im, in)
+// its 32 x 32 subtile.  The K loop runs over stages of KB blocks: every thread
+// loads a share of the stage's activation and weight bytes into registers
+// (threads 0..BM+BN-1 also one 16-byte run of KB fp16 scales) while the waves
+// multiply the previous stage from LDS, then writes them to the other LDS
+// buffer, q4_0 nibbles unpacked to q - 8 and the scales widened to fp32 on the
+// way.  Per block and subtile the arithmetic is that of k_mm_mfma: one int8
+// MFMA for the exact block sums, the exact scale outer product d_a * d_w (here
+// two blocks' from one v_mfma_f32_32x32x1_2b_f32, lanes 0..31 block k and
+// 32..63 block k + 1: an fp16 x fp16 product is exact in fp32 either way), an
+// fma into the accumulator of the block's residue mod 4, and at the end
 // ((p0 + p1) + p2) + p3 -- so every output is bit-identical to k_mm_mfma's.
 constexpr int MML_KB = 8;                                           // blocks per stage
 
@@ -173,68 +178,70 @@ template <int WT, int TM, int TN, int KB>
 __global__ __launch_bounds__(64 * TM * TN) void k_mm_lds(g4h_tensor W, const int8_t *__restrict__ qa,
                                                          const uint16_t *__restrict__ da, int M, float *__restrict__ Y) {
     constexpr int BM = 32 * TM, BN = 32 * TN, NT = 64 * TM * TN;
-    constexpr int WB = WT == Q8_0 ? 32 : 16;                        // weight bytes per block
-    constexpr int AS = KB * 32 + 16, BS = KB * WB + 16;             // padded LDS row strides (bytes)
-    constexpr int AC = BM * KB * 2, BC = BN * KB * WB / 16;         // 16-byte chunks per stage
-    constexpr int APT = (AC + NT - 1) / NT, BPT = (BC + NT - 1) / NT;
-    __shared__ __align__(16) int8_t As[2][BM * AS];
-    __shared__ __align__(16) uint8_t Bs[2][BN * BS];
-    __shared__ __align__(16) uint16_t Ad[2][BM * KB], Bd[2][BN * KB];
+    constexpr int WB = WT == Q8_0 ? 32 : 16;                        // weight bytes per block in memory
+    constexpr int RS = KB * 32 + 16;                                // padded LDS row stride (bytes), A and B
+    constexpr int ACH = 2 * KB, BCH = KB * WB / 16;                 // 16-byte chunks per row and stage
+    constexpr int APT = BM * ACH / NT, BPT = BN * BCH / NT;
+    static_assert(BM * ACH % NT == 0 && BN * BCH % NT == 0 && NT % ACH == 0 && NT % BCH == 0, "tile shape");
+    static_assert(BM + BN <= NT && KB == 8, "one 16-byte scale run per thread");
+    constexpr int ZR = BM + BN;                                     // scale columns: tokens, then weight rows
+    __shared__ __align__(16) int8_t As[2][BM * RS];
+    __shared__ __align__(16) int8_t Bs[2][BN * RS];
+    __shared__ __align__(16) float Sd[2][KB * ZR];                  // [block][token | row]: lanes read along a row
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const int im = wave % TM, in = wave / TM;
     const int li = lane & 31, kh = lane >> 5;
-    const int nb = (int)W.nb, nst = (nb + KB - 1) / KB;
+    const int nb = (int)W.nb, nst = nb / KB;
     const int m0 = blockIdx.y * BM;
     const int64_t n0 = (int64_t)blockIdx.x * BN;
 
+    // per-thread load offsets (bytes from the stage's base); chunk c = t + i NT
+    uint32_t aoff[APT], boff[BPT];
+#pragma unroll
+    for (int i = 0; i < APT; i++) {
+        const int c = t + i * NT, r = c / ACH, q = c % ACH;
+        aoff[i] = (uint32_t)(((size_t)min(m0 + r, M - 1) * nb) * 32 + 16 * q);
+    }
+#pragma unroll
+    for (int i = 0; i < BPT; i++) {
+        const int c = t + i * NT, r = c / BCH, q = c % BCH;
+        boff[i] = (uint32_t)(((size_t)min(n0 + r, W.nrows - 1) * nb) * WB + 16 * q);
+    }
+    // threads past the scale rows load a weight row's run too and keep it
+    const uint16_t *psc = t < BM ? da + (size_t)min(m0 + t, M - 1) * nb
+                                 : (const uint16_t *)W.sc + (size_t)min(n0 + min(t - BM, BN - 1), W.nrows - 1) * nb;
+
     struct Stage {
-        v4i a[APT], b[BPT];
-        uint16_t sa[KB], sb[KB];                                    // kept as loaded: no wait at load time
+        v4i a[APT], b[BPT], s;
     };
-    // chunk c of the A stage: token row c / (2 KB), 16 bytes (c % (2 KB)) of its KB blocks
     auto load = [&](Stage &S, int s) {
+        const int8_t *ab = qa + (size_t)s * KB * 32;
+        const uint8_t *bb = W.qs + (size_t)s * KB * WB;
 #pragma unroll
-        for (int i = 0; i < APT; i++) {
-            const int c = min(t + i * NT, AC - 1), r = c / (2 * KB), q = c % (2 * KB);
-            const int m = min(m0 + r, M - 1), b = min(s * KB + q / 2, nb - 1);
-            S.a[i] = *(const v4i *)(qa + ((size_t)m * nb + b) * 32 + 16 * (q & 1));
-        }
+        for (int i = 0; i < APT; i++) S.a[i] = *(const v4i *)(ab + aoff[i]);
 #pragma unroll
-        for (int i = 0; i < BPT; i++) {
-            const int c = min(t + i * NT, BC - 1), r = c / (KB * WB / 16), q = c % (KB * WB / 16);
-            const int64_t n = min(n0 + r, W.nrows - 1);
-            const int b = min(s * KB + q * 16 / WB, nb - 1);
-            S.b[i] = *(const v4i *)(W.qs + ((size_t)n * nb + b) * WB + (WT == Q8_0 ? 16 * (q & 1) : 0));
-        }
-        // scales: thread r < BM loads token r's KB fp16 scales, r < BN row r's
-        const int ra = min(t, BM - 1), rb = min(t, BN - 1);
-        const int ma = min(m0 + ra, M - 1);
-        const int64_t nr = min(n0 + rb, W.nrows - 1);
-#pragma unroll
-        for (int k = 0; k < KB; k++) {
-            const int b = min(s * KB + k, nb - 1);
-            S.sa[k] = da[(size_t)ma * nb + b];
-            S.sb[k] = ((const uint16_t *)W.sc)[(size_t)nr * nb + b];
-        }
+        for (int i = 0; i < BPT; i++) S.b[i] = *(const v4i *)(bb + boff[i]);
+        S.s = *(const v4i *)(psc + (size_t)s * KB);
     };
     auto store = [&](const Stage &S, int buf) {
 #pragma unroll
         for (int i = 0; i < APT; i++) {
             const int c = t + i * NT;
-            if (c < AC) *(v4i *)&As[buf][(c / (2 * KB)) * AS + 16 * (c % (2 * KB))] = S.a[i];
+            *(v4i *)&As[buf][(c / ACH) * RS + 16 * (c % ACH)] = S.a[i];
         }
 #pragma unroll
         for (int i = 0; i < BPT; i++) {
-            const int c = t + i * NT;
-            if (c < BC) *(v4i *)&Bs[buf][(c / (KB * WB / 16)) * BS + 16 * (c % (KB * WB / 16))] = S.b[i];
+            const int c = t + i * NT, r = c / BCH, q = c % BCH;
+            if constexpr (WT == Q8_0) {
+                *(v4i *)&Bs[buf][r * RS + 16 * q] = S.b[i];
+            } else {                                                    // block q: elements 0..15, 16..31
+                *(v4i *)&Bs[buf][r * RS + 32 * q] = q4_half(S.b[i], 0);
+                *(v4i *)&Bs[buf][r * RS + 32 * q + 16] = q4_half(S.b[i], 1);
+            }
         }
-        if (t < BM) {
+        if (t < ZR) {
 #pragma unroll
-            for (int k = 0; k < KB; k++) Ad[buf][t * KB + k] = S.sa[k];
-        }
-        if (t < BN) {
-#pragma unroll
-            for (int k = 0; k < KB; k++) Bd[buf][t * KB + k] = S.sb[k];
+            for (int j = 0; j < KB; j++) Sd[buf][j * ZR + t] = h2f((uint16_t)((uint32_t)S.s[j / 2] >> (16 * (j & 1))));
         }
     };
 
@@ -244,62 +251,76 @@ __global__ __launch_bounds__(64 * TM * TN) void k_mm_lds(g4h_tensor W, const int
 #pragma unroll
         for (int r = 0; r < 16; r++) acc[q][r] = 0.0f;
     const v16i zi = {};
-    const v16f zf = {};
-    // one block's two MFMAs (exact integer sums; the scale outer product)
-    auto mfmas = [&](int cur, int k, v16i &is, v16f &sc) {
-        const int8_t *arow = &As[cur][(32 * im + li) * AS + 16 * kh];
-        const uint8_t *brow = &Bs[cur][(32 * in + li) * BS + (WT == Q8_0 ? 16 * kh : 0)];
-        const v4i av = *(const v4i *)(arow + 32 * k);
-        const v4i wraw = *(const v4i *)(brow + WB * k);
-        const v4i wv = WT == Q8_0 ? wraw : q4_half(wraw, kh);
-        is = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, wv, zi, 0, 0, 0);
-        v8h ha = {}, hw = {};
-        if (kh == 0) {
-            ha[0] = __builtin_bit_cast(_Float16, Ad[cur][(32 * im + li) * KB + k]);
-            hw[0] = __builtin_bit_cast(_Float16, Bd[cur][(32 * in + li) * KB + k]);
-        }
-        sc = __builtin_amdgcn_mfma_f32_32x32x16_f16(ha, hw, zf, 0, 0, 0);
+    const int arow = (32 * im + li) * RS + 16 * kh, brow = (32 * in + li) * RS + 16 * kh;
+    const int sacol = kh * ZR + 32 * im + li, sbcol = kh * ZR + BM + 32 * in + li;
+    const v32f zf32 = {};
+    // block k's exact integer sums
+    auto isum = [&](int cur, int k) {
+        const v4i av = *(const v4i *)&As[cur][arow + 32 * k];
+        const v4i wv = *(const v4i *)&Bs[cur][brow + 32 * k];
+        return __builtin_amdgcn_mfma_i32_32x32x32_i8(av, wv, zi, 0, 0, 0);
     };
-    auto epi = [&](int b, const v16i &is, const v16f &sc) {
-        v16f &p = acc[b & 3];
+    // scale outer products of blocks k, k + 1 (k even): registers 0..15, 16..31
+    auto scales = [&](int cur, int k) {
+        return __builtin_amdgcn_mfma_f32_32x32x1f32(Sd[cur][k * ZR + sacol], Sd[cur][k * ZR + sbcol], zf32, 0, 0, 0);
+    };
+    // the empty asm pins the block's fmas here: left alone the compiler sinks
+    // every epilogue of the stage below the LDS stores, which keeps all the
+    // stage's MFMA results live at once
+    auto epi = [&](int k, const v16i &is, const v32f &sc) {
+        v16f &p = acc[k & 3];                                       // KB % 4 == 0: residue of the block
+        const int o = 16 * (k & 1);
 #pragma unroll
-        for (int r = 0; r < 16; r++) p[r] = __builtin_fmaf((float)is[r], sc[r], p[r]);
+        for (int r = 0; r < 16; r++) {
+            p[r] = __builtin_fmaf((float)is[r], sc[o + r], p[r]);
+            asm volatile("" : "+v"(p[r]));
+        }
     };
     // software-pipelined over the stage's blocks: block k + 1's MFMAs are
     // issued before block k's epilogue, so the VALU work of one block runs
-    // while the matrix cores work on the next
+    // while the matrix cores work on the next; the scheduling barriers keep
+    // the compiler from hoisting every MFMA of the stage (which would need
+    // more registers than a wave has)
     auto compute = [&](int s) {
         const int cur = s & 1;
-        const int kn = min(KB, nb - s * KB);                         // blocks in this stage (uniform)
-        v16i is0, is1;
-        v16f sc0, sc1;
-        mfmas(cur, 0, is0, sc0);
+        v16i is0 = isum(cur, 0), is1;
+        v32f sc[2];
+        sc[0] = scales(cur, 0);
 #pragma unroll
         for (int k = 0; k < KB; k += 2) {
-            if (k + 1 < kn) mfmas(cur, k + 1, is1, sc1);
-            if (k < kn) epi(s * KB + k, is0, sc0);
-            if (k + 2 < kn) mfmas(cur, k + 2, is0, sc0);
-            if (k + 1 < kn) epi(s * KB + k + 1, is1, sc1);
+            is1 = isum(cur, k + 1);
+            epi(k, is0, sc[(k >> 1) & 1]);
+            __builtin_amdgcn_sched_barrier(0);
+            if (k + 2 < KB) {
+                is0 = isum(cur, k + 2);
+                sc[((k >> 1) + 1) & 1] = scales(cur, k + 2);
+            }
+            epi(k + 1, is1, sc[(k >> 1) & 1]);
+            __builtin_amdgcn_sched_barrier(0);
         }
     };
     // two stages of loads in flight: while stage s is multiplied from LDS, the
     // registers hold stage s + 1 (loaded one stage earlier, stored to LDS after
-    // the multiply) and receive stage s + 2
+    // the multiply) and receive stage s + 2.  Every load is issued on every
+    // pass (past the end it repeats the last stage) and every store made, so
+    // the memory counter waits before a store cover only the stage stored, not
+    // the one just issued.
     Stage S0, S1;
     load(S0, 0);
-    if (nst > 1) load(S1, 1);
+    load(S1, min(1, nst - 1));
     store(S0, 0);
     __syncthreads();
-    for (int s = 0; s < nst; s += 2) {
-        if (s + 2 < nst) load(S0, s + 2);
+    for (int s = 0;; s += 2) {                                      // uniform
+        load(S0, min(s + 2, nst - 1));
         compute(s);
-        if (s + 1 < nst) store(S1, 1);
+        store(S1, 1);
         __syncthreads();
         if (s + 1 >= nst) break;
-        if (s + 3 < nst) load(S1, s + 3);
+        load(S1, min(s + 3, nst - 1));
         compute(s + 1);
-        if (s + 2 < nst) store(S0, 0);
+        store(S0, 0);
         __syncthreads();
+        if (s + 2 >= nst) break;
     }
     v16f out = acc[0];
 #pragma unroll
@@ -362,14 +383,18 @@ size_t mm_planar_bytes(int M, int64_t ncols) {
 }
 
 // One 32 x 32 tile per workgroup with the blocks split over 4 waves while
-// that gives at most 3 workgroups per CU, LDS-staged 64 x 128 tiles beyond.
+// that gives at most 3 workgroups per CU, LDS-staged 64 x 128 tiles beyond
+// (those need nb % 8 == 0 and 32-bit operand offsets; other shapes stay on the
+// one-tile kernel, whose outputs are the same bits).
 // Measured on q8_0 4096 x 4096: 128 tokens 39 us split / 58 us staged, 256
 // tokens 68 / 58 us, 512 tokens 128 / 61 us (the staged kernel runs at about
 // the same time for any token count: its per-workgroup latency, not the
 // memory system, bounds it).
 static bool mm_small(const g4h_tensor &W, int M) {
     const int64_t tiles = ((W.nrows + 31) / 32) * ((M + 31) / 32);
-    return tiles <= 3 * 256;
+    const uint64_t wb = W.type == Q8_0 ? 32 : 16;
+    return tiles <= 3 * 256 || W.nb % MML_KB != 0 || (uint64_t)M * W.nb * 32 >= (1ull << 32) ||
+           (uint64_t)W.nrows * W.nb * wb >= (1ull << 32);
 }
 
 void mm_describe(const g4h_tensor &W, int M, char *buf, size_t len) {
@@ -414,7 +439,6 @@ hipError_t launch_matmul_mfma(const g4h_tensor &W, const float *x, size_t x_stri
     const dim3 grid((unsigned)((W.nrows + 127) / 128), (unsigned)((M + 63) / 64));
     if (W.type == Q8_0) hipLaunchKernelGGL((k_mm_lds<Q8_0, 2, 4, MML_KB>), grid, dim3(512), 0, s, W, qa, da, M, Y);
     else hipLaunchKernelGGL((k_mm_lds<Q4_0, 2, 4, MML_KB>), grid, dim3(512), 0, s, W, qa, da, M, Y);
-    return hipGetLastError();
     return hipGetLastError();
 }
 

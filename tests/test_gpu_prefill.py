@@ -43,14 +43,21 @@ def test_ragged_shapes(gpu, oracle, qt):
 
 
 @pytest.mark.parametrize("qt", [8, 2])
-def test_token_results_independent_of_batch(gpu, oracle, qt):
+@pytest.mark.parametrize("rows,cols,M", [(384, 2048, 512), (4096, 512, 256)])
+def test_token_results_independent_of_batch(gpu, oracle, qt, rows, cols, M):
     """Within the matrix-core family a token's outputs are bit-identical for any
-    batch size (small-M and large-M tile variants keep the same fp32 order)."""
-    w, x, t = _setup(gpu, qt, 384, 2048, 512, seed=5)
-    full = gpu_matmul(gpu, t, x=x, nb=512, path=2)
-    for M in (16, 40, 64, 65, 200):
-        part = gpu_matmul(gpu, t, x=x[:M].copy(), nb=M, path=2)
-        assert np.array_equal(bits(part), bits(full[:M])), f"M={M}"
+    batch size (small-M and large-M tile variants keep the same fp32 order).
+    4096 rows x 256 tokens run the LDS-staged tiles, the smaller batches the
+    one-tile kernel."""
+    w, x, t = _setup(gpu, qt, rows, cols, M, seed=5)
+    full = gpu_matmul(gpu, t, x=x, nb=M, path=2)
+    if rows == 4096:
+        assert gpu.matmul_describe(t, M, 2).startswith("k_mm_lds")
+        assert gpu.matmul_describe(t, 16, 2).startswith("k_mm_mfma")
+        assert_close(full, oracle_matmul(oracle, qt, w, x), f"{rows}x{cols} M={M}")
+    for m in (16, 40, 64, 65, 200):
+        part = gpu_matmul(gpu, t, x=x[:m].copy(), nb=m, path=2)
+        assert np.array_equal(bits(part), bits(full[:m])), f"M={m}"
 
 
 @pytest.mark.parametrize("qt", [8, 2])
