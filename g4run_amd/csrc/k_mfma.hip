@@ -174,8 +174,8 @@ __global__ __launch_bounds__(256) void k_mm_mfma(g4h_tensor W, const int8_t *__r
 // ((p0 + p1) + p2) + p3 -- so every output is bit-identical to k_mm_mfma's.
 constexpr int MML_KB = 8;                                           // blocks per stage
 
-template <int WT, int TM, int TN, int KB>
-__global__ __launch_bounds__(64 * TM * TN) void k_mm_lds(g4h_tensor W, const int8_t *__restrict__ qa,
+template <int WT, int TM, int TN, int KB, int RST>
+__global__ __launch_bounds__(64 * TM * TN, 2) void k_mm_lds(g4h_tensor W, const int8_t *__restrict__ qa,
                                                          const uint16_t *__restrict__ da, int M, float *__restrict__ Y) {
     constexpr int BM = 32 * TM, BN = 32 * TN, NT = 64 * TM * TN;
     constexpr int WB = WT == Q8_0 ? 32 : 16;                        // weight bytes per block in memory
@@ -254,73 +254,103 @@ __global__ __launch_bounds__(64 * TM * TN) void k_mm_lds(g4h_tensor W, const int
     const int arow = (32 * im + li) * RS + 16 * kh, brow = (32 * in + li) * RS + 16 * kh;
     const int sacol = kh * ZR + 32 * im + li, sbcol = kh * ZR + BM + 32 * in + li;
     const v32f zf32 = {};
-    // block k's exact integer sums
-    auto isum = [&](int cur, int k) {
-        const v4i av = *(const v4i *)&As[cur][arow + 32 * k];
-        const v4i wv = *(const v4i *)&Bs[cur][brow + 32 * k];
-        return __builtin_amdgcn_mfma_i32_32x32x32_i8(av, wv, zi, 0, 0, 0);
+    // block k's operands, and its exact integer sums
+    struct Opnd {
+        v4i a, w;
     };
-    // scale outer products of blocks k, k + 1 (k even): registers 0..15, 16..31
-    auto scales = [&](int cur, int k) {
-        return __builtin_amdgcn_mfma_f32_32x32x1f32(Sd[cur][k * ZR + sacol], Sd[cur][k * ZR + sbcol], zf32, 0, 0, 0);
+    auto opnd = [&](int cur, int k) {
+        return Opnd{*(const v4i *)&As[cur][arow + 32 * k], *(const v4i *)&Bs[cur][brow + 32 * k]};
     };
+    auto isum = [&](const Opnd &o) { return __builtin_amdgcn_mfma_i32_32x32x32_i8(o.a, o.w, zi, 0, 0, 0); };
+    // scale outer products of blocks k, k + 1 (k even) from the operands read
+    // at (cur, k): registers 0..15, 16..31
+    struct Sop {
+        float a, b;
+    };
+    auto sop = [&](int cur, int k) { return Sop{Sd[cur][k * ZR + sacol], Sd[cur][k * ZR + sbcol]}; };
+    auto scales = [&](const Sop &o) { return __builtin_amdgcn_mfma_f32_32x32x1f32(o.a, o.b, zf32, 0, 0, 0); };
     // the empty asm pins the block's fmas here: left alone the compiler sinks
     // every epilogue of the stage below the LDS stores, which keeps all the
     // stage's MFMA results live at once
-    auto epi = [&](int k, const v16i &is, const v32f &sc) {
+    auto epi = [&](int k, const v16i &is, const v32f &sc, int r0 = 0, int r1 = 16) {
         v16f &p = acc[k & 3];                                       // KB % 4 == 0: residue of the block
         const int o = 16 * (k & 1);
 #pragma unroll
-        for (int r = 0; r < 16; r++) {
+        for (int r = r0; r < r1; r++) {
             p[r] = __builtin_fmaf((float)is[r], sc[o + r], p[r]);
             asm volatile("" : "+v"(p[r]));
         }
     };
-    // software-pipelined over the stage's blocks: block k + 1's MFMAs are
-    // issued before block k's epilogue, so the VALU work of one block runs
-    // while the matrix cores work on the next; the scheduling barriers keep
-    // the compiler from hoisting every MFMA of the stage (which would need
-    // more registers than a wave has)
+    // software-pipelined over the stage's blocks: block k + 1's integer MFMA
+    // and the next pair's scale MFMA are issued before block k's epilogue, so
+    // the VALU work of one block runs while the matrix cores work ahead of it;
+    // every LDS operand is read one epilogue before its MFMA.  The scheduling
+    // barriers keep the compiler from hoisting every MFMA of the stage (which
+    // would need more registers than a wave has).
     auto compute = [&](int s) {
         const int cur = s & 1;
-        v16i is0 = isum(cur, 0), is1;
+        Opnd o0 = opnd(cur, 0), o1 = opnd(cur, 1);
+        Sop so = sop(cur, 0);
+        v16i is0 = isum(o0), is1;
         v32f sc[2];
-        sc[0] = scales(cur, 0);
+        sc[0] = scales(so);
+        if (KB > 2) so = sop(cur, 2);
 #pragma unroll
         for (int k = 0; k < KB; k += 2) {
-            is1 = isum(cur, k + 1);
-            epi(k, is0, sc[(k >> 1) & 1]);
+            const int p = k >> 1;
+            is1 = isum(o1);
+            if (k + 2 < KB) o0 = opnd(cur, k + 2);
+            epi(k, is0, sc[p & 1], 0, 8);                            // the matrix core runs is1 meanwhile
+            __builtin_amdgcn_sched_barrier(0);
+            if (k + 2 < KB) sc[(p + 1) & 1] = scales(so);
+            epi(k, is0, sc[p & 1], 8, 16);
             __builtin_amdgcn_sched_barrier(0);
             if (k + 2 < KB) {
-                is0 = isum(cur, k + 2);
-                sc[((k >> 1) + 1) & 1] = scales(cur, k + 2);
+                is0 = isum(o0);
+                o1 = opnd(cur, k + 3);
+                if (k + 4 < KB) so = sop(cur, k + 4);
             }
-            epi(k + 1, is1, sc[(k >> 1) & 1]);
+            epi(k + 1, is1, sc[p & 1]);
             __builtin_amdgcn_sched_barrier(0);
         }
     };
-    // two stages of loads in flight: while stage s is multiplied from LDS, the
-    // registers hold stage s + 1 (loaded one stage earlier, stored to LDS after
-    // the multiply) and receive stage s + 2.  Every load is issued on every
-    // pass (past the end it repeats the last stage) and every store made, so
-    // the memory counter waits before a store cover only the stage stored, not
-    // the one just issued.
-    Stage S0, S1;
-    load(S0, 0);
-    load(S1, min(1, nst - 1));
-    store(S0, 0);
-    __syncthreads();
-    for (int s = 0;; s += 2) {                                      // uniform
-        load(S0, min(s + 2, nst - 1));
-        compute(s);
-        store(S1, 1);
-        __syncthreads();
-        if (s + 1 >= nst) break;
-        load(S1, min(s + 3, nst - 1));
-        compute(s + 1);
+    // RST = 2: two stages of loads in flight: while stage s is multiplied
+    // from LDS, the registers hold stage s + 1 (loaded one stage earlier,
+    // stored to LDS after the multiply) and receive stage s + 2.  RST = 1: the
+    // registers receive stage s + 1 only (fewer registers).  Every load is
+    // issued on every pass (past the end it repeats the last stage) and every
+    // store made, so the memory counter waits before a store cover only the
+    // stage stored, not the one just issued.
+    if constexpr (RST == 2) {
+        Stage S0, S1;
+        load(S0, 0);
+        load(S1, min(1, nst - 1));
         store(S0, 0);
         __syncthreads();
-        if (s + 2 >= nst) break;
+        for (int s = 0;; s += 2) {                                  // uniform
+            load(S0, min(s + 2, nst - 1));
+            compute(s);
+            store(S1, 1);
+            __syncthreads();
+            if (s + 1 >= nst) break;
+            load(S1, min(s + 3, nst - 1));
+            compute(s + 1);
+            store(S0, 0);
+            __syncthreads();
+            if (s + 2 >= nst) break;
+        }
+    } else {
+        Stage S0;
+        load(S0, 0);
+        store(S0, 0);
+        __syncthreads();
+        for (int s = 0;; s++) {                                     // uniform
+            load(S0, min(s + 1, nst - 1));
+            compute(s);
+            store(S0, (s + 1) & 1);
+            __syncthreads();
+            if (s + 1 >= nst) break;
+        }
     }
     v16f out = acc[0];
 #pragma unroll
@@ -339,25 +369,34 @@ __global__ __launch_bounds__(64 * TM * TN) void k_mm_lds(g4h_tensor W, const int
 }
 
 // x fp32 [M][ncols] (row stride xs floats) -> planar q8_0 with the quantizer
-// arithmetic of quants.c:74-109 (8 lanes per block).
+// arithmetic of quants.c:74-109 (8 lanes per block).  A thread quantizes QP
+// groups of 4 inputs, 256 groups apart, all loads issued first.
+constexpr int QP = 4;
 __global__ __launch_bounds__(256) void k_quantize_planar(const float *__restrict__ x, size_t xs, int64_t ncols, int M,
                                                          int8_t *__restrict__ qa, uint16_t *__restrict__ da) {
-    const int64_t ng = ncols / 4;
-    const int64_t gi = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int64_t ng = ncols / 4, nb = ncols / 32;
     const int m = blockIdx.y;
-    const bool own = gi < ng;
-    float v[4] = {0.f, 0.f, 0.f, 0.f};
-    if (own) f4(ldf4(x + (size_t)m * xs + 4 * gi), v);
-    float am = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
-    am = group_max<8>(am);
-    if (!own) return;
-    const float id = am != 0.0f ? 127.0f / am : 0.0f;
-    uint32_t pk = 0;
+    float v[QP][4];
 #pragma unroll
-    for (int j = 0; j < 4; j++) pk |= ((uint32_t)(int)__builtin_rintf(v[j] * id) & 0xffu) << (8 * j);
-    const int64_t nb = ncols / 32;
-    *(uint32_t *)(qa + ((size_t)m * nb) * 32 + 4 * gi) = pk;
-    if ((gi & 7) == 0) da[(size_t)m * nb + gi / 8] = f2h(am * (1.0f / 127.0f));
+    for (int j = 0; j < QP; j++) {
+        const int64_t gi = (int64_t)blockIdx.x * 256 * QP + j * 256 + threadIdx.x;
+        if (gi < ng) f4(ldf4(x + (size_t)m * xs + 4 * gi), v[j]);
+        else v[j][0] = v[j][1] = v[j][2] = v[j][3] = 0.0f;
+    }
+#pragma unroll
+    for (int j = 0; j < QP; j++) {
+        const int64_t gi = (int64_t)blockIdx.x * 256 * QP + j * 256 + threadIdx.x;
+        float am = fmaxf(fmaxf(fabsf(v[j][0]), fabsf(v[j][1])), fmaxf(fabsf(v[j][2]), fabsf(v[j][3])));
+        am = group_max<8>(am);
+        const float id = am != 0.0f ? 127.0f / am : 0.0f;
+        uint32_t pk = 0;
+#pragma unroll
+        for (int e = 0; e < 4; e++) pk |= ((uint32_t)(int)__builtin_rintf(v[j][e] * id) & 0xffu) << (8 * e);
+        if (gi < ng) {
+            *(uint32_t *)(qa + ((size_t)m * nb) * 32 + 4 * gi) = pk;
+            if ((gi & 7) == 0) da[(size_t)m * nb + gi / 8] = f2h(am * (1.0f / 127.0f));
+        }
+    }
 }
 
 // GGUF q8_0 activation rows (stride bytes) -> planar
@@ -397,14 +436,24 @@ static bool mm_small(const g4h_tensor &W, int M) {
            (uint64_t)W.nrows * W.nb * wb >= (1ull << 32);
 }
 
+// Staged tile shape: 64 x 128 (8 waves, two register stages) when that still
+// gives every CU a workgroup, else 64 x 64 (4 waves, one register stage).
+// Measured on q8_0 4096 x 4096: 256 tokens 26.4 us as 64 x 64 / 35.7 us as
+// 64 x 128; 512 tokens 41.7 / 40.4 us.  Both give the same bits.
+static bool mm_wide(const g4h_tensor &W, int M) { return ((W.nrows + 127) / 128) * ((M + 63) / 64) >= 256; }
+
 void mm_describe(const g4h_tensor &W, int M, char *buf, size_t len) {
+    const char *tn = W.type == Q8_0 ? "q8_0" : "q4_0";
     if (mm_small(W, M)) {
-        snprintf(buf, len, "k_mm_mfma<%s,wm=1,wn=1,ks=4,kb=%d> grid=%lldx%d block=256", W.type == Q8_0 ? "q8_0" : "q4_0",
-                 MM_KB_SMALL, (long long)((W.nrows + 31) / 32), (M + 31) / 32);
-        return;
+        snprintf(buf, len, "k_mm_mfma<%s,wm=1,wn=1,ks=4,kb=%d> grid=%lldx%d block=256", tn, MM_KB_SMALL,
+                 (long long)((W.nrows + 31) / 32), (M + 31) / 32);
+    } else if (mm_wide(W, M)) {
+        snprintf(buf, len, "k_mm_lds<%s,tm=2,tn=4,kb=%d,rst=2> grid=%lldx%d block=512", tn, MML_KB,
+                 (long long)((W.nrows + 127) / 128), (M + 63) / 64);
+    } else {
+        snprintf(buf, len, "k_mm_lds<%s,tm=2,tn=2,kb=%d,rst=1> grid=%lldx%d block=256", tn, MML_KB,
+                 (long long)((W.nrows + 63) / 64), (M + 63) / 64);
     }
-    snprintf(buf, len, "k_mm_lds<%s,tm=2,tn=4,kb=%d> grid=%lldx%d block=512", W.type == Q8_0 ? "q8_0" : "q4_0", MML_KB,
-             (long long)((W.nrows + 127) / 128), (M + 63) / 64);
 }
 
 template <int WT, int WM, int WN, int KS, int KB>
@@ -424,7 +473,7 @@ hipError_t launch_matmul_mfma(const g4h_tensor &W, const float *x, size_t x_stri
     int8_t *qa = (int8_t *)ws;
     uint16_t *da = (uint16_t *)(ws + (((size_t)M * nb * 32 + 255) & ~(size_t)255));
     if (x) {
-        hipLaunchKernelGGL(k_quantize_planar, dim3((unsigned)((W.ncols / 4 + 255) / 256), M), dim3(256), 0, s, x, x_stride,
+        hipLaunchKernelGGL(k_quantize_planar, dim3((unsigned)((W.ncols / 4 + 256 * QP - 1) / (256 * QP)), M), dim3(256), 0, s, x, x_stride,
                            W.ncols, M, qa, da);
     } else {
         const int64_t n = (int64_t)M * nb * 4;
@@ -436,9 +485,15 @@ hipError_t launch_matmul_mfma(const g4h_tensor &W, const float *x, size_t x_stri
         if (W.type == Q8_0) return mm_go<Q8_0, 1, 1, 4, MM_KB_SMALL>(W, qa, da, M, Y, s);
         return mm_go<Q4_0, 1, 1, 4, MM_KB_SMALL>(W, qa, da, M, Y, s);
     }
-    const dim3 grid((unsigned)((W.nrows + 127) / 128), (unsigned)((M + 63) / 64));
-    if (W.type == Q8_0) hipLaunchKernelGGL((k_mm_lds<Q8_0, 2, 4, MML_KB>), grid, dim3(512), 0, s, W, qa, da, M, Y);
-    else hipLaunchKernelGGL((k_mm_lds<Q4_0, 2, 4, MML_KB>), grid, dim3(512), 0, s, W, qa, da, M, Y);
+    if (mm_wide(W, M)) {
+        const dim3 grid((unsigned)((W.nrows + 127) / 128), (unsigned)((M + 63) / 64));
+        if (W.type == Q8_0) hipLaunchKernelGGL((k_mm_lds<Q8_0, 2, 4, MML_KB, 2>), grid, dim3(512), 0, s, W, qa, da, M, Y);
+        else hipLaunchKernelGGL((k_mm_lds<Q4_0, 2, 4, MML_KB, 2>), grid, dim3(512), 0, s, W, qa, da, M, Y);
+    } else {
+        const dim3 grid((unsigned)((W.nrows + 63) / 64), (unsigned)((M + 63) / 64));
+        if (W.type == Q8_0) hipLaunchKernelGGL((k_mm_lds<Q8_0, 2, 2, MML_KB, 1>), grid, dim3(256), 0, s, W, qa, da, M, Y);
+        else hipLaunchKernelGGL((k_mm_lds<Q4_0, 2, 2, MML_KB, 1>), grid, dim3(256), 0, s, W, qa, da, M, Y);
+    }
     return hipGetLastError();
 }
 
