@@ -144,7 +144,9 @@ extern "C" int g4h_graph_launch(void *exec, void *s) { G4_HIP(hipGraphLaunch((hi
 extern "C" int g4h_graph_destroy(void *exec) { G4_HIP(hipGraphExecDestroy((hipGraphExec_t)exec)); return G4H_OK; }
 
 // ------------------------------------------------------------- sizes ----
-static bool supported(int t) { return t == Q4_0 || t == Q8_0 || t == Q2_K || t == Q3_K || t == Q4_K || t == Q5_K || t == Q6_K; }
+static bool supported(int t) {
+    return t == Q4_0 || t == Q8_0 || t == Q2_K || t == Q3_K || t == Q4_K || t == Q5_K || t == Q6_K || t == TQ2_0;
+}
 
 extern "C" size_t g4h_row_size(int type, int64_t n) {
     const int b = blck(type);
@@ -154,7 +156,7 @@ extern "C" size_t g4h_row_size(int type, int64_t n) {
 extern "C" int g4h_act_type(int wtype) {
     switch (wtype) {
     case Q4_0: case Q8_0: return Q8_0;
-    case Q2_K: case Q3_K: case Q4_K: case Q5_K: case Q6_K: return Q8_K;
+    case Q2_K: case Q3_K: case Q4_K: case Q5_K: case Q6_K: case TQ2_0: return Q8_K;
     default: return -1;
     }
 }
@@ -268,6 +270,7 @@ extern "C" int g4h_tensor_create(int type, int64_t ncols, int64_t nrows, g4h_ten
     case Q2_K: qs = n * 64; sc = n * 16; ex = n * 4; break;
     case Q3_K: qs = n * 64; ex = n * 32; sc = n * 12; dd = n * 2; break;
     case Q6_K: qs = n * 128; ex = n * 64; sc = n * 16; dd = n * 2; break;
+    case TQ2_0: qs = n * 64; sc = n * 2; break;
     }
     const size_t total = al256(qs) + al256(sc) + al256(ex) + al256(dd);
     g4h_tensor *t = new g4h_tensor();
@@ -379,6 +382,7 @@ static const char *type_name(int t) {
     case Q3_K: return "q3_K";
     case Q5_K: return "q5_K";
     case Q6_K: return "q6_K";
+    case TQ2_0: return "tq2_0";
     case Q4_K: return "q4_K";
     default: return "?";
     }

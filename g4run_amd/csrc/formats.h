@@ -202,6 +202,7 @@ template <> struct StageOf<Q3_K> { using S = StageQ8_K; };
 template <> struct StageOf<Q4_K> { using S = StageQ8_K; };
 template <> struct StageOf<Q5_K> { using S = StageQ8_K; };
 template <> struct StageOf<Q6_K> { using S = StageQ8_K; };
+template <> struct StageOf<TQ2_0> { using S = StageQ8_K; };
 
 // ------------------------------------------------------------------ q8_0 --
 struct FQ8_0 {
@@ -525,6 +526,45 @@ struct FQ6_K {
             total += sc * (s - 32 * bs[8 * h + 2 * j + k]);
         }
         return total;
+    }
+    static __device__ __forceinline__ float accum(const Frag &f, const Act &A, int u, float acc) {
+        return __builtin_fmaf(A.d(u >> 2) * h2f(f.d), (float)isum(f, A, u), acc);
+    }
+    static constexpr int nsums = 1;
+    static __device__ __forceinline__ void sums(const Frag &f, const Act &A, int u, int *out) { out[0] = isum(f, A, u); }
+};
+
+// ----------------------------------------------------------------- tq2_0 --
+// 66-byte superblock: 64 bytes of trits and an fp16 d (g4run.h:111).  Element
+// e = 128h + 32j + 16k + l is (qs[32h + 16k + l] >> 2j) & 3, value trit - 1
+// (quants.c:402-411, 564-580): q2_K's quant layout without its scales.  So
+// sum (t - 1) a = sum t a - the unit's four 16-element activation group sums.
+struct FTQ2_0 {
+    static constexpr int type = TQ2_0;
+    using Act = ActQ8_K;
+    static constexpr int units_per_block = 4;
+    struct Frag { int4 q; uint16_t d; };
+    static __device__ __forceinline__ void load(Frag &f, const g4h_tensor &W, int64_t row, int u) {
+        const size_t j = (size_t)row * W.nb + (u >> 2);
+        f.q = ld4s(W.qs + j * 64 + 16 * (u & 3));
+        f.d = ((const uint16_t *)W.sc)[j];
+    }
+    static __device__ __forceinline__ int isum(const Frag &f, const Act &A, int u) {
+        const int sb = u >> 2, p = u & 3, h = p >> 1, k = p & 1;
+        const uint32_t w[4] = {(uint32_t)f.q.x, (uint32_t)f.q.y, (uint32_t)f.q.z, (uint32_t)f.q.w};
+        const int8_t *aq = A.q(sb) + 128 * h + 16 * k;
+        const int16_t *bs = A.bs(sb);
+        int s = 0, b = 0;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int4 a = *(const int4 *)(aq + 32 * j);
+            s = dot4((w[0] >> (2 * j)) & 0x03030303, a.x, s);
+            s = dot4((w[1] >> (2 * j)) & 0x03030303, a.y, s);
+            s = dot4((w[2] >> (2 * j)) & 0x03030303, a.z, s);
+            s = dot4((w[3] >> (2 * j)) & 0x03030303, a.w, s);
+            b += bs[8 * h + 2 * j + k];
+        }
+        return s - b;
     }
     static __device__ __forceinline__ float accum(const Frag &f, const Act &A, int u, float acc) {
         return __builtin_fmaf(A.d(u >> 2) * h2f(f.d), (float)isum(f, A, u), acc);

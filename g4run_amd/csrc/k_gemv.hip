@@ -14,6 +14,7 @@ hipError_t launch_gemv_q3_K(const g4h_tensor &, const uint8_t *, size_t, const f
 hipError_t launch_gemv_q5_K(const g4h_tensor &, const uint8_t *, size_t, const float *, float *, int, hipStream_t, int, int);
 hipError_t launch_gemv_q6_K(const g4h_tensor &, const uint8_t *, size_t, const float *, float *, int, hipStream_t, int, int);
 hipError_t launch_gemv_q2_K(const g4h_tensor &, const uint8_t *, size_t, const float *, float *, int, hipStream_t, int, int);
+hipError_t launch_gemv_tq2_0(const g4h_tensor &, const uint8_t *, size_t, const float *, float *, int, hipStream_t, int, int);
 
 // Exact per-block integer sums of every row against token `tok`: one thread
 // per (row, block); the parts of a superblock are added as integers.
@@ -79,6 +80,7 @@ static hipError_t gemv_dispatch(const g4h_tensor &W, const uint8_t *act, size_t 
     case Q5_K: return launch_gemv_q5_K(W, act, stride, x, Y, nb, s, lpr, upl);
     case Q6_K: return launch_gemv_q6_K(W, act, stride, x, Y, nb, s, lpr, upl);
     case Q2_K: return launch_gemv_q2_K(W, act, stride, x, Y, nb, s, lpr, upl);
+    case TQ2_0: return launch_gemv_tq2_0(W, act, stride, x, Y, nb, s, lpr, upl);
     default: return hipErrorInvalidValue;
     }
 }
@@ -176,6 +178,7 @@ hipError_t launch_block_sums(const g4h_tensor &W, const uint8_t *act, size_t str
     case Q5_K: return bs_go<FQ5_K>(W, act, stride, tok, out, s);
     case Q6_K: return bs_go<FQ6_K>(W, act, stride, tok, out, s);
     case Q2_K: return bs_go<FQ2_K>(W, act, stride, tok, out, s);
+    case TQ2_0: return bs_go<FTQ2_0>(W, act, stride, tok, out, s);
     default: return hipErrorInvalidValue;
     }
 }

@@ -209,6 +209,12 @@ __global__ __launch_bounds__(256) void k_dequant(int type, const uint8_t *__rest
         const int q = ((j >= 2 ? byte >> 4 : byte & 15) | (((b[128 + 32 * h + l] >> (2 * j)) & 3) << 4)) - 32;
         out = h2f(ld16(b + 208)) * (float)(int8_t)b[192 + (ee >> 4)] * (float)q;
     } break;
+    case TQ2_0: {                                                  // quants.c:402-411
+        const uint8_t *b = row + (e >> 8) * 66;
+        const int ee = (int)(e & 255), h = ee >> 7, j = (ee >> 5) & 3, k = (ee >> 4) & 1, l = ee & 15;
+        const int q = (b[32 * h + 16 * k + l] >> (2 * j)) & 3;
+        out = (float)(q - 1) * h2f(ld16(b + 64));
+    } break;
     case F16: out = h2f(ld16(row + 2 * e)); break;
     default: out = ((const float *)row)[e]; break;
     }
@@ -237,6 +243,7 @@ __global__ __launch_bounds__(256) void k_repack(g4h_tensor t, uint8_t *__restric
     case Q2_K: mv(t.sc + i * 16, 0, 16); mv(t.qs + i * 64, 16, 64); mv(t.ex + i * 4, 80, 4); break;
     case Q3_K: mv(t.ex + i * 32, 0, 32); mv(t.qs + i * 64, 32, 64); mv(t.sc + i * 12, 96, 12); mv(t.dd + i * 2, 108, 2); break;
     case Q6_K: mv(t.qs + i * 128, 0, 128); mv(t.ex + i * 64, 128, 64); mv(t.sc + i * 16, 192, 16); mv(t.dd + i * 2, 208, 2); break;
+    case TQ2_0: mv(t.qs + i * 64, 0, 64); mv(t.sc + i * 2, 64, 2); break;
     default: break;
     }
 }
@@ -286,6 +293,11 @@ template <> __device__ void raw_frag<FQ6_K>(FQ6_K::Frag &f, const uint8_t *row, 
     const int p = u & 3, h = p >> 1, k = p & 1;
     f.l0 = ldu128(b + 64 * h + 16 * k); f.l1 = ldu128(b + 64 * h + 32 + 16 * k); f.hb = ldu128(b + 128 + 32 * h + 16 * k);
     f.s = make_uint2((uint32_t)ldu32(b + 192 + 8 * h), (uint32_t)ldu32(b + 196 + 8 * h)); f.d = ld16(b + 208);
+}
+
+template <> __device__ void raw_frag<FTQ2_0>(FTQ2_0::Frag &f, const uint8_t *row, int u) {
+    const uint8_t *b = row + (size_t)(u >> 2) * 66;
+    f.q = ldu128(b + 16 * (u & 3)); f.d = ld16(b + 64);
 }
 
 template <class F>
@@ -359,6 +371,7 @@ hipError_t launch_vec_dot_raw(int wtype, const uint8_t *w, size_t ws, const uint
     case Q2_K: return vd_go<FQ2_K>(w, ws, a, n, rows, out, s);
     case Q5_K: return vd_go<FQ5_K>(w, ws, a, n, rows, out, s);
     case Q6_K: return vd_go<FQ6_K>(w, ws, a, n, rows, out, s);
+    case TQ2_0: return vd_go<FTQ2_0>(w, ws, a, n, rows, out, s);
     default: return hipErrorInvalidValue;
     }
 }

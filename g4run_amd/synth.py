@@ -6,17 +6,18 @@ the same seed gives the same bytes on every host):
   q4_0  nibbles uniform in 0..15,     d = fp16(|N(0,1)| * 0.02/8)
   q2_K / q3_K / q4_K / q5_K / q6_K  every quant, scale and hmask bit uniform random;
         d and dmin = fp16(|N(0,1)| * 1e-4) so that they are finite.
+  tq2_0 every 2-bit field uniform in 0..3 (value -1..2), d = fp16(|N(0,1)| * 0.02).
 Activations x ~ N(0,1) in fp32.
 """
 from __future__ import annotations
 
 import numpy as np
 
-from . import BLCK, Q2_K, Q3_K, Q4_0, Q4_K, Q5_K, Q6_K, Q8_0, SIZE
+from . import BLCK, Q2_K, Q3_K, Q4_0, Q4_K, Q5_K, Q6_K, Q8_0, SIZE, TQ2_0
 
 # byte offsets of the fp16 scale fields inside each block (g4run.h:107-118)
-_SCALE_FIELDS = {Q8_0: (0,), Q4_0: (0,), Q2_K: (80, 82), Q3_K: (108,), Q4_K: (0, 2), Q5_K: (0, 2), Q6_K: (208,)}
-_SCALE_MUL = {Q8_0: 0.02 / 127, Q4_0: 0.02 / 8, Q2_K: 1e-4, Q3_K: 1e-4, Q4_K: 1e-4, Q5_K: 1e-4, Q6_K: 1e-5}
+_SCALE_FIELDS = {Q8_0: (0,), Q4_0: (0,), Q2_K: (80, 82), Q3_K: (108,), Q4_K: (0, 2), Q5_K: (0, 2), Q6_K: (208,), TQ2_0: (64,)}
+_SCALE_MUL = {Q8_0: 0.02 / 127, Q4_0: 0.02 / 8, Q2_K: 1e-4, Q3_K: 1e-4, Q4_K: 1e-4, Q5_K: 1e-4, Q6_K: 1e-5, TQ2_0: 0.02}
 
 
 def _fp16_bits(v: np.ndarray) -> np.ndarray:
@@ -53,6 +54,7 @@ GEMV_CONFIGS = {
     # beyond BASELINE config 2: the next K-quant formats of the same boundary
     "q5_K_4096x11008": (Q5_K, 4096, 11008),
     "q6_K_4096x11008": (Q6_K, 4096, 11008),
+    "tq2_0_4096x11008": (TQ2_0, 4096, 11008),
 }
 
 SEEDS = {"weights": 1234, "x": 99}

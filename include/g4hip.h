@@ -27,7 +27,8 @@ extern "C" {
  * used by the reference only as the K-quant activation format). */
 enum {
     G4H_F32 = 0, G4H_F16 = 1, G4H_Q4_0 = 2, G4H_Q8_0 = 8,
-    G4H_Q2_K = 10, G4H_Q3_K = 11, G4H_Q4_K = 12, G4H_Q5_K = 13, G4H_Q6_K = 14, G4H_Q8_K = 15
+    G4H_Q2_K = 10, G4H_Q3_K = 11, G4H_Q4_K = 12, G4H_Q5_K = 13, G4H_Q6_K = 14, G4H_Q8_K = 15,
+    G4H_TQ2_0 = 35
 };
 
 enum {
@@ -75,7 +76,8 @@ int g4h_graph_destroy(void *graph_exec);
  * block size or the type is unknown. */
 size_t g4h_row_size(int type, int64_t n);
 /* act_class (model.c:132-141): activation format a weight type dots against
- * (G4H_Q8_0 for q4_0/q8_0, G4H_Q8_K for q2_K/q3_K/q4_K/q5_K/q6_K), -1 otherwise. */
+ * (G4H_Q8_0 for q4_0/q8_0, G4H_Q8_K for q2_K/q3_K/q4_K/q5_K/q6_K/tq2_0), -1
+ * otherwise. */
 int    g4h_act_type(int wtype);
 /* prep_act stride (model.c:148-149,156-157): per-token bytes, 64-B padded. */
 size_t g4h_act_stride(int wtype, int64_t ncols);
@@ -143,7 +145,7 @@ int g4h_matmul_path(const g4h_tensor *W, int nb);
 int g4h_matmul_describe(const g4h_tensor *W, int nb, int path, char *buf, size_t len);
 
 /* Per-block integer sums of every row of W against token `tok` of pre_dev:
- * q8_0/q4_0 one int32 per 32-block, q3_K/q6_K one per superblock, q2_K/q4_K/q5_K
+ * q8_0/q4_0 one int32 per 32-block, q3_K/q6_K/tq2_0 one per superblock, q2_K/q4_K/q5_K
  * two per superblock (scale-weighted quant sum, min-weighted bsum), i.e. the
  * integers the reference's dots scale (quants.c:535-818).
  * sums_dev: nrows x count. */

@@ -24,7 +24,8 @@ extern "C" {
 /* ggml type ids, g4run.h:80-94 (values are a file-format contract). */
 enum {
     G4O_F32 = 0, G4O_F16 = 1, G4O_Q4_0 = 2, G4O_Q8_0 = 8,
-    G4O_Q2_K = 10, G4O_Q3_K = 11, G4O_Q4_K = 12, G4O_Q5_K = 13, G4O_Q6_K = 14, G4O_Q8_K = 15
+    G4O_Q2_K = 10, G4O_Q3_K = 11, G4O_Q4_K = 12, G4O_Q5_K = 13, G4O_Q6_K = 14, G4O_Q8_K = 15,
+    G4O_TQ2_0 = 35
 };
 
 /* Packed block layouts, g4run.h:107-118.  Byte-for-byte the GGUF formats. */
@@ -37,6 +38,7 @@ typedef struct { uint8_t hmask[32]; uint8_t qs[64]; uint8_t scales[12]; uint16_t
 typedef struct { uint16_t d, dmin; uint8_t scales[12]; uint8_t qs[128]; } g4o_q4_K;       /* 144 B */
 typedef struct { uint16_t d, dmin; uint8_t scales[12]; uint8_t qh[32]; uint8_t qs[128]; } g4o_q5_K; /* 176 B */
 typedef struct { uint8_t ql[128]; uint8_t qh[64]; int8_t scales[16]; uint16_t d; } g4o_q6_K; /* 210 B */
+typedef struct { uint8_t qs[64]; uint16_t d; } g4o_tq2_0;                                    /* 66 B */
 #pragma pack(pop)
 
 /* ---- type table (gguf.c:11-46) ---- */
@@ -66,7 +68,8 @@ int  g4o_dequant_row(int type, const void *x, float *y, int64_t n);  /* returns 
  *              d_a*(d_w*isum - dmin_w*msum)   (quants.c:633-652, 743-758).
  * q3_K: one int32 per superblock, isum = sum_s (scale_s-32) * sum q3*q8.
  * q6_K: one int32 per superblock, isum = sum_s scale_s * sum (q6-32)*q8
- *       (quants.c:582-622).                                                   */
+ *       (quants.c:582-622).
+ * tq2_0: one int32 per superblock, sum (trit-1)*q8 (quants.c:564-580).       */
 void g4o_block_sums(int type, const void *w, const void *a, int64_t n, int32_t *out);
 
 /* ---- scalar reference dots (quants.c:535-762), sequential fp32 order ---- */

@@ -19,11 +19,11 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "liboracle.so")
 REF_PATH = os.path.join(HERE, "_ref", "libg4ref.so")
 
-F32, F16, Q4_0, Q8_0, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, Q8_K = 0, 1, 2, 8, 10, 11, 12, 13, 14, 15
-BLCK = {F32: 1, F16: 1, Q4_0: 32, Q8_0: 32, Q2_K: 256, Q3_K: 256, Q4_K: 256, Q5_K: 256, Q6_K: 256, Q8_K: 256}
-SIZE = {F32: 4, F16: 2, Q4_0: 18, Q8_0: 34, Q2_K: 84, Q3_K: 110, Q4_K: 144, Q5_K: 176, Q6_K: 210, Q8_K: 292}
-NAMES = {Q4_0: "q4_0", Q8_0: "q8_0", Q2_K: "q2_K", Q3_K: "q3_K", Q4_K: "q4_K", Q5_K: "q5_K", Q6_K: "q6_K"}
-ACT = {Q4_0: Q8_0, Q8_0: Q8_0, Q2_K: Q8_K, Q3_K: Q8_K, Q4_K: Q8_K, Q5_K: Q8_K, Q6_K: Q8_K}
+F32, F16, Q4_0, Q8_0, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, Q8_K, TQ2_0 = 0, 1, 2, 8, 10, 11, 12, 13, 14, 15, 35
+BLCK = {F32: 1, F16: 1, Q4_0: 32, Q8_0: 32, Q2_K: 256, Q3_K: 256, Q4_K: 256, Q5_K: 256, Q6_K: 256, Q8_K: 256, TQ2_0: 256}
+SIZE = {F32: 4, F16: 2, Q4_0: 18, Q8_0: 34, Q2_K: 84, Q3_K: 110, Q4_K: 144, Q5_K: 176, Q6_K: 210, Q8_K: 292, TQ2_0: 66}
+NAMES = {Q4_0: "q4_0", Q8_0: "q8_0", Q2_K: "q2_K", Q3_K: "q3_K", Q4_K: "q4_K", Q5_K: "q5_K", Q6_K: "q6_K", TQ2_0: "tq2_0"}
+ACT = {Q4_0: Q8_0, Q8_0: Q8_0, Q2_K: Q8_K, Q3_K: Q8_K, Q4_K: Q8_K, Q5_K: Q8_K, Q6_K: Q8_K, TQ2_0: Q8_K}
 
 _lib = None
 _ref = None
@@ -119,7 +119,7 @@ def ref():
             f.argtypes = [_vp, _vp, _i64]
         R.g4_dequant_row.restype = None
         R.g4_dequant_row.argtypes = [C.c_int, _vp, _vp, _i64]
-        for nm in ("q4_0_q8_0", "q8_0_q8_0", "q2_K_q8_K", "q3_K_q8_K", "q4_K_q8_K", "q5_K_q8_K", "q6_K_q8_K"):
+        for nm in ("q4_0_q8_0", "q8_0_q8_0", "q2_K_q8_K", "q3_K_q8_K", "q4_K_q8_K", "q5_K_q8_K", "q6_K_q8_K", "tq2_0_q8_K"):
             for suf in ("", "_ref"):
                 f = getattr(R, "g4_dot_" + nm + suf)
                 f.restype = C.c_float
@@ -135,7 +135,7 @@ def ref():
 
 
 DOT_NAME = {Q4_0: "q4_0_q8_0", Q8_0: "q8_0_q8_0", Q2_K: "q2_K_q8_K", Q3_K: "q3_K_q8_K", Q4_K: "q4_K_q8_K",
-            Q5_K: "q5_K_q8_K", Q6_K: "q6_K_q8_K"}
+            Q5_K: "q5_K_q8_K", Q6_K: "q6_K_q8_K", TQ2_0: "tq2_0_q8_K"}
 
 
 # ------------------------------------------------------------------ wrappers

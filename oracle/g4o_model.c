@@ -25,6 +25,7 @@ static float dot_q2_K(const void *w, const void *a, int64_t n) { return g4o_dot(
 static float dot_q3_K(const void *w, const void *a, int64_t n) { return g4o_dot(G4O_Q3_K, w, a, n); }
 static float dot_q5_K(const void *w, const void *a, int64_t n) { return g4o_dot(G4O_Q5_K, w, a, n); }
 static float dot_q6_K(const void *w, const void *a, int64_t n) { return g4o_dot(G4O_Q6_K, w, a, n); }
+static float dot_tq2_0(const void *w, const void *a, int64_t n) { return g4o_dot(G4O_TQ2_0, w, a, n); }
 static float dot_q4_K(const void *w, const void *a, int64_t n) { return g4o_dot(G4O_Q4_K, w, a, n); }
 
 static g4o_dot_fn dot_override[16];
@@ -38,6 +39,7 @@ static g4o_dot_fn dot_for(int wtype) {
     case G4O_Q3_K: return dot_q3_K;
     case G4O_Q5_K: return dot_q5_K;
     case G4O_Q6_K: return dot_q6_K;
+    case G4O_TQ2_0: return dot_tq2_0;
     case G4O_Q4_K: return dot_q4_K;
     default: return NULL;
     }
@@ -127,7 +129,7 @@ void g4o_parallel_for(int64_t total, g4o_pf_fn fn, void *ud) {
 int g4o_act_type(int wtype) {
     switch (wtype) {
     case G4O_Q4_0: case G4O_Q8_0: return G4O_Q8_0;
-    case G4O_Q2_K: case G4O_Q3_K: case G4O_Q4_K: case G4O_Q5_K: case G4O_Q6_K: return G4O_Q8_K;
+    case G4O_Q2_K: case G4O_Q3_K: case G4O_Q4_K: case G4O_Q5_K: case G4O_Q6_K: case G4O_TQ2_0: return G4O_Q8_K;
     default: return -1;
     }
 }

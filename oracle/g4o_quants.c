@@ -18,7 +18,7 @@ int g4o_type_blck(int t) {
     switch (t) {
     case G4O_F32: case G4O_F16: return 1;
     case G4O_Q4_0: case G4O_Q8_0: return 32;
-    case G4O_Q2_K: case G4O_Q3_K: case G4O_Q4_K: case G4O_Q5_K: case G4O_Q6_K: case G4O_Q8_K: return 256;
+    case G4O_Q2_K: case G4O_Q3_K: case G4O_Q4_K: case G4O_Q5_K: case G4O_Q6_K: case G4O_Q8_K: case G4O_TQ2_0: return 256;
     default: return 0;
     }
 }
@@ -32,6 +32,7 @@ size_t g4o_type_size(int t) {
     case G4O_Q3_K: return sizeof(g4o_q3_K);
     case G4O_Q5_K: return sizeof(g4o_q5_K);
     case G4O_Q6_K: return sizeof(g4o_q6_K);
+    case G4O_TQ2_0: return sizeof(g4o_tq2_0);
     case G4O_Q4_K: return sizeof(g4o_q4_K);
     case G4O_Q8_K: return sizeof(g4o_q8_K);
     default: return 0;
@@ -234,6 +235,12 @@ static inline int q6k_q(const g4o_q6_K *b, int e) {
     int hi = (b->qh[32 * h + l] >> (2 * j)) & 3;
     return (lo | (hi << 4)) - 32;
 }
+/* element e of a tq2_0 superblock: trit - 1 (quants.c:402-411): e = 128h + 32j
+ * + m is (qs[32h + m] >> 2j) & 3. */
+static inline int tq2_q(const g4o_tq2_0 *b, int e) {
+    int h = e >> 7, j = (e >> 5) & 3, m = e & 31;
+    return ((b->qs[32 * h + m] >> (2 * j)) & 3) - 1;
+}
 /* element e of a q4_K superblock: 0..15 and sub-block e/32 (quants.c:479-495). */
 static inline int q4k_q(const g4o_q4_K *b, int e) {
     int p = e >> 6, hi = (e >> 5) & 1, l = e & 31;
@@ -319,6 +326,14 @@ int g4o_dequant_row(int type, const void *vx, float *y, int64_t n) {
         }
         return 0;
     }
+    case G4O_TQ2_0: {                                      /* quants.c:402-411: (q-1)*d */
+        const g4o_tq2_0 *x = vx;
+        for (int64_t b = 0; b < n / 256; b++) {
+            float d = g4o_fp16_to_fp32(x[b].d);
+            for (int e = 0; e < 256; e++) y[256 * b + e] = (float)tq2_q(&x[b], e) * d;
+        }
+        return 0;
+    }
     default: return -1;
     }
 }
@@ -376,6 +391,11 @@ static int32_t sum_q6_K(const g4o_q6_K *w, const g4o_q8_K *a) {
     for (int e = 0; e < 256; e++) s += w->scales[e >> 4] * q6k_q(w, e) * a->qs[e];
     return s;
 }
+static int32_t sum_tq2_0(const g4o_tq2_0 *w, const g4o_q8_K *a) {
+    int32_t s = 0;
+    for (int e = 0; e < 256; e++) s += tq2_q(w, e) * a->qs[e];
+    return s;
+}
 
 void g4o_block_sums(int type, const void *w, const void *a, int64_t n, int32_t *out) {
     switch (type) {
@@ -385,6 +405,7 @@ void g4o_block_sums(int type, const void *w, const void *a, int64_t n, int32_t *
     case G4O_Q3_K: for (int64_t b = 0; b < n / 256; b++) out[b] = sum_q3_K((const g4o_q3_K *)w + b, (const g4o_q8_K *)a + b); break;
     case G4O_Q5_K: for (int64_t b = 0; b < n / 256; b++) sums_q5_K((const g4o_q5_K *)w + b, (const g4o_q8_K *)a + b, &out[2 * b], &out[2 * b + 1]); break;
     case G4O_Q6_K: for (int64_t b = 0; b < n / 256; b++) out[b] = sum_q6_K((const g4o_q6_K *)w + b, (const g4o_q8_K *)a + b); break;
+    case G4O_TQ2_0: for (int64_t b = 0; b < n / 256; b++) out[b] = sum_tq2_0((const g4o_tq2_0 *)w + b, (const g4o_q8_K *)a + b); break;
     case G4O_Q4_K: for (int64_t b = 0; b < n / 256; b++) sums_q4_K((const g4o_q4_K *)w + b, (const g4o_q8_K *)a + b, &out[2 * b], &out[2 * b + 1]); break;
     default: break;
     }
@@ -405,6 +426,11 @@ float g4o_dot_ref(int type, const void *vw, const void *va, int64_t n) {
         const g4o_q4_0 *w = vw; const g4o_q8_0 *a = va;
         for (int64_t b = 0; b < n / 32; b++)
             acc += (float)sum_q4_0(&w[b], &a[b]) * g4o_fp16_to_fp32(w[b].d) * g4o_fp16_to_fp32(a[b].d);
+        return acc;
+    }
+    case G4O_TQ2_0: {                                     /* quants.c:564-580 */
+        const g4o_tq2_0 *w = vw; const g4o_q8_K *a = va;
+        for (int64_t b = 0; b < n / 256; b++) acc += (float)sum_tq2_0(&w[b], &a[b]) * (a[b].d * g4o_fp16_to_fp32(w[b].d));
         return acc;
     }
     case G4O_Q2_K: {                                      /* quants.c:624-655 */
@@ -547,6 +573,14 @@ static float dot_q6_K_avx2(const g4o_q6_K *w, const g4o_q8_K *a, int64_t nb) {
     }
     return hsum8(acc);
 }
+/* tq2_0 (quants.c:1001-1026): the integer sum of a superblock is exact
+ * (trits 0..2 against q8 minus the bsums), and it is scaled into one scalar
+ * accumulator; the shipped build contracts the multiply-add into one fma. */
+static float dot_tq2_0_avx2(const g4o_tq2_0 *w, const g4o_q8_K *a, int64_t nb) {
+    float acc = 0.0f;
+    for (int64_t b = 0; b < nb; b++) acc = fmaf((float)sum_tq2_0(&w[b], &a[b]), a[b].d * g4o_fp16_to_fp32(w[b].d), acc);
+    return acc;
+}
 /* q5_K (quants.c:1261-1313): the mins sum of a superblock goes to one scalar
  * accumulator, the scale-weighted products to 8 lanes as in q4_K; the result
  * is hsum_float_8(acc) + summs.  The shipped -Ofast build evaluates
@@ -600,6 +634,7 @@ float g4o_dot(int type, const void *w, const void *a, int64_t n) {
     case G4O_Q4_K: return dot_q4_K_avx2(w, a, n / 256);
     case G4O_Q5_K: return dot_q5_K_avx2(w, a, n / 256);
     case G4O_Q6_K: return dot_q6_K_avx2(w, a, n / 256);
+    case G4O_TQ2_0: return dot_tq2_0_avx2(w, a, n / 256);
     default: return NAN;
     }
 }

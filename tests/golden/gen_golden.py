@@ -26,14 +26,16 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(os.path.dirname(HERE))
 REF = os.path.join(ROOT, "oracle", "_ref", "libg4ref.so")
 
-Q4_0, Q8_0, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, Q8_K = 2, 8, 10, 11, 12, 13, 14, 15
-BLCK = {Q4_0: 32, Q8_0: 32, Q2_K: 256, Q3_K: 256, Q4_K: 256, Q5_K: 256, Q6_K: 256, Q8_K: 256}
-SIZE = {Q4_0: 18, Q8_0: 34, Q2_K: 84, Q3_K: 110, Q4_K: 144, Q5_K: 176, Q6_K: 210, Q8_K: 292}
-ACT = {Q4_0: Q8_0, Q8_0: Q8_0, Q2_K: Q8_K, Q3_K: Q8_K, Q4_K: Q8_K, Q5_K: Q8_K, Q6_K: Q8_K}
-NAME = {Q4_0: "q4_0", Q8_0: "q8_0", Q2_K: "q2_K", Q3_K: "q3_K", Q4_K: "q4_K", Q5_K: "q5_K", Q6_K: "q6_K", Q8_K: "q8_K"}
-DOT = {Q4_0: "q4_0_q8_0", Q8_0: "q8_0_q8_0", Q2_K: "q2_K_q8_K", Q3_K: "q3_K_q8_K", Q4_K: "q4_K_q8_K", Q5_K: "q5_K_q8_K", Q6_K: "q6_K_q8_K"}
+Q4_0, Q8_0, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, Q8_K, TQ2_0 = 2, 8, 10, 11, 12, 13, 14, 15, 35
+BLCK = {Q4_0: 32, Q8_0: 32, Q2_K: 256, Q3_K: 256, Q4_K: 256, Q5_K: 256, Q6_K: 256, Q8_K: 256, TQ2_0: 256}
+SIZE = {Q4_0: 18, Q8_0: 34, Q2_K: 84, Q3_K: 110, Q4_K: 144, Q5_K: 176, Q6_K: 210, Q8_K: 292, TQ2_0: 66}
+ACT = {Q4_0: Q8_0, Q8_0: Q8_0, Q2_K: Q8_K, Q3_K: Q8_K, Q4_K: Q8_K, Q5_K: Q8_K, Q6_K: Q8_K, TQ2_0: Q8_K}
+NAME = {Q4_0: "q4_0", Q8_0: "q8_0", Q2_K: "q2_K", Q3_K: "q3_K", Q4_K: "q4_K", Q5_K: "q5_K", Q6_K: "q6_K", Q8_K: "q8_K",
+        TQ2_0: "tq2_0"}
+DOT = {Q4_0: "q4_0_q8_0", Q8_0: "q8_0_q8_0", Q2_K: "q2_K_q8_K", Q3_K: "q3_K_q8_K", Q4_K: "q4_K_q8_K", Q5_K: "q5_K_q8_K",
+       Q6_K: "q6_K_q8_K", TQ2_0: "tq2_0_q8_K"}
 # fp16 scale fields (d, dmin) inside a weight block and the f32 d of q8_K
-SCALES = {Q8_0: (0,), Q4_0: (0,), Q2_K: (80, 82), Q3_K: (108,), Q4_K: (0, 2), Q5_K: (0, 2), Q6_K: (208,)}
+SCALES = {Q8_0: (0,), Q4_0: (0,), Q2_K: (80, 82), Q3_K: (108,), Q4_K: (0, 2), Q5_K: (0, 2), Q6_K: (208,), TQ2_0: (64,)}
 
 vp = C.c_void_p
 
@@ -120,7 +122,7 @@ def unit_sums(R, qt, w_row, a_row, n):
             ab[0:4] = np.frombuffer(np.float32(1.0).tobytes(), np.uint8)
         one = np.frombuffer(np.float16(1.0).tobytes(), np.uint8)
         zero = np.zeros(2, np.uint8)
-        if qt in (Q8_0, Q4_0, Q3_K, Q6_K):
+        if qt in (Q8_0, Q4_0, Q3_K, Q6_K, TQ2_0):
             wb[SCALES[qt][0]:SCALES[qt][0] + 2] = one
             out[b] = int(f(ptr(wb), ptr(ab), BLCK[qt]))
         else:
@@ -148,7 +150,7 @@ def main(only=None):
         np.savez_compressed(os.path.join(HERE, f"quant_{NAME[qt]}.npz"), x=x, y=quant(R, qt, x), flags=flags)
 
     # dots, x4, dequant, per-block sums
-    for qt in (Q8_0, Q4_0, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K):
+    for qt in (Q8_0, Q4_0, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, TQ2_0):
         if only and NAME[qt] not in only:
             continue
         rng = np.random.default_rng(100 + qt)

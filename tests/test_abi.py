@@ -38,6 +38,7 @@ def test_row_size_matches_type_table():
     assert G.row_size(G.Q2_K, 11008) == 3612
     assert G.row_size(G.Q5_K, 11008) == 43 * 176
     assert G.row_size(G.Q6_K, 11008) == 43 * 210
+    assert G.row_size(G.TQ2_0, 11008) == 43 * 66
     assert G.row_size(G.Q8_K, 11008) == 43 * 292
     assert G.row_size(G.Q8_0, 33) == 0
     assert G.row_size(G.Q4_K, 1000) == 0

@@ -13,7 +13,7 @@ import pytest
 pytestmark = pytest.mark.gpu
 
 GOLD = os.path.join(os.path.dirname(__file__), "golden")
-FMTS = [("q8_0", 8), ("q4_0", 2), ("q2_K", 10), ("q3_K", 11), ("q4_K", 12), ("q5_K", 13), ("q6_K", 14)]
+FMTS = [("q8_0", 8), ("q4_0", 2), ("q2_K", 10), ("q3_K", 11), ("q4_K", 12), ("q5_K", 13), ("q6_K", 14), ("tq2_0", 35)]
 RTOL, ATOL = 1e-3, 1e-5
 
 
@@ -115,7 +115,7 @@ def test_block_sums_vs_reference_fixture(gpu, name, qt):
 
 
 CONFIG_SHAPES = {8: [(4096, 4096)], 2: [(10240, 2560), (2560, 10240)], 12: [(4096, 11008)], 11: [(4096, 11008)],
-                 10: [(4096, 11008)], 13: [(4096, 11008)], 14: [(4096, 11008)]}
+                 10: [(4096, 11008)], 13: [(4096, 11008)], 14: [(4096, 11008)], 35: [(4096, 11008)]}
 
 
 @pytest.mark.parametrize("name,qt", FMTS)

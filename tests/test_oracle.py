@@ -88,7 +88,7 @@ def test_quantize_q8_K_closed_form(oracle):
 
 
 # ---------------------------------------------------- dots / dequant / sums
-FMTS = [("q8_0", 8), ("q4_0", 2), ("q2_K", 10), ("q3_K", 11), ("q4_K", 12), ("q5_K", 13), ("q6_K", 14)]
+FMTS = [("q8_0", 8), ("q4_0", 2), ("q2_K", 10), ("q3_K", 11), ("q4_K", 12), ("q5_K", 13), ("q6_K", 14), ("tq2_0", 35)]
 
 
 @pytest.mark.parametrize("name,qt", FMTS)
@@ -141,6 +141,8 @@ def test_block_sums_brute_force(oracle, name, qt):
         wv[:, :, 108:110] = one
     elif qt == 14:
         wv[:, :, 208:210] = one
+    elif qt == 35:
+        wv[:, :, 64:66] = one
     elif qt == 10:
         wv[:, :, 80:82] = one; wv[:, :, 82:84] = zero
     else:
