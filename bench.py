@@ -81,7 +81,20 @@ class GemvSet:
         G.synchronize()
         self.x = G.Buffer.from_array(synth.activations(1, cols, seed=seed + 1))
         self.act = G.Buffer(G.act_stride(qt, cols))
-        G.quantize(G.act_type(qt), self.x, cols, 1, self.act)
+        if qt in (G.F16, G.BF16):
+            # prep_act's conversions (model.c:163-180): f16 round-to-nearest-even,
+            # bf16 round-to-nearest-even widened back to fp32 (finite inputs)
+            xh = synth.activations(1, cols, seed=seed + 1)
+            if qt == G.F16:
+                a = xh.astype(np.float16)
+            else:
+                u = xh.view(np.uint32)
+                a = (((u + 0x7FFF + ((u >> 16) & 1)) >> 16) << 16).astype(np.uint32).view(np.float32)
+            pad = np.zeros(G.act_stride(qt, cols), np.uint8)
+            pad[: a.nbytes] = np.ascontiguousarray(a).view(np.uint8).ravel()
+            self.act.upload(pad)
+        else:
+            G.quantize(G.act_type(qt), self.x, cols, 1, self.act)
         self.Y = G.Buffer(rows * 4)
         self.bytes = synth.algorithmic_bytes(qt, rows, cols)
         self.w_host = w

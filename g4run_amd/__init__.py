@@ -19,11 +19,12 @@ LIB_PATH = os.environ.get("G4H_LIB") or os.path.join(HERE, "libg4hip.so")
 INCLUDE = os.path.join(os.path.dirname(HERE), "include", "g4hip.h")
 
 # type ids (g4run.h:80-94)
-F32, F16, Q4_0, Q8_0, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, Q8_K, TQ2_0 = 0, 1, 2, 8, 10, 11, 12, 13, 14, 15, 35
-BLCK = {F32: 1, F16: 1, Q4_0: 32, Q8_0: 32, Q2_K: 256, Q3_K: 256, Q4_K: 256, Q5_K: 256, Q6_K: 256, Q8_K: 256, TQ2_0: 256}
-SIZE = {F32: 4, F16: 2, Q4_0: 18, Q8_0: 34, Q2_K: 84, Q3_K: 110, Q4_K: 144, Q5_K: 176, Q6_K: 210, Q8_K: 292, TQ2_0: 66}
+F32, F16, Q4_0, Q8_0, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, Q8_K, BF16, TQ2_0 = 0, 1, 2, 8, 10, 11, 12, 13, 14, 15, 30, 35
+BLCK = {F32: 1, F16: 1, BF16: 1, Q4_0: 32, Q8_0: 32, Q2_K: 256, Q3_K: 256, Q4_K: 256, Q5_K: 256, Q6_K: 256, Q8_K: 256,
+        TQ2_0: 256}
+SIZE = {F32: 4, F16: 2, BF16: 2, Q4_0: 18, Q8_0: 34, Q2_K: 84, Q3_K: 110, Q4_K: 144, Q5_K: 176, Q6_K: 210, Q8_K: 292, TQ2_0: 66}
 TYPE_NAMES = {Q4_0: "q4_0", Q8_0: "q8_0", Q2_K: "q2_K", Q3_K: "q3_K", Q4_K: "q4_K", Q5_K: "q5_K", Q6_K: "q6_K", Q8_K: "q8_K",
-              TQ2_0: "tq2_0", F16: "f16", F32: "f32"}
+              TQ2_0: "tq2_0", F16: "f16", BF16: "bf16", F32: "f32"}
 
 OK, ERR_ARG, ERR_TYPE, ERR_SHAPE, ERR_NOMEM, ERR_DEVICE, ERR_HIP = range(7)
 

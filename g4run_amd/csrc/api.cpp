@@ -147,6 +147,8 @@ extern "C" int g4h_graph_destroy(void *exec) { G4_HIP(hipGraphExecDestroy((hipGr
 static bool supported(int t) {
     return t == Q4_0 || t == Q8_0 || t == Q2_K || t == Q3_K || t == Q4_K || t == Q5_K || t == Q6_K || t == TQ2_0;
 }
+// f16 / bf16 weights (matmul_b's G4_F16 / G4_BF16 rows, model.c:238-239)
+static bool is_float(int t) { return t == F16 || t == BF16; }
 
 extern "C" size_t g4h_row_size(int type, int64_t n) {
     const int b = blck(type);
@@ -157,6 +159,8 @@ extern "C" int g4h_act_type(int wtype) {
     switch (wtype) {
     case Q4_0: case Q8_0: return Q8_0;
     case Q2_K: case Q3_K: case Q4_K: case Q5_K: case Q6_K: case TQ2_0: return Q8_K;
+    case F16: return F16;                                   // AC_F16 (model.c:163-170)
+    case BF16: return F32;                                  // AC_BF16: bf16-rounded fp32 (model.c:172-180)
     default: return -1;
     }
 }
@@ -228,7 +232,7 @@ extern "C" int g4h_quantize_q4_0(const float *x, size_t xs, void *y, size_t ys, 
 extern "C" int g4h_dequant_rows(int type, const void *x, size_t xs, float *y, size_t ys, int64_t n, int rows, void *s) {
     G4_NEED_INIT();
     if (!x || !y || n <= 0 || rows < 0) return fail(G4H_ERR_ARG, "g4h_dequant_rows: bad argument");
-    if (!supported(type) && type != F16 && type != F32) return fail(G4H_ERR_TYPE, "g4h_dequant_rows: type %d unsupported", type);
+    if (!supported(type) && !is_float(type) && type != F32) return fail(G4H_ERR_TYPE, "g4h_dequant_rows: type %d unsupported", type);
     if (n % blck(type)) return fail(G4H_ERR_SHAPE, "g4h_dequant_rows: n=%lld not a multiple of %d", (long long)n, blck(type));
     if (rows == 0) return G4H_OK;
     G4_HIP(launch_dequant(type, (const uint8_t *)x, xs, y, ys, n, rows, (hipStream_t)s));
@@ -238,6 +242,16 @@ extern "C" int g4h_dequant_rows(int type, const void *x, size_t xs, float *y, si
 extern "C" int g4h_vec_dot(int wtype, const void *w, size_t ws, const void *a, int64_t n, int rows, float *out, void *s) {
     G4_NEED_INIT();
     if (!w || !a || !out || n <= 0 || rows < 0) return fail(G4H_ERR_ARG, "g4h_vec_dot: bad argument");
+    if (is_float(wtype)) {
+        // g4_dot_f16 / g4_dot_bf16: f16 or fp32 activation, aligned rows
+        if (n % 8 || (uintptr_t)w % 16 || (uintptr_t)a % 16 || (rows > 1 && ws % 16))
+            return fail(G4H_ERR_ARG, "g4h_vec_dot: f16/bf16 rows need n %% 8 == 0 and 16-byte aligned rows and activation");
+        if (rows > 1 && ws < g4h_row_size(wtype, n)) return fail(G4H_ERR_ARG, "g4h_vec_dot: row stride smaller than a row");
+        if (rows == 0) return G4H_OK;
+        G4_HIP(launch_gemv_float(wtype, (const uint8_t *)w, rows > 1 ? ws : 16 * ((g4h_row_size(wtype, n) + 15) / 16), rows, n,
+                                 (const uint8_t *)a, 0, out, 0, 1, (hipStream_t)s));
+        return G4H_OK;
+    }
     if (!supported(wtype)) return fail(G4H_ERR_TYPE, "g4h_vec_dot: weight type %d unsupported", wtype);
     if (n % blck(wtype)) return fail(G4H_ERR_SHAPE, "g4h_vec_dot: n=%lld not a multiple of %d", (long long)n, blck(wtype));
     if ((uintptr_t)a % 4) return fail(G4H_ERR_ARG, "g4h_vec_dot: activation must be 4-byte aligned");
@@ -255,11 +269,13 @@ extern "C" int g4h_tensor_create(int type, int64_t ncols, int64_t nrows, g4h_ten
     G4_NEED_INIT();
     if (!out) return fail(G4H_ERR_ARG, "g4h_tensor_create: null out");
     *out = nullptr;
-    if (!supported(type)) return fail(G4H_ERR_TYPE, "g4h_tensor_create: type %d unsupported", type);
+    if (!supported(type) && !is_float(type)) return fail(G4H_ERR_TYPE, "g4h_tensor_create: type %d unsupported", type);
+    if (is_float(type) && ncols % 8) return fail(G4H_ERR_SHAPE, "g4h_tensor_create: f16/bf16 rows need ncols %% 8 == 0");
     if (ncols <= 0 || nrows <= 0) return fail(G4H_ERR_ARG, "g4h_tensor_create: empty shape");
     if (ncols % blck(type)) return fail(G4H_ERR_SHAPE, "g4h_tensor_create: ncols=%lld not a multiple of %d", (long long)ncols, blck(type));
     const int64_t nb = ncols / blck(type);
-    if (gemv_lds_bytes(type, 1, nb) > 65536) return fail(G4H_ERR_SHAPE, "g4h_tensor_create: ncols=%lld exceeds the supported row length", (long long)ncols);
+    if (!is_float(type) && gemv_lds_bytes(type, 1, nb) > 65536)
+        return fail(G4H_ERR_SHAPE, "g4h_tensor_create: ncols=%lld exceeds the supported row length", (long long)ncols);
     const size_t n = (size_t)(nrows * nb);
     size_t qs = 0, sc = 0, ex = 0, dd = 0;
     switch (type) {
@@ -271,6 +287,7 @@ extern "C" int g4h_tensor_create(int type, int64_t ncols, int64_t nrows, g4h_ten
     case Q3_K: qs = n * 64; ex = n * 32; sc = n * 12; dd = n * 2; break;
     case Q6_K: qs = n * 128; ex = n * 64; sc = n * 16; dd = n * 2; break;
     case TQ2_0: qs = n * 64; sc = n * 2; break;
+    case F16: case BF16: qs = n * 2; break;
     }
     const size_t total = al256(qs) + al256(sc) + al256(ex) + al256(dd);
     g4h_tensor *t = new g4h_tensor();
@@ -383,6 +400,8 @@ static const char *type_name(int t) {
     case Q5_K: return "q5_K";
     case Q6_K: return "q6_K";
     case TQ2_0: return "tq2_0";
+    case F16: return "f16";
+    case BF16: return "bf16";
     case Q4_K: return "q4_K";
     default: return "?";
     }
@@ -394,6 +413,12 @@ extern "C" int g4h_matmul_describe(const g4h_tensor *W, int nb, int path, char *
     if (path == 2) {
         if (!mfma_capable(W)) return fail(G4H_ERR_TYPE, "g4h_matmul_describe: the matrix-core path takes q8_0 / q4_0 weights");
         mm_describe(*W, nb, buf, len);
+        return G4H_OK;
+    }
+    if (is_float(W->type)) {
+        const int chunk = nb >= 8 ? 8 : nb >= 4 ? 4 : nb >= 2 ? 2 : 1;
+        snprintf(buf, len, "k_gemv_float<%s,nb=%d> grid=%lld block=256 (x%d launches); fp32 x converted by a separate launch",
+                 type_name(W->type), chunk, (long long)((W->nrows + 3) / 4), (nb + chunk - 1) / chunk);
         return G4H_OK;
     }
     int lpr, upl, wpg;
@@ -433,6 +458,34 @@ extern "C" int g4h_matmul_ex(const g4h_tensor *W, const float *x, const void *pr
         if (int rc = scratch_for(s, mm_planar_bytes(nb, W->ncols), &buf)) return rc;
         const hipError_t e = launch_matmul_mfma(*W, x, W->ncols, (const uint8_t *)pre, pre_stride, nb, Y, (uint8_t *)buf, s);
         if (e != hipSuccess) return hip_fail(e, "g4h_matmul: matrix-core launch");
+        return G4H_OK;
+    }
+    if (is_float(W->type)) {
+        // prep_act's conversion (model.c:163-180), then the float GEMV in token
+        // chunks of 8/4/2/1
+        const uint8_t *act = (const uint8_t *)pre;
+        size_t stride = pre_stride;
+        if (x) {
+            if ((uintptr_t)x % 4) return fail(G4H_ERR_ARG, "g4h_matmul: x must be 4-byte aligned");
+            stride = g4h_act_stride(W->type, W->ncols);
+            void *buf;
+            if (int rc = scratch_for(s, stride * nb, &buf)) return rc;
+            const hipError_t e = launch_act_float(W->type, x, W->ncols, W->ncols, nb, (uint8_t *)buf, stride, s);
+            if (e != hipSuccess) return hip_fail(e, "g4h_matmul: activation conversion");
+            act = (const uint8_t *)buf;
+        } else {
+            if (int rc = check_act("g4h_matmul", W, pre, pre_stride, nb)) return rc;
+            if ((uintptr_t)pre % 16 || (nb > 1 && pre_stride % 16))
+                return fail(G4H_ERR_ARG, "g4h_matmul: f16/bf16 activations must be 16-byte aligned with a 16-byte multiple stride");
+            if (nb == 1) stride = 16;
+        }
+        for (int done = 0; done < nb;) {
+            const int left = nb - done, chunk = left >= 8 ? 8 : left >= 4 ? 4 : left >= 2 ? 2 : 1;
+            const hipError_t e = launch_gemv_float(W->type, W->qs, (size_t)W->ncols * 2, W->nrows, W->ncols, act + (size_t)done * stride,
+                                                   stride, Y + (size_t)done * W->nrows, W->nrows, chunk, s);
+            if (e != hipSuccess) return hip_fail(e, "g4h_matmul: gemv launch");
+            done += chunk;
+        }
         return G4H_OK;
     }
     const uint8_t *act = (const uint8_t *)pre;
@@ -480,6 +533,7 @@ extern "C" int g4h_matmul(const g4h_tensor *W, const float *x, const void *pre, 
 extern "C" int g4h_block_sums(const g4h_tensor *W, const void *pre, size_t pre_stride, int tok, int32_t *sums, void *s) {
     G4_NEED_INIT();
     if (!W || !pre || !sums || tok < 0) return fail(G4H_ERR_ARG, "g4h_block_sums: bad argument");
+    if (is_float(W->type)) return fail(G4H_ERR_TYPE, "g4h_block_sums: f16/bf16 weights have no integer block sums");
     if (int rc = check_act("g4h_block_sums", W, pre, pre_stride, tok + 1)) return rc;
     G4_HIP(launch_block_sums(*W, (const uint8_t *)pre, pre_stride, tok, sums, (hipStream_t)s));
     return G4H_OK;

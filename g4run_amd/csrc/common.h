@@ -8,18 +8,18 @@
 
 namespace g4 {
 
-enum : int { F32 = 0, F16 = 1, Q4_0 = 2, Q8_0 = 8, Q2_K = 10, Q3_K = 11, Q4_K = 12, Q5_K = 13, Q6_K = 14, Q8_K = 15, TQ2_0 = 35 };
+enum : int { F32 = 0, F16 = 1, Q4_0 = 2, Q8_0 = 8, Q2_K = 10, Q3_K = 11, Q4_K = 12, Q5_K = 13, Q6_K = 14, Q8_K = 15, BF16 = 30, TQ2_0 = 35 };
 
 constexpr int WAVE = 64;
 
 // GGUF block geometry (g4run.h:107-118, gguf.c:11-25)
 __host__ __device__ constexpr int blck(int t) {
     return (t == Q4_0 || t == Q8_0) ? 32 : (t == Q2_K || t == Q3_K || t == Q4_K || t == Q5_K || t == Q6_K || t == Q8_K || t == TQ2_0) ? 256
-         : (t == F32 || t == F16) ? 1 : 0;
+         : (t == F32 || t == F16 || t == BF16) ? 1 : 0;
 }
 __host__ __device__ constexpr int bsize(int t) {
     return t == Q4_0 ? 18 : t == Q8_0 ? 34 : t == Q2_K ? 84 : t == Q3_K ? 110 : t == Q4_K ? 144 : t == Q5_K ? 176 : t == Q6_K ? 210 : t == Q8_K ? 292 : t == TQ2_0 ? 66
-         : t == F16 ? 2 : t == F32 ? 4 : 0;
+         : (t == F16 || t == BF16) ? 2 : t == F32 ? 4 : 0;
 }
 
 // ---------------------------------------------------------------- fp16 ----
@@ -181,6 +181,7 @@ __device__ __forceinline__ void issue_order() {
 //   q6_K: qs plane  [r][j][128] low nibbles (ql), ex plane [r][j][64] high
 //         bits (qh), sc plane [r][j][16] int8 scales, d plane [r][j] fp16
 //  tq2_0: qs plane  [r][j][64] 2-bit trits  sc plane [r][j] fp16 d
+//  f16 / bf16: qs plane [r][ncols] the 16-bit values (ncols % 8 == 0)
 // Every plane starts 256-B aligned; quant rows are 16-B multiples so every
 // quant load is an aligned 128-bit load.
 struct g4h_tensor {

@@ -216,6 +216,7 @@ __global__ __launch_bounds__(256) void k_dequant(int type, const uint8_t *__rest
         out = (float)(q - 1) * h2f(ld16(b + 64));
     } break;
     case F16: out = h2f(ld16(row + 2 * e)); break;
+    case BF16: out = __uint_as_float((uint32_t)ld16(row + 2 * e) << 16); break;      // quants.c:520
     default: out = ((const float *)row)[e]; break;
     }
     y[r * ys + e] = out;
@@ -244,6 +245,7 @@ __global__ __launch_bounds__(256) void k_repack(g4h_tensor t, uint8_t *__restric
     case Q3_K: mv(t.ex + i * 32, 0, 32); mv(t.qs + i * 64, 32, 64); mv(t.sc + i * 12, 96, 12); mv(t.dd + i * 2, 108, 2); break;
     case Q6_K: mv(t.qs + i * 128, 0, 128); mv(t.ex + i * 64, 128, 64); mv(t.sc + i * 16, 192, 16); mv(t.dd + i * 2, 208, 2); break;
     case TQ2_0: mv(t.qs + i * 64, 0, 64); mv(t.sc + i * 2, 64, 2); break;
+    case F16: case BF16: mv(t.qs + i * 2, 0, 2); break;
     default: break;
     }
 }

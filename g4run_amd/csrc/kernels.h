@@ -63,6 +63,12 @@ hipError_t launch_gemv(const g4h_tensor &W, const uint8_t *act, size_t stride, f
 // launch_quantize_q8_0 followed by launch_gemv
 bool gemv_fused_fits(const g4h_tensor &W, int nb);
 hipError_t launch_gemv_x(const g4h_tensor &W, const float *x, float *Y, int nb, hipStream_t s);
+// k_gemv_f16.hip: f16 / bf16 weight rows (W at ws bytes per row, 16-byte
+// aligned, ncols % 8 == 0) against nb in {1, 2, 4, 8} prepared activation rows
+// (f16 for F16, bf16-rounded fp32 for BF16) at `as` bytes; Y rows at ys floats
+hipError_t launch_gemv_float(int wtype, const uint8_t *W, size_t ws, int64_t nrows, int64_t ncols, const uint8_t *act, size_t as,
+                             float *Y, size_t ys, int nb, hipStream_t s);
+hipError_t launch_act_float(int wtype, const float *x, size_t xs, int64_t ncols, int nb, uint8_t *out, size_t os, hipStream_t s);
 hipError_t launch_block_sums(const g4h_tensor &W, const uint8_t *act, size_t stride, int tok, int32_t *out, hipStream_t s);
 int block_sums_per_block(int type);
 

@@ -7,13 +7,14 @@ the same seed gives the same bytes on every host):
   q2_K / q3_K / q4_K / q5_K / q6_K  every quant, scale and hmask bit uniform random;
         d and dmin = fp16(|N(0,1)| * 1e-4) so that they are finite.
   tq2_0 every 2-bit field uniform in 0..3 (value -1..2), d = fp16(|N(0,1)| * 0.02).
+  f16 / bf16  N(0, 0.02) values, rounded to f16 / truncated to bf16.
 Activations x ~ N(0,1) in fp32.
 """
 from __future__ import annotations
 
 import numpy as np
 
-from . import BLCK, Q2_K, Q3_K, Q4_0, Q4_K, Q5_K, Q6_K, Q8_0, SIZE, TQ2_0
+from . import BF16, BLCK, F16, Q2_K, Q3_K, Q4_0, Q4_K, Q5_K, Q6_K, Q8_0, SIZE, TQ2_0
 
 # byte offsets of the fp16 scale fields inside each block (g4run.h:107-118)
 _SCALE_FIELDS = {Q8_0: (0,), Q4_0: (0,), Q2_K: (80, 82), Q3_K: (108,), Q4_K: (0, 2), Q5_K: (0, 2), Q6_K: (208,), TQ2_0: (64,)}
@@ -27,6 +28,10 @@ def _fp16_bits(v: np.ndarray) -> np.ndarray:
 def weights(qtype: int, nrows: int, ncols: int, seed: int) -> np.ndarray:
     """GGUF rows [nrows, row_bytes] of a synthetic weight matrix."""
     rng = np.random.default_rng(seed)
+    if qtype in (F16, BF16):
+        wf = (rng.standard_normal((nrows, ncols)) * 0.02).astype(np.float32)
+        w = wf.astype(np.float16).view(np.uint16) if qtype == F16 else (wf.view(np.uint32) >> 16).astype(np.uint16)
+        return np.ascontiguousarray(w).view(np.uint8).reshape(nrows, 2 * ncols)
     nb = ncols // BLCK[qtype]
     bs = SIZE[qtype]
     w = rng.integers(0, 256, size=(nrows, nb, bs), dtype=np.uint8)
@@ -55,6 +60,8 @@ GEMV_CONFIGS = {
     "q5_K_4096x11008": (Q5_K, 4096, 11008),
     "q6_K_4096x11008": (Q6_K, 4096, 11008),
     "tq2_0_4096x11008": (TQ2_0, 4096, 11008),
+    "f16_4096x4096": (F16, 4096, 4096),
+    "bf16_4096x4096": (BF16, 4096, 4096),
 }
 
 SEEDS = {"weights": 1234, "x": 99}

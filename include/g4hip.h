@@ -28,7 +28,7 @@ extern "C" {
 enum {
     G4H_F32 = 0, G4H_F16 = 1, G4H_Q4_0 = 2, G4H_Q8_0 = 8,
     G4H_Q2_K = 10, G4H_Q3_K = 11, G4H_Q4_K = 12, G4H_Q5_K = 13, G4H_Q6_K = 14, G4H_Q8_K = 15,
-    G4H_TQ2_0 = 35
+    G4H_BF16 = 30, G4H_TQ2_0 = 35
 };
 
 enum {
@@ -76,8 +76,8 @@ int g4h_graph_destroy(void *graph_exec);
  * block size or the type is unknown. */
 size_t g4h_row_size(int type, int64_t n);
 /* act_class (model.c:132-141): activation format a weight type dots against
- * (G4H_Q8_0 for q4_0/q8_0, G4H_Q8_K for q2_K/q3_K/q4_K/q5_K/q6_K/tq2_0), -1
- * otherwise. */
+ * (G4H_Q8_0 for q4_0/q8_0, G4H_Q8_K for q2_K/q3_K/q4_K/q5_K/q6_K/tq2_0, G4H_F16
+ * for f16, G4H_F32 -- bf16-rounded fp32 rows -- for bf16), -1 otherwise. */
 int    g4h_act_type(int wtype);
 /* prep_act stride (model.c:148-149,156-157): per-token bytes, 64-B padded. */
 size_t g4h_act_stride(int wtype, int64_t ncols);

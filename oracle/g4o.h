@@ -25,7 +25,7 @@ extern "C" {
 enum {
     G4O_F32 = 0, G4O_F16 = 1, G4O_Q4_0 = 2, G4O_Q8_0 = 8,
     G4O_Q2_K = 10, G4O_Q3_K = 11, G4O_Q4_K = 12, G4O_Q5_K = 13, G4O_Q6_K = 14, G4O_Q8_K = 15,
-    G4O_TQ2_0 = 35
+    G4O_BF16 = 30, G4O_TQ2_0 = 35
 };
 
 /* Packed block layouts, g4run.h:107-118.  Byte-for-byte the GGUF formats. */
@@ -81,6 +81,8 @@ float g4o_dot_ref(int type, const void *w, const void *a, int64_t n);
  *      AVX2 build. ---- */
 float g4o_dot(int type, const void *w, const void *a, int64_t n);
 float g4o_dot_f16(const uint16_t *w, const uint16_t *a, int64_t n);   /* quants.c:1319-1331 */
+float g4o_dot_bf16(const uint16_t *w, const float *a, int64_t n);     /* quants.c:1333-1347 */
+uint16_t g4o_fp32_to_bf16(float f);                                   /* g4run.h:64-68 */
 
 /* ---- activation class + prep, matmul driver (model.c:132-270) ---- */
 int    g4o_act_type(int wtype);                 /* G4O_Q8_0 or G4O_Q8_K, -1 otherwise */

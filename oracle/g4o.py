@@ -19,11 +19,14 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "liboracle.so")
 REF_PATH = os.path.join(HERE, "_ref", "libg4ref.so")
 
-F32, F16, Q4_0, Q8_0, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, Q8_K, TQ2_0 = 0, 1, 2, 8, 10, 11, 12, 13, 14, 15, 35
-BLCK = {F32: 1, F16: 1, Q4_0: 32, Q8_0: 32, Q2_K: 256, Q3_K: 256, Q4_K: 256, Q5_K: 256, Q6_K: 256, Q8_K: 256, TQ2_0: 256}
-SIZE = {F32: 4, F16: 2, Q4_0: 18, Q8_0: 34, Q2_K: 84, Q3_K: 110, Q4_K: 144, Q5_K: 176, Q6_K: 210, Q8_K: 292, TQ2_0: 66}
-NAMES = {Q4_0: "q4_0", Q8_0: "q8_0", Q2_K: "q2_K", Q3_K: "q3_K", Q4_K: "q4_K", Q5_K: "q5_K", Q6_K: "q6_K", TQ2_0: "tq2_0"}
-ACT = {Q4_0: Q8_0, Q8_0: Q8_0, Q2_K: Q8_K, Q3_K: Q8_K, Q4_K: Q8_K, Q5_K: Q8_K, Q6_K: Q8_K, TQ2_0: Q8_K}
+F32, F16, Q4_0, Q8_0, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K, Q8_K, BF16, TQ2_0 = 0, 1, 2, 8, 10, 11, 12, 13, 14, 15, 30, 35
+BLCK = {F32: 1, F16: 1, BF16: 1, Q4_0: 32, Q8_0: 32, Q2_K: 256, Q3_K: 256, Q4_K: 256, Q5_K: 256, Q6_K: 256, Q8_K: 256,
+        TQ2_0: 256}
+SIZE = {F32: 4, F16: 2, BF16: 2, Q4_0: 18, Q8_0: 34, Q2_K: 84, Q3_K: 110, Q4_K: 144, Q5_K: 176, Q6_K: 210, Q8_K: 292, TQ2_0: 66}
+NAMES = {Q4_0: "q4_0", Q8_0: "q8_0", Q2_K: "q2_K", Q3_K: "q3_K", Q4_K: "q4_K", Q5_K: "q5_K", Q6_K: "q6_K", TQ2_0: "tq2_0",
+         F16: "f16", BF16: "bf16"}
+# activation class (model.c:132-141); bf16 weights take bf16-rounded fp32 rows
+ACT = {Q4_0: Q8_0, Q8_0: Q8_0, Q2_K: Q8_K, Q3_K: Q8_K, Q4_K: Q8_K, Q5_K: Q8_K, Q6_K: Q8_K, TQ2_0: Q8_K, F16: F16, BF16: F32}
 
 _lib = None
 _ref = None
@@ -76,6 +79,10 @@ def lib():
             f.argtypes = [C.c_int, _vp, _vp, _i64]
         L.g4o_dot_f16.restype = C.c_float
         L.g4o_dot_f16.argtypes = [_vp, _vp, _i64]
+        L.g4o_dot_bf16.restype = C.c_float
+        L.g4o_dot_bf16.argtypes = [_vp, _vp, _i64]
+        L.g4o_fp32_to_bf16.restype = C.c_uint16
+        L.g4o_fp32_to_bf16.argtypes = [C.c_float]
         L.g4o_matmul.restype = None
         L.g4o_matmul.argtypes = [C.c_int, _vp, _vp, C.c_size_t, _vp, _i64, _i64, C.c_int, C.c_int]
         L.g4o_prep_act.restype = None
@@ -127,15 +134,17 @@ def ref():
             f = getattr(R, "g4_dot_" + nm + "_x4")
             f.restype = None
             f.argtypes = [_vp, C.POINTER(_vp), _i64, _vp]
-        R.g4_dot_f16.restype = C.c_float
-        R.g4_dot_f16.argtypes = [_vp, _vp, _i64]
+        for nm in ("f16", "bf16"):
+            f = getattr(R, "g4_dot_" + nm)
+            f.restype = C.c_float
+            f.argtypes = [_vp, _vp, _i64]
         R.g4_selftest_quants.restype = C.c_int
         _ref = R
     return _ref
 
 
 DOT_NAME = {Q4_0: "q4_0_q8_0", Q8_0: "q8_0_q8_0", Q2_K: "q2_K_q8_K", Q3_K: "q3_K_q8_K", Q4_K: "q4_K_q8_K",
-            Q5_K: "q5_K_q8_K", Q6_K: "q6_K_q8_K", TQ2_0: "tq2_0_q8_K"}
+            Q5_K: "q5_K_q8_K", Q6_K: "q6_K_q8_K", TQ2_0: "tq2_0_q8_K", F16: "f16", BF16: "bf16"}
 
 
 # ------------------------------------------------------------------ wrappers

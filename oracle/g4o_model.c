@@ -26,12 +26,14 @@ static float dot_q3_K(const void *w, const void *a, int64_t n) { return g4o_dot(
 static float dot_q5_K(const void *w, const void *a, int64_t n) { return g4o_dot(G4O_Q5_K, w, a, n); }
 static float dot_q6_K(const void *w, const void *a, int64_t n) { return g4o_dot(G4O_Q6_K, w, a, n); }
 static float dot_tq2_0(const void *w, const void *a, int64_t n) { return g4o_dot(G4O_TQ2_0, w, a, n); }
+static float dot_f16w(const void *w, const void *a, int64_t n) { return g4o_dot_f16(w, a, n); }
+static float dot_bf16w(const void *w, const void *a, int64_t n) { return g4o_dot_bf16(w, a, n); }
 static float dot_q4_K(const void *w, const void *a, int64_t n) { return g4o_dot(G4O_Q4_K, w, a, n); }
 
-static g4o_dot_fn dot_override[16];
+static g4o_dot_fn dot_override[64];
 
 static g4o_dot_fn dot_for(int wtype) {
-    if (wtype >= 0 && wtype < 16 && dot_override[wtype]) return dot_override[wtype];
+    if (wtype >= 0 && wtype < 64 && dot_override[wtype]) return dot_override[wtype];
     switch (wtype) {
     case G4O_Q8_0: return dot_q8_0;
     case G4O_Q4_0: return dot_q4_0;
@@ -40,12 +42,14 @@ static g4o_dot_fn dot_for(int wtype) {
     case G4O_Q5_K: return dot_q5_K;
     case G4O_Q6_K: return dot_q6_K;
     case G4O_TQ2_0: return dot_tq2_0;
+    case G4O_F16: return dot_f16w;
+    case G4O_BF16: return dot_bf16w;
     case G4O_Q4_K: return dot_q4_K;
     default: return NULL;
     }
 }
 void g4o_set_dot_fn(int wtype, g4o_dot_fn fn) {
-    if (wtype >= 0 && wtype < 16) dot_override[wtype] = fn;
+    if (wtype >= 0 && wtype < 64) dot_override[wtype] = fn;
 }
 static g4o_dot_f16_fn dot_f16_override;
 void g4o_set_dot_f16_fn(g4o_dot_f16_fn fn) { dot_f16_override = fn; }
@@ -130,6 +134,8 @@ int g4o_act_type(int wtype) {
     switch (wtype) {
     case G4O_Q4_0: case G4O_Q8_0: return G4O_Q8_0;
     case G4O_Q2_K: case G4O_Q3_K: case G4O_Q4_K: case G4O_Q5_K: case G4O_Q6_K: case G4O_TQ2_0: return G4O_Q8_K;
+    case G4O_F16: return G4O_F16;                     /* AC_F16 (model.c:163-170) */
+    case G4O_BF16: return G4O_F32;                    /* AC_BF16: bf16-rounded fp32 (model.c:172-180) */
     default: return -1;
     }
 }
@@ -142,8 +148,19 @@ void g4o_prep_act(int wtype, const float *x, int64_t ncols, int nb, void *qa) {
     size_t st = g4o_act_stride(wtype, ncols);
     for (int b = 0; b < nb; b++) {
         uint8_t *dst = (uint8_t *)qa + (size_t)b * st;
-        if (g4o_act_type(wtype) == G4O_Q8_0) g4o_quantize_q8_0(x + (size_t)b * ncols, (g4o_q8_0 *)dst, ncols);
-        else g4o_quantize_q8_K(x + (size_t)b * ncols, (g4o_q8_K *)dst, ncols);
+        const float *src = x + (size_t)b * ncols;
+        if (wtype == G4O_F16) {
+            for (int64_t i = 0; i < ncols; i++) ((uint16_t *)dst)[i] = g4o_fp32_to_fp16(src[i]);
+        } else if (wtype == G4O_BF16) {
+            for (int64_t i = 0; i < ncols; i++) {
+                uint32_t u = (uint32_t)g4o_fp32_to_bf16(src[i]) << 16;
+                memcpy((float *)dst + i, &u, 4);
+            }
+        } else if (g4o_act_type(wtype) == G4O_Q8_0) {
+            g4o_quantize_q8_0(src, (g4o_q8_0 *)dst, ncols);
+        } else {
+            g4o_quantize_q8_K(src, (g4o_q8_K *)dst, ncols);
+        }
     }
 }
 

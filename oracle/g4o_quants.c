@@ -16,7 +16,7 @@
 /* gguf.c:11-25: elements per block / bytes per block. */
 int g4o_type_blck(int t) {
     switch (t) {
-    case G4O_F32: case G4O_F16: return 1;
+    case G4O_F32: case G4O_F16: case G4O_BF16: return 1;
     case G4O_Q4_0: case G4O_Q8_0: return 32;
     case G4O_Q2_K: case G4O_Q3_K: case G4O_Q4_K: case G4O_Q5_K: case G4O_Q6_K: case G4O_Q8_K: case G4O_TQ2_0: return 256;
     default: return 0;
@@ -25,7 +25,7 @@ int g4o_type_blck(int t) {
 size_t g4o_type_size(int t) {
     switch (t) {
     case G4O_F32: return 4;
-    case G4O_F16: return 2;
+    case G4O_F16: case G4O_BF16: return 2;
     case G4O_Q4_0: return sizeof(g4o_q4_0);
     case G4O_Q8_0: return sizeof(g4o_q8_0);
     case G4O_Q2_K: return sizeof(g4o_q2_K);
@@ -253,6 +253,11 @@ int g4o_dequant_row(int type, const void *vx, float *y, int64_t n) {
     switch (type) {
     case G4O_F32: memcpy(y, vx, (size_t)n * 4); return 0;
     case G4O_F16: { const uint16_t *h = vx; for (int64_t i = 0; i < n; i++) y[i] = g4o_fp16_to_fp32(h[i]); return 0; }
+    case G4O_BF16: {                                       /* quants.c:520: the high half of an fp32 */
+        const uint16_t *h = vx;
+        for (int64_t i = 0; i < n; i++) { uint32_t u = (uint32_t)h[i] << 16; memcpy(&y[i], &u, 4); }
+        return 0;
+    }
     case G4O_Q8_0: {                                       /* quants.c:373-378 */
         const g4o_q8_0 *x = vx;
         for (int64_t b = 0; b < n / 32; b++) {
@@ -416,6 +421,16 @@ void g4o_block_sums(int type, const void *w, const void *a, int64_t n, int32_t *
 float g4o_dot_ref(int type, const void *vw, const void *va, int64_t n) {
     float acc = 0.0f;
     switch (type) {
+    case G4O_F16: {                                       /* quants.c:1509-1513 (non-AVX2 build) */
+        const uint16_t *w = vw, *a = va;
+        for (int64_t i = 0; i < n; i++) acc += g4o_fp16_to_fp32(w[i]) * g4o_fp16_to_fp32(a[i]);
+        return acc;
+    }
+    case G4O_BF16: {                                      /* quants.c:1514-1518 */
+        const uint16_t *w = vw; const float *a = va;
+        for (int64_t i = 0; i < n; i++) { uint32_t u = (uint32_t)w[i] << 16; float f; memcpy(&f, &u, 4); acc += f * a[i]; }
+        return acc;
+    }
     case G4O_Q8_0: {                                      /* quants.c:552-562 */
         const g4o_q8_0 *w = vw, *a = va;
         for (int64_t b = 0; b < n / 32; b++)
@@ -635,10 +650,33 @@ float g4o_dot(int type, const void *w, const void *a, int64_t n) {
     case G4O_Q5_K: return dot_q5_K_avx2(w, a, n / 256);
     case G4O_Q6_K: return dot_q6_K_avx2(w, a, n / 256);
     case G4O_TQ2_0: return dot_tq2_0_avx2(w, a, n / 256);
+    case G4O_F16: return g4o_dot_f16(w, a, n);
+    case G4O_BF16: return g4o_dot_bf16(w, a, n);
     default: return NAN;
     }
 }
 
+/* g4run.h:64-68: a NaN keeps its high half with the quiet bit set; otherwise
+ * round to nearest even by adding 0x7fff plus the kept lsb, then truncating. */
+uint16_t g4o_fp32_to_bf16(float f) {
+    uint32_t x; memcpy(&x, &f, 4);
+    if ((x & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((x >> 16) | 64u);
+    return (uint16_t)((x + (0x7fffu + ((x >> 16) & 1u))) >> 16);
+}
+/* quants.c:1333-1347: as g4_dot_f16 with the weights widened by a 16-bit shift
+ * and fp32 activations. */
+float g4o_dot_bf16(const uint16_t *w, const float *a, int64_t n) {
+    float acc[8] = {0};
+    int64_t i = 0;
+    for (; i + 8 <= n; i += 8)
+        for (int l = 0; l < 8; l++) {
+            uint32_t u = (uint32_t)w[i + l] << 16; float f; memcpy(&f, &u, 4);
+            acc[l] = fmaf(f, a[i + l], acc[l]);
+        }
+    float s = hsum8(acc);
+    for (; i < n; i++) { uint32_t u = (uint32_t)w[i] << 16; float f; memcpy(&f, &u, 4); s += f * a[i]; }
+    return s;
+}
 /* quants.c:1319-1331: 8 fp32 lanes of fused products, tree sum, scalar tail. */
 float g4o_dot_f16(const uint16_t *w, const uint16_t *a, int64_t n) {
     float acc[8] = {0};

@@ -12,6 +12,11 @@ Each fixture holds inputs and the reference build's outputs, nothing else:
                     activations, AVX2 dots, scalar _ref dots, x4 dots,
                     dequantized rows and per-block integer sums obtained from
                     the reference's scalar dots with unit scales
+  dot_f16.npz / dot_bf16.npz  f16 / bf16 weight rows, fp32 activations, the
+                    activations as prep_act converts them (model.c:163-180,
+                    with the header's inline conversions restated by the
+                    oracle), the reference build's g4_dot_f16 / g4_dot_bf16
+                    and its dequantized rows
   tables.npz        fp16->fp32 table and GELU fp16 table of g4_init_tables
 """
 from __future__ import annotations
@@ -177,6 +182,28 @@ def main(only=None):
         sums = np.array([unit_sums(R, qt, w[r], a[0], n) for r in range(rows)])
         np.savez_compressed(os.path.join(HERE, f"dot_{NAME[qt]}.npz"), w=w, x=x, a=a, dot=dot, dot_ref=dot_ref,
                             dot_x4=dot_x4, deq=deq, sums=sums, n=n, flags=flags)
+
+    # f16 / bf16 weights (quants.c:1319-1347); n has a tail past the 8-lane loop
+    for name, wt in (("f16", 1), ("bf16", 30)):
+        if only and name not in only:
+            continue
+        sys.path.insert(0, ROOT)
+        from oracle import g4o
+        rng = np.random.default_rng(200 + wt)
+        rows, nb_tok, n = 16, 4, 2053
+        wf = (rng.standard_normal((rows, n)) * 0.02).astype(np.float32)
+        w = g4o.fp32_to_fp16(wf).reshape(rows, n) if wt == 1 else (wf.view(np.uint32) >> 16).astype(np.uint16)
+        x = rng.standard_normal((nb_tok, n)).astype(np.float32)
+        a = np.stack([g4o.prep_act(wt, x[t:t + 1])[0][: n * (2 if wt == 1 else 4)] for t in range(nb_tok)])
+        fn = getattr(R, "g4_dot_" + name)
+        fn.restype = C.c_float
+        fn.argtypes = [vp, vp, C.c_int64]
+        dot = np.array([[fn(ptr(w[r]), ptr(a[t]), n) for r in range(rows)] for t in range(nb_tok)], np.float32)
+        deq = np.zeros((rows, n), np.float32)
+        for r in range(rows):
+            R.g4_dequant_row(wt, ptr(w[r]), ptr(deq[r]), n)
+        np.savez_compressed(os.path.join(HERE, f"dot_{name}.npz"), w=w.view(np.uint8).reshape(rows, 2 * n), x=x, a=a,
+                            dot=dot, deq=deq, n=n, flags=flags)
 
     if only:
         print("fixtures written to", HERE)

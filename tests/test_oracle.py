@@ -223,3 +223,61 @@ def test_gelu_table_matches_reference(oracle):
     mine = oracle.gelu_table()
     diff = np.nonzero(mine != g)[0]
     assert diff.size == 0, f"{diff.size} GELU codes differ, first {diff[:8]}"
+
+
+# ------------------------------------------------------ f16 / bf16 weights
+FLOAT_FMTS = [("f16", 1), ("bf16", 30)]
+
+
+@pytest.mark.parametrize("name,wt", FLOAT_FMTS)
+def test_float_dots_match_reference_fixtures(oracle, name, wt):
+    """g4_dot_f16 / g4_dot_bf16 of the reference build (8 fused lanes, the
+    hsum tree, a scalar tail: n = 2053) reproduced bit for bit."""
+    g = gold(f"dot_{name}.npz")
+    n = int(g["n"])
+    w = g["w"]
+    assert np.array_equal(np.stack([oracle.prep_act(wt, g["x"][t:t + 1])[0][: g["a"].shape[1]] for t in range(g["x"].shape[0])]), g["a"])
+    d = np.array([[oracle.dot(wt, w[r], g["a"][t], n) for r in range(w.shape[0])] for t in range(g["a"].shape[0])], np.float32)
+    assert np.array_equal(bits(d), bits(g["dot"]))
+    assert np.array_equal(bits(oracle.dequant(wt, w, n)), bits(g["deq"]))
+    # the scalar fallback order only to the selftest's tolerance
+    ref = np.array([[oracle.dot(wt, w[r], g["a"][t], n, "ref") for r in range(w.shape[0])] for t in range(g["a"].shape[0])])
+    assert np.all(np.abs(ref - g["dot"]) <= 1e-3 * (1 + np.abs(g["dot"])))
+
+
+def test_bf16_rounding_is_nearest_even(oracle):
+    """g4_fp32_to_bf16 (g4run.h:64-68), through prep_act's AC_BF16 rows
+    (model.c:172-180), against a selection made in float64: the nearer of the
+    two bf16 neighbours (2^128 standing in past the largest finite value),
+    ties to the even mantissa, NaN kept quiet with its high half.  The values
+    go in as an array: a subnormal passed as a C float argument would be
+    flushed by the -Ofast reference library's FTZ mode in this process."""
+    rng = np.random.default_rng(11)
+    u = rng.integers(0, 2 ** 32, size=20000, dtype=np.uint64).astype(np.uint32)
+    special = np.array([0x00000000, 0x80000000, 0x7f800000, 0xff800000, 0x7f7fffff, 0x00008000, 0x00018000,
+                        0x3f808000, 0x3f818000, 0x7fc00001, 0xffa00000, 0x7f800001, 0x00203f76, 0xff7f8d0d], np.uint32)
+    xs = np.concatenate([u, special])
+    got = oracle.prep_act(30, xs.view(np.float32)[None, :])[0][: 4 * xs.size].view(np.uint32) >> 16
+    import math
+
+    def val(b):                                           # exact value of fp32 bits, no FPU subnormal path
+        sg = -1.0 if b >> 31 else 1.0
+        e, m = (b >> 23) & 0xFF, b & 0x7FFFFF
+        return sg * (math.ldexp(m, -149) if e == 0 else math.ldexp(m | 0x800000, e - 150))
+
+    for x, g in zip(xs.tolist(), got.tolist()):
+        if (x & 0x7FFFFFFF) > 0x7F800000:
+            assert g == ((x >> 16) | 64)
+            continue
+        lo, hi = x >> 16, (x >> 16) + 1
+        f, flo = val(x), val(lo << 16)
+        if (hi & 0x7FFF) == 0x7F80:                       # overflow: IEEE measures against 2^128
+            fhi = (-1.0 if x >> 31 else 1.0) * 2.0 ** 128
+        else:
+            fhi = val((hi & 0xFFFF) << 16)
+        if (x & 0x7FFFFFFF) == 0x7F800000:
+            assert g == lo
+            continue
+        dl, dh = abs(f - flo), abs(fhi - f)
+        want = lo if (dl < dh or (dl == dh and lo % 2 == 0)) else hi
+        assert g == (want & 0xFFFF), hex(x)
