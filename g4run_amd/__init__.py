@@ -82,6 +82,7 @@ _SIGS = [
     ("g4h_attn_workspace_bytes", _sz, [_int, _int, _int]),
     ("g4h_attn_passes", _int, [_int, _int, _int, _int, _int, C.POINTER(_int)]),
     ("g4h_attn_decode", _int, [_vp, _vp, _vp, _int, _int, _int, _int, _int, _vp, _vp, _sz, _vp]),
+    ("g4h_attn_prefill", _int, [_vp, _vp, _vp, _int, _int, _int, _int, _int, _int, _vp, _vp, _sz, _vp]),
     ("g4h_kv_store", _int, [_int, _vp, _vp, _int, _int, _sz, _vp]),
     ("g4h_model_create", _int, [_vp, C.c_uint64, C.POINTER(_vp)]),
     ("g4h_model_free", _int, [_vp]),
@@ -356,6 +357,16 @@ def attn_decode(q, kc, vc, kv_type: int, n_head: int, n_kv: int, hd: int, n_pos:
         ws = Buffer(need)
     check(lib().g4h_attn_decode(_p(q), _p(kc), _p(vc), kv_type, n_head, n_kv, hd, n_pos, _p(out), _p(ws),
                                 ws.nbytes if isinstance(ws, Buffer) else need, stream))
+
+
+def attn_prefill(q, kc, vc, kv_type: int, n_head: int, n_kv: int, hd: int, pos0: int, nb: int, out, ws=None,
+                 stream=None) -> None:
+    """attn_kernel for nb new tokens at positions pos0.. (causal)."""
+    need = attn_workspace_bytes(n_head, hd, pos0 + nb)
+    if ws is None:
+        ws = Buffer(need)
+    check(lib().g4h_attn_prefill(_p(q), _p(kc), _p(vc), kv_type, n_head, n_kv, hd, pos0, nb, _p(out), _p(ws),
+                                 ws.nbytes if isinstance(ws, Buffer) else need, stream))
 
 
 def kv_store(kv_type: int, src, dst, hd: int, rows: int = 1, dst_stride: int = 0, stream=None) -> None:

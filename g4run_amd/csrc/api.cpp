@@ -586,6 +586,21 @@ extern "C" int g4h_attn_decode(const float *q, const void *kc, const void *vc, i
     return G4H_OK;
 }
 
+extern "C" int g4h_attn_prefill(const float *q, const void *kc, const void *vc, int kv_type, int n_head, int n_kv, int hd,
+                                int pos0, int nb, float *out, void *ws, size_t ws_bytes, void *s) {
+    G4_NEED_INIT();
+    if (!q || !out || nb < 0 || pos0 < 0 || n_head <= 0 || hd <= 0) return fail(G4H_ERR_ARG, "g4h_attn_prefill: bad argument");
+    if (nb == 0) return G4H_OK;
+    if (ws_bytes < g4h_attn_workspace_bytes(n_head, hd, pos0 + nb))
+        return fail(G4H_ERR_ARG, "g4h_attn_prefill: workspace smaller than g4h_attn_workspace_bytes(n_head, hd, pos0 + nb)");
+    // model.c:514-521: token b at pos0 + b attends [0, pos0 + b]
+    for (int b = 0; b < nb; b++) {
+        const size_t off = (size_t)b * n_head * hd;
+        if (int rc = g4h_attn_decode(q + off, kc, vc, kv_type, n_head, n_kv, hd, pos0 + b + 1, out + off, ws, ws_bytes, s)) return rc;
+    }
+    return G4H_OK;
+}
+
 extern "C" int g4h_kv_store(int kv_type, const float *src, void *dst, int hd, int rows, size_t dst_stride, void *stream) {
     G4_NEED_INIT();
     if (!src || !dst || hd <= 0 || rows < 0) return fail(G4H_ERR_ARG, "g4h_kv_store: bad argument");

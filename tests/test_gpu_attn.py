@@ -123,3 +123,26 @@ def test_attention_long_context_falls_back_to_three_passes(gpu, oracle):
     got = _attn(G, q, kb, vb, G.F16, n_head, n_kv, hd, n_pos, None)
     ref = oracle.attn_decode(q, kh, vh, G.F16, n_head, n_kv, hd, n_pos - 1)
     assert (np.abs(got - ref) <= ATOL + RTOL * np.abs(ref)).all()
+
+
+@pytest.mark.parametrize("kv_type", [1, 8, 2], ids=["f16", "q8_0", "q4_0"])
+@pytest.mark.parametrize("pos0,nb", [(0, 9), (300, 7), (4090, 6)])
+def test_batched_prefill_attention_is_causal(gpu, oracle, kv_type, pos0, nb):
+    """attn_kernel with nb > 1 (model.c:509-545): token b at pos0 + b attends
+    exactly the positions up to its own, the batch's rows already cached."""
+    G = gpu
+    n_head, n_kv, hd = 8, 4, 256
+    n_slot = pos0 + nb
+    kb, vb, kh, vh = make_cache(G, oracle, kv_type, n_slot, n_kv, hd, seed=n_slot)
+    q = (np.random.default_rng(nb).standard_normal((nb, n_head, hd)) * 0.5).astype(np.float32)
+    out = G.Buffer(nb * n_head * hd * 4)
+    G.attn_prefill(G.Buffer.from_array(q), kb, vb, kv_type, n_head, n_kv, hd, pos0, nb, out)
+    got = out.download(np.float32, (nb, n_head, hd))
+    for b in range(nb):
+        ref = oracle.attn_decode(q[b], kh, vh, kv_type, n_head, n_kv, hd, pos0 + b)
+        err = np.abs(got[b].astype(np.float64) - ref)
+        assert not (err > ATOL + RTOL * np.abs(ref)).any(), f"token {b}: worst {err.max():.3g}"
+    # the first token sees only its own position when pos0 = 0: output = its V row
+    if pos0 == 0 and kv_type == 1:
+        v0 = oracle.fp16_to_fp32(vh[:n_kv].view(np.uint16).reshape(n_kv, hd))
+        assert np.allclose(got[0], np.repeat(v0, n_head // n_kv, axis=0), rtol=0, atol=0)
