@@ -156,12 +156,19 @@ int    g4o_model_decode(const g4o_model *m, int token, int pos, float *logits,
  *   quantize_q8_0/q8_K    bit-exact vs the reference build oracle/_ref and the
  *                         committed fixtures; closed-form special cases
  *   quantize_q4_0         bit-exact vs oracle/_ref
- *   dequant (5 formats)   bit-exact vs oracle/_ref on random blocks
+ *   dequant               bit-exact vs oracle/_ref on random blocks and the
+ *                         committed fixtures (q8_0 .. q6_K, tq2_0, f16, bf16)
  *   block_sums            brute-force dequant identity in exact integer math,
  *                         and unit-scale calls of the reference _ref dots
  *   dot_ref               bit-exact vs the reference's scalar _ref dots
  *   dot (AVX2 order)      bit-exact vs the reference's AVX2 dots (oracle/_ref)
- *   dot_f16               bit-exact vs the reference's g4_dot_f16
+ *   dot_f16 / dot_bf16    bit-exact vs the reference's g4_dot_f16 / g4_dot_bf16
+ *                         (fixtures with a scalar tail, n = 2053)
+ *   tq2_0 (dequant, sums, dots)
+ *                         bit-exact vs the reference's fixtures and live build,
+ *                         sums also by the brute-force dequant identity
+ *   fp32_to_bf16          float64 nearest-even selection over random and
+ *                         special bit patterns (NaN, overflow, subnormals)
  *   matmul                row loop of dot(); x4 == x1 invariant
  *   rms_norm, rope, attention, decode graph
  *                         model.c does not compile here (windows.h), so these
