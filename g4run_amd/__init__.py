@@ -26,7 +26,9 @@ SIZE = {F32: 4, F16: 2, BF16: 2, Q4_0: 18, Q8_0: 34, Q2_K: 84, Q3_K: 110, Q4_K: 
 TYPE_NAMES = {Q4_0: "q4_0", Q8_0: "q8_0", Q2_K: "q2_K", Q3_K: "q3_K", Q4_K: "q4_K", Q5_K: "q5_K", Q6_K: "q6_K", Q8_K: "q8_K",
               TQ2_0: "tq2_0", F16: "f16", BF16: "bf16", F32: "f32"}
 
-OK, ERR_ARG, ERR_TYPE, ERR_SHAPE, ERR_NOMEM, ERR_DEVICE, ERR_HIP = range(7)
+OK, ERR_ARG, ERR_TYPE, ERR_SHAPE, ERR_NOMEM, ERR_DEVICE, ERR_HIP, ERR_TIMEOUT = range(8)
+# g4h_model_status flags
+STATUS_CTX_FULL, STATUS_ATTN_TIMEOUT = 1, 2
 
 _vp, _i64, _sz, _int = C.c_void_p, C.c_int64, C.c_size_t, C.c_int
 
@@ -43,6 +45,7 @@ _SIGS = [
     ("g4h_last_error", C.c_char_p, []),
     ("g4h_status_str", C.c_char_p, [_int]),
     ("g4h_debug_fail_alloc", None, [_int]),
+    ("g4h_debug_attn_timeout", None, [_int]),
     ("g4h_malloc", _int, [C.POINTER(_vp), _sz]),
     ("g4h_free", _int, [_vp]),
     ("g4h_memcpy_h2d", _int, [_vp, _vp, _sz, _vp]),
@@ -82,6 +85,7 @@ _SIGS = [
     ("g4h_attn_workspace_bytes", _sz, [_int, _int, _int]),
     ("g4h_attn_passes", _int, [_int, _int, _int, _int, _int, C.POINTER(_int)]),
     ("g4h_attn_decode", _int, [_vp, _vp, _vp, _int, _int, _int, _int, _int, _vp, _vp, _sz, _vp]),
+    ("g4h_attn_status", _int, [_vp, C.POINTER(_int), _vp]),
     ("g4h_attn_prefill", _int, [_vp, _vp, _vp, _int, _int, _int, _int, _int, _int, _vp, _vp, _sz, _vp]),
     ("g4h_kv_store", _int, [_int, _vp, _vp, _int, _int, _sz, _vp]),
     ("g4h_model_create", _int, [_vp, C.c_uint64, C.POINTER(_vp)]),
@@ -91,6 +95,9 @@ _SIGS = [
     ("g4h_forward_state", _int, [_vp, _vp]),
     ("g4h_model_set_state", _int, [_vp, _int, _int, _vp]),
     ("g4h_model_get_state", _int, [_vp, C.POINTER(_int), C.POINTER(_int), _vp]),
+    ("g4h_model_status", _int, [_vp, C.POINTER(_int), _vp]),
+    ("g4h_model_gelu_table", _vp, [_vp]),
+    ("g4h_model_trace", _int, [_vp, _vp]),
     ("g4h_model_logits", _vp, [_vp]),
     ("g4h_model_matrix", _vp, [_vp, _int, _int]),
     ("g4h_model_norm", _vp, [_vp, _int, _int]),
@@ -359,6 +366,19 @@ def attn_decode(q, kc, vc, kv_type: int, n_head: int, n_kv: int, hd: int, n_pos:
                                 ws.nbytes if isinstance(ws, Buffer) else need, stream))
 
 
+def attn_status(ws, stream=None) -> bool:
+    """True if an attention call on ws had a hand-off wait give up since the
+    last query (its outputs are NaN); clears the flag."""
+    f = _int()
+    check(lib().g4h_attn_status(_p(ws), C.byref(f), stream))
+    return bool(f.value)
+
+
+def debug_attn_timeout(on: bool) -> None:
+    """Test hook: every attention hand-off wait gives up (bounded), or normal operation."""
+    lib().g4h_debug_attn_timeout(1 if on else 0)
+
+
 def attn_prefill(q, kc, vc, kv_type: int, n_head: int, n_kv: int, hd: int, pos0: int, nb: int, out, ws=None,
                  stream=None) -> None:
     """attn_kernel for nb new tokens at positions pos0.. (causal)."""
@@ -437,6 +457,36 @@ class Model:
         t, p = _int(), _int()
         check(lib().g4h_model_get_state(self.ptr, C.byref(t), C.byref(p), stream))
         return t.value, p.value
+
+    def status(self, stream=None) -> int:
+        """STATUS_* flags of the device-side steps since the last set_state."""
+        f = _int()
+        check(lib().g4h_model_status(self.ptr, C.byref(f), stream))
+        return f.value
+
+    def trace(self, buf) -> None:
+        """Copy each layer's input x, q|k|v projection and attention output (and
+        the final x) into buf every step (trace_floats() floats), or stop with None."""
+        check(lib().g4h_model_trace(self.ptr, _p(buf) if buf is not None else None))
+
+    def trace_fields(self):
+        """(name, offset, length) of the per-layer trace record, and its size."""
+        c = self.cfg
+        E, R, Q, F = c["n_embd"], (c["n_head"] + 2 * c["n_kv"]) * c["head_dim"], c["n_head"] * c["head_dim"], c["n_ff"]
+        fields, off = [], 0
+        for name, n in (("x", E), ("qkv", R), ("att", Q), ("wo", E), ("xmid", E), ("h", F), ("down", E)):
+            fields.append((name, off, n))
+            off += n
+        return fields, off
+
+    def trace_floats(self) -> int:
+        _, rec = self.trace_fields()
+        return self.cfg["n_layer"] * rec + self.cfg["n_embd"]
+
+    def gelu_table(self) -> np.ndarray:
+        out = np.empty(65536, np.uint16)
+        check(lib().g4h_memcpy_d2h(out.ctypes.data_as(_vp), lib().g4h_model_gelu_table(self.ptr), out.nbytes, None))
+        return out
 
     def logits(self) -> np.ndarray:
         n = self.cfg["n_vocab"]

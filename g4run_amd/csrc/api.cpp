@@ -51,11 +51,13 @@ extern "C" const char *g4h_status_str(int s) {
     case G4H_ERR_NOMEM: return "out of device memory";
     case G4H_ERR_DEVICE: return "no usable device";
     case G4H_ERR_HIP: return "HIP runtime error";
+    case G4H_ERR_TIMEOUT: return "device-side wait gave up";
     default: return "unknown status";
     }
 }
 
 extern "C" void g4h_debug_fail_alloc(int n) { g_fail_alloc.store(n < 0 ? 0 : n); }
+extern "C" void g4h_debug_attn_timeout(int on) { attn_force_timeout(on != 0); }
 
 extern "C" int g4h_init(int device) {
     int n = 0;
@@ -583,6 +585,21 @@ extern "C" int g4h_attn_decode(const float *q, const void *kc, const void *vc, i
     a.kc = (uint8_t *)kc;          // read only: no preparation on this entry point
     a.vc = (uint8_t *)vc;
     G4_HIP(launch_attn_decode(q, nullptr, a, n_pos, nullptr, n_pos, out, nullptr, (uint8_t *)ws, (hipStream_t)stream));
+    return G4H_OK;
+}
+
+extern "C" int g4h_attn_status(void *ws, int *failed, void *stream) {
+    G4_NEED_INIT();
+    if (!ws || !failed) return fail(G4H_ERR_ARG, "g4h_attn_status: null pointer");
+    const hipStream_t s = (hipStream_t)stream;
+    unsigned err = 0;
+    G4_HIP(hipMemcpyAsync(&err, (uint8_t *)ws + ATTN_ERR_OFFSET, sizeof err, hipMemcpyDeviceToHost, s));
+    G4_HIP(hipStreamSynchronize(s));
+    *failed = err ? 1 : 0;
+    if (err) {
+        G4_HIP(hipMemsetAsync((uint8_t *)ws + ATTN_ERR_OFFSET, 0, sizeof err, s));
+        G4_HIP(hipStreamSynchronize(s));
+    }
     return G4H_OK;
 }
 

@@ -33,7 +33,8 @@
 // double grouping of the normaliser differ from the CPU's sequential loops;
 // the one-launch and three-launch forms give identical bits.
 #include <algorithm>
-
+#include <map>
+#include <mutex>
 #include <type_traits>
 
 #include "formats.h"
@@ -156,6 +157,8 @@ struct AttnCtx {
     const unsigned *epoch;
     unsigned tag_mul, tag_add;
     unsigned *err;           // set when a poll gives up
+    unsigned spin;           // polls give up after this many retries
+    uint32_t poll_xor;       // nonzero (test hook only): polls wait for a tag no store carries
     // one launch with the q|k|v projection folded in (decode step): every
     // workgroup computes qrows projection rows of W from the RMSNorm prologue
     // `pro` and publishes them as tagged words QT [rows] (one 128-byte line
@@ -845,9 +848,12 @@ __global__ __launch_bounds__(256) void k_attn_combine(AttnCtx c) {
 // across the XCDs' L2 caches).  A 64-bit store is single-copy atomic, so a
 // reader that sees the current tag sees the value stored with it; readers poll
 // until every word they need carries the tag.  Tags never repeat on one
-// workspace (see AttnCtx::tag).  A poll gives up after ATT_SPIN_LIMIT tries:
-// it sets the error word and writes NaN into the outputs it owns, so the
-// launch always ends.  Same arithmetic as the three passes: outputs are
+// workspace (see AttnCtx::tag).  A poll gives up after AttnCtx::spin retries
+// (ATT_SPIN_LIMIT): the workgroup writes NaN into the outputs it owns and sets
+// the error word, so the launch always ends and the host sees the failure
+// (g4h_attn_status, g4h_model_status).  A test hook makes every poll wait for
+// a tag that no store carries, with a short limit, so the failure path runs
+// deterministically while every kernel still ends.  Same arithmetic as the three passes: outputs are
 // bit-identical to theirs.
 constexpr unsigned ATT_SPIN_LIMIT = 1u << 20;
 constexpr int ATT_FUSED_MAXC = 128;  // chunks per KV head (two per lane)
@@ -864,7 +870,7 @@ __device__ __forceinline__ void st_tag(uint64_t *p, uint32_t bits, uint32_t tag)
 // current, the stale words are reloaded together
 template <int N>
 __device__ __forceinline__ bool poll_words(const uint64_t *const (&src)[N], const bool (&need)[N], uint32_t tag,
-                                           uint32_t (&bits)[N]) {
+                                           uint32_t (&bits)[N], unsigned spin) {
     uint64_t w[N];
 #pragma unroll
     for (int k = 0; k < N; k++) w[k] = need[k] ? ld_ag(src[k]) : ((uint64_t)tag << 32);
@@ -873,7 +879,7 @@ __device__ __forceinline__ bool poll_words(const uint64_t *const (&src)[N], cons
 #pragma unroll
         for (int k = 0; k < N; k++) all &= (uint32_t)(w[k] >> 32) == tag;
         if (all) break;
-        if (it == ATT_SPIN_LIMIT) return false;
+        if (it >= spin) return false;
         __builtin_amdgcn_s_sleep(ATT_POLL_SLEEP);
 #pragma unroll
         for (int k = 0; k < N; k++)
@@ -904,7 +910,7 @@ __device__ __forceinline__ bool prep_f16_poll(PrepF16<GRP> &st, const AttnCtx &c
                 src[e] = c.QT + (size_t)src_row * hd + lane * epl + min(e, epl - 1);
                 need[e] = e < epl;
             }
-            ok &= poll_words<4>(src, need, tag, bits);
+            ok &= poll_words<4>(src, need, tag ^ c.poll_xor, bits, c.spin);
 #pragma unroll
             for (int e = 0; e < 4; e++) st.pr[sl].v[e] = e < epl ? __uint_as_float(bits[e]) : 0.0f;
         }
@@ -1092,7 +1098,7 @@ __global__ __launch_bounds__(256) void k_attn_fused_f16(AttnCtx c) {
                         src[3 * r + k] = w3 + (size_t)min(ci, nch - 1) * ATT_TW + k;
                         need[3 * r + k] = ci < nch;
                     }
-                if (!poll_words<6>(src, need, tag, bits)) bad = 1;
+                if (!poll_words<6>(src, need, tag ^ c.poll_xor, bits, c.spin)) bad = 1;
                 float mc[2];
                 double lc[2];
 #pragma unroll
@@ -1163,7 +1169,7 @@ __global__ __launch_bounds__(256) void k_attn_fused_f16(AttnCtx c) {
             src[q] = base + (size_t)min(k, nch - 1) * hd;
             need[q] = k < nch;
         }
-        if (!poll_words<PER>(src, need, tag, bits)) bad = 1;
+        if (!poll_words<PER>(src, need, tag ^ c.poll_xor, bits, c.spin)) bad = 1;
 #pragma unroll
         for (int q = 0; q < PER; q++)
             if (need[q]) vals[(r0 + 8 * q) * 32 + i] = __uint_as_float(bits[q]);
@@ -1200,10 +1206,7 @@ __global__ __launch_bounds__(256) void k_attn_fused_f16(AttnCtx c) {
 #pragma unroll
                 for (int q = 0; q < 8; q++) r += v[q];
             }
-            if (bad) {
-                r = __builtin_nanf("");
-                st_ag(c.err, 1u);
-            }
+            if (bad) r = __builtin_nanf("");
             c.out[(size_t)(h0 + g) * hd + e0 + t] = r;
         }
         if (c.q8out) {                                               // uniform
@@ -1218,6 +1221,10 @@ __global__ __launch_bounds__(256) void k_attn_fused_f16(AttnCtx c) {
             }
         }
     }
+    // any poll of this workgroup that gave up (its partials or outputs are not
+    // valid) is reported, whether or not it owned a combine block
+    lds_barrier();
+    if (t == 0 && bad) st_ag(c.err, 1u);
 }
 
 // ------------------------------------------------------------- KV store --
@@ -1233,43 +1240,61 @@ __global__ void k_attn_clear(uint64_t *w, size_t n) {
     for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) w[i] = 0;
 }
 
-// Workspace: S [n_head][npos] f32 scores, Mc [n_head][nc] f32 chunk maxima,
-// Lc [n_head][nc] f64 chunk sums, P [n_head][nc][hd] f32 partials (three
-// passes); then the fused launch's words: T [n_head][nc][ATT_TW] (3 used), PT
-// [n_head][nc][hd], and epoch, error (one 64-bit word each).
+// Workspace: the error word (offset 0, the same for every shape, sticky until
+// g4h_attn_status reads it), S [n_head][npos] f32 scores, Mc [n_head][nc] f32
+// chunk maxima, Lc [n_head][nc] f64 chunk sums, P [n_head][nc][hd] f32
+// partials (three passes); then the fused launch's epoch word and its tagged
+// words T [n_head][nc][ATT_TW] (3 used) and PT [n_head][nc][hd].
 static size_t al256(size_t v) { return (v + 255) & ~(size_t)255; }
 struct AttnWs {
-    size_t S, Mc, Lc, P, T, PT, misc, total;
+    size_t err, S, Mc, Lc, P, epoch, T, PT, total;
 };
 static AttnWs attn_ws(int n_head, int hd, int npos_max) {
     const size_t nc = (npos_max + ATT_CHUNK - 1) / ATT_CHUNK;
     AttnWs w;
-    w.S = 0;
+    w.err = 0;
+    w.S = 256;
     w.Mc = w.S + al256((size_t)n_head * npos_max * 4);
     w.Lc = w.Mc + al256((size_t)n_head * nc * 4);
     w.P = w.Lc + al256((size_t)n_head * nc * 8);
-    w.T = w.P + al256((size_t)n_head * nc * hd * 4);
+    w.epoch = w.P + al256((size_t)n_head * nc * hd * 4);
+    w.T = w.epoch + 256;
     w.PT = w.T + al256((size_t)n_head * nc * ATT_TW * 8);
-    w.misc = w.PT + al256((size_t)n_head * nc * hd * 8);
-    w.total = w.misc + 256;
+    w.total = w.PT + al256((size_t)n_head * nc * hd * 8);
     return w;
 }
 size_t attn_workspace_bytes(int n_head, int hd, int npos_max) { return attn_ws(n_head, hd, npos_max).total; }
-uint64_t *attn_ws_epoch(uint8_t *ws, int n_head, int hd, int npos_max) {
-    return (uint64_t *)(ws + attn_ws(n_head, hd, npos_max).misc);
+
+static unsigned g_attn_spin = ATT_SPIN_LIMIT;
+static uint32_t g_attn_poll_xor = 0;
+void attn_force_timeout(bool on) {
+    g_attn_spin = on ? 64u : ATT_SPIN_LIMIT;
+    g_attn_poll_xor = on ? 0x80000000u : 0u;
 }
 
-// workgroups of the fused kernel the device holds resident at once
+// workgroups of 256 threads of one kernel instantiation, with `lds` bytes of
+// dynamic LDS, that the device holds resident at once (cached per instantiation
+// and LDS size)
+static int resident_capacity(const void *kernel, size_t lds) {
+    static std::mutex mu;
+    static std::map<std::pair<const void *, size_t>, int> cache;
+    std::lock_guard<std::mutex> lk(mu);
+    const auto key = std::make_pair(kernel, lds);
+    const auto it = cache.find(key);
+    if (it != cache.end()) return it->second;
+    int dev = 0, cus = 0, occ = 0;
+    int cap = 0;
+    if (hipGetDevice(&dev) == hipSuccess && hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, kernel, 256, lds) == hipSuccess)
+        cap = cus * occ;
+    cache[key] = cap;
+    return cap;
+}
+
+// workgroups of the plain fused kernel the device holds resident at once
 template <int GRP, int HD>
 static int fused_capacity() {
-    static const int cap = [] {
-        int dev = 0, cus = 0, occ = 0;
-        if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-            hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, k_attn_fused_f16<GRP, HD>, 256, 0) != hipSuccess)
-            return 0;
-        return cus * occ;
-    }();
-    return cap;
+    return resident_capacity(reinterpret_cast<const void *>(k_attn_fused_f16<GRP, HD>), 0);
 }
 
 template <int HD>
@@ -1302,16 +1327,18 @@ static hipError_t attn_go(AttnCtx c, int n_head, int n_kv, int npos_max, uint8_t
         if (attn_fused_fits(KV, n_head, n_kv, HD, npos_max)) {
             c.T = (uint64_t *)(ws + w.T);
             c.PT = (uint64_t *)(ws + w.PT);
-            c.err = (unsigned *)(ws + w.misc + 8);
+            c.err = (unsigned *)(ws + w.err);
+            c.spin = g_attn_spin;
+            c.poll_xor = g_attn_poll_xor;
             if (tg) {
                 c.epoch = tg->epoch;
                 c.tag_mul = tg->mul;
                 c.tag_add = tg->add;
             } else {                                                 // tags start over on a cleared workspace
-                const size_t nw = (w.total - w.T) / 8;
+                const size_t nw = (w.total - w.epoch) / 8;           // epoch and tagged words, not the error word
                 hipLaunchKernelGGL(k_attn_clear, dim3((unsigned)std::min<size_t>((nw + 255) / 256, 1024)), dim3(256), 0, s,
-                                   (uint64_t *)(ws + w.T), nw);
-                c.epoch = (const unsigned *)(ws + w.misc);
+                                   (uint64_t *)(ws + w.epoch), nw);
+                c.epoch = (const unsigned *)(ws + w.epoch);
                 c.tag_mul = 1;
                 c.tag_add = 0;
             }
@@ -1335,7 +1362,9 @@ static hipError_t attn_qkv_go(AttnCtx c, int npos_max, uint8_t *ws, hipStream_t 
     c.nc = nc;
     c.T = (uint64_t *)(ws + w.T);
     c.PT = (uint64_t *)(ws + w.PT);
-    c.err = (unsigned *)(ws + w.misc + 8);
+    c.err = (unsigned *)(ws + w.err);
+    c.spin = g_attn_spin;
+    c.poll_xor = g_attn_poll_xor;
     // rows per workgroup: a multiple of 16, so each workgroup's words fill whole 128-byte lines
     c.qrows = (int)(((c.W.nrows + nwg - 1) / nwg + 15) / 16 * 16);
     const size_t lds = ActQ8_0::bytes_per_token((int)c.W.nb) + kStageDump;
@@ -1353,6 +1382,19 @@ static hipError_t attn_qkv_fmt(const AttnCtx &c, int lpr, int upl, int npos_max,
     return hipErrorInvalidValue;
 }
 
+// resident capacity of the exact projection-in-attention instantiation that
+// launch_attn_qkv would launch, with its dynamic LDS (its register use differs
+// from the plain kernel's, so the plain kernel's capacity does not bound it)
+template <int GRP, int HD>
+static int qkv_capacity(int wtype, int lpr, int upl, size_t lds) {
+#define G4_AC(F, L, U)      \
+    if (lpr == L && upl == U) return resident_capacity(reinterpret_cast<const void *>(k_attn_fused_f16<GRP, HD, F, L, U>), lds)
+    if (wtype == Q4_0) { G4_AC(FQ4_0, 16, 2); G4_AC(FQ4_0, 32, 4); G4_AC(FQ4_0, 64, 2); }
+    if (wtype == Q8_0) { G4_AC(FQ8_0, 16, 2); G4_AC(FQ8_0, 32, 4); G4_AC(FQ8_0, 64, 2); }
+#undef G4_AC
+    return 0;
+}
+
 bool attn_qkv_fits(const g4h_tensor &W, const QkvArgs &a, int npos_max) {
     if (a.kv_type != F16 || !attn_fused_fits(F16, a.n_head, a.n_kv, a.hd, npos_max)) return false;
     if (W.type != Q4_0 && W.type != Q8_0) return false;
@@ -1362,7 +1404,11 @@ bool attn_qkv_fits(const g4h_tensor &W, const QkvArgs &a, int npos_max) {
     int lpr, upl;
     gemv_shape(W.type, W.nb, &lpr, &upl);
     const bool shape = (lpr == 16 && upl == 2) || (lpr == 32 && upl == 4) || (lpr == 64 && upl == 2);
-    return shape && W.nb * blck(W.type) / 32 <= (int64_t)lpr * upl;
+    if (!shape || W.nb * blck(W.type) / 32 > (int64_t)lpr * upl) return false;
+    const size_t lds = ActQ8_0::bytes_per_token((int)W.nb) + kStageDump;
+    const int cap = a.hd == 256 ? qkv_capacity<2, 256>(W.type, lpr, upl, lds) : qkv_capacity<2, 64>(W.type, lpr, upl, lds);
+    const int nc = (npos_max + ATT_CHUNK - 1) / ATT_CHUNK;
+    return (int64_t)a.n_kv * nc <= cap;
 }
 
 hipError_t launch_attn_qkv(const g4h_tensor &W, const GemvPro &pro, const QkvArgs &a, const int *npos_dev, int npos_max,

@@ -88,7 +88,7 @@ __global__ __launch_bounds__(256) void k_gelu_quant(const float *gu, int n_ff, c
 __device__ __forceinline__ void argmax_merge(float &v, int &i, float v2, int i2) {
     if (v2 > v || (v2 == v && i2 < i)) { v = v2; i = i2; }
 }
-__global__ __launch_bounds__(1024) void k_argmax_advance(const float *logits, int n, int *state) {
+__global__ __launch_bounds__(1024) void k_argmax_advance(const float *logits, int n, int *state, int n_ctx) {
     __shared__ float bv[16];
     __shared__ int bi[16];
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
@@ -119,8 +119,12 @@ __global__ __launch_bounds__(1024) void k_argmax_advance(const float *logits, in
     if (t == 0) {
         for (int w = 1; w < (int)(blockDim.x >> 6); w++) argmax_merge(best, idx, bv[w], bi[w]);
         state[0] = (idx == 0x7fffffff || __builtin_isnan(logits[0])) ? 0 : idx;
-        state[1] += 1;
-        state[2] = state[1] + 1;
+        if (state[1] + 1 < n_ctx) {
+            state[1] += 1;
+            state[2] = state[1] + 1;
+        } else {
+            state[4] |= STATE_CTX_FULL;                  // the cache is full: pos stays in bounds
+        }
         state[3] += 1;                                   // steps taken (never reset)
     }
 }
@@ -148,8 +152,8 @@ hipError_t launch_gelu_quant(const float *gu, int n_ff, const uint16_t *tab, uin
     hipLaunchKernelGGL(k_gelu_quant, dim3((n_ff / 4 + 255) / 256), dim3(256), 0, s, gu, n_ff, tab, act);
     return hipGetLastError();
 }
-hipError_t launch_argmax_advance(const float *logits, int n, int *state, hipStream_t s) {
-    hipLaunchKernelGGL(k_argmax_advance, dim3(1), dim3(1024), 0, s, logits, n, state);
+hipError_t launch_argmax_advance(const float *logits, int n, int *state, int n_ctx, hipStream_t s) {
+    hipLaunchKernelGGL(k_argmax_advance, dim3(1), dim3(1024), 0, s, logits, n, state, n_ctx);
     return hipGetLastError();
 }
 

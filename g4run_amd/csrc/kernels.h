@@ -86,7 +86,11 @@ hipError_t launch_embed_norm(const g4h_tensor &head, const int *token, float *x,
 hipError_t launch_norm_quant(float *x, const float *delta, const float *w_post, const float *w_pre, float eps, int n,
                              uint8_t *act, hipStream_t s);
 hipError_t launch_gelu_quant(const float *gu, int n_ff, const uint16_t *tab, uint8_t *act, hipStream_t s);
-hipError_t launch_argmax_advance(const float *logits, int n, int *state, hipStream_t s);
+// state: token, pos, npos = pos + 1, steps taken, flags.  Advances pos unless
+// pos + 1 == n_ctx: then pos stays and flags |= STATE_CTX_FULL (no later step can
+// index past the cache).
+constexpr int STATE_CTX_FULL = 1;
+hipError_t launch_argmax_advance(const float *logits, int n, int *state, int n_ctx, hipStream_t s);
 
 // k_mfma.hip: many-token matmul on the int8 matrix cores (q8_0 / q4_0 weights)
 size_t mm_planar_bytes(int M, int64_t ncols);
@@ -96,6 +100,13 @@ hipError_t launch_matmul_mfma(const g4h_tensor &W, const float *x, size_t x_stri
 
 // k_attn.hip
 size_t attn_workspace_bytes(int n_head, int hd, int npos_max);
+// The one-launch form's bounded polls give up after a fixed retry count; a
+// workgroup that gives up writes NaN and sets the workspace's error word at
+// offset 0 (ATTN_ERR_OFFSET), which stays set until the host clears it.  Test
+// hook: with `on`, every poll waits for a tag no store carries and gives up
+// after 64 retries, so the failure path runs deterministically.
+void attn_force_timeout(bool on);
+constexpr size_t ATTN_ERR_OFFSET = 0;
 // f16 caches run as one fused launch when its grid fits on the device at once
 // (attn_fused_fits).  Its hand-off words in ws carry a tag that must differ
 // from every earlier launch on that ws: *epoch * mul + add + 1 when `tag` is

@@ -76,13 +76,14 @@ struct g4h_model {
     size_t kv_layer_bytes = 0;       // one of K or V for one layer
     float *rope = nullptr;           // [n_ctx][hd] cos/sin pairs
     uint16_t *gelu = nullptr;        // 65536 fp16 codes
-    int *state = nullptr;            // token, pos, npos, steps taken
+    int *state = nullptr;            // token, pos, npos, steps taken, flags (STATE_*)
     float *x = nullptr, *x2 = nullptr, *xb = nullptr, *qkv = nullptr, *q = nullptr, *att = nullptr, *ff = nullptr, *logits = nullptr;
     uint8_t *act = nullptr, *ws = nullptr;
     uint64_t *qt = nullptr;          // FUSE_QATT: tagged q|k|v projection rows
     size_t act_bytes = 0, ws_bytes = 0;
     std::vector<void *> allocs;
     int fuse = 0;                    // FUSE_* steps folded into the GEMVs
+    float *trace = nullptr;          // optional per-layer x | qkv | att rows, then the final x (g4h_model_trace)
 };
 
 // Steps of the chain folded into the persistent GEMV family (gemv_p.h) or
@@ -294,7 +295,16 @@ extern "C" int g4h_forward_state(g4h_model *m, void *stream) {
     const hipStream_t s = (hipStream_t)stream;
     const g4h_model_config &c = m->c;
     const int E = c.n_embd, H = c.n_head, KV = c.n_kv, hd = c.head_dim, F = c.n_ff;
+    const int qkv_rows = (H + 2 * KV) * hd;
     int *token = m->state, *npos = m->state + 2;    // state: token, pos, npos = pos + 1
+    // trace record (g4h_model_trace): x | qkv | att | wo | xmid | h | down
+    const size_t TR_X = 0, TR_QKV = E, TR_ATT = TR_QKV + qkv_rows, TR_WO = TR_ATT + (size_t)H * hd, TR_XMID = TR_WO + E,
+                 TR_H = TR_XMID + E, TR_DOWN = TR_H + F, trace_rec = TR_DOWN + E;
+    auto trace_copy = [&](float *rec, size_t off, const float *src, int n) -> int {
+        if (!rec) return G4H_OK;
+        M_HIP(hipMemcpyAsync(rec + off, src, (size_t)n * 4, hipMemcpyDeviceToDevice, s));
+        return G4H_OK;
+    };
     const size_t ast = m->act_bytes;
     const int fz = m->fuse;
     float *x = m->x, *xn = m->x2;    // residual; a norm prologue writes x' to xn and the two swap
@@ -359,9 +369,17 @@ extern "C" int g4h_forward_state(g4h_model *m, void *stream) {
             }
             M_HIP(launch_attn_decode(nullptr, m->qkv, qa, 0, npos, c.n_ctx, m->att, m->act, m->ws, s, &tag));
         }
+        float *tr = m->trace ? m->trace + (size_t)l * trace_rec : nullptr;
+        // x holds this layer's input once its Wqkv launch is queued
+        M_RC(trace_copy(tr, TR_X, x, E));
+        M_RC(trace_copy(tr, TR_QKV, m->qkv, qkv_rows));
+        M_RC(trace_copy(tr, TR_ATT, m->att, H * hd));
         M_HIP(launch_gemv(*m->wo[l], m->act, ast, m->xb, 1, s));
+        M_RC(trace_copy(tr, TR_WO, m->xb, E));
         if (fz & FUSE_GU) {
             M_HIP(norm_gemv(*m->wgu[l], m->xb, norm_of(m, l, G4H_N_POST_ATTN), norm_of(m, l, G4H_N_FFN), nullptr, true));
+            M_RC(trace_copy(tr, TR_XMID, x, E));
+            M_RC(trace_copy(tr, TR_H, m->ff, F));
             if (fz & FUSE_DOWN) {
                 GemvPro pro;
                 pro.kind = PRO_QUANT;
@@ -376,10 +394,12 @@ extern "C" int g4h_forward_state(g4h_model *m, void *stream) {
             }
         } else {
             M_HIP(launch_norm_quant(x, m->xb, norm_of(m, l, G4H_N_POST_ATTN), norm_of(m, l, G4H_N_FFN), c.rms_eps, E, m->act, s));
+            M_RC(trace_copy(tr, TR_XMID, x, E));
             M_HIP(launch_gemv(*m->wgu[l], m->act, ast, m->ff, 1, s));
             M_HIP(launch_gelu_quant(m->ff, F, m->gelu, m->act, s));
             M_HIP(launch_gemv(*m->wdown[l], m->act, ast, m->xb, 1, s));
         }
+        M_RC(trace_copy(tr, TR_DOWN, m->xb, E));
     }
     const float *last_post = norm_of(m, c.n_layer - 1, G4H_N_POST_FFW), *out_norm = norm_of(m, c.n_layer, 0);
     if (fz & FUSE_HEAD) {
@@ -388,7 +408,14 @@ extern "C" int g4h_forward_state(g4h_model *m, void *stream) {
         M_HIP(launch_norm_quant(x, m->xb, last_post, out_norm, c.rms_eps, E, m->act, s));
         M_HIP(launch_gemv(*m->head, m->act, ast, m->logits, 1, s));
     }
-    M_HIP(launch_argmax_advance(m->logits, c.n_vocab, m->state, s));
+    M_RC(trace_copy(m->trace ? m->trace + (size_t)c.n_layer * trace_rec : nullptr, TR_X, x, E));
+    M_HIP(launch_argmax_advance(m->logits, c.n_vocab, m->state, c.n_ctx, s));
+    return G4H_OK;
+}
+
+extern "C" int g4h_model_trace(g4h_model *m, float *trace_dev) {
+    if (!m) return g4h_internal_fail(G4H_ERR_ARG, "g4h_model_trace: null model");
+    m->trace = trace_dev;
     return G4H_OK;
 }
 
@@ -398,7 +425,24 @@ extern "C" int g4h_model_set_state(g4h_model *m, int token, int pos, void *strea
     if (token < 0 || token >= m->c.n_vocab) return g4h_internal_fail(G4H_ERR_ARG, "g4h_model_set_state: token out of range");
     const int st[3] = {token, pos, pos + 1};
     M_HIP(hipMemcpyAsync(m->state, st, sizeof st, hipMemcpyHostToDevice, (hipStream_t)stream));
+    M_HIP(hipMemsetAsync(m->state + 4, 0, sizeof(int), (hipStream_t)stream));     // flags start clear
     M_HIP(hipStreamSynchronize((hipStream_t)stream));
+    return G4H_OK;
+}
+
+extern "C" int g4h_model_status(g4h_model *m, int *flags, void *stream) {
+    if (!m || !flags) return g4h_internal_fail(G4H_ERR_ARG, "g4h_model_status: null argument");
+    const hipStream_t s = (hipStream_t)stream;
+    int st[5];
+    unsigned err = 0;
+    M_HIP(hipMemcpyAsync(st, m->state, sizeof st, hipMemcpyDeviceToHost, s));
+    M_HIP(hipMemcpyAsync(&err, m->ws + ATTN_ERR_OFFSET, sizeof err, hipMemcpyDeviceToHost, s));
+    M_HIP(hipStreamSynchronize(s));
+    *flags = ((st[4] & STATE_CTX_FULL) ? G4H_STATUS_CTX_FULL : 0) | (err ? G4H_STATUS_ATTN_TIMEOUT : 0);
+    if (err) {                                               // reported once
+        M_HIP(hipMemsetAsync(m->ws + ATTN_ERR_OFFSET, 0, sizeof err, s));
+        M_HIP(hipStreamSynchronize(s));
+    }
     return G4H_OK;
 }
 
@@ -416,8 +460,14 @@ extern "C" int g4h_forward(g4h_model *m, int token, int pos, int *next_token, vo
     M_RC(g4h_model_set_state(m, token, pos, stream));
     M_RC(g4h_forward_state(m, stream));
     if (next_token) M_RC(g4h_model_get_state(m, next_token, nullptr, stream));
+    int flags = 0;
+    M_RC(g4h_model_status(m, &flags, stream));
+    if (flags & G4H_STATUS_ATTN_TIMEOUT)
+        return g4h_internal_fail(G4H_ERR_TIMEOUT, "g4h_forward: an attention hand-off wait gave up; the logits are NaN");
     return G4H_OK;
 }
+
+extern "C" const uint16_t *g4h_model_gelu_table(const g4h_model *m) { return m ? m->gelu : nullptr; }
 
 extern "C" const float *g4h_model_logits(const g4h_model *m) { return m ? m->logits : nullptr; }
 

@@ -39,7 +39,10 @@ enum {
                              silently truncates, e.g. quants.c:966)        */
     G4H_ERR_NOMEM = 4,    /* device allocation failed                     */
     G4H_ERR_DEVICE = 5,   /* no gfx950 device / not initialised           */
-    G4H_ERR_HIP = 6       /* a HIP runtime call failed                    */
+    G4H_ERR_HIP = 6,      /* a HIP runtime call failed                    */
+    G4H_ERR_TIMEOUT = 7   /* a bounded device-side wait gave up (the
+                             one-launch attention's hand-off); the outputs
+                             it owned are NaN                             */
 };
 
 /* ------------------------------------------------------------ runtime ---- */
@@ -51,6 +54,12 @@ const char *g4h_status_str(int status);
 /* Test hook: make the next `n` device allocations fail with G4H_ERR_NOMEM
  * (lets host code exercise the failure path without a real OOM). */
 void        g4h_debug_fail_alloc(int n);
+/* Test hook: with on != 0, the one-launch attention's hand-off polls wait for
+ * a tag that no store carries and give up after 64 retries (instead of 2^20),
+ * so every such wait fails while every kernel still runs to its end and the
+ * failure path (g4h_attn_status, g4h_model_status, G4H_ERR_TIMEOUT) can be
+ * tested deterministically.  0 restores normal operation. */
+void        g4h_debug_attn_timeout(int on);
 
 /* Plumbing (thin wrappers over HIP so that callers need no HIP headers). */
 int g4h_malloc(void **ptr, size_t bytes);
@@ -170,6 +179,13 @@ int g4h_attn_passes(int kv_type, int n_head, int n_kv, int hd, int n_pos, int *p
 int g4h_attn_decode(const float *q_dev, const void *kc_dev, const void *vc_dev, int kv_type,
                     int n_head, int n_kv, int hd, int n_pos, float *out_dev,
                     void *ws_dev, size_t ws_bytes, void *stream);
+/* Whether any attention call on ws_dev since the last query had a hand-off wait
+ * give up (*failed = 1; its outputs hold NaN), else *failed = 0.  The
+ * attention calls are asynchronous (and may be graph-replayed), so they cannot
+ * return this status themselves; this call synchronizes `stream`, reads the
+ * workspace's error word and clears it.  No reference counterpart: the CPU
+ * attention (model.c:509-580) has no cross-thread wait. */
+int g4h_attn_status(void *ws_dev, int *failed, void *stream);
 /* attn_kernel over a batch of nb new tokens (model.c:509-545 with nb > 1):
  * token b sits at position pos0 + b and attends cached positions
  * [0, pos0 + b] -- causal, the batch's own rows already stored in kc/vc.
@@ -221,7 +237,34 @@ int  g4h_forward(g4h_model *m, int token, int pos, int *next_token, void *stream
 int  g4h_forward_state(g4h_model *m, void *stream);
 int  g4h_model_set_state(g4h_model *m, int token, int pos, void *stream);
 int  g4h_model_get_state(g4h_model *m, int *token, int *pos, void *stream);
+/* Device-side conditions of the state-driven steps since the last set_state
+ * (synchronizes `stream`): G4H_STATUS_CTX_FULL -- a step ran at the last
+ * position n_ctx-1, so pos did not advance (the reference's full-attention
+ * cache has n_ctx slots, model.c:442; a further step re-decodes n_ctx-1 and
+ * never indexes past the cache); G4H_STATUS_ATTN_TIMEOUT -- an attention
+ * hand-off wait gave up and the logits are NaN (reported once, then cleared).
+ * g4h_forward returns G4H_ERR_TIMEOUT in the second case. */
+enum { G4H_STATUS_CTX_FULL = 1, G4H_STATUS_ATTN_TIMEOUT = 2 };
+int  g4h_model_status(g4h_model *m, int *flags, void *stream);
 const float *g4h_model_logits(const g4h_model *m);
+/* Diagnostic (no reference counterpart): with trace_dev non-NULL, every later
+ * step also copies its intermediate vectors into trace_dev (device memory, fp32):
+ * per layer l a record of 4 n_embd + (n_head + 2 n_kv) head_dim + n_head head_dim
+ * + n_ff floats -- x (the layer's input; layer 0: the scaled embedding), q|k|v
+ * (the projection output; not written when the projection runs inside the
+ * attention launch, G4H_DECODE_FUSE bit 16), att (attention output), wo (Wo
+ * output), xmid (x after the attention residual), h (gelu(gate)*up; not written
+ * without G4H_DECODE_FUSE bit 2) and down (Wdown output) -- then n_embd floats,
+ * the x the head normalises.  A CPU implementation can then
+ * check each part of each layer on the GPU's own inputs: the whole stack is
+ * chaotic at the ulp level (the fp16 rounding of q ahead of the unscaled
+ * softmax, model.c:530-538, turns a last-bit difference of the projection into
+ * a visible change of the attention output), so only such part-by-part checks
+ * hold a per-element tolerance.  NULL turns it off. */
+int g4h_model_trace(g4h_model *m, float *trace_dev);
+/* The model's fp16 GELU table (65536 codes, device memory): entry h =
+ * fp16(gelu_tanh(fp32(h))) as quants.c:48-58 builds g4_gelu_table. */
+const uint16_t *g4h_model_gelu_table(const g4h_model *m);
 /* Parameter access (for checking against a CPU implementation).  The
  * G4H_W_GU matrix holds its 2*n_ff rows interleaved: row 2i is gate row i,
  * row 2i+1 is up row i (the reference's w_gate_up is [gate | up]). */

@@ -148,6 +148,19 @@ typedef struct {
 size_t g4o_model_scratch_bytes(const g4o_model *m);
 int    g4o_model_decode(const g4o_model *m, int token, int pos, float *logits,
                         void *scratch, int nthreads);
+/* The step's parts: the embedding x = dequant(head row) * sqrt(n_embd), one
+ * layer in place on x (its K/V rows stored at pos), and the head (returns the
+ * argmax).  g4o_model_decode is embed, every layer, head. */
+void   g4o_model_embed(const g4o_model *m, int token, float *x);
+void   g4o_model_layer(const g4o_model *m, int il, int pos, float *x, void *scratch, int nthreads);
+/* The layer's parts (g4o_model_layer = qkv, attn, post): the Wqkv projection
+ * of x into qkv[(n_head + 2 n_kv) hd]; the q/k/v preparation, K/V store at pos
+ * and attention from qkv (prepared in place) into att[n_head hd]; and Wo, the
+ * residual adds and the FFN from att onto x in place. */
+void   g4o_model_qkv(const g4o_model *m, int il, const float *x, float *qkv, void *scratch, int nthreads);
+void   g4o_model_attn(const g4o_model *m, int il, int pos, float *qkv, float *att, void *scratch, int nthreads);
+void   g4o_model_post(const g4o_model *m, int il, float *x, const float *att, void *scratch, int nthreads);
+int    g4o_model_head(const g4o_model *m, const float *x, float *logits, void *scratch, int nthreads);
 
 /*
  * Pinning (checks that are not a retyping of the function's own formula):
@@ -160,7 +173,10 @@ int    g4o_model_decode(const g4o_model *m, int token, int pos, float *logits,
  *                         committed fixtures (q8_0 .. q6_K, tq2_0, f16, bf16)
  *   block_sums            brute-force dequant identity in exact integer math,
  *                         and unit-scale calls of the reference _ref dots
- *   dot_ref               bit-exact vs the reference's scalar _ref dots
+ *   dot_ref               within the reference selftest's tolerance (1e-3,
+ *                         quants.c:1583) of the reference build's scalar _ref
+ *                         dots: the README build vectorises those under
+ *                         -Ofast, so their bits are not the C text's
  *   dot (AVX2 order)      bit-exact vs the reference's AVX2 dots (oracle/_ref)
  *   dot_f16 / dot_bf16    bit-exact vs the reference's g4_dot_f16 / g4_dot_bf16
  *                         (fixtures with a scalar tail, n = 2053)
@@ -175,6 +191,12 @@ int    g4o_model_decode(const g4o_model *m, int token, int pos, float *logits,
  *                         are checked by invariants (softmax of a one-hot,
  *                         rope as a rotation, attention of identical keys,
  *                         float64 recomputation) -- see tests/test_oracle_model.py
+ *   attention, q8_0/q4_0 caches
+ *                         identical keys give exactly the fp32 weight
+ *                         (float)(1/n) (an fp16-rounded weight fails at n = 3),
+ *                         a one-hot key, and a float64 recomputation from the
+ *                         dequantized K/V and the q8_0-quantized query that
+ *                         rejects an fp16 query or fp16 weights by 10x
  *   gelu table            against math.tanh-based float64 recomputation
  */
 

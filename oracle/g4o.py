@@ -106,6 +106,13 @@ def lib():
         L.g4o_model_scratch_bytes.argtypes = [_vp]
         L.g4o_model_decode.restype = C.c_int
         L.g4o_model_decode.argtypes = [_vp, C.c_int, C.c_int, _vp, _vp, C.c_int]
+        L.g4o_model_embed.argtypes = [_vp, C.c_int, _vp]
+        L.g4o_model_layer.argtypes = [_vp, C.c_int, C.c_int, _vp, _vp, C.c_int]
+        L.g4o_model_qkv.argtypes = [_vp, C.c_int, _vp, _vp, _vp, C.c_int]
+        L.g4o_model_attn.argtypes = [_vp, C.c_int, C.c_int, _vp, _vp, _vp, C.c_int]
+        L.g4o_model_post.argtypes = [_vp, C.c_int, _vp, _vp, _vp, C.c_int]
+        L.g4o_model_head.restype = C.c_int
+        L.g4o_model_head.argtypes = [_vp, _vp, _vp, _vp, C.c_int]
         _lib = L
     return _lib
 
@@ -278,6 +285,20 @@ def gelu_table() -> np.ndarray:
     return np.array([L.g4o_gelu_table_entry(i) for i in range(65536)], dtype=np.uint16)
 
 
+_gelu_tab = None
+
+
+def gelu(x: np.ndarray) -> np.ndarray:
+    """g4o_gelu over an array: 0 for x <= -10, x for x >= 10, else the fp16
+    table entry of fp16(x) (g4run.h:73-77, quants.c:49-58)."""
+    global _gelu_tab
+    if _gelu_tab is None:
+        _gelu_tab = gelu_table()
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    y = fp16_to_fp32(_gelu_tab[fp32_to_fp16(x)])
+    return np.where(x <= -10.0, np.float32(0.0), np.where(x >= 10.0, x, y)).astype(np.float32)
+
+
 def attn_decode(q: np.ndarray, kc: np.ndarray, vc: np.ndarray, kv_type: int, n_head: int,
                 n_kv: int, hd: int, pos: int, nthreads: int = 1) -> np.ndarray:
     q = np.ascontiguousarray(q, dtype=np.float32)
@@ -336,6 +357,46 @@ class Model:
             setattr(m, k, C.cast(a, C.POINTER(_vp)))
         self._m = m
         self._scratch = np.zeros(lib().g4o_model_scratch_bytes(C.byref(m)), dtype=np.uint8)
+
+    def embed(self, token: int) -> np.ndarray:
+        x = np.zeros(self.cfg["n_embd"], dtype=np.float32)
+        lib().g4o_model_embed(C.byref(self._m), token, _ptr(x))
+        return x
+
+    def layer(self, il: int, pos: int, x: np.ndarray, nthreads: int = 1) -> np.ndarray:
+        """Layer il at pos applied to a copy of x (stores its K/V rows)."""
+        y = np.ascontiguousarray(x, dtype=np.float32).copy()
+        lib().g4o_model_layer(C.byref(self._m), il, pos, _ptr(y), _ptr(self._scratch), nthreads)
+        return y
+
+    def qkv(self, il: int, x: np.ndarray, nthreads: int = 1) -> np.ndarray:
+        c = self.cfg
+        out = np.zeros((c["n_head"] + 2 * c["n_kv"]) * c["hd"], dtype=np.float32)
+        lib().g4o_model_qkv(C.byref(self._m), il, _ptr(np.ascontiguousarray(x, dtype=np.float32)), _ptr(out),
+                            _ptr(self._scratch), nthreads)
+        return out
+
+    def attn(self, il: int, pos: int, qkv: np.ndarray, nthreads: int = 1, prepared: bool = False):
+        """Prepare q/k/v from the projection output (a copy), store K/V at pos,
+        attend; returns the attention output [n_head * hd] (and, with
+        prepared=True, the prepared q|k|v rows as well)."""
+        c = self.cfg
+        q = np.ascontiguousarray(qkv, dtype=np.float32).copy()
+        out = np.zeros(c["n_head"] * c["hd"], dtype=np.float32)
+        lib().g4o_model_attn(C.byref(self._m), il, pos, _ptr(q), _ptr(out), _ptr(self._scratch), nthreads)
+        return (out, q) if prepared else out
+
+    def post(self, il: int, x: np.ndarray, att: np.ndarray, nthreads: int = 1) -> np.ndarray:
+        y = np.ascontiguousarray(x, dtype=np.float32).copy()
+        lib().g4o_model_post(C.byref(self._m), il, _ptr(y), _ptr(np.ascontiguousarray(att, dtype=np.float32)),
+                             _ptr(self._scratch), nthreads)
+        return y
+
+    def head(self, x: np.ndarray, nthreads: int = 1):
+        logits = np.zeros(self.cfg["n_vocab"], dtype=np.float32)
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        tok = lib().g4o_model_head(C.byref(self._m), _ptr(x), _ptr(logits), _ptr(self._scratch), nthreads)
+        return tok, logits
 
     def decode(self, token: int, pos: int, nthreads: int = 1):
         logits = np.zeros(self.cfg["n_vocab"], dtype=np.float32)

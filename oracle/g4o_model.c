@@ -373,53 +373,83 @@ static void mm(const g4o_model *m, int wtype, const void *W, const float *x, int
 }
 
 /* The layer order of model.c:647-736 without the gemma4-only parts
- * (per-layer embeddings, SWA ring, shared KV, softcap):
- *   xb = rms(x)*attn_norm; q|k|v = Wqkv xb; q,k <- rms-norm per head with
- *   q_norm/k_norm then RoPE; v <- rms-norm without weight (model.c:684);
- *   store k,v at pos; attention; xb = Wo att; x += rms(xb)*post_attn_norm;
- *   xb = rms(x)*ffn_norm; g|u = Wgu xb; h = gelu(g)*u; xb = Wdown h;
- *   x += rms(xb)*post_ffw_norm.
- * Embedding: dequantized head row times sqrt(n_embd) (model.c:605-612);
- * head: rms(x)*output_norm, logits = head x (model.c:767-769), greedy argmax. */
-int g4o_model_decode(const g4o_model *m, int token, int pos, float *logits, void *scratch, int nthreads) {
+ * (per-layer embeddings, SWA ring, shared KV, softcap), in three parts:
+ *   qkv   xb = rms(x)*attn_norm; q|k|v = Wqkv xb
+ *   attn  q,k <- rms-norm per head with q_norm/k_norm then RoPE; v <- rms-norm
+ *         without weight (model.c:684); store k,v at pos; attention
+ *   post  xb = Wo att; x += rms(xb)*post_attn_norm; xb = rms(x)*ffn_norm;
+ *         g|u = Wgu xb; h = gelu(g)*u; xb = Wdown h; x += rms(xb)*post_ffw_norm */
+void g4o_model_qkv(const g4o_model *m, int il, const float *x, float *qkv, void *scratch, int nthreads) {
     scratch_t s = carve(m, scratch);
-    const int E = m->n_embd, hd = m->hd, H = m->n_head, KV = m->n_kv, F = m->n_ff;
+    const int E = m->n_embd, rows = (m->n_head + 2 * m->n_kv) * m->hd;
+    g4o_rms_norm(x, m->attn_norm[il], s.xb, E, m->eps);
+    mm(m, m->wtype, m->wqkv[il], s.xb, E, rows, qkv, s.qa, nthreads);
+}
+
+void g4o_model_attn(const g4o_model *m, int il, int pos, float *qkv, float *att, void *scratch, int nthreads) {
+    scratch_t s = carve(m, scratch);
+    const int hd = m->hd, H = m->n_head, KV = m->n_kv;
     const int qrows = H * hd, kvrows = KV * hd;
     const size_t kv_row = m->kv_type == G4O_F16 ? (size_t)hd * 2 : g4o_row_size(m->kv_type, hd);
-
-    g4o_dequant_row(m->head_type, (const uint8_t *)m->head + (size_t)token * g4o_row_size(m->head_type, E), s.x, E);
-    const float es = sqrtf((float)E);
-    for (int i = 0; i < E; i++) s.x[i] *= es;
     g4o_rope_cache(s.rc, hd, pos, m->rope_base);
-
-    for (int il = 0; il < m->n_layer; il++) {
-        g4o_rms_norm(s.x, m->attn_norm[il], s.xb, E, m->eps);
-        mm(m, m->wtype, m->wqkv[il], s.xb, E, qrows + 2 * kvrows, s.qkv, s.qa, nthreads);
-        float *q = s.qkv, *k = s.qkv + qrows, *v = s.qkv + qrows + kvrows;
-        for (int h = 0; h < H; h++) {
-            g4o_rms_norm(q + h * hd, m->q_norm[il], q + h * hd, hd, m->eps);
-            g4o_rope_apply(q + h * hd, s.rc, hd);
-        }
-        for (int h = 0; h < KV; h++) {
-            g4o_rms_norm(k + h * hd, m->k_norm[il], k + h * hd, hd, m->eps);
-            g4o_rope_apply(k + h * hd, s.rc, hd);
-            g4o_rms_norm(v + h * hd, NULL, v + h * hd, hd, m->eps);
-            g4o_kv_store(m->kv_type, (uint8_t *)m->kc[il] + ((size_t)pos * KV + h) * kv_row, k + h * hd, hd);
-            g4o_kv_store(m->kv_type, (uint8_t *)m->vc[il] + ((size_t)pos * KV + h) * kv_row, v + h * hd, hd);
-        }
-        g4o_attn_decode(q, m->kc[il], m->vc[il], m->kv_type, H, KV, hd, pos, s.att, nthreads);
-        mm(m, m->wtype, m->wo[il], s.att, qrows, E, s.xb, s.qa, nthreads);
-        g4o_rms_norm(s.xb, m->post_attn_norm[il], s.xb, E, m->eps);
-        for (int i = 0; i < E; i++) s.x[i] += s.xb[i];
-
-        g4o_rms_norm(s.x, m->ffn_norm[il], s.xb, E, m->eps);
-        mm(m, m->wtype, m->wgu[il], s.xb, E, 2 * F, s.ff, s.qa, nthreads);
-        for (int i = 0; i < F; i++) s.ff[i] = g4o_gelu(s.ff[i]) * s.ff[F + i];
-        mm(m, m->wtype, m->wdown[il], s.ff, F, E, s.xb, s.qa, nthreads);
-        g4o_rms_norm(s.xb, m->post_ffw_norm[il], s.xb, E, m->eps);
-        for (int i = 0; i < E; i++) s.x[i] += s.xb[i];
+    float *q = qkv, *k = qkv + qrows, *v = qkv + qrows + kvrows;
+    for (int h = 0; h < H; h++) {
+        g4o_rms_norm(q + h * hd, m->q_norm[il], q + h * hd, hd, m->eps);
+        g4o_rope_apply(q + h * hd, s.rc, hd);
     }
-    g4o_rms_norm(s.x, m->output_norm, s.xb, E, m->eps);
-    mm(m, m->head_type, m->head, s.xb, E, m->n_vocab, logits, s.qa, nthreads);
+    for (int h = 0; h < KV; h++) {
+        g4o_rms_norm(k + h * hd, m->k_norm[il], k + h * hd, hd, m->eps);
+        g4o_rope_apply(k + h * hd, s.rc, hd);
+        g4o_rms_norm(v + h * hd, NULL, v + h * hd, hd, m->eps);
+        g4o_kv_store(m->kv_type, (uint8_t *)m->kc[il] + ((size_t)pos * KV + h) * kv_row, k + h * hd, hd);
+        g4o_kv_store(m->kv_type, (uint8_t *)m->vc[il] + ((size_t)pos * KV + h) * kv_row, v + h * hd, hd);
+    }
+    g4o_attn_decode(q, m->kc[il], m->vc[il], m->kv_type, H, KV, hd, pos, att, nthreads);
+}
+
+void g4o_model_post(const g4o_model *m, int il, float *x, const float *att, void *scratch, int nthreads) {
+    scratch_t s = carve(m, scratch);
+    const int E = m->n_embd, F = m->n_ff;
+    mm(m, m->wtype, m->wo[il], att, m->n_head * m->hd, E, s.xb, s.qa, nthreads);
+    g4o_rms_norm(s.xb, m->post_attn_norm[il], s.xb, E, m->eps);
+    for (int i = 0; i < E; i++) x[i] += s.xb[i];
+
+    g4o_rms_norm(x, m->ffn_norm[il], s.xb, E, m->eps);
+    mm(m, m->wtype, m->wgu[il], s.xb, E, 2 * F, s.ff, s.qa, nthreads);
+    for (int i = 0; i < F; i++) s.ff[i] = g4o_gelu(s.ff[i]) * s.ff[F + i];
+    mm(m, m->wtype, m->wdown[il], s.ff, F, E, s.xb, s.qa, nthreads);
+    g4o_rms_norm(s.xb, m->post_ffw_norm[il], s.xb, E, m->eps);
+    for (int i = 0; i < E; i++) x[i] += s.xb[i];
+}
+
+/* One layer, in place on x[n_embd]. */
+void g4o_model_layer(const g4o_model *m, int il, int pos, float *x, void *scratch, int nthreads) {
+    scratch_t s = carve(m, scratch);
+    g4o_model_qkv(m, il, x, s.qkv, scratch, nthreads);
+    g4o_model_attn(m, il, pos, s.qkv, s.att, scratch, nthreads);
+    g4o_model_post(m, il, x, s.att, scratch, nthreads);
+}
+
+/* Embedding: dequantized head row times sqrt(n_embd) (model.c:605-612). */
+void g4o_model_embed(const g4o_model *m, int token, float *x) {
+    const int E = m->n_embd;
+    g4o_dequant_row(m->head_type, (const uint8_t *)m->head + (size_t)token * g4o_row_size(m->head_type, E), x, E);
+    const float es = sqrtf((float)E);
+    for (int i = 0; i < E; i++) x[i] *= es;
+}
+
+/* Head: rms(x)*output_norm, logits = head x (model.c:767-769), greedy argmax
+ * (sampler.c:139-144). */
+int g4o_model_head(const g4o_model *m, const float *x, float *logits, void *scratch, int nthreads) {
+    scratch_t s = carve(m, scratch);
+    g4o_rms_norm(x, m->output_norm, s.xb, m->n_embd, m->eps);
+    mm(m, m->head_type, m->head, s.xb, m->n_embd, m->n_vocab, logits, s.qa, nthreads);
     return g4o_argmax(logits, m->n_vocab);
+}
+
+int g4o_model_decode(const g4o_model *m, int token, int pos, float *logits, void *scratch, int nthreads) {
+    scratch_t s = carve(m, scratch);
+    g4o_model_embed(m, token, s.x);
+    for (int il = 0; il < m->n_layer; il++) g4o_model_layer(m, il, pos, s.x, scratch, nthreads);
+    return g4o_model_head(m, s.x, logits, scratch, nthreads);
 }

@@ -146,3 +146,30 @@ def test_batched_prefill_attention_is_causal(gpu, oracle, kv_type, pos0, nb):
     if pos0 == 0 and kv_type == 1:
         v0 = oracle.fp16_to_fp32(vh[:n_kv].view(np.uint16).reshape(n_kv, hd))
         assert np.allclose(got[0], np.repeat(v0, n_head // n_kv, axis=0), rtol=0, atol=0)
+
+
+def test_attention_timeout_reported_by_status(gpu, oracle):
+    """The one-launch attention's bounded waits: forced to give up (the test
+    hook makes them wait for a tag no store carries, 64 retries), every kernel
+    still ends and g4h_attn_status reports it once; in normal operation the
+    same call gives the oracle's result and a clear status."""
+    G = gpu
+    n_head, n_kv, hd, n_pos = 8, 4, 256, 8192
+    assert G.attn_passes(G.F16, n_head, n_kv, hd, n_pos) == 1
+    kb, vb, kh, vh = make_cache(G, oracle, G.F16, n_pos, n_kv, hd, seed=77)
+    q = np.random.default_rng(6).standard_normal((n_head, hd)).astype(np.float32)
+    qb, out = G.Buffer.from_array(q), G.Buffer(n_head * hd * 4)
+    ws = G.Buffer(G.attn_workspace_bytes(n_head, hd, n_pos))
+    ws.zero()
+    try:
+        G.debug_attn_timeout(True)
+        G.attn_decode(qb, kb, vb, G.F16, n_head, n_kv, hd, n_pos, out, ws=ws)
+        assert G.attn_status(ws)
+        assert not G.attn_status(ws)                       # reported once
+    finally:
+        G.debug_attn_timeout(False)
+    G.attn_decode(qb, kb, vb, G.F16, n_head, n_kv, hd, n_pos, out, ws=ws)
+    assert not G.attn_status(ws)
+    got = out.download(np.float32, (n_head, hd))
+    ref = oracle.attn_decode(q, kh, vh, G.F16, n_head, n_kv, hd, n_pos - 1)
+    assert np.all(np.abs(got.astype(np.float64) - ref) <= ATOL + RTOL * np.abs(ref))

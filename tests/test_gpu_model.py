@@ -7,6 +7,8 @@ carry through a multi-layer stack: q8_0 re-quantization of activations between
 layers turns an fp32-order difference of one ulp into an occasional one-step
 change of an 8-bit code, so the stack is held to the range-relative bar.
 """
+import os
+
 import numpy as np
 import pytest
 
@@ -14,6 +16,12 @@ pytestmark = pytest.mark.gpu
 
 SMALL = dict(n_layer=2, n_embd=256, n_head=4, n_kv=2, head_dim=64, n_ff=512, n_vocab=512, n_ctx=64,
              rope_base=1e6, rms_eps=1e-6)
+# the BASELINE decode step's layer shapes (d_model 2560, FFN 10240, 8 q / 4 KV
+# heads of 256) with 2 layers and 1024 positions: the persistent GEMV walks
+# 2-3 row groups per wave on Wgu, and the attention spans 8 chunks of 128
+# positions with the q/k/v preparation inside the launch
+MID = dict(n_layer=2, n_embd=2560, n_head=8, n_kv=4, head_dim=256, n_ff=10240, n_vocab=4096, n_ctx=1024,
+           rope_base=1e6, rms_eps=1e-6)
 
 
 def oracle_model(oracle, G, m):
@@ -26,25 +34,290 @@ def oracle_model(oracle, G, m):
     return oracle.Model(ocfg, w, kc, vc)
 
 
-@pytest.mark.parametrize("kv_type,wtype", [(1, 2), (8, 2), (2, 2), (1, 8)], ids=["f16-q4_0", "q8_0-q4_0", "q4_0-q4_0", "f16-q8_0"])
-def test_decode_steps_match_oracle(gpu, oracle, kv_type, wtype):
-    G = gpu
-    m = G.Model(seed=11, kv_type=kv_type, wtype=wtype, **SMALL)
-    m.fill_kv(seed=12)
-    om = oracle_model(oracle, G, m)
-    tok, pos = 7, 40
-    for step in range(4):
+def check_steps(m, om, tok, pos, steps, nthreads=1):
+    """Decode `steps` tokens on the GPU and on the oracle from (tok, pos): the
+    logits agree to 1e-3 of their range and the tokens are equal unless the
+    oracle's top two logits are a near-tie."""
+    for step in range(steps):
         nxt = m.forward(tok, pos)
         lg = m.logits()
-        otok, olg = om.decode(tok, pos)
+        otok, olg = om.decode(tok, pos, nthreads=nthreads)
         rng = float(olg.max() - olg.min())
         err = float(np.abs(lg.astype(np.float64) - olg).max())
+        print(f"step {step} pos {pos}: gpu token {nxt}, oracle token {otok}, max logit diff {err:.3g} (range {rng:.3g})",
+              flush=True)
         assert err <= 1e-3 * rng, f"step {step}: max logit diff {err:.3g} vs range {rng:.3g}"
         assert nxt == int(np.argmax(lg))
         top2 = np.sort(olg)[-2:]
         if top2[1] - top2[0] > 2e-3 * rng:          # not a near-tie
             assert nxt == otok, f"step {step}: token {nxt} vs oracle {otok}"
         tok, pos = otok, pos + 1
+    return tok, pos
+
+
+@pytest.mark.parametrize("kv_type,wtype", [(1, 2), (8, 2), (2, 2), (1, 8)], ids=["f16-q4_0", "q8_0-q4_0", "q4_0-q4_0", "f16-q8_0"])
+def test_decode_steps_match_oracle(gpu, oracle, kv_type, wtype):
+    G = gpu
+    m = G.Model(seed=11, kv_type=kv_type, wtype=wtype, **SMALL)
+    m.fill_kv(seed=12)
+    om = oracle_model(oracle, G, m)
+    check_steps(m, om, 7, 40, 4)
+    m.free()
+
+
+def _cache_rows(G, m, layer, pos):
+    """The K and V cache rows (all KV heads) at pos of one layer, as bytes."""
+    import ctypes as C
+    c = m.cfg
+    rb = c["head_dim"] * 2 if c["kv_type"] == G.F16 else G.row_size(c["kv_type"], c["head_dim"])
+    k, v, nb = C.c_void_p(), C.c_void_p(), C.c_size_t()
+    G.check(G.lib().g4h_model_kv(m.ptr, layer, C.byref(k), C.byref(v), C.byref(nb)))
+    out = []
+    for p in (k, v):
+        a = np.empty(c["n_kv"] * rb, np.uint8)
+        G.check(G.lib().g4h_memcpy_d2h(a.ctypes.data_as(C.c_void_p), p.value + pos * c["n_kv"] * rb, a.nbytes, None))
+        out.append(a)
+    return out
+
+
+def _close(got, ref, what, slack=0.0):
+    got, ref = got.astype(np.float64), np.asarray(ref, np.float64)
+    err = np.abs(got - ref)
+    bad = err > 1e-5 + 1e-3 * np.abs(ref) + slack
+    assert not bad.any(), f"{what}: {int(bad.sum())} of {bad.size} outside 1e-3/1e-5, worst {err.max():.3g}"
+    return float(err.max())
+
+
+def _attn_slack(o, om, l, pos, qprep):
+    """Per output element, the most that rounding the attention weights of an
+    f16 V cache to fp16 (model.c:555) can move it where the GPU's weight may
+    round to the neighbouring fp16 code: weights w_j = e_j * inv (float64 here)
+    within 1e-4 relative of a rounding midpoint, each contributing one fp16 ulp
+    of w_j times |V_j|.  The GPU's scores differ from the CPU's by the fp32
+    order of the f16 dot (~1e-7 relative), so only such weights can differ."""
+    c = om.cfg
+    H, KV, hd = c["n_head"], c["n_kv"], c["hd"]
+    grp = H // KV
+    K = np.frombuffer(om.kc[l].tobytes(), np.float16).reshape(-1, KV, hd)[:pos + 1].astype(np.float64)
+    V = np.frombuffer(om.vc[l].tobytes(), np.float16).reshape(-1, KV, hd)[:pos + 1].astype(np.float64)
+    slack = np.zeros((H, hd))
+    for h in range(H):
+        q16 = qprep[h * hd:(h + 1) * hd].astype(np.float16).astype(np.float64)
+        sc = K[:, h // grp] @ q16
+        w = np.exp(sc - sc.max())
+        w /= w.sum()
+        w16 = w.astype(np.float32).astype(np.float16)
+        a = w16.astype(np.float64)
+        # the two fp16 neighbours of w and the midpoints between them
+        up = np.nextafter(w16, np.float16(np.inf)).astype(np.float64)
+        dn = np.nextafter(w16, np.float16(-np.inf)).astype(np.float64)
+        near_up = np.abs(w - (a + up) / 2) <= 1e-4 * w
+        near_dn = np.abs(w - (a + dn) / 2) <= 1e-4 * w
+        ulp = np.where(near_up, up - a, 0.0) + np.where(near_dn, a - dn, 0.0)
+        slack[h] = ulp @ np.abs(V[:, h // grp])
+    return slack.ravel()
+
+
+def _check_gelu(o, h, g, u, what):
+    """h = gelu(g) * u with gelu looked up in the fp16 table at fp16(g)
+    (g4run.h:73-77).  The GPU's gate g differs from the oracle's by the fp32
+    order of its dot (~1e-7 relative), so where the oracle's g lies within
+    1e-5 relative of a rounding midpoint between two fp16 codes the GPU may
+    land on the neighbouring code: such an element must equal the table entry
+    of that neighbour times u.  Every other element is held to 1e-3/1e-5.
+    Returns (max error against the matched entry, number of neighbour codes)."""
+    g = np.asarray(g, np.float32)
+    c = o.fp32_to_fp16(g).astype(np.int64)
+    ref = o.gelu(g) * u
+    err = np.abs(h.astype(np.float64) - ref)
+    ok = err <= 1e-5 + 1e-3 * np.abs(ref)
+    flips = 0
+    for i in np.flatnonzero(~ok):
+        lo = o.fp16_to_fp32(np.array([c[i]], np.uint16))[0]
+        matched = False
+        for nb in (c[i] - 1, c[i] + 1):
+            if not 0 <= nb < 0x7c00 and not 0x8000 <= nb < 0xfc00:
+                continue
+            hi = o.fp16_to_fp32(np.array([nb], np.uint16))[0]
+            mid = (np.float64(lo) + np.float64(hi)) / 2
+            near = abs(np.float64(g[i]) - mid) <= 1e-5 * abs(mid)
+            alt = np.float64(o.gelu(np.array([hi], np.float32))[0]) * u[i] if abs(g[i]) < 10 else ref[i]
+            if near and abs(np.float64(h[i]) - alt) <= 1e-5 + 1e-3 * abs(alt):
+                matched = True
+                err[i] = abs(np.float64(h[i]) - alt)
+        assert matched, f"{what}: h[{i}] = {h[i]!r}, oracle {ref[i]!r} (gate {g[i]!r}), not a neighbouring table entry"
+        flips += 1
+    return float(err.max()), flips
+
+
+def check_layers(G, m, om, tok, pos, nthreads=1):
+    """One GPU step with its intermediate vectors traced; each part of each
+    layer is then computed by the oracle from the GPU's own inputs to that part
+    and held to the per-element bar |gpu - cpu| <= 1e-5 + 1e-3 |cpu|:
+      projection  q|k|v = Wqkv q8_0(rms(x) attn_norm)          from the GPU's x
+      attention   q/k/v preparation, K/V store at pos, attention  from its q|k|v
+      Wo          Wo q8_0(att)                                    from its att
+      residual    xmid = x + rms(wo) post_attn_norm               from its x, wo
+      FFN         h = gelu(g) u, g|u = Wgu q8_0(rms(xmid) ffn_norm)  from its xmid
+      Wdown       Wdown q8_0(h)                                   from its h
+      residual    x' = xmid + rms(down) post_ffw_norm             from its xmid, down
+      head        output norm, logits, argmax                     from its final x
+    and the K/V rows stored at pos must equal the oracle's bit for bit.  Part by
+    part, because the whole stack is chaotic at the ulp level: q is rounded to
+    fp16 (model.c:530) ahead of an unscaled softmax (model.c:538), and h is
+    looked up in an fp16 GELU table and re-quantized, so a last-bit difference
+    in an fp32 sum can move a layer's output by ~1e-3 of its scale (measured,
+    also for the oracle against itself under a one-ulp change of its input)."""
+    c = m.cfg
+    E, L, F = c["n_embd"], c["n_layer"], c["n_ff"]
+    wt, eps = c["wtype"], c["rms_eps"]
+    fields, rec = m.trace_fields()
+    off = {nm: (o, n) for nm, o, n in fields}
+    tb = G.Buffer(m.trace_floats() * 4)
+    m.trace(tb)
+    try:
+        nxt = m.forward(tok, pos)
+    finally:
+        m.trace(None)
+    tr = tb.download(np.float32, (m.trace_floats(),))
+    lg = m.logits()
+    from oracle import g4o as o
+    w = om.w
+    mm = lambda W, x, ncols: o.matmul(wt, W, o.prep_act(wt, x[None]), ncols, nthreads=nthreads)[0]
+    assert np.array_equal(tr[:E].view(np.uint32), om.embed(tok).view(np.uint32)), "embedding differs"
+    for l in range(L):
+        r = tr[l * rec:(l + 1) * rec]
+        v = {nm: r[a:a + n] for nm, (a, n) in off.items()}
+        xn = tr[(l + 1) * rec:(l + 1) * rec + E]
+        e = {}
+        e["qkv"] = _close(v["qkv"], om.qkv(l, v["x"], nthreads=nthreads), f"layer {l} projection")
+        att_ref, qprep = om.attn(l, pos, v["qkv"], nthreads=nthreads, prepared=True)
+        slack = _attn_slack(o, om, l, pos, qprep) if c["kv_type"] == G.F16 else 0.0
+        e["att"] = _close(v["att"], att_ref, f"layer {l} attention", slack)
+        k_gpu, v_gpu = _cache_rows(G, m, l, pos)
+        rb = k_gpu.size
+        assert np.array_equal(k_gpu, om.kc[l][pos * rb:(pos + 1) * rb]), f"layer {l}: K row at {pos} differs"
+        assert np.array_equal(v_gpu, om.vc[l][pos * rb:(pos + 1) * rb]), f"layer {l}: V row at {pos} differs"
+        e["wo"] = _close(v["wo"], mm(w["wo"][l], v["att"], v["att"].size), f"layer {l} Wo")
+        e["xmid"] = _close(v["xmid"], v["x"] + o.rms_norm(v["wo"], w["post_attn_norm"][l], eps), f"layer {l} attention residual")
+        gu = mm(w["wgu"][l], o.rms_norm(v["xmid"], w["ffn_norm"][l], eps), E)
+        e["h"], flips = _check_gelu(o, v["h"], gu[:F], gu[F:], f"layer {l} FFN")
+        e["down"] = _close(v["down"], mm(w["wdown"][l], v["h"], F), f"layer {l} Wdown")
+        e["x'"] = _close(xn, v["xmid"] + o.rms_norm(v["down"], w["post_ffw_norm"][l], eps), f"layer {l} FFN residual")
+        print(f"layer {l}: max err " + ", ".join(f"{k} {x:.3g}" for k, x in e.items()) + f"; GELU index flips {flips}",
+              flush=True)
+    otok, olg = om.head(tr[L * rec:L * rec + E], nthreads=nthreads)
+    e4 = _close(lg, olg, "head")
+    assert nxt == otok == int(np.argmax(lg))
+    print(f"head: max err {e4:.3g}, token {nxt}", flush=True)
+    return nxt
+
+
+def _pool(oracle):
+    n = max(1, min(16, os.cpu_count() or 1))
+    oracle.pool_start(n)
+    return n
+
+
+@pytest.mark.parametrize("kv_type", [1, 8], ids=["f16", "q8_0"])
+def test_decode_mid_size_matches_oracle(gpu, oracle, kv_type):
+    """MID: the multi-group persistent-GEMV walk and the multi-chunk attention
+    with the q/k/v preparation inside the launch, at positions 900-902."""
+    G = gpu
+    m = G.Model(seed=31, kv_type=kv_type, **MID)
+    m.fill_kv(seed=32)
+    om = oracle_model(oracle, G, m)
+    n = _pool(oracle)
+    try:
+        t = check_layers(G, m, om, 17, 900, nthreads=n)
+        check_layers(G, m, om, t, 901, nthreads=n)
+    finally:
+        oracle.pool_stop()
+        m.free()
+
+
+def test_decode_full_config_matches_oracle(gpu, oracle):
+    """BASELINE configs[4] itself (26 layers, d_model 2560, 8 q / 4 KV heads of
+    256, FFN 10240, vocab 32768, f16 KV filled to 8192): the last two positions
+    decoded on the GPU and by the oracle on the same weights and cache.  After
+    the step at the last position the device state does not advance past the
+    cache and reports it."""
+    G = gpu
+    m = G.Model(seed=1)
+    assert m.cfg["n_layer"] == 26 and m.cfg["n_ctx"] == 8192 and m.cfg["n_vocab"] == 32768
+    m.fill_kv(seed=2)
+    om = oracle_model(oracle, G, m)
+    n = _pool(oracle)
+    try:
+        t = check_layers(G, m, om, 1, 8190, nthreads=n)
+        check_layers(G, m, om, t, 8191, nthreads=n)
+    finally:
+        oracle.pool_stop()
+    tok, pos = m.get_state()
+    assert pos == 8191
+    assert m.status() == G.STATUS_CTX_FULL
+    m.free()
+
+
+def test_gelu_table_matches_reference_lut(gpu):
+    """The model's fp16 GELU table (built on the host at model creation) equals
+    the reference build's g4_gelu_table bit for bit (quants.c:48-58; fixture
+    written from the reference build)."""
+    G = gpu
+    ref = np.load(os.path.join(os.path.dirname(__file__), "golden", "tables.npz"))["gelu"]
+    m = G.Model(seed=3, **SMALL)
+    tab = m.gelu_table()
+    m.free()
+    assert tab.dtype == np.uint16 and tab.shape == ref.shape
+    diff = np.flatnonzero(tab != ref.astype(np.uint16))
+    assert diff.size == 0, f"{diff.size} codes differ, first {diff[:8]}"
+
+
+def test_replay_stops_at_context_end(gpu):
+    """Graph replays past the last position keep pos in the cache (the reference
+    full-attention cache has n_ctx slots, model.c:442) and flag it."""
+    G = gpu
+    m = G.Model(seed=5, **SMALL)
+    m.fill_kv(seed=6)
+    st = G.Stream()
+    n_ctx = SMALL["n_ctx"]
+    m.set_state(3, n_ctx - 2, st.ptr)
+    g = G.Graph(st.ptr, lambda: m.forward_state(st.ptr))
+    g.launch(st.ptr)
+    st.synchronize()
+    assert m.get_state(st.ptr)[1] == n_ctx - 1 and m.status(st.ptr) == 0
+    for _ in range(3):
+        g.launch(st.ptr)
+    st.synchronize()
+    assert m.get_state(st.ptr)[1] == n_ctx - 1
+    assert m.status(st.ptr) == G.STATUS_CTX_FULL
+    assert np.isfinite(m.logits()).all()
+    m.set_state(3, 10, st.ptr)                                  # a new position clears the flag
+    assert m.status(st.ptr) == 0
+    m.free()
+
+
+def test_attention_timeout_is_reported(gpu):
+    """With the attention hand-off waits forced to give up (test hook; every
+    kernel still ends), g4h_forward returns G4H_ERR_TIMEOUT instead of
+    returning NaN logits silently; in normal operation the same step gives the
+    same bits as before."""
+    G = gpu
+    cfg = dict(MID, n_layer=1, n_ctx=4096)
+    m = G.Model(seed=41, **cfg)
+    m.fill_kv(seed=42)
+    assert G.attn_passes(G.F16, cfg["n_head"], cfg["n_kv"], cfg["head_dim"], cfg["n_ctx"]) == 1
+    ok_tok = m.forward(5, 4000)
+    ok_logits = m.logits()
+    try:
+        G.debug_attn_timeout(True)
+        with pytest.raises(G.G4HError) as e:
+            m.forward(5, 4000)
+        assert e.value.status == G.ERR_TIMEOUT
+    finally:
+        G.debug_attn_timeout(False)
+    assert m.forward(5, 4000) == ok_tok
+    assert np.array_equal(m.logits().view(np.uint32), ok_logits.view(np.uint32))
     m.free()
 
 
@@ -73,9 +346,11 @@ def test_graph_replay_matches_eager(gpu):
         assert np.array_equal(m2.logits().view(np.uint32), eager[i][1].view(np.uint32))
 
 
-@pytest.mark.parametrize("kv_type,fuse", [(1, None), (8, None), (2, None), (1, "19"), (1, "31")],
-                         ids=["f16-default", "q8_0-default", "q4_0-default", "f16-qkv-in-attention", "f16-all"])
-def test_fused_step_equals_unfused(gpu, monkeypatch, kv_type, fuse):
+@pytest.mark.parametrize("cfg,kv_type,fuse", [("SMALL", 1, None), ("SMALL", 8, None), ("SMALL", 2, None), ("SMALL", 1, "19"),
+                                              ("SMALL", 1, "31"), ("MID", 1, None), ("MID", 1, "19"), ("MID", 8, None)],
+                         ids=["f16-default", "q8_0-default", "q4_0-default", "f16-qkv-in-attention", "f16-all",
+                              "mid-f16-default", "mid-f16-qkv-in-attention", "mid-q8_0-default"])
+def test_fused_step_equals_unfused(gpu, monkeypatch, cfg, kv_type, fuse):
     """The step with the residual norms folded into the Wqkv / Wgu prologues and
     GELU into the Wgu epilogue (the default), or with the Wqkv GEMV inside the
     attention launch (G4H_DECODE_FUSE bit 16), gives the same tokens and
@@ -88,10 +363,12 @@ def test_fused_step_equals_unfused(gpu, monkeypatch, kv_type, fuse):
             monkeypatch.delenv("G4H_DECODE_FUSE", raising=False)
         else:
             monkeypatch.setenv("G4H_DECODE_FUSE", f)
-        m = G.Model(seed=21, kv_type=kv_type, **SMALL)
+        shape = SMALL if cfg == "SMALL" else MID
+        m = G.Model(seed=21, kv_type=kv_type, **shape)
         m.fill_kv(seed=22)
         out, tok = [], 9
-        for pos in range(30, 33):
+        p0 = 30 if cfg == "SMALL" else 950
+        for pos in range(p0, p0 + 3):
             tok = m.forward(tok, pos)
             out.append((tok, m.logits()))
         m.free()

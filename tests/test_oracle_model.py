@@ -197,3 +197,83 @@ def test_decode_graph_float64_recomputation(oracle):
     # a gate/up swap gives 0.15 and a dropped post-attention norm 0.10
     np.testing.assert_allclose(logits, ref, rtol=0, atol=3e-3 * scale)
     assert tok == int(np.argmax(logits))
+
+
+# ------------------------------------------------- attention, quantized KV
+# model.c:530-577 over a q8_0 / q4_0 cache: the query is quantized to q8_0
+# (model.c:533), each score is the K row's q8_0 / q4_0 dot with it (model.c:538),
+# and the V rows are dequantized and weighted by the fp32 probability e*inv
+# with no fp16 rounding (model.c:571-577), unlike the f16 cache (model.c:555).
+def _qkv_cache(oracle, kv_type, x):
+    """Rows of x [..., hd] stored as kv_type blocks, and their dequantized values."""
+    hd = x.shape[-1]
+    rows = oracle.quantize(kv_type, x.reshape(-1, hd).astype(np.float32))
+    return rows, oracle.dequant(kv_type, rows, hd).astype(np.float64).reshape(x.shape)
+
+
+@pytest.mark.parametrize("kv_type", [Q8_0, Q4_0], ids=["q8_0", "q4_0"])
+@pytest.mark.parametrize("npos", [3, 300])
+def test_attention_quantized_identical_keys_fp32_weights(oracle, kv_type, npos):
+    """Identical keys give equal scores, so every weight is exactly the fp32
+    inv = (float)(1/n).  With n = 3, fp16(1/3) differs from it by 2.4e-4
+    relative, so a weight rounded to fp16 (the f16-cache rule) fails the bar."""
+    hd, n_head, n_kv = 64, 2, 1
+    rng = np.random.default_rng(40 + npos)
+    krow, _ = _qkv_cache(oracle, kv_type, rng.standard_normal(hd))
+    k = np.tile(krow, (npos, 1))
+    v, v64 = _qkv_cache(oracle, kv_type, rng.standard_normal((npos, hd)))
+    q = rng.standard_normal((n_head, hd)).astype(np.float32)
+    out = oracle.attn_decode(q, k, v, kv_type, n_head, n_kv, hd, npos - 1)
+    w = np.float64(np.float32(1.0 / npos))
+    ref = w * v64.sum(0)
+    scale = np.abs(v64).max()
+    for h in range(n_head):
+        np.testing.assert_allclose(out[h], ref, rtol=1e-6, atol=1e-6 * scale * np.sqrt(npos))
+    if npos == 3:
+        wrong = np.float64(np.float16(1.0 / npos)) * v64.sum(0)
+        assert np.abs(out[0] - wrong).max() > 50 * 1e-6 * scale      # the check can tell the two rules apart
+
+
+@pytest.mark.parametrize("kv_type", [Q8_0, Q4_0], ids=["q8_0", "q4_0"])
+def test_attention_quantized_one_hot_key(oracle, kv_type):
+    hd, n_head, n_kv, npos = 128, 4, 2, 130
+    rng = np.random.default_rng(41)
+    kx = rng.standard_normal((npos, n_kv, hd)) * 0.05
+    q = rng.standard_normal((n_head, hd)).astype(np.float32)
+    kx[77, 0] = q[0] * 30                                               # dominant for heads 0 and 1 of KV head 0
+    kx[12, 1] = q[2] * 30                                               # and for heads 2, 3 of KV head 1
+    k, _ = _qkv_cache(oracle, kv_type, kx)
+    v, v64 = _qkv_cache(oracle, kv_type, rng.standard_normal((npos, n_kv, hd)))
+    out = oracle.attn_decode(q, k, v, kv_type, n_head, n_kv, hd, npos - 1)
+    np.testing.assert_allclose(out[0], v64[77, 0], atol=1e-4 * np.abs(v64).max())
+    np.testing.assert_allclose(out[2], v64[12, 1], atol=1e-4 * np.abs(v64).max())
+
+
+@pytest.mark.parametrize("kv_type", [Q8_0, Q4_0], ids=["q8_0", "q4_0"])
+def test_attention_quantized_float64_recomputation(oracle, kv_type):
+    """float64 attention from the dequantized K/V rows and the q8_0-quantized
+    query, fp32 weights, within 5e-6 of the largest output (measured: 5.4e-7).
+    An fp16 query (the f16-cache rule) moves the outputs by >= 1.4e-3 and fp16
+    weights by >= 5e-5 of the largest output on every head here, so the same
+    bar rejects both rules by 10x or more."""
+    hd, n_head, n_kv, npos = 256, 8, 4, 65
+    rng = np.random.default_rng(42)
+    k, k64 = _qkv_cache(oracle, kv_type, rng.standard_normal((npos, n_kv, hd)) * 0.15)
+    v, v64 = _qkv_cache(oracle, kv_type, rng.standard_normal((npos, n_kv, hd)))
+    q = rng.standard_normal((n_head, hd)).astype(np.float32)
+    out = oracle.attn_decode(q, k, v, kv_type, n_head, n_kv, hd, npos - 1)
+    qd = oracle.dequant(Q8_0, oracle.quantize(Q8_0, q), hd).astype(np.float64)
+    for h in range(n_head):
+        g = h // (n_head // n_kv)
+        s = k64[:, g] @ qd[h]
+        e = np.exp(s - s.max())
+        w = (e / e.sum()).astype(np.float32).astype(np.float64)
+        ref = w @ v64[:, g]
+        bar = 5e-6 * np.abs(ref).max()
+        np.testing.assert_allclose(out[h], ref, rtol=0, atol=bar)
+        # the same bar with the other rounding rules fails (so it pins them)
+        s16 = k64[:, g] @ np.float16(q[h]).astype(np.float64)
+        e16 = np.exp(s16 - s16.max())
+        assert np.abs(out[h] - (e16 / e16.sum()) @ v64[:, g]).max() > 10 * bar
+        wh = (e / e.sum()).astype(np.float32).astype(np.float16).astype(np.float64)
+        assert np.abs(out[h] - wh @ v64[:, g]).max() > 10 * bar
