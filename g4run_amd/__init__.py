@@ -80,6 +80,8 @@ _SIGS = [
     ("g4h_matmul", _int, [_vp, _vp, _vp, _sz, _vp, _int, _vp]),
     ("g4h_matmul_ex", _int, [_vp, _vp, _vp, _sz, _vp, _int, _int, _vp]),
     ("g4h_matmul_path", _int, [_vp, _int]),
+    ("g4h_matmul_noalloc", _int, [_vp, _vp, _vp, _sz, _vp, _int, _int, _vp]),
+    ("g4h_matmul_noalloc_max_bytes", _sz, []),
     ("g4h_matmul_describe", _int, [_vp, _int, _int, C.c_char_p, C.c_size_t]),
     ("g4h_block_sums", _int, [_vp, _vp, _sz, _int, _vp, _vp]),
     ("g4h_attn_workspace_bytes", _sz, [_int, _int, _int]),

@@ -33,6 +33,15 @@ static int hip_fail(hipError_t e, const char *what) {
     } while (0)
 
 static int g_device = -1;
+
+// Fixed scratch of the allocation-free matmul (g4h_matmul_noalloc), 4 MiB: each
+// device holds its own copy until the process ends.  Host code never uses the
+// array's name as an address: g4h_init resolves it once per device with
+// hipGetSymbolAddress, and calls pass that address to the kernels.
+static constexpr size_t kNoAllocBytes = (size_t)4 << 20;
+static __device__ __align__(256) uint8_t scratch[kNoAllocBytes];
+static std::mutex g_noalloc_mu;
+static std::unordered_map<int, void *> g_noalloc_ptr;     // device -> address of `scratch` there
 static std::atomic<int> g_fail_alloc{0};
 
 #define G4_NEED_INIT() \
@@ -69,6 +78,15 @@ extern "C" int g4h_init(int device) {
     G4_HIP(hipGetDeviceProperties(&p, device));
     if (strncmp(p.gcnArchName, "gfx950", 6) != 0)
         return fail(G4H_ERR_DEVICE, "device %d is %s; this library is built for gfx950 only", device, p.gcnArchName);
+    // the allocation-free matmul's scratch: its address on this device, once
+    {
+        std::lock_guard<std::mutex> lk(g_noalloc_mu);
+        if (!g_noalloc_ptr.count(device)) {
+            void *ptr = nullptr;
+            G4_HIP(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)));
+            g_noalloc_ptr[device] = ptr;
+        }
+    }
     g_device = device;
     return G4H_OK;
 }
@@ -441,8 +459,48 @@ static int check_act(const char *fn, const g4h_tensor *W, const void *pre, size_
     return G4H_OK;
 }
 
+
+// where g4h_matmul_ex / g4h_matmul_noalloc take the scratch of one call from
+struct ScratchSrc {
+    void *fixed = nullptr;      // the device's `scratch` (no allocation), or null: the per-stream pool
+    int get(hipStream_t s, size_t bytes, void **out) const {
+        if (!fixed) return scratch_for(s, bytes, out);
+        if (bytes > kNoAllocBytes)
+            return fail(G4H_ERR_ARG, "g4h_matmul_noalloc: this call needs %zu bytes of scratch, more than the fixed %zu "
+                                     "(use g4h_matmul)", bytes, kNoAllocBytes);
+        *out = fixed;
+        return G4H_OK;
+    }
+};
+
+static int matmul_impl(const g4h_tensor *W, const float *x, const void *pre, size_t pre_stride, float *Y, int nb, int path,
+                       void *stream, const ScratchSrc &scr);
+
 extern "C" int g4h_matmul_ex(const g4h_tensor *W, const float *x, const void *pre, size_t pre_stride, float *Y, int nb,
                              int path, void *stream) {
+    return matmul_impl(W, x, pre, pre_stride, Y, nb, path, stream, ScratchSrc());
+}
+
+extern "C" size_t g4h_matmul_noalloc_max_bytes(void) { return kNoAllocBytes; }
+
+extern "C" int g4h_matmul_noalloc(const g4h_tensor *W, const float *x, const void *pre, size_t pre_stride, float *Y, int nb,
+                                  int path, void *stream) {
+    G4_NEED_INIT();
+    int dev = -1;
+    G4_HIP(hipGetDevice(&dev));
+    ScratchSrc scr;
+    {
+        std::lock_guard<std::mutex> lk(g_noalloc_mu);
+        const auto it = g_noalloc_ptr.find(dev);
+        if (it == g_noalloc_ptr.end())
+            return fail(G4H_ERR_DEVICE, "g4h_matmul_noalloc: g4h_init(%d) has not been called for the current device", dev);
+        scr.fixed = it->second;
+    }
+    return matmul_impl(W, x, pre, pre_stride, Y, nb, path, stream, scr);
+}
+
+static int matmul_impl(const g4h_tensor *W, const float *x, const void *pre, size_t pre_stride, float *Y, int nb, int path,
+                       void *stream, const ScratchSrc &scr) {
     G4_NEED_INIT();
     if (!W || !Y) return fail(G4H_ERR_ARG, "g4h_matmul: null tensor or output");
     if ((x == nullptr) == (pre == nullptr)) return fail(G4H_ERR_ARG, "g4h_matmul: pass exactly one of x_dev and pre_dev");
@@ -457,7 +515,7 @@ extern "C" int g4h_matmul_ex(const g4h_tensor *W, const float *x, const void *pr
         if (!x)
             if (int rc = check_act("g4h_matmul", W, pre, pre_stride, nb)) return rc;
         void *buf;
-        if (int rc = scratch_for(s, mm_planar_bytes(nb, W->ncols), &buf)) return rc;
+        if (int rc = scr.get(s, mm_planar_bytes(nb, W->ncols), &buf)) return rc;
         const hipError_t e = launch_matmul_mfma(*W, x, W->ncols, (const uint8_t *)pre, pre_stride, nb, Y, (uint8_t *)buf, s);
         if (e != hipSuccess) return hip_fail(e, "g4h_matmul: matrix-core launch");
         return G4H_OK;
@@ -471,7 +529,7 @@ extern "C" int g4h_matmul_ex(const g4h_tensor *W, const float *x, const void *pr
             if ((uintptr_t)x % 4) return fail(G4H_ERR_ARG, "g4h_matmul: x must be 4-byte aligned");
             stride = g4h_act_stride(W->type, W->ncols);
             void *buf;
-            if (int rc = scratch_for(s, stride * nb, &buf)) return rc;
+            if (int rc = scr.get(s, stride * nb, &buf)) return rc;
             const hipError_t e = launch_act_float(W->type, x, W->ncols, W->ncols, nb, (uint8_t *)buf, stride, s);
             if (e != hipSuccess) return hip_fail(e, "g4h_matmul: activation conversion");
             act = (const uint8_t *)buf;
@@ -508,7 +566,7 @@ extern "C" int g4h_matmul_ex(const g4h_tensor *W, const float *x, const void *pr
         if ((uintptr_t)x % 4) return fail(G4H_ERR_ARG, "g4h_matmul: x must be 4-byte aligned");
         stride = g4h_act_stride(W->type, W->ncols);
         void *buf;
-        if (int rc = scratch_for(s, stride * nb, &buf)) return rc;
+        if (int rc = scr.get(s, stride * nb, &buf)) return rc;
         const hipError_t e = g4h_act_type(W->type) == Q8_0
                                  ? launch_quantize_q8_0(x, W->ncols, (uint8_t *)buf, stride, W->ncols, nb, s)
                                  : launch_quantize_q8_K(x, W->ncols, (uint8_t *)buf, stride, W->ncols, nb, s);

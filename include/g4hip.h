@@ -147,6 +147,20 @@ int g4h_matmul(const g4h_tensor *W, const float *x_dev, const void *pre_dev, siz
 int g4h_matmul_ex(const g4h_tensor *W, const float *x_dev, const void *pre_dev, size_t pre_stride,
                   float *Y_dev, int nb, int path, void *stream);
 int g4h_matmul_path(const g4h_tensor *W, int nb);
+/* g4h_matmul_ex without any device allocation -- no counterpart in the
+ * reference; for callers that cannot allocate (code under HIP graph capture,
+ * serving loops, harnesses that forbid hipMalloc).  Where g4h_matmul_ex takes
+ * its scratch (the activations quantized from x_dev, the matrix-core path's
+ * planar copy) from a per-stream pool it may grow, this call uses a fixed
+ * scratch array of g4h_matmul_noalloc_max_bytes() (4 MiB) per device, set up by
+ * g4h_init; a call that needs more fails with G4H_ERR_ARG.  The caller still
+ * passes W, x_dev / pre_dev and Y_dev.  Results equal g4h_matmul_ex's bit for
+ * bit.  Every call on one device shares that array: calls that overlap on one
+ * device (different streams, different host threads) race; nothing in the
+ * array needs to start at zero. */
+int    g4h_matmul_noalloc(const g4h_tensor *W, const float *x_dev, const void *pre_dev, size_t pre_stride,
+                          float *Y_dev, int nb, int path, void *stream);
+size_t g4h_matmul_noalloc_max_bytes(void);
 /* Diagnostic (no reference counterpart): the kernel instantiation and launch
  * shape g4h_matmul_ex would use, e.g. "k_gemv<q4_0,nb=1,lpr=32,upl=4> grid=256
  * block=512", written NUL-terminated into buf (at most len bytes).  Profiles
