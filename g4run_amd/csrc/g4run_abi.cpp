@@ -1,0 +1,238 @@
+// g4run_abi.cpp -- g4run.h's quantized-kernel entry points (include/g4run_abi.h)
+// under their reference names, each one a GPU batch call of the C ABI in
+// include/g4hip.h on host buffers: the call's inputs are staged to device
+// memory of the calling thread, the gfx950 kernel runs on that thread's
+// stream, and the result is copied back before the call returns.
+#include "../../include/g4run_abi.h"
+
+#include <cmath>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <mutex>
+
+#include "../../include/g4hip.h"
+#include "host_fp16.h"
+
+using namespace g4;
+
+extern "C" int g4h_internal_fail(int status, const char *msg);
+
+float g4_fp16_to_fp32_table[65536];
+g4_fp16 g4_gelu_fp16_table[65536];
+int g4_avx512 = 0;
+
+extern "C" void g4_set_avx512(int on) { (void)on; }     // no AVX-512 kernels here: the dots run on the GPU
+extern "C" int g4_avx512_available(void) { return 0; }
+
+static std::once_flag g_tables_once;
+static int g_init_status = G4H_ERR_DEVICE;
+
+extern "C" void g4_init_tables(void) {
+    std::call_once(g_tables_once, [] {
+        for (uint32_t h = 0; h < 65536; h++) {
+            g4_fp16_to_fp32_table[h] = host_h2f((uint16_t)h);
+            g4_gelu_fp16_table[h] = gelu_table_entry((uint16_t)h);
+        }
+        const char *d = getenv("G4H_DEVICE");
+        g_init_status = g4h_init(d ? atoi(d) : 0);
+        if (g_init_status)
+            fprintf(stderr, "g4run_abi: g4_init_tables: no usable device (%s); the g4_* kernels will return NaN\n",
+                    g4h_last_error());
+    });
+}
+
+// ------------------------------------------------------------ type table ----
+// The ggml types of g4run.h:80-94 with their block geometry (gguf.c:11-25).
+namespace {
+struct TypeRow {
+    int t;
+    const char *name;
+    int blck, size;
+};
+const TypeRow kTypes[] = {
+    {G4H_F32, "F32", 1, 4},       {G4H_F16, "F16", 1, 2},        {G4H_BF16, "BF16", 1, 2},
+    {G4H_Q4_0, "Q4_0", 32, 18},   {G4H_Q8_0, "Q8_0", 32, 34},    {G4H_Q2_K, "Q2_K", 256, 84},
+    {G4H_Q3_K, "Q3_K", 256, 110}, {G4H_Q4_K, "Q4_K", 256, 144},  {G4H_Q5_K, "Q5_K", 256, 176},
+    {G4H_Q6_K, "Q6_K", 256, 210}, {G4H_TQ2_0, "TQ2_0", 256, 66}, {24, "I8", 1, 1},
+    {25, "I16", 1, 2},            {26, "I32", 1, 4},             {27, "I64", 1, 8},
+    {28, "F64", 1, 8},
+};
+const TypeRow *find_type(int t) {
+    for (const TypeRow &r : kTypes)
+        if (r.t == t) return &r;
+    return nullptr;
+}
+}  // namespace
+
+extern "C" const char *g4_type_name(int t) { const TypeRow *r = find_type(t); return r ? r->name : "?"; }
+extern "C" int g4_type_blck(int t) { const TypeRow *r = find_type(t); return r ? r->blck : 0; }
+extern "C" size_t g4_type_size(int t) { const TypeRow *r = find_type(t); return r ? (size_t)r->size : 0; }
+extern "C" size_t g4_row_size(int t, int64_t n) {
+    const int b = g4_type_blck(t);
+    if (!b || n % b) return 0;
+    return (size_t)(n / b) * g4_type_size(t);
+}
+
+// -------------------------------------------------------------- staging ----
+// Per host thread: one stream and one growing device buffer, kept until the
+// process ends (pool threads call the dots concurrently, as model.c's do).
+namespace {
+struct Staging {
+    void *stream = nullptr;
+    uint8_t *buf = nullptr;
+    size_t cap = 0;
+};
+thread_local Staging tl;
+
+size_t al256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+// device memory of at least `bytes` on this thread's stream, or null
+uint8_t *stage(size_t bytes) {
+    g4_init_tables();
+    if (g_init_status) return nullptr;
+    if (!tl.stream && g4h_stream_create(&tl.stream)) return nullptr;
+    if (tl.cap < bytes) {
+        if (tl.buf) {
+            g4h_stream_synchronize(tl.stream);
+            g4h_free(tl.buf);
+            tl.buf = nullptr;
+            tl.cap = 0;
+        }
+        const size_t want = bytes < ((size_t)1 << 20) ? ((size_t)1 << 20) : al256(bytes);
+        void *p = nullptr;
+        if (g4h_malloc(&p, want)) return nullptr;
+        tl.buf = (uint8_t *)p;
+        tl.cap = want;
+    }
+    return tl.buf;
+}
+
+void report(const char *fn) {
+    static std::once_flag once;
+    std::call_once(once, [fn] { fprintf(stderr, "g4run_abi: %s failed: %s\n", fn, g4h_last_error()); });
+}
+
+// activation bytes one dot reads for n elements of weight type wt
+size_t act_bytes(int wt, int64_t n) {
+    if (wt == G4H_F16) return (size_t)n * 2;
+    if (wt == G4H_BF16) return (size_t)n * 4;
+    return g4h_row_size(g4h_act_type(wt), n);
+}
+
+// nt dots of one weight row against nt activations; out[i] for a[i].  Float
+// rows are padded with zeros to a multiple of 8 elements (the GPU row unit),
+// which adds only +0 products.
+bool dots(int wt, const void *w, const void *const *a, int nt, int64_t n, float *out) {
+    const int b = g4_type_blck(wt);
+    n -= n % b;                                          // whole blocks, as the reference's loops
+    if (n <= 0) {
+        for (int i = 0; i < nt; i++) out[i] = 0.0f;
+        return true;
+    }
+    const bool fl = wt == G4H_F16 || wt == G4H_BF16;
+    const int64_t np = fl ? (n + 7) / 8 * 8 : n;
+    const size_t wb = fl ? (size_t)n * 2 : g4h_row_size(wt, n), wbp = fl ? (size_t)np * 2 : wb;
+    const size_t ab = act_bytes(wt, n), abp = act_bytes(wt, np);
+    const size_t o_w = 0, o_a = al256(wbp), o_o = o_a + (size_t)nt * al256(abp), total = o_o + 256;
+    uint8_t *d = stage(total);
+    if (!d) return false;
+    void *s = tl.stream;
+    if (fl && np != n) {
+        if (g4h_memset(d + o_w, 0, wbp, s)) return false;
+        for (int i = 0; i < nt; i++)
+            if (g4h_memset(d + o_a + (size_t)i * al256(abp), 0, abp, s)) return false;
+    }
+    if (g4h_memcpy_h2d(d + o_w, w, wb, s)) return false;
+    for (int i = 0; i < nt; i++)
+        if (g4h_memcpy_h2d(d + o_a + (size_t)i * al256(abp), a[i], ab, s)) return false;
+    for (int i = 0; i < nt; i++)
+        if (g4h_vec_dot(wt, d + o_w, wbp, d + o_a + (size_t)i * al256(abp), np, 1, (float *)(d + o_o) + i, s)) return false;
+    return g4h_memcpy_d2h(out, d + o_o, (size_t)nt * 4, s) == G4H_OK;
+}
+
+float dot1(int wt, const void *w, const void *a, int64_t n, const char *fn) {
+    float r;
+    const void *aa[1] = {a};
+    if (!dots(wt, w, aa, 1, n, &r)) {
+        report(fn);
+        return NAN;
+    }
+    return r;
+}
+
+void dot4(int wt, const void *w, const void *const a[4], int64_t n, float out[4], const char *fn) {
+    if (!dots(wt, w, a, 4, n, out)) {
+        report(fn);
+        for (int i = 0; i < 4; i++) out[i] = NAN;
+    }
+}
+
+typedef int (*QuantFn)(const float *, size_t, void *, size_t, int64_t, int, void *);
+
+void quantize(QuantFn q, int qt, const float *x, void *y, int64_t n, const char *fn) {
+    n -= n % (qt == G4H_Q8_K ? 256 : 32);                // whole blocks (q8_K is not in the tensor type table)
+    if (n <= 0) return;
+    const size_t xb = (size_t)n * 4, yb = g4h_row_size(qt, n);
+    uint8_t *d = stage(al256(xb) + yb);
+    void *s = tl.stream;
+    if (!d || g4h_memcpy_h2d(d, x, xb, s) || q((const float *)d, (size_t)n, d + al256(xb), yb, n, 1, s) ||
+        g4h_memcpy_d2h(y, d + al256(xb), yb, s))
+        report(fn);
+}
+}  // namespace
+
+// ------------------------------------------------------------ quantizers ----
+extern "C" void g4_quantize_q8_0(const float *x, block_q8_0 *y, int64_t n) {
+    quantize(g4h_quantize_q8_0, G4H_Q8_0, x, y, n, "g4_quantize_q8_0");
+}
+extern "C" void g4_quantize_q8_K(const float *x, block_q8_K *y, int64_t n) {
+    quantize(g4h_quantize_q8_K, G4H_Q8_K, x, y, n, "g4_quantize_q8_K");
+}
+extern "C" void g4_quantize_q4_0(const float *x, block_q4_0 *y, int64_t n) {
+    quantize(g4h_quantize_q4_0, G4H_Q4_0, x, y, n, "g4_quantize_q4_0");
+}
+
+// --------------------------------------------------------------- dequant ----
+extern "C" void g4_dequant_row(int type, const void *x, float *y, int64_t n) {
+    const int b = g4_type_blck(type);
+    if (b) n -= n % b;                                   // whole blocks, as the reference's loops
+    const size_t xb = b ? g4_row_size(type, n) : 0;
+    bool ok = b != 0 && type != 24 && type != 25 && type != 26 && type != 27 && type != 28;
+    if (ok && n > 0) {
+        uint8_t *d = stage(al256(xb) + (size_t)n * 4);
+        void *s = tl.stream;
+        ok = d && !g4h_memcpy_h2d(d, x, xb, s) &&
+             !g4h_dequant_rows(type, d, xb, (float *)(d + al256(xb)), (size_t)n, n, 1, s) &&
+             !g4h_memcpy_d2h(y, d + al256(xb), (size_t)n * 4, s);
+    } else if (!ok) {
+        char msg[96];
+        snprintf(msg, sizeof msg, "g4_dequant_row: type %d unsupported", type);
+        g4h_internal_fail(G4H_ERR_TYPE, msg);
+    }
+    if (!ok) {
+        report("g4_dequant_row");
+        for (int64_t i = 0; i < n; i++) y[i] = NAN;
+    }
+}
+
+// ------------------------------------------------------------------ dots ----
+#define G4_DOT(NAME, WT)                                                                       \
+    extern "C" float g4_dot_##NAME(const void *w, const void *a, int64_t n) {                 \
+        return dot1(WT, w, a, n, "g4_dot_" #NAME);                                             \
+    }                                                                                          \
+    extern "C" void g4_dot_##NAME##_x4(const void *w, const void *const a[4], int64_t n, float out[4]) { \
+        dot4(WT, w, a, n, out, "g4_dot_" #NAME "_x4");                                         \
+    }
+G4_DOT(q4_0_q8_0, G4H_Q4_0)
+G4_DOT(q8_0_q8_0, G4H_Q8_0)
+G4_DOT(q6_K_q8_K, G4H_Q6_K)
+G4_DOT(tq2_0_q8_K, G4H_TQ2_0)
+G4_DOT(q2_K_q8_K, G4H_Q2_K)
+G4_DOT(q3_K_q8_K, G4H_Q3_K)
+G4_DOT(q4_K_q8_K, G4H_Q4_K)
+G4_DOT(q5_K_q8_K, G4H_Q5_K)
+#undef G4_DOT
+
+extern "C" float g4_dot_f16(const void *w, const g4_fp16 *a, int64_t n) { return dot1(G4H_F16, w, a, n, "g4_dot_f16"); }
+extern "C" float g4_dot_bf16(const void *w, const float *a, int64_t n) { return dot1(G4H_BF16, w, a, n, "g4_dot_bf16"); }

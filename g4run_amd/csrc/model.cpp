@@ -24,6 +24,7 @@
 #include <cstring>
 #include <vector>
 
+#include "host_fp16.h"
 #include "kernels.h"
 
 using namespace g4;
@@ -31,40 +32,6 @@ using namespace g4;
 
 extern "C" int g4h_internal_fail(int status, const char *msg);
 
-
-// Host-side fp16 conversions for building the GELU table, written from the
-// IEEE-754 binary16 definition (round to nearest even, gradual underflow).
-static float host_h2f(uint16_t h) {
-    const uint32_t sign = (uint32_t)(h >> 15) << 31, e = (h >> 10) & 31u, m = h & 1023u;
-    uint32_t u;
-    if (e == 31) u = sign | 0x7f800000u | (m << 13);
-    else if (e == 0) {
-        if (m == 0) u = sign;
-        else {
-            float f = std::ldexp((float)m, -24);
-            std::memcpy(&u, &f, 4);
-            u |= sign;
-        }
-    } else u = sign | ((e + 112u) << 23) | (m << 13);
-    float f;
-    std::memcpy(&f, &u, 4);
-    return f;
-}
-static uint16_t host_f2h(float f) {
-    uint32_t u;
-    std::memcpy(&u, &f, 4);
-    const uint16_t sign = (uint16_t)((u >> 16) & 0x8000u);
-    const uint32_t mag = u & 0x7fffffffu;
-    if (mag > 0x7f800000u) return (uint16_t)(sign | 0x7e00u | ((mag >> 13) & 1023u ? (mag >> 13) & 1023u : 1u));
-    if (mag >= 0x47800000u) return (uint16_t)(sign | 0x7c00u);
-    if (mag < 0x38800000u) {
-        // subnormal result: value / 2^-24 rounded half-even
-        const float scaled = std::fabs(f) * 16777216.0f;           // exact (power-of-two scaling)
-        return (uint16_t)(sign | (uint16_t)std::nearbyint(scaled));
-    }
-    const uint32_t r = mag + 0x0fffu + ((mag >> 13) & 1u);
-    return (uint16_t)(sign | ((r - 0x38000000u) >> 13));
-}
 
 struct g4h_model {
     g4h_model_config c;
@@ -221,11 +188,7 @@ extern "C" int g4h_model_create(const g4h_model_config *cfg, uint64_t seed, g4h_
 
     // GELU fp16 table (quants.c:48-58)
     std::vector<uint16_t> gt(65536);
-    for (uint32_t h = 0; h < 65536; h++) {
-        const float x = host_h2f((uint16_t)h);
-        const float g = 0.5f * x * (1.0f + tanhf(0.79788456080286535587989211986876f * x * (1.0f + 0.044715f * x * x)));
-        gt[h] = host_f2h(g);
-    }
+    for (uint32_t h = 0; h < 65536; h++) gt[h] = gelu_table_entry((uint16_t)h);
     if ((rc = model_alloc(m, (void **)&m->gelu, 65536 * 2))) return bail(rc);
     if (hipMemcpy(m->gelu, gt.data(), 65536 * 2, hipMemcpyHostToDevice) != hipSuccess) return bail(G4H_ERR_HIP);
 
