@@ -125,14 +125,42 @@ def time_graph(G, stream, fn, k):
     return ms
 
 
-def cpu_baseline(sets, seconds: float):
-    """Reference AVX2 dots (oracle/_ref) through the restated row-split pool."""
+def cpu_share() -> int:
+    """CPUs this process may run on (the GPU box gives each job a share of the
+    host: affinity mask and OMP_NUM_THREADS)."""
+    n = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    omp = os.environ.get("OMP_NUM_THREADS")
+    if omp and omp.isdigit() and int(omp) > 0:
+        n = min(n, int(omp))
+    return max(1, n)
+
+
+def cpu_threads():
+    """The reference's thread rule (main.c:11-23: -t = physical cores) and its
+    silent cap at 32 (model.c:101), then the box share this job may use."""
+    requested = physical_cores()
+    capped = min(requested, 32)
+    used = min(capped, cpu_share())
+    return requested, capped, used
+
+
+def cpu_kind():
+    """'reference': the reference's own quants.c dots (oracle/_ref, compiled
+    in place from the reference sources by `make -C oracle ref`); 'port': the
+    oracle's restated dots (pinned bit for bit to the reference build) when
+    that library is not present."""
     from oracle import g4o
-    if not g4o.ref_available():
-        return None
-    ncores = physical_cores()
-    threads = min(ncores, 32, 16)      # reference caps at 32 (model.c:101); box share is 16
-    g4o.use_reference_dots(True)
+    return "reference" if g4o.ref_available() else "port"
+
+
+def cpu_baseline(sets, seconds: float):
+    """The reference's AVX2 dots (or their pinned restatement) through the
+    restated row-split pool (model.c:59-65): the same up+down q4_0 pair."""
+    from oracle import g4o
+    kind = cpu_kind()
+    ncores, capped, threads = cpu_threads()
+    if kind == "reference":
+        g4o.use_reference_dots(True)
     g4o.pool_start(threads)
     try:
         host = []
@@ -144,26 +172,33 @@ def cpu_baseline(sets, seconds: float):
         times = []
         t_end = time.perf_counter() + seconds
         step = 0
-        while time.perf_counter() < t_end or step < 3:
+        while time.perf_counter() < t_end or step < 23:           # >= 20 timed reps after 3 warm-ups
             t0 = time.perf_counter()
             for s, ws, x in host:
                 act = g4o.prep_act(s.qt, x)
                 g4o.matmul(s.qt, ws[step % len(ws)], act, s.cols, nthreads=threads)
             times.append(time.perf_counter() - t0)
             step += 1
-        times = times[3:] if len(times) > 6 else times
+        times = times[3:]
         med = float(np.median(times))
         nbytes = sum(s.bytes for s, _, _ in host)
-        return {"value": round(nbytes / med / 1e9, 2), "unit": "GB/s", "cores": threads, "kind": "reference",
-                "sample": f"{len(times)} steps of the same up+down q4_0 GEMV pair (median), weights rotated over "
-                          f"{len(host[0][1])} host copies; reference quants.c AVX2 dots built with README flags "
-                          f"(-Ofast -march=x86-64-v3), pthread row split of model.c:59-65; "
-                          f"{ncores} physical cores ({cpu_model()}), {threads} threads (the box's share; the "
-                          f"reference caps at 32)",
+        dots = ("the reference's quants.c AVX2 dots built with its README flags (-Ofast -march=x86-64-v3, "
+                "oracle/_ref)" if kind == "reference" else
+                "the oracle's restated AVX2-order dots (bit-identical to the reference build)")
+        return {"value": round(nbytes / med / 1e9, 2), "unit": "GB/s", "cores": threads, "kind": kind,
+                "threads_requested": ncores, "threads_reference_cap": capped, "threads_used": threads,
+                "sample": f"{len(times)} steps of the same up+down q4_0 GEMV pair (median after 3 warm-ups), "
+                          f"weights rotated over {len(host[0][1])} host copies beyond the LLC; {dots}, pthread row "
+                          f"split of model.c:59-65; host {cpu_model()}: {ncores} physical cores requested "
+                          f"(main.c:11-23), {capped} after the reference's cap of 32 (model.c:101), {threads} used "
+                          f"(this job's CPU share)" + ("" if threads == capped else
+                                                        "; the share binds before the cap, so an uncapped run "
+                                                        "would use the same threads"),
                 "ms_per_step": round(med * 1e3, 3)}
     finally:
         g4o.pool_stop()
-        g4o.use_reference_dots(False)
+        if kind == "reference":
+            g4o.use_reference_dots(False)
 
 
 def bench_prefill(G, stream, Ms=(1, 8, 16, 32, 64, 128, 256, 512)):
@@ -185,7 +220,9 @@ def bench_prefill(G, stream, Ms=(1, 8, 16, 32, 64, 128, 256, 512)):
             fn = lambda i: G.matmul(s.W[i % len(s.W)], Yb, nb=M, x=xb, path=path, stream=stream.ptr)
             us = time_graph(G, stream, fn, k) / k * 1e3
             row[name] = {"us": round(us, 2), "GBps": round(alg / us / 1e3, 1), "TOPS": round(ops / us / 1e6, 1),
-                         "pct_int8_peak": round(100 * ops / us / 1e6 / PEAK_INT8, 2)}
+                         "hbm_frac": round(alg / us / 1e3 / PEAK_HBM, 4),
+                         "pct_int8_peak": round(100 * ops / us / 1e6 / PEAK_INT8, 2),
+                         "kernel": G.matmul_describe(s.W[0], M, path).split(";")[0]}
         row["auto_path"] = G.matmul_path(s.W[0], M)
         out[str(M)] = row
         log(f"bench: prefill M={M}: gemv {row['gemv']['us']} us, mfma {row['mfma']['us']} us "
@@ -248,7 +285,8 @@ def bench_decode(G, steps: int, cpu_seconds: float, want_cpu: bool):
     e1.record(st.ptr)
     ms = e0.elapsed_ms(e1)
     tok, pos = m.get_state(st.ptr)
-    assert pos == c["n_ctx"], pos
+    # the last step ran at n_ctx - 1: the state stays there and reports the full cache
+    assert pos == c["n_ctx"] - 1 and m.status(st.ptr) == G.STATUS_CTX_FULL, (pos, m.status(st.ptr))
     ms_tok = ms / steps
     mean_ctx = pos0 + (steps + 1) / 2.0
     kv_row = c["head_dim"] * 2
@@ -263,14 +301,16 @@ def bench_decode(G, steps: int, cpu_seconds: float, want_cpu: bool):
     log(f"bench: decode {out['tok_per_s']} tok/s ({ms_tok:.3f} ms/token, {out['GBps']} GB/s algorithmic)")
     if want_cpu:
         from oracle import g4o
-        if g4o.ref_available():
+        kind = cpu_kind()
+        if True:
             w, kc, vc = m.host_copy()
             om = g4o.Model({"n_layer": c["n_layer"], "n_embd": c["n_embd"], "n_head": c["n_head"], "n_kv": c["n_kv"],
                             "hd": c["head_dim"], "n_ff": c["n_ff"], "n_vocab": c["n_vocab"], "n_ctx": c["n_ctx"],
                             "rope_base": c["rope_base"], "eps": c["rms_eps"], "kv_type": c["kv_type"],
                             "wtype": c["wtype"], "head_type": c["head_type"]}, w, kc, vc)
-            threads = min(physical_cores(), 32, 16)
-            g4o.use_reference_dots(True)
+            ncores, capped, threads = cpu_threads()
+            if kind == "reference":
+                g4o.use_reference_dots(True)
             g4o.pool_start(threads)
             try:
                 times, t_end, p = [], time.perf_counter() + cpu_seconds, c["n_ctx"] - 64
@@ -281,13 +321,17 @@ def bench_decode(G, steps: int, cpu_seconds: float, want_cpu: bool):
                     p = p + 1 if p + 1 < c["n_ctx"] else c["n_ctx"] - 64
             finally:
                 g4o.pool_stop()
-                g4o.use_reference_dots(False)
+                if kind == "reference":
+                    g4o.use_reference_dots(False)
             med = float(np.median(times))
+            dots = "reference AVX2 dots incl. g4_dot_f16 for scores" if kind == "reference" else \
+                "the oracle's restated AVX2-order dots"
             out["cpu_baseline"] = {"tok_per_s": round(1 / med, 2), "ms_per_token": round(med * 1e3, 2), "cores": threads,
-                                   "kind": "reference",
+                                   "kind": kind, "threads_requested": ncores, "threads_reference_cap": capped,
+                                   "threads_used": threads,
                                    "sample": f"{len(times)} decode steps at positions {c['n_ctx'] - 64}..{c['n_ctx'] - 1} "
-                                             "of the same model (weights and KV copied from the GPU); reference AVX2 dots "
-                                             "incl. g4_dot_f16 for scores; pthread row split (model.c:59-65), heads in "
+                                             "of the same model (weights and KV copied from the GPU); "
+                                             f"{dots}; pthread row split (model.c:59-65), heads in "
                                              f"parallel (model.c:706); {cpu_model()}"}
             log(f"bench: cpu decode {out['cpu_baseline']['tok_per_s']} tok/s on {threads} threads")
     m.free()
@@ -301,10 +345,11 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--all-configs", action="store_true", help="also time every GEMV config (stderr + JSON)")
+    ap.add_argument("--no-configs", action="store_true",
+                    help="skip the per-config GEMV sweep (BASELINE configs 0 and 2, plus the further formats)")
     ap.add_argument("--decode-steps", type=int, default=128, help="decode steps timed at context ~8192 (0 = skip)")
-    ap.add_argument("--prefill", nargs="?", const="1,8,16,32,64,128,256,512", default=None, metavar="M,...",
-                    help="also time config 3 (GEMV vs matrix-core crossover) at these token counts")
+    ap.add_argument("--prefill", default="1,8,64,512", metavar="M,...",
+                    help="token counts of config 3 (GEMV vs matrix-core crossover); '' skips it")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="start with one 256 MiB device copy (the reference dispatch for rocprofv3 --pmc byte counters)")
     args = ap.parse_args()
@@ -352,7 +397,7 @@ def main():
     kernel = G.matmul_describe(up.W[0], 1, 1).split(";")[0]
 
     extra = {}
-    if args.all_configs:
+    if not args.no_configs:
         from g4run_amd import synth
         for name, (qt, rows, cols) in synth.GEMV_CONFIGS.items():
             s = GemvSet(G, qt, rows, cols, copies_for(rows * G.row_size(qt, cols)), seed=77)
@@ -361,12 +406,15 @@ def main():
             t_fus = time_graph(G, stream, lambda i: s.call(G, i, stream.ptr, fused=True), k) / k * 1e3
             extra[name] = {"gemv_us": round(t_pre, 3), "GBps": round(s.bytes / t_pre / 1e3, 1),
                            "pct_peak": round(100 * s.bytes / t_pre / 1e3 / PEAK_HBM, 1),
-                           "with_quantize_us": round(t_fus, 3), "alg_bytes": s.bytes}
+                           "frac": round(s.bytes / t_pre / 1e3 / PEAK_HBM, 4),
+                           "with_quantize_us": round(t_fus, 3), "alg_bytes": s.bytes,
+                           "kernel": G.matmul_describe(s.W[0], 1, 1).split(";")[0],
+                           "copies": len(s.W)}
             log(f"bench: {name}: {t_pre:.3f} us/launch  {s.bytes / t_pre / 1e3:.0f} GB/s "
                 f"({100 * s.bytes / t_pre / 1e3 / PEAK_HBM:.1f}% of 8 TB/s); with quantize {t_fus:.3f} us")
             del s
 
-    prefill_ms = args.prefill or ("1,8,16,32,64,128,256,512" if args.all_configs else None)
+    prefill_ms = args.prefill
     prefill = bench_prefill(G, stream, tuple(int(m) for m in prefill_ms.split(","))) if prefill_ms else None
     attention = bench_attention(G, stream)
 
