@@ -24,6 +24,7 @@
 // weights), and k_mm_lds, 64 x 128 tiles staged through LDS in 8-block stages
 // shared by 8 waves (many tokens: 1/8 of the operand traffic per output).
 #include <cstdio>
+#include <type_traits>
 
 #include "formats.h"
 #include "kernels.h"
@@ -36,6 +37,8 @@ typedef int v16i __attribute__((ext_vector_type(16)));
 typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 typedef float v16f __attribute__((ext_vector_type(16)));
 typedef float v32f __attribute__((ext_vector_type(32)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef _Float16 v4h __attribute__((ext_vector_type(4)));
 
 constexpr int MM_KB_SMALL = 8;       // blocks per operand set, one-tile workgroups
 
@@ -368,6 +371,188 @@ __global__ __launch_bounds__(64 * TM * TN, 2) void k_mm_lds(g4h_tensor W, const 
     }
 }
 
+// Few tokens (M <= 32): 16-row strips.  A workgroup of 4 waves owns 16 weight
+// rows and every token, so each weight byte is read from HBM once per call.
+// The activations of a chunk of KC blocks (all tokens) are copied into LDS
+// with direct-to-LDS loads (no registers, [block][token] layout so a wave's
+// operand read is one contiguous 512-byte run), the next chunk's copy issued
+// while the current one is used.  Wave w multiplies blocks w, w + 4, ... (the
+// blocks of residue w mod 4): its weight operands (16 rows x 8 bytes per lane
+// and block) and scales stream straight into registers MMS_D of its blocks
+// ahead -- about 36 KB per CU in flight and no barrier inside a chunk.  Per
+// block and 16 x 16 (token x row) tile: one v_mfma_i32_16x16x32_i8 for the
+// exact block sums, one v_mfma_f32_16x16x16_f16 for the exact scale outer
+// product d_a * d_w (only k = 0 non-zero), and an fma into the wave's
+// partial -- the arithmetic of k_mm_mfma (residue partials, blocks in
+// increasing order, ((p0 + p1) + p2) + p3 through LDS), so every output is
+// the same bits.
+constexpr int MMS_D = 16;            // a wave's blocks in flight
+constexpr int MMS_MAXM = 32;
+
+typedef long v1l;
+
+// f(integral_constant<int, I>) for I = 0 .. N-1 as straight-line code (every
+// array index a constant from the start, so the arrays stay in registers)
+template <int I, int N, class F>
+__device__ __forceinline__ void static_for(F &&f) {
+    if constexpr (I < N) {
+        f(std::integral_constant<int, I>{});
+        static_for<I + 1, N>(f);
+    }
+}
+
+// s_waitcnt immediate that waits until at most n vector-memory operations
+// (loads, including direct-to-LDS loads) of this wave are outstanding
+constexpr int vmcnt_imm(int n) { return (n & 15) | (7 << 4) | (15 << 8) | ((n >> 4) << 14); }
+
+template <int MT>
+struct StripGeo {
+    static constexpr int MP = 16 * MT;                                // tokens staged (padded)
+    static constexpr int KC = MT == 1 ? 128 : 64;                    // blocks per activation chunk
+    static constexpr int QCH = MP * KC * 2;                          // 16-byte chunks of a chunk's quants
+    static constexpr int SCH = MP * KC;                              // 2-byte scales of a chunk
+    static_assert(QCH % 256 == 0 && SCH % 256 == 0, "whole DMA instructions per thread");
+    static_assert(KC % (4 * MMS_D) == 0, "a chunk is whole prefetch rounds");
+};
+
+// the LDS pointer type of the direct-to-LDS load builtin
+typedef void __attribute__((address_space(3))) *lds_ptr_t;
+typedef const void __attribute__((address_space(1))) *glb_ptr_t;
+
+template <int WT, int MT>
+__global__ __launch_bounds__(256) void k_mm_strip(g4h_tensor W, const int8_t *__restrict__ qa,
+                                                   const uint16_t *__restrict__ da, int M, float *__restrict__ Y) {
+    using G = StripGeo<MT>;
+    constexpr int MP = G::MP, KC = G::KC, WB = WT == Q8_0 ? 32 : 16;
+    // two activation chunk buffers, separate objects so that the compiler can
+    // tell a read of one from a direct-to-LDS write of the other
+    __shared__ __align__(16) int8_t As0[KC * MP * 32], As1[KC * MP * 32];     // [blk][tok][32]
+    __shared__ __align__(16) uint16_t Ad0[KC * MP], Ad1[KC * MP];             // [blk][tok]
+    __shared__ float red[3 * MT * 4 * 64];
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int li = lane & 15, kg = lane >> 4;
+    const int nb = (int)W.nb, nch = (nb + KC - 1) / KC;
+    const int64_t row = min((int64_t)blockIdx.x * 16 + li, W.nrows - 1);
+
+    // chunk c of the activations: this thread's 16-byte runs ([blk][tok][half]
+    // order) and 2-byte scales ([blk][tok]) into registers, later into LDS
+    constexpr int QPT = G::QCH / 256, SPT = G::SCH / 256;
+    v4i aq[QPT];
+    uint16_t ad[SPT];
+    auto a_issue = [&](int c) __attribute__((always_inline)) {
+        static_for<0, QPT>([&](auto I) {
+            const int q = I.value * 256 + t;
+            const int blk = q / (MP * 2), tok = min((q >> 1) % MP, M - 1), half = q & 1;
+            const int b = min(c * KC + blk, nb - 1);
+            aq[I.value] = *(const v4i *)(qa + ((size_t)tok * nb + b) * 32 + 16 * half);
+        });
+        static_for<0, SPT>([&](auto I) {
+            const int q = I.value * 256 + t;
+            const int blk = q / MP, tok = min(q % MP, M - 1);
+            const int b = min(c * KC + blk, nb - 1);
+            ad[I.value] = da[(size_t)tok * nb + b];
+        });
+    };
+    auto a_store = [&](int8_t *As, uint16_t *Ad) __attribute__((always_inline)) {
+        static_for<0, QPT>([&](auto I) { *(v4i *)(As + (size_t)(I.value * 256 + t) * 16) = aq[I.value]; });
+        static_for<0, SPT>([&](auto I) { Ad[I.value * 256 + t] = ad[I.value]; });
+    };
+    // the wave's j-th block (block 4 j + wave), clamped to the last block
+    struct WOp {
+        v1l q;
+        uint16_t d;
+    };
+    auto w_load = [&](int j) __attribute__((always_inline)) -> WOp {
+        const int b = min(4 * j + wave, nb - 1);
+        WOp o;
+        if constexpr (WT == Q8_0) o.q = *(const v1l *)(W.qs + ((size_t)row * nb + b) * WB + 8 * kg);
+        else o.q = *(const v1l *)(W.qs + ((size_t)row * nb + b) * WB + 8 * (kg & 1));
+        o.d = ((const uint16_t *)W.sc)[(size_t)row * nb + b];
+        return o;
+    };
+    const v4i zi = {};
+    const v4f zf = {};
+    v4f acc[MT];
+#pragma unroll
+    for (int tt = 0; tt < MT; tt++) acc[tt] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+    auto mac = [&](const WOp &o, const int8_t *As, const uint16_t *Ad, int blk) __attribute__((always_inline)) {
+        v1l wv = o.q;
+        if constexpr (WT == Q4_0) {
+            // elements 8 kg .. 8 kg + 7: low nibbles of bytes 8 (kg & 1).. for kg < 2, high nibbles for kg >= 2
+            // (quants.c:542-545), each as q - 8
+            const uint64_t u = (uint64_t)o.q;
+            const uint32_t sh = 4 * (kg >> 1);
+            const uint32_t lo = ((uint32_t)u >> sh) & 0x0F0F0F0Fu, hi = ((uint32_t)(u >> 32) >> sh) & 0x0F0F0F0Fu;
+            wv = (v1l)(((uint64_t)((hi + 0x78787878u) ^ 0x80808080u) << 32) | ((lo + 0x78787878u) ^ 0x80808080u));
+        }
+        v4h hw = {};
+        if (kg == 0) hw[0] = __builtin_bit_cast(_Float16, o.d);
+#pragma unroll
+        for (int tt = 0; tt < MT; tt++) {
+            const v1l av = *(const v1l *)(As + (blk * MP + tt * 16 + li) * 32 + 8 * kg);
+            const v4i is = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, wv, zi, 0, 0, 0);
+            v4h ha = {};
+            if (kg == 0) ha[0] = __builtin_bit_cast(_Float16, Ad[blk * MP + tt * 16 + li]);
+            const v4f sc = __builtin_amdgcn_mfma_f32_16x16x16f16(ha, hw, zf, 0, 0, 0);
+#pragma unroll
+            for (int r = 0; r < 4; r++) acc[tt][r] = __builtin_fmaf((float)is[r], sc[r], acc[tt][r]);
+        }
+    };
+
+    // issue order keeps every wait exact: chunk 0's activations, then the
+    // first MMS_D weight blocks; each chunk's activations are issued ahead of
+    // the weight blocks of that chunk's rounds
+    a_issue(0);
+    WOp wr[MMS_D];
+    static_for<0, MMS_D>([&](auto I) { wr[I.value] = w_load(I.value); });
+    const int nj = (nb - wave + 3) / 4;                                  // this wave's blocks
+    // one chunk: its activations from registers into LDS (they were issued
+    // ahead of every weight load not yet consumed, so the wait for them waits
+    // for nothing still streaming), a bare barrier (a fenced __syncthreads would
+    // also wait for the weight loads in flight), the next chunk's activation
+    // loads, then the wave's blocks in rounds of MMS_D.  Two buffers: chunk c
+    // is stored while no wave reads the other one any more.
+    auto chunk = [&](int c, int8_t *As, uint16_t *Ad) __attribute__((always_inline)) {
+        a_store(As, Ad);
+        lds_barrier();
+        if (c + 1 < nch) a_issue(c + 1);
+        for (int r0 = 0; r0 < KC / 4; r0 += MMS_D) {
+            static_for<0, MMS_D>([&](auto I) {
+                const int jl = r0 + I.value, j = c * (KC / 4) + jl;
+                const WOp o = wr[I.value];
+                wr[I.value] = w_load(j + MMS_D);
+                if (j < nj) mac(o, As, Ad, 4 * jl + wave);               // uniform
+            });
+        }
+    };
+    for (int c = 0; c < nch; c += 2) {
+        chunk(c, As0, Ad0);
+        if (c + 1 < nch) chunk(c + 1, As1, Ad1);
+    }
+
+    // ((p0 + p1) + p2) + p3 through LDS; C[i][j]: i = 4 kg + r (token), j = li (row)
+    if (wave > 0) {
+#pragma unroll
+        for (int tt = 0; tt < MT; tt++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) red[(((wave - 1) * MT + tt) * 4 + r) * 64 + lane] = acc[tt][r];
+    }
+    __syncthreads();
+    if (wave > 0) return;
+    const int64_t orow = (int64_t)blockIdx.x * 16 + li;
+#pragma unroll
+    for (int tt = 0; tt < MT; tt++) {
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            float o = acc[tt][r];
+#pragma unroll
+            for (int q = 1; q < 4; q++) o += red[(((q - 1) * MT + tt) * 4 + r) * 64 + lane];
+            const int m = tt * 16 + 4 * kg + r;
+            if (m < M && orow < W.nrows) Y[(size_t)m * W.nrows + orow] = o;
+        }
+    }
+}
+
 // x fp32 [M][ncols] (row stride xs floats) -> planar q8_0 with the quantizer
 // arithmetic of quants.c:74-109 (8 lanes per block).  A thread quantizes QP
 // groups of 4 inputs, 256 groups apart, all loads issued first.
@@ -442,9 +627,20 @@ static bool mm_small(const g4h_tensor &W, int M) {
 // 64 x 128; 512 tokens 41.7 / 40.4 us.  Both give the same bits.
 static bool mm_wide(const g4h_tensor &W, int M) { return ((W.nrows + 127) / 128) * ((M + 63) / 64) >= 256; }
 
+// The 16-row strip kernel serves up to MMS_MAXM tokens (it reads each weight
+// byte once; the tiled kernels read it once per 32 or 64 tokens).  Its LDS
+// holds two activation chunks of KC blocks: 64 KB for 32 tokens.
+static bool mm_strip(const g4h_tensor &W, int M) {
+    if (const char *e = getenv("G4H_MM_STRIP"))
+        if (atoi(e) == 0) return false;
+    return M <= MMS_MAXM && (uint64_t)M * W.nb * 32 < (1ull << 31);
+}
+
 void mm_describe(const g4h_tensor &W, int M, char *buf, size_t len) {
     const char *tn = W.type == Q8_0 ? "q8_0" : "q4_0";
-    if (mm_small(W, M)) {
+    if (mm_strip(W, M)) {
+        snprintf(buf, len, "k_mm_strip<%s,mt=%d> grid=%lld block=256", tn, (M + 15) / 16, (long long)((W.nrows + 15) / 16));
+    } else if (mm_small(W, M)) {
         snprintf(buf, len, "k_mm_mfma<%s,wm=1,wn=1,ks=4,kb=%d> grid=%lldx%d block=256", tn, MM_KB_SMALL,
                  (long long)((W.nrows + 31) / 32), (M + 31) / 32);
     } else if (mm_wide(W, M)) {
@@ -480,6 +676,18 @@ hipError_t launch_matmul_mfma(const g4h_tensor &W, const float *x, size_t x_stri
         hipLaunchKernelGGL(k_act_planar, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, act, stride, nb, M, qa, da);
     }
     if (hipError_t e = hipGetLastError()) return e;
+    if (mm_strip(W, M)) {
+        const dim3 grid((unsigned)((W.nrows + 15) / 16));
+#define G4_MS(T)                                                                                              \
+    if ((M + 15) / 16 == T) {                                                                                 \
+        if (W.type == Q8_0) hipLaunchKernelGGL((k_mm_strip<Q8_0, T>), grid, dim3(256), 0, s, W, qa, da, M, Y); \
+        else hipLaunchKernelGGL((k_mm_strip<Q4_0, T>), grid, dim3(256), 0, s, W, qa, da, M, Y);              \
+        return hipGetLastError();                                                                             \
+    }
+        G4_MS(1) G4_MS(2)
+#undef G4_MS
+        return hipErrorInvalidValue;
+    }
     const bool small = mm_small(W, M);
     if (small) {
         if (W.type == Q8_0) return mm_go<Q8_0, 1, 1, 4, MM_KB_SMALL>(W, qa, da, M, Y, s);

@@ -53,7 +53,7 @@ def test_token_results_independent_of_batch(gpu, oracle, qt, rows, cols, M):
     full = gpu_matmul(gpu, t, x=x, nb=M, path=2)
     if rows == 4096:
         assert gpu.matmul_describe(t, M, 2).startswith("k_mm_lds")
-        assert gpu.matmul_describe(t, 16, 2).startswith("k_mm_mfma")
+        assert gpu.matmul_describe(t, 16, 2).startswith("k_mm_strip")
         assert_close(full, oracle_matmul(oracle, qt, w, x), f"{rows}x{cols} M={M}")
     for m in (16, 40, 64, 65, 200):
         part = gpu_matmul(gpu, t, x=x[:m].copy(), nb=m, path=2)
@@ -87,3 +87,22 @@ def test_path_selection_and_errors(gpu):
     with pytest.raises(G.G4HError) as e:
         G.matmul(tk, Y, nb=16, x=x, path=2)
     assert e.value.status == G.ERR_TYPE
+
+
+@pytest.mark.parametrize("qt", [8, 2])
+@pytest.mark.parametrize("rows,cols,Ms", [(4096, 4096, (1, 8, 16, 32)), (100, 2080, (1, 5, 17, 32)),
+                                          (33, 1056, (2, 31, 32)), (17, 10240, (3, 16, 19))])
+def test_strip_kernel_equals_tile_kernel(gpu, oracle, monkeypatch, qt, rows, cols, Ms):
+    """The 16-row strip kernel (up to 32 tokens; each weight byte read once)
+    gives the tile kernel's bits (G4H_MM_STRIP=0): the same exact block sums,
+    exact scale products and residue-mod-4 partial sums.  Ragged rows, token
+    counts off the 16-token tile and block counts off the 8-block stage."""
+    w, x, t = _setup(gpu, qt, rows, cols, max(Ms), seed=rows * 7 + cols)
+    for M in Ms:
+        assert gpu.matmul_describe(t, M, 2).startswith("k_mm_strip")
+        strip = gpu_matmul(gpu, t, x=x[:M].copy(), nb=M, path=2)
+        monkeypatch.setenv("G4H_MM_STRIP", "0")
+        tile = gpu_matmul(gpu, t, x=x[:M].copy(), nb=M, path=2)
+        monkeypatch.delenv("G4H_MM_STRIP")
+        assert np.array_equal(bits(strip), bits(tile)), f"{rows}x{cols} M={M}"
+        assert_close(strip, oracle_matmul(oracle, qt, w, x[:M]), f"{rows}x{cols} M={M}")
