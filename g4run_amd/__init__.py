@@ -105,6 +105,18 @@ _SIGS = [
     ("g4h_model_norm", _vp, [_vp, _int, _int]),
     ("g4h_model_kv", _int, [_vp, _int, C.POINTER(_vp), C.POINTER(_vp), C.POINTER(_sz)]),
     ("g4h_model_weight_bytes", _sz, [_vp]),
+    ("g4h_sampler_default_params", None, [_vp]),
+    ("g4h_sampler_create", _int, [_int, _vp, C.POINTER(_vp)]),
+    ("g4h_sampler_free", _int, [_vp]),
+    ("g4h_sampler_set_params", _int, [_vp, _vp, _vp]),
+    ("g4h_sampler_set_rng", _int, [_vp, C.POINTER(C.c_uint64), _vp]),
+    ("g4h_sampler_reset", _int, [_vp, _vp]),
+    ("g4h_sampler_ban", _int, [_vp, _int, _vp]),
+    ("g4h_sampler_accept", _int, [_vp, C.POINTER(_int), _int, _vp]),
+    ("g4h_sample", _int, [_vp, _vp, _vp, _int, _vp]),
+    ("g4h_sampler_get_state", _int, [_vp, C.POINTER(C.c_uint64), C.POINTER(_int), C.POINTER(_int), C.POINTER(_int),
+                                     _vp]),
+    ("g4h_model_set_sampler", _int, [_vp, _vp]),
 ]
 
 _lib = None
@@ -428,6 +440,74 @@ class _View:
         return b.download(np.uint8, (self.nrows, rs))
 
 
+class SamplerParams(C.Structure):
+    """g4h_sampler_params: the settings of g4_sampler (g4run.h:465-473)."""
+    _fields_ = [("temp", C.c_float), ("top_k", _int), ("top_p", C.c_float), ("repeat_penalty", C.c_float),
+                ("repeat_last_n", _int), ("freq_penalty", C.c_float), ("presence_penalty", C.c_float),
+                ("no_repeat_ngram", _int), ("seed", C.c_uint64)]
+
+
+SAMPLER_RING = 4096
+
+
+class Sampler:
+    """Device-resident sampling chain (g4h_sampler, the GPU form of sampler.c).
+    Keyword settings override g4_sampler_init's defaults."""
+
+    def __init__(self, n_vocab: int, **params):
+        init()
+        self.n_vocab = n_vocab
+        self._p = SamplerParams()
+        lib().g4h_sampler_default_params(C.byref(self._p))
+        for k, v in params.items():
+            setattr(self._p, k, v)
+        p = _vp()
+        check(lib().g4h_sampler_create(n_vocab, C.byref(self._p), C.byref(p)))
+        self.ptr = p.value
+
+    def set(self, stream=None, **params) -> None:
+        for k, v in params.items():
+            setattr(self._p, k, v)
+        check(lib().g4h_sampler_set_params(self.ptr, C.byref(self._p), stream))
+
+    def set_rng(self, words, stream=None) -> None:
+        w = (C.c_uint64 * 4)(*[int(x) for x in words])
+        check(lib().g4h_sampler_set_rng(self.ptr, w, stream))
+
+    def reset(self, stream=None) -> None:
+        check(lib().g4h_sampler_reset(self.ptr, stream))
+
+    def ban(self, tok: int, stream=None) -> None:
+        check(lib().g4h_sampler_ban(self.ptr, int(tok), stream))
+
+    def accept(self, ids, stream=None) -> None:
+        a = np.ascontiguousarray(np.atleast_1d(ids), dtype=np.int32)
+        check(lib().g4h_sampler_accept(self.ptr, a.ctypes.data_as(C.POINTER(_int)), a.size, stream))
+
+    def sample(self, logits, out=None, accept: bool = False, stream=None) -> None:
+        """Draw from device logits (rewritten in place); the id goes to device out."""
+        check(lib().g4h_sample(self.ptr, _p(logits), _p(out) if out is not None else None, int(accept), stream))
+
+    def state(self, stream=None):
+        """(rng words, ring oldest first, slow-path draw count)."""
+        rng = (C.c_uint64 * 4)()
+        rec = (_int * SAMPLER_RING)()
+        n, slow = _int(), _int()
+        check(lib().g4h_sampler_get_state(self.ptr, rng, rec, C.byref(n), C.byref(slow), stream))
+        return [int(x) for x in rng], [int(rec[i]) for i in range(n.value)], slow.value
+
+    def free(self) -> None:
+        if getattr(self, "ptr", None):
+            lib().g4h_sampler_free(self.ptr)
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
 class Model:
     """Device-resident decoder (g4h_model) and its decode step."""
 
@@ -459,6 +539,11 @@ class Model:
         t, p = _int(), _int()
         check(lib().g4h_model_get_state(self.ptr, C.byref(t), C.byref(p), stream))
         return t.value, p.value
+
+    def set_sampler(self, sampler) -> None:
+        """Draw each step's token with a Sampler (accepting it), or greedily with None."""
+        check(lib().g4h_model_set_sampler(self.ptr, sampler.ptr if sampler is not None else None))
+        self._sampler = sampler
 
     def status(self, stream=None) -> int:
         """STATUS_* flags of the device-side steps since the last set_state."""

@@ -81,52 +81,13 @@ __global__ __launch_bounds__(256) void k_gelu_quant(const float *gu, int n_ff, c
 }
 
 // ---------------------------------------------------- argmax + advance --
-// First index of the maximum (sampler.c:139-144: best starts at index 0 and
-// later values must be strictly larger, so NaNs never win and a NaN at index 0
-// keeps index 0); then token <- argmax, pos <- pos + 1, npos <- pos + 1 and
-// the step count (the attention hand-off tags) + 1.
-__device__ __forceinline__ void argmax_merge(float &v, int &i, float v2, int i2) {
-    if (v2 > v || (v2 == v && i2 < i)) { v = v2; i = i2; }
-}
+// token <- the first index of the maximum (wg_first_argmax), then the
+// position advances (state_advance).
 __global__ __launch_bounds__(1024) void k_argmax_advance(const float *logits, int n, int *state, int n_ctx) {
     __shared__ float bv[16];
     __shared__ int bi[16];
-    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-    float best = -INFINITY;
-    int idx = 0x7fffffff;
-    const int ng = n >> 2;
-    for (int base = 0; base < ng; base += 8 * 1024) {
-        float4 v[8];
-#pragma unroll
-        for (int k = 0; k < 8; k++) {
-            const int gi = base + k * 1024 + t;
-            v[k] = gi < ng ? ldf4(logits + 4 * gi) : make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
-        }
-#pragma unroll
-        for (int k = 0; k < 8; k++) {
-            const int gi = base + k * 1024 + t;
-            const float e[4] = {v[k].x, v[k].y, v[k].z, v[k].w};
-#pragma unroll
-            for (int j = 0; j < 4; j++)
-                if (e[j] > best) { best = e[j]; idx = 4 * gi + j; }
-        }
-    }
-    for (int i = 4 * ng + t; i < n; i += 1024)
-        if (logits[i] > best) { best = logits[i]; idx = i; }
-    for (int k = 32; k >= 1; k >>= 1) argmax_merge(best, idx, __shfl_xor(best, k, 64), __shfl_xor(idx, k, 64));
-    if (lane == 0) { bv[wave] = best; bi[wave] = idx; }
-    __syncthreads();
-    if (t == 0) {
-        for (int w = 1; w < (int)(blockDim.x >> 6); w++) argmax_merge(best, idx, bv[w], bi[w]);
-        state[0] = (idx == 0x7fffffff || __builtin_isnan(logits[0])) ? 0 : idx;
-        if (state[1] + 1 < n_ctx) {
-            state[1] += 1;
-            state[2] = state[1] + 1;
-        } else {
-            state[4] |= STATE_CTX_FULL;                  // the cache is full: pos stays in bounds
-        }
-        state[3] += 1;                                   // steps taken (never reset)
-    }
+    const int id = wg_first_argmax(logits, n, bv, bi);
+    if (threadIdx.x == 0) state_advance(state, id, n_ctx);
 }
 
 // ------------------------------------------------------------ launchers --

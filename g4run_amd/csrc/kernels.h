@@ -92,6 +92,41 @@ hipError_t launch_gelu_quant(const float *gu, int n_ff, const uint16_t *tab, uin
 constexpr int STATE_CTX_FULL = 1;
 hipError_t launch_argmax_advance(const float *logits, int n, int *state, int n_ctx, hipStream_t s);
 
+// k_sample.hip: the sampling chain of sampler.c:74-210 on one workgroup.
+// Device image of a sampler: g4_sampler's settings and state (g4run.h:464-482)
+// with a fixed ring of SAMPLER_RING ids (the reference's recent_cap,
+// sampler.c:10) and the ban list after the struct (n_vocab ints).  The
+// per-id counts the reference keeps in accept are not kept: g4_sample never
+// reads them.
+constexpr int SAMPLER_RING = 4096;
+constexpr int SAMPLER_TOPK_MAX = 512;     // sampler.c:147
+struct SamplerDev {
+    float temp;
+    int top_k;
+    float top_p;
+    float repeat_penalty;
+    int repeat_last_n;
+    float freq_penalty;
+    float presence_penalty;
+    int no_repeat_ngram;
+    uint64_t seed;
+    uint64_t rng[4];
+    int n_vocab, recent_n, recent_head, n_ban;
+    int slow_draws;                       // draws that took the exact heap emulation (ties / NaN)
+    int pad_[3];
+    int recent[SAMPLER_RING];
+};
+inline size_t sampler_dev_bytes(int n_vocab) { return sizeof(SamplerDev) + (size_t)n_vocab * sizeof(int); }
+__host__ __device__ inline int *sampler_bans(SamplerDev *S) { return reinterpret_cast<int *>(S + 1); }
+// Draws one id from logits[n_vocab] (rewritten in place as sampler.c does),
+// writes it to *out if out, pushes it into the ring if accept, and if state is
+// given (the model's token, pos, npos, steps, flags) stores it there and
+// advances the position as launch_argmax_advance does.
+hipError_t launch_sample(SamplerDev *S, int n_vocab, float *logits, int *out, int accept, int *state, int n_ctx,
+                         hipStream_t s);
+// Pushes n ids into the ring in order (sampler.c:37-48).
+hipError_t launch_sampler_push(SamplerDev *S, const int *ids, int n, hipStream_t s);
+
 // k_mfma.hip: many-token matmul on the int8 matrix cores (q8_0 / q4_0 weights)
 size_t mm_planar_bytes(int M, int64_t ncols);
 void mm_describe(const g4h_tensor &W, int M, char *buf, size_t len);

@@ -31,6 +31,9 @@ using namespace g4;
 
 
 extern "C" int g4h_internal_fail(int status, const char *msg);
+// sampler.cpp
+int sampler_n_vocab(const g4h_sampler *s);
+SamplerDev *sampler_device(g4h_sampler *s);
 
 
 struct g4h_model {
@@ -51,6 +54,7 @@ struct g4h_model {
     std::vector<void *> allocs;
     int fuse = 0;                    // FUSE_* steps folded into the GEMVs
     float *trace = nullptr;          // optional per-layer x | qkv | att rows, then the final x (g4h_model_trace)
+    g4h_sampler *sampler = nullptr;  // draws the next token (g4h_model_set_sampler); null: greedy argmax
 };
 
 // Steps of the chain folded into the persistent GEMV family (gemv_p.h) or
@@ -372,7 +376,18 @@ extern "C" int g4h_forward_state(g4h_model *m, void *stream) {
         M_HIP(launch_gemv(*m->head, m->act, ast, m->logits, 1, s));
     }
     M_RC(trace_copy(m->trace ? m->trace + (size_t)c.n_layer * trace_rec : nullptr, TR_X, x, E));
-    M_HIP(launch_argmax_advance(m->logits, c.n_vocab, m->state, c.n_ctx, s));
+    if (m->sampler)
+        M_HIP(launch_sample(sampler_device(m->sampler), c.n_vocab, m->logits, nullptr, 1, m->state, c.n_ctx, s));
+    else
+        M_HIP(launch_argmax_advance(m->logits, c.n_vocab, m->state, c.n_ctx, s));
+    return G4H_OK;
+}
+
+extern "C" int g4h_model_set_sampler(g4h_model *m, g4h_sampler *s) {
+    if (!m) return g4h_internal_fail(G4H_ERR_ARG, "g4h_model_set_sampler: null model");
+    if (s && sampler_n_vocab(s) != m->c.n_vocab)
+        return g4h_internal_fail(G4H_ERR_SHAPE, "g4h_model_set_sampler: the sampler's n_vocab differs from the model's");
+    m->sampler = s;
     return G4H_OK;
 }
 

@@ -143,4 +143,60 @@ __device__ void wg_norm_quant(float *x, const float *delta, const float *w_post,
     }
 }
 
+// The decode state after a step drew `id` (state: token, pos, npos, steps
+// taken, flags): token <- id, pos <- pos + 1 and npos <- pos + 1 unless the
+// cache is full (pos + 1 == n_ctx: pos stays, flags |= STATE_CTX_FULL), and
+// the step count (the attention hand-off tags) + 1.  One thread.
+__device__ __forceinline__ void state_advance(int *state, int id, int n_ctx) {
+    state[0] = id;
+    if (state[1] + 1 < n_ctx) {
+        state[1] += 1;
+        state[2] = state[1] + 1;
+    } else {
+        state[4] |= STATE_CTX_FULL;
+    }
+    state[3] += 1;
+}
+
+// First index of the maximum of logits[0..n) (sampler.c:140-144: the best
+// starts at index 0 and later values must be strictly larger, so NaNs never
+// win and a NaN at index 0 keeps index 0).  All threads of the workgroup
+// (a multiple of 64, at most 1024) call it; bv / bi hold one slot per wave.
+// Returns the index in thread 0 (other threads: their wave's partial).
+__device__ __forceinline__ void argmax_merge(float &v, int &i, float v2, int i2) {
+    if (v2 > v || (v2 == v && i2 < i)) { v = v2; i = i2; }
+}
+__device__ __forceinline__ int wg_first_argmax(const float *logits, int n, float *bv, int *bi) {
+    const int t = threadIdx.x, nt = blockDim.x, lane = t & 63, wave = t >> 6;
+    float best = -INFINITY;
+    int idx = 0x7fffffff;
+    const int ng = n >> 2;
+    for (int base = 0; base < ng; base += 8 * nt) {
+        float4 v[8];
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const int gi = base + k * nt + t;
+            v[k] = gi < ng ? ldf4(logits + 4 * gi) : make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
+        }
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            const int gi = base + k * nt + t;
+            const float e[4] = {v[k].x, v[k].y, v[k].z, v[k].w};
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+                if (e[j] > best) { best = e[j]; idx = 4 * gi + j; }
+        }
+    }
+    for (int i = 4 * ng + t; i < n; i += nt)
+        if (logits[i] > best) { best = logits[i]; idx = i; }
+    for (int k = 32; k >= 1; k >>= 1) argmax_merge(best, idx, __shfl_xor(best, k, 64), __shfl_xor(idx, k, 64));
+    if (lane == 0) { bv[wave] = best; bi[wave] = idx; }
+    __syncthreads();
+    if (t == 0) {
+        for (int w = 1; w < (nt >> 6); w++) argmax_merge(best, idx, bv[w], bi[w]);
+        idx = (idx == 0x7fffffff || __builtin_isnan(logits[0])) ? 0 : idx;
+    }
+    return idx;
+}
+
 }  // namespace g4

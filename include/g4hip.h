@@ -243,11 +243,13 @@ int  g4h_model_free(g4h_model *m);
 /* Fill every KV slot of every layer with N(0,1) values (stored as kv_type). */
 int  g4h_model_fill_kv(g4h_model *m, uint64_t seed, void *stream);
 /* g4_forward (g4run.h:309-311): one decode step for `token` at `pos`
- * (synchronous); logits stay on the device (g4h_model_logits), the greedy next
- * token is returned in *next_token. */
+ * (synchronous); logits stay on the device (g4h_model_logits), the next token
+ * (greedy argmax, or the draw of the sampler set by g4h_model_set_sampler) is
+ * returned in *next_token. */
 int  g4h_forward(g4h_model *m, int token, int pos, int *next_token, void *stream);
 /* The same step reading token/pos from device state and advancing it
- * (token <- argmax, pos <- pos+1): asynchronous, capturable in a graph. */
+ * (token <- argmax or the sampler's draw, pos <- pos+1): asynchronous,
+ * capturable in a graph. */
 int  g4h_forward_state(g4h_model *m, void *stream);
 int  g4h_model_set_state(g4h_model *m, int token, int pos, void *stream);
 int  g4h_model_get_state(g4h_model *m, int *token, int *pos, void *stream);
@@ -286,6 +288,64 @@ g4h_tensor *g4h_model_matrix(g4h_model *m, int layer, int which);
 float      *g4h_model_norm(g4h_model *m, int layer, int which);
 int         g4h_model_kv(g4h_model *m, int layer, void **k_dev, void **v_dev, size_t *bytes);
 size_t      g4h_model_weight_bytes(const g4h_model *m);
+
+/* ------------------------------------------------------------ sampler ---- */
+/* The sampling chain of sampler.c (g4run.h:464-489) with its settings, RNG,
+ * ring of recent ids and ban list resident on the device, so a decode step
+ * draws its next token without a host round trip.  Draws are the reference's
+ * bit for bit: the same ids, the same rewritten logits (bans and n-gram hits
+ * at -inf, penalised ids) and the same RNG words, for the same settings,
+ * history and logits.  The ring holds the last 4096 ids (sampler.c:10); the
+ * per-id counts g4_sampler_accept keeps are not kept (g4_sample never reads
+ * them). */
+typedef struct g4h_sampler g4h_sampler;
+typedef struct {                  /* the settings of g4_sampler, g4run.h:465-473 */
+    float temp;                   /* <= 0: greedy (first index of the maximum) */
+    int   top_k;                  /* 1..511, else 512 (sampler.c:147) */
+    float top_p;
+    float repeat_penalty;
+    int   repeat_last_n;
+    float freq_penalty;
+    float presence_penalty;
+    int   no_repeat_ngram;        /* 0/1 off, else the n-gram length */
+    uint64_t seed;                /* seeds the RNG while its state is all zero */
+} g4h_sampler_params;
+/* g4_sampler_init's defaults (sampler.c:5-14): temp 1, top_k 64, top_p 0.95,
+ * repeat_penalty 1, repeat_last_n 128, seed 0xdeadbeef, the rest 0. */
+void g4h_sampler_default_params(g4h_sampler_params *p);
+/* g4_sampler_init (sampler.c:5-14); p NULL: the defaults.  Synchronous. */
+int  g4h_sampler_create(int n_vocab, const g4h_sampler_params *p, g4h_sampler **out);
+/* g4_sampler_free (sampler.c:22-25) */
+int  g4h_sampler_free(g4h_sampler *s);
+/* Assigning g4_sampler's setting fields: the RNG state is kept (as in the
+ * reference, a new seed only matters while the state is all zero). */
+int  g4h_sampler_set_params(g4h_sampler *s, const g4h_sampler_params *p, void *stream);
+/* The xoshiro256+ state words (sampler.c:51-70); all zero re-seeds from seed
+ * on the next draw. */
+int  g4h_sampler_set_rng(g4h_sampler *s, const uint64_t rng[4], void *stream);
+/* g4_sampler_reset (sampler.c:16-20): empties the ring; bans stay. */
+int  g4h_sampler_reset(g4h_sampler *s, void *stream);
+/* g4_sampler_ban (sampler.c:27-35): ids outside [0, n_vocab) and repeats are
+ * ignored. */
+int  g4h_sampler_ban(g4h_sampler *s, int id, void *stream);
+/* g4_sampler_accept (sampler.c:37-48) for n host ids, in order (synchronous). */
+int  g4h_sampler_accept(g4h_sampler *s, const int *ids, int n, void *stream);
+/* g4_sample (sampler.c:74-210) on logits_dev[n_vocab] (device, 16-byte
+ * aligned, rewritten in place as the reference rewrites its argument): the
+ * drawn id goes to *out_dev (device, may be NULL); accept != 0 also pushes it
+ * into the ring, as main.c:265-277 follows each g4_sample with
+ * g4_sampler_accept.  Asynchronous, capturable in a graph. */
+int  g4h_sample(g4h_sampler *s, float *logits_dev, int *out_dev, int accept, void *stream);
+/* Read back (synchronous): the RNG words, the ring oldest first into
+ * recent[4096] (either may be NULL), its length, and how many draws so far
+ * took the exact heap replay of top-k (ties among the k+1 largest logits or a
+ * NaN; the other draws take the sort-based path). */
+int  g4h_sampler_get_state(g4h_sampler *s, uint64_t rng[4], int *recent, int *recent_n, int *slow_draws,
+                           void *stream);
+/* The model's decode steps draw with s (accepting each id) instead of the
+ * greedy argmax; NULL restores the argmax.  s must have the model's n_vocab
+ * and outlive its use. */
+int  g4h_model_set_sampler(g4h_model *m, g4h_sampler *s);
 
 #ifdef __cplusplus
 }

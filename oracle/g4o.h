@@ -162,6 +162,34 @@ void   g4o_model_attn(const g4o_model *m, int il, int pos, float *qkv, float *at
 void   g4o_model_post(const g4o_model *m, int il, float *x, const float *att, void *scratch, int nthreads);
 int    g4o_model_head(const g4o_model *m, const float *x, float *logits, void *scratch, int nthreads);
 
+/* ---- sampling chain (sampler.c), laid out as g4run.h:464-482's g4_sampler
+ *      so one structure drives this restatement and the reference build ---- */
+typedef struct {
+    float temp;                      /* <= 0: greedy */
+    int   top_k;
+    float top_p;
+    float repeat_penalty;
+    int   repeat_last_n;
+    float freq_penalty;
+    float presence_penalty;
+    int   no_repeat_ngram;           /* 0/1 off, else the n-gram length */
+    uint64_t seed;
+    uint64_t rng[4];                 /* all zero: seeded from `seed` on first use */
+    int  *recent;                    /* ring of the last recent_cap accepted ids */
+    int   recent_cap, recent_n, recent_head;
+    int  *cnt;                       /* per-id counts kept by accept */
+    int  *ban_ids;
+    int   n_ban, ban_cap;
+    int   n_vocab;
+} g4o_sampler;
+void     g4o_sampler_init(g4o_sampler *s, int n_vocab);   /* sampler.c:5-14 */
+void     g4o_sampler_reset(g4o_sampler *s);               /* sampler.c:16-20 */
+void     g4o_sampler_free(g4o_sampler *s);                /* sampler.c:22-25 */
+void     g4o_sampler_ban(g4o_sampler *s, int id);         /* sampler.c:27-35 */
+void     g4o_sampler_accept(g4o_sampler *s, int id);      /* sampler.c:37-48 */
+uint64_t g4o_sampler_rng_next(g4o_sampler *s);            /* sampler.c:51-70 */
+int      g4o_sample(g4o_sampler *s, float *logits);       /* sampler.c:74-210 */
+
 /*
  * Pinning (checks that are not a retyping of the function's own formula):
  *   fp16 both ways        exhaustive 65536-code round trip; RNE on ties and
@@ -198,6 +226,14 @@ int    g4o_model_head(const g4o_model *m, const float *x, float *logits, void *s
  *                         dequantized K/V and the q8_0-quantized query that
  *                         rejects an fp16 query or fp16 weights by 10x
  *   gelu table            against math.tanh-based float64 recomputation
+ *   sampler               bit-exact vs the reference's sampler.c built in place
+ *                         with the same IEEE flags (oracle/_ref): drawn ids,
+ *                         rewritten logits and RNG words over seeded runs with
+ *                         bans, n-gram blocks, penalties, ties, NaN and -inf;
+ *                         without that build, by closed forms (greedy = first
+ *                         argmax, top_k = 1, the splitmix/xoshiro words of a
+ *                         published seed, draw frequencies of a two-token
+ *                         softmax)
  */
 
 #ifdef __cplusplus

@@ -402,3 +402,94 @@ class Model:
         logits = np.zeros(self.cfg["n_vocab"], dtype=np.float32)
         tok = lib().g4o_model_decode(C.byref(self._m), token, pos, _ptr(logits), _ptr(self._scratch), nthreads)
         return tok, logits
+
+
+# ------------------------------------------------------------------ sampler
+REF_SAMPLER_PATH = os.path.join(HERE, "_ref", "libg4refsampler.so")
+
+
+class SamplerStruct(C.Structure):
+    """g4_sampler as laid out by g4run.h:464-482 (and g4o_sampler)."""
+    _fields_ = [("temp", C.c_float), ("top_k", C.c_int), ("top_p", C.c_float), ("repeat_penalty", C.c_float),
+                ("repeat_last_n", C.c_int), ("freq_penalty", C.c_float), ("presence_penalty", C.c_float),
+                ("no_repeat_ngram", C.c_int), ("seed", C.c_uint64), ("rng", C.c_uint64 * 4),
+                ("recent", C.POINTER(C.c_int)), ("recent_cap", C.c_int), ("recent_n", C.c_int),
+                ("recent_head", C.c_int), ("cnt", C.POINTER(C.c_int)), ("ban_ids", C.POINTER(C.c_int)),
+                ("n_ban", C.c_int), ("ban_cap", C.c_int), ("n_vocab", C.c_int)]
+
+
+_ref_sampler = None
+
+
+def ref_sampler_available() -> bool:
+    return os.path.exists(REF_SAMPLER_PATH)
+
+
+def _sampler_lib(use_ref: bool):
+    global _ref_sampler
+    if not use_ref:
+        L = lib()
+        names = {"init": L.g4o_sampler_init, "reset": L.g4o_sampler_reset, "free": L.g4o_sampler_free,
+                 "ban": L.g4o_sampler_ban, "accept": L.g4o_sampler_accept, "sample": L.g4o_sample}
+    else:
+        if _ref_sampler is None:
+            _ref_sampler = C.CDLL(REF_SAMPLER_PATH)
+        R = _ref_sampler
+        names = {"init": R.g4_sampler_init, "reset": R.g4_sampler_reset, "free": R.g4_sampler_free,
+                 "ban": R.g4_sampler_ban, "accept": R.g4_sampler_accept, "sample": R.g4_sample}
+    P = C.POINTER(SamplerStruct)
+    names["init"].argtypes = [P, C.c_int]
+    names["reset"].argtypes = [P]
+    names["free"].argtypes = [P]
+    names["ban"].argtypes = [P, C.c_int]
+    names["accept"].argtypes = [P, C.c_int]
+    names["sample"].argtypes = [P, _vp]
+    names["sample"].restype = C.c_int
+    for f in ("init", "reset", "free", "ban", "accept"):
+        names[f].restype = None
+    return names
+
+
+class Sampler:
+    """The sampling chain of sampler.c: the restatement (default) or, with
+    use_ref=True, the reference's sampler.c built in oracle/_ref."""
+    PARAMS = ("temp", "top_k", "top_p", "repeat_penalty", "repeat_last_n", "freq_penalty", "presence_penalty",
+              "no_repeat_ngram", "seed")
+
+    def __init__(self, n_vocab: int, use_ref: bool = False, **params):
+        self._f = _sampler_lib(use_ref)
+        self.s = SamplerStruct()
+        self._f["init"](C.byref(self.s), n_vocab)
+        for k, v in params.items():
+            if k not in self.PARAMS:
+                raise KeyError(k)
+            setattr(self.s, k, v)
+
+    def __del__(self):
+        try:
+            self._f["free"](C.byref(self.s))
+        except Exception:
+            pass
+
+    def ban(self, tok: int) -> None:
+        self._f["ban"](C.byref(self.s), int(tok))
+
+    def accept(self, tok: int) -> None:
+        self._f["accept"](C.byref(self.s), int(tok))
+
+    def reset(self) -> None:
+        self._f["reset"](C.byref(self.s))
+
+    def sample(self, logits: np.ndarray) -> int:
+        """Draw from logits (float32, rewritten in place as the reference does)."""
+        assert logits.dtype == np.float32 and logits.flags["C_CONTIGUOUS"] and logits.size == self.s.n_vocab
+        return int(self._f["sample"](C.byref(self.s), _ptr(logits)))
+
+    @property
+    def rng(self):
+        return [int(self.s.rng[i]) for i in range(4)]
+
+    def recent(self):
+        """The accepted ids in the ring, oldest first."""
+        s = self.s
+        return [s.recent[(s.recent_head + i) % s.recent_cap] for i in range(s.recent_n)]
