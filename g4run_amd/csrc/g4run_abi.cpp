@@ -10,9 +10,11 @@
 #include <cstdlib>
 #include <cstring>
 #include <mutex>
+#include <vector>
 
 #include "../../include/g4hip.h"
 #include "host_fp16.h"
+#include "kernels.h"
 
 using namespace g4;
 
@@ -236,3 +238,111 @@ G4_DOT(q5_K_q8_K, G4H_Q5_K)
 
 extern "C" float g4_dot_f16(const void *w, const g4_fp16 *a, int64_t n) { return dot1(G4H_F16, w, a, n, "g4_dot_f16"); }
 extern "C" float g4_dot_bf16(const void *w, const float *a, int64_t n) { return dot1(G4H_BF16, w, a, n, "g4_dot_bf16"); }
+
+// --------------------------------------------------------------- sampler ----
+// Host bookkeeping of sampler.c:5-48 on the reference's struct; the draw runs
+// on the GPU.
+extern "C" void g4_sampler_init(g4_sampler *s, int n_vocab) {
+    std::memset(s, 0, sizeof *s);
+    s->temp = 1.0f;
+    s->top_k = 64;
+    s->top_p = 0.95f;
+    s->repeat_penalty = 1.0f;
+    s->repeat_last_n = 128;
+    s->n_vocab = n_vocab;
+    s->recent_cap = SAMPLER_RING;
+    s->recent = (int *)std::malloc((size_t)s->recent_cap * sizeof(int));
+    s->cnt = (int *)std::calloc((size_t)(n_vocab > 0 ? n_vocab : 1), sizeof(int));
+    s->seed = 0xdeadbeefull;
+}
+
+extern "C" void g4_sampler_reset(g4_sampler *s) {
+    s->recent_n = 0;
+    s->recent_head = 0;
+    if (s->cnt) std::memset(s->cnt, 0, (size_t)s->n_vocab * sizeof(int));
+}
+
+extern "C" void g4_sampler_free(g4_sampler *s) {
+    std::free(s->recent);
+    std::free(s->cnt);
+    std::free(s->ban_ids);
+    std::memset(s, 0, sizeof *s);
+}
+
+extern "C" void g4_sampler_ban(g4_sampler *s, int id) {
+    if (id < 0 || id >= s->n_vocab) return;
+    for (int i = 0; i < s->n_ban; i++)
+        if (s->ban_ids[i] == id) return;
+    if (s->n_ban == s->ban_cap) {
+        const int cap = s->ban_cap ? 2 * s->ban_cap : 16;
+        int *p = (int *)std::realloc(s->ban_ids, (size_t)cap * sizeof(int));
+        if (!p) return;
+        s->ban_ids = p;
+        s->ban_cap = cap;
+    }
+    s->ban_ids[s->n_ban++] = id;
+}
+
+extern "C" void g4_sampler_accept(g4_sampler *s, int id) {
+    const int cap = s->recent_cap;
+    if (s->recent_n == cap) {
+        const int old = s->recent[s->recent_head];
+        if (s->cnt[old] > 0) s->cnt[old]--;
+        s->recent[s->recent_head] = id;
+        s->recent_head = (s->recent_head + 1) % cap;
+    } else {
+        s->recent[(s->recent_head + s->recent_n) % cap] = id;
+        s->recent_n++;
+    }
+    s->cnt[id]++;
+}
+
+// The device image (settings, RNG words, the ring from its oldest id, bans)
+// and the logits go up in one staged buffer; the kernel draws without
+// accepting (g4_sample does not accept); logits, id and RNG words come back.
+extern "C" int g4_sample(g4_sampler *s, float *logits) {
+    if (s->recent_cap != SAMPLER_RING || s->n_vocab <= 0 || s->recent_n > SAMPLER_RING) {
+        g4h_internal_fail(G4H_ERR_ARG, "g4_sample: the ring must be g4_sampler_init's (4096 ids)");
+        report("g4_sample");
+        return -1;
+    }
+    const int nv = s->n_vocab;
+    const size_t img = al256(sampler_dev_bytes(0) + (size_t)s->n_ban * sizeof(int));
+    const size_t o_l = img, o_o = o_l + al256((size_t)nv * 4);
+    uint8_t *d = stage(o_o + 256);
+    if (!d) {
+        report("g4_sample");
+        return -1;
+    }
+    void *st = tl.stream;
+    std::vector<uint8_t> h(img, 0);
+    SamplerDev *S = reinterpret_cast<SamplerDev *>(h.data());
+    S->temp = s->temp;
+    S->top_k = s->top_k;
+    S->top_p = s->top_p;
+    S->repeat_penalty = s->repeat_penalty;
+    S->repeat_last_n = s->repeat_last_n;
+    S->freq_penalty = s->freq_penalty;
+    S->presence_penalty = s->presence_penalty;
+    S->no_repeat_ngram = s->no_repeat_ngram;
+    S->seed = s->seed;
+    for (int i = 0; i < 4; i++) S->rng[i] = s->rng[i];
+    S->n_vocab = nv;
+    S->recent_n = s->recent_n;
+    S->recent_head = 0;
+    S->n_ban = s->n_ban;
+    for (int i = 0; i < s->recent_n; i++) S->recent[i] = s->recent[(s->recent_head + i) % s->recent_cap];
+    if (s->n_ban) std::memcpy(sampler_bans(S), s->ban_ids, (size_t)s->n_ban * sizeof(int));
+    SamplerDev *dS = reinterpret_cast<SamplerDev *>(d);
+    int id = -1;
+    const bool ok = !g4h_memcpy_h2d(d, h.data(), img, st) && !g4h_memcpy_h2d(d + o_l, logits, (size_t)nv * 4, st) &&
+                    launch_sample(dS, nv, (float *)(d + o_l), (int *)(d + o_o), 0, nullptr, 0, (hipStream_t)st) ==
+                        hipSuccess &&
+                    !g4h_memcpy_d2h(logits, d + o_l, (size_t)nv * 4, st) && !g4h_memcpy_d2h(&id, d + o_o, sizeof id, st) &&
+                    !g4h_memcpy_d2h(s->rng, dS->rng, sizeof s->rng, st);
+    if (!ok) {
+        report("g4_sample");
+        return -1;
+    }
+    return id;
+}

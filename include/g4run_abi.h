@@ -30,6 +30,7 @@
  * HIP error) never exits the process; dots return NaN, dequant writes NaN,
  * quantizers leave the output untouched, and g4h_last_error() (g4hip.h)
  * holds the message.
+ * The sampler entry points (g4run.h:464-489) are exported too; see below.
  * Not exported: the scalar _ref twins and g4_selftest_quants (the
  * reference's own CPU self-test oracle, g4run.h:159-169) and the JIT requant
  * quantizers g4_quantize_q2_K / q3_K (g4run.h:124-125, a load-time
@@ -125,6 +126,41 @@ typedef struct {
     uint64_t    offset;
     const void *data;
 } g4_tensor;
+
+/* g4run.h:464-489: the sampling chain, with the reference's struct.  The
+ * state-keeping calls are host bookkeeping with sampler.c's semantics
+ * (sampler.c:5-48: defaults, the 4096-id ring, per-id counts, deduplicated
+ * bans); g4_sample stages the logits and the state to the device, runs the
+ * chain on the GPU (the kernel of g4h_sample) and copies back the rewritten
+ * logits and the RNG words, so the draw, the logits and s->rng are the
+ * reference's bit for bit.  g4_sample returns -1 (g4h_last_error() says why)
+ * when it cannot run: no device, or a recent_cap other than
+ * g4_sampler_init's 4096. */
+typedef struct {
+    float temp;
+    int   top_k;
+    float top_p;
+    float repeat_penalty;
+    int   repeat_last_n;
+    float freq_penalty;
+    float presence_penalty;
+    int   no_repeat_ngram;
+    uint64_t seed;
+    uint64_t rng[4];
+    int  *recent;
+    int   recent_cap, recent_n, recent_head;
+    int  *cnt;
+    int  *ban_ids;
+    int   n_ban, ban_cap;
+    int   n_vocab;
+} g4_sampler;
+
+void g4_sampler_init(g4_sampler *s, int n_vocab);
+void g4_sampler_reset(g4_sampler *s);
+void g4_sampler_ban(g4_sampler *s, int id);
+void g4_sampler_free(g4_sampler *s);
+void g4_sampler_accept(g4_sampler *s, int id);
+int  g4_sample(g4_sampler *s, float *logits);
 
 #ifdef __cplusplus
 }

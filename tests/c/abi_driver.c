@@ -9,6 +9,9 @@
  *               dots bit for bit
  *   matmul      g4gpu_matmul (tests/c/g4gpu.c, the INTEGRATION.md backend) on
  *               uploaded g4_tensor weights against the oracle's prep_act+matmul
+ *   sampler     g4_sampler_init/ban/accept/free and g4_sample on the reference's
+ *               struct against the oracle's chain: ids, rewritten logits, RNG
+ *               words and ring bookkeeping bit for bit
  * Prints one line per check and exits non-zero on the first failure. */
 #include <math.h>
 #include <stdio.h>
@@ -248,6 +251,53 @@ static void check_matmul(void) {
     }
 }
 
+static void check_sampler(void) {
+    /* the reference's struct and calls against the oracle's restatement */
+    const int nv = 32768;
+    float *lg = malloc(nv * 4), *l1 = malloc(nv * 4), *l2 = malloc(nv * 4);
+    for (int cfg = 0; cfg < 4; cfg++) {
+        g4_sampler a;
+        g4o_sampler b;
+        g4_sampler_init(&a, nv);
+        g4o_sampler_init(&b, nv);
+        const float temps[4] = {0.8f, 0.0f, 1.3f, 1.0f};
+        a.temp = b.temp = temps[cfg];
+        a.top_k = b.top_k = cfg == 2 ? 600 : 40;
+        a.repeat_penalty = b.repeat_penalty = 1.1f;
+        a.freq_penalty = b.freq_penalty = cfg == 3 ? 0.2f : 0.0f;
+        a.no_repeat_ngram = b.no_repeat_ngram = cfg == 1 ? 0 : 3;
+        a.seed = b.seed = 1000 + (uint64_t)cfg;
+        g4_sampler_ban(&a, 5);
+        g4o_sampler_ban(&b, 5);
+        for (int i = 0; i < 300; i++) {
+            const int t = (int)(rand() % 40);
+            g4_sampler_accept(&a, t);
+            g4o_sampler_accept(&b, t);
+        }
+        for (int step = 0; step < 8; step++) {
+            for (int i = 0; i < nv; i++) lg[i] = gauss() * 3.0f;
+            if (cfg == 3)
+                for (int i = 0; i < nv; i++) lg[i] = roundf(lg[i]);   /* ties: the exact heap replay */
+            memcpy(l1, lg, nv * 4);
+            memcpy(l2, lg, nv * 4);
+            const int t1 = g4_sample(&a, l1), t2 = g4o_sample(&b, l2);
+            CHECK(t1 == t2, "g4_sample cfg %d step %d: %d vs oracle %d", cfg, step, t1, t2);
+            CHECK(!memcmp(l1, l2, nv * 4), "g4_sample cfg %d step %d: rewritten logits", cfg, step);
+            CHECK(!memcmp(a.rng, b.rng, sizeof a.rng), "g4_sample cfg %d step %d: rng words", cfg, step);
+            g4_sampler_accept(&a, t1);
+            g4o_sampler_accept(&b, t2);
+        }
+        int same = a.recent_n == b.recent_n && a.recent_head == b.recent_head && !memcmp(a.cnt, b.cnt, sizeof(int) * (size_t)nv);
+        for (int i = 0; same && i < a.recent_n; i++)      /* the filled part of the ring (malloc'd, not zeroed) */
+            same = a.recent[(a.recent_head + i) % a.recent_cap] == b.recent[(b.recent_head + i) % b.recent_cap];
+        CHECK(same, "g4_sampler bookkeeping cfg %d", cfg);
+        g4_sampler_free(&a);
+        g4o_sampler_free(&b);
+    }
+    free(lg); free(l1); free(l2);
+    printf("ok g4_sampler_* / g4_sample (n_vocab %d, 4 settings, ties)\n", nv);
+}
+
 int main(void) {
     setvbuf(stdout, NULL, _IOLBF, 0);
     check_tables();
@@ -256,6 +306,7 @@ int main(void) {
     check_dequant_and_dots();
     check_float_dots();
     check_matmul();
+    check_sampler();
     printf("PASS (%d failures)\n", failures);
     return 0;
 }
