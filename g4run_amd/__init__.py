@@ -117,6 +117,9 @@ _SIGS = [
     ("g4h_sampler_get_state", _int, [_vp, C.POINTER(C.c_uint64), C.POINTER(_int), C.POINTER(_int), C.POINTER(_int),
                                      _vp]),
     ("g4h_model_set_sampler", _int, [_vp, _vp]),
+    ("g4h_forward_batch", _int, [_vp, C.POINTER(_int), _int, _int, _int, _vp]),
+    ("g4h_forward_batch_heads", _int, [_vp, C.POINTER(_int), _int, _int, _vp, _vp, _vp]),
+    ("g4h_argmax_rows", _int, [_vp, _int, _int, _vp, _vp]),
 ]
 
 _lib = None
@@ -440,6 +443,11 @@ class _View:
         return b.download(np.uint8, (self.nrows, rs))
 
 
+def argmax_rows(logits, n: int, nb: int, out, stream=None) -> None:
+    """out[b] = first index of the maximum of device row b of logits [nb][n]."""
+    check(lib().g4h_argmax_rows(_p(logits), n, nb, _p(out), stream))
+
+
 class SamplerParams(C.Structure):
     """g4h_sampler_params: the settings of g4_sampler (g4run.h:465-473)."""
     _fields_ = [("temp", C.c_float), ("top_k", _int), ("top_p", C.c_float), ("repeat_penalty", C.c_float),
@@ -539,6 +547,24 @@ class Model:
         t, p = _int(), _int()
         check(lib().g4h_model_get_state(self.ptr, C.byref(t), C.byref(p), stream))
         return t.value, p.value
+
+    def forward_batch(self, tokens, pos0: int, want_logits: bool = True, stream=None):
+        """g4_forward_batch: layers for the tokens at pos0.., the last token's
+        logits (host copy) if want_logits."""
+        t = np.ascontiguousarray(tokens, dtype=np.int32)
+        check(lib().g4h_forward_batch(self.ptr, t.ctypes.data_as(C.POINTER(_int)), t.size, pos0, int(want_logits), stream))
+        return self.logits() if want_logits else None
+
+    def forward_batch_heads(self, tokens, pos0: int, logits=None, hnext=None, stream=None):
+        """g4_forward_batch_heads into device buffers (allocated if not given);
+        returns (logits Buffer [nb][n_vocab], hnext Buffer [nb][n_embd])."""
+        t = np.ascontiguousarray(tokens, dtype=np.int32)
+        nb = t.size
+        logits = logits if logits is not None else Buffer(nb * self.cfg["n_vocab"] * 4)
+        hnext = hnext if hnext is not None else Buffer(nb * self.cfg["n_embd"] * 4)
+        check(lib().g4h_forward_batch_heads(self.ptr, t.ctypes.data_as(C.POINTER(_int)), nb, pos0, _p(logits), _p(hnext),
+                                            stream))
+        return logits, hnext
 
     def set_sampler(self, sampler) -> None:
         """Draw each step's token with a Sampler (accepting it), or greedily with None."""

@@ -114,14 +114,13 @@ hipError_t launch_gemv_p_q4_0(const g4h_tensor &, const uint8_t *, float *, cons
 
 // Persistent family: the one-shot kernel's LPR/UPL (identical results), a
 // single pass over each row (units <= LPR*UPL), prologue inputs <= 16384 wide.
-// The GELU epilogue pairs rows inside a wave, so it caps LPR at 32.
+// The GELU epilogue pairs rows inside a wave, so it takes only shapes whose
+// one-shot LPR is at most 32: any other LPR would sum each row in another
+// order than the one-shot kernel (e.g. q8_0 rows of 2560, LPR 64), and the
+// decode step runs GELU as its own step there.
 static bool gemv_p_shape(const g4h_tensor &W, const GemvEpi &epi, int *lpr, int *upl) {
     gemv_shape(W.type, W.nb, lpr, upl);
-    if (epi.kind == EPI_GELU && *lpr > 32) {
-        *lpr = 32;
-        const int per = (int)((W.nb + 31) / 32);
-        *upl = per <= 2 ? 2 : per <= 4 ? 4 : 8;
-    }
+    if (epi.kind == EPI_GELU && *lpr > 32) return false;
     return W.nb <= (int64_t)(*lpr) * (*upl);
 }
 

@@ -31,35 +31,44 @@ __global__ __launch_bounds__(256) void k_rand_normal(float *y, int64_t n, uint64
 // read from the resident planes (qs [row][blk][32], d fp16); then
 // act = q8_0(rms(x)*w_pre), the first layer's attention-norm activation
 // (skipped without w_pre, when that norm runs in the Wqkv GEMV).  512 threads,
-// n <= 8192.
+// n <= 8192; workgroup b takes token[b] into x + b*n and act + b*ast.
 __global__ __launch_bounds__(512) void k_embed_norm(const int8_t *qs, const uint16_t *sc, int64_t nb, const int *token,
-                                                    float *x, int n, float es, const float *w_pre, float eps, uint8_t *act) {
-    const int64_t r = *token;
+                                                    float *x, int n, float es, const float *w_pre, float eps, uint8_t *act,
+                                                    size_t ast) {
+    const int b = blockIdx.x;
+    const int64_t r = token[b];
+    x += (size_t)b * n;
     for (int i = threadIdx.x; i < n; i += blockDim.x) {
         const int64_t j = r * nb + (i >> 5);
         const float v = (float)qs[j * 32 + (i & 31)] * h2f(sc[j]);
         x[i] = v * es;
     }
     __syncthreads();
-    if (w_pre) wg_norm_quant<4>(x, nullptr, nullptr, w_pre, eps, n, act);
+    if (w_pre) wg_norm_quant<4>(x, nullptr, nullptr, w_pre, eps, n, act + (size_t)b * ast);
 }
 
 // ------------------------------------------------------ norm + quantize --
-// One workgroup of 512 threads (n <= 8192, n % 32 == 0): if delta,
-// x += rms(delta)*w_post (the post-norm residual, model.c:711-716 / 731-736);
-// then act = q8_0(rms(x)*w_pre), the next projection's activation
-// (model.c:657-661 / 721-722).
+// One workgroup of 512 threads per token row b (n <= 8192, n % 32 == 0): if
+// delta, x += rms(delta)*w_post (the post-norm residual, model.c:711-716 /
+// 731-736); then act = q8_0(rms(x)*w_pre), the next projection's activation
+// (model.c:657-661 / 721-722), and y = rms(x)*w_pre in fp32 if y is given
+// (the head's input feature, model.c:791-793).  Rows at n floats; act rows at
+// ast bytes.
 __global__ __launch_bounds__(512) void k_norm_quant(float *x, const float *delta, const float *w_post, const float *w_pre,
-                                                    float eps, int n, uint8_t *act) {
-    wg_norm_quant<4>(x, delta, w_post, w_pre, eps, n, act);
+                                                    float eps, int n, uint8_t *act, size_t ast, float *y) {
+    const size_t b = blockIdx.x;
+    wg_norm_quant<4>(x + b * n, delta ? delta + b * n : nullptr, w_post, w_pre, eps, n, act + b * ast, y ? y + b * n : nullptr);
 }
 
 // -------------------------------------------------------- gelu * up --
 // h = gelu(g) * u with the fp16 GELU table (model.c:725-729), quantized to
 // q8_0 for the down projection; gu holds the (gate, up) pairs interleaved,
-// as the Wgu rows are stored.  256 threads, 4 elements each.
-__global__ __launch_bounds__(256) void k_gelu_quant(const float *gu, int n_ff, const uint16_t *tab, uint8_t *act) {
+// as the Wgu rows are stored.  256 threads, 4 elements each; grid.y token
+// rows (gu rows of 2 n_ff floats, act rows at ast bytes).
+__global__ __launch_bounds__(256) void k_gelu_quant(const float *gu, int n_ff, const uint16_t *tab, uint8_t *act, size_t ast) {
     const int gi = blockIdx.x * 256 + threadIdx.x;
+    gu += (size_t)blockIdx.y * 2 * n_ff;             // token row blockIdx.y
+    act += (size_t)blockIdx.y * ast;
     const bool own = 4 * gi < n_ff;
     float g[4] = {0.f, 0.f, 0.f, 0.f}, u[4] = {0.f, 0.f, 0.f, 0.f}, h[4];
     if (own) {
@@ -90,27 +99,41 @@ __global__ __launch_bounds__(1024) void k_argmax_advance(const float *logits, in
     if (threadIdx.x == 0) state_advance(state, id, n_ctx);
 }
 
+// out[b] = the first index of the maximum of row b (main.c:348-349's ARGMAX
+// over each verified position); one workgroup per row of n floats.
+__global__ __launch_bounds__(1024) void k_argmax_rows(const float *logits, int n, int *out) {
+    __shared__ float bv[16];
+    __shared__ int bi[16];
+    const int id = wg_first_argmax(logits + (size_t)blockIdx.x * n, n, bv, bi);
+    if (threadIdx.x == 0) out[blockIdx.x] = id;
+}
+
 // ------------------------------------------------------------ launchers --
 hipError_t launch_rand_normal(float *y, int64_t n, uint64_t seed, float mean, float std, hipStream_t s) {
     hipLaunchKernelGGL(k_rand_normal, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, y, n, seed, mean, std);
     return hipGetLastError();
 }
 hipError_t launch_embed_norm(const g4h_tensor &head, const int *token, float *x, float es, const float *w_pre, float eps,
-                             uint8_t *act, hipStream_t s) {
-    if (head.type != Q8_0 || head.ncols % 32 || head.ncols > 8192) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_embed_norm, dim3(1), dim3(512), 0, s, (const int8_t *)head.qs, (const uint16_t *)head.sc, head.nb,
-                       token, x, (int)head.ncols, es, w_pre, eps, act);
+                             uint8_t *act, hipStream_t s, int nb, size_t ast) {
+    if (head.type != Q8_0 || head.ncols % 32 || head.ncols > 8192 || nb < 1) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_embed_norm, dim3(nb), dim3(512), 0, s, (const int8_t *)head.qs, (const uint16_t *)head.sc, head.nb,
+                       token, x, (int)head.ncols, es, w_pre, eps, act, ast);
     return hipGetLastError();
 }
 hipError_t launch_norm_quant(float *x, const float *delta, const float *w_post, const float *w_pre, float eps, int n,
-                             uint8_t *act, hipStream_t s) {
-    if (n % 32 || n > 8192) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_norm_quant, dim3(1), dim3(512), 0, s, x, delta, w_post, w_pre, eps, n, act);
+                             uint8_t *act, hipStream_t s, int nb, size_t ast, float *y) {
+    if (n % 32 || n > 8192 || nb < 1) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_norm_quant, dim3(nb), dim3(512), 0, s, x, delta, w_post, w_pre, eps, n, act, ast, y);
     return hipGetLastError();
 }
-hipError_t launch_gelu_quant(const float *gu, int n_ff, const uint16_t *tab, uint8_t *act, hipStream_t s) {
-    if (n_ff % 32) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_gelu_quant, dim3((n_ff / 4 + 255) / 256), dim3(256), 0, s, gu, n_ff, tab, act);
+hipError_t launch_gelu_quant(const float *gu, int n_ff, const uint16_t *tab, uint8_t *act, hipStream_t s, int nb, size_t ast) {
+    if (n_ff % 32 || nb < 1) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_gelu_quant, dim3((n_ff / 4 + 255) / 256, nb), dim3(256), 0, s, gu, n_ff, tab, act, ast);
+    return hipGetLastError();
+}
+hipError_t launch_argmax_rows(const float *logits, int n, int nb, int *out, hipStream_t s) {
+    if (n < 1 || nb < 1 || ((uintptr_t)logits & 15) || (nb > 1 && n % 4)) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_argmax_rows, dim3(nb), dim3(1024), 0, s, logits, n, out);
     return hipGetLastError();
 }
 hipError_t launch_argmax_advance(const float *logits, int n, int *state, int n_ctx, hipStream_t s) {

@@ -81,11 +81,17 @@ struct QkvArgs {
     float eps = 0.0f;
 };
 hipError_t launch_rand_normal(float *y, int64_t n, uint64_t seed, float mean, float std, hipStream_t s);
+// The row forms (nb tokens): x / delta / y rows of n floats, gu rows of 2 n_ff
+// floats, act rows at ast bytes; token[b] feeds row b.
 hipError_t launch_embed_norm(const g4h_tensor &head, const int *token, float *x, float es, const float *w_pre, float eps,
-                             uint8_t *act, hipStream_t s);
+                             uint8_t *act, hipStream_t s, int nb = 1, size_t ast = 0);
 hipError_t launch_norm_quant(float *x, const float *delta, const float *w_post, const float *w_pre, float eps, int n,
-                             uint8_t *act, hipStream_t s);
-hipError_t launch_gelu_quant(const float *gu, int n_ff, const uint16_t *tab, uint8_t *act, hipStream_t s);
+                             uint8_t *act, hipStream_t s, int nb = 1, size_t ast = 0, float *y = nullptr);
+hipError_t launch_gelu_quant(const float *gu, int n_ff, const uint16_t *tab, uint8_t *act, hipStream_t s, int nb = 1,
+                             size_t ast = 0);
+// out[b] = first index of the maximum of row b of logits [nb][n] (16-byte
+// aligned rows)
+hipError_t launch_argmax_rows(const float *logits, int n, int nb, int *out, hipStream_t s);
 // state: token, pos, npos = pos + 1, steps taken, flags.  Advances pos unless
 // pos + 1 == n_ctx: then pos stays and flags |= STATE_CTX_FULL (no later step can
 // index past the cache).

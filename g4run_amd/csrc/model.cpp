@@ -55,7 +55,14 @@ struct g4h_model {
     int fuse = 0;                    // FUSE_* steps folded into the GEMVs
     float *trace = nullptr;          // optional per-layer x | qkv | att rows, then the final x (g4h_model_trace)
     g4h_sampler *sampler = nullptr;  // draws the next token (g4h_model_set_sampler); null: greedy argmax
+    // rows of the batched forward (g4h_forward_batch*), for up to kBatchMax
+    // tokens, allocated by its first call; bws is its own attention workspace
+    float *bx = nullptr, *bxb = nullptr, *bqkv = nullptr, *batt = nullptr, *bff = nullptr, *bhn = nullptr;
+    uint8_t *bact = nullptr, *bws = nullptr;
+    int *btok = nullptr;
 };
+
+static constexpr int kBatchMax = 64;   // G4_BATCH_MAX, g4run.h:23
 
 // Steps of the chain folded into the persistent GEMV family (gemv_p.h) or
 // into the attention launch:
@@ -298,6 +305,16 @@ extern "C" int g4h_forward_state(g4h_model *m, void *stream) {
         return e;
     };
     const bool qkv_pro = fz & (FUSE_QKV | FUSE_QATT);     // the attention norm runs in a projection prologue
+    // whether W takes the GELU epilogue (the persistent family sums its rows in
+    // the one-shot kernel's order only where its LPR allows row pairs in a wave)
+    auto gelu_fits = [&](const g4h_tensor &W) {
+        GemvPro p;
+        p.kind = PRO_NORM;
+        p.n = (int)W.ncols;
+        GemvEpi e;
+        e.kind = EPI_GELU;
+        return gemv_p_fits(W, p, e);
+    };
     M_HIP(launch_embed_norm(*m->head, token, x, sqrtf((float)E), qkv_pro ? nullptr : norm_of(m, 0, G4H_N_ATTN),
                             c.rms_eps, m->act, s));
     for (int l = 0; l < c.n_layer; l++) {
@@ -343,7 +360,13 @@ extern "C" int g4h_forward_state(g4h_model *m, void *stream) {
         M_RC(trace_copy(tr, TR_ATT, m->att, H * hd));
         M_HIP(launch_gemv(*m->wo[l], m->act, ast, m->xb, 1, s));
         M_RC(trace_copy(tr, TR_WO, m->xb, E));
-        if (fz & FUSE_GU) {
+        if ((fz & FUSE_GU) && !gelu_fits(*m->wgu[l])) {
+            // the residual norm in the Wgu prologue, GELU * up as its own step
+            M_HIP(norm_gemv(*m->wgu[l], m->xb, norm_of(m, l, G4H_N_POST_ATTN), norm_of(m, l, G4H_N_FFN), m->ff, false));
+            M_RC(trace_copy(tr, TR_XMID, x, E));
+            M_HIP(launch_gelu_quant(m->ff, F, m->gelu, m->act, s));
+            M_HIP(launch_gemv(*m->wdown[l], m->act, ast, m->xb, 1, s));
+        } else if (fz & FUSE_GU) {
             M_HIP(norm_gemv(*m->wgu[l], m->xb, norm_of(m, l, G4H_N_POST_ATTN), norm_of(m, l, G4H_N_FFN), nullptr, true));
             M_RC(trace_copy(tr, TR_XMID, x, E));
             M_RC(trace_copy(tr, TR_H, m->ff, F));
@@ -388,6 +411,114 @@ extern "C" int g4h_model_set_sampler(g4h_model *m, g4h_sampler *s) {
     if (s && sampler_n_vocab(s) != m->c.n_vocab)
         return g4h_internal_fail(G4H_ERR_SHAPE, "g4h_model_set_sampler: the sampler's n_vocab differs from the model's");
     m->sampler = s;
+    return G4H_OK;
+}
+
+// ------------------------------------------------------- batched forward ----
+static int batch_alloc(g4h_model *m) {
+    if (m->bx) return G4H_OK;
+    const g4h_model_config &c = m->c;
+    const size_t E = c.n_embd, R = (size_t)(c.n_head + 2 * c.n_kv) * c.head_dim, Q = (size_t)c.n_head * c.head_dim,
+                 F = c.n_ff, B = kBatchMax;
+    M_RC(model_alloc(m, (void **)&m->bx, B * E * 4));
+    M_RC(model_alloc(m, (void **)&m->bxb, B * E * 4));
+    M_RC(model_alloc(m, (void **)&m->bhn, B * E * 4));
+    M_RC(model_alloc(m, (void **)&m->bqkv, B * R * 4));
+    M_RC(model_alloc(m, (void **)&m->batt, B * Q * 4));
+    M_RC(model_alloc(m, (void **)&m->bff, B * 2 * F * 4));
+    M_RC(model_alloc(m, (void **)&m->bact, B * m->act_bytes));
+    M_RC(model_alloc(m, (void **)&m->bws, m->ws_bytes));
+    M_RC(model_alloc(m, (void **)&m->btok, B * sizeof(int)));
+    M_HIP(hipMemset(m->bws, 0, m->ws_bytes));
+    return G4H_OK;
+}
+
+// forward_layers (model.c:592-736) for nb tokens at positions pos0 .. pos0+nb-1:
+// every row takes exactly the arithmetic of the decode step (the GEMV family
+// for every projection, whose token rows are bit-identical for any token
+// count; the decode attention per token with its q/k/v preparation, K/V rows
+// stored at pos0 + b before token b attends 0 .. pos0 + b), so row b equals
+// the decode step of tokens[b] at pos0 + b after tokens[0 .. b-1] bit for
+// bit.  Leaves the residual rows in bx and the last Wdown output in bxb.
+static int forward_rows(g4h_model *m, const int *tokens, int nb, int pos0, hipStream_t s) {
+    const g4h_model_config &c = m->c;
+    if (nb < 1 || nb > kBatchMax) return g4h_internal_fail(G4H_ERR_ARG, "g4h_forward_batch: nb must be 1..64 (G4_BATCH_MAX)");
+    if (pos0 < 0 || pos0 + nb > c.n_ctx) return g4h_internal_fail(G4H_ERR_ARG, "g4h_forward_batch: positions outside the context");
+    if (!tokens) return g4h_internal_fail(G4H_ERR_ARG, "g4h_forward_batch: null tokens");
+    for (int b = 0; b < nb; b++)
+        if (tokens[b] < 0 || tokens[b] >= c.n_vocab) return g4h_internal_fail(G4H_ERR_ARG, "g4h_forward_batch: token out of range");
+    M_RC(batch_alloc(m));
+    const int E = c.n_embd, H = c.n_head, KV = c.n_kv, hd = c.head_dim, F = c.n_ff;
+    const int R = (H + 2 * KV) * hd, Q = H * hd;
+    const size_t ast = m->act_bytes;
+    M_HIP(hipMemcpyAsync(m->btok, tokens, (size_t)nb * sizeof(int), hipMemcpyHostToDevice, s));
+    M_HIP(launch_embed_norm(*m->head, m->btok, m->bx, sqrtf((float)E), norm_of(m, 0, G4H_N_ATTN), c.rms_eps, m->bact, s, nb, ast));
+    for (int l = 0; l < c.n_layer; l++) {
+        if (l)
+            M_HIP(launch_norm_quant(m->bx, m->bxb, norm_of(m, l - 1, G4H_N_POST_FFW), norm_of(m, l, G4H_N_ATTN), c.rms_eps, E,
+                                    m->bact, s, nb, ast));
+        M_RC(g4h_matmul_ex(m->wqkv[l], nullptr, m->bact, ast, m->bqkv, nb, 1, s));
+        QkvArgs qa;
+        qa.n_head = H;
+        qa.n_kv = KV;
+        qa.hd = hd;
+        qa.kv_type = c.kv_type;
+        qa.q_norm = norm_of(m, l, G4H_N_Q);
+        qa.k_norm = norm_of(m, l, G4H_N_K);
+        qa.rope = m->rope;
+        qa.kc = m->kv + (size_t)(2 * l) * m->kv_layer_bytes;
+        qa.vc = qa.kc + m->kv_layer_bytes;
+        qa.eps = c.rms_eps;
+        for (int b = 0; b < nb; b++)
+            M_HIP(launch_attn_decode(nullptr, m->bqkv + (size_t)b * R, qa, pos0 + b + 1, nullptr, c.n_ctx, m->batt + (size_t)b * Q,
+                                     m->bact + (size_t)b * ast, m->bws, s));
+        M_RC(g4h_matmul_ex(m->wo[l], nullptr, m->bact, ast, m->bxb, nb, 1, s));
+        M_HIP(launch_norm_quant(m->bx, m->bxb, norm_of(m, l, G4H_N_POST_ATTN), norm_of(m, l, G4H_N_FFN), c.rms_eps, E, m->bact,
+                                s, nb, ast));
+        M_RC(g4h_matmul_ex(m->wgu[l], nullptr, m->bact, ast, m->bff, nb, 1, s));
+        M_HIP(launch_gelu_quant(m->bff, F, m->gelu, m->bact, s, nb, ast));
+        M_RC(g4h_matmul_ex(m->wdown[l], nullptr, m->bact, ast, m->bxb, nb, 1, s));
+    }
+    return G4H_OK;
+}
+
+extern "C" int g4h_forward_batch(g4h_model *m, const int *tokens, int nb, int pos0, int want_logits, void *stream) {
+    if (!m) return g4h_internal_fail(G4H_ERR_ARG, "g4h_forward_batch: null model");
+    const hipStream_t s = (hipStream_t)stream;
+    const g4h_model_config &c = m->c;
+    M_RC(forward_rows(m, tokens, nb, pos0, s));
+    if (want_logits) {
+        // head of the last token only (model.c:760-769)
+        const size_t E = c.n_embd, last = (size_t)(nb - 1) * E;
+        M_HIP(launch_norm_quant(m->bx + last, m->bxb + last, norm_of(m, c.n_layer - 1, G4H_N_POST_FFW), norm_of(m, c.n_layer, 0),
+                                c.rms_eps, c.n_embd, m->bact, s));
+        M_RC(g4h_matmul_ex(m->head, nullptr, m->bact, m->act_bytes, m->logits, 1, 1, s));
+    }
+    M_HIP(hipStreamSynchronize(s));
+    return G4H_OK;
+}
+
+extern "C" int g4h_forward_batch_heads(g4h_model *m, const int *tokens, int nb, int pos0, float *logits_dev, float *hnext_dev,
+                                       void *stream) {
+    if (!m || !logits_dev) return g4h_internal_fail(G4H_ERR_ARG, "g4h_forward_batch_heads: null argument");
+    if ((uintptr_t)logits_dev % 16 || (hnext_dev && (uintptr_t)hnext_dev % 16))
+        return g4h_internal_fail(G4H_ERR_ARG, "g4h_forward_batch_heads: outputs must be 16-byte aligned");
+    const hipStream_t s = (hipStream_t)stream;
+    const g4h_model_config &c = m->c;
+    M_RC(forward_rows(m, tokens, nb, pos0, s));
+    // every position's head input feature and logits (model.c:790-793)
+    M_HIP(launch_norm_quant(m->bx, m->bxb, norm_of(m, c.n_layer - 1, G4H_N_POST_FFW), norm_of(m, c.n_layer, 0), c.rms_eps,
+                            c.n_embd, m->bact, s, nb, m->act_bytes, hnext_dev ? hnext_dev : m->bhn));
+    M_RC(g4h_matmul_ex(m->head, nullptr, m->bact, m->act_bytes, logits_dev, nb, 1, s));
+    M_HIP(hipStreamSynchronize(s));
+    return G4H_OK;
+}
+
+extern "C" int g4h_argmax_rows(const float *logits_dev, int n, int nb, int *out_dev, void *stream) {
+    if (!logits_dev || !out_dev || n < 1 || nb < 1) return g4h_internal_fail(G4H_ERR_ARG, "g4h_argmax_rows: bad argument");
+    if ((uintptr_t)logits_dev % 16 || (nb > 1 && n % 4))
+        return g4h_internal_fail(G4H_ERR_ARG, "g4h_argmax_rows: rows must be 16-byte aligned");
+    M_HIP(launch_argmax_rows(logits_dev, n, nb, out_dev, (hipStream_t)stream));
     return G4H_OK;
 }
 

@@ -93,11 +93,12 @@ __device__ __forceinline__ void q4_store4(const float v[4], int gi, bool own, ui
 __device__ __forceinline__ float4 ldf4(const float *p) { return *(const float4 *)p; }
 __device__ __forceinline__ void f4(const float4 a, float o[4]) { o[0] = a.x; o[1] = a.y; o[2] = a.z; o[3] = a.w; }
 
-// If delta: x <- x + rms(delta)*w_post (stored back).  Then act <- q8_0(rms(x)*w_pre).
+// If delta: x <- x + rms(delta)*w_post (stored back).  Then act <- q8_0(rms(x)*w_pre),
+// and y (if given) <- rms(x)*w_pre in fp32.
 // n % 32 == 0 and n/4 <= S * blockDim.x; all threads of the workgroup call it.
 template <int S>
 __device__ void wg_norm_quant(float *x, const float *delta, const float *w_post, const float *w_pre, float eps, int n,
-                              uint8_t *act) {
+                              uint8_t *act, float *y = nullptr) {
     __shared__ double red[16];
     const int ng = n >> 2, bd = blockDim.x, t = threadIdx.x;
     float v[S][4], d[S][4], wp[S][4], wq[S][4];
@@ -139,6 +140,7 @@ __device__ void wg_norm_quant(float *x, const float *delta, const float *w_post,
         float o[4];
 #pragma unroll
         for (int k = 0; k < 4; k++) o[k] = v[s][k] * sc * wq[s][k];
+        if (y && gi < ng) *(float4 *)(y + 4 * gi) = make_float4(o[0], o[1], o[2], o[3]);
         q8_store4(o, gi, gi < ng, act);
     }
 }

@@ -289,6 +289,26 @@ float      *g4h_model_norm(g4h_model *m, int layer, int which);
 int         g4h_model_kv(g4h_model *m, int layer, void **k_dev, void **v_dev, size_t *bytes);
 size_t      g4h_model_weight_bytes(const g4h_model *m);
 
+/* ---------------------------------------------------- batched forward ---- */
+/* g4_forward_batch (g4run.h:312-313, model.c:758-776): the layers for nb
+ * tokens (host ids, 1 <= nb <= 64 = G4_BATCH_MAX) at positions pos0 ..
+ * pos0+nb-1 (< n_ctx), their K/V rows stored; with want_logits the last
+ * token's logits go to g4h_model_logits.  Synchronous.  Row b is computed
+ * with exactly the decode step's arithmetic, so the logits equal those of
+ * decoding tokens[0..nb-1] one by one, bit for bit.  The decode state
+ * (g4h_model_set_state) is not touched. */
+int g4h_forward_batch(g4h_model *m, const int *tokens, int nb, int pos0, int want_logits, void *stream);
+/* g4_forward_batch_heads (model.c:780-799), the speculative-decoding verify
+ * batch (main.c:383-397): the same layers, then every position's head:
+ * logits_dev [nb][n_vocab] and, if hnext_dev, the head's input feature
+ * rms(x)*output_norm [nb][n_embd] (device, 16-byte aligned).  Synchronous. */
+int g4h_forward_batch_heads(g4h_model *m, const int *tokens, int nb, int pos0, float *logits_dev, float *hnext_dev,
+                            void *stream);
+/* The greedy choice of every row (main.c:348-349's ARGMAX): out_dev[b] = the
+ * first index of the maximum of logits_dev[b][0..n) (rows 16-byte aligned,
+ * n % 4 == 0 when nb > 1).  Asynchronous. */
+int g4h_argmax_rows(const float *logits_dev, int n, int nb, int *out_dev, void *stream);
+
 /* ------------------------------------------------------------ sampler ---- */
 /* The sampling chain of sampler.c (g4run.h:464-489) with its settings, RNG,
  * ring of recent ids and ban list resident on the device, so a decode step

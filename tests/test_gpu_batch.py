@@ -1,0 +1,106 @@
+"""The batched forward (g4h_forward_batch, g4h_forward_batch_heads: the GPU
+form of forward_layers for nb tokens, model.c:592-799) and the verify step of
+speculative decoding built on it (main.c:383-404).
+
+Bar: bit-exact.  Row b of the batch uses the decode step's arithmetic, so its
+logits must equal those of decoding tokens[0..b] one at a time; the verify
+step must accept exactly the drafted prefix the greedy decode agrees with and
+return the greedy token after it.  The decode step itself is checked against
+the CPU oracle in test_gpu_model.py; here the batch's head input feature is
+also checked against the oracle's rms_norm of the decode step's final x.
+"""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+SMALL = dict(n_layer=2, n_embd=256, n_head=4, n_kv=2, head_dim=64, n_ff=512, n_vocab=512, n_ctx=64,
+             rope_base=1e6, rms_eps=1e-6)
+MID = dict(n_layer=2, n_embd=2560, n_head=8, n_kv=4, head_dim=256, n_ff=10240, n_vocab=4096, n_ctx=1024,
+           rope_base=1e6, rms_eps=1e-6)
+
+
+def make_model(G, cfg, kv_type, wtype, seed=7):
+    m = G.Model(seed=seed, kv_type=kv_type, wtype=wtype, **cfg)
+    m.fill_kv(seed + 1)
+    return m
+
+
+@pytest.mark.parametrize("cfg,kv_type,wtype,nb,pos0", [
+    (SMALL, 1, 2, 1, 20), (SMALL, 1, 2, 5, 20), (SMALL, 8, 2, 13, 40), (SMALL, 2, 8, 8, 3),
+    (MID, 1, 2, 4, 900), (MID, 8, 2, 9, 1000), (MID, 1, 8, 24, 600)],
+    ids=["small-f16-nb1", "small-f16-nb5", "small-q8kv-nb13", "small-q4kv-q8w-nb8", "mid-f16-nb4", "mid-q8kv-nb9",
+         "mid-f16-q8w-nb24"])
+def test_batch_rows_equal_decode_steps(gpu, oracle, cfg, kv_type, wtype, nb, pos0):
+    G = gpu
+    m = make_model(G, cfg, kv_type, wtype)
+    V, E = cfg["n_vocab"], cfg["n_embd"]
+    rs = np.random.default_rng(nb * 31 + pos0)
+    tokens = rs.integers(0, V, nb).astype(np.int32)
+    print(f"batch of {nb} at pos {pos0} ({cfg['n_embd']}d, kv {kv_type}, w {wtype})", flush=True)
+    L, H = m.forward_batch_heads(tokens, pos0)
+    G.synchronize()
+    bl = L.download(np.float32, (nb, V))
+    hn = H.download(np.float32, (nb, E))
+    am = G.Buffer(4 * nb)
+    G.argmax_rows(L, V, nb, am)
+    G.synchronize()
+    assert list(am.download(np.int32, nb)) == [int(np.argmax(r)) for r in bl]
+    # the same tokens decoded one by one (the batch's K/V rows are rewritten
+    # with the same values); the trace gives each step's final x
+    trace = G.Buffer(m.trace_floats() * 4)
+    m.trace(trace)
+    out_norm = m.norm(0, "output_norm")
+    fields, rec = m.trace_fields()
+    try:
+        for b in range(nb):
+            m.forward(int(tokens[b]), pos0 + b)
+            lg = m.logits()
+            assert lg.tobytes() == bl[b].tobytes(), f"row {b}: batch logits differ from the decode step"
+            xf = trace.download(np.float32, E, offset=cfg["n_layer"] * rec * 4)
+            ref = oracle.rms_norm(xf, out_norm, cfg["rms_eps"])
+            np.testing.assert_allclose(hn[b], ref, rtol=1e-6, atol=1e-6)
+    finally:
+        m.trace(None)
+    # g4_forward_batch: the last token's logits
+    lg = m.forward_batch(tokens, pos0)
+    assert lg.tobytes() == bl[-1].tobytes()
+
+
+@pytest.mark.parametrize("cfg,K", [(SMALL, 4), (MID, 6)], ids=["small-K4", "mid-K6"])
+def test_verify_accepts_the_greedy_prefix(gpu, cfg, K):
+    """main.c:383-404: the target runs [next_tok, drafts] at pos..pos+K; the
+    accepted prefix is where its greedy choice equals the draft, and the bonus
+    is its choice at the first mismatch."""
+    G = gpu
+    m = make_model(G, cfg, 1, 2, seed=3)
+    V = cfg["n_vocab"]
+    pos = cfg["n_ctx"] - K - 8
+    tok0 = 17
+    greedy, t = [], tok0
+    for i in range(K + 1):                     # the plain greedy continuation
+        t = m.forward(t, pos + i)
+        greedy.append(t)
+    am = G.Buffer(4 * (K + 1))
+    for j in range(K + 1):                     # drafts correct up to j
+        draft = [greedy[i] if i < j else (greedy[i] + 1) % V for i in range(K)]
+        L, _ = m.forward_batch_heads([tok0] + draft, pos)
+        G.argmax_rows(L, V, K + 1, am)
+        G.synchronize()
+        a = list(am.download(np.int32, K + 1))
+        n_acc = 0
+        while n_acc < K and a[n_acc] == draft[n_acc]:
+            n_acc += 1
+        assert n_acc == min(j, K), f"j={j}: accepted {n_acc}"
+        assert a[n_acc] == greedy[n_acc], f"j={j}: bonus {a[n_acc]} vs greedy {greedy[n_acc]}"
+
+
+def test_batch_argument_errors(gpu):
+    G = gpu
+    m = make_model(G, SMALL, 1, 2)
+    with pytest.raises(G.G4HError):
+        m.forward_batch(list(range(65)), 0)                 # more than G4_BATCH_MAX
+    with pytest.raises(G.G4HError):
+        m.forward_batch([1, 2, 3], SMALL["n_ctx"] - 2)       # runs past the context
+    with pytest.raises(G.G4HError):
+        m.forward_batch([1, SMALL["n_vocab"]], 0)            # token out of range

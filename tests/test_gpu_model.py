@@ -346,11 +346,13 @@ def test_graph_replay_matches_eager(gpu):
         assert np.array_equal(m2.logits().view(np.uint32), eager[i][1].view(np.uint32))
 
 
-@pytest.mark.parametrize("cfg,kv_type,fuse", [("SMALL", 1, None), ("SMALL", 8, None), ("SMALL", 2, None), ("SMALL", 1, "19"),
-                                              ("SMALL", 1, "31"), ("MID", 1, None), ("MID", 1, "19"), ("MID", 8, None)],
-                         ids=["f16-default", "q8_0-default", "q4_0-default", "f16-qkv-in-attention", "f16-all",
-                              "mid-f16-default", "mid-f16-qkv-in-attention", "mid-q8_0-default"])
-def test_fused_step_equals_unfused(gpu, monkeypatch, cfg, kv_type, fuse):
+@pytest.mark.parametrize("cfg,kv_type,fuse,wtype", [
+    ("SMALL", 1, None, 2), ("SMALL", 8, None, 2), ("SMALL", 2, None, 2), ("SMALL", 1, "19", 2), ("SMALL", 1, "31", 2),
+    ("MID", 1, None, 2), ("MID", 1, "19", 2), ("MID", 8, None, 2), ("SMALL", 1, None, 8), ("MID", 1, None, 8),
+    ("MID", 1, "31", 8)],
+    ids=["f16-default", "q8_0-default", "q4_0-default", "f16-qkv-in-attention", "f16-all", "mid-f16-default",
+         "mid-f16-qkv-in-attention", "mid-q8_0-default", "q8w-f16-default", "mid-q8w-f16-default", "mid-q8w-f16-all"])
+def test_fused_step_equals_unfused(gpu, monkeypatch, cfg, kv_type, fuse, wtype):
     """The step with the residual norms folded into the Wqkv / Wgu prologues and
     GELU into the Wgu epilogue (the default), or with the Wqkv GEMV inside the
     attention launch (G4H_DECODE_FUSE bit 16), gives the same tokens and
@@ -364,11 +366,13 @@ def test_fused_step_equals_unfused(gpu, monkeypatch, cfg, kv_type, fuse):
         else:
             monkeypatch.setenv("G4H_DECODE_FUSE", f)
         shape = SMALL if cfg == "SMALL" else MID
-        m = G.Model(seed=21, kv_type=kv_type, **shape)
+        m = G.Model(seed=21, kv_type=kv_type, wtype=wtype, **shape)
         m.fill_kv(seed=22)
         out, tok = [], 9
         p0 = 30 if cfg == "SMALL" else 950
-        for pos in range(p0, p0 + 3):
+        # q8_0 rows of 2560 sum in 64-lane rows: an epilogue in another shape
+        # showed up as a rare one-ulp difference, so those runs take more steps
+        for pos in range(p0, p0 + (12 if wtype == 8 else 3)):
             tok = m.forward(tok, pos)
             out.append((tok, m.logits()))
         m.free()
