@@ -39,6 +39,7 @@
 #ifndef G4RUN_ABI_H
 #define G4RUN_ABI_H
 
+#include <stdbool.h>
 #include <stddef.h>
 #include <stdint.h>
 
@@ -126,6 +127,71 @@ typedef struct {
     uint64_t    offset;
     const void *data;
 } g4_tensor;
+
+/* g4run.h:172-246: the GGUF model file.  g4_gguf_open maps the file (a
+ * read-only private mmap; the reference uses a Win32 view, gguf.c:124-160)
+ * and parses GGUF v2/v3 as gguf.c:162-404 does: the same metadata keys and
+ * defaults, tensor table, alignment, data offsets and bounds checks, and the
+ * same architecture checks (gemma4, gemma4-assistant, qwen35).  Tensor data
+ * pointers point into the mapping.  g4_gguf_write (a pruning export) and
+ * g4_gguf_dump (a debug print) are not exported. */
+#define G4_MAX_LAYERS 64                     /* g4run.h:22 */
+typedef struct {
+    const char *ptr;                         /* into the mapping, not NUL-terminated */
+    uint32_t    len;
+} g4_str;
+
+typedef struct {
+    void    *map_base;
+    uint64_t map_size;
+    void    *h_file, *h_map;                 /* unused here (NULL) */
+    uint32_t version;
+    uint64_t n_tensors, n_kv;
+    uint64_t data_start;
+    uint64_t kv_end;
+    uint64_t ff_len_off;
+    int      ff_len_vt;
+    uint32_t alignment;
+    g4_tensor *tensors;
+    char  arch[32];
+    int   n_layer, n_embd, n_vocab, n_head, n_head_kv;
+    int   n_embd_per_layer;
+    int   n_ff[G4_MAX_LAYERS];
+    int   head_dim_full, head_dim_swa;
+    int   n_rot_full, n_rot_swa;
+    float rope_base_full, rope_base_swa;
+    float rms_eps;
+    float final_softcap;
+    int   n_swa;
+    int   n_kv_shared;
+    int   n_layer_kv;
+    uint8_t is_swa[G4_MAX_LAYERS];
+    int   n_ctx_train;
+    bool  is_assistant;
+    int   n_embd_out;
+    int   n_nextn;
+    bool  is_qwen35;
+    int   n_embd_head_k, n_embd_head_v;
+    int   ssm_d_conv, ssm_d_inner, ssm_d_state, ssm_dt_rank, ssm_n_group;
+    int   full_attn_interval;
+    int   rope_sections[4];
+    uint8_t is_recr[G4_MAX_LAYERS];
+    int   tok_pre;
+    int      tok_n;
+    g4_str  *tok_text;
+    const int32_t *tok_type;
+    int      merges_n;
+    g4_str  *merges;
+    int   bos_id, eos_id, eot_id, unk_id, pad_id;
+    bool  add_bos;
+    float meta_temp, meta_top_p;
+    int   meta_top_k;
+    g4_str chat_template;
+} g4_model_file;
+
+int  g4_gguf_open(g4_model_file *mf, const char *path, bool verbose);
+void g4_gguf_close(g4_model_file *mf);
+const g4_tensor *g4_find_tensor(const g4_model_file *mf, const char *name);
 
 /* g4run.h:464-489: the sampling chain, with the reference's struct.  The
  * state-keeping calls are host bookkeeping with sampler.c's semantics
