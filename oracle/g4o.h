@@ -110,6 +110,7 @@ void g4o_set_dot_f16_fn(g4o_dot_f16_fn fn);      /* attention's f16 score dot */
  *      sampler.c:139-144) ---- */
 void     g4o_rms_norm(const float *x, const float *w, float *y, int n, float eps);
 void     g4o_rope_cache(float *cs, int n_dims, int pos, float freq_base);
+void     g4o_rope_cache_ff(float *cs, int n_dims, int pos, float freq_base, const float *ff);
 void     g4o_rope_apply(float *x, const float *cs, int n_dims);
 uint16_t g4o_gelu_table_entry(uint16_t h);      /* fp16(gelu_tanh(fp32(h))) */
 float    g4o_gelu(float x);
@@ -121,6 +122,10 @@ int      g4o_argmax(const float *v, int n);
  *      Attends positions 0..pos (no ring wrap; slots >= pos+1). ---- */
 void g4o_attn_decode(const float *q, const void *kc, const void *vc, int kv_type,
                      int n_head, int n_kv, int hd, int pos, float *out, int nthreads);
+/* The same over positions j0..pos held in slot j % slots (the sliding window
+ * and KV ring of model.c:517-537); out is zero when pos < j0. */
+void g4o_attn_window(const float *q, const void *kc, const void *vc, int kv_type, int n_head, int n_kv, int hd,
+                     int pos, int j0, int slots, float *out, int nthreads);
 /* kv_store (model.c:583-589) */
 void g4o_kv_store(int kv_type, void *dst, const float *src, int hd);
 
@@ -161,6 +166,36 @@ void   g4o_model_qkv(const g4o_model *m, int il, const float *x, float *qkv, voi
 void   g4o_model_attn(const g4o_model *m, int il, int pos, float *qkv, float *att, void *scratch, int nthreads);
 void   g4o_model_post(const g4o_model *m, int il, float *x, const float *att, void *scratch, int nthreads);
 int    g4o_model_head(const g4o_model *m, const float *x, float *logits, void *scratch, int nthreads);
+
+/* ---- the gemma4 forward (model.c:592-799) ----
+ * One KV head; sliding-window layers (is_swa) use head dim hd_swa, RoPE base
+ * rope_base_swa and a ring of 576 slots (G4_SWA_RING, g4run.h:24-26); full
+ * layers hd_full, rope_base_full with frequency factors rope_freqs and n_ctx
+ * slots.  Layers >= n_layer_kv have no K/V projection and attend the cache of
+ * layer n_layer_kv-2 (sliding) or n_layer_kv-1 (full).  RoPE covers the whole
+ * head (n_rot == head dim). */
+typedef struct { const void *data; int type; int64_t ncols, nrows; } g4o_mat;   /* GGUF rows */
+typedef struct {
+    g4o_mat wq, wk, wv, wo, gate, up, down, inp_gate, proj;     /* wv.data NULL: V = K */
+    const float *attn_norm, *q_norm, *k_norm, *post_attn_norm, *ffn_norm, *post_ffw_norm, *post_norm;
+    float out_scale;
+} g4o_gemma_layer;
+typedef struct {
+    int n_layer, n_layer_kv, n_embd, n_head, n_vocab, n_embd_per_layer, hd_full, hd_swa, n_swa, n_ctx;
+    float rope_base_full, rope_base_swa, eps, softcap;
+    const uint8_t *is_swa;
+    const int *n_ff;
+    int kv_type;                         /* G4O_F16, G4O_Q8_0 or G4O_Q4_0 */
+    g4o_mat tok_embd, per_layer_tok_embd, per_layer_model_proj;
+    const float *per_layer_proj_norm, *output_norm, *rope_freqs;
+    const g4o_gemma_layer *layers;
+    void **kc, **vc;                     /* [n_layer_kv] caches, g4o_gemma_cache_bytes each */
+} g4o_gemma;
+size_t g4o_gemma_cache_bytes(const g4o_gemma *g, int il);
+/* tokens[0..nb) at positions pos0..: logits [nb][n_vocab] of every position
+ * and, if hnext, the head's input rms(x)*output_norm [nb][n_embd] */
+void   g4o_gemma_forward(const g4o_gemma *g, const int *tokens, int nb, int pos0, float *logits, float *hnext,
+                         int nthreads);
 
 /* ---- sampling chain (sampler.c), laid out as g4run.h:464-482's g4_sampler
  *      so one structure drives this restatement and the reference build ---- */

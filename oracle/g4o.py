@@ -493,3 +493,104 @@ class Sampler:
         """The accepted ids in the ring, oldest first."""
         s = self.s
         return [s.recent[(s.recent_head + i) % s.recent_cap] for i in range(s.recent_n)]
+
+
+# ------------------------------------------------------------------- gemma4
+class _Mat(C.Structure):
+    _fields_ = [("data", _vp), ("type", C.c_int), ("ncols", _i64), ("nrows", _i64)]
+
+
+class _GemmaLayer(C.Structure):
+    _fields_ = [(n, _Mat) for n in ("wq", "wk", "wv", "wo", "gate", "up", "down", "inp_gate", "proj")] + \
+               [(n, _vp) for n in ("attn_norm", "q_norm", "k_norm", "post_attn_norm", "ffn_norm", "post_ffw_norm",
+                                   "post_norm")] + [("out_scale", C.c_float)]
+
+
+class _Gemma(C.Structure):
+    _fields_ = [(n, C.c_int) for n in ("n_layer", "n_layer_kv", "n_embd", "n_head", "n_vocab", "n_embd_per_layer",
+                                       "hd_full", "hd_swa", "n_swa", "n_ctx")] + \
+               [(n, C.c_float) for n in ("rope_base_full", "rope_base_swa", "eps", "softcap")] + \
+               [("is_swa", _vp), ("n_ff", _vp), ("kv_type", C.c_int),
+                ("tok_embd", _Mat), ("per_layer_tok_embd", _Mat), ("per_layer_model_proj", _Mat),
+                ("per_layer_proj_norm", _vp), ("output_norm", _vp), ("rope_freqs", _vp),
+                ("layers", _vp), ("kc", _vp), ("vc", _vp)]
+
+
+class Gemma:
+    """The gemma4 forward of model.c:592-799 (oracle/g4o_gemma.c) over GGUF
+    tensors given by name: {name: (ggml_type, ne list, raw bytes as uint8 or
+    float32 array)}; hp uses g4_model_file's field names."""
+
+    def __init__(self, hp: dict, tensors: dict, kv_type: int, n_ctx: int):
+        L = lib()
+        L.g4o_gemma_forward.argtypes = [_vp, _vp, C.c_int, C.c_int, _vp, _vp, C.c_int]
+        L.g4o_gemma_forward.restype = None
+        L.g4o_gemma_cache_bytes.argtypes = [_vp, C.c_int]
+        L.g4o_gemma_cache_bytes.restype = C.c_size_t
+        self.hp, self._keep = hp, []
+
+        def arr(a, dt):
+            a = np.ascontiguousarray(a, dtype=dt)
+            self._keep.append(a)
+            return a
+
+        def mat(name):
+            m = _Mat()
+            if name not in tensors:
+                return m
+            t, ne, raw = tensors[name]
+            a = arr(np.frombuffer(np.ascontiguousarray(raw).tobytes(), np.uint8), np.uint8)
+            m.data, m.type, m.ncols, m.nrows = a.ctypes.data, t, ne[0], ne[1] if len(ne) > 1 else 1
+            return m
+
+        def vec(name):
+            if name not in tensors:
+                return None
+            return arr(np.frombuffer(np.ascontiguousarray(tensors[name][2]).tobytes(), np.float32), np.float32).ctypes.data
+
+        nl = hp["n_layer"]
+        layers = (_GemmaLayer * nl)()
+        for il in range(nl):
+            p = f"blk.{il}."
+            ly = layers[il]
+            for f, n in (("wq", "attn_q"), ("wk", "attn_k"), ("wv", "attn_v"), ("wo", "attn_output"), ("gate", "ffn_gate"),
+                         ("up", "ffn_up"), ("down", "ffn_down"), ("inp_gate", "inp_gate"), ("proj", "proj")):
+                setattr(ly, f, mat(p + n + ".weight"))
+            for f, n in (("attn_norm", "attn_norm"), ("q_norm", "attn_q_norm"), ("k_norm", "attn_k_norm"),
+                         ("post_attn_norm", "post_attention_norm"), ("ffn_norm", "ffn_norm"),
+                         ("post_ffw_norm", "post_ffw_norm"), ("post_norm", "post_norm")):
+                setattr(ly, f, vec(p + n + ".weight"))
+            sc = p + "layer_output_scale.weight"
+            ly.out_scale = float(np.frombuffer(np.ascontiguousarray(tensors[sc][2]).tobytes(), np.float32)[0]) \
+                if sc in tensors else 1.0
+        self._layers = layers
+        g = _Gemma()
+        for f in ("n_layer", "n_layer_kv", "n_embd", "n_head", "n_vocab", "n_embd_per_layer", "n_swa"):
+            setattr(g, f, hp[f])
+        g.hd_full, g.hd_swa, g.n_ctx = hp["head_dim_full"], hp["head_dim_swa"], n_ctx
+        g.rope_base_full, g.rope_base_swa = hp["rope_base_full"], hp["rope_base_swa"]
+        g.eps, g.softcap = hp["rms_eps"], hp.get("final_softcap", 0.0)
+        g.is_swa = arr(hp["is_swa"][:nl], np.uint8).ctypes.data
+        g.n_ff = arr(hp["n_ff"][:nl], np.int32).ctypes.data
+        g.kv_type = kv_type
+        g.tok_embd, g.per_layer_tok_embd = mat("token_embd.weight"), mat("per_layer_token_embd.weight")
+        g.per_layer_model_proj = mat("per_layer_model_proj.weight")
+        g.per_layer_proj_norm, g.output_norm = vec("per_layer_proj_norm.weight"), vec("output_norm.weight")
+        g.rope_freqs = vec("rope_freqs.weight")
+        g.layers = C.cast(layers, _vp)
+        self._g = g
+        nkv = hp["n_layer_kv"]
+        self.kc = [np.zeros(L.g4o_gemma_cache_bytes(C.byref(g), il), np.uint8) for il in range(nkv)]
+        self.vc = [np.zeros(L.g4o_gemma_cache_bytes(C.byref(g), il), np.uint8) for il in range(nkv)]
+        self._kp = (_vp * max(nkv, 1))(*[a.ctypes.data for a in self.kc])
+        self._vp_ = (_vp * max(nkv, 1))(*[a.ctypes.data for a in self.vc])
+        g.kc, g.vc = C.cast(self._kp, _vp), C.cast(self._vp_, _vp)
+
+    def forward(self, tokens, pos0: int, nthreads: int = 1):
+        """(logits [nb][n_vocab], hnext [nb][n_embd]) of every position."""
+        t = np.ascontiguousarray(tokens, np.int32)
+        nb = t.size
+        logits = np.zeros((nb, self.hp["n_vocab"]), np.float32)
+        hn = np.zeros((nb, self.hp["n_embd"]), np.float32)
+        lib().g4o_gemma_forward(C.byref(self._g), _ptr(t), nb, pos0, _ptr(logits), _ptr(hn), nthreads)
+        return logits, hn

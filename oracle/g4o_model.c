@@ -204,12 +204,16 @@ void g4o_rms_norm(const float *x, const float *w, float *y, int n, float eps) {
 
 /* model.c:349-358: theta_i = pos * base^(-2i/n), accumulated by repeated
  * multiplication as the reference does. */
-void g4o_rope_cache(float *cs, int n_dims, int pos, float freq_base) {
+void g4o_rope_cache(float *cs, int n_dims, int pos, float freq_base) { g4o_rope_cache_ff(cs, n_dims, pos, freq_base, NULL); }
+
+/* with per-pair frequency factors ff (model.c:352-353: theta / ff[i]) */
+void g4o_rope_cache_ff(float *cs, int n_dims, int pos, float freq_base, const float *ff) {
     const float theta_scale = powf(freq_base, -2.0f / n_dims);
     float theta = (float)pos;
     for (int i = 0; i < n_dims / 2; i++) {
-        cs[2 * i] = cosf(theta);
-        cs[2 * i + 1] = sinf(theta);
+        const float t = ff ? theta / ff[i] : theta;
+        cs[2 * i] = cosf(t);
+        cs[2 * i + 1] = sinf(t);
         theta *= theta_scale;
     }
 }
@@ -262,6 +266,7 @@ typedef struct {
     const float *q; const uint8_t *kc, *vc; int kv_type;
     int n_head, n_kv, hd, pos; float *out;
     size_t row_bytes;
+    int j0, slots;           /* first attended position; positions live in slot j % slots */
 } attn_job;
 
 /* model.c:509-580 for one decode token, one query head per work item.
@@ -271,7 +276,7 @@ typedef struct {
 static void attn_heads(int64_t h0, int64_t h1, void *p, int tid) {
     (void)tid;
     const attn_job *u = p;
-    const int hd = u->hd, nv = u->pos + 1, grp = u->n_head / u->n_kv;
+    const int hd = u->hd, nv = u->pos - u->j0 + 1, grp = u->n_head / u->n_kv;
     float *att = malloc((size_t)nv * sizeof(float));
     float *vtmp = malloc((size_t)hd * sizeof(float));
     uint16_t *q16 = malloc((size_t)hd * 2);
@@ -284,7 +289,7 @@ static void attn_heads(int64_t h0, int64_t h1, void *p, int tid) {
         else g4o_quantize_q8_0(qh, q8, hd);
         float mx = -INFINITY;
         for (int j = 0; j < nv; j++) {
-            const uint8_t *krow = u->kc + ((size_t)j * u->n_kv + kvh) * u->row_bytes;
+            const uint8_t *krow = u->kc + ((size_t)((u->j0 + j) % u->slots) * u->n_kv + kvh) * u->row_bytes;
             float s;
             if (u->kv_type == G4O_F16) s = dot_f16((const uint16_t *)krow, q16, hd);
             else s = dot_for(u->kv_type)(krow, q8, hd);
@@ -296,7 +301,7 @@ static void attn_heads(int64_t h0, int64_t h1, void *p, int tid) {
         const float inv = (float)(1.0 / sum);
         for (int i = 0; i < hd; i++) o[i] = 0.0f;
         for (int j = 0; j < nv; j++) {
-            const uint8_t *vrow = u->vc + ((size_t)j * u->n_kv + kvh) * u->row_bytes;
+            const uint8_t *vrow = u->vc + ((size_t)((u->j0 + j) % u->slots) * u->n_kv + kvh) * u->row_bytes;
             if (u->kv_type == G4O_F16) {
                 const float wj = g4o_fp16_to_fp32(g4o_fp32_to_fp16(att[j] * inv));
                 const uint16_t *v = (const uint16_t *)vrow;
@@ -321,12 +326,21 @@ static void attn_heads(int64_t h0, int64_t h1, void *p, int tid) {
     free(att); free(vtmp); free(q16); free(q8);
 }
 
-void g4o_attn_decode(const float *q, const void *kc, const void *vc, int kv_type,
-                     int n_head, int n_kv, int hd, int pos, float *out, int nthreads) {
+void g4o_attn_window(const float *q, const void *kc, const void *vc, int kv_type, int n_head, int n_kv, int hd,
+                     int pos, int j0, int slots, float *out, int nthreads) {
     attn_job u = { q, kc, vc, kv_type, n_head, n_kv, hd, pos, out,
-                   kv_type == G4O_F16 ? (size_t)hd * 2 : g4o_row_size(kv_type, hd) };
+                   kv_type == G4O_F16 ? (size_t)hd * 2 : g4o_row_size(kv_type, hd), j0, slots };
+    if (pos < j0) {                                   /* nothing to attend (model.c:523) */
+        for (int64_t i = 0; i < (int64_t)n_head * hd; i++) out[i] = 0.0f;
+        return;
+    }
     if (nthreads > 1) g4o_parallel_for(n_head, attn_heads, &u);
     else attn_heads(0, n_head, &u, 0);
+}
+
+void g4o_attn_decode(const float *q, const void *kc, const void *vc, int kv_type,
+                     int n_head, int n_kv, int hd, int pos, float *out, int nthreads) {
+    g4o_attn_window(q, kc, vc, kv_type, n_head, n_kv, hd, pos, 0, pos + 1, out, nthreads);
 }
 
 /* ---------------------------------------------------------- decode step -- */
