@@ -88,6 +88,7 @@ _SIGS = [
     ("g4h_attn_passes", _int, [_int, _int, _int, _int, _int, C.POINTER(_int)]),
     ("g4h_attn_decode", _int, [_vp, _vp, _vp, _int, _int, _int, _int, _int, _vp, _vp, _sz, _vp]),
     ("g4h_attn_status", _int, [_vp, C.POINTER(_int), _vp]),
+    ("g4h_attn_decode_window", _int, [_vp, _vp, _vp, _int, _int, _int, _int, _int, _int, _int, _vp, _vp, _sz, _vp]),
     ("g4h_attn_prefill", _int, [_vp, _vp, _vp, _int, _int, _int, _int, _int, _int, _vp, _vp, _sz, _vp]),
     ("g4h_kv_store", _int, [_int, _vp, _vp, _int, _int, _sz, _vp]),
     ("g4h_model_create", _int, [_vp, C.c_uint64, C.POINTER(_vp)]),
@@ -120,6 +121,11 @@ _SIGS = [
     ("g4h_forward_batch", _int, [_vp, C.POINTER(_int), _int, _int, _int, _vp]),
     ("g4h_forward_batch_heads", _int, [_vp, C.POINTER(_int), _int, _int, _vp, _vp, _vp]),
     ("g4h_argmax_rows", _int, [_vp, _int, _int, _vp, _vp]),
+    ("g4h_gemma_create", _int, [_vp, _int, _int, C.POINTER(_vp)]),
+    ("g4h_gemma_open", _int, [C.c_char_p, _int, _int, C.POINTER(_vp)]),
+    ("g4h_gemma_free", _int, [_vp]),
+    ("g4h_gemma_info", _int, [_vp, C.POINTER(_int), C.POINTER(_int), C.POINTER(_int), C.POINTER(_int)]),
+    ("g4h_gemma_forward", _int, [_vp, C.POINTER(_int), _int, _int, _vp, _vp, _vp]),
 ]
 
 _lib = None
@@ -383,6 +389,17 @@ def attn_decode(q, kc, vc, kv_type: int, n_head: int, n_kv: int, hd: int, n_pos:
                                 ws.nbytes if isinstance(ws, Buffer) else need, stream))
 
 
+def attn_decode_window(q, kc, vc, kv_type: int, n_head: int, n_kv: int, hd: int, n_pos: int, window: int, ring: int, out,
+                       ws=None, stream=None) -> None:
+    """attn_kernel with a sliding window over a (doubled) KV ring."""
+    rows = window if 0 < window < n_pos else n_pos
+    need = attn_workspace_bytes(n_head, hd, rows)
+    if ws is None:
+        ws = Buffer(need)
+    check(lib().g4h_attn_decode_window(_p(q), _p(kc), _p(vc), kv_type, n_head, n_kv, hd, n_pos, window, ring, _p(out),
+                                       _p(ws), ws.nbytes if isinstance(ws, Buffer) else need, stream))
+
+
 def attn_status(ws, stream=None) -> bool:
     """True if an attention call on ws had a hand-off wait give up since the
     last query (its outputs are NaN); clears the flag."""
@@ -441,6 +458,38 @@ class _View:
         b = Buffer(rs * self.nrows)
         check(lib().g4h_tensor_store(self.ptr, b.ptr, None))
         return b.download(np.uint8, (self.nrows, rs))
+
+
+class Gemma:
+    """A gemma4 GGUF model resident on the device (g4h_gemma)."""
+
+    def __init__(self, path: str, n_ctx: int = 8192, kv_type: int = F16):
+        init()
+        p = _vp()
+        check(lib().g4h_gemma_open(str(path).encode(), n_ctx, kv_type, C.byref(p)))
+        self.ptr = p.value
+        v, e, nl, nc = _int(), _int(), _int(), _int()
+        check(lib().g4h_gemma_info(self.ptr, C.byref(v), C.byref(e), C.byref(nl), C.byref(nc)))
+        self.n_vocab, self.n_embd, self.n_layer, self.n_ctx = v.value, e.value, nl.value, nc.value
+
+    def forward(self, tokens, pos0: int, stream=None):
+        """Every position's (logits [nb][n_vocab], hnext [nb][n_embd]) as numpy."""
+        t = np.ascontiguousarray(np.atleast_1d(tokens), dtype=np.int32)
+        nb = t.size
+        L, Hn = Buffer(nb * self.n_vocab * 4), Buffer(nb * self.n_embd * 4)
+        check(lib().g4h_gemma_forward(self.ptr, t.ctypes.data_as(C.POINTER(_int)), nb, pos0, L.ptr, Hn.ptr, stream))
+        return L.download(np.float32, (nb, self.n_vocab)), Hn.download(np.float32, (nb, self.n_embd))
+
+    def free(self) -> None:
+        if getattr(self, "ptr", None):
+            lib().g4h_gemma_free(self.ptr)
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
 
 
 def argmax_rows(logits, n: int, nb: int, out, stream=None) -> None:

@@ -646,6 +646,32 @@ extern "C" int g4h_attn_decode(const float *q, const void *kc, const void *vc, i
     return G4H_OK;
 }
 
+extern "C" int g4h_attn_decode_window(const float *q, const void *kc, const void *vc, int kv_type, int n_head, int n_kv, int hd,
+                                      int n_pos, int window, int ring, float *out, void *ws, size_t ws_bytes, void *stream) {
+    G4_NEED_INIT();
+    if (!q || !kc || !vc || !out || !ws) return fail(G4H_ERR_ARG, "g4h_attn_decode_window: null pointer");
+    if (int rc = check_attn_shape("g4h_attn_decode_window", kv_type, n_head, n_kv, hd)) return rc;
+    if (n_pos <= 0 || window < 0 || ring < 0) return fail(G4H_ERR_ARG, "g4h_attn_decode_window: n_pos=%d window=%d ring=%d", n_pos, window, ring);
+    if (ring && (!window || window > ring)) return fail(G4H_ERR_ARG, "g4h_attn_decode_window: a ring needs 0 < window <= ring");
+    const int rows = window && window < n_pos ? window : n_pos;
+    if (ws_bytes < attn_workspace_bytes(n_head, hd, rows))
+        return fail(G4H_ERR_ARG, "g4h_attn_decode_window: workspace %zu < %zu bytes", ws_bytes, attn_workspace_bytes(n_head, hd, rows));
+    const uintptr_t al = kv_type == F16 ? 8 : 4;
+    if ((uintptr_t)kc % al || (uintptr_t)vc % al)
+        return fail(G4H_ERR_ARG, "g4h_attn_decode_window: caches must be %zu-byte aligned", (size_t)al);
+    QkvArgs a;
+    a.n_head = n_head;
+    a.n_kv = n_kv;
+    a.hd = hd;
+    a.kv_type = kv_type;
+    a.kc = (uint8_t *)kc;          // read only: no preparation on this entry point
+    a.vc = (uint8_t *)vc;
+    a.window = window;
+    a.ring = ring;
+    G4_HIP(launch_attn_decode(q, nullptr, a, n_pos, nullptr, rows, out, nullptr, (uint8_t *)ws, (hipStream_t)stream));
+    return G4H_OK;
+}
+
 extern "C" int g4h_attn_status(void *ws, int *failed, void *stream) {
     G4_NEED_INIT();
     if (!ws || !failed) return fail(G4H_ERR_ARG, "g4h_attn_status: null pointer");

@@ -1,0 +1,403 @@
+// gemma.cpp -- a gemma4 model from a GGUF file resident on one MI355X and its
+// forward (the GPU form of g4_ctx_init + forward_layers / g4_forward_batch_heads,
+// model.c:373-477 and 592-799).
+//
+// Every weight matrix of the file is uploaded once and repacked into the
+// resident layout (g4h_tensor_load); token_embd (tied with the head) and
+// per_layer_token_embd also stay as GGUF rows for the embedding gather.
+// Per token, the forward runs model.c's steps with this library's kernels:
+// the projections on the GEMV family (any weight format, the input prepared
+// in the weight's activation class as matmul_b does), the decode attention
+// with its q/k/v preparation and, for sliding-window layers, a window over a
+// KV ring (rows stored twice so every window is one contiguous run), layers
+// past n_layer_kv reading the cache of layer n_layer_kv-2 (sliding) or
+// n_layer_kv-1 (full), the per-layer embedding injection and the soft-cap.
+#include "../../include/g4hip.h"
+#include "../../include/g4run_abi.h"
+
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <vector>
+
+#include "host_fp16.h"
+#include "kernels.h"
+
+using namespace g4;
+
+extern "C" int g4h_internal_fail(int status, const char *msg);
+
+namespace {
+constexpr int kRows = 64;          // G4_BATCH_MAX (g4run.h:23)
+constexpr int kRing = 576;         // G4_SWA_RING (g4run.h:24-26)
+constexpr int kWindowMax = 512;    // G4_SWA_WINDOW_MAX
+
+struct GLayer {
+    g4h_tensor *wq = nullptr, *wk = nullptr, *wv = nullptr, *wo = nullptr, *gate = nullptr, *up = nullptr, *down = nullptr,
+               *inp_gate = nullptr, *proj = nullptr;
+    float *attn_norm = nullptr, *q_norm = nullptr, *k_norm = nullptr, *post_attn_norm = nullptr, *ffn_norm = nullptr,
+          *post_ffw_norm = nullptr, *post_norm = nullptr;
+    float out_scale = 1.0f;
+    int swa = 0, hd = 0, n_ff = 0;
+};
+}  // namespace
+
+struct g4h_gemma {
+    int n_layer = 0, n_layer_kv = 0, E = 0, H = 0, V = 0, PE = 0, hd_full = 0, hd_swa = 0, n_swa = 0, n_ctx = 0, kv_type = 0,
+        max_ff = 0, hd_max = 0;
+    float eps = 0, softcap = 0;
+    std::vector<GLayer> L;
+    g4h_tensor *head = nullptr, *ple_proj = nullptr;
+    uint8_t *tok_raw = nullptr, *ple_raw = nullptr;
+    int tok_type = 0, ple_type = 0;
+    size_t tok_rb = 0, ple_rb = 0;
+    float *ple_norm = nullptr, *out_norm = nullptr, *rope_swa = nullptr, *rope_full = nullptr;
+    std::vector<uint8_t *> kc, vc;
+    float *x = nullptr, *xb = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *qkv = nullptr, *att = nullptr, *g = nullptr,
+          *u = nullptr, *pl = nullptr, *plp = nullptr, *plg = nullptr, *hn = nullptr;
+    uint8_t *ws = nullptr;
+    uint16_t *gelu = nullptr;
+    std::vector<void *> allocs;
+    std::vector<g4h_tensor *> tensors;
+};
+
+#define G_HIP(call)                                                                \
+    do {                                                                           \
+        hipError_t e_ = (call);                                                    \
+        if (e_ != hipSuccess) return g4h_internal_fail(G4H_ERR_HIP, hipGetErrorString(e_)); \
+    } while (0)
+#define G_RC(call)                  \
+    do {                            \
+        int rc_ = (call);           \
+        if (rc_) return rc_;        \
+    } while (0)
+
+namespace {
+
+int gfail(int status, const char *fmt, const char *a = "") {
+    char msg[256];
+    snprintf(msg, sizeof msg, fmt, a);
+    return g4h_internal_fail(status, msg);
+}
+
+int galloc(g4h_gemma *m, void **p, size_t bytes) {
+    G_RC(g4h_malloc(p, bytes));
+    m->allocs.push_back(*p);
+    return G4H_OK;
+}
+
+const g4_tensor *find(const g4_model_file *mf, const char *fmt, int il, bool need, int *rc) {
+    char name[96];
+    snprintf(name, sizeof name, fmt, il);
+    const g4_tensor *t = g4_find_tensor(mf, name);
+    if (!t && need) *rc = gfail(G4H_ERR_ARG, "g4h_gemma_create: missing tensor %s", name);
+    return t;
+}
+
+// a 2-D weight matrix, uploaded and repacked
+int up_matrix(g4h_gemma *m, const g4_tensor *t, g4h_tensor **out) {
+    if (t->ndim > 2 || t->ne[2] != 1 || t->ne[3] != 1) return gfail(G4H_ERR_SHAPE, "g4h_gemma_create: %s is not a matrix", t->name);
+    G_RC(g4h_tensor_create(t->type, t->ne[0], t->ne[1], out));
+    m->tensors.push_back(*out);
+    return g4h_tensor_load(*out, t->data, 0, nullptr);
+}
+
+// an f32 vector of n values
+int up_vec(g4h_gemma *m, const g4_tensor *t, int64_t n, float **out) {
+    if (t->type != G4H_F32 || t->ne[0] * t->ne[1] * t->ne[2] * t->ne[3] != n)
+        return gfail(G4H_ERR_SHAPE, "g4h_gemma_create: %s must be an f32 vector of the model's width", t->name);
+    G_RC(galloc(m, (void **)out, (size_t)n * 4));
+    G_HIP(hipMemcpy(*out, t->data, (size_t)n * 4, hipMemcpyHostToDevice));
+    return G4H_OK;
+}
+
+// rope_cache (model.c:349-357) for every position: [n_ctx][hd] (cos, sin) pairs
+std::vector<float> rope_table(int n_ctx, int hd, float base, const float *ff) {
+    std::vector<float> t((size_t)n_ctx * hd);
+    const float theta_scale = powf(base, -2.0f / hd);
+    for (int p = 0; p < n_ctx; p++) {
+        float theta = (float)p;
+        for (int i = 0; i < hd / 2; i++) {
+            const float a = ff ? theta / ff[i] : theta;
+            t[(size_t)p * hd + 2 * i] = cosf(a);
+            t[(size_t)p * hd + 2 * i + 1] = sinf(a);
+            theta *= theta_scale;
+        }
+    }
+    return t;
+}
+
+bool attn_hd(int hd) { return hd == 64 || hd == 128 || hd == 192 || hd == 256; }
+
+int create(const g4_model_file *mf, int n_ctx, int kv_type, g4h_gemma *m) {
+    if (std::strcmp(mf->arch, "gemma4") != 0) return gfail(G4H_ERR_TYPE, "g4h_gemma_create: architecture %s is not gemma4", mf->arch);
+    if (kv_type != G4H_F16 && kv_type != G4H_Q8_0 && kv_type != G4H_Q4_0)
+        return gfail(G4H_ERR_TYPE, "g4h_gemma_create: KV type must be f16, q8_0 or q4_0");
+    m->n_layer = mf->n_layer;
+    m->n_layer_kv = mf->n_layer_kv;
+    m->E = mf->n_embd;
+    m->H = mf->n_head;
+    m->V = mf->n_vocab;
+    m->PE = mf->n_embd_per_layer;
+    m->hd_full = mf->head_dim_full;
+    m->hd_swa = mf->head_dim_swa;
+    m->n_swa = mf->n_swa;
+    m->n_ctx = n_ctx;
+    m->kv_type = kv_type;
+    m->eps = mf->rms_eps;
+    m->softcap = mf->final_softcap;
+    if (m->n_layer < 1 || m->n_layer_kv < 2 || m->E <= 0 || m->V <= 0 || m->PE <= 0 || n_ctx <= 0)
+        return gfail(G4H_ERR_SHAPE, "g4h_gemma_create: bad dimensions");
+    if (!attn_hd(m->hd_full) || !attn_hd(m->hd_swa))
+        return gfail(G4H_ERR_SHAPE, "g4h_gemma_create: head dims must be 64, 128, 192 or 256 (the attention kernels' rows)");
+    if (mf->n_rot_full != m->hd_full || mf->n_rot_swa != m->hd_swa)
+        return gfail(G4H_ERR_SHAPE, "g4h_gemma_create: RoPE must cover the whole head (n_rot == head dim)");
+    if (m->H != 1 && m->H != 2 && m->H != 4 && m->H != 8)
+        return gfail(G4H_ERR_SHAPE, "g4h_gemma_create: 1, 2, 4 or 8 query heads per KV head");
+    if (m->n_swa < 1 || m->n_swa > kWindowMax) return gfail(G4H_ERR_SHAPE, "g4h_gemma_create: sliding window must be 1..512");
+    if (m->PE > 1024 || m->PE % 4 || m->E % 4) return gfail(G4H_ERR_SHAPE, "g4h_gemma_create: per-layer width <= 1024, widths % 4");
+    int rc = G4H_OK;
+    const g4_tensor *t_tok = find(mf, "token_embd.weight", 0, true, &rc), *t_ple = find(mf, "per_layer_token_embd.weight", 0, true, &rc),
+                    *t_pproj = find(mf, "per_layer_model_proj.weight", 0, true, &rc),
+                    *t_pnorm = find(mf, "per_layer_proj_norm.weight", 0, true, &rc),
+                    *t_onorm = find(mf, "output_norm.weight", 0, true, &rc), *t_rf = find(mf, "rope_freqs.weight", 0, true, &rc);
+    if (rc) return rc;
+    const int NPL = m->n_layer * m->PE;
+    if (t_tok->ne[0] != m->E || t_tok->ne[1] != m->V || t_ple->ne[0] != NPL || t_ple->ne[1] < m->V)
+        return gfail(G4H_ERR_SHAPE, "g4h_gemma_create: embedding shapes");
+    G_RC(up_matrix(m, t_tok, &m->head));
+    G_RC(up_matrix(m, t_pproj, &m->ple_proj));
+    m->tok_type = t_tok->type;
+    m->ple_type = t_ple->type;
+    m->tok_rb = g4h_row_size(t_tok->type, m->E);
+    m->ple_rb = g4h_row_size(t_ple->type, NPL);
+    G_RC(galloc(m, (void **)&m->tok_raw, m->tok_rb * m->V));
+    G_RC(galloc(m, (void **)&m->ple_raw, m->ple_rb * m->V));
+    G_HIP(hipMemcpy(m->tok_raw, t_tok->data, m->tok_rb * m->V, hipMemcpyHostToDevice));
+    G_HIP(hipMemcpy(m->ple_raw, t_ple->data, m->ple_rb * m->V, hipMemcpyHostToDevice));
+    G_RC(up_vec(m, t_pnorm, m->PE, &m->ple_norm));
+    G_RC(up_vec(m, t_onorm, m->E, &m->out_norm));
+    if (t_rf->type != G4H_F32 || t_rf->ne[0] < m->hd_full / 2) return gfail(G4H_ERR_SHAPE, "g4h_gemma_create: rope_freqs");
+    {
+        const std::vector<float> rs = rope_table(n_ctx, m->hd_swa, mf->rope_base_swa, nullptr);
+        const std::vector<float> rf = rope_table(n_ctx, m->hd_full, mf->rope_base_full, (const float *)t_rf->data);
+        G_RC(galloc(m, (void **)&m->rope_swa, rs.size() * 4));
+        G_RC(galloc(m, (void **)&m->rope_full, rf.size() * 4));
+        G_HIP(hipMemcpy(m->rope_swa, rs.data(), rs.size() * 4, hipMemcpyHostToDevice));
+        G_HIP(hipMemcpy(m->rope_full, rf.data(), rf.size() * 4, hipMemcpyHostToDevice));
+    }
+    m->L.resize(m->n_layer);
+    for (int il = 0; il < m->n_layer; il++) {
+        GLayer &L = m->L[il];
+        L.swa = mf->is_swa[il] != 0;
+        L.hd = L.swa ? m->hd_swa : m->hd_full;
+        L.n_ff = mf->n_ff[il];
+        m->max_ff = std::max(m->max_ff, L.n_ff);
+        const bool kv = il < m->n_layer_kv;
+        struct { const char *name; g4h_tensor **dst; bool need; } mats[] = {
+            {"blk.%d.attn_q.weight", &L.wq, true},     {"blk.%d.attn_k.weight", &L.wk, kv},
+            {"blk.%d.attn_v.weight", &L.wv, false},    {"blk.%d.attn_output.weight", &L.wo, true},
+            {"blk.%d.ffn_gate.weight", &L.gate, true}, {"blk.%d.ffn_up.weight", &L.up, true},
+            {"blk.%d.ffn_down.weight", &L.down, true}, {"blk.%d.inp_gate.weight", &L.inp_gate, true},
+            {"blk.%d.proj.weight", &L.proj, true}};
+        for (auto &mm : mats) {
+            if (!kv && (mm.dst == &L.wk || mm.dst == &L.wv)) continue;
+            const g4_tensor *t = find(mf, mm.name, il, mm.need, &rc);
+            if (rc) return rc;
+            if (t) G_RC(up_matrix(m, t, mm.dst));
+        }
+        struct { const char *name; float **dst; int64_t n; bool need; } vecs[] = {
+            {"blk.%d.attn_norm.weight", &L.attn_norm, m->E, true},
+            {"blk.%d.attn_q_norm.weight", &L.q_norm, L.hd, true},
+            {"blk.%d.attn_k_norm.weight", &L.k_norm, L.hd, kv},
+            {"blk.%d.post_attention_norm.weight", &L.post_attn_norm, m->E, true},
+            {"blk.%d.ffn_norm.weight", &L.ffn_norm, m->E, true},
+            {"blk.%d.post_ffw_norm.weight", &L.post_ffw_norm, m->E, true},
+            {"blk.%d.post_norm.weight", &L.post_norm, m->E, true}};
+        for (auto &vv : vecs) {
+            if (!kv && vv.dst == &L.k_norm) continue;
+            const g4_tensor *t = find(mf, vv.name, il, vv.need, &rc);
+            if (rc) return rc;
+            if (t) G_RC(up_vec(m, t, vv.n, vv.dst));
+        }
+        if (const g4_tensor *t = find(mf, "blk.%d.layer_output_scale.weight", il, false, &rc)) {
+            if (t->type != G4H_F32) return gfail(G4H_ERR_TYPE, "g4h_gemma_create: %s must be f32", t->name);
+            L.out_scale = *(const float *)t->data;
+        }
+        // shapes the forward relies on (model.c:421-433)
+        const int64_t qrows = (int64_t)m->H * L.hd;
+        if (L.wq->nrows != qrows || L.wq->ncols != m->E || L.wo->ncols != qrows || L.wo->nrows != m->E ||
+            (kv && (L.wk->nrows != L.hd || (L.wv && L.wv->nrows != L.hd))) || L.gate->nrows != L.n_ff || L.up->nrows != L.n_ff ||
+            L.down->ncols != L.n_ff || L.inp_gate->nrows != m->PE || L.proj->ncols != m->PE || L.proj->nrows != m->E)
+            return gfail(G4H_ERR_SHAPE, "g4h_gemma_create: layer shapes differ from the hparams");
+        if (L.n_ff % 4) return gfail(G4H_ERR_SHAPE, "g4h_gemma_create: FFN width % 4");
+    }
+    m->hd_max = std::max(m->hd_full, m->hd_swa);
+    // KV caches: sliding layers a ring of kRing slots stored twice, full layers n_ctx slots
+    for (int il = 0; il < m->n_layer_kv; il++) {
+        const GLayer &L = m->L[il];
+        const size_t row = kv_type == G4H_F16 ? (size_t)L.hd * 2 : g4h_row_size(kv_type, L.hd);
+        const size_t bytes = row * (L.swa ? 2 * kRing : (size_t)n_ctx);
+        uint8_t *k, *v;
+        G_RC(galloc(m, (void **)&k, bytes));
+        G_RC(galloc(m, (void **)&v, bytes));
+        G_HIP(hipMemset(k, 0, bytes));
+        G_HIP(hipMemset(v, 0, bytes));
+        m->kc.push_back(k);
+        m->vc.push_back(v);
+    }
+    const size_t B = kRows, E = m->E, Q = (size_t)m->H * m->hd_max;
+    G_RC(galloc(m, (void **)&m->x, B * E * 4));
+    G_RC(galloc(m, (void **)&m->xb, B * E * 4));
+    G_RC(galloc(m, (void **)&m->hn, B * E * 4));
+    G_RC(galloc(m, (void **)&m->q, B * Q * 4));
+    G_RC(galloc(m, (void **)&m->k, B * m->hd_max * 4));
+    G_RC(galloc(m, (void **)&m->v, B * m->hd_max * 4));
+    G_RC(galloc(m, (void **)&m->qkv, B * (Q + 2 * m->hd_max) * 4));
+    G_RC(galloc(m, (void **)&m->att, B * Q * 4));
+    G_RC(galloc(m, (void **)&m->g, B * m->max_ff * 4));
+    G_RC(galloc(m, (void **)&m->u, B * m->max_ff * 4));
+    G_RC(galloc(m, (void **)&m->pl, B * NPL * 4));
+    G_RC(galloc(m, (void **)&m->plp, B * NPL * 4));
+    G_RC(galloc(m, (void **)&m->plg, B * m->PE * 4));
+    const size_t wsb = g4h_attn_workspace_bytes(m->H, m->hd_max, n_ctx);
+    G_RC(galloc(m, (void **)&m->ws, wsb));
+    G_HIP(hipMemset(m->ws, 0, wsb));
+    std::vector<uint16_t> gt(65536);
+    for (uint32_t h = 0; h < 65536; h++) gt[h] = gelu_table_entry((uint16_t)h);
+    G_RC(galloc(m, (void **)&m->gelu, 65536 * 2));
+    G_HIP(hipMemcpy(m->gelu, gt.data(), 65536 * 2, hipMemcpyHostToDevice));
+    G_HIP(hipDeviceSynchronize());
+    return G4H_OK;
+}
+
+// Y[b] = W x[b], x rows of W->ncols floats prepared in W's activation class
+// (the GEMV family: token rows bit-identical for any count)
+int mm(const g4h_tensor *W, const float *x, float *Y, int nb, hipStream_t s) {
+    return g4h_matmul_ex(W, x, nullptr, 0, Y, nb, 1, s);
+}
+
+}  // namespace
+
+extern "C" int g4h_gemma_free(g4h_gemma *m) {
+    if (!m) return G4H_OK;
+    for (g4h_tensor *t : m->tensors) g4h_tensor_free(t);
+    for (void *p : m->allocs) g4h_free(p);
+    delete m;
+    return G4H_OK;
+}
+
+extern "C" int g4h_gemma_create(const void *model_file, int n_ctx, int kv_type, g4h_gemma **out) {
+    if (!model_file || !out) return g4h_internal_fail(G4H_ERR_ARG, "g4h_gemma_create: null argument");
+    *out = nullptr;
+    g4h_gemma *m = new g4h_gemma();
+    if (int rc = create((const g4_model_file *)model_file, n_ctx, kv_type, m)) {
+        g4h_gemma_free(m);
+        return rc;
+    }
+    *out = m;
+    return G4H_OK;
+}
+
+extern "C" int g4h_gemma_open(const char *path, int n_ctx, int kv_type, g4h_gemma **out) {
+    if (!path || !out) return g4h_internal_fail(G4H_ERR_ARG, "g4h_gemma_open: null argument");
+    g4_model_file mf;
+    if (g4_gguf_open(&mf, path, false) != 0) return gfail(G4H_ERR_ARG, "g4h_gemma_open: cannot read GGUF file %s", path);
+    const int rc = g4h_gemma_create(&mf, n_ctx, kv_type, out);
+    g4_gguf_close(&mf);                      // every tensor now lives on the device
+    return rc;
+}
+
+extern "C" int g4h_gemma_info(const g4h_gemma *m, int *n_vocab, int *n_embd, int *n_layer, int *n_ctx) {
+    if (!m) return g4h_internal_fail(G4H_ERR_ARG, "g4h_gemma_info: null model");
+    if (n_vocab) *n_vocab = m->V;
+    if (n_embd) *n_embd = m->E;
+    if (n_layer) *n_layer = m->n_layer;
+    if (n_ctx) *n_ctx = m->n_ctx;
+    return G4H_OK;
+}
+
+extern "C" int g4h_gemma_forward(g4h_gemma *m, const int *tokens, int nb, int pos0, float *logits_dev, float *hnext_dev,
+                                 void *stream) {
+    if (!m || !tokens || !logits_dev) return g4h_internal_fail(G4H_ERR_ARG, "g4h_gemma_forward: null argument");
+    if (nb < 1 || nb > kRows) return g4h_internal_fail(G4H_ERR_ARG, "g4h_gemma_forward: nb must be 1..64 (G4_BATCH_MAX)");
+    if (pos0 < 0 || pos0 + nb > m->n_ctx) return g4h_internal_fail(G4H_ERR_ARG, "g4h_gemma_forward: positions outside the context");
+    for (int b = 0; b < nb; b++)
+        if (tokens[b] < 0 || tokens[b] >= m->V) return g4h_internal_fail(G4H_ERR_ARG, "g4h_gemma_forward: token out of range");
+    const hipStream_t s = (hipStream_t)stream;
+    const int E = m->E, H = m->H, PE = m->PE, NPL = m->n_layer * PE;
+    const float eps = m->eps;
+
+    // embeddings and per-layer token rows (model.c:602-615)
+    for (int b = 0; b < nb; b++) {
+        G_HIP(launch_dequant(m->tok_type, m->tok_raw + (size_t)tokens[b] * m->tok_rb, m->tok_rb, m->x + (size_t)b * E, E, E, 1, s));
+        G_HIP(launch_dequant(m->ple_type, m->ple_raw + (size_t)tokens[b] * m->ple_rb, m->ple_rb, m->pl + (size_t)b * NPL, NPL, NPL,
+                             1, s));
+    }
+    G_HIP(launch_scale(m->x, (int64_t)nb * E, sqrtf((float)E), s));
+    G_HIP(launch_scale(m->pl, (int64_t)nb * NPL, sqrtf((float)PE), s));
+    // per-layer input projection (model.c:617-635)
+    G_RC(mm(m->ple_proj, m->x, m->plp, nb, s));
+    G_HIP(launch_ple_prep(m->plp, m->pl, m->ple_norm, PE, m->n_layer, nb, 1.0f / sqrtf((float)E), 1.0f / sqrtf(2.0f), eps, s));
+
+    for (int il = 0; il < m->n_layer; il++) {
+        const GLayer &L = m->L[il];
+        const int hd = L.hd, nq = H * hd, F = L.n_ff;
+        const float *rope = L.swa ? m->rope_swa : m->rope_full;
+        G_HIP(launch_rms_rows(m->x, L.attn_norm, m->xb, E, nb, eps, s));
+        G_RC(mm(L.wq, m->xb, m->q, nb, s));
+        QkvArgs qa;
+        qa.n_head = H;
+        qa.n_kv = 1;
+        qa.hd = hd;
+        qa.kv_type = m->kv_type;
+        qa.q_norm = L.q_norm;
+        qa.k_norm = L.k_norm;
+        qa.rope = rope;
+        qa.eps = eps;
+        qa.window = L.swa ? m->n_swa : 0;
+        qa.ring = L.swa ? kRing : 0;
+        const int npos_max = L.swa ? std::min(m->n_ctx, m->n_swa) : m->n_ctx;
+        if (il < m->n_layer_kv) {
+            // own K/V: q | k | v prepared, stored at the position and attended in one step (model.c:664-689)
+            G_RC(mm(L.wk, m->xb, m->k, nb, s));
+            if (L.wv) G_RC(mm(L.wv, m->xb, m->v, nb, s));
+            G_HIP(launch_pack_qkv(m->q, m->k, L.wv ? m->v : nullptr, m->qkv, nq, hd, nb, s));
+            qa.kc = m->kc[il];
+            qa.vc = m->vc[il];
+            for (int b = 0; b < nb; b++)
+                G_HIP(launch_attn_decode(nullptr, m->qkv + (size_t)b * (nq + 2 * hd), qa, pos0 + b + 1, nullptr, npos_max,
+                                         m->att + (size_t)b * nq, nullptr, m->ws, s));
+        } else {
+            // a shared cache: the queries are prepared here (model.c:666-672, 692)
+            const int cil = L.swa ? m->n_layer_kv - 2 : m->n_layer_kv - 1;
+            G_HIP(launch_head_prep(m->q, H, hd, nb, L.q_norm, rope, pos0, eps, s));
+            qa.kc = m->kc[cil];
+            qa.vc = m->vc[cil];
+            for (int b = 0; b < nb; b++)
+                G_HIP(launch_attn_decode(m->q + (size_t)b * nq, nullptr, qa, pos0 + b + 1, nullptr, npos_max,
+                                         m->att + (size_t)b * nq, nullptr, m->ws, s));
+        }
+        G_RC(mm(L.wo, m->att, m->xb, nb, s));
+        G_HIP(launch_resid(m->x, m->xb, L.post_attn_norm, E, nb, eps, 1.0f, s));
+        // FFN (model.c:718-736)
+        G_HIP(launch_rms_rows(m->x, L.ffn_norm, m->xb, E, nb, eps, s));
+        G_RC(mm(L.gate, m->xb, m->g, nb, s));
+        G_RC(mm(L.up, m->xb, m->u, nb, s));
+        G_HIP(launch_gelu_mul(m->g, F, m->u, F, F, nb, m->gelu, s));
+        G_RC(mm(L.down, m->g, m->xb, nb, s));
+        G_HIP(launch_resid(m->x, m->xb, L.post_ffw_norm, E, nb, eps, 1.0f, s));
+        // per-layer embedding injection (model.c:738-752)
+        G_RC(mm(L.inp_gate, m->x, m->plg, nb, s));
+        G_HIP(launch_gelu_mul(m->plg, PE, m->pl + (size_t)il * PE, NPL, PE, nb, m->gelu, s));
+        G_RC(mm(L.proj, m->plg, m->xb, nb, s));
+        G_HIP(launch_resid(m->x, m->xb, L.post_norm, E, nb, eps, L.out_scale, s));
+    }
+    // every position's head (model.c:790-798)
+    float *hn = hnext_dev ? hnext_dev : m->hn;
+    G_HIP(launch_rms_rows(m->x, m->out_norm, hn, E, nb, eps, s));
+    G_RC(mm(m->head, hn, logits_dev, nb, s));
+    if (m->softcap > 0) G_HIP(launch_softcap(logits_dev, (int64_t)nb * m->V, m->softcap, s));
+    G_HIP(hipStreamSynchronize(s));
+    return G4H_OK;
+}

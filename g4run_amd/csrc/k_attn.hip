@@ -167,9 +167,37 @@ struct AttnCtx {
     GemvPro pro;
     uint64_t *QT;
     int qrows;
+    int pabs, mirror;        // set by attn_view
 };
 
 __device__ __forceinline__ int npos_of(const AttnCtx &c) { return c.npos_dev ? *c.npos_dev : c.npos; }
+
+// The rows a launch attends as a linear cache (every kernel starts here):
+// positions j0 .. npos-1 with j0 = max(0, npos - window) (a sliding window,
+// model.c:517-519; window 0: all positions).  On a ring of `ring` slots each
+// row is stored twice, at slot s and s + ring (s = position % ring), so any
+// window of at most `ring` positions is contiguous from slot j0 % ring: the
+// cache pointers are moved there and the caller sees rows 0 .. nv-1.  Sets
+// c.pabs (the current position, the RoPE row) and c.mirror (the row index of
+// the current row's second copy, relative to the moved pointers, or INT_MIN).
+__device__ __forceinline__ int attn_view(AttnCtx &c) {
+    const int npos = npos_of(c);
+    c.pabs = npos - 1;
+    c.mirror = INT_MIN;
+    if (!c.a.window) return npos;
+    const int j0 = npos > c.a.window ? npos - c.a.window : 0;
+    const int base = c.a.ring ? j0 % c.a.ring : j0;
+    const size_t row = c.a.kv_type == F16 ? (size_t)c.a.hd * 2 : (size_t)(c.a.hd / 32) * (c.a.kv_type == Q4_0 ? 18 : 34);
+    const size_t slot = (size_t)c.a.n_kv * row;
+    c.a.kc += (size_t)base * slot;
+    c.a.vc += (size_t)base * slot;
+    const int nv = npos - j0;
+    if (c.a.ring) {
+        const int s = base + nv - 1;                               // slot of the current row's first copy
+        c.mirror = (s < c.a.ring ? s + c.a.ring : s - c.a.ring) - base;
+    }
+    return nv;
+}
 
 // loads and stores of data shared between the workgroups of one launch:
 // agent scope, coherent across the XCDs' L2 caches
@@ -244,7 +272,7 @@ __device__ __forceinline__ void prep_f16_issue_w(PrepF16<GRP> &st, const AttnCtx
     constexpr int hd = HD, epl = hd >> 6;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     st.nrow = GRP + (pos_chunk ? 2 : 0);
-    rope_load(st.cs, st.sn, c.a.rope, p, hd);
+    rope_load(st.cs, st.sn, c.a.rope, c.pabs, hd);
 #pragma unroll
     for (int sl = 0; sl < PrepF16<GRP>::SL; sl++) {
         const int r = wave + 4 * sl;
@@ -262,7 +290,7 @@ __device__ __forceinline__ void prep_f16_issue(PrepF16<GRP> &st, const AttnCtx &
     const int t = threadIdx.x, wave = t >> 6, h0 = kvh * GRP;
     st.nrow = c.qkv ? GRP + (pos_chunk ? 2 : 0) : 0;
     if (c.qkv) {
-        rope_load(st.cs, st.sn, c.a.rope, p, hd);
+        rope_load(st.cs, st.sn, c.a.rope, c.pabs, hd);
 #pragma unroll
         for (int sl = 0; sl < PrepF16<GRP>::SL; sl++) {
             const int r = wave + 4 * sl;
@@ -302,6 +330,8 @@ __device__ __forceinline__ void prep_f16_finish(const PrepF16<GRP> &st, const At
                 } else {
                     uint8_t *cache = r == GRP ? c.a.kc : c.a.vc;
                     cache_store(y, F16, cache + ((size_t)p * c.a.n_kv + kvh) * hd * 2, hd, nullptr);
+                    if (c.mirror != INT_MIN)                               // the ring's second copy
+                        cache_store(y, F16, cache + ((ptrdiff_t)c.mirror * c.a.n_kv + kvh) * hd * 2, hd, nullptr);
                     uint16_t *keep = r == GRP ? kpos : vpos;
                     if (keep) {
 #pragma unroll
@@ -431,7 +461,7 @@ __global__ __launch_bounds__(256) void k_attn_scores_f16(AttnCtx c) {
     __shared__ float sc[GRP][ATT_CHUNK];
     __shared__ float wm[4][GRP];
     __shared__ double wl[4][GRP];
-    const int npos = npos_of(c);
+    const int npos = attn_view(c);
     const int kvh = blockIdx.x, ch = blockIdx.y, t = threadIdx.x;
     const int lane = t & 63, wave = t >> 6;
     const int h0 = kvh * GRP, p = npos - 1;
@@ -476,7 +506,7 @@ __global__ __launch_bounds__(128) void k_attn_scores_q8(AttnCtx c) {
     __shared__ float qrow[GRP][256];
     __shared__ float wm[2][GRP];
     __shared__ double wl[2][GRP];
-    const int npos = npos_of(c);
+    const int npos = attn_view(c);
     const int kvh = blockIdx.x, ch = blockIdx.y, t = threadIdx.x, lane = t & 63, wave = t >> 6;
     constexpr int hd = HD;
     const int n_kv = c.a.n_kv, h0 = kvh * GRP, p = npos - 1;
@@ -485,7 +515,7 @@ __global__ __launch_bounds__(128) void k_attn_scores_q8(AttnCtx c) {
     // queries (prepared here or given) as fp32 rows in LDS; new key/value to the caches
     if (c.qkv) {
         float cs[4], sn[4];
-        rope_load(cs, sn, c.a.rope, p, hd);
+        rope_load(cs, sn, c.a.rope, c.pabs, hd);
         const int nrow = GRP + (pos_chunk ? 2 : 0);
         for (int r = wave; r < nrow; r += 2) {                         // uniform over the wave
             const int src_row = r < GRP ? h0 + r : r == GRP ? c.a.n_head + kvh : c.a.n_head + n_kv + kvh;
@@ -499,6 +529,9 @@ __global__ __launch_bounds__(128) void k_attn_scores_q8(AttnCtx c) {
             } else {
                 uint8_t *dst = (r == GRP ? c.a.kc : c.a.vc) + ((size_t)p * n_kv + kvh) * (hd / 32) * BS;
                 cache_store(y, KV, dst, hd, wbuf[wave]);
+                if (c.mirror != INT_MIN)                                   // the ring's second copy
+                    cache_store(y, KV, (r == GRP ? c.a.kc : c.a.vc) + ((ptrdiff_t)c.mirror * n_kv + kvh) * (hd / 32) * BS, hd,
+                                wbuf[wave]);
                 if (r == GRP) cache_store(y, KV, kpos, hd, wbuf[wave]);
             }
         }
@@ -682,7 +715,7 @@ __global__ __launch_bounds__(256) void k_attn_v(AttnCtx c) {
     __shared__ float part[4][GRP][256];
     __shared__ __align__(16) float wl[GRP][ATT_CHUNK];
     __shared__ float inv_s[GRP], max_s[GRP];
-    const int npos = npos_of(c);
+    const int npos = attn_view(c);
     const int kvh = blockIdx.x, ch = blockIdx.y, t = threadIdx.x, lane = t & 63, wave = t >> 6;
     constexpr int hd = HD;
     const int n_kv = c.a.n_kv, h0 = kvh * GRP;
@@ -827,7 +860,7 @@ __device__ __forceinline__ void combine_head(const AttnCtx &c, int h, int nch, f
 // grid n_head
 __global__ __launch_bounds__(256) void k_attn_combine(AttnCtx c) {
     __shared__ float row[256];
-    const int npos = npos_of(c);
+    const int npos = attn_view(c);
     combine_head<false>(c, blockIdx.x, (npos + ATT_CHUNK - 1) / ATT_CHUNK, row);
 }
 
@@ -969,7 +1002,7 @@ __global__ __launch_bounds__(256) void k_attn_fused_f16(AttnCtx c) {
     __shared__ float vals[ATT_FUSED_MAXC * 32];                      // combine: [chunk][32]
     __shared__ float gsum[ATT_FUSED_MAXC / ATT_CSUM * 32];           // combine: [chunk group][32]
     __shared__ int bad;
-    const int npos = npos_of(c);
+    const int npos = attn_view(c);
     const uint32_t tag = tag_of(c);
     const int kvh = blockIdx.x, ch = blockIdx.y, t = threadIdx.x;
     const int lane = t & 63, wave = t >> 6;

@@ -79,6 +79,11 @@ struct QkvArgs {
     const float *q_norm = nullptr, *k_norm = nullptr, *rope = nullptr;
     uint8_t *kc = nullptr, *vc = nullptr;
     float eps = 0.0f;
+    // sliding window: attend the last `window` positions (0: all); on a ring
+    // cache of `ring` slots every row is stored at slot pos % ring and again
+    // at that slot + ring (the caches hold 2 * ring slots), so a window of at
+    // most ring positions reads as one contiguous run (model.c:517-537)
+    int window = 0, ring = 0;
 };
 hipError_t launch_rand_normal(float *y, int64_t n, uint64_t seed, float mean, float std, hipStream_t s);
 // The row forms (nb tokens): x / delta / y rows of n floats, gu rows of 2 n_ff
@@ -132,6 +137,18 @@ hipError_t launch_sample(SamplerDev *S, int n_vocab, float *logits, int *out, in
                          hipStream_t s);
 // Pushes n ids into the ring in order (sampler.c:37-48).
 hipError_t launch_sampler_push(SamplerDev *S, const int *ids, int n, hipStream_t s);
+
+// k_gemma.hip: the gemma4 forward's row steps (nb token rows each)
+hipError_t launch_rms_rows(const float *x, const float *w, float *y, int n, int nb, float eps, hipStream_t s);
+hipError_t launch_resid(float *x, const float *d, const float *w, int n, int nb, float eps, float os, hipStream_t s);
+hipError_t launch_scale(float *y, int64_t n, float sc, hipStream_t s);
+hipError_t launch_ple_prep(const float *plp, float *pl, const float *w, int pe, int n_layer, int nb, float ps, float is2,
+                           float eps, hipStream_t s);
+hipError_t launch_gelu_mul(float *g, size_t gs, const float *u, size_t us, int n, int nb, const uint16_t *tab, hipStream_t s);
+hipError_t launch_head_prep(float *q, int n_head, int hd, int nb, const float *w, const float *rope, int pos0, float eps,
+                            hipStream_t s);
+hipError_t launch_pack_qkv(const float *q, const float *k, const float *v, float *qkv, int nq, int hd, int nb, hipStream_t s);
+hipError_t launch_softcap(float *l, int64_t n, float cap, hipStream_t s);
 
 // k_mfma.hip: many-token matmul on the int8 matrix cores (q8_0 / q4_0 weights)
 size_t mm_planar_bytes(int M, int64_t ncols);

@@ -200,6 +200,16 @@ int g4h_attn_decode(const float *q_dev, const void *kc_dev, const void *vc_dev, 
  * workspace's error word and clears it.  No reference counterpart: the CPU
  * attention (model.c:509-580) has no cross-thread wait. */
 int g4h_attn_status(void *ws_dev, int *failed, void *stream);
+/* The same with the sliding window and KV ring of model.c:517-537: the
+ * current position is n_pos-1 and it attends positions max(0, n_pos -
+ * window) .. n_pos-1 (window 0: all).  ring > 0 (then 0 < window <= ring):
+ * the caches are a ring in which position j's row sits at slot j % ring and
+ * again at slot j % ring + ring (2*ring slots), so every window is one
+ * contiguous run -- the reference keeps one copy in G4_SWA_RING slots.
+ * ws_bytes must cover g4h_attn_workspace_bytes(n_head, hd, min(window, n_pos)). */
+int g4h_attn_decode_window(const float *q_dev, const void *kc_dev, const void *vc_dev, int kv_type, int n_head, int n_kv,
+                           int hd, int n_pos, int window, int ring, float *out_dev, void *ws_dev, size_t ws_bytes,
+                           void *stream);
 /* attn_kernel over a batch of nb new tokens (model.c:509-545 with nb > 1):
  * token b sits at position pos0 + b and attends cached positions
  * [0, pos0 + b] -- causal, the batch's own rows already stored in kc/vc.
@@ -308,6 +318,29 @@ int g4h_forward_batch_heads(g4h_model *m, const int *tokens, int nb, int pos0, f
  * first index of the maximum of logits_dev[b][0..n) (rows 16-byte aligned,
  * n % 4 == 0 when nb > 1).  Asynchronous. */
 int g4h_argmax_rows(const float *logits_dev, int n, int nb, int *out_dev, void *stream);
+
+/* ------------------------------------------------------------- gemma4 ---- */
+/* A gemma4 GGUF model resident on the device: g4_ctx_init (g4run.h:302-303,
+ * model.c:373-477) for the model file parsed by g4_gguf_open (model_file is a
+ * `const g4_model_file *`, include/g4run_abi.h), or straight from a GGUF path
+ * (g4h_gemma_open maps, uploads and unmaps).  Every weight matrix is uploaded
+ * and repacked once; the KV caches (kv_type G4H_F16, G4H_Q8_0 or G4H_Q4_0)
+ * hold n_ctx positions for full layers and a ring of 576 (G4_SWA_RING) for
+ * sliding-window layers.  Limits of this path: head dims 64/128/192/256 with
+ * RoPE over the whole head, 1/2/4/8 query heads per KV head, a window of at
+ * most 512 (G4_SWA_WINDOW_MAX), per-layer width <= 1024.  Synchronous. */
+typedef struct g4h_gemma g4h_gemma;
+int g4h_gemma_create(const void *model_file, int n_ctx, int kv_type, g4h_gemma **out);
+int g4h_gemma_open(const char *path, int n_ctx, int kv_type, g4h_gemma **out);
+int g4h_gemma_free(g4h_gemma *g);
+int g4h_gemma_info(const g4h_gemma *g, int *n_vocab, int *n_embd, int *n_layer, int *n_ctx);
+/* g4_forward_batch_heads (model.c:780-799) of the gemma4 forward: nb (1..64)
+ * host token ids at positions pos0.. (K/V stored): every position's logits
+ * [nb][n_vocab] (soft-capped) into logits_dev and, if hnext_dev, the head
+ * input rms(x)*output_norm [nb][n_embd].  nb = 1 is g4_forward (g4run.h:309-311).
+ * Row b equals the same forward run one token at a time, bit for bit.
+ * Synchronous. */
+int g4h_gemma_forward(g4h_gemma *g, const int *tokens, int nb, int pos0, float *logits_dev, float *hnext_dev, void *stream);
 
 /* ------------------------------------------------------------ sampler ---- */
 /* The sampling chain of sampler.c (g4run.h:464-489) with its settings, RNG,

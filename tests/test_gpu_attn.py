@@ -173,3 +173,51 @@ def test_attention_timeout_reported_by_status(gpu, oracle):
     got = out.download(np.float32, (n_head, hd))
     ref = oracle.attn_decode(q, kh, vh, G.F16, n_head, n_kv, hd, n_pos - 1)
     assert np.all(np.abs(got.astype(np.float64) - ref) <= ATOL + RTOL * np.abs(ref))
+
+
+@pytest.mark.parametrize("kv_type", [1, 8, 2], ids=["f16", "q8_0", "q4_0"])
+@pytest.mark.parametrize("n_head,hd,n_pos,window,ring", [
+    (4, 64, 9, 8, 40), (4, 64, 100, 8, 40), (8, 256, 1000, 512, 576), (8, 256, 700, 512, 576), (2, 128, 300, 300, 0),
+    (4, 64, 50, 1, 40), (8, 128, 5, 512, 576), (8, 256, 1300, 129, 576)])
+def test_window_ring_attention_vs_oracle(gpu, oracle, kv_type, n_head, hd, n_pos, window, ring):
+    """model.c:517-537: a sliding window over a KV ring (GPU: rows stored at
+    slot j % ring and j % ring + ring; oracle: one copy in `ring` slots) and,
+    with ring 0, a window over a linear cache."""
+    G = gpu
+    n_kv = 1
+    slots = 2 * ring if ring else n_pos
+    rows = np.random.default_rng(n_pos + window).standard_normal((2, n_pos, hd)).astype(np.float32)
+    rb = hd * 2 if kv_type == G.F16 else G.row_size(kv_type, hd)
+
+    def stored(x):
+        b = G.Buffer(n_pos * rb)
+        G.kv_store(kv_type, G.Buffer.from_array(x), b, hd, rows=n_pos, dst_stride=rb)
+        return b.download(np.uint8, (n_pos, rb))
+
+    lin = [stored(rows[0]), stored(rows[1])]
+    gpu_c = [np.zeros((slots, rb), np.uint8) for _ in range(2)]
+    ora_c = [np.zeros((ring if ring else n_pos, rb), np.uint8) for _ in range(2)]
+    for j in range(n_pos):                       # the caches as n_pos decode steps leave them
+        for c in range(2):
+            if ring:
+                gpu_c[c][j % ring] = lin[c][j]
+                gpu_c[c][j % ring + ring] = lin[c][j]
+                ora_c[c][j % ring] = lin[c][j]
+            else:
+                gpu_c[c][j] = lin[c][j]
+                ora_c[c][j] = lin[c][j]
+    q = np.random.default_rng(7).standard_normal((n_head, hd)).astype(np.float32)
+    out = G.Buffer(n_head * hd * 4)
+    G.attn_decode_window(G.Buffer.from_array(q), G.Buffer.from_array(gpu_c[0]), G.Buffer.from_array(gpu_c[1]), kv_type,
+                         n_head, n_kv, hd, n_pos, window, ring, out)
+    got = out.download(np.float32, (n_head, hd))
+    pos = n_pos - 1
+    j0 = max(0, pos - window + 1) if window else 0
+    ref = np.zeros((n_head, hd), np.float32)
+    L = oracle.lib()
+    L.g4o_attn_window.argtypes = [oracle._vp] * 3 + [oracle.C.c_int] * 7 + [oracle._vp, oracle.C.c_int]
+    L.g4o_attn_window(q.ctypes.data, ora_c[0].ctypes.data, ora_c[1].ctypes.data, kv_type, n_head, n_kv, hd, pos, j0,
+                      ring if ring else n_pos, ref.ctypes.data, 1)
+    err = np.abs(got.astype(np.float64) - ref)
+    bad = err > ATOL + RTOL * np.abs(ref)
+    assert not bad.any(), f"{bad.sum()} outside tolerance, worst {err.max():.3g}"
