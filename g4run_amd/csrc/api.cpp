@@ -551,7 +551,8 @@ static int matmul_impl(const g4h_tensor *W, const float *x, const void *pre, siz
     const uint8_t *act = (const uint8_t *)pre;
     size_t stride = pre_stride;
     if (x && (uintptr_t)x % 16 == 0 && fused_quant_enabled()) {
-        // q8_0 / q4_0 weights: every chunk quantizes its fp32 tokens in the GEMV prologue
+        // q8_0 / q4_0 weights (and one K-quant token): every chunk quantizes its
+        // fp32 tokens in the GEMV prologue
         if (x_fused(*W, nb)) {
             for (int done = 0; done < nb;) {
                 const int chunk = gemv_chunk_at(*W, nb, done);

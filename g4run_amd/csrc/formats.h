@@ -140,6 +140,49 @@ __device__ __forceinline__ void q8_lds4(const float v[4], int j, bool own, uint8
     }
 }
 
+// q8_K quantization of fp32 activations straight into the LDS layout, with the
+// arithmetic of the standalone quantizer (k_quant.hip, quants.c:146-175), so
+// the staged token is bit-identical to quantizing first.  One wave holds one
+// 256-element superblock sb of token t (lane l: elements 4l..4l+3); the whole
+// wave calls it (the maximum and the 16-element sums are lane shuffles) and
+// writes only with `own` (uniform over the wave).
+__device__ __forceinline__ void q8K_lds4(const float v[4], int sb, bool own, uint8_t *lds, int nb, int t) {
+    const int l = threadIdx.x & 63;
+    // value of largest magnitude, first occurrence on ties (quants.c:150-154):
+    // the wave maximum of |x| (VALU lane exchanges), then the lowest element
+    // index that reaches it (ballots), then that element's signed value
+    const float am = group_max<64>(fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3]))));
+    int first = 256;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const uint64_t m = __ballot(fabsf(v[i]) == am);
+        if (m) first = min(first, 4 * __builtin_ctzll(m) + i);
+    }
+    const int fi = first & 3;
+    const float mine = fi == 0 ? v[0] : fi == 1 ? v[1] : fi == 2 ? v[2] : v[3];
+    const float bv = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, mine), first >> 2));
+    uint32_t pk = 0;
+    int s = 0;
+    float d = 0.0f;
+    if (am != 0.0f) {
+        const float iscale = -127.0f / bv;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            int q = rne_prod(iscale, v[i]);
+            q = q < 127 ? q : 127;
+            pk |= ((uint32_t)q & 0xffu) << (8 * i);
+            s += q;
+        }
+        d = bv * (-1.0f / 127.0f);
+    }
+    s = group_isum<4>(s);                                          // the 16 elements of lanes 4k..4k+3
+    if (!own) return;
+    uint8_t *p = lds + (size_t)t * ActQ8_K::bytes_per_token(nb) + (size_t)sb * ActQ8_K::SB;
+    ((uint32_t *)(p + 16))[l] = pk;
+    if ((l & 3) == 0) ((int16_t *)(p + 272))[l >> 2] = (int16_t)s;
+    if (l == 0) *(float *)(p + 12) = d;
+}
+
 template <int NB>
 __device__ void stage_q8_0(uint8_t *lds, const uint8_t *act, size_t stride, int nb) {
     StageQ8_0 S;

@@ -25,8 +25,10 @@ size_t act_lds_bytes(int nb_tokens, int64_t nblk) { return (size_t)nb_tokens * F
 
 // XQ = 0: the NB activations are GGUF q8_0 / q8_K rows (act, act_stride).
 // XQ > 0: x holds the NB tokens as fp32 rows of ncols (contiguous) and every
-// workgroup quantizes them to q8_0 itself, in LDS (q8_lds4: the arithmetic of
-// the standalone quantizer, so results equal quantize-then-GEMV bit for bit);
+// workgroup quantizes them to q8_0 (q4_0 / q8_0 weights) or q8_K (K-quant
+// weights: one wave per superblock) itself, in LDS (q8_lds4 / q8K_lds4: the
+// arithmetic of the standalone quantizers, so results equal quantize-then-GEMV
+// bit for bit);
 // XQ is the number of 4-float groups per thread (NB*ncols/4 <= XQ*blockDim).
 // The x loads go out before the weight stream and the quantization runs while
 // the weights are in flight; an LDS-only barrier hands the activation over
@@ -43,7 +45,6 @@ __global__ __launch_bounds__(XQ == 4 ? 1024 : 512) void k_gemv(g4h_tensor W, con
     const bool row_ok = row0 < W.nrows;
     const int64_t row = row_ok ? row0 : W.nrows - 1;
     constexpr bool QK = F::type == Q4_0 || F::type == Q8_0;
-    static_assert(XQ == 0 || QK, "the fused quantizer produces q8_0 activations");
 
     // activation loads first, then the weight stream (see formats.h); one
     // K-quant token needs about two q8_K items per thread, both issued here
@@ -78,7 +79,8 @@ __global__ __launch_bounds__(XQ == 4 ? 1024 : 512) void k_gemv(g4h_tensor W, con
         for (int s = 0; s < XQ; s++) {                                   // no branch: keeps the x loads up front
             const int gi = threadIdx.x + s * blockDim.x;
             const int t = gi / gpt;
-            q8_lds4(xv[s], gi - t * gpt, gi < NB * gpt, lds, (int)W.nb, t);
+            if constexpr (QK) q8_lds4(xv[s], gi - t * gpt, gi < NB * gpt, lds, (int)W.nb, t);
+            else q8K_lds4(xv[s], (gi - t * gpt) >> 6, gi < NB * gpt, lds, (int)W.nb, t);   // a wave = a superblock
         }
     } else if constexpr (QK) {
         stage_q8_0_store(stg[0], lds, (int)W.nb, stage_dump<ActQ8_0>(lds, NB, (int)W.nb));
@@ -185,7 +187,10 @@ static hipError_t go(const g4h_tensor &W, const uint8_t *act, size_t stride, con
         hipLaunchKernelGGL((k_gemv<F, NB, LPR, UPL, 0>), dim3(grid), dim3(64 * wpg), lds, s, W, act, stride, x, Y, units);
         return hipGetLastError();
     }
-    if constexpr (F::type == Q4_0 || F::type == Q8_0) {
+    constexpr bool QK = F::type == Q4_0 || F::type == Q8_0;
+    if constexpr (!QK && NB != 1) {
+        return hipErrorInvalidValue;                                 // K-quants: one fused token (gemv_fused_fits)
+    } else {
         int xwpg;
         const int xq = gemv_xq_shape(W.ncols, NB, waves, wpg, &xwpg);
         if (xq == 2) {
@@ -199,7 +204,6 @@ static hipError_t go(const g4h_tensor &W, const uint8_t *act, size_t stride, con
         }
         return hipGetLastError();
     }
-    return hipErrorInvalidValue;
 }
 
 template <class F, int NB>

@@ -93,7 +93,8 @@ hipError_t launch_gemv(const g4h_tensor &W, const uint8_t *act, size_t stride, f
 // thread of the launch holds at most 2 groups of 4 inputs, or 4 for one token
 // (gemv_xq_shape).
 bool gemv_fused_fits(const g4h_tensor &W, int nb) {
-    if (W.type != Q8_0 && W.type != Q4_0) return false;
+    const bool kq = blck(W.type) == 256 && W.type != Q8_K;          // K-quants: q8_K activations, one token
+    if (W.type != Q8_0 && W.type != Q4_0 && !(kq && nb == 1)) return false;
     if (nb != 1 && nb != 2 && nb != 4 && nb != 8) return false;
     int lpr, upl, wpg, xwpg;
     int64_t grid;

@@ -58,9 +58,10 @@ int gemv_p_grid_size();
 hipError_t launch_gemv_p(const g4h_tensor &W, const uint8_t *act, float *Y, const GemvPro &pro, const GemvEpi &epi,
                          hipStream_t s);
 hipError_t launch_gemv(const g4h_tensor &W, const uint8_t *act, size_t stride, float *Y, int nb, hipStream_t s);
-// fp32 tokens x [nb][ncols] quantized to q8_0 inside the GEMV (q8_0 / q4_0
-// weights, nb in {1, 2, 4, 8}, when gemv_fused_fits); bit-identical to
-// launch_quantize_q8_0 followed by launch_gemv
+// fp32 tokens x [nb][ncols] quantized inside the GEMV when gemv_fused_fits:
+// to q8_0 for q8_0 / q4_0 weights (nb in {1, 2, 4, 8}), to q8_K for one
+// token of K-quant weights; bit-identical to the standalone quantizer
+// followed by launch_gemv
 bool gemv_fused_fits(const g4h_tensor &W, int nb);
 hipError_t launch_gemv_x(const g4h_tensor &W, const float *x, float *Y, int nb, hipStream_t s);
 // k_gemv_f16.hip: f16 / bf16 weight rows (W at ws bytes per row, 16-byte

@@ -202,11 +202,14 @@ def test_fused_quantizer_equals_prequantized(gpu, oracle, name, qt):
 @pytest.mark.parametrize("qt,rows,cols,nb", [
     (2, 10240, 2560, 1), (2, 2560, 10240, 1), (8, 4096, 4096, 1), (2, 2048, 11008, 1), (8, 1000, 6400, 1),
     (8, 4096, 2048, 2), (2, 4096, 256, 8),
+    (12, 4096, 11008, 1), (11, 4096, 11008, 1), (10, 4096, 11008, 1), (13, 1000, 2560, 1), (14, 333, 11008, 1),
+    (35, 4096, 4096, 1), (12, 64, 256, 1),
 ])
 def test_in_kernel_quantizer_equals_prequantized(gpu, oracle, qt, rows, cols, nb):
     """The shapes whose fp32 input is quantized inside the GEMV (two groups of
-    four inputs per thread, or four for one token in larger workgroups) give
-    the bits of the GEMV on the separately quantized input."""
+    four inputs per thread, or four for one token in larger workgroups; q8_0
+    for q8_0 / q4_0 weights, q8_K with one wave per superblock for K-quants)
+    give the bits of the GEMV on the separately quantized input."""
     from g4run_amd import synth
     w = synth.weights(qt, rows, cols, seed=rows + cols)
     x = synth.activations(nb, cols, seed=nb)
