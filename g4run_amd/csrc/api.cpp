@@ -401,9 +401,11 @@ static bool x_fused(const g4h_tensor &W, int nb) {
 }
 
 // Token count from which the matrix-core family replaces the GEMV family for
-// q8_0 / q4_0 weights: the measured crossover on q8_0 4096x4096 lies between 16
-// tokens (GEMV 18.5 us, matrix cores 20.3 us) and 32 (33.6 us vs 24.2 us).
-static constexpr int kMfmaMinTokens = 24;
+// q8_0 / q4_0 weights: the measured crossover on q8_0 4096x4096 (graph-timed
+// calls, quantization included) lies between 8 tokens (GEMV 9.5 us, matrix
+// cores 11.5 us) and 16 (17.0 us vs 11.5 us); past 8 tokens the GEMV family
+// takes a second launch.
+static constexpr int kMfmaMinTokens = 9;
 
 static bool mfma_capable(const g4h_tensor *W) { return W && (W->type == Q8_0 || W->type == Q4_0); }
 
@@ -443,8 +445,8 @@ extern "C" int g4h_matmul_describe(const g4h_tensor *W, int nb, int path, char *
     }
     int lpr, upl, wpg;
     int64_t grid;
-    gemv_launch_shape(*W, &lpr, &upl, &wpg, &grid);
     const int chunk = nb >= 8 ? 8 : nb >= 4 ? 4 : nb >= 2 ? 2 : 1;
+    gemv_launch_shape(*W, &lpr, &upl, &wpg, &grid, chunk);
     upl = gemv_upl_final(W->type, W->nb, chunk, lpr, upl);
     snprintf(buf, len, "k_gemv<%s,nb=%d,lpr=%d,upl=%d> grid=%lld block=%d (x%d launches); fp32 x %s", type_name(W->type), chunk,
              lpr, upl, (long long)grid, 64 * wpg, (nb + chunk - 1) / chunk,

@@ -129,19 +129,35 @@ __global__ __launch_bounds__(XQ == 4 ? 1024 : 512) void k_gemv(g4h_tensor W, con
 
 // Waves per workgroup chosen so the grid is (close to) a multiple of the 256
 // CUs with equal rows per workgroup: every CU streams the same bytes.
-static inline int gemv_waves_per_group(int64_t nrows, int rpw) {
+// `stage` is the cost of one workgroup's activation staging in units of one
+// wave's rows: 0 for one token (measured: its staging hides under the weight
+// stream), half a row per restaged token row otherwise (gemv_stage_cost).
+static inline int gemv_waves_per_group(int64_t nrows, int rpw, double stage = 0.0) {
     const int64_t waves = (nrows + rpw - 1) / rpw;
     if (const char *e = getenv("G4H_GEMV_WPG")) return atoi(e) < 1 ? 1 : atoi(e) > 8 ? 8 : atoi(e);
-    // minimise the waves of the busiest CU, ceil(grid/256)*wpg, preferring
-    // larger groups (fewer activation stagings) on ties
+    // minimise the busiest CU's work, ceil(grid/256) * (wpg + stage),
+    // preferring larger groups (fewer activation stagings) on ties
     int best = 1;
-    int64_t best_cost = INT64_MAX;
+    double best_cost = 1e300;
     for (int w = 1; w <= 8; w++) {
         const int64_t grid = (waves + w - 1) / w;
-        const int64_t cost = (grid + 255) / 256 * w;
+        const double cost = (double)((grid + 255) / 256) * (w + stage);
         if (cost <= best_cost) { best_cost = cost; best = w; }
     }
     return best;
+}
+
+// Staging cost of nb > 1 tokens for gemv_waves_per_group: each token's
+// activation row (q8_0 for q8_0 / q4_0 weights, q8_K for K-quants) against
+// the rpw weight rows of one wave, at half the cost of a streamed weight byte
+// (the activations come from L2).  Without it 8 tokens of q8_0 11008x4096
+// ran one-row workgroups that each staged all 8 rows: 82.6 us against 29.6 us
+// for the 4096x11008 transpose.
+static inline double gemv_stage_cost(int type, int64_t nblk, int nb, int rpw) {
+    if (nb <= 1) return 0.0;
+    const bool kq = blck(type) == 256;
+    const double act = kq ? 292.0 * nblk : 34.0 * nblk;               // q8_K / q8_0 bytes per token row
+    return 0.5 * nb * act / ((double)rpw * (double)bsize(type) * (double)nblk);
 }
 
 // 4-float groups per thread the fused quantizer needs (0 = no fused variant).
@@ -179,7 +195,7 @@ static inline int gemv_xq_shape(int64_t ncols, int nb, int64_t waves, int wpg, i
 template <class F, int NB, int LPR, int UPL>
 static hipError_t go(const g4h_tensor &W, const uint8_t *act, size_t stride, const float *x, float *Y, int units, hipStream_t s) {
     constexpr int RPW = 64 / LPR;
-    const int wpg = gemv_waves_per_group(W.nrows, RPW);
+    const int wpg = gemv_waves_per_group(W.nrows, RPW, gemv_stage_cost(W.type, W.nb, NB, RPW));
     const int64_t waves = (W.nrows + RPW - 1) / RPW;
     const unsigned grid = (unsigned)((waves + wpg - 1) / wpg);
     const size_t lds = act_lds_bytes<F>(NB, W.nb);

@@ -12,17 +12,19 @@
 //   acc[t][r] = fma(float(isum_b[t][r]), d_a[t][b] * d_w[r][b], acc[t][r]),
 // blocks in increasing order (a different fp32 order from the GEMV family,
 // within the path's fp32 tolerance).  q4_0 nibbles are unpacked to q-8 in
-// registers.  Each output keeps four fp32 partial sums (block residue mod 4)
-// added in a fixed order, so a token's result does not depend on the batch
-// size or on the tile variant (the x4 contract of g4run.h:148-157 within this
-// family).
+// registers.  Each output keeps four fp32 partial sums (residue pair
+// b / 2 mod 4 of block b) added in a fixed order, so a token's result does not
+// depend on the batch size or on the kernel variant (the x4 contract of
+// g4run.h:148-157 within this family).
 //
 // Activations are first laid out planar (qa [M][nb][32] int8, da [M][nb] fp16)
-// so every operand load is an aligned 16-byte load.  Kernels: k_mm_mfma, one
-// 32 x 32 tile per workgroup whose blocks are split over 4 waves and added in
-// wave order through LDS (fewer tokens: enough waves in flight to stream the
-// weights), and k_mm_lds, 64 x 128 tiles staged through LDS in 8-block stages
+// so every operand load is an aligned 16-byte load.  Kernels: k_mm_few, 16-row
+// strips that read each weight byte once for up to 64 tokens (their own
+// tile-major activation layout); k_mm_mfma, one 32 x 32 tile per workgroup
+// whose residue pairs are split over 4 waves and added in wave order through
+// LDS; and k_mm_lds, 64 x 128 tiles staged through LDS in 8-block stages
 // shared by 8 waves (many tokens: 1/8 of the operand traffic per output).
+#include <algorithm>
 #include <cstdio>
 #include <type_traits>
 
@@ -55,15 +57,16 @@ __device__ __forceinline__ v4i q4_half(v4i w, int kh) {
     return r;
 }
 
-template <int WT, int WM, int WN, int KS, int KB>
+template <int WT, int WM, int WN, int KB>
 __global__ __launch_bounds__(256) void k_mm_mfma(g4h_tensor W, const int8_t *__restrict__ qa,
                                                   const uint16_t *__restrict__ da, int M, float *__restrict__ Y) {
-    // Four partial sums per output, one per block residue mod 4, each over its
-    // blocks in increasing order, then ((p0 + p1) + p2) + p3: the same fp32
-    // arithmetic whether one wave holds all four (KS = 1) or KS waves split them.
-    constexpr int NR = 4 / KS;                                  // residues per wave
-    static_assert(KB % NR == 0 && 4 % KS == 0, "tile shape");
-    __shared__ float red[KS > 1 ? (KS - 1) * 64 * 16 : 1];
+    // Four partial sums per output, one per residue pair (the blocks b with
+    // b / 2 mod 4 = r), each over its blocks in increasing order, then
+    // ((p0 + p1) + p2) + p3.  Wave ks of the four on a tile holds residue
+    // pair ks: blocks 8 j + 2 ks and 8 j + 2 ks + 1 for j = 0, 1, ...
+    constexpr int KS = 4;
+    static_assert(KB % 2 == 0, "a set is whole pair steps");
+    __shared__ float red[(KS - 1) * 64 * 16];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int wm = wave % WM, wn = (wave / WM) % WN, ks = wave / (WM * WN);
     const int m0 = (blockIdx.y * WM + wm) * 32, n0 = (blockIdx.x * WN + wn) * 32;
@@ -76,34 +79,33 @@ __global__ __launch_bounds__(256) void k_mm_mfma(g4h_tensor W, const int8_t *__r
     const uint8_t *pw = WT == Q8_0 ? W.qs + (size_t)row * nb * 32 + 16 * kh : W.qs + (size_t)row * nb * 16;
     const uint16_t *pdw = (const uint16_t *)W.sc + (size_t)row * nb;
 
-    v16f acc[NR];
+    v16f acc;
 #pragma unroll
-    for (int q = 0; q < NR; q++)
-#pragma unroll
-        for (int r = 0; r < 16; r++) acc[q][r] = 0.0f;
+    for (int r = 0; r < 16; r++) acc[r] = 0.0f;
     const v16i zi = {};
     const v16f zf = {};
-    // operands of KB blocks; two sets alternate so the next set's loads are in
-    // flight while the current one is multiplied
+    // operands of KB blocks (KB / 2 pair steps); two sets alternate so the
+    // next set's loads are in flight while the current one is multiplied
     struct Ops {
         v4i a[KB], w[KB];
         uint16_t sa[KB], sw[KB];
     };
-    auto load = [&](Ops &o, int b0) {
+    // block k of the set that starts at pair step j0
+    auto blk = [&](int j0, int k) { return 8 * (j0 + (k >> 1)) + 2 * ks + (k & 1); };
+    auto load = [&](Ops &o, int j0) {
 #pragma unroll
         for (int k = 0; k < KB; k++) {
-            const int b = min(b0 + k * KS, nb - 1);
+            const int b = min(blk(j0, k), nb - 1);
             o.a[k] = *(const v4i *)(pa + (size_t)b * 32);
             o.w[k] = *(const v4i *)(pw + (size_t)b * (WT == Q8_0 ? 32 : 16));
             o.sa[k] = pda[b];
             o.sw[k] = pdw[b];
         }
     };
-    // wave ks takes blocks ks, ks + KS, ...; block b0 + k*KS has residue (ks + k*KS) % 4
-    auto mul = [&](const Ops &o, int b0) {
+    auto mul = [&](const Ops &o, int j0) {
 #pragma unroll
         for (int k = 0; k < KB; k++) {
-            if (b0 + k * KS < nb) {                                  // uniform
+            if (blk(j0, k) < nb) {                                   // uniform
                 const v4i wv = WT == Q8_0 ? o.w[k] : q4_half(o.w[k], kh);
                 const v16i is = __builtin_amdgcn_mfma_i32_32x32x32_i8(o.a[k], wv, zi, 0, 0, 0);
                 v8h ha = {}, hw = {};
@@ -112,45 +114,36 @@ __global__ __launch_bounds__(256) void k_mm_mfma(g4h_tensor W, const int8_t *__r
                     hw[0] = __builtin_bit_cast(_Float16, o.sw[k]);
                 }
                 const v16f sc = __builtin_amdgcn_mfma_f32_32x32x16_f16(ha, hw, zf, 0, 0, 0);
-                v16f &p = acc[k % NR];
 #pragma unroll
-                for (int r = 0; r < 16; r++) p[r] = __builtin_fmaf((float)is[r], sc[r], p[r]);
+                for (int r = 0; r < 16; r++) acc[r] = __builtin_fmaf((float)is[r], sc[r], acc[r]);
             }
         }
     };
-    constexpr int STEP = KS * KB;
+    constexpr int STEP = KB / 2;
     Ops o0, o1;
-    load(o0, ks);
-    for (int b0 = ks;;) {
-        if (b0 + STEP < nb) load(o1, b0 + STEP);
-        mul(o0, b0);
-        b0 += STEP;
-        if (b0 >= nb) break;
-        if (b0 + STEP < nb) load(o0, b0 + STEP);
-        mul(o1, b0);
-        b0 += STEP;
-        if (b0 >= nb) break;
+    load(o0, 0);
+    for (int j0 = 0;;) {
+        if (blk(j0 + STEP, 0) < nb) load(o1, j0 + STEP);
+        mul(o0, j0);
+        j0 += STEP;
+        if (blk(j0, 0) >= nb) break;
+        if (blk(j0 + STEP, 0) < nb) load(o0, j0 + STEP);
+        mul(o1, j0);
+        j0 += STEP;
+        if (blk(j0, 0) >= nb) break;
     }
-    v16f out = acc[0];
-    if constexpr (KS == 1) {
+    // partials of waves 1..3 through LDS, added to wave 0's in wave order
+    v16f out = acc;
+    if (ks > 0) {
 #pragma unroll
-        for (int q = 1; q < 4; q++)
-#pragma unroll
-            for (int r = 0; r < 16; r++) out[r] += acc[q][r];
-    } else {
-        // partials of waves 1..KS-1 through LDS, added to wave 0's in wave order
-        static_assert(KS == 4, "KS is 1 or 4");
-        if (ks > 0) {
-#pragma unroll
-            for (int r = 0; r < 16; r++) red[((ks - 1) * 16 + r) * 64 + lane] = out[r];
-        }
-        __syncthreads();
-        if (ks > 0) return;
-#pragma unroll
-        for (int q = 1; q < KS; q++)
-#pragma unroll
-            for (int r = 0; r < 16; r++) out[r] += red[((q - 1) * 16 + r) * 64 + lane];
+        for (int r = 0; r < 16; r++) red[((ks - 1) * 16 + r) * 64 + lane] = out[r];
     }
+    __syncthreads();
+    if (ks > 0) return;
+#pragma unroll
+    for (int q = 1; q < KS; q++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) out[r] += red[((q - 1) * 16 + r) * 64 + lane];
     // C[i][j]: j = lane % 32 (weight row), i = 8*(r/4) + 4*(lane/32) + r%4 (token)
     const int64_t n = n0 + li;
     if (n < W.nrows) {
@@ -173,7 +166,7 @@ __global__ __launch_bounds__(256) void k_mm_mfma(g4h_tensor W, const int8_t *__r
 // MFMA for the exact block sums, the exact scale outer product d_a * d_w (here
 // two blocks' from one v_mfma_f32_32x32x1_2b_f32, lanes 0..31 block k and
 // 32..63 block k + 1: an fp16 x fp16 product is exact in fp32 either way), an
-// fma into the accumulator of the block's residue mod 4, and at the end
+// fma into the accumulator of the block's residue pair, and at the end
 // ((p0 + p1) + p2) + p3 -- so every output is bit-identical to k_mm_mfma's.
 constexpr int MML_KB = 8;                                           // blocks per stage
 
@@ -276,7 +269,7 @@ __global__ __launch_bounds__(64 * TM * TN, 2) void k_mm_lds(g4h_tensor W, const 
     // every epilogue of the stage below the LDS stores, which keeps all the
     // stage's MFMA results live at once
     auto epi = [&](int k, const v16i &is, const v32f &sc, int r0 = 0, int r1 = 16) {
-        v16f &p = acc[k & 3];                                       // KB % 4 == 0: residue of the block
+        v16f &p = acc[(k >> 1) & 3];                                // KB % 8 == 0: residue pair of the block
         const int o = 16 * (k & 1);
 #pragma unroll
         for (int r = r0; r < r1; r++) {
@@ -371,25 +364,36 @@ __global__ __launch_bounds__(64 * TM * TN, 2) void k_mm_lds(g4h_tensor W, const 
     }
 }
 
-// Few tokens (M <= 32): 16-row strips.  A workgroup of 4 waves owns 16 weight
-// rows and every token, so each weight byte is read from HBM once per call.
-// The activations of a chunk of KC blocks (all tokens) are copied into LDS
-// with direct-to-LDS loads (no registers, [block][token] layout so a wave's
-// operand read is one contiguous 512-byte run), the next chunk's copy issued
-// while the current one is used.  Wave w multiplies blocks w, w + 4, ... (the
-// blocks of residue w mod 4): its weight operands (16 rows x 8 bytes per lane
-// and block) and scales stream straight into registers MMS_D of its blocks
-// ahead -- about 36 KB per CU in flight and no barrier inside a chunk.  Per
-// block and 16 x 16 (token x row) tile: one v_mfma_i32_16x16x32_i8 for the
-// exact block sums, one v_mfma_f32_16x16x16_f16 for the exact scale outer
-// product d_a * d_w (only k = 0 non-zero), and an fma into the wave's
-// partial -- the arithmetic of k_mm_mfma (residue partials, blocks in
-// increasing order, ((p0 + p1) + p2) + p3 through LDS), so every output is
-// the same bits.
-constexpr int MMS_D = 16;            // a wave's blocks in flight
-constexpr int MMS_MAXM = 32;
+// Few tokens (M <= 64): 16-row strips.  A workgroup of 4 waves owns 16 weight
+// rows and every token, so each weight byte is read from HBM once per call;
+// there is no LDS staging and no barrier until the final sum.  Wave w takes
+// the blocks of residue pair w (blocks 8 j + 2 w, 8 j + 2 w + 1: a "pair
+// step").  Per pair step and lane: one 16-byte weight load (q8_0; 8 bytes of
+// nibbles for q4_0) covering both blocks of its row (lane groups 0, 1 block
+// 2 p, groups 2, 3 block 2 p + 1), one 2-byte weight scale, one 16-byte
+// activation load per 16-token tile and one 8-byte load of four tiles'
+// activation scales.  A wave takes its pair steps in segments of few_seg
+// steps whose loads are all issued before the segment's first multiply (the
+// wave's memory-level parallelism: 16 KB of weights per wave for one tile).
+// One v_permlane32_swap per dword pair turns the loaded halves into the
+// operands of the two blocks' int8 MFMAs (lane group g then holds slice
+// sigma(g) of the block: (0, 2, 1, 3) for q8_0, g for q4_0), and the
+// activations are laid out so that each lane's 16 bytes are its slice of both
+// blocks (k_quantize_few).  Per block and 16 x 16 tile: one
+// v_mfma_i32_16x16x32_i8 for the exact block sums, one v_mfma_f32_16x16x16_f16
+// for the exact scale product d_a * d_w (one non-zero k per lane group picks
+// the block and tile), and an fma into the tile's accumulator -- the
+// arithmetic of k_mm_mfma and k_mm_lds, so every output is the same bits.
+//
+// Activation layout for M <= 64 (MT 16-token tiles, np = ceil(nb / 2) block
+// pairs, padding tokens and the padding block zero):
+//   qa [np][MT][16 tok][4 slices][2 blocks][8 bytes]
+//   da [np][16 tok][2 blocks][4 tiles] fp16 (tile slots past MT zero)
+constexpr int MMF_MAXM = 64;
+
 
 typedef long v1l;
+typedef int v2i __attribute__((ext_vector_type(2)));
 
 // f(integral_constant<int, I>) for I = 0 .. N-1 as straight-line code (every
 // array index a constant from the start, so the arrays stay in registers)
@@ -401,133 +405,125 @@ __device__ __forceinline__ void static_for(F &&f) {
     }
 }
 
-// s_waitcnt immediate that waits until at most n vector-memory operations
-// (loads, including direct-to-LDS loads) of this wave are outstanding
-constexpr int vmcnt_imm(int n) { return (n & 15) | (7 << 4) | (15 << 8) | ((n >> 4) << 14); }
+size_t mm_few_bytes(int M, int64_t ncols) {
+    const int64_t np = (ncols / 32 + 1) / 2, mt = (M + 15) / 16;
+    return (((size_t)np * mt * 1024 + 255) & ~(size_t)255) + (size_t)np * 256;
+}
 
+// pair steps per segment: a segment's loads (MT + 3 per step) are all issued
+// before its first multiply -- straight-line code, so the compiler's memory
+// counter waits are exact (a register ring carried around a loop is undone by
+// the compiler: the loads sink to the loop head and every iteration drains) --
+// within the 63 loads the memory counter tracks and the register file
 template <int MT>
-struct StripGeo {
-    static constexpr int MP = 16 * MT;                                // tokens staged (padded)
-    static constexpr int KC = MT == 1 ? 128 : 64;                    // blocks per activation chunk
-    static constexpr int QCH = MP * KC * 2;                          // 16-byte chunks of a chunk's quants
-    static constexpr int SCH = MP * KC;                              // 2-byte scales of a chunk
-    static_assert(QCH % 256 == 0 && SCH % 256 == 0, "whole DMA instructions per thread");
-    static_assert(KC % (4 * MMS_D) == 0, "a chunk is whole prefetch rounds");
-};
-
-// the LDS pointer type of the direct-to-LDS load builtin
-typedef void __attribute__((address_space(3))) *lds_ptr_t;
-typedef const void __attribute__((address_space(1))) *glb_ptr_t;
+constexpr int few_seg() { return MT == 1 ? 16 : MT == 2 ? 8 : MT == 3 ? 6 : 4; }
 
 template <int WT, int MT>
-__global__ __launch_bounds__(256) void k_mm_strip(g4h_tensor W, const int8_t *__restrict__ qa,
-                                                   const uint16_t *__restrict__ da, int M, float *__restrict__ Y) {
-    using G = StripGeo<MT>;
-    constexpr int MP = G::MP, KC = G::KC, WB = WT == Q8_0 ? 32 : 16;
-    // two activation chunk buffers, separate objects so that the compiler can
-    // tell a read of one from a direct-to-LDS write of the other
-    __shared__ __align__(16) int8_t As0[KC * MP * 32], As1[KC * MP * 32];     // [blk][tok][32]
-    __shared__ __align__(16) uint16_t Ad0[KC * MP], Ad1[KC * MP];             // [blk][tok]
+__global__ __launch_bounds__(256) void k_mm_few(g4h_tensor W, const int8_t *__restrict__ qa,
+                                                const uint16_t *__restrict__ da, int M, float *__restrict__ Y) {
+    constexpr int S = few_seg<MT>(), WB = WT == Q8_0 ? 32 : 16;
+    using WV = std::conditional_t<WT == Q8_0, v4i, v2i>;
     __shared__ float red[3 * MT * 4 * 64];
-    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    // the wave index in a scalar register: the first lane's thread index / 64
+    // (the compiler folds a readfirstlane of threadIdx.x / 64 itself away and
+    // then keeps the value in a vector register).  Every per-step branch and
+    // address part below is then scalar, with no exec-masked flow blocks.
+    const int t = threadIdx.x, lane = t & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(t) >> 6;
     const int li = lane & 15, kg = lane >> 4;
-    const int nb = (int)W.nb, nch = (nb + KC - 1) / KC;
+    const int nb = (int)W.nb, np = (nb + 1) >> 1;
+    const int nj = (np - wave + 3) >> 2;                                    // this wave's pair steps
     const int64_t row = min((int64_t)blockIdx.x * 16 + li, W.nrows - 1);
+    // the slice of a block this lane group feeds the int8 MFMA after the swap
+    const int sl = WT == Q8_0 ? ((kg & 1) << 1) | (kg >> 1) : kg;
+    // per-lane 32-bit byte offsets, fixed over the loop; the per-step part is
+    // uniform (the launch keeps the weight planes under 4 GB).  The weight
+    // bytes of an odd last pair's missing block are the next row's (or, past
+    // the last row, the scale plane's that follows the quants): loaded, never
+    // used.  Its scale index is clamped to the row.
+    const uint32_t wlane = (uint32_t)((uint64_t)row * nb * WB) + (WB / 2) * kg;
+    const uint32_t slane1 = (uint32_t)((uint64_t)row * nb * 2) + 2 * (kg & 1), slane0 = slane1 - 2 * (kg & 1);
+    const uint32_t alane = li * 64 + 16 * sl, dlane = 8 * (2 * li + (kg & 1));
 
-    // chunk c of the activations: this thread's 16-byte runs ([blk][tok][half]
-    // order) and 2-byte scales ([blk][tok]) into registers, later into LDS
-    constexpr int QPT = G::QCH / 256, SPT = G::SCH / 256;
-    v4i aq[QPT];
-    uint16_t ad[SPT];
-    auto a_issue = [&](int c) __attribute__((always_inline)) {
-        static_for<0, QPT>([&](auto I) {
-            const int q = I.value * 256 + t;
-            const int blk = q / (MP * 2), tok = min((q >> 1) % MP, M - 1), half = q & 1;
-            const int b = min(c * KC + blk, nb - 1);
-            aq[I.value] = *(const v4i *)(qa + ((size_t)tok * nb + b) * 32 + 16 * half);
-        });
-        static_for<0, SPT>([&](auto I) {
-            const int q = I.value * 256 + t;
-            const int blk = q / MP, tok = min(q % MP, M - 1);
-            const int b = min(c * KC + blk, nb - 1);
-            ad[I.value] = da[(size_t)tok * nb + b];
-        });
+    struct Op {
+        WV w;
+        v4i a[MT];
+        uint64_t d;
+        uint32_t s;
     };
-    auto a_store = [&](int8_t *As, uint16_t *Ad) __attribute__((always_inline)) {
-        static_for<0, QPT>([&](auto I) { *(v4i *)(As + (size_t)(I.value * 256 + t) * 16) = aq[I.value]; });
-        static_for<0, SPT>([&](auto I) { Ad[I.value * 256 + t] = ad[I.value]; });
-    };
-    // the wave's j-th block (block 4 j + wave), clamped to the last block
-    struct WOp {
-        v1l q;
-        uint16_t d;
-    };
-    auto w_load = [&](int j) __attribute__((always_inline)) -> WOp {
-        const int b = min(4 * j + wave, nb - 1);
-        WOp o;
-        if constexpr (WT == Q8_0) o.q = *(const v1l *)(W.qs + ((size_t)row * nb + b) * WB + 8 * kg);
-        else o.q = *(const v1l *)(W.qs + ((size_t)row * nb + b) * WB + 8 * (kg & 1));
-        o.d = ((const uint16_t *)W.sc)[(size_t)row * nb + b];
+    // pair step j of this wave: pair 4 j + wave, clamped to the last pair
+    auto load = [&](int j) __attribute__((always_inline)) -> Op {
+        const int p = min(4 * j + wave, np - 1);
+        Op o;
+        o.w = *(const WV *)(W.qs + (size_t)p * 2 * WB + wlane);
+        o.s = *(const uint16_t *)(W.sc + (size_t)p * 4 + (2 * p + 1 < nb ? slane1 : slane0));
+        // a step past the wave's last, or the missing block of an odd last
+        // pair, gets weight scale 0: its products add +0 to the accumulator,
+        // which never holds -0, so the sums keep their bits
+        const bool live = j < nj, live1 = live && 2 * p + 1 < nb;            // uniform
+        if (!((kg & 1) ? live1 : live)) o.s = 0;
+        static_for<0, MT>([&](auto I) { o.a[I.value] = *(const v4i *)(qa + ((size_t)p * MT + I.value) * 1024 + alane); });
+        o.d = *(const uint64_t *)((const uint8_t *)da + (size_t)p * 256 + dlane);
         return o;
     };
-    const v4i zi = {};
-    const v4f zf = {};
     v4f acc[MT];
 #pragma unroll
     for (int tt = 0; tt < MT; tt++) acc[tt] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
-    auto mac = [&](const WOp &o, const int8_t *As, const uint16_t *Ad, int blk) __attribute__((always_inline)) {
-        v1l wv = o.q;
-        if constexpr (WT == Q4_0) {
-            // elements 8 kg .. 8 kg + 7: low nibbles of bytes 8 (kg & 1).. for kg < 2, high nibbles for kg >= 2
-            // (quants.c:542-545), each as q - 8
-            const uint64_t u = (uint64_t)o.q;
-            const uint32_t sh = 4 * (kg >> 1);
-            const uint32_t lo = ((uint32_t)u >> sh) & 0x0F0F0F0Fu, hi = ((uint32_t)(u >> 32) >> sh) & 0x0F0F0F0Fu;
-            wv = (v1l)(((uint64_t)((hi + 0x78787878u) ^ 0x80808080u) << 32) | ((lo + 0x78787878u) ^ 0x80808080u));
+    const v4i zi = {};
+    const v4f zf = {};
+    auto mac = [&](const Op &o) __attribute__((always_inline)) {
+        uint32_t x0, x1, y0, y1;
+        if constexpr (WT == Q8_0) {
+            x0 = (uint32_t)o.w[0], x1 = (uint32_t)o.w[1], y0 = (uint32_t)o.w[2], y1 = (uint32_t)o.w[3];
+        } else {
+            // bytes 8 (kg & 1) .. + 7 of a block: low nibbles are slice kg & 1,
+            // high nibbles slice 2 + (kg & 1) (quants.c:542-545), each as q - 8
+            const uint32_t u0 = (uint32_t)o.w[0], u1 = (uint32_t)o.w[1];
+            x0 = ((u0 & 0x0F0F0F0Fu) + 0x78787878u) ^ 0x80808080u;
+            x1 = ((u1 & 0x0F0F0F0Fu) + 0x78787878u) ^ 0x80808080u;
+            y0 = (((u0 >> 4) & 0x0F0F0F0Fu) + 0x78787878u) ^ 0x80808080u;
+            y1 = (((u1 >> 4) & 0x0F0F0F0Fu) + 0x78787878u) ^ 0x80808080u;
         }
-        v4h hw = {};
-        if (kg == 0) hw[0] = __builtin_bit_cast(_Float16, o.d);
+        // lanes 32..63 of x trade with lanes 0..31 of y: x becomes block 2 p
+        // in all four lane groups, y block 2 p + 1
+        const auto s0 = __builtin_amdgcn_permlane32_swap(x0, y0, false, false);
+        const auto s1 = __builtin_amdgcn_permlane32_swap(x1, y1, false, false);
+        const v1l bx = (v1l)(((uint64_t)s1[0] << 32) | s0[0]), by = (v1l)(((uint64_t)s1[1] << 32) | s0[1]);
+        // scale operands: lane group 0 holds d_w of block 2 p, group 1 that of
+        // 2 p + 1; hw[h][e] has it at k = 4 h + e, where the activation
+        // operand holds d_a of block h for tile 2 (tt / 2) + e
+        const _Float16 sw = __builtin_bit_cast(_Float16, (uint16_t)o.s);
+        v4h hw[2][2] = {};
+        if (kg == 0) hw[0][0][0] = sw, hw[0][1][1] = sw;
+        if (kg == 1) hw[1][0][0] = sw, hw[1][1][1] = sw;
 #pragma unroll
         for (int tt = 0; tt < MT; tt++) {
-            const v1l av = *(const v1l *)(As + (blk * MP + tt * 16 + li) * 32 + 8 * kg);
-            const v4i is = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, wv, zi, 0, 0, 0);
-            v4h ha = {};
-            if (kg == 0) ha[0] = __builtin_bit_cast(_Float16, Ad[blk * MP + tt * 16 + li]);
-            const v4f sc = __builtin_amdgcn_mfma_f32_16x16x16f16(ha, hw, zf, 0, 0, 0);
+            const v2i dv = {(int)(uint32_t)(o.d >> (32 * (tt >> 1))), 0};
+            const v4h ha = __builtin_bit_cast(v4h, dv);
+            const v1l a0 = (v1l)(((uint64_t)(uint32_t)o.a[tt][1] << 32) | (uint32_t)o.a[tt][0]);
+            const v1l a1 = (v1l)(((uint64_t)(uint32_t)o.a[tt][3] << 32) | (uint32_t)o.a[tt][2]);
+            const v4i i0 = __builtin_amdgcn_mfma_i32_16x16x32_i8(a0, bx, zi, 0, 0, 0);
+            const v4f c0 = __builtin_amdgcn_mfma_f32_16x16x16f16(ha, hw[0][tt & 1], zf, 0, 0, 0);
 #pragma unroll
-            for (int r = 0; r < 4; r++) acc[tt][r] = __builtin_fmaf((float)is[r], sc[r], acc[tt][r]);
+            for (int r = 0; r < 4; r++) acc[tt][r] = __builtin_fmaf((float)i0[r], c0[r], acc[tt][r]);
+            const v4i i1 = __builtin_amdgcn_mfma_i32_16x16x32_i8(a1, by, zi, 0, 0, 0);
+            const v4f c1 = __builtin_amdgcn_mfma_f32_16x16x16f16(ha, hw[1][tt & 1], zf, 0, 0, 0);
+#pragma unroll
+            for (int r = 0; r < 4; r++) acc[tt][r] = __builtin_fmaf((float)i1[r], c1[r], acc[tt][r]);
         }
     };
 
-    // issue order keeps every wait exact: chunk 0's activations, then the
-    // first MMS_D weight blocks; each chunk's activations are issued ahead of
-    // the weight blocks of that chunk's rounds
-    a_issue(0);
-    WOp wr[MMS_D];
-    static_for<0, MMS_D>([&](auto I) { wr[I.value] = w_load(I.value); });
-    const int nj = (nb - wave + 3) / 4;                                  // this wave's blocks
-    // one chunk: its activations from registers into LDS (they were issued
-    // ahead of every weight load not yet consumed, so the wait for them waits
-    // for nothing still streaming), a bare barrier (a fenced __syncthreads would
-    // also wait for the weight loads in flight), the next chunk's activation
-    // loads, then the wave's blocks in rounds of MMS_D.  Two buffers: chunk c
-    // is stored while no wave reads the other one any more.
-    auto chunk = [&](int c, int8_t *As, uint16_t *Ad) __attribute__((always_inline)) {
-        a_store(As, Ad);
-        lds_barrier();
-        if (c + 1 < nch) a_issue(c + 1);
-        for (int r0 = 0; r0 < KC / 4; r0 += MMS_D) {
-            static_for<0, MMS_D>([&](auto I) {
-                const int jl = r0 + I.value, j = c * (KC / 4) + jl;
-                const WOp o = wr[I.value];
-                wr[I.value] = w_load(j + MMS_D);
-                if (j < nj) mac(o, As, Ad, 4 * jl + wave);               // uniform
-            });
-        }
-    };
-    for (int c = 0; c < nch; c += 2) {
-        chunk(c, As0, Ad0);
-        if (c + 1 < nch) chunk(c + 1, As1, Ad1);
+    for (int j0 = 0; j0 < nj; j0 += S) {
+        Op ops[S];
+        static_for<0, S>([&](auto I) { ops[I.value] = load(j0 + I.value); });
+        // scheduling barriers: every load of the segment before the first
+        // multiply, and one step's multiplies at a time (left alone the
+        // compiler hoists the whole segment's MFMAs and runs out of registers)
+        __builtin_amdgcn_sched_barrier(0);
+        static_for<0, S>([&](auto I) {
+            mac(ops[I.value]);
+            __builtin_amdgcn_sched_barrier(0);
+        });
     }
 
     // ((p0 + p1) + p2) + p3 through LDS; C[i][j]: i = 4 kg + r (token), j = li (row)
@@ -553,19 +549,32 @@ __global__ __launch_bounds__(256) void k_mm_strip(g4h_tensor W, const int8_t *__
     }
 }
 
-// x fp32 [M][ncols] (row stride xs floats) -> planar q8_0 with the quantizer
-// arithmetic of quants.c:74-109 (8 lanes per block).  A thread quantizes QP
-// groups of 4 inputs, 256 groups apart, all loads issued first.
+// byte offset of codes e .. (block b, token m) in the few-token layout, and
+// the fp16 index of its scale
+__device__ __forceinline__ size_t few_q(int64_t b, int m, int mt, int e) {
+    return ((((size_t)(b >> 1) * mt + (m >> 4)) * 16 + (m & 15)) * 64) + 16 * (e >> 3) + 8 * (b & 1) + (e & 7);
+}
+__device__ __forceinline__ size_t few_d(int64_t b, int m) { return ((((size_t)(b >> 1) * 16 + (m & 15)) * 2 + (b & 1)) * 4) + (m >> 4); }
+
+// x fp32 [M][ncols] (row stride xs floats) -> q8_0 codes and fp16 scales with
+// the quantizer arithmetic of quants.c:74-109 (8 lanes per block), laid out
+// token-major (qa [M][nb][32], da [M][nb]) or, FEW, in k_mm_few's layout of
+// mt tiles: there grid.y also covers the padding tokens up to an even tile
+// count and grid.x the padding block of an odd nb, which get zero codes and
+// scales.  A thread quantizes QP groups of 4 inputs, 256 groups apart, all
+// loads issued first.
 constexpr int QP = 4;
-__global__ __launch_bounds__(256) void k_quantize_planar(const float *__restrict__ x, size_t xs, int64_t ncols, int M,
+template <bool FEW>
+__global__ __launch_bounds__(256) void k_quantize_planar(const float *__restrict__ x, size_t xs, int64_t ncols, int M, int mt,
                                                          int8_t *__restrict__ qa, uint16_t *__restrict__ da) {
     const int64_t ng = ncols / 4, nb = ncols / 32;
+    const int64_t ngo = FEW ? ((nb + 1) & ~(int64_t)1) * 8 : ng;     // groups written per token
     const int m = blockIdx.y;
     float v[QP][4];
 #pragma unroll
     for (int j = 0; j < QP; j++) {
         const int64_t gi = (int64_t)blockIdx.x * 256 * QP + j * 256 + threadIdx.x;
-        if (gi < ng) f4(ldf4(x + (size_t)m * xs + 4 * gi), v[j]);
+        if (m < M && gi < ng) f4(ldf4(x + (size_t)m * xs + 4 * gi), v[j]);
         else v[j][0] = v[j][1] = v[j][2] = v[j][3] = 0.0f;
     }
 #pragma unroll
@@ -577,33 +586,62 @@ __global__ __launch_bounds__(256) void k_quantize_planar(const float *__restrict
         uint32_t pk = 0;
 #pragma unroll
         for (int e = 0; e < 4; e++) pk |= ((uint32_t)(int)__builtin_rintf(v[j][e] * id) & 0xffu) << (8 * e);
-        if (gi < ng) {
-            *(uint32_t *)(qa + ((size_t)m * nb) * 32 + 4 * gi) = pk;
-            if ((gi & 7) == 0) da[(size_t)m * nb + gi / 8] = f2h(am * (1.0f / 127.0f));
+        if (gi < ngo) {
+            const uint16_t d = f2h(am * (1.0f / 127.0f));
+            if constexpr (FEW) {
+                const int64_t b = gi >> 3;
+                const int g = (int)(gi & 7);
+                if ((m >> 4) < mt) *(uint32_t *)(qa + few_q(b, m, mt, 4 * g)) = pk;
+                if (g == 0) da[few_d(b, m)] = d;
+            } else {
+                *(uint32_t *)(qa + ((size_t)m * nb) * 32 + 4 * gi) = pk;
+                if ((gi & 7) == 0) da[(size_t)m * nb + gi / 8] = d;
+            }
         }
     }
 }
 
-// GGUF q8_0 activation rows (stride bytes) -> planar
-__global__ __launch_bounds__(256) void k_act_planar(const uint8_t *__restrict__ act, size_t stride, int64_t nb, int M,
+// GGUF q8_0 activation rows (stride bytes) -> token-major or (FEW) few-token
+// layout, padding as k_quantize_planar's
+template <bool FEW>
+__global__ __launch_bounds__(256) void k_act_planar(const uint8_t *__restrict__ act, size_t stride, int64_t nb, int M, int mt,
                                                     int8_t *__restrict__ qa, uint16_t *__restrict__ da) {
+    const int64_t nbo = FEW ? (nb + 1) & ~(int64_t)1 : nb;
+    const int mo = FEW ? 16 * ((mt + 1) & ~1) : M;
     const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;    // (token, block, quarter)
-    if (i >= (int64_t)M * nb * 4) return;
-    const int64_t m = i / (nb * 4), r = i - m * nb * 4, b = r >> 2, q = r & 3;
-    const uint8_t *blk = act + (size_t)m * stride + (size_t)b * 34;
-    uint32_t w[2];
+    if (i >= (int64_t)mo * nbo * 4) return;
+    const int64_t m = i / (nbo * 4), r = i - m * nbo * 4, b = r >> 2, q = r & 3;
+    uint32_t w[2] = {0, 0};
+    uint16_t d = 0;
+    if (m < M && b < nb) {
+        const uint8_t *blk = act + (size_t)m * stride + (size_t)b * 34;
 #pragma unroll
-    for (int k = 0; k < 2; k++) {
-        const uint8_t *p = blk + 2 + 8 * q + 4 * k;
-        w[k] = (uint32_t)p[0] | ((uint32_t)p[1] << 8) | ((uint32_t)p[2] << 16) | ((uint32_t)p[3] << 24);
+        for (int k = 0; k < 2; k++) {
+            const uint8_t *p = blk + 2 + 8 * q + 4 * k;
+            w[k] = (uint32_t)p[0] | ((uint32_t)p[1] << 8) | ((uint32_t)p[2] << 16) | ((uint32_t)p[3] << 24);
+        }
+        d = (uint16_t)(blk[0] | (blk[1] << 8));
     }
-    *(uint2 *)(qa + ((size_t)m * nb + b) * 32 + 8 * q) = make_uint2(w[0], w[1]);
-    if (q == 0) da[(size_t)m * nb + b] = (uint16_t)(blk[0] | (blk[1] << 8));
+    if constexpr (FEW) {
+        if ((m >> 4) < mt) *(uint2 *)(qa + few_q(b, (int)m, mt, 8 * (int)q)) = make_uint2(w[0], w[1]);
+        if (q == 0) da[few_d(b, (int)m)] = d;
+    } else {
+        *(uint2 *)(qa + ((size_t)m * nb + b) * 32 + 8 * q) = make_uint2(w[0], w[1]);
+        if (q == 0) da[(size_t)m * nb + b] = d;
+    }
+}
+
+// k_mm_few for up to 64 tokens while its 32-bit weight offsets reach every row
+static bool mm_few(const g4h_tensor &W, int M) {
+    if (const char *e = getenv("G4H_MM_FEW"))
+        if (atoi(e) == 0) return false;
+    return M <= MMF_MAXM && (uint64_t)W.nrows * W.nb * (W.type == Q8_0 ? 32 : 16) < (1ull << 32) - 256;
 }
 
 size_t mm_planar_bytes(int M, int64_t ncols) {
     const int64_t nb = ncols / 32;
-    return (((size_t)M * nb * 32 + 255) & ~(size_t)255) + (size_t)M * nb * 2;
+    const size_t planar = (((size_t)M * nb * 32 + 255) & ~(size_t)255) + (size_t)M * nb * 2;
+    return M <= MMF_MAXM ? std::max(planar, mm_few_bytes(M, ncols)) : planar;
 }
 
 // One 32 x 32 tile per workgroup with the blocks split over 4 waves while
@@ -627,21 +665,12 @@ static bool mm_small(const g4h_tensor &W, int M) {
 // 64 x 128; 512 tokens 41.7 / 40.4 us.  Both give the same bits.
 static bool mm_wide(const g4h_tensor &W, int M) { return ((W.nrows + 127) / 128) * ((M + 63) / 64) >= 256; }
 
-// The 16-row strip kernel serves up to MMS_MAXM tokens (it reads each weight
-// byte once; the tiled kernels read it once per 32 or 64 tokens).  Its LDS
-// holds two activation chunks of KC blocks: 64 KB for 32 tokens.
-static bool mm_strip(const g4h_tensor &W, int M) {
-    if (const char *e = getenv("G4H_MM_STRIP"))
-        if (atoi(e) == 0) return false;
-    return M <= MMS_MAXM && (uint64_t)M * W.nb * 32 < (1ull << 31);
-}
-
 void mm_describe(const g4h_tensor &W, int M, char *buf, size_t len) {
     const char *tn = W.type == Q8_0 ? "q8_0" : "q4_0";
-    if (mm_strip(W, M)) {
-        snprintf(buf, len, "k_mm_strip<%s,mt=%d> grid=%lld block=256", tn, (M + 15) / 16, (long long)((W.nrows + 15) / 16));
+    if (mm_few(W, M)) {
+        snprintf(buf, len, "k_mm_few<%s,mt=%d> grid=%lld block=256", tn, (M + 15) / 16, (long long)((W.nrows + 15) / 16));
     } else if (mm_small(W, M)) {
-        snprintf(buf, len, "k_mm_mfma<%s,wm=1,wn=1,ks=4,kb=%d> grid=%lldx%d block=256", tn, MM_KB_SMALL,
+        snprintf(buf, len, "k_mm_mfma<%s,wm=1,wn=1,kb=%d> grid=%lldx%d block=256", tn, MM_KB_SMALL,
                  (long long)((W.nrows + 31) / 32), (M + 31) / 32);
     } else if (mm_wide(W, M)) {
         snprintf(buf, len, "k_mm_lds<%s,tm=2,tn=4,kb=%d,rst=2> grid=%lldx%d block=512", tn, MML_KB,
@@ -652,46 +681,57 @@ void mm_describe(const g4h_tensor &W, int M, char *buf, size_t len) {
     }
 }
 
-template <int WT, int WM, int WN, int KS, int KB>
+template <int WT, int WM, int WN, int KB>
 static hipError_t mm_go(const g4h_tensor &W, const int8_t *qa, const uint16_t *da, int M, float *Y, hipStream_t s) {
     const dim3 grid((unsigned)((W.nrows + 32 * WN - 1) / (32 * WN)), (unsigned)((M + 32 * WM - 1) / (32 * WM)));
-    hipLaunchKernelGGL((k_mm_mfma<WT, WM, WN, KS, KB>), grid, dim3(64 * WM * WN * KS), 0, s, W, qa, da, M, Y);
+    hipLaunchKernelGGL((k_mm_mfma<WT, WM, WN, KB>), grid, dim3(256 * WM * WN), 0, s, W, qa, da, M, Y);
     return hipGetLastError();
 }
 
 // Y[M][nrows] = W * act^T on the matrix cores.  `act` is GGUF q8_0 rows at
 // `stride` (x == nullptr) or x fp32 rows (x_stride floats); `ws` holds the
-// planar activations (mm_planar_bytes).
+// re-laid activations (mm_planar_bytes).
 hipError_t launch_matmul_mfma(const g4h_tensor &W, const float *x, size_t x_stride, const uint8_t *act, size_t stride, int M,
                               float *Y, uint8_t *ws, hipStream_t s) {
     if ((W.type != Q8_0 && W.type != Q4_0) || M <= 0 || W.ncols % 32) return hipErrorInvalidValue;
     const int64_t nb = W.nb;
     int8_t *qa = (int8_t *)ws;
-    uint16_t *da = (uint16_t *)(ws + (((size_t)M * nb * 32 + 255) & ~(size_t)255));
-    if (x) {
-        hipLaunchKernelGGL(k_quantize_planar, dim3((unsigned)((W.ncols / 4 + 256 * QP - 1) / (256 * QP)), M), dim3(256), 0, s, x, x_stride,
-                           W.ncols, M, qa, da);
-    } else {
-        const int64_t n = (int64_t)M * nb * 4;
-        hipLaunchKernelGGL(k_act_planar, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, act, stride, nb, M, qa, da);
-    }
-    if (hipError_t e = hipGetLastError()) return e;
-    if (mm_strip(W, M)) {
+    if (mm_few(W, M)) {
+        const int mt = (M + 15) / 16, mte = (mt + 1) & ~1;
+        const int64_t np = (nb + 1) / 2;
+        uint16_t *da = (uint16_t *)(ws + (((size_t)np * mt * 1024 + 255) & ~(size_t)255));
+        if (x) {
+            hipLaunchKernelGGL(k_quantize_planar<true>, dim3((unsigned)((np * 16 + 256 * QP - 1) / (256 * QP)), 16 * mte), dim3(256), 0,
+                               s, x, x_stride, W.ncols, M, mt, qa, da);
+        } else {
+            const int64_t n = (int64_t)16 * mte * np * 2 * 4;
+            hipLaunchKernelGGL(k_act_planar<true>, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, act, stride, nb, M, mt, qa, da);
+        }
+        if (hipError_t e = hipGetLastError()) return e;
         const dim3 grid((unsigned)((W.nrows + 15) / 16));
-#define G4_MS(T)                                                                                              \
-    if ((M + 15) / 16 == T) {                                                                                 \
-        if (W.type == Q8_0) hipLaunchKernelGGL((k_mm_strip<Q8_0, T>), grid, dim3(256), 0, s, W, qa, da, M, Y); \
-        else hipLaunchKernelGGL((k_mm_strip<Q4_0, T>), grid, dim3(256), 0, s, W, qa, da, M, Y);              \
-        return hipGetLastError();                                                                             \
+#define G4_MF(T)                                                                                             \
+    if (mt == T) {                                                                                           \
+        if (W.type == Q8_0) hipLaunchKernelGGL((k_mm_few<Q8_0, T>), grid, dim3(256), 0, s, W, qa, da, M, Y); \
+        else hipLaunchKernelGGL((k_mm_few<Q4_0, T>), grid, dim3(256), 0, s, W, qa, da, M, Y);              \
+        return hipGetLastError();                                                                            \
     }
-        G4_MS(1) G4_MS(2)
-#undef G4_MS
+        G4_MF(1) G4_MF(2) G4_MF(3) G4_MF(4)
+#undef G4_MF
         return hipErrorInvalidValue;
     }
+    uint16_t *da = (uint16_t *)(ws + (((size_t)M * nb * 32 + 255) & ~(size_t)255));
+    if (x) {
+        hipLaunchKernelGGL(k_quantize_planar<false>, dim3((unsigned)((W.ncols / 4 + 256 * QP - 1) / (256 * QP)), M), dim3(256), 0, s,
+                           x, x_stride, W.ncols, M, 0, qa, da);
+    } else {
+        const int64_t n = (int64_t)M * nb * 4;
+        hipLaunchKernelGGL(k_act_planar<false>, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, act, stride, nb, M, 0, qa, da);
+    }
+    if (hipError_t e = hipGetLastError()) return e;
     const bool small = mm_small(W, M);
     if (small) {
-        if (W.type == Q8_0) return mm_go<Q8_0, 1, 1, 4, MM_KB_SMALL>(W, qa, da, M, Y, s);
-        return mm_go<Q4_0, 1, 1, 4, MM_KB_SMALL>(W, qa, da, M, Y, s);
+        if (W.type == Q8_0) return mm_go<Q8_0, 1, 1, MM_KB_SMALL>(W, qa, da, M, Y, s);
+        return mm_go<Q4_0, 1, 1, MM_KB_SMALL>(W, qa, da, M, Y, s);
     }
     if (mm_wide(W, M)) {
         const dim3 grid((unsigned)((W.nrows + 127) / 128), (unsigned)((M + 63) / 64));

@@ -53,7 +53,7 @@ def test_token_results_independent_of_batch(gpu, oracle, qt, rows, cols, M):
     full = gpu_matmul(gpu, t, x=x, nb=M, path=2)
     if rows == 4096:
         assert gpu.matmul_describe(t, M, 2).startswith("k_mm_lds")
-        assert gpu.matmul_describe(t, 16, 2).startswith("k_mm_strip")
+        assert gpu.matmul_describe(t, 16, 2).startswith("k_mm_few")
         assert_close(full, oracle_matmul(oracle, qt, w, x), f"{rows}x{cols} M={M}")
     for m in (16, 40, 64, 65, 200):
         part = gpu_matmul(gpu, t, x=x[:m].copy(), nb=m, path=2)
@@ -80,7 +80,7 @@ def test_path_selection_and_errors(gpu):
     G = gpu
     t8 = G.Tensor.from_rows(8, synth.weights(8, 64, 256, seed=1), 256)
     tk = G.Tensor.from_rows(12, synth.weights(12, 64, 256, seed=1), 256)
-    assert [G.matmul_path(t8, n) for n in (1, 8, 23, 24, 512)] == [1, 1, 1, 2, 2]
+    assert [G.matmul_path(t8, n) for n in (1, 8, 9, 16, 512)] == [1, 1, 2, 2, 2]
     assert G.matmul_path(tk, 512) == 1
     Y = G.Buffer(64 * 16 * 4)
     x = G.Buffer.from_array(synth.activations(16, 256, seed=2))
@@ -90,19 +90,33 @@ def test_path_selection_and_errors(gpu):
 
 
 @pytest.mark.parametrize("qt", [8, 2])
-@pytest.mark.parametrize("rows,cols,Ms", [(4096, 4096, (1, 8, 16, 32)), (100, 2080, (1, 5, 17, 32)),
-                                          (33, 1056, (2, 31, 32)), (17, 10240, (3, 16, 19))])
-def test_strip_kernel_equals_tile_kernel(gpu, oracle, monkeypatch, qt, rows, cols, Ms):
-    """The 16-row strip kernel (up to 32 tokens; each weight byte read once)
-    gives the tile kernel's bits (G4H_MM_STRIP=0): the same exact block sums,
-    exact scale products and residue-mod-4 partial sums.  Ragged rows, token
-    counts off the 16-token tile and block counts off the 8-block stage."""
+@pytest.mark.parametrize("rows,cols,Ms", [(4096, 4096, (1, 8, 16, 32, 48, 64)), (100, 2080, (1, 5, 17, 33, 64)),
+                                          (33, 1056, (2, 31, 32, 49)), (17, 10240, (3, 16, 19, 63)),
+                                          (48, 64, (1, 64)), (16, 32, (7,))])
+def test_few_kernel_equals_tile_kernel(gpu, oracle, monkeypatch, qt, rows, cols, Ms):
+    """The few-token kernel (up to 64 tokens; each weight byte read once,
+    operands of a block pair swapped across lane halves) gives the tile
+    kernel's bits (G4H_MM_FEW=0): the same exact block sums, exact scale
+    products and residue-pair partial sums.  Ragged rows, token counts off the
+    16-token tile, odd block counts (a lone last block) and block counts off
+    the 8-block stage, one and two blocks per row."""
     w, x, t = _setup(gpu, qt, rows, cols, max(Ms), seed=rows * 7 + cols)
     for M in Ms:
-        assert gpu.matmul_describe(t, M, 2).startswith("k_mm_strip")
-        strip = gpu_matmul(gpu, t, x=x[:M].copy(), nb=M, path=2)
-        monkeypatch.setenv("G4H_MM_STRIP", "0")
+        assert gpu.matmul_describe(t, M, 2).startswith("k_mm_few")
+        few = gpu_matmul(gpu, t, x=x[:M].copy(), nb=M, path=2)
+        monkeypatch.setenv("G4H_MM_FEW", "0")
         tile = gpu_matmul(gpu, t, x=x[:M].copy(), nb=M, path=2)
-        monkeypatch.delenv("G4H_MM_STRIP")
-        assert np.array_equal(bits(strip), bits(tile)), f"{rows}x{cols} M={M}"
-        assert_close(strip, oracle_matmul(oracle, qt, w, x[:M]), f"{rows}x{cols} M={M}")
+        monkeypatch.delenv("G4H_MM_FEW")
+        assert np.array_equal(bits(few), bits(tile)), f"{rows}x{cols} M={M}"
+        assert_close(few, oracle_matmul(oracle, qt, w, x[:M]), f"{rows}x{cols} M={M}")
+
+
+@pytest.mark.parametrize("qt", [8, 2])
+def test_few_kernel_prequantized_rows(gpu, oracle, qt):
+    """GGUF q8_0 activation rows (the act path) re-laid for the few-token
+    kernel give the bits of the fused quantizer's layout."""
+    w, x, t = _setup(gpu, qt, 200, 2080, 37, seed=11)
+    a = gpu_matmul(gpu, t, x=x, nb=37, path=2)
+    b = gpu_matmul(gpu, t, act=oracle.prep_act(qt, x), nb=37, path=2)
+    assert gpu.matmul_describe(t, 37, 2).startswith("k_mm_few")
+    assert np.array_equal(bits(a), bits(b))
