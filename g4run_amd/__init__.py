@@ -90,6 +90,7 @@ _SIGS = [
     ("g4h_attn_status", _int, [_vp, C.POINTER(_int), _vp]),
     ("g4h_attn_decode_window", _int, [_vp, _vp, _vp, _int, _int, _int, _int, _int, _int, _int, _vp, _vp, _sz, _vp]),
     ("g4h_attn_prefill", _int, [_vp, _vp, _vp, _int, _int, _int, _int, _int, _int, _vp, _vp, _sz, _vp]),
+    ("g4h_attn_prefill_workspace_bytes", _sz, [_int, _int, _int, _int]),
     ("g4h_kv_store", _int, [_int, _vp, _vp, _int, _int, _sz, _vp]),
     ("g4h_model_create", _int, [_vp, C.c_uint64, C.POINTER(_vp)]),
     ("g4h_model_free", _int, [_vp]),
@@ -413,10 +414,16 @@ def debug_attn_timeout(on: bool) -> None:
     lib().g4h_debug_attn_timeout(1 if on else 0)
 
 
+def attn_prefill_workspace_bytes(n_head: int, hd: int, pos0: int, nb: int) -> int:
+    return lib().g4h_attn_prefill_workspace_bytes(n_head, hd, pos0, nb)
+
+
 def attn_prefill(q, kc, vc, kv_type: int, n_head: int, n_kv: int, hd: int, pos0: int, nb: int, out, ws=None,
-                 stream=None) -> None:
-    """attn_kernel for nb new tokens at positions pos0.. (causal)."""
-    need = attn_workspace_bytes(n_head, hd, pos0 + nb)
+                 stream=None, batched: bool = True) -> None:
+    """attn_kernel for nb new tokens at positions pos0.. (causal): one set of
+    launches for the whole batch, or (batched=False, a smaller workspace) one
+    decode launch per token."""
+    need = attn_prefill_workspace_bytes(n_head, hd, pos0, nb) if batched else attn_workspace_bytes(n_head, hd, pos0 + nb)
     if ws is None:
         ws = Buffer(need)
     check(lib().g4h_attn_prefill(_p(q), _p(kc), _p(vc), kv_type, n_head, n_kv, hd, pos0, nb, _p(out), _p(ws),

@@ -690,14 +690,37 @@ extern "C" int g4h_attn_status(void *ws, int *failed, void *stream) {
     return G4H_OK;
 }
 
+extern "C" size_t g4h_attn_prefill_workspace_bytes(int n_head, int hd, int pos0, int nb) {
+    if (n_head <= 0 || hd <= 0 || pos0 < 0 || nb <= 0) return 0;
+    return attn_batch_workspace_bytes(n_head, hd, pos0 + nb, nb);
+}
+
 extern "C" int g4h_attn_prefill(const float *q, const void *kc, const void *vc, int kv_type, int n_head, int n_kv, int hd,
                                 int pos0, int nb, float *out, void *ws, size_t ws_bytes, void *s) {
     G4_NEED_INIT();
     if (!q || !out || nb < 0 || pos0 < 0 || n_head <= 0 || hd <= 0) return fail(G4H_ERR_ARG, "g4h_attn_prefill: bad argument");
     if (nb == 0) return G4H_OK;
+    if (!kc || !vc || !ws) return fail(G4H_ERR_ARG, "g4h_attn_prefill: null pointer");
+    if (int rc = check_attn_shape("g4h_attn_prefill", kv_type, n_head, n_kv, hd)) return rc;
+    if (nb <= 65535 && ws_bytes >= g4h_attn_prefill_workspace_bytes(n_head, hd, pos0, nb)) {
+        // model.c:514-521, all tokens in one set of launches
+        const uintptr_t al = kv_type == F16 ? 8 : 4;
+        if ((uintptr_t)kc % al || (uintptr_t)vc % al)
+            return fail(G4H_ERR_ARG, "g4h_attn_prefill: caches must be %zu-byte aligned", (size_t)al);
+        QkvArgs a;
+        a.n_head = n_head;
+        a.n_kv = n_kv;
+        a.hd = hd;
+        a.kv_type = kv_type;
+        a.kc = (uint8_t *)kc;
+        a.vc = (uint8_t *)vc;
+        G4_HIP(launch_attn_batch(q, a, pos0 + 1, nb, out, nullptr, (uint8_t *)ws, (hipStream_t)s));
+        return G4H_OK;
+    }
     if (ws_bytes < g4h_attn_workspace_bytes(n_head, hd, pos0 + nb))
         return fail(G4H_ERR_ARG, "g4h_attn_prefill: workspace smaller than g4h_attn_workspace_bytes(n_head, hd, pos0 + nb)");
-    // model.c:514-521: token b at pos0 + b attends [0, pos0 + b]
+    // a smaller workspace: one decode call per token (model.c:514-521: token b
+    // at pos0 + b attends [0, pos0 + b])
     for (int b = 0; b < nb; b++) {
         const size_t off = (size_t)b * n_head * hd;
         if (int rc = g4h_attn_decode(q + off, kc, vc, kv_type, n_head, n_kv, hd, pos0 + b + 1, out + off, ws, ws_bytes, s)) return rc;

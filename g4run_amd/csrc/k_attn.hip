@@ -168,9 +168,32 @@ struct AttnCtx {
     uint64_t *QT;
     int qrows;
     int pabs, mirror;        // set by attn_view
+    // a batch of ntok > 1 tokens on grid.z (the three passes only): token b
+    // attends npos + b positions with query / output rows b, its q8_0 output
+    // row q8_tok bytes further and its own workspace block ws_tok bytes further
+    int ntok;
+    size_t ws_tok, q8_tok;
 };
 
 __device__ __forceinline__ int npos_of(const AttnCtx &c) { return c.npos_dev ? *c.npos_dev : c.npos; }
+
+// token blockIdx.z of a batch (causal prefill, model.c:514-521: token b at
+// position pos0 + b attends positions 0 .. pos0 + b): its rows, its
+// positions and its workspace block; every three-pass kernel starts here
+__device__ __forceinline__ void attn_token(AttnCtx &c) {
+    if (c.ntok <= 1) return;
+    const int b = blockIdx.z;
+    const size_t rows = (size_t)b * c.a.n_head * c.a.hd;
+    c.q += rows;
+    c.out += rows;
+    if (c.q8out) c.q8out += b * c.q8_tok;
+    c.npos += b;
+    const size_t sh = b * c.ws_tok;
+    c.S = (float *)((uint8_t *)c.S + sh);
+    c.Mc = (float *)((uint8_t *)c.Mc + sh);
+    c.Lc = (double *)((uint8_t *)c.Lc + sh);
+    c.P = (float *)((uint8_t *)c.P + sh);
+}
 
 // The rows a launch attends as a linear cache (every kernel starts here):
 // positions j0 .. npos-1 with j0 = max(0, npos - window) (a sliding window,
@@ -461,6 +484,7 @@ __global__ __launch_bounds__(256) void k_attn_scores_f16(AttnCtx c) {
     __shared__ float sc[GRP][ATT_CHUNK];
     __shared__ float wm[4][GRP];
     __shared__ double wl[4][GRP];
+    attn_token(c);
     const int npos = attn_view(c);
     const int kvh = blockIdx.x, ch = blockIdx.y, t = threadIdx.x;
     const int lane = t & 63, wave = t >> 6;
@@ -506,6 +530,7 @@ __global__ __launch_bounds__(128) void k_attn_scores_q8(AttnCtx c) {
     __shared__ float qrow[GRP][256];
     __shared__ float wm[2][GRP];
     __shared__ double wl[2][GRP];
+    attn_token(c);
     const int npos = attn_view(c);
     const int kvh = blockIdx.x, ch = blockIdx.y, t = threadIdx.x, lane = t & 63, wave = t >> 6;
     constexpr int hd = HD;
@@ -715,6 +740,7 @@ __global__ __launch_bounds__(256) void k_attn_v(AttnCtx c) {
     __shared__ float part[4][GRP][256];
     __shared__ __align__(16) float wl[GRP][ATT_CHUNK];
     __shared__ float inv_s[GRP], max_s[GRP];
+    attn_token(c);
     const int npos = attn_view(c);
     const int kvh = blockIdx.x, ch = blockIdx.y, t = threadIdx.x, lane = t & 63, wave = t >> 6;
     constexpr int hd = HD;
@@ -857,9 +883,10 @@ __device__ __forceinline__ void combine_head(const AttnCtx &c, int h, int nch, f
     }
 }
 
-// grid n_head
+// grid n_head (x tokens)
 __global__ __launch_bounds__(256) void k_attn_combine(AttnCtx c) {
     __shared__ float row[256];
+    attn_token(c);
     const int npos = attn_view(c);
     combine_head<false>(c, blockIdx.x, (npos + ATT_CHUNK - 1) / ATT_CHUNK, row);
 }
@@ -1384,6 +1411,122 @@ static hipError_t attn_go(AttnCtx c, int n_head, int n_kv, int npos_max, uint8_t
     hipLaunchKernelGGL((k_attn_v<KV, GRP, HD>), dim3(n_kv, nc), dim3(256), 0, s, c);
     hipLaunchKernelGGL(k_attn_combine, dim3(n_head), dim3(256), 0, s, c);
     return hipGetLastError();
+}
+
+// ------------------------------------------------ causal batch (prefill) --
+// nb tokens whose first attends npos0 positions, the last npos0 + nb - 1: the
+// three passes once over grid.z = nb, each token with its own block of
+// scores S, chunk statistics Mc / Lc and partials P sized for npos0 + nb - 1
+// positions; chunks past a token's last position return at once.  Per token
+// the arithmetic of the three passes, which the one-launch form shares: every
+// token's rows are bit-identical to a decode call at its position.
+struct AttnBatchWs {
+    size_t S, Mc, Lc, P, tok;
+};
+static AttnBatchWs attn_batch_ws(int n_head, int hd, int npos_max) {
+    const size_t nc = (npos_max + ATT_CHUNK - 1) / ATT_CHUNK;
+    AttnBatchWs w;
+    w.S = 0;
+    w.Mc = al256((size_t)n_head * npos_max * 4);
+    w.Lc = w.Mc + al256((size_t)n_head * nc * 4);
+    w.P = w.Lc + al256((size_t)n_head * nc * 8);
+    w.tok = w.P + al256((size_t)n_head * nc * hd * 4);
+    return w;
+}
+size_t attn_batch_workspace_bytes(int n_head, int hd, int npos_max, int nb) {
+    return (size_t)nb * attn_batch_ws(n_head, hd, npos_max).tok;
+}
+
+template <int KV, int GRP, int HD>
+static hipError_t attn_batch_go(AttnCtx c, int n_head, int n_kv, int npos0, int nb, uint8_t *ws, hipStream_t s) {
+    const int npos_max = npos0 + nb - 1;
+    const AttnBatchWs w = attn_batch_ws(n_head, c.a.hd, npos_max);
+    const int nc = (npos_max + ATT_CHUNK - 1) / ATT_CHUNK;
+    c.nc = nc;
+    c.S = (float *)(ws + w.S);
+    c.Mc = (float *)(ws + w.Mc);
+    c.Lc = (double *)(ws + w.Lc);
+    c.P = (float *)(ws + w.P);
+    c.ntok = nb;
+    c.ws_tok = w.tok;
+    if (!c.q8_tok) c.q8_tok = (size_t)n_head * (c.a.hd / 32) * 34;
+    const dim3 grid(n_kv, nc, nb);
+    if constexpr (KV == F16) hipLaunchKernelGGL((k_attn_scores_f16<GRP, HD>), grid, dim3(256), 0, s, c);
+    else hipLaunchKernelGGL((k_attn_scores_q8<KV, GRP, HD>), grid, dim3(128), 0, s, c);
+    hipLaunchKernelGGL((k_attn_v<KV, GRP, HD>), grid, dim3(256), 0, s, c);
+    hipLaunchKernelGGL(k_attn_combine, dim3(n_head, 1, nb), dim3(256), 0, s, c);
+    return hipGetLastError();
+}
+
+// The rows of nb tokens prepared as the decode kernels prepare them
+// (model.c:664-687, the preparation steps of k_attn_scores_* / the fused
+// kernel): grid (token, KV head), one wave per row -- the group's queries
+// (RMSNorm x q_norm, NeoX RoPE at pos0 + b) into q rows of qout, the key
+// (RMSNorm x k_norm, RoPE) and value (RMSNorm) into the caches at pos0 + b.
+// Runs before the batch attends, so every token finds the earlier tokens'
+// rows in the caches.
+template <int HD>
+__global__ __launch_bounds__(256) void k_attn_prep_rows(QkvArgs a, const float *__restrict__ qkv, int pos0, float *__restrict__ qout) {
+    __shared__ float wb[4][256];                                     // q8_0 / q4_0 stores
+    constexpr int epl = HD >> 6;
+    const int b = blockIdx.x, kvh = blockIdx.y, wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int grp = a.n_head / a.n_kv, h0 = kvh * grp, p = pos0 + b;
+    const float *src = qkv + (size_t)b * (a.n_head + 2 * a.n_kv) * HD;
+    const size_t rb = a.kv_type == F16 ? (size_t)HD * 2 : (size_t)(HD / 32) * (a.kv_type == Q4_0 ? 18 : 34);
+    float cs[4], sn[4];
+    rope_load(cs, sn, a.rope, p, HD);
+    for (int r = wave; r < grp + 2; r += 4) {                        // uniform over the wave
+        const int src_row = r < grp ? h0 + r : r == grp ? a.n_head + kvh : a.n_head + a.n_kv + kvh;
+        const float *w = r < grp ? a.q_norm : r == grp ? a.k_norm : nullptr;
+        PrepRow pr;
+        prep_load(pr, src + (size_t)src_row * HD, w, HD);
+        float y[4];
+        prep_finish(pr, r <= grp, r <= grp, cs, sn, HD, a.eps, y);
+        if (r < grp) {
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+                if (e < epl) qout[((size_t)b * a.n_head + h0 + r) * HD + lane * epl + e] = y[e];
+        } else {
+            cache_store(y, a.kv_type, (r == grp ? a.kc : a.vc) + ((size_t)p * a.n_kv + kvh) * rb, HD, wb[wave]);
+        }
+    }
+}
+
+hipError_t launch_attn_prep_rows(const float *qkv, const QkvArgs &a, int pos0, int nb, float *qout, hipStream_t s) {
+    if (a.hd % 64 || a.hd > 256 || a.n_kv <= 0 || a.n_head % a.n_kv || nb < 1 || nb > 65535 || a.window || a.ring)
+        return hipErrorInvalidValue;
+    if (!a.rope || !a.q_norm || !a.k_norm) return hipErrorInvalidValue;
+    const dim3 grid(nb, a.n_kv);
+    if (a.hd == 64) hipLaunchKernelGGL(k_attn_prep_rows<64>, grid, dim3(256), 0, s, a, qkv, pos0, qout);
+    else if (a.hd == 128) hipLaunchKernelGGL(k_attn_prep_rows<128>, grid, dim3(256), 0, s, a, qkv, pos0, qout);
+    else if (a.hd == 192) hipLaunchKernelGGL(k_attn_prep_rows<192>, grid, dim3(256), 0, s, a, qkv, pos0, qout);
+    else hipLaunchKernelGGL(k_attn_prep_rows<256>, grid, dim3(256), 0, s, a, qkv, pos0, qout);
+    return hipGetLastError();
+}
+
+hipError_t launch_attn_batch(const float *q, const QkvArgs &a, int npos0, int nb, float *out, uint8_t *q8out, uint8_t *ws,
+                             hipStream_t s, size_t q8_stride) {
+    if (a.hd % 64 || a.hd > 256 || a.n_kv <= 0 || a.n_head % a.n_kv || nb < 1 || npos0 < 1 || nb > 65535) return hipErrorInvalidValue;
+    AttnCtx c{};
+    c.q = q;
+    c.a = a;
+    c.npos = npos0;
+    c.out = out;
+    c.q8out = q8out;
+    c.q8_tok = q8_stride;
+    const int grp = a.n_head / a.n_kv;
+#define G4_ATT(KV, G)                                                                        \
+    if (a.kv_type == KV && grp == G) {                                                       \
+        if (a.hd == 64) return attn_batch_go<KV, G, 64>(c, a.n_head, a.n_kv, npos0, nb, ws, s);   \
+        if (a.hd == 128) return attn_batch_go<KV, G, 128>(c, a.n_head, a.n_kv, npos0, nb, ws, s); \
+        if (a.hd == 192) return attn_batch_go<KV, G, 192>(c, a.n_head, a.n_kv, npos0, nb, ws, s); \
+        if (a.hd == 256) return attn_batch_go<KV, G, 256>(c, a.n_head, a.n_kv, npos0, nb, ws, s); \
+    }
+    G4_ATT(F16, 1); G4_ATT(F16, 2); G4_ATT(F16, 4); G4_ATT(F16, 8);
+    G4_ATT(Q8_0, 1); G4_ATT(Q8_0, 2); G4_ATT(Q8_0, 4); G4_ATT(Q8_0, 8);
+    G4_ATT(Q4_0, 1); G4_ATT(Q4_0, 2); G4_ATT(Q4_0, 4); G4_ATT(Q4_0, 8);
+#undef G4_ATT
+    return hipErrorInvalidValue;
 }
 
 // ------------------------------------------- projection + attention launch --

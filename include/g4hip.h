@@ -213,13 +213,19 @@ int g4h_attn_decode_window(const float *q_dev, const void *kc_dev, const void *v
 /* attn_kernel over a batch of nb new tokens (model.c:509-545 with nb > 1):
  * token b sits at position pos0 + b and attends cached positions
  * [0, pos0 + b] -- causal, the batch's own rows already stored in kc/vc.
- * q_dev / out_dev: nb x n_head x hd fp32.  ws_bytes must cover
- * g4h_attn_workspace_bytes(n_head, hd, pos0 + nb); the tokens run as
- * stream-ordered decode-attention launches on ws, each with the single-token
- * bits of g4h_attn_decode at its position. */
+ * q_dev / out_dev: nb x n_head x hd fp32.  With ws_bytes covering
+ * g4h_attn_prefill_workspace_bytes(n_head, hd, pos0, nb) all tokens run in
+ * one set of three launches (scores, values, combine; a token grid
+ * dimension); with at least g4h_attn_workspace_bytes(n_head, hd, pos0 + nb)
+ * they run as stream-ordered decode-attention launches on ws.  Either way
+ * every token's row has the bits of g4h_attn_decode at its position. */
 int g4h_attn_prefill(const float *q_dev, const void *kc_dev, const void *vc_dev, int kv_type,
                      int n_head, int n_kv, int hd, int pos0, int nb, float *out_dev,
                      void *ws_dev, size_t ws_bytes, void *stream);
+/* workspace bytes of g4h_attn_prefill's one-set form (a block of scores,
+ * chunk statistics and partials per token); 0 for a bad argument.  No
+ * counterpart in the reference, which attends on the CPU. */
+size_t g4h_attn_prefill_workspace_bytes(int n_head, int hd, int pos0, int nb);
 /* kv_store (model.c:583-589): `rows` rows of hd floats into cache rows
  * dst_stride bytes apart (0 = packed rows), as f16 (RNE) or q8_0 / q4_0
  * blocks. */

@@ -148,6 +148,33 @@ def test_batched_prefill_attention_is_causal(gpu, oracle, kv_type, pos0, nb):
         assert np.allclose(got[0], np.repeat(v0, n_head // n_kv, axis=0), rtol=0, atol=0)
 
 
+@pytest.mark.parametrize("kv_type,n_head,n_kv,hd,pos0,nb", [
+    (1, 8, 4, 256, 120, 20), (8, 8, 4, 256, 250, 11), (2, 8, 4, 256, 0, 5),
+    (1, 4, 4, 64, 1000, 33), (8, 8, 1, 128, 127, 2), (2, 16, 2, 192, 383, 3), (1, 2, 2, 64, 0, 1)])
+def test_batched_prefill_equals_per_token_calls(gpu, oracle, kv_type, n_head, n_kv, hd, pos0, nb):
+    """The one-set batch (three launches, a token grid dimension, a workspace
+    block per token) gives every token the bits of a decode call at its
+    position -- the per-token launches of the smaller-workspace form and a
+    direct g4h_attn_decode -- across chunk boundaries (positions 127/128,
+    255/256, 383/384), group sizes 1 to 8 and head sizes 64 to 256."""
+    G = gpu
+    n_slot = pos0 + nb
+    kb, vb, kh, vh = make_cache(G, oracle, kv_type, n_slot, n_kv, hd, seed=n_slot + hd)
+    q = (np.random.default_rng(nb + hd).standard_normal((nb, n_head, hd)) * 0.5).astype(np.float32)
+    qb = G.Buffer.from_array(q)
+    one, loop = G.Buffer(nb * n_head * hd * 4), G.Buffer(nb * n_head * hd * 4)
+    G.attn_prefill(qb, kb, vb, kv_type, n_head, n_kv, hd, pos0, nb, one)
+    G.attn_prefill(qb, kb, vb, kv_type, n_head, n_kv, hd, pos0, nb, loop, batched=False)
+    a = one.download(np.float32, (nb, n_head, hd))
+    assert a.tobytes() == loop.download(np.float32, (nb, n_head, hd)).tobytes()
+    for b in (0, nb - 1):
+        d = G.Buffer(n_head * hd * 4)
+        G.attn_decode(G.Buffer.from_array(q[b]), kb, vb, kv_type, n_head, n_kv, hd, pos0 + b + 1, d)
+        assert d.download(np.float32, (n_head, hd)).tobytes() == a[b].tobytes(), f"token {b}"
+        ref = oracle.attn_decode(q[b], kh, vh, kv_type, n_head, n_kv, hd, pos0 + b)
+        assert (np.abs(a[b].astype(np.float64) - ref) <= ATOL + RTOL * np.abs(ref)).all(), f"token {b}"
+
+
 def test_attention_timeout_reported_by_status(gpu, oracle):
     """The one-launch attention's bounded waits: forced to give up (the test
     hook makes them wait for a tag no store carries, 64 retries), every kernel
