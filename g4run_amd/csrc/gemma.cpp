@@ -55,7 +55,7 @@ struct g4h_gemma {
     std::vector<uint8_t *> kc, vc;
     float *x = nullptr, *xb = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *qkv = nullptr, *att = nullptr, *g = nullptr,
           *u = nullptr, *pl = nullptr, *plp = nullptr, *plg = nullptr, *hn = nullptr;
-    uint8_t *ws = nullptr;
+    uint8_t *ws = nullptr, *bws = nullptr;     // decode attention / batch attention workspaces
     uint16_t *gelu = nullptr;
     std::vector<void *> allocs;
     std::vector<g4h_tensor *> tensors;
@@ -263,6 +263,7 @@ int create(const g4_model_file *mf, int n_ctx, int kv_type, g4h_gemma *m) {
     const size_t wsb = g4h_attn_workspace_bytes(m->H, m->hd_max, n_ctx);
     G_RC(galloc(m, (void **)&m->ws, wsb));
     G_HIP(hipMemset(m->ws, 0, wsb));
+    G_RC(galloc(m, (void **)&m->bws, attn_batch_workspace_bytes(m->H, m->hd_max, n_ctx, kRows)));
     std::vector<uint16_t> gt(65536);
     for (uint32_t h = 0; h < 65536; h++) gt[h] = gelu_table_entry((uint16_t)h);
     G_RC(galloc(m, (void **)&m->gelu, 65536 * 2));
@@ -365,18 +366,20 @@ extern "C" int g4h_gemma_forward(g4h_gemma *m, const int *tokens, int nb, int po
             G_HIP(launch_pack_qkv(m->q, m->k, L.wv ? m->v : nullptr, m->qkv, nq, hd, nb, s));
             qa.kc = m->kc[il];
             qa.vc = m->vc[il];
-            for (int b = 0; b < nb; b++)
-                G_HIP(launch_attn_decode(nullptr, m->qkv + (size_t)b * (nq + 2 * hd), qa, pos0 + b + 1, nullptr, npos_max,
-                                         m->att + (size_t)b * nq, nullptr, m->ws, s));
+            if (nb > 1) {                                            // every row stored, then the batch attends
+                G_HIP(launch_attn_prep_rows(m->qkv, qa, pos0, nb, m->q, s));
+                G_HIP(launch_attn_batch(m->q, qa, pos0 + 1, nb, m->att, nullptr, m->bws, s));
+            } else {
+                G_HIP(launch_attn_decode(nullptr, m->qkv, qa, pos0 + 1, nullptr, npos_max, m->att, nullptr, m->ws, s));
+            }
         } else {
             // a shared cache: the queries are prepared here (model.c:666-672, 692)
             const int cil = L.swa ? m->n_layer_kv - 2 : m->n_layer_kv - 1;
             G_HIP(launch_head_prep(m->q, H, hd, nb, L.q_norm, rope, pos0, eps, s));
             qa.kc = m->kc[cil];
             qa.vc = m->vc[cil];
-            for (int b = 0; b < nb; b++)
-                G_HIP(launch_attn_decode(m->q + (size_t)b * nq, nullptr, qa, pos0 + b + 1, nullptr, npos_max,
-                                         m->att + (size_t)b * nq, nullptr, m->ws, s));
+            if (nb > 1) G_HIP(launch_attn_batch(m->q, qa, pos0 + 1, nb, m->att, nullptr, m->bws, s));
+            else G_HIP(launch_attn_decode(m->q, nullptr, qa, pos0 + 1, nullptr, npos_max, m->att, nullptr, m->ws, s));
         }
         G_RC(mm(L.wo, m->att, m->xb, nb, s));
         G_HIP(launch_resid(m->x, m->xb, L.post_attn_norm, E, nb, eps, 1.0f, s));

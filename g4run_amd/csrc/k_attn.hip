@@ -1439,7 +1439,8 @@ size_t attn_batch_workspace_bytes(int n_head, int hd, int npos_max, int nb) {
 
 template <int KV, int GRP, int HD>
 static hipError_t attn_batch_go(AttnCtx c, int n_head, int n_kv, int npos0, int nb, uint8_t *ws, hipStream_t s) {
-    const int npos_max = npos0 + nb - 1;
+    // rows any token attends: all positions, or at most the window
+    const int npos_max = c.a.window ? std::min(c.a.window, npos0 + nb - 1) : npos0 + nb - 1;
     const AttnBatchWs w = attn_batch_ws(n_head, c.a.hd, npos_max);
     const int nc = (npos_max + ATT_CHUNK - 1) / ATT_CHUNK;
     c.nc = nc;
@@ -1464,7 +1465,11 @@ static hipError_t attn_batch_go(AttnCtx c, int n_head, int n_kv, int npos0, int 
 // (RMSNorm x q_norm, NeoX RoPE at pos0 + b) into q rows of qout, the key
 // (RMSNorm x k_norm, RoPE) and value (RMSNorm) into the caches at pos0 + b.
 // Runs before the batch attends, so every token finds the earlier tokens'
-// rows in the caches.
+// rows in the caches.  On a ring (a.ring > 0) a row goes to slot p % ring and
+// again to p % ring + ring, the two copies the decode kernels store; with a
+// window and no ring, to slot p.  Within a batch of at most ring - window + 1
+// tokens no token's store overwrites a row an earlier token of the batch
+// still attends.
 template <int HD>
 __global__ __launch_bounds__(256) void k_attn_prep_rows(QkvArgs a, const float *__restrict__ qkv, int pos0, float *__restrict__ qout) {
     __shared__ float wb[4][256];                                     // q8_0 / q4_0 stores
@@ -1487,14 +1492,17 @@ __global__ __launch_bounds__(256) void k_attn_prep_rows(QkvArgs a, const float *
             for (int e = 0; e < 4; e++)
                 if (e < epl) qout[((size_t)b * a.n_head + h0 + r) * HD + lane * epl + e] = y[e];
         } else {
-            cache_store(y, a.kv_type, (r == grp ? a.kc : a.vc) + ((size_t)p * a.n_kv + kvh) * rb, HD, wb[wave]);
+            uint8_t *cache = r == grp ? a.kc : a.vc;
+            const int slot = a.ring ? p % a.ring : p;
+            cache_store(y, a.kv_type, cache + ((size_t)slot * a.n_kv + kvh) * rb, HD, wb[wave]);
+            if (a.ring) cache_store(y, a.kv_type, cache + ((size_t)(slot + a.ring) * a.n_kv + kvh) * rb, HD, wb[wave]);
         }
     }
 }
 
 hipError_t launch_attn_prep_rows(const float *qkv, const QkvArgs &a, int pos0, int nb, float *qout, hipStream_t s) {
-    if (a.hd % 64 || a.hd > 256 || a.n_kv <= 0 || a.n_head % a.n_kv || nb < 1 || nb > 65535 || a.window || a.ring)
-        return hipErrorInvalidValue;
+    if (a.hd % 64 || a.hd > 256 || a.n_kv <= 0 || a.n_head % a.n_kv || nb < 1 || nb > 65535) return hipErrorInvalidValue;
+    if (a.ring && (a.window <= 0 || a.window > a.ring || nb > a.ring - a.window + 1)) return hipErrorInvalidValue;
     if (!a.rope || !a.q_norm || !a.k_norm) return hipErrorInvalidValue;
     const dim3 grid(nb, a.n_kv);
     if (a.hd == 64) hipLaunchKernelGGL(k_attn_prep_rows<64>, grid, dim3(256), 0, s, a, qkv, pos0, qout);

@@ -177,8 +177,10 @@ struct AttnTag {
 };
 bool attn_fused_fits(int kv_type, int n_head, int n_kv, int hd, int npos_max);
 // causal attention of nb tokens over one cache (the first attends npos0
-// positions, token b npos0 + b), three passes with a token grid dimension;
-// ws of attn_batch_workspace_bytes(n_head, hd, npos0 + nb - 1, nb)
+// positions, token b npos0 + b; with a.window, the last window of them),
+// three passes with a token grid dimension; ws of
+// attn_batch_workspace_bytes(n_head, hd, rows, nb), rows = npos0 + nb - 1 or,
+// with a window, at most the window
 size_t attn_batch_workspace_bytes(int n_head, int hd, int npos_max, int nb);
 // q8out (optional): q8_0 rows of each token's output, q8_stride bytes apart
 // (0: packed rows)
@@ -187,7 +189,8 @@ hipError_t launch_attn_batch(const float *q, const QkvArgs &a, int npos0, int nb
 // the query / key / value rows of nb tokens from the fused projection output
 // (rows of (n_head + 2 n_kv) hd floats) prepared as the decode kernels do:
 // queries into qout [nb][n_head][hd], key and value rows into the caches at
-// pos0 .. pos0 + nb - 1 (no window or ring)
+// pos0 .. pos0 + nb - 1 (on a ring both copies; at most ring - window + 1
+// tokens)
 hipError_t launch_attn_prep_rows(const float *qkv, const QkvArgs &a, int pos0, int nb, float *qout, hipStream_t s);
 hipError_t launch_attn_decode(const float *q, const float *qkv, const QkvArgs &a, int npos, const int *npos_dev, int npos_max,
                               float *out, uint8_t *q8out, uint8_t *ws, hipStream_t s, const AttnTag *tag = nullptr);
