@@ -21,7 +21,7 @@ def _setup(G, qt, rows, cols, M, seed):
     return w, x, G.Tensor.from_rows(qt, w, cols)
 
 
-@pytest.mark.parametrize("M", [16, 64, 512])
+@pytest.mark.parametrize("M", [1, 8, 16, 64, 512])
 def test_config3_q8_0_vs_oracle(gpu, oracle, M):
     w, x, t = _setup(gpu, 8, 4096, 4096, M, seed=1234)
     y = gpu_matmul(gpu, t, x=x, nb=M, path=2)
