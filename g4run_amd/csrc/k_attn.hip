@@ -173,6 +173,13 @@ struct AttnCtx {
     // row q8_tok bytes further and its own workspace block ws_tok bytes further
     int ntok;
     size_t ws_tok, q8_tok;
+    // the output projection folded into the one-launch form (decode step):
+    // the head rows' q8_0 blocks go out as tagged words QO [block][16] (one
+    // 128-byte line each, 9 words used) and every workgroup then computes Wo
+    // row groups into wo_out with the GEMV family's arithmetic
+    g4h_tensor Wo;
+    float *wo_out;
+    uint64_t *QO;
 };
 
 __device__ __forceinline__ int npos_of(const AttnCtx &c) { return c.npos_dev ? *c.npos_dev : c.npos; }
@@ -1014,9 +1021,12 @@ struct QkvRows {
     }
 };
 
-template <int GRP, int HD, class FQ = void, int LPR = 32, int UPL = 4>
+constexpr int ATT_WO_MAXB = 64;      // q8_0 blocks of the attention output the Wo fold takes (n_head * hd <= 2048)
+
+template <int GRP, int HD, class FQ = void, int LPR = 32, int UPL = 4, class FO = void, int LPRO = 16, int UPLO = 4>
 __global__ __launch_bounds__(256) void k_attn_fused_f16(AttnCtx c) {
     constexpr bool QKV = !std::is_void<FQ>::value;
+    constexpr bool WO = !std::is_void<FO>::value;
     extern __shared__ __align__(16) uint8_t act_lds[];               // QKV: the projection's q8_0 activation
     __shared__ __align__(16) float4 qf[GRP][64];
     __shared__ __align__(16) uint16_t kpos[256], vpos[256];
@@ -1210,6 +1220,25 @@ __global__ __launch_bounds__(256) void k_attn_fused_f16(AttnCtx c) {
             st_tag(&c.PT[((size_t)(h0 + g) * c.nc + ch) * hd + e], __float_as_uint(r), tag);
         }
     }
+    // Wo fold: the wave's first row group of Wo goes out now, behind this
+    // launch's K/V streams (their registers are free again), so it lands
+    // during the hand-offs below; row groups gw, gw + NWV, ... of all waves
+    using FW = std::conditional_t<WO, FO, FQ4_0>;                   // a frag type also when there is no fold
+    constexpr int RPWO = 64 / LPRO;
+    const int64_t gw = ((int64_t)blockIdx.y * gridDim.x + blockIdx.x) * 4 + wave;
+    const int64_t NWV = (int64_t)gridDim.x * gridDim.y * 4;
+    const int go = lane % LPRO, rgo = lane / LPRO;
+    const int units_o = WO ? (int)(c.Wo.nb * FW::units_per_block) : 1;
+    typename FW::Frag fo[UPLO];
+    auto wo_load = [&](int64_t gq) __attribute__((always_inline)) {
+        const int64_t row = min(gq * RPWO + rgo, c.Wo.nrows - 1);
+#pragma unroll
+        for (int k = 0; k < UPLO; k++) FW::load(fo[k], c.Wo, row, min(go + k * LPRO, units_o - 1));
+    };
+    if constexpr (WO) {
+        wo_load(gw);
+        issue_order();
+    }
     // combine, shared by every workgroup of the KV head: blocks ch, ch + nwg, ...
     // of its GRP*hd outputs; thread (slot r = t / 32, element i = t % 32)
     // gathers chunks r, r + 8, ... into LDS, then 32 threads add them in chunk
@@ -1269,7 +1298,7 @@ __global__ __launch_bounds__(256) void k_attn_fused_f16(AttnCtx c) {
             if (bad) r = __builtin_nanf("");
             c.out[(size_t)(h0 + g) * hd + e0 + t] = r;
         }
-        if (c.q8out) {                                               // uniform
+        if (c.q8out || WO) {                                         // uniform
             lds_barrier();
             if (t < 32) vals[t] = r;
             lds_barrier();
@@ -1277,8 +1306,65 @@ __global__ __launch_bounds__(256) void k_attn_fused_f16(AttnCtx c) {
                 float v4[4];
 #pragma unroll
                 for (int k = 0; k < 4; k++) v4[k] = vals[4 * t + k];
-                q8_store4(v4, t, true, c.q8out + (size_t)(h0 + g) * (hd / 32) * 34 + (size_t)(e0 / 32) * 34);
+                if constexpr (WO) {
+                    // the block as tagged words: quant words 0..7, the fp16 scale in word 8
+                    uint16_t d16;
+                    const uint32_t pk = q8_pack4(v4, &d16);
+                    uint64_t *qo = c.QO + ((size_t)(h0 + g) * (hd / 32) + e0 / 32) * 16;
+                    st_tag(qo + t, pk, tag);
+                    if (t == 0) st_tag(qo + 8, d16, tag);
+                } else {
+                    q8_store4(v4, t, true, c.q8out + (size_t)(h0 + g) * (hd / 32) * 34 + (size_t)(e0 / 32) * 34);
+                }
             }
+        }
+    }
+    if constexpr (WO) {
+        // every workgroup: all blocks of the head rows (9 tagged words each)
+        // into the GEMV family's q8_0 activation layout in LDS, then its waves'
+        // Wo row groups (the lanes, units and reduction of k_gemv with this
+        // LPR / UPL, so each row has the bits of the separate Wo launch)
+        __shared__ uint32_t wo_raw[WO ? ATT_WO_MAXB * 9 : 1];
+        __shared__ __align__(16) uint8_t wo_act[WO ? ATT_WO_MAXB * 40 : 16];
+        const int nbo = (int)c.Wo.nb, nw = nbo * 9;
+        for (int i0 = 0; i0 < nw; i0 += 4 * 256) {                    // uniform
+            const uint64_t *src[4];
+            bool need[4];
+            uint32_t bits[4];
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const int i = i0 + q * 256 + t, ic = min(i, nw - 1);
+                src[q] = c.QO + (size_t)(ic / 9) * 16 + ic % 9;
+                need[q] = i < nw;
+            }
+            if (!poll_words<4>(src, need, tag ^ c.poll_xor, bits, c.spin)) bad = 1;
+#pragma unroll
+            for (int q = 0; q < 4; q++)
+                if (need[q]) wo_raw[i0 + q * 256 + t] = bits[q];
+        }
+        lds_barrier();
+        const ActQ8_0 A(wo_act, nbo, 0);
+        for (int k = t; k < nbo; k += 256) {
+            const uint32_t *w9 = wo_raw + 9 * k;
+            const int4 a0 = make_int4(w9[0], w9[1], w9[2], w9[3]), a1 = make_int4(w9[4], w9[5], w9[6], w9[7]);
+            A.q0[k] = a0;
+            A.q1[k] = a1;
+            A.d[k] = h2f((uint16_t)(w9[8] & 0xffff));
+            A.s[k] = sum_i8x16(a0) + sum_i8x16(a1);
+        }
+        lds_barrier();
+        const int64_t ngo = (c.Wo.nrows + RPWO - 1) / RPWO;
+        for (int64_t gq = gw; gq < ngo; gq += NWV) {                   // wave-uniform
+            if (gq != gw) wo_load(gq);
+            float acc = 0.0f;
+#pragma unroll
+            for (int k = 0; k < UPLO; k++) {
+                const int u = go + k * LPRO;
+                if (u < units_o) acc = FW::accum(fo[k], A, u, acc);
+            }
+            acc = group_sum<LPRO>(acc);
+            const int64_t row = gq * RPWO + rgo;
+            if (go == 0 && row < c.Wo.nrows) c.wo_out[row] = bad ? __builtin_nanf("") : acc;
         }
     }
     // any poll of this workgroup that gave up (its partials or outputs are not
@@ -1307,7 +1393,7 @@ __global__ void k_attn_clear(uint64_t *w, size_t n) {
 // words T [n_head][nc][ATT_TW] (3 used) and PT [n_head][nc][hd].
 static size_t al256(size_t v) { return (v + 255) & ~(size_t)255; }
 struct AttnWs {
-    size_t err, S, Mc, Lc, P, epoch, T, PT, total;
+    size_t err, S, Mc, Lc, P, epoch, T, PT, QO, total;
 };
 static AttnWs attn_ws(int n_head, int hd, int npos_max) {
     const size_t nc = (npos_max + ATT_CHUNK - 1) / ATT_CHUNK;
@@ -1320,7 +1406,8 @@ static AttnWs attn_ws(int n_head, int hd, int npos_max) {
     w.epoch = w.P + al256((size_t)n_head * nc * hd * 4);
     w.T = w.epoch + 256;
     w.PT = w.T + al256((size_t)n_head * nc * ATT_TW * 8);
-    w.total = w.PT + al256((size_t)n_head * nc * hd * 8);
+    w.QO = w.PT + al256((size_t)n_head * nc * hd * 8);
+    w.total = w.QO + al256((size_t)n_head * hd / 32 * 128);
     return w;
 }
 size_t attn_workspace_bytes(int n_head, int hd, int npos_max) { return attn_ws(n_head, hd, npos_max).total; }
@@ -1374,6 +1461,53 @@ bool attn_fused_fits(int kv_type, int n_head, int n_kv, int hd, int npos_max) {
     return (int64_t)n_kv * nc <= cap;
 }
 
+// ------------------------------------------------------------- Wo fold --
+// The (type, LPR, UPL) shapes of the output projection the one-launch form
+// takes (gemv_shape's choice for Wo; q4_0 / q8_0 rows of 256 and 2048), for
+// groups of 2 query heads of 64 or 256.
+#define G4_WO_SHAPES(X) X(FQ4_0, 16, 2) X(FQ4_0, 16, 4) X(FQ8_0, 16, 2) X(FQ8_0, 32, 2)
+
+template <int GRP, int HD>
+static hipError_t attn_wo_go(AttnCtx c, int n_kv, int nc, uint8_t *qo, hipStream_t s) {
+    if constexpr (GRP == 2 && (HD == 64 || HD == 256)) {
+        c.QO = (uint64_t *)qo;
+        int lpr, upl;
+        gemv_shape(c.Wo.type, c.Wo.nb, &lpr, &upl);
+#define G4_WOL(F, L, U)                                                                                    \
+        if (c.Wo.type == F::type && lpr == L && upl == U) {                                                 \
+            hipLaunchKernelGGL((k_attn_fused_f16<GRP, HD, void, 32, 4, F, L, U>), dim3(n_kv, nc), dim3(256), 0, s, c); \
+            return hipGetLastError();                                                                      \
+        }
+        G4_WO_SHAPES(G4_WOL)
+#undef G4_WOL
+    }
+    return hipErrorInvalidValue;
+}
+
+template <int GRP, int HD>
+static int wo_capacity(int wtype, int lpr, int upl) {
+    if constexpr (GRP == 2 && (HD == 64 || HD == 256)) {
+#define G4_WOC(F, L, U)                                                                                     \
+        if (wtype == F::type && lpr == L && upl == U)                                                       \
+            return resident_capacity(reinterpret_cast<const void *>(k_attn_fused_f16<GRP, HD, void, 32, 4, F, L, U>), 0);
+        G4_WO_SHAPES(G4_WOC)
+#undef G4_WOC
+    }
+    return 0;
+}
+
+bool attn_wo_fits(const g4h_tensor &Wo, const QkvArgs &a, int npos_max) {
+    if (a.kv_type != F16 || a.window || a.ring || !attn_fused_fits(F16, a.n_head, a.n_kv, a.hd, npos_max)) return false;
+    if (a.n_head / a.n_kv != 2 || (a.hd != 64 && a.hd != 256)) return false;
+    if ((Wo.type != Q4_0 && Wo.type != Q8_0) || Wo.ncols != (int64_t)a.n_head * a.hd || Wo.nb > ATT_WO_MAXB) return false;
+    int lpr, upl;
+    gemv_shape(Wo.type, Wo.nb, &lpr, &upl);
+    if (Wo.nb > (int64_t)lpr * upl) return false;                     // one pass over each row
+    const int nc = (npos_max + ATT_CHUNK - 1) / ATT_CHUNK;
+    const int cap = a.hd == 64 ? wo_capacity<2, 64>(Wo.type, lpr, upl) : wo_capacity<2, 256>(Wo.type, lpr, upl);
+    return (int64_t)a.n_kv * nc <= cap;
+}
+
 template <int KV, int GRP, int HD>
 static hipError_t attn_go(AttnCtx c, int n_head, int n_kv, int npos_max, uint8_t *ws, const AttnTag *tg, hipStream_t s) {
     const AttnWs w = attn_ws(n_head, c.a.hd, npos_max);
@@ -1402,10 +1536,12 @@ static hipError_t attn_go(AttnCtx c, int n_head, int n_kv, int npos_max, uint8_t
                 c.tag_mul = 1;
                 c.tag_add = 0;
             }
+            if (c.wo_out) return attn_wo_go<GRP, HD>(c, n_kv, nc, ws + w.QO, s);
             hipLaunchKernelGGL((k_attn_fused_f16<GRP, HD>), dim3(n_kv, nc), dim3(256), 0, s, c);
             return hipGetLastError();
         }
     }
+    if (c.wo_out) return hipErrorInvalidValue;                        // the fold exists in the one-launch form only
     if constexpr (KV == F16) hipLaunchKernelGGL((k_attn_scores_f16<GRP, HD>), dim3(n_kv, nc), dim3(256), 0, s, c);
     else hipLaunchKernelGGL((k_attn_scores_q8<KV, GRP, HD>), dim3(n_kv, nc), dim3(128), 0, s, c);
     hipLaunchKernelGGL((k_attn_v<KV, GRP, HD>), dim3(n_kv, nc), dim3(256), 0, s, c);
@@ -1618,9 +1754,11 @@ hipError_t launch_attn_qkv(const g4h_tensor &W, const GemvPro &pro, const QkvArg
 // q: prepared queries, or nullptr with `qkv` the raw q|k|v projection output
 // to prepare (its k/v rows go into the caches at position npos - 1).
 hipError_t launch_attn_decode(const float *q, const float *qkv, const QkvArgs &a, int npos, const int *npos_dev, int npos_max,
-                              float *out, uint8_t *q8out, uint8_t *ws, hipStream_t s, const AttnTag *tag) {
+                              float *out, uint8_t *q8out, uint8_t *ws, hipStream_t s, const AttnTag *tag, const g4h_tensor *Wo,
+                              float *wo_out) {
     if (a.hd % 64 || a.hd > 256 || a.n_kv <= 0 || a.n_head % a.n_kv) return hipErrorInvalidValue;
     if (qkv && (!a.rope || !a.q_norm || !a.k_norm)) return hipErrorInvalidValue;
+    if (Wo && (!wo_out || !attn_wo_fits(*Wo, a, npos_max))) return hipErrorInvalidValue;
     AttnCtx c{};
     c.q = q;
     c.qkv = qkv;
@@ -1629,6 +1767,10 @@ hipError_t launch_attn_decode(const float *q, const float *qkv, const QkvArgs &a
     c.npos_dev = npos_dev;
     c.out = out;
     c.q8out = q8out;
+    if (Wo) {
+        c.Wo = *Wo;
+        c.wo_out = wo_out;
+    }
     const int grp = a.n_head / a.n_kv;
 #define G4_ATT(KV, G)                                                                                 \
     if (a.kv_type == KV && grp == G) {                                                                \

@@ -74,13 +74,19 @@ static constexpr int kBatchMax = 64;   // G4_BATCH_MAX, g4run.h:23
 //   FUSE_HEAD  residual + output RMSNorm + q8_0 in front of the head
 //   FUSE_QATT  the Wqkv GEMV with its norm prologue inside the one-launch
 //              attention, its rows computed while the K stream is in flight
-enum { FUSE_QKV = 1, FUSE_GU = 2, FUSE_DOWN = 4, FUSE_HEAD = 8, FUSE_QATT = 16 };
+//   FUSE_WO    the Wo GEMV inside the one-launch attention, after a hand-off
+//              of the q8_0 head rows (its weights prefetched during the
+//              attention's own hand-offs)
+enum { FUSE_QKV = 1, FUSE_GU = 2, FUSE_DOWN = 4, FUSE_HEAD = 8, FUSE_QATT = 16, FUSE_WO = 32 };
 // measured on the BASELINE decode step (tok/s, 128 steps at ctx 8192): none
-// 842, QKV 856, GU 928, QKV|GU 955, QKV|GU|QATT 929.  In the QATT launch a
-// wave that has queued its K stream cannot run the projection until the
+// 842, QKV 856, GU 928, QKV|GU 955, QKV|GU|QATT 929; QKV|GU 968 against
+// QKV|GU|WO 991 (two runs each, after later kernel work).  In the QATT launch
+// a wave that has queued its K stream cannot run the projection until the
 // stream drains far enough to accept its loads, so the rows come out ~5.6 us
 // into the launch and the attention starts later than after a separate GEMV.
-static constexpr int kDefaultFuse = FUSE_QKV | FUSE_GU;
+// The WO hand-off costs most of the Wo launch it replaces (~0.9 us net per
+// layer).
+static constexpr int kDefaultFuse = FUSE_QKV | FUSE_GU | FUSE_WO;
 
 static int model_alloc(g4h_model *m, void **p, size_t bytes) {
     if (int rc = g4h_malloc(p, bytes)) return rc;
@@ -138,7 +144,7 @@ extern "C" int g4h_model_create(const g4h_model_config *cfg, uint64_t seed, g4h_
     g4h_model *m = new g4h_model();
     m->c = c;
     m->fuse = kDefaultFuse;
-    if (const char *e = getenv("G4H_DECODE_FUSE")) m->fuse = atoi(e) & 31;
+    if (const char *e = getenv("G4H_DECODE_FUSE")) m->fuse = atoi(e) & 63;
     const int E = c.n_embd, H = c.n_head, KV = c.n_kv, hd = c.head_dim, F = c.n_ff;
     const int qkv_rows = (H + 2 * KV) * hd, qd = H * hd;
     hipStream_t s = nullptr;
@@ -334,6 +340,7 @@ extern "C" int g4h_forward_state(g4h_model *m, void *stream) {
         qa.vc = vc;
         qa.eps = c.rms_eps;
         const AttnTag tag{(const unsigned *)(m->state + 3), (unsigned)c.n_layer, (unsigned)l};
+        bool wo_done = false;                                         // Wo computed inside the attention launch
         if ((fz & FUSE_QATT) && attn_qkv_fits(*m->wqkv[l], qa, c.n_ctx)) {
             GemvPro pro;
             pro.kind = PRO_NORM;
@@ -353,14 +360,16 @@ extern "C" int g4h_forward_state(g4h_model *m, void *stream) {
                 if (l) M_HIP(launch_norm_quant(x, m->xb, prev_post, norm_of(m, l, G4H_N_ATTN), c.rms_eps, E, m->act, s));
                 M_HIP(launch_gemv(*m->wqkv[l], m->act, ast, m->qkv, 1, s));
             }
-            M_HIP(launch_attn_decode(nullptr, m->qkv, qa, 0, npos, c.n_ctx, m->att, m->act, m->ws, s, &tag));
+            wo_done = (fz & FUSE_WO) && attn_wo_fits(*m->wo[l], qa, c.n_ctx);
+            M_HIP(launch_attn_decode(nullptr, m->qkv, qa, 0, npos, c.n_ctx, m->att, m->act, m->ws, s, &tag,
+                                     wo_done ? m->wo[l] : nullptr, wo_done ? m->xb : nullptr));
         }
         float *tr = m->trace ? m->trace + (size_t)l * trace_rec : nullptr;
         // x holds this layer's input once its Wqkv launch is queued
         M_RC(trace_copy(tr, TR_X, x, E));
         M_RC(trace_copy(tr, TR_QKV, m->qkv, qkv_rows));
         M_RC(trace_copy(tr, TR_ATT, m->att, H * hd));
-        M_HIP(launch_gemv(*m->wo[l], m->act, ast, m->xb, 1, s));
+        if (!wo_done) M_HIP(launch_gemv(*m->wo[l], m->act, ast, m->xb, 1, s));
         M_RC(trace_copy(tr, TR_WO, m->xb, E));
         if ((fz & FUSE_GU) && !gelu_fits(*m->wgu[l])) {
             // the residual norm in the Wgu prologue, GELU * up as its own step

@@ -32,23 +32,32 @@ __device__ __forceinline__ double wg_sum_double(double v, double *red) {
     return r;
 }
 
-// q8_0 of four consecutive values; the 8 consecutive lanes of a 32-element
-// block all call this (the block is owned by all of them or none).  Group gi
-// writes quants 4*(gi%8).. of GGUF block gi/8 of dst; its first lane the scale.
-__device__ __forceinline__ void q8_store4(const float v[4], int gi, bool own, uint8_t *dst) {
+// q8_0 of four consecutive values (quants.c:74-109): lane k's 4 quant bytes
+// (elements 4k..4k+3 of the block) and the block's fp16 scale; the 8 lanes of
+// a block call it together
+__device__ __forceinline__ uint32_t q8_pack4(const float v[4], uint16_t *d16) {
     float am = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
     am = group_max<8>(am);
-    if (!own) return;
     const float id = am != 0.0f ? 127.0f / am : 0.0f;
     uint32_t pk = 0;
 #pragma unroll
     for (int j = 0; j < 4; j++) pk |= ((uint32_t)(int)__builtin_rintf(v[j] * id) & 0xffu) << (8 * j);
+    *d16 = f2h(am * (1.0f / 127.0f));
+    return pk;
+}
+// the same into GGUF blocks: the 8 consecutive lanes of a 32-element block all
+// call this (the block is owned by all of them or none).  Group gi writes
+// quants 4*(gi%8).. of block gi/8 of dst; its first lane the scale.
+__device__ __forceinline__ void q8_store4(const float v[4], int gi, bool own, uint8_t *dst) {
+    uint16_t d16;
+    const uint32_t pk = q8_pack4(v, &d16);
+    if (!own) return;
     const int b = gi >> 3, k = gi & 7;
     uint8_t *blk = dst + (size_t)b * 34;
     uint16_t *p16 = (uint16_t *)(blk + 2 + 4 * k);
     p16[0] = (uint16_t)(pk & 0xffff);
     p16[1] = (uint16_t)(pk >> 16);
-    if (k == 0) *(uint16_t *)blk = f2h(am * (1.0f / 127.0f));
+    if (k == 0) *(uint16_t *)blk = d16;
 }
 
 // q4_0 of four consecutive values (quants.c:125-144 as the reference build
