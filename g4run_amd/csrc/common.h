@@ -73,6 +73,21 @@ __device__ __forceinline__ uint32_t partner_u32(uint32_t v) {
         return (threadIdx.x & 32) ? r[0] : r[1];
     }
 }
+// Unsigned maximum over the wave, returned as a wave-uniform value: four
+// exchanges within each 16-lane row, then the broadcasts of lane 15 into rows
+// 1 and 3 and of lane 31 into rows 2 and 3, after which lane 63 holds the
+// maximum.  For non-negative floats the bit patterns order as the values, so
+// this is also their maximum (no NaN canonicalisation per step).
+__device__ __forceinline__ uint32_t wave_umax(uint32_t u) {
+    u = max(u, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)u, 0xB1, 0xF, 0xF, false));    // quad_perm [1,0,3,2]
+    u = max(u, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)u, 0x4E, 0xF, 0xF, false));    // quad_perm [2,3,0,1]
+    u = max(u, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)u, 0x141, 0xF, 0xF, false));   // row_half_mirror
+    u = max(u, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)u, 0x140, 0xF, 0xF, false));   // row_mirror
+    u = max(u, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)u, 0x142, 0xA, 0xF, false));   // row_bcast:15
+    u = max(u, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)u, 0x143, 0xC, 0xF, false));   // row_bcast:31
+    return (uint32_t)__builtin_amdgcn_readlane((int)u, 63);
+}
+
 // exactly lane ^ 8 (DPP row_ror:8), for exchanges between lanes that hold
 // different quantities (partner<8> pairs lane i with 15 - i)
 __device__ __forceinline__ float xor8(float v) {

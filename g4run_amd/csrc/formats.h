@@ -140,19 +140,26 @@ __device__ __forceinline__ void q8_lds4(const float v[4], int j, bool own, uint8
     }
 }
 
-// q8_K quantization of fp32 activations straight into the LDS layout, with the
-// arithmetic of the standalone quantizer (k_quant.hip, quants.c:146-175), so
-// the staged token is bit-identical to quantizing first.  One wave holds one
-// 256-element superblock sb of token t (lane l: elements 4l..4l+3); the whole
-// wave calls it (the maximum and the 16-element sums are lane shuffles) and
-// writes only with `own` (uniform over the wave).
-__device__ __forceinline__ void q8K_lds4(const float v[4], int sb, bool own, uint8_t *lds, int nb, int t) {
-    const int l = threadIdx.x & 63;
+// q8_K arithmetic of one 256-element superblock held by one wave (lane l:
+// elements 4l..4l+3; quants.c:146-175), shared by the standalone quantizer and
+// the GEMV's in-kernel one, so both give the same bits.  The whole wave calls
+// it.  pk: the lane's four quants; s16: the sum of the 16 quants of lanes
+// 4k..4k+3; d: the superblock scale (max * fp32(-1/127), the shipped build's
+// folding of 1/iscale).
+struct Q8KLane {
+    uint32_t pk;
+    int s16;
+    float d;
+};
+__device__ __forceinline__ Q8KLane q8K_wave(const float v[4]) {
     // value of largest magnitude, first occurrence on ties (quants.c:150-154):
-    // the wave maximum of |x| (VALU lane exchanges), then the lowest element
-    // index that reaches it (ballots), then that element's signed value
-    const float am = group_max<64>(fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3]))));
-    int first = 256;
+    // the wave maximum of |x| (unsigned lane exchanges of the bit patterns),
+    // then the lowest element index that reaches it (ballots), then that
+    // element's signed value.  NaN elements are passed over, as the reference's
+    // `ax > amax` passes them; an all-NaN superblock quantizes as all-zero.
+    const float lm = fmaxf(fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), 0.0f), fmaxf(fabsf(v[2]), fabsf(v[3])));
+    const float am = __builtin_bit_cast(float, wave_umax(__builtin_bit_cast(uint32_t, lm)));
+    int first = 255;
 #pragma unroll
     for (int i = 0; i < 4; i++) {
         const uint64_t m = __ballot(fabsf(v[i]) == am);
@@ -161,26 +168,34 @@ __device__ __forceinline__ void q8K_lds4(const float v[4], int sb, bool own, uin
     const int fi = first & 3;
     const float mine = fi == 0 ? v[0] : fi == 1 ? v[1] : fi == 2 ? v[2] : v[3];
     const float bv = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, mine), first >> 2));
-    uint32_t pk = 0;
-    int s = 0;
-    float d = 0.0f;
+    Q8KLane r{0u, 0, 0.0f};
     if (am != 0.0f) {
         const float iscale = -127.0f / bv;
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             int q = rne_prod(iscale, v[i]);
             q = q < 127 ? q : 127;
-            pk |= ((uint32_t)q & 0xffu) << (8 * i);
-            s += q;
+            r.pk |= ((uint32_t)q & 0xffu) << (8 * i);
+            r.s16 += q;
         }
-        d = bv * (-1.0f / 127.0f);
+        r.d = bv * (-1.0f / 127.0f);
     }
-    s = group_isum<4>(s);                                          // the 16 elements of lanes 4k..4k+3
+    r.s16 = group_isum<4>(r.s16);
+    return r;
+}
+
+// q8_K quantization of fp32 activations straight into the LDS layout (the
+// arithmetic of q8K_wave, so the staged token is bit-identical to quantizing
+// first).  One wave holds superblock sb of token t; the whole wave calls it
+// and writes only with `own` (uniform over the wave).
+__device__ __forceinline__ void q8K_lds4(const float v[4], int sb, bool own, uint8_t *lds, int nb, int t) {
+    const int l = threadIdx.x & 63;
+    const Q8KLane r = q8K_wave(v);
     if (!own) return;
     uint8_t *p = lds + (size_t)t * ActQ8_K::bytes_per_token(nb) + (size_t)sb * ActQ8_K::SB;
-    ((uint32_t *)(p + 16))[l] = pk;
-    if ((l & 3) == 0) ((int16_t *)(p + 272))[l >> 2] = (int16_t)s;
-    if (l == 0) *(float *)(p + 12) = d;
+    ((uint32_t *)(p + 16))[l] = r.pk;
+    if ((l & 3) == 0) ((int16_t *)(p + 272))[l >> 2] = (int16_t)r.s16;
+    if (l == 0) *(float *)(p + 12) = r.d;
 }
 
 template <int NB>
@@ -320,13 +335,21 @@ struct FQ4_K {
         f.h = ld4(b);
         f.q0 = ld4(b + 16 + 32 * p); f.q1 = ld4(b + 32 + 32 * p);   // plain: the header shares these lines
     }
-    static __device__ __forceinline__ uint32_t sbyte(const Frag &f, int k) {   // scales[k], k < 12
-        const uint32_t w = k < 4 ? (uint32_t)f.h.y : k < 8 ? (uint32_t)f.h.z : (uint32_t)f.h.w;
-        return (w >> (8 * (k & 3))) & 0xff;
-    }
-    static __device__ __forceinline__ void scale_min(const Frag &f, int j, int &sc, int &mn) {
-        if (j < 4) { sc = sbyte(f, j) & 63; mn = sbyte(f, j + 4) & 63; }
-        else { sc = (sbyte(f, j + 4) & 15) | ((sbyte(f, j - 4) >> 6) << 4); mn = (sbyte(f, j + 4) >> 4) | ((sbyte(f, j) >> 6) << 4); }
+    // 6-bit scale and min of sub-blocks 2p and 2p+1 (quants.c get_scale_min_k4:
+    // j < 4 from the low six bits of scales[j] / scales[j+4]; j >= 4 from the
+    // nibbles of scales[j+4] and the top two bits of scales[j-4] / scales[j]),
+    // built four sub-blocks at a time in one register and without a branch on
+    // p: the lanes of a wave hold different parts.
+    static __device__ __forceinline__ void scale_min_pair(const Frag &f, int p, int &sc0, int &m0, int &sc1, int &m1) {
+        const uint32_t y = (uint32_t)f.h.y, z = (uint32_t)f.h.z, w = (uint32_t)f.h.w;
+        const bool hi = p >= 2;
+        const uint32_t sc = hi ? (w & 0x0f0f0f0fu) | ((y >> 2) & 0x30303030u) : y & 0x3f3f3f3fu;
+        const uint32_t mn = hi ? ((w >> 4) & 0x0f0f0f0fu) | ((z >> 2) & 0x30303030u) : z & 0x3f3f3f3fu;
+        const int sh = 16 * (p & 1);
+        sc0 = (int)((sc >> sh) & 0xff);
+        sc1 = (int)((sc >> (sh + 8)) & 0xff);
+        m0 = (int)((mn >> sh) & 0xff);
+        m1 = (int)((mn >> (sh + 8)) & 0xff);
     }
     static __device__ __forceinline__ void isums(const Frag &f, const Act &A, int u, int &is, int &ms) {
         const int sb = u >> 2, p = u & 3, m = 0x0F0F0F0F;
@@ -341,11 +364,11 @@ struct FQ4_K {
         sh = dot4((w[1] >> 4) & m, h0.y, sh); sh = dot4((w[2] >> 4) & m, h0.z, sh); sh = dot4((w[3] >> 4) & m, h0.w, sh);
         sh = dot4((w[4] >> 4) & m, h1.x, sh); sh = dot4((w[5] >> 4) & m, h1.y, sh); sh = dot4((w[6] >> 4) & m, h1.z, sh); sh = dot4((w[7] >> 4) & m, h1.w, sh);
         int sc0, m0, sc1, m1;
-        scale_min(f, 2 * p, sc0, m0);
-        scale_min(f, 2 * p + 1, sc1, m1);
+        scale_min_pair(f, p, sc0, m0, sc1, m1);
         const int16_t *bs = A.bs(sb) + 4 * p;
-        is = sc0 * sl + sc1 * sh;
-        ms = m0 * (bs[0] + bs[1]) + m1 * (bs[2] + bs[3]);
+        // 24-bit products: |sl|, |sh| <= 32*15*128 and |bs[i] + bs[i+1]| <= 4096
+        is = __mul24(sc0, sl) + __mul24(sc1, sh);
+        ms = __mul24(m0, bs[0] + bs[1]) + __mul24(m1, bs[2] + bs[3]);
     }
     // superblock value d_a*(d_w*isum - dmin_w*msum) (quants.c:744-758), spread
     // over the four parts
@@ -403,11 +426,11 @@ struct FQ5_K {
         FQ4_K::Frag hf;
         hf.h = f.h;
         int sc0, m0, sc1, m1;
-        FQ4_K::scale_min(hf, c0, sc0, m0);
-        FQ4_K::scale_min(hf, c1, sc1, m1);
+        FQ4_K::scale_min_pair(hf, p, sc0, m0, sc1, m1);
         const int16_t *bs = A.bs(sb) + 4 * p;
-        is = sc0 * sl + sc1 * sh;
-        ms = m0 * (bs[0] + bs[1]) + m1 * (bs[2] + bs[3]);
+        // 24-bit products: |sl|, |sh| <= 32*31*128 and |bs[i] + bs[i+1]| <= 4096
+        is = __mul24(sc0, sl) + __mul24(sc1, sh);
+        ms = __mul24(m0, bs[0] + bs[1]) + __mul24(m1, bs[2] + bs[3]);
     }
     // superblock value d_a*(d_w*isum - dmin_w*msum), spread over the four parts
     static __device__ __forceinline__ float accum(const Frag &f, const Act &A, int u, float acc) {

@@ -74,13 +74,22 @@ __global__ __launch_bounds__(XQ == 4 ? 1024 : 512) void k_gemv(g4h_tensor W, con
 #pragma unroll
     for (int k = 0; k < UPL; k++) F::load(fr[k], W, row, min(g + k * LPR, units - 1));
     issue_order();                                                   // the whole stream goes out before any wait
-    if constexpr (XQ > 0) {
+    if constexpr (XQ > 0 && QK) {
 #pragma unroll
         for (int s = 0; s < XQ; s++) {                                   // no branch: keeps the x loads up front
             const int gi = threadIdx.x + s * blockDim.x;
             const int t = gi / gpt;
-            if constexpr (QK) q8_lds4(xv[s], gi - t * gpt, gi < NB * gpt, lds, (int)W.nb, t);
-            else q8K_lds4(xv[s], (gi - t * gpt) >> 6, gi < NB * gpt, lds, (int)W.nb, t);   // a wave = a superblock
+            q8_lds4(xv[s], gi - t * gpt, gi < NB * gpt, lds, (int)W.nb, t);
+        }
+    } else if constexpr (XQ > 0) {
+        // a wave = a superblock per slot (one token: gemv_fused_fits); slots
+        // past the last superblock are skipped by the whole wave
+        static_assert(NB == 1, "K-quant weights quantize one fp32 token in-kernel");
+        const int wbase = (int)(threadIdx.x & ~63u);
+#pragma unroll
+        for (int s = 0; s < XQ; s++) {
+            const int gw = wbase + s * (int)blockDim.x;                 // the wave's first group in this slot
+            if (__builtin_amdgcn_readfirstlane(gw) < gpt) q8K_lds4(xv[s], gw >> 6, true, lds, (int)W.nb, 0);
         }
     } else if constexpr (QK) {
         stage_q8_0_store(stg[0], lds, (int)W.nb, stage_dump<ActQ8_0>(lds, NB, (int)W.nb));

@@ -62,36 +62,12 @@ __global__ __launch_bounds__(256) void k_quantize_q8_K(const float *__restrict__
     const float *src = x + r * xs + (size_t)sb * 256 + 4 * l;
     float v[4];
     for (int i = 0; i < 4; i++) v[i] = src[i];
-    // value of largest magnitude, first occurrence on ties (quants.c:150-154)
-    float ba = fabsf(v[0]), bv = v[0];
-    int bi = 4 * l;
-    for (int i = 1; i < 4; i++)
-        if (fabsf(v[i]) > ba) { ba = fabsf(v[i]); bv = v[i]; bi = 4 * l + i; }
-    for (int m = 1; m < 64; m <<= 1) {
-        const float oa = shfl_xor(ba, m), ov = shfl_xor(bv, m);
-        const int oi = shfl_xor(bi, m);
-        if (oa > ba || (oa == ba && oi < bi)) { ba = oa; bv = ov; bi = oi; }
-    }
-    uint8_t *blk = y + r * ys + (size_t)sb * 292;
-    uint32_t packed = 0;
-    int s = 0;
-    float d = 0.0f;
-    if (ba != 0.0f) {
-        const float iscale = -127.0f / bv;
-        for (int i = 0; i < 4; i++) {
-            int q = rne_prod(iscale, v[i]);
-            q = q < 127 ? q : 127;
-            packed |= ((uint32_t)q & 0xffu) << (8 * i);
-            s += q;
-        }
-        d = bv * (-1.0f / 127.0f);
-    }
-    s += shfl_xor(s, 1);
-    s += shfl_xor(s, 2);
+    const Q8KLane q = q8K_wave(v);
     if (ok) {
-        ((uint32_t *)(blk + 4))[l] = packed;
-        if ((l & 3) == 0) ((int16_t *)(blk + 260))[l >> 2] = (int16_t)s;
-        if (l == 0) *(float *)blk = d;
+        uint8_t *blk = y + r * ys + (size_t)sb * 292;
+        ((uint32_t *)(blk + 4))[l] = q.pk;
+        if ((l & 3) == 0) ((int16_t *)(blk + 260))[l >> 2] = (int16_t)q.s16;
+        if (l == 0) *(float *)blk = q.d;
     }
 }
 

@@ -73,6 +73,29 @@ def test_quantizers_random_bit_exact(gpu, oracle, qt):
         assert np.array_equal(dev_quantize(gpu, qt, x), oracle.quantize(qt, x)), f"scale {scale}"
 
 
+def _q8_K_special_rows(cols, seed):
+    """fp32 rows whose superblocks hold the q8_K quantizer's corner cases:
+    equal magnitudes of both signs (first one wins), NaN elements, a superblock
+    of NaNs, +-inf, subnormals, a lone non-zero, signed zeros."""
+    rng = np.random.default_rng(seed)
+    x = rng.standard_normal((8, cols)).astype(np.float32)
+    x[0, 10], x[0, 200] = -4.0, 4.0                                   # tie, first is negative
+    x[0, 256 + 3], x[0, 256 + 2] = 5.0, -5.0                          # tie inside one lane
+    x[1, rng.integers(0, cols, 9)] = np.nan
+    x[2, :256] = np.nan
+    x[3, 17], x[3, 300] = np.inf, -np.inf
+    x[4] *= np.float32(1e-41)                                         # subnormal inputs
+    x[5] = 0.0
+    x[5, 123] = -0.75
+    x[6] = -0.0
+    return x
+
+
+def test_q8_K_quantizer_special_values(gpu, oracle):
+    x = _q8_K_special_rows(1024, 21)
+    assert np.array_equal(dev_quantize(gpu, 15, x), oracle.quantize(15, x))
+
+
 # ------------------------------------------------------- dequant / layout
 @pytest.mark.parametrize("name,qt", FMTS)
 def test_dequant_bit_exact(gpu, name, qt):
@@ -220,6 +243,25 @@ def test_in_kernel_quantizer_equals_prequantized(gpu, oracle, qt, rows, cols, nb
     assert np.array_equal(bits(a), bits(b))
     if nb == 1:
         assert_close(a, oracle_matmul(oracle, qt, w, x), f"{qt} {rows}x{cols}")
+
+
+@pytest.mark.parametrize("qt", [12, 14])
+def test_in_kernel_q8_K_special_values(gpu, oracle, qt):
+    """Ties, NaN elements, a NaN superblock, subnormals and zeros quantized
+    inside the GEMV give the bits of the GEMV on the standalone quantizer's
+    output, row by row."""
+    from g4run_amd import synth
+    cols = 11008 if qt == 12 else 2560
+    x = _q8_K_special_rows(cols, 5)
+    w = synth.weights(qt, 4096, cols, seed=qt)
+    t = gpu.Tensor.from_rows(qt, w, cols)
+    assert "quantized in-kernel" in gpu.matmul_describe(t, 1, 1)
+    for r in range(x.shape[0]):
+        if r == 3:
+            continue                                                  # inf scales: NaN outputs
+        a = gpu_matmul(gpu, t, x=x[r:r + 1].copy(), nb=1)
+        b = gpu_matmul(gpu, t, act=dev_quantize(gpu, 15, x[r:r + 1]), nb=1)
+        assert np.array_equal(bits(a), bits(b)), f"row {r}"
 
 
 @pytest.mark.parametrize("name,qt", FMTS)

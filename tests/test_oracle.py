@@ -87,6 +87,25 @@ def test_quantize_q8_K_closed_form(oracle):
     assert d == np.float32(-2.0) * np.float32(-1.0 / 127.0)
 
 
+def test_quantize_q8_K_ties_nan_and_empty(oracle):
+    # the first element of largest |x| sets the scale (quants.c:150-154
+    # compares strictly): +127 at 7 beats -127 at 9, so iscale = -1, x[7] ->
+    # -127, x[9] -> +127 and 2.5 -> -2.5 -> -2 (half to even); NaN elements
+    # fail `ax > amax` and, quantized, give 0 (their bits under the 1.5*2^23
+    # trick); a superblock of NaNs has amax 0 and stores zeros (quants.c:155-160)
+    x = np.zeros((1, 3 * 256), np.float32)
+    x[0, 7], x[0, 9], x[0, 20] = 127.0, -127.0, 2.5
+    x[0, 256], x[0, 300], x[0, 306] = np.nan, 2.0, np.nan
+    x[0, 512:] = np.nan
+    y = oracle.quantize(15, x)[0].reshape(3, 292)
+    q = y[:, 4:260].view(np.int8).astype(int)
+    d = y[:, 0:4].view(np.float32)[:, 0]
+    assert (q[0, 7], q[0, 9], q[0, 20]) == (-127, 127, -2) and not np.delete(q[0], [7, 9, 20]).any()
+    assert d[0] == np.float32(127.0) * np.float32(-1.0 / 127.0)
+    assert q[1, 44] == -127 and q[1, 0] == 0 and q[1, 50] == 0 and d[1] == np.float32(2.0) * np.float32(-1.0 / 127.0)
+    assert not y[2].any()
+
+
 # ---------------------------------------------------- dots / dequant / sums
 FMTS = [("q8_0", 8), ("q4_0", 2), ("q2_K", 10), ("q3_K", 11), ("q4_K", 12), ("q5_K", 13), ("q6_K", 14), ("tq2_0", 35)]
 
