@@ -113,7 +113,9 @@ extern "C" int g4h_malloc(void **ptr, size_t bytes) {
     return dev_alloc(ptr, bytes);
 }
 extern "C" int g4h_free(void *ptr) {
-    if (ptr) G4_HIP(hipFree(ptr));
+    if (!ptr) return G4H_OK;
+    g4::attn_ws_forget(ptr);                                     // a later allocation there starts uncleared
+    G4_HIP(hipFree(ptr));
     return G4H_OK;
 }
 extern "C" int g4h_memcpy_h2d(void *d, const void *s, size_t n, void *st) {

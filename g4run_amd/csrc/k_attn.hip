@@ -156,6 +156,12 @@ struct AttnCtx {
     uint64_t *T, *PT;
     const unsigned *epoch;
     unsigned tag_mul, tag_add;
+    // self-advancing epoch (calls without an external epoch): every workgroup
+    // stores a tagged word in SW [grid] once it has this launch's tag; the
+    // last workgroup polls them all and then stores the tag into *adv, so the
+    // next launch on the workspace gets the next tag
+    unsigned *adv;
+    uint64_t *SW;
     unsigned *err;           // set when a poll gives up
     unsigned spin;           // polls give up after this many retries
     uint32_t poll_xor;       // nonzero (test hook only): polls wait for a tag no store carries
@@ -1048,6 +1054,7 @@ __global__ __launch_bounds__(256) void k_attn_fused_f16(AttnCtx c) {
     const int nch = (npos + ATT_CHUNK - 1) / ATT_CHUNK;
     const bool live = ch < nch;                                      // uniform over the workgroup
     if (t == 0) bad = 0;
+    if (c.adv && t == 0) st_tag(c.SW + ((size_t)ch * gridDim.x + kvh), 0u, tag);
     const int j0 = ch * ATT_CHUNK + wave * 32, j = j0 + lane;      // lane < 32 owns position j
     const bool pos_chunk = (QKV || c.qkv) && ch == p / ATT_CHUNK;
     PrepF16<GRP> st;
@@ -1367,6 +1374,25 @@ __global__ __launch_bounds__(256) void k_attn_fused_f16(AttnCtx c) {
             if (go == 0 && row < c.Wo.nrows) c.wo_out[row] = bad ? __builtin_nanf("") : acc;
         }
     }
+    if (c.adv && kvh == (int)gridDim.x - 1 && ch == (int)gridDim.y - 1) {   // uniform over the workgroup
+        // every workgroup of the launch has read the epoch word: advance it
+        // (also after a poll gave up, so that tags never repeat)
+        const int nwg = (int)(gridDim.x * gridDim.y);
+        for (int i0 = 0; i0 < nwg; i0 += 4 * 256) {                  // uniform
+            const uint64_t *src[4];
+            bool need[4];
+            uint32_t bits[4];
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const int i = i0 + q * 256 + t;
+                src[q] = c.SW + min(i, nwg - 1);
+                need[q] = i < nwg;
+            }
+            if (!poll_words<4>(src, need, tag ^ c.poll_xor, bits, c.spin)) bad = 1;
+        }
+        lds_barrier();
+        if (t == 0) st_ag(c.adv, tag);                              // the epoch this launch's tag follows
+    }
     // any poll of this workgroup that gave up (its partials or outputs are not
     // valid) is reported, whether or not it owned a combine block
     lds_barrier();
@@ -1393,7 +1419,7 @@ __global__ void k_attn_clear(uint64_t *w, size_t n) {
 // words T [n_head][nc][ATT_TW] (3 used) and PT [n_head][nc][hd].
 static size_t al256(size_t v) { return (v + 255) & ~(size_t)255; }
 struct AttnWs {
-    size_t err, S, Mc, Lc, P, epoch, T, PT, QO, total;
+    size_t err, S, Mc, Lc, P, epoch, T, PT, QO, SW, total;
 };
 static AttnWs attn_ws(int n_head, int hd, int npos_max) {
     const size_t nc = (npos_max + ATT_CHUNK - 1) / ATT_CHUNK;
@@ -1407,10 +1433,45 @@ static AttnWs attn_ws(int n_head, int hd, int npos_max) {
     w.T = w.epoch + 256;
     w.PT = w.T + al256((size_t)n_head * nc * ATT_TW * 8);
     w.QO = w.PT + al256((size_t)n_head * nc * hd * 8);
-    w.total = w.QO + al256((size_t)n_head * hd / 32 * 128);
+    w.SW = w.QO + al256((size_t)n_head * hd / 32 * 128);
+    w.total = w.SW + al256((size_t)n_head * nc * 8);
     return w;
 }
+
 size_t attn_workspace_bytes(int n_head, int hd, int npos_max) { return attn_ws(n_head, hd, npos_max).total; }
+
+// Workspaces whose epoch and tagged words are known to be in order for their
+// layout (cleared once, then advanced on the device by every launch): the
+// workspace pointer with its layout's (epoch offset, size), or (0, 0) for a
+// workspace seen before whose words are not in order.  A clear recorded into
+// a graph capture does not count, since it runs only with the graph.
+static std::mutex g_ws_mu;
+static std::map<uintptr_t, std::pair<size_t, size_t>> g_ws_ready;
+enum WsState { WS_READY, WS_CLEAR_TAGS, WS_CLEAR_ALL };
+static WsState attn_ws_ready(const uint8_t *ws, const AttnWs &w, hipStream_t s) {
+    hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(s, &st) != hipSuccess) st = hipStreamCaptureStatusNone;
+    const auto key = std::make_pair(w.epoch, w.total);
+    std::lock_guard<std::mutex> lk(g_ws_mu);
+    const auto it = g_ws_ready.find((uintptr_t)ws);
+    if (it != g_ws_ready.end() && it->second == key) return WS_READY;
+    const WsState r = it == g_ws_ready.end() ? WS_CLEAR_ALL : WS_CLEAR_TAGS;   // a new workspace: its error word too
+    // the caller clears it now, in stream order (under capture only when the graph runs)
+    g_ws_ready[(uintptr_t)ws] = st == hipStreamCaptureStatusNone ? key : std::make_pair(size_t(0), size_t(0));
+    return r;
+}
+void attn_ws_forget(const void *p) {
+    std::lock_guard<std::mutex> lk(g_ws_mu);
+    g_ws_ready.erase((uintptr_t)p);
+}
+// a launch that writes the workspace in another layout (scores, partials)
+// may overwrite the registered layout's epoch and tagged words
+static void attn_ws_other_layout(const uint8_t *ws, const AttnWs *w) {
+    std::lock_guard<std::mutex> lk(g_ws_mu);
+    const auto it = g_ws_ready.find((uintptr_t)ws);
+    if (it != g_ws_ready.end() && (!w || it->second != std::make_pair(w->epoch, w->total)))
+        it->second = std::make_pair(size_t(0), size_t(0));
+}
 
 static unsigned g_attn_spin = ATT_SPIN_LIMIT;
 static uint32_t g_attn_poll_xor = 0;
@@ -1528,13 +1589,22 @@ static hipError_t attn_go(AttnCtx c, int n_head, int n_kv, int npos_max, uint8_t
                 c.epoch = tg->epoch;
                 c.tag_mul = tg->mul;
                 c.tag_add = tg->add;
-            } else {                                                 // tags start over on a cleared workspace
-                const size_t nw = (w.total - w.epoch) / 8;           // epoch and tagged words, not the error word
-                hipLaunchKernelGGL(k_attn_clear, dim3((unsigned)std::min<size_t>((nw + 255) / 256, 1024)), dim3(256), 0, s,
-                                   (uint64_t *)(ws + w.epoch), nw);
+            } else {
+                // the workspace's own epoch word, advanced by each launch: the
+                // words are cleared on a workspace's first use with a layout
+                const WsState ready = attn_ws_ready(ws, w, s);
+                if (ready != WS_READY) {
+                    const size_t nw = (w.total - w.epoch) / 8;       // epoch and tagged words
+                    hipLaunchKernelGGL(k_attn_clear, dim3((unsigned)std::min<size_t>((nw + 255) / 256, 1024)), dim3(256), 0, s,
+                                       (uint64_t *)(ws + w.epoch), nw);
+                    if (ready == WS_CLEAR_ALL)                       // and the error word of a new workspace
+                        hipLaunchKernelGGL(k_attn_clear, dim3(1), dim3(256), 0, s, (uint64_t *)(ws + w.err), (size_t)1);
+                }
                 c.epoch = (const unsigned *)(ws + w.epoch);
                 c.tag_mul = 1;
                 c.tag_add = 0;
+                c.adv = (unsigned *)(ws + w.epoch);
+                c.SW = (uint64_t *)(ws + w.SW);
             }
             if (c.wo_out) return attn_wo_go<GRP, HD>(c, n_kv, nc, ws + w.QO, s);
             hipLaunchKernelGGL((k_attn_fused_f16<GRP, HD>), dim3(n_kv, nc), dim3(256), 0, s, c);
@@ -1542,6 +1612,7 @@ static hipError_t attn_go(AttnCtx c, int n_head, int n_kv, int npos_max, uint8_t
         }
     }
     if (c.wo_out) return hipErrorInvalidValue;                        // the fold exists in the one-launch form only
+    attn_ws_other_layout(ws, &w);                                    // this layout's S..P lie below its epoch word
     if constexpr (KV == F16) hipLaunchKernelGGL((k_attn_scores_f16<GRP, HD>), dim3(n_kv, nc), dim3(256), 0, s, c);
     else hipLaunchKernelGGL((k_attn_scores_q8<KV, GRP, HD>), dim3(n_kv, nc), dim3(128), 0, s, c);
     hipLaunchKernelGGL((k_attn_v<KV, GRP, HD>), dim3(n_kv, nc), dim3(256), 0, s, c);
@@ -1651,6 +1722,7 @@ hipError_t launch_attn_prep_rows(const float *qkv, const QkvArgs &a, int pos0, i
 hipError_t launch_attn_batch(const float *q, const QkvArgs &a, int npos0, int nb, float *out, uint8_t *q8out, uint8_t *ws,
                              hipStream_t s, size_t q8_stride) {
     if (a.hd % 64 || a.hd > 256 || a.n_kv <= 0 || a.n_head % a.n_kv || nb < 1 || npos0 < 1 || nb > 65535) return hipErrorInvalidValue;
+    attn_ws_other_layout(ws, nullptr);                               // blocks per token: any byte may change
     AttnCtx c{};
     c.q = q;
     c.a = a;

@@ -159,6 +159,8 @@ hipError_t launch_matmul_mfma(const g4h_tensor &W, const float *x, size_t x_stri
 
 // k_attn.hip
 size_t attn_workspace_bytes(int n_head, int hd, int npos_max);
+// drop a workspace from the cleared-workspace registry (its memory is freed)
+void attn_ws_forget(const void *p);
 // The one-launch form's bounded polls give up after a fixed retry count; a
 // workgroup that gives up writes NaN and sets the workspace's error word at
 // offset 0 (ATTN_ERR_OFFSET), which stays set until the host clears it.  Test

@@ -182,7 +182,13 @@ int g4h_block_sums(const g4h_tensor *W, const void *pre_dev, size_t pre_stride, 
  * head h reads KV head h/(n_head/n_kv) (model.c:1099); no 1/sqrt(hd) factor
  * (model.c:538).  hd in {64,128,192,256}; n_head/n_kv in {1,2,4,8}.
  * ws_dev: g4h_attn_workspace_bytes() bytes of caller-owned scratch (the
- * reference's attbuf, model.c:465).  out_dev: n_head x hd fp32. */
+ * reference's attbuf, model.c:465).  out_dev: n_head x hd fp32.
+ * The workspace carries state from call to call for the one-launch form (an
+ * epoch word each launch advances on the device, and hand-off words tagged
+ * with it): the first call on a workspace pointer with a given shape clears
+ * it, later calls (graph replays included) do not.  Memory that held anything
+ * else since must have been freed with g4h_free, or be zeroed before it is
+ * used as a workspace again.  Calls that overlap on one workspace race. */
 size_t g4h_attn_workspace_bytes(int n_head, int hd, int n_pos);
 /* Diagnostic (no reference counterpart): *passes = the launches
  * g4h_attn_decode makes for this shape, 1 when the f16 cache runs as one fused

@@ -112,6 +112,49 @@ def test_attention_fused_equals_three_passes(gpu, oracle, monkeypatch, n_head, n
     assert (np.abs(fused[0] - ref) <= ATOL + RTOL * np.abs(ref)).all()
 
 
+def test_attention_epoch_advances_on_device(gpu, oracle, monkeypatch):
+    """The one-launch form tags its hand-off words with a workspace epoch word
+    that every launch advances on the device, so a workspace is cleared on its
+    first use only: back-to-back calls on a workspace that starts as garbage,
+    graph replays with new queries between them and eager calls between the
+    replays all give the three-pass bits."""
+    G = gpu
+    n_head, n_kv, hd, n_pos = 8, 4, 256, 4100
+    assert G.attn_passes(G.F16, n_head, n_kv, hd, n_pos) == 1
+    kb, vb, kh, vh = make_cache(G, oracle, G.F16, n_pos, n_kv, hd, seed=91)
+    rng = np.random.default_rng(92)
+    qs = [(rng.standard_normal((n_head, hd)) * 0.5).astype(np.float32) for _ in range(9)]
+    monkeypatch.setenv("G4H_ATTN_PASSES", "3")
+    ref = [_attn(G, q, kb, vb, G.F16, n_head, n_kv, hd, n_pos, None) for q in qs]
+    monkeypatch.delenv("G4H_ATTN_PASSES")
+    ws = G.Buffer(G.attn_workspace_bytes(n_head, hd, n_pos))
+    ws.upload(np.full(ws.nbytes, 0xA5, np.uint8))                  # not a cleared workspace
+    for i in range(4):
+        got = _attn(G, qs[i], kb, vb, G.F16, n_head, n_kv, hd, n_pos, ws)
+        assert np.array_equal(got.view(np.uint32), ref[i].view(np.uint32)), f"call {i}"
+    st = G.Stream()
+    qb = [G.Buffer(n_head * hd * 4) for _ in range(3)]
+    outs = [G.Buffer(n_head * hd * 4) for _ in range(3)]
+    for j in range(3):
+        qb[j].upload(qs[j])
+    g = G.Graph(st.ptr, lambda: [G.attn_decode(qb[j], kb, vb, G.F16, n_head, n_kv, hd, n_pos, outs[j], ws=ws,
+                                               stream=st.ptr) for j in range(3)])
+    for r in range(3):
+        sel = [(3 * r + j + 1) % 9 for j in range(3)]
+        for j in range(3):
+            qb[j].upload(qs[sel[j]])
+        g.launch(st.ptr)
+        st.synchronize()
+        for j in range(3):
+            got = outs[j].download(np.float32, (n_head, hd))
+            assert np.array_equal(got.view(np.uint32), ref[sel[j]].view(np.uint32)), f"replay {r} call {j}"
+        got = _attn(G, qs[8 - r], kb, vb, G.F16, n_head, n_kv, hd, n_pos, ws)   # an eager call between replays
+        assert np.array_equal(got.view(np.uint32), ref[8 - r].view(np.uint32)), f"eager after replay {r}"
+    assert not G.attn_status(ws)
+    o = oracle.attn_decode(qs[0], kh, vh, G.F16, n_head, n_kv, hd, n_pos - 1)
+    assert (np.abs(ref[0] - o) <= ATOL + RTOL * np.abs(o)).all()
+
+
 def test_attention_long_context_falls_back_to_three_passes(gpu, oracle):
     """A grid larger than the device holds at once runs the three passes."""
     G = gpu
