@@ -476,8 +476,8 @@ struct FQ2_K {
             s = dot4((w[3] >> (2 * j)) & 0x03030303, a.w, s);
             const int g = 8 * h + 2 * j + k;                       // 16-element group / scale index
             const int sc = (sw[g >> 2] >> (8 * (g & 3))) & 0xff;
-            isum += (sc & 15) * s;
-            msum += (sc >> 4) * bs[g];
+            isum += __mul24(sc & 15, s);                           // |s| <= 16*3*128, |bs| <= 2048
+            msum += __mul24(sc >> 4, (int)bs[g]);
         }
         is = isum; ms = msum;
     }
@@ -521,20 +521,26 @@ struct FQ3_K {
         const int sb = u >> 2, p = u & 3, h = p >> 1, k = p & 1;
         const uint32_t w[4] = {(uint32_t)f.q.x, (uint32_t)f.q.y, (uint32_t)f.q.z, (uint32_t)f.q.w};
         const uint32_t hb[4] = {(uint32_t)f.hm.x, (uint32_t)f.hm.y, (uint32_t)f.hm.z, (uint32_t)f.hm.w};
+        // hmask bit 4h+j of each byte brought to bit 2+j once per unit, so that
+        // (hh >> j) & 4 is the high bit in place: h = 1 shifts right by 2,
+        // h = 0 left by 2 (the bits that spill into the next byte land at bits
+        // 0-1 there, below any bit read)
+        uint32_t hh[4];
+#pragma unroll
+        for (int d = 0; d < 4; d++) hh[d] = h ? hb[d] >> 2 : hb[d] << 2;
         const int8_t *aq = A.q(sb) + 128 * h + 16 * k;
         const int16_t *bs = A.bs(sb);
         int total = 0;
 #pragma unroll
         for (int j = 0; j < 4; j++) {
             const int4 a = *(const int4 *)(aq + 32 * j);
-            const int sh = 4 * h + j;
             int s = 0;
-            s = dot4(((w[0] >> (2 * j)) & 0x03030303) | (((hb[0] >> sh) & 0x01010101) << 2), a.x, s);
-            s = dot4(((w[1] >> (2 * j)) & 0x03030303) | (((hb[1] >> sh) & 0x01010101) << 2), a.y, s);
-            s = dot4(((w[2] >> (2 * j)) & 0x03030303) | (((hb[2] >> sh) & 0x01010101) << 2), a.z, s);
-            s = dot4(((w[3] >> (2 * j)) & 0x03030303) | (((hb[3] >> sh) & 0x01010101) << 2), a.w, s);
+            s = dot4(((w[0] >> (2 * j)) & 0x03030303) | ((hh[0] >> j) & 0x04040404), a.x, s);
+            s = dot4(((w[1] >> (2 * j)) & 0x03030303) | ((hh[1] >> j) & 0x04040404), a.y, s);
+            s = dot4(((w[2] >> (2 * j)) & 0x03030303) | ((hh[2] >> j) & 0x04040404), a.z, s);
+            s = dot4(((w[3] >> (2 * j)) & 0x03030303) | ((hh[3] >> j) & 0x04040404), a.w, s);
             const int g = 8 * h + 2 * j + k;
-            total += scale(f, g) * (s - 4 * bs[g]);
+            total += __mul24(scale(f, g), s - 4 * bs[g]);                // |s - 4 bs| <= 16*7*128 + 4*2048
         }
         return total;
     }
@@ -589,7 +595,7 @@ struct FQ6_K {
             s = dot4(q[3], a.w, s);
             const int sbyte = k + 2 * j;                               // scales[8h + k + 2j]
             const int sc = (int)(int8_t)(((sbyte < 4 ? f.s.x : f.s.y) >> (8 * (sbyte & 3))) & 0xff);
-            total += sc * (s - 32 * bs[8 * h + 2 * j + k]);
+            total += __mul24(sc, s - 32 * bs[8 * h + 2 * j + k]);       // |s - 32 bs| <= 16*63*128 + 32*2048
         }
         return total;
     }
