@@ -647,7 +647,8 @@ extern "C" int g4h_attn_decode(const float *q, const void *kc, const void *vc, i
     a.kv_type = kv_type;
     a.kc = (uint8_t *)kc;          // read only: no preparation on this entry point
     a.vc = (uint8_t *)vc;
-    G4_HIP(launch_attn_decode(q, nullptr, a, n_pos, nullptr, n_pos, out, nullptr, (uint8_t *)ws, (hipStream_t)stream));
+    G4_HIP(launch_attn_decode(q, nullptr, a, n_pos, nullptr, n_pos, out, nullptr, (uint8_t *)ws, (hipStream_t)stream, nullptr,
+                              nullptr, nullptr, ws_bytes));
     return G4H_OK;
 }
 
@@ -673,7 +674,8 @@ extern "C" int g4h_attn_decode_window(const float *q, const void *kc, const void
     a.vc = (uint8_t *)vc;
     a.window = window;
     a.ring = ring;
-    G4_HIP(launch_attn_decode(q, nullptr, a, n_pos, nullptr, rows, out, nullptr, (uint8_t *)ws, (hipStream_t)stream));
+    G4_HIP(launch_attn_decode(q, nullptr, a, n_pos, nullptr, rows, out, nullptr, (uint8_t *)ws, (hipStream_t)stream, nullptr,
+                              nullptr, nullptr, ws_bytes));
     return G4H_OK;
 }
 

@@ -1440,37 +1440,38 @@ static AttnWs attn_ws(int n_head, int hd, int npos_max) {
 
 size_t attn_workspace_bytes(int n_head, int hd, int npos_max) { return attn_ws(n_head, hd, npos_max).total; }
 
-// Workspaces whose epoch and tagged words are known to be in order for their
-// layout (cleared once, then advanced on the device by every launch): the
-// workspace pointer with its layout's (epoch offset, size), or (0, 0) for a
-// workspace seen before whose words are not in order.  A clear recorded into
-// a graph capture does not count, since it runs only with the graph.
+// The epoch word of calls without an external epoch sits at a fixed offset of
+// the workspace header, so that it survives changes of layout (the layout
+// follows the position count): every tagged word ever stored in a workspace
+// carries a tag drawn from that one counter, at most its current value, so a
+// launch's new tag matches no stale word wherever the regions fall.
+constexpr size_t ATT_EPOCH_OFF = 128;
+// Workspaces known to hold only zeros and such tagged words ("clean"): the
+// first call on a workspace clears all of it (ws_bytes when known), a launch
+// that writes untagged data into it (the three passes, the batch form) makes
+// it unclean, and g4h_free drops it.  A clear recorded into a graph capture
+// does not count, since it runs only with the graph.
 static std::mutex g_ws_mu;
-static std::map<uintptr_t, std::pair<size_t, size_t>> g_ws_ready;
+static std::map<uintptr_t, bool> g_ws_clean;
 enum WsState { WS_READY, WS_CLEAR_TAGS, WS_CLEAR_ALL };
-static WsState attn_ws_ready(const uint8_t *ws, const AttnWs &w, hipStream_t s) {
+static WsState attn_ws_ready(const uint8_t *ws, hipStream_t s) {
     hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
     if (hipStreamIsCapturing(s, &st) != hipSuccess) st = hipStreamCaptureStatusNone;
-    const auto key = std::make_pair(w.epoch, w.total);
     std::lock_guard<std::mutex> lk(g_ws_mu);
-    const auto it = g_ws_ready.find((uintptr_t)ws);
-    if (it != g_ws_ready.end() && it->second == key) return WS_READY;
-    const WsState r = it == g_ws_ready.end() ? WS_CLEAR_ALL : WS_CLEAR_TAGS;   // a new workspace: its error word too
-    // the caller clears it now, in stream order (under capture only when the graph runs)
-    g_ws_ready[(uintptr_t)ws] = st == hipStreamCaptureStatusNone ? key : std::make_pair(size_t(0), size_t(0));
+    const auto it = g_ws_clean.find((uintptr_t)ws);
+    if (it != g_ws_clean.end() && it->second) return WS_READY;
+    const WsState r = it == g_ws_clean.end() ? WS_CLEAR_ALL : WS_CLEAR_TAGS;   // a new workspace: its error word too
+    g_ws_clean[(uintptr_t)ws] = st == hipStreamCaptureStatusNone;   // the caller clears it now, in stream order
     return r;
 }
 void attn_ws_forget(const void *p) {
     std::lock_guard<std::mutex> lk(g_ws_mu);
-    g_ws_ready.erase((uintptr_t)p);
+    g_ws_clean.erase((uintptr_t)p);
 }
-// a launch that writes the workspace in another layout (scores, partials)
-// may overwrite the registered layout's epoch and tagged words
-static void attn_ws_other_layout(const uint8_t *ws, const AttnWs *w) {
+static void attn_ws_untagged(const uint8_t *ws) {
     std::lock_guard<std::mutex> lk(g_ws_mu);
-    const auto it = g_ws_ready.find((uintptr_t)ws);
-    if (it != g_ws_ready.end() && (!w || it->second != std::make_pair(w->epoch, w->total)))
-        it->second = std::make_pair(size_t(0), size_t(0));
+    const auto it = g_ws_clean.find((uintptr_t)ws);
+    if (it != g_ws_clean.end()) it->second = false;
 }
 
 static unsigned g_attn_spin = ATT_SPIN_LIMIT;
@@ -1570,7 +1571,8 @@ bool attn_wo_fits(const g4h_tensor &Wo, const QkvArgs &a, int npos_max) {
 }
 
 template <int KV, int GRP, int HD>
-static hipError_t attn_go(AttnCtx c, int n_head, int n_kv, int npos_max, uint8_t *ws, const AttnTag *tg, hipStream_t s) {
+static hipError_t attn_go(AttnCtx c, int n_head, int n_kv, int npos_max, uint8_t *ws, const AttnTag *tg, hipStream_t s,
+                          size_t ws_bytes) {
     const AttnWs w = attn_ws(n_head, c.a.hd, npos_max);
     const int nc = (npos_max + ATT_CHUNK - 1) / ATT_CHUNK;
     c.nc = nc;
@@ -1590,20 +1592,18 @@ static hipError_t attn_go(AttnCtx c, int n_head, int n_kv, int npos_max, uint8_t
                 c.tag_mul = tg->mul;
                 c.tag_add = tg->add;
             } else {
-                // the workspace's own epoch word, advanced by each launch: the
-                // words are cleared on a workspace's first use with a layout
-                const WsState ready = attn_ws_ready(ws, w, s);
+                // the workspace's own epoch word, advanced by each launch
+                const WsState ready = attn_ws_ready(ws, s);
                 if (ready != WS_READY) {
-                    const size_t nw = (w.total - w.epoch) / 8;       // epoch and tagged words
+                    const size_t from = ready == WS_CLEAR_ALL ? w.err : ATT_EPOCH_OFF;   // the error word of a new one too
+                    const size_t nw = ((ws_bytes ? ws_bytes : w.total) - from) / 8;
                     hipLaunchKernelGGL(k_attn_clear, dim3((unsigned)std::min<size_t>((nw + 255) / 256, 1024)), dim3(256), 0, s,
-                                       (uint64_t *)(ws + w.epoch), nw);
-                    if (ready == WS_CLEAR_ALL)                       // and the error word of a new workspace
-                        hipLaunchKernelGGL(k_attn_clear, dim3(1), dim3(256), 0, s, (uint64_t *)(ws + w.err), (size_t)1);
+                                       (uint64_t *)(ws + from), nw);
                 }
-                c.epoch = (const unsigned *)(ws + w.epoch);
+                c.epoch = (const unsigned *)(ws + ATT_EPOCH_OFF);
                 c.tag_mul = 1;
                 c.tag_add = 0;
-                c.adv = (unsigned *)(ws + w.epoch);
+                c.adv = (unsigned *)(ws + ATT_EPOCH_OFF);
                 c.SW = (uint64_t *)(ws + w.SW);
             }
             if (c.wo_out) return attn_wo_go<GRP, HD>(c, n_kv, nc, ws + w.QO, s);
@@ -1612,7 +1612,7 @@ static hipError_t attn_go(AttnCtx c, int n_head, int n_kv, int npos_max, uint8_t
         }
     }
     if (c.wo_out) return hipErrorInvalidValue;                        // the fold exists in the one-launch form only
-    attn_ws_other_layout(ws, &w);                                    // this layout's S..P lie below its epoch word
+    attn_ws_untagged(ws);                                            // scores, statistics and partials
     if constexpr (KV == F16) hipLaunchKernelGGL((k_attn_scores_f16<GRP, HD>), dim3(n_kv, nc), dim3(256), 0, s, c);
     else hipLaunchKernelGGL((k_attn_scores_q8<KV, GRP, HD>), dim3(n_kv, nc), dim3(128), 0, s, c);
     hipLaunchKernelGGL((k_attn_v<KV, GRP, HD>), dim3(n_kv, nc), dim3(256), 0, s, c);
@@ -1722,7 +1722,7 @@ hipError_t launch_attn_prep_rows(const float *qkv, const QkvArgs &a, int pos0, i
 hipError_t launch_attn_batch(const float *q, const QkvArgs &a, int npos0, int nb, float *out, uint8_t *q8out, uint8_t *ws,
                              hipStream_t s, size_t q8_stride) {
     if (a.hd % 64 || a.hd > 256 || a.n_kv <= 0 || a.n_head % a.n_kv || nb < 1 || npos0 < 1 || nb > 65535) return hipErrorInvalidValue;
-    attn_ws_other_layout(ws, nullptr);                               // blocks per token: any byte may change
+    attn_ws_untagged(ws);                                            // blocks per token of untagged data
     AttnCtx c{};
     c.q = q;
     c.a = a;
@@ -1827,7 +1827,7 @@ hipError_t launch_attn_qkv(const g4h_tensor &W, const GemvPro &pro, const QkvArg
 // to prepare (its k/v rows go into the caches at position npos - 1).
 hipError_t launch_attn_decode(const float *q, const float *qkv, const QkvArgs &a, int npos, const int *npos_dev, int npos_max,
                               float *out, uint8_t *q8out, uint8_t *ws, hipStream_t s, const AttnTag *tag, const g4h_tensor *Wo,
-                              float *wo_out) {
+                              float *wo_out, size_t ws_bytes) {
     if (a.hd % 64 || a.hd > 256 || a.n_kv <= 0 || a.n_head % a.n_kv) return hipErrorInvalidValue;
     if (qkv && (!a.rope || !a.q_norm || !a.k_norm)) return hipErrorInvalidValue;
     if (Wo && (!wo_out || !attn_wo_fits(*Wo, a, npos_max))) return hipErrorInvalidValue;
@@ -1846,10 +1846,10 @@ hipError_t launch_attn_decode(const float *q, const float *qkv, const QkvArgs &a
     const int grp = a.n_head / a.n_kv;
 #define G4_ATT(KV, G)                                                                                 \
     if (a.kv_type == KV && grp == G) {                                                                \
-        if (a.hd == 64) return attn_go<KV, G, 64>(c, a.n_head, a.n_kv, npos_max, ws, tag, s);       \
-        if (a.hd == 128) return attn_go<KV, G, 128>(c, a.n_head, a.n_kv, npos_max, ws, tag, s);     \
-        if (a.hd == 192) return attn_go<KV, G, 192>(c, a.n_head, a.n_kv, npos_max, ws, tag, s);     \
-        if (a.hd == 256) return attn_go<KV, G, 256>(c, a.n_head, a.n_kv, npos_max, ws, tag, s);     \
+        if (a.hd == 64) return attn_go<KV, G, 64>(c, a.n_head, a.n_kv, npos_max, ws, tag, s, ws_bytes);       \
+        if (a.hd == 128) return attn_go<KV, G, 128>(c, a.n_head, a.n_kv, npos_max, ws, tag, s, ws_bytes);     \
+        if (a.hd == 192) return attn_go<KV, G, 192>(c, a.n_head, a.n_kv, npos_max, ws, tag, s, ws_bytes);     \
+        if (a.hd == 256) return attn_go<KV, G, 256>(c, a.n_head, a.n_kv, npos_max, ws, tag, s, ws_bytes);     \
     }
     G4_ATT(F16, 1); G4_ATT(F16, 2); G4_ATT(F16, 4); G4_ATT(F16, 8);
     G4_ATT(Q8_0, 1); G4_ATT(Q8_0, 2); G4_ATT(Q8_0, 4); G4_ATT(Q8_0, 8);

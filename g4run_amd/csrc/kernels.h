@@ -199,7 +199,7 @@ hipError_t launch_attn_prep_rows(const float *qkv, const QkvArgs &a, int pos0, i
 // GEMV on q8out's rows, with the same bits
 hipError_t launch_attn_decode(const float *q, const float *qkv, const QkvArgs &a, int npos, const int *npos_dev, int npos_max,
                               float *out, uint8_t *q8out, uint8_t *ws, hipStream_t s, const AttnTag *tag = nullptr,
-                              const g4h_tensor *Wo = nullptr, float *wo_out = nullptr);
+                              const g4h_tensor *Wo = nullptr, float *wo_out = nullptr, size_t ws_bytes = 0);
 bool attn_wo_fits(const g4h_tensor &Wo, const QkvArgs &a, int npos_max);
 hipError_t launch_kv_store(int kv_type, const float *src, uint8_t *dst, int hd, int rows, size_t dst_stride, hipStream_t s);
 // The decode step's q|k|v projection W (q4_0 / q8_0) with its PRO_NORM

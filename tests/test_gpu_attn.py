@@ -153,6 +153,17 @@ def test_attention_epoch_advances_on_device(gpu, oracle, monkeypatch):
     assert not G.attn_status(ws)
     o = oracle.attn_decode(qs[0], kh, vh, G.F16, n_head, n_kv, hd, n_pos - 1)
     assert (np.abs(ref[0] - o) <= ATOL + RTOL * np.abs(o)).all()
+    # a decode loop's growing position count changes the workspace layout
+    # every call (stale words of other layouts lie everywhere), and a
+    # three-pass call writes untagged data into the same workspace
+    for n in (n_pos - 300, n_pos - 299, n_pos - 171, 129, 128, 1, n_pos):
+        q = qs[n % 9]
+        monkeypatch.setenv("G4H_ATTN_PASSES", "3")
+        three = _attn(G, q, kb, vb, G.F16, n_head, n_kv, hd, n, ws if n == 129 else None)
+        monkeypatch.delenv("G4H_ATTN_PASSES")
+        got = _attn(G, q, kb, vb, G.F16, n_head, n_kv, hd, n, ws)
+        assert np.array_equal(got.view(np.uint32), three.view(np.uint32)), f"n_pos {n}"
+    assert not G.attn_status(ws)
 
 
 def test_attention_long_context_falls_back_to_three_passes(gpu, oracle):
