@@ -185,10 +185,11 @@ int g4h_block_sums(const g4h_tensor *W, const void *pre_dev, size_t pre_stride, 
  * reference's attbuf, model.c:465).  out_dev: n_head x hd fp32.
  * The workspace carries state from call to call for the one-launch form (an
  * epoch word each launch advances on the device, and hand-off words tagged
- * with it): the first call on a workspace pointer with a given shape clears
- * it, later calls (graph replays included) do not.  Memory that held anything
- * else since must have been freed with g4h_free, or be zeroed before it is
- * used as a workspace again.  Calls that overlap on one workspace race. */
+ * with it): the first call on a workspace clears it (ws_bytes of it), later
+ * calls of any position count (graph replays included) do not, until a
+ * three-pass or batch call stores untagged data there.  Memory that held
+ * anything else since must have been freed with g4h_free, or be zeroed before
+ * it is used as a workspace again.  Calls that overlap on one workspace race. */
 size_t g4h_attn_workspace_bytes(int n_head, int hd, int n_pos);
 /* Diagnostic (no reference counterpart): *passes = the launches
  * g4h_attn_decode makes for this shape, 1 when the f16 cache runs as one fused
