@@ -40,17 +40,23 @@ struct ProLoads {
     float v[GP_MAXS][4], d[GP_MAXS][4], wp[GP_MAXS][4], wq[GP_MAXS][4];
 };
 
+// The prologue's threads are the first bd of the workgroup (bd a multiple of
+// 64; every thread by default): thread t takes the groups of 4 inputs t,
+// t + bd, ...  A larger workgroup that runs it with the persistent family's
+// bd keeps its sums, and so its bits.  load_delta = false leaves r.d at zero
+// for the caller to fill (a delta handed over inside the launch).
 template <int PRO, int S>
-__device__ __forceinline__ void pro_issue(ProLoads &r, const GemvPro &p) {
-    const int ng = p.n >> 2, bd = blockDim.x, t = threadIdx.x;
+__device__ __forceinline__ void pro_issue(ProLoads &r, const GemvPro &p, int bd = blockDim.x, bool load_delta = true) {
+    const int ng = p.n >> 2, t = threadIdx.x;
+    const bool act = t < bd;
     const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
     for (int s = 0; s < S; s++) {
         const int gi = t + s * bd;
-        const bool own = gi < ng;
+        const bool own = act && gi < ng;
         f4(own ? ldf4(p.x + 4 * gi) : z, r.v[s]);
         if constexpr (PRO == PRO_NORM) {
-            f4(own && p.delta ? ldf4(p.delta + 4 * gi) : z, r.d[s]);
+            f4(own && p.delta && load_delta ? ldf4(p.delta + 4 * gi) : z, r.d[s]);
             f4(own && p.delta ? ldf4(p.w_post + 4 * gi) : z, r.wp[s]);
             f4(own ? ldf4(p.w_pre + 4 * gi) : z, r.wq[s]);
         }
@@ -58,9 +64,11 @@ __device__ __forceinline__ void pro_issue(ProLoads &r, const GemvPro &p) {
 }
 
 template <int PRO, int S>
-__device__ void pro_finish(ProLoads &r, const GemvPro &p, uint8_t *lds, int nb, bool first = blockIdx.x == 0) {
+__device__ void pro_finish(ProLoads &r, const GemvPro &p, uint8_t *lds, int nb, bool first = blockIdx.x == 0,
+                           int bd = blockDim.x) {
     __shared__ double red[16];
-    const int ng = p.n >> 2, bd = blockDim.x, t = threadIdx.x;
+    const int ng = p.n >> 2, t = threadIdx.x;
+    const bool act = t < bd;                                         // uniform over each wave
     if constexpr (PRO == PRO_NORM) {
         if (p.delta) {
             double ss = 0.0;
@@ -78,7 +86,7 @@ __device__ void pro_finish(ProLoads &r, const GemvPro &p, uint8_t *lds, int nb, 
 #pragma unroll
             for (int s = 0; s < S; s++) {
                 const int gi = t + s * bd;
-                if (gi < ng) *(float4 *)(p.x_out + 4 * gi) = make_float4(r.v[s][0], r.v[s][1], r.v[s][2], r.v[s][3]);
+                if (act && gi < ng) *(float4 *)(p.x_out + 4 * gi) = make_float4(r.v[s][0], r.v[s][1], r.v[s][2], r.v[s][3]);
             }
         }
         double ss = 0.0;
@@ -96,7 +104,7 @@ __device__ void pro_finish(ProLoads &r, const GemvPro &p, uint8_t *lds, int nb, 
     for (int s = 0; s < S; s++) {
         if (s * bd >= ng) break;                                     // uniform
         const int gi = t + s * bd;
-        q8_lds4(r.v[s], gi, gi < ng, lds, nb, 0);
+        if (act) q8_lds4(r.v[s], gi, gi < ng, lds, nb, 0);
     }
 }
 

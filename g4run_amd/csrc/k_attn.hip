@@ -39,6 +39,7 @@
 
 #include "formats.h"
 #include "gemv_p.h"
+#include "handoff.h"
 #include "kernels.h"
 #include "steps.h"
 
@@ -59,9 +60,6 @@ constexpr int ATT_CSUM = 8;          // chunks per group in the combine's two-le
 #endif
 #ifndef ATT_QKV_VFIRST
 #define ATT_QKV_VFIRST 0
-#endif
-#ifndef ATT_POLL_SLEEP
-#define ATT_POLL_SLEEP 1
 #endif
 
 __device__ __forceinline__ float wave_max(float v) { return group_max<64>(v); }
@@ -235,16 +233,6 @@ __device__ __forceinline__ int attn_view(AttnCtx &c) {
     return nv;
 }
 
-// loads and stores of data shared between the workgroups of one launch:
-// agent scope, coherent across the XCDs' L2 caches
-template <class T>
-__device__ __forceinline__ T ld_ag(const T *p) {
-    return __hip_atomic_load(const_cast<T *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-template <class T>
-__device__ __forceinline__ void st_ag(T *p, T v) {
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
 
 // chunk statistics of GRP heads from per-thread scores: m_c over the valid
 // lanes (wave max + LDS), then l_c = sum exp((double)(s - m_c)) over the lanes
@@ -937,31 +925,6 @@ constexpr int ATT_FUSED_MAXC = 128;  // chunks per KV head (two per lane)
 constexpr int ATT_TW = 16;
 
 __device__ __forceinline__ uint32_t tag_of(const AttnCtx &c) { return *c.epoch * c.tag_mul + c.tag_add + 1u; }
-__device__ __forceinline__ void st_tag(uint64_t *p, uint32_t bits, uint32_t tag) { st_ag(p, ((uint64_t)tag << 32) | bits); }
-
-// N tagged words: all loads issued together; while any tag is not yet
-// current, the stale words are reloaded together
-template <int N>
-__device__ __forceinline__ bool poll_words(const uint64_t *const (&src)[N], const bool (&need)[N], uint32_t tag,
-                                           uint32_t (&bits)[N], unsigned spin) {
-    uint64_t w[N];
-#pragma unroll
-    for (int k = 0; k < N; k++) w[k] = need[k] ? ld_ag(src[k]) : ((uint64_t)tag << 32);
-    for (unsigned it = 0;; it++) {
-        bool all = true;
-#pragma unroll
-        for (int k = 0; k < N; k++) all &= (uint32_t)(w[k] >> 32) == tag;
-        if (all) break;
-        if (it >= spin) return false;
-        __builtin_amdgcn_s_sleep(ATT_POLL_SLEEP);
-#pragma unroll
-        for (int k = 0; k < N; k++)
-            if ((uint32_t)(w[k] >> 32) != tag) w[k] = ld_ag(src[k]);
-    }
-#pragma unroll
-    for (int k = 0; k < N; k++) bits[k] = (uint32_t)w[k];
-    return true;
-}
 
 // the attention rows (queries, and the new key / value in the chunk of the
 // current position) from the projection's tagged words, for prep_f16_finish
@@ -1480,6 +1443,8 @@ void attn_force_timeout(bool on) {
     g_attn_spin = on ? 64u : ATT_SPIN_LIMIT;
     g_attn_poll_xor = on ? 0x80000000u : 0u;
 }
+unsigned attn_spin_limit() { return g_attn_spin; }
+uint32_t attn_poll_xor() { return g_attn_poll_xor; }
 
 // workgroups of 256 threads of one kernel instantiation, with `lds` bytes of
 // dynamic LDS, that the device holds resident at once (cached per instantiation
