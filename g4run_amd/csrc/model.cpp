@@ -89,7 +89,8 @@ enum { FUSE_QKV = 1, FUSE_GU = 2, FUSE_DOWN = 4, FUSE_HEAD = 8, FUSE_QATT = 16, 
 // stream drains far enough to accept its loads, so the rows come out ~5.6 us
 // into the launch and the attention starts later than after a separate GEMV.
 // The WO hand-off costs most of the Wo launch it replaces (~0.9 us net per
-// layer).
+// layer).  QKV|GU|WO|DQ 896 against 962: gathering Wdown's rows in every
+// workgroup waits for poll round trips behind the other CUs' streams.
 static constexpr int kDefaultFuse = FUSE_QKV | FUSE_GU | FUSE_WO;
 
 static int model_alloc(g4h_model *m, void **p, size_t bytes) {
