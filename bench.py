@@ -266,6 +266,72 @@ def bench_attention(G, stream, n_pos=8192, n_head=8, n_kv=4, hd=256, k=200):
     return res
 
 
+def _timed(G, fn, reps: int = 5) -> float:
+    """median ms of fn() over reps calls on the default stream (one warm-up)."""
+    fn()
+    G.synchronize()
+    ts = []
+    for _ in range(reps):
+        e0, e1 = G.Event(), G.Event()
+        e0.record()
+        fn()
+        e1.record()
+        G.synchronize()
+        ts.append(e0.elapsed_ms(e1))
+    return float(np.median(ts))
+
+
+def bench_next(G, m):
+    """The rows after the decode path (rank 3-4 of the scope table) on the same
+    model and shapes: a speculative-decoding verify batch and a prefill chunk
+    through the batched forward, the device sampler's full chain, and causal
+    attention over a batch of new tokens (one set of launches against one
+    decode launch per token)."""
+    c = m.cfg
+    out = {}
+    rs = np.random.default_rng(5)
+    pos0 = 4096
+    for nb in (4, 8):
+        toks = rs.integers(0, c["n_vocab"], nb).astype(np.int32)
+        lg, hn = G.Buffer(nb * c["n_vocab"] * 4), G.Buffer(nb * c["n_embd"] * 4)
+        ms = _timed(G, lambda: m.forward_batch_heads(toks, pos0, lg, hn))
+        out[f"verify_{nb}"] = {"ms": round(ms, 3), "tok_per_s": round(nb / ms * 1e3, 1),
+                               "what": f"g4h_forward_batch_heads, {nb} tokens at position {pos0}: logits and next "
+                                       "hidden row of every position (model.c:780-799)"}
+    toks = rs.integers(0, c["n_vocab"], 64).astype(np.int32)
+    ms = _timed(G, lambda: m.forward_batch(toks, pos0, want_logits=False))
+    out["prefill_chunk_64"] = {"ms": round(ms, 3), "tok_per_s": round(64 / ms * 1e3, 1),
+                               "what": f"g4h_forward_batch, 64 tokens at position {pos0} (g4_forward_batch)"}
+    smp = G.Sampler(c["n_vocab"], temp=0.8, top_k=40, top_p=0.95, repeat_penalty=1.1, seed=7)
+    lgv = G.Buffer.from_array((rs.standard_normal(c["n_vocab"]) * 3).astype(np.float32))
+    tok = G.Buffer(4)
+    ms = _timed(G, lambda: smp.sample(lgv, tok, accept=True), reps=20)
+    out["sampler"] = {"us": round(ms * 1e3, 2), "what": f"g4h_sample over {c['n_vocab']} logits: repeat penalty, "
+                                                         "top-k 40, top-p 0.95, temperature 0.8, xoshiro draw "
+                                                         "(sampler.c:74-210), accepted into the ring"}
+    smp.free()
+    H, KV, hd, nb = c["n_head"], c["n_kv"], c["head_dim"], 64
+    slots = pos0 + nb
+    kc, vc = G.Buffer(slots * KV * hd * 2), G.Buffer(slots * KV * hd * 2)
+    for b in (kc, vc):
+        G.kv_store(G.F16, G.Buffer.from_array((rs.standard_normal((slots * KV, hd))).astype(np.float32)), b, hd,
+                   rows=slots * KV, dst_stride=hd * 2)
+    q = G.Buffer.from_array((rs.standard_normal((nb, H, hd)) * 0.3).astype(np.float32))
+    o = G.Buffer(nb * H * hd * 4)
+    wsb = G.Buffer(G.attn_prefill_workspace_bytes(H, hd, pos0, nb))
+    wst = G.Buffer(G.attn_workspace_bytes(H, hd, pos0 + nb))
+    ms_b = _timed(G, lambda: G.attn_prefill(q, kc, vc, G.F16, H, KV, hd, pos0, nb, o, ws=wsb))
+    ms_t = _timed(G, lambda: G.attn_prefill(q, kc, vc, G.F16, H, KV, hd, pos0, nb, o, ws=wst, batched=False))
+    kvb = 2 * (pos0 + nb) * KV * hd * 2
+    out["prefill_attention_64"] = {"us": round(ms_b * 1e3, 1), "per_token_launches_us": round(ms_t * 1e3, 1),
+                                   "GBps": round(kvb / (ms_b * 1e-3) / 1e9, 1),
+                                   "what": f"g4h_attn_prefill, {nb} new tokens after {pos0} cached positions, "
+                                           f"{H} q / {KV} kv heads x {hd}, f16 cache (model.c:509-545): one set of "
+                                           "launches; KV read once per chunk per token block"}
+    log("bench: next rows " + ", ".join(f"{k} {v.get('ms', v.get('us'))}" for k, v in out.items()))
+    return out
+
+
 def bench_decode(G, steps: int, cpu_seconds: float, want_cpu: bool):
     """tokens/s of the full decode step at context ~8192."""
     m = G.Model(seed=1)
@@ -334,6 +400,7 @@ def bench_decode(G, steps: int, cpu_seconds: float, want_cpu: bool):
                                              f"{dots}; pthread row split (model.c:59-65), heads in "
                                              f"parallel (model.c:706); {cpu_model()}"}
             log(f"bench: cpu decode {out['cpu_baseline']['tok_per_s']} tok/s on {threads} threads")
+    out["next"] = bench_next(G, m)
     m.free()
     return out
 

@@ -16,8 +16,11 @@
 // different (float compare, so -0 == +0 counts as a tie) and no logit is NaN,
 // its result is fixed by the values alone: the k largest, in descending order.
 // The fast path finds them with a 16-ary search over the order-preserving
-// 32-bit keys for a threshold with between k+1 and 4096 elements at or above
-// it, gathers those into LDS, bitonic-sorts them and checks the condition.
+// 32-bit keys for a threshold with between k+1 and 1024 elements at or above
+// it (the row held in registers when it has at most 32 values per thread,
+// else read in batches of 8 per thread), gathers those, bitonic-sorts them one
+// per thread (lane shuffles within a wave, LDS across waves) and checks the
+// condition.
 // Otherwise (ties, NaN, or more than 4096 elements sharing the boundary key)
 // wave 0 replays the reference's heap exactly, skipping 64 ids at a time
 // whose values cannot enter it, and the heap array is ordered as the
@@ -40,7 +43,9 @@ namespace {
 
 constexpr int NT = 1024;            // threads per workgroup
 constexpr int NW = NT / 64;         // waves
-constexpr int CAP = 4096;           // gathered candidates (LDS)
+constexpr int CAP = 4096;           // LDS key array (penalty window, sorts)
+constexpr int GT = 1024;            // gathered candidates of the fast path: one per thread
+constexpr int RPT = 32;             // row values per thread held in registers (n_vocab <= RPT * NT)
 constexpr int KMAX = SAMPLER_TOPK_MAX;
 
 // order-preserving key: larger float <=> larger key (-0 < +0; NaNs at the ends)
@@ -71,6 +76,34 @@ __device__ void lds_bitonic(T *a, int n) {
             }
             __syncthreads();
         }
+}
+
+// descending bitonic sort of a[0..n) (n a power of two <= NT, distinct keys
+// apart from zero padding), one key per thread: exchanges within a wave are
+// lane shuffles, wider ones go through a[] in LDS.  The same compare-exchange
+// network as lds_bitonic<uint64_t, true>; every thread calls it.
+__device__ void reg_bitonic_desc(uint64_t *a, int n) {
+    const int t = threadIdx.x;
+    uint64_t x = t < n ? a[t] : 0;
+    for (int k = 2; k <= n; k <<= 1)
+        for (int j = k >> 1; j > 0; j >>= 1) {
+            uint64_t y;
+            if (j >= 64) {                                           // uniform
+                __syncthreads();
+                if (t < n) a[t] = x;
+                __syncthreads();
+                y = t < n ? a[t ^ j] : 0;
+            } else {
+                const uint32_t lo = (uint32_t)__shfl_xor((int)(uint32_t)x, j, 64);
+                const uint32_t hi = (uint32_t)__shfl_xor((int)(uint32_t)(x >> 32), j, 64);
+                y = ((uint64_t)hi << 32) | lo;
+            }
+            const bool lower = (t & j) == 0, asc = (t & k) != 0;     // descending overall
+            x = (lower == asc) ? (x < y ? x : y) : (x < y ? y : x);
+        }
+    __syncthreads();
+    if (t < n) a[t] = x;
+    __syncthreads();
 }
 
 __device__ __forceinline__ int wave_isum(int v) {
@@ -131,40 +164,32 @@ struct Lds {
     float hv[KMAX];                       // exact heap (slow path)
     int hi[KMAX];
     int red[NW][16];
+    int cred[2][NW][16];                  // per-round wave counts of the threshold search
     int cnt[16];
     float bv[NW];
     int bi[NW];
     int suf[64];
     int flag, n_keep, gathered, id;
+    double dsum;
 };
 
-// Counts, for 15 thresholds p[0..14], the elements with key >= p[j] (all
-// threads receive the totals).
-__device__ void count_ge(const float *L, int nv, const uint32_t p[15], int out[15], Lds &sh) {
-    int c[15];
-#pragma unroll
-    for (int j = 0; j < 15; j++) c[j] = 0;
-    for (int i = threadIdx.x; i < nv; i += NT) {
-        const uint32_t k = okey(L[i]);
-#pragma unroll
-        for (int j = 0; j < 15; j++) c[j] += k >= p[j];
-    }
+// Workgroup totals of 15 per-thread counts (wave sums by lane exchanges, the
+// waves' sums through LDS; buf alternates between calls so one barrier does)
+__device__ __forceinline__ void wg_counts15(int c[15], Lds &sh, int buf) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    int (*cr)[16] = sh.cred[buf & 1];
 #pragma unroll
     for (int j = 0; j < 15; j++) {
-        const int v = wave_isum(c[j]);
-        if (lane == 0) sh.red[wave][j] = v;
-    }
-    __syncthreads();
-    if (threadIdx.x < 15) {
-        int v = 0;
-        for (int w = 0; w < NW; w++) v += sh.red[w][threadIdx.x];
-        sh.cnt[threadIdx.x] = v;
+        const int v = group_isum<64>(c[j]);
+        if (lane == j) cr[wave][j] = v;
     }
     __syncthreads();
 #pragma unroll
-    for (int j = 0; j < 15; j++) out[j] = sh.cnt[j];
-    __syncthreads();
+    for (int j = 0; j < 15; j++) {
+        int v = 0;
+        for (int w = 0; w < NW; w++) v += cr[w][j];
+        c[j] = v;
+    }
 }
 
 // The reference's heap over ids 0..nv-1 (sampler.c:149-168) on wave 0;
@@ -215,6 +240,7 @@ __device__ void heap_replay(const float *L, int nv, int k, Lds &sh) {
     }
 }
 
+template <int REG>
 __global__ __launch_bounds__(NT) void k_sample(SamplerDev *S, float *L, int *out, int accept, int *state, int n_ctx) {
     __shared__ Lds sh;
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
@@ -281,43 +307,95 @@ __global__ __launch_bounds__(NT) void k_sample(SamplerDev *S, float *L, int *out
     if (k > nv) k = nv;
     const int K1 = k < nv ? k + 1 : k;     // the k largest plus the next one, to see a tie at the edge
 
-    // NaN scan and the largest key
-    uint32_t kmax = 0;
+    // the row after bans and penalties: in registers (REG per thread), or read
+    // again per pass in batches of 8 per thread (their loads in flight together)
+    float lv[REG > 0 ? REG : 1];
+    if constexpr (REG > 0) {
+#pragma unroll
+        for (int r = 0; r < REG; r++) {
+            const int i = t + r * NT;
+            lv[r] = i < nv ? L[i] : 0.0f;
+        }
+    }
+    auto each = [&](auto &&f) {
+        if constexpr (REG > 0) {
+#pragma unroll
+            for (int r = 0; r < REG; r++) {
+                const int i = t + r * NT;
+                if (i < nv) f(i, lv[r]);
+            }
+        } else {
+            for (int i0 = t; i0 < nv; i0 += 8 * NT) {
+                float b[8];
+#pragma unroll
+                for (int q = 0; q < 8; q++) {
+                    const int i = i0 + q * NT;
+                    b[q] = i < nv ? L[i] : 0.0f;
+                }
+#pragma unroll
+                for (int q = 0; q < 8; q++) {
+                    const int i = i0 + q * NT;
+                    if (i < nv) f(i, b[q]);
+                }
+            }
+        }
+    };
+
+    // NaN scan, the largest and the smallest key (wave maxima by lane
+    // exchanges, the NaN flag by a ballot)
+    uint32_t kmax = 0, kmin_c = 0;                 // kmin_c: complement of the smallest key
     int nan = 0;
-    for (int i = t; i < nv; i += NT) {
-        const float v = L[i];
+    each([&](int, float v) {
         nan |= __builtin_isnan(v);
         const uint32_t kk = okey(v);
         kmax = kk > kmax ? kk : kmax;
-    }
-    for (int m = 32; m >= 1; m >>= 1) {
-        kmax = max(kmax, (uint32_t)__shfl_xor((int)kmax, m, 64));
-        nan |= __shfl_xor(nan, m, 64);
-    }
-    if (lane == 0) { sh.red[wave][0] = (int)kmax; sh.red[wave][1] = nan; }
+        kmin_c = ~kk > kmin_c ? ~kk : kmin_c;
+    });
+    kmax = wave_umax(kmax);
+    kmin_c = wave_umax(kmin_c);
+    const bool wnan = __ballot(nan != 0) != 0;
+    if (lane == 0) { sh.red[wave][0] = (int)kmax; sh.red[wave][1] = wnan; sh.red[wave][2] = (int)kmin_c; }
     if (t == 0) { sh.gathered = 0; sh.flag = 0; }
     __syncthreads();
     kmax = 0;
+    kmin_c = 0;
     nan = 0;
     for (int w = 0; w < NW; w++) {
         kmax = max(kmax, (uint32_t)sh.red[w][0]);
+        kmin_c = max(kmin_c, (uint32_t)sh.red[w][2]);
         nan |= sh.red[w][1];
     }
     __syncthreads();
 
     bool slow = nan != 0;
-    uint32_t lo = 1;                       // count(key >= lo) >= K1; NaN-free keys are >= 0x007fffff
+    uint32_t lo = ~kmin_c;                 // count(key >= lo) >= K1: every element
     if (!slow) {
         uint64_t hi = (uint64_t)kmax + 1;  // count(key >= hi) < K1
-        int c_lo = nv;
-        while (c_lo > CAP) {
+        int c_lo = nv, buf = 0;
+        // the 15 counts of keys >= p[j] over the row
+        auto row_counts = [&](const uint32_t p[15], int c[15]) {
+#pragma unroll
+            for (int j = 0; j < 15; j++) c[j] = 0;
+            each([&](int, float v) {
+                const uint32_t k = okey(v);
+#pragma unroll
+                for (int j = 0; j < 15; j++) c[j] += k >= p[j];
+            });
+            wg_counts15(c, sh, buf++);
+        };
+        for (int round = 0; c_lo > GT; round++) {
             const uint64_t span = hi - lo;
-            if (span <= 1) { slow = true; break; }       // > CAP elements share the boundary key: ties
+            if (span <= 1) { slow = true; break; }       // > GT elements share the boundary key: ties
             uint32_t p[15];
             int c[15];
+            // the first round's thresholds close in on the largest key
+            // geometrically (hi - span / 2^m, m = 15 .. 1: the k largest of a
+            // row of logits sit in a narrow band of keys at its top), later
+            // rounds split the bracket evenly
 #pragma unroll
-            for (int j = 0; j < 15; j++) p[j] = (uint32_t)(lo + (span * (uint64_t)(j + 1)) / 16);
-            count_ge(L, nv, p, c, sh);
+            for (int j = 0; j < 15; j++)
+                p[j] = round == 0 ? (uint32_t)(hi - (span >> (j + 1))) : (uint32_t)(lo + (span * (uint64_t)(j + 1)) / 16);
+            row_counts(p, c);
             int jbest = -1;
 #pragma unroll
             for (int j = 0; j < 15; j++)
@@ -332,10 +410,9 @@ __global__ __launch_bounds__(NT) void k_sample(SamplerDev *S, float *L, int *out
     }
 
     if (!slow) {
-        // gather every element with key >= lo (at most CAP) by wave-ballot compaction
-        for (int i0 = 0; i0 < nv; i0 += NT) {
-            const int i = i0 + t;
-            const uint32_t kk = i < nv ? okey(L[i]) : 0u;
+        // gather every element with key >= lo (at most GT) by wave-ballot compaction
+        auto gather = [&](int i, float v) {                          // every lane of the wave, each step
+            const uint32_t kk = i < nv ? okey(v) : 0u;
             const bool keep = i < nv && kk >= lo;
             const uint64_t m = __ballot(keep);
             int base = 0;
@@ -345,6 +422,12 @@ __global__ __launch_bounds__(NT) void k_sample(SamplerDev *S, float *L, int *out
                 const int slot = base + __builtin_popcountll(m & ((1ull << lane) - 1));
                 sh.keys[slot] = ((uint64_t)kk << 32) | (uint32_t)~(uint32_t)i;
             }
+        };
+        if constexpr (REG > 0) {
+#pragma unroll
+            for (int r = 0; r < REG; r++) gather(t + r * NT, lv[r]);
+        } else {
+            for (int i0 = 0; i0 < nv; i0 += NT) gather(i0 + t, i0 + t < nv ? L[i0 + t] : 0.0f);
         }
         __syncthreads();
         const int G = sh.gathered;
@@ -352,7 +435,7 @@ __global__ __launch_bounds__(NT) void k_sample(SamplerDev *S, float *L, int *out
         while (P < G) P <<= 1;
         for (int i = G + t; i < P; i += NT) sh.keys[i] = 0;
         __syncthreads();
-        lds_bitonic<uint64_t, true>(sh.keys, P);
+        reg_bitonic_desc(sh.keys, P);
         // the k largest must be strictly decreasing and the (k+1)-th strictly smaller
         for (int i = t; i + 1 < K1; i += NT)
             if (okey_val((uint32_t)(sh.keys[i] >> 32)) == okey_val((uint32_t)(sh.keys[i + 1] >> 32))) sh.flag = 1;
@@ -378,7 +461,7 @@ __global__ __launch_bounds__(NT) void k_sample(SamplerDev *S, float *L, int *out
                 sh.keys[i] = i < k ? ((uint64_t)okey(v == 0.0f ? 0.0f : v) << 32) | (uint32_t)(0xffffffffu - i) : 0;
             }
             __syncthreads();
-            lds_bitonic<uint64_t, true>(sh.keys, P);
+            reg_bitonic_desc(sh.keys, P);
             for (int i = t; i < k; i += NT) {
                 const int slot = (int)(0xffffffffu - (uint32_t)sh.keys[i]);
                 sh.cv[i] = sh.hv[slot];
@@ -405,22 +488,49 @@ __global__ __launch_bounds__(NT) void k_sample(SamplerDev *S, float *L, int *out
     }
 
     // ---- top-p (179-194) ----
+    // The sums and running sums are one thread's, in index order as in the
+    // reference; it reads the LDS terms 8 at a time so their latencies overlap
+    // and runs each batch without branches (terms past the end are +0, which
+    // leaves a sum of non-negative terms unchanged; a running sum past its
+    // cut no longer matters), and the quotients pf[i] / sum come from all
+    // threads.
     for (int i = t; i < k; i += NT) sh.pf[i] = (float)exp((double)(sh.cv[i] - sh.cv[0]));
     __syncthreads();
-    if (t == 0) {
+    const bool cut = top_p < 1.0f && top_p > 0.0f;
+    if (t == 0 && cut) {                                             // the sum serves the cut only
         double sum = 0;
-        for (int i = 0; i < k; i++) sum += sh.pf[i];
-        int n = k;
-        if (top_p < 1.0f && top_p > 0.0f) {
-            double cum = 0;
-            for (int i = 0; i < k; i++) {
-                cum += sh.pf[i] / sum;
-                if (cum >= top_p) { n = i + 1; break; }
-            }
+        for (int i0 = 0; i0 < k; i0 += 8) {
+            float b[8];
+#pragma unroll
+            for (int q = 0; q < 8; q++) b[q] = i0 + q < k ? sh.pf[i0 + q] : 0.0f;
+#pragma unroll
+            for (int q = 0; q < 8; q++) sum += b[q];
         }
-        sh.n_keep = n;
+        sh.dsum = sum;
     }
+    if (t == 0) sh.n_keep = k;
     __syncthreads();
+    if (cut) {
+        const double sum = sh.dsum;
+        for (int i = t; i < k; i += NT) sh.pd[i] = sh.pf[i] / sum;
+        __syncthreads();
+        if (t == 0) {
+            double cum = 0;
+            int n = k;
+            for (int i0 = 0; i0 < k && n == k; i0 += 8) {
+                double b[8];
+#pragma unroll
+                for (int q = 0; q < 8; q++) b[q] = i0 + q < k ? sh.pd[i0 + q] : 0.0;
+#pragma unroll
+                for (int q = 0; q < 8; q++) {
+                    cum += b[q];
+                    n = (n == k && i0 + q < k && cum >= top_p) ? i0 + q + 1 : n;
+                }
+            }
+            sh.n_keep = n;
+        }
+        __syncthreads();
+    }
     const int n = sh.n_keep;
 
     // ---- temperature and the draw (197-209) ----
@@ -429,14 +539,27 @@ __global__ __launch_bounds__(NT) void k_sample(SamplerDev *S, float *L, int *out
     __syncthreads();
     if (t == 0) {
         double sum = 0;
-        for (int i = 0; i < n; i++) sum += sh.pd[i];
+        for (int i0 = 0; i0 < n; i0 += 8) {
+            double b[8];
+#pragma unroll
+            for (int q = 0; q < 8; q++) b[q] = i0 + q < n ? sh.pd[i0 + q] : 0.0;
+#pragma unroll
+            for (int q = 0; q < 8; q++) sum += b[q];
+        }
         const double r = (double)(rng_next(S) >> 11) / 9007199254740992.0 * sum;
         double cum = 0;
-        int id = sh.ci[n - 1];
-        for (int i = 0; i < n; i++) {
-            cum += sh.pd[i];
-            if (r < cum) { id = sh.ci[i]; break; }
+        int id = sh.ci[n - 1], hit = -1;
+        for (int i0 = 0; i0 < n && hit < 0; i0 += 8) {
+            double b[8];
+#pragma unroll
+            for (int q = 0; q < 8; q++) b[q] = i0 + q < n ? sh.pd[i0 + q] : 0.0;
+#pragma unroll
+            for (int q = 0; q < 8; q++) {
+                cum += b[q];
+                hit = (hit < 0 && i0 + q < n && r < cum) ? i0 + q : hit;
+            }
         }
+        if (hit >= 0) id = sh.ci[hit];
         if (out) *out = id;
         if (accept) ring_push(S, id);
         if (state) state_advance(state, id, n_ctx);
@@ -453,7 +576,8 @@ __global__ __launch_bounds__(64) void k_sampler_push(SamplerDev *S, const int *i
 hipError_t launch_sample(SamplerDev *S, int n_vocab, float *logits, int *out, int accept, int *state, int n_ctx,
                          hipStream_t s) {
     if (!S || !logits || n_vocab <= 0 || ((uintptr_t)logits & 15)) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_sample, dim3(1), dim3(NT), 0, s, S, logits, out, accept, state, n_ctx);
+    if (n_vocab <= RPT * NT) hipLaunchKernelGGL(k_sample<RPT>, dim3(1), dim3(NT), 0, s, S, logits, out, accept, state, n_ctx);
+    else hipLaunchKernelGGL(k_sample<0>, dim3(1), dim3(NT), 0, s, S, logits, out, accept, state, n_ctx);
     return hipGetLastError();
 }
 
