@@ -1605,8 +1605,12 @@ static AttnBatchWs attn_batch_ws(int n_head, int hd, int npos_max) {
     w.tok = w.P + al256((size_t)n_head * nc * hd * 4);
     return w;
 }
+// The batch blocks start after the decode layout's 256-byte header, so the
+// error word (offset 0) and the epoch word (offset 128) of a workspace shared
+// with the decode form keep their values.
+constexpr size_t ATT_BATCH_OFF = 256;
 size_t attn_batch_workspace_bytes(int n_head, int hd, int npos_max, int nb) {
-    return (size_t)nb * attn_batch_ws(n_head, hd, npos_max).tok;
+    return ATT_BATCH_OFF + (size_t)nb * attn_batch_ws(n_head, hd, npos_max).tok;
 }
 
 template <int KV, int GRP, int HD>
@@ -1616,6 +1620,7 @@ static hipError_t attn_batch_go(AttnCtx c, int n_head, int n_kv, int npos0, int 
     const AttnBatchWs w = attn_batch_ws(n_head, c.a.hd, npos_max);
     const int nc = (npos_max + ATT_CHUNK - 1) / ATT_CHUNK;
     c.nc = nc;
+    ws += ATT_BATCH_OFF;
     c.S = (float *)(ws + w.S);
     c.Mc = (float *)(ws + w.Mc);
     c.Lc = (double *)(ws + w.Lc);

@@ -187,7 +187,8 @@ int g4h_block_sums(const g4h_tensor *W, const void *pre_dev, size_t pre_stride, 
  * epoch word each launch advances on the device, and hand-off words tagged
  * with it): the first call on a workspace clears it (ws_bytes of it), later
  * calls of any position count (graph replays included) do not, until a
- * three-pass or batch call stores untagged data there.  Memory that held
+ * three-pass or batch call stores untagged data there (past its first 256
+ * bytes, which hold the error and epoch words).  Memory that held
  * anything else since must have been freed with g4h_free, or be zeroed before
  * it is used as a workspace again.  Calls that overlap on one workspace race. */
 size_t g4h_attn_workspace_bytes(int n_head, int hd, int n_pos);

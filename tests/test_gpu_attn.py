@@ -166,6 +166,36 @@ def test_attention_epoch_advances_on_device(gpu, oracle, monkeypatch):
     assert not G.attn_status(ws)
 
 
+def test_attention_workspace_reuse_after_free_and_batch(gpu, oracle, monkeypatch):
+    """A workspace freed with g4h_free and memory handed out again at the same
+    address starts over (cleared on its next use), and a batch call that
+    writes its untagged blocks into a workspace makes the next one-launch call
+    clear it: both give the three-pass bits."""
+    G = gpu
+    n_head, n_kv, hd, n_pos = 8, 4, 256, 2000
+    kb, vb, kh, vh = make_cache(G, oracle, G.F16, n_pos + 8, n_kv, hd, seed=93)
+    q = (np.random.default_rng(94).standard_normal((n_head, hd)) * 0.5).astype(np.float32)
+    monkeypatch.setenv("G4H_ATTN_PASSES", "3")
+    ref = _attn(G, q, kb, vb, G.F16, n_head, n_kv, hd, n_pos, None)
+    monkeypatch.delenv("G4H_ATTN_PASSES")
+    nbytes = max(G.attn_workspace_bytes(n_head, hd, n_pos + 8), G.attn_prefill_workspace_bytes(n_head, hd, n_pos, 8))
+    ws = G.Buffer(nbytes)
+    for _ in range(2):
+        assert np.array_equal(_attn(G, q, kb, vb, G.F16, n_head, n_kv, hd, n_pos, ws).view(np.uint32), ref.view(np.uint32))
+    addr = ws.ptr
+    ws.free()
+    ws2 = G.Buffer(nbytes)
+    ws2.upload(np.full(nbytes, 0xFF, np.uint8))                     # garbage, maybe at the same address
+    got = _attn(G, q, kb, vb, G.F16, n_head, n_kv, hd, n_pos, ws2)
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), f"reused at the same address: {ws2.ptr == addr}"
+    qb = G.Buffer.from_array(np.tile(q, (8, 1, 1)))
+    out = G.Buffer(8 * n_head * hd * 4)
+    G.attn_prefill(qb, kb, vb, G.F16, n_head, n_kv, hd, n_pos - 1, 8, out, ws=ws2)     # untagged blocks
+    got = _attn(G, q, kb, vb, G.F16, n_head, n_kv, hd, n_pos, ws2)
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+    assert not G.attn_status(ws2)
+
+
 def test_attention_long_context_falls_back_to_three_passes(gpu, oracle):
     """A grid larger than the device holds at once runs the three passes."""
     G = gpu
