@@ -91,7 +91,9 @@ enum { FUSE_QKV = 1, FUSE_GU = 2, FUSE_DOWN = 4, FUSE_HEAD = 8, FUSE_QATT = 16, 
 // The WO hand-off costs most of the Wo launch it replaces (~0.9 us net per
 // layer).  QKV|GU|WO|DQ 896 against 962: gathering Wdown's rows in every
 // workgroup waits for poll round trips behind the other CUs' streams.
-static constexpr int kDefaultFuse = FUSE_QKV | FUSE_GU | FUSE_WO;
+// QKV|GU|WO|HEAD 965-970 against QKV|GU|WO 960-966 (six alternating pairs,
+// HEAD ahead in each); QKV|GU|WO|DOWN 887.
+static constexpr int kDefaultFuse = FUSE_QKV | FUSE_GU | FUSE_WO | FUSE_HEAD;
 
 static int model_alloc(g4h_model *m, void **p, size_t bytes) {
     if (int rc = g4h_malloc(p, bytes)) return rc;
