@@ -382,11 +382,26 @@ static bool fused_quant_enabled() {
     return on;
 }
 
+// The LDS a GEMV launch over W may stage its activations in: 64 KB, or for
+// eight q8_0 / q4_0 tokens what one workgroup may hold on this device (those
+// launches take up to 16 waves per workgroup, one workgroup per CU).
+static size_t gemv_lds_cap(const g4h_tensor &W, int chunk) {
+    if (chunk != 8 || (W.type != Q4_0 && W.type != Q8_0)) return kMaxLds;
+    static const size_t dev_max = [] {
+        int dev = 0, v = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&v, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess || v <= 0)
+            return kMaxLds;
+        return (size_t)v;
+    }();
+    return dev_max > kMaxLds ? dev_max : kMaxLds;
+}
+
 // GEMV token chunks of 8/4/2/1 within the LDS budget: the chunk that starts at
 // token `done` of nb
 static int gemv_chunk_at(const g4h_tensor &W, int nb, int done) {
     int chunk = 8;
-    while (chunk > nb - done || (chunk > 1 && gemv_lds_bytes(W.type, chunk, W.nb) > kMaxLds)) chunk >>= 1;
+    while (chunk > nb - done || (chunk > 1 && gemv_lds_bytes(W.type, chunk, W.nb) > gemv_lds_cap(W, chunk))) chunk >>= 1;
     return chunk;
 }
 
@@ -447,12 +462,14 @@ extern "C" int g4h_matmul_describe(const g4h_tensor *W, int nb, int path, char *
     }
     int lpr, upl, wpg;
     int64_t grid;
-    const int chunk = nb >= 8 ? 8 : nb >= 4 ? 4 : nb >= 2 ? 2 : 1;
-    gemv_launch_shape(*W, &lpr, &upl, &wpg, &grid, chunk);
+    const int chunk = gemv_chunk_at(*W, nb, 0);
+    int launches = 0;
+    for (int done = 0; done < nb; launches++) done += gemv_chunk_at(*W, nb, done);
+    const bool xq = x_fused(*W, nb);
+    gemv_launch_shape(*W, &lpr, &upl, &wpg, &grid, chunk, xq);
     upl = gemv_upl_final(W->type, W->nb, chunk, lpr, upl);
     snprintf(buf, len, "k_gemv<%s,nb=%d,lpr=%d,upl=%d> grid=%lld block=%d (x%d launches); fp32 x %s", type_name(W->type), chunk,
-             lpr, upl, (long long)grid, 64 * wpg, (nb + chunk - 1) / chunk,
-             x_fused(*W, nb) ? "quantized in-kernel" : "quantized by a separate launch");
+             lpr, upl, (long long)grid, 64 * wpg, launches, xq ? "quantized in-kernel" : "quantized by a separate launch");
     return G4H_OK;
 }
 

@@ -11,6 +11,7 @@
 // LPR only (chosen from the row length), never on NB, so token b's result is
 // bit-identical for any batch size (the x4 contract of g4run.h:148-157).
 #pragma once
+#include <algorithm>
 #include <cstdint>
 #include <cstdlib>
 
@@ -33,8 +34,16 @@ size_t act_lds_bytes(int nb_tokens, int64_t nblk) { return (size_t)nb_tokens * F
 // The x loads go out before the weight stream and the quantization runs while
 // the weights are in flight; an LDS-only barrier hands the activation over
 // without waiting for the stream.
+// Eight pre-quantized tokens over q8_0 / q4_0 weights may stage more than
+// 64 KB of activations (rows of 10240 and more): that variant takes up to 16
+// waves (gemv_big_stage below).
+template <class F>
+constexpr bool gemv_qk() { return F::type == Q4_0 || F::type == Q8_0; }
+template <class F, int NB, int XQ>
+constexpr int gemv_max_threads() { return XQ == 4 || (NB == 8 && XQ == 0 && gemv_qk<F>()) ? 1024 : 512; }
+
 template <class F, int NB, int LPR, int UPL, int XQ>
-__global__ __launch_bounds__(XQ == 4 ? 1024 : 512) void k_gemv(g4h_tensor W, const uint8_t *__restrict__ act, size_t act_stride,
+__global__ __launch_bounds__((gemv_max_threads<F, NB, XQ>())) void k_gemv(g4h_tensor W, const uint8_t *__restrict__ act, size_t act_stride,
                                                const float *__restrict__ x, float *__restrict__ Y, int units) {
     extern __shared__ __align__(16) uint8_t lds[];
     using Act = typename F::Act;
@@ -169,6 +178,38 @@ static inline double gemv_stage_cost(int type, int64_t nblk, int nb, int rpw) {
     return 0.5 * nb * act / ((double)rpw * (double)bsize(type) * (double)nblk);
 }
 
+// LDS of one CU, and the staging size from which fewer than three
+// workgroups fit on it.
+constexpr size_t kCuLds = 160 * 1024;
+constexpr size_t kLdsSmall = 64 * 1024;
+// Eight pre-quantized tokens over q8_0 / q4_0 rows whose activations take
+// more than 64 KB of LDS (8 x 10240 inputs: 105 KB) leave room for one
+// workgroup per CU.  The waves per workgroup then go up to 16 and the choice
+// counts rounds of resident workgroups: 2560 rows of 10240 run as 256
+// workgroups of 10 waves in one round, where 8 waves would need 320
+// workgroups, a second round for 64 of them.
+static inline bool gemv_big_stage(int type, int nb, bool xq, size_t lds) {
+    return nb == 8 && !xq && (type == Q4_0 || type == Q8_0) && lds > kLdsSmall;
+}
+static inline int gemv_waves_big(int64_t nrows, int rpw, double stage, size_t lds) {
+    const int64_t waves = (nrows + rpw - 1) / rpw;
+    const int64_t res = std::max<int64_t>(1, (int64_t)(kCuLds / lds));  // workgroups a CU holds
+    int best = 1;
+    double best_cost = 1e300;
+    for (int w = 1; w <= 16; w++) {
+        const int64_t n = ((waves + w - 1) / w + 255) / 256;           // workgroups per CU
+        const int64_t rounds = (n + res - 1) / res;
+        const double cost = (double)rounds * (double)std::min(n, res) * (w + stage);
+        if (cost <= best_cost) { best_cost = cost; best = w; }
+    }
+    return best;
+}
+static inline int gemv_pick_waves(const g4h_tensor &W, int nb, int rpw, bool xq, size_t lds) {
+    const double stage = gemv_stage_cost(W.type, W.nb, nb, rpw);
+    return gemv_big_stage(W.type, nb, xq, lds) ? gemv_waves_big(W.nrows, rpw, stage, lds)
+                                               : gemv_waves_per_group(W.nrows, rpw, stage);
+}
+
 // 4-float groups per thread the fused quantizer needs (0 = no fused variant).
 // Every workgroup reads and quantizes all of x, so the fused form pays only
 // while x is small next to the workgroup's weights: up to two groups per
@@ -204,11 +245,12 @@ static inline int gemv_xq_shape(int64_t ncols, int nb, int64_t waves, int wpg, i
 template <class F, int NB, int LPR, int UPL>
 static hipError_t go(const g4h_tensor &W, const uint8_t *act, size_t stride, const float *x, float *Y, int units, hipStream_t s) {
     constexpr int RPW = 64 / LPR;
-    const int wpg = gemv_waves_per_group(W.nrows, RPW, gemv_stage_cost(W.type, W.nb, NB, RPW));
+    const size_t lds = act_lds_bytes<F>(NB, W.nb);
+    const int wpg = gemv_pick_waves(W, NB, RPW, x != nullptr, lds);
     const int64_t waves = (W.nrows + RPW - 1) / RPW;
     const unsigned grid = (unsigned)((waves + wpg - 1) / wpg);
-    const size_t lds = act_lds_bytes<F>(NB, W.nb);
     if (!x) {
+        if (64 * wpg > gemv_max_threads<F, NB, 0>()) return hipErrorInvalidValue;
         hipLaunchKernelGGL((k_gemv<F, NB, LPR, UPL, 0>), dim3(grid), dim3(64 * wpg), lds, s, W, act, stride, x, Y, units);
         return hipGetLastError();
     }

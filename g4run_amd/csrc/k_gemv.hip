@@ -56,10 +56,10 @@ void gemv_shape(int type, int64_t nblk, int *lpr, int *upl) {
     *upl = per <= 2 ? 2 : per <= 4 ? 4 : 8;
 }
 
-void gemv_launch_shape(const g4h_tensor &W, int *lpr, int *upl, int *wpg, int64_t *grid, int nb) {
+void gemv_launch_shape(const g4h_tensor &W, int *lpr, int *upl, int *wpg, int64_t *grid, int nb, bool xq) {
     gemv_shape(W.type, W.nb, lpr, upl);
     const int rpw = 64 / *lpr;
-    *wpg = gemv_waves_per_group(W.nrows, rpw, gemv_stage_cost(W.type, W.nb, nb, rpw));
+    *wpg = gemv_pick_waves(W, nb, rpw, xq, gemv_lds_bytes(W.type, nb, W.nb));
     const int64_t waves = (W.nrows + rpw - 1) / rpw;
     *grid = (waves + *wpg - 1) / *wpg;
 }
@@ -98,7 +98,7 @@ bool gemv_fused_fits(const g4h_tensor &W, int nb) {
     if (nb != 1 && nb != 2 && nb != 4 && nb != 8) return false;
     int lpr, upl, wpg, xwpg;
     int64_t grid;
-    gemv_launch_shape(W, &lpr, &upl, &wpg, &grid, nb);
+    gemv_launch_shape(W, &lpr, &upl, &wpg, &grid, nb, true);
     const int64_t waves = (W.nrows + 64 / lpr - 1) / (64 / lpr);
     return gemv_xq_shape(W.ncols, nb, waves, wpg, &xwpg) != 0;
 }

@@ -31,7 +31,7 @@ inline int gemv_upl_final(int type, int64_t nblk, int nb_tokens, int lpr, int up
     return (upb == 4 && nb_tokens == 8 && upl > 2) ? 2 : upl;
 }
 size_t gemv_lds_bytes(int type, int nb_tokens, int64_t nblk);
-void gemv_launch_shape(const g4h_tensor &W, int *lpr, int *upl, int *wpg, int64_t *grid, int nb = 1);
+void gemv_launch_shape(const g4h_tensor &W, int *lpr, int *upl, int *wpg, int64_t *grid, int nb = 1, bool xq = false);
 
 // Persistent single-token GEMV (gemv_p.h) over q4_0 / q8_0 rows with a fused
 // activation prologue and an optional GELU epilogue.

@@ -210,6 +210,28 @@ def test_batch_bit_identical_to_single_token(gpu, oracle, name, qt):
     assert_close(singles, oracle.matmul(qt, w, act, cols), name)
 
 
+@pytest.mark.parametrize("qt,rows,cols", [(2, 2560, 10240), (8, 2560, 10240), (2, 700, 14336), (8, 300, 12800)])
+def test_eight_tokens_with_large_staging(gpu, oracle, qt, rows, cols):
+    """Eight tokens whose q8_0 activations take more than 64 KB of LDS (rows
+    of 10240 and more) run as one launch of up to 16 waves per workgroup, one
+    workgroup per CU; token b still has the 1-token bits (g4run.h:148-157),
+    and 9 tokens (8 + 1) as well."""
+    from g4run_amd import synth
+    w = synth.weights(qt, rows, cols, seed=rows + 5)
+    x = synth.activations(9, cols, seed=cols + 6)
+    act = oracle.prep_act(qt, x)
+    t = gpu.Tensor.from_rows(qt, w, cols)
+    d = gpu.matmul_describe(t, 8, 1)
+    assert "nb=8" in d and "(x1 launches)" in d, d
+    if (rows, cols) == (2560, 10240):
+        assert "grid=256 block=640" in d, d                          # 10 waves, one round
+    singles = np.stack([gpu_matmul(gpu, t, act=act[i:i + 1])[0] for i in range(9)])
+    for nb in (8, 9):
+        y = gpu_matmul(gpu, t, act=act[:nb].copy(), nb=nb, path=1)
+        assert np.array_equal(bits(y), bits(singles[:nb])), f"nb={nb}"
+    assert_close(singles[:2], oracle.matmul(qt, w, act[:2], cols), f"{qt} {rows}x{cols}")
+
+
 @pytest.mark.parametrize("name,qt", FMTS)
 def test_fused_quantizer_equals_prequantized(gpu, oracle, name, qt):
     from g4run_amd import synth
