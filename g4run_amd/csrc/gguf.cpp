@@ -11,9 +11,11 @@
 #include <sys/stat.h>
 #include <unistd.h>
 
+#include <climits>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <initializer_list>
 
 namespace {
 
@@ -33,6 +35,15 @@ struct Reader {
         }
         std::memcpy(dst, p, n);
         p += n;
+        return true;
+    }
+    // whether n items of at least `unit` bytes each can still follow (a
+    // count from the file is checked so before anything is sized by it)
+    bool fits(uint64_t n, uint64_t unit) {
+        if (bad || n > (uint64_t)(end - p) / unit) {
+            bad = true;
+            return false;
+        }
         return true;
     }
     bool skip(uint64_t n) {
@@ -165,6 +176,7 @@ extern "C" int g4_gguf_open(g4_model_file *mf, const char *path, bool verbose) {
         if (r.bad) break;
         if (vt == V_STR) {
             const g4_str v = r.str();
+            if (r.bad) break;
             if (is(key, "general.architecture")) {
                 const size_t n = v.len < sizeof mf->arch - 1 ? v.len : sizeof mf->arch - 1;
                 std::memcpy(mf->arch, v.ptr, n);
@@ -182,6 +194,11 @@ extern "C" int g4_gguf_open(g4_model_file *mf, const char *path, bool verbose) {
             const uint32_t et = r.get<uint32_t>();
             const uint64_t n = r.get<uint64_t>();
             if (r.bad || et > V_F64 || et == V_ARR) {
+                r.bad = true;
+                break;
+            }
+            if (et == V_STR ? !r.fits(n, 8) : !r.fits(n, (uint64_t)kScalarBytes[et])) break;   // 8: a string's length
+            if (n > 0x7fffffff) {
                 r.bad = true;
                 break;
             }
@@ -218,8 +235,10 @@ extern "C" int g4_gguf_open(g4_model_file *mf, const char *path, bool verbose) {
         }
         const uint64_t off = (uint64_t)(r.p - (const uint8_t *)base);
         const double v = r.scalar(vt);
-        const int iv = (int)v;
-        if (is(key, "general.alignment")) mf->alignment = (uint32_t)v;
+        // conversions of any file value stay defined: out of range (or NaN)
+        // becomes a value the checks below refuse
+        const int iv = v > -2147483648.0 && v < 2147483648.0 ? (int)v : v > 0 ? INT_MAX : INT_MIN;
+        if (is(key, "general.alignment")) mf->alignment = v >= 0.0 && v < 4294967296.0 ? (uint32_t)v : 0u;
         else if (hkey(key, "block_count")) mf->n_layer = iv;
         else if (hkey(key, "context_length")) mf->n_ctx_train = iv;
         else if (hkey(key, "embedding_length")) mf->n_embd = iv;
@@ -274,7 +293,9 @@ extern "C" int g4_gguf_open(g4_model_file *mf, const char *path, bool verbose) {
     mf->kv_end = (uint64_t)(r.p - (const uint8_t *)base);
 
     // ---- tensor table (gguf.c:303-333) ----
+    if (!r.fits(mf->n_tensors, 24)) return fail(mf, "tensor info parse error");   // name length, ndim, type, offset
     mf->tensors = (g4_tensor *)std::calloc(mf->n_tensors ? mf->n_tensors : 1, sizeof(g4_tensor));
+    if (!mf->tensors) return fail(mf, "out of memory for the tensor table");
     for (uint64_t i = 0; i < mf->n_tensors && !r.bad; i++) {
         g4_tensor *t = &mf->tensors[i];
         const g4_str name = r.str();
@@ -295,13 +316,23 @@ extern "C" int g4_gguf_open(g4_model_file *mf, const char *path, bool verbose) {
     if (mf->alignment == 0) return fail(mf, "bad alignment");
     const uint64_t header_end = (uint64_t)(r.p - (const uint8_t *)base);
     mf->data_start = (header_end + mf->alignment - 1) / mf->alignment * mf->alignment;
+    if (mf->data_start > mf->map_size) return fail(mf, "tensor data past the end of the file");
     for (uint64_t i = 0; i < mf->n_tensors; i++) {
         g4_tensor *t = &mf->tensors[i];
-        const int64_t nel = t->ne[0] * t->ne[1] * t->ne[2] * t->ne[3];
-        const size_t rs = t->ne[0] > 0 ? g4_row_size(t->type, t->ne[0]) : 0;
+        // every dimension at least 1, a row no longer than the file could hold
+        // (at most 4 elements per byte in any type), and the byte count
+        // computed without overflow, so a corrupt table cannot wrap the
+        // bounds check below
+        bool shape_ok = t->ne[0] >= 1 && (uint64_t)t->ne[0] <= 4 * mf->map_size;
+        uint64_t rows = 1;
+        for (int d = 1; d < 4 && shape_ok; d++)
+            shape_ok = t->ne[d] >= 1 && !__builtin_mul_overflow(rows, (uint64_t)t->ne[d], &rows);
+        if (!shape_ok) return fail(mf, "tensor %s has a bad shape", t->name);
+        const size_t rs = g4_row_size(t->type, t->ne[0]);
         if (!rs) return fail(mf, "tensor %s has an unsupported type or row length", t->name);
-        const uint64_t bytes = (uint64_t)rs * (uint64_t)(nel / t->ne[0]);
-        if (mf->data_start + t->offset + bytes > mf->map_size || t->offset > mf->map_size)
+        uint64_t bytes = 0;
+        if (__builtin_mul_overflow((uint64_t)rs, rows, &bytes) || t->offset > mf->map_size || bytes > mf->map_size ||
+            mf->data_start + t->offset + bytes > mf->map_size)
             return fail(mf, "tensor %s out of bounds", t->name);
         t->data = (const uint8_t *)base + mf->data_start + t->offset;
     }
@@ -320,9 +351,10 @@ extern "C" int g4_gguf_open(g4_model_file *mf, const char *path, bool verbose) {
     if (std::strcmp(mf->arch, "gemma4") != 0 && !mf->is_assistant)
         return fail(mf, "unsupported architecture '%s' (need gemma4, gemma4-assistant, or qwen35)", mf->arch);
     mf->add_bos = true;                               // gemma4 always adds BOS (gguf.c:383-385)
-    mf->n_layer_kv = mf->n_layer - mf->n_kv_shared;
-    if (mf->n_layer > G4_MAX_LAYERS || mf->n_layer < 0 || (!mf->is_assistant && mf->n_layer_kv < 2))
+    if (mf->n_layer > G4_MAX_LAYERS || mf->n_layer < 0 || mf->n_kv_shared < 0 || mf->n_kv_shared > mf->n_layer)
         return fail(mf, "bad layer config");
+    mf->n_layer_kv = mf->n_layer - mf->n_kv_shared;
+    if (!mf->is_assistant && mf->n_layer_kv < 2) return fail(mf, "bad layer config");
     if (verbose)
         std::fprintf(stderr, "g4: %s: %llu tensors, %llu kv, data @ %llu; arch=%s n_layer=%d n_embd=%d n_vocab=%d\n", path,
                      (unsigned long long)mf->n_tensors, (unsigned long long)mf->n_kv, (unsigned long long)mf->data_start,
