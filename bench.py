@@ -281,6 +281,69 @@ def _timed(G, fn, reps: int = 5) -> float:
     return float(np.median(ts))
 
 
+class _GpuQuant:
+    """quantize(t, rows) through the library's own quantizer launch: the
+    synthetic GGUF writer of the tests needs q8_0 / q4_0 rows, and the bench
+    makes them without the oracle."""
+
+    def __init__(self, G):
+        self.G = G
+
+    def quantize(self, t, x):
+        G = self.G
+        x = np.ascontiguousarray(x, np.float32)
+        rows, n = x.shape
+        xb, yb = G.Buffer.from_array(x), G.Buffer(G.row_size(t, n) * rows)
+        G.quantize(t, xb, n, rows, yb)
+        return yb.download(np.uint8, (rows, G.row_size(t, n)))
+
+
+def bench_gemma(G, pos_fill=1024, steps=32):
+    """A gemma4 model from a GGUF file (scope rank 1: reader, residency, the
+    gemma4 step): a synthetic file of 8 layers, width 2048, FFN 6144, 32768
+    tokens, written here, loaded with g4h_gemma_open, filled to pos_fill with
+    64-token batches, then `steps` single-token forwards timed (host-driven and
+    synchronous, logits copied back each call)."""
+    import tempfile
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import gemma_util as GM
+    spec = dict(GM.SMALL, n_layer=8, n_kv_shared=2, n_embd=2048, n_head=8, head_dim_full=256, head_dim_swa=256,
+                n_ff=[6144] * 8, n_embd_per_layer=256, n_vocab=32768, n_swa=512,
+                is_swa=[1, 1, 1, 0, 1, 1, 1, 0])
+    hp, T = GM.make_gemma(_GpuQuant(G), 9, spec=spec)
+    fd, path = tempfile.mkstemp(suffix=".gguf")
+    os.close(fd)
+    try:
+        GM.write_gemma(path, hp, T)
+        nbytes = os.path.getsize(path)
+        del T
+        g = G.Gemma(path, n_ctx=pos_fill + steps + 64)
+        rs = np.random.default_rng(8)
+        for p0 in range(0, pos_fill, 64):
+            g.forward(rs.integers(0, g.n_vocab, 64).astype(np.int32), p0)
+        toks = rs.integers(0, g.n_vocab, steps).astype(np.int32)
+        G.synchronize()
+        t0 = time.perf_counter()
+        for i in range(steps):
+            g.forward(toks[i:i + 1], pos_fill + i)
+        G.synchronize()
+        ms = (time.perf_counter() - t0) * 1e3 / steps
+        t0 = time.perf_counter()
+        g.forward(rs.integers(0, g.n_vocab, 64).astype(np.int32), pos_fill + steps)
+        G.synchronize()
+        ms64 = (time.perf_counter() - t0) * 1e3
+        g.free()
+    finally:
+        os.unlink(path)
+    return {"decode_tok_per_s": round(1e3 / ms, 1), "ms_per_token": round(ms, 3), "batch_64_ms": round(ms64, 2),
+            "file_bytes": nbytes,
+            "what": f"gemma4 from a synthetic {nbytes / 1e6:.0f} MB GGUF (g4h_gemma_open: mmap reader, upload and "
+                    "repack): 8 layers (6 sliding-window on the KV ring, 2 shared-KV), width 2048, 8 heads x 256, "
+                    "FFN 6144, per-layer embeddings 256, 32768 tokens, soft-cap; q8_0/q4_0/q4_K/q6_K/f16/bf16 "
+                    f"weights; single-token forwards at positions {pos_fill}..{pos_fill + steps - 1}, host-driven, "
+                    "logits copied back per call; and one 64-token batch"}
+
+
 def bench_next(G, m):
     """The rows after the decode path (rank 3-4 of the scope table) on the same
     model and shapes: a speculative-decoding verify batch and a prefill chunk
@@ -330,7 +393,11 @@ def bench_next(G, m):
                                            f"{H} q / {KV} kv heads x {hd}, f16 cache (model.c:509-545): one set of "
                                            "launches over a token grid dimension, each token's K/V prefix read "
                                            "for that token (bytes counted so)"}
-    log("bench: next rows " + ", ".join(f"{k} {v.get('ms', v.get('us'))}" for k, v in out.items()))
+    try:
+        out["gemma4_gguf"] = bench_gemma(G)
+    except Exception as e:                      # reported in the line; the other rows stand
+        out["gemma4_gguf"] = {"error": f"{type(e).__name__}: {e}"}
+    log("bench: next rows " + ", ".join(f"{k} {v.get('ms', v.get('us', v.get('ms_per_token')))}" for k, v in out.items()))
     return out
 
 
