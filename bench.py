@@ -28,10 +28,10 @@ sys.path.insert(0, ROOT)
 PEAK_HBM = 8000.0          # GB/s, MI355X published
 PEAK_INT8 = 5000.0         # dense int8 MFMA TOPS, MI355X published
 # HBM bytes per launch of the roofline kernel (q4_0 10240x2560 GEMV) from two
-# rocprofv3 --pmc passes: FETCH_SIZE 7281.1 KiB x 2.00 + WRITE_SIZE 64.0 KiB x
+# rocprofv3 --pmc passes: FETCH_SIZE 7275.6 KiB x 2.00 + WRITE_SIZE 64.0 KiB x
 # 1.00, scales from a 256 MiB device copy in the same runs
 # (profiles/gemv_q4_0_ffn_traffic.md).
-TRAFFIC_UP = int((7281.1 * 2.00 + 64.0 * 1.00) * 1024)
+TRAFFIC_UP = int((7275.6 * 2.00 + 64.0 * 1.00) * 1024)
 MALL = 256 << 20
 
 
@@ -110,16 +110,47 @@ def copies_for(nbytes: int) -> int:
     return max(2, -(-2 * MALL // nbytes))
 
 
-def time_graph(G, stream, fn, k):
-    """Capture fn(i) for i < k into one graph; time one replay with events."""
+MAX_GRAPH_NODES = 512
+# --eager: launch every timed call directly instead of replaying graphs.  Under
+# rocprofv3 --kernel-trace, hipGraphLaunch ended in a host-side segmentation
+# fault inside the runtime (graphs of 13 000 and of 512 launches alike), so a
+# traced run uses this mode; the kernel durations it records are the same
+# kernels'.
+EAGER = False
+
+
+def time_graph(G, stream, fn, k, per_call=2):
+    """Device time (ms) of the k calls fn(0) .. fn(k-1) on `stream`.
+
+    The calls are captured into graphs of at most MAX_GRAPH_NODES launches
+    (per_call: launches one call makes); a graph of ~13 000 launches ended in a
+    host-side fault of the runtime's graph launch under rocprofv3.  The graphs
+    are replayed once (first-launch set-up), then once more without waiting,
+    and HIP events on the stream bracket a third replay queued behind that
+    one: the device is busy while the timed replay is submitted, so the timed
+    region holds exactly the k calls and no host submission gap."""
+    per = max(1, min(k, MAX_GRAPH_NODES // max(1, per_call)))
     fn(0)                               # outside capture: sizes any scratch first
     stream.synchronize()
-    graph = G.Graph(stream.ptr, lambda: [fn(i) for i in range(k)])
-    graph.launch(stream.ptr)            # warm replay
+    if EAGER:
+        e0, e1 = G.Event(), G.Event()
+        e0.record(stream.ptr)
+        for i in range(k):
+            fn(i)
+        e1.record(stream.ptr)
+        return e0.elapsed_ms(e1)
+    graphs = [G.Graph(stream.ptr, lambda c0=c0: [fn(i) for i in range(c0, min(k, c0 + per))]) for c0 in range(0, k, per)]
+
+    def replay():
+        for g in graphs:
+            g.launch(stream.ptr)
+
+    replay()
     stream.synchronize()
+    replay()                            # keeps the device busy while the timed pass is queued
     e0, e1 = G.Event(), G.Event()
     e0.record(stream.ptr)
-    graph.launch(stream.ptr)
+    replay()
     e1.record(stream.ptr)
     ms = e0.elapsed_ms(e1)
     return ms
@@ -201,6 +232,73 @@ def cpu_baseline(sets, seconds: float):
             g4o.use_reference_dots(False)
 
 
+def read_floor_us(G, stream, nbytes: int, k: int, threads: int = 256, loads: int = 1, ny: int = 0) -> float:
+    """Per-launch time of g4h_read_floor over nbytes (weights-sized buffers
+    rotated past the MALL like the GEMV's copies), optionally writing ny floats."""
+    bufs = [G.Buffer(nbytes) for _ in range(copies_for(nbytes))]
+    for b in bufs:
+        b.zero()
+    y = G.Buffer(max(4, ny * 4))
+    G.synchronize()
+    us = time_graph(G, stream, lambda i: G.read_floor(bufs[i % len(bufs)], nbytes, y if ny else None, ny, threads, loads,
+                                                      stream=stream.ptr), k, per_call=1) / k * 1e3
+    for b in bufs:
+        b.free()
+    return us
+
+
+def bench_floor(G, stream, s, gemv_us: float):
+    """The read floor of the roofline GEMV's launch: a launch that only reads as
+    many bytes as its weights (g4h_read_floor, 128-bit non-temporal loads), in
+    the fastest measured shape (256-thread workgroups, one load per thread),
+    and in the GEMV's workgroup size and loads per thread with its y written."""
+    wbytes = s.rows * G.row_size(s.qt, s.cols)
+    desc = G.matmul_describe(s.W[0], 1, 1)
+    block = int(desc.split("block=")[1].split()[0])
+    upl = int(desc.split("upl=")[1].split(">")[0])
+    k = 300
+    t_best = read_floor_us(G, stream, wbytes, k)
+    t_shape = read_floor_us(G, stream, wbytes, k, threads=block, loads=upl, ny=s.rows)
+    out = {"bytes": wbytes, "read_us": round(t_best, 3), "read_GBps": round(wbytes / t_best / 1e3, 1),
+           "gemv_shape_read_write_us": round(t_shape, 3),
+           "gemv_us": round(gemv_us, 3), "gemv_frac_of_floor": round(t_best / gemv_us, 4),
+           "what": f"g4h_read_floor over {wbytes} B (the weights of q4_0 {s.rows}x{s.cols}), copies rotated past the MALL: "
+                   f"256-thread workgroups with one 16-byte load per thread; and {block}-thread workgroups with {upl} "
+                   f"loads per thread writing {s.rows} floats (the GEMV's launch shape and output)"}
+    log(f"bench: read floor {t_best:.3f} us ({out['read_GBps']} GB/s), GEMV shape {t_shape:.3f} us; "
+        f"GEMV {gemv_us:.3f} us = {100 * out['gemv_frac_of_floor']:.1f}% of the floor rate")
+    return out
+
+
+STEADY = {"q4_0_32768x10240": (2, 32768, 10240), "q8_0_16384x10240": (8, 16384, 10240)}
+
+
+def bench_steady(G, stream):
+    """q4_0 / q8_0 GEMVs of >= 150 MB, where the ~1.5 us launch ramp and drain
+    are a few per cent of the launch: the weight stream's own rate, beside the
+    read floor of the same byte count."""
+    out = {}
+    for name, (qt, rows, cols) in STEADY.items():
+        s = GemvSet(G, qt, rows, cols, copies_for(rows * G.row_size(qt, cols)), seed=55)
+        k = 24
+        t_pre = time_graph(G, stream, lambda i: s.call(G, i, stream.ptr, fused=False), k, per_call=1) / k * 1e3
+        t_x = time_graph(G, stream, lambda i: s.call(G, i, stream.ptr, fused=True), k, per_call=2) / k * 1e3
+        wbytes = rows * G.row_size(qt, cols)
+        kernel = G.matmul_describe(s.W[0], 1, 1).split(";")[0]
+        for t in s.W:
+            t.free()
+        t_fl = read_floor_us(G, stream, wbytes, k)
+        out[name] = {"alg_bytes": s.bytes, "gemv_us": round(t_pre, 3), "GBps": round(s.bytes / t_pre / 1e3, 1),
+                     "frac": round(s.bytes / t_pre / 1e3 / PEAK_HBM, 4),
+                     "with_quantize_us": round(t_x, 3), "with_quantize_GBps": round(s.bytes / t_x / 1e3, 1),
+                     "read_floor_us": round(t_fl, 3), "read_floor_GBps": round(wbytes / t_fl / 1e3, 1),
+                     "kernel": kernel, "copies": len(s.W)}
+        log(f"bench: steady {name}: {t_pre:.3f} us {out[name]['GBps']} GB/s ({100 * out[name]['frac']:.1f}%), "
+            f"with quantize {t_x:.3f} us; read floor {t_fl:.3f} us {out[name]['read_floor_GBps']} GB/s")
+        del s
+    return out
+
+
 def bench_prefill(G, stream, Ms=(1, 8, 16, 32, 64, 128, 256, 512)):
     """q8_0 4096x4096 x M tokens on the GEMV family (path 1)
     and on the int8 matrix cores (path 2); weights rotated beyond the MALL,
@@ -218,7 +316,7 @@ def bench_prefill(G, stream, Ms=(1, 8, 16, 32, 64, 128, 256, 512)):
         for path, name in ((1, "gemv"), (2, "mfma")):
             k = 100 if M <= 64 else 40
             fn = lambda i: G.matmul(s.W[i % len(s.W)], Yb, nb=M, x=xb, path=path, stream=stream.ptr)
-            us = time_graph(G, stream, fn, k) / k * 1e3
+            us = time_graph(G, stream, fn, k, per_call=2 if path == 2 else -(-M // 8) + 1) / k * 1e3
             row[name] = {"us": round(us, 2), "GBps": round(alg / us / 1e3, 1), "TOPS": round(ops / us / 1e6, 1),
                          "hbm_frac": round(alg / us / 1e3 / PEAK_HBM, 4),
                          "pct_int8_peak": round(100 * ops / us / 1e6 / PEAK_INT8, 2),
@@ -385,14 +483,18 @@ def bench_next(G, m):
     wst = G.Buffer(G.attn_workspace_bytes(H, hd, pos0 + nb))
     ms_b = _timed(G, lambda: G.attn_prefill(q, kc, vc, G.F16, H, KV, hd, pos0, nb, o, ws=wsb))
     ms_t = _timed(G, lambda: G.attn_prefill(q, kc, vc, G.F16, H, KV, hd, pos0, nb, o, ws=wst, batched=False))
-    # each token reads its own prefix of K and V, as attn_kernel does per (token, head)
-    alg = sum(2 * (pos0 + b + 1) * KV * hd * 2 for b in range(nb))
+    # unique HBM bytes: every cached K/V row once, plus q and out; each token
+    # attends its own prefix (attn_kernel per (token, head)), which the
+    # launches read from the caches' shared rows
+    uniq = 2 * (pos0 + nb) * KV * hd * 2 + 2 * nb * H * hd * 4
+    prefix = sum(2 * (pos0 + b + 1) * KV * hd * 2 for b in range(nb))
     out["prefill_attention_64"] = {"us": round(ms_b * 1e3, 1), "per_token_launches_us": round(ms_t * 1e3, 1),
-                                   "alg_bytes": alg, "GBps": round(alg / (ms_b * 1e-3) / 1e9, 1),
+                                   "alg_bytes": uniq, "GBps": round(uniq / (ms_b * 1e-3) / 1e9, 1),
+                                   "prefix_bytes_per_token_sum": prefix,
                                    "what": f"g4h_attn_prefill, {nb} new tokens after {pos0} cached positions, "
                                            f"{H} q / {KV} kv heads x {hd}, f16 cache (model.c:509-545): one set of "
-                                           "launches over a token grid dimension, each token's K/V prefix read "
-                                           "for that token (bytes counted so)"}
+                                           "launches over a token grid dimension; bytes are the unique K/V rows "
+                                           "read plus q and out (the sum of the tokens' prefixes is given apart)"}
     try:
         out["gemma4_gguf"] = bench_gemma(G)
     except Exception as e:                      # reported in the line; the other rows stand
@@ -409,14 +511,15 @@ def bench_decode(G, steps: int, cpu_seconds: float, want_cpu: bool):
     st = G.Stream()
     pos0 = c["n_ctx"] - steps
     m.set_state(1, pos0, st.ptr)
-    graph = G.Graph(st.ptr, lambda: m.forward_state(st.ptr))
-    graph.launch(st.ptr)                 # warm replay
+    graph = None if EAGER else G.Graph(st.ptr, lambda: m.forward_state(st.ptr))
+    step = (lambda: m.forward_state(st.ptr)) if EAGER else (lambda: graph.launch(st.ptr))
+    step()                               # warm replay
     st.synchronize()
     m.set_state(1, pos0, st.ptr)
     e0, e1 = G.Event(), G.Event()
     e0.record(st.ptr)
     for _ in range(steps):
-        graph.launch(st.ptr)
+        step()
     e1.record(st.ptr)
     ms = e0.elapsed_ms(e1)
     tok, pos = m.get_state(st.ptr)
@@ -484,6 +587,9 @@ def main():
     ap.add_argument("--no-configs", action="store_true",
                     help="skip the per-config GEMV sweep (BASELINE configs 0 and 2, plus the further formats)")
     ap.add_argument("--decode-steps", type=int, default=128, help="decode steps timed at context ~8192 (0 = skip)")
+    ap.add_argument("--no-steady", action="store_true", help="skip the >= 150 MB q4_0 / q8_0 GEMV rows")
+    ap.add_argument("--eager", action="store_true",
+                    help="direct launches instead of graph replays (for rocprofv3 --kernel-trace runs)")
     ap.add_argument("--prefill", default="1,8,64,512", metavar="M,...",
                     help="token counts of config 3 (GEMV vs matrix-core crossover); '' skips it")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -494,6 +600,8 @@ def main():
               "the GEMV shards by output rows across GPUs, see DESIGN.md", file=sys.stderr)
         sys.exit(2)
 
+    global EAGER
+    EAGER = args.eager
     import g4run_amd as G
     G.init(0)
     stream = G.Stream()
@@ -531,6 +639,7 @@ def main():
     per_launch_us = ms_k / kr * 1e3
     achieved = up.bytes / (per_launch_us * 1e-6) / 1e9
     kernel = G.matmul_describe(up.W[0], 1, 1).split(";")[0]
+    floor = bench_floor(G, stream, up, per_launch_us)
 
     extra = {}
     if not args.no_configs:
@@ -550,6 +659,7 @@ def main():
                 f"({100 * s.bytes / t_pre / 1e3 / PEAK_HBM:.1f}% of 8 TB/s); with quantize {t_fus:.3f} us")
             del s
 
+    steady = None if args.no_steady else bench_steady(G, stream)
     prefill_ms = args.prefill
     prefill = bench_prefill(G, stream, tuple(int(m) for m in prefill_ms.split(","))) if prefill_ms else None
     attention = bench_attention(G, stream)
@@ -579,9 +689,13 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM, "unit": "GB/s",
                      "frac": round(achieved / PEAK_HBM, 4), "traffic": TRAFFIC_UP,
                      "kernel": kernel + " (q4_0 10240x2560, pre-quantized q8_0 input)",
-                     "alg_bytes_per_launch": up.bytes, "avg_launch_us": round(per_launch_us, 3)},
+                     "alg_bytes_per_launch": up.bytes, "avg_launch_us": round(per_launch_us, 3),
+                     "read_floor_us": floor["read_us"], "frac_of_read_floor": floor["gemv_frac_of_floor"]},
+        "read_floor": floor,
         "cpu_baseline": cpu,
     }
+    if steady:
+        out["steady_state"] = steady
     if extra:
         out["configs"] = extra
     if prefill:

@@ -127,6 +127,7 @@ _SIGS = [
     ("g4h_gemma_free", _int, [_vp]),
     ("g4h_gemma_info", _int, [_vp, C.POINTER(_int), C.POINTER(_int), C.POINTER(_int), C.POINTER(_int)]),
     ("g4h_gemma_forward", _int, [_vp, C.POINTER(_int), _int, _int, _vp, _vp, _vp]),
+    ("g4h_read_floor", _int, [_vp, _sz, _vp, C.c_int64, _int, _int, _vp]),
 ]
 
 _lib = None
@@ -358,6 +359,12 @@ def matmul_describe(W: Tensor, nb: int = 1, path: int = 0) -> str:
     buf = C.create_string_buffer(256)
     check(lib().g4h_matmul_describe(W.ptr, nb, path, buf, 256))
     return buf.value.decode()
+
+
+def read_floor(src, nbytes: int, y=None, ny: int = 0, threads: int = 256, loads: int = 1, stream=None) -> None:
+    """One launch that only reads nbytes of src (128-bit non-temporal loads)
+    and writes ny floats of y: the yardstick a GEMV launch is timed against."""
+    check(lib().g4h_read_floor(_p(src), nbytes, _p(y) if y is not None else None, ny, threads, loads, stream))
 
 
 def block_sums(W: Tensor, pre, out, tok: int = 0, pre_stride: int = 0, stream=None) -> None:

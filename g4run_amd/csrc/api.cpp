@@ -301,7 +301,7 @@ extern "C" int g4h_tensor_create(int type, int64_t ncols, int64_t nrows, g4h_ten
     const size_t n = (size_t)(nrows * nb);
     size_t qs = 0, sc = 0, ex = 0, dd = 0;
     switch (type) {
-    case Q8_0: qs = n * 32; sc = n * 2; break;
+    case Q8_0: qs = al256(n * 16) + n * 16; sc = n * 2; break;   // lo | hi halves (common.h)
     case Q4_0: qs = n * 16; sc = n * 2; break;
     case Q4_K: qs = n * 144; break;
     case Q5_K: qs = n * 176; break;
@@ -322,6 +322,7 @@ extern "C" int g4h_tensor_create(int type, int64_t ncols, int64_t nrows, g4h_ten
     t->sc = t->qs + al256(qs);
     t->ex = t->sc + al256(sc);
     t->dd = t->ex + al256(ex);
+    if (type == Q8_0) t->ex = t->qs + al256(n * 16);            // bytes 16..31 of every block
     *out = t;
     return G4H_OK;
 }
@@ -610,6 +611,15 @@ static int matmul_impl(const g4h_tensor *W, const float *x, const void *pre, siz
 
 extern "C" int g4h_matmul(const g4h_tensor *W, const float *x, const void *pre, size_t pre_stride, float *Y, int nb, void *s) {
     return g4h_matmul_ex(W, x, pre, pre_stride, Y, nb, 0, s);
+}
+
+extern "C" int g4h_read_floor(const void *src, size_t bytes, float *y, int64_t ny, int threads, int loads, void *s) {
+    G4_NEED_INIT();
+    if (!src || bytes < 16 || bytes % 16 || (uintptr_t)src % 16 || threads < 64 || threads > 1024 || threads % 64 || loads < 1 ||
+        loads > 8 || ny < 0 || (ny > 0 && !y))
+        return fail(G4H_ERR_ARG, "g4h_read_floor: bad argument");
+    G4_HIP(launch_read_floor((const uint8_t *)src, bytes, y, ny, threads, loads, (hipStream_t)s));
+    return G4H_OK;
 }
 
 extern "C" int g4h_block_sums(const g4h_tensor *W, const void *pre, size_t pre_stride, int tok, int32_t *sums, void *s) {

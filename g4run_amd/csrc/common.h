@@ -185,7 +185,12 @@ __device__ __forceinline__ void issue_order() {
 
 // Resident weight matrix (the object behind the C ABI's g4h_tensor).
 // Layout per type, per row r and per (super)block j, with nb blocks per row:
-//   q8_0: qs plane  [r][j][32] int8          sc plane [r][j] fp16 d
+//   q8_0: qs plane  [r][j][16] int8 quants 0..15 of each block, then (at
+//         ex = qs + the first half's 256-B aligned size) [r][j][16] quants
+//         16..31; sc plane [r][j] fp16 d.  Lane l's 16-byte load of a row's
+//         block l then sits next to lane l+1's: every wave load of a half is
+//         one contiguous run (two 16-byte loads 32 bytes apart per block
+//         streamed 16 % slower at 178 MB).
 //   q4_0: qs plane  [r][j][16] nibbles       sc plane [r][j] fp16 d
 //   q4_K: qs plane  [r][j][144] the GGUF block unchanged (16-B header + qs)
 //   q5_K: qs plane  [r][j][176] the GGUF block unchanged (16-B header, qh, qs)
@@ -206,6 +211,6 @@ struct g4h_tensor {
     size_t bytes;
     uint8_t *qs;                // quant plane
     uint8_t *sc;                // scale plane (q8_0/q4_0/tq2_0: fp16 d; q2_K/q3_K: packed scales)
-    uint8_t *ex;                // q2_K: {d,dmin}; q3_K: hmask; q6_K: qh
+    uint8_t *ex;                // q8_0: quants 16..31; q2_K: {d,dmin}; q3_K: hmask; q6_K: qh
     uint8_t *dd;                // q3_K / q6_K: fp16 d
 };

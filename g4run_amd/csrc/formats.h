@@ -70,7 +70,7 @@ template <int NB>
 __device__ __forceinline__ void stage_q8_0_load(StageQ8_0 &S, int item, const uint8_t *act, size_t stride, int nb) {
     const int npair = nb >> 1;
     S.ok = item < NB * npair;
-    S.t = S.ok ? item / npair : 0;
+    S.t = (NB == 1 || !S.ok) ? 0 : item / npair;                     // one token: no division ahead of the stream
     S.pr = S.ok ? item - S.t * npair : 0;
     const uint32_t *src = S.ok ? (const uint32_t *)(act + (size_t)S.t * stride + (size_t)S.pr * 68) : g_stage_pad;
 #pragma unroll
@@ -219,7 +219,7 @@ __device__ __forceinline__ void stage_q8_K_load(StageQ8_K &S, int item, const ui
     const int per = nb * 19;
     S.ok = item < NB * per;
     const int it = S.ok ? item : 0;
-    S.t = it / per;
+    S.t = NB == 1 ? 0 : it / per;                                    // one token: no division ahead of the stream
     const int r = it - S.t * per;
     S.sb = r / 19;
     S.s = r - S.sb * 19;
@@ -270,8 +270,7 @@ struct FQ8_0 {
     struct Frag { int4 w0, w1; uint16_t d; };
     static __device__ __forceinline__ void load(Frag &f, const g4h_tensor &W, int64_t row, int u) {
         const size_t j = (size_t)row * W.nb + u;
-        const uint8_t *q = W.qs + j * 32;
-        f.w0 = ld4s(q); f.w1 = ld4s(q + 16);
+        f.w0 = ld4s(W.qs + j * 16); f.w1 = ld4s(W.ex + j * 16);      // the two half-block planes
         f.d = ((const uint16_t *)W.sc)[j];
     }
     static __device__ __forceinline__ int isum(const Frag &f, const Act &A, int u) {

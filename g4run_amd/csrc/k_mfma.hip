@@ -76,7 +76,8 @@ __global__ __launch_bounds__(256) void k_mm_mfma(g4h_tensor W, const int8_t *__r
     const int64_t row = min((int64_t)(n0 + li), W.nrows - 1);
     const int8_t *pa = qa + (size_t)tok * nb * 32 + 16 * kh;
     const uint16_t *pda = da + (size_t)tok * nb;
-    const uint8_t *pw = WT == Q8_0 ? W.qs + (size_t)row * nb * 32 + 16 * kh : W.qs + (size_t)row * nb * 16;
+    // q8_0: lane half kh reads its half-block plane (common.h); 16 bytes per block either way
+    const uint8_t *pw = (WT == Q8_0 && kh ? W.ex : W.qs) + (size_t)row * nb * 16;
     const uint16_t *pdw = (const uint16_t *)W.sc + (size_t)row * nb;
 
     v16f acc;
@@ -97,7 +98,7 @@ __global__ __launch_bounds__(256) void k_mm_mfma(g4h_tensor W, const int8_t *__r
         for (int k = 0; k < KB; k++) {
             const int b = min(blk(j0, k), nb - 1);
             o.a[k] = *(const v4i *)(pa + (size_t)b * 32);
-            o.w[k] = *(const v4i *)(pw + (size_t)b * (WT == Q8_0 ? 32 : 16));
+            o.w[k] = *(const v4i *)(pw + (size_t)b * 16);
             o.sa[k] = pda[b];
             o.sw[k] = pdw[b];
         }
@@ -198,10 +199,14 @@ __global__ __launch_bounds__(64 * TM * TN, 2) void k_mm_lds(g4h_tensor W, const 
         const int c = t + i * NT, r = c / ACH, q = c % ACH;
         aoff[i] = (uint32_t)(((size_t)min(m0 + r, M - 1) * nb) * 32 + 16 * q);
     }
+    // q8_0 chunk q of a row's stage: half q & 1 of block q / 2, from that
+    // half's plane (common.h); q4_0 chunk q: block q
+    const uint32_t hoff = (uint32_t)(W.ex - W.qs);
 #pragma unroll
     for (int i = 0; i < BPT; i++) {
         const int c = t + i * NT, r = c / BCH, q = c % BCH;
-        boff[i] = (uint32_t)(((size_t)min(n0 + r, W.nrows - 1) * nb) * WB + 16 * q);
+        const size_t rb = (size_t)min(n0 + r, W.nrows - 1) * nb * 16;
+        boff[i] = WT == Q8_0 ? (uint32_t)(rb + 16 * (q >> 1)) + ((q & 1) ? hoff : 0u) : (uint32_t)(rb + 16 * q);
     }
     // threads past the scale rows load a weight row's run too and keep it
     const uint16_t *psc = t < BM ? da + (size_t)min(m0 + t, M - 1) * nb
@@ -212,7 +217,7 @@ __global__ __launch_bounds__(64 * TM * TN, 2) void k_mm_lds(g4h_tensor W, const 
     };
     auto load = [&](Stage &S, int s) {
         const int8_t *ab = qa + (size_t)s * KB * 32;
-        const uint8_t *bb = W.qs + (size_t)s * KB * WB;
+        const uint8_t *bb = W.qs + (size_t)s * KB * 16;
 #pragma unroll
         for (int i = 0; i < APT; i++) S.a[i] = *(const v4i *)(ab + aoff[i]);
 #pragma unroll
@@ -421,7 +426,7 @@ constexpr int few_seg() { return MT == 1 ? 16 : MT == 2 ? 8 : MT == 3 ? 6 : 4; }
 template <int WT, int MT>
 __global__ __launch_bounds__(256) void k_mm_few(g4h_tensor W, const int8_t *__restrict__ qa,
                                                 const uint16_t *__restrict__ da, int M, float *__restrict__ Y) {
-    constexpr int S = few_seg<MT>(), WB = WT == Q8_0 ? 32 : 16;
+    constexpr int S = few_seg<MT>();
     using WV = std::conditional_t<WT == Q8_0, v4i, v2i>;
     __shared__ float red[3 * MT * 4 * 64];
     // the wave index in a scalar register: the first lane's thread index / 64
@@ -437,11 +442,14 @@ __global__ __launch_bounds__(256) void k_mm_few(g4h_tensor W, const int8_t *__re
     // the slice of a block this lane group feeds the int8 MFMA after the swap
     const int sl = WT == Q8_0 ? ((kg & 1) << 1) | (kg >> 1) : kg;
     // per-lane 32-bit byte offsets, fixed over the loop; the per-step part is
-    // uniform (the launch keeps the weight planes under 4 GB).  The weight
-    // bytes of an odd last pair's missing block are the next row's (or, past
-    // the last row, the scale plane's that follows the quants): loaded, never
-    // used.  Its scale index is clamped to the row.
-    const uint32_t wlane = (uint32_t)((uint64_t)row * nb * WB) + (WB / 2) * kg;
+    // uniform (the launch keeps the weight planes under 4 GB).  q8_0: lane
+    // group kg takes half kg & 1 of block 2 p + kg / 2 from that half's plane
+    // (common.h); q4_0: bytes 8 kg .. 8 kg + 7 of the pair's 32 nibble bytes.
+    // The weight bytes of an odd last pair's missing block are the next row's
+    // (or, past the last row, the next plane's): loaded, never used.  Its
+    // scale index is clamped to the row.
+    const uint32_t wlane = WT == Q8_0 ? (uint32_t)((uint64_t)row * nb * 16) + 16 * (kg >> 1) + ((kg & 1) ? (uint32_t)(W.ex - W.qs) : 0u)
+                                      : (uint32_t)((uint64_t)row * nb * 16) + 8 * kg;
     const uint32_t slane1 = (uint32_t)((uint64_t)row * nb * 2) + 2 * (kg & 1), slane0 = slane1 - 2 * (kg & 1);
     const uint32_t alane = li * 64 + 16 * sl, dlane = 8 * (2 * li + (kg & 1));
 
@@ -455,7 +463,7 @@ __global__ __launch_bounds__(256) void k_mm_few(g4h_tensor W, const int8_t *__re
     auto load = [&](int j) __attribute__((always_inline)) -> Op {
         const int p = min(4 * j + wave, np - 1);
         Op o;
-        o.w = *(const WV *)(W.qs + (size_t)p * 2 * WB + wlane);
+        o.w = *(const WV *)(W.qs + (size_t)p * 32 + wlane);
         o.s = *(const uint16_t *)(W.sc + (size_t)p * 4 + (2 * p + 1 < nb ? slane1 : slane0));
         // a step past the wave's last, or the missing block of an odd last
         // pair, gets weight scale 0: its products add +0 to the accumulator,
@@ -656,7 +664,7 @@ static bool mm_small(const g4h_tensor &W, int M) {
     const int64_t tiles = ((W.nrows + 31) / 32) * ((M + 31) / 32);
     const uint64_t wb = W.type == Q8_0 ? 32 : 16;
     return tiles <= 3 * 256 || W.nb % MML_KB != 0 || (uint64_t)M * W.nb * 32 >= (1ull << 32) ||
-           (uint64_t)W.nrows * W.nb * wb >= (1ull << 32);
+           (uint64_t)W.nrows * W.nb * wb >= (1ull << 32) - 512;     // q8_0: the second half-plane starts 256-B aligned
 }
 
 // Staged tile shape: 64 x 128 (8 waves, two register stages) when that still

@@ -28,11 +28,12 @@ __global__ __launch_bounds__(256) void k_rand_normal(float *y, int64_t n, uint64
 
 // ------------------------------------------------------------- embedding --
 // x = dequant(row `token` of the tied q8_0 head) * sqrt(n_embd) (model.c:605-612),
-// read from the resident planes (qs [row][blk][32], d fp16); then
+// read from the resident planes (quants 0..15 of each block in lo, 16..31 in
+// hi, d fp16); then
 // act = q8_0(rms(x)*w_pre), the first layer's attention-norm activation
 // (skipped without w_pre, when that norm runs in the Wqkv GEMV).  512 threads,
 // n <= 8192; workgroup b takes token[b] into x + b*n and act + b*ast.
-__global__ __launch_bounds__(512) void k_embed_norm(const int8_t *qs, const uint16_t *sc, int64_t nb, const int *token,
+__global__ __launch_bounds__(512) void k_embed_norm(const int8_t *lo, const int8_t *hi, const uint16_t *sc, int64_t nb, const int *token,
                                                     float *x, int n, float es, const float *w_pre, float eps, uint8_t *act,
                                                     size_t ast) {
     const int b = blockIdx.x;
@@ -40,7 +41,8 @@ __global__ __launch_bounds__(512) void k_embed_norm(const int8_t *qs, const uint
     x += (size_t)b * n;
     for (int i = threadIdx.x; i < n; i += blockDim.x) {
         const int64_t j = r * nb + (i >> 5);
-        const float v = (float)qs[j * 32 + (i & 31)] * h2f(sc[j]);
+        const int e = i & 31;
+        const float v = (float)(e < 16 ? lo : hi)[j * 16 + (e & 15)] * h2f(sc[j]);
         x[i] = v * es;
     }
     __syncthreads();
@@ -116,7 +118,8 @@ hipError_t launch_rand_normal(float *y, int64_t n, uint64_t seed, float mean, fl
 hipError_t launch_embed_norm(const g4h_tensor &head, const int *token, float *x, float es, const float *w_pre, float eps,
                              uint8_t *act, hipStream_t s, int nb, size_t ast) {
     if (head.type != Q8_0 || head.ncols % 32 || head.ncols > 8192 || nb < 1) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_embed_norm, dim3(nb), dim3(512), 0, s, (const int8_t *)head.qs, (const uint16_t *)head.sc, head.nb,
+    hipLaunchKernelGGL(k_embed_norm, dim3(nb), dim3(512), 0, s, (const int8_t *)head.qs, (const int8_t *)head.ex,
+                       (const uint16_t *)head.sc, head.nb,
                        token, x, (int)head.ncols, es, w_pre, eps, act, ast);
     return hipGetLastError();
 }

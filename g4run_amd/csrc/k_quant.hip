@@ -213,7 +213,7 @@ __global__ __launch_bounds__(256) void k_repack(g4h_tensor t, uint8_t *__restric
         }
     };
     switch (t.type) {
-    case Q8_0: mv(t.sc + i * 2, 0, 2); mv(t.qs + i * 32, 2, 32); break;
+    case Q8_0: mv(t.sc + i * 2, 0, 2); mv(t.qs + i * 16, 2, 16); mv(t.ex + i * 16, 18, 16); break;
     case Q4_0: mv(t.sc + i * 2, 0, 2); mv(t.qs + i * 16, 2, 16); break;
     case Q4_K: mv(t.qs + i * 144, 0, 144); break;
     case Q5_K: mv(t.qs + i * 176, 0, 176); break;

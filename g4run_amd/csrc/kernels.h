@@ -15,6 +15,11 @@ hipError_t launch_unpack(const g4h_tensor &t, uint8_t *rows, hipStream_t s);
 hipError_t launch_vec_dot_raw(int wtype, const uint8_t *w, size_t ws, const uint8_t *a, int64_t n, int rows, float *out,
                               hipStream_t s);
 
+// k_stream.hip: one launch reading bytes (a 16-byte multiple) once with
+// 128-bit non-temporal loads, workgroups of `threads`, `loads` per thread, and
+// writing ny floats of y (the read floor a GEMV launch is measured against)
+hipError_t launch_read_floor(const uint8_t *p, size_t bytes, float *y, int64_t ny, int threads, int loads, hipStream_t s);
+
 // k_gemv.hip
 
 void gemv_shape(int type, int64_t nblk, int *lpr, int *upl);

@@ -143,7 +143,7 @@ int g4h_matmul(const g4h_tensor *W, const float *x_dev, const void *pre_dev, siz
  * GEMV family (token chunks of <= 8 staged per workgroup), 2 = int8 matrix-core
  * tiles (q8_0 / q4_0 weights; every per-block integer sum exact, fp32 block
  * scaling in block order).  g4h_matmul_path returns the family auto picks:
- * 2 for q8_0 / q4_0 weights from 24 tokens on, else 1. */
+ * 2 for q8_0 / q4_0 weights from 9 tokens on, else 1. */
 int g4h_matmul_ex(const g4h_tensor *W, const float *x_dev, const void *pre_dev, size_t pre_stride,
                   float *Y_dev, int nb, int path, void *stream);
 int g4h_matmul_path(const g4h_tensor *W, int nb);
@@ -166,6 +166,14 @@ size_t g4h_matmul_noalloc_max_bytes(void);
  * block=512", written NUL-terminated into buf (at most len bytes).  Profiles
  * and benchmarks name the kernel they time with it. */
 int g4h_matmul_describe(const g4h_tensor *W, int nb, int path, char *buf, size_t len);
+/* Diagnostic (no reference counterpart): the read floor.  One launch reads
+ * `bytes` (a multiple of 16, src 16-byte aligned) once with the GEMV's 128-bit
+ * non-temporal loads -- workgroups of `threads` (64..1024, a multiple of 64),
+ * `loads` (1..8) loads per thread -- and writes ny floats of y (0 to skip), the
+ * one output per row a GEMV writes.  It computes nothing: benchmarks time it
+ * beside a GEMV over the same bytes to show what the memory system gives one
+ * launch of that size. */
+int g4h_read_floor(const void *src, size_t bytes, float *y, int64_t ny, int threads, int loads, void *stream);
 
 /* Per-block integer sums of every row of W against token `tok` of pre_dev:
  * q8_0/q4_0 one int32 per 32-block, q3_K/q6_K/tq2_0 one per superblock, q2_K/q4_K/q5_K
