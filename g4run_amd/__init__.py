@@ -642,7 +642,8 @@ class Model:
 
     def trace(self, buf) -> None:
         """Copy each layer's input x, q|k|v projection and attention output (and
-        the final x) into buf every step (trace_floats() floats), or stop with None."""
+        the final x) into buf every step (trace_floats() floats; a batched
+        forward of nb tokens writes nb such traces), or stop with None."""
         check(lib().g4h_model_trace(self.ptr, _p(buf) if buf is not None else None))
 
     def trace_fields(self):

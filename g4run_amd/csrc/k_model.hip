@@ -67,7 +67,8 @@ __global__ __launch_bounds__(512) void k_norm_quant(float *x, const float *delta
 // q8_0 for the down projection; gu holds the (gate, up) pairs interleaved,
 // as the Wgu rows are stored.  256 threads, 4 elements each; grid.y token
 // rows (gu rows of 2 n_ff floats, act rows at ast bytes).
-__global__ __launch_bounds__(256) void k_gelu_quant(const float *gu, int n_ff, const uint16_t *tab, uint8_t *act, size_t ast) {
+__global__ __launch_bounds__(256) void k_gelu_quant(const float *gu, int n_ff, const uint16_t *tab, uint8_t *act, size_t ast,
+                                                    float *hout, size_t hs) {
     const int gi = blockIdx.x * 256 + threadIdx.x;
     gu += (size_t)blockIdx.y * 2 * n_ff;             // token row blockIdx.y
     act += (size_t)blockIdx.y * ast;
@@ -88,6 +89,7 @@ __global__ __launch_bounds__(256) void k_gelu_quant(const float *gu, int n_ff, c
         else gg = h2f(tab[f2h(g[k])]);
         h[k] = gg * u[k];
     }
+    if (hout && own) *(float4 *)(hout + (size_t)blockIdx.y * hs + 4 * gi) = make_float4(h[0], h[1], h[2], h[3]);
     q8_store4(h, gi, own, act);
 }
 
@@ -129,9 +131,10 @@ hipError_t launch_norm_quant(float *x, const float *delta, const float *w_post, 
     hipLaunchKernelGGL(k_norm_quant, dim3(nb), dim3(512), 0, s, x, delta, w_post, w_pre, eps, n, act, ast, y);
     return hipGetLastError();
 }
-hipError_t launch_gelu_quant(const float *gu, int n_ff, const uint16_t *tab, uint8_t *act, hipStream_t s, int nb, size_t ast) {
-    if (n_ff % 32 || nb < 1) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_gelu_quant, dim3((n_ff / 4 + 255) / 256, nb), dim3(256), 0, s, gu, n_ff, tab, act, ast);
+hipError_t launch_gelu_quant(const float *gu, int n_ff, const uint16_t *tab, uint8_t *act, hipStream_t s, int nb, size_t ast,
+                             float *hout, size_t hs) {
+    if (n_ff % 32 || nb < 1 || (hout && ((uintptr_t)hout % 16 || hs % 4))) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_gelu_quant, dim3((n_ff / 4 + 255) / 256, nb), dim3(256), 0, s, gu, n_ff, tab, act, ast, hout, hs);
     return hipGetLastError();
 }
 hipError_t launch_argmax_rows(const float *logits, int n, int nb, int *out, hipStream_t s) {

@@ -98,8 +98,9 @@ hipError_t launch_embed_norm(const g4h_tensor &head, const int *token, float *x,
                              uint8_t *act, hipStream_t s, int nb = 1, size_t ast = 0);
 hipError_t launch_norm_quant(float *x, const float *delta, const float *w_post, const float *w_pre, float eps, int n,
                              uint8_t *act, hipStream_t s, int nb = 1, size_t ast = 0, float *y = nullptr);
+// hout (optional): the h rows themselves, hs floats apart (16-byte aligned)
 hipError_t launch_gelu_quant(const float *gu, int n_ff, const uint16_t *tab, uint8_t *act, hipStream_t s, int nb = 1,
-                             size_t ast = 0);
+                             size_t ast = 0, float *hout = nullptr, size_t hs = 0);
 // out[b] = first index of the maximum of row b of logits [nb][n] (16-byte
 // aligned rows)
 hipError_t launch_argmax_rows(const float *logits, int n, int nb, int *out, hipStream_t s);

@@ -501,15 +501,25 @@ static int batch_alloc(g4h_model *m) {
     return G4H_OK;
 }
 
-// forward_layers (model.c:592-736) for nb tokens at positions pos0 .. pos0+nb-1:
-// every row takes exactly the arithmetic of the decode step (the GEMV family
-// for every projection, whose token rows are bit-identical for any token
-// count; the decode step's q/k/v preparation for every token, K/V rows stored
-// at pos0 .. pos0 + nb - 1 before token b attends 0 .. pos0 + b with the
-// decode attention's arithmetic), so row b equals
-// the decode step of tokens[b] at pos0 + b after tokens[0 .. b-1] bit for
-// bit.  Leaves the residual rows in bx and the last Wdown output in bxb.
-static int forward_rows(g4h_model *m, const int *tokens, int nb, int pos0, hipStream_t s) {
+// floats of one step's trace record per layer, and of the whole step's trace
+static size_t trace_rec_floats(const g4h_model_config &c) {
+    return 4 * (size_t)c.n_embd + (size_t)(c.n_head + 2 * c.n_kv) * c.head_dim + (size_t)c.n_head * c.head_dim + c.n_ff;
+}
+static size_t trace_step_floats(const g4h_model_config &c) { return (size_t)c.n_layer * trace_rec_floats(c) + c.n_embd; }
+
+// forward_layers (model.c:592-736) for nb tokens at positions pos0 .. pos0+nb-1.
+// Attention and the row steps take the decode step's arithmetic (its q/k/v
+// preparation for every token, K/V rows stored at pos0 .. pos0 + nb - 1
+// before token b attends 0 .. pos0 + b).  The projections run on kernel family
+// `path` of g4h_matmul_ex: 1, the GEMV family of the decode step, makes row b
+// equal the decode step of tokens[b] at pos0 + b after tokens[0 .. b-1] bit
+// for bit (what speculative verify compares); 0 lets a prompt chunk of 9 or
+// more q8_0 / q4_0 tokens read each weight once on the int8 matrix cores, whose
+// rows agree with the decode step within the fp32 tolerance instead.  With a
+// trace (g4h_model_trace) each token's per-layer record and final x are copied
+// out as the decode step's are, token b's at b times a step's trace size.
+// Leaves the residual rows in bx and the last Wdown output in bxb.
+static int forward_rows(g4h_model *m, const int *tokens, int nb, int pos0, hipStream_t s, int path) {
     const g4h_model_config &c = m->c;
     if (nb < 1 || nb > kBatchMax) return g4h_internal_fail(G4H_ERR_ARG, "g4h_forward_batch: nb must be 1..64 (G4_BATCH_MAX)");
     if (pos0 < 0 || pos0 + nb > c.n_ctx) return g4h_internal_fail(G4H_ERR_ARG, "g4h_forward_batch: positions outside the context");
@@ -520,13 +530,25 @@ static int forward_rows(g4h_model *m, const int *tokens, int nb, int pos0, hipSt
     const int E = c.n_embd, H = c.n_head, KV = c.n_kv, hd = c.head_dim, F = c.n_ff;
     const int R = (H + 2 * KV) * hd, Q = H * hd;
     const size_t ast = m->act_bytes;
+    // trace: the decode step's record (x | qkv | att | wo | xmid | h | down) per
+    // layer, then the final x; token b's trace starts at b * tf floats
+    const size_t TR_QKV = E, TR_ATT = TR_QKV + R, TR_WO = TR_ATT + Q, TR_XMID = TR_WO + E, TR_H = TR_XMID + E,
+                 TR_DOWN = TR_H + F, rec = TR_DOWN + E, tf = trace_step_floats(c);
+    auto trace_rows = [&](int l, size_t off, const float *src, size_t src_stride, int n) -> int {
+        if (!m->trace) return G4H_OK;
+        M_HIP(hipMemcpy2DAsync(m->trace + (size_t)l * rec + off, tf * 4, src, src_stride * 4, (size_t)n * 4, nb,
+                               hipMemcpyDeviceToDevice, s));
+        return G4H_OK;
+    };
     M_HIP(hipMemcpyAsync(m->btok, tokens, (size_t)nb * sizeof(int), hipMemcpyHostToDevice, s));
     M_HIP(launch_embed_norm(*m->head, m->btok, m->bx, sqrtf((float)E), norm_of(m, 0, G4H_N_ATTN), c.rms_eps, m->bact, s, nb, ast));
     for (int l = 0; l < c.n_layer; l++) {
         if (l)
             M_HIP(launch_norm_quant(m->bx, m->bxb, norm_of(m, l - 1, G4H_N_POST_FFW), norm_of(m, l, G4H_N_ATTN), c.rms_eps, E,
                                     m->bact, s, nb, ast));
-        M_RC(g4h_matmul_ex(m->wqkv[l], nullptr, m->bact, ast, m->bqkv, nb, 1, s));
+        M_RC(trace_rows(l, 0, m->bx, E, E));
+        M_RC(g4h_matmul_ex(m->wqkv[l], nullptr, m->bact, ast, m->bqkv, nb, path, s));
+        M_RC(trace_rows(l, TR_QKV, m->bqkv, R, R));
         QkvArgs qa;
         qa.n_head = H;
         qa.n_kv = KV;
@@ -548,12 +570,17 @@ static int forward_rows(g4h_model *m, const int *tokens, int nb, int pos0, hipSt
                 M_HIP(launch_attn_decode(nullptr, m->bqkv + (size_t)b * R, qa, pos0 + b + 1, nullptr, c.n_ctx,
                                          m->batt + (size_t)b * Q, m->bact + (size_t)b * ast, m->bws, s));
         }
-        M_RC(g4h_matmul_ex(m->wo[l], nullptr, m->bact, ast, m->bxb, nb, 1, s));
+        M_RC(trace_rows(l, TR_ATT, m->batt, Q, Q));
+        M_RC(g4h_matmul_ex(m->wo[l], nullptr, m->bact, ast, m->bxb, nb, path, s));
+        M_RC(trace_rows(l, TR_WO, m->bxb, E, E));
         M_HIP(launch_norm_quant(m->bx, m->bxb, norm_of(m, l, G4H_N_POST_ATTN), norm_of(m, l, G4H_N_FFN), c.rms_eps, E, m->bact,
                                 s, nb, ast));
-        M_RC(g4h_matmul_ex(m->wgu[l], nullptr, m->bact, ast, m->bff, nb, 1, s));
-        M_HIP(launch_gelu_quant(m->bff, F, m->gelu, m->bact, s, nb, ast));
-        M_RC(g4h_matmul_ex(m->wdown[l], nullptr, m->bact, ast, m->bxb, nb, 1, s));
+        M_RC(trace_rows(l, TR_XMID, m->bx, E, E));
+        M_RC(g4h_matmul_ex(m->wgu[l], nullptr, m->bact, ast, m->bff, nb, path, s));
+        M_HIP(launch_gelu_quant(m->bff, F, m->gelu, m->bact, s, nb, ast, m->trace ? m->trace + (size_t)l * rec + TR_H : nullptr,
+                                tf));
+        M_RC(g4h_matmul_ex(m->wdown[l], nullptr, m->bact, ast, m->bxb, nb, path, s));
+        M_RC(trace_rows(l, TR_DOWN, m->bxb, E, E));
     }
     return G4H_OK;
 }
@@ -562,12 +589,15 @@ extern "C" int g4h_forward_batch(g4h_model *m, const int *tokens, int nb, int po
     if (!m) return g4h_internal_fail(G4H_ERR_ARG, "g4h_forward_batch: null model");
     const hipStream_t s = (hipStream_t)stream;
     const g4h_model_config &c = m->c;
-    M_RC(forward_rows(m, tokens, nb, pos0, s));
+    M_RC(forward_rows(m, tokens, nb, pos0, s, 0));
     if (want_logits) {
         // head of the last token only (model.c:760-769)
         const size_t E = c.n_embd, last = (size_t)(nb - 1) * E;
         M_HIP(launch_norm_quant(m->bx + last, m->bxb + last, norm_of(m, c.n_layer - 1, G4H_N_POST_FFW), norm_of(m, c.n_layer, 0),
                                 c.rms_eps, c.n_embd, m->bact, s));
+        if (m->trace)                                        // the last token's final x
+            M_HIP(hipMemcpyAsync(m->trace + (size_t)(nb - 1) * trace_step_floats(c) + (size_t)c.n_layer * trace_rec_floats(c),
+                                 m->bx + last, E * 4, hipMemcpyDeviceToDevice, s));
         M_RC(g4h_matmul_ex(m->head, nullptr, m->bact, m->act_bytes, m->logits, 1, 1, s));
     }
     M_HIP(hipStreamSynchronize(s));
@@ -581,10 +611,13 @@ extern "C" int g4h_forward_batch_heads(g4h_model *m, const int *tokens, int nb, 
         return g4h_internal_fail(G4H_ERR_ARG, "g4h_forward_batch_heads: outputs must be 16-byte aligned");
     const hipStream_t s = (hipStream_t)stream;
     const g4h_model_config &c = m->c;
-    M_RC(forward_rows(m, tokens, nb, pos0, s));
+    M_RC(forward_rows(m, tokens, nb, pos0, s, 1));
     // every position's head input feature and logits (model.c:790-793)
     M_HIP(launch_norm_quant(m->bx, m->bxb, norm_of(m, c.n_layer - 1, G4H_N_POST_FFW), norm_of(m, c.n_layer, 0), c.rms_eps,
                             c.n_embd, m->bact, s, nb, m->act_bytes, hnext_dev ? hnext_dev : m->bhn));
+    if (m->trace)                                            // every token's final x
+        M_HIP(hipMemcpy2DAsync(m->trace + (size_t)c.n_layer * trace_rec_floats(c), trace_step_floats(c) * 4, m->bx,
+                               (size_t)c.n_embd * 4, (size_t)c.n_embd * 4, nb, hipMemcpyDeviceToDevice, s));
     M_RC(g4h_matmul_ex(m->head, nullptr, m->bact, m->act_bytes, logits_dev, nb, 1, s));
     M_HIP(hipStreamSynchronize(s));
     return G4H_OK;

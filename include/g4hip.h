@@ -308,7 +308,10 @@ const float *g4h_model_logits(const g4h_model *m);
  * chaotic at the ulp level (the fp16 rounding of q ahead of the unscaled
  * softmax, model.c:530-538, turns a last-bit difference of the projection into
  * a visible change of the attention output), so only such part-by-part checks
- * hold a per-element tolerance.  NULL turns it off. */
+ * hold a per-element tolerance.  The batched forwards write one such step
+ * trace per token (token b's at b times a step's size, so trace_dev must hold
+ * nb of them; g4h_forward_batch writes the final x of its last token only).
+ * NULL turns it off. */
 int g4h_model_trace(g4h_model *m, float *trace_dev);
 /* The model's fp16 GELU table (65536 codes, device memory): entry h =
  * fp16(gelu_tanh(fp32(h))) as quants.c:48-58 builds g4_gelu_table. */
@@ -325,14 +328,19 @@ size_t      g4h_model_weight_bytes(const g4h_model *m);
 /* g4_forward_batch (g4run.h:312-313, model.c:758-776): the layers for nb
  * tokens (host ids, 1 <= nb <= 64 = G4_BATCH_MAX) at positions pos0 ..
  * pos0+nb-1 (< n_ctx), their K/V rows stored; with want_logits the last
- * token's logits go to g4h_model_logits.  Synchronous.  Row b is computed
- * with exactly the decode step's arithmetic, so the logits equal those of
- * decoding tokens[0..nb-1] one by one, bit for bit.  The decode state
- * (g4h_model_set_state) is not touched. */
+ * token's logits go to g4h_model_logits.  Synchronous.  A prompt chunk:
+ * attention and the row steps take the decode step's arithmetic, and the
+ * projections the kernel family g4h_matmul_path picks for nb tokens -- from 9
+ * tokens on q8_0 / q4_0 weights stream once through the int8 matrix cores, so
+ * rows agree with decoding the tokens one by one within the fp32 tolerance
+ * (below 9, bit for bit).  The decode state (g4h_model_set_state) is not
+ * touched. */
 int g4h_forward_batch(g4h_model *m, const int *tokens, int nb, int pos0, int want_logits, void *stream);
 /* g4_forward_batch_heads (model.c:780-799), the speculative-decoding verify
- * batch (main.c:383-397): the same layers, then every position's head:
- * logits_dev [nb][n_vocab] and, if hnext_dev, the head's input feature
+ * batch (main.c:383-397): the same layers with every projection on the decode
+ * step's GEMV family, so row b's logits equal those of decoding tokens[0..b]
+ * one by one, bit for bit; then every position's head: logits_dev
+ * [nb][n_vocab] and, if hnext_dev, the head's input feature
  * rms(x)*output_norm [nb][n_embd] (device, 16-byte aligned).  Synchronous. */
 int g4h_forward_batch_heads(g4h_model *m, const int *tokens, int nb, int pos0, float *logits_dev, float *hnext_dev,
                             void *stream);
