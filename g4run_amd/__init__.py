@@ -128,6 +128,8 @@ _SIGS = [
     ("g4h_gemma_info", _int, [_vp, C.POINTER(_int), C.POINTER(_int), C.POINTER(_int), C.POINTER(_int)]),
     ("g4h_gemma_forward", _int, [_vp, C.POINTER(_int), _int, _int, _vp, _vp, _vp]),
     ("g4h_read_floor", _int, [_vp, _sz, _vp, C.c_int64, _int, _int, _vp]),
+    ("g4h_gemma_trace", _int, [_vp, _vp, C.POINTER(_sz)]),
+    ("g4h_gemma_kv", _int, [_vp, _int, C.POINTER(_vp), C.POINTER(_vp), C.POINTER(_sz)]),
 ]
 
 _lib = None
@@ -493,6 +495,24 @@ class Gemma:
         L, Hn = Buffer(nb * self.n_vocab * 4), Buffer(nb * self.n_embd * 4)
         check(lib().g4h_gemma_forward(self.ptr, t.ctypes.data_as(C.POINTER(_int)), nb, pos0, L.ptr, Hn.ptr, stream))
         return L.download(np.float32, (nb, self.n_vocab)), Hn.download(np.float32, (nb, self.n_embd))
+
+    def trace(self, buf) -> int:
+        """Per-token intermediate vectors of later forwards into buf (None: off);
+        returns the floats per token (g4h_gemma_trace)."""
+        n = _sz()
+        check(lib().g4h_gemma_trace(self.ptr, _p(buf) if buf is not None else None, C.byref(n)))
+        return n.value
+
+    def kv(self, layer: int):
+        """(K bytes, V bytes) of a layer's cache as numpy uint8 (host copies)."""
+        k, v, n = _vp(), _vp(), _sz()
+        check(lib().g4h_gemma_kv(self.ptr, layer, C.byref(k), C.byref(v), C.byref(n)))
+        out = []
+        for p in (k, v):
+            a = np.empty(n.value, np.uint8)
+            check(lib().g4h_memcpy_d2h(a.ctypes.data_as(_vp), p.value, a.nbytes, None))
+            out.append(a)
+        return out
 
     def free(self) -> None:
         if getattr(self, "ptr", None):

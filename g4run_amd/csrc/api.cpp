@@ -50,6 +50,23 @@ static std::atomic<int> g_fail_alloc{0};
 extern "C" const char *g4h_last_error(void) { return g_err; }
 // status + message for the library's other host files (not part of the ABI)
 extern "C" int g4h_internal_fail(int status, const char *msg) { return fail(status, "%s", msg); }
+// After a synchronised call that ran one-launch attention on workspace ws: the
+// error word a bounded hand-off wait sets when it gives up (the outputs are
+// then NaN) is read, cleared and reported as G4H_ERR_TIMEOUT.  The workspace
+// is then cleared before its next use: a workgroup that started after the
+// launch's last one advanced the epoch took the next launch's tag, and its
+// words must not be read as that launch's.
+extern "C" int g4h_internal_attn_error(void *ws, void *stream, const char *fn) {
+    const hipStream_t s = (hipStream_t)stream;
+    unsigned err = 0;
+    G4_HIP(hipMemcpyAsync(&err, (uint8_t *)ws + ATTN_ERR_OFFSET, sizeof err, hipMemcpyDeviceToHost, s));
+    G4_HIP(hipStreamSynchronize(s));
+    if (!err) return G4H_OK;
+    G4_HIP(hipMemsetAsync((uint8_t *)ws + ATTN_ERR_OFFSET, 0, sizeof err, s));
+    G4_HIP(hipStreamSynchronize(s));
+    attn_ws_forget(ws);
+    return fail(G4H_ERR_TIMEOUT, "%s: an attention hand-off wait gave up; the outputs are NaN", fn);
+}
 
 extern "C" const char *g4h_status_str(int s) {
     switch (s) {
@@ -643,7 +660,11 @@ static int check_attn_shape(const char *fn, int kv_type, int n_head, int n_kv, i
     if (n_kv <= 0 || n_head <= 0 || n_head % n_kv) return fail(G4H_ERR_SHAPE, "%s: n_head=%d not a multiple of n_kv=%d", fn, n_head, n_kv);
     const int grp = n_head / n_kv;
     if (grp != 1 && grp != 2 && grp != 4 && grp != 8) return fail(G4H_ERR_SHAPE, "%s: group size %d unsupported", fn, grp);
-    if (hd % 64 || hd > 256) return fail(G4H_ERR_SHAPE, "%s: hd=%d (must be a multiple of 64, at most 256)", fn, hd);
+    if (hd == 512) {                         // gemma4's full-attention heads: one KV head (model.c:443-444)
+        if (n_kv != 1) return fail(G4H_ERR_SHAPE, "%s: hd=512 takes one KV head (n_kv=%d)", fn, n_kv);
+        return G4H_OK;
+    }
+    if (hd % 64 || hd > 256) return fail(G4H_ERR_SHAPE, "%s: hd=%d (must be a multiple of 64 up to 256, or 512)", fn, hd);
     return G4H_OK;
 }
 
@@ -652,7 +673,7 @@ extern "C" int g4h_attn_passes(int kv_type, int n_head, int n_kv, int hd, int n_
     if (!passes) return fail(G4H_ERR_ARG, "g4h_attn_passes: null pointer");
     if (int rc = check_attn_shape("g4h_attn_passes", kv_type, n_head, n_kv, hd)) return rc;
     if (n_pos <= 0) return fail(G4H_ERR_ARG, "g4h_attn_passes: n_pos=%d", n_pos);
-    *passes = attn_fused_fits(kv_type, n_head, n_kv, hd, n_pos) ? 1 : 3;
+    *passes = hd == 512 ? 6 : attn_fused_fits(kv_type, n_head, n_kv, hd, n_pos) ? 1 : 3;   // 512: halves, joined
     return G4H_OK;
 }
 
@@ -717,6 +738,7 @@ extern "C" int g4h_attn_status(void *ws, int *failed, void *stream) {
     if (err) {
         G4_HIP(hipMemsetAsync((uint8_t *)ws + ATTN_ERR_OFFSET, 0, sizeof err, s));
         G4_HIP(hipStreamSynchronize(s));
+        attn_ws_forget(ws);                  // cleared before its next use (g4h_internal_attn_error)
     }
     return G4H_OK;
 }

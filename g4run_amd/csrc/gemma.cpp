@@ -26,6 +26,7 @@
 using namespace g4;
 
 extern "C" int g4h_internal_fail(int status, const char *msg);
+extern "C" int g4h_internal_attn_error(void *ws, void *stream, const char *fn);
 
 namespace {
 constexpr int kRows = 64;          // G4_BATCH_MAX (g4run.h:23)
@@ -57,6 +58,7 @@ struct g4h_gemma {
           *u = nullptr, *pl = nullptr, *plp = nullptr, *plg = nullptr, *hn = nullptr;
     uint8_t *ws = nullptr, *bws = nullptr;     // decode attention / batch attention workspaces
     uint16_t *gelu = nullptr;
+    float *trace = nullptr;                    // optional per-token trace (g4h_gemma_trace)
     std::vector<void *> allocs;
     std::vector<g4h_tensor *> tensors;
 };
@@ -127,7 +129,7 @@ std::vector<float> rope_table(int n_ctx, int hd, float base, const float *ff) {
     return t;
 }
 
-bool attn_hd(int hd) { return hd == 64 || hd == 128 || hd == 192 || hd == 256; }
+bool attn_hd(int hd) { return hd == 64 || hd == 128 || hd == 192 || hd == 256 || hd == 512; }
 
 int create(const g4_model_file *mf, int n_ctx, int kv_type, g4h_gemma *m) {
     if (std::strcmp(mf->arch, "gemma4") != 0) return gfail(G4H_ERR_TYPE, "g4h_gemma_create: architecture %s is not gemma4", mf->arch);
@@ -149,7 +151,7 @@ int create(const g4_model_file *mf, int n_ctx, int kv_type, g4h_gemma *m) {
     if (m->n_layer < 1 || m->n_layer_kv < 2 || m->E <= 0 || m->V <= 0 || m->PE <= 0 || n_ctx <= 0)
         return gfail(G4H_ERR_SHAPE, "g4h_gemma_create: bad dimensions");
     if (!attn_hd(m->hd_full) || !attn_hd(m->hd_swa))
-        return gfail(G4H_ERR_SHAPE, "g4h_gemma_create: head dims must be 64, 128, 192 or 256 (the attention kernels' rows)");
+        return gfail(G4H_ERR_SHAPE, "g4h_gemma_create: head dims must be 64, 128, 192, 256 or 512 (the attention kernels' rows)");
     if (mf->n_rot_full != m->hd_full || mf->n_rot_swa != m->hd_swa)
         return gfail(G4H_ERR_SHAPE, "g4h_gemma_create: RoPE must cover the whole head (n_rot == head dim)");
     if (m->H != 1 && m->H != 2 && m->H != 4 && m->H != 8)
@@ -233,6 +235,18 @@ int create(const g4_model_file *mf, int n_ctx, int kv_type, g4h_gemma *m) {
         if (L.n_ff % 4) return gfail(G4H_ERR_SHAPE, "g4h_gemma_create: FFN width % 4");
     }
     m->hd_max = std::max(m->hd_full, m->hd_swa);
+    // layers past n_layer_kv read the cache of layer n_layer_kv - 2 (sliding) or
+    // n_layer_kv - 1 (full) (model.c:692): that layer must be of the same kind,
+    // so its cache holds rows of the width and the slot count the reader assumes
+    for (int il = m->n_layer_kv; il < m->n_layer; il++) {
+        const GLayer &L = m->L[il];
+        const int cil = L.swa ? m->n_layer_kv - 2 : m->n_layer_kv - 1;
+        if (cil < 0 || m->L[cil].swa != L.swa || m->L[cil].hd != L.hd) {
+            char msg[160];
+            snprintf(msg, sizeof msg, "g4h_gemma_create: shared-KV layer %d would read layer %d's cache of another kind", il, cil);
+            return g4h_internal_fail(G4H_ERR_SHAPE, msg);
+        }
+    }
     // KV caches: sliding layers a ring of kRing slots stored twice, full layers n_ctx slots
     for (int il = 0; il < m->n_layer_kv; il++) {
         const GLayer &L = m->L[il];
@@ -260,10 +274,12 @@ int create(const g4_model_file *mf, int n_ctx, int kv_type, g4h_gemma *m) {
     G_RC(galloc(m, (void **)&m->pl, B * NPL * 4));
     G_RC(galloc(m, (void **)&m->plp, B * NPL * 4));
     G_RC(galloc(m, (void **)&m->plg, B * m->PE * 4));
-    const size_t wsb = g4h_attn_workspace_bytes(m->H, m->hd_max, n_ctx);
+    // 512-wide heads take another layout than the 256-wide ones: the larger of the two
+    const size_t wsb = std::max(g4h_attn_workspace_bytes(m->H, m->hd_full, n_ctx), g4h_attn_workspace_bytes(m->H, m->hd_swa, n_ctx));
     G_RC(galloc(m, (void **)&m->ws, wsb));
     G_HIP(hipMemset(m->ws, 0, wsb));
-    G_RC(galloc(m, (void **)&m->bws, attn_batch_workspace_bytes(m->H, m->hd_max, n_ctx, kRows)));
+    G_RC(galloc(m, (void **)&m->bws, std::max(attn_batch_workspace_bytes(m->H, m->hd_full, n_ctx, kRows),
+                                              attn_batch_workspace_bytes(m->H, m->hd_swa, n_ctx, kRows))));
     std::vector<uint16_t> gt(65536);
     for (uint32_t h = 0; h < 65536; h++) gt[h] = gelu_table_entry((uint16_t)h);
     G_RC(galloc(m, (void **)&m->gelu, 65536 * 2));
@@ -278,7 +294,34 @@ int mm(const g4h_tensor *W, const float *x, float *Y, int nb, hipStream_t s) {
     return g4h_matmul_ex(W, x, nullptr, 0, Y, nb, 1, s);
 }
 
+// floats of one token's trace: the per-layer inputs, n_layer records of
+// x | q | k | v | att | wo | xmid | g | u | h | down | xffn | plg | plh | proj
+// (q and att H * hd_max, k and v hd_max, g | u | h the widest FFN, plg | plh the
+// per-layer width, the rest n_embd), then the final x
+size_t gemma_trace_floats(const g4h_gemma *m) {
+    const size_t E = m->E, Qm = (size_t)m->H * m->hd_max, Fm = m->max_ff, PE = m->PE;
+    const size_t rec = 6 * E + 2 * Qm + 2 * (size_t)m->hd_max + 3 * Fm + 2 * PE;
+    return (size_t)m->n_layer * PE + (size_t)m->n_layer * rec + E;
+}
+
 }  // namespace
+
+extern "C" int g4h_gemma_trace(g4h_gemma *m, float *trace_dev, size_t *floats_per_token) {
+    if (!m) return g4h_internal_fail(G4H_ERR_ARG, "g4h_gemma_trace: null model");
+    m->trace = trace_dev;
+    if (floats_per_token) *floats_per_token = gemma_trace_floats(m);
+    return G4H_OK;
+}
+
+extern "C" int g4h_gemma_kv(g4h_gemma *m, int layer, void **k_dev, void **v_dev, size_t *bytes) {
+    if (!m || layer < 0 || layer >= m->n_layer_kv) return g4h_internal_fail(G4H_ERR_ARG, "g4h_gemma_kv: bad layer");
+    const GLayer &L = m->L[layer];
+    const size_t row = m->kv_type == G4H_F16 ? (size_t)L.hd * 2 : g4h_row_size(m->kv_type, L.hd);
+    if (k_dev) *k_dev = m->kc[layer];
+    if (v_dev) *v_dev = m->vc[layer];
+    if (bytes) *bytes = row * (L.swa ? 2 * kRing : (size_t)m->n_ctx);
+    return G4H_OK;
+}
 
 extern "C" int g4h_gemma_free(g4h_gemma *m) {
     if (!m) return G4H_OK;
@@ -328,6 +371,20 @@ extern "C" int g4h_gemma_forward(g4h_gemma *m, const int *tokens, int nb, int po
     const hipStream_t s = (hipStream_t)stream;
     const int E = m->E, H = m->H, PE = m->PE, NPL = m->n_layer * PE;
     const float eps = m->eps;
+    // per-token trace (g4h_gemma_trace): pl, then per layer the record below, then the final x
+    const size_t Qm = (size_t)H * m->hd_max, Fm = m->max_ff;
+    const size_t T_X = 0, T_Q = E, T_K = T_Q + Qm, T_V = T_K + m->hd_max, T_ATT = T_V + m->hd_max, T_WO = T_ATT + Qm,
+                 T_XMID = T_WO + E, T_G = T_XMID + E, T_U = T_G + Fm, T_H = T_U + Fm, T_DOWN = T_H + Fm, T_XFFN = T_DOWN + E,
+                 T_PLG = T_XFFN + E, T_PLH = T_PLG + PE, T_PROJ = T_PLH + PE, rec = T_PROJ + E;
+    const size_t tf = gemma_trace_floats(m);
+    auto tr = [&](size_t off, const float *src, size_t stride, size_t n) -> int {
+        if (!m->trace) return G4H_OK;
+        G_HIP(hipMemcpy2DAsync(m->trace + off, tf * 4, src, stride * 4, n * 4, nb, hipMemcpyDeviceToDevice, s));
+        return G4H_OK;
+    };
+    auto trl = [&](int il, size_t off, const float *src, size_t stride, size_t n) {
+        return tr((size_t)NPL + (size_t)il * rec + off, src, stride, n);
+    };
 
     // embeddings and per-layer token rows (model.c:602-615)
     for (int b = 0; b < nb; b++) {
@@ -340,13 +397,16 @@ extern "C" int g4h_gemma_forward(g4h_gemma *m, const int *tokens, int nb, int po
     // per-layer input projection (model.c:617-635)
     G_RC(mm(m->ple_proj, m->x, m->plp, nb, s));
     G_HIP(launch_ple_prep(m->plp, m->pl, m->ple_norm, PE, m->n_layer, nb, 1.0f / sqrtf((float)E), 1.0f / sqrtf(2.0f), eps, s));
+    G_RC(tr(0, m->pl, NPL, NPL));
 
     for (int il = 0; il < m->n_layer; il++) {
         const GLayer &L = m->L[il];
         const int hd = L.hd, nq = H * hd, F = L.n_ff;
         const float *rope = L.swa ? m->rope_swa : m->rope_full;
+        G_RC(trl(il, T_X, m->x, E, E));
         G_HIP(launch_rms_rows(m->x, L.attn_norm, m->xb, E, nb, eps, s));
         G_RC(mm(L.wq, m->xb, m->q, nb, s));
+        G_RC(trl(il, T_Q, m->q, nq, nq));
         QkvArgs qa;
         qa.n_head = H;
         qa.n_kv = 1;
@@ -363,12 +423,17 @@ extern "C" int g4h_gemma_forward(g4h_gemma *m, const int *tokens, int nb, int po
             // own K/V: q | k | v prepared, stored at the position and attended in one step (model.c:664-689)
             G_RC(mm(L.wk, m->xb, m->k, nb, s));
             if (L.wv) G_RC(mm(L.wv, m->xb, m->v, nb, s));
+            G_RC(trl(il, T_K, m->k, hd, hd));
+            if (L.wv) G_RC(trl(il, T_V, m->v, hd, hd));
             G_HIP(launch_pack_qkv(m->q, m->k, L.wv ? m->v : nullptr, m->qkv, nq, hd, nb, s));
             qa.kc = m->kc[il];
             qa.vc = m->vc[il];
             if (nb > 1) {                                            // every row stored, then the batch attends
                 G_HIP(launch_attn_prep_rows(m->qkv, qa, pos0, nb, m->q, s));
                 G_HIP(launch_attn_batch(m->q, qa, pos0 + 1, nb, m->att, nullptr, m->bws, s));
+            } else if (hd == 512) {                                  // wide heads: rows prepared first, then the halves attend
+                G_HIP(launch_attn_prep_rows(m->qkv, qa, pos0, 1, m->q, s));
+                G_HIP(launch_attn_decode(m->q, nullptr, qa, pos0 + 1, nullptr, npos_max, m->att, nullptr, m->ws, s));
             } else {
                 G_HIP(launch_attn_decode(nullptr, m->qkv, qa, pos0 + 1, nullptr, npos_max, m->att, nullptr, m->ws, s));
             }
@@ -381,26 +446,38 @@ extern "C" int g4h_gemma_forward(g4h_gemma *m, const int *tokens, int nb, int po
             if (nb > 1) G_HIP(launch_attn_batch(m->q, qa, pos0 + 1, nb, m->att, nullptr, m->bws, s));
             else G_HIP(launch_attn_decode(m->q, nullptr, qa, pos0 + 1, nullptr, npos_max, m->att, nullptr, m->ws, s));
         }
+        G_RC(trl(il, T_ATT, m->att, nq, nq));
         G_RC(mm(L.wo, m->att, m->xb, nb, s));
+        G_RC(trl(il, T_WO, m->xb, E, E));
         G_HIP(launch_resid(m->x, m->xb, L.post_attn_norm, E, nb, eps, 1.0f, s));
+        G_RC(trl(il, T_XMID, m->x, E, E));
         // FFN (model.c:718-736)
         G_HIP(launch_rms_rows(m->x, L.ffn_norm, m->xb, E, nb, eps, s));
         G_RC(mm(L.gate, m->xb, m->g, nb, s));
         G_RC(mm(L.up, m->xb, m->u, nb, s));
+        G_RC(trl(il, T_G, m->g, F, F));
+        G_RC(trl(il, T_U, m->u, F, F));
         G_HIP(launch_gelu_mul(m->g, F, m->u, F, F, nb, m->gelu, s));
+        G_RC(trl(il, T_H, m->g, F, F));
         G_RC(mm(L.down, m->g, m->xb, nb, s));
+        G_RC(trl(il, T_DOWN, m->xb, E, E));
         G_HIP(launch_resid(m->x, m->xb, L.post_ffw_norm, E, nb, eps, 1.0f, s));
+        G_RC(trl(il, T_XFFN, m->x, E, E));
         // per-layer embedding injection (model.c:738-752)
         G_RC(mm(L.inp_gate, m->x, m->plg, nb, s));
+        G_RC(trl(il, T_PLG, m->plg, PE, PE));
         G_HIP(launch_gelu_mul(m->plg, PE, m->pl + (size_t)il * PE, NPL, PE, nb, m->gelu, s));
+        G_RC(trl(il, T_PLH, m->plg, PE, PE));
         G_RC(mm(L.proj, m->plg, m->xb, nb, s));
+        G_RC(trl(il, T_PROJ, m->xb, E, E));
         G_HIP(launch_resid(m->x, m->xb, L.post_norm, E, nb, eps, L.out_scale, s));
     }
+    G_RC(tr((size_t)NPL + (size_t)m->n_layer * rec, m->x, E, E));
     // every position's head (model.c:790-798)
     float *hn = hnext_dev ? hnext_dev : m->hn;
     G_HIP(launch_rms_rows(m->x, m->out_norm, hn, E, nb, eps, s));
     G_RC(mm(m->head, hn, logits_dev, nb, s));
     if (m->softcap > 0) G_HIP(launch_softcap(logits_dev, (int64_t)nb * m->V, m->softcap, s));
     G_HIP(hipStreamSynchronize(s));
-    return G4H_OK;
+    return g4h_internal_attn_error(m->ws, s, "g4h_gemma_forward");
 }

@@ -46,6 +46,8 @@
 namespace g4 {
 
 constexpr int ATT_CHUNK = 128;       // positions per score / V workgroup
+constexpr int ATT_WIDE = 512;        // gemma4's full-attention head width (one KV head), run as two halves
+constexpr int ATT_HALF = 256;
 constexpr int ATT_CSUM = 8;          // chunks per group in the combine's two-level sum
 // one-launch form: V loads per lane issued while K is scored; the rest are
 // issued after the statistics hand-off
@@ -67,42 +69,48 @@ __device__ __forceinline__ double wave_sum_d(double v) { return group_sum_t<64>(
 
 // ------------------------------------------------------- row preparation --
 // One projection row handled by one wave, lane holding hd/64 consecutive
-// elements (<= 4): the loads are issued by prep_load, the arithmetic by
-// prep_finish (RMSNorm in double, weight, NeoX rotation of (i, i + hd/2) whose
-// partner is 32 lanes away), as in model.c:338-367.
-struct PrepRow {
-    float v[4], w[4];
+// elements (<= N: 4 for rows up to 256, 8 for the 512-wide heads): the loads
+// are issued by prep_load, the arithmetic by prep_finish (RMSNorm in double,
+// weight, NeoX rotation of (i, i + hd/2) whose partner is 32 lanes away), as in
+// model.c:338-367.
+template <int N>
+struct PrepRowN {
+    float v[N], w[N];
 };
-__device__ __forceinline__ void prep_load(PrepRow &r, const float *src, const float *w, int hd) {
+using PrepRow = PrepRowN<4>;
+template <int N>
+__device__ __forceinline__ void prep_load(PrepRowN<N> &r, const float *src, const float *w, int hd) {
     const int lane = threadIdx.x & 63, epl = hd >> 6;
 #pragma unroll
-    for (int e = 0; e < 4; e++) {
+    for (int e = 0; e < N; e++) {
         r.v[e] = e < epl ? src[lane * epl + e] : 0.0f;
         r.w[e] = e < epl && w ? w[lane * epl + e] : 1.0f;
     }
 }
-__device__ __forceinline__ void rope_load(float cs[4], float sn[4], const float *rope, int p, int hd) {
+template <int N>
+__device__ __forceinline__ void rope_load(float (&cs)[N], float (&sn)[N], const float *rope, int p, int hd) {
     const int lane = threadIdx.x & 63, epl = hd >> 6, half = hd >> 1;
 #pragma unroll
-    for (int e = 0; e < 4; e++) {
+    for (int e = 0; e < N; e++) {
         const int t = lane * epl + e, i = t < half ? t : t - half;
         cs[e] = e < epl ? rope[(size_t)p * hd + 2 * i] : 1.0f;
         sn[e] = e < epl ? rope[(size_t)p * hd + 2 * i + 1] : 0.0f;
     }
 }
-__device__ __forceinline__ void prep_finish(const PrepRow &r, bool weighted, bool rotate, const float cs[4], const float sn[4],
-                                            int hd, float eps, float y[4]) {
+template <int N>
+__device__ __forceinline__ void prep_finish(const PrepRowN<N> &r, bool weighted, bool rotate, const float (&cs)[N],
+                                            const float (&sn)[N], int hd, float eps, float (&y)[N]) {
     const int lane = threadIdx.x & 63, epl = hd >> 6;
     double ss = 0.0;
 #pragma unroll
-    for (int e = 0; e < 4; e++) ss += (double)r.v[e] * r.v[e];
+    for (int e = 0; e < N; e++) ss += (double)r.v[e] * r.v[e];
     const float sc = rms_scale(wave_sum_dd(ss), hd, eps);
 #pragma unroll
-    for (int e = 0; e < 4; e++) y[e] = weighted ? r.v[e] * sc * r.w[e] : r.v[e] * sc;
+    for (int e = 0; e < N; e++) y[e] = weighted ? r.v[e] * sc * r.w[e] : r.v[e] * sc;
     if (rotate) {
         const bool lo = lane < 32;
 #pragma unroll
-        for (int e = 0; e < 4; e++) {
+        for (int e = 0; e < N; e++) {
             if (e < epl) {                                           // uniform over the wave
                 const float other = partner<32>(y[e]);
                 const float a = lo ? y[e] : other, b = lo ? other : y[e];
@@ -112,27 +120,32 @@ __device__ __forceinline__ void prep_finish(const PrepRow &r, bool weighted, boo
     }
 }
 // a prepared row into a cache slot (f16 RNE, or q8_0 / q4_0 blocks via an LDS
-// row of 256 floats for this wave); the whole wave calls it
-__device__ __forceinline__ void cache_store(const float y[4], int kv_type, uint8_t *dst, int hd, float *wb) {
+// row of 64 N floats for this wave); the whole wave calls it
+template <int N>
+__device__ __forceinline__ void cache_store(const float (&y)[N], int kv_type, uint8_t *dst, int hd, float *wb) {
     const int lane = threadIdx.x & 63, epl = hd >> 6;
     if (kv_type == F16) {
 #pragma unroll
-        for (int e = 0; e < 4; e++)
+        for (int e = 0; e < N; e++)
             if (e < epl) ((uint16_t *)dst)[lane * epl + e] = f2h(y[e]);
         return;
     }
 #pragma unroll
-    for (int e = 0; e < 4; e++)
+    for (int e = 0; e < N; e++)
         if (e < epl) wb[lane * epl + e] = y[e];
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    const bool own = lane < hd / 4;
-    float o[4] = {0.f, 0.f, 0.f, 0.f};
-    if (own)
-        for (int k = 0; k < 4; k++) o[k] = wb[4 * lane + k];
-    if (kv_type == Q4_0) q4_store4(o, lane, own, dst);
-    else q8_store4(o, lane, own, dst);
+#pragma unroll
+    for (int k = 0; k < N / 4; k++) {                                // groups of 4 elements: lane + 64 k
+        const int gi = lane + 64 * k;
+        const bool own = gi < hd / 4;
+        float o[4] = {0.f, 0.f, 0.f, 0.f};
+        if (own)
+            for (int i = 0; i < 4; i++) o[i] = wb[4 * gi + i];
+        if (kv_type == Q4_0) q4_store4(o, gi, own, dst);
+        else q8_store4(o, gi, own, dst);
+    }
     __builtin_amdgcn_wave_barrier();
 }
 
@@ -1401,7 +1414,11 @@ static AttnWs attn_ws(int n_head, int hd, int npos_max) {
     return w;
 }
 
-size_t attn_workspace_bytes(int n_head, int hd, int npos_max) { return attn_ws(n_head, hd, npos_max).total; }
+size_t attn_batch_workspace_bytes(int n_head, int hd, int npos_max, int nb);
+size_t attn_workspace_bytes(int n_head, int hd, int npos_max) {
+    if (hd == ATT_WIDE) return attn_batch_workspace_bytes(n_head, hd, npos_max, 1);   // the wide form's layout
+    return attn_ws(n_head, hd, npos_max).total;
+}
 
 // The epoch word of calls without an external epoch sits at a fixed offset of
 // the workspace header, so that it survives changes of layout (the layout
@@ -1609,7 +1626,12 @@ static AttnBatchWs attn_batch_ws(int n_head, int hd, int npos_max) {
 // error word (offset 0) and the epoch word (offset 128) of a workspace shared
 // with the decode form keep their values.
 constexpr size_t ATT_BATCH_OFF = 256;
+// 512-wide heads run as twice the heads of 256 (attn_wide_go), plus the
+// half-major query and output rows
+static size_t wide_rows_bytes(int n_head, int nb) { return al256((size_t)nb * n_head * ATT_WIDE * 4); }
 size_t attn_batch_workspace_bytes(int n_head, int hd, int npos_max, int nb) {
+    if (hd == ATT_WIDE)
+        return ATT_BATCH_OFF + (size_t)nb * attn_batch_ws(2 * n_head, ATT_HALF, npos_max).tok + 2 * wide_rows_bytes(n_head, nb);
     return ATT_BATCH_OFF + (size_t)nb * attn_batch_ws(n_head, hd, npos_max).tok;
 }
 
@@ -1649,24 +1671,25 @@ static hipError_t attn_batch_go(AttnCtx c, int n_head, int n_kv, int npos0, int 
 // still attends.
 template <int HD>
 __global__ __launch_bounds__(256) void k_attn_prep_rows(QkvArgs a, const float *__restrict__ qkv, int pos0, float *__restrict__ qout) {
-    __shared__ float wb[4][256];                                     // q8_0 / q4_0 stores
+    constexpr int N = HD > 256 ? 8 : 4;                              // elements per lane held
+    __shared__ float wb[4][64 * N];                                  // q8_0 / q4_0 stores
     constexpr int epl = HD >> 6;
     const int b = blockIdx.x, kvh = blockIdx.y, wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int grp = a.n_head / a.n_kv, h0 = kvh * grp, p = pos0 + b;
     const float *src = qkv + (size_t)b * (a.n_head + 2 * a.n_kv) * HD;
     const size_t rb = a.kv_type == F16 ? (size_t)HD * 2 : (size_t)(HD / 32) * (a.kv_type == Q4_0 ? 18 : 34);
-    float cs[4], sn[4];
+    float cs[N], sn[N];
     rope_load(cs, sn, a.rope, p, HD);
     for (int r = wave; r < grp + 2; r += 4) {                        // uniform over the wave
         const int src_row = r < grp ? h0 + r : r == grp ? a.n_head + kvh : a.n_head + a.n_kv + kvh;
         const float *w = r < grp ? a.q_norm : r == grp ? a.k_norm : nullptr;
-        PrepRow pr;
+        PrepRowN<N> pr;
         prep_load(pr, src + (size_t)src_row * HD, w, HD);
-        float y[4];
+        float y[N];
         prep_finish(pr, r <= grp, r <= grp, cs, sn, HD, a.eps, y);
         if (r < grp) {
 #pragma unroll
-            for (int e = 0; e < 4; e++)
+            for (int e = 0; e < N; e++)
                 if (e < epl) qout[((size_t)b * a.n_head + h0 + r) * HD + lane * epl + e] = y[e];
         } else {
             uint8_t *cache = r == grp ? a.kc : a.vc;
@@ -1678,20 +1701,25 @@ __global__ __launch_bounds__(256) void k_attn_prep_rows(QkvArgs a, const float *
 }
 
 hipError_t launch_attn_prep_rows(const float *qkv, const QkvArgs &a, int pos0, int nb, float *qout, hipStream_t s) {
-    if (a.hd % 64 || a.hd > 256 || a.n_kv <= 0 || a.n_head % a.n_kv || nb < 1 || nb > 65535) return hipErrorInvalidValue;
+    if (a.hd % 64 || (a.hd > 256 && a.hd != 512) || a.n_kv <= 0 || a.n_head % a.n_kv || nb < 1 || nb > 65535)
+        return hipErrorInvalidValue;
     if (a.ring && (a.window <= 0 || a.window > a.ring || nb > a.ring - a.window + 1)) return hipErrorInvalidValue;
     if (!a.rope || !a.q_norm || !a.k_norm) return hipErrorInvalidValue;
     const dim3 grid(nb, a.n_kv);
     if (a.hd == 64) hipLaunchKernelGGL(k_attn_prep_rows<64>, grid, dim3(256), 0, s, a, qkv, pos0, qout);
     else if (a.hd == 128) hipLaunchKernelGGL(k_attn_prep_rows<128>, grid, dim3(256), 0, s, a, qkv, pos0, qout);
     else if (a.hd == 192) hipLaunchKernelGGL(k_attn_prep_rows<192>, grid, dim3(256), 0, s, a, qkv, pos0, qout);
-    else hipLaunchKernelGGL(k_attn_prep_rows<256>, grid, dim3(256), 0, s, a, qkv, pos0, qout);
+    else if (a.hd == 256) hipLaunchKernelGGL(k_attn_prep_rows<256>, grid, dim3(256), 0, s, a, qkv, pos0, qout);
+    else hipLaunchKernelGGL(k_attn_prep_rows<512>, grid, dim3(256), 0, s, a, qkv, pos0, qout);
     return hipGetLastError();
 }
 
+static hipError_t attn_wide(const AttnCtx &c, int npos_max, int nb, uint8_t *ws, hipStream_t s);
+
 hipError_t launch_attn_batch(const float *q, const QkvArgs &a, int npos0, int nb, float *out, uint8_t *q8out, uint8_t *ws,
                              hipStream_t s, size_t q8_stride) {
-    if (a.hd % 64 || a.hd > 256 || a.n_kv <= 0 || a.n_head % a.n_kv || nb < 1 || npos0 < 1 || nb > 65535) return hipErrorInvalidValue;
+    if (a.hd % 64 || (a.hd > 256 && a.hd != ATT_WIDE) || a.n_kv <= 0 || a.n_head % a.n_kv || nb < 1 || npos0 < 1 || nb > 65535)
+        return hipErrorInvalidValue;
     attn_ws_untagged(ws);                                            // blocks per token of untagged data
     AttnCtx c{};
     c.q = q;
@@ -1700,6 +1728,7 @@ hipError_t launch_attn_batch(const float *q, const QkvArgs &a, int npos0, int nb
     c.out = out;
     c.q8out = q8out;
     c.q8_tok = q8_stride;
+    if (a.hd == ATT_WIDE) return attn_wide(c, a.window ? std::min(a.window, npos0 + nb - 1) : npos0 + nb - 1, nb, ws, s);
     const int grp = a.n_head / a.n_kv;
 #define G4_ATT(KV, G)                                                                        \
     if (a.kv_type == KV && grp == G) {                                                       \
@@ -1712,6 +1741,98 @@ hipError_t launch_attn_batch(const float *q, const QkvArgs &a, int npos0, int nb
     G4_ATT(Q8_0, 1); G4_ATT(Q8_0, 2); G4_ATT(Q8_0, 4); G4_ATT(Q8_0, 8);
     G4_ATT(Q4_0, 1); G4_ATT(Q4_0, 2); G4_ATT(Q4_0, 4); G4_ATT(Q4_0, 8);
 #undef G4_ATT
+    return hipErrorInvalidValue;
+}
+
+// ---------------------------------------------------- 512-wide heads --
+// gemma4's full-attention heads are 512 wide over one KV head (g4run.h:283-292,
+// model.c:530, 571).  They run on the 256-wide three passes as two halves:
+// the cache rows [slot][512] are read as [slot][2][256], i.e. as two KV heads
+// of 256, and the query rows are laid out half-major, [2][n_head][256], so the
+// queries of half k fall on KV head k.  The score pass forms each half's
+// partial dot; k_attn_wide_join adds the two (s = s_lo + s_hi: the f16 dot's
+// fp32 order, which differs from the CPU's 8-lane order in rounding only) into
+// the score rows of both halves and forms the chunk statistics of the sums
+// (chunk_stats, as the score pass would), so the value passes of both halves
+// take the same softmax weights, every output element's sum being that of a
+// 256-wide head.  The outputs come back to [n_head][512].
+__global__ __launch_bounds__(128) void k_attn_wide_rows(const float *__restrict__ src, float *__restrict__ dst, int n_head,
+                                                        int to_halves) {
+    // grid (n_head, nb): one 512-float row, a float4 per thread
+    const int h = blockIdx.x, b = blockIdx.y, t = threadIdx.x, half = t >> 6, e = 4 * (t & 63);
+    const size_t row = ((size_t)b * n_head + h) * ATT_WIDE + half * ATT_HALF + e;            // [b][h][half][e]
+    const size_t hm = (((size_t)b * 2 + half) * n_head + h) * ATT_HALF + e;                  // [b][half][h][e]
+    if (to_halves) *(float4 *)(dst + hm) = *(const float4 *)(src + row);
+    else *(float4 *)(dst + row) = *(const float4 *)(src + hm);
+}
+
+template <int GRP>
+__global__ __launch_bounds__(256) void k_attn_wide_join(AttnCtx c) {
+    __shared__ float wm[4][GRP];
+    __shared__ double wl[4][GRP];
+    attn_token(c);
+    const int npos = attn_view(c);
+    const int ch = blockIdx.y, lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    if (ch * ATT_CHUNK >= npos) return;
+    // lane l < 32 of wave w holds position ch * 128 + 32 w + l, as in the score pass
+    const int j = ch * ATT_CHUNK + wave * 32 + lane;
+    const bool ok = lane < 32 && j < npos;
+    float s[GRP];
+#pragma unroll
+    for (int g = 0; g < GRP; g++) {
+        float *lo = c.S + (size_t)g * npos + j, *hi = c.S + (size_t)(GRP + g) * npos + j;
+        s[g] = ok ? *lo + *hi : 0.0f;
+        if (ok) *lo = *hi = s[g];
+    }
+    chunk_stats<GRP, 4, false>(s, ok, lane < 32, c, 0, ch, wm, wl);
+    chunk_stats<GRP, 4, false>(s, ok, lane < 32, c, GRP, ch, wm, wl);
+}
+
+// heads of 512 over one KV head: q rows prepared (no preparation, projection
+// or Wo fold in this form), nb tokens as a batch (token b attends npos0 + b
+// positions) or one token with a device position count (npos_dev)
+template <int KV, int GRP>
+static hipError_t attn_wide_go(AttnCtx c, int npos_max, int nb, uint8_t *ws, hipStream_t s) {
+    const int H = c.a.n_head;
+    const AttnBatchWs w = attn_batch_ws(2 * H, ATT_HALF, npos_max);
+    const int nc = (npos_max + ATT_CHUNK - 1) / ATT_CHUNK;
+    uint8_t *base = ws + ATT_BATCH_OFF;
+    float *qh = (float *)(base + (size_t)nb * w.tok), *oh = (float *)((uint8_t *)qh + wide_rows_bytes(H, nb));
+    float *out = c.out;
+    c.nc = nc;
+    c.S = (float *)(base + w.S);
+    c.Mc = (float *)(base + w.Mc);
+    c.Lc = (double *)(base + w.Lc);
+    c.P = (float *)(base + w.P);
+    c.ntok = nb;
+    c.ws_tok = w.tok;
+    c.a.n_head = 2 * H;
+    c.a.n_kv = 2;
+    c.a.hd = ATT_HALF;
+    attn_ws_untagged(ws);
+    hipLaunchKernelGGL(k_attn_wide_rows, dim3(H, nb), dim3(128), 0, s, c.q, qh, H, 1);
+    c.q = qh;
+    c.out = oh;
+    const dim3 grid(2, nc, nb);
+    if constexpr (KV == F16) hipLaunchKernelGGL((k_attn_scores_f16<GRP, ATT_HALF>), grid, dim3(256), 0, s, c);
+    else hipLaunchKernelGGL((k_attn_scores_q8<KV, GRP, ATT_HALF>), grid, dim3(128), 0, s, c);
+    hipLaunchKernelGGL((k_attn_wide_join<GRP>), dim3(1, nc, nb), dim3(256), 0, s, c);
+    hipLaunchKernelGGL((k_attn_v<KV, GRP, ATT_HALF>), grid, dim3(256), 0, s, c);
+    hipLaunchKernelGGL(k_attn_combine, dim3(2 * H, 1, nb), dim3(256), 0, s, c);
+    hipLaunchKernelGGL(k_attn_wide_rows, dim3(H, nb), dim3(128), 0, s, oh, out, H, 0);
+    return hipGetLastError();
+}
+
+static hipError_t attn_wide(const AttnCtx &c, int npos_max, int nb, uint8_t *ws, hipStream_t s) {
+    const QkvArgs &a = c.a;
+    if (a.n_kv != 1 || !c.q || c.qkv || c.q8out || c.wo_out) return hipErrorInvalidValue;
+    const int grp = a.n_head;
+#define G4_AW(KV, G) \
+    if (a.kv_type == KV && grp == G) return attn_wide_go<KV, G>(c, npos_max, nb, ws, s)
+    G4_AW(F16, 1); G4_AW(F16, 2); G4_AW(F16, 4); G4_AW(F16, 8);
+    G4_AW(Q8_0, 1); G4_AW(Q8_0, 2); G4_AW(Q8_0, 4); G4_AW(Q8_0, 8);
+    G4_AW(Q4_0, 1); G4_AW(Q4_0, 2); G4_AW(Q4_0, 4); G4_AW(Q4_0, 8);
+#undef G4_AW
     return hipErrorInvalidValue;
 }
 
@@ -1798,7 +1919,7 @@ hipError_t launch_attn_qkv(const g4h_tensor &W, const GemvPro &pro, const QkvArg
 hipError_t launch_attn_decode(const float *q, const float *qkv, const QkvArgs &a, int npos, const int *npos_dev, int npos_max,
                               float *out, uint8_t *q8out, uint8_t *ws, hipStream_t s, const AttnTag *tag, const g4h_tensor *Wo,
                               float *wo_out, size_t ws_bytes) {
-    if (a.hd % 64 || a.hd > 256 || a.n_kv <= 0 || a.n_head % a.n_kv) return hipErrorInvalidValue;
+    if (a.hd % 64 || (a.hd > 256 && a.hd != ATT_WIDE) || a.n_kv <= 0 || a.n_head % a.n_kv) return hipErrorInvalidValue;
     if (qkv && (!a.rope || !a.q_norm || !a.k_norm)) return hipErrorInvalidValue;
     if (Wo && (!wo_out || !attn_wo_fits(*Wo, a, npos_max))) return hipErrorInvalidValue;
     AttnCtx c{};
@@ -1813,6 +1934,7 @@ hipError_t launch_attn_decode(const float *q, const float *qkv, const QkvArgs &a
         c.Wo = *Wo;
         c.wo_out = wo_out;
     }
+    if (a.hd == ATT_WIDE) return tag ? hipErrorInvalidValue : attn_wide(c, npos_max, 1, ws, s);
     const int grp = a.n_head / a.n_kv;
 #define G4_ATT(KV, G)                                                                                 \
     if (a.kv_type == KV && grp == G) {                                                                \

@@ -31,6 +31,7 @@ using namespace g4;
 
 
 extern "C" int g4h_internal_fail(int status, const char *msg);
+extern "C" int g4h_internal_attn_error(void *ws, void *stream, const char *fn);
 // sampler.cpp
 int sampler_n_vocab(const g4h_sampler *s);
 SamplerDev *sampler_device(g4h_sampler *s);
@@ -601,7 +602,7 @@ extern "C" int g4h_forward_batch(g4h_model *m, const int *tokens, int nb, int po
         M_RC(g4h_matmul_ex(m->head, nullptr, m->bact, m->act_bytes, m->logits, 1, 1, s));
     }
     M_HIP(hipStreamSynchronize(s));
-    return G4H_OK;
+    return g4h_internal_attn_error(m->bws, s, "g4h_forward_batch");           // per-token one-launch attention
 }
 
 extern "C" int g4h_forward_batch_heads(g4h_model *m, const int *tokens, int nb, int pos0, float *logits_dev, float *hnext_dev,
@@ -620,7 +621,7 @@ extern "C" int g4h_forward_batch_heads(g4h_model *m, const int *tokens, int nb, 
                                (size_t)c.n_embd * 4, (size_t)c.n_embd * 4, nb, hipMemcpyDeviceToDevice, s));
     M_RC(g4h_matmul_ex(m->head, nullptr, m->bact, m->act_bytes, logits_dev, nb, 1, s));
     M_HIP(hipStreamSynchronize(s));
-    return G4H_OK;
+    return g4h_internal_attn_error(m->bws, s, "g4h_forward_batch_heads");
 }
 
 extern "C" int g4h_argmax_rows(const float *logits_dev, int n, int nb, int *out_dev, void *stream) {

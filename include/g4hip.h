@@ -213,8 +213,10 @@ int g4h_attn_decode(const float *q_dev, const void *kc_dev, const void *vc_dev, 
  * give up (*failed = 1; its outputs hold NaN), else *failed = 0.  The
  * attention calls are asynchronous (and may be graph-replayed), so they cannot
  * return this status themselves; this call synchronizes `stream`, reads the
- * workspace's error word and clears it.  No reference counterpart: the CPU
- * attention (model.c:509-580) has no cross-thread wait. */
+ * workspace's error word and clears it; after a failure the next call on
+ * ws_dev clears the whole workspace first (a workgroup that started late may
+ * have left words under the next launch's tag).  No reference counterpart:
+ * the CPU attention (model.c:509-580) has no cross-thread wait. */
 int g4h_attn_status(void *ws_dev, int *failed, void *stream);
 /* The same with the sliding window and KV ring of model.c:517-537: the
  * current position is n_pos-1 and it attends positions max(0, n_pos -
@@ -356,9 +358,11 @@ int g4h_argmax_rows(const float *logits_dev, int n, int nb, int *out_dev, void *
  * (g4h_gemma_open maps, uploads and unmaps).  Every weight matrix is uploaded
  * and repacked once; the KV caches (kv_type G4H_F16, G4H_Q8_0 or G4H_Q4_0)
  * hold n_ctx positions for full layers and a ring of 576 (G4_SWA_RING) for
- * sliding-window layers.  Limits of this path: head dims 64/128/192/256 with
- * RoPE over the whole head, 1/2/4/8 query heads per KV head, a window of at
- * most 512 (G4_SWA_WINDOW_MAX), per-layer width <= 1024.  Synchronous. */
+ * sliding-window layers.  Limits of this path: head dims 64/128/192/256/512
+ * with RoPE over the whole head, 1/2/4/8 query heads per KV head, a window of
+ * at most 512 (G4_SWA_WINDOW_MAX), per-layer width <= 1024; the layers past
+ * n_layer_kv must be of the kind of the layer whose cache they read.
+ * Synchronous. */
 typedef struct g4h_gemma g4h_gemma;
 int g4h_gemma_create(const void *model_file, int n_ctx, int kv_type, g4h_gemma **out);
 int g4h_gemma_open(const char *path, int n_ctx, int kv_type, g4h_gemma **out);
@@ -369,8 +373,29 @@ int g4h_gemma_info(const g4h_gemma *g, int *n_vocab, int *n_embd, int *n_layer, 
  * [nb][n_vocab] (soft-capped) into logits_dev and, if hnext_dev, the head
  * input rms(x)*output_norm [nb][n_embd].  nb = 1 is g4_forward (g4run.h:309-311).
  * Row b equals the same forward run one token at a time, bit for bit.
- * Synchronous. */
+ * Synchronous; G4H_ERR_TIMEOUT if a one-launch attention wait gave up (the
+ * logits are then NaN). */
 int g4h_gemma_forward(g4h_gemma *g, const int *tokens, int nb, int pos0, float *logits_dev, float *hnext_dev, void *stream);
+/* Diagnostic (no reference counterpart): with trace_dev non-NULL, every later
+ * g4h_gemma_forward copies each token's intermediate vectors into trace_dev
+ * (fp32, *floats_per_token floats per token, token b's at b times that): the
+ * per-layer inputs (n_layer * n_embd_per_layer, after their projection and
+ * norm, model.c:617-635), then per layer x (the layer's input) | q | k | v (the
+ * raw projections, before their norms and RoPE; k and v not written on
+ * shared-KV layers, v not without attn_v) | att | wo (Wo output) | xmid (x
+ * after the attention residual) | g | u (gate and up outputs) | h
+ * (gelu(g) * u) | down | xffn (x after the FFN residual) | plg (inp_gate
+ * output) | plh (gelu(plg) * per-layer input) | proj | -- q and att
+ * n_head * hd_max floats, k and v hd_max, g, u and h the widest FFN, plg and
+ * plh n_embd_per_layer, the rest n_embd, each part's leading elements written
+ * -- then the final x.  A CPU implementation can then check each part of each
+ * layer on the GPU's own inputs.  NULL turns it off. */
+int g4h_gemma_trace(g4h_gemma *g, float *trace_dev, size_t *floats_per_token);
+/* Diagnostic: layer `layer`'s K and V caches (device) and their bytes; rows of
+ * one KV head, n_ctx slots for full layers, a ring of 576 slots stored twice
+ * (slot p % 576 and p % 576 + 576) for sliding-window layers.  Layers past
+ * n_layer_kv have no cache of their own. */
+int g4h_gemma_kv(g4h_gemma *g, int layer, void **k_dev, void **v_dev, size_t *bytes);
 
 /* ------------------------------------------------------------ sampler ---- */
 /* The sampling chain of sampler.c (g4run.h:464-489) with its settings, RNG,

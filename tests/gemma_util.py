@@ -13,6 +13,11 @@ F32, F16, Q4_0, Q8_0, Q4_K, Q6_K, BF16 = 0, 1, 2, 8, 12, 14, 30
 SMALL = dict(n_layer=4, n_kv_shared=1, n_embd=256, n_head=4, head_dim_full=128, head_dim_swa=64,
              n_ff=[512, 768, 512, 512], n_embd_per_layer=32, n_vocab=512, n_swa=8, is_swa=[1, 1, 0, 1],
              rope_base_full=1e6, rope_base_swa=1e4, rms_eps=1e-6, final_softcap=15.0)
+# the reference's gemma4 head widths (g4run.h:283-292: 8 query heads of 512 on
+# the full-attention layers, 256 on the sliding ones), at small model width
+WIDE = dict(n_layer=4, n_kv_shared=1, n_embd=512, n_head=8, head_dim_full=512, head_dim_swa=256,
+            n_ff=[1024, 768, 1024, 1024], n_embd_per_layer=64, n_vocab=512, n_swa=16, is_swa=[1, 1, 0, 1],
+            rope_base_full=1e6, rope_base_swa=1e4, rms_eps=1e-6, final_softcap=15.0)
 
 
 def _bf16(x):

@@ -34,6 +34,8 @@ def make_cache(G, oracle, kv_type, n_slot, n_kv, hd, seed):
 @pytest.mark.parametrize("n_head,n_kv,hd,n_pos,qscale", [
     (8, 4, 256, 1, 1.0), (8, 4, 256, 65, 1.0), (8, 4, 256, 1000, 1.0), (8, 4, 256, 8192, 1.0),
     (8, 4, 256, 3000, 0.02), (4, 4, 128, 300, 0.1), (8, 1, 64, 777, 0.3), (16, 2, 192, 129, 1.0),
+    # gemma4's full-attention heads: 8 query heads of 512 over one KV head (g4run.h:283-292)
+    (8, 1, 512, 1, 1.0), (8, 1, 512, 777, 0.3), (8, 1, 512, 4096, 0.2), (2, 1, 512, 130, 1.0),
 ])
 def test_attention_vs_oracle(gpu, oracle, kv_type, n_head, n_kv, hd, n_pos, qscale):
     G = gpu
@@ -68,6 +70,50 @@ def test_attention_identical_keys_average_values(gpu, oracle):
     assert np.allclose(got, expect[None, :], rtol=1e-5, atol=1e-6)
 
 
+@pytest.mark.parametrize("kv_type", [1, 8], ids=["f16", "q8_0"])
+def test_wide_heads_identical_keys_and_halves(gpu, oracle, kv_type):
+    """512-wide heads run as two halves whose partial scores are joined: with
+    all keys equal every weight is fp16(1/n) (f16 V) or 1/n, so the output is
+    the mean of V (closed form); and keys whose second half is zero give the
+    scores of the first half alone, i.e. the 256-wide attention of the first
+    halves, element for element in the first half of the output."""
+    G = gpu
+    n_head, n_kv, hd, n_pos = 4, 1, 512, 300
+    rng = np.random.default_rng(17)
+    k = np.tile(rng.standard_normal(hd).astype(np.float32), (n_pos, 1))
+    v = rng.standard_normal((n_pos, hd)).astype(np.float32)
+    rb = hd * 2 if kv_type == G.F16 else G.row_size(kv_type, hd)
+    kb, vb = G.Buffer(n_pos * rb), G.Buffer(n_pos * rb)
+    G.kv_store(kv_type, G.Buffer.from_array(k), kb, hd, rows=n_pos, dst_stride=rb)
+    G.kv_store(kv_type, G.Buffer.from_array(v), vb, hd, rows=n_pos, dst_stride=rb)
+    q = rng.standard_normal((n_head, hd)).astype(np.float32)
+    out = G.Buffer(n_head * hd * 4)
+    G.attn_decode(G.Buffer.from_array(q), kb, vb, kv_type, n_head, n_kv, hd, n_pos, out)
+    got = out.download(np.float32, (n_head, hd))
+    vh = vb.download(np.uint8, (n_pos, rb))
+    if kv_type == G.F16:
+        w = np.float64(np.float16(np.float32(1.0 / n_pos)))
+        vf = oracle.fp16_to_fp32(vh.view(np.uint16).reshape(n_pos, hd)).astype(np.float64)
+    else:
+        w = np.float64(np.float32(1.0 / n_pos))
+        vf = oracle.dequant(kv_type, vh, hd).astype(np.float64)
+    assert np.allclose(got, (w * vf).sum(0)[None, :], rtol=1e-5, atol=1e-6)
+    # second halves of K zero: the first output half equals the 256-wide attention of the first halves
+    k2 = rng.standard_normal((n_pos, hd)).astype(np.float32)
+    k2[:, 256:] = 0.0
+    kb2 = G.Buffer(n_pos * rb)
+    G.kv_store(kv_type, G.Buffer.from_array(k2), kb2, hd, rows=n_pos, dst_stride=rb)
+    G.attn_decode(G.Buffer.from_array(q), kb2, vb, kv_type, n_head, n_kv, hd, n_pos, out)
+    wide = out.download(np.float32, (n_head, hd))
+    half_k, half_v = G.Buffer(n_pos * rb // 2), G.Buffer(n_pos * rb // 2)
+    G.kv_store(kv_type, G.Buffer.from_array(np.ascontiguousarray(k2[:, :256])), half_k, 256, rows=n_pos, dst_stride=rb // 2)
+    G.kv_store(kv_type, G.Buffer.from_array(np.ascontiguousarray(v[:, :256])), half_v, 256, rows=n_pos, dst_stride=rb // 2)
+    o256 = G.Buffer(n_head * 256 * 4)
+    G.attn_decode(G.Buffer.from_array(np.ascontiguousarray(q[:, :256])), half_k, half_v, kv_type, n_head, n_kv, 256, n_pos, o256)
+    narrow = o256.download(np.float32, (n_head, 256))
+    assert np.array_equal(wide[:, :256].view(np.uint32), narrow.view(np.uint32))
+
+
 def test_attention_bad_shapes(gpu):
     import ctypes as C
     G = gpu
@@ -76,6 +122,7 @@ def test_attention_bad_shapes(gpu):
     assert L.g4h_attn_decode(b.ptr, b.ptr, b.ptr, G.Q4_K, 8, 4, 256, 10, b.ptr, b.ptr, b.nbytes, None) == G.ERR_TYPE
     assert L.g4h_attn_decode(b.ptr, b.ptr, b.ptr, G.F16, 8, 3, 256, 10, b.ptr, b.ptr, b.nbytes, None) == G.ERR_SHAPE
     assert L.g4h_attn_decode(b.ptr, b.ptr, b.ptr, G.F16, 8, 4, 96, 10, b.ptr, b.ptr, b.nbytes, None) == G.ERR_SHAPE
+    assert L.g4h_attn_decode(b.ptr, b.ptr, b.ptr, G.F16, 8, 2, 512, 10, b.ptr, b.ptr, b.nbytes, None) == G.ERR_SHAPE   # one KV head
     assert L.g4h_attn_decode(b.ptr, b.ptr, b.ptr, G.F16, 8, 4, 256, 10, b.ptr, b.ptr, 16, None) == G.ERR_ARG
 
 
@@ -234,7 +281,8 @@ def test_batched_prefill_attention_is_causal(gpu, oracle, kv_type, pos0, nb):
 
 @pytest.mark.parametrize("kv_type,n_head,n_kv,hd,pos0,nb", [
     (1, 8, 4, 256, 120, 20), (8, 8, 4, 256, 250, 11), (2, 8, 4, 256, 0, 5),
-    (1, 4, 4, 64, 1000, 33), (8, 8, 1, 128, 127, 2), (2, 16, 2, 192, 383, 3), (1, 2, 2, 64, 0, 1)])
+    (1, 4, 4, 64, 1000, 33), (8, 8, 1, 128, 127, 2), (2, 16, 2, 192, 383, 3), (1, 2, 2, 64, 0, 1),
+    (1, 8, 1, 512, 120, 20), (8, 8, 1, 512, 255, 4), (2, 4, 1, 512, 0, 9)])
 def test_batched_prefill_equals_per_token_calls(gpu, oracle, kv_type, n_head, n_kv, hd, pos0, nb):
     """The one-set batch (three launches, a token grid dimension, a workspace
     block per token) gives every token the bits of a decode call at its
@@ -289,7 +337,7 @@ def test_attention_timeout_reported_by_status(gpu, oracle):
 @pytest.mark.parametrize("kv_type", [1, 8, 2], ids=["f16", "q8_0", "q4_0"])
 @pytest.mark.parametrize("n_head,hd,n_pos,window,ring", [
     (4, 64, 9, 8, 40), (4, 64, 100, 8, 40), (8, 256, 1000, 512, 576), (8, 256, 700, 512, 576), (2, 128, 300, 300, 0),
-    (4, 64, 50, 1, 40), (8, 128, 5, 512, 576), (8, 256, 1300, 129, 576)])
+    (4, 64, 50, 1, 40), (8, 128, 5, 512, 576), (8, 256, 1300, 129, 576), (8, 512, 700, 512, 576), (8, 512, 300, 0, 0)])
 def test_window_ring_attention_vs_oracle(gpu, oracle, kv_type, n_head, hd, n_pos, window, ring):
     """model.c:517-537: a sliding window over a KV ring (GPU: rows stored at
     slot j % ring and j % ring + ring; oracle: one copy in `ring` slots) and,
