@@ -396,19 +396,18 @@ class _GpuQuant:
         return yb.download(np.uint8, (rows, G.row_size(t, n)))
 
 
-def bench_gemma(G, pos_fill=1024, steps=32):
+def bench_gemma(G, pos_fill=1024, steps=64):
     """A gemma4 model from a GGUF file (scope rank 1: reader, residency, the
-    gemma4 step): a synthetic file of 8 layers, width 2048, FFN 6144, 32768
-    tokens, written here, loaded with g4h_gemma_open, filled to pos_fill with
-    64-token batches, then `steps` single-token forwards timed (host-driven and
-    synchronous, logits copied back each call)."""
+    gemma4 step): a synthetic file with the reference's head widths (tests'
+    gemma_util.BENCH: 8 layers, width 2048, 8 heads of 512 / 256, FFN 6144,
+    32768 tokens), written here, loaded with g4h_gemma_open, filled to pos_fill
+    with 64-token batches; then `steps` greedy decode steps timed as replays of
+    one captured g4h_gemma_step (token and position on the device), and the
+    host-driven g4h_gemma_forward (synchronous, logits copied back) beside it."""
     import tempfile
     sys.path.insert(0, os.path.join(ROOT, "tests"))
     import gemma_util as GM
-    spec = dict(GM.SMALL, n_layer=8, n_kv_shared=2, n_embd=2048, n_head=8, head_dim_full=256, head_dim_swa=256,
-                n_ff=[6144] * 8, n_embd_per_layer=256, n_vocab=32768, n_swa=512,
-                is_swa=[1, 1, 1, 0, 1, 1, 1, 0])
-    hp, T = GM.make_gemma(_GpuQuant(G), 9, spec=spec)
+    hp, T = GM.make_gemma(_GpuQuant(G), 9, spec=GM.BENCH)
     fd, path = tempfile.mkstemp(suffix=".gguf")
     os.close(fd)
     try:
@@ -422,10 +421,26 @@ def bench_gemma(G, pos_fill=1024, steps=32):
         toks = rs.integers(0, g.n_vocab, steps).astype(np.int32)
         G.synchronize()
         t0 = time.perf_counter()
-        for i in range(steps):
+        for i in range(8):
             g.forward(toks[i:i + 1], pos_fill + i)
         G.synchronize()
-        ms = (time.perf_counter() - t0) * 1e3 / steps
+        ms_host = (time.perf_counter() - t0) * 1e3 / 8
+        st = G.Stream()
+        g.set_state(int(toks[0]), pos_fill, st.ptr)
+        g.step(st.ptr)                                   # outside the capture: workspaces set up
+        st.synchronize()
+        g.set_state(int(toks[0]), pos_fill, st.ptr)
+        graph = G.Graph(st.ptr, lambda: g.step(st.ptr))
+        graph.launch(st.ptr)                             # warm replay
+        st.synchronize()
+        g.set_state(int(toks[0]), pos_fill, st.ptr)
+        e0, e1 = G.Event(), G.Event()
+        e0.record(st.ptr)
+        for _ in range(steps):
+            graph.launch(st.ptr)
+        e1.record(st.ptr)
+        ms = e0.elapsed_ms(e1) / steps
+        assert g.get_state(st.ptr)[1] == pos_fill + steps
         t0 = time.perf_counter()
         g.forward(rs.integers(0, g.n_vocab, 64).astype(np.int32), pos_fill + steps)
         G.synchronize()
@@ -433,13 +448,14 @@ def bench_gemma(G, pos_fill=1024, steps=32):
         g.free()
     finally:
         os.unlink(path)
-    return {"decode_tok_per_s": round(1e3 / ms, 1), "ms_per_token": round(ms, 3), "batch_64_ms": round(ms64, 2),
-            "file_bytes": nbytes,
+    return {"decode_tok_per_s": round(1e3 / ms, 1), "ms_per_token": round(ms, 4),
+            "host_driven_tok_per_s": round(1e3 / ms_host, 1), "batch_64_ms": round(ms64, 2), "file_bytes": nbytes,
             "what": f"gemma4 from a synthetic {nbytes / 1e6:.0f} MB GGUF (g4h_gemma_open: mmap reader, upload and "
-                    "repack): 8 layers (6 sliding-window on the KV ring, 2 shared-KV), width 2048, 8 heads x 256, "
-                    "FFN 6144, per-layer embeddings 256, 32768 tokens, soft-cap; q8_0/q4_0/q4_K/q6_K/f16/bf16 "
-                    f"weights; single-token forwards at positions {pos_fill}..{pos_fill + steps - 1}, host-driven, "
-                    "logits copied back per call; and one 64-token batch"}
+                    "repack): 8 layers (5 sliding-window on the KV ring, 3 full, 2 of them shared-KV), width 2048, "
+                    "8 heads x 512 (full) / 256 (sliding) over one KV head, FFN 6144, per-layer embeddings 256, 32768 "
+                    "tokens, soft-cap; q8_0/q4_0/q4_K/q6_K/f16/bf16 weights; greedy decode steps at positions "
+                    f"{pos_fill}..{pos_fill + steps - 1} as replays of one captured g4h_gemma_step (the host-driven "
+                    "g4h_gemma_forward beside it); and one 64-token batch"}
 
 
 def bench_next(G, m):

@@ -129,6 +129,11 @@ _SIGS = [
     ("g4h_gemma_forward", _int, [_vp, C.POINTER(_int), _int, _int, _vp, _vp, _vp]),
     ("g4h_read_floor", _int, [_vp, _sz, _vp, C.c_int64, _int, _int, _vp]),
     ("g4h_gemma_trace", _int, [_vp, _vp, C.POINTER(_sz)]),
+    ("g4h_gemma_set_state", _int, [_vp, _int, _int, _vp]),
+    ("g4h_gemma_step", _int, [_vp, _vp]),
+    ("g4h_gemma_get_state", _int, [_vp, C.POINTER(_int), C.POINTER(_int), _vp]),
+    ("g4h_gemma_status", _int, [_vp, C.POINTER(_int), _vp]),
+    ("g4h_gemma_logits", _vp, [_vp]),
     ("g4h_gemma_kv", _int, [_vp, _int, C.POINTER(_vp), C.POINTER(_vp), C.POINTER(_sz)]),
 ]
 
@@ -495,6 +500,28 @@ class Gemma:
         L, Hn = Buffer(nb * self.n_vocab * 4), Buffer(nb * self.n_embd * 4)
         check(lib().g4h_gemma_forward(self.ptr, t.ctypes.data_as(C.POINTER(_int)), nb, pos0, L.ptr, Hn.ptr, stream))
         return L.download(np.float32, (nb, self.n_vocab)), Hn.download(np.float32, (nb, self.n_embd))
+
+    def set_state(self, token: int, pos: int, stream=None) -> None:
+        check(lib().g4h_gemma_set_state(self.ptr, token, pos, stream))
+
+    def step(self, stream=None) -> None:
+        """One decode step from the device state (graph-capturable)."""
+        check(lib().g4h_gemma_step(self.ptr, stream))
+
+    def get_state(self, stream=None):
+        t, p = _int(), _int()
+        check(lib().g4h_gemma_get_state(self.ptr, C.byref(t), C.byref(p), stream))
+        return t.value, p.value
+
+    def status(self, stream=None) -> int:
+        f = _int()
+        check(lib().g4h_gemma_status(self.ptr, C.byref(f), stream))
+        return f.value
+
+    def logits(self) -> np.ndarray:
+        out = np.empty(self.n_vocab, np.float32)
+        check(lib().g4h_memcpy_d2h(out.ctypes.data_as(_vp), lib().g4h_gemma_logits(self.ptr), out.nbytes, None))
+        return out
 
     def trace(self, buf) -> int:
         """Per-token intermediate vectors of later forwards into buf (None: off);

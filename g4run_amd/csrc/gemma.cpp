@@ -56,7 +56,11 @@ struct g4h_gemma {
     std::vector<uint8_t *> kc, vc;
     float *x = nullptr, *xb = nullptr, *q = nullptr, *k = nullptr, *v = nullptr, *qkv = nullptr, *att = nullptr, *g = nullptr,
           *u = nullptr, *pl = nullptr, *plp = nullptr, *plg = nullptr, *hn = nullptr;
-    uint8_t *ws = nullptr, *bws = nullptr;     // decode attention / batch attention workspaces
+    uint8_t *ws = nullptr, *wsf = nullptr;     // one-token attention workspaces: sliding / full layers
+    uint8_t *bws = nullptr;                    // batch attention workspace
+    int *tok = nullptr;                        // device token ids of a call (kRows)
+    int *state = nullptr;                      // decode state: token, pos, npos = pos + 1, steps, flags
+    float *logits = nullptr;                   // the step's logits (n_vocab)
     uint16_t *gelu = nullptr;
     float *trace = nullptr;                    // optional per-token trace (g4h_gemma_trace)
     std::vector<void *> allocs;
@@ -274,10 +278,18 @@ int create(const g4_model_file *mf, int n_ctx, int kv_type, g4h_gemma *m) {
     G_RC(galloc(m, (void **)&m->pl, B * NPL * 4));
     G_RC(galloc(m, (void **)&m->plp, B * NPL * 4));
     G_RC(galloc(m, (void **)&m->plg, B * m->PE * 4));
-    // 512-wide heads take another layout than the 256-wide ones: the larger of the two
-    const size_t wsb = std::max(g4h_attn_workspace_bytes(m->H, m->hd_full, n_ctx), g4h_attn_workspace_bytes(m->H, m->hd_swa, n_ctx));
-    G_RC(galloc(m, (void **)&m->ws, wsb));
-    G_HIP(hipMemset(m->ws, 0, wsb));
+    // one workspace per layer kind (the 512-wide heads' three passes leave
+    // untagged words that the one-launch form of the other kind would clear)
+    const size_t wss = g4h_attn_workspace_bytes(m->H, m->hd_swa, std::min(n_ctx, m->n_swa)),
+                 wsf = g4h_attn_workspace_bytes(m->H, m->hd_full, n_ctx);
+    G_RC(galloc(m, (void **)&m->ws, wss));
+    G_RC(galloc(m, (void **)&m->wsf, wsf));
+    G_HIP(hipMemset(m->ws, 0, wss));
+    G_HIP(hipMemset(m->wsf, 0, wsf));
+    G_RC(galloc(m, (void **)&m->tok, kRows * sizeof(int)));
+    G_RC(galloc(m, (void **)&m->state, 8 * sizeof(int)));
+    G_RC(galloc(m, (void **)&m->logits, (size_t)m->V * 4));
+    G_HIP(hipMemset(m->state, 0, 8 * sizeof(int)));
     G_RC(galloc(m, (void **)&m->bws, std::max(attn_batch_workspace_bytes(m->H, m->hd_full, n_ctx, kRows),
                                               attn_batch_workspace_bytes(m->H, m->hd_swa, n_ctx, kRows))));
     std::vector<uint16_t> gt(65536);
@@ -361,14 +373,14 @@ extern "C" int g4h_gemma_info(const g4h_gemma *m, int *n_vocab, int *n_embd, int
     return G4H_OK;
 }
 
-extern "C" int g4h_gemma_forward(g4h_gemma *m, const int *tokens, int nb, int pos0, float *logits_dev, float *hnext_dev,
-                                 void *stream) {
-    if (!m || !tokens || !logits_dev) return g4h_internal_fail(G4H_ERR_ARG, "g4h_gemma_forward: null argument");
-    if (nb < 1 || nb > kRows) return g4h_internal_fail(G4H_ERR_ARG, "g4h_gemma_forward: nb must be 1..64 (G4_BATCH_MAX)");
-    if (pos0 < 0 || pos0 + nb > m->n_ctx) return g4h_internal_fail(G4H_ERR_ARG, "g4h_gemma_forward: positions outside the context");
-    for (int b = 0; b < nb; b++)
-        if (tokens[b] < 0 || tokens[b] >= m->V) return g4h_internal_fail(G4H_ERR_ARG, "g4h_gemma_forward: token out of range");
-    const hipStream_t s = (hipStream_t)stream;
+// The forward of nb tokens whose ids are in tok_dev (device) at positions
+// pos0 .. pos0 + nb - 1; with `st` (one token, the decode state token | pos |
+// npos on the device) the position comes from st instead, and the call is
+// stream-ordered only (graph-capturable).  Every position's logits go to
+// logits_dev, the head inputs to hnext_dev if given.
+static int run(g4h_gemma *m, const int *tok_dev, int nb, int pos0, const int *st, float *logits_dev, float *hnext_dev,
+               hipStream_t s) {
+    const int *pos_dev = st ? st + 1 : nullptr, *npos_dev = st ? st + 2 : nullptr;
     const int E = m->E, H = m->H, PE = m->PE, NPL = m->n_layer * PE;
     const float eps = m->eps;
     // per-token trace (g4h_gemma_trace): pl, then per layer the record below, then the final x
@@ -386,12 +398,9 @@ extern "C" int g4h_gemma_forward(g4h_gemma *m, const int *tokens, int nb, int po
         return tr((size_t)NPL + (size_t)il * rec + off, src, stride, n);
     };
 
-    // embeddings and per-layer token rows (model.c:602-615)
-    for (int b = 0; b < nb; b++) {
-        G_HIP(launch_dequant(m->tok_type, m->tok_raw + (size_t)tokens[b] * m->tok_rb, m->tok_rb, m->x + (size_t)b * E, E, E, 1, s));
-        G_HIP(launch_dequant(m->ple_type, m->ple_raw + (size_t)tokens[b] * m->ple_rb, m->ple_rb, m->pl + (size_t)b * NPL, NPL, NPL,
-                             1, s));
-    }
+    // embeddings and per-layer token rows (model.c:602-615), gathered on the device
+    G_HIP(launch_dequant(m->tok_type, m->tok_raw, m->tok_rb, m->x, E, E, nb, s, tok_dev));
+    G_HIP(launch_dequant(m->ple_type, m->ple_raw, m->ple_rb, m->pl, NPL, NPL, nb, s, tok_dev));
     G_HIP(launch_scale(m->x, (int64_t)nb * E, sqrtf((float)E), s));
     G_HIP(launch_scale(m->pl, (int64_t)nb * NPL, sqrtf((float)PE), s));
     // per-layer input projection (model.c:617-635)
@@ -419,6 +428,7 @@ extern "C" int g4h_gemma_forward(g4h_gemma *m, const int *tokens, int nb, int po
         qa.window = L.swa ? m->n_swa : 0;
         qa.ring = L.swa ? kRing : 0;
         const int npos_max = L.swa ? std::min(m->n_ctx, m->n_swa) : m->n_ctx;
+        uint8_t *ws = L.swa ? m->ws : m->wsf;
         if (il < m->n_layer_kv) {
             // own K/V: q | k | v prepared, stored at the position and attended in one step (model.c:664-689)
             G_RC(mm(L.wk, m->xb, m->k, nb, s));
@@ -432,19 +442,19 @@ extern "C" int g4h_gemma_forward(g4h_gemma *m, const int *tokens, int nb, int po
                 G_HIP(launch_attn_prep_rows(m->qkv, qa, pos0, nb, m->q, s));
                 G_HIP(launch_attn_batch(m->q, qa, pos0 + 1, nb, m->att, nullptr, m->bws, s));
             } else if (hd == 512) {                                  // wide heads: rows prepared first, then the halves attend
-                G_HIP(launch_attn_prep_rows(m->qkv, qa, pos0, 1, m->q, s));
-                G_HIP(launch_attn_decode(m->q, nullptr, qa, pos0 + 1, nullptr, npos_max, m->att, nullptr, m->ws, s));
+                G_HIP(launch_attn_prep_rows(m->qkv, qa, pos0, 1, m->q, s, pos_dev));
+                G_HIP(launch_attn_decode(m->q, nullptr, qa, pos0 + 1, npos_dev, npos_max, m->att, nullptr, ws, s));
             } else {
-                G_HIP(launch_attn_decode(nullptr, m->qkv, qa, pos0 + 1, nullptr, npos_max, m->att, nullptr, m->ws, s));
+                G_HIP(launch_attn_decode(nullptr, m->qkv, qa, pos0 + 1, npos_dev, npos_max, m->att, nullptr, ws, s));
             }
         } else {
             // a shared cache: the queries are prepared here (model.c:666-672, 692)
             const int cil = L.swa ? m->n_layer_kv - 2 : m->n_layer_kv - 1;
-            G_HIP(launch_head_prep(m->q, H, hd, nb, L.q_norm, rope, pos0, eps, s));
+            G_HIP(launch_head_prep(m->q, H, hd, nb, L.q_norm, rope, pos0, eps, s, pos_dev));
             qa.kc = m->kc[cil];
             qa.vc = m->vc[cil];
             if (nb > 1) G_HIP(launch_attn_batch(m->q, qa, pos0 + 1, nb, m->att, nullptr, m->bws, s));
-            else G_HIP(launch_attn_decode(m->q, nullptr, qa, pos0 + 1, nullptr, npos_max, m->att, nullptr, m->ws, s));
+            else G_HIP(launch_attn_decode(m->q, nullptr, qa, pos0 + 1, npos_dev, npos_max, m->att, nullptr, ws, s));
         }
         G_RC(trl(il, T_ATT, m->att, nq, nq));
         G_RC(mm(L.wo, m->att, m->xb, nb, s));
@@ -478,6 +488,64 @@ extern "C" int g4h_gemma_forward(g4h_gemma *m, const int *tokens, int nb, int po
     G_HIP(launch_rms_rows(m->x, m->out_norm, hn, E, nb, eps, s));
     G_RC(mm(m->head, hn, logits_dev, nb, s));
     if (m->softcap > 0) G_HIP(launch_softcap(logits_dev, (int64_t)nb * m->V, m->softcap, s));
-    G_HIP(hipStreamSynchronize(s));
-    return g4h_internal_attn_error(m->ws, s, "g4h_gemma_forward");
+    return G4H_OK;
 }
+
+extern "C" int g4h_gemma_forward(g4h_gemma *m, const int *tokens, int nb, int pos0, float *logits_dev, float *hnext_dev,
+                                 void *stream) {
+    if (!m || !tokens || !logits_dev) return g4h_internal_fail(G4H_ERR_ARG, "g4h_gemma_forward: null argument");
+    if (nb < 1 || nb > kRows) return g4h_internal_fail(G4H_ERR_ARG, "g4h_gemma_forward: nb must be 1..64 (G4_BATCH_MAX)");
+    if (pos0 < 0 || pos0 + nb > m->n_ctx) return g4h_internal_fail(G4H_ERR_ARG, "g4h_gemma_forward: positions outside the context");
+    for (int b = 0; b < nb; b++)
+        if (tokens[b] < 0 || tokens[b] >= m->V) return g4h_internal_fail(G4H_ERR_ARG, "g4h_gemma_forward: token out of range");
+    const hipStream_t s = (hipStream_t)stream;
+    G_HIP(hipMemcpyAsync(m->tok, tokens, (size_t)nb * sizeof(int), hipMemcpyHostToDevice, s));
+    G_RC(run(m, m->tok, nb, pos0, nullptr, logits_dev, hnext_dev, s));
+    G_HIP(hipStreamSynchronize(s));
+    const int e0 = g4h_internal_attn_error(m->ws, s, "g4h_gemma_forward");   // both read and cleared
+    const int e1 = g4h_internal_attn_error(m->wsf, s, "g4h_gemma_forward");
+    return e0 ? e0 : e1;
+}
+
+// ------------------------------------------------ device-driven decode --
+extern "C" int g4h_gemma_set_state(g4h_gemma *m, int token, int pos, void *stream) {
+    if (!m) return g4h_internal_fail(G4H_ERR_ARG, "g4h_gemma_set_state: null model");
+    if (pos < 0 || pos >= m->n_ctx) return g4h_internal_fail(G4H_ERR_ARG, "g4h_gemma_set_state: pos outside the context");
+    if (token < 0 || token >= m->V) return g4h_internal_fail(G4H_ERR_ARG, "g4h_gemma_set_state: token out of range");
+    const int st[5] = {token, pos, pos + 1, 0, 0};
+    G_HIP(hipMemcpyAsync(m->state, st, sizeof st, hipMemcpyHostToDevice, (hipStream_t)stream));
+    G_HIP(hipStreamSynchronize((hipStream_t)stream));
+    return G4H_OK;
+}
+
+extern "C" int g4h_gemma_step(g4h_gemma *m, void *stream) {
+    if (!m) return g4h_internal_fail(G4H_ERR_ARG, "g4h_gemma_step: null model");
+    const hipStream_t s = (hipStream_t)stream;
+    G_RC(run(m, m->state, 1, 0, m->state, m->logits, nullptr, s));
+    G_HIP(launch_argmax_advance(m->logits, m->V, m->state, m->n_ctx, s));   // token <- first argmax, pos += 1
+    return G4H_OK;
+}
+
+extern "C" int g4h_gemma_get_state(g4h_gemma *m, int *token, int *pos, void *stream) {
+    if (!m) return g4h_internal_fail(G4H_ERR_ARG, "g4h_gemma_get_state: null model");
+    int st[3];
+    G_HIP(hipMemcpyAsync(st, m->state, sizeof st, hipMemcpyDeviceToHost, (hipStream_t)stream));
+    G_HIP(hipStreamSynchronize((hipStream_t)stream));
+    if (token) *token = st[0];
+    if (pos) *pos = st[1];
+    return G4H_OK;
+}
+
+extern "C" int g4h_gemma_status(g4h_gemma *m, int *flags, void *stream) {
+    if (!m || !flags) return g4h_internal_fail(G4H_ERR_ARG, "g4h_gemma_status: null argument");
+    const hipStream_t s = (hipStream_t)stream;
+    int st[5];
+    G_HIP(hipMemcpyAsync(st, m->state, sizeof st, hipMemcpyDeviceToHost, s));
+    G_HIP(hipStreamSynchronize(s));
+    const int t0 = g4h_internal_attn_error(m->ws, s, "g4h_gemma_status"), t1 = g4h_internal_attn_error(m->wsf, s, "g4h_gemma_status");
+    if ((t0 && t0 != G4H_ERR_TIMEOUT) || (t1 && t1 != G4H_ERR_TIMEOUT)) return t0 ? t0 : t1;
+    *flags = ((st[4] & STATE_CTX_FULL) ? G4H_STATUS_CTX_FULL : 0) | (t0 || t1 ? G4H_STATUS_ATTN_TIMEOUT : 0);
+    return G4H_OK;
+}
+
+extern "C" const float *g4h_gemma_logits(const g4h_gemma *m) { return m ? m->logits : nullptr; }

@@ -1670,7 +1670,9 @@ static hipError_t attn_batch_go(AttnCtx c, int n_head, int n_kv, int npos0, int 
 // tokens no token's store overwrites a row an earlier token of the batch
 // still attends.
 template <int HD>
-__global__ __launch_bounds__(256) void k_attn_prep_rows(QkvArgs a, const float *__restrict__ qkv, int pos0, float *__restrict__ qout) {
+__global__ __launch_bounds__(256) void k_attn_prep_rows(QkvArgs a, const float *__restrict__ qkv, int pos0, float *__restrict__ qout,
+                                                        const int *pos_dev) {
+    if (pos_dev) pos0 = *pos_dev;
     constexpr int N = HD > 256 ? 8 : 4;                              // elements per lane held
     __shared__ float wb[4][64 * N];                                  // q8_0 / q4_0 stores
     constexpr int epl = HD >> 6;
@@ -1700,17 +1702,18 @@ __global__ __launch_bounds__(256) void k_attn_prep_rows(QkvArgs a, const float *
     }
 }
 
-hipError_t launch_attn_prep_rows(const float *qkv, const QkvArgs &a, int pos0, int nb, float *qout, hipStream_t s) {
+hipError_t launch_attn_prep_rows(const float *qkv, const QkvArgs &a, int pos0, int nb, float *qout, hipStream_t s,
+                                 const int *pos_dev) {
     if (a.hd % 64 || (a.hd > 256 && a.hd != 512) || a.n_kv <= 0 || a.n_head % a.n_kv || nb < 1 || nb > 65535)
         return hipErrorInvalidValue;
     if (a.ring && (a.window <= 0 || a.window > a.ring || nb > a.ring - a.window + 1)) return hipErrorInvalidValue;
     if (!a.rope || !a.q_norm || !a.k_norm) return hipErrorInvalidValue;
     const dim3 grid(nb, a.n_kv);
-    if (a.hd == 64) hipLaunchKernelGGL(k_attn_prep_rows<64>, grid, dim3(256), 0, s, a, qkv, pos0, qout);
-    else if (a.hd == 128) hipLaunchKernelGGL(k_attn_prep_rows<128>, grid, dim3(256), 0, s, a, qkv, pos0, qout);
-    else if (a.hd == 192) hipLaunchKernelGGL(k_attn_prep_rows<192>, grid, dim3(256), 0, s, a, qkv, pos0, qout);
-    else if (a.hd == 256) hipLaunchKernelGGL(k_attn_prep_rows<256>, grid, dim3(256), 0, s, a, qkv, pos0, qout);
-    else hipLaunchKernelGGL(k_attn_prep_rows<512>, grid, dim3(256), 0, s, a, qkv, pos0, qout);
+    if (a.hd == 64) hipLaunchKernelGGL(k_attn_prep_rows<64>, grid, dim3(256), 0, s, a, qkv, pos0, qout, pos_dev);
+    else if (a.hd == 128) hipLaunchKernelGGL(k_attn_prep_rows<128>, grid, dim3(256), 0, s, a, qkv, pos0, qout, pos_dev);
+    else if (a.hd == 192) hipLaunchKernelGGL(k_attn_prep_rows<192>, grid, dim3(256), 0, s, a, qkv, pos0, qout, pos_dev);
+    else if (a.hd == 256) hipLaunchKernelGGL(k_attn_prep_rows<256>, grid, dim3(256), 0, s, a, qkv, pos0, qout, pos_dev);
+    else hipLaunchKernelGGL(k_attn_prep_rows<512>, grid, dim3(256), 0, s, a, qkv, pos0, qout, pos_dev);
     return hipGetLastError();
 }
 

@@ -79,7 +79,8 @@ __global__ __launch_bounds__(256) void k_gelu_mul(float *g, size_t gs, const flo
 // pos0 + token, in place; rows of n_head * hd floats; rope table rows of hd
 // (cos, sin pairs)
 __global__ __launch_bounds__(256) void k_head_prep(float *q, int n_head, int hd, const float *w, const float *rope, int pos0,
-                                                   float eps) {
+                                                   float eps, const int *pos_dev) {
+    if (pos_dev) pos0 = *pos_dev;
     __shared__ double red[4];
     __shared__ float y[512];
     float *x = q + ((size_t)blockIdx.y * n_head + blockIdx.x) * hd;
@@ -140,9 +141,9 @@ hipError_t launch_gelu_mul(float *g, size_t gs, const float *u, size_t us, int n
     return hipGetLastError();
 }
 hipError_t launch_head_prep(float *q, int n_head, int hd, int nb, const float *w, const float *rope, int pos0, float eps,
-                            hipStream_t s) {
+                            hipStream_t s, const int *pos_dev) {
     if (hd > 512 || hd % 2) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_head_prep, dim3(n_head, nb), dim3(256), 0, s, q, n_head, hd, w, rope, pos0, eps);
+    hipLaunchKernelGGL(k_head_prep, dim3(n_head, nb), dim3(256), 0, s, q, n_head, hd, w, rope, pos0, eps, pos_dev);
     return hipGetLastError();
 }
 hipError_t launch_pack_qkv(const float *q, const float *k, const float *v, float *qkv, int nq, int hd, int nb, hipStream_t s) {

@@ -126,11 +126,11 @@ __device__ __forceinline__ void q4k_sm(const uint8_t *s, int j, int &sc, int &mn
 // One thread per element; every product below is exact in fp32, so only the
 // final subtraction rounds (as in quants.c:364-495).
 __global__ __launch_bounds__(256) void k_dequant(int type, const uint8_t *__restrict__ x, size_t xs, float *__restrict__ y,
-                                                 size_t ys, int64_t n, int rows) {
+                                                 size_t ys, int64_t n, int rows, const int *__restrict__ ridx) {
     const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
     if (gid >= n * rows) return;
     const int64_t r = gid / n, e = gid - r * n;
-    const uint8_t *row = x + r * xs;
+    const uint8_t *row = x + (ridx ? (int64_t)ridx[r] : r) * xs;       // ridx: source rows chosen on the device
     float out;
     switch (type) {
     case Q8_0: {
@@ -319,8 +319,9 @@ hipError_t launch_quantize_q4_0(const float *x, size_t xs, uint8_t *y, size_t ys
     hipLaunchKernelGGL(k_quantize_q4_0, dim3(nblocks((int64_t)rows * nb * 8)), dim3(256), 0, s, x, xs, y, ys, nb, rows);
     return hipGetLastError();
 }
-hipError_t launch_dequant(int type, const uint8_t *x, size_t xs, float *y, size_t ys, int64_t n, int rows, hipStream_t s) {
-    hipLaunchKernelGGL(k_dequant, dim3(nblocks(n * rows)), dim3(256), 0, s, type, x, xs, y, ys, n, rows);
+hipError_t launch_dequant(int type, const uint8_t *x, size_t xs, float *y, size_t ys, int64_t n, int rows, hipStream_t s,
+                          const int *ridx) {
+    hipLaunchKernelGGL(k_dequant, dim3(nblocks(n * rows)), dim3(256), 0, s, type, x, xs, y, ys, n, rows, ridx);
     return hipGetLastError();
 }
 hipError_t launch_repack(const g4h_tensor &t, const uint8_t *rows, hipStream_t s) {

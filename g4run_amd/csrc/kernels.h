@@ -9,7 +9,10 @@ namespace g4 {
 hipError_t launch_quantize_q8_0(const float *x, size_t xs, uint8_t *y, size_t ys, int64_t n, int rows, hipStream_t s);
 hipError_t launch_quantize_q8_K(const float *x, size_t xs, uint8_t *y, size_t ys, int64_t n, int rows, hipStream_t s);
 hipError_t launch_quantize_q4_0(const float *x, size_t xs, uint8_t *y, size_t ys, int64_t n, int rows, hipStream_t s);
-hipError_t launch_dequant(int type, const uint8_t *x, size_t xs, float *y, size_t ys, int64_t n, int rows, hipStream_t s);
+// ridx (optional, device): output row r dequantizes source row ridx[r] (an
+// embedding gather whose token ids live on the device)
+hipError_t launch_dequant(int type, const uint8_t *x, size_t xs, float *y, size_t ys, int64_t n, int rows, hipStream_t s,
+                          const int *ridx = nullptr);
 hipError_t launch_repack(const g4h_tensor &t, const uint8_t *rows, hipStream_t s);
 hipError_t launch_unpack(const g4h_tensor &t, uint8_t *rows, hipStream_t s);
 hipError_t launch_vec_dot_raw(int wtype, const uint8_t *w, size_t ws, const uint8_t *a, int64_t n, int rows, float *out,
@@ -152,8 +155,9 @@ hipError_t launch_scale(float *y, int64_t n, float sc, hipStream_t s);
 hipError_t launch_ple_prep(const float *plp, float *pl, const float *w, int pe, int n_layer, int nb, float ps, float is2,
                            float eps, hipStream_t s);
 hipError_t launch_gelu_mul(float *g, size_t gs, const float *u, size_t us, int n, int nb, const uint16_t *tab, hipStream_t s);
+// pos_dev (optional, device): the first row's position instead of pos0
 hipError_t launch_head_prep(float *q, int n_head, int hd, int nb, const float *w, const float *rope, int pos0, float eps,
-                            hipStream_t s);
+                            hipStream_t s, const int *pos_dev = nullptr);
 hipError_t launch_pack_qkv(const float *q, const float *k, const float *v, float *qkv, int nq, int hd, int nb, hipStream_t s);
 hipError_t launch_softcap(float *l, int64_t n, float cap, hipStream_t s);
 
@@ -199,7 +203,8 @@ hipError_t launch_attn_batch(const float *q, const QkvArgs &a, int npos0, int nb
 // queries into qout [nb][n_head][hd], key and value rows into the caches at
 // pos0 .. pos0 + nb - 1 (on a ring both copies; at most ring - window + 1
 // tokens)
-hipError_t launch_attn_prep_rows(const float *qkv, const QkvArgs &a, int pos0, int nb, float *qout, hipStream_t s);
+hipError_t launch_attn_prep_rows(const float *qkv, const QkvArgs &a, int pos0, int nb, float *qout, hipStream_t s,
+                                 const int *pos_dev = nullptr);
 // Wo (optional, with wo_out): the output projection folded into the
 // one-launch form (attn_wo_fits), its rows into wo_out instead of a separate
 // GEMV on q8out's rows, with the same bits

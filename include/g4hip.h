@@ -376,6 +376,23 @@ int g4h_gemma_info(const g4h_gemma *g, int *n_vocab, int *n_embd, int *n_layer, 
  * Synchronous; G4H_ERR_TIMEOUT if a one-launch attention wait gave up (the
  * logits are then NaN). */
 int g4h_gemma_forward(g4h_gemma *g, const int *tokens, int nb, int pos0, float *logits_dev, float *hnext_dev, void *stream);
+/* The decode step of the gemma4 model driven from device state (g4_forward,
+ * g4run.h:309-311, as the synthetic model's g4h_forward_state): set_state puts
+ * (token, pos) on the device; each g4h_gemma_step runs the forward of that
+ * token at that position, its logits into g4h_gemma_logits, then token <- the
+ * first maximum of the logits and pos += 1 (at pos == n_ctx - 1 pos stays and
+ * g4h_gemma_status reports G4H_STATUS_CTX_FULL).  The step only enqueues work
+ * (no host synchronisation, no host-side token or position), so a stream
+ * capture of it is replayed once per token; run one step before capturing so
+ * the attention workspaces are set up outside the capture.  Its logits equal
+ * those of g4h_gemma_forward of the same token at the same position, bit for
+ * bit.  status also reports an attention wait that gave up
+ * (G4H_STATUS_ATTN_TIMEOUT). */
+int g4h_gemma_set_state(g4h_gemma *g, int token, int pos, void *stream);
+int g4h_gemma_step(g4h_gemma *g, void *stream);
+int g4h_gemma_get_state(g4h_gemma *g, int *token, int *pos, void *stream);
+int g4h_gemma_status(g4h_gemma *g, int *flags, void *stream);
+const float *g4h_gemma_logits(const g4h_gemma *g);
 /* Diagnostic (no reference counterpart): with trace_dev non-NULL, every later
  * g4h_gemma_forward copies each token's intermediate vectors into trace_dev
  * (fp32, *floats_per_token floats per token, token b's at b times that): the

@@ -18,6 +18,12 @@ SMALL = dict(n_layer=4, n_kv_shared=1, n_embd=256, n_head=4, head_dim_full=128, 
 WIDE = dict(n_layer=4, n_kv_shared=1, n_embd=512, n_head=8, head_dim_full=512, head_dim_swa=256,
             n_ff=[1024, 768, 1024, 1024], n_embd_per_layer=64, n_vocab=512, n_swa=16, is_swa=[1, 1, 0, 1],
             rope_base_full=1e6, rope_base_swa=1e4, rms_eps=1e-6, final_softcap=15.0)
+# the model bench.py times: 8 layers of width 2048, the reference's heads (8 x
+# 512 on full layers, 8 x 256 on sliding ones), two shared-KV layers (a sliding
+# one reading layer 4, a full one reading layer 5), FFN 6144, 32768 tokens
+BENCH = dict(n_layer=8, n_kv_shared=2, n_embd=2048, n_head=8, head_dim_full=512, head_dim_swa=256,
+             n_ff=[6144] * 8, n_embd_per_layer=256, n_vocab=32768, n_swa=512, is_swa=[1, 1, 1, 0, 1, 0, 1, 0],
+             rope_base_full=1e6, rope_base_swa=1e4, rms_eps=1e-6, final_softcap=30.0)
 
 
 def _bf16(x):

@@ -389,6 +389,44 @@ def test_attention_timeout_reported_then_recovers(gpu, oracle, tmp_path):
     m.free()
 
 
+@pytest.mark.parametrize("spec,kv_type", [("SMALL", 1), ("WIDE", 8), ("WIDE", 1)],
+                         ids=["small-f16", "wide-q8_0", "wide-f16"])
+def test_device_step_graph_equals_forward(gpu, oracle, tmp_path, spec, kv_type):
+    """g4h_gemma_step (device token and position) captured once and replayed
+    per token: every step's logits equal g4h_gemma_forward's on a second model
+    fed the same tokens, bit for bit, the state advances to the greedy token,
+    and the last position of the context is reported, not passed."""
+    G = gpu
+    hp, T = GM.make_gemma(oracle, 31, spec=getattr(GM, spec))
+    path = tmp_path / "g.gguf"
+    GM.write_gemma(path, hp, T)
+    n_ctx = 40
+    a, b = G.Gemma(path, n_ctx=n_ctx, kv_type=kv_type), G.Gemma(path, n_ctx=n_ctx, kv_type=kv_type)
+    toks = np.random.default_rng(3).integers(0, hp["n_vocab"], 20)
+    a.forward(toks, 0)
+    b.forward(toks, 0)
+    st = G.Stream()
+    a.set_state(5, 20, st.ptr)
+    a.step(st.ptr)                                      # outside the capture: workspaces set up
+    st.synchronize()
+    tok0 = int(toks[-1])
+    a.set_state(tok0, 20, st.ptr)
+    g = G.Graph(st.ptr, lambda: a.step(st.ptr))
+    tok = tok0
+    for pos in range(20, n_ctx):
+        g.launch(st.ptr)
+        st.synchronize()
+        lg = a.logits()
+        ref, _ = b.forward([tok], pos)
+        assert lg.tobytes() == ref[0].tobytes(), f"pos {pos}: step logits differ from the forward"
+        tok = int(np.argmax(ref[0]))
+        t, p = a.get_state(st.ptr)
+        assert t == tok and p == min(pos + 1, n_ctx - 1)
+    assert a.status(st.ptr) == G.STATUS_CTX_FULL
+    a.free()
+    b.free()
+
+
 def _ok(oracle, tmp_path):
     hp, T = GM.make_gemma(oracle, 14)
     p = tmp_path / "ok.gguf"
