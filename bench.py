@@ -299,18 +299,18 @@ def bench_steady(G, stream):
     return out
 
 
-def bench_prefill(G, stream, Ms=(1, 8, 16, 32, 64, 128, 256, 512)):
-    """q8_0 4096x4096 x M tokens on the GEMV family (path 1)
-    and on the int8 matrix cores (path 2); weights rotated beyond the MALL,
+def _prefill_rows(G, stream, qt, rows, cols, Ms, seed):
+    """q x M-token matmuls of one weight shape on the GEMV family (path 1) and
+    on the int8 matrix cores (path 2); weights rotated beyond the MALL,
     activations quantized in the call (x fp32 resident)."""
     from g4run_amd import synth
-    rows = cols = 4096
-    s = GemvSet(G, G.Q8_0, rows, cols, copies_for(rows * G.row_size(G.Q8_0, cols)), seed=1234)
+    s = GemvSet(G, qt, rows, cols, copies_for(rows * G.row_size(qt, cols)), seed=seed)
+    ast = G.act_stride(qt, cols)
     out = {}
     for M in Ms:
         xb = G.Buffer.from_array(synth.activations(M, cols, seed=99))
         Yb = G.Buffer(M * rows * 4)
-        alg = s.bytes - G.act_stride(G.Q8_0, cols) - rows * 4 + M * (G.act_stride(G.Q8_0, cols) + rows * 4)
+        alg = s.bytes - ast - rows * 4 + M * (ast + rows * 4)
         ops = 2.0 * M * rows * cols
         row = {"alg_bytes": int(alg), "gops": round(ops / 1e9, 3)}
         for path, name in ((1, "gemv"), (2, "mfma")):
@@ -323,11 +323,22 @@ def bench_prefill(G, stream, Ms=(1, 8, 16, 32, 64, 128, 256, 512)):
                          "kernel": G.matmul_describe(s.W[0], M, path).split(";")[0]}
         row["auto_path"] = G.matmul_path(s.W[0], M)
         out[str(M)] = row
-        log(f"bench: prefill M={M}: gemv {row['gemv']['us']} us, mfma {row['mfma']['us']} us "
-            f"({row['mfma']['TOPS']} TOPS, {row['mfma']['GBps']} GB/s)")
+        log(f"bench: prefill {G.TYPE_NAMES[qt]} {rows}x{cols} M={M}: gemv {row['gemv']['us']} us, "
+            f"mfma {row['mfma']['us']} us ({row['mfma']['TOPS']} TOPS, {row['mfma']['GBps']} GB/s)")
     for t in s.W:
         t.free()
     return out
+
+
+def bench_prefill(G, stream, Ms=(1, 8, 16, 32, 64, 128, 256, 512)):
+    """q8_0 4096x4096 x M tokens."""
+    return _prefill_rows(G, stream, G.Q8_0, 4096, 4096, Ms, seed=1234)
+
+
+def bench_prefill_kquant(G, stream, Ms=(8, 9, 16, 64, 512)):
+    """q4_K and q6_K weights (configs[2]'s 4096x11008, the formats gemma GGUFs
+    carry) x M tokens on both families."""
+    return {G.TYPE_NAMES[qt]: _prefill_rows(G, stream, qt, 4096, 11008, Ms, seed=4321) for qt in (G.Q4_K, G.Q6_K)}
 
 
 def bench_attention(G, stream, n_pos=8192, n_head=8, n_kv=4, hd=256, k=200):
@@ -608,6 +619,8 @@ def main():
                     help="direct launches instead of graph replays (for rocprofv3 --kernel-trace runs)")
     ap.add_argument("--prefill", default="1,8,64,512", metavar="M,...",
                     help="token counts of config 3 (GEMV vs matrix-core crossover); '' skips it")
+    ap.add_argument("--prefill-k", default="8,16,64,512", metavar="M,...",
+                    help="token counts of the q4_K / q6_K 4096x11008 prefill rows; '' skips them")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="start with one 256 MiB device copy (the reference dispatch for rocprofv3 --pmc byte counters)")
     args = ap.parse_args()
@@ -678,6 +691,7 @@ def main():
     steady = None if args.no_steady else bench_steady(G, stream)
     prefill_ms = args.prefill
     prefill = bench_prefill(G, stream, tuple(int(m) for m in prefill_ms.split(","))) if prefill_ms else None
+    prefill_k = bench_prefill_kquant(G, stream, tuple(int(m) for m in args.prefill_k.split(","))) if args.prefill_k else None
     attention = bench_attention(G, stream)
 
     cpu = None if args.no_cpu else cpu_baseline(sets, args.cpu_seconds)
@@ -716,6 +730,8 @@ def main():
         out["configs"] = extra
     if prefill:
         out["prefill"] = prefill
+    if prefill_k:
+        out["prefill_kquant"] = prefill_k
     out["attention"] = attention
     if decode:
         out["decode"] = decode

@@ -442,7 +442,7 @@ static bool x_fused(const g4h_tensor &W, int nb) {
 // takes a second launch.
 static constexpr int kMfmaMinTokens = 9;
 
-static bool mfma_capable(const g4h_tensor *W) { return W && (W->type == Q8_0 || W->type == Q4_0); }
+static bool mfma_capable(const g4h_tensor *W) { return W && (W->type == Q8_0 || W->type == Q4_0 || mmk_capable(W->type)); }
 
 extern "C" int g4h_matmul_path(const g4h_tensor *W, int nb) {
     return mfma_capable(W) && nb >= kMfmaMinTokens ? 2 : 1;
@@ -468,8 +468,9 @@ extern "C" int g4h_matmul_describe(const g4h_tensor *W, int nb, int path, char *
     if (!W || !buf || len == 0 || nb <= 0 || path < 0 || path > 2) return fail(G4H_ERR_ARG, "g4h_matmul_describe: bad argument");
     if (path == 0) path = g4h_matmul_path(W, nb);
     if (path == 2) {
-        if (!mfma_capable(W)) return fail(G4H_ERR_TYPE, "g4h_matmul_describe: the matrix-core path takes q8_0 / q4_0 weights");
-        mm_describe(*W, nb, buf, len);
+        if (!mfma_capable(W)) return fail(G4H_ERR_TYPE, "g4h_matmul_describe: the matrix-core path takes q8_0 / q4_0 / q4_K / q6_K weights");
+        if (mmk_capable(W->type)) mmk_describe(*W, nb, buf, len);
+        else mm_describe(*W, nb, buf, len);
         return G4H_OK;
     }
     if (is_float(W->type)) {
@@ -548,8 +549,28 @@ static int matmul_impl(const g4h_tensor *W, const float *x, const void *pre, siz
     if (nb == 0) return G4H_OK;
     const hipStream_t s = (hipStream_t)stream;
     if (path == 0) path = g4h_matmul_path(W, nb);
+    if (path == 2 && mfma_capable(W) && mmk_capable(W->type)) {
+        // K-quants: q8_K activation rows (quantized here from x, or given), read as they are
+        const uint8_t *act = (const uint8_t *)pre;
+        size_t stride = pre_stride;
+        if (x) {
+            if ((uintptr_t)x % 4) return fail(G4H_ERR_ARG, "g4h_matmul: x must be 4-byte aligned");
+            stride = g4h_act_stride(W->type, W->ncols);
+            void *buf;
+            if (int rc = scr.get(s, stride * nb, &buf)) return rc;
+            const hipError_t e = launch_quantize_q8_K(x, W->ncols, (uint8_t *)buf, stride, W->ncols, nb, s);
+            if (e != hipSuccess) return hip_fail(e, "g4h_matmul: quantize");
+            act = (const uint8_t *)buf;
+        } else {
+            if (int rc = check_act("g4h_matmul", W, pre, pre_stride, nb)) return rc;
+            if (nb == 1) stride = g4h_act_stride(W->type, W->ncols);
+        }
+        const hipError_t e = launch_matmul_mfma_k(*W, act, stride, nb, Y, s);
+        if (e != hipSuccess) return hip_fail(e, "g4h_matmul: matrix-core launch");
+        return G4H_OK;
+    }
     if (path == 2) {
-        if (!mfma_capable(W)) return fail(G4H_ERR_TYPE, "g4h_matmul: the matrix-core path takes q8_0 / q4_0 weights");
+        if (!mfma_capable(W)) return fail(G4H_ERR_TYPE, "g4h_matmul: the matrix-core path takes q8_0 / q4_0 / q4_K / q6_K weights");
         if (x && (uintptr_t)x % 16) return fail(G4H_ERR_ARG, "g4h_matmul: x must be 16-byte aligned on the matrix-core path");
         if (!x)
             if (int rc = check_act("g4h_matmul", W, pre, pre_stride, nb)) return rc;

@@ -167,6 +167,12 @@ void mm_describe(const g4h_tensor &W, int M, char *buf, size_t len);
 hipError_t launch_matmul_mfma(const g4h_tensor &W, const float *x, size_t x_stride, const uint8_t *act, size_t stride, int M,
                               float *Y, uint8_t *ws, hipStream_t s);
 
+// k_mfma_k.hip: many-token matmul on the int8 matrix cores for q4_K / q6_K
+// weights against GGUF q8_K activation rows at `stride` bytes
+bool mmk_capable(int type);
+void mmk_describe(const g4h_tensor &W, int M, char *buf, size_t len);
+hipError_t launch_matmul_mfma_k(const g4h_tensor &W, const uint8_t *act, size_t stride, int M, float *Y, hipStream_t s);
+
 // k_attn.hip
 size_t attn_workspace_bytes(int n_head, int hd, int npos_max);
 // drop a workspace from the cleared-workspace registry (its memory is freed)

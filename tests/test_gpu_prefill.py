@@ -1,6 +1,7 @@
 """GPU parity of the batched-prefill matmul on the int8 matrix cores (path 2)
-against the CPU oracle's shipped-order dots (q8_0 4096x4096
-x M tokens), plus its batch-size invariance and error paths.
+against the CPU oracle's shipped-order dots (q8_0 4096x4096 x M tokens, q4_0
+FFN shapes, q4_K / q6_K 4096x11008), plus its batch-size invariance and error
+paths.
 
 The per-block integer sums come out of one int8 MFMA per block and are exact
 by construction; the fp32 results must be within |gpu - cpu| <= 1e-5 +
@@ -79,8 +80,12 @@ def test_path_selection_and_errors(gpu):
     from g4run_amd import synth
     G = gpu
     t8 = G.Tensor.from_rows(8, synth.weights(8, 64, 256, seed=1), 256)
-    tk = G.Tensor.from_rows(12, synth.weights(12, 64, 256, seed=1), 256)
     assert [G.matmul_path(t8, n) for n in (1, 8, 9, 16, 512)] == [1, 1, 2, 2, 2]
+    for qt in (12, 14):
+        t = G.Tensor.from_rows(qt, synth.weights(qt, 64, 256, seed=1), 256)
+        assert [G.matmul_path(t, n) for n in (1, 8, 9, 512)] == [1, 1, 2, 2]
+        assert G.matmul_describe(t, 64, 2).startswith("k_mmk")
+    tk = G.Tensor.from_rows(13, synth.weights(13, 64, 256, seed=1), 256)
     assert G.matmul_path(tk, 512) == 1
     Y = G.Buffer(64 * 16 * 4)
     x = G.Buffer.from_array(synth.activations(16, 256, seed=2))
@@ -119,4 +124,86 @@ def test_few_kernel_prequantized_rows(gpu, oracle, qt):
     a = gpu_matmul(gpu, t, x=x, nb=37, path=2)
     b = gpu_matmul(gpu, t, act=oracle.prep_act(qt, x), nb=37, path=2)
     assert gpu.matmul_describe(t, 37, 2).startswith("k_mm_few")
+    assert np.array_equal(bits(a), bits(b))
+
+
+# ------------------------------------------------- K-quant weights (k_mmk)
+KQ = [("q4_K", 12), ("q6_K", 14)]
+
+
+@pytest.mark.parametrize("name,qt", KQ)
+@pytest.mark.parametrize("M", [64, 512])
+def test_kquant_config_vs_oracle(gpu, oracle, name, qt, M):
+    w, x, t = _setup(gpu, qt, 4096, 11008, M, seed=77 + qt)
+    assert gpu.matmul_describe(t, M, 2).startswith("k_mmk")
+    assert gpu.matmul_path(t, M) == 2
+    assert_close(gpu_matmul(gpu, t, x=x, nb=M), oracle_matmul(oracle, qt, w, x), f"{name} 4096x11008 M={M}")
+
+
+def _unit_scales(qt, w, cols, which):
+    """Copies of GGUF rows with every superblock's fp16 scales set so that the
+    row's output is an integer: q4_K d = 1, dmin = 0 ('isum') or d = 0,
+    dmin = 1 ('msum'); q6_K d = 1."""
+    w = np.array(w, dtype=np.uint8).reshape(w.shape[0], cols // 256, -1)
+    one, zero = np.uint16(0x3C00), np.uint16(0)
+    if qt == 12:
+        hdr = w[:, :, 0:4].copy().view(np.uint16)
+        hdr[..., 0] = one if which == "isum" else zero
+        hdr[..., 1] = zero if which == "isum" else one
+        w[:, :, 0:4] = hdr.view(np.uint8)
+    else:
+        w[:, :, 208:210] = np.frombuffer(one.tobytes(), np.uint8)
+    return w.reshape(w.shape[0], -1)
+
+
+@pytest.mark.parametrize("name,qt,which", [("q4_K", 12, "isum"), ("q4_K", 12, "msum"), ("q6_K", 14, "isum")])
+@pytest.mark.parametrize("rows,cols,M", [(96, 2048, 40), (33, 256, 9)])
+def test_kquant_superblock_sums_exact(gpu, oracle, name, qt, which, rows, cols, M):
+    """With unit scales (weight d or dmin 1, activation d 1) every output is
+    the sum of the row's exact per-superblock integers: q4_K's sum_j sc_j q.a
+    (or minus sum_j m_j bsum), q6_K's sum_s sc_s (q - 32).a.  The GPU's must
+    equal the oracle's block sums to the bit (each partial sum stays below
+    2^24, where fp32 holds integers exactly)."""
+    from g4run_amd import synth
+    w = _unit_scales(qt, synth.weights(qt, rows, cols, seed=rows + M), cols, which)
+    act = oracle.prep_act(qt, synth.activations(M, cols, seed=cols + M))
+    for b in range(cols // 256):
+        act[:, 292 * b:292 * b + 4] = np.frombuffer(np.float32(1.0).tobytes(), np.uint8)
+    t = gpu.Tensor.from_rows(qt, w, cols)
+    y = gpu_matmul(gpu, t, act=act, nb=M, path=2)
+    k = 0 if which == "isum" else 1          # q4_K sums come in (isum, msum) pairs per superblock
+    exp = np.zeros((M, rows), np.int64)
+    for m in range(M):
+        s = oracle.block_sums(qt, w, act[m], cols).astype(np.int64)
+        s = s[:, k::2] if qt == 12 else s
+        assert np.abs(np.cumsum(s, axis=1)).max() < 1 << 24
+        exp[m] = s.sum(axis=1) if which == "isum" else -s.sum(axis=1)
+    assert np.array_equal(y.astype(np.int64), exp), f"{name} {which} {rows}x{cols} M={M}"
+    assert np.array_equal(y, exp.astype(np.float32))
+
+
+@pytest.mark.parametrize("name,qt", KQ)
+def test_kquant_ragged_shapes(gpu, oracle, name, qt):
+    """Row counts off the 32-row tile, token counts off the 32-token tile and
+    the 128-token workgroup, one superblock per row."""
+    for rows, cols, M in ((1, 256, 1), (31, 512, 17), (100, 2304, 33), (65, 768, 65), (257, 1024, 100), (33, 4096, 129)):
+        w, x, t = _setup(gpu, qt, rows, cols, M, seed=rows + cols)
+        assert_close(gpu_matmul(gpu, t, x=x, nb=M, path=2), oracle_matmul(oracle, qt, w, x), f"{name} {rows}x{cols} M={M}")
+
+
+@pytest.mark.parametrize("name,qt", KQ)
+def test_kquant_token_results_independent_of_batch(gpu, oracle, name, qt):
+    w, x, t = _setup(gpu, qt, 320, 2560, 300, seed=13)
+    full = gpu_matmul(gpu, t, x=x, nb=300, path=2)
+    assert_close(full, oracle_matmul(oracle, qt, w, x), f"{name} M=300")
+    for m in (9, 32, 33, 100, 128, 129, 257):
+        part = gpu_matmul(gpu, t, x=x[:m].copy(), nb=m, path=2)
+        assert np.array_equal(bits(part), bits(full[:m])), f"{name} M={m}"
+
+
+@pytest.mark.parametrize("name,qt", KQ)
+def test_kquant_fused_quantizer_equals_prequantized(gpu, oracle, name, qt):
+    w, x, t = _setup(gpu, qt, 130, 2816, 45, seed=21)
+    a = gpu_matmul(gpu, t, x=x, nb=45, path=2)
+    b = gpu_matmul(gpu, t, act=oracle.prep_act(qt, x), nb=45, path=2)
     assert np.array_equal(bits(a), bits(b))
