@@ -428,7 +428,7 @@ def bench_gemma(G, pos_fill=1024, steps=64):
         g = G.Gemma(path, n_ctx=pos_fill + steps + 64)
         rs = np.random.default_rng(8)
         for p0 in range(0, pos_fill, 64):
-            g.forward(rs.integers(0, g.n_vocab, 64).astype(np.int32), p0)
+            g.prefill(rs.integers(0, g.n_vocab, 64).astype(np.int32), p0, want_logits=False)
         toks = rs.integers(0, g.n_vocab, steps).astype(np.int32)
         G.synchronize()
         t0 = time.perf_counter()
@@ -456,17 +456,24 @@ def bench_gemma(G, pos_fill=1024, steps=64):
         g.forward(rs.integers(0, g.n_vocab, 64).astype(np.int32), pos_fill + steps)
         G.synchronize()
         ms64 = (time.perf_counter() - t0) * 1e3
+        t0 = time.perf_counter()                                   # the same 64 positions again, as a prompt chunk
+        g.prefill(rs.integers(0, g.n_vocab, 64).astype(np.int32), pos_fill + steps)
+        G.synchronize()
+        ms_pf = (time.perf_counter() - t0) * 1e3
         g.free()
     finally:
         os.unlink(path)
     return {"decode_tok_per_s": round(1e3 / ms, 1), "ms_per_token": round(ms, 4),
-            "host_driven_tok_per_s": round(1e3 / ms_host, 1), "batch_64_ms": round(ms64, 2), "file_bytes": nbytes,
+            "host_driven_tok_per_s": round(1e3 / ms_host, 1), "batch_64_ms": round(ms64, 2),
+            "prefill_64_ms": round(ms_pf, 2), "prefill_64_tok_per_s": round(64e3 / ms_pf, 1), "file_bytes": nbytes,
             "what": f"gemma4 from a synthetic {nbytes / 1e6:.0f} MB GGUF (g4h_gemma_open: mmap reader, upload and "
                     "repack): 8 layers (5 sliding-window on the KV ring, 3 full, 2 of them shared-KV), width 2048, "
                     "8 heads x 512 (full) / 256 (sliding) over one KV head, FFN 6144, per-layer embeddings 256, 32768 "
                     "tokens, soft-cap; q8_0/q4_0/q4_K/q6_K/f16/bf16 weights; greedy decode steps at positions "
                     f"{pos_fill}..{pos_fill + steps - 1} as replays of one captured g4h_gemma_step (the host-driven "
-                    "g4h_gemma_forward beside it); and one 64-token batch"}
+                    "g4h_gemma_forward beside it); one 64-token batch with every position's logits "
+                    "(g4h_gemma_forward, decode-identical rows) and one 64-token prompt chunk (g4h_gemma_prefill, "
+                    "matrix-core projections, last logits)"}
 
 
 def bench_next(G, m):

@@ -127,6 +127,7 @@ _SIGS = [
     ("g4h_gemma_free", _int, [_vp]),
     ("g4h_gemma_info", _int, [_vp, C.POINTER(_int), C.POINTER(_int), C.POINTER(_int), C.POINTER(_int)]),
     ("g4h_gemma_forward", _int, [_vp, C.POINTER(_int), _int, _int, _vp, _vp, _vp]),
+    ("g4h_gemma_prefill", _int, [_vp, C.POINTER(_int), _int, _int, _vp, _vp]),
     ("g4h_read_floor", _int, [_vp, _sz, _vp, C.c_int64, _int, _int, _vp]),
     ("g4h_gemma_trace", _int, [_vp, _vp, C.POINTER(_sz)]),
     ("g4h_gemma_set_state", _int, [_vp, _int, _int, _vp]),
@@ -500,6 +501,14 @@ class Gemma:
         L, Hn = Buffer(nb * self.n_vocab * 4), Buffer(nb * self.n_embd * 4)
         check(lib().g4h_gemma_forward(self.ptr, t.ctypes.data_as(C.POINTER(_int)), nb, pos0, L.ptr, Hn.ptr, stream))
         return L.download(np.float32, (nb, self.n_vocab)), Hn.download(np.float32, (nb, self.n_embd))
+
+    def prefill(self, tokens, pos0: int, want_logits: bool = True, stream=None):
+        """g4h_gemma_prefill: the last position's logits (or None)."""
+        t = np.ascontiguousarray(tokens, dtype=np.int32).ravel()
+        L = Buffer(self.n_vocab * 4) if want_logits else None
+        check(lib().g4h_gemma_prefill(self.ptr, t.ctypes.data_as(C.POINTER(_int)), t.size, pos0, L.ptr if L else None,
+                                      stream))
+        return L.download(np.float32, (self.n_vocab,)) if L else None
 
     def set_state(self, token: int, pos: int, stream=None) -> None:
         check(lib().g4h_gemma_set_state(self.ptr, token, pos, stream))

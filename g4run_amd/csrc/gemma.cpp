@@ -300,10 +300,11 @@ int create(const g4_model_file *mf, int n_ctx, int kv_type, g4h_gemma *m) {
     return G4H_OK;
 }
 
-// Y[b] = W x[b], x rows of W->ncols floats prepared in W's activation class
-// (the GEMV family: token rows bit-identical for any count)
-int mm(const g4h_tensor *W, const float *x, float *Y, int nb, hipStream_t s) {
-    return g4h_matmul_ex(W, x, nullptr, 0, Y, nb, 1, s);
+// Y[b] = W x[b], x rows of W->ncols floats prepared in W's activation class;
+// `path` of g4h_matmul_ex: 1, the GEMV family (token rows bit-identical for any
+// count), or 0 (prompt prefill: the int8 matrix cores from 9 tokens)
+int mm(const g4h_tensor *W, const float *x, float *Y, int nb, int path, hipStream_t s) {
+    return g4h_matmul_ex(W, x, nullptr, 0, Y, nb, path, s);
 }
 
 // floats of one token's trace: the per-layer inputs, n_layer records of
@@ -376,10 +377,12 @@ extern "C" int g4h_gemma_info(const g4h_gemma *m, int *n_vocab, int *n_embd, int
 // The forward of nb tokens whose ids are in tok_dev (device) at positions
 // pos0 .. pos0 + nb - 1; with `st` (one token, the decode state token | pos |
 // npos on the device) the position comes from st instead, and the call is
-// stream-ordered only (graph-capturable).  Every position's logits go to
-// logits_dev, the head inputs to hnext_dev if given.
+// stream-ordered only (graph-capturable).  With `last` false every position's
+// logits go to logits_dev, the head inputs to hnext_dev if given; with `last`
+// true only the last position's logits, if logits_dev (g4_forward_batch).
+// `path` is the projections' matmul path (mm).
 static int run(g4h_gemma *m, const int *tok_dev, int nb, int pos0, const int *st, float *logits_dev, float *hnext_dev,
-               hipStream_t s) {
+               int path, bool last, hipStream_t s) {
     const int *pos_dev = st ? st + 1 : nullptr, *npos_dev = st ? st + 2 : nullptr;
     const int E = m->E, H = m->H, PE = m->PE, NPL = m->n_layer * PE;
     const float eps = m->eps;
@@ -404,7 +407,7 @@ static int run(g4h_gemma *m, const int *tok_dev, int nb, int pos0, const int *st
     G_HIP(launch_scale(m->x, (int64_t)nb * E, sqrtf((float)E), s));
     G_HIP(launch_scale(m->pl, (int64_t)nb * NPL, sqrtf((float)PE), s));
     // per-layer input projection (model.c:617-635)
-    G_RC(mm(m->ple_proj, m->x, m->plp, nb, s));
+    G_RC(mm(m->ple_proj, m->x, m->plp, nb, path, s));
     G_HIP(launch_ple_prep(m->plp, m->pl, m->ple_norm, PE, m->n_layer, nb, 1.0f / sqrtf((float)E), 1.0f / sqrtf(2.0f), eps, s));
     G_RC(tr(0, m->pl, NPL, NPL));
 
@@ -414,7 +417,7 @@ static int run(g4h_gemma *m, const int *tok_dev, int nb, int pos0, const int *st
         const float *rope = L.swa ? m->rope_swa : m->rope_full;
         G_RC(trl(il, T_X, m->x, E, E));
         G_HIP(launch_rms_rows(m->x, L.attn_norm, m->xb, E, nb, eps, s));
-        G_RC(mm(L.wq, m->xb, m->q, nb, s));
+        G_RC(mm(L.wq, m->xb, m->q, nb, path, s));
         G_RC(trl(il, T_Q, m->q, nq, nq));
         QkvArgs qa;
         qa.n_head = H;
@@ -431,8 +434,8 @@ static int run(g4h_gemma *m, const int *tok_dev, int nb, int pos0, const int *st
         uint8_t *ws = L.swa ? m->ws : m->wsf;
         if (il < m->n_layer_kv) {
             // own K/V: q | k | v prepared, stored at the position and attended in one step (model.c:664-689)
-            G_RC(mm(L.wk, m->xb, m->k, nb, s));
-            if (L.wv) G_RC(mm(L.wv, m->xb, m->v, nb, s));
+            G_RC(mm(L.wk, m->xb, m->k, nb, path, s));
+            if (L.wv) G_RC(mm(L.wv, m->xb, m->v, nb, path, s));
             G_RC(trl(il, T_K, m->k, hd, hd));
             if (L.wv) G_RC(trl(il, T_V, m->v, hd, hd));
             G_HIP(launch_pack_qkv(m->q, m->k, L.wv ? m->v : nullptr, m->qkv, nq, hd, nb, s));
@@ -457,54 +460,72 @@ static int run(g4h_gemma *m, const int *tok_dev, int nb, int pos0, const int *st
             else G_HIP(launch_attn_decode(m->q, nullptr, qa, pos0 + 1, npos_dev, npos_max, m->att, nullptr, ws, s));
         }
         G_RC(trl(il, T_ATT, m->att, nq, nq));
-        G_RC(mm(L.wo, m->att, m->xb, nb, s));
+        G_RC(mm(L.wo, m->att, m->xb, nb, path, s));
         G_RC(trl(il, T_WO, m->xb, E, E));
         G_HIP(launch_resid(m->x, m->xb, L.post_attn_norm, E, nb, eps, 1.0f, s));
         G_RC(trl(il, T_XMID, m->x, E, E));
         // FFN (model.c:718-736)
         G_HIP(launch_rms_rows(m->x, L.ffn_norm, m->xb, E, nb, eps, s));
-        G_RC(mm(L.gate, m->xb, m->g, nb, s));
-        G_RC(mm(L.up, m->xb, m->u, nb, s));
+        G_RC(mm(L.gate, m->xb, m->g, nb, path, s));
+        G_RC(mm(L.up, m->xb, m->u, nb, path, s));
         G_RC(trl(il, T_G, m->g, F, F));
         G_RC(trl(il, T_U, m->u, F, F));
         G_HIP(launch_gelu_mul(m->g, F, m->u, F, F, nb, m->gelu, s));
         G_RC(trl(il, T_H, m->g, F, F));
-        G_RC(mm(L.down, m->g, m->xb, nb, s));
+        G_RC(mm(L.down, m->g, m->xb, nb, path, s));
         G_RC(trl(il, T_DOWN, m->xb, E, E));
         G_HIP(launch_resid(m->x, m->xb, L.post_ffw_norm, E, nb, eps, 1.0f, s));
         G_RC(trl(il, T_XFFN, m->x, E, E));
         // per-layer embedding injection (model.c:738-752)
-        G_RC(mm(L.inp_gate, m->x, m->plg, nb, s));
+        G_RC(mm(L.inp_gate, m->x, m->plg, nb, path, s));
         G_RC(trl(il, T_PLG, m->plg, PE, PE));
         G_HIP(launch_gelu_mul(m->plg, PE, m->pl + (size_t)il * PE, NPL, PE, nb, m->gelu, s));
         G_RC(trl(il, T_PLH, m->plg, PE, PE));
-        G_RC(mm(L.proj, m->plg, m->xb, nb, s));
+        G_RC(mm(L.proj, m->plg, m->xb, nb, path, s));
         G_RC(trl(il, T_PROJ, m->xb, E, E));
         G_HIP(launch_resid(m->x, m->xb, L.post_norm, E, nb, eps, L.out_scale, s));
     }
     G_RC(tr((size_t)NPL + (size_t)m->n_layer * rec, m->x, E, E));
+    if (last) {
+        // the last token's head (model.c:757-776)
+        if (!logits_dev) return G4H_OK;
+        G_HIP(launch_rms_rows(m->x + (size_t)(nb - 1) * E, m->out_norm, m->hn, E, 1, eps, s));
+        G_RC(mm(m->head, m->hn, logits_dev, 1, 1, s));
+        if (m->softcap > 0) G_HIP(launch_softcap(logits_dev, m->V, m->softcap, s));
+        return G4H_OK;
+    }
     // every position's head (model.c:790-798)
     float *hn = hnext_dev ? hnext_dev : m->hn;
     G_HIP(launch_rms_rows(m->x, m->out_norm, hn, E, nb, eps, s));
-    G_RC(mm(m->head, hn, logits_dev, nb, s));
+    G_RC(mm(m->head, hn, logits_dev, nb, path, s));
     if (m->softcap > 0) G_HIP(launch_softcap(logits_dev, (int64_t)nb * m->V, m->softcap, s));
     return G4H_OK;
+}
+
+// the host tokens checked and uploaded, the forward run, its attention waits checked
+static int batch_call(g4h_gemma *m, const int *tokens, int nb, int pos0, float *logits_dev, float *hnext_dev, int path,
+                      bool last, hipStream_t s, const char *fn) {
+    if (nb < 1 || nb > kRows) return gfail(G4H_ERR_ARG, "%s: nb must be 1..64 (G4_BATCH_MAX)", fn);
+    if (pos0 < 0 || pos0 + nb > m->n_ctx) return gfail(G4H_ERR_ARG, "%s: positions outside the context", fn);
+    for (int b = 0; b < nb; b++)
+        if (tokens[b] < 0 || tokens[b] >= m->V) return gfail(G4H_ERR_ARG, "%s: token out of range", fn);
+    G_HIP(hipMemcpyAsync(m->tok, tokens, (size_t)nb * sizeof(int), hipMemcpyHostToDevice, s));
+    G_RC(run(m, m->tok, nb, pos0, nullptr, logits_dev, hnext_dev, path, last, s));
+    G_HIP(hipStreamSynchronize(s));
+    const int e0 = g4h_internal_attn_error(m->ws, s, fn);                 // both read and cleared
+    const int e1 = g4h_internal_attn_error(m->wsf, s, fn);
+    return e0 ? e0 : e1;
 }
 
 extern "C" int g4h_gemma_forward(g4h_gemma *m, const int *tokens, int nb, int pos0, float *logits_dev, float *hnext_dev,
                                  void *stream) {
     if (!m || !tokens || !logits_dev) return g4h_internal_fail(G4H_ERR_ARG, "g4h_gemma_forward: null argument");
-    if (nb < 1 || nb > kRows) return g4h_internal_fail(G4H_ERR_ARG, "g4h_gemma_forward: nb must be 1..64 (G4_BATCH_MAX)");
-    if (pos0 < 0 || pos0 + nb > m->n_ctx) return g4h_internal_fail(G4H_ERR_ARG, "g4h_gemma_forward: positions outside the context");
-    for (int b = 0; b < nb; b++)
-        if (tokens[b] < 0 || tokens[b] >= m->V) return g4h_internal_fail(G4H_ERR_ARG, "g4h_gemma_forward: token out of range");
-    const hipStream_t s = (hipStream_t)stream;
-    G_HIP(hipMemcpyAsync(m->tok, tokens, (size_t)nb * sizeof(int), hipMemcpyHostToDevice, s));
-    G_RC(run(m, m->tok, nb, pos0, nullptr, logits_dev, hnext_dev, s));
-    G_HIP(hipStreamSynchronize(s));
-    const int e0 = g4h_internal_attn_error(m->ws, s, "g4h_gemma_forward");   // both read and cleared
-    const int e1 = g4h_internal_attn_error(m->wsf, s, "g4h_gemma_forward");
-    return e0 ? e0 : e1;
+    return batch_call(m, tokens, nb, pos0, logits_dev, hnext_dev, 1, false, (hipStream_t)stream, "g4h_gemma_forward");
+}
+
+extern "C" int g4h_gemma_prefill(g4h_gemma *m, const int *tokens, int nb, int pos0, float *logits_dev, void *stream) {
+    if (!m || !tokens) return g4h_internal_fail(G4H_ERR_ARG, "g4h_gemma_prefill: null argument");
+    return batch_call(m, tokens, nb, pos0, logits_dev, nullptr, 0, true, (hipStream_t)stream, "g4h_gemma_prefill");
 }
 
 // ------------------------------------------------ device-driven decode --
@@ -521,7 +542,7 @@ extern "C" int g4h_gemma_set_state(g4h_gemma *m, int token, int pos, void *strea
 extern "C" int g4h_gemma_step(g4h_gemma *m, void *stream) {
     if (!m) return g4h_internal_fail(G4H_ERR_ARG, "g4h_gemma_step: null model");
     const hipStream_t s = (hipStream_t)stream;
-    G_RC(run(m, m->state, 1, 0, m->state, m->logits, nullptr, s));
+    G_RC(run(m, m->state, 1, 0, m->state, m->logits, nullptr, 1, false, s));
     G_HIP(launch_argmax_advance(m->logits, m->V, m->state, m->n_ctx, s));   // token <- first argmax, pos += 1
     return G4H_OK;
 }

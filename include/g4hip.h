@@ -376,6 +376,15 @@ int g4h_gemma_info(const g4h_gemma *g, int *n_vocab, int *n_embd, int *n_layer, 
  * Synchronous; G4H_ERR_TIMEOUT if a one-launch attention wait gave up (the
  * logits are then NaN). */
 int g4h_gemma_forward(g4h_gemma *g, const int *tokens, int nb, int pos0, float *logits_dev, float *hnext_dev, void *stream);
+/* g4_forward_batch (model.c:757-776), the prompt prefill of the gemma4 forward:
+ * nb (1..64) host token ids at positions pos0.. (K/V stored); then, if
+ * logits_dev, the last position's logits [n_vocab] (soft-capped).  The
+ * projections take g4h_matmul's automatic path, so from 9 tokens the q8_0,
+ * q4_0, q4_K and q6_K weights run on the int8 matrix cores, each weight
+ * matrix streamed once per batch; rows then differ from g4h_gemma_forward's
+ * within the matrix-core path's tolerance.  Synchronous; G4H_ERR_TIMEOUT as
+ * g4h_gemma_forward. */
+int g4h_gemma_prefill(g4h_gemma *g, const int *tokens, int nb, int pos0, float *logits_dev, void *stream);
 /* The decode step of the gemma4 model driven from device state (g4_forward,
  * g4run.h:309-311, as the synthetic model's g4h_forward_state): set_state puts
  * (token, pos) on the device; each g4h_gemma_step runs the forward of that

@@ -87,10 +87,12 @@ def _weight_slack(o, q, kc, vc, H, hd, pos, j0, slots):
 RING = 576
 
 
-def traced_forward(G, o, hp, T, m, kv_type, toks, pos0, n_ctx):
-    """m.forward(toks, pos0) with the per-token trace; then every part of every
+def traced_forward(G, o, hp, T, m, kv_type, toks, pos0, n_ctx, prefill=False):
+    """m.forward(toks, pos0) (or, with `prefill`, m.prefill: the last
+    position's logits only) with the per-token trace; then every part of every
     layer of every token against the oracle on the GPU's own inputs.  Returns
-    (logits, hnext) and the worst error per part."""
+    (logits, hnext) -- ([1][n_vocab], None) for a prefill -- and the worst
+    error per part."""
     toks = np.atleast_1d(np.asarray(toks, np.int64))
     nb = toks.size
     E, H, PE, NL, NKV = hp["n_embd"], hp["n_head"], hp["n_embd_per_layer"], hp["n_layer"], hp["n_layer_kv"]
@@ -106,7 +108,10 @@ def traced_forward(G, o, hp, T, m, kv_type, toks, pos0, n_ctx):
     tb = G.Buffer(nb * m.trace(None) * 4)
     tf = m.trace(tb)
     try:
-        lg, hn = m.forward(toks, pos0)
+        if prefill:
+            lg, hn = m.prefill(toks, pos0)[None], None
+        else:
+            lg, hn = m.forward(toks, pos0)
     finally:
         m.trace(None)
     tr = tb.download(np.float32, (nb, tf))
@@ -220,15 +225,17 @@ def traced_forward(G, o, hp, T, m, kv_type, toks, pos0, n_ctx):
             xo = (xffn + o.rms_norm(proj, vec(p + "post_norm.weight"), eps)) * np.float32(sc[0] if sc is not None else 1.0)
             xn = tr[b, NPL + (il + 1) * rec:NPL + (il + 1) * rec + E] if il + 1 < NL else tr[b, NPL + NL * rec:]
             note("x'", _close(xn, xo, f"{tag} layer output"))
-    # every position's head with the soft-cap (model.c:790-798)
-    for b in range(nb):
+    # every position's head with the soft-cap (model.c:790-798), or the last
+    # one's (model.c:766-775)
+    for i, b in enumerate([nb - 1] if prefill else range(nb)):
         hnr = o.rms_norm(tr[b, NPL + NL * rec:], vec("output_norm.weight"), eps)
-        note("hnext", _close(hn[b], hnr, f"token {b} head input"))
-        lr = mm("token_embd.weight", hn[b])
+        if not prefill:
+            note("hnext", _close(hn[b], hnr, f"token {b} head input"))
+        lr = mm("token_embd.weight", hnr if prefill else hn[b])
         cap = hp.get("final_softcap", 0.0)
         if cap > 0:
             lr = (cap * np.tanh(lr.astype(np.float64) / cap)).astype(np.float32)
-        note("logits", _close(lg[b], lr, f"token {b} logits"))
+        note("logits", _close(lg[i], lr, f"token {b} logits"))
     return lg, hn, worst
 
 
@@ -332,6 +339,45 @@ def test_ring_wrap_and_batch_equals_single_tokens(gpu, oracle, tmp_path, kv_type
     single = [b.forward([toks[p]], p)[0] for p in range(610)]
     b.free()
     assert np.concatenate(rows).tobytes() == np.concatenate(single).tobytes()
+
+
+@pytest.mark.parametrize("kv_type", [8, 1], ids=["q8_0", "f16"])
+@pytest.mark.parametrize("spec", ["SMALL", "WIDE"])
+def test_prefill_on_matrix_cores_part_by_part(gpu, oracle, tmp_path, spec, kv_type):
+    """g4h_gemma_prefill (g4_forward_batch, model.c:757-776): batches of 9 or
+    more tokens run the q8_0 / q4_0 / q4_K / q6_K projections on the int8
+    matrix cores.  Every part of every token is held against the oracle on the
+    GPU's own inputs (the K/V rows stored bit for bit), the last logits
+    against the oracle's forward, and decode steps then run on the caches the
+    prefill wrote."""
+    G = gpu
+    hp, T = GM.make_gemma(oracle, 31, spec=getattr(GM, spec))
+    path = tmp_path / "g.gguf"
+    GM.write_gemma(path, hp, T)
+    n_ctx = 96
+    m = G.Gemma(path, n_ctx=n_ctx, kv_type=kv_type)
+    om = oracle.Gemma(hp, T, kv_type, n_ctx)
+    toks = np.random.default_rng(17).integers(0, hp["n_vocab"], 64)
+    pos = 0
+    oracle.pool_start(8)
+    try:
+        for nb in (33, 9, 16):
+            lg, _, _ = traced_forward(G, oracle, hp, T, m, kv_type, toks[pos:pos + nb], pos, n_ctx, prefill=True)
+            olg, ohn = om.forward(toks[pos:pos + nb], pos, nthreads=8)
+            compare(f"prefill@{pos}", lg, olg[-1:], ohn[-1:], ohn[-1:])
+            pos += nb
+        assert m.prefill(toks[pos:pos + 3], pos, want_logits=False) is None
+        om.forward(toks[pos:pos + 3], pos, nthreads=8)
+        pos += 3
+        tok = int(toks[pos])
+        for _ in range(3):
+            lg, hn, _ = traced_forward(G, oracle, hp, T, m, kv_type, [tok], pos, n_ctx)
+            olg, ohn = om.forward([tok], pos, nthreads=8)
+            compare(f"decode@{pos}", lg, olg, hn, ohn)
+            tok, pos = int(np.argmax(olg[0])), pos + 1
+    finally:
+        oracle.pool_stop()
+        m.free()
 
 
 def test_model_file_errors(gpu, oracle, tmp_path):
