@@ -141,9 +141,10 @@ int g4h_matmul(const g4h_tensor *W, const float *x_dev, const void *pre_dev, siz
                float *Y_dev, int nb, void *stream);
 /* Same with an explicit kernel family: 0 = auto (g4h_matmul_path), 1 = the
  * GEMV family (token chunks of <= 8 staged per workgroup), 2 = int8 matrix-core
- * tiles (q8_0 / q4_0 weights; every per-block integer sum exact, fp32 block
- * scaling in block order).  g4h_matmul_path returns the family auto picks:
- * 2 for q8_0 / q4_0 weights from 9 tokens on, else 1. */
+ * tiles (q8_0 / q4_0 / q4_K / q6_K weights; every per-block or per-superblock
+ * integer sum exact, fp32 scaling in a fixed order, token rows independent of
+ * nb).  g4h_matmul_path returns the family auto picks: 2 for those weights
+ * from 9 tokens on, else 1. */
 int g4h_matmul_ex(const g4h_tensor *W, const float *x_dev, const void *pre_dev, size_t pre_stride,
                   float *Y_dev, int nb, int path, void *stream);
 int g4h_matmul_path(const g4h_tensor *W, int nb);
