@@ -517,18 +517,25 @@ def bench_next(G, m):
     wst = G.Buffer(G.attn_workspace_bytes(H, hd, pos0 + nb))
     ms_b = _timed(G, lambda: G.attn_prefill(q, kc, vc, G.F16, H, KV, hd, pos0, nb, o, ws=wsb))
     ms_t = _timed(G, lambda: G.attn_prefill(q, kc, vc, G.F16, H, KV, hd, pos0, nb, o, ws=wst, batched=False))
+    ms_m = _timed(G, lambda: G.attn_prefill_mm(q, kc, vc, G.F16, H, KV, hd, pos0, nb, o, ws=wsb))
+    # matrix-core flops: scores and weighted values, 2 * 2 * hd per (token, head, attended position)
+    flops = 4.0 * hd * H * sum(pos0 + b + 1 for b in range(nb))
     # unique HBM bytes: every cached K/V row once, plus q and out; each token
     # attends its own prefix (attn_kernel per (token, head)), which the
     # launches read from the caches' shared rows
     uniq = 2 * (pos0 + nb) * KV * hd * 2 + 2 * nb * H * hd * 4
     prefix = sum(2 * (pos0 + b + 1) * KV * hd * 2 for b in range(nb))
     out["prefill_attention_64"] = {"us": round(ms_b * 1e3, 1), "per_token_launches_us": round(ms_t * 1e3, 1),
+                                   "matrix_cores_us": round(ms_m * 1e3, 1),
+                                   "matrix_cores_TFLOPs": round(flops / (ms_m * 1e-3) / 1e12, 1),
                                    "alg_bytes": uniq, "GBps": round(uniq / (ms_b * 1e-3) / 1e9, 1),
                                    "prefix_bytes_per_token_sum": prefix,
                                    "what": f"g4h_attn_prefill, {nb} new tokens after {pos0} cached positions, "
                                            f"{H} q / {KV} kv heads x {hd}, f16 cache (model.c:509-545): one set of "
                                            "launches over a token grid dimension; bytes are the unique K/V rows "
-                                           "read plus q and out (the sum of the tokens' prefixes is given apart)"}
+                                           "read plus q and out (the sum of the tokens' prefixes is given apart); "
+                                           "matrix_cores_us: g4h_attn_prefill_mm, the prompt-prefill form (tiles of "
+                                           "32 (token, head) rows on f16 MFMA) that g4h_forward_batch takes"}
     try:
         out["gemma4_gguf"] = bench_gemma(G)
     except Exception as e:                      # reported in the line; the other rows stand

@@ -127,6 +127,7 @@ _SIGS = [
     ("g4h_gemma_free", _int, [_vp]),
     ("g4h_gemma_info", _int, [_vp, C.POINTER(_int), C.POINTER(_int), C.POINTER(_int), C.POINTER(_int)]),
     ("g4h_gemma_forward", _int, [_vp, C.POINTER(_int), _int, _int, _vp, _vp, _vp]),
+    ("g4h_attn_prefill_mm", _int, [_vp, _vp, _vp, _int, _int, _int, _int, _int, _int, _int, _int, _vp, _vp, _sz, _vp]),
     ("g4h_gemma_prefill", _int, [_vp, C.POINTER(_int), _int, _int, _vp, _vp]),
     ("g4h_read_floor", _int, [_vp, _sz, _vp, C.c_int64, _int, _int, _vp]),
     ("g4h_gemma_trace", _int, [_vp, _vp, C.POINTER(_sz)]),
@@ -431,6 +432,16 @@ def debug_attn_timeout(on: bool) -> None:
 
 def attn_prefill_workspace_bytes(n_head: int, hd: int, pos0: int, nb: int) -> int:
     return lib().g4h_attn_prefill_workspace_bytes(n_head, hd, pos0, nb)
+
+
+def attn_prefill_mm(q, kc, vc, kv_type: int, n_head: int, n_kv: int, hd: int, pos0: int, nb: int, out, window: int = 0,
+                    ring: int = 0, ws=None, stream=None) -> None:
+    """g4h_attn_prefill_mm: the prompt batch's attention on the matrix cores."""
+    need = attn_prefill_workspace_bytes(n_head, hd, pos0, nb)
+    if ws is None:
+        ws = Buffer(need)
+    check(lib().g4h_attn_prefill_mm(_p(q), _p(kc), _p(vc), kv_type, n_head, n_kv, hd, pos0, nb, window, ring, _p(out),
+                                    _p(ws), ws.nbytes if isinstance(ws, Buffer) else need, stream))
 
 
 def attn_prefill(q, kc, vc, kv_type: int, n_head: int, n_kv: int, hd: int, pos0: int, nb: int, out, ws=None,

@@ -435,17 +435,17 @@ static bool x_fused(const g4h_tensor &W, int nb) {
     return true;
 }
 
-// Token count from which the matrix-core family replaces the GEMV family for
-// q8_0 / q4_0 weights: the measured crossover on q8_0 4096x4096 (graph-timed
-// calls, quantization included) lies between 8 tokens (GEMV 9.5 us, matrix
-// cores 11.5 us) and 16 (17.0 us vs 11.5 us); past 8 tokens the GEMV family
-// takes a second launch.
-static constexpr int kMfmaMinTokens = 9;
+// From kMmMinTokens tokens the matrix-core family replaces the GEMV family:
+// the measured crossover on q8_0 4096x4096 (graph-timed calls, quantization
+// included) lies between 8 tokens (GEMV 9.5 us, matrix cores 11.5 us) and 16
+// (17.0 us vs 11.5 us), past 8 tokens the GEMV family taking a second launch;
+// q4_K / q6_K 4096x11008 are already faster on the matrix cores at 8 tokens
+// (23.0 / 31.1 us against 24.8 / 33.7 us).
 
 static bool mfma_capable(const g4h_tensor *W) { return W && (W->type == Q8_0 || W->type == Q4_0 || mmk_capable(W->type)); }
 
 extern "C" int g4h_matmul_path(const g4h_tensor *W, int nb) {
-    return mfma_capable(W) && nb >= kMfmaMinTokens ? 2 : 1;
+    return mfma_capable(W) && nb >= kMmMinTokens ? 2 : 1;
 }
 
 static const char *type_name(int t) {
@@ -767,6 +767,32 @@ extern "C" int g4h_attn_status(void *ws, int *failed, void *stream) {
 extern "C" size_t g4h_attn_prefill_workspace_bytes(int n_head, int hd, int pos0, int nb) {
     if (n_head <= 0 || hd <= 0 || pos0 < 0 || nb <= 0) return 0;
     return attn_batch_workspace_bytes(n_head, hd, pos0 + nb, nb);
+}
+
+extern "C" int g4h_attn_prefill_mm(const float *q, const void *kc, const void *vc, int kv_type, int n_head, int n_kv, int hd,
+                                   int pos0, int nb, int window, int ring, float *out, void *ws, size_t ws_bytes, void *s) {
+    G4_NEED_INIT();
+    if (!q || !out || !kc || !vc || !ws || nb < 1 || nb > 65535 || pos0 < 0 || window < 0 || ring < 0)
+        return fail(G4H_ERR_ARG, "g4h_attn_prefill_mm: bad argument");
+    if (int rc = check_attn_shape("g4h_attn_prefill_mm", kv_type, n_head, n_kv, hd)) return rc;
+    QkvArgs a;
+    a.n_head = n_head;
+    a.n_kv = n_kv;
+    a.hd = hd;
+    a.kv_type = kv_type;
+    a.kc = (uint8_t *)kc;
+    a.vc = (uint8_t *)vc;
+    a.window = window;
+    a.ring = ring;
+    if (!attn_batch_mm_ok(a)) return fail(G4H_ERR_TYPE, "g4h_attn_prefill_mm: takes f16 caches, head dims 64/128/256");
+    if (ring && (!window || window > ring || nb > ring - window + 1))
+        return fail(G4H_ERR_ARG, "g4h_attn_prefill_mm: a ring needs 0 < window <= ring and nb <= ring - window + 1");
+    if ((uintptr_t)kc % 16 || (uintptr_t)vc % 16) return fail(G4H_ERR_ARG, "g4h_attn_prefill_mm: caches must be 16-byte aligned");
+    const int rows = window ? std::min(window, pos0 + nb) : pos0 + nb;
+    if (ws_bytes < attn_batch_mm_workspace_bytes(n_head, hd, rows, nb))
+        return fail(G4H_ERR_ARG, "g4h_attn_prefill_mm: workspace smaller than g4h_attn_prefill_workspace_bytes");
+    G4_HIP(launch_attn_batch_mm(q, a, pos0 + 1, nb, out, nullptr, (uint8_t *)ws, ws_bytes, (hipStream_t)s));
+    return G4H_OK;
 }
 
 extern "C" int g4h_attn_prefill(const float *q, const void *kc, const void *vc, int kv_type, int n_head, int n_kv, int hd,

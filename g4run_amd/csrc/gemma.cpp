@@ -374,6 +374,20 @@ extern "C" int g4h_gemma_info(const g4h_gemma *m, int *n_vocab, int *n_embd, int
     return G4H_OK;
 }
 
+// the batch's attention over the cache of qa: a prompt batch (path 0) of
+// kMmMinTokens or more on the matrix cores where the layer allows, else the
+// per-token arithmetic of the decode kernels
+static int attend_batch(g4h_gemma *m, const QkvArgs &qa, int pos0, int nb, int path, hipStream_t s) {
+    if (path != 1 && nb >= kMmMinTokens && attn_batch_mm_ok(qa)) {
+        const size_t wsb = std::max(attn_batch_workspace_bytes(m->H, m->hd_full, m->n_ctx, kRows),
+                                    attn_batch_workspace_bytes(m->H, m->hd_swa, m->n_ctx, kRows));
+        G_HIP(launch_attn_batch_mm(m->q, qa, pos0 + 1, nb, m->att, nullptr, m->bws, wsb, s));
+    } else {
+        G_HIP(launch_attn_batch(m->q, qa, pos0 + 1, nb, m->att, nullptr, m->bws, s));
+    }
+    return G4H_OK;
+}
+
 // The forward of nb tokens whose ids are in tok_dev (device) at positions
 // pos0 .. pos0 + nb - 1; with `st` (one token, the decode state token | pos |
 // npos on the device) the position comes from st instead, and the call is
@@ -443,7 +457,7 @@ static int run(g4h_gemma *m, const int *tok_dev, int nb, int pos0, const int *st
             qa.vc = m->vc[il];
             if (nb > 1) {                                            // every row stored, then the batch attends
                 G_HIP(launch_attn_prep_rows(m->qkv, qa, pos0, nb, m->q, s));
-                G_HIP(launch_attn_batch(m->q, qa, pos0 + 1, nb, m->att, nullptr, m->bws, s));
+                G_RC(attend_batch(m, qa, pos0, nb, path, s));
             } else if (hd == 512) {                                  // wide heads: rows prepared first, then the halves attend
                 G_HIP(launch_attn_prep_rows(m->qkv, qa, pos0, 1, m->q, s, pos_dev));
                 G_HIP(launch_attn_decode(m->q, nullptr, qa, pos0 + 1, npos_dev, npos_max, m->att, nullptr, ws, s));
@@ -456,7 +470,7 @@ static int run(g4h_gemma *m, const int *tok_dev, int nb, int pos0, const int *st
             G_HIP(launch_head_prep(m->q, H, hd, nb, L.q_norm, rope, pos0, eps, s, pos_dev));
             qa.kc = m->kc[cil];
             qa.vc = m->vc[cil];
-            if (nb > 1) G_HIP(launch_attn_batch(m->q, qa, pos0 + 1, nb, m->att, nullptr, m->bws, s));
+            if (nb > 1) G_RC(attend_batch(m, qa, pos0, nb, path, s));
             else G_HIP(launch_attn_decode(m->q, nullptr, qa, pos0 + 1, npos_dev, npos_max, m->att, nullptr, ws, s));
         }
         G_RC(trl(il, T_ATT, m->att, nq, nq));

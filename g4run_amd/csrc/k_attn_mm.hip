@@ -1,0 +1,301 @@
+// k_attn_mm.hip -- causal attention of a prompt batch on the matrix cores:
+// attn_kernel (model.c:509-545) for nb new tokens over an f16 KV cache, the
+// tokens of a tile sharing every K and V row they read.
+//
+// Rows of a tile are (token, query head) pairs of one KV head: 32 / GRP
+// tokens x GRP heads = 32 rows.  Token b sits at position p0 + b and attends
+// positions j0(b) .. p0 + b, j0 = max(0, p + 1 - window) with a window (else
+// 0); the batch spans positions jb = j0(0) .. p0 + nb - 1 (on a ring, position
+// j's row is at slot j % ring).
+//   scores   grid (KV head x tile, 128-position chunk), 4 waves x 32
+//            positions: S = fp16(q) . K_j (model.c:530-538, no 1/sqrt(d)) as
+//            one v_mfma_f32_32x32x16_f16 per 16 head elements (exact
+//            products, fp32 sums); per row and chunk the maximum m_c and
+//            l_c = sum exp((double)(s - m_c)) over the row's positions.
+//   values   grid (KV head x tile, 256-position span): per row the global
+//            maximum M and normaliser (sum_c l_c exp(m_c - M) in double) as in
+//            the decode kernels, the weights fp16((float)exp(s - M) * inv)
+//            (model.c:547-555) into LDS (0 outside a row's positions), then
+//            sum_j w_j V_j on v_mfma_f32_32x32x16_f16 with the positions as
+//            the contraction: lane (c, half) loads V[j][2c], V[j][2c + 1] of
+//            its 8 positions, the even and the odd columns of a 64-column
+//            group being two 32-column tiles.
+//   combine  per (token, head) the spans' partials added in order.
+// Differences from the per-token kernels are the fp32 orders of the score and
+// value sums and the grouping of the double normaliser: within the
+// attention's tolerance of the CPU, not bit-identical to them.  A non-finite
+// V row (an f16 overflow) reaches the earlier rows of its tile as 0 * inf.
+#include <algorithm>
+#include <cmath>
+
+#include "formats.h"
+#include "kernels.h"
+#include "steps.h"
+
+namespace g4 {
+
+typedef _Float16 am_v8h __attribute__((ext_vector_type(8)));
+typedef float am_v16f __attribute__((ext_vector_type(16)));
+
+constexpr int AMM_CH = 128;          // positions per score workgroup
+constexpr int AMM_NP = 256;          // positions per value workgroup
+constexpr size_t AMM_OFF = 256;      // the decode layout's header (error and epoch words) stays untouched
+
+struct AmmArgs {
+    const float *q;                  // [nb][n_head][hd] prepared queries
+    float *out;                      // [nb][n_head][hd]
+    uint8_t *q8out;                  // optional q8_0 rows of out, q8_stride bytes per token
+    size_t q8_stride;
+    const uint8_t *kc, *vc;
+    int n_head, n_kv, window, ring;
+    int p0, nb, jb, span, nch, nchv, ntt;
+    float *S;                        // [nb * n_head][span]
+    float *Mc;                       // [nb * n_head][nch]
+    double *Lc;                      // [nb * n_head][nch]
+    float *P;                        // [nb * n_head][nchv][hd]
+};
+
+static size_t amm_al(size_t v) { return (v + 255) & ~(size_t)255; }
+struct AmmWs {
+    size_t S, Mc, Lc, P, total;
+};
+static AmmWs amm_ws(int n_head, int hd, int nb, int span) {
+    const size_t R = (size_t)nb * n_head, nch = (span + AMM_CH - 1) / AMM_CH, nchv = (span + AMM_NP - 1) / AMM_NP;
+    AmmWs w;
+    w.S = AMM_OFF;
+    w.Mc = w.S + amm_al(R * span * 4);
+    w.Lc = w.Mc + amm_al(R * nch * 4);
+    w.P = w.Lc + amm_al(R * nch * 8);
+    w.total = w.P + amm_al(R * nchv * hd * 4);
+    return w;
+}
+size_t attn_batch_mm_workspace_bytes(int n_head, int hd, int npos_max, int nb) {
+    return amm_ws(n_head, hd, nb, npos_max + nb).total;
+}
+
+__device__ __forceinline__ am_v8h amm_ld8(const void *p) { return *(const am_v8h *)p; }
+__device__ __forceinline__ am_v16f amm_mma(am_v8h a, am_v8h b, am_v16f c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ const uint8_t *amm_row(const AmmArgs &c, const uint8_t *cache, int j, int kvh, int hd) {
+    const int slot = c.ring ? j % c.ring : j;
+    return cache + ((size_t)slot * c.n_kv + kvh) * hd * 2;
+}
+// tile row i: token b and head h; the row's positions j0 .. p
+template <int GRP>
+__device__ __forceinline__ void amm_rowinfo(const AmmArgs &c, int kvh, int tt, int i, int &b, int &h, int &j0, int &p) {
+    constexpr int T = 32 / GRP;
+    b = tt * T + i / GRP;
+    h = kvh * GRP + i % GRP;
+    p = c.p0 + b;
+    j0 = c.window ? std::max(0, p + 1 - c.window) : 0;
+}
+
+template <int HD, int GRP>
+__global__ __launch_bounds__(256) void k_amm_scores(AmmArgs c) {
+    constexpr int T = 32 / GRP, QS = HD + 8;
+    __shared__ __align__(16) uint16_t qs[32][QS];                   // fp16 queries of the tile
+    __shared__ float wm[4][32];
+    __shared__ double wl[4][32];
+    const int kvh = blockIdx.x / c.ntt, tt = blockIdx.x % c.ntt, ch = blockIdx.y;
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6, li = lane & 31, kh = lane >> 5;
+    const int jl = ch * AMM_CH + wave * 32 + li, j = c.jb + jl;    // the lane's position (MFMA column)
+    const uint8_t *krow = amm_row(c, c.kc, std::min(j, c.jb + c.span - 1), kvh, HD);
+    am_v8h kb[HD / 16];
+#pragma unroll
+    for (int s = 0; s < HD / 16; s++) kb[s] = amm_ld8(krow + (16 * s + 8 * kh) * 2);
+    for (int x = t; x < 32 * HD; x += 256) {
+        const int i = x / HD, e = x % HD, b = tt * T + i / GRP, h = kvh * GRP + i % GRP;
+        qs[i][e] = f2h(b < c.nb ? c.q[((size_t)b * c.n_head + h) * HD + e] : 0.0f);
+    }
+    __syncthreads();
+    am_v16f acc = {};
+#pragma unroll
+    for (int s = 0; s < HD / 16; s++) acc = amm_mma(amm_ld8(&qs[li][16 * s + 8 * kh]), kb[s], acc);
+    // C[i][li]: rows i = 8 (r / 4) + 4 kh + r % 4
+    bool ok[16];
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+        const int i = 8 * (r >> 2) + 4 * kh + (r & 3);
+        int b, h, j0, p;
+        amm_rowinfo<GRP>(c, kvh, tt, i, b, h, j0, p);
+        ok[r] = b < c.nb && jl < c.span && j >= j0 && j <= p;
+        if (ok[r]) c.S[((size_t)b * c.n_head + h) * c.span + jl] = acc[r];
+        const float m = group_max<32>(ok[r] ? acc[r] : -INFINITY);
+        if (li == 0) wm[wave][i] = m;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+        const int i = 8 * (r >> 2) + 4 * kh + (r & 3);
+        const float mc = fmaxf(fmaxf(wm[0][i], wm[1][i]), fmaxf(wm[2][i], wm[3][i]));
+        const double l = group_sum_t<32>(ok[r] ? exp((double)(acc[r] - mc)) : 0.0);
+        if (li == 0) wl[wave][i] = l;
+    }
+    __syncthreads();
+    if (t < 32) {
+        int b, h, j0, p;
+        amm_rowinfo<GRP>(c, kvh, tt, t, b, h, j0, p);
+        if (b < c.nb) {
+            const size_t R = (size_t)b * c.n_head + h;
+            c.Mc[R * c.nch + ch] = fmaxf(fmaxf(wm[0][t], wm[1][t]), fmaxf(wm[2][t], wm[3][t]));
+            c.Lc[R * c.nch + ch] = ((wl[0][t] + wl[1][t]) + wl[2][t]) + wl[3][t];
+        }
+    }
+}
+
+template <int HD, int GRP>
+__global__ __launch_bounds__(256) void k_amm_v(AmmArgs c) {
+    constexpr int WS = AMM_NP + 8;
+    __shared__ __align__(16) uint16_t wsh[32][WS];                  // fp16 weights of the span
+    __shared__ float mx[32], iv[32];
+    const int kvh = blockIdx.x / c.ntt, tt = blockIdx.x % c.ntt, cv = blockIdx.y;
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6, li = lane & 31, kh = lane >> 5;
+    const int jl0 = cv * AMM_NP;
+    // 1. per row the global maximum and normaliser (wave w: rows 8 w .. 8 w + 7)
+    for (int k = 0; k < 8; k++) {
+        const int i = wave * 8 + k;
+        int b, h, j0, p;
+        amm_rowinfo<GRP>(c, kvh, tt, i, b, h, j0, p);
+        const bool rv = b < c.nb;                                     // uniform over the wave
+        const size_t R = (size_t)(rv ? b : 0) * c.n_head + h;
+        float m = -INFINITY;
+        for (int c0 = 0; c0 < c.nch; c0 += 64)
+            m = fmaxf(m, group_max<64>(rv && c0 + lane < c.nch ? c.Mc[R * c.nch + c0 + lane] : -INFINITY));
+        double sum = 0.0;
+        for (int c0 = 0; c0 < c.nch; c0 += 64) {
+            const bool on = rv && c0 + lane < c.nch;
+            const float mc = on ? c.Mc[R * c.nch + c0 + lane] : 0.0f;
+            const double lc = on ? c.Lc[R * c.nch + c0 + lane] : 0.0;
+            sum += group_sum_t<64>(on ? lc * exp((double)mc - (double)m) : 0.0);
+        }
+        if (lane == 0) {
+            mx[i] = m;
+            iv[i] = (float)(1.0 / sum);
+        }
+    }
+    __syncthreads();
+    // 2. the weights (0 outside a row's positions)
+    for (int x = t; x < 32 * AMM_NP; x += 256) {
+        const int i = x / AMM_NP, pp = x % AMM_NP, jl = jl0 + pp, j = c.jb + jl;
+        int b, h, j0, p;
+        amm_rowinfo<GRP>(c, kvh, tt, i, b, h, j0, p);
+        float w = 0.0f;
+        if (b < c.nb && jl < c.span && j >= j0 && j <= p) {
+            const float s = c.S[((size_t)b * c.n_head + h) * c.span + jl];
+            w = (float)exp((double)(s - mx[i])) * iv[i];
+        }
+        wsh[i][pp] = f2h(w);
+    }
+    __syncthreads();
+    // 3. sum_j w_j V_j: wave w takes the column groups g = w, w + 4, .. of 64
+    const int jlast = c.jb + c.span - 1;
+    for (int g = wave; g < HD / 64; g += 4) {
+        const int col = 64 * g + 2 * li;
+        am_v16f ae = {}, ao = {};
+#pragma unroll 4
+        for (int s = 0; s < AMM_NP / 16; s++) {
+            const int jb8 = c.jb + jl0 + 16 * s + 8 * kh;
+            uint32_t x[8];
+#pragma unroll
+            for (int k = 0; k < 8; k++) x[k] = *(const uint32_t *)(amm_row(c, c.vc, std::min(jb8 + k, jlast), kvh, HD) + col * 2);
+            am_v8h be, bo;
+#pragma unroll
+            for (int k = 0; k < 8; k++) {
+                be[k] = __builtin_bit_cast(_Float16, (uint16_t)(x[k] & 0xffff));
+                bo[k] = __builtin_bit_cast(_Float16, (uint16_t)(x[k] >> 16));
+            }
+            const am_v8h a = amm_ld8(&wsh[li][16 * s + 8 * kh]);
+            ae = amm_mma(a, be, ae);
+            ao = amm_mma(a, bo, ao);
+        }
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            const int i = 8 * (r >> 2) + 4 * kh + (r & 3);
+            int b, h, j0, p;
+            amm_rowinfo<GRP>(c, kvh, tt, i, b, h, j0, p);
+            if (b < c.nb) {
+                float *dst = c.P + (((size_t)b * c.n_head + h) * c.nchv + cv) * HD;
+                *(float2 *)(dst + col) = make_float2(ae[r], ao[r]);
+            }
+        }
+    }
+}
+
+// grid (n_head, nb), 256 threads: the spans' partials in order; with q8out,
+// the head row as q8_0 blocks too (quants.c:74-109)
+template <int HD>
+__global__ __launch_bounds__(256) void k_amm_combine(AmmArgs c) {
+    __shared__ float row[256];
+    const int h = blockIdx.x, b = blockIdx.y, e = threadIdx.x;
+    const size_t R = (size_t)b * c.n_head + h;
+    const int last = (c.p0 + b - c.jb) / AMM_NP;                    // the token's last span
+    if (e < HD) {
+        const float *p = c.P + R * c.nchv * HD + e;
+        float r = 0.0f;
+        for (int cv = 0; cv <= last; cv++) r += p[(size_t)cv * HD];
+        c.out[R * HD + e] = r;
+        row[e] = r;
+    }
+    if (c.q8out) {
+        __syncthreads();
+        const bool own = e < HD / 4;
+        float v[4] = {0.f, 0.f, 0.f, 0.f};
+        if (own)
+            for (int k = 0; k < 4; k++) v[k] = row[4 * e + k];
+        if (e < 64) q8_store4(v, e, own, c.q8out + (size_t)b * c.q8_stride + (size_t)h * (HD / 32) * 34);
+    }
+}
+
+bool attn_batch_mm_ok(const QkvArgs &a) {
+    const int grp = a.n_kv > 0 ? a.n_head / a.n_kv : 0;
+    return a.kv_type == F16 && (a.hd == 64 || a.hd == 128 || a.hd == 256) && a.n_kv > 0 && a.n_head % a.n_kv == 0 &&
+           (grp == 1 || grp == 2 || grp == 4 || grp == 8);
+}
+
+template <int HD, int GRP>
+static void amm_go(const AmmArgs &c, hipStream_t s) {
+    hipLaunchKernelGGL((k_amm_scores<HD, GRP>), dim3(c.n_kv * c.ntt, c.nch), dim3(256), 0, s, c);
+    hipLaunchKernelGGL((k_amm_v<HD, GRP>), dim3(c.n_kv * c.ntt, c.nchv), dim3(256), 0, s, c);
+    hipLaunchKernelGGL(k_amm_combine<HD>, dim3(c.n_head, c.nb), dim3(256), 0, s, c);
+}
+
+hipError_t launch_attn_batch_mm(const float *q, const QkvArgs &a, int npos0, int nb, float *out, uint8_t *q8out, uint8_t *ws,
+                                size_t ws_bytes, hipStream_t s, size_t q8_stride) {
+    if (!attn_batch_mm_ok(a) || !q || !out || !ws || nb < 1 || npos0 < 1 || nb > 65535) return hipErrorInvalidValue;
+    if (a.ring && (a.window <= 0 || a.window > a.ring || nb > a.ring - a.window + 1)) return hipErrorInvalidValue;
+    AmmArgs c{};
+    c.q = q;
+    c.out = out;
+    c.q8out = q8out;
+    c.q8_stride = q8_stride ? q8_stride : (size_t)a.n_head * (a.hd / 32) * 34;
+    c.kc = a.kc;
+    c.vc = a.vc;
+    c.n_head = a.n_head;
+    c.n_kv = a.n_kv;
+    c.window = a.window;
+    c.ring = a.ring;
+    c.p0 = npos0 - 1;
+    c.nb = nb;
+    c.jb = a.window ? std::max(0, c.p0 + 1 - a.window) : 0;
+    c.span = c.p0 + nb - c.jb;
+    c.nch = (c.span + AMM_CH - 1) / AMM_CH;
+    c.nchv = (c.span + AMM_NP - 1) / AMM_NP;
+    const int grp = a.n_head / a.n_kv;
+    c.ntt = (nb + 32 / grp - 1) / (32 / grp);
+    const AmmWs w = amm_ws(a.n_head, a.hd, nb, c.span);
+    if (ws_bytes < w.total || (size_t)c.n_kv * c.ntt > 0x7fffffff) return hipErrorInvalidValue;
+    c.S = (float *)(ws + w.S);
+    c.Mc = (float *)(ws + w.Mc);
+    c.Lc = (double *)(ws + w.Lc);
+    c.P = (float *)(ws + w.P);
+#define G4_AMM(HD_, G_) \
+    if (a.hd == HD_ && grp == G_) amm_go<HD_, G_>(c, s);
+    G4_AMM(64, 1) G4_AMM(64, 2) G4_AMM(64, 4) G4_AMM(64, 8)
+    G4_AMM(128, 1) G4_AMM(128, 2) G4_AMM(128, 4) G4_AMM(128, 8)
+    G4_AMM(256, 1) G4_AMM(256, 2) G4_AMM(256, 4) G4_AMM(256, 8)
+#undef G4_AMM
+    return hipGetLastError();
+}
+
+}  // namespace g4

@@ -204,6 +204,18 @@ size_t attn_batch_workspace_bytes(int n_head, int hd, int npos_max, int nb);
 // (0: packed rows)
 hipError_t launch_attn_batch(const float *q, const QkvArgs &a, int npos0, int nb, float *out, uint8_t *q8out, uint8_t *ws,
                              hipStream_t s, size_t q8_stride = 0);
+// The same causal batch on the matrix cores (f16 caches, hd 64 / 128 / 256,
+// 1 / 2 / 4 / 8 query heads per KV head; attn_batch_mm_ok): tiles of 32
+// (token, head) rows share every K and V row they read; within the
+// attention's tolerance of launch_attn_batch, not bit-identical to it.  ws of
+// attn_batch_workspace_bytes (which covers both forms), ws_bytes its size.
+bool attn_batch_mm_ok(const QkvArgs &a);
+// prompt batches of at least this many tokens take the matrix-core kernels
+// (g4h_matmul_path, the batched forwards' attention)
+constexpr int kMmMinTokens = 9;
+size_t attn_batch_mm_workspace_bytes(int n_head, int hd, int npos_max, int nb);
+hipError_t launch_attn_batch_mm(const float *q, const QkvArgs &a, int npos0, int nb, float *out, uint8_t *q8out, uint8_t *ws,
+                                size_t ws_bytes, hipStream_t s, size_t q8_stride = 0);
 // the query / key / value rows of nb tokens from the fused projection output
 // (rows of (n_head + 2 n_kv) hd floats) prepared as the decode kernels do:
 // queries into qout [nb][n_head][hd], key and value rows into the caches at

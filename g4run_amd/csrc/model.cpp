@@ -565,7 +565,11 @@ static int forward_rows(g4h_model *m, const int *tokens, int nb, int pos0, hipSt
             // every token's rows prepared and its key / value stored first, then
             // the batch attends in one set of launches
             M_HIP(launch_attn_prep_rows(m->bqkv, qa, pos0, nb, m->bq, s));
-            M_HIP(launch_attn_batch(m->bq, qa, pos0 + 1, nb, m->batt, m->bact, m->bbw, s, ast));
+            if (path != 1 && nb >= kMmMinTokens && attn_batch_mm_ok(qa))    // a prompt batch: the matrix cores
+                M_HIP(launch_attn_batch_mm(m->bq, qa, pos0 + 1, nb, m->batt, m->bact, m->bbw,
+                                           attn_batch_workspace_bytes(c.n_head, c.head_dim, c.n_ctx, kBatchMax), s, ast));
+            else
+                M_HIP(launch_attn_batch(m->bq, qa, pos0 + 1, nb, m->batt, m->bact, m->bbw, s, ast));
         } else {
             for (int b = 0; b < nb; b++)
                 M_HIP(launch_attn_decode(nullptr, m->bqkv + (size_t)b * R, qa, pos0 + b + 1, nullptr, c.n_ctx,

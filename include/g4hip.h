@@ -241,6 +241,19 @@ int g4h_attn_decode_window(const float *q_dev, const void *kc_dev, const void *v
 int g4h_attn_prefill(const float *q_dev, const void *kc_dev, const void *vc_dev, int kv_type,
                      int n_head, int n_kv, int hd, int pos0, int nb, float *out_dev,
                      void *ws_dev, size_t ws_bytes, void *stream);
+/* The same batch on the matrix cores, for prompt prefill: f16 caches, head
+ * dims 64 / 128 / 256, 1 / 2 / 4 / 8 query heads per KV head, with the
+ * sliding window and ring of g4h_attn_decode_window (window 0: all positions;
+ * on a ring nb <= ring - window + 1).  Tiles of 32 (token, head) rows share
+ * every K and V row: scores and weighted value sums on f16 MFMA (exact
+ * products, fp32 sums), the softmax statistics and the fp16 weights of the
+ * decode kernels.  Rows are within the attention's tolerance of
+ * g4h_attn_prefill's, not bit-identical to them; a non-finite V row reaches
+ * the earlier rows of its tile.  ws_bytes >= g4h_attn_prefill_workspace_bytes
+ * (n_head, hd, pos0, nb).  Asynchronous.  No counterpart in the reference. */
+int g4h_attn_prefill_mm(const float *q_dev, const void *kc_dev, const void *vc_dev, int kv_type, int n_head, int n_kv,
+                        int hd, int pos0, int nb, int window, int ring, float *out_dev, void *ws_dev, size_t ws_bytes,
+                        void *stream);
 /* workspace bytes of g4h_attn_prefill's one-set form (a block of scores,
  * chunk statistics and partials per token); 0 for a bad argument.  No
  * counterpart in the reference, which attends on the CPU. */

@@ -380,3 +380,119 @@ def test_window_ring_attention_vs_oracle(gpu, oracle, kv_type, n_head, hd, n_pos
     err = np.abs(got.astype(np.float64) - ref)
     bad = err > ATOL + RTOL * np.abs(ref)
     assert not bad.any(), f"{bad.sum()} outside tolerance, worst {err.max():.3g}"
+
+
+# ------------------------------------------ prompt batch on the matrix cores
+def _mm_slack(q, kc, vc, n_head, n_kv, hd, rows):
+    """f16 V: where a softmax weight lies within 1e-4 of an fp16 rounding
+    midpoint, the GPU's weight (its scores differ from the CPU's by the fp32
+    order of the dot) may take the neighbouring code; per output element the
+    most that can move it.  rows: the cache rows the token attends."""
+    K = np.frombuffer(kc.tobytes(), np.float16).reshape(-1, n_kv, hd)[rows].astype(np.float64)
+    V = np.frombuffer(vc.tobytes(), np.float16).reshape(-1, n_kv, hd)[rows].astype(np.float64)
+    grp = n_head // n_kv
+    slack = np.zeros((n_head, hd))
+    for h in range(n_head):
+        sc = K[:, h // grp] @ q[h].astype(np.float16).astype(np.float64)
+        w = np.exp(sc - sc.max())
+        w /= w.sum()
+        w16 = w.astype(np.float32).astype(np.float16)
+        a = w16.astype(np.float64)
+        up = np.nextafter(w16, np.float16(np.inf)).astype(np.float64)
+        dn = np.nextafter(w16, np.float16(-np.inf)).astype(np.float64)
+        ulp = np.where(np.abs(w - (a + up) / 2) <= 1e-4 * w, up - a, 0.0) + \
+            np.where(np.abs(w - (a + dn) / 2) <= 1e-4 * w, a - dn, 0.0)
+        slack[h] = ulp @ np.abs(V[:, h // grp])
+    return slack
+
+
+@pytest.mark.parametrize("n_head,n_kv,hd,pos0,nb", [
+    (8, 4, 256, 4096, 64), (8, 4, 256, 0, 9), (8, 4, 256, 300, 33), (8, 1, 256, 1000, 17), (4, 4, 128, 200, 40),
+    (8, 2, 64, 77, 20), (16, 8, 128, 513, 100), (8, 4, 256, 127, 1)])
+def test_prefill_matrix_cores_vs_oracle(gpu, oracle, n_head, n_kv, hd, pos0, nb):
+    """g4h_attn_prefill_mm (model.c:509-545 for a prompt batch): every token's
+    row against the oracle's attention at its position (with the fp16-weight
+    slack of _mm_slack); tiles of 1 / 2 / 4 / 8 query heads per KV head,
+    batches off the tile size, chunks and spans ragged, the first token at
+    position 0."""
+    G = gpu
+    n_slot = pos0 + nb
+    kb, vb, kh, vh = make_cache(G, oracle, G.F16, n_slot, n_kv, hd, seed=n_slot + hd)
+    q = (np.random.default_rng(nb + hd).standard_normal((nb, n_head, hd)) * 0.5).astype(np.float32)
+    out = G.Buffer(nb * n_head * hd * 4)
+    G.attn_prefill_mm(G.Buffer.from_array(q), kb, vb, G.F16, n_head, n_kv, hd, pos0, nb, out)
+    got = out.download(np.float32, (nb, n_head, hd))
+    oracle.pool_start(8)
+    try:
+        for b in range(nb):
+            ref = oracle.attn_decode(q[b], kh, vh, G.F16, n_head, n_kv, hd, pos0 + b, nthreads=8)
+            err = np.abs(got[b].astype(np.float64) - ref)
+            bad = err > ATOL + RTOL * np.abs(ref)
+            if bad.any():
+                bad &= err > ATOL + RTOL * np.abs(ref) + _mm_slack(q[b], kh, vh, n_head, n_kv, hd, np.arange(pos0 + b + 1))
+            assert not bad.any(), f"token {b}: {bad.sum()} outside tolerance, worst {err.max():.3g}"
+    finally:
+        oracle.pool_stop()
+
+
+@pytest.mark.parametrize("hd,pos0,nb,window,ring", [(256, 700, 64, 512, 576), (256, 100, 30, 512, 576), (64, 50, 25, 16, 40),
+                                                    (128, 0, 12, 8, 20), (256, 300, 40, 300, 0)])
+def test_prefill_matrix_cores_window_ring(gpu, oracle, hd, pos0, nb, window, ring):
+    """The sliding window over a KV ring (model.c:517-537): token b attends
+    max(0, p + 1 - window) .. p; on a ring each position's row sits at slot
+    p % ring and again at p % ring + ring, written as the decode steps and
+    the batch's own row preparation leave them."""
+    G = gpu
+    n_head, n_kv = 8, 1
+    n_pos = pos0 + nb
+    slots = 2 * ring if ring else n_pos
+    rows = np.random.default_rng(n_pos + window).standard_normal((2, n_pos, hd)).astype(np.float32)
+    rb = hd * 2
+
+    def stored(x):
+        b = G.Buffer(n_pos * rb)
+        G.kv_store(G.F16, G.Buffer.from_array(x), b, hd, rows=n_pos, dst_stride=rb)
+        return b.download(np.uint8, (n_pos, rb))
+
+    lin = [stored(rows[0]), stored(rows[1])]
+    gpu_c = [np.zeros((slots, rb), np.uint8) for _ in range(2)]
+    for j in range(n_pos):
+        for c in range(2):
+            if ring:
+                gpu_c[c][j % ring] = lin[c][j]
+                gpu_c[c][j % ring + ring] = lin[c][j]
+            else:
+                gpu_c[c][j] = lin[c][j]
+    q = (np.random.default_rng(7).standard_normal((nb, n_head, hd)) * 0.5).astype(np.float32)
+    out = G.Buffer(nb * n_head * hd * 4)
+    G.attn_prefill_mm(G.Buffer.from_array(q), G.Buffer.from_array(gpu_c[0]), G.Buffer.from_array(gpu_c[1]), G.F16,
+                      n_head, n_kv, hd, pos0, nb, out, window=window, ring=ring)
+    got = out.download(np.float32, (nb, n_head, hd))
+    L = oracle.lib()
+    L.g4o_attn_window.argtypes = [oracle._vp] * 3 + [oracle.C.c_int] * 7 + [oracle._vp, oracle.C.c_int]
+    for b in range(nb):
+        pos = pos0 + b
+        j0 = max(0, pos - window + 1) if window else 0
+        ref = np.zeros((n_head, hd), np.float32)
+        qb = np.ascontiguousarray(q[b])
+        L.g4o_attn_window(qb.ctypes.data, lin[0].ctypes.data, lin[1].ctypes.data, G.F16, n_head, n_kv, hd, pos, j0, n_pos,
+                          ref.ctypes.data, 1)
+        err = np.abs(got[b].astype(np.float64) - ref)
+        bad = err > ATOL + RTOL * np.abs(ref)
+        if bad.any():
+            bad &= err > ATOL + RTOL * np.abs(ref) + _mm_slack(qb, lin[0], lin[1], n_head, n_kv, hd, np.arange(j0, pos + 1))
+        assert not bad.any(), f"token {b}: {bad.sum()} outside tolerance, worst {err.max():.3g}"
+
+
+def test_prefill_matrix_cores_errors(gpu):
+    G = gpu
+    b = G.Buffer(1 << 20)
+    with pytest.raises(G.G4HError) as e:                              # q8_0 caches stay on the per-token form
+        G.attn_prefill_mm(b, b, b, G.Q8_0, 8, 4, 256, 10, 16, b)
+    assert e.value.status == G.ERR_TYPE
+    with pytest.raises(G.G4HError) as e:                              # 512-wide heads too
+        G.attn_prefill_mm(b, b, b, G.F16, 8, 1, 512, 10, 16, b)
+    assert e.value.status in (G.ERR_TYPE, G.ERR_SHAPE)
+    with pytest.raises(G.G4HError) as e:                              # a batch longer than the ring allows
+        G.attn_prefill_mm(b, b, b, G.F16, 8, 1, 256, 10, 70, b, window=512, ring=576)
+    assert e.value.status == G.ERR_ARG

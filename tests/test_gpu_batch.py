@@ -71,14 +71,16 @@ def test_batch_rows_equal_decode_steps(gpu, oracle, cfg, kv_type, wtype, nb, pos
     finally:
         m.trace(None)
     # g4_forward_batch: the last token's logits; from 9 tokens its projections
-    # run on the matrix cores (another fp32 order: the stack agrees to 1e-3
-    # of the logit range, as decode steps against the oracle do)
+    # and its attention run on the matrix cores (other fp32 orders, and fp16
+    # softmax weights that may take the neighbouring code, a relative 5e-4 of
+    # a weight): the stack agrees to 1e-2 of the logit range, each part of it
+    # to 1e-3 / 1e-5 (test_prefill_rows_match_oracle_per_part)
     lg = m.forward_batch(tokens, pos0)
     if nb < 9:
         assert lg.tobytes() == bl[-1].tobytes()
     else:
         rng = float(bl[-1].max() - bl[-1].min())
-        assert float(np.abs(lg.astype(np.float64) - bl[-1]).max()) <= 1e-3 * rng
+        assert float(np.abs(lg.astype(np.float64) - bl[-1]).max()) <= 1e-2 * rng
 
 
 @pytest.mark.parametrize("cfg,kv_type,wtype,nb,pos0", [
@@ -86,8 +88,9 @@ def test_batch_rows_equal_decode_steps(gpu, oracle, cfg, kv_type, wtype, nb, pos
     ids=["small-f16-q4w-nb13", "mid-f16-q4w-nb24", "mid-q8kv-q8w-nb16"])
 def test_prefill_rows_match_oracle_per_part(gpu, oracle, cfg, kv_type, wtype, nb, pos0):
     """g4_forward_batch of a prompt chunk (projections on the int8 matrix
-    cores): with the per-token trace, each part of each layer of every row is
-    recomputed by the oracle from the GPU's own inputs to that part."""
+    cores; with an f16 cache the attention too): with the per-token trace,
+    each part of each layer of every row is recomputed by the oracle from the
+    GPU's own inputs to that part."""
     from test_gpu_model import _attn_slack, _cache_rows, _check_gelu, _close, oracle_model
     from oracle import g4o as o
     G = gpu
