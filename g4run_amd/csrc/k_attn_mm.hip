@@ -104,9 +104,19 @@ __global__ __launch_bounds__(256) void k_amm_scores(AmmArgs c) {
     am_v8h kb[HD / 16];
 #pragma unroll
     for (int s = 0; s < HD / 16; s++) kb[s] = amm_ld8(krow + (16 * s + 8 * kh) * 2);
-    for (int x = t; x < 32 * HD; x += 256) {
-        const int i = x / HD, e = x % HD, b = tt * T + i / GRP, h = kvh * GRP + i % GRP;
-        qs[i][e] = f2h(b < c.nb ? c.q[((size_t)b * c.n_head + h) * HD + e] : 0.0f);
+    // the tile's queries: all of a thread's loads issued before any conversion
+    constexpr int NQ = 32 * HD / 4 / 256;                           // float4 per thread
+    float4 qv[NQ];
+#pragma unroll
+    for (int k = 0; k < NQ; k++) {
+        const int x = t + 256 * k, i = x / (HD / 4), e4 = x % (HD / 4), b = tt * T + i / GRP, h = kvh * GRP + i % GRP;
+        qv[k] = b < c.nb ? *(const float4 *)(c.q + ((size_t)b * c.n_head + h) * HD + 4 * e4) : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+#pragma unroll
+    for (int k = 0; k < NQ; k++) {
+        const int x = t + 256 * k, i = x / (HD / 4), e4 = x % (HD / 4);
+        const uint32_t lo = f2h(qv[k].x) | ((uint32_t)f2h(qv[k].y) << 16), hi = f2h(qv[k].z) | ((uint32_t)f2h(qv[k].w) << 16);
+        *(uint2 *)&qs[i][4 * e4] = make_uint2(lo, hi);
     }
     __syncthreads();
     am_v16f acc = {};
@@ -152,40 +162,71 @@ __global__ __launch_bounds__(256) void k_amm_v(AmmArgs c) {
     const int kvh = blockIdx.x / c.ntt, tt = blockIdx.x % c.ntt, cv = blockIdx.y;
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6, li = lane & 31, kh = lane >> 5;
     const int jl0 = cv * AMM_NP;
-    // 1. per row the global maximum and normaliser (wave w: rows 8 w .. 8 w + 7)
-    for (int k = 0; k < 8; k++) {
-        const int i = wave * 8 + k;
-        int b, h, j0, p;
-        amm_rowinfo<GRP>(c, kvh, tt, i, b, h, j0, p);
-        const bool rv = b < c.nb;                                     // uniform over the wave
-        const size_t R = (size_t)(rv ? b : 0) * c.n_head + h;
-        float m = -INFINITY;
-        for (int c0 = 0; c0 < c.nch; c0 += 64)
-            m = fmaxf(m, group_max<64>(rv && c0 + lane < c.nch ? c.Mc[R * c.nch + c0 + lane] : -INFINITY));
-        double sum = 0.0;
-        for (int c0 = 0; c0 < c.nch; c0 += 64) {
-            const bool on = rv && c0 + lane < c.nch;
-            const float mc = on ? c.Mc[R * c.nch + c0 + lane] : 0.0f;
-            const double lc = on ? c.Lc[R * c.nch + c0 + lane] : 0.0;
-            sum += group_sum_t<64>(on ? lc * exp((double)mc - (double)m) : 0.0);
+    // 1. per row the global maximum and normaliser (wave w: rows 8 w .. 8 w +
+    // 7, lane = chunk, chunks past 64 in further rounds), the eight rows'
+    // loads of a round issued together
+    {
+        float mcv[8], m[8];
+        double lcv[8], sum[8];
+        bool on[8];
+        auto load = [&](int c0, int k, bool &o, float &mc, double &lc) {
+            int b, h, j0, p;
+            amm_rowinfo<GRP>(c, kvh, tt, wave * 8 + k, b, h, j0, p);
+            o = b < c.nb && c0 + lane < c.nch;
+            const size_t at = ((size_t)(b < c.nb ? b : 0) * c.n_head + h) * c.nch + c0 + lane;
+            mc = o ? c.Mc[at] : -INFINITY;
+            lc = o ? c.Lc[at] : 0.0;
+        };
+#pragma unroll
+        for (int k = 0; k < 8; k++) load(0, k, on[k], mcv[k], lcv[k]);
+#pragma unroll
+        for (int k = 0; k < 8; k++) m[k] = group_max<64>(mcv[k]);
+        for (int c1 = 64; c1 < c.nch; c1 += 64) {
+#pragma unroll
+            for (int k = 0; k < 8; k++) {
+                bool o;
+                float mc;
+                double lc;
+                load(c1, k, o, mc, lc);
+                m[k] = fmaxf(m[k], group_max<64>(mc));
+            }
         }
-        if (lane == 0) {
-            mx[i] = m;
-            iv[i] = (float)(1.0 / sum);
+#pragma unroll
+        for (int k = 0; k < 8; k++) sum[k] = group_sum_t<64>(on[k] ? lcv[k] * exp((double)mcv[k] - (double)m[k]) : 0.0);
+        for (int c1 = 64; c1 < c.nch; c1 += 64) {
+#pragma unroll
+            for (int k = 0; k < 8; k++) {
+                bool o;
+                float mc;
+                double lc;
+                load(c1, k, o, mc, lc);
+                sum[k] += group_sum_t<64>(o ? lc * exp((double)mc - (double)m[k]) : 0.0);
+            }
         }
+        if (lane == 0)
+#pragma unroll
+            for (int k = 0; k < 8; k++) {
+                mx[wave * 8 + k] = m[k];
+                iv[wave * 8 + k] = (float)(1.0 / sum[k]);
+            }
     }
     __syncthreads();
-    // 2. the weights (0 outside a row's positions)
-    for (int x = t; x < 32 * AMM_NP; x += 256) {
-        const int i = x / AMM_NP, pp = x % AMM_NP, jl = jl0 + pp, j = c.jb + jl;
-        int b, h, j0, p;
-        amm_rowinfo<GRP>(c, kvh, tt, i, b, h, j0, p);
-        float w = 0.0f;
-        if (b < c.nb && jl < c.span && j >= j0 && j <= p) {
-            const float s = c.S[((size_t)b * c.n_head + h) * c.span + jl];
-            w = (float)exp((double)(s - mx[i])) * iv[i];
+    // 2. the weights (0 outside a row's positions): thread t owns position t
+    // of the span in every row, its 32 score loads issued together
+    static_assert(AMM_NP == 256, "one position per thread");
+    {
+        const int jl = jl0 + t, j = c.jb + jl;
+        float sv[32];
+        bool ok[32];
+#pragma unroll
+        for (int i = 0; i < 32; i++) {
+            int b, h, j0, p;
+            amm_rowinfo<GRP>(c, kvh, tt, i, b, h, j0, p);
+            ok[i] = b < c.nb && jl < c.span && j >= j0 && j <= p;
+            sv[i] = ok[i] ? c.S[((size_t)b * c.n_head + h) * c.span + jl] : 0.0f;
         }
-        wsh[i][pp] = f2h(w);
+#pragma unroll
+        for (int i = 0; i < 32; i++) wsh[i][t] = f2h(ok[i] ? (float)exp((double)(sv[i] - mx[i])) * iv[i] : 0.0f);
     }
     __syncthreads();
     // 3. sum_j w_j V_j: wave w takes the column groups g = w, w + 4, .. of 64
@@ -233,7 +274,14 @@ __global__ __launch_bounds__(256) void k_amm_combine(AmmArgs c) {
     if (e < HD) {
         const float *p = c.P + R * c.nchv * HD + e;
         float r = 0.0f;
-        for (int cv = 0; cv <= last; cv++) r += p[(size_t)cv * HD];
+        for (int c0 = 0; c0 <= last; c0 += 8) {                      // eight loads in flight, added in order
+            float v[8];
+#pragma unroll
+            for (int k = 0; k < 8; k++) v[k] = c0 + k <= last ? p[(size_t)(c0 + k) * HD] : 0.0f;
+#pragma unroll
+            for (int k = 0; k < 8; k++)
+                if (c0 + k <= last) r += v[k];
+        }
         c.out[R * HD + e] = r;
         row[e] = r;
     }
