@@ -374,14 +374,17 @@ extern "C" int g4h_gemma_info(const g4h_gemma *m, int *n_vocab, int *n_embd, int
     return G4H_OK;
 }
 
-// the batch's attention over the cache of qa: a prompt batch (path 0) of
-// kMmMinTokens or more on the matrix cores where the layer allows, else the
-// per-token arithmetic of the decode kernels
-static int attend_batch(g4h_gemma *m, const QkvArgs &qa, int pos0, int nb, int path, hipStream_t s) {
-    if (path != 1 && nb >= kMmMinTokens && attn_batch_mm_ok(qa)) {
+// The attention of nb tokens over the cache of qa, the queries prepared in
+// m->q: on the matrix cores where the layer allows (f16 cache, head dim up to
+// 256), for every call -- a token's row has the same bits in any batch, so
+// decode steps, verify batches and prompt batches agree --, else the
+// per-token kernels' batch form.  pos_dev: token 0's position on the device
+// (a decode step), then npos_max bounds the positions attended.
+static int attend(g4h_gemma *m, const QkvArgs &qa, int pos0, int nb, const int *pos_dev, int npos_max, hipStream_t s) {
+    if (attn_batch_mm_ok(qa)) {
         const size_t wsb = std::max(attn_batch_workspace_bytes(m->H, m->hd_full, m->n_ctx, kRows),
                                     attn_batch_workspace_bytes(m->H, m->hd_swa, m->n_ctx, kRows));
-        G_HIP(launch_attn_batch_mm(m->q, qa, pos0 + 1, nb, m->att, nullptr, m->bws, wsb, s));
+        G_HIP(launch_attn_batch_mm(m->q, qa, pos0 + 1, nb, m->att, nullptr, m->bws, wsb, s, 0, pos_dev, npos_max));
     } else {
         G_HIP(launch_attn_batch(m->q, qa, pos0 + 1, nb, m->att, nullptr, m->bws, s));
     }
@@ -430,7 +433,7 @@ static int run(g4h_gemma *m, const int *tok_dev, int nb, int pos0, const int *st
         const int hd = L.hd, nq = H * hd, F = L.n_ff;
         const float *rope = L.swa ? m->rope_swa : m->rope_full;
         G_RC(trl(il, T_X, m->x, E, E));
-        G_HIP(launch_rms_rows(m->x, L.attn_norm, m->xb, E, nb, eps, s));
+        if (il == 0) G_HIP(launch_rms_rows(m->x, L.attn_norm, m->xb, E, nb, eps, s));   // later layers: the previous residual's launch
         G_RC(mm(L.wq, m->xb, m->q, nb, path, s));
         G_RC(trl(il, T_Q, m->q, nq, nq));
         QkvArgs qa;
@@ -455,9 +458,12 @@ static int run(g4h_gemma *m, const int *tok_dev, int nb, int pos0, const int *st
             G_HIP(launch_pack_qkv(m->q, m->k, L.wv ? m->v : nullptr, m->qkv, nq, hd, nb, s));
             qa.kc = m->kc[il];
             qa.vc = m->vc[il];
-            if (nb > 1) {                                            // every row stored, then the batch attends
+            if (attn_batch_mm_ok(qa)) {                              // every row stored, then the matrix cores attend
+                G_HIP(launch_attn_prep_rows(m->qkv, qa, pos0, nb, m->q, s, pos_dev));
+                G_RC(attend(m, qa, pos0, nb, pos_dev, npos_max, s));
+            } else if (nb > 1) {                                     // every row stored, then the batch attends
                 G_HIP(launch_attn_prep_rows(m->qkv, qa, pos0, nb, m->q, s));
-                G_RC(attend_batch(m, qa, pos0, nb, path, s));
+                G_RC(attend(m, qa, pos0, nb, nullptr, 0, s));
             } else if (hd == 512) {                                  // wide heads: rows prepared first, then the halves attend
                 G_HIP(launch_attn_prep_rows(m->qkv, qa, pos0, 1, m->q, s, pos_dev));
                 G_HIP(launch_attn_decode(m->q, nullptr, qa, pos0 + 1, npos_dev, npos_max, m->att, nullptr, ws, s));
@@ -470,16 +476,16 @@ static int run(g4h_gemma *m, const int *tok_dev, int nb, int pos0, const int *st
             G_HIP(launch_head_prep(m->q, H, hd, nb, L.q_norm, rope, pos0, eps, s, pos_dev));
             qa.kc = m->kc[cil];
             qa.vc = m->vc[cil];
-            if (nb > 1) G_RC(attend_batch(m, qa, pos0, nb, path, s));
+            if (nb > 1 || attn_batch_mm_ok(qa)) G_RC(attend(m, qa, pos0, nb, pos_dev, npos_max, s));
             else G_HIP(launch_attn_decode(m->q, nullptr, qa, pos0 + 1, npos_dev, npos_max, m->att, nullptr, ws, s));
         }
         G_RC(trl(il, T_ATT, m->att, nq, nq));
         G_RC(mm(L.wo, m->att, m->xb, nb, path, s));
         G_RC(trl(il, T_WO, m->xb, E, E));
-        G_HIP(launch_resid(m->x, m->xb, L.post_attn_norm, E, nb, eps, 1.0f, s));
+        // the attention residual and the FFN's RMSNorm in one launch
+        G_HIP(launch_resid(m->x, m->xb, L.post_attn_norm, E, nb, eps, 1.0f, s, L.ffn_norm, m->xb));
         G_RC(trl(il, T_XMID, m->x, E, E));
         // FFN (model.c:718-736)
-        G_HIP(launch_rms_rows(m->x, L.ffn_norm, m->xb, E, nb, eps, s));
         G_RC(mm(L.gate, m->xb, m->g, nb, path, s));
         G_RC(mm(L.up, m->xb, m->u, nb, path, s));
         G_RC(trl(il, T_G, m->g, F, F));
@@ -497,7 +503,9 @@ static int run(g4h_gemma *m, const int *tok_dev, int nb, int pos0, const int *st
         G_RC(trl(il, T_PLH, m->plg, PE, PE));
         G_RC(mm(L.proj, m->plg, m->xb, nb, path, s));
         G_RC(trl(il, T_PROJ, m->xb, E, E));
-        G_HIP(launch_resid(m->x, m->xb, L.post_norm, E, nb, eps, L.out_scale, s));
+        // the layer's last residual and the next layer's RMSNorm in one launch
+        const float *next_norm = il + 1 < m->n_layer ? m->L[il + 1].attn_norm : nullptr;
+        G_HIP(launch_resid(m->x, m->xb, L.post_norm, E, nb, eps, L.out_scale, s, next_norm, next_norm ? m->xb : nullptr));
     }
     G_RC(tr((size_t)NPL + (size_t)m->n_layer * rec, m->x, E, E));
     if (last) {

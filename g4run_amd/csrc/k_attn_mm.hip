@@ -5,8 +5,13 @@
 // Rows of a tile are (token, query head) pairs of one KV head: 32 / GRP
 // tokens x GRP heads = 32 rows.  Token b sits at position p0 + b and attends
 // positions j0(b) .. p0 + b, j0 = max(0, p + 1 - window) with a window (else
-// 0); the batch spans positions jb = j0(0) .. p0 + nb - 1 (on a ring, position
-// j's row is at slot j % ring).
+// 0); on a ring, position j's row is at slot j % ring.  The batch's positions
+// are cut at multiples of 128 (score chunks) and 256 (value spans) counted
+// from 0, so every sum a row takes -- its scores, its chunk statistics, the
+// normaliser over its own chunks (lane k = its k-th chunk), each span's
+// weighted values and the spans added in order -- has the same operands in
+// the same order whatever other tokens share the batch: a token's row has
+// the same bits in any batch, alone included.
 //   scores   grid (KV head x tile, 128-position chunk), 4 waves x 32
 //            positions: S = fp16(q) . K_j (model.c:530-538, no 1/sqrt(d)) as
 //            one v_mfma_f32_32x32x16_f16 per 16 head elements (exact
@@ -20,7 +25,10 @@
 //            the contraction: lane (c, half) loads V[j][2c], V[j][2c + 1] of
 //            its 8 positions, the even and the odd columns of a 64-column
 //            group being two 32-column tiles.
-//   combine  per (token, head) the spans' partials added in order.
+//   combine  per (token, head) its spans' partials added in order.
+// With a device position (decode steps replayed from a graph) the grids are
+// sized for the most positions a call can span and the workgroups past the
+// call's last position return at once.
 // Differences from the per-token kernels are the fp32 orders of the score and
 // value sums and the grouping of the double normaliser: within the
 // attention's tolerance of the CPU, not bit-identical to them.  A non-finite
@@ -48,8 +56,11 @@ struct AmmArgs {
     size_t q8_stride;
     const uint8_t *kc, *vc;
     int n_head, n_kv, window, ring;
-    int p0, nb, jb, span, nch, nchv, ntt;
-    float *S;                        // [nb * n_head][span]
+    int p0, nb;                      // token 0's position (or *pos_dev) and the token count
+    const int *pos_dev;
+    int nch, nchv, ntt;              // the grid: chunks, spans (the strides of Mc / Lc and P), token tiles
+    int jb, span;                    // set on the device by amm_view: first position (a multiple of AMM_NP) and count
+    float *S;                        // [nb * n_head][nch * AMM_CH]
     float *Mc;                       // [nb * n_head][nch]
     double *Lc;                      // [nb * n_head][nch]
     float *P;                        // [nb * n_head][nchv][hd]
@@ -59,18 +70,30 @@ static size_t amm_al(size_t v) { return (v + 255) & ~(size_t)255; }
 struct AmmWs {
     size_t S, Mc, Lc, P, total;
 };
+// most positions a batch spans: its last token's window (or all of its
+// positions) plus the earlier tokens, from a multiple of AMM_NP
+static int amm_span_max(int npos_max, int nb) { return npos_max + nb - 1 + AMM_NP - 1; }
 static AmmWs amm_ws(int n_head, int hd, int nb, int span) {
     const size_t R = (size_t)nb * n_head, nch = (span + AMM_CH - 1) / AMM_CH, nchv = (span + AMM_NP - 1) / AMM_NP;
     AmmWs w;
     w.S = AMM_OFF;
-    w.Mc = w.S + amm_al(R * span * 4);
+    w.Mc = w.S + amm_al(R * nch * AMM_CH * 4);
     w.Lc = w.Mc + amm_al(R * nch * 4);
     w.P = w.Lc + amm_al(R * nch * 8);
     w.total = w.P + amm_al(R * nchv * hd * 4);
     return w;
 }
 size_t attn_batch_mm_workspace_bytes(int n_head, int hd, int npos_max, int nb) {
-    return amm_ws(n_head, hd, nb, npos_max + nb).total;
+    return amm_ws(n_head, hd, nb, amm_span_max(npos_max, nb)).total;
+}
+
+// the call's positions: token 0's position, the first position any token
+// attends rounded down to a multiple of AMM_NP, and the count from there
+__device__ __forceinline__ void amm_view(AmmArgs &c) {
+    if (c.pos_dev) c.p0 = *c.pos_dev;
+    const int j0 = c.window ? max(0, c.p0 + 1 - c.window) : 0;
+    c.jb = j0 / AMM_NP * AMM_NP;
+    c.span = c.p0 + c.nb - c.jb;
 }
 
 __device__ __forceinline__ am_v8h amm_ld8(const void *p) { return *(const am_v8h *)p; }
@@ -97,10 +120,13 @@ __global__ __launch_bounds__(256) void k_amm_scores(AmmArgs c) {
     __shared__ __align__(16) uint16_t qs[32][QS];                   // fp16 queries of the tile
     __shared__ float wm[4][32];
     __shared__ double wl[4][32];
+    amm_view(c);
     const int kvh = blockIdx.x / c.ntt, tt = blockIdx.x % c.ntt, ch = blockIdx.y;
+    if (ch * AMM_CH >= c.span) return;                               // past the call's last position
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6, li = lane & 31, kh = lane >> 5;
     const int jl = ch * AMM_CH + wave * 32 + li, j = c.jb + jl;    // the lane's position (MFMA column)
-    const uint8_t *krow = amm_row(c, c.kc, std::min(j, c.jb + c.span - 1), kvh, HD);
+    const int jfirst = c.window ? max(0, c.p0 + 1 - c.window) : 0;
+    const uint8_t *krow = amm_row(c, c.kc, std::min(std::max(j, jfirst), c.jb + c.span - 1), kvh, HD);
     am_v8h kb[HD / 16];
 #pragma unroll
     for (int s = 0; s < HD / 16; s++) kb[s] = amm_ld8(krow + (16 * s + 8 * kh) * 2);
@@ -130,7 +156,7 @@ __global__ __launch_bounds__(256) void k_amm_scores(AmmArgs c) {
         int b, h, j0, p;
         amm_rowinfo<GRP>(c, kvh, tt, i, b, h, j0, p);
         ok[r] = b < c.nb && jl < c.span && j >= j0 && j <= p;
-        if (ok[r]) c.S[((size_t)b * c.n_head + h) * c.span + jl] = acc[r];
+        if (ok[r]) c.S[((size_t)b * c.n_head + h) * c.nch * AMM_CH + jl] = acc[r];
         const float m = group_max<32>(ok[r] ? acc[r] : -INFINITY);
         if (li == 0) wm[wave][i] = m;
     }
@@ -159,50 +185,52 @@ __global__ __launch_bounds__(256) void k_amm_v(AmmArgs c) {
     constexpr int WS = AMM_NP + 8;
     __shared__ __align__(16) uint16_t wsh[32][WS];                  // fp16 weights of the span
     __shared__ float mx[32], iv[32];
+    amm_view(c);
     const int kvh = blockIdx.x / c.ntt, tt = blockIdx.x % c.ntt, cv = blockIdx.y;
+    if (cv * AMM_NP >= c.span) return;                               // past the call's last position
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6, li = lane & 31, kh = lane >> 5;
     const int jl0 = cv * AMM_NP;
-    // 1. per row the global maximum and normaliser (wave w: rows 8 w .. 8 w +
-    // 7, lane = chunk, chunks past 64 in further rounds), the eight rows'
-    // loads of a round issued together
+    // 1. per row the global maximum and normaliser over the row's own chunks
+    // (wave w: rows 8 w .. 8 w + 7; lane k: the row's k-th chunk, 64 per
+    // round), the eight rows' loads of a round issued together
     {
+        const int nca = (c.span + AMM_CH - 1) / AMM_CH;              // >= any row's chunk count
+        int clo[8], nrc[8];
+        size_t base[8];
+        bool rv[8];
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+            int b, h, j0, p;
+            amm_rowinfo<GRP>(c, kvh, tt, wave * 8 + k, b, h, j0, p);
+            rv[k] = b < c.nb;
+            clo[k] = rv[k] ? (j0 - c.jb) / AMM_CH : 0;
+            nrc[k] = rv[k] ? (p - c.jb) / AMM_CH - clo[k] + 1 : 0;
+            base[k] = ((size_t)(rv[k] ? b : 0) * c.n_head + h) * c.nch + clo[k];
+        }
         float mcv[8], m[8];
         double lcv[8], sum[8];
         bool on[8];
-        auto load = [&](int c0, int k, bool &o, float &mc, double &lc) {
-            int b, h, j0, p;
-            amm_rowinfo<GRP>(c, kvh, tt, wave * 8 + k, b, h, j0, p);
-            o = b < c.nb && c0 + lane < c.nch;
-            const size_t at = ((size_t)(b < c.nb ? b : 0) * c.n_head + h) * c.nch + c0 + lane;
-            mc = o ? c.Mc[at] : -INFINITY;
-            lc = o ? c.Lc[at] : 0.0;
-        };
 #pragma unroll
-        for (int k = 0; k < 8; k++) load(0, k, on[k], mcv[k], lcv[k]);
+        for (int k = 0; k < 8; k++) {
+            on[k] = lane < nrc[k];
+            mcv[k] = on[k] ? c.Mc[base[k] + lane] : -INFINITY;
+            lcv[k] = on[k] ? c.Lc[base[k] + lane] : 0.0;
+        }
 #pragma unroll
         for (int k = 0; k < 8; k++) m[k] = group_max<64>(mcv[k]);
-        for (int c1 = 64; c1 < c.nch; c1 += 64) {
+        for (int c1 = 64; c1 < nca; c1 += 64)
 #pragma unroll
-            for (int k = 0; k < 8; k++) {
-                bool o;
-                float mc;
-                double lc;
-                load(c1, k, o, mc, lc);
-                m[k] = fmaxf(m[k], group_max<64>(mc));
-            }
-        }
+            for (int k = 0; k < 8; k++) m[k] = fmaxf(m[k], group_max<64>(c1 + lane < nrc[k] ? c.Mc[base[k] + c1 + lane] : -INFINITY));
 #pragma unroll
         for (int k = 0; k < 8; k++) sum[k] = group_sum_t<64>(on[k] ? lcv[k] * exp((double)mcv[k] - (double)m[k]) : 0.0);
-        for (int c1 = 64; c1 < c.nch; c1 += 64) {
+        for (int c1 = 64; c1 < nca; c1 += 64)
 #pragma unroll
             for (int k = 0; k < 8; k++) {
-                bool o;
-                float mc;
-                double lc;
-                load(c1, k, o, mc, lc);
+                const bool o = c1 + lane < nrc[k];
+                const float mc = o ? c.Mc[base[k] + c1 + lane] : 0.0f;
+                const double lc = o ? c.Lc[base[k] + c1 + lane] : 0.0;
                 sum[k] += group_sum_t<64>(o ? lc * exp((double)mc - (double)m[k]) : 0.0);
             }
-        }
         if (lane == 0)
 #pragma unroll
             for (int k = 0; k < 8; k++) {
@@ -223,23 +251,27 @@ __global__ __launch_bounds__(256) void k_amm_v(AmmArgs c) {
             int b, h, j0, p;
             amm_rowinfo<GRP>(c, kvh, tt, i, b, h, j0, p);
             ok[i] = b < c.nb && jl < c.span && j >= j0 && j <= p;
-            sv[i] = ok[i] ? c.S[((size_t)b * c.n_head + h) * c.span + jl] : 0.0f;
+            sv[i] = ok[i] ? c.S[((size_t)b * c.n_head + h) * c.nch * AMM_CH + jl] : 0.0f;
         }
 #pragma unroll
         for (int i = 0; i < 32; i++) wsh[i][t] = f2h(ok[i] ? (float)exp((double)(sv[i] - mx[i])) * iv[i] : 0.0f);
     }
     __syncthreads();
     // 3. sum_j w_j V_j: wave w takes the column groups g = w, w + 4, .. of 64
-    const int jlast = c.jb + c.span - 1;
+    // V rows are read at positions clamped to those the batch attends, so
+    // every row loaded holds a stored value (a zero weight times a finite
+    // value); loads below the first attended position are never needed
+    const int jfirst = c.window ? max(0, c.p0 + 1 - c.window) : 0, jlast = c.jb + c.span - 1;
     for (int g = wave; g < HD / 64; g += 4) {
         const int col = 64 * g + 2 * li;
         am_v16f ae = {}, ao = {};
-#pragma unroll 4
+#pragma unroll
         for (int s = 0; s < AMM_NP / 16; s++) {
             const int jb8 = c.jb + jl0 + 16 * s + 8 * kh;
             uint32_t x[8];
 #pragma unroll
-            for (int k = 0; k < 8; k++) x[k] = *(const uint32_t *)(amm_row(c, c.vc, std::min(jb8 + k, jlast), kvh, HD) + col * 2);
+            for (int k = 0; k < 8; k++)
+                x[k] = *(const uint32_t *)(amm_row(c, c.vc, std::min(std::max(jb8 + k, jfirst), jlast), kvh, HD) + col * 2);
             am_v8h be, bo;
 #pragma unroll
             for (int k = 0; k < 8; k++) {
@@ -268,16 +300,18 @@ __global__ __launch_bounds__(256) void k_amm_v(AmmArgs c) {
 template <int HD>
 __global__ __launch_bounds__(256) void k_amm_combine(AmmArgs c) {
     __shared__ float row[256];
+    amm_view(c);
     const int h = blockIdx.x, b = blockIdx.y, e = threadIdx.x;
     const size_t R = (size_t)b * c.n_head + h;
-    const int last = (c.p0 + b - c.jb) / AMM_NP;                    // the token's last span
+    const int p = c.p0 + b, j0 = c.window ? max(0, p + 1 - c.window) : 0;
+    const int first = (j0 - c.jb) / AMM_NP, last = (p - c.jb) / AMM_NP;   // the token's spans
     if (e < HD) {
-        const float *p = c.P + R * c.nchv * HD + e;
+        const float *src = c.P + R * c.nchv * HD + e;
         float r = 0.0f;
-        for (int c0 = 0; c0 <= last; c0 += 8) {                      // eight loads in flight, added in order
+        for (int c0 = first; c0 <= last; c0 += 8) {                  // eight loads in flight, added in order
             float v[8];
 #pragma unroll
-            for (int k = 0; k < 8; k++) v[k] = c0 + k <= last ? p[(size_t)(c0 + k) * HD] : 0.0f;
+            for (int k = 0; k < 8; k++) v[k] = c0 + k <= last ? src[(size_t)(c0 + k) * HD] : 0.0f;
 #pragma unroll
             for (int k = 0; k < 8; k++)
                 if (c0 + k <= last) r += v[k];
@@ -309,8 +343,9 @@ static void amm_go(const AmmArgs &c, hipStream_t s) {
 }
 
 hipError_t launch_attn_batch_mm(const float *q, const QkvArgs &a, int npos0, int nb, float *out, uint8_t *q8out, uint8_t *ws,
-                                size_t ws_bytes, hipStream_t s, size_t q8_stride) {
-    if (!attn_batch_mm_ok(a) || !q || !out || !ws || nb < 1 || npos0 < 1 || nb > 65535) return hipErrorInvalidValue;
+                                size_t ws_bytes, hipStream_t s, size_t q8_stride, const int *pos_dev, int npos_max) {
+    if (!attn_batch_mm_ok(a) || !q || !out || !ws || nb < 1 || nb > 65535 || (!pos_dev && npos0 < 1) || (pos_dev && npos_max < 1))
+        return hipErrorInvalidValue;
     if (a.ring && (a.window <= 0 || a.window > a.ring || nb > a.ring - a.window + 1)) return hipErrorInvalidValue;
     AmmArgs c{};
     c.q = q;
@@ -325,13 +360,21 @@ hipError_t launch_attn_batch_mm(const float *q, const QkvArgs &a, int npos0, int
     c.ring = a.ring;
     c.p0 = npos0 - 1;
     c.nb = nb;
-    c.jb = a.window ? std::max(0, c.p0 + 1 - a.window) : 0;
-    c.span = c.p0 + nb - c.jb;
-    c.nch = (c.span + AMM_CH - 1) / AMM_CH;
-    c.nchv = (c.span + AMM_NP - 1) / AMM_NP;
+    c.pos_dev = pos_dev;
+    // the grid: this call's positions, or with a device position the most a
+    // call can span (npos_max positions attended by its last token)
+    int span;
+    if (pos_dev) {
+        span = amm_span_max(a.window ? std::min(a.window, npos_max) : npos_max, nb);
+    } else {
+        const int j0 = a.window ? std::max(0, c.p0 + 1 - a.window) : 0;
+        span = c.p0 + nb - j0 / AMM_NP * AMM_NP;
+    }
+    c.nch = (span + AMM_CH - 1) / AMM_CH;
+    c.nchv = (span + AMM_NP - 1) / AMM_NP;
     const int grp = a.n_head / a.n_kv;
     c.ntt = (nb + 32 / grp - 1) / (32 / grp);
-    const AmmWs w = amm_ws(a.n_head, a.hd, nb, c.span);
+    const AmmWs w = amm_ws(a.n_head, a.hd, nb, span);
     if (ws_bytes < w.total || (size_t)c.n_kv * c.ntt > 0x7fffffff) return hipErrorInvalidValue;
     c.S = (float *)(ws + w.S);
     c.Mc = (float *)(ws + w.Mc);

@@ -15,31 +15,97 @@ namespace g4 {
 
 namespace {
 
-// scale = 1/sqrt(mean(x^2) + eps) of one row of n floats (256 threads)
+// scale = 1/sqrt(mean(x^2) + eps) of one row of n floats (256 threads),
+// eight loads in flight per thread
 __device__ float row_rms_scale(const float *x, int n, float eps, double *red) {
     double ss = 0.0;
+#pragma unroll 8
     for (int i = threadIdx.x; i < n; i += blockDim.x) ss += (double)x[i] * x[i];
     return rms_scale(wg_sum_double(ss, red), n, eps);
 }
 
-// y = rms(x) * w (w may be null); rows at stride n (blockIdx.x = token)
+// y = rms(x) * w (w may be null); rows at stride n (blockIdx.x = token).
+// K > 0: row elements t + 256 k (k < K) held in registers, every load issued
+// first (n <= 256 K); K = 0: any n.
+template <int K>
 __global__ __launch_bounds__(256) void k_rms_rows(const float *x, const float *w, float *y, int n, float eps) {
     __shared__ double red[4];
     const size_t b = blockIdx.x;
     x += b * n;
     y += b * n;
-    const float sc = row_rms_scale(x, n, eps, red);
-    for (int i = threadIdx.x; i < n; i += blockDim.x) y[i] = w ? x[i] * sc * w[i] : x[i] * sc;
+    if constexpr (K == 0) {
+        const float sc = row_rms_scale(x, n, eps, red);
+#pragma unroll 8
+        for (int i = threadIdx.x; i < n; i += blockDim.x) y[i] = w ? x[i] * sc * w[i] : x[i] * sc;
+    } else {
+        float xv[K], wv[K];
+        double ss = 0.0;
+#pragma unroll
+        for (int k = 0; k < K; k++) {
+            const int i = threadIdx.x + 256 * k;
+            xv[k] = i < n ? x[i] : 0.0f;
+            wv[k] = i < n && w ? w[i] : 1.0f;
+        }
+#pragma unroll
+        for (int k = 0; k < K; k++) ss += (double)xv[k] * xv[k];
+        const float sc = rms_scale(wg_sum_double(ss, red), n, eps);
+#pragma unroll
+        for (int k = 0; k < K; k++) {
+            const int i = threadIdx.x + 256 * k;
+            if (i < n) y[i] = w ? xv[k] * sc * wv[k] : xv[k] * sc;
+        }
+    }
 }
 
-// x = (x + rms(d) * w) * os (model.c:711-716, 731-736 with os = 1; 748-751)
-__global__ __launch_bounds__(256) void k_resid(float *x, const float *d, const float *w, int n, float eps, float os) {
+// x = (x + rms(d) * w) * os (model.c:711-716, 731-736 with os = 1; 748-751);
+// then, with w2 (the next RMSNorm, model.c:695, 718), y = rms(x) * w2 -- the
+// arithmetic of k_resid followed by k_rms_rows, in one launch.  y may be d.
+template <int K>
+__global__ __launch_bounds__(256) void k_resid(float *x, const float *d, const float *w, int n, float eps, float os,
+                                               const float *w2, float *y) {
     __shared__ double red[4];
     const size_t b = blockIdx.x;
     x += b * n;
     d += b * n;
-    const float sc = row_rms_scale(d, n, eps, red);
-    for (int i = threadIdx.x; i < n; i += blockDim.x) x[i] = (x[i] + d[i] * sc * w[i]) * os;
+    if constexpr (K == 0) {
+        const float sc = row_rms_scale(d, n, eps, red);
+#pragma unroll 8
+        for (int i = threadIdx.x; i < n; i += blockDim.x) x[i] = (x[i] + d[i] * sc * w[i]) * os;
+    } else {
+        float xv[K], dv[K], wv[K], w2v[K];
+#pragma unroll
+        for (int k = 0; k < K; k++) {
+            const int i = threadIdx.x + 256 * k;
+            const bool in = i < n;
+            dv[k] = in ? d[i] : 0.0f;
+            xv[k] = in ? x[i] : 0.0f;
+            wv[k] = in ? w[i] : 0.0f;
+            w2v[k] = in && w2 ? w2[i] : 1.0f;
+        }
+        double ss = 0.0;
+#pragma unroll
+        for (int k = 0; k < K; k++) ss += (double)dv[k] * dv[k];
+        const float sc = rms_scale(wg_sum_double(ss, red), n, eps);
+        double s2 = 0.0;
+#pragma unroll
+        for (int k = 0; k < K; k++) {
+            const int i = threadIdx.x + 256 * k;
+            if (i < n) {
+                xv[k] = (xv[k] + dv[k] * sc * wv[k]) * os;
+                x[i] = xv[k];
+            }
+            s2 += (double)xv[k] * xv[k];                               // 0 past n
+        }
+        if (y) {                                                       // uniform
+            const float sc2 = rms_scale(wg_sum_double(s2, red), n, eps);
+            y += b * n;
+#pragma unroll
+            for (int k = 0; k < K; k++) {
+                const int i = threadIdx.x + 256 * k;
+                if (i < n) y[i] = xv[k] * sc2 * w2v[k];
+            }
+        }
+    }
 }
 
 // y = y * s over nb rows of n (the embedding scales, model.c:609-614)
@@ -118,12 +184,33 @@ unsigned blocks(int64_t n) { return (unsigned)((n + 255) / 256); }
 
 }  // namespace
 
+// elements per thread held in registers for a row of n (0: the loop form)
+static int row_regs(int n) { return n <= 512 ? 2 : n <= 1024 ? 4 : n <= 2048 ? 8 : n <= 4096 ? 16 : n <= 6144 ? 24 : 0; }
 hipError_t launch_rms_rows(const float *x, const float *w, float *y, int n, int nb, float eps, hipStream_t s) {
-    hipLaunchKernelGGL(k_rms_rows, dim3(nb), dim3(256), 0, s, x, w, y, n, eps);
+    switch (row_regs(n)) {
+    case 2: hipLaunchKernelGGL(k_rms_rows<2>, dim3(nb), dim3(256), 0, s, x, w, y, n, eps); break;
+    case 4: hipLaunchKernelGGL(k_rms_rows<4>, dim3(nb), dim3(256), 0, s, x, w, y, n, eps); break;
+    case 8: hipLaunchKernelGGL(k_rms_rows<8>, dim3(nb), dim3(256), 0, s, x, w, y, n, eps); break;
+    case 16: hipLaunchKernelGGL(k_rms_rows<16>, dim3(nb), dim3(256), 0, s, x, w, y, n, eps); break;
+    case 24: hipLaunchKernelGGL(k_rms_rows<24>, dim3(nb), dim3(256), 0, s, x, w, y, n, eps); break;
+    default: hipLaunchKernelGGL(k_rms_rows<0>, dim3(nb), dim3(256), 0, s, x, w, y, n, eps); break;
+    }
     return hipGetLastError();
 }
-hipError_t launch_resid(float *x, const float *d, const float *w, int n, int nb, float eps, float os, hipStream_t s) {
-    hipLaunchKernelGGL(k_resid, dim3(nb), dim3(256), 0, s, x, d, w, n, eps, os);
+hipError_t launch_resid(float *x, const float *d, const float *w, int n, int nb, float eps, float os, hipStream_t s,
+                        const float *w2, float *y) {
+    if ((w2 == nullptr) != (y == nullptr)) return hipErrorInvalidValue;
+    switch (row_regs(n)) {
+    case 2: hipLaunchKernelGGL(k_resid<2>, dim3(nb), dim3(256), 0, s, x, d, w, n, eps, os, w2, y); break;
+    case 4: hipLaunchKernelGGL(k_resid<4>, dim3(nb), dim3(256), 0, s, x, d, w, n, eps, os, w2, y); break;
+    case 8: hipLaunchKernelGGL(k_resid<8>, dim3(nb), dim3(256), 0, s, x, d, w, n, eps, os, w2, y); break;
+    case 16: hipLaunchKernelGGL(k_resid<16>, dim3(nb), dim3(256), 0, s, x, d, w, n, eps, os, w2, y); break;
+    case 24: hipLaunchKernelGGL(k_resid<24>, dim3(nb), dim3(256), 0, s, x, d, w, n, eps, os, w2, y); break;
+    default:                                                           // two launches
+        hipLaunchKernelGGL(k_resid<0>, dim3(nb), dim3(256), 0, s, x, d, w, n, eps, os, nullptr, nullptr);
+        if (y) hipLaunchKernelGGL(k_rms_rows<0>, dim3(nb), dim3(256), 0, s, x, w2, y, n, eps);
+        break;
+    }
     return hipGetLastError();
 }
 hipError_t launch_scale(float *y, int64_t n, float sc, hipStream_t s) {

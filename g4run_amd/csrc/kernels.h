@@ -150,7 +150,10 @@ hipError_t launch_sampler_push(SamplerDev *S, const int *ids, int n, hipStream_t
 
 // k_gemma.hip: the gemma4 forward's row steps (nb token rows each)
 hipError_t launch_rms_rows(const float *x, const float *w, float *y, int n, int nb, float eps, hipStream_t s);
-hipError_t launch_resid(float *x, const float *d, const float *w, int n, int nb, float eps, float os, hipStream_t s);
+// x = (x + rms(d) * w) * os; with w2 and y also y = rms(x) * w2 (the next
+// RMSNorm, y may be d)
+hipError_t launch_resid(float *x, const float *d, const float *w, int n, int nb, float eps, float os, hipStream_t s,
+                        const float *w2 = nullptr, float *y = nullptr);
 hipError_t launch_scale(float *y, int64_t n, float sc, hipStream_t s);
 hipError_t launch_ple_prep(const float *plp, float *pl, const float *w, int pe, int n_layer, int nb, float ps, float is2,
                            float eps, hipStream_t s);
@@ -207,15 +210,19 @@ hipError_t launch_attn_batch(const float *q, const QkvArgs &a, int npos0, int nb
 // The same causal batch on the matrix cores (f16 caches, hd 64 / 128 / 256,
 // 1 / 2 / 4 / 8 query heads per KV head; attn_batch_mm_ok): tiles of 32
 // (token, head) rows share every K and V row they read; within the
-// attention's tolerance of launch_attn_batch, not bit-identical to it.  ws of
+// attention's tolerance of launch_attn_batch, not bit-identical to it, and a
+// token's row has the same bits in any batch.  ws of
 // attn_batch_workspace_bytes (which covers both forms), ws_bytes its size.
+// With pos_dev, token 0's position is read on the device (npos0 unused) and
+// the grid covers a last token attending up to npos_max positions.
 bool attn_batch_mm_ok(const QkvArgs &a);
 // prompt batches of at least this many tokens take the matrix-core kernels
 // (g4h_matmul_path, the batched forwards' attention)
 constexpr int kMmMinTokens = 9;
 size_t attn_batch_mm_workspace_bytes(int n_head, int hd, int npos_max, int nb);
 hipError_t launch_attn_batch_mm(const float *q, const QkvArgs &a, int npos0, int nb, float *out, uint8_t *q8out, uint8_t *ws,
-                                size_t ws_bytes, hipStream_t s, size_t q8_stride = 0);
+                                size_t ws_bytes, hipStream_t s, size_t q8_stride = 0, const int *pos_dev = nullptr,
+                                int npos_max = 0);
 // the query / key / value rows of nb tokens from the fused projection output
 // (rows of (n_head + 2 n_kv) hd floats) prepared as the decode kernels do:
 // queries into qout [nb][n_head][hd], key and value rows into the caches at

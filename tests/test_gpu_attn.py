@@ -484,6 +484,46 @@ def test_prefill_matrix_cores_window_ring(gpu, oracle, hd, pos0, nb, window, rin
         assert not bad.any(), f"token {b}: {bad.sum()} outside tolerance, worst {err.max():.3g}"
 
 
+@pytest.mark.parametrize("hd,grp,pos0,nb,window,ring", [(256, 8, 300, 40, 0, 0), (128, 2, 700, 24, 16, 40),
+                                                         (256, 8, 700, 40, 512, 576), (64, 4, 5, 30, 0, 0)])
+def test_prefill_matrix_cores_rows_independent_of_batch(gpu, oracle, hd, grp, pos0, nb, window, ring):
+    """A token's row has the same bits in any batch, alone included: positions
+    are cut at multiples of 128 / 256 counted from 0, and each row's sums take
+    its own operands in its own order (what lets decode steps, verify batches
+    and prompt batches of the gemma4 model share these kernels)."""
+    G = gpu
+    n_kv = 1 if grp == 8 else 2
+    n_head = grp * n_kv
+    n_pos = pos0 + nb
+    slots = 2 * ring if ring else n_pos
+    rng = np.random.default_rng(hd + nb)
+    rb = hd * 2
+    caches = []
+    for c in range(2):
+        lin = G.Buffer(n_pos * n_kv * rb)
+        G.kv_store(G.F16, G.Buffer.from_array(rng.standard_normal((n_pos * n_kv, hd)).astype(np.float32)), lin, hd,
+                   rows=n_pos * n_kv, dst_stride=rb)
+        h = lin.download(np.uint8, (n_pos, n_kv * rb))
+        g = np.zeros((slots, n_kv * rb), np.uint8)
+        for j in range(n_pos):
+            g[j % ring if ring else j] = h[j]
+            if ring:
+                g[j % ring + ring] = h[j]
+        caches.append(G.Buffer.from_array(g))
+    q = (rng.standard_normal((nb, n_head, hd)) * 0.5).astype(np.float32)
+
+    def run(b0, cnt):
+        out = G.Buffer(cnt * n_head * hd * 4)
+        G.attn_prefill_mm(G.Buffer.from_array(np.ascontiguousarray(q[b0:b0 + cnt])), caches[0], caches[1], G.F16, n_head,
+                          n_kv, hd, pos0 + b0, cnt, out, window=window, ring=ring)
+        return out.download(np.float32, (cnt, n_head, hd))
+
+    full = run(0, nb)
+    for b0, cnt in ((0, 1), (5, 1), (nb - 1, 1), (3, 9), (10, nb - 10)):
+        part = run(b0, cnt)
+        assert part.tobytes() == full[b0:b0 + cnt].tobytes(), f"tokens {b0}..{b0 + cnt - 1}"
+
+
 def test_prefill_matrix_cores_errors(gpu):
     G = gpu
     b = G.Buffer(1 << 20)

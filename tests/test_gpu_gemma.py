@@ -409,30 +409,30 @@ def test_model_file_errors(gpu, oracle, tmp_path):
         m.forward([hp["n_vocab"]], 0)
 
 
-def test_attention_timeout_reported_then_recovers(gpu, oracle, tmp_path):
-    """A one-launch attention wait forced to give up (test hook): the forward
-    reports G4H_ERR_TIMEOUT instead of returning NaN logits as if valid; the
-    next forward on the same model is held part by part against the oracle."""
+def test_attention_has_no_bounded_waits(gpu, oracle, tmp_path):
+    """The gemma4 forward attends on the matrix cores (f16 cache, heads up to
+    256) or with the three-pass kernels (512-wide heads, quantized caches):
+    no launch waits on other workgroups, so the test hook that makes the
+    one-launch kernels' waits give up changes nothing -- the forward returns
+    G4H_OK and is held part by part against the oracle."""
     G = gpu
-    hp, T = GM.make_gemma(oracle, 15)
-    path = tmp_path / "t.gguf"
-    GM.write_gemma(path, hp, T)
-    m = G.Gemma(path, n_ctx=32, kv_type=G.F16)
-    m.forward(np.arange(5), 0)
-    try:
-        G.debug_attn_timeout(True)
-        with pytest.raises(G.G4HError) as ei:
-            m.forward([7], 5)
-        assert ei.value.status == G.ERR_TIMEOUT
-    finally:
-        G.debug_attn_timeout(False)
-    oracle.pool_start(8)
-    try:
-        lg, _, _ = traced_forward(G, oracle, hp, T, m, G.F16, [7], 5, 32)
-    finally:
-        oracle.pool_stop()
-    assert np.isfinite(lg).all()
-    m.free()
+    for spec in ("SMALL", "WIDE"):
+        hp, T = GM.make_gemma(oracle, 15, spec=getattr(GM, spec))
+        path = tmp_path / f"t{spec}.gguf"
+        GM.write_gemma(path, hp, T)
+        m = G.Gemma(path, n_ctx=32, kv_type=G.F16)
+        m.forward(np.arange(5), 0)
+        oracle.pool_start(8)
+        try:
+            G.debug_attn_timeout(True)
+            lg, _, _ = traced_forward(G, oracle, hp, T, m, G.F16, [7], 5, 32)
+        finally:
+            G.debug_attn_timeout(False)
+            oracle.pool_stop()
+        assert np.isfinite(lg).all()
+        flags = m.status()
+        assert not flags & G.STATUS_ATTN_TIMEOUT
+        m.free()
 
 
 @pytest.mark.parametrize("spec,kv_type", [("SMALL", 1), ("WIDE", 8), ("WIDE", 1)],
