@@ -784,7 +784,7 @@ extern "C" int g4h_attn_prefill_mm(const float *q, const void *kc, const void *v
     a.vc = (uint8_t *)vc;
     a.window = window;
     a.ring = ring;
-    if (!attn_batch_mm_ok(a)) return fail(G4H_ERR_TYPE, "g4h_attn_prefill_mm: takes f16 caches, head dims 64/128/256");
+    if (!attn_batch_mm_ok(a)) return fail(G4H_ERR_TYPE, "g4h_attn_prefill_mm: takes f16 caches, head dims 64/128/256/512");
     if (ring && (!window || window > ring || nb > ring - window + 1))
         return fail(G4H_ERR_ARG, "g4h_attn_prefill_mm: a ring needs 0 < window <= ring and nb <= ring - window + 1");
     if ((uintptr_t)kc % 16 || (uintptr_t)vc % 16) return fail(G4H_ERR_ARG, "g4h_attn_prefill_mm: caches must be 16-byte aligned");

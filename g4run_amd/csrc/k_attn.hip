@@ -1631,7 +1631,8 @@ constexpr size_t ATT_BATCH_OFF = 256;
 static size_t wide_rows_bytes(int n_head, int nb) { return al256((size_t)nb * n_head * ATT_WIDE * 4); }
 size_t attn_batch_workspace_bytes(int n_head, int hd, int npos_max, int nb) {
     if (hd == ATT_WIDE)
-        return ATT_BATCH_OFF + (size_t)nb * attn_batch_ws(2 * n_head, ATT_HALF, npos_max).tok + 2 * wide_rows_bytes(n_head, nb);
+        return std::max(ATT_BATCH_OFF + (size_t)nb * attn_batch_ws(2 * n_head, ATT_HALF, npos_max).tok + 2 * wide_rows_bytes(n_head, nb),
+                        attn_batch_mm_workspace_bytes(n_head, hd, npos_max, nb));
     return std::max(ATT_BATCH_OFF + (size_t)nb * attn_batch_ws(n_head, hd, npos_max).tok,
                     attn_batch_mm_workspace_bytes(n_head, hd, npos_max, nb));   // either form
 }

@@ -1,5 +1,6 @@
 // k_attn_mm.hip -- causal attention of a prompt batch on the matrix cores:
-// attn_kernel (model.c:509-545) for nb new tokens over an f16 KV cache, the
+// attn_kernel (model.c:509-545) for nb new tokens over an f16 KV cache (head
+// dims 64 to 512, gemma4's full layers included), the
 // tokens of a tile sharing every K and V row they read.
 //
 // Rows of a tile are (token, query head) pairs of one KV head: 32 / GRP
@@ -240,34 +241,37 @@ __global__ __launch_bounds__(256) void k_amm_v(AmmArgs c) {
     }
     __syncthreads();
     // 2. the weights (0 outside a row's positions): thread t owns position t
-    // of the span in every row, its 32 score loads issued together
+    // of the span in every row, its score loads issued 16 rows at a time
     static_assert(AMM_NP == 256, "one position per thread");
-    {
-        const int jl = jl0 + t, j = c.jb + jl;
-        float sv[32];
-        bool ok[32];
 #pragma unroll
-        for (int i = 0; i < 32; i++) {
+    for (int i0 = 0; i0 < 32; i0 += 16) {
+        const int jl = jl0 + t, j = c.jb + jl;
+        float sv[16];
+        bool ok[16];
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
             int b, h, j0, p;
-            amm_rowinfo<GRP>(c, kvh, tt, i, b, h, j0, p);
+            amm_rowinfo<GRP>(c, kvh, tt, i0 + i, b, h, j0, p);
             ok[i] = b < c.nb && jl < c.span && j >= j0 && j <= p;
             sv[i] = ok[i] ? c.S[((size_t)b * c.n_head + h) * c.nch * AMM_CH + jl] : 0.0f;
         }
 #pragma unroll
-        for (int i = 0; i < 32; i++) wsh[i][t] = f2h(ok[i] ? (float)exp((double)(sv[i] - mx[i])) * iv[i] : 0.0f);
+        for (int i = 0; i < 16; i++) wsh[i0 + i][t] = f2h(ok[i] ? (float)exp((double)(sv[i] - mx[i0 + i])) * iv[i0 + i] : 0.0f);
     }
     __syncthreads();
-    // 3. sum_j w_j V_j: wave w takes the column groups g = w, w + 4, .. of 64
-    // V rows are read at positions clamped to those the batch attends, so
-    // every row loaded holds a stored value (a zero weight times a finite
-    // value); loads below the first attended position are never needed
+    // 3. sum_j w_j V_j over the span's 16 steps of 16 positions, in step
+    // order (the MFMA's accumulation): wave w takes the 64-column groups w,
+    // w + 4, ..; lane (c, half) loads columns 2c, 2c + 1 of its 8 positions
+    // per step (the even and the odd columns two 32-column tiles).  V rows
+    // are read at positions clamped to those the batch attends, so every row
+    // loaded holds a stored value (a zero weight times a finite value).
     const int jfirst = c.window ? max(0, c.p0 + 1 - c.window) : 0, jlast = c.jb + c.span - 1;
     for (int g = wave; g < HD / 64; g += 4) {
         const int col = 64 * g + 2 * li;
         am_v16f ae = {}, ao = {};
-#pragma unroll
-        for (int s = 0; s < AMM_NP / 16; s++) {
-            const int jb8 = c.jb + jl0 + 16 * s + 8 * kh;
+#pragma unroll 4
+        for (int st = 0; st < AMM_NP / 16; st++) {
+            const int jb8 = c.jb + jl0 + 16 * st + 8 * kh;
             uint32_t x[8];
 #pragma unroll
             for (int k = 0; k < 8; k++)
@@ -278,7 +282,7 @@ __global__ __launch_bounds__(256) void k_amm_v(AmmArgs c) {
                 be[k] = __builtin_bit_cast(_Float16, (uint16_t)(x[k] & 0xffff));
                 bo[k] = __builtin_bit_cast(_Float16, (uint16_t)(x[k] >> 16));
             }
-            const am_v8h a = amm_ld8(&wsh[li][16 * s + 8 * kh]);
+            const am_v8h a = amm_ld8(&wsh[li][16 * st + 8 * kh]);
             ae = amm_mma(a, be, ae);
             ao = amm_mma(a, bo, ao);
         }
@@ -295,43 +299,49 @@ __global__ __launch_bounds__(256) void k_amm_v(AmmArgs c) {
     }
 }
 
-// grid (n_head, nb), 256 threads: the spans' partials in order; with q8out,
-// the head row as q8_0 blocks too (quants.c:74-109)
+// grid (n_head, nb), 256 threads (elements e and e + 256): the spans'
+// partials in order; with q8out, the head row as q8_0 blocks too
+// (quants.c:74-109)
 template <int HD>
 __global__ __launch_bounds__(256) void k_amm_combine(AmmArgs c) {
-    __shared__ float row[256];
+    constexpr int EP = (HD + 255) / 256;                             // elements per thread
+    __shared__ float row[HD];
     amm_view(c);
-    const int h = blockIdx.x, b = blockIdx.y, e = threadIdx.x;
+    const int h = blockIdx.x, b = blockIdx.y, t = threadIdx.x;
     const size_t R = (size_t)b * c.n_head + h;
     const int p = c.p0 + b, j0 = c.window ? max(0, p + 1 - c.window) : 0;
     const int first = (j0 - c.jb) / AMM_NP, last = (p - c.jb) / AMM_NP;   // the token's spans
-    if (e < HD) {
-        const float *src = c.P + R * c.nchv * HD + e;
-        float r = 0.0f;
-        for (int c0 = first; c0 <= last; c0 += 8) {                  // eight loads in flight, added in order
-            float v[8];
 #pragma unroll
-            for (int k = 0; k < 8; k++) v[k] = c0 + k <= last ? src[(size_t)(c0 + k) * HD] : 0.0f;
+    for (int q = 0; q < EP; q++) {
+        const int e = t + 256 * q;
+        if (e < HD) {
+            const float *src = c.P + R * c.nchv * HD + e;
+            float r = 0.0f;
+            for (int c0 = first; c0 <= last; c0 += 8) {              // eight loads in flight, added in order
+                float v[8];
 #pragma unroll
-            for (int k = 0; k < 8; k++)
-                if (c0 + k <= last) r += v[k];
+                for (int k = 0; k < 8; k++) v[k] = c0 + k <= last ? src[(size_t)(c0 + k) * HD] : 0.0f;
+#pragma unroll
+                for (int k = 0; k < 8; k++)
+                    if (c0 + k <= last) r += v[k];
+            }
+            c.out[R * HD + e] = r;
+            row[e] = r;
         }
-        c.out[R * HD + e] = r;
-        row[e] = r;
     }
     if (c.q8out) {
         __syncthreads();
-        const bool own = e < HD / 4;
+        const bool own = t < HD / 4;
         float v[4] = {0.f, 0.f, 0.f, 0.f};
         if (own)
-            for (int k = 0; k < 4; k++) v[k] = row[4 * e + k];
-        if (e < 64) q8_store4(v, e, own, c.q8out + (size_t)b * c.q8_stride + (size_t)h * (HD / 32) * 34);
+            for (int k = 0; k < 4; k++) v[k] = row[4 * t + k];
+        if (t < (HD / 4 + 63) / 64 * 64) q8_store4(v, t, own, c.q8out + (size_t)b * c.q8_stride + (size_t)h * (HD / 32) * 34);
     }
 }
 
 bool attn_batch_mm_ok(const QkvArgs &a) {
     const int grp = a.n_kv > 0 ? a.n_head / a.n_kv : 0;
-    return a.kv_type == F16 && (a.hd == 64 || a.hd == 128 || a.hd == 256) && a.n_kv > 0 && a.n_head % a.n_kv == 0 &&
+    return a.kv_type == F16 && (a.hd == 64 || a.hd == 128 || a.hd == 256 || a.hd == 512) && a.n_kv > 0 && a.n_head % a.n_kv == 0 &&
            (grp == 1 || grp == 2 || grp == 4 || grp == 8);
 }
 
@@ -385,6 +395,7 @@ hipError_t launch_attn_batch_mm(const float *q, const QkvArgs &a, int npos0, int
     G4_AMM(64, 1) G4_AMM(64, 2) G4_AMM(64, 4) G4_AMM(64, 8)
     G4_AMM(128, 1) G4_AMM(128, 2) G4_AMM(128, 4) G4_AMM(128, 8)
     G4_AMM(256, 1) G4_AMM(256, 2) G4_AMM(256, 4) G4_AMM(256, 8)
+    G4_AMM(512, 1) G4_AMM(512, 2) G4_AMM(512, 4) G4_AMM(512, 8)
 #undef G4_AMM
     return hipGetLastError();
 }

@@ -242,14 +242,15 @@ int g4h_attn_prefill(const float *q_dev, const void *kc_dev, const void *vc_dev,
                      int n_head, int n_kv, int hd, int pos0, int nb, float *out_dev,
                      void *ws_dev, size_t ws_bytes, void *stream);
 /* The same batch on the matrix cores, for prompt prefill: f16 caches, head
- * dims 64 / 128 / 256, 1 / 2 / 4 / 8 query heads per KV head, with the
+ * dims 64 / 128 / 256 / 512, 1 / 2 / 4 / 8 query heads per KV head, with the
  * sliding window and ring of g4h_attn_decode_window (window 0: all positions;
  * on a ring nb <= ring - window + 1).  Tiles of 32 (token, head) rows share
  * every K and V row: scores and weighted value sums on f16 MFMA (exact
  * products, fp32 sums), the softmax statistics and the fp16 weights of the
  * decode kernels.  Rows are within the attention's tolerance of
- * g4h_attn_prefill's, not bit-identical to them; a non-finite V row reaches
- * the earlier rows of its tile.  ws_bytes >= g4h_attn_prefill_workspace_bytes
+ * g4h_attn_prefill's, not bit-identical to them, and a token's row has the
+ * same bits in any batch (positions cut at fixed multiples of 128 / 256);
+ * a non-finite V row reaches the earlier rows of its tile.  ws_bytes >= g4h_attn_prefill_workspace_bytes
  * (n_head, hd, pos0, nb).  Asynchronous.  No counterpart in the reference. */
 int g4h_attn_prefill_mm(const float *q_dev, const void *kc_dev, const void *vc_dev, int kv_type, int n_head, int n_kv,
                         int hd, int pos0, int nb, int window, int ring, float *out_dev, void *ws_dev, size_t ws_bytes,

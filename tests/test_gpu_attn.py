@@ -408,7 +408,9 @@ def _mm_slack(q, kc, vc, n_head, n_kv, hd, rows):
 
 @pytest.mark.parametrize("n_head,n_kv,hd,pos0,nb", [
     (8, 4, 256, 4096, 64), (8, 4, 256, 0, 9), (8, 4, 256, 300, 33), (8, 1, 256, 1000, 17), (4, 4, 128, 200, 40),
-    (8, 2, 64, 77, 20), (16, 8, 128, 513, 100), (8, 4, 256, 127, 1)])
+    (8, 2, 64, 77, 20), (16, 8, 128, 513, 100), (8, 4, 256, 127, 1),
+    # gemma4's full-attention heads: 8 query heads of 512 over one KV head
+    (8, 1, 512, 700, 33), (8, 1, 512, 0, 12), (2, 1, 512, 130, 1)])
 def test_prefill_matrix_cores_vs_oracle(gpu, oracle, n_head, n_kv, hd, pos0, nb):
     """g4h_attn_prefill_mm (model.c:509-545 for a prompt batch): every token's
     row against the oracle's attention at its position (with the fp16-weight
@@ -436,7 +438,7 @@ def test_prefill_matrix_cores_vs_oracle(gpu, oracle, n_head, n_kv, hd, pos0, nb)
 
 
 @pytest.mark.parametrize("hd,pos0,nb,window,ring", [(256, 700, 64, 512, 576), (256, 100, 30, 512, 576), (64, 50, 25, 16, 40),
-                                                    (128, 0, 12, 8, 20), (256, 300, 40, 300, 0)])
+                                                    (128, 0, 12, 8, 20), (256, 300, 40, 300, 0), (512, 600, 20, 300, 0)])
 def test_prefill_matrix_cores_window_ring(gpu, oracle, hd, pos0, nb, window, ring):
     """The sliding window over a KV ring (model.c:517-537): token b attends
     max(0, p + 1 - window) .. p; on a ring each position's row sits at slot
@@ -485,7 +487,8 @@ def test_prefill_matrix_cores_window_ring(gpu, oracle, hd, pos0, nb, window, rin
 
 
 @pytest.mark.parametrize("hd,grp,pos0,nb,window,ring", [(256, 8, 300, 40, 0, 0), (128, 2, 700, 24, 16, 40),
-                                                         (256, 8, 700, 40, 512, 576), (64, 4, 5, 30, 0, 0)])
+                                                         (256, 8, 700, 40, 512, 576), (64, 4, 5, 30, 0, 0),
+                                                         (512, 8, 1000, 33, 0, 0)])
 def test_prefill_matrix_cores_rows_independent_of_batch(gpu, oracle, hd, grp, pos0, nb, window, ring):
     """A token's row has the same bits in any batch, alone included: positions
     are cut at multiples of 128 / 256 counted from 0, and each row's sums take
@@ -530,9 +533,9 @@ def test_prefill_matrix_cores_errors(gpu):
     with pytest.raises(G.G4HError) as e:                              # q8_0 caches stay on the per-token form
         G.attn_prefill_mm(b, b, b, G.Q8_0, 8, 4, 256, 10, 16, b)
     assert e.value.status == G.ERR_TYPE
-    with pytest.raises(G.G4HError) as e:                              # 512-wide heads too
-        G.attn_prefill_mm(b, b, b, G.F16, 8, 1, 512, 10, 16, b)
-    assert e.value.status in (G.ERR_TYPE, G.ERR_SHAPE)
+    with pytest.raises(G.G4HError) as e:                              # head dims are 64 / 128 / 256 / 512
+        G.attn_prefill_mm(b, b, b, G.F16, 8, 4, 192, 10, 16, b)
+    assert e.value.status == G.ERR_TYPE
     with pytest.raises(G.G4HError) as e:                              # a batch longer than the ring allows
         G.attn_prefill_mm(b, b, b, G.F16, 8, 1, 256, 10, 70, b, window=512, ring=576)
     assert e.value.status == G.ERR_ARG
