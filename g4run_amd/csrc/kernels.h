@@ -248,15 +248,6 @@ bool attn_qkv_fits(const g4h_tensor &W, const QkvArgs &a, int npos_max);
 // the bounded-wait settings every hand-off poll uses (attn_force_timeout)
 unsigned attn_spin_limit();
 uint32_t attn_poll_xor();
-// k_fold.hip: the decode step's Wdown (fp32 h quantized to q8_0 inside) and
-// the next layer's Wqkv with its PRO_NORM prologue, whose delta is Wdown's
-// output handed over as tagged words in `words` (nwords of them, zeroed
-// once, 128-byte aligned; the launch needs about Wd.nrows plus 16 per
-// workgroup); yd and yq bit-identical to launch_gemv_x(Wd) then
-// launch_gemv_p(Wq, pro)
-bool down_qkv_fits(const g4h_tensor &Wd, const g4h_tensor &Wq, const GemvPro &pro, size_t nwords);
-hipError_t launch_down_qkv(const g4h_tensor &Wd, const float *h, float *yd, uint64_t *words, size_t nwords, const g4h_tensor &Wq,
-                           const GemvPro &pro, float *yq, const AttnTag &tag, unsigned *err, hipStream_t s);
 hipError_t launch_attn_qkv(const g4h_tensor &W, const GemvPro &pro, const QkvArgs &a, const int *npos_dev, int npos_max,
                            float *out, uint8_t *q8out, uint8_t *ws, uint64_t *qt, hipStream_t s, const AttnTag &tag);
 

@@ -51,8 +51,6 @@ struct g4h_model {
     float *x = nullptr, *x2 = nullptr, *xb = nullptr, *qkv = nullptr, *q = nullptr, *att = nullptr, *ff = nullptr, *logits = nullptr;
     uint8_t *act = nullptr, *ws = nullptr;
     uint64_t *qt = nullptr;          // FUSE_QATT: tagged q|k|v projection rows
-    uint64_t *dq = nullptr;          // FUSE_DQ: tagged Wdown rows
-    size_t dq_words = 0;
     size_t act_bytes = 0, ws_bytes = 0;
     std::vector<void *> allocs;
     int fuse = 0;                    // FUSE_* steps folded into the GEMVs
@@ -80,9 +78,7 @@ static constexpr int kBatchMax = 64;   // G4_BATCH_MAX, g4run.h:23
 //   FUSE_WO    the Wo GEMV inside the one-launch attention, after a hand-off
 //              of the q8_0 head rows (its weights prefetched during the
 //              attention's own hand-offs)
-//   FUSE_DQ    Wdown and the next layer's Wqkv (with FUSE_QKV's prologue) in
-//              one launch, Wdown's rows handed over as tagged words
-enum { FUSE_QKV = 1, FUSE_GU = 2, FUSE_DOWN = 4, FUSE_HEAD = 8, FUSE_QATT = 16, FUSE_WO = 32, FUSE_DQ = 64 };
+enum { FUSE_QKV = 1, FUSE_GU = 2, FUSE_DOWN = 4, FUSE_HEAD = 8, FUSE_QATT = 16, FUSE_WO = 32 };
 // measured on the BASELINE decode step (tok/s, 128 steps at ctx 8192): none
 // 842, QKV 856, GU 928, QKV|GU 955, QKV|GU|QATT 929; QKV|GU 968 against
 // QKV|GU|WO 991 (two runs each, after later kernel work).  In the QATT launch
@@ -90,8 +86,10 @@ enum { FUSE_QKV = 1, FUSE_GU = 2, FUSE_DOWN = 4, FUSE_HEAD = 8, FUSE_QATT = 16, 
 // stream drains far enough to accept its loads, so the rows come out ~5.6 us
 // into the launch and the attention starts later than after a separate GEMV.
 // The WO hand-off costs most of the Wo launch it replaces (~0.9 us net per
-// layer).  QKV|GU|WO|DQ 896 against 962: gathering Wdown's rows in every
-// workgroup waits for poll round trips behind the other CUs' streams.
+// layer).  (Wdown and the next layer's Wqkv in one launch, Wdown's rows handed
+// over as tagged words, measured 896 against 962 and was taken out: gathering
+// those rows in every workgroup waits for poll round trips behind the other
+// CUs' streams.)
 // QKV|GU|WO|HEAD 965-970 against QKV|GU|WO 960-966 (six alternating pairs,
 // HEAD ahead in each); QKV|GU|WO|DOWN 887.
 static constexpr int kDefaultFuse = FUSE_QKV | FUSE_GU | FUSE_WO | FUSE_HEAD;
@@ -152,7 +150,7 @@ extern "C" int g4h_model_create(const g4h_model_config *cfg, uint64_t seed, g4h_
     g4h_model *m = new g4h_model();
     m->c = c;
     m->fuse = kDefaultFuse;
-    if (const char *e = getenv("G4H_DECODE_FUSE")) m->fuse = atoi(e) & 127;
+    if (const char *e = getenv("G4H_DECODE_FUSE")) m->fuse = atoi(e) & 63;
     const int E = c.n_embd, H = c.n_head, KV = c.n_kv, hd = c.head_dim, F = c.n_ff;
     const int qkv_rows = (H + 2 * KV) * hd, qd = H * hd;
     hipStream_t s = nullptr;
@@ -236,9 +234,6 @@ extern "C" int g4h_model_create(const g4h_model_config *cfg, uint64_t seed, g4h_
     if ((rc = model_alloc(m, (void **)&m->ws, m->ws_bytes))) return bail(rc);
     if ((rc = model_alloc(m, (void **)&m->qt, (size_t)qkv_rows * 8))) return bail(rc);
     if (hipMemset(m->qt, 0, (size_t)qkv_rows * 8) != hipSuccess) return bail(G4H_ERR_HIP);
-    m->dq_words = (size_t)c.n_embd + 16 * 1024;                      // rows plus a line per workgroup
-    if ((rc = model_alloc(m, (void **)&m->dq, m->dq_words * 8))) return bail(rc);
-    if (hipMemset(m->dq, 0, m->dq_words * 8) != hipSuccess) return bail(G4H_ERR_HIP);
     (void)wide;
     if (hipMemset(m->state, 0, 64) != hipSuccess) return bail(G4H_ERR_HIP);
     if (hipMemset(m->ws, 0, m->ws_bytes) != hipSuccess) return bail(G4H_ERR_HIP);   // no attention tag seen yet
@@ -336,7 +331,6 @@ extern "C" int g4h_forward_state(g4h_model *m, void *stream) {
     };
     M_HIP(launch_embed_norm(*m->head, token, x, sqrtf((float)E), qkv_pro ? nullptr : norm_of(m, 0, G4H_N_ATTN),
                             c.rms_eps, m->act, s));
-    bool qkv_folded = false;                                          // this layer's Wqkv ran in the last Wdown launch
     for (int l = 0; l < c.n_layer; l++) {
         uint8_t *kc = m->kv + (size_t)(2 * l) * m->kv_layer_bytes, *vc = kc + m->kv_layer_bytes;
         const float *prev_post = l ? norm_of(m, l - 1, G4H_N_POST_FFW) : nullptr;
@@ -353,7 +347,6 @@ extern "C" int g4h_forward_state(g4h_model *m, void *stream) {
         qa.eps = c.rms_eps;
         const AttnTag tag{(const unsigned *)(m->state + 3), (unsigned)c.n_layer, (unsigned)l};
         bool wo_done = false;                                         // Wo computed inside the attention launch
-        bool next_folded = false;                                     // the next layer's Wqkv runs with this Wdown
         if ((fz & FUSE_QATT) && attn_qkv_fits(*m->wqkv[l], qa, c.n_ctx)) {
             GemvPro pro;
             pro.kind = PRO_NORM;
@@ -367,9 +360,7 @@ extern "C" int g4h_forward_state(g4h_model *m, void *stream) {
             M_HIP(launch_attn_qkv(*m->wqkv[l], pro, qa, npos, c.n_ctx, m->att, m->act, m->ws, m->qt, s, tag));
             std::swap(x, xn);
         } else {
-            if (qkv_folded) {
-                std::swap(x, xn);                                     // its prologue wrote the residual to xn
-            } else if (qkv_pro) {
+            if (qkv_pro) {
                 M_HIP(norm_gemv(*m->wqkv[l], l ? m->xb : nullptr, prev_post, norm_of(m, l, G4H_N_ATTN), m->qkv, false));
             } else {
                 if (l) M_HIP(launch_norm_quant(x, m->xb, prev_post, norm_of(m, l, G4H_N_ATTN), c.rms_eps, E, m->act, s));
@@ -403,34 +394,7 @@ extern "C" int g4h_forward_state(g4h_model *m, void *stream) {
                 pro.n = F;
                 M_HIP(launch_gemv_p(*m->wdown[l], nullptr, m->xb, pro, GemvEpi(), s));
             } else if (gemv_fused_fits(*m->wdown[l], 1) && (uintptr_t)m->ff % 16 == 0) {
-                // with FUSE_DQ the next layer's Wqkv and its residual-norm
-                // prologue run in the same launch (not where that layer takes
-                // its projection inside the attention)
-                GemvPro pro;
-                pro.kind = PRO_NORM;
-                pro.x = x;
-                pro.x_out = xn;
-                pro.delta = m->xb;
-                pro.eps = c.rms_eps;
-                pro.n = E;
-                if (l + 1 < c.n_layer) {
-                    pro.w_post = norm_of(m, l, G4H_N_POST_FFW);
-                    pro.w_pre = norm_of(m, l + 1, G4H_N_ATTN);
-                }
-                QkvArgs qn = qa;
-                qn.kc = m->kv + (size_t)(2 * (l + 1)) * m->kv_layer_bytes;
-                qn.vc = qn.kc + m->kv_layer_bytes;
-                const bool fold = (fz & FUSE_DQ) && (fz & FUSE_QKV) && l + 1 < c.n_layer &&
-                                  !((fz & FUSE_QATT) && attn_qkv_fits(*m->wqkv[l + 1], qn, c.n_ctx)) &&
-                                  down_qkv_fits(*m->wdown[l], *m->wqkv[l + 1], pro, m->dq_words);
-                if (fold) {
-                    const AttnTag dtag{(const unsigned *)(m->state + 3), (unsigned)c.n_layer, (unsigned)l};
-                    M_HIP(launch_down_qkv(*m->wdown[l], m->ff, m->xb, m->dq, m->dq_words, *m->wqkv[l + 1], pro, m->qkv, dtag,
-                                          (unsigned *)m->ws, s));
-                    next_folded = true;
-                } else {
-                    M_HIP(launch_gemv_x(*m->wdown[l], m->ff, m->xb, 1, s));  // h quantized in the GEMV
-                }
+                M_HIP(launch_gemv_x(*m->wdown[l], m->ff, m->xb, 1, s));      // h quantized in the GEMV
             } else {
                 M_HIP(launch_quantize_q8_0(m->ff, F, m->act, ast, F, 1, s));
                 M_HIP(launch_gemv(*m->wdown[l], m->act, ast, m->xb, 1, s));
@@ -443,7 +407,6 @@ extern "C" int g4h_forward_state(g4h_model *m, void *stream) {
             M_HIP(launch_gemv(*m->wdown[l], m->act, ast, m->xb, 1, s));
         }
         M_RC(trace_copy(tr, TR_DOWN, m->xb, E));
-        qkv_folded = next_folded;
     }
     const float *last_post = norm_of(m, c.n_layer - 1, G4H_N_POST_FFW), *out_norm = norm_of(m, c.n_layer, 0);
     if (fz & FUSE_HEAD) {
