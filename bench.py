@@ -441,14 +441,15 @@ def bench_gemma(G, pos_fill=1024, steps=64):
         g.step(st.ptr)                                   # outside the capture: workspaces set up
         st.synchronize()
         g.set_state(int(toks[0]), pos_fill, st.ptr)
-        graph = G.Graph(st.ptr, lambda: g.step(st.ptr))
-        graph.launch(st.ptr)                             # warm replay
+        graph = None if EAGER else G.Graph(st.ptr, lambda: g.step(st.ptr))
+        run_step = (lambda: g.step(st.ptr)) if EAGER else (lambda: graph.launch(st.ptr))
+        run_step()                                       # warm replay
         st.synchronize()
         g.set_state(int(toks[0]), pos_fill, st.ptr)
         e0, e1 = G.Event(), G.Event()
         e0.record(st.ptr)
         for _ in range(steps):
-            graph.launch(st.ptr)
+            run_step()
         e1.record(st.ptr)
         ms = e0.elapsed_ms(e1) / steps
         assert g.get_state(st.ptr)[1] == pos_fill + steps
@@ -629,6 +630,8 @@ def main():
                     help="skip the per-config GEMV sweep (BASELINE configs 0 and 2, plus the further formats)")
     ap.add_argument("--decode-steps", type=int, default=128, help="decode steps timed at context ~8192 (0 = skip)")
     ap.add_argument("--no-steady", action="store_true", help="skip the >= 150 MB q4_0 / q8_0 GEMV rows")
+    ap.add_argument("--only", choices=["gemma"], default=None,
+                    help="run one row alone and print it (a diagnostic line, not the bench contract's)")
     ap.add_argument("--eager", action="store_true",
                     help="direct launches instead of graph replays (for rocprofv3 --kernel-trace runs)")
     ap.add_argument("--prefill", default="1,8,64,512", metavar="M,...",
@@ -647,6 +650,9 @@ def main():
     EAGER = args.eager
     import g4run_amd as G
     G.init(0)
+    if args.only == "gemma":                    # the gemma4 row alone (profiling runs)
+        print(json.dumps({"gemma4_gguf": bench_gemma(G)}), flush=True)
+        return
     stream = G.Stream()
     if args.copy_calibration:
         # one device copy of known size: the FETCH_SIZE / WRITE_SIZE scale for --pmc runs
