@@ -1030,6 +1030,11 @@ __global__ __launch_bounds__(256) void k_attn_fused_f16(AttnCtx c) {
     const int nch = (npos + ATT_CHUNK - 1) / ATT_CHUNK;
     const bool live = ch < nch;                                      // uniform over the workgroup
     if (t == 0) bad = 0;
+    // a launch on a workspace whose error word is still set (an earlier launch
+    // gave up and no status call has cleared it) writes NaN: a workgroup of
+    // that launch which started after its last workgroup advanced the epoch
+    // took this launch's tag, and its words may be read as this launch's
+    const bool stale = c.adv && ld_ag(c.err) != 0u;
     if (c.adv && t == 0) st_tag(c.SW + ((size_t)ch * gridDim.x + kvh), 0u, tag);
     const int j0 = ch * ATT_CHUNK + wave * 32, j = j0 + lane;      // lane < 32 owns position j
     const bool pos_chunk = (QKV || c.qkv) && ch == p / ATT_CHUNK;
@@ -1278,7 +1283,7 @@ __global__ __launch_bounds__(256) void k_attn_fused_f16(AttnCtx c) {
 #pragma unroll
                 for (int q = 0; q < 8; q++) r += v[q];
             }
-            if (bad) r = __builtin_nanf("");
+            if (bad || stale) r = __builtin_nanf("");
             c.out[(size_t)(h0 + g) * hd + e0 + t] = r;
         }
         if (c.q8out || WO) {                                         // uniform
@@ -1347,7 +1352,7 @@ __global__ __launch_bounds__(256) void k_attn_fused_f16(AttnCtx c) {
             }
             acc = group_sum<LPRO>(acc);
             const int64_t row = gq * RPWO + rgo;
-            if (go == 0 && row < c.Wo.nrows) c.wo_out[row] = bad ? __builtin_nanf("") : acc;
+            if (go == 0 && row < c.Wo.nrows) c.wo_out[row] = bad || stale ? __builtin_nanf("") : acc;
         }
     }
     if (c.adv && kvh == (int)gridDim.x - 1 && ch == (int)gridDim.y - 1) {   // uniform over the workgroup

@@ -334,6 +334,39 @@ def test_attention_timeout_reported_by_status(gpu, oracle):
     assert np.all(np.abs(got.astype(np.float64) - ref) <= ATOL + RTOL * np.abs(ref))
 
 
+def test_attention_after_unread_timeout_is_nan_until_status(gpu, oracle):
+    """A give-up that no status call has read yet: the next calls on that
+    workspace (waits no longer forced) write NaN, since a workgroup of the
+    failed launch that started after its epoch advance may have left words
+    under the next launch's tag; the status call then reports the failure
+    once, the workspace is cleared before its next use, and results are the
+    oracle's again."""
+    G = gpu
+    n_head, n_kv, hd, n_pos = 8, 4, 256, 1000
+    assert G.attn_passes(G.F16, n_head, n_kv, hd, n_pos) == 1
+    kb, vb, kh, vh = make_cache(G, oracle, G.F16, n_pos, n_kv, hd, seed=78)
+    q = np.random.default_rng(7).standard_normal((n_head, hd)).astype(np.float32)
+    qb, out = G.Buffer.from_array(q), G.Buffer(n_head * hd * 4)
+    ws = G.Buffer(G.attn_workspace_bytes(n_head, hd, n_pos))
+    ws.zero()
+    try:
+        G.debug_attn_timeout(True)
+        G.attn_decode(qb, kb, vb, G.F16, n_head, n_kv, hd, n_pos, out, ws=ws)
+    finally:
+        G.debug_attn_timeout(False)
+    for _ in range(2):
+        G.attn_decode(qb, kb, vb, G.F16, n_head, n_kv, hd, n_pos, out, ws=ws)
+        assert np.isnan(out.download(np.float32, (n_head, hd))).all()
+    assert G.attn_status(ws)
+    assert not G.attn_status(ws)
+    ref = oracle.attn_decode(q, kh, vh, G.F16, n_head, n_kv, hd, n_pos - 1)
+    for _ in range(2):
+        G.attn_decode(qb, kb, vb, G.F16, n_head, n_kv, hd, n_pos, out, ws=ws)
+        got = out.download(np.float32, (n_head, hd))
+        assert np.all(np.abs(got.astype(np.float64) - ref) <= ATOL + RTOL * np.abs(ref))
+    assert not G.attn_status(ws)
+
+
 @pytest.mark.parametrize("kv_type", [1, 8, 2], ids=["f16", "q8_0", "q4_0"])
 @pytest.mark.parametrize("n_head,hd,n_pos,window,ring", [
     (4, 64, 9, 8, 40), (4, 64, 100, 8, 40), (8, 256, 1000, 512, 576), (8, 256, 700, 512, 576), (2, 128, 300, 300, 0),
