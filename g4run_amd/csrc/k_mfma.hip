@@ -653,17 +653,19 @@ size_t mm_planar_bytes(int M, int64_t ncols) {
 }
 
 // One 32 x 32 tile per workgroup with the blocks split over 4 waves while
-// that gives at most 3 workgroups per CU, LDS-staged 64 x 128 tiles beyond
-// (those need nb % 8 == 0 and 32-bit operand offsets; other shapes stay on the
-// one-tile kernel, whose outputs are the same bits).
-// Measured on q8_0 4096 x 4096: 128 tokens 39 us split / 58 us staged, 256
-// tokens 68 / 58 us, 512 tokens 128 / 61 us (the staged kernel runs at about
-// the same time for any token count: its per-workgroup latency, not the
-// memory system, bounds it).
+// that gives at most one workgroup per CU, LDS-staged tiles beyond (those need
+// nb % 8 == 0 and 32-bit operand offsets; other shapes stay on the one-tile
+// kernel, whose outputs are the same bits).  Measured (x quantized in the
+// call, us one-tile / staged): q8_0 4096 x 4096 at 72 tokens 33.0 / 25.3, 128
+// tokens 39.7 / 25.7, 192 tokens 54.7 / 26.0; q4_0 2560 x 2048 at 96 tokens
+// (240 tiles) 14.3 / 15.0, 128 tokens 21.5 / 15.0; q4_0 2560 x 10240 at 96
+// tokens 51.2 / 54.0, 128 tokens 79.5 / 54.5, 256 tokens 120.9 / 56.3.
 static bool mm_small(const g4h_tensor &W, int M) {
     const int64_t tiles = ((W.nrows + 31) / 32) * ((M + 31) / 32);
     const uint64_t wb = W.type == Q8_0 ? 32 : 16;
-    return tiles <= 3 * 256 || W.nb % MML_KB != 0 || (uint64_t)M * W.nb * 32 >= (1ull << 32) ||
+    int64_t most = 256;                                              // G4H_MM_SMALL_TILES overrides (measurement)
+    if (const char *e = getenv("G4H_MM_SMALL_TILES")) most = atoll(e);
+    return tiles <= most || W.nb % MML_KB != 0 || (uint64_t)M * W.nb * 32 >= (1ull << 32) ||
            (uint64_t)W.nrows * W.nb * wb >= (1ull << 32) - 512;     // q8_0: the second half-plane starts 256-B aligned
 }
 

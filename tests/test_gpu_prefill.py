@@ -48,8 +48,8 @@ def test_ragged_shapes(gpu, oracle, qt):
 def test_token_results_independent_of_batch(gpu, oracle, qt, rows, cols, M):
     """Within the matrix-core family a token's outputs are bit-identical for any
     batch size (small-M and large-M tile variants keep the same fp32 order).
-    4096 rows x 256 tokens run the LDS-staged tiles, the smaller batches the
-    one-tile kernel."""
+    4096 rows from 65 tokens run the LDS-staged tiles, 384 rows the one-tile
+    kernel, up to 64 tokens the few-token kernel."""
     w, x, t = _setup(gpu, qt, rows, cols, M, seed=5)
     full = gpu_matmul(gpu, t, x=x, nb=M, path=2)
     if rows == 4096:
@@ -59,6 +59,23 @@ def test_token_results_independent_of_batch(gpu, oracle, qt, rows, cols, M):
     for m in (16, 40, 64, 65, 200):
         part = gpu_matmul(gpu, t, x=x[:m].copy(), nb=m, path=2)
         assert np.array_equal(bits(part), bits(full[:m])), f"M={m}"
+
+
+@pytest.mark.parametrize("qt", [8, 2])
+@pytest.mark.parametrize("rows,cols,M", [(4096, 4096, 128), (2560, 2048, 96), (640, 1024, 300)])
+def test_one_tile_kernel_equals_staged_tiles(gpu, oracle, monkeypatch, qt, rows, cols, M):
+    """The one-tile kernel and the LDS-staged tiles give the same bits on the
+    same call: the selection between them (by tile count, G4H_MM_SMALL_TILES
+    overriding it) moves no output."""
+    w, x, t = _setup(gpu, qt, rows, cols, M, seed=rows + M)
+    out = {}
+    for most, name in (("1000000", "k_mm_mfma"), ("0", "k_mm_lds")):
+        monkeypatch.setenv("G4H_MM_SMALL_TILES", most)
+        assert gpu.matmul_describe(t, M, 2).startswith(name)
+        out[name] = gpu_matmul(gpu, t, x=x, nb=M, path=2)
+    monkeypatch.delenv("G4H_MM_SMALL_TILES")
+    assert np.array_equal(bits(out["k_mm_mfma"]), bits(out["k_mm_lds"]))
+    assert_close(out["k_mm_lds"], oracle_matmul(oracle, qt, w, x), f"{rows}x{cols} M={M}")
 
 
 @pytest.mark.parametrize("qt", [8, 2])
