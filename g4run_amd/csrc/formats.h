@@ -184,18 +184,71 @@ __device__ __forceinline__ Q8KLane q8K_wave(const float v[4]) {
     return r;
 }
 
-// q8_K quantization of fp32 activations straight into the LDS layout (the
-// arithmetic of q8K_wave, so the staged token is bit-identical to quantizing
-// first).  One wave holds superblock sb of token t; the whole wave calls it
-// and writes only with `own` (uniform over the wave).
-__device__ __forceinline__ void q8K_lds4(const float v[4], int sb, bool own, uint8_t *lds, int nb, int t) {
-    const int l = threadIdx.x & 63;
-    const Q8KLane r = q8K_wave(v);
-    if (!own) return;
-    uint8_t *p = lds + (size_t)t * ActQ8_K::bytes_per_token(nb) + (size_t)sb * ActQ8_K::SB;
-    ((uint32_t *)(p + 16))[l] = r.pk;
-    if ((l & 3) == 0) ((int16_t *)(p + 272))[l >> 2] = (int16_t)r.s16;
-    if (l == 0) *(float *)(p + 12) = r.d;
+// q8_K quantization of one fp32 token straight into the LDS layout, a
+// superblock per row of L = 64 / XQ lanes (16 or 32): lane i of row sb holds
+// its elements 4 XQ i .. 4 XQ i + 4 XQ - 1 (XQ groups of 4).  The arithmetic
+// is q8K_wave's, so the staged token is bit-identical to quantizing first:
+// the row maximum of |x| (NaN passed over), the lowest element index that
+// reaches it (a row minimum of 2 index + sign), -127 / that value as iscale,
+// the same rounded products, their 16-element sums and d.  Rows are
+// independent (every exchange stays inside its 16 or 32 lanes), so a row past
+// the token's superblocks just skips it; the wave need not be uniform.
+template <int XQ>
+__device__ __forceinline__ void q8K_rows(const float (&v)[XQ][4], int sb, int nsb, uint8_t *lds, int nb) {
+    static_assert(XQ == 2 || XQ == 4, "16 or 32 lanes per superblock");
+    constexpr int L = 64 / XQ, E = 4 * XQ;                           // lanes per superblock, elements per lane
+    if (sb >= nsb) return;
+    const int i = threadIdx.x & (L - 1);
+    float lm = 0.0f;
+#pragma unroll
+    for (int s = 0; s < XQ; s++)
+#pragma unroll
+        for (int k = 0; k < 4; k++) lm = fmaxf(lm, fabsf(v[s][k]));
+    uint32_t u = __builtin_bit_cast(uint32_t, lm);                   // non-negative: bits order as values
+    u = max(u, partner_u32<1>(u));
+    u = max(u, partner_u32<2>(u));
+    u = max(u, partner_u32<4>(u));
+    u = max(u, partner_u32<8>(u));
+    if constexpr (L == 32) u = max(u, partner_u32<16>(u));
+    const float am = __builtin_bit_cast(float, u);
+    uint32_t key = 0xffffffffu;
+#pragma unroll
+    for (int s = XQ - 1; s >= 0; s--)
+#pragma unroll
+        for (int k = 3; k >= 0; k--)
+            if (fabsf(v[s][k]) == am) key = 2u * (uint32_t)(E * i + 4 * s + k) + (__builtin_bit_cast(uint32_t, v[s][k]) >> 31);
+    key = min(key, partner_u32<1>(key));
+    key = min(key, partner_u32<2>(key));
+    key = min(key, partner_u32<4>(key));
+    key = min(key, partner_u32<8>(key));
+    if constexpr (L == 32) key = min(key, partner_u32<16>(key));
+    uint32_t pk[XQ] = {};
+    int sum = 0;
+    float d = 0.0f;
+    if (am != 0.0f) {
+        const float bv = (key & 1u) ? -am : am;                      // the element itself: |x| == am
+        const float iscale = -127.0f / bv;
+#pragma unroll
+        for (int s = 0; s < XQ; s++)
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                int q = rne_prod(iscale, v[s][k]);
+                q = q < 127 ? q : 127;
+                pk[s] |= ((uint32_t)q & 0xffu) << (8 * k);
+                sum += q;
+            }
+        d = bv * (-1.0f / 127.0f);
+    }
+    if constexpr (L == 32) sum += partner<1>(sum);                   // lanes 2 g, 2 g + 1: bsums group g
+    uint8_t *p = lds + (size_t)sb * ActQ8_K::SB;
+    if constexpr (XQ == 4) {
+        *(uint4 *)(p + 16 + 16 * i) = make_uint4(pk[0], pk[1], pk[2], pk[3]);
+        ((int16_t *)(p + 272))[i] = (int16_t)sum;
+    } else {
+        *(uint2 *)(p + 16 + 8 * i) = make_uint2(pk[0], pk[1]);
+        if ((i & 1) == 0) ((int16_t *)(p + 272))[i >> 1] = (int16_t)sum;
+    }
+    if (i == 0) *(float *)(p + 12) = d;
 }
 
 template <int NB>

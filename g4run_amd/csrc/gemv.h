@@ -27,7 +27,7 @@ size_t act_lds_bytes(int nb_tokens, int64_t nblk) { return (size_t)nb_tokens * F
 // XQ = 0: the NB activations are GGUF q8_0 / q8_K rows (act, act_stride).
 // XQ > 0: x holds the NB tokens as fp32 rows of ncols (contiguous) and every
 // workgroup quantizes them to q8_0 (q4_0 / q8_0 weights) or q8_K (K-quant
-// weights: one wave per superblock) itself, in LDS (q8_lds4 / q8K_lds4: the
+// weights: a superblock per 16 or 32 threads) itself, in LDS (q8_lds4 / q8K_rows: the
 // arithmetic of the standalone quantizers, so results equal quantize-then-GEMV
 // bit for bit);
 // XQ is the number of 4-float groups per thread (NB*ncols/4 <= XQ*blockDim).
@@ -62,9 +62,11 @@ __global__ __launch_bounds__((gemv_max_threads<F, NB, XQ>())) void k_gemv(g4h_te
     float xv[XQ > 0 ? XQ : 1][4];
     const int gpt = (int)(W.ncols >> 2);                            // 4-float groups per token
     if constexpr (XQ > 0) {
+        // q8_0: groups t, t + blockDim, ..; K-quants (one token): the XQ
+        // consecutive groups XQ t .. (a superblock per 64 / XQ threads)
 #pragma unroll
         for (int s = 0; s < XQ; s++) {                                   // clamped, unconditional
-            const int gi = min((int)(threadIdx.x + s * blockDim.x), NB * gpt - 1);
+            const int gi = QK ? min((int)(threadIdx.x + s * blockDim.x), NB * gpt - 1) : min((int)(XQ * threadIdx.x) + s, gpt - 1);
             const float4 v = *(const float4 *)(x + 4 * (size_t)gi);
             xv[s][0] = v.x; xv[s][1] = v.y; xv[s][2] = v.z; xv[s][3] = v.w;
         }
@@ -91,15 +93,11 @@ __global__ __launch_bounds__((gemv_max_threads<F, NB, XQ>())) void k_gemv(g4h_te
             q8_lds4(xv[s], gi - t * gpt, gi < NB * gpt, lds, (int)W.nb, t);
         }
     } else if constexpr (XQ > 0) {
-        // a wave = a superblock per slot (one token: gemv_fused_fits); slots
-        // past the last superblock are skipped by the whole wave
+        // a superblock per row of 64 / XQ threads (one token: gemv_fused_fits,
+        // whose shapes give every superblock a row); rows past the last one
+        // skip it
         static_assert(NB == 1, "K-quant weights quantize one fp32 token in-kernel");
-        const int wbase = (int)(threadIdx.x & ~63u);
-#pragma unroll
-        for (int s = 0; s < XQ; s++) {
-            const int gw = wbase + s * (int)blockDim.x;                 // the wave's first group in this slot
-            if (__builtin_amdgcn_readfirstlane(gw) < gpt) q8K_lds4(xv[s], gw >> 6, true, lds, (int)W.nb, 0);
-        }
+        q8K_rows<XQ>(xv, (int)threadIdx.x / (64 / XQ), (int)(W.ncols >> 8), lds, (int)W.nb);
     } else if constexpr (QK) {
         stage_q8_0_store(stg[0], lds, (int)W.nb, stage_dump<ActQ8_0>(lds, NB, (int)W.nb));
         stage_q8_0_rest<NB>(lds, act, act_stride, (int)W.nb);

@@ -253,7 +253,8 @@ def test_fused_quantizer_equals_prequantized(gpu, oracle, name, qt):
 def test_in_kernel_quantizer_equals_prequantized(gpu, oracle, qt, rows, cols, nb):
     """The shapes whose fp32 input is quantized inside the GEMV (two groups of
     four inputs per thread, or four for one token in larger workgroups; q8_0
-    for q8_0 / q4_0 weights, q8_K with one wave per superblock for K-quants)
+    for q8_0 / q4_0 weights, q8_K with a superblock per 16 or 32 threads for
+    K-quants: both lane widths are among these shapes)
     give the bits of the GEMV on the separately quantized input."""
     from g4run_amd import synth
     w = synth.weights(qt, rows, cols, seed=rows + cols)
