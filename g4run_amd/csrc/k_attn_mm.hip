@@ -181,7 +181,11 @@ __global__ __launch_bounds__(256) void k_amm_scores(AmmArgs c) {
     }
 }
 
-template <int HD, int GRP>
+// PF: steps of V loads in flight per wave in the value sums (4, or 16 / 8
+// for calls of one row tile -- decode steps and short verify batches -- whose
+// few workgroups are bound by that chain's round trips; the MFMAs and their
+// order are the same either way)
+template <int HD, int GRP, int PF>
 __global__ __launch_bounds__(256) void k_amm_v(AmmArgs c) {
     constexpr int WS = AMM_NP + 8;
     __shared__ __align__(16) uint16_t wsh[32][WS];                  // fp16 weights of the span
@@ -266,25 +270,31 @@ __global__ __launch_bounds__(256) void k_amm_v(AmmArgs c) {
     // are read at positions clamped to those the batch attends, so every row
     // loaded holds a stored value (a zero weight times a finite value).
     const int jfirst = c.window ? max(0, c.p0 + 1 - c.window) : 0, jlast = c.jb + c.span - 1;
+#pragma unroll 1
     for (int g = wave; g < HD / 64; g += 4) {
         const int col = 64 * g + 2 * li;
         am_v16f ae = {}, ao = {};
-#pragma unroll 4
-        for (int st = 0; st < AMM_NP / 16; st++) {
-            const int jb8 = c.jb + jl0 + 16 * st + 8 * kh;
-            uint32_t x[8];
+        for (int st0 = 0; st0 < AMM_NP / 16; st0 += PF) {
+            uint32_t x[PF][8];
 #pragma unroll
-            for (int k = 0; k < 8; k++)
-                x[k] = *(const uint32_t *)(amm_row(c, c.vc, std::min(std::max(jb8 + k, jfirst), jlast), kvh, HD) + col * 2);
-            am_v8h be, bo;
+            for (int q = 0; q < PF; q++) {
+                const int jb8 = c.jb + jl0 + 16 * (st0 + q) + 8 * kh;
 #pragma unroll
-            for (int k = 0; k < 8; k++) {
-                be[k] = __builtin_bit_cast(_Float16, (uint16_t)(x[k] & 0xffff));
-                bo[k] = __builtin_bit_cast(_Float16, (uint16_t)(x[k] >> 16));
+                for (int k = 0; k < 8; k++)
+                    x[q][k] = *(const uint32_t *)(amm_row(c, c.vc, std::min(std::max(jb8 + k, jfirst), jlast), kvh, HD) + col * 2);
             }
-            const am_v8h a = amm_ld8(&wsh[li][16 * st + 8 * kh]);
-            ae = amm_mma(a, be, ae);
-            ao = amm_mma(a, bo, ao);
+#pragma unroll
+            for (int q = 0; q < PF; q++) {
+                am_v8h be, bo;
+#pragma unroll
+                for (int k = 0; k < 8; k++) {
+                    be[k] = __builtin_bit_cast(_Float16, (uint16_t)(x[q][k] & 0xffff));
+                    bo[k] = __builtin_bit_cast(_Float16, (uint16_t)(x[q][k] >> 16));
+                }
+                const am_v8h a = amm_ld8(&wsh[li][16 * (st0 + q) + 8 * kh]);
+                ae = amm_mma(a, be, ae);
+                ao = amm_mma(a, bo, ao);
+            }
         }
 #pragma unroll
         for (int r = 0; r < 16; r++) {
@@ -348,7 +358,9 @@ bool attn_batch_mm_ok(const QkvArgs &a) {
 template <int HD, int GRP>
 static void amm_go(const AmmArgs &c, hipStream_t s) {
     hipLaunchKernelGGL((k_amm_scores<HD, GRP>), dim3(c.n_kv * c.ntt, c.nch), dim3(256), 0, s, c);
-    hipLaunchKernelGGL((k_amm_v<HD, GRP>), dim3(c.n_kv * c.ntt, c.nchv), dim3(256), 0, s, c);
+    constexpr int PF1 = HD == 512 ? 8 : 16;                          // 16 steps of 512-wide rows spill
+    if (c.ntt == 1) hipLaunchKernelGGL((k_amm_v<HD, GRP, PF1>), dim3(c.n_kv * c.ntt, c.nchv), dim3(256), 0, s, c);
+    else hipLaunchKernelGGL((k_amm_v<HD, GRP, 4>), dim3(c.n_kv * c.ntt, c.nchv), dim3(256), 0, s, c);
     hipLaunchKernelGGL(k_amm_combine<HD>, dim3(c.n_head, c.nb), dim3(256), 0, s, c);
 }
 
