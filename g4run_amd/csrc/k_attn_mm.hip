@@ -165,6 +165,10 @@ __global__ __launch_bounds__(256) void k_amm_scores(AmmArgs c) {
 #pragma unroll
     for (int r = 0; r < 16; r++) {
         const int i = 8 * (r >> 2) + 4 * kh + (r & 3);
+        // rows 8 (r / 4) .. 8 (r / 4) + 7 hold tokens from (8 (r / 4)) / GRP
+        // on: none of them in the batch (a decode step's later rows) skips
+        // the double exp for the whole wave
+        if (tt * T + 8 * (r >> 2) / GRP >= c.nb) continue;           // uniform
         const float mc = fmaxf(fmaxf(wm[0][i], wm[1][i]), fmaxf(wm[2][i], wm[3][i]));
         const double l = group_sum_t<32>(ok[r] ? exp((double)(acc[r] - mc)) : 0.0);
         if (li == 0) wl[wave][i] = l;
@@ -195,6 +199,42 @@ __global__ __launch_bounds__(256) void k_amm_v(AmmArgs c) {
     if (cv * AMM_NP >= c.span) return;                               // past the call's last position
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6, li = lane & 31, kh = lane >> 5;
     const int jl0 = cv * AMM_NP;
+    const int jfirst = c.window ? max(0, c.p0 + 1 - c.window) : 0, jlast = c.jb + c.span - 1;
+    // the attended positions jfirst .. jlast are at most `ring` apart, so on
+    // a ring (rows stored at j % ring and again at j % ring + ring) they are
+    // one contiguous run of slots from jfirst % ring: one modulo per thread
+    // instead of one per row loaded
+    const uint8_t *vbase = c.vc + ((size_t)(c.ring ? jfirst % c.ring : jfirst) * c.n_kv + kvh) * HD * 2;
+    // lane (c, half)'s V words of step st in column group g (columns 2c,
+    // 2c + 1 of its 8 positions): rows clamped to the positions the batch
+    // attends, so every row loaded holds a stored value
+    auto vword = [&](int g, int st, int k) __attribute__((always_inline)) {
+        const int jb8 = c.jb + jl0 + 16 * st + 8 * kh;
+        return *(const uint32_t *)(vbase + (size_t)(std::min(std::max(jb8 + k, jfirst), jlast) - jfirst) * c.n_kv * HD * 2 +
+                                   (64 * g + 2 * li) * 2);
+    };
+    // one row tile with one column group per wave: every load of the kernel
+    // (this wave's V words, this thread's scores) goes out first, so the
+    // three phases below wait on one round trip instead of three
+    constexpr bool EARLY = PF == 16 && HD <= 256;
+    uint32_t xe[EARLY ? 16 : 1][8];
+    float se[EARLY ? 32 : 1];
+    if constexpr (EARLY) {
+        if (wave < HD / 64) {                                        // uniform
+#pragma unroll
+            for (int q = 0; q < 16; q++)
+#pragma unroll
+                for (int k = 0; k < 8; k++) xe[q][k] = vword(wave, q, k);
+        }
+        const int jl = jl0 + t, j = c.jb + jl;
+#pragma unroll
+        for (int i = 0; i < 32; i++) {
+            int b, h, j0, p;
+            amm_rowinfo<GRP>(c, kvh, tt, i, b, h, j0, p);
+            const bool ok = b < c.nb && jl < c.span && j >= j0 && j <= p;
+            se[i] = ok ? c.S[((size_t)b * c.n_head + h) * c.nch * AMM_CH + jl] : 0.0f;
+        }
+    }
     // 1. per row the global maximum and normaliser over the row's own chunks
     // (wave w: rows 8 w .. 8 w + 7; lane k: the row's k-th chunk, 64 per
     // round), the eight rows' loads of a round issued together
@@ -227,7 +267,8 @@ __global__ __launch_bounds__(256) void k_amm_v(AmmArgs c) {
 #pragma unroll
             for (int k = 0; k < 8; k++) m[k] = fmaxf(m[k], group_max<64>(c1 + lane < nrc[k] ? c.Mc[base[k] + c1 + lane] : -INFINITY));
 #pragma unroll
-        for (int k = 0; k < 8; k++) sum[k] = group_sum_t<64>(on[k] ? lcv[k] * exp((double)mcv[k] - (double)m[k]) : 0.0);
+        for (int k = 0; k < 8; k++)                                  // rows outside the batch (uniform) skip the exp
+            sum[k] = rv[k] ? group_sum_t<64>(on[k] ? lcv[k] * exp((double)mcv[k] - (double)m[k]) : 0.0) : 1.0;
         for (int c1 = 64; c1 < nca; c1 += 64)
 #pragma unroll
             for (int k = 0; k < 8; k++) {
@@ -257,19 +298,23 @@ __global__ __launch_bounds__(256) void k_amm_v(AmmArgs c) {
             int b, h, j0, p;
             amm_rowinfo<GRP>(c, kvh, tt, i0 + i, b, h, j0, p);
             ok[i] = b < c.nb && jl < c.span && j >= j0 && j <= p;
-            sv[i] = ok[i] ? c.S[((size_t)b * c.n_head + h) * c.nch * AMM_CH + jl] : 0.0f;
+            if constexpr (EARLY) sv[i] = se[i0 + i];
+            else sv[i] = ok[i] ? c.S[((size_t)b * c.n_head + h) * c.nch * AMM_CH + jl] : 0.0f;
         }
 #pragma unroll
-        for (int i = 0; i < 16; i++) wsh[i0 + i][t] = f2h(ok[i] ? (float)exp((double)(sv[i] - mx[i0 + i])) * iv[i0 + i] : 0.0f);
+        for (int i = 0; i < 16; i++) {
+            int b, h, j0, p;
+            amm_rowinfo<GRP>(c, kvh, tt, i0 + i, b, h, j0, p);
+            // a row outside the batch (uniform: a decode step's rows past
+            // its GRP heads) takes weight 0 without the double exp
+            wsh[i0 + i][t] = b < c.nb ? f2h(ok[i] ? (float)exp((double)(sv[i] - mx[i0 + i])) * iv[i0 + i] : 0.0f) : (uint16_t)0;
+        }
     }
     __syncthreads();
     // 3. sum_j w_j V_j over the span's 16 steps of 16 positions, in step
     // order (the MFMA's accumulation): wave w takes the 64-column groups w,
     // w + 4, ..; lane (c, half) loads columns 2c, 2c + 1 of its 8 positions
-    // per step (the even and the odd columns two 32-column tiles).  V rows
-    // are read at positions clamped to those the batch attends, so every row
-    // loaded holds a stored value (a zero weight times a finite value).
-    const int jfirst = c.window ? max(0, c.p0 + 1 - c.window) : 0, jlast = c.jb + c.span - 1;
+    // per step (the even and the odd columns two 32-column tiles)
 #pragma unroll 1
     for (int g = wave; g < HD / 64; g += 4) {
         const int col = 64 * g + 2 * li;
@@ -277,12 +322,12 @@ __global__ __launch_bounds__(256) void k_amm_v(AmmArgs c) {
         for (int st0 = 0; st0 < AMM_NP / 16; st0 += PF) {
             uint32_t x[PF][8];
 #pragma unroll
-            for (int q = 0; q < PF; q++) {
-                const int jb8 = c.jb + jl0 + 16 * (st0 + q) + 8 * kh;
+            for (int q = 0; q < PF; q++)
 #pragma unroll
-                for (int k = 0; k < 8; k++)
-                    x[q][k] = *(const uint32_t *)(amm_row(c, c.vc, std::min(std::max(jb8 + k, jfirst), jlast), kvh, HD) + col * 2);
-            }
+                for (int k = 0; k < 8; k++) {
+                    if constexpr (EARLY) x[q][k] = xe[q][k];                  // loaded at the start (g == wave)
+                    else x[q][k] = vword(g, st0 + q, k);
+                }
 #pragma unroll
             for (int q = 0; q < PF; q++) {
                 am_v8h be, bo;
