@@ -585,6 +585,20 @@ static int matmul_impl(const g4h_tensor *W, const float *x, const void *pre, siz
         // chunks of 8/4/2/1
         const uint8_t *act = (const uint8_t *)pre;
         size_t stride = pre_stride;
+        if (x && nb <= 2 && (uintptr_t)x % 16 == 0 && W->ncols % 8 == 0) {
+            // one or two aligned fp32 tokens: converted inside the GEMV, same
+            // bits, one launch (larger batches convert once up front: every
+            // wave would reread and convert all of their tokens)
+            for (int done = 0; done < nb;) {
+                const int left = nb - done, chunk = left >= 8 ? 8 : left >= 4 ? 4 : left >= 2 ? 2 : 1;
+                const hipError_t e = launch_gemv_float_x(W->type, W->qs, (size_t)W->ncols * 2, W->nrows, W->ncols,
+                                                         x + (size_t)done * W->ncols, W->ncols, Y + (size_t)done * W->nrows,
+                                                         W->nrows, chunk, s);
+                if (e != hipSuccess) return hip_fail(e, "g4h_matmul: gemv launch");
+                done += chunk;
+            }
+            return G4H_OK;
+        }
         if (x) {
             if ((uintptr_t)x % 4) return fail(G4H_ERR_ARG, "g4h_matmul: x must be 4-byte aligned");
             stride = g4h_act_stride(W->type, W->ncols);

@@ -51,7 +51,10 @@ __device__ __forceinline__ void widen8(const uint4 w, float (&f)[8]) {
 
 // One wave per row.  W rows at `ws` bytes, activations of NB tokens at `as`
 // bytes (f16 for F16 weights, fp32 for BF16), 16-byte aligned, ncols % 8 == 0.
-template <int WT, int NB>
+// XF: `act` holds the tokens as fp32 rows instead, converted on load with
+// k_act_float's arithmetic (f16 round-to-nearest-even, or bf16 rounding), so
+// the sums are those of converting first -- one launch instead of two.
+template <int WT, int NB, bool XF>
 __global__ __launch_bounds__(256) void k_gemv_float(const uint8_t *__restrict__ W, size_t ws, int64_t nrows, int64_t ncols,
                                                     const uint8_t *__restrict__ act, size_t as, float *__restrict__ Y,
                                                     size_t ys) {
@@ -70,7 +73,14 @@ __global__ __launch_bounds__(256) void k_gemv_float(const uint8_t *__restrict__ 
 #pragma unroll
         for (int t = 0; t < NB; t++) {
             float af[8];
-            if constexpr (WT == F16) {
+            if constexpr (XF) {
+                const float4 a0 = *(const float4 *)(act + (size_t)t * as + 32 * g);
+                const float4 a1 = *(const float4 *)(act + (size_t)t * as + 32 * g + 16);
+                const float xr[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+#pragma unroll
+                for (int e = 0; e < 8; e++)
+                    af[e] = WT == F16 ? h2f(f2h(xr[e])) : __uint_as_float((uint32_t)f2bf(xr[e]) << 16);
+            } else if constexpr (WT == F16) {
                 widen8<F16>(*(const uint4 *)(act + (size_t)t * as + 16 * g), af);
             } else {
                 const float4 a0 = *(const float4 *)(act + (size_t)t * as + 32 * g);
@@ -89,15 +99,15 @@ __global__ __launch_bounds__(256) void k_gemv_float(const uint8_t *__restrict__ 
     }
 }
 
-template <int WT>
+template <int WT, bool XF>
 static hipError_t gf_go(const uint8_t *W, size_t ws, int64_t nrows, int64_t ncols, const uint8_t *act, size_t as, float *Y,
                         size_t ys, int nb, hipStream_t s) {
     const dim3 grid((unsigned)((nrows + 3) / 4));
     switch (nb) {
-    case 1: hipLaunchKernelGGL((k_gemv_float<WT, 1>), grid, dim3(256), 0, s, W, ws, nrows, ncols, act, as, Y, ys); break;
-    case 2: hipLaunchKernelGGL((k_gemv_float<WT, 2>), grid, dim3(256), 0, s, W, ws, nrows, ncols, act, as, Y, ys); break;
-    case 4: hipLaunchKernelGGL((k_gemv_float<WT, 4>), grid, dim3(256), 0, s, W, ws, nrows, ncols, act, as, Y, ys); break;
-    case 8: hipLaunchKernelGGL((k_gemv_float<WT, 8>), grid, dim3(256), 0, s, W, ws, nrows, ncols, act, as, Y, ys); break;
+    case 1: hipLaunchKernelGGL((k_gemv_float<WT, 1, XF>), grid, dim3(256), 0, s, W, ws, nrows, ncols, act, as, Y, ys); break;
+    case 2: hipLaunchKernelGGL((k_gemv_float<WT, 2, XF>), grid, dim3(256), 0, s, W, ws, nrows, ncols, act, as, Y, ys); break;
+    case 4: hipLaunchKernelGGL((k_gemv_float<WT, 4, XF>), grid, dim3(256), 0, s, W, ws, nrows, ncols, act, as, Y, ys); break;
+    case 8: hipLaunchKernelGGL((k_gemv_float<WT, 8, XF>), grid, dim3(256), 0, s, W, ws, nrows, ncols, act, as, Y, ys); break;
     default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
@@ -106,8 +116,18 @@ static hipError_t gf_go(const uint8_t *W, size_t ws, int64_t nrows, int64_t ncol
 hipError_t launch_gemv_float(int wtype, const uint8_t *W, size_t ws, int64_t nrows, int64_t ncols, const uint8_t *act, size_t as,
                              float *Y, size_t ys, int nb, hipStream_t s) {
     if (ncols % 8 || ws % 16 || as % 16 || (uintptr_t)W % 16 || (uintptr_t)act % 16) return hipErrorInvalidValue;
-    return wtype == F16 ? gf_go<F16>(W, ws, nrows, ncols, act, as, Y, ys, nb, s)
-         : wtype == BF16 ? gf_go<BF16>(W, ws, nrows, ncols, act, as, Y, ys, nb, s)
+    return wtype == F16 ? gf_go<F16, false>(W, ws, nrows, ncols, act, as, Y, ys, nb, s)
+         : wtype == BF16 ? gf_go<BF16, false>(W, ws, nrows, ncols, act, as, Y, ys, nb, s)
+                         : hipErrorInvalidValue;
+}
+
+// the same from fp32 tokens x (row stride xs floats), converted on load
+hipError_t launch_gemv_float_x(int wtype, const uint8_t *W, size_t ws, int64_t nrows, int64_t ncols, const float *x, size_t xs,
+                               float *Y, size_t ys, int nb, hipStream_t s) {
+    if (ncols % 8 || ws % 16 || xs % 4 || (uintptr_t)W % 16 || (uintptr_t)x % 16) return hipErrorInvalidValue;
+    const uint8_t *a = (const uint8_t *)x;
+    return wtype == F16 ? gf_go<F16, true>(W, ws, nrows, ncols, a, xs * 4, Y, ys, nb, s)
+         : wtype == BF16 ? gf_go<BF16, true>(W, ws, nrows, ncols, a, xs * 4, Y, ys, nb, s)
                          : hipErrorInvalidValue;
 }
 

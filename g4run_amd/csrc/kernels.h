@@ -78,6 +78,10 @@ hipError_t launch_gemv_x(const g4h_tensor &W, const float *x, float *Y, int nb, 
 hipError_t launch_gemv_float(int wtype, const uint8_t *W, size_t ws, int64_t nrows, int64_t ncols, const uint8_t *act, size_t as,
                              float *Y, size_t ys, int nb, hipStream_t s);
 hipError_t launch_act_float(int wtype, const float *x, size_t xs, int64_t ncols, int nb, uint8_t *out, size_t os, hipStream_t s);
+// the float GEMV straight from fp32 tokens (x 16-byte aligned, row stride xs
+// floats a multiple of 4), with launch_act_float's conversion on load
+hipError_t launch_gemv_float_x(int wtype, const uint8_t *W, size_t ws, int64_t nrows, int64_t ncols, const float *x, size_t xs,
+                               float *Y, size_t ys, int nb, hipStream_t s);
 hipError_t launch_block_sums(const g4h_tensor &W, const uint8_t *act, size_t stride, int tok, int32_t *out, hipStream_t s);
 int block_sums_per_block(int type);
 

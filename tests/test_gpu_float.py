@@ -57,6 +57,9 @@ def test_in_call_conversion_equals_prep_act_and_round_trip(gpu, oracle, name, wt
         a = gpu_matmul(gpu, t, x=x, nb=3)
         b = gpu_matmul(gpu, t, act=oracle.prep_act(wt, x), nb=3)
         assert np.array_equal(bits(a), bits(b))
+        for nb in (1, 2):                                   # converted inside the GEMV (one launch)
+            a = gpu_matmul(gpu, t, x=x[:nb].copy(), nb=nb)
+            assert np.array_equal(bits(a), bits(b[:nb])), f"nb={nb}"
         assert np.array_equal(t.to_rows(), w)
     finally:
         t.free()
