@@ -420,13 +420,17 @@ size_t mm_few_bytes(int M, int64_t ncols) {
 // counter waits are exact (a register ring carried around a loop is undone by
 // the compiler: the loads sink to the loop head and every iteration drains) --
 // within the 63 loads the memory counter tracks and the register file
-template <int MT>
-constexpr int few_seg() { return MT == 1 ? 16 : MT == 2 ? 8 : MT == 3 ? 6 : 4; }
+// (TALL: at least two workgroups per CU -- then shorter segments, fewer
+// registers and more waves per SIMD pay: q4_0 20480x2560 at 64 tokens 37.5 ->
+// 31.0 us with 2 steps instead of 4, at 16 tokens 40.1 -> 22.5 us with 12
+// instead of 16; with one workgroup per CU or fewer the longer segments)
+template <int MT, bool TALL>
+constexpr int few_seg() { return MT == 1 ? (TALL ? 12 : 16) : MT == 2 ? 8 : MT == 3 ? 6 : (TALL ? 2 : 4); }
 
-template <int WT, int MT>
+template <int WT, int MT, bool TALL>
 __global__ __launch_bounds__(256) void k_mm_few(g4h_tensor W, const int8_t *__restrict__ qa,
                                                 const uint16_t *__restrict__ da, int M, float *__restrict__ Y) {
-    constexpr int S = few_seg<MT>();
+    constexpr int S = few_seg<MT, TALL>();
     using WV = std::conditional_t<WT == Q8_0, v4i, v2i>;
     __shared__ float red[3 * MT * 4 * 64];
     // the wave index in a scalar register: the first lane's thread index / 64
@@ -646,6 +650,13 @@ static bool mm_few(const g4h_tensor &W, int M) {
     return M <= MMF_MAXM && (uint64_t)W.nrows * W.nb * (W.type == Q8_0 ? 32 : 16) < (1ull << 32) - 256;
 }
 
+// the few-token kernel's short segments (few_seg): one token tile from two
+// workgroups per CU on, four tiles from one
+static bool few_tall(const g4h_tensor &W, int mt) {
+    const int64_t wgs = (W.nrows + 15) / 16;
+    return mt == 1 ? wgs >= 2 * 256 : mt == 4 ? wgs >= 256 : false;
+}
+
 size_t mm_planar_bytes(int M, int64_t ncols) {
     const int64_t nb = ncols / 32;
     const size_t planar = (((size_t)M * nb * 32 + 255) & ~(size_t)255) + (size_t)M * nb * 2;
@@ -678,7 +689,8 @@ static bool mm_wide(const g4h_tensor &W, int M) { return ((W.nrows + 127) / 128)
 void mm_describe(const g4h_tensor &W, int M, char *buf, size_t len) {
     const char *tn = W.type == Q8_0 ? "q8_0" : "q4_0";
     if (mm_few(W, M)) {
-        snprintf(buf, len, "k_mm_few<%s,mt=%d> grid=%lld block=256", tn, (M + 15) / 16, (long long)((W.nrows + 15) / 16));
+        snprintf(buf, len, "k_mm_few<%s,mt=%d,seg=%s> grid=%lld block=256", tn, (M + 15) / 16,
+                 few_tall(W, (M + 15) / 16) ? "short" : "long", (long long)((W.nrows + 15) / 16));
     } else if (mm_small(W, M)) {
         snprintf(buf, len, "k_mm_mfma<%s,wm=1,wn=1,kb=%d> grid=%lldx%d block=256", tn, MM_KB_SMALL,
                  (long long)((W.nrows + 31) / 32), (M + 31) / 32);
@@ -719,13 +731,15 @@ hipError_t launch_matmul_mfma(const g4h_tensor &W, const float *x, size_t x_stri
         }
         if (hipError_t e = hipGetLastError()) return e;
         const dim3 grid((unsigned)((W.nrows + 15) / 16));
-#define G4_MF(T)                                                                                             \
-    if (mt == T) {                                                                                           \
-        if (W.type == Q8_0) hipLaunchKernelGGL((k_mm_few<Q8_0, T>), grid, dim3(256), 0, s, W, qa, da, M, Y); \
-        else hipLaunchKernelGGL((k_mm_few<Q4_0, T>), grid, dim3(256), 0, s, W, qa, da, M, Y);              \
-        return hipGetLastError();                                                                            \
+        const bool tall = few_tall(W, mt);
+#define G4_MF(T, TL)                                                                                                \
+    if (mt == T && tall == TL) {                                                                                    \
+        if (W.type == Q8_0) hipLaunchKernelGGL((k_mm_few<Q8_0, T, TL>), grid, dim3(256), 0, s, W, qa, da, M, Y);   \
+        else hipLaunchKernelGGL((k_mm_few<Q4_0, T, TL>), grid, dim3(256), 0, s, W, qa, da, M, Y);                \
+        return hipGetLastError();                                                                                   \
     }
-        G4_MF(1) G4_MF(2) G4_MF(3) G4_MF(4)
+        G4_MF(1, false) G4_MF(2, false) G4_MF(3, false) G4_MF(4, false)
+        G4_MF(1, true) G4_MF(4, true)
 #undef G4_MF
         return hipErrorInvalidValue;
     }
