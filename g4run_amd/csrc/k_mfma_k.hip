@@ -4,9 +4,9 @@
 // batched dots are x1 dots four times (quants.c:1535-1547).
 //
 // A workgroup owns a 32-token x 32-row output tile; its MMK_NW waves split
-// the row's superblocks (wave w takes s = w, w + MMK_NW, ...), each holding
-// the next superblock's operands in registers while it multiplies the
-// current one, and their partial tiles are summed through LDS in wave order.
+// the row's superblocks (wave w takes s = w, w + MMK_NW, ...), two
+// superblocks' operands loaded at a time, and their partial tiles are summed
+// through LDS in wave order.
 // Per superblock every integer the reference forms is exact:
 //   q4_K (quants.c:713-762): isum = sum_j sc_j * sum_32 q4 * q8 over the 8
 //     sub-blocks j of 32 -- one v_mfma_i32_32x32x32_i8 per sub-block, each
@@ -84,7 +84,7 @@ __device__ __forceinline__ mk_v8h mk_bsums(const mk_v4i &bs) {
 // one q4_K superblock: exact isum tile, exact summ tile, and the scale
 // products (P[0..15] = d_a d, P[16..31] = d_a dmin)
 struct Q4KSb {
-    static constexpr int T = Q4_K;
+    static constexpr int T = Q4_K, SEG = 2;                              // superblocks whose loads go out together
     // the lane's row: 16-byte header (d | dmin | 12 scale bytes) and its
     // k-half of the 4 nibble rows of 32 bytes
     struct W {
@@ -147,7 +147,7 @@ struct Q4KSb {
 // and 16 + 8 kh .. + 7 of every group, activations and weights alike, so
 // each sub-block is one v_mfma_i32_32x32x16_i8 on 8 bytes of each operand.
 struct Q6KSb {
-    static constexpr int T = Q6_K;
+    static constexpr int T = Q6_K, SEG = 1;
     struct W {
         mk_v4i l0[2], l1[2], hb[2], sc;
         uint16_t d;
@@ -228,20 +228,36 @@ __global__ __launch_bounds__(64 * MMK_NW) void k_mmk(g4h_tensor W, const uint8_t
     const uint8_t *arow = act + (size_t)std::min(m0 + li, M - 1) * stride;
     const int nb = (int)W.nb;
     mk_v16f acc = {};
-    if (wave < nb) {
-        typename S::W w;
-        MkAct a;
-        S::load(w, W, row, wave, kh);
-        S::load_act(a, arow + (size_t)wave * 292, kh);
-        for (int s = wave; s < nb; s += MMK_NW) {
-            const int sn = std::min(s + MMK_NW, nb - 1);                  // the last turn reloads a superblock, unused
-            typename S::W wn;
-            MkAct an;
-            S::load(wn, W, row, sn, kh);
-            S::load_act(an, arow + (size_t)sn * 292, kh);
-            S::mul(w, a, kh, acc);
-            a = an;
-            w = wn;
+    // the wave's superblocks s = wave, wave + MMK_NW, .. two at a time: both
+    // superblocks' operands are loaded before the first multiply, in
+    // straight-line code (a register ring carried around the loop was undone
+    // by the compiler: its loads sank to their uses, several round trips per
+    // superblock)
+    // q4_K: a lone last superblock is loaded twice; its second multiply gets the
+    // activation scale 0, so its products add +0 to an accumulator that never
+    // holds -0 (no branch: the compiler would sink that superblock's loads
+    // into it).
+    for (int s0 = wave; s0 < nb; s0 += S::SEG * MMK_NW) {               // uniform over the wave
+        if constexpr (S::SEG == 2) {
+            const bool two = s0 + MMK_NW < nb;
+            const int s1 = two ? s0 + MMK_NW : s0;
+            typename S::W w0, w1;
+            MkAct a0, a1;
+            S::load(w0, W, row, s0, kh);
+            S::load_act(a0, arow + (size_t)s0 * 292, kh);
+            S::load(w1, W, row, s1, kh);
+            S::load_act(a1, arow + (size_t)s1 * 292, kh);
+            if (!two) a1.d = 0.0f;
+            __builtin_amdgcn_sched_barrier(0);
+            S::mul(w0, a0, kh, acc);
+            __builtin_amdgcn_sched_barrier(0);
+            S::mul(w1, a1, kh, acc);
+        } else {                                                          // q6_K: two superblocks' operands spill
+            typename S::W w0;
+            MkAct a0;
+            S::load(w0, W, row, s0, kh);
+            S::load_act(a0, arow + (size_t)s0 * 292, kh);
+            S::mul(w0, a0, kh, acc);
         }
     }
     // C[i][j]: j = lane % 32 (weight row), i = 8 (r / 4) + 4 kh + r % 4 (token)
