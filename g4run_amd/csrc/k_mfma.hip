@@ -109,11 +109,11 @@ __global__ __launch_bounds__(256) void k_mm_mfma(g4h_tensor W, const int8_t *__r
             if (blk(j0, k) < nb) {                                   // uniform
                 const v4i wv = WT == Q8_0 ? o.w[k] : q4_half(o.w[k], kh);
                 const v16i is = __builtin_amdgcn_mfma_i32_32x32x32_i8(o.a[k], wv, zi, 0, 0, 0);
-                v8h ha = {}, hw = {};
-                if (kh == 0) {
-                    ha[0] = __builtin_bit_cast(_Float16, o.sa[k]);
-                    hw[0] = __builtin_bit_cast(_Float16, o.sw[k]);
-                }
+                // selects, not a lane-divergent branch (which splits the loop
+                // into exec-masked blocks)
+                const _Float16 zh = (_Float16)0.0f;
+                const v8h ha = {kh == 0 ? __builtin_bit_cast(_Float16, o.sa[k]) : zh, zh, zh, zh, zh, zh, zh, zh};
+                const v8h hw = {kh == 0 ? __builtin_bit_cast(_Float16, o.sw[k]) : zh, zh, zh, zh, zh, zh, zh, zh};
                 const v16f sc = __builtin_amdgcn_mfma_f32_32x32x16_f16(ha, hw, zf, 0, 0, 0);
 #pragma unroll
                 for (int r = 0; r < 16; r++) acc[r] = __builtin_fmaf((float)is[r], sc[r], acc[r]);
@@ -377,9 +377,8 @@ __global__ __launch_bounds__(64 * TM * TN, 2) void k_mm_lds(g4h_tensor W, const 
 // nibbles for q4_0) covering both blocks of its row (lane groups 0, 1 block
 // 2 p, groups 2, 3 block 2 p + 1), one 2-byte weight scale, one 16-byte
 // activation load per 16-token tile and one 8-byte load of four tiles'
-// activation scales.  A wave takes its pair steps in segments of few_seg
-// steps whose loads are all issued before the segment's first multiply (the
-// wave's memory-level parallelism: 16 KB of weights per wave for one tile).
+// activation scales.  A wave keeps the loads of FEW_AHEAD pair steps in
+// flight: step k + FEW_AHEAD's loads go out before step k multiplies.
 // One v_permlane32_swap per dword pair turns the loaded halves into the
 // operands of the two blocks' int8 MFMAs (lane group g then holds slice
 // sigma(g) of the block: (0, 2, 1, 3) for q8_0, g for q4_0), and the
@@ -415,22 +414,23 @@ size_t mm_few_bytes(int M, int64_t ncols) {
     return (((size_t)np * mt * 1024 + 255) & ~(size_t)255) + (size_t)np * 256;
 }
 
-// pair steps per segment: a segment's loads (MT + 3 per step) are all issued
-// before its first multiply -- straight-line code, so the compiler's memory
-// counter waits are exact (a register ring carried around a loop is undone by
-// the compiler: the loads sink to the loop head and every iteration drains) --
-// within the 63 loads the memory counter tracks and the register file
-// (TALL: at least two workgroups per CU -- then shorter segments, fewer
-// registers and more waves per SIMD pay: q4_0 20480x2560 at 64 tokens 37.5 ->
-// 31.0 us with 2 steps instead of 4, at 16 tokens 40.1 -> 22.5 us with 12
-// instead of 16; with one workgroup per CU or fewer the longer segments)
-template <int MT, bool TALL>
-constexpr int few_seg() { return MT == 1 ? (TALL ? 12 : 16) : MT == 2 ? 8 : MT == 3 ? 6 : (TALL ? 2 : 4); }
+// The pair steps run as straight-line chunks of FEW_CHUNK steps (then one
+// chunk each of 8, 4, 2, 1 for the rest, so no step is wasted), FEW_AHEAD
+// steps of loads in flight (MT + 3 loads per step, within the 63 the memory
+// counter tracks).  Straight-line code keeps the compiler's memory-counter
+// waits exact: a register ring carried around a loop is undone (InstCombine
+// folds the phi of loads into one load at the loop head, buffer loads sink to
+// the latch) and every iteration drains.  Measured against whole segments of
+// loads issued before their multiplies (x quantized in the call, us):
+// q8_0 4096x4096 at 32 / 64 tokens 12.95 -> 11.79 / 16.36 -> 14.89; q4_0
+// 2560x10240 at 1 token 22.4 -> 18.4; q4_0 20480x2560 at 32 tokens 35.0 ->
+// 25.1; q8_0 2048x2048 at 1 token 9.86 -> 7.58.  A window of 8 steps was
+// slower at 64 tokens (16.0 us).
+constexpr int FEW_CHUNK = 16, FEW_AHEAD = 4;
 
-template <int WT, int MT, bool TALL>
+template <int WT, int MT>
 __global__ __launch_bounds__(256) void k_mm_few(g4h_tensor W, const int8_t *__restrict__ qa,
                                                 const uint16_t *__restrict__ da, int M, float *__restrict__ Y) {
-    constexpr int S = few_seg<MT, TALL>();
     using WV = std::conditional_t<WT == Q8_0, v4i, v2i>;
     __shared__ float red[3 * MT * 4 * 64];
     // the wave index in a scalar register: the first lane's thread index / 64
@@ -504,10 +504,12 @@ __global__ __launch_bounds__(256) void k_mm_few(g4h_tensor W, const int8_t *__re
         // scale operands: lane group 0 holds d_w of block 2 p, group 1 that of
         // 2 p + 1; hw[h][e] has it at k = 4 h + e, where the activation
         // operand holds d_a of block h for tile 2 (tt / 2) + e
-        const _Float16 sw = __builtin_bit_cast(_Float16, (uint16_t)o.s);
-        v4h hw[2][2] = {};
-        if (kg == 0) hw[0][0][0] = sw, hw[0][1][1] = sw;
-        if (kg == 1) hw[1][0][0] = sw, hw[1][1][1] = sw;
+        // (selects, not branches: lane-divergent ifs here split the loop into
+        // exec-masked blocks, across which the compiler kept every step's
+        // MFMA results live -- 256 registers and more instead of 84 to 166)
+        const _Float16 sw = __builtin_bit_cast(_Float16, (uint16_t)o.s), zh = (_Float16)0.0f;
+        const _Float16 sw0 = kg == 0 ? sw : zh, sw1 = kg == 1 ? sw : zh;
+        const v4h hw[2][2] = {{v4h{sw0, zh, zh, zh}, v4h{zh, sw0, zh, zh}}, {v4h{sw1, zh, zh, zh}, v4h{zh, sw1, zh, zh}}};
 #pragma unroll
         for (int tt = 0; tt < MT; tt++) {
             const v2i dv = {(int)(uint32_t)(o.d >> (32 * (tt >> 1))), 0};
@@ -525,18 +527,30 @@ __global__ __launch_bounds__(256) void k_mm_few(g4h_tensor W, const int8_t *__re
         }
     };
 
-    for (int j0 = 0; j0 < nj; j0 += S) {
-        Op ops[S];
-        static_for<0, S>([&](auto I) { ops[I.value] = load(j0 + I.value); });
-        // scheduling barriers: every load of the segment before the first
-        // multiply, and one step's multiplies at a time (left alone the
-        // compiler hoists the whole segment's MFMAs and runs out of registers)
+    // a chunk of C pair steps from j0; scheduling barriers keep each step's
+    // loads where they are issued and one step's multiplies at a time (left
+    // alone the compiler hoists the chunk's MFMAs and runs out of registers)
+    auto chunk = [&](auto Cc, int j0) __attribute__((always_inline)) {
+        constexpr int C = decltype(Cc)::value, A = FEW_AHEAD < C ? FEW_AHEAD : C;
+        Op ops[C];
+        static_for<0, A>([&](auto I) { ops[I.value] = load(j0 + I.value); });
         __builtin_amdgcn_sched_barrier(0);
-        static_for<0, S>([&](auto I) {
-            mac(ops[I.value]);
+        static_for<0, C>([&](auto I) {
+            constexpr int k = I.value;
+            if constexpr (k + A < C) ops[k + A] = load(j0 + k + A);
+            __builtin_amdgcn_sched_barrier(0);
+            mac(ops[k]);
             __builtin_amdgcn_sched_barrier(0);
         });
-    }
+    };
+    int j0 = 0;
+    for (; j0 + FEW_CHUNK <= nj; j0 += FEW_CHUNK) chunk(std::integral_constant<int, FEW_CHUNK>{}, j0);
+    const int rest = nj - j0;                                                // uniform in the wave
+    static_assert(FEW_CHUNK == 16, "the rest is taken as 8 + 4 + 2 + 1");
+    if (rest & 8) chunk(std::integral_constant<int, 8>{}, j0), j0 += 8;
+    if (rest & 4) chunk(std::integral_constant<int, 4>{}, j0), j0 += 4;
+    if (rest & 2) chunk(std::integral_constant<int, 2>{}, j0), j0 += 2;
+    if (rest & 1) chunk(std::integral_constant<int, 1>{}, j0);
 
     // ((p0 + p1) + p2) + p3 through LDS; C[i][j]: i = 4 kg + r (token), j = li (row)
     if (wave > 0) {
@@ -650,13 +664,6 @@ static bool mm_few(const g4h_tensor &W, int M) {
     return M <= MMF_MAXM && (uint64_t)W.nrows * W.nb * (W.type == Q8_0 ? 32 : 16) < (1ull << 32) - 256;
 }
 
-// the few-token kernel's short segments (few_seg): one token tile from two
-// workgroups per CU on, four tiles from one
-static bool few_tall(const g4h_tensor &W, int mt) {
-    const int64_t wgs = (W.nrows + 15) / 16;
-    return mt == 1 ? wgs >= 2 * 256 : mt == 4 ? wgs >= 256 : false;
-}
-
 size_t mm_planar_bytes(int M, int64_t ncols) {
     const int64_t nb = ncols / 32;
     const size_t planar = (((size_t)M * nb * 32 + 255) & ~(size_t)255) + (size_t)M * nb * 2;
@@ -689,8 +696,7 @@ static bool mm_wide(const g4h_tensor &W, int M) { return ((W.nrows + 127) / 128)
 void mm_describe(const g4h_tensor &W, int M, char *buf, size_t len) {
     const char *tn = W.type == Q8_0 ? "q8_0" : "q4_0";
     if (mm_few(W, M)) {
-        snprintf(buf, len, "k_mm_few<%s,mt=%d,seg=%s> grid=%lld block=256", tn, (M + 15) / 16,
-                 few_tall(W, (M + 15) / 16) ? "short" : "long", (long long)((W.nrows + 15) / 16));
+        snprintf(buf, len, "k_mm_few<%s,mt=%d> grid=%lld block=256", tn, (M + 15) / 16, (long long)((W.nrows + 15) / 16));
     } else if (mm_small(W, M)) {
         snprintf(buf, len, "k_mm_mfma<%s,wm=1,wn=1,kb=%d> grid=%lldx%d block=256", tn, MM_KB_SMALL,
                  (long long)((W.nrows + 31) / 32), (M + 31) / 32);
@@ -731,15 +737,13 @@ hipError_t launch_matmul_mfma(const g4h_tensor &W, const float *x, size_t x_stri
         }
         if (hipError_t e = hipGetLastError()) return e;
         const dim3 grid((unsigned)((W.nrows + 15) / 16));
-        const bool tall = few_tall(W, mt);
-#define G4_MF(T, TL)                                                                                                \
-    if (mt == T && tall == TL) {                                                                                    \
-        if (W.type == Q8_0) hipLaunchKernelGGL((k_mm_few<Q8_0, T, TL>), grid, dim3(256), 0, s, W, qa, da, M, Y);   \
-        else hipLaunchKernelGGL((k_mm_few<Q4_0, T, TL>), grid, dim3(256), 0, s, W, qa, da, M, Y);                \
+#define G4_MF(T)                                                                                                    \
+    if (mt == T) {                                                                                                  \
+        if (W.type == Q8_0) hipLaunchKernelGGL((k_mm_few<Q8_0, T>), grid, dim3(256), 0, s, W, qa, da, M, Y);       \
+        else hipLaunchKernelGGL((k_mm_few<Q4_0, T>), grid, dim3(256), 0, s, W, qa, da, M, Y);                    \
         return hipGetLastError();                                                                                   \
     }
-        G4_MF(1, false) G4_MF(2, false) G4_MF(3, false) G4_MF(4, false)
-        G4_MF(1, true) G4_MF(4, true)
+        G4_MF(1) G4_MF(2) G4_MF(3) G4_MF(4)
 #undef G4_MF
         return hipErrorInvalidValue;
     }

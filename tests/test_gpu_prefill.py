@@ -114,15 +114,18 @@ def test_path_selection_and_errors(gpu):
 @pytest.mark.parametrize("qt", [8, 2])
 @pytest.mark.parametrize("rows,cols,Ms", [(4096, 4096, (1, 8, 16, 32, 48, 64)), (100, 2080, (1, 5, 17, 33, 64)),
                                           (33, 1056, (2, 31, 32, 49)), (17, 10240, (3, 16, 19, 63)), (8200, 512, (1, 16, 64)),
-                                          (48, 64, (1, 64)), (16, 32, (7,))])
+                                          (48, 64, (1, 64)), (16, 32, (7,)), (40, 1408, (5, 64))])
 def test_few_kernel_equals_tile_kernel(gpu, oracle, monkeypatch, qt, rows, cols, Ms):
     """The few-token kernel (up to 64 tokens; each weight byte read once,
     operands of a block pair swapped across lane halves) gives the tile
     kernel's bits (G4H_MM_FEW=0): the same exact block sums, exact scale
     products and residue-pair partial sums.  Ragged rows, token counts off the
     16-token tile, odd block counts (a lone last block) and block counts off
-    the 8-block stage, one and two blocks per row; 8200 rows take the short
-    segments of tall matrices."""
+    the 8-block stage, one and two blocks per row, several workgroups per CU
+    (8200 rows).  A wave's pair steps run as 16-step chunks and then one chunk
+    each of 8, 4, 2 and 1 for the rest: 10240 columns take 16 + 16 + 8, 2080
+    columns 8 + 1 (and 8), 1408 columns 4 + 2 (and 4 + 1), 64 columns one step
+    in one wave and none in the other three."""
     w, x, t = _setup(gpu, qt, rows, cols, max(Ms), seed=rows * 7 + cols)
     for M in Ms:
         assert gpu.matmul_describe(t, M, 2).startswith("k_mm_few")
