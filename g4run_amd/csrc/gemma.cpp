@@ -434,8 +434,12 @@ static int run(g4h_gemma *m, const int *tok_dev, int nb, int pos0, const int *st
         const float *rope = L.swa ? m->rope_swa : m->rope_full;
         G_RC(trl(il, T_X, m->x, E, E));
         if (il == 0) G_HIP(launch_rms_rows(m->x, L.attn_norm, m->xb, E, nb, eps, s));   // later layers: the previous residual's launch
-        G_RC(mm(L.wq, m->xb, m->q, nb, path, s));
-        G_RC(trl(il, T_Q, m->q, nq, nq));
+        // one token of a layer with its own K and V: the projections write the
+        // attention's q | k | v row in place (no packing launch)
+        const bool direct = nb == 1 && il < m->n_layer_kv && L.wv;
+        float *qraw = direct ? m->qkv : m->q;
+        G_RC(mm(L.wq, m->xb, qraw, nb, path, s));
+        G_RC(trl(il, T_Q, qraw, nq, nq));
         QkvArgs qa;
         qa.n_head = H;
         qa.n_kv = 1;
@@ -451,11 +455,12 @@ static int run(g4h_gemma *m, const int *tok_dev, int nb, int pos0, const int *st
         uint8_t *ws = L.swa ? m->ws : m->wsf;
         if (il < m->n_layer_kv) {
             // own K/V: q | k | v prepared, stored at the position and attended in one step (model.c:664-689)
-            G_RC(mm(L.wk, m->xb, m->k, nb, path, s));
-            if (L.wv) G_RC(mm(L.wv, m->xb, m->v, nb, path, s));
-            G_RC(trl(il, T_K, m->k, hd, hd));
-            if (L.wv) G_RC(trl(il, T_V, m->v, hd, hd));
-            G_HIP(launch_pack_qkv(m->q, m->k, L.wv ? m->v : nullptr, m->qkv, nq, hd, nb, s));
+            float *kraw = direct ? m->qkv + nq : m->k, *vraw = direct ? m->qkv + nq + hd : m->v;
+            G_RC(mm(L.wk, m->xb, kraw, nb, path, s));
+            if (L.wv) G_RC(mm(L.wv, m->xb, vraw, nb, path, s));
+            G_RC(trl(il, T_K, kraw, hd, hd));
+            if (L.wv) G_RC(trl(il, T_V, vraw, hd, hd));
+            if (!direct) G_HIP(launch_pack_qkv(m->q, m->k, L.wv ? m->v : nullptr, m->qkv, nq, hd, nb, s));
             qa.kc = m->kc[il];
             qa.vc = m->vc[il];
             if (attn_batch_mm_ok(qa)) {                              // every row stored, then the matrix cores attend
