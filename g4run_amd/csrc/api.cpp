@@ -514,7 +514,7 @@ struct ScratchSrc {
 };
 
 static int matmul_impl(const g4h_tensor *W, const float *x, const void *pre, size_t pre_stride, float *Y, int nb, int path,
-                       void *stream, const ScratchSrc &scr);
+                       void *stream, const ScratchSrc &scr, const GemvOut &out = GemvOut());
 
 extern "C" int g4h_matmul_ex(const g4h_tensor *W, const float *x, const void *pre, size_t pre_stride, float *Y, int nb,
                              int path, void *stream) {
@@ -540,7 +540,7 @@ extern "C" int g4h_matmul_noalloc(const g4h_tensor *W, const float *x, const voi
 }
 
 static int matmul_impl(const g4h_tensor *W, const float *x, const void *pre, size_t pre_stride, float *Y, int nb, int path,
-                       void *stream, const ScratchSrc &scr) {
+                       void *stream, const ScratchSrc &scr, const GemvOut &out) {
     G4_NEED_INIT();
     if (!W || !Y) return fail(G4H_ERR_ARG, "g4h_matmul: null tensor or output");
     if ((x == nullptr) == (pre == nullptr)) return fail(G4H_ERR_ARG, "g4h_matmul: pass exactly one of x_dev and pre_dev");
@@ -548,6 +548,10 @@ static int matmul_impl(const g4h_tensor *W, const float *x, const void *pre, siz
     if (path < 0 || path > 2) return fail(G4H_ERR_ARG, "g4h_matmul: path=%d", path);
     if (nb == 0) return G4H_OK;
     const hipStream_t s = (hipStream_t)stream;
+    if (out.mode != OUT_STORE) {
+        if (nb != 1 || path == 2) return fail(G4H_ERR_ARG, "g4h_matmul: a GELU-product store takes one token on the GEMV family");
+        path = 1;
+    }
     if (path == 0) path = g4h_matmul_path(W, nb);
     if (path == 2 && mfma_capable(W) && mmk_capable(W->type)) {
         // K-quants: q8_K activation rows (quantized here from x, or given), read as they are
@@ -593,7 +597,7 @@ static int matmul_impl(const g4h_tensor *W, const float *x, const void *pre, siz
                 const int left = nb - done, chunk = left >= 8 ? 8 : left >= 4 ? 4 : left >= 2 ? 2 : 1;
                 const hipError_t e = launch_gemv_float_x(W->type, W->qs, (size_t)W->ncols * 2, W->nrows, W->ncols,
                                                          x + (size_t)done * W->ncols, W->ncols, Y + (size_t)done * W->nrows,
-                                                         W->nrows, chunk, s);
+                                                         W->nrows, chunk, s, out);
                 if (e != hipSuccess) return hip_fail(e, "g4h_matmul: gemv launch");
                 done += chunk;
             }
@@ -616,7 +620,7 @@ static int matmul_impl(const g4h_tensor *W, const float *x, const void *pre, siz
         for (int done = 0; done < nb;) {
             const int left = nb - done, chunk = left >= 8 ? 8 : left >= 4 ? 4 : left >= 2 ? 2 : 1;
             const hipError_t e = launch_gemv_float(W->type, W->qs, (size_t)W->ncols * 2, W->nrows, W->ncols, act + (size_t)done * stride,
-                                                   stride, Y + (size_t)done * W->nrows, W->nrows, chunk, s);
+                                                   stride, Y + (size_t)done * W->nrows, W->nrows, chunk, s, out);
             if (e != hipSuccess) return hip_fail(e, "g4h_matmul: gemv launch");
             done += chunk;
         }
@@ -630,7 +634,7 @@ static int matmul_impl(const g4h_tensor *W, const float *x, const void *pre, siz
         if (x_fused(*W, nb)) {
             for (int done = 0; done < nb;) {
                 const int chunk = gemv_chunk_at(*W, nb, done);
-                const hipError_t e = launch_gemv_x(*W, x + (size_t)done * W->ncols, Y + (size_t)done * W->nrows, chunk, s);
+                const hipError_t e = launch_gemv_x(*W, x + (size_t)done * W->ncols, Y + (size_t)done * W->nrows, chunk, s, out);
                 if (e != hipSuccess) return hip_fail(e, "g4h_matmul: gemv launch");
                 done += chunk;
             }
@@ -654,7 +658,7 @@ static int matmul_impl(const g4h_tensor *W, const float *x, const void *pre, siz
     int done = 0;
     while (done < nb) {
         const int chunk = gemv_chunk_at(*W, nb, done);
-        const hipError_t e = launch_gemv(*W, act + (size_t)done * stride, stride, Y + (size_t)done * W->nrows, chunk, s);
+        const hipError_t e = launch_gemv(*W, act + (size_t)done * stride, stride, Y + (size_t)done * W->nrows, chunk, s, out);
         if (e != hipSuccess) return hip_fail(e, "g4h_matmul: gemv launch");
         done += chunk;
     }
@@ -664,6 +668,12 @@ static int matmul_impl(const g4h_tensor *W, const float *x, const void *pre, siz
 extern "C" int g4h_matmul(const g4h_tensor *W, const float *x, const void *pre, size_t pre_stride, float *Y, int nb, void *s) {
     return g4h_matmul_ex(W, x, pre, pre_stride, Y, nb, 0, s);
 }
+
+namespace g4 {
+int matmul_out(const g4h_tensor *W, const float *x, float *Y, int nb, void *stream, const GemvOut &out) {
+    return matmul_impl(W, x, nullptr, 0, Y, nb, 1, stream, ScratchSrc(), out);
+}
+}  // namespace g4
 
 extern "C" int g4h_read_floor(const void *src, size_t bytes, float *y, int64_t ny, int threads, int loads, void *s) {
     G4_NEED_INIT();

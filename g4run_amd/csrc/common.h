@@ -37,6 +37,14 @@ __device__ __forceinline__ float opaque(float f) {
 __device__ __forceinline__ float h2f(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
 __device__ __forceinline__ uint16_t f2h(float f) { return __builtin_bit_cast(uint16_t, (_Float16)opaque(f)); }
 
+// gelu(x) through the fp16 table of quants.c:49-58 (g4run.h:73-77): 0 for
+// x <= -10, x for x >= 10, else the table entry of fp16(x)
+__device__ __forceinline__ float gelu_lut(const uint16_t *tab, float x) {
+    if (x <= -10.0f) return 0.0f;
+    if (x >= 10.0f) return x;
+    return h2f(tab[f2h(x)]);
+}
+
 __device__ __forceinline__ int dot4(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }
 
 // Round-half-even of the exact product a*b (valid for |a*b| < 2^22): the fused

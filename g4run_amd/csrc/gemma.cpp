@@ -490,21 +490,39 @@ static int run(g4h_gemma *m, const int *tok_dev, int nb, int pos0, const int *st
         // the attention residual and the FFN's RMSNorm in one launch
         G_HIP(launch_resid(m->x, m->xb, L.post_attn_norm, E, nb, eps, 1.0f, s, L.ffn_norm, m->xb));
         G_RC(trl(il, T_XMID, m->x, E, E));
-        // FFN (model.c:718-736)
+        // FFN (model.c:718-736); one untraced token: h = gelu(gate) * up in the
+        // up projection's store (k_gelu_mul's arithmetic, one launch fewer)
+        const bool fold = nb == 1 && !m->trace;
         G_RC(mm(L.gate, m->xb, m->g, nb, path, s));
-        G_RC(mm(L.up, m->xb, m->u, nb, path, s));
-        G_RC(trl(il, T_G, m->g, F, F));
-        G_RC(trl(il, T_U, m->u, F, F));
-        G_HIP(launch_gelu_mul(m->g, F, m->u, F, F, nb, m->gelu, s));
+        if (fold) {
+            GemvOut o;
+            o.mode = OUT_GELU_E;
+            o.e = m->g;
+            o.gelu = m->gelu;
+            G_RC(matmul_out(L.up, m->xb, m->g, 1, s, o));
+        } else {
+            G_RC(mm(L.up, m->xb, m->u, nb, path, s));
+            G_RC(trl(il, T_G, m->g, F, F));
+            G_RC(trl(il, T_U, m->u, F, F));
+            G_HIP(launch_gelu_mul(m->g, F, m->u, F, F, nb, m->gelu, s));
+        }
         G_RC(trl(il, T_H, m->g, F, F));
         G_RC(mm(L.down, m->g, m->xb, nb, path, s));
         G_RC(trl(il, T_DOWN, m->xb, E, E));
         G_HIP(launch_resid(m->x, m->xb, L.post_ffw_norm, E, nb, eps, 1.0f, s));
         G_RC(trl(il, T_XFFN, m->x, E, E));
         // per-layer embedding injection (model.c:738-752)
-        G_RC(mm(L.inp_gate, m->x, m->plg, nb, path, s));
-        G_RC(trl(il, T_PLG, m->plg, PE, PE));
-        G_HIP(launch_gelu_mul(m->plg, PE, m->pl + (size_t)il * PE, NPL, PE, nb, m->gelu, s));
+        if (fold) {                                                      // gelu(gate) * the layer's row, in the store
+            GemvOut o;
+            o.mode = OUT_GELU_ACC;
+            o.e = m->pl + (size_t)il * PE;
+            o.gelu = m->gelu;
+            G_RC(matmul_out(L.inp_gate, m->x, m->plg, 1, s, o));
+        } else {
+            G_RC(mm(L.inp_gate, m->x, m->plg, nb, path, s));
+            G_RC(trl(il, T_PLG, m->plg, PE, PE));
+            G_HIP(launch_gelu_mul(m->plg, PE, m->pl + (size_t)il * PE, NPL, PE, nb, m->gelu, s));
+        }
         G_RC(trl(il, T_PLH, m->plg, PE, PE));
         G_RC(mm(L.proj, m->plg, m->xb, nb, path, s));
         G_RC(trl(il, T_PROJ, m->xb, E, E));

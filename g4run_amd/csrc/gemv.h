@@ -45,102 +45,32 @@ constexpr int gemv_max_threads() { return XQ == 4 || (NB == 8 && XQ == 0 && gemv
 template <class F, int NB, int LPR, int UPL, int XQ>
 __global__ __launch_bounds__((gemv_max_threads<F, NB, XQ>())) void k_gemv(g4h_tensor W, const uint8_t *__restrict__ act, size_t act_stride,
                                                const float *__restrict__ x, float *__restrict__ Y, int units) {
-    extern __shared__ __align__(16) uint8_t lds[];
-    using Act = typename F::Act;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, wpg = blockDim.x >> 6;
-    const int g = lane % LPR, rg = lane / LPR;
-    constexpr int RPW = 64 / LPR;
-    const int64_t row0 = ((int64_t)blockIdx.x * wpg + wave) * RPW + rg;
-    const bool row_ok = row0 < W.nrows;
-    const int64_t row = row_ok ? row0 : W.nrows - 1;
-    constexpr bool QK = F::type == Q4_0 || F::type == Q8_0;
+#define G4_GEMV_STORE(v) (v)
+#include "gemv_body.inc"
+#undef G4_GEMV_STORE
+}
 
-    // activation loads first, then the weight stream (see formats.h); one
-    // K-quant token needs about two q8_K items per thread, both issued here
-    constexpr int KS = (!QK && NB == 1) ? 2 : 1;
-    typename StageOf<F::type>::S stg[KS];
-    float xv[XQ > 0 ? XQ : 1][4];
-    const int gpt = (int)(W.ncols >> 2);                            // 4-float groups per token
-    if constexpr (XQ > 0) {
-        // q8_0: groups t, t + blockDim, ..; K-quants (one token): the XQ
-        // consecutive groups XQ t .. (a superblock per 64 / XQ threads)
-#pragma unroll
-        for (int s = 0; s < XQ; s++) {                                   // clamped, unconditional
-            const int gi = QK ? min((int)(threadIdx.x + s * blockDim.x), NB * gpt - 1) : min((int)(XQ * threadIdx.x) + s, gpt - 1);
-            const float4 v = *(const float4 *)(x + 4 * (size_t)gi);
-            xv[s][0] = v.x; xv[s][1] = v.y; xv[s][2] = v.z; xv[s][3] = v.w;
-        }
-    } else if constexpr (QK) {
-        stage_q8_0_load<NB>(stg[0], threadIdx.x, act, act_stride, (int)W.nb);
-    } else {
-#pragma unroll
-        for (int s = 0; s < KS; s++) stage_q8_K_load<NB>(stg[s], threadIdx.x + s * blockDim.x, act, act_stride, (int)W.nb);
-    }
+// one token whose store is `out` (a GELU product, GemvOut): a kernel of its
+// own, so the plain store carries neither the argument nor the branch
+template <class F, int LPR, int UPL, int XQ>
+__global__ __launch_bounds__((gemv_max_threads<F, 1, XQ>())) void k_gemv_out(g4h_tensor W, const uint8_t *__restrict__ act, size_t act_stride,
+                                               const float *__restrict__ x, float *__restrict__ Y, int units, GemvOut out) {
+    constexpr int NB = 1;
+#define G4_GEMV_STORE(v) gemv_out_value(out, row, (v))
+#include "gemv_body.inc"
+#undef G4_GEMV_STORE
+}
 
-    issue_barrier();
-    // branch-free stream: lanes past the row's last unit reload that unit and
-    // leave it out of the sums (a load under a branch would make the compiler
-    // wait for the whole stream before the prologue below)
-    typename F::Frag fr[UPL];
-#pragma unroll
-    for (int k = 0; k < UPL; k++) F::load(fr[k], W, row, min(g + k * LPR, units - 1));
-    issue_order();                                                   // the whole stream goes out before any wait
-    if constexpr (XQ > 0 && QK) {
-#pragma unroll
-        for (int s = 0; s < XQ; s++) {                                   // no branch: keeps the x loads up front
-            const int gi = threadIdx.x + s * blockDim.x;
-            const int t = gi / gpt;
-            q8_lds4(xv[s], gi - t * gpt, gi < NB * gpt, lds, (int)W.nb, t);
-        }
-    } else if constexpr (XQ > 0) {
-        // a superblock per row of 64 / XQ threads (one token: gemv_fused_fits,
-        // whose shapes give every superblock a row); rows past the last one
-        // skip it
-        static_assert(NB == 1, "K-quant weights quantize one fp32 token in-kernel");
-        q8K_rows<XQ>(xv, (int)threadIdx.x / (64 / XQ), (int)(W.ncols >> 8), lds, (int)W.nb);
-    } else if constexpr (QK) {
-        stage_q8_0_store(stg[0], lds, (int)W.nb, stage_dump<ActQ8_0>(lds, NB, (int)W.nb));
-        stage_q8_0_rest<NB>(lds, act, act_stride, (int)W.nb);
-    } else {
-#pragma unroll
-        for (int s = 0; s < KS; s++) stage_q8_K_store(stg[s], lds, (int)W.nb, stage_dump<ActQ8_K>(lds, NB, (int)W.nb));
-        stage_q8_K_rest<NB>(lds, act, act_stride, (int)W.nb, KS);
-    }
-    lds_barrier();
-
-    float acc[NB];
-#pragma unroll
-    for (int t = 0; t < NB; t++) acc[t] = 0.0f;
-#pragma unroll
-    for (int k = 0; k < UPL; k++) {
-        const int u = g + k * LPR;
-        if (u < units) {
-#pragma unroll
-            for (int t = 0; t < NB; t++) acc[t] = F::accum(fr[k], Act(lds, (int)W.nb, t), u, acc[t]);
+template <class F, int NB, int LPR, int UPL, int XQ>
+static void gemv_launch(dim3 grid, dim3 block, size_t lds, hipStream_t s, const g4h_tensor &W, const uint8_t *act, size_t stride,
+                        const float *x, float *Y, int units, const GemvOut &out) {
+    if constexpr (NB == 1) {
+        if (out.mode != OUT_STORE) {
+            hipLaunchKernelGGL((k_gemv_out<F, LPR, UPL, XQ>), grid, block, lds, s, W, act, stride, x, Y, units, out);
+            return;
         }
     }
-    // units beyond LPR*UPL (very long rows): further passes in the same order
-    for (int base = LPR * UPL; base < units; base += LPR * UPL) {
-#pragma unroll
-        for (int k = 0; k < UPL; k++) {
-            const int u = base + g + k * LPR;
-            if (u < units) F::load(fr[k], W, row, u);
-        }
-#pragma unroll
-        for (int k = 0; k < UPL; k++) {
-            const int u = base + g + k * LPR;
-            if (u < units) {
-#pragma unroll
-                for (int t = 0; t < NB; t++) acc[t] = F::accum(fr[k], Act(lds, (int)W.nb, t), u, acc[t]);
-            }
-        }
-    }
-#pragma unroll
-    for (int t = 0; t < NB; t++) acc[t] = group_sum<LPR>(acc[t]);
-    if (g == 0 && row_ok) {
-#pragma unroll
-        for (int t = 0; t < NB; t++) Y[(size_t)t * W.nrows + row] = acc[t];
-    }
+    hipLaunchKernelGGL((k_gemv<F, NB, LPR, UPL, XQ>), grid, block, lds, s, W, act, stride, x, Y, units);
 }
 
 // Waves per workgroup chosen so the grid is (close to) a multiple of the 256
@@ -243,7 +173,8 @@ static inline int gemv_xq_shape(int64_t ncols, int nb, int64_t waves, int wpg, i
 }
 
 template <class F, int NB, int LPR, int UPL>
-static hipError_t go(const g4h_tensor &W, const uint8_t *act, size_t stride, const float *x, float *Y, int units, hipStream_t s) {
+static hipError_t go(const g4h_tensor &W, const uint8_t *act, size_t stride, const float *x, float *Y, int units, hipStream_t s,
+                     const GemvOut &out) {
     constexpr int RPW = 64 / LPR;
     const size_t lds = act_lds_bytes<F>(NB, W.nb);
     const int wpg = gemv_pick_waves(W, NB, RPW, x != nullptr, lds);
@@ -251,7 +182,7 @@ static hipError_t go(const g4h_tensor &W, const uint8_t *act, size_t stride, con
     const unsigned grid = (unsigned)((waves + wpg - 1) / wpg);
     if (!x) {
         if (64 * wpg > gemv_max_threads<F, NB, 0>()) return hipErrorInvalidValue;
-        hipLaunchKernelGGL((k_gemv<F, NB, LPR, UPL, 0>), dim3(grid), dim3(64 * wpg), lds, s, W, act, stride, x, Y, units);
+        gemv_launch<F, NB, LPR, UPL, 0>(dim3(grid), dim3(64 * wpg), lds, s, W, act, stride, x, Y, units, out);
         return hipGetLastError();
     }
     constexpr bool QK = F::type == Q4_0 || F::type == Q8_0;
@@ -261,11 +192,11 @@ static hipError_t go(const g4h_tensor &W, const uint8_t *act, size_t stride, con
         int xwpg;
         const int xq = gemv_xq_shape(W.ncols, NB, waves, wpg, &xwpg);
         if (xq == 2) {
-            hipLaunchKernelGGL((k_gemv<F, NB, LPR, UPL, 2>), dim3(grid), dim3(64 * wpg), lds, s, W, act, stride, x, Y, units);
+            gemv_launch<F, NB, LPR, UPL, 2>(dim3(grid), dim3(64 * wpg), lds, s, W, act, stride, x, Y, units, out);
         } else if constexpr (NB == 1) {
             if (xq != 4) return hipErrorInvalidValue;
             const unsigned grid4 = (unsigned)((waves + xwpg - 1) / xwpg);
-            hipLaunchKernelGGL((k_gemv<F, 1, LPR, UPL, 4>), dim3(grid4), dim3(64 * xwpg), lds, s, W, act, stride, x, Y, units);
+            gemv_launch<F, 1, LPR, UPL, 4>(dim3(grid4), dim3(64 * xwpg), lds, s, W, act, stride, x, Y, units, out);
         } else {
             return hipErrorInvalidValue;
         }
@@ -275,9 +206,9 @@ static hipError_t go(const g4h_tensor &W, const uint8_t *act, size_t stride, con
 
 template <class F, int NB>
 static hipError_t pick(const g4h_tensor &W, const uint8_t *act, size_t stride, const float *x, float *Y, hipStream_t s, int lpr,
-                       int upl) {
+                       int upl, const GemvOut &out) {
     const int units = (int)(W.nb * F::units_per_block);
-#define G4_CASE(L, U) if (lpr == L && upl == U) return go<F, NB, L, U>(W, act, stride, x, Y, units, s)
+#define G4_CASE(L, U) if (lpr == L && upl == U) return go<F, NB, L, U>(W, act, stride, x, Y, units, s, out)
     upl = gemv_upl_final(W.type, W.nb, NB, lpr, upl);
     if constexpr (NB == 1) {
         G4_CASE(16, 1); G4_CASE(16, 2); G4_CASE(16, 3); G4_CASE(16, 4); G4_CASE(16, 5); G4_CASE(16, 6); G4_CASE(16, 7);
@@ -297,12 +228,13 @@ static hipError_t pick(const g4h_tensor &W, const uint8_t *act, size_t stride, c
 // the caller checks gemv_fused_fits)
 template <class F>
 hipError_t gemv_format(const g4h_tensor &W, const uint8_t *act, size_t stride, const float *x, float *Y, int nb, hipStream_t s,
-                       int lpr, int upl) {
+                       int lpr, int upl, const GemvOut &out) {
+    if (out.mode != OUT_STORE && nb != 1) return hipErrorInvalidValue;
     switch (nb) {
-    case 1: return pick<F, 1>(W, act, stride, x, Y, s, lpr, upl);
-    case 2: return pick<F, 2>(W, act, stride, x, Y, s, lpr, upl);
-    case 4: return pick<F, 4>(W, act, stride, x, Y, s, lpr, upl);
-    case 8: return pick<F, 8>(W, act, stride, x, Y, s, lpr, upl);
+    case 1: return pick<F, 1>(W, act, stride, x, Y, s, lpr, upl, out);
+    case 2: return pick<F, 2>(W, act, stride, x, Y, s, lpr, upl, out);
+    case 4: return pick<F, 4>(W, act, stride, x, Y, s, lpr, upl, out);
+    case 8: return pick<F, 8>(W, act, stride, x, Y, s, lpr, upl, out);
     default: return hipErrorInvalidValue;
     }
 }

@@ -30,12 +30,6 @@ namespace g4 {
 constexpr int GP_WAVES = 8;                      // waves per workgroup
 constexpr int GP_MAXS = 8;                       // prologue groups of 4 per thread
 
-__device__ __forceinline__ float gelu_lut(const uint16_t *tab, float x) {
-    if (x <= -10.0f) return 0.0f;
-    if (x >= 10.0f) return x;
-    return h2f(tab[f2h(x)]);
-}
-
 struct ProLoads {
     float v[GP_MAXS][4], d[GP_MAXS][4], wp[GP_MAXS][4], wq[GP_MAXS][4];
 };

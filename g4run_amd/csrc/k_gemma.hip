@@ -135,9 +135,7 @@ __global__ __launch_bounds__(256) void k_gelu_mul(float *g, size_t gs, const flo
     if (i >= n) return;
     g += blockIdx.y * gs;
     u += blockIdx.y * us;
-    const float x = g[i];
-    const float gl = x <= -10.0f ? 0.0f : x >= 10.0f ? x : h2f(tab[f2h(x)]);
-    g[i] = gl * u[i];
+    g[i] = gelu_lut(tab, g[i]) * u[i];
 }
 
 // queries of a layer without its own K/V (model.c:666-672): every head of

@@ -7,14 +7,14 @@
 
 namespace g4 {
 
-hipError_t launch_gemv_q8_0(const g4h_tensor &, const uint8_t *, size_t, const float *, float *, int, hipStream_t, int, int);
-hipError_t launch_gemv_q4_0(const g4h_tensor &, const uint8_t *, size_t, const float *, float *, int, hipStream_t, int, int);
-hipError_t launch_gemv_q4_K(const g4h_tensor &, const uint8_t *, size_t, const float *, float *, int, hipStream_t, int, int);
-hipError_t launch_gemv_q3_K(const g4h_tensor &, const uint8_t *, size_t, const float *, float *, int, hipStream_t, int, int);
-hipError_t launch_gemv_q5_K(const g4h_tensor &, const uint8_t *, size_t, const float *, float *, int, hipStream_t, int, int);
-hipError_t launch_gemv_q6_K(const g4h_tensor &, const uint8_t *, size_t, const float *, float *, int, hipStream_t, int, int);
-hipError_t launch_gemv_q2_K(const g4h_tensor &, const uint8_t *, size_t, const float *, float *, int, hipStream_t, int, int);
-hipError_t launch_gemv_tq2_0(const g4h_tensor &, const uint8_t *, size_t, const float *, float *, int, hipStream_t, int, int);
+hipError_t launch_gemv_q8_0(const g4h_tensor &, const uint8_t *, size_t, const float *, float *, int, hipStream_t, int, int, const GemvOut &);
+hipError_t launch_gemv_q4_0(const g4h_tensor &, const uint8_t *, size_t, const float *, float *, int, hipStream_t, int, int, const GemvOut &);
+hipError_t launch_gemv_q4_K(const g4h_tensor &, const uint8_t *, size_t, const float *, float *, int, hipStream_t, int, int, const GemvOut &);
+hipError_t launch_gemv_q3_K(const g4h_tensor &, const uint8_t *, size_t, const float *, float *, int, hipStream_t, int, int, const GemvOut &);
+hipError_t launch_gemv_q5_K(const g4h_tensor &, const uint8_t *, size_t, const float *, float *, int, hipStream_t, int, int, const GemvOut &);
+hipError_t launch_gemv_q6_K(const g4h_tensor &, const uint8_t *, size_t, const float *, float *, int, hipStream_t, int, int, const GemvOut &);
+hipError_t launch_gemv_q2_K(const g4h_tensor &, const uint8_t *, size_t, const float *, float *, int, hipStream_t, int, int, const GemvOut &);
+hipError_t launch_gemv_tq2_0(const g4h_tensor &, const uint8_t *, size_t, const float *, float *, int, hipStream_t, int, int, const GemvOut &);
 
 // Exact per-block integer sums of every row against token `tok`: one thread
 // per (row, block); the parts of a superblock are added as integers.
@@ -69,24 +69,24 @@ size_t gemv_lds_bytes(int type, int nb_tokens, int64_t nblk) {
 }
 
 static hipError_t gemv_dispatch(const g4h_tensor &W, const uint8_t *act, size_t stride, const float *x, float *Y, int nb,
-                                hipStream_t s) {
+                                hipStream_t s, const GemvOut &out) {
     int lpr, upl;
     gemv_shape(W.type, W.nb, &lpr, &upl);
     switch (W.type) {
-    case Q8_0: return launch_gemv_q8_0(W, act, stride, x, Y, nb, s, lpr, upl);
-    case Q4_0: return launch_gemv_q4_0(W, act, stride, x, Y, nb, s, lpr, upl);
-    case Q4_K: return launch_gemv_q4_K(W, act, stride, x, Y, nb, s, lpr, upl);
-    case Q3_K: return launch_gemv_q3_K(W, act, stride, x, Y, nb, s, lpr, upl);
-    case Q5_K: return launch_gemv_q5_K(W, act, stride, x, Y, nb, s, lpr, upl);
-    case Q6_K: return launch_gemv_q6_K(W, act, stride, x, Y, nb, s, lpr, upl);
-    case Q2_K: return launch_gemv_q2_K(W, act, stride, x, Y, nb, s, lpr, upl);
-    case TQ2_0: return launch_gemv_tq2_0(W, act, stride, x, Y, nb, s, lpr, upl);
+    case Q8_0: return launch_gemv_q8_0(W, act, stride, x, Y, nb, s, lpr, upl, out);
+    case Q4_0: return launch_gemv_q4_0(W, act, stride, x, Y, nb, s, lpr, upl, out);
+    case Q4_K: return launch_gemv_q4_K(W, act, stride, x, Y, nb, s, lpr, upl, out);
+    case Q3_K: return launch_gemv_q3_K(W, act, stride, x, Y, nb, s, lpr, upl, out);
+    case Q5_K: return launch_gemv_q5_K(W, act, stride, x, Y, nb, s, lpr, upl, out);
+    case Q6_K: return launch_gemv_q6_K(W, act, stride, x, Y, nb, s, lpr, upl, out);
+    case Q2_K: return launch_gemv_q2_K(W, act, stride, x, Y, nb, s, lpr, upl, out);
+    case TQ2_0: return launch_gemv_tq2_0(W, act, stride, x, Y, nb, s, lpr, upl, out);
     default: return hipErrorInvalidValue;
     }
 }
 
-hipError_t launch_gemv(const g4h_tensor &W, const uint8_t *act, size_t stride, float *Y, int nb, hipStream_t s) {
-    return gemv_dispatch(W, act, stride, nullptr, Y, nb, s);
+hipError_t launch_gemv(const g4h_tensor &W, const uint8_t *act, size_t stride, float *Y, int nb, hipStream_t s, const GemvOut &out) {
+    return gemv_dispatch(W, act, stride, nullptr, Y, nb, s, out);
 }
 
 // The fused-quantizer variant exists for q8_0 / q4_0 weights when every
@@ -103,9 +103,9 @@ bool gemv_fused_fits(const g4h_tensor &W, int nb) {
     return gemv_xq_shape(W.ncols, nb, waves, wpg, &xwpg) != 0;
 }
 
-hipError_t launch_gemv_x(const g4h_tensor &W, const float *x, float *Y, int nb, hipStream_t s) {
+hipError_t launch_gemv_x(const g4h_tensor &W, const float *x, float *Y, int nb, hipStream_t s, const GemvOut &out) {
     if (!gemv_fused_fits(W, nb) || !x) return hipErrorInvalidValue;
-    return gemv_dispatch(W, nullptr, 0, x, Y, nb, s);
+    return gemv_dispatch(W, nullptr, 0, x, Y, nb, s, out);
 }
 
 hipError_t launch_gemv_p_q8_0(const g4h_tensor &, const uint8_t *, float *, const GemvPro &, const GemvEpi &, hipStream_t, int,

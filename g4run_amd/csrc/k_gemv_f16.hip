@@ -54,10 +54,10 @@ __device__ __forceinline__ void widen8(const uint4 w, float (&f)[8]) {
 // XF: `act` holds the tokens as fp32 rows instead, converted on load with
 // k_act_float's arithmetic (f16 round-to-nearest-even, or bf16 rounding), so
 // the sums are those of converting first -- one launch instead of two.
-template <int WT, int NB, bool XF>
+template <int WT, int NB, bool XF, bool OUT>
 __global__ __launch_bounds__(256) void k_gemv_float(const uint8_t *__restrict__ W, size_t ws, int64_t nrows, int64_t ncols,
                                                     const uint8_t *__restrict__ act, size_t as, float *__restrict__ Y,
-                                                    size_t ys) {
+                                                    size_t ys, GemvOut out) {
     const int lane = threadIdx.x & 63;
     const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     if (row >= nrows) return;                                       // wave-uniform
@@ -95,39 +95,44 @@ __global__ __launch_bounds__(256) void k_gemv_float(const uint8_t *__restrict__ 
 #pragma unroll
     for (int t = 0; t < NB; t++) {
         const float s = group_sum<64>(acc[t]);
-        if (lane == 0) Y[(size_t)t * ys + row] = s;
+        if (lane == 0) Y[(size_t)t * ys + row] = OUT ? gemv_out_value(out, row, s) : s;
     }
 }
 
 template <int WT, bool XF>
 static hipError_t gf_go(const uint8_t *W, size_t ws, int64_t nrows, int64_t ncols, const uint8_t *act, size_t as, float *Y,
-                        size_t ys, int nb, hipStream_t s) {
+                        size_t ys, int nb, hipStream_t s, const GemvOut &out) {
+    if (out.mode != OUT_STORE && nb != 1) return hipErrorInvalidValue;
     const dim3 grid((unsigned)((nrows + 3) / 4));
+    if (out.mode != OUT_STORE) {
+        hipLaunchKernelGGL((k_gemv_float<WT, 1, XF, true>), grid, dim3(256), 0, s, W, ws, nrows, ncols, act, as, Y, ys, out);
+        return hipGetLastError();
+    }
     switch (nb) {
-    case 1: hipLaunchKernelGGL((k_gemv_float<WT, 1, XF>), grid, dim3(256), 0, s, W, ws, nrows, ncols, act, as, Y, ys); break;
-    case 2: hipLaunchKernelGGL((k_gemv_float<WT, 2, XF>), grid, dim3(256), 0, s, W, ws, nrows, ncols, act, as, Y, ys); break;
-    case 4: hipLaunchKernelGGL((k_gemv_float<WT, 4, XF>), grid, dim3(256), 0, s, W, ws, nrows, ncols, act, as, Y, ys); break;
-    case 8: hipLaunchKernelGGL((k_gemv_float<WT, 8, XF>), grid, dim3(256), 0, s, W, ws, nrows, ncols, act, as, Y, ys); break;
+    case 1: hipLaunchKernelGGL((k_gemv_float<WT, 1, XF, false>), grid, dim3(256), 0, s, W, ws, nrows, ncols, act, as, Y, ys, out); break;
+    case 2: hipLaunchKernelGGL((k_gemv_float<WT, 2, XF, false>), grid, dim3(256), 0, s, W, ws, nrows, ncols, act, as, Y, ys, out); break;
+    case 4: hipLaunchKernelGGL((k_gemv_float<WT, 4, XF, false>), grid, dim3(256), 0, s, W, ws, nrows, ncols, act, as, Y, ys, out); break;
+    case 8: hipLaunchKernelGGL((k_gemv_float<WT, 8, XF, false>), grid, dim3(256), 0, s, W, ws, nrows, ncols, act, as, Y, ys, out); break;
     default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
 }
 
 hipError_t launch_gemv_float(int wtype, const uint8_t *W, size_t ws, int64_t nrows, int64_t ncols, const uint8_t *act, size_t as,
-                             float *Y, size_t ys, int nb, hipStream_t s) {
+                             float *Y, size_t ys, int nb, hipStream_t s, const GemvOut &out) {
     if (ncols % 8 || ws % 16 || as % 16 || (uintptr_t)W % 16 || (uintptr_t)act % 16) return hipErrorInvalidValue;
-    return wtype == F16 ? gf_go<F16, false>(W, ws, nrows, ncols, act, as, Y, ys, nb, s)
-         : wtype == BF16 ? gf_go<BF16, false>(W, ws, nrows, ncols, act, as, Y, ys, nb, s)
+    return wtype == F16 ? gf_go<F16, false>(W, ws, nrows, ncols, act, as, Y, ys, nb, s, out)
+         : wtype == BF16 ? gf_go<BF16, false>(W, ws, nrows, ncols, act, as, Y, ys, nb, s, out)
                          : hipErrorInvalidValue;
 }
 
 // the same from fp32 tokens x (row stride xs floats), converted on load
 hipError_t launch_gemv_float_x(int wtype, const uint8_t *W, size_t ws, int64_t nrows, int64_t ncols, const float *x, size_t xs,
-                               float *Y, size_t ys, int nb, hipStream_t s) {
+                               float *Y, size_t ys, int nb, hipStream_t s, const GemvOut &out) {
     if (ncols % 8 || ws % 16 || xs % 4 || (uintptr_t)W % 16 || (uintptr_t)x % 16) return hipErrorInvalidValue;
     const uint8_t *a = (const uint8_t *)x;
-    return wtype == F16 ? gf_go<F16, true>(W, ws, nrows, ncols, a, xs * 4, Y, ys, nb, s)
-         : wtype == BF16 ? gf_go<BF16, true>(W, ws, nrows, ncols, a, xs * 4, Y, ys, nb, s)
+    return wtype == F16 ? gf_go<F16, true>(W, ws, nrows, ncols, a, xs * 4, Y, ys, nb, s, out)
+         : wtype == BF16 ? gf_go<BF16, true>(W, ws, nrows, ncols, a, xs * 4, Y, ys, nb, s, out)
                          : hipErrorInvalidValue;
 }
 

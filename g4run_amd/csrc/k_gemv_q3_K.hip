@@ -3,7 +3,7 @@
 
 namespace g4 {
 hipError_t launch_gemv_q3_K(const g4h_tensor &W, const uint8_t *act, size_t stride, const float *x, float *Y, int nb, hipStream_t s, int lpr,
-                          int upl) {
-    return gemv_format<FQ3_K>(W, act, stride, x, Y, nb, s, lpr, upl);
+                          int upl, const GemvOut &out) {
+    return gemv_format<FQ3_K>(W, act, stride, x, Y, nb, s, lpr, upl, out);
 }
 }  // namespace g4

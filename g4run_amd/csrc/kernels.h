@@ -41,6 +41,25 @@ inline int gemv_upl_final(int type, int64_t nblk, int nb_tokens, int lpr, int up
 size_t gemv_lds_bytes(int type, int nb_tokens, int64_t nblk);
 void gemv_launch_shape(const g4h_tensor &W, int *lpr, int *upl, int *wpg, int64_t *grid, int nb = 1, bool xq = false);
 
+// The store of the one-shot GEMVs for one token: Y[row] = acc (OUT_STORE),
+// or a GELU product folded in with k_gelu_mul's arithmetic, so the bits of the
+// two launches it replaces: gelu(e[row]) * acc (OUT_GELU_E; Y may be e) or
+// gelu(acc) * e[row] (OUT_GELU_ACC), through the fp16 table `gelu`.
+enum { OUT_STORE = 0, OUT_GELU_E = 1, OUT_GELU_ACC = 2 };
+struct GemvOut {
+    int mode = OUT_STORE;
+    const float *e = nullptr;
+    const uint16_t *gelu = nullptr;
+};
+__device__ __forceinline__ float gemv_out_value(const GemvOut &o, int64_t row, float acc) {
+    if (o.mode == OUT_GELU_E) return gelu_lut(o.gelu, o.e[row]) * acc;
+    if (o.mode == OUT_GELU_ACC) return gelu_lut(o.gelu, acc) * o.e[row];
+    return acc;
+}
+
+// g4h_matmul_ex on the GEMV family with the store `out` (api.cpp); fp32 x
+int matmul_out(const g4h_tensor *W, const float *x, float *Y, int nb, void *stream, const GemvOut &out);
+
 // Persistent single-token GEMV (gemv_p.h) over q4_0 / q8_0 rows with a fused
 // activation prologue and an optional GELU epilogue.
 enum { PRO_ACT = 0, PRO_QUANT = 1, PRO_NORM = 2 };
@@ -65,23 +84,25 @@ bool gemv_p_fits(const g4h_tensor &W, const GemvPro &pro, const GemvEpi &epi);
 int gemv_p_grid_size();
 hipError_t launch_gemv_p(const g4h_tensor &W, const uint8_t *act, float *Y, const GemvPro &pro, const GemvEpi &epi,
                          hipStream_t s);
-hipError_t launch_gemv(const g4h_tensor &W, const uint8_t *act, size_t stride, float *Y, int nb, hipStream_t s);
+// out: one token only (nb == 1 unless out.mode == OUT_STORE)
+hipError_t launch_gemv(const g4h_tensor &W, const uint8_t *act, size_t stride, float *Y, int nb, hipStream_t s,
+                       const GemvOut &out = GemvOut());
 // fp32 tokens x [nb][ncols] quantized inside the GEMV when gemv_fused_fits:
 // to q8_0 for q8_0 / q4_0 weights (nb in {1, 2, 4, 8}), to q8_K for one
 // token of K-quant weights; bit-identical to the standalone quantizer
 // followed by launch_gemv
 bool gemv_fused_fits(const g4h_tensor &W, int nb);
-hipError_t launch_gemv_x(const g4h_tensor &W, const float *x, float *Y, int nb, hipStream_t s);
+hipError_t launch_gemv_x(const g4h_tensor &W, const float *x, float *Y, int nb, hipStream_t s, const GemvOut &out = GemvOut());
 // k_gemv_f16.hip: f16 / bf16 weight rows (W at ws bytes per row, 16-byte
 // aligned, ncols % 8 == 0) against nb in {1, 2, 4, 8} prepared activation rows
 // (f16 for F16, bf16-rounded fp32 for BF16) at `as` bytes; Y rows at ys floats
 hipError_t launch_gemv_float(int wtype, const uint8_t *W, size_t ws, int64_t nrows, int64_t ncols, const uint8_t *act, size_t as,
-                             float *Y, size_t ys, int nb, hipStream_t s);
+                             float *Y, size_t ys, int nb, hipStream_t s, const GemvOut &out = GemvOut());
 hipError_t launch_act_float(int wtype, const float *x, size_t xs, int64_t ncols, int nb, uint8_t *out, size_t os, hipStream_t s);
 // the float GEMV straight from fp32 tokens (x 16-byte aligned, row stride xs
 // floats a multiple of 4), with launch_act_float's conversion on load
 hipError_t launch_gemv_float_x(int wtype, const uint8_t *W, size_t ws, int64_t nrows, int64_t ncols, const float *x, size_t xs,
-                               float *Y, size_t ys, int nb, hipStream_t s);
+                               float *Y, size_t ys, int nb, hipStream_t s, const GemvOut &out = GemvOut());
 hipError_t launch_block_sums(const g4h_tensor &W, const uint8_t *act, size_t stride, int tok, int32_t *out, hipStream_t s);
 int block_sums_per_block(int type);
 
