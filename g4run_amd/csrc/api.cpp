@@ -442,7 +442,10 @@ static bool x_fused(const g4h_tensor &W, int nb) {
 // q4_K / q6_K 4096x11008 are already faster on the matrix cores at 8 tokens
 // (23.0 / 31.1 us against 24.8 / 33.7 us).
 
-static bool mfma_capable(const g4h_tensor *W) { return W && (W->type == Q8_0 || W->type == Q4_0 || mmk_capable(W->type)); }
+// f16 / bf16 rows need whole 16-column steps (k_mm_float)
+static bool mfma_capable(const g4h_tensor *W) {
+    return W && (W->type == Q8_0 || W->type == Q4_0 || mmk_capable(W->type) || (is_float(W->type) && W->ncols % 16 == 0));
+}
 
 extern "C" int g4h_matmul_path(const g4h_tensor *W, int nb) {
     return mfma_capable(W) && nb >= kMmMinTokens ? 2 : 1;
@@ -468,8 +471,11 @@ extern "C" int g4h_matmul_describe(const g4h_tensor *W, int nb, int path, char *
     if (!W || !buf || len == 0 || nb <= 0 || path < 0 || path > 2) return fail(G4H_ERR_ARG, "g4h_matmul_describe: bad argument");
     if (path == 0) path = g4h_matmul_path(W, nb);
     if (path == 2) {
-        if (!mfma_capable(W)) return fail(G4H_ERR_TYPE, "g4h_matmul_describe: the matrix-core path takes q8_0 / q4_0 / q4_K / q6_K weights");
+        if (!mfma_capable(W)) return fail(G4H_ERR_TYPE, "g4h_matmul_describe: the matrix-core path takes q8_0 / q4_0 / q4_K / q6_K weights and f16 / bf16 rows of whole 16-column steps");
         if (mmk_capable(W->type)) mmk_describe(*W, nb, buf, len);
+        else if (is_float(W->type))
+            snprintf(buf, len, "k_mm_float<%s> grid=%lldx%d block=512 (matrix cores, 32x32 tiles, 8 waves split the columns)",
+                     type_name(W->type), (long long)((W->nrows + 31) / 32), (nb + 31) / 32);
         else mm_describe(*W, nb, buf, len);
         return G4H_OK;
     }
@@ -573,8 +579,26 @@ static int matmul_impl(const g4h_tensor *W, const float *x, const void *pre, siz
         if (e != hipSuccess) return hip_fail(e, "g4h_matmul: matrix-core launch");
         return G4H_OK;
     }
+    if (path == 2 && is_float(W->type) && mfma_capable(W)) {
+        // f16 / bf16 rows on the matrix cores: fp32 x rounded on load, or the
+        // prepared rows (f16 / bf16-rounded fp32) as they are
+        hipError_t e;
+        if (x) {
+            if ((uintptr_t)x % 16) return fail(G4H_ERR_ARG, "g4h_matmul: x must be 16-byte aligned on the matrix-core path");
+            e = launch_mm_float(W->type, W->qs, (size_t)W->ncols * 2, W->nrows, W->ncols, x, W->ncols, nullptr, 0, nb, Y, s);
+        } else {
+            if (int rc = check_act("g4h_matmul", W, pre, pre_stride, nb)) return rc;
+            const size_t stride = nb == 1 ? g4h_act_stride(W->type, W->ncols) : pre_stride;
+            if ((uintptr_t)pre % 16 || stride % 16)
+                return fail(G4H_ERR_ARG, "g4h_matmul: f16/bf16 activations must be 16-byte aligned with a 16-byte multiple stride");
+            e = launch_mm_float(W->type, W->qs, (size_t)W->ncols * 2, W->nrows, W->ncols, nullptr, 0, (const uint8_t *)pre, stride, nb,
+                                Y, s);
+        }
+        if (e != hipSuccess) return hip_fail(e, "g4h_matmul: matrix-core launch");
+        return G4H_OK;
+    }
     if (path == 2) {
-        if (!mfma_capable(W)) return fail(G4H_ERR_TYPE, "g4h_matmul: the matrix-core path takes q8_0 / q4_0 / q4_K / q6_K weights");
+        if (!mfma_capable(W)) return fail(G4H_ERR_TYPE, "g4h_matmul: the matrix-core path takes q8_0 / q4_0 / q4_K / q6_K weights and f16 / bf16 rows of whole 16-column steps");
         if (x && (uintptr_t)x % 16) return fail(G4H_ERR_ARG, "g4h_matmul: x must be 16-byte aligned on the matrix-core path");
         if (!x)
             if (int rc = check_act("g4h_matmul", W, pre, pre_stride, nb)) return rc;

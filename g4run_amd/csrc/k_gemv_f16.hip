@@ -9,6 +9,8 @@
 // lanes.  The fp32 order differs from the CPU's 8-lane AVX2 order (within the
 // path's fp32 tolerance) but does not depend on the token count, so a batch
 // gives every token the single-token bits.
+#include <type_traits>
+
 #include "common.h"
 #include "kernels.h"
 
@@ -134,6 +136,135 @@ hipError_t launch_gemv_float_x(int wtype, const uint8_t *W, size_t ws, int64_t n
     return wtype == F16 ? gf_go<F16, true>(W, ws, nrows, ncols, a, xs * 4, Y, ys, nb, s, out)
          : wtype == BF16 ? gf_go<BF16, true>(W, ws, nrows, ncols, a, xs * 4, Y, ys, nb, s, out)
                          : hipErrorInvalidValue;
+}
+
+// Prompt batches on the matrix cores (g4h_matmul path 2): Y[t][r] = sum_k
+// W[r][k] a[t][k] for 32-token x 32-row tiles, one v_mfma_f32_32x32x16_f16 /
+// _bf16 per 16 columns.  The operands are the GEMV family's: f16 weights
+// against f16-rounded activations, bf16 weights against bf16-rounded ones
+// (prep_act's AC_F16 / AC_BF16, model.c:163-180), so every product is exact
+// in fp32 (11 x 11 or 8 x 8 significant bits) and only the fp32 order of the
+// sums differs from the CPU's and from the GEMV family's (within the path's
+// tolerance).  The MMF_W waves of a workgroup split the 16-column steps (wave
+// w takes steps w, w + MMF_W, ..., each chained into its accumulator in
+// increasing order) and the waves' tiles are added in wave order through
+// LDS: a token's result does not depend on the batch size.  Operand layout:
+// lane l holds A[l % 32][8 (l / 32) .. + 7] and B[l % 32][8 (l / 32) .. + 7];
+// C[i][j] with j = l % 32 (weight row), i = 8 (r / 4) + 4 (l / 32) + r % 4.
+typedef _Float16 mf_v8h __attribute__((ext_vector_type(8)));
+typedef __bf16 mf_v8bf __attribute__((ext_vector_type(8)));
+typedef float mf_v16f __attribute__((ext_vector_type(16)));
+
+constexpr int MMF_W = 8;              // waves per workgroup
+
+// XF: fp32 token rows (row stride `as` bytes) rounded on load with
+// k_act_float's arithmetic; else prepared rows (f16 for F16, bf16-rounded
+// fp32 for BF16)
+template <int WT, bool XF>
+__global__ __launch_bounds__(64 * MMF_W) void k_mm_float(const uint8_t *__restrict__ W, size_t ws, int64_t nrows, int64_t ncols,
+                                                         const uint8_t *__restrict__ act, size_t as, int M, float *__restrict__ Y) {
+    __shared__ float part[MMF_W - 1][16][64];
+    constexpr bool A32 = XF || WT == BF16;                          // activation rows of fp32
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x) >> 6;
+    const int li = lane & 31, kh = lane >> 5;
+    const int64_t n0 = (int64_t)blockIdx.x * 32;
+    const int m0 = (int)blockIdx.y * 32;
+    const int64_t row = min(n0 + li, nrows - 1);
+    const int tok = min(m0 + li, M - 1);
+    const uint8_t *wr = W + (size_t)row * ws + 16 * kh;
+    const uint8_t *ar = act + (size_t)tok * as + (A32 ? 32 : 16) * kh;
+    const int nk = (int)(ncols >> 4);
+    const int nj = (nk - wave + MMF_W - 1) / MMF_W;                 // this wave's steps (uniform)
+    struct Op {
+        uint4 w, a0, a1;
+    };
+    auto load = [&](int j) __attribute__((always_inline)) -> Op {
+        const size_t sk = (size_t)(wave + MMF_W * j);
+        Op o;
+        o.w = *(const uint4 *)(wr + 32 * sk);
+        o.a0 = *(const uint4 *)(ar + (A32 ? 64 : 32) * sk);
+        if constexpr (A32) o.a1 = *(const uint4 *)(ar + 64 * sk + 16);
+        return o;
+    };
+    mf_v16f acc = {};
+    auto mac = [&](const Op &o) __attribute__((always_inline)) {
+        uint32_t ab[4];
+        if constexpr (A32) {
+            const float v[8] = {__uint_as_float(o.a0.x), __uint_as_float(o.a0.y), __uint_as_float(o.a0.z), __uint_as_float(o.a0.w),
+                                __uint_as_float(o.a1.x), __uint_as_float(o.a1.y), __uint_as_float(o.a1.z), __uint_as_float(o.a1.w)};
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                uint32_t lo, hi;
+                if constexpr (WT == F16) {
+                    lo = f2h(v[2 * k]), hi = f2h(v[2 * k + 1]);
+                } else if constexpr (XF) {
+                    lo = f2bf(v[2 * k]), hi = f2bf(v[2 * k + 1]);
+                } else {                                            // already bf16-rounded: the high halves
+                    lo = __float_as_uint(v[2 * k]) >> 16, hi = __float_as_uint(v[2 * k + 1]) >> 16;
+                }
+                ab[k] = lo | (hi << 16);
+            }
+        } else {
+            ab[0] = o.a0.x, ab[1] = o.a0.y, ab[2] = o.a0.z, ab[3] = o.a0.w;
+        }
+        const uint4 av = make_uint4(ab[0], ab[1], ab[2], ab[3]);
+        if constexpr (WT == F16)
+            acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(mf_v8h, av), __builtin_bit_cast(mf_v8h, o.w), acc, 0, 0, 0);
+        else
+            acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(mf_v8bf, av), __builtin_bit_cast(mf_v8bf, o.w), acc, 0, 0,
+                                                          0);
+    };
+    // straight-line chunks of steps whose loads all go out first
+    auto chunk = [&](auto Cc, int j0) __attribute__((always_inline)) {
+        constexpr int C = decltype(Cc)::value;
+        Op ops[C];
+#pragma unroll
+        for (int k = 0; k < C; k++) ops[k] = load(j0 + k);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int k = 0; k < C; k++) mac(ops[k]);
+    };
+    int j0 = 0;
+    for (; j0 + 4 <= nj; j0 += 4) chunk(std::integral_constant<int, 4>{}, j0);
+    if (nj - j0 >= 2) chunk(std::integral_constant<int, 2>{}, j0), j0 += 2;
+    if (nj - j0 >= 1) chunk(std::integral_constant<int, 1>{}, j0);
+
+    if (wave > 0) {
+#pragma unroll
+        for (int r = 0; r < 16; r++) part[wave - 1][r][lane] = acc[r];
+    }
+    __syncthreads();
+    if (wave > 0) return;
+    const int64_t n = n0 + li;
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+        float o = acc[r];
+#pragma unroll
+        for (int w = 1; w < MMF_W; w++) o += part[w - 1][r][lane];
+        const int m = m0 + 8 * (r >> 2) + 4 * kh + (r & 3);
+        if (m < M && n < nrows) Y[(size_t)m * nrows + n] = o;
+    }
+}
+
+// M tokens of f16 / bf16 weight rows (ws bytes apart, ncols % 16 == 0) on the
+// matrix cores: x fp32 rows (xs floats apart) or prepared activation rows at
+// `as` bytes (exactly one of x, act)
+hipError_t launch_mm_float(int wtype, const uint8_t *W, size_t ws, int64_t nrows, int64_t ncols, const float *x, size_t xs,
+                           const uint8_t *act, size_t as, int M, float *Y, hipStream_t s) {
+    if ((wtype != F16 && wtype != BF16) || ncols % 16 || ws % 16 || (uintptr_t)W % 16 || M < 1 || (x == nullptr) == (act == nullptr))
+        return hipErrorInvalidValue;
+    if (x ? ((uintptr_t)x % 16 || xs % 4) : ((uintptr_t)act % 16 || as % 16)) return hipErrorInvalidValue;
+    const dim3 grid((unsigned)((nrows + 31) / 32), (unsigned)((M + 31) / 32));
+    const uint8_t *a = x ? (const uint8_t *)x : act;
+    const size_t ab = x ? xs * 4 : as;
+    if (wtype == F16) {
+        if (x) hipLaunchKernelGGL((k_mm_float<F16, true>), grid, dim3(64 * MMF_W), 0, s, W, ws, nrows, ncols, a, ab, M, Y);
+        else hipLaunchKernelGGL((k_mm_float<F16, false>), grid, dim3(64 * MMF_W), 0, s, W, ws, nrows, ncols, a, ab, M, Y);
+    } else {
+        if (x) hipLaunchKernelGGL((k_mm_float<BF16, true>), grid, dim3(64 * MMF_W), 0, s, W, ws, nrows, ncols, a, ab, M, Y);
+        else hipLaunchKernelGGL((k_mm_float<BF16, false>), grid, dim3(64 * MMF_W), 0, s, W, ws, nrows, ncols, a, ab, M, Y);
+    }
+    return hipGetLastError();
 }
 
 hipError_t launch_act_float(int wtype, const float *x, size_t xs, int64_t ncols, int nb, uint8_t *out, size_t os, hipStream_t s) {

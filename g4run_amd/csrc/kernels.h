@@ -99,6 +99,11 @@ hipError_t launch_gemv_x(const g4h_tensor &W, const float *x, float *Y, int nb, 
 hipError_t launch_gemv_float(int wtype, const uint8_t *W, size_t ws, int64_t nrows, int64_t ncols, const uint8_t *act, size_t as,
                              float *Y, size_t ys, int nb, hipStream_t s, const GemvOut &out = GemvOut());
 hipError_t launch_act_float(int wtype, const float *x, size_t xs, int64_t ncols, int nb, uint8_t *out, size_t os, hipStream_t s);
+// M tokens of f16 / bf16 weights on the matrix cores (ncols % 16 == 0): x fp32
+// rows (xs floats apart, 16-byte aligned) or prepared activation rows at `as`
+// bytes; a token's row has the same bits in any batch
+hipError_t launch_mm_float(int wtype, const uint8_t *W, size_t ws, int64_t nrows, int64_t ncols, const float *x, size_t xs,
+                           const uint8_t *act, size_t as, int M, float *Y, hipStream_t s);
 // the float GEMV straight from fp32 tokens (x 16-byte aligned, row stride xs
 // floats a multiple of 4), with launch_act_float's conversion on load
 hipError_t launch_gemv_float_x(int wtype, const uint8_t *W, size_t ws, int64_t nrows, int64_t ncols, const float *x, size_t xs,

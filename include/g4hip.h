@@ -140,11 +140,12 @@ int    g4h_tensor_info(const g4h_tensor *t, int *type, int64_t *ncols, int64_t *
 int g4h_matmul(const g4h_tensor *W, const float *x_dev, const void *pre_dev, size_t pre_stride,
                float *Y_dev, int nb, void *stream);
 /* Same with an explicit kernel family: 0 = auto (g4h_matmul_path), 1 = the
- * GEMV family (token chunks of <= 8 staged per workgroup), 2 = int8 matrix-core
- * tiles (q8_0 / q4_0 / q4_K / q6_K weights; every per-block or per-superblock
- * integer sum exact, fp32 scaling in a fixed order, token rows independent of
- * nb).  g4h_matmul_path returns the family auto picks: 2 for those weights
- * from 9 tokens on, else 1. */
+ * GEMV family (token chunks of <= 8 staged per workgroup), 2 = matrix-core
+ * tiles: int8 for q8_0 / q4_0 / q4_K / q6_K weights (every per-block or
+ * per-superblock integer sum exact, fp32 scaling in a fixed order), f16 / bf16
+ * for f16 / bf16 rows of whole 16-column steps (exact products, fp32 sums);
+ * token rows independent of nb.  g4h_matmul_path returns the family auto
+ * picks: 2 for those weights from 9 tokens on, else 1. */
 int g4h_matmul_ex(const g4h_tensor *W, const float *x_dev, const void *pre_dev, size_t pre_stride,
                   float *Y_dev, int nb, int path, void *stream);
 int g4h_matmul_path(const g4h_tensor *W, int nb);
@@ -395,9 +396,10 @@ int g4h_gemma_forward(g4h_gemma *g, const int *tokens, int nb, int pos0, float *
  * nb (1..64) host token ids at positions pos0.. (K/V stored); then, if
  * logits_dev, the last position's logits [n_vocab] (soft-capped).  The
  * projections take g4h_matmul's automatic path, so from 9 tokens the q8_0,
- * q4_0, q4_K and q6_K weights run on the int8 matrix cores, each weight
- * matrix streamed once per batch; rows then differ from g4h_gemma_forward's
- * within the matrix-core path's tolerance.  Synchronous; G4H_ERR_TIMEOUT as
+ * q4_0, q4_K and q6_K weights run on the int8 matrix cores and f16 / bf16
+ * rows on the f16 / bf16 ones, each weight matrix streamed once per batch;
+ * rows then differ from g4h_gemma_forward's within the matrix-core path's
+ * tolerance.  Synchronous; G4H_ERR_TIMEOUT as
  * g4h_gemma_forward. */
 int g4h_gemma_prefill(g4h_gemma *g, const int *tokens, int nb, int pos0, float *logits_dev, void *stream);
 /* The decode step of the gemma4 model driven from device state (g4_forward,

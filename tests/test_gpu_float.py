@@ -97,10 +97,11 @@ def test_float_weight_errors(gpu):
     with pytest.raises(G.G4HError) as e:
         G.Tensor(1, 12, 4)                                          # rows must be a multiple of 8 values
     assert e.value.status == G.ERR_SHAPE
-    t = G.Tensor.from_rows(30, _weights(30, 8, 64, seed=1), 64)
+    t = G.Tensor.from_rows(30, _weights(30, 8, 72, seed=1), 72)     # 72 columns: not whole 16-column steps
+    t64 = G.Tensor.from_rows(30, _weights(30, 8, 64, seed=1), 64)
     try:
         Y = G.Buffer(8 * 4 * 4)
-        x = G.Buffer.from_array(np.ones((4, 64), np.float32))
+        x = G.Buffer.from_array(np.ones((4, 72), np.float32))
         with pytest.raises(G.G4HError) as e:
             G.matmul(t, Y, nb=4, x=x, path=2)
         assert e.value.status == G.ERR_TYPE
@@ -108,5 +109,52 @@ def test_float_weight_errors(gpu):
             G.block_sums(t, x, G.Buffer(64))
         assert e.value.status == G.ERR_TYPE
         assert G.matmul_path(t, 512) == 1
+        assert [G.matmul_path(t64, n) for n in (1, 8, 9, 512)] == [1, 1, 2, 2]
+    finally:
+        t.free()
+        t64.free()
+
+
+@pytest.mark.parametrize("name,wt", FLOAT)
+@pytest.mark.parametrize("rows,cols,M", [(256, 2048, 64), (2048, 256, 64), (4096, 4096, 40), (100, 80, 33), (33, 1040, 9),
+                                         (1, 16, 1)])
+def test_matrix_cores_vs_oracle(gpu, oracle, name, wt, rows, cols, M):
+    """Prompt batches on the matrix cores (path 2, k_mm_float): 32 x 32 tiles
+    of exact f16 x f16 / bf16 x bf16 products summed in fp32, 8 waves splitting
+    the 16-column steps and added in wave order; within the fp32 tolerance of
+    the oracle's dots.  The fp32 x rounded on load gives the bits of prep_act's
+    prepared rows.  Ragged rows and tokens, 5 steps (three waves idle), one
+    step, and step counts that take each chunk size."""
+    from g4run_amd import synth
+    w = _weights(wt, rows, cols, seed=rows * 3 + cols + wt)
+    x = synth.activations(M, cols, seed=cols + M)
+    t = gpu.Tensor.from_rows(wt, w, cols)
+    try:
+        assert gpu.matmul_describe(t, M, 2).startswith("k_mm_float")
+        y = gpu_matmul(gpu, t, x=x, nb=M, path=2)
+        assert_close(y, oracle_matmul(oracle, wt, w, x), f"{name} {rows}x{cols} M={M}")
+        b = gpu_matmul(gpu, t, act=oracle.prep_act(wt, x), nb=M, path=2)
+        assert np.array_equal(bits(y), bits(b)), f"{name} {rows}x{cols} M={M}: x rounded on load != prepared rows"
+    finally:
+        t.free()
+
+
+@pytest.mark.parametrize("name,wt", FLOAT)
+def test_matrix_cores_token_results_independent_of_batch(gpu, oracle, name, wt):
+    """A token's row from k_mm_float has the same bits in any batch (its
+    tile's sums do not depend on the other tokens), and auto path selection
+    takes the matrix cores from 9 tokens."""
+    from g4run_amd import synth
+    w = _weights(wt, 96, 1056, seed=5)
+    x = synth.activations(70, 1056, seed=6)
+    t = gpu.Tensor.from_rows(wt, w, 1056)
+    try:
+        full = gpu_matmul(gpu, t, x=x, nb=70, path=2)
+        assert_close(full, oracle_matmul(oracle, wt, w, x), f"{name} M=70")
+        for m in (1, 9, 31, 32, 33, 64):
+            part = gpu_matmul(gpu, t, x=x[:m].copy(), nb=m, path=2)
+            assert np.array_equal(bits(part), bits(full[:m])), f"{name} M={m}"
+        auto = gpu_matmul(gpu, t, x=x[:9].copy(), nb=9)
+        assert np.array_equal(bits(auto), bits(full[:9]))
     finally:
         t.free()
