@@ -1676,12 +1676,13 @@ static hipError_t attn_batch_go(AttnCtx c, int n_head, int n_kv, int npos0, int 
 // window and no ring, to slot p.  Within a batch of at most ring - window + 1
 // tokens no token's store overwrites a row an earlier token of the batch
 // still attends.
+constexpr int PREP_MAXW = 10;                                        // one wave per row: GQA-8 groups + K + V
 template <int HD>
-__global__ __launch_bounds__(256) void k_attn_prep_rows(QkvArgs a, const float *__restrict__ qkv, int pos0, float *__restrict__ qout,
-                                                        const int *pos_dev) {
+__global__ __launch_bounds__(64 * PREP_MAXW) void k_attn_prep_rows(QkvArgs a, const float *__restrict__ qkv, int pos0,
+                                                                   float *__restrict__ qout, const int *pos_dev) {
     if (pos_dev) pos0 = *pos_dev;
     constexpr int N = HD > 256 ? 8 : 4;                              // elements per lane held
-    __shared__ float wb[4][64 * N];                                  // q8_0 / q4_0 stores
+    __shared__ float wb[PREP_MAXW][64 * N];                          // q8_0 / q4_0 stores
     constexpr int epl = HD >> 6;
     const int b = blockIdx.x, kvh = blockIdx.y, wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int grp = a.n_head / a.n_kv, h0 = kvh * grp, p = pos0 + b;
@@ -1689,7 +1690,7 @@ __global__ __launch_bounds__(256) void k_attn_prep_rows(QkvArgs a, const float *
     const size_t rb = a.kv_type == F16 ? (size_t)HD * 2 : (size_t)(HD / 32) * (a.kv_type == Q4_0 ? 18 : 34);
     float cs[N], sn[N];
     rope_load(cs, sn, a.rope, p, HD);
-    for (int r = wave; r < grp + 2; r += 4) {                        // uniform over the wave
+    for (int r = wave; r < grp + 2; r += (int)(blockDim.x >> 6)) {   // uniform over the wave
         const int src_row = r < grp ? h0 + r : r == grp ? a.n_head + kvh : a.n_head + a.n_kv + kvh;
         const float *w = r < grp ? a.q_norm : r == grp ? a.k_norm : nullptr;
         PrepRowN<N> pr;
@@ -1715,12 +1716,12 @@ hipError_t launch_attn_prep_rows(const float *qkv, const QkvArgs &a, int pos0, i
         return hipErrorInvalidValue;
     if (a.ring && (a.window <= 0 || a.window > a.ring || nb > a.ring - a.window + 1)) return hipErrorInvalidValue;
     if (!a.rope || !a.q_norm || !a.k_norm) return hipErrorInvalidValue;
-    const dim3 grid(nb, a.n_kv);
-    if (a.hd == 64) hipLaunchKernelGGL(k_attn_prep_rows<64>, grid, dim3(256), 0, s, a, qkv, pos0, qout, pos_dev);
-    else if (a.hd == 128) hipLaunchKernelGGL(k_attn_prep_rows<128>, grid, dim3(256), 0, s, a, qkv, pos0, qout, pos_dev);
-    else if (a.hd == 192) hipLaunchKernelGGL(k_attn_prep_rows<192>, grid, dim3(256), 0, s, a, qkv, pos0, qout, pos_dev);
-    else if (a.hd == 256) hipLaunchKernelGGL(k_attn_prep_rows<256>, grid, dim3(256), 0, s, a, qkv, pos0, qout, pos_dev);
-    else hipLaunchKernelGGL(k_attn_prep_rows<512>, grid, dim3(256), 0, s, a, qkv, pos0, qout, pos_dev);
+    const dim3 grid(nb, a.n_kv), block(64 * std::min(a.n_head / a.n_kv + 2, PREP_MAXW));   // a wave per row
+    if (a.hd == 64) hipLaunchKernelGGL(k_attn_prep_rows<64>, grid, block, 0, s, a, qkv, pos0, qout, pos_dev);
+    else if (a.hd == 128) hipLaunchKernelGGL(k_attn_prep_rows<128>, grid, block, 0, s, a, qkv, pos0, qout, pos_dev);
+    else if (a.hd == 192) hipLaunchKernelGGL(k_attn_prep_rows<192>, grid, block, 0, s, a, qkv, pos0, qout, pos_dev);
+    else if (a.hd == 256) hipLaunchKernelGGL(k_attn_prep_rows<256>, grid, block, 0, s, a, qkv, pos0, qout, pos_dev);
+    else hipLaunchKernelGGL(k_attn_prep_rows<512>, grid, block, 0, s, a, qkv, pos0, qout, pos_dev);
     return hipGetLastError();
 }
 
