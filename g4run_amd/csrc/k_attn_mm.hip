@@ -17,10 +17,11 @@
 //            positions: S = fp16(q) . K_j (model.c:530-538, no 1/sqrt(d)) as
 //            one v_mfma_f32_32x32x16_f16 per 16 head elements (exact
 //            products, fp32 sums); per row and chunk the maximum m_c and
-//            l_c = sum exp((double)(s - m_c)) over the row's positions.
+//            l_c = sum expf(s - m_c) over the row's positions, summed in
+//            double.
 //   values   grid (KV head x tile, 256-position span): per row the global
 //            maximum M and normaliser (sum_c l_c exp(m_c - M) in double) as in
-//            the decode kernels, the weights fp16((float)exp(s - M) * inv)
+//            the decode kernels, the weights fp16(expf(s - M) * inv)
 //            (model.c:547-555) into LDS (0 outside a row's positions), then
 //            sum_j w_j V_j on v_mfma_f32_32x32x16_f16 with the positions as
 //            the contraction: lane (c, half) loads V[j][2c], V[j][2c + 1] of
@@ -31,8 +32,11 @@
 // sized for the most positions a call can span and the workgroups past the
 // call's last position return at once.
 // Differences from the per-token kernels are the fp32 orders of the score and
-// value sums and the grouping of the double normaliser: within the
-// attention's tolerance of the CPU, not bit-identical to them.  A non-finite
+// value sums, the grouping of the double normaliser and the exponentials of
+// the scores and weights taken in fp32 (expf, about 1 ulp; the reference
+// rounds exp in double to float: the weights' fp16 rounding can differ by
+// one step where a product lands within ~1e-7 of a rounding boundary):
+// within the attention's tolerance of the CPU, not bit-identical to them.  A non-finite
 // V row (an f16 overflow) reaches the earlier rows of its tile as 0 * inf.
 #include <algorithm>
 #include <cmath>
@@ -167,10 +171,10 @@ __global__ __launch_bounds__(256) void k_amm_scores(AmmArgs c) {
         const int i = 8 * (r >> 2) + 4 * kh + (r & 3);
         // rows 8 (r / 4) .. 8 (r / 4) + 7 hold tokens from (8 (r / 4)) / GRP
         // on: none of them in the batch (a decode step's later rows) skips
-        // the double exp for the whole wave
+        // the exps for the whole wave
         if (tt * T + 8 * (r >> 2) / GRP >= c.nb) continue;           // uniform
         const float mc = fmaxf(fmaxf(wm[0][i], wm[1][i]), fmaxf(wm[2][i], wm[3][i]));
-        const double l = group_sum_t<32>(ok[r] ? exp((double)(acc[r] - mc)) : 0.0);
+        const double l = group_sum_t<32>(ok[r] ? (double)expf(acc[r] - mc) : 0.0);
         if (li == 0) wl[wave][i] = l;
     }
     __syncthreads();
@@ -306,8 +310,8 @@ __global__ __launch_bounds__(256) void k_amm_v(AmmArgs c) {
             int b, h, j0, p;
             amm_rowinfo<GRP>(c, kvh, tt, i0 + i, b, h, j0, p);
             // a row outside the batch (uniform: a decode step's rows past
-            // its GRP heads) takes weight 0 without the double exp
-            wsh[i0 + i][t] = b < c.nb ? f2h(ok[i] ? (float)exp((double)(sv[i] - mx[i0 + i])) * iv[i0 + i] : 0.0f) : (uint16_t)0;
+            // its GRP heads) takes weight 0 without the exp
+            wsh[i0 + i][t] = b < c.nb ? f2h(ok[i] ? expf(sv[i] - mx[i0 + i]) * iv[i0 + i] : 0.0f) : (uint16_t)0;
         }
     }
     __syncthreads();
