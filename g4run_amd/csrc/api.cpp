@@ -697,6 +697,16 @@ namespace g4 {
 int matmul_out(const g4h_tensor *W, const float *x, float *Y, int nb, void *stream, const GemvOut &out) {
     return matmul_impl(W, x, nullptr, 0, Y, nb, 1, stream, ScratchSrc(), out);
 }
+bool matmul_few_ready(const g4h_tensor *W, int nb, int path) {
+    if (!W || nb < 1 || path == 1 || (path == 0 && g4h_matmul_path(W, nb) != 2)) return false;
+    return mm_few_ready(*W, nb);
+}
+int matmul_few(const g4h_tensor *W, const FewAct &a, float *Y, int nb, void *stream) {
+    if (!W || !Y) return fail(G4H_ERR_ARG, "g4h_matmul: null tensor or output");
+    const hipError_t e = launch_mm_few_ready(*W, a, nb, Y, (hipStream_t)stream);
+    if (e != hipSuccess) return hip_fail(e, "g4h_matmul: matrix-core launch");
+    return G4H_OK;
+}
 }  // namespace g4
 
 extern "C" int g4h_read_floor(const void *src, size_t bytes, float *y, int64_t ny, int threads, int loads, void *s) {

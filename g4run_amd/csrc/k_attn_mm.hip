@@ -59,6 +59,7 @@ struct AmmArgs {
     float *out;                      // [nb][n_head][hd]
     uint8_t *q8out;                  // optional q8_0 rows of out, q8_stride bytes per token
     size_t q8_stride;
+    FewAct few;                      // or (few.qa set) out as q8_0 in k_mm_few's layout
     const uint8_t *kc, *vc;
     int n_head, n_kv, window, ring;
     int p0, nb;                      // token 0's position (or *pos_dev) and the token count
@@ -359,7 +360,7 @@ __global__ __launch_bounds__(256) void k_amm_v(AmmArgs c) {
 }
 
 // grid (n_head, nb), 256 threads (elements e and e + 256): the spans'
-// partials in order; with q8out, the head row as q8_0 blocks too
+// partials in order; with q8out (or few), the head row as q8_0 blocks too
 // (quants.c:74-109)
 template <int HD>
 __global__ __launch_bounds__(256) void k_amm_combine(AmmArgs c) {
@@ -388,13 +389,16 @@ __global__ __launch_bounds__(256) void k_amm_combine(AmmArgs c) {
             row[e] = r;
         }
     }
-    if (c.q8out) {
+    if (c.q8out || c.few.qa) {
         __syncthreads();
         const bool own = t < HD / 4;
         float v[4] = {0.f, 0.f, 0.f, 0.f};
         if (own)
             for (int k = 0; k < 4; k++) v[k] = row[4 * t + k];
-        if (t < (HD / 4 + 63) / 64 * 64) q8_store4(v, t, own, c.q8out + (size_t)b * c.q8_stride + (size_t)h * (HD / 32) * 34);
+        if (t < (HD / 4 + 63) / 64 * 64) {
+            if (c.few.qa) q8_store4_few(v, h * (HD / 4) + t, own, c.few, b);
+            else q8_store4(v, t, own, c.q8out + (size_t)b * c.q8_stride + (size_t)h * (HD / 32) * 34);
+        }
     }
 }
 
@@ -414,8 +418,10 @@ static void amm_go(const AmmArgs &c, hipStream_t s) {
 }
 
 hipError_t launch_attn_batch_mm(const float *q, const QkvArgs &a, int npos0, int nb, float *out, uint8_t *q8out, uint8_t *ws,
-                                size_t ws_bytes, hipStream_t s, size_t q8_stride, const int *pos_dev, int npos_max) {
-    if (!attn_batch_mm_ok(a) || !q || !out || !ws || nb < 1 || nb > 65535 || (!pos_dev && npos0 < 1) || (pos_dev && npos_max < 1))
+                                size_t ws_bytes, hipStream_t s, size_t q8_stride, const int *pos_dev, int npos_max,
+                                const FewAct &few) {
+    if (!attn_batch_mm_ok(a) || !q || !out || !ws || nb < 1 || nb > 65535 || (!pos_dev && npos0 < 1) || (pos_dev && npos_max < 1) ||
+        (few.qa && nb > 16 * few.mt))
         return hipErrorInvalidValue;
     if (a.ring && (a.window <= 0 || a.window > a.ring || nb > a.ring - a.window + 1)) return hipErrorInvalidValue;
     AmmArgs c{};
@@ -423,6 +429,7 @@ hipError_t launch_attn_batch_mm(const float *q, const QkvArgs &a, int npos0, int
     c.out = out;
     c.q8out = q8out;
     c.q8_stride = q8_stride ? q8_stride : (size_t)a.n_head * (a.hd / 32) * 34;
+    c.few = few;
     c.kc = a.kc;
     c.vc = a.vc;
     c.n_head = a.n_head;

@@ -575,13 +575,6 @@ __global__ __launch_bounds__(256) void k_mm_few(g4h_tensor W, const int8_t *__re
     }
 }
 
-// byte offset of codes e .. (block b, token m) in the few-token layout, and
-// the fp16 index of its scale
-__device__ __forceinline__ size_t few_q(int64_t b, int m, int mt, int e) {
-    return ((((size_t)(b >> 1) * mt + (m >> 4)) * 16 + (m & 15)) * 64) + 16 * (e >> 3) + 8 * (b & 1) + (e & 7);
-}
-__device__ __forceinline__ size_t few_d(int64_t b, int m) { return ((((size_t)(b >> 1) * 16 + (m & 15)) * 2 + (b & 1)) * 4) + (m >> 4); }
-
 // x fp32 [M][ncols] (row stride xs floats) -> q8_0 codes and fp16 scales with
 // the quantizer arithmetic of quants.c:74-109 (8 lanes per block), laid out
 // token-major (qa [M][nb][32], da [M][nb]) or, FEW, in k_mm_few's layout of
@@ -709,6 +702,44 @@ void mm_describe(const g4h_tensor &W, int M, char *buf, size_t len) {
     }
 }
 
+bool mm_few_ready(const g4h_tensor &W, int M) { return (W.type == Q8_0 || W.type == Q4_0) && W.nb % 2 == 0 && mm_few(W, M); }
+
+size_t few_act_bytes(int64_t ncols, int M, size_t *da_off) {
+    const size_t np = (size_t)(ncols / 32 + 1) / 2, mt = (M + 15) / 16;
+    *da_off = (np * mt * 1024 + 255) & ~(size_t)255;
+    return mm_few_bytes(M, ncols);
+}
+
+__global__ __launch_bounds__(256) void k_clear(uint4 *p, size_t n) {
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i < n) p[i] = make_uint4(0, 0, 0, 0);
+}
+hipError_t launch_few_clear(uint8_t *buf, size_t bytes, hipStream_t s) {
+    if ((uintptr_t)buf % 16 || bytes % 16) return hipErrorInvalidValue;
+    const size_t n = bytes / 16;
+    if (n) hipLaunchKernelGGL(k_clear, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, (uint4 *)buf, n);
+    return hipGetLastError();
+}
+
+static hipError_t few_go(const g4h_tensor &W, const int8_t *qa, const uint16_t *da, int M, float *Y, hipStream_t s) {
+    const int mt = (M + 15) / 16;
+    const dim3 grid((unsigned)((W.nrows + 15) / 16));
+#define G4_MF(T)                                                                                                    \
+    if (mt == T) {                                                                                                  \
+        if (W.type == Q8_0) hipLaunchKernelGGL((k_mm_few<Q8_0, T>), grid, dim3(256), 0, s, W, qa, da, M, Y);       \
+        else hipLaunchKernelGGL((k_mm_few<Q4_0, T>), grid, dim3(256), 0, s, W, qa, da, M, Y);                    \
+        return hipGetLastError();                                                                                   \
+    }
+    G4_MF(1) G4_MF(2) G4_MF(3) G4_MF(4)
+#undef G4_MF
+    return hipErrorInvalidValue;
+}
+
+hipError_t launch_mm_few_ready(const g4h_tensor &W, const FewAct &a, int M, float *Y, hipStream_t s) {
+    if (M <= 0 || !mm_few_ready(W, M) || !a.qa || !a.da || a.mt != (M + 15) / 16) return hipErrorInvalidValue;
+    return few_go(W, a.qa, a.da, M, Y, s);
+}
+
 template <int WT, int WM, int WN, int KB>
 static hipError_t mm_go(const g4h_tensor &W, const int8_t *qa, const uint16_t *da, int M, float *Y, hipStream_t s) {
     const dim3 grid((unsigned)((W.nrows + 32 * WN - 1) / (32 * WN)), (unsigned)((M + 32 * WM - 1) / (32 * WM)));
@@ -736,16 +767,7 @@ hipError_t launch_matmul_mfma(const g4h_tensor &W, const float *x, size_t x_stri
             hipLaunchKernelGGL(k_act_planar<true>, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, act, stride, nb, M, mt, qa, da);
         }
         if (hipError_t e = hipGetLastError()) return e;
-        const dim3 grid((unsigned)((W.nrows + 15) / 16));
-#define G4_MF(T)                                                                                                    \
-    if (mt == T) {                                                                                                  \
-        if (W.type == Q8_0) hipLaunchKernelGGL((k_mm_few<Q8_0, T>), grid, dim3(256), 0, s, W, qa, da, M, Y);       \
-        else hipLaunchKernelGGL((k_mm_few<Q4_0, T>), grid, dim3(256), 0, s, W, qa, da, M, Y);                    \
-        return hipGetLastError();                                                                                   \
-    }
-        G4_MF(1) G4_MF(2) G4_MF(3) G4_MF(4)
-#undef G4_MF
-        return hipErrorInvalidValue;
+        return few_go(W, qa, da, M, Y, s);
     }
     uint16_t *da = (uint16_t *)(ws + (((size_t)M * nb * 32 + 255) & ~(size_t)255));
     if (x) {

@@ -35,7 +35,7 @@ __global__ __launch_bounds__(256) void k_rand_normal(float *y, int64_t n, uint64
 // n <= 8192; workgroup b takes token[b] into x + b*n and act + b*ast.
 __global__ __launch_bounds__(512) void k_embed_norm(const int8_t *lo, const int8_t *hi, const uint16_t *sc, int64_t nb, const int *token,
                                                     float *x, int n, float es, const float *w_pre, float eps, uint8_t *act,
-                                                    size_t ast) {
+                                                    size_t ast, FewAct few) {
     const int b = blockIdx.x;
     const int64_t r = token[b];
     x += (size_t)b * n;
@@ -46,7 +46,7 @@ __global__ __launch_bounds__(512) void k_embed_norm(const int8_t *lo, const int8
         x[i] = v * es;
     }
     __syncthreads();
-    if (w_pre) wg_norm_quant<4>(x, nullptr, nullptr, w_pre, eps, n, act + (size_t)b * ast);
+    if (w_pre) wg_norm_quant<4>(x, nullptr, nullptr, w_pre, eps, n, act + (size_t)b * ast, nullptr, few, b);
 }
 
 // ------------------------------------------------------ norm + quantize --
@@ -57,18 +57,19 @@ __global__ __launch_bounds__(512) void k_embed_norm(const int8_t *lo, const int8
 // (the head's input feature, model.c:791-793).  Rows at n floats; act rows at
 // ast bytes.
 __global__ __launch_bounds__(512) void k_norm_quant(float *x, const float *delta, const float *w_post, const float *w_pre,
-                                                    float eps, int n, uint8_t *act, size_t ast, float *y) {
+                                                    float eps, int n, uint8_t *act, size_t ast, float *y, FewAct few) {
     const size_t b = blockIdx.x;
-    wg_norm_quant<4>(x + b * n, delta ? delta + b * n : nullptr, w_post, w_pre, eps, n, act + b * ast, y ? y + b * n : nullptr);
+    wg_norm_quant<4>(x + b * n, delta ? delta + b * n : nullptr, w_post, w_pre, eps, n, act + b * ast, y ? y + b * n : nullptr,
+                     few, (int)b);
 }
 
 // -------------------------------------------------------- gelu * up --
 // h = gelu(g) * u with the fp16 GELU table (model.c:725-729), quantized to
 // q8_0 for the down projection; gu holds the (gate, up) pairs interleaved,
 // as the Wgu rows are stored.  256 threads, 4 elements each; grid.y token
-// rows (gu rows of 2 n_ff floats, act rows at ast bytes).
+// rows (gu rows of 2 n_ff floats, act rows at ast bytes, or few's layout).
 __global__ __launch_bounds__(256) void k_gelu_quant(const float *gu, int n_ff, const uint16_t *tab, uint8_t *act, size_t ast,
-                                                    float *hout, size_t hs) {
+                                                    float *hout, size_t hs, FewAct few) {
     const int gi = blockIdx.x * 256 + threadIdx.x;
     gu += (size_t)blockIdx.y * 2 * n_ff;             // token row blockIdx.y
     act += (size_t)blockIdx.y * ast;
@@ -90,7 +91,7 @@ __global__ __launch_bounds__(256) void k_gelu_quant(const float *gu, int n_ff, c
         h[k] = gg * u[k];
     }
     if (hout && own) *(float4 *)(hout + (size_t)blockIdx.y * hs + 4 * gi) = make_float4(h[0], h[1], h[2], h[3]);
-    q8_store4(h, gi, own, act);
+    act_store4(h, gi, own, act, few, blockIdx.y);
 }
 
 // ---------------------------------------------------- argmax + advance --
@@ -118,23 +119,25 @@ hipError_t launch_rand_normal(float *y, int64_t n, uint64_t seed, float mean, fl
     return hipGetLastError();
 }
 hipError_t launch_embed_norm(const g4h_tensor &head, const int *token, float *x, float es, const float *w_pre, float eps,
-                             uint8_t *act, hipStream_t s, int nb, size_t ast) {
-    if (head.type != Q8_0 || head.ncols % 32 || head.ncols > 8192 || nb < 1) return hipErrorInvalidValue;
+                             uint8_t *act, hipStream_t s, int nb, size_t ast, const FewAct &few) {
+    if (head.type != Q8_0 || head.ncols % 32 || head.ncols > 8192 || nb < 1 || (few.qa && nb > 16 * few.mt))
+        return hipErrorInvalidValue;
     hipLaunchKernelGGL(k_embed_norm, dim3(nb), dim3(512), 0, s, (const int8_t *)head.qs, (const int8_t *)head.ex,
                        (const uint16_t *)head.sc, head.nb,
-                       token, x, (int)head.ncols, es, w_pre, eps, act, ast);
+                       token, x, (int)head.ncols, es, w_pre, eps, act, ast, few);
     return hipGetLastError();
 }
 hipError_t launch_norm_quant(float *x, const float *delta, const float *w_post, const float *w_pre, float eps, int n,
-                             uint8_t *act, hipStream_t s, int nb, size_t ast, float *y) {
-    if (n % 32 || n > 8192 || nb < 1) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_norm_quant, dim3(nb), dim3(512), 0, s, x, delta, w_post, w_pre, eps, n, act, ast, y);
+                             uint8_t *act, hipStream_t s, int nb, size_t ast, float *y, const FewAct &few) {
+    if (n % 32 || n > 8192 || nb < 1 || (few.qa && nb > 16 * few.mt)) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_norm_quant, dim3(nb), dim3(512), 0, s, x, delta, w_post, w_pre, eps, n, act, ast, y, few);
     return hipGetLastError();
 }
 hipError_t launch_gelu_quant(const float *gu, int n_ff, const uint16_t *tab, uint8_t *act, hipStream_t s, int nb, size_t ast,
-                             float *hout, size_t hs) {
-    if (n_ff % 32 || nb < 1 || (hout && ((uintptr_t)hout % 16 || hs % 4))) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(k_gelu_quant, dim3((n_ff / 4 + 255) / 256, nb), dim3(256), 0, s, gu, n_ff, tab, act, ast, hout, hs);
+                             float *hout, size_t hs, const FewAct &few) {
+    if (n_ff % 32 || nb < 1 || (hout && ((uintptr_t)hout % 16 || hs % 4)) || (few.qa && nb > 16 * few.mt))
+        return hipErrorInvalidValue;
+    hipLaunchKernelGGL(k_gelu_quant, dim3((n_ff / 4 + 255) / 256, nb), dim3(256), 0, s, gu, n_ff, tab, act, ast, hout, hs, few);
     return hipGetLastError();
 }
 hipError_t launch_argmax_rows(const float *logits, int n, int nb, int *out, hipStream_t s) {

@@ -57,8 +57,23 @@ __device__ __forceinline__ float gemv_out_value(const GemvOut &o, int64_t row, f
     return acc;
 }
 
+// A producer's q8_0 activation written straight into k_mm_few's operand
+// layout (k_mfma.hip) for mt 16-token tiles instead of GGUF rows (qa ==
+// nullptr: rows).  Codes and scales of the padding tokens are never written:
+// the buffers hold zeros there (launch_few_clear).
+struct FewAct {
+    int8_t *qa = nullptr;
+    uint16_t *da = nullptr;
+    int mt = 0;
+};
+
 // g4h_matmul_ex on the GEMV family with the store `out` (api.cpp); fp32 x
 int matmul_out(const g4h_tensor *W, const float *x, float *Y, int nb, void *stream, const GemvOut &out);
+// whether g4h_matmul_ex(W, nb tokens of GGUF rows, path) runs k_mm_few on
+// whole block pairs, so that its producer may write the FewAct layout, and
+// that matmul on activations already in it
+bool matmul_few_ready(const g4h_tensor *W, int nb, int path);
+int matmul_few(const g4h_tensor *W, const FewAct &a, float *Y, int nb, void *stream);
 
 // Persistent single-token GEMV (gemv_p.h) over q4_0 / q8_0 rows with a fused
 // activation prologue and an optional GELU epilogue.
@@ -127,13 +142,16 @@ struct QkvArgs {
 hipError_t launch_rand_normal(float *y, int64_t n, uint64_t seed, float mean, float std, hipStream_t s);
 // The row forms (nb tokens): x / delta / y rows of n floats, gu rows of 2 n_ff
 // floats, act rows at ast bytes; token[b] feeds row b.
+// With few.qa set the activations go to that layout (token b as token b of
+// the tiles) and act is not written.
 hipError_t launch_embed_norm(const g4h_tensor &head, const int *token, float *x, float es, const float *w_pre, float eps,
-                             uint8_t *act, hipStream_t s, int nb = 1, size_t ast = 0);
+                             uint8_t *act, hipStream_t s, int nb = 1, size_t ast = 0, const FewAct &few = FewAct());
 hipError_t launch_norm_quant(float *x, const float *delta, const float *w_post, const float *w_pre, float eps, int n,
-                             uint8_t *act, hipStream_t s, int nb = 1, size_t ast = 0, float *y = nullptr);
+                             uint8_t *act, hipStream_t s, int nb = 1, size_t ast = 0, float *y = nullptr,
+                             const FewAct &few = FewAct());
 // hout (optional): the h rows themselves, hs floats apart (16-byte aligned)
 hipError_t launch_gelu_quant(const float *gu, int n_ff, const uint16_t *tab, uint8_t *act, hipStream_t s, int nb = 1,
-                             size_t ast = 0, float *hout = nullptr, size_t hs = 0);
+                             size_t ast = 0, float *hout = nullptr, size_t hs = 0, const FewAct &few = FewAct());
 // out[b] = first index of the maximum of row b of logits [nb][n] (16-byte
 // aligned rows)
 hipError_t launch_argmax_rows(const float *logits, int n, int nb, int *out, hipStream_t s);
@@ -199,6 +217,15 @@ size_t mm_planar_bytes(int M, int64_t ncols);
 void mm_describe(const g4h_tensor &W, int M, char *buf, size_t len);
 hipError_t launch_matmul_mfma(const g4h_tensor &W, const float *x, size_t x_stride, const uint8_t *act, size_t stride, int M,
                               float *Y, uint8_t *ws, hipStream_t s);
+// k_mm_few on activations a producer wrote in its layout (FewAct, mt = (M +
+// 15) / 16): mm_few_ready says whether launch_matmul_mfma would take k_mm_few
+// for W at M tokens and W has whole block pairs (no padding block);
+// few_act_bytes sizes the buffers for rows of up to ncols columns (the scales
+// at *da_off); launch_few_clear zeroes them for a new token count.
+bool mm_few_ready(const g4h_tensor &W, int M);
+size_t few_act_bytes(int64_t ncols, int M, size_t *da_off);
+hipError_t launch_few_clear(uint8_t *buf, size_t bytes, hipStream_t s);
+hipError_t launch_mm_few_ready(const g4h_tensor &W, const FewAct &a, int M, float *Y, hipStream_t s);
 
 // k_mfma_k.hip: many-token matmul on the int8 matrix cores for q4_K / q6_K
 // weights against GGUF q8_K activation rows at `stride` bytes
@@ -252,7 +279,7 @@ constexpr int kMmMinTokens = 9;
 size_t attn_batch_mm_workspace_bytes(int n_head, int hd, int npos_max, int nb);
 hipError_t launch_attn_batch_mm(const float *q, const QkvArgs &a, int npos0, int nb, float *out, uint8_t *q8out, uint8_t *ws,
                                 size_t ws_bytes, hipStream_t s, size_t q8_stride = 0, const int *pos_dev = nullptr,
-                                int npos_max = 0);
+                                int npos_max = 0, const FewAct &few = FewAct());
 // the query / key / value rows of nb tokens from the fused projection output
 // (rows of (n_head + 2 n_kv) hd floats) prepared as the decode kernels do:
 // queries into qout [nb][n_head][hd], key and value rows into the caches at

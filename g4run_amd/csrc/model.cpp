@@ -63,6 +63,11 @@ struct g4h_model {
     float *bx = nullptr, *bxb = nullptr, *bqkv = nullptr, *batt = nullptr, *bff = nullptr, *bhn = nullptr, *bq = nullptr;
     uint8_t *bact = nullptr, *bws = nullptr, *bbw = nullptr;
     int *btok = nullptr;
+    // a prompt batch's activations in k_mm_few's layout (FewAct) for rows of
+    // up to few_cols columns; zeroed for few_nb tokens
+    uint8_t *bfew = nullptr;
+    int64_t few_cols = 0;
+    int few_nb = 0;
 };
 
 static constexpr int kBatchMax = 64;   // G4_BATCH_MAX, g4run.h:23
@@ -445,6 +450,13 @@ static bool batch_attn() {
     return on;
 }
 
+// G4H_FEW_DIRECT=0 keeps the prompt batch's activations in GGUF rows, re-laid
+// per projection (measurement, and the check that both give the same bits)
+static bool few_direct() {
+    const char *e = getenv("G4H_FEW_DIRECT");
+    return !e || atoi(e) != 0;
+}
+
 static int batch_alloc(g4h_model *m) {
     if (m->bx) return G4H_OK;
     const g4h_model_config &c = m->c;
@@ -461,6 +473,9 @@ static int batch_alloc(g4h_model *m) {
     M_RC(model_alloc(m, (void **)&m->bq, B * Q * 4));
     M_RC(model_alloc(m, (void **)&m->bbw, attn_batch_workspace_bytes(c.n_head, c.head_dim, c.n_ctx, kBatchMax)));
     M_RC(model_alloc(m, (void **)&m->btok, B * sizeof(int)));
+    size_t da_off;
+    m->few_cols = std::max(E, std::max(Q, F));
+    M_RC(model_alloc(m, (void **)&m->bfew, few_act_bytes(m->few_cols, kBatchMax, &da_off)));
     M_HIP(hipMemset(m->bws, 0, m->ws_bytes));
     return G4H_OK;
 }
@@ -504,14 +519,40 @@ static int forward_rows(g4h_model *m, const int *tokens, int nb, int pos0, hipSt
                                hipMemcpyDeviceToDevice, s));
         return G4H_OK;
     };
+    // A prompt batch whose projections run k_mm_few: each activation's
+    // producer writes that kernel's operand layout itself, sparing the
+    // re-layout launch per projection (same codes and scales, so the same
+    // bits).  One buffer serves every activation: a block pair's place does
+    // not depend on the row length, and the padding tokens stay zero.
+    FewAct fa;
+    if (path != 1 && nb >= kMmMinTokens && few_direct()) {
+        size_t da_off;
+        const size_t bytes = few_act_bytes(m->few_cols, nb, &da_off);
+        fa.qa = (int8_t *)m->bfew;
+        fa.da = (uint16_t *)(m->bfew + da_off);
+        fa.mt = (nb + 15) / 16;
+        if (m->few_nb != nb) {
+            M_HIP(launch_few_clear(m->bfew, bytes, s));
+            m->few_nb = nb;
+        }
+    }
+    auto dst = [&](const g4h_tensor *W) { return fa.qa && matmul_few_ready(W, nb, path) ? fa : FewAct(); };
+    auto proj = [&](const g4h_tensor *W, const FewAct &f, float *Y) -> int {
+        if (f.qa) return matmul_few(W, f, Y, nb, s);
+        return g4h_matmul_ex(W, nullptr, m->bact, ast, Y, nb, path, s);
+    };
     M_HIP(hipMemcpyAsync(m->btok, tokens, (size_t)nb * sizeof(int), hipMemcpyHostToDevice, s));
-    M_HIP(launch_embed_norm(*m->head, m->btok, m->bx, sqrtf((float)E), norm_of(m, 0, G4H_N_ATTN), c.rms_eps, m->bact, s, nb, ast));
+    FewAct f = dst(m->wqkv[0]);
+    M_HIP(launch_embed_norm(*m->head, m->btok, m->bx, sqrtf((float)E), norm_of(m, 0, G4H_N_ATTN), c.rms_eps, m->bact, s, nb, ast,
+                            f));
     for (int l = 0; l < c.n_layer; l++) {
-        if (l)
+        if (l) {
+            f = dst(m->wqkv[l]);
             M_HIP(launch_norm_quant(m->bx, m->bxb, norm_of(m, l - 1, G4H_N_POST_FFW), norm_of(m, l, G4H_N_ATTN), c.rms_eps, E,
-                                    m->bact, s, nb, ast));
+                                    m->bact, s, nb, ast, nullptr, f));
+        }
         M_RC(trace_rows(l, 0, m->bx, E, E));
-        M_RC(g4h_matmul_ex(m->wqkv[l], nullptr, m->bact, ast, m->bqkv, nb, path, s));
+        M_RC(proj(m->wqkv[l], f, m->bqkv));
         M_RC(trace_rows(l, TR_QKV, m->bqkv, R, R));
         QkvArgs qa;
         qa.n_head = H;
@@ -524,30 +565,36 @@ static int forward_rows(g4h_model *m, const int *tokens, int nb, int pos0, hipSt
         qa.kc = m->kv + (size_t)(2 * l) * m->kv_layer_bytes;
         qa.vc = qa.kc + m->kv_layer_bytes;
         qa.eps = c.rms_eps;
+        f = FewAct();
         if (nb > 1 && batch_attn()) {
             // every token's rows prepared and its key / value stored first, then
             // the batch attends in one set of launches
             M_HIP(launch_attn_prep_rows(m->bqkv, qa, pos0, nb, m->bq, s));
-            if (path != 1 && nb >= kMmMinTokens && attn_batch_mm_ok(qa))    // a prompt batch: the matrix cores
+            if (path != 1 && nb >= kMmMinTokens && attn_batch_mm_ok(qa)) {  // a prompt batch: the matrix cores
+                f = dst(m->wo[l]);
                 M_HIP(launch_attn_batch_mm(m->bq, qa, pos0 + 1, nb, m->batt, m->bact, m->bbw,
-                                           attn_batch_workspace_bytes(c.n_head, c.head_dim, c.n_ctx, kBatchMax), s, ast));
-            else
+                                           attn_batch_workspace_bytes(c.n_head, c.head_dim, c.n_ctx, kBatchMax), s, ast,
+                                           nullptr, 0, f));
+            } else {
                 M_HIP(launch_attn_batch(m->bq, qa, pos0 + 1, nb, m->batt, m->bact, m->bbw, s, ast));
+            }
         } else {
             for (int b = 0; b < nb; b++)
                 M_HIP(launch_attn_decode(nullptr, m->bqkv + (size_t)b * R, qa, pos0 + b + 1, nullptr, c.n_ctx,
                                          m->batt + (size_t)b * Q, m->bact + (size_t)b * ast, m->bws, s));
         }
         M_RC(trace_rows(l, TR_ATT, m->batt, Q, Q));
-        M_RC(g4h_matmul_ex(m->wo[l], nullptr, m->bact, ast, m->bxb, nb, path, s));
+        M_RC(proj(m->wo[l], f, m->bxb));
         M_RC(trace_rows(l, TR_WO, m->bxb, E, E));
+        f = dst(m->wgu[l]);
         M_HIP(launch_norm_quant(m->bx, m->bxb, norm_of(m, l, G4H_N_POST_ATTN), norm_of(m, l, G4H_N_FFN), c.rms_eps, E, m->bact,
-                                s, nb, ast));
+                                s, nb, ast, nullptr, f));
         M_RC(trace_rows(l, TR_XMID, m->bx, E, E));
-        M_RC(g4h_matmul_ex(m->wgu[l], nullptr, m->bact, ast, m->bff, nb, path, s));
+        M_RC(proj(m->wgu[l], f, m->bff));
+        f = dst(m->wdown[l]);
         M_HIP(launch_gelu_quant(m->bff, F, m->gelu, m->bact, s, nb, ast, m->trace ? m->trace + (size_t)l * rec + TR_H : nullptr,
-                                tf));
-        M_RC(g4h_matmul_ex(m->wdown[l], nullptr, m->bact, ast, m->bxb, nb, path, s));
+                                tf, f));
+        M_RC(proj(m->wdown[l], f, m->bxb));
         M_RC(trace_rows(l, TR_DOWN, m->bxb, E, E));
     }
     return G4H_OK;

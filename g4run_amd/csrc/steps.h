@@ -60,6 +60,30 @@ __device__ __forceinline__ void q8_store4(const float v[4], int gi, bool own, ui
     if (k == 0) *(uint16_t *)blk = d16;
 }
 
+// k_mm_few's operand layout: the byte offset of codes e .. of (block b, token
+// m) with mt 16-token tiles, and the fp16 index of its scale.  Block pairs
+// outermost, then tiles, then the 16 tokens of a tile, each token's 64 bytes
+// holding codes 0-7 of the even block, 0-7 of the odd one, then 8-15, and so
+// on; the scales in 4 tile slots per (pair, token, block).
+__device__ __forceinline__ size_t few_q(int64_t b, int m, int mt, int e) {
+    return ((((size_t)(b >> 1) * mt + (m >> 4)) * 16 + (m & 15)) * 64) + 16 * (e >> 3) + 8 * (b & 1) + (e & 7);
+}
+__device__ __forceinline__ size_t few_d(int64_t b, int m) { return ((((size_t)(b >> 1) * 16 + (m & 15)) * 2 + (b & 1)) * 4) + (m >> 4); }
+// q8_store4 of token m's row into that layout
+__device__ __forceinline__ void q8_store4_few(const float v[4], int gi, bool own, const FewAct &f, int m) {
+    uint16_t d16;
+    const uint32_t pk = q8_pack4(v, &d16);
+    if (!own) return;
+    const int b = gi >> 3, k = gi & 7;
+    *(uint32_t *)(f.qa + few_q(b, m, f.mt, 4 * k)) = pk;
+    if (k == 0) f.da[few_d(b, m)] = d16;
+}
+// either form: token m's row at `row`, or the layout when f.qa is set
+__device__ __forceinline__ void act_store4(const float v[4], int gi, bool own, uint8_t *row, const FewAct &f, int m) {
+    if (f.qa) q8_store4_few(v, gi, own, f, m);
+    else q8_store4(v, gi, own, row);
+}
+
 // q4_0 of four consecutive values (quants.c:125-144 as the reference build
 // computes it): the 8 consecutive lanes of a 32-element block all call this
 // (the block is owned by all of them or none).  max = the element of largest
@@ -102,12 +126,13 @@ __device__ __forceinline__ void q4_store4(const float v[4], int gi, bool own, ui
 __device__ __forceinline__ float4 ldf4(const float *p) { return *(const float4 *)p; }
 __device__ __forceinline__ void f4(const float4 a, float o[4]) { o[0] = a.x; o[1] = a.y; o[2] = a.z; o[3] = a.w; }
 
-// If delta: x <- x + rms(delta)*w_post (stored back).  Then act <- q8_0(rms(x)*w_pre),
-// and y (if given) <- rms(x)*w_pre in fp32.
+// If delta: x <- x + rms(delta)*w_post (stored back).  Then act <- q8_0(rms(x)*w_pre)
+// (or, with few.qa set, token m of few's layout), and y (if given) <-
+// rms(x)*w_pre in fp32.
 // n % 32 == 0 and n/4 <= S * blockDim.x; all threads of the workgroup call it.
 template <int S>
 __device__ void wg_norm_quant(float *x, const float *delta, const float *w_post, const float *w_pre, float eps, int n,
-                              uint8_t *act, float *y = nullptr) {
+                              uint8_t *act, float *y = nullptr, const FewAct &few = FewAct(), int m = 0) {
     __shared__ double red[16];
     const int ng = n >> 2, bd = blockDim.x, t = threadIdx.x;
     float v[S][4], d[S][4], wp[S][4], wq[S][4];
@@ -150,7 +175,7 @@ __device__ void wg_norm_quant(float *x, const float *delta, const float *w_post,
 #pragma unroll
         for (int k = 0; k < 4; k++) o[k] = v[s][k] * sc * wq[s][k];
         if (y && gi < ng) *(float4 *)(y + 4 * gi) = make_float4(o[0], o[1], o[2], o[3]);
-        q8_store4(o, gi, gi < ng, act);
+        act_store4(o, gi, gi < ng, act, few, m);
     }
 }
 

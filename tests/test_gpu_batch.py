@@ -181,6 +181,38 @@ def test_verify_accepts_the_greedy_prefix(gpu, cfg, K):
         assert a[n_acc] == greedy[n_acc], f"j={j}: bonus {a[n_acc]} vs greedy {greedy[n_acc]}"
 
 
+def test_prompt_chunk_activation_layout_same_bits(gpu):
+    """A prompt chunk's producers write k_mm_few's operand layout themselves
+    (the norm, attention and GELU kernels); G4H_FEW_DIRECT=0 keeps GGUF rows
+    re-laid per projection.  Both must give every traced part of every row
+    and the logits bit for bit, across token counts that change the tile
+    count and its padding (40 tokens: three tiles, 8 padding tokens; 64: four
+    full tiles; 13: one padded tile) in one model, so each count's padding is
+    cleared after the last."""
+    G = gpu
+    for cfg, wtype, counts in ((SMALL, 2, (13, 40, 13)), (MID, 8, (40, 64, 40)), (MID, 2, (64, 24))):
+        m = make_model(G, cfg, 1, wtype)
+        tb = G.Buffer(64 * m.trace_floats() * 4)
+        m.trace(tb)
+        try:
+            for i, nb in enumerate(counts):
+                tokens = np.random.default_rng(100 + i).integers(0, cfg["n_vocab"], nb).astype(np.int32)
+                pos0 = min(cfg["n_ctx"] // 2, cfg["n_ctx"] - nb)
+                res = []
+                for direct in ("1", "0", "1"):
+                    print(f"{cfg['n_embd']}d w {wtype}: chunk of {nb}, G4H_FEW_DIRECT={direct}", flush=True)
+                    os.environ["G4H_FEW_DIRECT"] = direct
+                    try:
+                        lg = m.forward_batch(tokens, pos0)
+                    finally:
+                        del os.environ["G4H_FEW_DIRECT"]
+                    res.append((lg.tobytes(), tb.download(np.float32, nb * m.trace_floats()).tobytes()))
+                assert res[0] == res[1] == res[2], f"chunk of {nb}: the producer-written layout changed the bits"
+        finally:
+            m.trace(None)
+            m.free()
+
+
 def test_batch_argument_errors(gpu):
     G = gpu
     m = make_model(G, SMALL, 1, 2)
