@@ -697,6 +697,10 @@ namespace g4 {
 int matmul_out(const g4h_tensor *W, const float *x, float *Y, int nb, void *stream, const GemvOut &out) {
     return matmul_impl(W, x, nullptr, 0, Y, nb, 1, stream, ScratchSrc(), out);
 }
+bool few_direct() {
+    const char *e = getenv("G4H_FEW_DIRECT");
+    return !e || atoi(e) != 0;
+}
 bool matmul_few_ready(const g4h_tensor *W, int nb, int path) {
     if (!W || nb < 1 || path == 1 || (path == 0 && g4h_matmul_path(W, nb) != 2)) return false;
     return mm_few_ready(*W, nb);

@@ -58,6 +58,7 @@ struct g4h_gemma {
           *u = nullptr, *pl = nullptr, *plp = nullptr, *plg = nullptr, *hn = nullptr;
     uint8_t *ws = nullptr, *wsf = nullptr;     // one-token attention workspaces: sliding / full layers
     uint8_t *bws = nullptr;                    // batch attention workspace
+    uint8_t *bfew = nullptr;                   // a prompt chunk's xb rows as q8_0 in k_mm_few's layout
     int *tok = nullptr;                        // device token ids of a call (kRows)
     int *state = nullptr;                      // decode state: token, pos, npos = pos + 1, steps, flags
     float *logits = nullptr;                   // the step's logits (n_vocab)
@@ -278,6 +279,8 @@ int create(const g4_model_file *mf, int n_ctx, int kv_type, g4h_gemma *m) {
     G_RC(galloc(m, (void **)&m->pl, B * NPL * 4));
     G_RC(galloc(m, (void **)&m->plp, B * NPL * 4));
     G_RC(galloc(m, (void **)&m->plg, B * m->PE * 4));
+    size_t da_off;
+    G_RC(galloc(m, (void **)&m->bfew, few_act_bytes(E, kRows, &da_off)));
     // one workspace per layer kind (the 512-wide heads' three passes leave
     // untagged words that the one-launch form of the other kind would clear)
     const size_t wss = g4h_attn_workspace_bytes(m->H, m->hd_swa, std::min(n_ctx, m->n_swa)),
@@ -418,6 +421,27 @@ static int run(g4h_gemma *m, const int *tok_dev, int nb, int pos0, const int *st
         return tr((size_t)NPL + (size_t)il * rec + off, src, stride, n);
     };
 
+    // A prompt chunk's projections of the xb rows that run k_mm_few (q / k /
+    // v, gate / up) share one quantizer launch per group: the codes are those
+    // each call would make, so the same bits.  fq_ok: fq holds the current xb.
+    FewAct fq;
+    bool fq_ok = false;
+    if (path != 1 && nb >= kMmMinTokens && nb <= kRows && few_direct()) {
+        size_t da_off;
+        few_act_bytes(E, nb, &da_off);
+        fq.qa = (int8_t *)m->bfew;
+        fq.da = (uint16_t *)(m->bfew + da_off);
+        fq.mt = (nb + 15) / 16;
+    }
+    auto mm_xb = [&](const g4h_tensor *W, float *Y) -> int {
+        if (!fq.qa || W->ncols != E || !matmul_few_ready(W, nb, path)) return mm(W, m->xb, Y, nb, path, s);
+        if (!fq_ok) {
+            G_HIP(launch_quantize_few(m->xb, E, E, nb, fq, s));
+            fq_ok = true;
+        }
+        return matmul_few(W, fq, Y, nb, s);
+    };
+
     // embeddings and per-layer token rows (model.c:602-615), gathered on the device
     G_HIP(launch_dequant(m->tok_type, m->tok_raw, m->tok_rb, m->x, E, E, nb, s, tok_dev));
     G_HIP(launch_dequant(m->ple_type, m->ple_raw, m->ple_rb, m->pl, NPL, NPL, nb, s, tok_dev));
@@ -434,11 +458,12 @@ static int run(g4h_gemma *m, const int *tok_dev, int nb, int pos0, const int *st
         const float *rope = L.swa ? m->rope_swa : m->rope_full;
         G_RC(trl(il, T_X, m->x, E, E));
         if (il == 0) G_HIP(launch_rms_rows(m->x, L.attn_norm, m->xb, E, nb, eps, s));   // later layers: the previous residual's launch
+        fq_ok = false;                                                  // xb rewritten: q / k / v read it next
         // one token of a layer with its own K and V: the projections write the
         // attention's q | k | v row in place (no packing launch)
         const bool direct = nb == 1 && il < m->n_layer_kv && L.wv;
         float *qraw = direct ? m->qkv : m->q;
-        G_RC(mm(L.wq, m->xb, qraw, nb, path, s));
+        G_RC(mm_xb(L.wq, qraw));
         G_RC(trl(il, T_Q, qraw, nq, nq));
         QkvArgs qa;
         qa.n_head = H;
@@ -456,8 +481,8 @@ static int run(g4h_gemma *m, const int *tok_dev, int nb, int pos0, const int *st
         if (il < m->n_layer_kv) {
             // own K/V: q | k | v prepared, stored at the position and attended in one step (model.c:664-689)
             float *kraw = direct ? m->qkv + nq : m->k, *vraw = direct ? m->qkv + nq + hd : m->v;
-            G_RC(mm(L.wk, m->xb, kraw, nb, path, s));
-            if (L.wv) G_RC(mm(L.wv, m->xb, vraw, nb, path, s));
+            G_RC(mm_xb(L.wk, kraw));
+            if (L.wv) G_RC(mm_xb(L.wv, vraw));
             G_RC(trl(il, T_K, kraw, hd, hd));
             if (L.wv) G_RC(trl(il, T_V, vraw, hd, hd));
             if (!direct) G_HIP(launch_pack_qkv(m->q, m->k, L.wv ? m->v : nullptr, m->qkv, nq, hd, nb, s));
@@ -493,7 +518,8 @@ static int run(g4h_gemma *m, const int *tok_dev, int nb, int pos0, const int *st
         // FFN (model.c:718-736); one untraced token: h = gelu(gate) * up in the
         // up projection's store (k_gelu_mul's arithmetic, one launch fewer)
         const bool fold = nb == 1 && !m->trace;
-        G_RC(mm(L.gate, m->xb, m->g, nb, path, s));
+        fq_ok = false;                                                  // xb rewritten: gate / up read it next
+        G_RC(mm_xb(L.gate, m->g));
         if (fold) {
             GemvOut o;
             o.mode = OUT_GELU_E;
@@ -501,7 +527,7 @@ static int run(g4h_gemma *m, const int *tok_dev, int nb, int pos0, const int *st
             o.gelu = m->gelu;
             G_RC(matmul_out(L.up, m->xb, m->g, 1, s, o));
         } else {
-            G_RC(mm(L.up, m->xb, m->u, nb, path, s));
+            G_RC(mm_xb(L.up, m->u));
             G_RC(trl(il, T_G, m->g, F, F));
             G_RC(trl(il, T_U, m->u, F, F));
             G_HIP(launch_gelu_mul(m->g, F, m->u, F, F, nb, m->gelu, s));

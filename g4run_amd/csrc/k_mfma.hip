@@ -735,6 +735,16 @@ static hipError_t few_go(const g4h_tensor &W, const int8_t *qa, const uint16_t *
     return hipErrorInvalidValue;
 }
 
+hipError_t launch_quantize_few(const float *x, size_t xs, int64_t ncols, int M, const FewAct &a, hipStream_t s) {
+    if (!x || !a.qa || !a.da || M <= 0 || M > MMF_MAXM || a.mt != (M + 15) / 16 || ncols % 32 || (uintptr_t)x % 16 || xs % 4)
+        return hipErrorInvalidValue;
+    const int mte = (a.mt + 1) & ~1;
+    const int64_t np = (ncols / 32 + 1) / 2;
+    hipLaunchKernelGGL(k_quantize_planar<true>, dim3((unsigned)((np * 16 + 256 * QP - 1) / (256 * QP)), 16 * mte), dim3(256), 0, s, x,
+                       xs, ncols, M, a.mt, a.qa, a.da);
+    return hipGetLastError();
+}
+
 hipError_t launch_mm_few_ready(const g4h_tensor &W, const FewAct &a, int M, float *Y, hipStream_t s) {
     if (M <= 0 || !mm_few_ready(W, M) || !a.qa || !a.da || a.mt != (M + 15) / 16) return hipErrorInvalidValue;
     return few_go(W, a.qa, a.da, M, Y, s);

@@ -73,6 +73,10 @@ int matmul_out(const g4h_tensor *W, const float *x, float *Y, int nb, void *stre
 // whole block pairs, so that its producer may write the FewAct layout, and
 // that matmul on activations already in it
 bool matmul_few_ready(const g4h_tensor *W, int nb, int path);
+// whether the batched forwards hand k_mm_few its layout directly (G4H_FEW_DIRECT=0:
+// GGUF rows or fp32 rows quantized per projection, for measurement and the
+// check that both give the same bits)
+bool few_direct();
 int matmul_few(const g4h_tensor *W, const FewAct &a, float *Y, int nb, void *stream);
 
 // Persistent single-token GEMV (gemv_p.h) over q4_0 / q8_0 rows with a fused
@@ -225,6 +229,9 @@ hipError_t launch_matmul_mfma(const g4h_tensor &W, const float *x, size_t x_stri
 bool mm_few_ready(const g4h_tensor &W, int M);
 size_t few_act_bytes(int64_t ncols, int M, size_t *da_off);
 hipError_t launch_few_clear(uint8_t *buf, size_t bytes, hipStream_t s);
+// x fp32 rows (xs floats apart) quantized to q8_0 into that layout, padding
+// tokens and block included (launch_matmul_mfma's own quantizer launch)
+hipError_t launch_quantize_few(const float *x, size_t xs, int64_t ncols, int M, const FewAct &a, hipStream_t s);
 hipError_t launch_mm_few_ready(const g4h_tensor &W, const FewAct &a, int M, float *Y, hipStream_t s);
 
 // k_mfma_k.hip: many-token matmul on the int8 matrix cores for q4_K / q6_K

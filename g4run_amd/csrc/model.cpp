@@ -450,13 +450,6 @@ static bool batch_attn() {
     return on;
 }
 
-// G4H_FEW_DIRECT=0 keeps the prompt batch's activations in GGUF rows, re-laid
-// per projection (measurement, and the check that both give the same bits)
-static bool few_direct() {
-    const char *e = getenv("G4H_FEW_DIRECT");
-    return !e || atoi(e) != 0;
-}
-
 static int batch_alloc(g4h_model *m) {
     if (m->bx) return G4H_OK;
     const g4h_model_config &c = m->c;

@@ -16,6 +16,8 @@ the other side of a rounding edge), so only such part-by-part checks hold a
 per-element tolerance; the whole-model runs are also held to the oracle's
 greedy token where its top-two gap is clear, and a batch to one token at a
 time bit for bit."""
+import os
+
 import numpy as np
 import pytest
 
@@ -377,6 +379,35 @@ def test_prefill_on_matrix_cores_part_by_part(gpu, oracle, tmp_path, spec, kv_ty
             tok, pos = int(np.argmax(olg[0])), pos + 1
     finally:
         oracle.pool_stop()
+        m.free()
+
+
+@pytest.mark.parametrize("spec", ["SMALL", "WIDE"])
+def test_prefill_shared_quantizer_same_bits(gpu, oracle, tmp_path, spec):
+    """The q / k / v and gate / up projections of a prompt chunk that run
+    k_mm_few share one quantizer launch of their xb rows; G4H_FEW_DIRECT=0
+    quantizes in every call.  Both give the same logits bit for bit, at token
+    counts of one, two (padded) and four tiles."""
+    G = gpu
+    hp, T = GM.make_gemma(oracle, 37, spec=getattr(GM, spec))
+    path = tmp_path / "g.gguf"
+    GM.write_gemma(path, hp, T)
+    m = G.Gemma(path, n_ctx=160, kv_type=1)
+    toks = np.random.default_rng(23).integers(0, hp["n_vocab"], 160)
+    try:
+        pos = 0
+        for nb in (9, 40, 64):
+            res = []
+            for direct in ("1", "0"):
+                print(f"{spec}: prefill of {nb} at {pos}, G4H_FEW_DIRECT={direct}", flush=True)
+                os.environ["G4H_FEW_DIRECT"] = direct
+                try:
+                    res.append(m.prefill(toks[pos:pos + nb], pos).tobytes())
+                finally:
+                    del os.environ["G4H_FEW_DIRECT"]
+            assert res[0] == res[1], f"prefill of {nb}: the shared quantizer changed the bits"
+            pos += nb
+    finally:
         m.free()
 
 
